@@ -1,0 +1,98 @@
+// Shared host/device helpers for the gfx950 SSM kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "../../include/mamba_hip.h"
+
+namespace mamba {
+
+// ---------------------------------------------------------------- errors ---
+void set_error(const std::string& msg);
+
+#define MAMBA_CHECK_ARG(cond, msg)                                  \
+    do {                                                            \
+        if (!(cond)) {                                              \
+            ::mamba::set_error(std::string(__func__) + ": " + msg); \
+            return MAMBA_ERR_INVALID_ARG;                           \
+        }                                                           \
+    } while (0)
+
+#define MAMBA_CHECK_HIP(expr)                                                         \
+    do {                                                                              \
+        hipError_t e_ = (expr);                                                       \
+        if (e_ != hipSuccess) {                                                       \
+            ::mamba::set_error(std::string(__func__) + ": " #expr " -> " +          \
+                               hipGetErrorString(e_));                                \
+            return MAMBA_ERR_HIP;                                                     \
+        }                                                                             \
+    } while (0)
+
+#define MAMBA_CHECK_LAUNCH() MAMBA_CHECK_HIP(hipGetLastError())
+
+// ----------------------------------------------------------------- bf16 ---
+typedef uint16_t bf16_t;  // storage type; arithmetic always in f32
+
+__device__ __forceinline__ float bf16_to_f32(bf16_t v) {
+    return __uint_as_float(((uint32_t)v) << 16);
+}
+
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
+    // round to nearest even; NaN stays NaN (quiet bit kept by the high half)
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (bf16_t)(u >> 16);
+}
+
+template <typename T>
+__device__ __forceinline__ float load_f32(const T* p);
+template <>
+__device__ __forceinline__ float load_f32<float>(const float* p) { return *p; }
+template <>
+__device__ __forceinline__ float load_f32<bf16_t>(const bf16_t* p) { return bf16_to_f32(*p); }
+
+template <typename T>
+__device__ __forceinline__ void store_f32(T* p, float v);
+template <>
+__device__ __forceinline__ void store_f32<float>(float* p, float v) { *p = v; }
+template <>
+__device__ __forceinline__ void store_f32<bf16_t>(bf16_t* p, float v) { *p = f32_to_bf16(v); }
+
+// ------------------------------------------------------------ numerics ---
+// softplus with the f32 threshold of src/modules/activation/softplus.rs:21-47
+__device__ __forceinline__ float softplus_f32(float x) {
+    const float thr = 18.f;
+    return x > thr ? x : log1pf(expf(fminf(x, thr)));
+}
+// silu(x) = x / (1 + exp(-x))  (src/modules/activation/silu.rs:24-27)
+__device__ __forceinline__ float silu_f32(float x) { return x / (expf(-x) + 1.f); }
+// div_eps(F32) of src/utils/mod.rs:59-65
+constexpr float kDivEpsF32 = 8.1584695e-8f;
+
+// ---------------------------------------------------- wave/block scans ---
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Inclusive prefix sum over a wave (64 lanes).
+__device__ __forceinline__ float wave_incl_scan(float v) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        float t = __shfl_up(v, o, 64);
+        if (lane >= o) v += t;
+    }
+    return v;
+}
+
+inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+}  // namespace mamba

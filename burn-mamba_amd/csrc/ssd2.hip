@@ -1,0 +1,296 @@
+// Mamba-2 chunked SSD forward for gfx950.
+//
+// Two code paths behind one entry point (mamba_ssd2_fwd):
+//   * the MFMA path (ssd2_mfma.hip) for headdim 64 and dstate 64/128 with
+//     chunk lengths 64/128/256, bf16 or f32 I/O;
+//   * the shape-generic path below for everything else: three SIMT kernels
+//     (chunk state, state passing, chunk scan) with f32 arithmetic.
+//
+// Reference: src/mamba2/ssd/serial.rs:34-506 (K1..K5) and the trait default
+// body src/mamba2/ssd/serial_recalculated/serial_recalculated.rs:98-155.
+
+#include "common.h"
+#include "ssd2.h"
+
+namespace mamba {
+
+// ------------------------------------------------------------ block scan --
+// Inclusive prefix sum of one value per thread over a 256-thread block.
+__device__ __forceinline__ float block_incl_scan256(float v, float* sh4) {
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    v = wave_incl_scan(v);
+    if (lane == 63) sh4[wid] = v;
+    __syncthreads();
+    float off = 0.f;
+    for (int w = 0; w < wid; ++w) off += sh4[w];
+    __syncthreads();
+    return v + off;
+}
+
+// Fills cs[0..Q) with the intra-chunk cumulative sum of dt*A (K1,
+// serial.rs:138-164) and dts[0..Q) with dt; positions past seqlen read as
+// dt = 0, which is exactly the zero padding of mamba2.rs:709-722.
+__device__ void chunk_cumsum(const Ssd2Params& p, int b, int c, int h, float* cs, float* dts,
+                             float* sh4) {
+    const float a = p.A[h];
+    float carry = 0.f;
+    for (int base = 0; base < p.Q; base += 256) {
+        const int l = base + threadIdx.x;
+        const int t = c * p.Q + l;
+        float dtv = 0.f;
+        if (l < p.Q && t < p.L) dtv = p.dt[(int64_t)b * p.dt_sb + (int64_t)t * p.dt_sl + (int64_t)h * p.dt_sh];
+        float s = block_incl_scan256(dtv * a, sh4) + carry;
+        if (l < p.Q) {
+            cs[l] = s;
+            dts[l] = dtv;
+        }
+        // carry = last element of this 256-segment
+        __syncthreads();
+        const int last = min(base + 256, p.Q) - 1;
+        carry = cs[last];
+        __syncthreads();
+    }
+}
+
+// ------------------------------------------------------- K1 + K3 (generic) --
+// S[b,c,h,p,n] = sum_l x[l,p] * (B[l,n] * (exp(cs_end - cs_l) * dt_l))
+template <typename T>
+__global__ __launch_bounds__(256) void ssd2_chunk_state_generic(Ssd2Params p, float* states,
+                                                                float* da_end) {
+    extern __shared__ float smem[];
+    const int h = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
+    const int g = h / (p.H / p.G);
+    const int Q = p.Q, P = p.P, N = p.N;
+    float* cs = smem;            // [Q]
+    float* dts = cs + Q;         // [Q]
+    float* sh4 = dts + Q;        // [4]
+    float* xt = sh4 + 4;         // [TL][P]
+    constexpr int TL = 16;
+    float* bt = xt + TL * P;     // [TL][N]
+    chunk_cumsum(p, b, c, h, cs, dts, sh4);
+    const float cs_end = cs[Q - 1];
+    if (threadIdx.x == 0) da_end[((int64_t)b * p.H + h) * p.nch + c] = cs_end;
+    const T* X = (const T*)p.x;
+    const T* Bm = (const T*)p.Bm;
+    float* Sout = states + (((int64_t)b * p.nch + c) * p.H + h) * P * N;
+    constexpr int OPT = 32;  // outputs per thread per pass
+    for (int e0 = 0; e0 < P * N; e0 += 256 * OPT) {
+        float acc[OPT];
+#pragma unroll
+        for (int k = 0; k < OPT; ++k) acc[k] = 0.f;
+        for (int l0 = 0; l0 < Q; l0 += TL) {
+            __syncthreads();
+            for (int i = threadIdx.x; i < TL * P; i += 256) {
+                const int l = l0 + i / P, pp = i % P, t = c * Q + l;
+                xt[i] = (l < Q && t < p.L)
+                            ? load_f32(X + (int64_t)b * p.x_sb + (int64_t)t * p.x_sl + (int64_t)h * p.x_sh + pp)
+                            : 0.f;
+            }
+            for (int i = threadIdx.x; i < TL * N; i += 256) {
+                const int l = l0 + i / N, n = i % N, t = c * Q + l;
+                float w = 0.f;
+                if (l < Q && t < p.L) {
+                    const float scale = expf(cs_end - cs[l]) * dts[l];
+                    w = load_f32(Bm + (int64_t)b * p.B_sb + (int64_t)t * p.B_sl + (int64_t)g * p.B_sg + n) * scale;
+                }
+                bt[i] = w;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int k = 0; k < OPT; ++k) {
+                const int e = e0 + k * 256 + threadIdx.x;
+                if (e < P * N) {
+                    const int pp = e / N, n = e % N;
+                    float a = acc[k];
+                    for (int l = 0; l < TL; ++l) a += xt[l * P + pp] * bt[l * N + n];
+                    acc[k] = a;
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < OPT; ++k) {
+            const int e = e0 + k * 256 + threadIdx.x;
+            if (e < P * N) Sout[e] = acc[k];
+        }
+    }
+}
+
+// ------------------------------------------------------------ K4 (generic) --
+// In place: states[c] <- state entering chunk c; final <- state after the last.
+__global__ __launch_bounds__(256) void ssd2_state_pass_generic(Ssd2Params p, float* states,
+                                                               const float* da_end) {
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int PN = p.P * p.N;
+    const int e = blockIdx.x * 256 + threadIdx.x;
+    if (e >= PN) return;
+    float run = p.h0 ? p.h0[((int64_t)b * p.H + h) * PN + e] : 0.f;
+    if (p.init_hpr) run += p.init_hpr[(int64_t)h * PN + e];
+    const float* de = da_end + ((int64_t)b * p.H + h) * p.nch;
+    for (int c = 0; c < p.nch; ++c) {
+        float* s = states + (((int64_t)b * p.nch + c) * p.H + h) * PN + e;
+        const float tmp = *s;
+        *s = run;
+        run = expf(de[c]) * run + tmp;
+    }
+    p.hT[((int64_t)b * p.H + h) * PN + e] = run;
+}
+
+// ------------------------------------------------------- K2 + K5 (generic) --
+// y[i,p] = exp(cs_i) C_i.h_in[p,:] + sum_{j<=i} (C_i.B_j) exp(cs_i-cs_j) dt_j x[j,p] + D x[i,p]
+template <typename T>
+__global__ __launch_bounds__(256) void ssd2_chunk_scan_generic(Ssd2Params p, const float* states) {
+    extern __shared__ float smem[];
+    const int h = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
+    const int g = h / (p.H / p.G);
+    const int Q = p.Q, P = p.P, N = p.N;
+    float* cs = smem;       // [Q]
+    float* dts = cs + Q;    // [Q]
+    float* sh4 = dts + Q;   // [4]
+    float* cb = sh4 + 4;    // [R][Q]
+    chunk_cumsum(p, b, c, h, cs, dts, sh4);
+    const T* X = (const T*)p.x;
+    const T* Bm = (const T*)p.Bm;
+    const T* Cm = (const T*)p.Cm;
+    T* Y = (T*)p.y;
+    const float* hin = states + (((int64_t)b * p.nch + c) * p.H + h) * P * N;
+    const float Dh = p.D ? p.D[h] : 0.f;
+    const int R = P >= 256 ? 1 : 256 / P;  // rows per pass
+    const int qvalid = min(Q, p.L - c * Q);
+    for (int i0 = 0; i0 < qvalid; i0 += R) {
+        __syncthreads();
+        // CB rows i0..i0+R (K2, serial.rs:170-185), lower triangle only
+        for (int k = threadIdx.x; k < R * Q; k += 256) {
+            const int ii = i0 + k / Q, j = k % Q;
+            float v = 0.f;
+            if (ii < qvalid && j <= ii) {
+                const int ti = c * Q + ii, tj = c * Q + j;
+                const T* crow = Cm + (int64_t)b * p.C_sb + (int64_t)ti * p.C_sl + (int64_t)g * p.C_sg;
+                const T* brow = Bm + (int64_t)b * p.B_sb + (int64_t)tj * p.B_sl + (int64_t)g * p.B_sg;
+                for (int n = 0; n < N; ++n) v += load_f32(crow + n) * load_f32(brow + n);
+            }
+            cb[k] = v;
+        }
+        __syncthreads();
+        for (int k = threadIdx.x; k < R * P; k += 256) {
+            const int ii = i0 + k / P, pp = k % P;
+            if (ii >= qvalid) continue;
+            const int ti = c * Q + ii;
+            const T* crow = Cm + (int64_t)b * p.C_sb + (int64_t)ti * p.C_sl + (int64_t)g * p.C_sg;
+            float blue = 0.f;
+            for (int n = 0; n < N; ++n) blue += load_f32(crow + n) * hin[pp * N + n];
+            blue *= expf(cs[ii]);
+            float orange = 0.f;
+            const float* cbr = cb + (k / P) * Q;
+            for (int j = 0; j <= ii; ++j) {
+                const int tj = c * Q + j;
+                const float xv = load_f32(X + (int64_t)b * p.x_sb + (int64_t)tj * p.x_sl + (int64_t)h * p.x_sh + pp);
+                orange += ((cbr[j] * expf(cs[ii] - cs[j])) * dts[j]) * xv;
+            }
+            const float xi = load_f32(X + (int64_t)b * p.x_sb + (int64_t)ti * p.x_sl + (int64_t)h * p.x_sh + pp);
+            store_f32(Y + (int64_t)b * p.y_sb + (int64_t)ti * p.y_sl + (int64_t)h * p.y_sh + pp,
+                      (blue + orange) + Dh * xi);
+        }
+    }
+}
+
+// ------------------------------------------------------------ host side --
+size_t ssd2_generic_workspace(const Ssd2Params& p) {
+    const size_t states = (size_t)p.nb * p.nch * p.H * p.P * p.N * sizeof(float);
+    const size_t daend = (size_t)p.nb * p.H * p.nch * sizeof(float);
+    return align_up(states, 256) + align_up(daend, 256);
+}
+
+int ssd2_generic_launch(const Ssd2Params& p, void* ws, hipStream_t stream) {
+    float* states = (float*)ws;
+    float* daend = (float*)((char*)ws + align_up((size_t)p.nb * p.nch * p.H * p.P * p.N * sizeof(float), 256));
+    dim3 grid(p.H, p.nch, p.nb);
+    const size_t sm_state = (2 * (size_t)p.Q + 4 + 16 * (size_t)p.P + 16 * (size_t)p.N) * sizeof(float);
+    const int R = p.P >= 256 ? 1 : 256 / p.P;
+    const size_t sm_scan = (2 * (size_t)p.Q + 4 + (size_t)R * p.Q) * sizeof(float);
+    if (p.io_dtype == MAMBA_BF16) {
+        hipLaunchKernelGGL(ssd2_chunk_state_generic<bf16_t>, grid, dim3(256), sm_state, stream, p, states, daend);
+    } else {
+        hipLaunchKernelGGL(ssd2_chunk_state_generic<float>, grid, dim3(256), sm_state, stream, p, states, daend);
+    }
+    MAMBA_CHECK_LAUNCH();
+    dim3 gpass(ceil_div(p.P * p.N, 256), p.H, p.nb);
+    hipLaunchKernelGGL(ssd2_state_pass_generic, gpass, dim3(256), 0, stream, p, states, daend);
+    MAMBA_CHECK_LAUNCH();
+    if (p.io_dtype == MAMBA_BF16) {
+        hipLaunchKernelGGL(ssd2_chunk_scan_generic<bf16_t>, grid, dim3(256), sm_scan, stream, p, states);
+    } else {
+        hipLaunchKernelGGL(ssd2_chunk_scan_generic<float>, grid, dim3(256), sm_scan, stream, p, states);
+    }
+    MAMBA_CHECK_LAUNCH();
+    return MAMBA_OK;
+}
+
+// Host-side validation of the public arguments (the reference asserts the same
+// conditions: mamba2.rs:562-566, serial_recalculated.rs:41-44, gqa.rs:37-41).
+int ssd2_make_params(const mamba_ssd2_args* a, Ssd2Params* out) {
+    MAMBA_CHECK_ARG(a != nullptr, "args is NULL");
+    MAMBA_CHECK_ARG(a->batch > 0 && a->seqlen > 0, "batch and seqlen must be >= 1");
+    MAMBA_CHECK_ARG(a->nheads > 0 && a->headdim > 0 && a->dstate > 0, "nheads/headdim/dstate must be >= 1");
+    MAMBA_CHECK_ARG(a->ngroups > 0 && a->nheads % a->ngroups == 0, "nheads must be a multiple of ngroups");
+    MAMBA_CHECK_ARG(a->chunk_len > 0 && a->chunk_len <= 1024, "chunk_len must be in [1, 1024]");
+    MAMBA_CHECK_ARG(a->io_dtype == MAMBA_F32 || a->io_dtype == MAMBA_BF16, "io_dtype must be MAMBA_F32 or MAMBA_BF16");
+    MAMBA_CHECK_ARG(a->x && a->dt && a->A && a->B && a->C && a->y && a->final_state,
+                    "x, dt, A, B, C, y and final_state are required");
+    MAMBA_CHECK_ARG(a->headdim <= 256 && a->dstate <= 256, "headdim and dstate must be <= 256");
+    Ssd2Params& p = *out;
+    p.nb = a->batch; p.L = a->seqlen; p.H = a->nheads; p.P = a->headdim; p.G = a->ngroups;
+    p.N = a->dstate; p.Q = a->chunk_len; p.nch = (a->seqlen + a->chunk_len - 1) / a->chunk_len;
+    p.io_dtype = a->io_dtype;
+    p.x = a->x; p.x_sb = a->x_sb; p.x_sl = a->x_sl; p.x_sh = a->x_sh;
+    p.dt = a->dt; p.dt_sb = a->dt_sb; p.dt_sl = a->dt_sl; p.dt_sh = a->dt_sh;
+    p.A = a->A; p.D = a->D;
+    p.Bm = a->B; p.B_sb = a->B_sb; p.B_sl = a->B_sl; p.B_sg = a->B_sg;
+    p.Cm = a->C; p.C_sb = a->C_sb; p.C_sl = a->C_sl; p.C_sg = a->C_sg;
+    p.h0 = a->initial_state; p.init_hpr = a->init_state_hpr;
+    p.y = a->y; p.y_sb = a->y_sb; p.y_sl = a->y_sl; p.y_sh = a->y_sh;
+    p.hT = a->final_state;
+    return MAMBA_OK;
+}
+
+}  // namespace mamba
+
+using namespace mamba;
+
+extern "C" size_t mamba_ssd2_workspace_size(const mamba_ssd2_args* a) {
+    Ssd2Params p;
+    if (ssd2_make_params(a, &p) != MAMBA_OK) return 0;
+    size_t ws = ssd2_generic_workspace(p);
+    const size_t fast = ssd2_mfma_workspace(p);
+    return ws > fast ? ws : fast;
+}
+
+extern "C" int mamba_ssd2_fwd_generic(const mamba_ssd2_args* a, void* ws, size_t ws_bytes,
+                                      mamba_stream_t stream) {
+    Ssd2Params p;
+    int st = ssd2_make_params(a, &p);
+    if (st != MAMBA_OK) return st;
+    if (ws == nullptr || ws_bytes < ssd2_generic_workspace(p)) {
+        set_error("mamba_ssd2_fwd_generic: workspace missing or too small");
+        return MAMBA_ERR_WORKSPACE;
+    }
+    return ssd2_generic_launch(p, ws, (hipStream_t)stream);
+}
+
+extern "C" int mamba_ssd2_fwd(const mamba_ssd2_args* a, void* ws, size_t ws_bytes,
+                              mamba_stream_t stream) {
+    Ssd2Params p;
+    int st = ssd2_make_params(a, &p);
+    if (st != MAMBA_OK) return st;
+    if (ssd2_mfma_supported(p)) {
+        if (ws == nullptr || ws_bytes < ssd2_mfma_workspace(p)) {
+            set_error("mamba_ssd2_fwd: workspace missing or too small");
+            return MAMBA_ERR_WORKSPACE;
+        }
+        return ssd2_mfma_launch(p, ws, (hipStream_t)stream);
+    }
+    if (ws == nullptr || ws_bytes < ssd2_generic_workspace(p)) {
+        set_error("mamba_ssd2_fwd: workspace missing or too small");
+        return MAMBA_ERR_WORKSPACE;
+    }
+    return ssd2_generic_launch(p, ws, (hipStream_t)stream);
+}

@@ -1,0 +1,9 @@
+"""mamba_hip — host side of the MI355X (gfx950) SSM hot path for burn-mamba.
+
+Thin Python mirror of the reference's operator interfaces over the C ABI of
+libmamba_hip.so (include/mamba_hip.h).  Every compute call goes to the HIP
+library; nothing here computes on the CPU.
+"""
+
+from ._lib import MambaHipError, exported_symbols, lib  # noqa: F401
+from .ssd import Mamba2SsdInput, Mamba2SsdPath, ssd2_fwd  # noqa: F401

@@ -1,0 +1,81 @@
+"""ctypes binding of libmamba_hip.so (include/mamba_hip.h).
+
+The library is the product: there is no fallback.  If it is missing, loading
+raises; if a call returns a non-zero status, ``MambaHipError`` is raised with
+the library's own message (the reference panics via ``assert!`` in the same
+situations).  Device memory and streams come from PyTorch (ROCm build) as
+plain pointers.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "..", "lib", "libmamba_hip.so")
+
+MAMBA_F32 = 0
+MAMBA_BF16 = 1
+
+c_i32 = ctypes.c_int32
+c_i64 = ctypes.c_int64
+c_vp = ctypes.c_void_p
+
+
+class MambaHipError(RuntimeError):
+    pass
+
+
+class Ssd2Args(ctypes.Structure):
+    _fields_ = [
+        ("batch", c_i32), ("seqlen", c_i32), ("nheads", c_i32), ("headdim", c_i32),
+        ("ngroups", c_i32), ("dstate", c_i32), ("chunk_len", c_i32), ("io_dtype", c_i32),
+        ("x", c_vp), ("x_sb", c_i64), ("x_sl", c_i64), ("x_sh", c_i64),
+        ("dt", c_vp), ("dt_sb", c_i64), ("dt_sl", c_i64), ("dt_sh", c_i64),
+        ("A", c_vp),
+        ("B", c_vp), ("B_sb", c_i64), ("B_sl", c_i64), ("B_sg", c_i64),
+        ("C", c_vp), ("C_sb", c_i64), ("C_sl", c_i64), ("C_sg", c_i64),
+        ("D", c_vp), ("initial_state", c_vp), ("init_state_hpr", c_vp),
+        ("y", c_vp), ("y_sb", c_i64), ("y_sl", c_i64), ("y_sh", c_i64),
+        ("final_state", c_vp),
+    ]
+
+
+# name -> (argtypes, restype); the exported symbol set of include/mamba_hip.h
+_SIGNATURES = {
+    "mamba_last_error": ([], ctypes.c_char_p),
+    "mamba_version": ([], ctypes.c_char_p),
+    "mamba_ssd2_workspace_size": ([ctypes.POINTER(Ssd2Args)], ctypes.c_size_t),
+    "mamba_ssd2_fwd": ([ctypes.POINTER(Ssd2Args), c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),
+    "mamba_ssd2_fwd_generic": ([ctypes.POINTER(Ssd2Args), c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),
+}
+
+_lib = None
+
+
+def lib():
+    """Load libmamba_hip.so once; raise if it is not built."""
+    global _lib
+    if _lib is None:
+        path = os.path.normpath(LIB_PATH)
+        if not os.path.exists(path):
+            raise MambaHipError(
+                f"{path} is not built; run `python burn-mamba_amd/build.py` (no CPU fallback exists)")
+        L = ctypes.CDLL(path)
+        for name, (argt, rest) in _SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.argtypes = argt
+            fn.restype = rest
+        _lib = L
+    return _lib
+
+
+def exported_symbols():
+    return sorted(_SIGNATURES)
+
+
+def check(status: int, what: str):
+    if status != 0:
+        msg = lib().mamba_last_error().decode(errors="replace")
+        raise MambaHipError(f"{what} failed with status {status}: {msg}")

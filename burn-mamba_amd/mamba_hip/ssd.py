@@ -1,0 +1,162 @@
+"""Mamba-2 SSD host interface, mirroring the reference's pluggable-SSD seam.
+
+Reference: ``Mamba2SsdPath`` / ``Mamba2SsdInput`` / ``run``
+(src/mamba2/ssd/ssd_path.rs:20-163) and the backend extension
+``Mamba2BackendExt::ssd_serial_recalculated``
+(src/mamba2/ssd/serial_recalculated/serial_recalculated.rs:73-156).
+
+All three reference algorithms (Minimal, Serial, SerialRecalculated) are exact
+reformulations of one function; on this backend every variant runs the same
+gfx950 kernels — the variant only carries the chunk length, as in the
+reference.  Tensors are PyTorch device tensors (used as plain memory).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import MAMBA_BF16, MAMBA_F32, Ssd2Args, check
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return MAMBA_F32
+    if t.dtype == torch.bfloat16:
+        return MAMBA_BF16
+    raise _lib.MambaHipError(f"unsupported dtype {t.dtype} (f32 or bf16)")
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+_WS = {}
+
+
+def workspace(device, nbytes: int) -> torch.Tensor:
+    """A cached per-device byte buffer of at least ``nbytes`` (stream-ordered use)."""
+    key = str(device)
+    buf = _WS.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+        _WS[key] = buf
+    return buf
+
+
+def _check_inner(t: torch.Tensor, name: str):
+    if t.stride(-1) != 1:
+        raise _lib.MambaHipError(f"{name}: innermost axis must be contiguous")
+
+
+def ssd2_fwd(x, dt, A, B, C, D=None, initial_state=None, init_state_hpr=None, chunk_len=None,
+             y=None, final_state=None, generic=False):
+    """Mamba-2 SSD forward through ``mamba_ssd2_fwd``.
+
+    x[b,l,h,p] (f32|bf16)  dt[b,l,h] f32  A[h] f32  B,C[b,l,g,n] (dtype of x)
+    D[h] f32  initial_state[b,h,p,n] f32  init_state_hpr[h,p,n] f32.
+    Any strides are accepted for the three outer axes; the innermost axis must
+    be contiguous.  Returns (y[b,l,h,p] dtype of x, final_state[b,h,p,n] f32).
+    """
+    b, l, h, p = x.shape
+    g, n = B.shape[2], B.shape[3]
+    if chunk_len is None:
+        chunk_len = Mamba2SsdPath.optimal_chunk_len(n, p)
+    for t, nm in ((x, "x"), (B, "B"), (C, "C")):
+        _check_inner(t, nm)
+    if not (dt.dtype == A.dtype == torch.float32):
+        raise _lib.MambaHipError("dt and A must be float32")
+    if y is None:
+        y = torch.empty((b, l, h, p), dtype=x.dtype, device=x.device)
+    if final_state is None:
+        final_state = torch.empty((b, h, p, n), dtype=torch.float32, device=x.device)
+    for t in (A, D, initial_state, init_state_hpr, final_state):
+        if t is not None and not t.is_contiguous():
+            raise _lib.MambaHipError("A, D and the states must be contiguous")
+    a = Ssd2Args()
+    a.batch, a.seqlen, a.nheads, a.headdim, a.ngroups, a.dstate = b, l, h, p, g, n
+    a.chunk_len, a.io_dtype = int(chunk_len), _dtype_code(x)
+    a.x = x.data_ptr(); a.x_sb, a.x_sl, a.x_sh = x.stride(0), x.stride(1), x.stride(2)
+    a.dt = dt.data_ptr(); a.dt_sb, a.dt_sl, a.dt_sh = dt.stride(0), dt.stride(1), dt.stride(2)
+    a.A = A.data_ptr()
+    a.B = B.data_ptr(); a.B_sb, a.B_sl, a.B_sg = B.stride(0), B.stride(1), B.stride(2)
+    a.C = C.data_ptr(); a.C_sb, a.C_sl, a.C_sg = C.stride(0), C.stride(1), C.stride(2)
+    a.D = None if D is None else D.data_ptr()
+    a.initial_state = None if initial_state is None else initial_state.data_ptr()
+    a.init_state_hpr = None if init_state_hpr is None else init_state_hpr.data_ptr()
+    a.y = y.data_ptr(); a.y_sb, a.y_sl, a.y_sh = y.stride(0), y.stride(1), y.stride(2)
+    a.final_state = final_state.data_ptr()
+    L = _lib.lib()
+    nbytes = L.mamba_ssd2_workspace_size(ctypes.byref(a))
+    ws = workspace(x.device, nbytes)
+    fn = L.mamba_ssd2_fwd_generic if generic else L.mamba_ssd2_fwd
+    check(fn(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(x.device)),
+          "mamba_ssd2_fwd")
+    return y, final_state
+
+
+class Mamba2SsdPath:
+    """Algorithm selector carrying an optional chunk length (ssd_path.rs:20-53)."""
+
+    MINIMAL, SERIAL, SERIAL_RECALCULATED = "Minimal", "Serial", "SerialRecalculated"
+
+    def __init__(self, kind: str = SERIAL_RECALCULATED, chunk_len: Optional[int] = None):
+        assert kind in (self.MINIMAL, self.SERIAL, self.SERIAL_RECALCULATED)
+        self.kind, self._chunk_len = kind, chunk_len
+
+    @staticmethod
+    def optimal_chunk_len(state_rank: int, per_head_dim: int) -> int:
+        """min(512, roundup32(isqrt(r*p))) — ssd_path.rs:109-114."""
+        v = math.isqrt(state_rank * per_head_dim)
+        v = (v + 31) // 32 * 32
+        return min(v, 512)
+
+    def chunk_len(self) -> Optional[int]:
+        return self._chunk_len
+
+    def chunk_len_or_optimal(self, state_rank: int, per_head_dim: int) -> int:
+        return self._chunk_len if self._chunk_len is not None else self.optimal_chunk_len(
+            state_rank, per_head_dim)
+
+
+@dataclass
+class Mamba2SsdInput:
+    """Pre-processed SSD inputs in the reference's chunked shapes (ssd_path.rs:58-87).
+
+    x_bnlhp[b,n,l,h,p]  dt_bnlh[b,n,l,h]  a_decay_h[h]  b_bnlhr/c_bnlhr[b,n,l,h,r]
+    (per head, or per group with the group count in place of h)  d_h[h]
+    initial_state_bhpr[b,h,p,r]  init_state_hpr[h,p,r] | None.
+    """
+
+    x_bnlhp: torch.Tensor
+    dt_bnlh: torch.Tensor
+    a_decay_h: torch.Tensor
+    b_bnlhr: torch.Tensor
+    c_bnlhr: torch.Tensor
+    d_h: torch.Tensor
+    initial_state_bhpr: torch.Tensor
+    init_state_hpr: Optional[torch.Tensor] = None
+
+    def run(self, path: Mamba2SsdPath):
+        """Returns (y_bnlhp, final_state_bhpr) — ssd_path.rs:149-155."""
+        b, nch, q, h, p = self.x_bnlhp.shape
+        g, r = self.b_bnlhr.shape[3], self.b_bnlhr.shape[4]
+        if nch < 1:
+            raise _lib.MambaHipError("sequence length must be at least 1")
+        L = nch * q
+        x = self.x_bnlhp.reshape(b, L, h, p)
+        dt = self.dt_bnlh.reshape(b, L, h)
+        Bm = self.b_bnlhr.reshape(b, L, g, r)
+        Cm = self.c_bnlhr.reshape(b, L, g, r)
+        y, hT = ssd2_fwd(x, dt, self.a_decay_h, Bm, Cm, self.d_h, self.initial_state_bhpr,
+                         self.init_state_hpr, chunk_len=q)
+        return y.reshape(b, nch, q, h, p), hT

@@ -1,0 +1,108 @@
+/*
+ * mamba_hip.h — C ABI of the MI355X (gfx950) SSM hot path for burn-mamba.
+ *
+ * One shared library, libmamba_hip.so, built from burn-mamba_amd/csrc/ with
+ * hipcc --offload-arch=gfx950.  Every entry point:
+ *   - takes plain device pointers, sizes and element strides (no framework types);
+ *   - is stream-ordered on the hipStream_t it is given and returns without a
+ *     host synchronisation;
+ *   - validates shapes/pointers on the host first and returns a non-zero
+ *     mamba_status (never launching a kernel) when they are wrong — the
+ *     reference panics via assert! in the same places, the Rust binding maps a
+ *     non-zero status back to a panic;
+ *   - allocates nothing: scratch memory comes from a caller-owned workspace
+ *     whose size the matching *_workspace_size() reports.
+ * Calls that share a workspace buffer must be ordered on one stream.
+ *
+ * Reference interfaces replaced (swfsql/burn-mamba, paths relative to its root):
+ *   mamba_ssd2_fwd      <- Mamba2BackendExt::ssd_serial_recalculated
+ *                          (src/mamba2/ssd/serial_recalculated/serial_recalculated.rs:86-98),
+ *                          reached from Mamba2SsdInput::run (src/mamba2/ssd/ssd_path.rs:149-155)
+ *   mamba_ssd3_fwd      <- Mamba3SingleSsdBackendExt::single_ssd_serial_recalculated
+ *                          (src/mamba3/single_ssd/ssd/serial_recalculated/serial_recalculated.rs:86-114)
+ *   mamba1_scan_fwd     <- Mamba1::selective_scan (src/mamba1/mamba1.rs:422-430)
+ *                          plus the silu(z) gate of Mamba1::forward (mamba1.rs:348)
+ *   mamba1_scan_step    <- Mamba1::selective_scan_step (src/mamba1/mamba1.rs:666-674)
+ *   mamba2_step_ssm     <- the body of Mamba2::step between in_proj and out_proj
+ *                          (src/mamba2/mamba2.rs:857-995)
+ *   mamba_linear_bf16   <- burn::nn::Linear::forward as used by in_proj/out_proj
+ *                          (src/mamba2/mamba2.rs:850,1000)
+ *   mamba_rmsnorm       <- RmsNorm::forward (src/modules/norm/rms_norm.rs:53-98), the
+ *                          pre-norm of Layer::step_one (src/modules/layer.rs:224-232)
+ */
+#ifndef MAMBA_HIP_H
+#define MAMBA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hipStream_t without pulling in the HIP headers (it is a pointer type). */
+typedef struct ihipStream_t* mamba_stream_t;
+
+typedef enum mamba_status {
+    MAMBA_OK = 0,
+    MAMBA_ERR_INVALID_ARG = 1,   /* bad shape, null required pointer, bad stride */
+    MAMBA_ERR_UNSUPPORTED = 2,   /* valid request this build does not implement */
+    MAMBA_ERR_WORKSPACE = 3,     /* workspace missing or smaller than *_workspace_size */
+    MAMBA_ERR_HIP = 4            /* a HIP runtime call failed (see mamba_last_error) */
+} mamba_status;
+
+typedef enum mamba_dtype {
+    MAMBA_F32 = 0,
+    MAMBA_BF16 = 1
+} mamba_dtype;
+
+/* Human-readable description of the last error raised on the calling thread. */
+const char* mamba_last_error(void);
+/* Library version string ("mamba_hip <semver> gfx950"). */
+const char* mamba_version(void);
+
+/* ------------------------------------------------------------------------- */
+/* Mamba-2 chunked SSD forward (K1 cumsum, K2 C.B^T, K3 chunk state, K4 state  */
+/* passing, K5 chunk scan).                                                   */
+/*                                                                             */
+/*   y[b,t,h,:] = sum_{s<=t} (C_t . B_s) exp(sum_{s<k<=t} dt_k A_h) dt_s x_s    */
+/*                + exp(sum_{k<=t} dt_k A_h) C_t . h0 + D_h x_t                 */
+/*                                                                             */
+/* Element strides are given for the three outer axes; the innermost axis      */
+/* (headdim for x/y, dstate for B/C) must be contiguous.  Head h reads group   */
+/* h / (nheads / ngroups) (src/modules/misc/gqa.rs:30-56); pass ngroups =      */
+/* nheads for the reference's per-head-expanded B/C.  dt is the discretised    */
+/* step (post softplus/clamp, src/mamba2/mamba2.rs:695) in f32; the reference  */
+/* seam's dt_bhnl layout is expressed with dt strides.  seqlen need not be a   */
+/* multiple of chunk_len: the tail behaves as the zero padding of              */
+/* src/mamba2/mamba2.rs:709-722.                                               */
+/* ------------------------------------------------------------------------- */
+typedef struct mamba_ssd2_args {
+    int32_t batch, seqlen, nheads, headdim, ngroups, dstate, chunk_len;
+    int32_t io_dtype;                 /* mamba_dtype of x, B, C and y */
+    const void* x;  int64_t x_sb, x_sl, x_sh;      /* [b, l, h, p]          */
+    const float* dt; int64_t dt_sb, dt_sl, dt_sh;  /* [b, l, h] f32         */
+    const float* A;                                 /* [h] f32, negative     */
+    const void* B;  int64_t B_sb, B_sl, B_sg;      /* [b, l, g, n]          */
+    const void* C;  int64_t C_sb, C_sl, C_sg;      /* [b, l, g, n]          */
+    const float* D;                                 /* [h] f32 or NULL (=0)  */
+    const float* initial_state;                     /* [b, h, p, n] f32 or NULL */
+    const float* init_state_hpr;                    /* [h, p, n] f32 or NULL (learnable h0) */
+    void* y;        int64_t y_sb, y_sl, y_sh;      /* [b, l, h, p]          */
+    float* final_state;                             /* [b, h, p, n] f32      */
+} mamba_ssd2_args;
+
+size_t mamba_ssd2_workspace_size(const mamba_ssd2_args* args);
+int mamba_ssd2_fwd(const mamba_ssd2_args* args, void* workspace, size_t workspace_bytes,
+                   mamba_stream_t stream);
+
+/* Same contract, forced onto the shape-generic kernels (no MFMA fast path);    */
+/* used to cross-check the fast path.                                           */
+int mamba_ssd2_fwd_generic(const mamba_ssd2_args* args, void* workspace, size_t workspace_bytes,
+                           mamba_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MAMBA_HIP_H */

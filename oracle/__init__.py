@@ -1,0 +1,195 @@
+"""CPU oracle for the burn-mamba SSM hot path — TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline``
+leg may import this package, and only as the checker (or the timed CPU
+baseline).  The product path (``burn-mamba_amd/``) never imports it.
+
+``liboracle.so`` (built from ``oracle_body.h`` by ``oracle/Makefile``) holds the
+C restatement of the reference algorithms at two precisions: ``prec=32`` runs
+every intermediate in f32 like the reference's f32 Burn ops, ``prec=64`` in f64
+("truth").  Each wrapper below names the reference function it restates; the
+exact file:line citations are in ``oracle_body.h``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+
+
+def build(force: bool = False) -> str:
+    """Compile liboracle.so with the committed Makefile (gcc, OpenMP)."""
+    if force or not os.path.exists(_LIB_PATH):
+        subprocess.run(["make", "-B" if force else "-s", "-C", _HERE, "liboracle.so"],
+                       check=True, stdout=subprocess.DEVNULL)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(_LIB_PATH)
+        for prec in (32, 64):
+            for name in ("ssd2_serial", "ssd2_minimal", "ssd2_recurrent", "mamba1_scan",
+                         "mamba1_step", "mamba2_step_ssm", "rmsnorm", "linear", "ssd3_serial",
+                         "ssd3_recurrent"):
+                getattr(_lib, f"orc{prec}_{name}").restype = None
+    return _lib
+
+
+def _ptr(a):
+    if a is None:
+        return None
+    assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"], (a.dtype, a.flags)
+    return a.ctypes.data_as(_f32p)
+
+
+def _f32(a):
+    return None if a is None else np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _fn(name, prec):
+    return getattr(lib(), f"orc{prec}_{name}")
+
+
+# --------------------------------------------------------------------------
+# Mamba-2 SSD core (src/mamba2/ssd/{serial,minimal}.rs; mamba2.rs:932-991)
+# --------------------------------------------------------------------------
+
+def ssd2(x, dt, A, B, C, D=None, h0=None, init_hpr=None, chunk=64, form="serial", prec=64):
+    """Mamba-2 SSD forward. x[b,l,h,p] dt[b,l,h] A[h] B,C[b,l,g,n] D[h] h0[b,h,p,n].
+
+    form: "serial" (K1..K5, serial.rs), "minimal" (segsum, minimal.rs) or
+    "recurrent" (token-by-token step recurrence, mamba2.rs:932-991).
+    Returns (y[b,l,h,p], final_state[b,h,p,n]) as float32.
+    """
+    x, dt, A, B, C, D, h0, init_hpr = map(_f32, (x, dt, A, B, C, D, h0, init_hpr))
+    b, l, h, p = x.shape
+    g, n = B.shape[2], B.shape[3]
+    assert dt.shape == (b, l, h) and A.shape == (h,) and B.shape == C.shape == (b, l, g, n)
+    assert h % g == 0
+    y = np.zeros_like(x)
+    hT = np.zeros((b, h, p, n), np.float32)
+    args = [_ptr(x), _ptr(dt), _ptr(A), _ptr(B), _ptr(C), _ptr(D), _ptr(h0), _ptr(init_hpr),
+            _ptr(y), _ptr(hT)]
+    if form == "recurrent":
+        _fn("ssd2_recurrent", prec)(b, l, h, p, g, n, *args)
+    else:
+        _fn(f"ssd2_{form}", prec)(b, l, h, p, g, n, chunk, *args)
+    return y, hT
+
+
+# --------------------------------------------------------------------------
+# Mamba-1 selective scan (src/mamba1/mamba1.rs:422-523, :666-733)
+# --------------------------------------------------------------------------
+
+def mamba1_scan(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
+                h0=None, prec=64):
+    """u,delta,z[b,d,l] A[d,n] B,C[b,n,l] D[d] h0[b,d,n] -> (y[b,d,l], hT[b,d,n])."""
+    u, delta, A, B, C, D, z, delta_bias, h0 = map(_f32, (u, delta, A, B, C, D, z, delta_bias, h0))
+    b, d, l = u.shape
+    n = A.shape[1]
+    assert delta.shape == u.shape and B.shape == C.shape == (b, n, l) and A.shape == (d, n)
+    y = np.zeros_like(u)
+    hT = np.zeros((b, d, n), np.float32)
+    _fn("mamba1_scan", prec)(b, d, l, n, _ptr(u), _ptr(delta), _ptr(A), _ptr(B), _ptr(C), _ptr(D),
+                             _ptr(z), _ptr(delta_bias), int(bool(delta_softplus)), _ptr(h0),
+                             _ptr(y), _ptr(hT))
+    return y, hT
+
+
+def mamba1_step(u, delta, A, B, C, state, D=None, z=None, delta_bias=None, delta_softplus=False,
+                prec=64):
+    """One token: u,delta,z[b,d] B,C[b,n] state[b,d,n] -> (y[b,d], new_state)."""
+    u, delta, A, B, C, D, z, delta_bias = map(_f32, (u, delta, A, B, C, D, z, delta_bias))
+    st = np.array(state, dtype=np.float32, copy=True)
+    b, d = u.shape
+    n = A.shape[1]
+    y = np.zeros_like(u)
+    _fn("mamba1_step", prec)(b, d, n, _ptr(u), _ptr(delta), _ptr(A), _ptr(B), _ptr(C), _ptr(D),
+                             _ptr(z), _ptr(delta_bias), int(bool(delta_softplus)), _ptr(st), _ptr(y))
+    return y, st
+
+
+# --------------------------------------------------------------------------
+# Mamba-2 block step (src/mamba2/mamba2.rs:820-1004)
+# --------------------------------------------------------------------------
+
+def mamba2_step_ssm(zxbcdt, conv_state, conv_w, conv_b, dt_bias, A, D, norm_w, ssm_state,
+                    nheads, headdim, ngroups, dstate, dt_limit=(0.0, 65504.0), prec=64):
+    """Everything of Mamba2::step between in_proj and out_proj.
+
+    Returns (out[b, d_inner], new_conv_state, new_ssm_state)."""
+    zxbcdt, conv_w, conv_b, dt_bias, A, D, norm_w = map(
+        _f32, (zxbcdt, conv_w, conv_b, dt_bias, A, D, norm_w))
+    cs = np.array(conv_state, dtype=np.float32, copy=True)
+    ss = np.array(ssm_state, dtype=np.float32, copy=True)
+    b = zxbcdt.shape[0]
+    k = conv_w.shape[1]
+    out = np.zeros((b, nheads * headdim), np.float32)
+    _fn("mamba2_step_ssm", prec)(b, nheads, headdim, ngroups, dstate, k, _ptr(zxbcdt), _ptr(cs),
+                                 _ptr(conv_w), _ptr(conv_b), _ptr(dt_bias), _ptr(A), _ptr(D),
+                                 ctypes.c_float(dt_limit[0]), ctypes.c_float(dt_limit[1]),
+                                 _ptr(norm_w), _ptr(ss), _ptr(out))
+    return out, cs, ss
+
+
+def rmsnorm(x, w, prec=64):
+    x, w = _f32(x), _f32(w)
+    out = np.zeros_like(x)
+    _fn("rmsnorm", prec)(x.shape[0], x.shape[1], _ptr(x), _ptr(w), _ptr(out))
+    return out
+
+
+def linear(x, W, bias=None, prec=64):
+    """x[r,k] @ W[k,c] (+bias) — Burn Linear (weight stored [d_in, d_out])."""
+    x, W, bias = _f32(x), _f32(W), _f32(bias)
+    out = np.zeros((x.shape[0], W.shape[1]), np.float32)
+    _fn("linear", prec)(x.shape[0], x.shape[1], W.shape[1], _ptr(x), _ptr(W), _ptr(bias), _ptr(out))
+    return out
+
+
+def mamba2_layer_step(u, params, conv_state, ssm_state, cfg, prec=64):
+    """Pre-norm Layer step around Mamba2::step (src/modules/layer.rs:224-232):
+    returns (u + out_proj(ssm(in_proj(RMSNorm(u)))), conv_state', ssm_state')."""
+    normed = rmsnorm(u, params["pre_norm_w"], prec)
+    zxbcdt = linear(normed, params["w_in"], None, prec)
+    out, cs, ss = mamba2_step_ssm(zxbcdt, conv_state, params["conv_w"], params["conv_b"],
+                                  params["dt_bias"], params["A"], params["D"], params["norm_w"],
+                                  ssm_state, cfg["nheads"], cfg["headdim"], cfg["ngroups"],
+                                  cfg["dstate"], prec=prec)
+    y = linear(out, params["w_out"], None, prec)
+    return u + y, cs, ss
+
+
+# --------------------------------------------------------------------------
+# Mamba-3 single-pass SSD (src/mamba3/single_ssd/ssd/serial.rs:56-268)
+# --------------------------------------------------------------------------
+
+def ssd3(v, da, B, C, gamma, scale, h0=None, chunk=64, form="serial", prec=64):
+    """v[b,l,m,h,p] da,gamma,scale[b,l,h] B,C[b,l,m,h,n] h0[b,h,p,n] -> (y[b,l,m,h,p], hT)."""
+    v, da, B, C, gamma, scale, h0 = map(_f32, (v, da, B, C, gamma, scale, h0))
+    b, l, m, h, p = v.shape
+    n = B.shape[-1]
+    assert B.shape == C.shape == (b, l, m, h, n) and da.shape == gamma.shape == scale.shape == (b, l, h)
+    y = np.zeros_like(v)
+    hT = np.zeros((b, h, p, n), np.float32)
+    args = [_ptr(v), _ptr(da), _ptr(B), _ptr(C), _ptr(gamma), _ptr(scale), _ptr(h0), _ptr(y), _ptr(hT)]
+    if form == "recurrent":
+        _fn("ssd3_recurrent", prec)(b, l, m, h, p, n, *args)
+    else:
+        _fn("ssd3_serial", prec)(b, l, m, h, p, n, chunk, *args)
+    return y, hT
+
+

@@ -1,0 +1,70 @@
+"""C-ABI checks that need no GPU: the library loads, exports exactly the
+functions include/mamba_hip.h declares, and the ctypes struct mirrors have the
+C layout (sizes and field offsets compiled by gcc from the header)."""
+
+import ctypes
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mamba_hip.h")
+
+
+def _declared_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    names = re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(mamba\w+)\s*\(", src, flags=re.M)
+    return sorted(set(names))
+
+
+def test_header_declares_what_binding_binds():
+    import mamba_hip
+    assert _declared_functions() == mamba_hip.exported_symbols()
+
+
+def test_library_loads_and_exports_every_symbol():
+    import mamba_hip
+    L = mamba_hip.lib()
+    for name in _declared_functions():
+        assert hasattr(L, name), name
+    assert L.mamba_version().decode().startswith("mamba_hip")
+
+
+def _c_layout(struct_name, fields):
+    body = "\n".join(f'printf("%zu\\n", offsetof({struct_name}, {f}));' for f in fields)
+    prog = f"""#include <stdio.h>
+#include <stddef.h>
+#include "mamba_hip.h"
+int main(void) {{ printf("%zu\\n", sizeof({struct_name})); {body} return 0; }}
+"""
+    with tempfile.TemporaryDirectory() as d:
+        c = os.path.join(d, "p.c")
+        exe = os.path.join(d, "p")
+        open(c, "w").write(prog)
+        subprocess.run(["gcc", "-I", os.path.dirname(HEADER), c, "-o", exe], check=True)
+        out = subprocess.run([exe], check=True, capture_output=True, text=True).stdout.split()
+    return [int(v) for v in out]
+
+
+@pytest.mark.parametrize("cls_name,c_name", [("Ssd2Args", "mamba_ssd2_args")])
+def test_struct_layouts_match_header(cls_name, c_name):
+    from mamba_hip import _lib
+    cls = getattr(_lib, cls_name)
+    fields = [f[0] for f in cls._fields_]
+    got = _c_layout(c_name, fields)
+    assert got[0] == ctypes.sizeof(cls)
+    assert got[1:] == [getattr(cls, f).offset for f in fields]
+
+
+def test_invalid_args_need_no_gpu():
+    """Host-side validation rejects bad shapes before any HIP call."""
+    from mamba_hip import _lib
+    a = _lib.Ssd2Args()
+    a.batch, a.seqlen, a.nheads, a.headdim, a.ngroups, a.dstate, a.chunk_len = 1, 8, 3, 4, 2, 4, 4
+    rc = _lib.lib().mamba_ssd2_fwd(ctypes.byref(a), None, 0, None)
+    assert rc == 1  # MAMBA_ERR_INVALID_ARG
+    assert b"ngroups" in _lib.lib().mamba_last_error()

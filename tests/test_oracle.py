@@ -1,0 +1,301 @@
+"""Pins the CPU oracle (oracle/) without running the reference.
+
+The reference is Rust over Burn; neither a Rust toolchain nor Burn's sources
+exist here and it ships no golden vectors, so each oracle function is checked
+against an independent formulation that a plausible slip (dropped term, wrong
+sign, off-by-one in the causal mask, transposed operand) would break:
+  * three algebraically distinct SSD forms (serial K1-K5, minimal/segsum,
+    token recurrence) must agree (the reference's own paths_agree tests,
+    src/mamba2/ssd/ssd_path/tests.rs:184-336);
+  * closed forms: A = 0, dt = 1 reduces the SSD to causal linear attention
+    y = tril(C B^T) X + D X (numpy matmuls); delta = 0 makes the Mamba-1 scan
+    y = D u; N = 1 with constant delta is a first-order IIR filter
+    (scipy.signal.lfilter);
+  * invariants: chunk-length independence; zero-dt padding is an identity
+    (src/mamba2/mamba2.rs:703-706); split == full (cache continuity);
+  * Mamba-3: the merged single-SSD equals the explicit two-term trapezoid
+    recurrence (src/mamba3/mamba3.rs:14-26), and lambda = 1 collapses it to
+    Mamba-2.
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+from inputs import mamba1_inputs, softplus, ssd2_inputs, ssd2_test_inputs
+
+SHAPES = [(2, 12, 2, 8, 2, 8, 4), (2, 12, 4, 8, 4, 8, 4), (2, 4, 2, 8, 1, 8, 4), (1, 37, 4, 8, 2, 8, 8)]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_ssd2_three_forms_agree(shape):
+    b, l, h, p, g, n, q = shape
+    inp = ssd2_test_inputs(1, b, l, h, p, g, n)
+    args = (inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"], inp["h0"])
+    ys, hs = oracle.ssd2(*args, chunk=q, form="serial")
+    ym, hm = oracle.ssd2(*args, chunk=q, form="minimal")
+    yr, hr = oracle.ssd2(*args, form="recurrent")
+    for a, r in ((ys, yr), (ym, yr), (hs, hr), (hm, hr)):
+        np.testing.assert_allclose(a, r, rtol=1e-6, atol=1e-6)
+    # the f32 restatement (the reference's own arithmetic width) stays within 1e-4
+    y32, h32 = oracle.ssd2(*args, chunk=q, form="serial", prec=32)
+    np.testing.assert_allclose(y32, yr, rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(h32, hr, rtol=1e-4, atol=1e-4)
+
+
+def test_ssd2_linear_attention_closed_form():
+    b, l, h, p, g, n = 2, 40, 3, 5, 1, 6
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((b, l, h, p)).astype(np.float32)
+    B = rng.standard_normal((b, l, g, n)).astype(np.float32)
+    C = rng.standard_normal((b, l, g, n)).astype(np.float32)
+    D = rng.standard_normal(h).astype(np.float32)
+    dt = np.ones((b, l, h), np.float32)
+    A = np.zeros(h, np.float32)
+    for form in ("serial", "minimal", "recurrent"):
+        y, hT = oracle.ssd2(x, dt, A, B, C, D, chunk=8, form=form)
+        for bi in range(b):
+            M = np.tril(C[bi, :, 0].astype(np.float64) @ B[bi, :, 0].astype(np.float64).T)
+            for hi in range(h):
+                ref = M @ x[bi, :, hi].astype(np.float64) + D[hi] * x[bi, :, hi]
+                np.testing.assert_allclose(y[bi, :, hi], ref, rtol=1e-5, atol=1e-5)
+                sref = x[bi, :, hi].astype(np.float64).T @ B[bi, :, 0].astype(np.float64)
+                np.testing.assert_allclose(hT[bi, hi], sref, rtol=1e-5, atol=1e-5)
+
+
+def test_ssd2_chunk_independence_and_padding():
+    inp = ssd2_inputs(2, b=2, l=70, h=3, p=8, g=1, n=8, h0=True)
+    args = (inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"], inp["h0"])
+    y0, h0 = oracle.ssd2(*args, chunk=70, form="serial")
+    for q in (1, 7, 16, 64, 128):
+        y, hT = oracle.ssd2(*args, chunk=q, form="serial")
+        np.testing.assert_allclose(y, y0, rtol=1e-6, atol=1e-6)
+        np.testing.assert_allclose(hT, h0, rtol=1e-6, atol=1e-6)
+    # zero-dt tokens appended: identity on the state, y there is D*x
+    pad = {k: (np.concatenate([v, np.zeros_like(v[:, :5])], 1) if k in ("x", "dt", "B", "C") else v)
+           for k, v in inp.items()}
+    y2, h2 = oracle.ssd2(pad["x"], pad["dt"], pad["A"], pad["B"], pad["C"], pad["D"], pad["h0"], chunk=16)
+    np.testing.assert_allclose(h2, h0, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(y2[:, :70], y0, rtol=1e-6, atol=1e-6)
+
+
+def test_ssd2_split_equals_full_and_init_hpr():
+    inp = ssd2_inputs(3, b=1, l=50, h=2, p=4, g=1, n=4, h0=True)
+    full = oracle.ssd2(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"], inp["h0"], chunk=8)
+    s = 21
+    ya, ha = oracle.ssd2(*(inp[k][:, :s] for k in ("x", "dt")), inp["A"], inp["B"][:, :s], inp["C"][:, :s],
+                         inp["D"], inp["h0"], chunk=8)
+    yb, hb = oracle.ssd2(*(inp[k][:, s:] for k in ("x", "dt")), inp["A"], inp["B"][:, s:], inp["C"][:, s:],
+                         inp["D"], ha, chunk=8)
+    np.testing.assert_allclose(np.concatenate([ya, yb], 1), full[0], rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(hb, full[1], rtol=1e-6, atol=1e-6)
+    # learnable init state adds to h0 (minimal.rs:316-328)
+    init = np.random.default_rng(4).standard_normal((2, 4, 4)).astype(np.float32)
+    y1, h1 = oracle.ssd2(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"], inp["h0"], init, chunk=8)
+    y2, h2 = oracle.ssd2(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"], inp["h0"] + init[None], chunk=8)
+    np.testing.assert_allclose(y1, y2, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(h1, h2, rtol=1e-6, atol=1e-6)
+
+
+def test_ssd2_golden_fixture_regression():
+    import os
+    f = np.load(os.path.join(os.path.dirname(__file__), "golden", "ssd2_cfg0_small.npz"))
+    y, hT = oracle.ssd2(f["x"], f["dt"], f["A"], f["B"], f["C"], f["D"], f["h0"], chunk=int(f["chunk"]))
+    np.testing.assert_allclose(y, f["y"], rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(hT, f["final_state"], rtol=1e-6, atol=1e-6)
+    yr, hr = oracle.ssd2(f["x"], f["dt"], f["A"], f["B"], f["C"], f["D"], f["h0"], form="recurrent")
+    np.testing.assert_allclose(yr, f["y"], rtol=1e-5, atol=1e-5)
+
+
+# ----------------------------------------------------------------- Mamba-1 --
+
+def _scan_loop(u, delta, A, B, C, D, z, h0):
+    b, d, l = u.shape
+    n = A.shape[1]
+    y = np.zeros((b, d, l))
+    h = np.zeros((b, d, n)) if h0 is None else h0.astype(np.float64).copy()
+    for t in range(l):
+        dl = delta[:, :, t].astype(np.float64)
+        a = np.exp(dl[:, :, None] * A[None].astype(np.float64))
+        h = h * a + (dl[:, :, None] * B[:, None, :, t]) * u[:, :, t, None]
+        y[:, :, t] = (h * C[:, None, :, t]).sum(-1) + D[None] * u[:, :, t]
+    if z is not None:
+        y = y * (z / (1 + np.exp(-z.astype(np.float64))))
+    return y, h
+
+
+def test_mamba1_matches_vectorised_loop():
+    inp = mamba1_inputs(1, b=2, d=5, l=33, n=4, h0=True)
+    y, hT = oracle.mamba1_scan(inp["u"], inp["delta"], inp["A"], inp["B"], inp["C"], inp["D"], inp["z"],
+                               h0=inp["h0"])
+    yr, hr = _scan_loop(inp["u"], inp["delta"], inp["A"], inp["B"], inp["C"], inp["D"], inp["z"], inp["h0"])
+    np.testing.assert_allclose(y, yr, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(hT, hr, rtol=1e-5, atol=1e-6)
+
+
+def test_mamba1_closed_forms():
+    from scipy.signal import lfilter
+    inp = mamba1_inputs(2, b=1, d=3, l=64, n=1)
+    # delta = 0: the state stays at h0 and y = C_t . h0 + D*u
+    h0 = np.full((1, 3, 1), 0.5, np.float32)
+    y, hT = oracle.mamba1_scan(inp["u"], np.zeros_like(inp["delta"]), inp["A"], inp["B"], inp["C"],
+                               inp["D"], h0=h0)
+    ref = 0.5 * inp["C"][:, 0][:, None, :] + inp["D"][None, :, None] * inp["u"]
+    np.testing.assert_allclose(y, ref, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(hT, h0, rtol=0, atol=0)
+    # N = 1, constant delta: h_t = a h_{t-1} + delta B_t u_t is an IIR filter
+    dl = np.full_like(inp["delta"], 0.07)
+    y, hT = oracle.mamba1_scan(inp["u"], dl, inp["A"], inp["B"], inp["C"], None)
+    for d in range(3):
+        a = np.exp(0.07 * inp["A"][d, 0])
+        hseq = lfilter([1.0], [1.0, -a], 0.07 * inp["B"][0, 0] * inp["u"][0, d])
+        np.testing.assert_allclose(y[0, d], hseq * inp["C"][0, 0], rtol=1e-5, atol=1e-6)
+        np.testing.assert_allclose(hT[0, d, 0], hseq[-1], rtol=1e-5)
+
+
+def test_mamba1_step_unroll_equals_scan():
+    inp = mamba1_inputs(3, b=2, d=4, l=9, n=3, h0=True)
+    y, hT = oracle.mamba1_scan(inp["u"], inp["delta"], inp["A"], inp["B"], inp["C"], inp["D"], inp["z"],
+                               h0=inp["h0"])
+    st = inp["h0"]
+    for t in range(9):
+        ys, st = oracle.mamba1_step(inp["u"][:, :, t], inp["delta"][:, :, t], inp["A"], inp["B"][:, :, t],
+                                    inp["C"][:, :, t], st, inp["D"], inp["z"][:, :, t])
+        np.testing.assert_allclose(ys, y[:, :, t], rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(st, hT, rtol=1e-5, atol=1e-6)
+
+
+def test_mamba1_delta_bias_softplus():
+    inp = mamba1_inputs(4, b=1, d=3, l=8, n=2)
+    bias = np.array([0.1, -0.2, 0.3], np.float32)
+    raw = np.random.default_rng(0).standard_normal(inp["u"].shape).astype(np.float32)
+    y1, h1 = oracle.mamba1_scan(inp["u"], raw, inp["A"], inp["B"], inp["C"], inp["D"], delta_bias=bias,
+                                delta_softplus=True)
+    dl = np.log1p(np.exp(raw.astype(np.float64) + bias[None, :, None])).astype(np.float32)
+    y2, h2 = oracle.mamba1_scan(inp["u"], dl, inp["A"], inp["B"], inp["C"], inp["D"])
+    np.testing.assert_allclose(y1, y2, rtol=1e-5, atol=1e-6)
+
+
+# ------------------------------------------------------- Mamba-2 step() ----
+
+def _silu(v):
+    return v / (1 + np.exp(-v))
+
+
+def test_mamba2_step_ssm_closed_form():
+    """conv + SiLU + softplus + state update + readout + gated RMSNorm, from
+    the formulas of mamba2.rs:865-995 written independently in numpy."""
+    rng = np.random.default_rng(9)
+    b, H, P, G, N, K = 2, 4, 8, 2, 6, 4
+    d_inner, conv_dim = H * P, H * P + 2 * G * N
+    zx = rng.standard_normal((b, d_inner + conv_dim + H)).astype(np.float32)
+    conv_state = rng.standard_normal((b, conv_dim, K)).astype(np.float32)
+    conv_w = rng.standard_normal((conv_dim, K)).astype(np.float32) * 0.5
+    conv_b = rng.standard_normal(conv_dim).astype(np.float32) * 0.1
+    dt_bias = rng.standard_normal(H).astype(np.float32)
+    A = -np.exp(rng.uniform(0, 2, H)).astype(np.float32)
+    D = rng.standard_normal(H).astype(np.float32)
+    nw = rng.standard_normal(d_inner).astype(np.float32)
+    ss = rng.standard_normal((b, H, P, N)).astype(np.float32)
+    out, cs2, ss2 = oracle.mamba2_step_ssm(zx, conv_state, conv_w, conv_b, dt_bias, A, D, nw, ss, H, P, G, N)
+    z, xbc, dtr = zx[:, :d_inner], zx[:, d_inner:d_inner + conv_dim], zx[:, d_inner + conv_dim:]
+    win = np.concatenate([conv_state[:, :, 1:], xbc[:, :, None]], 2)
+    np.testing.assert_array_equal(cs2, win)
+    act = _silu((win.astype(np.float64) * conv_w[None]).sum(-1) + conv_b)
+    xs = act[:, :d_inner].reshape(b, H, P)
+    Bg = act[:, d_inner:d_inner + G * N].reshape(b, G, N)
+    Cg = act[:, d_inner + G * N:].reshape(b, G, N)
+    dt = softplus(dtr.astype(np.float64) + dt_bias)
+    hpg = H // G
+    Bh, Ch = np.repeat(Bg, hpg, 1), np.repeat(Cg, hpg, 1)
+    hn = ss * np.exp(dt * A)[:, :, None, None] + dt[:, :, None, None] * Bh[:, :, None, :] * xs[:, :, :, None]
+    np.testing.assert_allclose(ss2, hn, rtol=1e-5, atol=1e-6)
+    y = (hn * Ch[:, :, None, :]).sum(-1) + D[None, :, None] * xs
+    gv = y.reshape(b, d_inner) * _silu(z.astype(np.float64))
+    ref = gv / np.sqrt((gv ** 2).mean(-1, keepdims=True) + 8.1584695e-8) * nw
+    np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-6)
+
+
+def test_mamba2_step_unroll_equals_ssd():
+    """forward == step unroll (the reference's src/mamba2/mamba2/tests.rs:202-328)
+    at the SSM level: stepping the state update token by token reproduces the
+    chunked SSD's final state and outputs."""
+    inp = ssd2_inputs(6, b=2, l=11, h=4, p=8, g=2, n=6, h0=True)
+    y, hT = oracle.ssd2(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"], inp["h0"], chunk=4)
+    st = inp["h0"].astype(np.float64)
+    hpg = 2
+    for t in range(11):
+        dt = inp["dt"][:, t].astype(np.float64)
+        Bh = np.repeat(inp["B"][:, t], hpg, 1)
+        Ch = np.repeat(inp["C"][:, t], hpg, 1)
+        st = st * np.exp(dt * inp["A"])[:, :, None, None] + dt[:, :, None, None] * Bh[:, :, None, :] * inp["x"][:, t, :, :, None]
+        yt = (st * Ch[:, :, None, :]).sum(-1) + inp["D"][None, :, None] * inp["x"][:, t]
+        np.testing.assert_allclose(y[:, t], yt, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(hT, st, rtol=1e-5, atol=1e-6)
+
+
+# ----------------------------------------------------------------- Mamba-3 --
+
+def _m3_inputs(seed, b, l, m, h, p, n, lam=None):
+    rng = np.random.default_rng(seed)
+    v = rng.standard_normal((b, l, m, h, p)).astype(np.float32)
+    B = (rng.standard_normal((b, l, m, h, n)) / np.sqrt(n)).astype(np.float32)
+    C = (rng.standard_normal((b, l, m, h, n)) / np.sqrt(n)).astype(np.float32)
+    dt = rng.uniform(0.01, 0.3, (b, l, h))
+    A = -rng.uniform(0.5, 2.0, h)
+    lam = 1.0 / (1.0 + np.exp(-rng.standard_normal((b, l, h)))) if lam is None else np.full((b, l, h), lam)
+    da = dt * A
+    gamma = lam * dt
+    nxt = np.concatenate([(1 - lam[:, 1:]) * dt[:, 1:], np.zeros((b, 1, h))], 1)
+    scale = gamma + nxt
+    beta = (1 - lam) * dt * np.exp(da)
+    h0 = (0.1 * rng.standard_normal((b, h, p, n))).astype(np.float32)
+    f = lambda a: np.asarray(a, np.float32)
+    return dict(v=v, B=B, C=C, da=f(da), gamma=f(gamma), scale=f(scale), beta=beta, dt=dt, A=A, lam=lam, h0=h0)
+
+
+def _trapezoid_loop(d, h0_boundary):
+    """Explicit trapezoid recurrence (src/mamba3/mamba3.rs:14-26; step form
+    double_ssd/double_ssd/mod.rs:713-748): h_t = a_t h_{t-1} + beta_t sum_m
+    B_{t-1,m} v_{t-1,m} + gamma_t sum_m B_t,m v_t,m ; y_t,m = C_t,m . h_t."""
+    v, B, C = (d[k].astype(np.float64) for k in ("v", "B", "C"))
+    b, l, m, h, p = v.shape
+    hs = h0_boundary.astype(np.float64).copy()
+    y = np.zeros_like(v)
+    prev = np.zeros((b, h, p, B.shape[-1]))
+    for t in range(l):
+        cur = np.einsum("bmhp,bmhn->bhpn", v[:, t], B[:, t])
+        hs = np.exp(d["da"][:, t].astype(np.float64))[:, :, None, None] * hs \
+            + d["beta"][:, t][:, :, None, None] * prev + d["gamma"][:, t].astype(np.float64)[:, :, None, None] * cur
+        y[:, t] = np.einsum("bmhn,bhpn->bmhp", C[:, t], hs)
+        prev = cur
+    return y, hs
+
+
+@pytest.mark.parametrize("m", [1, 2, 4])
+def test_ssd3_serial_equals_recurrent_and_trapezoid(m):
+    d = _m3_inputs(7, b=2, l=19, m=m, h=3, p=4, n=6)
+    args = (d["v"], d["da"], d["B"], d["C"], d["gamma"], d["scale"], d["h0"])
+    ys, hs = oracle.ssd3(*args, chunk=4)
+    yr, hr = oracle.ssd3(*args, form="recurrent")
+    np.testing.assert_allclose(ys, yr, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(hs, hr, rtol=1e-6, atol=1e-6)
+    # the merged (single-SSD) accumulator h'_t = h_t + (1-lam_{t+1}) dt_{t+1} sum B_t v_t
+    # so with zero initial state it must reproduce the explicit trapezoid outputs
+    d0 = dict(d, h0=np.zeros_like(d["h0"]))
+    y0, _ = oracle.ssd3(d0["v"], d0["da"], d0["B"], d0["C"], d0["gamma"], d0["scale"], d0["h0"], chunk=5)
+    yt, _ = _trapezoid_loop(d0, d0["h0"])
+    np.testing.assert_allclose(y0, yt, rtol=1e-5, atol=1e-6)
+
+
+def test_ssd3_lambda_one_is_mamba2():
+    """lam = 1 removes the beta term: gamma = scale = dt and the single-SSD is
+    the Mamba-2 SSD without D (src/mamba3/mamba3.rs:28)."""
+    d = _m3_inputs(8, b=1, l=21, m=1, h=2, p=4, n=5, lam=1.0)
+    y3, h3 = oracle.ssd3(d["v"], d["da"], d["B"], d["C"], d["gamma"], d["scale"], d["h0"], chunk=8)
+    x = d["v"][:, :, 0]
+    Bm = d["B"][:, :, 0]
+    Cm = d["C"][:, :, 0]
+    y2, h2 = oracle.ssd2(x, d["dt"].astype(np.float32), d["A"].astype(np.float32), Bm, Cm, None, d["h0"], chunk=8)
+    np.testing.assert_allclose(y3[:, :, 0], y2, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(h3, h2, rtol=1e-5, atol=1e-6)

@@ -1,0 +1,125 @@
+"""Mamba-2 SSD: libmamba_hip.so (through the C ABI) vs the CPU oracle.
+
+Tolerances: f32 I/O rtol 1e-4 (with a small atol
+for values near zero); bf16 inputs with f32 accumulation: rtol 2e-2 and
+atol 1e-2 on y; final states are compared in every case.  The oracle is fed
+exactly the bf16-rounded inputs the GPU sees.
+"""
+
+import numpy as np
+import pytest
+
+from inputs import bf16_round, ssd2_inputs, ssd2_test_inputs
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = dict(rtol=1e-4, atol=1e-5)
+BF16_TOL = dict(rtol=2e-2, atol=1e-2)
+
+
+def _run_gpu(inp, chunk, dtype, generic=False, dt_layout="blh", per_head=False):
+    import torch
+    import mamba_hip
+    dev = torch.device("cuda:0")
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    x = torch.from_numpy(inp["x"]).to(dev, tdt)
+    Bm = torch.from_numpy(inp["B"]).to(dev, tdt)
+    Cm = torch.from_numpy(inp["C"]).to(dev, tdt)
+    if per_head:
+        h = x.shape[2]
+        g = Bm.shape[2]
+        Bm = Bm.repeat_interleave(h // g, dim=2)
+        Cm = Cm.repeat_interleave(h // g, dim=2)
+    dt = torch.from_numpy(inp["dt"]).to(dev)
+    if dt_layout == "bhl":  # the reference seam's dt_bhnl layout, as a strided view
+        dt = dt.permute(0, 2, 1).contiguous().permute(0, 2, 1)
+    A = torch.from_numpy(inp["A"]).to(dev)
+    D = None if inp["D"] is None else torch.from_numpy(inp["D"]).to(dev)
+    h0 = None if inp["h0"] is None else torch.from_numpy(inp["h0"]).to(dev)
+    y, hT = mamba_hip.ssd2_fwd(x, dt, A, Bm, Cm, D, h0, chunk_len=chunk, generic=generic)
+    torch.cuda.synchronize()
+    return y.float().cpu().numpy(), hT.cpu().numpy()
+
+
+def _oracle(inp, chunk, dtype):
+    import oracle
+    x, B, C = inp["x"], inp["B"], inp["C"]
+    if dtype == "bf16":
+        x, B, C = bf16_round(x), bf16_round(B), bf16_round(C)
+    return oracle.ssd2(x, inp["dt"], inp["A"], B, C, inp["D"], inp["h0"], chunk=chunk)
+
+
+CASES = [
+    # (b, l, h, p, g, n, chunk)
+    (2, 512, 8, 64, 1, 64, 64),     # config 0
+    (2, 37, 4, 8, 2, 8, 8),         # ragged tail, GQA 2 groups
+    (1, 1, 2, 16, 1, 16, 64),       # single token
+    (2, 300, 4, 64, 1, 128, 96),    # reference optimal chunk (96) for r=128,p=64, ragged
+    (1, 256, 4, 32, 4, 32, 256),    # per-group == per-head, one chunk
+    (3, 130, 6, 16, 3, 24, 32),     # odd dims
+]
+
+
+@pytest.mark.parametrize("generic", [True, False])
+@pytest.mark.parametrize("case", CASES)
+def test_ssd2_f32(case, generic):
+    b, l, h, p, g, n, q = case
+    inp = ssd2_inputs(seed=hash(case) % 1000, b=b, l=l, h=h, p=p, g=g, n=n, h0=True)
+    y, hT = _run_gpu(inp, q, "f32", generic=generic)
+    yr, hr = _oracle(inp, q, "f32")
+    np.testing.assert_allclose(y, yr, **F32_TOL)
+    np.testing.assert_allclose(hT, hr, **F32_TOL)
+
+
+@pytest.mark.parametrize("generic", [True, False])
+@pytest.mark.parametrize("case", CASES)
+def test_ssd2_bf16(case, generic):
+    b, l, h, p, g, n, q = case
+    inp = ssd2_inputs(seed=7 + hash(case) % 1000, b=b, l=l, h=h, p=p, g=g, n=n, h0=True)
+    y, hT = _run_gpu(inp, q, "bf16", generic=generic)
+    yr, hr = _oracle(inp, q, "bf16")
+    np.testing.assert_allclose(y, yr, **BF16_TOL)
+    np.testing.assert_allclose(hT, hr, **BF16_TOL)
+
+
+def test_ssd2_reference_test_distribution():
+    """The reference's own agreement-test shapes and distributions
+    (src/mamba2/ssd/ssd_path/tests.rs:33-67, 184-336)."""
+    for (b, n_, l_, h, p, r) in [(2, 3, 4, 2, 8, 8), (2, 3, 4, 4, 8, 8), (2, 1, 4, 2, 8, 8)]:
+        inp = ssd2_test_inputs(seed=11, b=b, l=n_ * l_, h=h, p=p, g=h, n=r)
+        y, hT = _run_gpu(inp, l_, "f32")
+        yr, hr = _oracle(inp, l_, "f32")
+        np.testing.assert_allclose(y, yr, rtol=1e-4, atol=1e-4)
+        np.testing.assert_allclose(hT, hr, rtol=1e-4, atol=1e-4)
+
+
+def test_ssd2_seam_layouts():
+    """The Mamba2BackendExt seam passes dt as [b,h,n,l] and per-head B/C
+    (serial_recalculated.rs:48; mamba2.rs:733-734): same result."""
+    inp = ssd2_inputs(seed=3, b=2, l=256, h=8, p=64, g=1, n=64, h0=True)
+    y0, h0 = _run_gpu(inp, 64, "f32")
+    y1, h1 = _run_gpu(inp, 64, "f32", dt_layout="bhl", per_head=True)
+    np.testing.assert_allclose(y1, y0, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(h1, h0, rtol=1e-5, atol=1e-6)
+
+
+def test_ssd2_golden_fixture():
+    import os
+    path = os.path.join(os.path.dirname(__file__), "golden", "ssd2_cfg0_small.npz")
+    f = np.load(path)
+    inp = dict(x=f["x"], dt=f["dt"], A=f["A"], B=f["B"], C=f["C"], D=f["D"], h0=f["h0"])
+    y, hT = _run_gpu(inp, int(f["chunk"]), "f32")
+    np.testing.assert_allclose(y, f["y"], **F32_TOL)
+    np.testing.assert_allclose(hT, f["final_state"], **F32_TOL)
+
+
+def test_ssd2_invalid_args_rejected():
+    import torch
+    import mamba_hip
+    dev = torch.device("cuda:0")
+    x = torch.zeros(1, 8, 3, 4, device=dev)
+    dt = torch.zeros(1, 8, 3, device=dev)
+    A = torch.zeros(3, device=dev)
+    Bm = torch.zeros(1, 8, 2, 4, device=dev)  # 3 heads not a multiple of 2 groups
+    with pytest.raises(mamba_hip.MambaHipError, match="ngroups"):
+        mamba_hip.ssd2_fwd(x, dt, A, Bm, Bm, chunk_len=4)
