@@ -1,0 +1,181 @@
+"""Benchmark of the MI355X SSM hot path (one GPU).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload ssd2]
+                    [--no-cpu-baseline]
+
+A "step" is one pass of the hot path over one batch of synthetic input that is
+already resident in HBM.  The default workload is BASELINE.json configs[1]:
+the Mamba-2 2.7B-shaped SSD prefill (batch 8 x 4096 tokens, 80 heads x 64,
+d_state 128, one group, chunk 256, bf16 x/B/C/y, f32 dt/A/D and f32 state),
+run through the C ABI (mamba_ssd2_fwd) exactly as a caller would.
+
+Prints ONE JSON line.  `value` is whole-job tokens/s over K timed steps
+(bracketed by torch.cuda.synchronize()).  `roofline` is computed for the
+dominant kernel (the fused chunk-scan kernel): algorithmic HBM bytes of one
+call divided by that kernel's mean duration, measured with HIP events recorded
+by the library around that kernel on the launch stream.  `cpu_baseline` times
+the CPU restatement of the reference algorithm (oracle/, f32, OpenMP) on a
+bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "burn-mamba_amd"), os.path.join(ROOT, "tests")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, published
+BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA, published
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------- workloads --
+
+SSD2_CFG1 = dict(batch=8, seqlen=4096, nheads=80, headdim=64, dstate=128, ngroups=1, chunk=256)
+
+
+def ssd2_algorithmic(cfg):
+    """Compulsory HBM bytes and causal-exact FLOPs of one SSD forward:
+    x, y bf16; dt f32; B, C bf16 (per group); final state f32 (zero initial
+    state is not read); A, D f32.  FLOPs: per token H*(Q*P + 4*P*N) + G*Q*N."""
+    b, l, h, p, n, g, q = (cfg[k] for k in ("batch", "seqlen", "nheads", "headdim", "dstate",
+                                             "ngroups", "chunk"))
+    tok = b * l
+    bytes_ = tok * (h * p * (2 + 2) + h * 4 + 2 * g * n * 2) + b * h * p * n * 4 + 2 * h * 4
+    flops = tok * (h * (q * p + 4 * p * n) + g * q * n)
+    return bytes_, flops
+
+
+def make_ssd2_inputs(cfg, dev, seed=0):
+    """BASELINE.json configs[1] distributions, generated on the device:
+    x~N(0,1); dt = softplus(N(0,1) + b_h) with b_h = softplus^-1(exp(U(ln1e-3, ln0.1)));
+    A = -exp(U(ln1, ln16)); B, C ~ N(0,1)/sqrt(N); D ~ N(0,1)."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    b, l, h, p, n, G = (cfg[k] for k in ("batch", "seqlen", "nheads", "headdim", "dstate", "ngroups"))
+    x = torch.randn((b, l, h, p), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    dt_target = torch.exp(torch.empty(h, device=dev).uniform_(
+        float(torch.log(torch.tensor(1e-3))), float(torch.log(torch.tensor(0.1))), generator=g))
+    bias = dt_target + torch.log(-torch.expm1(-dt_target))
+    dt = torch.nn.functional.softplus(torch.randn((b, l, h), generator=g, device=dev) + bias)
+    A = -torch.exp(torch.empty(h, device=dev).uniform_(0.0, float(torch.log(torch.tensor(16.0))),
+                                                       generator=g))
+    Bm = (torch.randn((b, l, G, n), generator=g, device=dev) / n ** 0.5).to(torch.bfloat16)
+    Cm = (torch.randn((b, l, G, n), generator=g, device=dev) / n ** 0.5).to(torch.bfloat16)
+    D = torch.randn(h, generator=g, device=dev)
+    return dict(x=x, dt=dt.contiguous(), A=A.contiguous(), B=Bm, C=Cm, D=D)
+
+
+def cpu_baseline_ssd2(cfg, seed=0):
+    """The f32 CPU restatement of the reference's serial K1-K5 SSD
+    (oracle/, OpenMP over (batch, head)) on the whole workload (all
+    sequences, full length, all heads): about 10 s on 16 host cores."""
+    import numpy as np
+
+    import oracle
+    from inputs import ssd2_inputs
+    oracle.build()
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    inp = ssd2_inputs(seed, b=cfg["batch"], l=cfg["seqlen"], h=cfg["nheads"], p=cfg["headdim"],
+                      g=cfg["ngroups"], n=cfg["dstate"])
+    t0 = time.perf_counter()
+    oracle.ssd2(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"], None,
+                chunk=cfg["chunk"], form="serial", prec=32)
+    el = time.perf_counter() - t0
+    del np
+    return {"value": cfg["batch"] * cfg["seqlen"] / el, "unit": "tokens/s", "cores": threads,
+            "kind": "port",
+            "sample": f"the full workload ({cfg['batch']} x {cfg['seqlen']} tokens, {cfg['nheads']} heads), "
+                      f"f32 serial K1-K5 restatement of the reference, {el:.2f} s"}
+
+
+def bench_ssd2(args):
+    import torch
+
+    import mamba_hip
+    cfg = dict(SSD2_CFG1)
+    dev = torch.device("cuda:0")
+    inp = make_ssd2_inputs(cfg, dev)
+    b, l, h, p = inp["x"].shape
+    y = torch.empty((b, l, h, p), dtype=torch.bfloat16, device=dev)
+    hT = torch.empty((b, h, p, cfg["dstate"]), dtype=torch.float32, device=dev)
+
+    def step(events=None):
+        mamba_hip.ssd2_fwd(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"], None,
+                           chunk_len=cfg["chunk"], y=y, final_state=hT, events=events)
+
+    log(f"inputs ready {tuple(inp['x'].shape)}; warmup {args.warmup}")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} steps")
+    # whole-step timing: K back-to-back calls, synchronised on both sides
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    ms_per_step = el * 1e3 / args.steps
+    # dominant-kernel timing: HIP events recorded by the library around it
+    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+             for _ in range(args.steps)]
+    for ev in pairs:
+        step(events=ev)
+    torch.cuda.synchronize()
+    kern_ms = sum(a.elapsed_time(b_) for a, b_ in pairs) / len(pairs)
+    log(f"ms/step {ms_per_step:.3f}, dominant kernel {kern_ms:.3f} ms")
+    nbytes, flops = ssd2_algorithmic(cfg)
+    tokens = cfg["batch"] * cfg["seqlen"]
+    achieved = nbytes / (kern_ms * 1e-3) / 1e9
+    out = {
+        "metric": "SSD prefill tokens/s (Mamba-2 2.7B layer SSD, B=8 L=4096) + % HBM roofline",
+        "value": tokens / (ms_per_step * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (BASELINE.json configs[1] distributions, seed 0)",
+        "config": {"workload": "mamba2_ssd_prefill_cfg1", **cfg, "io": "x/B/C/y bf16, dt/A/D/state f32",
+                   "entry": "mamba_ssd2_fwd"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "kernel_ms": kern_ms, "algorithmic_bytes": nbytes,
+                     "mfma_tflops": flops / (kern_ms * 1e-3) / 1e12,
+                     "mfma_frac": flops / (kern_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS},
+    }
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="ssd2", choices=["ssd2"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the hot path shards by batch/head with no communication; see DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+    out = bench_ssd2(args)
+    if not args.no_cpu_baseline:
+        log("cpu baseline")
+        out["cpu_baseline"] = cpu_baseline_ssd2(SSD2_CFG1)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -21,10 +21,13 @@ struct Ssd2Params {
 
 int ssd2_make_params(const mamba_ssd2_args* a, Ssd2Params* out);
 size_t ssd2_generic_workspace(const Ssd2Params& p);
-int ssd2_generic_launch(const Ssd2Params& p, void* ws, hipStream_t stream);
+// ev0/ev1 (nullable hipEvent_t) are recorded around the dominant kernel.
+int ssd2_generic_launch(const Ssd2Params& p, void* ws, hipStream_t stream, hipEvent_t ev0 = nullptr,
+                        hipEvent_t ev1 = nullptr);
 
 bool ssd2_mfma_supported(const Ssd2Params& p);
 size_t ssd2_mfma_workspace(const Ssd2Params& p);
-int ssd2_mfma_launch(const Ssd2Params& p, void* ws, hipStream_t stream);
+int ssd2_mfma_launch(const Ssd2Params& p, void* ws, hipStream_t stream, hipEvent_t ev0 = nullptr,
+                     hipEvent_t ev1 = nullptr);
 
 }  // namespace mamba

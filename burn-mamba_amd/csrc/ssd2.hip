@@ -200,7 +200,8 @@ size_t ssd2_generic_workspace(const Ssd2Params& p) {
     return align_up(states, 256) + align_up(daend, 256);
 }
 
-int ssd2_generic_launch(const Ssd2Params& p, void* ws, hipStream_t stream) {
+int ssd2_generic_launch(const Ssd2Params& p, void* ws, hipStream_t stream, hipEvent_t ev0,
+                        hipEvent_t ev1) {
     float* states = (float*)ws;
     float* daend = (float*)((char*)ws + align_up((size_t)p.nb * p.nch * p.H * p.P * p.N * sizeof(float), 256));
     dim3 grid(p.H, p.nch, p.nb);
@@ -216,12 +217,14 @@ int ssd2_generic_launch(const Ssd2Params& p, void* ws, hipStream_t stream) {
     dim3 gpass(ceil_div(p.P * p.N, 256), p.H, p.nb);
     hipLaunchKernelGGL(ssd2_state_pass_generic, gpass, dim3(256), 0, stream, p, states, daend);
     MAMBA_CHECK_LAUNCH();
+    if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, stream));
     if (p.io_dtype == MAMBA_BF16) {
         hipLaunchKernelGGL(ssd2_chunk_scan_generic<bf16_t>, grid, dim3(256), sm_scan, stream, p, states);
     } else {
         hipLaunchKernelGGL(ssd2_chunk_scan_generic<float>, grid, dim3(256), sm_scan, stream, p, states);
     }
     MAMBA_CHECK_LAUNCH();
+    if (ev1) MAMBA_CHECK_HIP(hipEventRecord(ev1, stream));
     return MAMBA_OK;
 }
 
@@ -276,8 +279,8 @@ extern "C" int mamba_ssd2_fwd_generic(const mamba_ssd2_args* a, void* ws, size_t
     return ssd2_generic_launch(p, ws, (hipStream_t)stream);
 }
 
-extern "C" int mamba_ssd2_fwd(const mamba_ssd2_args* a, void* ws, size_t ws_bytes,
-                              mamba_stream_t stream) {
+static int ssd2_dispatch(const mamba_ssd2_args* a, void* ws, size_t ws_bytes, hipStream_t stream,
+                         hipEvent_t ev0, hipEvent_t ev1) {
     Ssd2Params p;
     int st = ssd2_make_params(a, &p);
     if (st != MAMBA_OK) return st;
@@ -286,11 +289,26 @@ extern "C" int mamba_ssd2_fwd(const mamba_ssd2_args* a, void* ws, size_t ws_byte
             set_error("mamba_ssd2_fwd: workspace missing or too small");
             return MAMBA_ERR_WORKSPACE;
         }
-        return ssd2_mfma_launch(p, ws, (hipStream_t)stream);
+        return ssd2_mfma_launch(p, ws, stream, ev0, ev1);
     }
     if (ws == nullptr || ws_bytes < ssd2_generic_workspace(p)) {
         set_error("mamba_ssd2_fwd: workspace missing or too small");
         return MAMBA_ERR_WORKSPACE;
     }
-    return ssd2_generic_launch(p, ws, (hipStream_t)stream);
+    return ssd2_generic_launch(p, ws, stream, ev0, ev1);
+}
+
+extern "C" int mamba_ssd2_fwd(const mamba_ssd2_args* a, void* ws, size_t ws_bytes,
+                              mamba_stream_t stream) {
+    return ssd2_dispatch(a, ws, ws_bytes, (hipStream_t)stream, nullptr, nullptr);
+}
+
+extern "C" int mamba_ssd2_fwd_timed(const mamba_ssd2_args* a, void* ws, size_t ws_bytes,
+                                    mamba_stream_t stream, void* ev_start, void* ev_stop) {
+    if (ev_start == nullptr || ev_stop == nullptr) {
+        set_error("mamba_ssd2_fwd_timed: both events are required");
+        return MAMBA_ERR_INVALID_ARG;
+    }
+    return ssd2_dispatch(a, ws, ws_bytes, (hipStream_t)stream, (hipEvent_t)ev_start,
+                         (hipEvent_t)ev_stop);
 }

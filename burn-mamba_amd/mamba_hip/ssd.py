@@ -59,7 +59,7 @@ def _check_inner(t: torch.Tensor, name: str):
 
 
 def ssd2_fwd(x, dt, A, B, C, D=None, initial_state=None, init_state_hpr=None, chunk_len=None,
-             y=None, final_state=None, generic=False):
+             y=None, final_state=None, generic=False, events=None):
     """Mamba-2 SSD forward through ``mamba_ssd2_fwd``.
 
     x[b,l,h,p] (f32|bf16)  dt[b,l,h] f32  A[h] f32  B,C[b,l,g,n] (dtype of x)
@@ -98,10 +98,26 @@ def ssd2_fwd(x, dt, A, B, C, D=None, initial_state=None, init_state_hpr=None, ch
     L = _lib.lib()
     nbytes = L.mamba_ssd2_workspace_size(ctypes.byref(a))
     ws = workspace(x.device, nbytes)
-    fn = L.mamba_ssd2_fwd_generic if generic else L.mamba_ssd2_fwd
-    check(fn(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(x.device)),
-          "mamba_ssd2_fwd")
+    wsp, st = ctypes.c_void_p(ws.data_ptr()), _stream(x.device)
+    if events is not None:
+        e0, e1 = _raw_events(events, x.device)
+        check(L.mamba_ssd2_fwd_timed(ctypes.byref(a), wsp, ws.numel(), st, e0, e1),
+              "mamba_ssd2_fwd_timed")
+    else:
+        fn = L.mamba_ssd2_fwd_generic if generic else L.mamba_ssd2_fwd
+        check(fn(ctypes.byref(a), wsp, ws.numel(), st), "mamba_ssd2_fwd")
     return y, final_state
+
+
+def _raw_events(events, device):
+    """hipEvent_t handles of a torch.cuda.Event pair (torch creates the HIP
+    event lazily on first record, so record once if needed)."""
+    out = []
+    for e in events:
+        if e.cuda_event == 0:
+            e.record(torch.cuda.current_stream(device))
+        out.append(ctypes.c_void_p(e.cuda_event))
+    return out
 
 
 class Mamba2SsdPath:

@@ -101,6 +101,14 @@ int mamba_ssd2_fwd(const mamba_ssd2_args* args, void* workspace, size_t workspac
 int mamba_ssd2_fwd_generic(const mamba_ssd2_args* args, void* workspace, size_t workspace_bytes,
                            mamba_stream_t stream);
 
+/* Same as mamba_ssd2_fwd, and additionally records the caller's HIP events   */
+/* (hipEvent_t, already created) on `stream` immediately before and after the  */
+/* dominant kernel of the call (the chunk-scan kernel), so a benchmark can     */
+/* time that kernel alone with hipEventElapsedTime.  No counterpart in the    */
+/* reference (its benches time whole blocks, benches/layer.rs:176-187).        */
+int mamba_ssd2_fwd_timed(const mamba_ssd2_args* args, void* workspace, size_t workspace_bytes,
+                         mamba_stream_t stream, void* event_start, void* event_stop);
+
 #ifdef __cplusplus
 }
 #endif
