@@ -1,8 +1,8 @@
 // Mamba-2 chunked SSD forward for gfx950.
 //
 // Two code paths behind one entry point (mamba_ssd2_fwd):
-//   * the MFMA path (ssd2_mfma.hip) for headdim 64 and dstate 64/128 with
-//     chunk lengths 64/128/256, bf16 or f32 I/O;
+//   * the MFMA path (ssd2_mfma.hip) for bf16 I/O, headdim 64, dstate 64/128
+//     and chunk lengths that are multiples of 32 up to 256;
 //   * the shape-generic path below for everything else: three SIMT kernels
 //     (chunk state, state passing, chunk scan) with f32 arithmetic.
 //
@@ -265,6 +265,12 @@ extern "C" size_t mamba_ssd2_workspace_size(const mamba_ssd2_args* a) {
     size_t ws = ssd2_generic_workspace(p);
     const size_t fast = ssd2_mfma_workspace(p);
     return ws > fast ? ws : fast;
+}
+
+extern "C" int mamba_ssd2_fast_path(const mamba_ssd2_args* a) {
+    Ssd2Params p;
+    if (ssd2_make_params(a, &p) != MAMBA_OK) return -1;
+    return ssd2_mfma_supported(p) ? 1 : 0;
 }
 
 extern "C" int mamba_ssd2_fwd_generic(const mamba_ssd2_args* a, void* ws, size_t ws_bytes,

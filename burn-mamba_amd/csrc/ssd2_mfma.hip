@@ -1,10 +1,599 @@
-// Mamba-2 SSD MFMA path (placeholder until the gfx950 kernel lands).
+// Mamba-2 chunked SSD forward, gfx950 MFMA path (bf16 in/out, f32 state).
+//
+// Reference: src/mamba2/ssd/serial.rs:34-506 (K1 cumsum, K2 C.B^T, K3 chunk
+// state, K4 state passing, K5 chunk scan) and the trait default body
+// src/mamba2/ssd/serial_recalculated/serial_recalculated.rs:98-155.
+//
+// Two launches per call:
+//   1. ssd2_cb_mfma / ssd2_bt_transpose (per batch, chunk, group): the
+//      group-shared C_c.B_c^T matrix in f32 (K2, computed once per group
+//      instead of once per head) and a time-major copy of B_c (so the chunk
+//      state contraction over time can read B directly as an MFMA operand).
+//   2. ssd2_scan_mfma: one workgroup per (batch, head[, half of headdim])
+//      walks the chunks in order.  The running state h[p, n] lives in MFMA
+//      accumulators for the whole sequence (K4 needs no HBM round trip); per
+//      chunk it computes K1 in registers/LDS, then
+//        y = exp(cs_i) C_i . h_in + sum_{j<=i} (C_i.B_j) dt_j exp(cs_i-cs_j) x_j + D x_i
+//        h_out = exp(cs_end) h_in + sum_j x_j^T (B_j dt_j exp(cs_end - cs_j))
+//      with every contraction on v_mfma_f32_32x32x16_bf16.  x is read from
+//      HBM once (staged time-major in LDS), y is written once.
+//
+// MFMA 32x32x16 operand/result layout (lane l, r = l % 32, half = l / 32):
+//   A[m][k]: lane holds row m = r, k = 8*half .. 8*half+7
+//   B[k][n]: lane holds col n = r, k = 8*half .. 8*half+7
+//   D[m][n]: lane holds col n = r, rows 8*(v/4) + 4*half + (v%4), v = 0..15
+// (Any permutation of k that A and B share leaves the product unchanged; the
+// row/col mappings and the D layout are what the indexing below relies on.)
+
+#include <cstdlib>
+
 #include "ssd2.h"
 
 namespace mamba {
-bool ssd2_mfma_supported(const Ssd2Params&) { return false; }
-size_t ssd2_mfma_workspace(const Ssd2Params&) { return 0; }
-int ssd2_mfma_launch(const Ssd2Params&, void*, hipStream_t, hipEvent_t, hipEvent_t) {
-    return MAMBA_ERR_UNSUPPORTED;
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kMaxQ = 256;
+
+__device__ __forceinline__ f32x16_t mfma32x32x16(bf16x8_t a, bf16x8_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
+
+__device__ __forceinline__ uint4 ld16(const void* ptr, bool ok) {
+    return ok ? *(const uint4*)ptr : make_uint4(0u, 0u, 0u, 0u);
+}
+
+// 8 packed bf16 (one uint4) -> 8 floats
+__device__ __forceinline__ void unpack8(uint4 v, float* f) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        f[2 * k] = __uint_as_float(w[k] << 16);
+        f[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+    }
+}
+
+__device__ __forceinline__ bf16x8_t pack8(const float* f) {
+    bf16x8_t r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = (__bf16)f[e];
+    return r;
+}
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
+    return __builtin_bit_cast(bf16x8_t, v);
+}
+
+__device__ __forceinline__ f32x16_t zero16() {
+    f32x16_t z;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) z[v] = 0.f;
+    return z;
+}
+
+// ------------------------------------------------ per-group operand prep --
+// Per (batch, chunk, group) -- shared by every head of the group -- write the
+// MFMA B operands of the scan kernel in fragment order, so that each wave
+// load there is one contiguous 1 KB read:
+//   cbf[it][ks][plane][lane][4] f32 : (C.B^T)[i = 32 it + lane%32][j = 16 ks + 8 (lane/32) + 4 plane + e]
+//   cf [it][kn][lane][8]     bf16   : C[i = 32 it + lane%32][n = 16 kn + 8 (lane/32) + e]
+//   bf [nt][ks][lane][8]     bf16   : B[j = 16 ks + 8 (lane/32) + e][n = 32 nt + lane%32]
+// Positions past seqlen read as zero.  Only the causal (ks <= 2 it + 1)
+// fragments of cbf are written (K2, src/mamba2/ssd/serial.rs:170-185).
+template <int N, int Q>
+__global__ __launch_bounds__(256) void ssd2_prep_mfma(Ssd2Params p, float* cbf, bf16_t* cf, bf16_t* bfr) {
+    constexpr int T = Q / 32, NK = N / 16, KS = Q / 16, NTN = N / 32;
+    constexpr int NTILE = T * (T + 1) / 2;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 31, half = lane >> 5;
+    const int s = blockIdx.x, S = gridDim.x;
+    const int cg = blockIdx.y, c = cg / p.G, g = cg % p.G, b = blockIdx.z;
+    const int64_t grp = ((int64_t)b * p.nch + c) * p.G + g;
+    const bf16_t* Cg = (const bf16_t*)p.Cm + (int64_t)b * p.C_sb + (int64_t)g * p.C_sg;
+    const bf16_t* Bg = (const bf16_t*)p.Bm + (int64_t)b * p.B_sb + (int64_t)g * p.B_sg;
+    // (C.B^T)^T tiles: D[j][i] = sum_n B[j][n] C[i][n]; the lane then holds
+    // column i = 32 it + r at rows j = 32 jt + 8 q + 4 half + u (v = 4 q + u)
+    float* cbase = cbf + grp * Q * Q;
+    for (int tile = s + S * wave; tile < NTILE; tile += 4 * S) {
+        int it = 0;
+        while ((it + 1) * (it + 2) / 2 <= tile) ++it;
+        const int jt = tile - it * (it + 1) / 2;
+        const int tj = c * Q + jt * 32 + r, ti = c * Q + it * 32 + r;
+        f32x16_t acc = zero16();
+#pragma unroll
+        for (int kn = 0; kn < NK; ++kn) {
+            const int n0 = kn * 16 + 8 * half;
+            const bf16x8_t a = as_bf16x8(ld16(Bg + (int64_t)tj * p.B_sl + n0, tj < p.L));
+            const bf16x8_t bb = as_bf16x8(ld16(Cg + (int64_t)ti * p.C_sl + n0, ti < p.L));
+            acc = mfma32x32x16(a, bb, acc);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int ks = 2 * jt + (q >> 1), lp = r + 32 * (q & 1);
+            const float4 val = make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
+            *(float4*)(cbase + (((int64_t)(it * KS + ks) * 2 + half) * 64 + lp) * 4) = val;
+        }
+    }
+    bf16_t* cbase2 = cf + grp * (int64_t)Q * N;
+    for (int f = s + S * wave; f < T * NK; f += 4 * S) {
+        const int it = f / NK, kn = f % NK;
+        const int t = c * Q + it * 32 + r;
+        *(uint4*)(cbase2 + ((int64_t)f * 64 + lane) * 8) =
+            ld16(Cg + (int64_t)t * p.C_sl + kn * 16 + 8 * half, t < p.L);
+    }
+    bf16_t* bbase = bfr + grp * (int64_t)Q * N;
+    for (int f = s + S * wave; f < NTN * KS; f += 4 * S) {
+        const int nt = f / KS, ks = f % KS;
+        const int n = nt * 32 + r;
+        uint32_t w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int t0 = c * Q + ks * 16 + 8 * half + 2 * k;
+            const uint32_t lo = t0 < p.L ? Bg[(int64_t)t0 * p.B_sl + n] : 0u;
+            const uint32_t hi = t0 + 1 < p.L ? Bg[(int64_t)(t0 + 1) * p.B_sl + n] : 0u;
+            w[k] = lo | (hi << 16);
+        }
+        *(uint4*)(bbase + ((int64_t)f * 64 + lane) * 8) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
+// Owner wave of i-tile `it` (snake order, balances the causal triangle).
+__device__ __forceinline__ int itile_owner(int it) {
+    return ((it >> 2) & 1) ? 3 - (it & 3) : (it & 3);
+}
+
+// ----------------------------------------------- K1 + K3 + K4 + K5 fused --
+// One workgroup (4 waves) per (batch, head[, headdim half]); chunks in order.
+// N = dstate, Q = chunk length (multiple of 32, <= 256), PT = 32-wide headdim
+// tiles per workgroup (2: the whole headdim 64; 1: one half).
+//
+// Outputs are computed transposed, y^T[p, i] (i = time along MFMA columns),
+// so every per-time factor is a per-lane scalar and the four consecutive
+// headdim values a lane holds are stored as one 8-byte write.  For output
+// time i in 32-row block it (r0 = 32*it), with e_i = exp(cs_i - cs_r0) <= 1:
+//   y_i = e_i [ exp(cs_r0) (h_in . C_i) + sum_{j < r0} x_j (C_i.B_j) f_it[j] ]
+//         + sum_{r0 <= j <= i} x_j (C_i.B_j) dt_j exp(cs_i - cs_j) + D x_i
+// where f_it[j] = dt_j exp(cs_r0 - cs_j) <= dt_j is tabulated per chunk in
+// LDS (s_f).  Every factor is <= 1, so nothing can overflow; the diagonal
+// block uses the exact exponent and carries D on its diagonal.
+template <int N, int Q, int PT>
+__global__ __launch_bounds__(256, 2) void ssd2_scan_mfma(Ssd2Params p, const float* cbf,
+                                                         const bf16_t* cf, const bf16_t* bfr) {
+    constexpr int T = Q / 32;                 // i-tiles per chunk
+    constexpr int NTN = N / 32;               // n tiles of the state
+    constexpr int NST = PT * NTN;             // state tiles per workgroup
+    constexpr int SPW = NST >= 4 ? NST / 4 : 1;  // state tiles per wave
+    constexpr int XP = Q + 8;                 // s_xT row pitch (bf16)
+    constexpr int HP = N + 8;                 // s_h row pitch (bf16)
+    constexpr int PV = PT * 4;                // 8-wide headdim vectors per time row
+    constexpr int XITEMS = (Q / 2) * PV;      // x staging items (2 time rows each)
+    constexpr int XPT = (XITEMS + 255) / 256; // items per thread
+    constexpr int NK = N / 16, KS = Q / 16;
+    constexpr int YP = PT * 32 + 8;           // s_y row pitch (bf16)
+    __shared__ __align__(16) float s_cs2[Q];
+    __shared__ __align__(16) float s_dt[Q];
+    __shared__ __align__(16) float s_w[Q];
+    __shared__ float s_red[4];
+    __shared__ __align__(16) float s_f[T > 1 ? T - 1 : 1][Q];
+    __shared__ __align__(16) bf16_t s_xT[PT * 32][XP];
+    __shared__ __align__(16) bf16_t s_h[PT * 32][HP];
+    __shared__ __align__(16) bf16_t s_y[4][32][YP];  // per-wave y tile staging
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 31, half = lane >> 5;
+    // XCD-aware work mapping: consecutive work items (same batch, neighbouring
+    // heads, sharing B/C/CB) land on the same XCD and its L2.
+    constexpr int splits = 2 / PT;
+    const int nwg = p.nb * p.H * splits;
+    int w = blockIdx.x;
+    if ((nwg & 7) == 0) w = (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3);
+    const int ph = w % splits, h = (w / splits) % p.H, b = w / (splits * p.H);
+    const int g = h / (p.H / p.G);
+    const int p0 = ph * 32 * PT;
+    const float A2 = p.A[h] * kLog2e;
+    const float Dh = p.D ? p.D[h] : 0.f;
+
+    // state tiles owned by this wave
+    int st_pt[SPW], st_nt[SPW];
+    bool st_ok[SPW];
+#pragma unroll
+    for (int k = 0; k < SPW; ++k) {
+        const int s = wave + 4 * k;
+        st_ok[k] = s < NST;
+        st_pt[k] = s / NTN;
+        st_nt[k] = s % NTN;
+    }
+    f32x16_t hacc[SPW];
+    const int64_t hbase = ((int64_t)b * p.H + h) * 64 * N;
+#pragma unroll
+    for (int k = 0; k < SPW; ++k) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int pp = p0 + st_pt[k] * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+            const int n = st_nt[k] * 32 + r;
+            float val = 0.f;
+            if (st_ok[k]) {
+                if (p.h0) val = p.h0[hbase + pp * N + n];
+                if (p.init_hpr) val += p.init_hpr[(int64_t)h * 64 * N + pp * N + n];
+            }
+            hacc[k][v] = val;
+        }
+    }
+    // bf16 copy of the state: the A operand of h . C^T
+#pragma unroll
+    for (int k = 0; k < SPW; ++k)
+        if (st_ok[k])
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+                s_h[st_pt[k] * 32 + 8 * (v >> 2) + 4 * half + (v & 3)][st_nt[k] * 32 + r] =
+                    __builtin_bit_cast(bf16_t, (__bf16)hacc[k][v]);
+
+    const bf16_t* X = (const bf16_t*)p.x;
+    bf16_t* Y = (bf16_t*)p.y;
+    const bf16_t* xhead = X + (int64_t)b * p.x_sb + (int64_t)h * p.x_sh + p0;
+    const float* dthead = p.dt + (int64_t)b * p.dt_sb + (int64_t)h * p.dt_sh;
+    bf16_t* yhead = Y + (int64_t)b * p.y_sb + (int64_t)h * p.y_sh + p0;
+
+    // register prefetch of the next chunk's x rows and dt
+    uint4 xq[XPT][2];
+    float dtq = 0.f;
+    auto fetch = [&](int c) {
+#pragma unroll
+        for (int m = 0; m < XPT; ++m) {
+            const int item = threadIdx.x + 256 * m;
+            const int jp = item / PV, pv = item % PV;
+            const int t0 = c * Q + 2 * jp;
+            const bool ok = item < XITEMS;
+            xq[m][0] = ld16(xhead + (int64_t)t0 * p.x_sl + pv * 8, ok && t0 < p.L);
+            xq[m][1] = ld16(xhead + (int64_t)(t0 + 1) * p.x_sl + pv * 8, ok && t0 + 1 < p.L);
+        }
+        const int tt = c * Q + threadIdx.x;
+        dtq = (threadIdx.x < Q && tt < p.L) ? dthead[(int64_t)tt * p.dt_sl] : 0.f;
+    };
+    fetch(0);
+    // L2 warm-up of the next chunk's group operands: the H/G heads (x headdim
+    // splits) of a group share them and sit on one XCD, so each workgroup
+    // touches one slice of the group's lines, one dword per line
+    constexpr int CB_LINES = 16 * T * (T + 1);  // causal C.B^T fragments
+    constexpr int FR_LINES = Q * N * 2 / 128;   // C or B fragments
+    constexpr int GRP_LINES = CB_LINES + 2 * FR_LINES;
+    const int nslice = (p.H / p.G) * splits;
+    const int slice = (h % (p.H / p.G)) * splits + ph;
+    const int pf_line = (int)(((int64_t)GRP_LINES * slice) / nslice) + threadIdx.x;
+    const bool pf_on = pf_line < (int)(((int64_t)GRP_LINES * (slice + 1)) / nslice);
+    int64_t pf_off = 0;  // byte offset of the line inside the group's block
+    if (pf_line < CB_LINES) {
+        int it = 0;
+        while (16 * (it + 1) * (it + 2) <= pf_line) ++it;
+        pf_off = ((int64_t)it * KS * 16 + (pf_line - 16 * it * (it + 1))) * 128;
+    } else if (pf_line < CB_LINES + FR_LINES) {
+        pf_off = (int64_t)(pf_line - CB_LINES) * 128;
+    } else {
+        pf_off = (int64_t)(pf_line - CB_LINES - FR_LINES) * 128;
+    }
+    const int pf_kind = pf_line < CB_LINES ? 0 : (pf_line < CB_LINES + FR_LINES ? 1 : 2);
+    uint32_t pf = 0u, pf_sink = 0u;
+
+    for (int c = 0; c < p.nch; ++c) {
+        // ---- commit prefetched x -> s_xT[p][j] (time-major) and K1 cumsum
+#pragma unroll
+        for (int m = 0; m < XPT; ++m) {
+            const int item = threadIdx.x + 256 * m;
+            if (item < XITEMS) {
+                const int jp = item / PV, pv = item % PV;
+                const uint32_t a0[4] = {xq[m][0].x, xq[m][0].y, xq[m][0].z, xq[m][0].w};
+                const uint32_t a1[4] = {xq[m][1].x, xq[m][1].y, xq[m][1].z, xq[m][1].w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    *(uint32_t*)&s_xT[pv * 8 + 2 * k][2 * jp] = (a0[k] & 0xffffu) | (a1[k] << 16);
+                    *(uint32_t*)&s_xT[pv * 8 + 2 * k + 1][2 * jp] =
+                        (a0[k] >> 16) | (a1[k] & 0xffff0000u);
+                }
+            }
+        }
+        {
+            const float dtv = dtq;
+            float v = wave_incl_scan(dtv * A2);
+            if (lane == 63) s_red[wave] = v;
+            __syncthreads();
+#pragma unroll
+            for (int k = 0; k < 3; ++k)
+                if (k < wave) v += s_red[k];
+            if (threadIdx.x < Q) {
+                s_cs2[threadIdx.x] = v;
+                s_dt[threadIdx.x] = dtv;
+            }
+        }
+        __syncthreads();
+        const float cs2_end = s_cs2[Q - 1];
+        // chunk-state weights dt_j exp(cs_end - cs_j) and the decay table
+        if (threadIdx.x < Q)
+            s_w[threadIdx.x] = s_dt[threadIdx.x] * __builtin_amdgcn_exp2f(cs2_end - s_cs2[threadIdx.x]);
+        for (int idx = threadIdx.x; idx < (T - 1) * Q; idx += 256) {
+            const int it = idx / Q + 1, j = idx % Q;
+            if (j < it * 32) s_f[it - 1][j] = s_dt[j] * __builtin_amdgcn_exp2f(s_cs2[it * 32] - s_cs2[j]);
+        }
+        __syncthreads();
+
+        pf_sink += pf;
+
+        // ---- K2 + K5: y^T for the i-tiles this wave owns
+        const int64_t grp = ((int64_t)b * p.nch + c) * p.G + g;
+        const float* cbg = cbf + grp * Q * Q + lane * 4;
+        const bf16_t* cfg = cf + grp * (int64_t)Q * N + lane * 8;
+#pragma unroll 1
+        for (int it = 0; it < T; ++it) {
+            if (itile_owner(it) != wave) continue;
+            const int il = it * 32 + r;  // this lane's output time (B-operand column)
+            // issue every global load of this tile before the first wait:
+            // the C fragments (inter-chunk term) and a 4-deep ring of CB fragments
+            uint4 craw[NK];
+#pragma unroll
+            for (int kn = 0; kn < NK; ++kn) craw[kn] = *(const uint4*)(cfg + (int64_t)(it * NK + kn) * 512);
+            const float* cbt = cbg + (int64_t)it * KS * 512;  // fragment (it, ks) at + ks * 512
+            const int nb = 2 * it;    // strictly-lower k-steps (even)
+            const int ntot = nb + 2;  // + the diagonal block
+            float4 ring[4][2];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (k < ntot) {
+                    ring[k][0] = *(const float4*)(cbt + k * 512);
+                    ring[k][1] = *(const float4*)(cbt + k * 512 + 256);
+                }
+            const float cs2_i = s_cs2[il];
+            const float cs2_r0 = s_cs2[it * 32];
+            f32x16_t yacc[PT];
+#pragma unroll
+            for (int pt = 0; pt < PT; ++pt) yacc[pt] = zero16();
+            // inter-chunk term h_in . C_i^T with raw C rows as the B operand
+#pragma unroll
+            for (int ks = 0; ks < NK; ++ks) {
+                const bf16x8_t bop = as_bf16x8(craw[ks]);
+#pragma unroll
+                for (int pt = 0; pt < PT; ++pt) {
+                    const bf16x8_t a = *(const bf16x8_t*)&s_h[pt * 32 + r][ks * 16 + 8 * half];
+                    yacc[pt] = mfma32x32x16(a, bop, yacc[pt]);
+                }
+            }
+            {
+                const float sc = __builtin_amdgcn_exp2f(cs2_r0);
+#pragma unroll
+                for (int pt = 0; pt < PT; ++pt)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) yacc[pt][v] *= sc;
+            }
+            // strictly-lower blocks: B operand (C_i.B_j) f_it[j]
+            for (int ks0 = 0; ks0 < nb; ks0 += 4) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int ks = ks0 + k;
+                    if (ks < nb) {
+                        const int j0 = ks * 16 + 8 * half;
+                        const float4 c0 = ring[k][0], c1 = ring[k][1];
+                        if (ks + 4 < ntot) {
+                            ring[k][0] = *(const float4*)(cbt + (ks + 4) * 512);
+                            ring[k][1] = *(const float4*)(cbt + (ks + 4) * 512 + 256);
+                        }
+                        const float4 f0 = *(const float4*)&s_f[it - 1][j0];
+                        const float4 f1 = *(const float4*)&s_f[it - 1][j0 + 4];
+                        const float m[8] = {c0.x * f0.x, c0.y * f0.y, c0.z * f0.z, c0.w * f0.w,
+                                            c1.x * f1.x, c1.y * f1.y, c1.z * f1.z, c1.w * f1.w};
+                        const bf16x8_t bop = pack8(m);
+#pragma unroll
+                        for (int pt = 0; pt < PT; ++pt) {
+                            const bf16x8_t a = *(const bf16x8_t*)&s_xT[pt * 32 + r][j0];
+                            yacc[pt] = mfma32x32x16(a, bop, yacc[pt]);
+                        }
+                    }
+                }
+            }
+            {
+                const float ei = __builtin_amdgcn_exp2f(cs2_i - cs2_r0);
+#pragma unroll
+                for (int pt = 0; pt < PT; ++pt)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) yacc[pt][v] *= ei;
+            }
+            // diagonal block, exact exponent, + D on the diagonal; its CB
+            // fragments sit in ring slots nb % 4 and nb % 4 + 1 (nb is even)
+            float4 dg[2][2];
+            if ((nb & 3) == 0) {
+                dg[0][0] = ring[0][0]; dg[0][1] = ring[0][1]; dg[1][0] = ring[1][0]; dg[1][1] = ring[1][1];
+            } else {
+                dg[0][0] = ring[2][0]; dg[0][1] = ring[2][1]; dg[1][0] = ring[3][0]; dg[1][1] = ring[3][1];
+            }
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                const int j0 = it * 32 + kk * 16 + 8 * half;
+                const float4 c0 = dg[kk][0], c1 = dg[kk][1];
+                const float4 d0 = *(const float4*)&s_dt[j0];
+                const float4 d1 = *(const float4*)&s_dt[j0 + 4];
+                const float4 s0 = *(const float4*)&s_cs2[j0];
+                const float4 s1 = *(const float4*)&s_cs2[j0 + 4];
+                const float cbv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+                const float dtv[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+                const float csv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+                float m[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int j = j0 + e;
+                    const float val = cbv[e] * dtv[e] * __builtin_amdgcn_exp2f(cs2_i - csv[e]);
+                    m[e] = (j < il) ? val : ((j == il) ? val + Dh : 0.f);
+                }
+                const bf16x8_t bop = pack8(m);
+#pragma unroll
+                for (int pt = 0; pt < PT; ++pt) {
+                    const bf16x8_t a = *(const bf16x8_t*)&s_xT[pt * 32 + r][j0];
+                    yacc[pt] = mfma32x32x16(a, bop, yacc[pt]);
+                }
+            }
+            // store: the lane holds y[il][4 consecutive p] per group of 4
+            // registers; stage the 32 x (32 PT) tile in LDS, then write whole rows
+#pragma unroll
+            for (int pt = 0; pt < PT; ++pt)
+#pragma unroll
+                for (int gq = 0; gq < 4; ++gq) {
+                    uint2 pk;
+                    pk.x = (uint32_t)__builtin_bit_cast(bf16_t, (__bf16)yacc[pt][4 * gq]) |
+                           ((uint32_t)__builtin_bit_cast(bf16_t, (__bf16)yacc[pt][4 * gq + 1]) << 16);
+                    pk.y = (uint32_t)__builtin_bit_cast(bf16_t, (__bf16)yacc[pt][4 * gq + 2]) |
+                           ((uint32_t)__builtin_bit_cast(bf16_t, (__bf16)yacc[pt][4 * gq + 3]) << 16);
+                    *(uint2*)&s_y[wave][r][pt * 32 + 8 * gq + 4 * half] = pk;
+                }
+            {
+                constexpr int CPR = PT * 4;       // 16-byte chunks per row
+                constexpr int RPI = 64 / CPR;     // rows per wave instruction
+#pragma unroll
+                for (int q = 0; q < 32 / RPI; ++q) {
+                    const int row = q * RPI + lane / CPR, ch = lane % CPR;
+                    const uint4 v = *(const uint4*)&s_y[wave][row][ch * 8];
+                    const int to = c * Q + it * 32 + row;
+                    if (to < p.L) *(uint4*)(yhead + (int64_t)to * p.y_sl + ch * 8) = v;
+                }
+            }
+        }
+
+        // ---- prefetch the next chunk's x / dt (lands during the state GEMM)
+        if (c + 1 < p.nch) fetch(c + 1);
+
+        // ---- K3 + K4: h <- exp(cs_end) h + x^T (B o w), B fragments in a 4-deep ring
+        {
+            const float dec = __builtin_amdgcn_exp2f(cs2_end);
+#pragma unroll
+            for (int k = 0; k < SPW; ++k)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) hacc[k][v] *= dec;
+            // all state tiles of a wave share one n tile (st_nt[0]) when SPW > 1
+            const bf16_t* btrow = bfr + grp * (int64_t)Q * N + ((int64_t)st_nt[0] * KS * 64 + lane) * 8;
+            uint4 bring[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) bring[k] = *(const uint4*)(btrow + k * 512);
+#pragma unroll
+            for (int ks = 0; ks < Q / 16; ++ks) {
+                const int j0 = ks * 16 + 8 * half;
+                float bf[8];
+                unpack8(bring[ks & 3], bf);
+                if (ks + 4 < Q / 16) bring[ks & 3] = *(const uint4*)(btrow + (ks + 4) * 512);
+                const float4 w0 = *(const float4*)&s_w[j0];
+                const float4 w1 = *(const float4*)&s_w[j0 + 4];
+                const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) bf[e] *= wv[e];
+                const bf16x8_t bop = pack8(bf);
+#pragma unroll
+                for (int k = 0; k < SPW; ++k) {
+                    if (!st_ok[k]) continue;
+                    const bf16x8_t a = *(const bf16x8_t*)&s_xT[st_pt[k] * 32 + r][j0];
+                    hacc[k] = mfma32x32x16(a, bop, hacc[k]);
+                }
+            }
+        }
+        // ---- warm L2 with the next chunk's group operands while the WG syncs and scans
+        if (c + 1 < p.nch && pf_on) {
+            const int64_t g1 = grp + p.G;  // (b, c + 1, g)
+            const char* blk = pf_kind == 0 ? (const char*)(cbf + g1 * Q * Q)
+                            : pf_kind == 1 ? (const char*)(cf + g1 * (int64_t)Q * N)
+                                           : (const char*)(bfr + g1 * (int64_t)Q * N);
+            pf = *(const uint32_t*)(blk + pf_off);
+        }
+        __syncthreads();  // all reads of s_h / s_xT / s_cs2 / s_dt / s_w / s_f done
+#pragma unroll
+        for (int k = 0; k < SPW; ++k)
+            if (st_ok[k])
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+                    s_h[st_pt[k] * 32 + 8 * (v >> 2) + 4 * half + (v & 3)][st_nt[k] * 32 + r] =
+                        __builtin_bit_cast(bf16_t, (__bf16)hacc[k][v]);
+    }
+    // keeps the L2 warm-up loads alive (the condition never holds: L >= 1)
+    if (p.L < 0 && pf_sink == 0x9e3779b9u) p.hT[0] = 0.f;
+    // final state (f32)
+#pragma unroll
+    for (int k = 0; k < SPW; ++k) {
+        if (!st_ok[k]) continue;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int pp = p0 + st_pt[k] * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
+            p.hT[hbase + pp * N + st_nt[k] * 32 + r] = hacc[k][v];
+        }
+    }
+}
+
+// ------------------------------------------------------------ host side --
+static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
+
+bool ssd2_mfma_supported(const Ssd2Params& p) {
+    if (p.io_dtype != MAMBA_BF16) return false;
+    if (p.P != 64 || (p.N != 64 && p.N != 128)) return false;
+    if (p.Q % 32 != 0 || p.Q > kMaxQ) return false;
+    if (!aligned16(p.x) || !aligned16(p.Bm) || !aligned16(p.Cm) || !aligned16(p.y)) return false;
+    const int64_t s[] = {p.x_sb, p.x_sl, p.x_sh, p.B_sb, p.B_sl, p.B_sg, p.C_sb, p.C_sl, p.C_sg};
+    for (int64_t v : s)
+        if (v % 8 != 0) return false;
+    return true;
+}
+
+// workspace: cbf (Q*Q f32) + cf (Q*N bf16) + bf (Q*N bf16) per (batch, chunk, group)
+static size_t cbf_bytes(const Ssd2Params& p) {
+    return align_up((size_t)p.nb * p.nch * p.G * p.Q * p.Q * sizeof(float), 256);
+}
+static size_t frag_bytes(const Ssd2Params& p) {
+    return align_up((size_t)p.nb * p.nch * p.G * p.N * p.Q * sizeof(bf16_t), 256);
+}
+
+size_t ssd2_mfma_workspace(const Ssd2Params& p) { return cbf_bytes(p) + 2 * frag_bytes(p); }
+
+// Headdim split: 2 workgroups per (batch, head) doubles the workgroup count
+// (better balance over 256 CUs) at the price of re-building the decay matrix
+// in both halves.  The environment variable MAMBA_SSD2_PSPLIT=0/1 (read on
+// every call) overrides the heuristic.
+static int choose_pt(const Ssd2Params& p) {
+    const char* e = getenv("MAMBA_SSD2_PSPLIT");
+    const int forced = e ? atoi(e) : -1;
+    if (forced == 0) return 2;
+    if (forced == 1) return 1;
+    return (int64_t)p.nb * p.H < 320 ? 1 : 2;
+}
+
+template <int N, int Q>
+static int launch_q(const Ssd2Params& p, void* ws, hipStream_t stream, hipEvent_t ev0, hipEvent_t ev1) {
+    float* cbf = (float*)ws;
+    bf16_t* cf = (bf16_t*)((char*)ws + cbf_bytes(p));
+    bf16_t* bfr = (bf16_t*)((char*)ws + cbf_bytes(p) + frag_bytes(p));
+    const int S = 4;  // prep workgroups per (batch, chunk, group)
+    hipLaunchKernelGGL((ssd2_prep_mfma<N, Q>), dim3(S, p.nch * p.G, p.nb), dim3(256), 0, stream, p, cbf,
+                       cf, bfr);
+    MAMBA_CHECK_LAUNCH();
+    if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, stream));
+    if (choose_pt(p) == 2) {
+        hipLaunchKernelGGL((ssd2_scan_mfma<N, Q, 2>), dim3(p.nb * p.H), dim3(256), 0, stream, p,
+                           (const float*)cbf, (const bf16_t*)cf, (const bf16_t*)bfr);
+    } else {
+        hipLaunchKernelGGL((ssd2_scan_mfma<N, Q, 1>), dim3(p.nb * p.H * 2), dim3(256), 0, stream, p,
+                           (const float*)cbf, (const bf16_t*)cf, (const bf16_t*)bfr);
+    }
+    MAMBA_CHECK_LAUNCH();
+    if (ev1) MAMBA_CHECK_HIP(hipEventRecord(ev1, stream));
+    return MAMBA_OK;
+}
+
+template <int N>
+static int launch_n(const Ssd2Params& p, void* ws, hipStream_t stream, hipEvent_t ev0, hipEvent_t ev1) {
+    switch (p.Q) {
+        case 32: return launch_q<N, 32>(p, ws, stream, ev0, ev1);
+        case 64: return launch_q<N, 64>(p, ws, stream, ev0, ev1);
+        case 96: return launch_q<N, 96>(p, ws, stream, ev0, ev1);
+        case 128: return launch_q<N, 128>(p, ws, stream, ev0, ev1);
+        case 160: return launch_q<N, 160>(p, ws, stream, ev0, ev1);
+        case 192: return launch_q<N, 192>(p, ws, stream, ev0, ev1);
+        case 224: return launch_q<N, 224>(p, ws, stream, ev0, ev1);
+        default: return launch_q<N, 256>(p, ws, stream, ev0, ev1);
+    }
+}
+
+int ssd2_mfma_launch(const Ssd2Params& p, void* ws, hipStream_t stream, hipEvent_t ev0, hipEvent_t ev1) {
+    if (p.N == 64) return launch_n<64>(p, ws, stream, ev0, ev1);
+    return launch_n<128>(p, ws, stream, ev0, ev1);
+}
+
 }  // namespace mamba

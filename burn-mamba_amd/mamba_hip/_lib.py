@@ -47,6 +47,7 @@ _SIGNATURES = {
     "mamba_last_error": ([], ctypes.c_char_p),
     "mamba_version": ([], ctypes.c_char_p),
     "mamba_ssd2_workspace_size": ([ctypes.POINTER(Ssd2Args)], ctypes.c_size_t),
+    "mamba_ssd2_fast_path": ([ctypes.POINTER(Ssd2Args)], ctypes.c_int),
     "mamba_ssd2_fwd": ([ctypes.POINTER(Ssd2Args), c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),
     "mamba_ssd2_fwd_generic": ([ctypes.POINTER(Ssd2Args), c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),
     "mamba_ssd2_fwd_timed": ([ctypes.POINTER(Ssd2Args), c_vp, ctypes.c_size_t, c_vp, c_vp, c_vp],

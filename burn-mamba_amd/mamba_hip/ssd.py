@@ -58,27 +58,13 @@ def _check_inner(t: torch.Tensor, name: str):
         raise _lib.MambaHipError(f"{name}: innermost axis must be contiguous")
 
 
-def ssd2_fwd(x, dt, A, B, C, D=None, initial_state=None, init_state_hpr=None, chunk_len=None,
-             y=None, final_state=None, generic=False, events=None):
-    """Mamba-2 SSD forward through ``mamba_ssd2_fwd``.
-
-    x[b,l,h,p] (f32|bf16)  dt[b,l,h] f32  A[h] f32  B,C[b,l,g,n] (dtype of x)
-    D[h] f32  initial_state[b,h,p,n] f32  init_state_hpr[h,p,n] f32.
-    Any strides are accepted for the three outer axes; the innermost axis must
-    be contiguous.  Returns (y[b,l,h,p] dtype of x, final_state[b,h,p,n] f32).
-    """
+def _ssd2_args(x, dt, A, B, C, D, initial_state, init_state_hpr, chunk_len, y, final_state):
     b, l, h, p = x.shape
     g, n = B.shape[2], B.shape[3]
-    if chunk_len is None:
-        chunk_len = Mamba2SsdPath.optimal_chunk_len(n, p)
     for t, nm in ((x, "x"), (B, "B"), (C, "C")):
         _check_inner(t, nm)
     if not (dt.dtype == A.dtype == torch.float32):
         raise _lib.MambaHipError("dt and A must be float32")
-    if y is None:
-        y = torch.empty((b, l, h, p), dtype=x.dtype, device=x.device)
-    if final_state is None:
-        final_state = torch.empty((b, h, p, n), dtype=torch.float32, device=x.device)
     for t in (A, D, initial_state, init_state_hpr, final_state):
         if t is not None and not t.is_contiguous():
             raise _lib.MambaHipError("A, D and the states must be contiguous")
@@ -93,8 +79,47 @@ def ssd2_fwd(x, dt, A, B, C, D=None, initial_state=None, init_state_hpr=None, ch
     a.D = None if D is None else D.data_ptr()
     a.initial_state = None if initial_state is None else initial_state.data_ptr()
     a.init_state_hpr = None if init_state_hpr is None else init_state_hpr.data_ptr()
-    a.y = y.data_ptr(); a.y_sb, a.y_sl, a.y_sh = y.stride(0), y.stride(1), y.stride(2)
-    a.final_state = final_state.data_ptr()
+    if y is not None:
+        a.y = y.data_ptr(); a.y_sb, a.y_sl, a.y_sh = y.stride(0), y.stride(1), y.stride(2)
+    if final_state is not None:
+        a.final_state = final_state.data_ptr()
+    return a
+
+
+def ssd2_fast_path(x, dt, A, B, C, chunk_len=None) -> bool:
+    """True if ``mamba_ssd2_fwd`` would take the MFMA fast path for these inputs."""
+    if chunk_len is None:
+        chunk_len = Mamba2SsdPath.optimal_chunk_len(B.shape[3], x.shape[3])
+    y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    hT = torch.empty((x.shape[0], x.shape[2], x.shape[3], B.shape[3]), dtype=torch.float32,
+                     device=x.device)
+    a = _ssd2_args(x, dt, A, B, C, None, None, None, chunk_len, y, hT)
+    r = _lib.lib().mamba_ssd2_fast_path(ctypes.byref(a))
+    if r < 0:
+        check(1, "mamba_ssd2_fast_path")
+    return r == 1
+
+
+def ssd2_fwd(x, dt, A, B, C, D=None, initial_state=None, init_state_hpr=None, chunk_len=None,
+             y=None, final_state=None, generic=False, events=None):
+    """Mamba-2 SSD forward through ``mamba_ssd2_fwd``.
+
+    x[b,l,h,p] (f32|bf16)  dt[b,l,h] f32  A[h] f32  B,C[b,l,g,n] (dtype of x)
+    D[h] f32  initial_state[b,h,p,n] f32  init_state_hpr[h,p,n] f32.
+    Any strides are accepted for the three outer axes; the innermost axis must
+    be contiguous.  Returns (y[b,l,h,p] dtype of x, final_state[b,h,p,n] f32).
+    ``events`` = (start, stop) torch.cuda.Event pair recorded around the
+    dominant kernel (``mamba_ssd2_fwd_timed``); used by the benchmark.
+    """
+    b, l, h, p = x.shape
+    n = B.shape[3]
+    if chunk_len is None:
+        chunk_len = Mamba2SsdPath.optimal_chunk_len(n, p)
+    if y is None:
+        y = torch.empty((b, l, h, p), dtype=x.dtype, device=x.device)
+    if final_state is None:
+        final_state = torch.empty((b, h, p, n), dtype=torch.float32, device=x.device)
+    a = _ssd2_args(x, dt, A, B, C, D, initial_state, init_state_hpr, chunk_len, y, final_state)
     L = _lib.lib()
     nbytes = L.mamba_ssd2_workspace_size(ctypes.byref(a))
     ws = workspace(x.device, nbytes)

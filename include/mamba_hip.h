@@ -93,6 +93,12 @@ typedef struct mamba_ssd2_args {
 } mamba_ssd2_args;
 
 size_t mamba_ssd2_workspace_size(const mamba_ssd2_args* args);
+/* 1 if mamba_ssd2_fwd takes the MFMA fast path for these arguments (bf16     */
+/* I/O, headdim 64, dstate 64 or 128, chunk_len a multiple of 32 up to 256,   */
+/* 16-byte aligned rows), 0 if it takes the shape-generic path, -1 if the     */
+/* arguments are invalid.  No counterpart in the reference (its backends have  */
+/* a single code path per op).                                                */
+int mamba_ssd2_fast_path(const mamba_ssd2_args* args);
 int mamba_ssd2_fwd(const mamba_ssd2_args* args, void* workspace, size_t workspace_bytes,
                    mamba_stream_t stream);
 

@@ -123,3 +123,83 @@ def test_ssd2_invalid_args_rejected():
     Bm = torch.zeros(1, 8, 2, 4, device=dev)  # 3 heads not a multiple of 2 groups
     with pytest.raises(mamba_hip.MambaHipError, match="ngroups"):
         mamba_hip.ssd2_fwd(x, dt, A, Bm, Bm, chunk_len=4)
+
+
+# ------------------------------------------------- MFMA fast path (bf16) ----
+
+FAST_CASES = [
+    # (b, l, h, p, g, n, chunk)
+    (1, 1024, 8, 64, 1, 128, 256),   # config-1 head shape, reduced batch/length
+    (2, 1000, 4, 64, 2, 128, 256),   # ragged tail, 2 groups
+    (2, 333, 6, 64, 3, 64, 64),      # dstate 64, ragged
+    (1, 77, 2, 64, 1, 128, 32),      # smallest chunk
+    (1, 512, 4, 64, 1, 64, 160),     # 5 row tiles per chunk
+    (3, 256, 80, 64, 1, 128, 256),   # all 80 heads of config 1, one chunk
+]
+
+
+def _to_dev(inp, dtype="bf16"):
+    import torch
+    dev = torch.device("cuda:0")
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    return dict(
+        x=torch.from_numpy(inp["x"]).to(dev, tdt), B=torch.from_numpy(inp["B"]).to(dev, tdt),
+        C=torch.from_numpy(inp["C"]).to(dev, tdt), dt=torch.from_numpy(inp["dt"]).to(dev),
+        A=torch.from_numpy(inp["A"]).to(dev),
+        D=None if inp["D"] is None else torch.from_numpy(inp["D"]).to(dev),
+        h0=None if inp["h0"] is None else torch.from_numpy(inp["h0"]).to(dev))
+
+
+@pytest.mark.parametrize("psplit", ["0", "1"])
+@pytest.mark.parametrize("case", FAST_CASES)
+def test_ssd2_mfma_bf16(case, psplit, monkeypatch):
+    import torch
+    import mamba_hip
+    monkeypatch.setenv("MAMBA_SSD2_PSPLIT", psplit)
+    b, l, h, p, g, n, q = case
+    inp = ssd2_inputs(seed=100 + sum(case), b=b, l=l, h=h, p=p, g=g, n=n, h0=True)
+    t = _to_dev(inp)
+    assert mamba_hip.ssd2_fast_path(t["x"], t["dt"], t["A"], t["B"], t["C"], chunk_len=q)
+    y, hT = mamba_hip.ssd2_fwd(t["x"], t["dt"], t["A"], t["B"], t["C"], t["D"], t["h0"], chunk_len=q)
+    torch.cuda.synchronize()
+    yr, hr = _oracle(inp, q, "bf16")
+    np.testing.assert_allclose(y.float().cpu().numpy(), yr, **BF16_TOL)
+    np.testing.assert_allclose(hT.cpu().numpy(), hr, **BF16_TOL)
+
+
+def test_ssd2_mfma_zero_state_and_init_hpr():
+    """No initial state (the config-1 case) and the learnable init_state_hpr
+    (added to h0 as minimal.rs:316-328 does) on the fast path."""
+    import torch
+    import mamba_hip
+    import oracle
+    inp = ssd2_inputs(seed=5, b=2, l=600, h=4, p=64, g=1, n=128, h0=False)
+    t = _to_dev(inp)
+    y, hT = mamba_hip.ssd2_fwd(t["x"], t["dt"], t["A"], t["B"], t["C"], t["D"], None, chunk_len=256)
+    torch.cuda.synchronize()
+    yr, hr = _oracle(inp, 256, "bf16")
+    np.testing.assert_allclose(y.float().cpu().numpy(), yr, **BF16_TOL)
+    np.testing.assert_allclose(hT.cpu().numpy(), hr, **BF16_TOL)
+    init = (0.1 * np.random.default_rng(1).standard_normal((4, 64, 128))).astype(np.float32)
+    y2, h2 = mamba_hip.ssd2_fwd(t["x"], t["dt"], t["A"], t["B"], t["C"], t["D"], None,
+                                torch.from_numpy(init).cuda(), chunk_len=256)
+    torch.cuda.synchronize()
+    xr, Br, Cr = bf16_round(inp["x"]), bf16_round(inp["B"]), bf16_round(inp["C"])
+    yr2, hr2 = oracle.ssd2(xr, inp["dt"], inp["A"], Br, Cr, inp["D"], None, init, chunk=256)
+    np.testing.assert_allclose(y2.float().cpu().numpy(), yr2, **BF16_TOL)
+    np.testing.assert_allclose(h2.cpu().numpy(), hr2, **BF16_TOL)
+
+
+def test_ssd2_mfma_matches_generic_closely():
+    """Fast path vs the f32 SIMT path on identical bf16 inputs: differences
+    come only from the bf16 rounding of the MFMA operands."""
+    import torch
+    import mamba_hip
+    inp = ssd2_inputs(seed=9, b=1, l=768, h=8, p=64, g=1, n=128, h0=True)
+    t = _to_dev(inp)
+    yf, hf = mamba_hip.ssd2_fwd(t["x"], t["dt"], t["A"], t["B"], t["C"], t["D"], t["h0"], chunk_len=256)
+    yg, hg = mamba_hip.ssd2_fwd(t["x"], t["dt"], t["A"], t["B"], t["C"], t["D"], t["h0"], chunk_len=256,
+                                generic=True)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(yf.float().cpu().numpy(), yg.float().cpu().numpy(), **BF16_TOL)
+    np.testing.assert_allclose(hf.cpu().numpy(), hg.cpu().numpy(), **BF16_TOL)
