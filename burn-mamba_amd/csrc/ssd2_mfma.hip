@@ -37,6 +37,27 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kMaxQ = 256;
 
+// Tuning constants of the scan kernel (compile-time; the defaults are the
+// measured best on MI355X for the 2.7B-layer shape).
+#ifndef MAMBA_SSD2_CB_RING
+#define MAMBA_SSD2_CB_RING 4  // in-flight C.B^T fragments per wave (2 or 4)
+#endif
+#ifndef MAMBA_SSD2_B_RING
+#define MAMBA_SSD2_B_RING 4   // in-flight B fragments per wave in the state GEMM
+#endif
+#ifndef MAMBA_SSD2_STATE_UNROLL
+#define MAMBA_SSD2_STATE_UNROLL 16  // must be a multiple of MAMBA_SSD2_B_RING
+#endif
+#ifndef MAMBA_SSD2_L2_WARM
+#define MAMBA_SSD2_L2_WARM 1  // touch the next chunk's group operands ahead of use
+#endif
+#ifndef MAMBA_SSD2_B_F32
+#define MAMBA_SSD2_B_F32 0    // B fragments of the state GEMM stored in f32 (else bf16)
+#endif
+#ifndef MAMBA_SSD2_DIAG_FACTORED
+#define MAMBA_SSD2_DIAG_FACTORED 0  // tabulated diagonal-block decay when its span allows
+#endif
+
 __device__ __forceinline__ f32x16_t mfma32x32x16(bf16x8_t a, bf16x8_t b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
@@ -79,11 +100,13 @@ __device__ __forceinline__ f32x16_t zero16() {
 // load there is one contiguous 1 KB read:
 //   cbf[it][ks][plane][lane][4] f32 : (C.B^T)[i = 32 it + lane%32][j = 16 ks + 8 (lane/32) + 4 plane + e]
 //   cf [it][kn][lane][8]     bf16   : C[i = 32 it + lane%32][n = 16 kn + 8 (lane/32) + e]
-//   bf [nt][ks][lane][8]     bf16   : B[j = 16 ks + 8 (lane/32) + e][n = 32 nt + lane%32]
+//   bf [nt][ks][plane][lane][4] f32 : B[j = 16 ks + 8 (lane/32) + 4 plane + e][n = 32 nt + lane%32]
+//      (or [nt][ks][lane][8] bf16 when MAMBA_SSD2_B_F32 is 0)
 // Positions past seqlen read as zero.  Only the causal (ks <= 2 it + 1)
-// fragments of cbf are written (K2, src/mamba2/ssd/serial.rs:170-185).
+// fragments of cbf are written (K2, src/mamba2/ssd/serial.rs:170-185), and
+// inside the diagonal 32x32 blocks the entries with j > i are stored as 0.
 template <int N, int Q>
-__global__ __launch_bounds__(256) void ssd2_prep_mfma(Ssd2Params p, float* cbf, bf16_t* cf, bf16_t* bfr) {
+__global__ __launch_bounds__(256) void ssd2_prep_mfma(Ssd2Params p, float* cbf, bf16_t* cf, void* bfr) {
     constexpr int T = Q / 32, NK = N / 16, KS = Q / 16, NTN = N / 32;
     constexpr int NTILE = T * (T + 1) / 2;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 31, half = lane >> 5;
@@ -108,6 +131,11 @@ __global__ __launch_bounds__(256) void ssd2_prep_mfma(Ssd2Params p, float* cbf, 
             const bf16x8_t bb = as_bf16x8(ld16(Cg + (int64_t)ti * p.C_sl + n0, ti < p.L));
             acc = mfma32x32x16(a, bb, acc);
         }
+        if (jt == it) {  // causal mask of the diagonal block: row j = 8 q + 4 half + u, column i = r
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+                if (8 * (v >> 2) + 4 * half + (v & 3) > r) acc[v] = 0.f;
+        }
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int ks = 2 * jt + (q >> 1), lp = r + 32 * (q & 1);
@@ -122,19 +150,31 @@ __global__ __launch_bounds__(256) void ssd2_prep_mfma(Ssd2Params p, float* cbf, 
         *(uint4*)(cbase2 + ((int64_t)f * 64 + lane) * 8) =
             ld16(Cg + (int64_t)t * p.C_sl + kn * 16 + 8 * half, t < p.L);
     }
-    bf16_t* bbase = bfr + grp * (int64_t)Q * N;
+#if MAMBA_SSD2_B_F32
+    float* bbase = (float*)bfr + grp * (int64_t)Q * N;
+#else
+    bf16_t* bbase = (bf16_t*)bfr + grp * (int64_t)Q * N;
+#endif
     for (int f = s + S * wave; f < NTN * KS; f += 4 * S) {
         const int nt = f / KS, ks = f % KS;
         const int n = nt * 32 + r;
-        uint32_t w[4];
+        uint32_t raw[8];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int t0 = c * Q + ks * 16 + 8 * half + 2 * k;
-            const uint32_t lo = t0 < p.L ? Bg[(int64_t)t0 * p.B_sl + n] : 0u;
-            const uint32_t hi = t0 + 1 < p.L ? Bg[(int64_t)(t0 + 1) * p.B_sl + n] : 0u;
-            w[k] = lo | (hi << 16);
+        for (int e = 0; e < 8; ++e) {
+            const int t = c * Q + ks * 16 + 8 * half + e;
+            raw[e] = t < p.L ? (uint32_t)Bg[(int64_t)t * p.B_sl + n] : 0u;
         }
-        *(uint4*)(bbase + ((int64_t)f * 64 + lane) * 8) = make_uint4(w[0], w[1], w[2], w[3]);
+#if MAMBA_SSD2_B_F32
+        float* dst = bbase + (int64_t)f * 512 + lane * 4;
+        *(float4*)dst = make_float4(__uint_as_float(raw[0] << 16), __uint_as_float(raw[1] << 16),
+                                    __uint_as_float(raw[2] << 16), __uint_as_float(raw[3] << 16));
+        *(float4*)(dst + 256) = make_float4(__uint_as_float(raw[4] << 16), __uint_as_float(raw[5] << 16),
+                                            __uint_as_float(raw[6] << 16), __uint_as_float(raw[7] << 16));
+#else
+        *(uint4*)(bbase + ((int64_t)f * 64 + lane) * 8) =
+            make_uint4(raw[0] | (raw[1] << 16), raw[2] | (raw[3] << 16), raw[4] | (raw[5] << 16),
+                       raw[6] | (raw[7] << 16));
+#endif
     }
 }
 
@@ -155,11 +195,14 @@ __device__ __forceinline__ int itile_owner(int it) {
 //   y_i = e_i [ exp(cs_r0) (h_in . C_i) + sum_{j < r0} x_j (C_i.B_j) f_it[j] ]
 //         + sum_{r0 <= j <= i} x_j (C_i.B_j) dt_j exp(cs_i - cs_j) + D x_i
 // where f_it[j] = dt_j exp(cs_r0 - cs_j) <= dt_j is tabulated per chunk in
-// LDS (s_f).  Every factor is <= 1, so nothing can overflow; the diagonal
-// block uses the exact exponent and carries D on its diagonal.
+// LDS (s_f); all these factors are <= 1.  The diagonal block uses the same
+// form, with fd[j] = dt_j exp(cs_r0 - cs_j) for r0 <= j (now >= dt_j) and D/e_i
+// on its diagonal, whenever the block's decay span cs_r0 - cs_{r0+31} keeps
+// both bounded (< 2^60); otherwise it falls back to the exact exponent
+// exp(cs_i - cs_j), accumulated after the e_i scaling.
 template <int N, int Q, int PT>
 __global__ __launch_bounds__(256, 2) void ssd2_scan_mfma(Ssd2Params p, const float* cbf,
-                                                         const bf16_t* cf, const bf16_t* bfr) {
+                                                         const bf16_t* cf, const void* bfr) {
     constexpr int T = Q / 32;                 // i-tiles per chunk
     constexpr int NTN = N / 32;               // n tiles of the state
     constexpr int NST = PT * NTN;             // state tiles per workgroup
@@ -172,8 +215,8 @@ __global__ __launch_bounds__(256, 2) void ssd2_scan_mfma(Ssd2Params p, const flo
     constexpr int NK = N / 16, KS = Q / 16;
     constexpr int YP = PT * 32 + 8;           // s_y row pitch (bf16)
     __shared__ __align__(16) float s_cs2[Q];
-    __shared__ __align__(16) float s_dt[Q];
     __shared__ __align__(16) float s_w[Q];
+    __shared__ __align__(16) float s_fd[Q];
     __shared__ float s_red[4];
     __shared__ __align__(16) float s_f[T > 1 ? T - 1 : 1][Q];
     __shared__ __align__(16) bf16_t s_xT[PT * 32][XP];
@@ -255,8 +298,8 @@ __global__ __launch_bounds__(256, 2) void ssd2_scan_mfma(Ssd2Params p, const flo
     // splits) of a group share them and sit on one XCD, so each workgroup
     // touches one slice of the group's lines, one dword per line
     constexpr int CB_LINES = 16 * T * (T + 1);  // causal C.B^T fragments
-    constexpr int FR_LINES = Q * N * 2 / 128;   // C or B fragments
-    constexpr int GRP_LINES = CB_LINES + 2 * FR_LINES;
+    constexpr int FR_LINES = Q * N * 2 / 128;   // C fragments (bf16)
+    constexpr int GRP_LINES = CB_LINES + (MAMBA_SSD2_B_F32 ? 3 : 2) * FR_LINES;  // + B fragments
     const int nslice = (p.H / p.G) * splits;
     const int slice = (h % (p.H / p.G)) * splits + ph;
     const int pf_line = (int)(((int64_t)GRP_LINES * slice) / nslice) + threadIdx.x;
@@ -291,27 +334,28 @@ __global__ __launch_bounds__(256, 2) void ssd2_scan_mfma(Ssd2Params p, const flo
                 }
             }
         }
+        const float dtv = dtq;  // dt of position threadIdx.x of this chunk
         {
-            const float dtv = dtq;
             float v = wave_incl_scan(dtv * A2);
             if (lane == 63) s_red[wave] = v;
             __syncthreads();
 #pragma unroll
             for (int k = 0; k < 3; ++k)
                 if (k < wave) v += s_red[k];
-            if (threadIdx.x < Q) {
-                s_cs2[threadIdx.x] = v;
-                s_dt[threadIdx.x] = dtv;
-            }
+            if (threadIdx.x < Q) s_cs2[threadIdx.x] = v;
         }
         __syncthreads();
         const float cs2_end = s_cs2[Q - 1];
         // chunk-state weights dt_j exp(cs_end - cs_j) and the decay table
-        if (threadIdx.x < Q)
-            s_w[threadIdx.x] = s_dt[threadIdx.x] * __builtin_amdgcn_exp2f(cs2_end - s_cs2[threadIdx.x]);
-        for (int idx = threadIdx.x; idx < (T - 1) * Q; idx += 256) {
-            const int it = idx / Q + 1, j = idx % Q;
-            if (j < it * 32) s_f[it - 1][j] = s_dt[j] * __builtin_amdgcn_exp2f(s_cs2[it * 32] - s_cs2[j]);
+        if (threadIdx.x < Q) {
+            const int j = threadIdx.x;
+            const float csj = s_cs2[j];
+            s_w[j] = dtv * __builtin_amdgcn_exp2f(cs2_end - csj);
+            s_fd[j] = dtv * __builtin_amdgcn_exp2f(s_cs2[j & ~31] - csj);
+            // decay table of the strictly-lower blocks: row block it > j / 32
+#pragma unroll
+            for (int it = 1; it < T; ++it)
+                if (j < it * 32) s_f[it - 1][j] = dtv * __builtin_amdgcn_exp2f(s_cs2[it * 32] - csj);
         }
         __syncthreads();
 
@@ -326,16 +370,17 @@ __global__ __launch_bounds__(256, 2) void ssd2_scan_mfma(Ssd2Params p, const flo
             if (itile_owner(it) != wave) continue;
             const int il = it * 32 + r;  // this lane's output time (B-operand column)
             // issue every global load of this tile before the first wait:
-            // the C fragments (inter-chunk term) and a 4-deep ring of CB fragments
+            // the C fragments (inter-chunk term) and a ring of CB fragments
             uint4 craw[NK];
 #pragma unroll
             for (int kn = 0; kn < NK; ++kn) craw[kn] = *(const uint4*)(cfg + (int64_t)(it * NK + kn) * 512);
             const float* cbt = cbg + (int64_t)it * KS * 512;  // fragment (it, ks) at + ks * 512
             const int nb = 2 * it;    // strictly-lower k-steps (even)
             const int ntot = nb + 2;  // + the diagonal block
-            float4 ring[4][2];
+            constexpr int RD = MAMBA_SSD2_CB_RING;  // CB fragment ring depth
+            float4 ring[RD][2];
 #pragma unroll
-            for (int k = 0; k < 4; ++k)
+            for (int k = 0; k < RD; ++k)
                 if (k < ntot) {
                     ring[k][0] = *(const float4*)(cbt + k * 512);
                     ring[k][1] = *(const float4*)(cbt + k * 512 + 256);
@@ -363,16 +408,16 @@ __global__ __launch_bounds__(256, 2) void ssd2_scan_mfma(Ssd2Params p, const flo
                     for (int v = 0; v < 16; ++v) yacc[pt][v] *= sc;
             }
             // strictly-lower blocks: B operand (C_i.B_j) f_it[j]
-            for (int ks0 = 0; ks0 < nb; ks0 += 4) {
+            for (int ks0 = 0; ks0 < nb; ks0 += RD) {
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
+                for (int k = 0; k < RD; ++k) {
                     const int ks = ks0 + k;
                     if (ks < nb) {
                         const int j0 = ks * 16 + 8 * half;
                         const float4 c0 = ring[k][0], c1 = ring[k][1];
-                        if (ks + 4 < ntot) {
-                            ring[k][0] = *(const float4*)(cbt + (ks + 4) * 512);
-                            ring[k][1] = *(const float4*)(cbt + (ks + 4) * 512 + 256);
+                        if (ks + RD < ntot) {
+                            ring[k][0] = *(const float4*)(cbt + (ks + RD) * 512);
+                            ring[k][1] = *(const float4*)(cbt + (ks + RD) * 512 + 256);
                         }
                         const float4 f0 = *(const float4*)&s_f[it - 1][j0];
                         const float4 f1 = *(const float4*)&s_f[it - 1][j0 + 4];
@@ -387,44 +432,69 @@ __global__ __launch_bounds__(256, 2) void ssd2_scan_mfma(Ssd2Params p, const flo
                     }
                 }
             }
-            {
-                const float ei = __builtin_amdgcn_exp2f(cs2_i - cs2_r0);
+            // diagonal block: its two CB fragments sit in ring slots nb % RD and
+            // nb % RD + 1 (nb is even).  The prep stored its upper triangle as 0.
+            static_assert(RD == 2 || RD == 4, "ring depth 2 or 4");
+            float4 dg[2][2];
+            if (RD == 2 || (nb & 3) == 0) {
+                dg[0][0] = ring[0][0]; dg[0][1] = ring[0][1]; dg[1][0] = ring[1][0]; dg[1][1] = ring[1][1];
+            } else {
+                dg[0][0] = ring[RD - 2][0]; dg[0][1] = ring[RD - 2][1];
+                dg[1][0] = ring[RD - 1][0]; dg[1][1] = ring[RD - 1][1];
+            }
+            const float ei = __builtin_amdgcn_exp2f(cs2_i - cs2_r0);
+            const float span = cs2_r0 - s_cs2[it * 32 + 31];
+            if (MAMBA_SSD2_DIAG_FACTORED && span < 60.f) {
+                // bounded: (C_i.B_j) fd[j] (+ D / e_i on the diagonal), then scale by e_i
+                const float dei = Dh / ei;
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+                    const int j0 = it * 32 + kk * 16 + 8 * half;
+                    const float4 c0 = dg[kk][0], c1 = dg[kk][1];
+                    const float4 f0 = *(const float4*)&s_fd[j0];
+                    const float4 f1 = *(const float4*)&s_fd[j0 + 4];
+                    const int d = il - j0;  // position of the diagonal in this fragment
+                    float m[8] = {c0.x * f0.x, c0.y * f0.y, c0.z * f0.z, c0.w * f0.w,
+                                  c1.x * f1.x, c1.y * f1.y, c1.z * f1.z, c1.w * f1.w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) m[e] += (e == d) ? dei : 0.f;
+                    const bf16x8_t bop = pack8(m);
+#pragma unroll
+                    for (int pt = 0; pt < PT; ++pt) {
+                        const bf16x8_t a = *(const bf16x8_t*)&s_xT[pt * 32 + r][j0];
+                        yacc[pt] = mfma32x32x16(a, bop, yacc[pt]);
+                    }
+                }
 #pragma unroll
                 for (int pt = 0; pt < PT; ++pt)
 #pragma unroll
                     for (int v = 0; v < 16; ++v) yacc[pt][v] *= ei;
-            }
-            // diagonal block, exact exponent, + D on the diagonal; its CB
-            // fragments sit in ring slots nb % 4 and nb % 4 + 1 (nb is even)
-            float4 dg[2][2];
-            if ((nb & 3) == 0) {
-                dg[0][0] = ring[0][0]; dg[0][1] = ring[0][1]; dg[1][0] = ring[1][0]; dg[1][1] = ring[1][1];
             } else {
-                dg[0][0] = ring[2][0]; dg[0][1] = ring[2][1]; dg[1][0] = ring[3][0]; dg[1][1] = ring[3][1];
-            }
+                // steep decay inside the block: exact exponent, after the e_i scaling
 #pragma unroll
-            for (int kk = 0; kk < 2; ++kk) {
-                const int j0 = it * 32 + kk * 16 + 8 * half;
-                const float4 c0 = dg[kk][0], c1 = dg[kk][1];
-                const float4 d0 = *(const float4*)&s_dt[j0];
-                const float4 d1 = *(const float4*)&s_dt[j0 + 4];
-                const float4 s0 = *(const float4*)&s_cs2[j0];
-                const float4 s1 = *(const float4*)&s_cs2[j0 + 4];
-                const float cbv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-                const float dtv[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
-                const float csv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-                float m[8];
+                for (int pt = 0; pt < PT; ++pt)
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const int j = j0 + e;
-                    const float val = cbv[e] * dtv[e] * __builtin_amdgcn_exp2f(cs2_i - csv[e]);
-                    m[e] = (j < il) ? val : ((j == il) ? val + Dh : 0.f);
-                }
-                const bf16x8_t bop = pack8(m);
+                    for (int v = 0; v < 16; ++v) yacc[pt][v] *= ei;
 #pragma unroll
-                for (int pt = 0; pt < PT; ++pt) {
-                    const bf16x8_t a = *(const bf16x8_t*)&s_xT[pt * 32 + r][j0];
-                    yacc[pt] = mfma32x32x16(a, bop, yacc[pt]);
+                for (int kk = 0; kk < 2; ++kk) {
+                    const int j0 = it * 32 + kk * 16 + 8 * half;
+                    const float4 c0 = dg[kk][0], c1 = dg[kk][1];
+                    const float cbv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+                    float m[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const int j = j0 + e;
+                        const int tj = c * Q + j;
+                        const float dtj = tj < p.L ? dthead[(int64_t)tj * p.dt_sl] : 0.f;
+                        const float val = cbv[e] * dtj * __builtin_amdgcn_exp2f(cs2_i - s_cs2[j]);
+                        m[e] = (j < il) ? val : ((j == il) ? val + Dh : 0.f);
+                    }
+                    const bf16x8_t bop = pack8(m);
+#pragma unroll
+                    for (int pt = 0; pt < PT; ++pt) {
+                        const bf16x8_t a = *(const bf16x8_t*)&s_xT[pt * 32 + r][j0];
+                        yacc[pt] = mfma32x32x16(a, bop, yacc[pt]);
+                    }
                 }
             }
             // store: the lane holds y[il][4 consecutive p] per group of 4
@@ -456,44 +526,63 @@ __global__ __launch_bounds__(256, 2) void ssd2_scan_mfma(Ssd2Params p, const flo
         // ---- prefetch the next chunk's x / dt (lands during the state GEMM)
         if (c + 1 < p.nch) fetch(c + 1);
 
-        // ---- K3 + K4: h <- exp(cs_end) h + x^T (B o w), B fragments in a 4-deep ring
-        {
+        // ---- K3 + K4: h <- exp(cs_end) h + x^T (B o w), B fragments in a small ring
+        if (wave < NST) {  // every state tile of this wave is valid (SPW > 1 iff NST >= 8)
             const float dec = __builtin_amdgcn_exp2f(cs2_end);
 #pragma unroll
             for (int k = 0; k < SPW; ++k)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) hacc[k][v] *= dec;
             // all state tiles of a wave share one n tile (st_nt[0]) when SPW > 1
-            const bf16_t* btrow = bfr + grp * (int64_t)Q * N + ((int64_t)st_nt[0] * KS * 64 + lane) * 8;
-            uint4 bring[4];
+            constexpr int BD = MAMBA_SSD2_B_RING;  // B fragment ring depth
+#if MAMBA_SSD2_B_F32
+            const float* btf = (const float*)bfr + grp * (int64_t)Q * N + (int64_t)st_nt[0] * KS * 512 + lane * 4;
+            float4 bring[BD][2];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) bring[k] = *(const uint4*)(btrow + k * 512);
+            for (int k = 0; k < BD; ++k) {
+                bring[k][0] = *(const float4*)(btf + k * 512);
+                bring[k][1] = *(const float4*)(btf + k * 512 + 256);
+            }
+#else
+            const bf16_t* btf = (const bf16_t*)bfr + grp * (int64_t)Q * N + ((int64_t)st_nt[0] * KS * 64 + lane) * 8;
+            uint4 bring[BD];
 #pragma unroll
-            for (int ks = 0; ks < Q / 16; ++ks) {
+            for (int k = 0; k < BD; ++k) bring[k] = *(const uint4*)(btf + k * 512);
+#endif
+#pragma unroll MAMBA_SSD2_STATE_UNROLL
+            for (int ks = 0; ks < KS; ++ks) {
                 const int j0 = ks * 16 + 8 * half;
-                float bf[8];
-                unpack8(bring[ks & 3], bf);
-                if (ks + 4 < Q / 16) bring[ks & 3] = *(const uint4*)(btrow + (ks + 4) * 512);
+#if MAMBA_SSD2_B_F32
+                const float4 b0 = bring[ks % BD][0], b1 = bring[ks % BD][1];
+                if (ks + BD < KS) {
+                    bring[ks % BD][0] = *(const float4*)(btf + (ks + BD) * 512);
+                    bring[ks % BD][1] = *(const float4*)(btf + (ks + BD) * 512 + 256);
+                }
+#else
+                float bu[8];
+                unpack8(bring[ks % BD], bu);
+                if (ks + BD < KS) bring[ks % BD] = *(const uint4*)(btf + (ks + BD) * 512);
+                const float4 b0 = make_float4(bu[0], bu[1], bu[2], bu[3]);
+                const float4 b1 = make_float4(bu[4], bu[5], bu[6], bu[7]);
+#endif
                 const float4 w0 = *(const float4*)&s_w[j0];
                 const float4 w1 = *(const float4*)&s_w[j0 + 4];
-                const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-                for (int e = 0; e < 8; ++e) bf[e] *= wv[e];
-                const bf16x8_t bop = pack8(bf);
+                const float bv[8] = {b0.x * w0.x, b0.y * w0.y, b0.z * w0.z, b0.w * w0.w,
+                                     b1.x * w1.x, b1.y * w1.y, b1.z * w1.z, b1.w * w1.w};
+                const bf16x8_t bop = pack8(bv);
 #pragma unroll
                 for (int k = 0; k < SPW; ++k) {
-                    if (!st_ok[k]) continue;
                     const bf16x8_t a = *(const bf16x8_t*)&s_xT[st_pt[k] * 32 + r][j0];
                     hacc[k] = mfma32x32x16(a, bop, hacc[k]);
                 }
             }
         }
         // ---- warm L2 with the next chunk's group operands while the WG syncs and scans
-        if (c + 1 < p.nch && pf_on) {
+        if (MAMBA_SSD2_L2_WARM && c + 1 < p.nch && pf_on) {
             const int64_t g1 = grp + p.G;  // (b, c + 1, g)
             const char* blk = pf_kind == 0 ? (const char*)(cbf + g1 * Q * Q)
                             : pf_kind == 1 ? (const char*)(cf + g1 * (int64_t)Q * N)
-                                           : (const char*)(bfr + g1 * (int64_t)Q * N);
+                                           : (const char*)bfr + g1 * (int64_t)Q * N * (MAMBA_SSD2_B_F32 ? 4 : 2);
             pf = *(const uint32_t*)(blk + pf_off);
         }
         __syncthreads();  // all reads of s_h / s_xT / s_cs2 / s_dt / s_w / s_f done
@@ -533,7 +622,7 @@ bool ssd2_mfma_supported(const Ssd2Params& p) {
     return true;
 }
 
-// workspace: cbf (Q*Q f32) + cf (Q*N bf16) + bf (Q*N bf16) per (batch, chunk, group)
+// workspace: cbf (Q*Q f32) + cf (Q*N bf16) + bf (Q*N f32 or bf16) per (batch, chunk, group)
 static size_t cbf_bytes(const Ssd2Params& p) {
     return align_up((size_t)p.nb * p.nch * p.G * p.Q * p.Q * sizeof(float), 256);
 }
@@ -541,7 +630,9 @@ static size_t frag_bytes(const Ssd2Params& p) {
     return align_up((size_t)p.nb * p.nch * p.G * p.N * p.Q * sizeof(bf16_t), 256);
 }
 
-size_t ssd2_mfma_workspace(const Ssd2Params& p) { return cbf_bytes(p) + 2 * frag_bytes(p); }
+size_t ssd2_mfma_workspace(const Ssd2Params& p) {
+    return cbf_bytes(p) + (MAMBA_SSD2_B_F32 ? 3 : 2) * frag_bytes(p);
+}
 
 // Headdim split: 2 workgroups per (batch, head) doubles the workgroup count
 // (better balance over 256 CUs) at the price of re-building the decay matrix
@@ -559,7 +650,7 @@ template <int N, int Q>
 static int launch_q(const Ssd2Params& p, void* ws, hipStream_t stream, hipEvent_t ev0, hipEvent_t ev1) {
     float* cbf = (float*)ws;
     bf16_t* cf = (bf16_t*)((char*)ws + cbf_bytes(p));
-    bf16_t* bfr = (bf16_t*)((char*)ws + cbf_bytes(p) + frag_bytes(p));
+    void* bfr = (void*)((char*)ws + cbf_bytes(p) + frag_bytes(p));
     const int S = 4;  // prep workgroups per (batch, chunk, group)
     hipLaunchKernelGGL((ssd2_prep_mfma<N, Q>), dim3(S, p.nch * p.G, p.nb), dim3(256), 0, stream, p, cbf,
                        cf, bfr);
@@ -567,10 +658,10 @@ static int launch_q(const Ssd2Params& p, void* ws, hipStream_t stream, hipEvent_
     if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, stream));
     if (choose_pt(p) == 2) {
         hipLaunchKernelGGL((ssd2_scan_mfma<N, Q, 2>), dim3(p.nb * p.H), dim3(256), 0, stream, p,
-                           (const float*)cbf, (const bf16_t*)cf, (const bf16_t*)bfr);
+                           (const float*)cbf, (const bf16_t*)cf, (const void*)bfr);
     } else {
         hipLaunchKernelGGL((ssd2_scan_mfma<N, Q, 1>), dim3(p.nb * p.H * 2), dim3(256), 0, stream, p,
-                           (const float*)cbf, (const bf16_t*)cf, (const bf16_t*)bfr);
+                           (const float*)cbf, (const bf16_t*)cf, (const void*)bfr);
     }
     MAMBA_CHECK_LAUNCH();
     if (ev1) MAMBA_CHECK_HIP(hipEventRecord(ev1, stream));
