@@ -100,6 +100,109 @@ def cpu_baseline_ssd2(cfg, seed=0):
                       f"f32 serial K1-K5 restatement of the reference, {el:.2f} s"}
 
 
+MAMBA1_CFG2 = dict(batch=8, dim=5120, seqlen=2048, dstate=16)
+
+
+def mamba1_algorithmic(cfg):
+    """Compulsory HBM bytes of one scan: u, delta, z read and y written (f32),
+    B, C [b, n, l], A [d, n], D [d] read, final state [b, d, n] written; FLOPs
+    ~ 6 per (token, state) (exp counted as one) + 4 per token."""
+    b, d, l, n = (cfg[k] for k in ("batch", "dim", "seqlen", "dstate"))
+    tok = b * l
+    bytes_ = 4 * (4 * tok * d + 2 * tok * n + d * n + d + b * d * n)
+    flops = tok * d * (6 * n + 4)
+    return bytes_, flops
+
+
+def make_mamba1_inputs(cfg, dev, seed=0):
+    """BASELINE.json configs[2]: u~N(0,1) [b,d,l]; delta = softplus(N(0,1)-4);
+    A = -(1..n) per channel (S4D-real); B, C ~ N(0,1) [b,n,l]; D = 1; z~N(0,1)."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    b, d, l, n = (cfg[k] for k in ("batch", "dim", "seqlen", "dstate"))
+    u = torch.randn((b, d, l), generator=g, device=dev)
+    delta = torch.nn.functional.softplus(torch.randn((b, d, l), generator=g, device=dev) - 4.0)
+    A = -torch.arange(1, n + 1, device=dev, dtype=torch.float32).repeat(d, 1).contiguous()
+    B = torch.randn((b, n, l), generator=g, device=dev)
+    C = torch.randn((b, n, l), generator=g, device=dev)
+    D = torch.ones(d, device=dev)
+    z = torch.randn((b, d, l), generator=g, device=dev)
+    return dict(u=u, delta=delta, A=A, B=B, C=C, D=D, z=z)
+
+
+def cpu_baseline_mamba1(cfg, seed=0):
+    """The f32 CPU restatement of Mamba1::selective_scan's sequential loop
+    (oracle/, OpenMP over (batch, channel)) on the whole workload."""
+    import oracle
+    from inputs import mamba1_inputs
+    oracle.build()
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    inp = mamba1_inputs(seed, b=cfg["batch"], d=cfg["dim"], l=cfg["seqlen"], n=cfg["dstate"])
+    t0 = time.perf_counter()
+    oracle.mamba1_scan(inp["u"], inp["delta"], inp["A"], inp["B"], inp["C"], inp["D"], inp["z"], prec=32)
+    el = time.perf_counter() - t0
+    return {"value": cfg["batch"] * cfg["seqlen"] / el, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"the full workload ({cfg['batch']} x {cfg['seqlen']} tokens, {cfg['dim']} channels), "
+                      f"f32 sequential restatement of the reference loop, {el:.2f} s"}
+
+
+def bench_mamba1(args):
+    import torch
+
+    import mamba_hip
+    cfg = dict(MAMBA1_CFG2)
+    dev = torch.device("cuda:0")
+    inp = make_mamba1_inputs(cfg, dev)
+    y = torch.empty_like(inp["u"])
+    hT = torch.empty((cfg["batch"], cfg["dim"], cfg["dstate"]), device=dev)
+
+    def step(events=None):
+        mamba_hip.mamba1_scan(inp["u"], inp["delta"], inp["A"], inp["B"], inp["C"], inp["D"], inp["z"],
+                              y=y, final_state=hT, events=events)
+
+    ms_per_step, kern_ms = _time_steps(args, step)
+    nbytes, flops = mamba1_algorithmic(cfg)
+    tokens = cfg["batch"] * cfg["seqlen"]
+    achieved = nbytes / (kern_ms * 1e-3) / 1e9
+    return {
+        "metric": "Mamba-1 selective scan tokens/s (2.8B layer, B=8 L=2048 D=5120 N=16) + % HBM roofline",
+        "value": tokens / (ms_per_step * 1e-3), "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (BASELINE.json configs[2] distributions, seed 0)",
+        "config": {"workload": "mamba1_scan_cfg2", **cfg, "gate": "silu(z)", "entry": "mamba1_scan_fwd"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel_ms": kern_ms,
+                     "algorithmic_bytes": nbytes},
+    }
+
+
+def _time_steps(args, step):
+    """W untimed steps, then K timed back-to-back steps between synchronisations
+    (ms/step), then K steps with the library's events around the dominant
+    kernel (mean kernel ms)."""
+    import torch
+    log(f"warmup {args.warmup}")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} steps")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+             for _ in range(args.steps)]
+    for ev in pairs:
+        step(events=ev)
+    torch.cuda.synchronize()
+    kern_ms = sum(a.elapsed_time(b_) for a, b_ in pairs) / len(pairs)
+    log(f"ms/step {ms_per_step:.4f}, dominant kernel {kern_ms:.4f} ms")
+    return ms_per_step, kern_ms
+
+
 def bench_ssd2(args):
     import torch
 
@@ -162,7 +265,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="ssd2", choices=["ssd2"])
+    ap.add_argument("--workload", default="ssd2", choices=["ssd2", "mamba1"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -170,10 +273,15 @@ def main():
               "(the hot path shards by batch/head with no communication; see DESIGN.md)",
               file=sys.stderr)
         sys.exit(2)
-    out = bench_ssd2(args)
+    if args.workload == "mamba1":
+        out = bench_mamba1(args)
+        base = (lambda: cpu_baseline_mamba1(MAMBA1_CFG2))
+    else:
+        out = bench_ssd2(args)
+        base = (lambda: cpu_baseline_ssd2(SSD2_CFG1))
     if not args.no_cpu_baseline:
         log("cpu baseline")
-        out["cpu_baseline"] = cpu_baseline_ssd2(SSD2_CFG1)
+        out["cpu_baseline"] = base()
     print(json.dumps(out), flush=True)
 
 

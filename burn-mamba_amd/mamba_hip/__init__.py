@@ -6,4 +6,5 @@ library; nothing here computes on the CPU.
 """
 
 from ._lib import MambaHipError, exported_symbols, lib  # noqa: F401
+from .mamba1 import mamba1_scan, selective_scan  # noqa: F401
 from .ssd import Mamba2SsdInput, Mamba2SsdPath, ssd2_fast_path, ssd2_fwd  # noqa: F401

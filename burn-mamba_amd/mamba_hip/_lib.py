@@ -42,6 +42,23 @@ class Ssd2Args(ctypes.Structure):
     ]
 
 
+class Mamba1ScanArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", c_i32), ("dim", c_i32), ("seqlen", c_i32), ("dstate", c_i32),
+        ("u", c_vp), ("u_sb", c_i64), ("u_sd", c_i64), ("u_sl", c_i64),
+        ("delta", c_vp), ("delta_sb", c_i64), ("delta_sd", c_i64), ("delta_sl", c_i64),
+        ("A", c_vp), ("A_sd", c_i64), ("A_sn", c_i64),
+        ("B", c_vp), ("B_sb", c_i64), ("B_sn", c_i64), ("B_sl", c_i64),
+        ("C", c_vp), ("C_sb", c_i64), ("C_sn", c_i64), ("C_sl", c_i64),
+        ("D", c_vp),
+        ("z", c_vp), ("z_sb", c_i64), ("z_sd", c_i64), ("z_sl", c_i64),
+        ("delta_bias", c_vp), ("delta_softplus", c_i32),
+        ("initial_state", c_vp),
+        ("y", c_vp), ("y_sb", c_i64), ("y_sd", c_i64), ("y_sl", c_i64),
+        ("final_state", c_vp),
+    ]
+
+
 # name -> (argtypes, restype); the exported symbol set of include/mamba_hip.h
 _SIGNATURES = {
     "mamba_last_error": ([], ctypes.c_char_p),
@@ -52,6 +69,8 @@ _SIGNATURES = {
     "mamba_ssd2_fwd_generic": ([ctypes.POINTER(Ssd2Args), c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),
     "mamba_ssd2_fwd_timed": ([ctypes.POINTER(Ssd2Args), c_vp, ctypes.c_size_t, c_vp, c_vp, c_vp],
                              ctypes.c_int),
+    "mamba1_scan_fwd": ([ctypes.POINTER(Mamba1ScanArgs), c_vp], ctypes.c_int),
+    "mamba1_scan_fwd_timed": ([ctypes.POINTER(Mamba1ScanArgs), c_vp, c_vp, c_vp], ctypes.c_int),
 }
 
 _lib = None

@@ -115,6 +115,45 @@ int mamba_ssd2_fwd_generic(const mamba_ssd2_args* args, void* workspace, size_t 
 int mamba_ssd2_fwd_timed(const mamba_ssd2_args* args, void* workspace, size_t workspace_bytes,
                          mamba_stream_t stream, void* event_start, void* event_stop);
 
+/* ------------------------------------------------------------------------- */
+/* Mamba-1 selective scan (f32), with the optional dt bias + softplus of       */
+/* Mamba1::ssm and the silu(z) gate of Mamba1::forward:                        */
+/*                                                                             */
+/*   dl = softplus(delta + delta_bias)  (or delta as given)                   */
+/*   h[b,d,n] <- exp(dl A[d,n]) h[b,d,n] + dl B[b,n,t] u[b,d,t]                */
+/*   y[b,d,t]  = (sum_n C[b,n,t] h[b,d,n] + D[d] u[b,d,t]) * silu(z[b,d,t])    */
+/*                                                                             */
+/* Every tensor is addressed through element strides, so both the reference's */
+/* layouts (u,y [b,l,d]; delta [l,b,d]; B [b,l,n]; C [l,b,n]) and the         */
+/* channel-major [b,d,l] / [b,n,l] layouts are accepted.  softplus(x) is      */
+/* evaluated as x above 20 (where it equals x in f32); the reference's Burn   */
+/* softplus returns inf above ~88.7.  Replaces Mamba1::selective_scan         */
+/* (src/mamba1/mamba1.rs:422-523) and, with delta_bias/delta_softplus/z, the  */
+/* scan part of Mamba1::ssm + the gate of Mamba1::forward (mamba1.rs:348,      */
+/* 391-394).                                                                   */
+/* ------------------------------------------------------------------------- */
+typedef struct mamba1_scan_args {
+    int32_t batch, dim, seqlen, dstate;
+    const float* u;     int64_t u_sb, u_sd, u_sl;          /* [b, d, l]            */
+    const float* delta; int64_t delta_sb, delta_sd, delta_sl;
+    const float* A;     int64_t A_sd, A_sn;                /* [d, n]               */
+    const float* B;     int64_t B_sb, B_sn, B_sl;          /* [b, n, l]            */
+    const float* C;     int64_t C_sb, C_sn, C_sl;          /* [b, n, l]            */
+    const float* D;                                         /* [d] or NULL          */
+    const float* z;     int64_t z_sb, z_sd, z_sl;          /* [b, d, l] or NULL    */
+    const float* delta_bias;                                /* [d] or NULL          */
+    int32_t delta_softplus;                                 /* 0 or 1               */
+    const float* initial_state;                             /* [b, d, n] or NULL    */
+    float* y;           int64_t y_sb, y_sd, y_sl;          /* [b, d, l]            */
+    float* final_state;                                     /* [b, d, n] or NULL    */
+} mamba1_scan_args;
+
+int mamba1_scan_fwd(const mamba1_scan_args* args, mamba_stream_t stream);
+/* As mamba1_scan_fwd, recording the caller's HIP events around the scan      */
+/* kernel (benchmark timing; no counterpart in the reference).                */
+int mamba1_scan_fwd_timed(const mamba1_scan_args* args, mamba_stream_t stream, void* event_start,
+                          void* event_stop);
+
 #ifdef __cplusplus
 }
 #endif

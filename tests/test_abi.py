@@ -50,7 +50,8 @@ int main(void) {{ printf("%zu\\n", sizeof({struct_name})); {body} return 0; }}
     return [int(v) for v in out]
 
 
-@pytest.mark.parametrize("cls_name,c_name", [("Ssd2Args", "mamba_ssd2_args")])
+@pytest.mark.parametrize("cls_name,c_name", [("Ssd2Args", "mamba_ssd2_args"),
+                                             ("Mamba1ScanArgs", "mamba1_scan_args")])
 def test_struct_layouts_match_header(cls_name, c_name):
     from mamba_hip import _lib
     cls = getattr(_lib, cls_name)
