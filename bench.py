@@ -178,6 +178,142 @@ def bench_mamba1(args):
     }
 
 
+DECODE_CFG3 = dict(n_layers=64, d_model=2560, expand=2, headdim=64, dstate=128, ngroups=1, conv_kernel=4,
+                   batch=64)
+
+
+def _decode_model_cfg(cfg):
+    import mamba_hip
+    return mamba_hip.Mamba2Config(d_model=cfg["d_model"], expand=cfg["expand"], per_head_dim=cfg["headdim"],
+                                  state_rank=cfg["dstate"], ngroups=cfg["ngroups"],
+                                  conv_kernel=cfg["conv_kernel"])
+
+
+def decode_algorithmic(cfg):
+    """Compulsory HBM bytes of one decode step of the stack, and of one launch
+    of its state-update kernel.
+
+    Step: every layer's weights read once (in_proj/out_proj bf16, conv weight
+    and bias, dt_bias, A, D, both norm gammas f32), every layer's caches read
+    and written once (ssm_bhpr and conv_bvk, f32), the token in and the output
+    out (f32).  Kernel (one layer): its state tile read and written, its x-channel
+    conv windows read and written, the B/C windows read, the in_proj row read
+    (bf16), the gated values and per-head sums of squares written (f32)."""
+    c = _decode_model_cfg(cfg)
+    b, nl = cfg["batch"], cfg["n_layers"]
+    H, P, N, K = c.nheads, c.per_head_dim, c.state_rank, c.conv_kernel
+    weights = (c.d_model * c.d_in_proj + c.d_inner * c.d_model) * 2 + c.conv_dim * (K + 1) * 4 \
+        + 3 * H * 4 + c.d_inner * 4 + c.d_model * 4
+    caches = b * (H * P * N + c.conv_dim * K) * 4 * 2
+    step_bytes = nl * (weights + caches) + b * c.d_model * 4 * 2
+    kernel_bytes = b * (H * P * N * 4 * 2 + c.d_inner * K * 4 * 2 + 2 * c.ngroups * N * K * 4
+                        + c.d_in_proj * 2 + c.d_inner * 4 + H * 4)
+    return step_bytes, kernel_bytes, weights, caches
+
+
+def bench_decode(args):
+    import torch
+
+    import mamba_hip
+    cfg = dict(DECODE_CFG3)
+    cfg["batch"] = args.batch
+    c = _decode_model_cfg(cfg)
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    log(f"init {cfg['n_layers']} layers (bf16 weights, reference init)")
+    stack = mamba_hip.Mamba2Stack.init(c, cfg["n_layers"], dev, torch.bfloat16, gen)
+    b = cfg["batch"]
+    caches = stack.new_caches(b)
+    for cc in caches:  # pre-filled states: ssm ~ N(0, 0.1), conv windows ~ N(0, 1)
+        cc.ssm_bhpr.normal_(0.0, 0.1, generator=gen)
+        cc.conv_bvk.normal_(0.0, 1.0, generator=gen)
+    x_in = torch.randn((b, c.d_model), generator=gen, device=dev)
+    x_res = torch.empty_like(x_in)
+    stack.buffers(b, dev)
+
+    def eager(events=None):
+        x_res.copy_(x_in)
+        stack.step_(x_res, caches, events)
+
+    log("capture the 64-layer step in a HIP graph")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        eager()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        eager()
+
+    def step(events=None):
+        if events is None:
+            graph.replay()
+        else:
+            eager(events)
+
+    ms_per_step, kern_ms = _time_steps(args, step)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        eager()
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    step_bytes, kernel_bytes, weights, caches_b = decode_algorithmic(cfg)
+    achieved = kernel_bytes / (kern_ms * 1e-3) / 1e9
+    step_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
+    return {
+        "metric": f"decode step us at batch {b} (64-layer Mamba-2 2.7B-shaped stack, 1 GPU) + % HBM roofline",
+        "value": ms_per_step * 1e3, "unit": "us/step",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (BASELINE.json configs[3]: reference init, states ~N(0,0.1), seed 0)",
+        "config": {"workload": "mamba2_decode_step_cfg3", **cfg, "weights": "bf16", "state": "f32",
+                   "graph": "hip graph of the whole step", "eager_ms_per_step": eager_ms,
+                   "step_bytes": step_bytes, "step_hbm_gbs": step_gbs, "step_hbm_frac": step_gbs / HBM_PEAK_GBS,
+                   "entry": "mamba_rmsnorm + torch.mm + mamba2_step_ssm + torch.mm per layer"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel_ms": kern_ms,
+                     "algorithmic_bytes": kernel_bytes, "kernel": "step2_ssm_fast<128> (layer 0)"},
+    }
+
+
+def cpu_baseline_decode(cfg, budget_s=10.0, seed=0):
+    """The f32 CPU restatement of the pre-norm Layer around Mamba2::step
+    (oracle/, OpenMP over batch rows) at the same batch, run layer by layer
+    until ~budget_s of work, then scaled to the full stack depth."""
+    import numpy as np
+
+    import oracle
+    oracle.build()
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    c = _decode_model_cfg(cfg)
+    b = cfg["batch"]
+    rng = np.random.default_rng(seed)
+    f = np.float32
+    p = dict(pre_norm_w=np.ones(c.d_model, f),
+             w_in=rng.uniform(-1, 1, (c.d_model, c.d_in_proj)).astype(f) / np.sqrt(c.d_model).astype(f),
+             conv_w=rng.uniform(-0.5, 0.5, (c.conv_dim, c.conv_kernel)).astype(f),
+             conv_b=rng.uniform(-0.5, 0.5, c.conv_dim).astype(f),
+             dt_bias=np.full(c.nheads, -4.0, f), A=-rng.uniform(1, 16, c.nheads).astype(f),
+             D=np.ones(c.nheads, f), norm_w=np.ones(c.d_inner, f),
+             w_out=rng.uniform(-1, 1, (c.d_inner, c.d_model)).astype(f) / np.sqrt(c.d_inner).astype(f))
+    conv = rng.standard_normal((b, c.conv_dim, c.conv_kernel)).astype(f)
+    ssm = (0.1 * rng.standard_normal((b, c.nheads, c.per_head_dim, c.state_rank))).astype(f)
+    u = rng.standard_normal((b, c.d_model)).astype(f)
+    cd = dict(nheads=c.nheads, headdim=c.per_head_dim, ngroups=c.ngroups, dstate=c.state_rank)
+    layers, el = 0, 0.0
+    while el < budget_s and layers < cfg["n_layers"]:
+        t0 = time.perf_counter()
+        u, conv, ssm = oracle.mamba2_layer_step(u, p, conv, ssm, cd, prec=32)
+        el += time.perf_counter() - t0
+        layers += 1
+    us = el / layers * cfg["n_layers"] * 1e6
+    return {"value": us, "unit": "us/step", "cores": threads, "kind": "port",
+            "sample": f"{layers} of {cfg['n_layers']} layers at batch {b} ({el:.1f} s), scaled to the full "
+                      f"stack; f32 restatement of RmsNorm + Mamba2::step + residual"}
+
+
 def _time_steps(args, step):
     """W untimed steps, then K timed back-to-back steps between synchronisations
     (ms/step), then K steps with the library's events around the dominant
@@ -265,7 +401,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="ssd2", choices=["ssd2", "mamba1"])
+    ap.add_argument("--workload", default="ssd2", choices=["ssd2", "mamba1", "decode"])
+    ap.add_argument("--batch", type=int, default=DECODE_CFG3["batch"], help="decode batch")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -273,7 +410,10 @@ def main():
               "(the hot path shards by batch/head with no communication; see DESIGN.md)",
               file=sys.stderr)
         sys.exit(2)
-    if args.workload == "mamba1":
+    if args.workload == "decode":
+        out = bench_decode(args)
+        base = (lambda: cpu_baseline_decode(dict(DECODE_CFG3, batch=args.batch)))
+    elif args.workload == "mamba1":
         out = bench_mamba1(args)
         base = (lambda: cpu_baseline_mamba1(MAMBA1_CFG2))
     else:

@@ -1,0 +1,426 @@
+// Mamba-2 recurrent decode step for gfx950: the part of Mamba2::step between
+// in_proj and out_proj (burn-mamba src/mamba2/mamba2.rs:857-995), plus the
+// residual + RmsNorm of the pre-norm Layer (src/modules/layer.rs:224-232).
+//
+// The step is HBM-bound: per token and head it streams the f32 state
+// [headdim, dstate] in and out once (64 KB at P=64, N=128) and does ~6 flops
+// per state element, so there is no MFMA here.  Two kernels per call:
+//
+//   step2_ssm_*     one workgroup per (batch row, head).  Issues the state
+//                   loads first, then slides this head's x-channel conv
+//                   windows in place and convolves the group's B/C channels
+//                   from their (old) windows, updates the state with
+//                   coalesced float4 traffic, reduces y = sum_n h C across the
+//                   lanes of each state row with a reduce-scatter (8 partial
+//                   rows per lane -> one), gates by z, and writes the gated
+//                   values plus a per-(row, head) sum of squares to the
+//                   workspace.
+//   step2_finish    one workgroup per (1024-channel slice, batch row):
+//                   finishes the row's RMS from the per-head partials and
+//                   writes out; slice 0 also slides the shared B/C conv
+//                   windows.  That slide cannot live in step2_ssm: every head
+//                   of a group reads the old B/C window, and kernel order on
+//                   the stream is what makes the in-place update safe.
+//
+// HBM layout: the caches are the reference's Mamba2Cache tensors unchanged
+// (conv_bvk [b, conv_dim, K] f32 and ssm_bhpr [b, H, P, N] f32, cache.rs:98-122),
+// so a state tile of one (b, h) is one contiguous P*N*4-byte block.
+#include "common.h"
+
+namespace mamba {
+
+struct Step2Params {
+    int nb, H, P, G, N, K, d_inner, conv_dim, hpg;
+    bool zx_bf16, out_bf16, norm_before_gate;
+    const void* zx; int64_t zx_sb;
+    float* conv; const float* conv_w; const float* conv_b;
+    const float* dt_bias; const float* A; const float* Dv;
+    float dt_lo, dt_hi;
+    const float* norm_w;
+    float* ssm;
+    void* out; int64_t out_sb;
+    float* g_ws;    // [nb, d_inner]  gated (or raw, if norm_before_gate) y
+    float* ssq_ws;  // [nb, H]        sum of squares of g_ws per head
+};
+
+__device__ __forceinline__ float ld_act(const void* base, int64_t i, bool bf16) {
+    return bf16 ? bf16_to_f32(static_cast<const bf16_t*>(base)[i]) : static_cast<const float*>(base)[i];
+}
+
+__device__ __forceinline__ float silu_fast(float x) { return x / (__expf(-x) + 1.f); }
+
+// dt = clamp(softplus(dt_raw + dt_bias), lo, hi), mamba2.rs:924 with the f32
+// softplus threshold of src/modules/activation/softplus.rs:21-47.
+__device__ __forceinline__ float step_dt(const Step2Params& p, const void* zrow, int h) {
+    float v = ld_act(zrow, p.d_inner + p.conv_dim + h, p.zx_bf16);
+    if (p.dt_bias) v += p.dt_bias[h];
+    float dt = v > 18.f ? v : log1pf(__expf(v));
+    return fminf(fmaxf(dt, p.dt_lo), p.dt_hi);
+}
+
+// Sum over the 256 threads of a workgroup; every thread gets the result.
+__device__ __forceinline__ float block_sum_256(float v, float* s_red) {
+    v = wave_sum(v);
+    const int wave = threadIdx.x >> 6;
+    __syncthreads();  // s_red may still be read by a previous call
+    if ((threadIdx.x & 63) == 0) s_red[wave] = v;
+    __syncthreads();
+    return s_red[0] + s_red[1] + s_red[2] + s_red[3];
+}
+
+// ---------------------------------------------------------------------------
+// Fast path: headdim 64, dstate N in {64, 128}, conv width 4, 256 threads.
+// Thread t owns float4 column n4 = t % (N/4) of rows row0 + i*RPI, i < R.
+// ---------------------------------------------------------------------------
+template <int N>
+__global__ __launch_bounds__(256) void step2_ssm_fast(Step2Params p) {
+    constexpr int P = 64;
+    constexpr int LPR = N / 4;      // lanes per state row
+    constexpr int RPI = 256 / LPR;  // rows covered by one pass of the workgroup
+    constexpr int R = P / RPI;      // float4 per thread (= LPR / 4)
+    static_assert(R * 4 == LPR, "reduce-scatter assumes R = LPR / 4");
+    __shared__ float s_x[P];
+    __shared__ __align__(16) float s_B[N];
+    __shared__ __align__(16) float s_C[N];
+    __shared__ float s_red[4];
+
+    const int t = threadIdx.x;
+    const int bh = blockIdx.x;
+    const int b = bh / p.H, h = bh - b * p.H;
+    const int g = h / p.hpg;
+    const int n4 = t % LPR, row0 = t / LPR;
+
+    // 1. state tile loads first: they are the bytes that matter
+    float4* st = reinterpret_cast<float4*>(p.ssm) + (int64_t)bh * (P * LPR);
+    float4 hv[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) hv[i] = st[(row0 + i * RPI) * LPR + n4];
+
+    // 2. causal conv, one channel per thread (mamba2.rs:865-902)
+    const char* zrow = static_cast<const char*>(p.zx) + b * p.zx_sb * (p.zx_bf16 ? 2 : 4);
+    float4* win_base = reinterpret_cast<float4*>(p.conv) + (int64_t)b * p.conv_dim;
+    const float4* cw = reinterpret_cast<const float4*>(p.conv_w);
+    for (int c = t; c < P + 2 * N; c += 256) {
+        int ch;
+        if (c < P) ch = h * P + c;
+        else if (c < P + N) ch = p.d_inner + g * N + (c - P);
+        else ch = p.d_inner + (p.G + g) * N + (c - P - N);
+        const float4 win = win_base[ch];
+        const float4 w = cw[ch];
+        const float xin = ld_act(zrow, p.d_inner + ch, p.zx_bf16);
+        float acc = win.y * w.x;
+        acc += win.z * w.y;
+        acc += win.w * w.z;
+        acc += xin * w.w;
+        if (p.conv_b) acc += p.conv_b[ch];
+        const float v = silu_fast(acc);
+        if (c < P) {
+            s_x[c] = v;
+            win_base[ch] = make_float4(win.y, win.z, win.w, xin);
+        } else if (c < P + N) {
+            s_B[c - P] = v;
+        } else {
+            s_C[c - P - N] = v;
+        }
+    }
+    const float dt = step_dt(p, zrow, h);
+    const float dA = __expf(dt * p.A[h]);
+    const float Dh = p.Dv ? p.Dv[h] : 0.f;
+    __syncthreads();
+
+    // 3. h <- h dA + (dt B) x ; partial y per row over this lane's 4 states
+    const float4 B4 = reinterpret_cast<const float4*>(s_B)[n4];
+    const float4 C4 = reinterpret_cast<const float4*>(s_C)[n4];
+    const float4 dB = make_float4(dt * B4.x, dt * B4.y, dt * B4.z, dt * B4.w);
+    float v[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        const float xv = s_x[row0 + i * RPI];
+        float4 hn;
+        hn.x = hv[i].x * dA + dB.x * xv;
+        hn.y = hv[i].y * dA + dB.y * xv;
+        hn.z = hv[i].z * dA + dB.z * xv;
+        hn.w = hv[i].w * dA + dB.w * xv;
+        st[(row0 + i * RPI) * LPR + n4] = hn;
+        v[i] = hn.x * C4.x + hn.y * C4.y + hn.z * C4.z + hn.w * C4.w;
+    }
+
+    // 4. reduce-scatter over the LPR lanes of each row group: at xor distance
+    //    s the lane with bit s set keeps the upper half of its partials.  After
+    //    log2(R) steps lane n4 holds row index (n4 >> 2), summed over 8 lanes;
+    //    two more butterflies finish the sum over all LPR lanes.
+#pragma unroll
+    for (int half = R / 2, s = 2 * R; half >= 1; half >>= 1, s >>= 1) {
+        const bool up = (n4 & s) != 0;
+#pragma unroll
+        for (int j = 0; j < half; ++j) {
+            const float keep = up ? v[j + half] : v[j];
+            const float send = up ? v[j] : v[j + half];
+            v[j] = keep + __shfl_xor(send, s, 64);
+        }
+    }
+    float ysum = v[0];
+    ysum += __shfl_xor(ysum, 2, 64);
+    ysum += __shfl_xor(ysum, 1, 64);
+
+    // 5. y = C.h + D x, gate, write gated value and its square
+    float sq = 0.f;
+    if ((n4 & 3) == 0) {
+        const int pr = row0 + (n4 >> 2) * RPI;
+        const float y = ysum + Dh * s_x[pr];
+        float gv = y;
+        if (!p.norm_before_gate) gv *= silu_fast(ld_act(zrow, h * P + pr, p.zx_bf16));
+        p.g_ws[(int64_t)b * p.d_inner + h * P + pr] = gv;
+        sq = gv * gv;
+    }
+    sq = block_sum_256(sq, s_red);
+    if (t == 0) p.ssq_ws[bh] = sq;
+}
+
+// ---------------------------------------------------------------------------
+// Shape-generic path: any headdim/dstate/conv width; one workgroup per
+// (batch row, head), rows over waves, states over lanes.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void step2_ssm_generic(Step2Params p) {
+    extern __shared__ float s_dyn[];  // [P + 2N]
+    __shared__ float s_red[4];
+    float* s_x = s_dyn;
+    float* s_B = s_dyn + p.P;
+    float* s_C = s_B + p.N;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int bh = blockIdx.x;
+    const int b = bh / p.H, h = bh - b * p.H;
+    const int g = h / p.hpg;
+    const int P = p.P, N = p.N, K = p.K;
+    const char* zrow = static_cast<const char*>(p.zx) + b * p.zx_sb * (p.zx_bf16 ? 2 : 4);
+    for (int c = t; c < P + 2 * N; c += 256) {
+        int ch;
+        if (c < P) ch = h * P + c;
+        else if (c < P + N) ch = p.d_inner + g * N + (c - P);
+        else ch = p.d_inner + (p.G + g) * N + (c - P - N);
+        float* win = p.conv + ((int64_t)b * p.conv_dim + ch) * K;
+        const float* w = p.conv_w + (int64_t)ch * K;
+        const float xin = ld_act(zrow, p.d_inner + ch, p.zx_bf16);
+        float acc = 0.f;
+        for (int k = 0; k + 1 < K; ++k) acc += win[k + 1] * w[k];
+        acc += xin * w[K - 1];
+        if (p.conv_b) acc += p.conv_b[ch];
+        const float v = silu_fast(acc);
+        if (c < P) {
+            s_x[c] = v;
+            for (int k = 0; k + 1 < K; ++k) win[k] = win[k + 1];
+            win[K - 1] = xin;
+        } else if (c < P + N) {
+            s_B[c - P] = v;
+        } else {
+            s_C[c - P - N] = v;
+        }
+    }
+    const float dt = step_dt(p, zrow, h);
+    const float dA = __expf(dt * p.A[h]);
+    const float Dh = p.Dv ? p.Dv[h] : 0.f;
+    __syncthreads();
+    float sq = 0.f;
+    for (int pr = wave; pr < P; pr += 4) {
+        float* row = p.ssm + ((int64_t)bh * P + pr) * N;
+        const float xv = s_x[pr];
+        float acc = 0.f;
+        for (int n = lane; n < N; n += 64) {
+            const float hn = row[n] * dA + (dt * s_B[n]) * xv;
+            row[n] = hn;
+            acc += hn * s_C[n];
+        }
+        acc = wave_sum(acc);
+        if (lane == 0) {
+            const float y = acc + Dh * xv;
+            float gv = y;
+            if (!p.norm_before_gate) gv *= silu_fast(ld_act(zrow, h * P + pr, p.zx_bf16));
+            p.g_ws[(int64_t)b * p.d_inner + h * P + pr] = gv;
+            sq += gv * gv;
+        }
+    }
+    sq = block_sum_256(sq, s_red);
+    if (t == 0) p.ssq_ws[bh] = sq;
+}
+
+// ---------------------------------------------------------------------------
+// Row RMS + normalisation (rms_norm_gated.rs:70-135) and the B/C window slide.
+// grid (ceil(d_inner / 1024), nb), 256 threads.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void step2_finish(Step2Params p) {
+    __shared__ float s_red[4];
+    const int b = blockIdx.y, t = threadIdx.x;
+    float s = 0.f;
+    for (int i = t; i < p.H; i += 256) s += p.ssq_ws[(int64_t)b * p.H + i];
+    s = block_sum_256(s, s_red);
+    const float rms = sqrtf(s / (float)p.d_inner + kDivEpsF32);
+    const char* zrow = static_cast<const char*>(p.zx) + b * p.zx_sb * (p.zx_bf16 ? 2 : 4);
+    const int i0 = blockIdx.x * 1024;
+    const int i1 = min(p.d_inner, i0 + 1024);
+    for (int i = i0 + t; i < i1; i += 256) {
+        float v = (p.g_ws[(int64_t)b * p.d_inner + i] / rms) * p.norm_w[i];
+        if (p.norm_before_gate) v *= silu_fast(ld_act(zrow, i, p.zx_bf16));
+        if (p.out_bf16)
+            static_cast<bf16_t*>(p.out)[b * p.out_sb + i] = f32_to_bf16(v);
+        else
+            static_cast<float*>(p.out)[b * p.out_sb + i] = v;
+    }
+    if (blockIdx.x == 0) {
+        const int nbc = 2 * p.G * p.N;
+        for (int c = t; c < nbc; c += 256) {
+            const int ch = p.d_inner + c;
+            float* win = p.conv + ((int64_t)b * p.conv_dim + ch) * p.K;
+            const float xin = ld_act(zrow, p.d_inner + ch, p.zx_bf16);
+            for (int k = 0; k + 1 < p.K; ++k) win[k] = win[k + 1];
+            win[p.K - 1] = xin;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Residual add + RmsNorm: one workgroup per row.
+// ---------------------------------------------------------------------------
+struct RmsParams {
+    int rows, cols;
+    bool add_bf16, out_bf16;
+    float* x; int64_t x_sr;
+    const void* add; int64_t add_sr;
+    const float* w;
+    void* out; int64_t out_sr;
+};
+
+__global__ __launch_bounds__(256) void rmsnorm_residual(RmsParams p) {
+    __shared__ float s_red[4];
+    const int r = blockIdx.x, t = threadIdx.x;
+    float* x = p.x + (int64_t)r * p.x_sr;
+    float ss = 0.f;
+    for (int c = t; c < p.cols; c += 256) {
+        float v = x[c];
+        if (p.add) {
+            v += ld_act(p.add, (int64_t)r * p.add_sr + c, p.add_bf16);
+            x[c] = v;
+        }
+        ss += v * v;
+    }
+    if (!p.out) return;
+    ss = block_sum_256(ss, s_red);
+    const float rms = sqrtf(ss / (float)p.cols + kDivEpsF32);
+    for (int c = t; c < p.cols; c += 256) {
+        const float v = (x[c] / rms) * p.w[c];
+        if (p.out_bf16)
+            static_cast<bf16_t*>(p.out)[(int64_t)r * p.out_sr + c] = f32_to_bf16(v);
+        else
+            static_cast<float*>(p.out)[(int64_t)r * p.out_sr + c] = v;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+static size_t step2_ws_bytes(const mamba2_step_args* a) {
+    const size_t d_inner = (size_t)a->nheads * a->headdim;
+    return align_up((size_t)a->batch * d_inner * 4, 256) + align_up((size_t)a->batch * a->nheads * 4, 256);
+}
+
+static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
+
+static int step2_make_params(const mamba2_step_args* a, void* ws, size_t ws_bytes, Step2Params* out) {
+    MAMBA_CHECK_ARG(a != nullptr, "args is NULL");
+    MAMBA_CHECK_ARG(a->batch > 0 && a->nheads > 0 && a->headdim > 0 && a->ngroups > 0 && a->dstate > 0,
+                    "batch, nheads, headdim, ngroups and dstate must be >= 1");
+    MAMBA_CHECK_ARG(a->nheads % a->ngroups == 0, "nheads must be divisible by ngroups");
+    MAMBA_CHECK_ARG(a->conv_kernel >= 1 && a->conv_kernel <= 16, "conv_kernel must be in [1, 16]");
+    MAMBA_CHECK_ARG(a->zxbcdt_dtype == MAMBA_F32 || a->zxbcdt_dtype == MAMBA_BF16, "bad zxbcdt_dtype");
+    MAMBA_CHECK_ARG(a->out_dtype == MAMBA_F32 || a->out_dtype == MAMBA_BF16, "bad out_dtype");
+    MAMBA_CHECK_ARG(a->zxbcdt && a->conv_state && a->conv_w && a->A && a->norm_w && a->ssm_state && a->out,
+                    "zxbcdt, conv_state, conv_w, A, norm_w, ssm_state and out are required");
+    const int64_t d_inner = (int64_t)a->nheads * a->headdim;
+    const int64_t conv_dim = d_inner + 2ll * a->ngroups * a->dstate;
+    MAMBA_CHECK_ARG(d_inner + conv_dim + a->nheads < (1ll << 30), "row too long");
+    MAMBA_CHECK_ARG(a->zxbcdt_sb >= d_inner + conv_dim + a->nheads, "zxbcdt_sb shorter than a row");
+    MAMBA_CHECK_ARG(a->out_sb >= d_inner, "out_sb shorter than a row");
+    MAMBA_CHECK_ARG(!(a->dt_min > a->dt_max), "dt_min > dt_max");
+    const size_t need = step2_ws_bytes(a);
+    if (ws == nullptr || ws_bytes < need) {
+        set_error("mamba2_step_ssm: workspace of " + std::to_string(need) + " bytes required, got " +
+                  std::to_string(ws == nullptr ? 0 : ws_bytes));
+        return MAMBA_ERR_WORKSPACE;
+    }
+    Step2Params& p = *out;
+    p.nb = a->batch; p.H = a->nheads; p.P = a->headdim; p.G = a->ngroups; p.N = a->dstate;
+    p.K = a->conv_kernel; p.d_inner = (int)d_inner; p.conv_dim = (int)conv_dim; p.hpg = p.H / p.G;
+    p.zx_bf16 = a->zxbcdt_dtype == MAMBA_BF16; p.out_bf16 = a->out_dtype == MAMBA_BF16;
+    p.norm_before_gate = a->norm_before_gate != 0;
+    p.zx = a->zxbcdt; p.zx_sb = a->zxbcdt_sb;
+    p.conv = a->conv_state; p.conv_w = a->conv_w; p.conv_b = a->conv_b;
+    p.dt_bias = a->dt_bias; p.A = a->A; p.Dv = a->D;
+    p.dt_lo = a->dt_min; p.dt_hi = a->dt_max;
+    p.norm_w = a->norm_w; p.ssm = a->ssm_state;
+    p.out = a->out; p.out_sb = a->out_sb;
+    p.g_ws = static_cast<float*>(ws);
+    p.ssq_ws = reinterpret_cast<float*>(static_cast<char*>(ws) + align_up((size_t)p.nb * d_inner * 4, 256));
+    return MAMBA_OK;
+}
+
+static int step2_dispatch(const mamba2_step_args* a, void* ws, size_t ws_bytes, hipStream_t stream,
+                          hipEvent_t ev0, hipEvent_t ev1) {
+    Step2Params p;
+    int st = step2_make_params(a, ws, ws_bytes, &p);
+    if (st != MAMBA_OK) return st;
+    const bool fast = p.P == 64 && (p.N == 64 || p.N == 128) && p.K == 4 && aligned16(p.ssm) &&
+                      aligned16(p.conv) && aligned16(p.conv_w);
+    const dim3 grid(p.nb * p.H);
+    if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, stream));
+    if (fast && p.N == 128)
+        hipLaunchKernelGGL(step2_ssm_fast<128>, grid, dim3(256), 0, stream, p);
+    else if (fast)
+        hipLaunchKernelGGL(step2_ssm_fast<64>, grid, dim3(256), 0, stream, p);
+    else
+        hipLaunchKernelGGL(step2_ssm_generic, grid, dim3(256), (p.P + 2 * p.N) * sizeof(float), stream, p);
+    MAMBA_CHECK_LAUNCH();
+    if (ev1) MAMBA_CHECK_HIP(hipEventRecord(ev1, stream));
+    hipLaunchKernelGGL(step2_finish, dim3(ceil_div(p.d_inner, 1024), p.nb), dim3(256), 0, stream, p);
+    MAMBA_CHECK_LAUNCH();
+    return MAMBA_OK;
+}
+
+}  // namespace mamba
+
+using namespace mamba;
+
+extern "C" size_t mamba2_step_workspace_size(const mamba2_step_args* a) {
+    return a ? step2_ws_bytes(a) : 0;
+}
+
+extern "C" int mamba2_step_ssm(const mamba2_step_args* a, void* ws, size_t ws_bytes, mamba_stream_t stream) {
+    return step2_dispatch(a, ws, ws_bytes, (hipStream_t)stream, nullptr, nullptr);
+}
+
+extern "C" int mamba2_step_ssm_timed(const mamba2_step_args* a, void* ws, size_t ws_bytes,
+                                     mamba_stream_t stream, void* ev_start, void* ev_stop) {
+    if (ev_start == nullptr || ev_stop == nullptr) {
+        set_error("mamba2_step_ssm_timed: both events are required");
+        return MAMBA_ERR_INVALID_ARG;
+    }
+    return step2_dispatch(a, ws, ws_bytes, (hipStream_t)stream, (hipEvent_t)ev_start, (hipEvent_t)ev_stop);
+}
+
+extern "C" int mamba_rmsnorm(const mamba_rmsnorm_args* a, mamba_stream_t stream) {
+    MAMBA_CHECK_ARG(a != nullptr, "args is NULL");
+    MAMBA_CHECK_ARG(a->rows > 0 && a->cols > 0, "rows and cols must be >= 1");
+    MAMBA_CHECK_ARG(a->x != nullptr, "x is required");
+    MAMBA_CHECK_ARG(a->add || a->out, "nothing to do: add and out are both NULL");
+    MAMBA_CHECK_ARG(!a->out || a->weight, "weight is required with out");
+    MAMBA_CHECK_ARG(a->add_dtype == MAMBA_F32 || a->add_dtype == MAMBA_BF16, "bad add_dtype");
+    MAMBA_CHECK_ARG(a->out_dtype == MAMBA_F32 || a->out_dtype == MAMBA_BF16, "bad out_dtype");
+    MAMBA_CHECK_ARG(a->x_sr >= a->cols && (!a->add || a->add_sr >= a->cols) && (!a->out || a->out_sr >= a->cols),
+                    "row strides shorter than cols");
+    RmsParams p;
+    p.rows = a->rows; p.cols = a->cols;
+    p.add_bf16 = a->add_dtype == MAMBA_BF16; p.out_bf16 = a->out_dtype == MAMBA_BF16;
+    p.x = a->x; p.x_sr = a->x_sr; p.add = a->add; p.add_sr = a->add_sr;
+    p.w = a->weight; p.out = a->out; p.out_sr = a->out_sr;
+    hipLaunchKernelGGL(rmsnorm_residual, dim3(p.rows), dim3(256), 0, (hipStream_t)stream, p);
+    MAMBA_CHECK_LAUNCH();
+    return MAMBA_OK;
+}

@@ -59,6 +59,30 @@ class Mamba1ScanArgs(ctypes.Structure):
     ]
 
 
+class Mamba2StepArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", c_i32), ("nheads", c_i32), ("headdim", c_i32), ("ngroups", c_i32),
+        ("dstate", c_i32), ("conv_kernel", c_i32),
+        ("zxbcdt_dtype", c_i32), ("out_dtype", c_i32), ("norm_before_gate", c_i32),
+        ("zxbcdt", c_vp), ("zxbcdt_sb", c_i64),
+        ("conv_state", c_vp), ("conv_w", c_vp), ("conv_b", c_vp),
+        ("dt_bias", c_vp), ("A", c_vp), ("D", c_vp),
+        ("dt_min", ctypes.c_float), ("dt_max", ctypes.c_float),
+        ("norm_w", c_vp), ("ssm_state", c_vp),
+        ("out", c_vp), ("out_sb", c_i64),
+    ]
+
+
+class RmsNormArgs(ctypes.Structure):
+    _fields_ = [
+        ("rows", c_i32), ("cols", c_i32), ("add_dtype", c_i32), ("out_dtype", c_i32),
+        ("x", c_vp), ("x_sr", c_i64),
+        ("add", c_vp), ("add_sr", c_i64),
+        ("weight", c_vp),
+        ("out", c_vp), ("out_sr", c_i64),
+    ]
+
+
 # name -> (argtypes, restype); the exported symbol set of include/mamba_hip.h
 _SIGNATURES = {
     "mamba_last_error": ([], ctypes.c_char_p),
@@ -71,6 +95,11 @@ _SIGNATURES = {
                              ctypes.c_int),
     "mamba1_scan_fwd": ([ctypes.POINTER(Mamba1ScanArgs), c_vp], ctypes.c_int),
     "mamba1_scan_fwd_timed": ([ctypes.POINTER(Mamba1ScanArgs), c_vp, c_vp, c_vp], ctypes.c_int),
+    "mamba2_step_workspace_size": ([ctypes.POINTER(Mamba2StepArgs)], ctypes.c_size_t),
+    "mamba2_step_ssm": ([ctypes.POINTER(Mamba2StepArgs), c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),
+    "mamba2_step_ssm_timed": ([ctypes.POINTER(Mamba2StepArgs), c_vp, ctypes.c_size_t, c_vp, c_vp, c_vp],
+                              ctypes.c_int),
+    "mamba_rmsnorm": ([ctypes.POINTER(RmsNormArgs), c_vp], ctypes.c_int),
 }
 
 _lib = None

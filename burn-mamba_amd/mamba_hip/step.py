@@ -1,0 +1,317 @@
+"""Mamba-2 recurrent decode step, mirroring the reference's block signatures.
+
+Reference:
+  * ``Mamba2::step(input_bm, Option<Mamba2Cache>) -> (out_bm, Mamba2Cache)``
+    (src/mamba2/mamba2.rs:820-1004)
+  * ``Mamba2Cache { conv_bvk, ssm_bhpr }`` (src/mamba2/cache.rs:98-122)
+  * ``Mamba2Config`` defaults and ``init`` (src/mamba2/mamba2.rs:250-505)
+  * the pre-norm ``Layer::step_one`` (src/modules/layer.rs:224-232):
+    ``x + block_step(RmsNorm(x))``.
+
+The in_proj / out_proj products run on the ROCm BLAS through ``torch.mm``
+(plain library GEMMs); everything between them (conv window, softplus, state
+update, readout, gated RMSNorm) is one ``mamba2_step_ssm`` call into
+libmamba_hip.so, and the residual + pre-norm is one ``mamba_rmsnorm`` call.
+Nothing here computes on the CPU; a missing library raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass, field
+from typing import List, Optional, Tuple
+
+import torch
+
+from . import _lib
+from ._lib import Mamba2StepArgs, RmsNormArgs, check
+from .ssd import _dtype_code, _raw_events, _stream
+
+
+@dataclass
+class Mamba2Cache:
+    """conv_bvk [batch, conv_dim, conv_kernel] and ssm_bhpr [batch, nheads, headdim, dstate], f32."""
+    conv_bvk: torch.Tensor
+    ssm_bhpr: torch.Tensor
+
+
+@dataclass
+class Mamba2Config:
+    """Mamba2Config (src/mamba2/mamba2.rs:250-330) with the reference defaults."""
+    d_model: int
+    state_rank: int = 128
+    conv_kernel: int = 4
+    expand: int = 2
+    per_head_dim: int = 64
+    ngroups: int = 1
+    a_init_range: Tuple[float, float] = (1.0, 16.0)
+    is_norm_before_gate: bool = False
+    dt_min: float = 1e-3
+    dt_max: float = 0.1
+    dt_init_floor: float = 1e-4
+    dt_limit: Tuple[float, float] = (0.0, 6.5504e4)
+    has_proj_bias: bool = False
+    has_conv_bias: bool = True
+
+    @property
+    def d_inner(self) -> int:
+        return self.expand * self.d_model
+
+    @property
+    def nheads(self) -> int:
+        return self.d_inner // self.per_head_dim
+
+    @property
+    def conv_dim(self) -> int:
+        return self.d_inner + 2 * self.ngroups * self.state_rank
+
+    @property
+    def d_in_proj(self) -> int:
+        return self.d_inner + self.conv_dim + self.nheads
+
+    def init(self, device, dtype=torch.bfloat16, generator: Optional[torch.Generator] = None) -> "Mamba2":
+        """Random init following Mamba2Config::init (mamba2.rs:391-505).
+
+        Projection weights are stored in ``dtype`` ([d_in, d_out], Burn's Linear
+        layout); the per-channel parameters stay f32.  Values are drawn on the
+        generator's device (CPU when no generator is given)."""
+        assert self.nheads * self.per_head_dim == self.d_inner and self.nheads % self.ngroups == 0
+        g = generator
+        gdev = g.device if g is not None else torch.device("cpu")
+
+        def rand(shape):
+            return torch.rand(shape, generator=g, device=gdev, dtype=torch.float32)
+
+        def uni(shape, fan_in):
+            bound = 1.0 / math.sqrt(fan_in)
+            return (rand(shape) * 2 - 1) * bound
+
+        H = self.nheads
+        in_w = uni((self.d_model, self.d_in_proj), self.d_model)
+        conv_w = uni((self.conv_dim, self.conv_kernel), self.conv_kernel)
+        conv_b = uni((self.conv_dim,), self.conv_kernel) if self.has_conv_bias else None
+        lo, hi = math.log(self.dt_min), math.log(self.dt_max)
+        dt = torch.exp(rand(H).double() * (hi - lo) + lo)
+        dt = dt.clamp(min=self.dt_init_floor)
+        dt_bias = dt + torch.log(-torch.expm1(-dt))
+        a0, a1 = self.a_init_range
+        a_log = torch.log(rand(H).double() * (a1 - a0) + a0)
+        out_w = uni((self.d_inner, self.d_model), self.d_inner)
+        f32 = dict(device=device, dtype=torch.float32)
+        return Mamba2(
+            cfg=self,
+            in_proj_w=in_w.to(device=device, dtype=dtype),
+            in_proj_b=torch.zeros(self.d_in_proj, device=device, dtype=dtype) if self.has_proj_bias else None,
+            conv_w=conv_w.to(**f32),
+            conv_b=None if conv_b is None else conv_b.to(**f32),
+            dt_bias=dt_bias.to(**f32),
+            a_log=a_log.to(**f32),
+            d=torch.ones(H, **f32),
+            norm_w=torch.ones(self.d_inner, **f32),
+            out_proj_w=out_w.to(device=device, dtype=dtype),
+            out_proj_b=torch.zeros(self.d_model, device=device, dtype=dtype) if self.has_proj_bias else None,
+        )
+
+
+def step_ssm_args(cfg: Mamba2Config, zxbcdt: torch.Tensor, cache: Mamba2Cache, conv_w, conv_b, dt_bias,
+                  A, D, norm_w, out: torch.Tensor) -> Mamba2StepArgs:
+    b = zxbcdt.shape[0]
+    if zxbcdt.stride(-1) != 1 or out.stride(-1) != 1:
+        raise _lib.MambaHipError("zxbcdt and out need a contiguous last axis")
+    for t, nm in ((cache.conv_bvk, "conv_bvk"), (cache.ssm_bhpr, "ssm_bhpr"), (conv_w, "conv_w")):
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            raise _lib.MambaHipError(f"{nm} must be contiguous float32")
+    if tuple(cache.ssm_bhpr.shape) != (b, cfg.nheads, cfg.per_head_dim, cfg.state_rank):
+        raise _lib.MambaHipError(f"ssm_bhpr shape {tuple(cache.ssm_bhpr.shape)} does not match the config")
+    if tuple(cache.conv_bvk.shape) != (b, cfg.conv_dim, cfg.conv_kernel):
+        raise _lib.MambaHipError(f"conv_bvk shape {tuple(cache.conv_bvk.shape)} does not match the config")
+    if zxbcdt.shape[1] != cfg.d_in_proj or out.shape != (b, cfg.d_inner):
+        raise _lib.MambaHipError("zxbcdt / out shapes do not match the config")
+    a = Mamba2StepArgs()
+    a.batch, a.nheads, a.headdim = b, cfg.nheads, cfg.per_head_dim
+    a.ngroups, a.dstate, a.conv_kernel = cfg.ngroups, cfg.state_rank, cfg.conv_kernel
+    a.zxbcdt_dtype, a.out_dtype = _dtype_code(zxbcdt), _dtype_code(out)
+    a.norm_before_gate = int(cfg.is_norm_before_gate)
+    a.zxbcdt, a.zxbcdt_sb = zxbcdt.data_ptr(), zxbcdt.stride(0)
+    a.conv_state, a.conv_w = cache.conv_bvk.data_ptr(), conv_w.data_ptr()
+    a.conv_b = None if conv_b is None else conv_b.data_ptr()
+    a.dt_bias = None if dt_bias is None else dt_bias.data_ptr()
+    a.A = A.data_ptr()
+    a.D = None if D is None else D.data_ptr()
+    a.dt_min, a.dt_max = float(cfg.dt_limit[0]), float(cfg.dt_limit[1])
+    a.norm_w, a.ssm_state = norm_w.data_ptr(), cache.ssm_bhpr.data_ptr()
+    a.out, a.out_sb = out.data_ptr(), out.stride(0)
+    return a
+
+
+def step_ssm(args: Mamba2StepArgs, workspace: torch.Tensor, events=None):
+    """One mamba2_step_ssm call on the current stream (workspace: uint8 device buffer).
+
+    ``events``: optional torch.cuda.Event pair recorded around the state-update kernel."""
+    L = _lib.lib()
+    need = L.mamba2_step_workspace_size(ctypes.byref(args))
+    if workspace.numel() < need:
+        raise _lib.MambaHipError(f"workspace of {need} bytes required, got {workspace.numel()}")
+    stream = _stream(workspace.device)
+    if events is None:
+        check(L.mamba2_step_ssm(ctypes.byref(args), ctypes.c_void_p(workspace.data_ptr()), need, stream),
+              "mamba2_step_ssm")
+    else:
+        e0, e1 = _raw_events(events, workspace.device)
+        check(L.mamba2_step_ssm_timed(ctypes.byref(args), ctypes.c_void_p(workspace.data_ptr()), need, stream,
+                                      e0, e1),
+              "mamba2_step_ssm_timed")
+
+
+def rmsnorm(x: torch.Tensor, weight: Optional[torch.Tensor], out: Optional[torch.Tensor] = None,
+            add: Optional[torch.Tensor] = None):
+    """x += add (when given, in place); out = RmsNorm(x) * weight (when out is given)."""
+    if x.dtype != torch.float32 or x.dim() != 2 or x.stride(1) != 1:
+        raise _lib.MambaHipError("x must be a row-contiguous 2-d float32 tensor")
+    a = RmsNormArgs()
+    a.rows, a.cols = x.shape
+    a.x, a.x_sr = x.data_ptr(), x.stride(0)
+    a.add_dtype = a.out_dtype = 0
+    if add is not None:
+        if add.shape != x.shape or add.stride(1) != 1:
+            raise _lib.MambaHipError("add must match x")
+        a.add, a.add_sr, a.add_dtype = add.data_ptr(), add.stride(0), _dtype_code(add)
+    if out is not None:
+        if out.shape != x.shape or out.stride(1) != 1 or weight is None:
+            raise _lib.MambaHipError("out must match x and needs weight")
+        a.out, a.out_sr, a.out_dtype = out.data_ptr(), out.stride(0), _dtype_code(out)
+        a.weight = weight.data_ptr()
+    check(_lib.lib().mamba_rmsnorm(ctypes.byref(a), _stream(x.device)), "mamba_rmsnorm")
+
+
+@dataclass
+class Mamba2:
+    """Decode-side Mamba2 block (parameters of src/mamba2/mamba2.rs:391-505)."""
+    cfg: Mamba2Config
+    in_proj_w: torch.Tensor            # [d_model, d_in_proj]
+    in_proj_b: Optional[torch.Tensor]
+    conv_w: torch.Tensor               # [conv_dim, conv_kernel] f32
+    conv_b: Optional[torch.Tensor]     # [conv_dim] f32
+    dt_bias: torch.Tensor              # [nheads] f32
+    a_log: torch.Tensor                # [nheads] f32
+    d: torch.Tensor                    # [nheads] f32
+    norm_w: torch.Tensor               # [d_inner] f32
+    out_proj_w: torch.Tensor           # [d_inner, d_model]
+    out_proj_b: Optional[torch.Tensor]
+    A: torch.Tensor = field(init=False, repr=False)   # [nheads] f32, -exp(a_log)
+
+    def __post_init__(self):
+        # A = -exp(a_log) (mamba2.rs:929), computed once at construction so that
+        # a captured step never allocates it
+        self.A = -torch.exp(self.a_log)
+
+    @property
+    def dtype(self):
+        return self.in_proj_w.dtype
+
+    def new_cache(self, batch: int) -> Mamba2Cache:
+        c = self.cfg
+        dev = self.in_proj_w.device
+        return Mamba2Cache(
+            conv_bvk=torch.zeros(batch, c.conv_dim, c.conv_kernel, device=dev, dtype=torch.float32),
+            ssm_bhpr=torch.zeros(batch, c.nheads, c.per_head_dim, c.state_rank, device=dev, dtype=torch.float32))
+
+    def step_into(self, x: torch.Tensor, cache: Mamba2Cache, zx: torch.Tensor, y: torch.Tensor,
+                  out: torch.Tensor, workspace: torch.Tensor, events=None):
+        """Allocation-free step: x [b, d_model] (weight dtype) -> out [b, d_model]; cache updated in place."""
+        torch.mm(x, self.in_proj_w, out=zx)
+        if self.in_proj_b is not None:
+            zx.add_(self.in_proj_b)
+        args = step_ssm_args(self.cfg, zx, cache, self.conv_w, self.conv_b, self.dt_bias, self.A, self.d,
+                             self.norm_w, y)
+        step_ssm(args, workspace, events)
+        torch.mm(y, self.out_proj_w, out=out)
+        if self.out_proj_b is not None:
+            out.add_(self.out_proj_b)
+
+    def step(self, input_bm: torch.Tensor, cache: Optional[Mamba2Cache] = None):
+        """Mamba2::step (mamba2.rs:820-1004): returns (out_bm, cache); the cache is updated in place."""
+        b = input_bm.shape[0]
+        if cache is None:
+            cache = self.new_cache(b)
+        dev, dt = input_bm.device, self.dtype
+        zx = torch.empty(b, self.cfg.d_in_proj, device=dev, dtype=dt)
+        y = torch.empty(b, self.cfg.d_inner, device=dev, dtype=dt)
+        out = torch.empty(b, self.cfg.d_model, device=dev, dtype=dt)
+        args = step_ssm_args(self.cfg, zx, cache, self.conv_w, self.conv_b, self.dt_bias, self.A, self.d,
+                             self.norm_w, y)
+        ws = torch.empty(_lib.lib().mamba2_step_workspace_size(ctypes.byref(args)), device=dev, dtype=torch.uint8)
+        self.step_into(input_bm.to(dt), cache, zx, y, out, ws)
+        return out, cache
+
+
+@dataclass
+class Mamba2Layer:
+    """Pre-norm residual layer (src/modules/layer.rs:224-232) around a Mamba2 block."""
+    norm_w: torch.Tensor   # [d_model] f32 RmsNorm gamma
+    mixer: Mamba2
+
+
+class Mamba2Stack:
+    """A stack of pre-norm Mamba2 layers stepped one token at a time.
+
+    The residual stream is kept in f32.  The residual add of layer l is fused
+    with the RmsNorm of layer l+1 (one mamba_rmsnorm call), so a layer is five
+    launches: rmsnorm, in_proj, mamba2_step_ssm (two kernels), out_proj.  All
+    activations live in buffers allocated once per batch size, so ``step_``
+    allocates nothing and can be captured in a HIP graph."""
+
+    def __init__(self, layers: List[Mamba2Layer]):
+        assert layers
+        self.layers = layers
+        self.cfg = layers[0].mixer.cfg
+        self._bufs = {}
+
+    @staticmethod
+    def init(cfg: Mamba2Config, n_layers: int, device, dtype=torch.bfloat16,
+             generator: Optional[torch.Generator] = None) -> "Mamba2Stack":
+        return Mamba2Stack([Mamba2Layer(norm_w=torch.ones(cfg.d_model, device=device, dtype=torch.float32),
+                                        mixer=cfg.init(device, dtype, generator)) for _ in range(n_layers)])
+
+    def new_caches(self, batch: int) -> List[Mamba2Cache]:
+        return [l.mixer.new_cache(batch) for l in self.layers]
+
+    def buffers(self, batch: int, device):
+        key = (batch, str(device))
+        if key not in self._bufs:
+            c, dt = self.cfg, self.layers[0].mixer.dtype
+            bufs = dict(
+                normed=torch.empty(batch, c.d_model, device=device, dtype=dt),
+                zx=torch.empty(batch, c.d_in_proj, device=device, dtype=dt),
+                y=torch.empty(batch, c.d_inner, device=device, dtype=dt),
+                out=torch.empty(batch, c.d_model, device=device, dtype=dt))
+            probe = Mamba2StepArgs()
+            probe.batch, probe.nheads, probe.headdim = batch, c.nheads, c.per_head_dim
+            n = _lib.lib().mamba2_step_workspace_size(ctypes.byref(probe))
+            bufs["ws"] = torch.empty(n, device=device, dtype=torch.uint8)
+            self._bufs[key] = bufs
+        return self._bufs[key]
+
+    def step_(self, x_res: torch.Tensor, caches: List[Mamba2Cache], events=None):
+        """In-place step of the whole stack: x_res [b, d_model] f32 becomes the stack output.
+
+        ``events`` (start, stop) raw hipEvent_t pair: recorded around the state
+        update kernel of the first layer (benchmark timing)."""
+        bufs = self.buffers(x_res.shape[0], x_res.device)
+        prev = None
+        for i, layer in enumerate(self.layers):
+            rmsnorm(x_res, layer.norm_w, out=bufs["normed"], add=prev)
+            layer.mixer.step_into(bufs["normed"], caches[i], bufs["zx"], bufs["y"], bufs["out"], bufs["ws"],
+                                  events if i == 0 else None)
+            prev = bufs["out"]
+        rmsnorm(x_res, None, add=prev)
+        return x_res
+
+    def step(self, x: torch.Tensor, caches: Optional[List[Mamba2Cache]] = None):
+        """Out-of-place convenience: returns (y [b, d_model] f32, caches)."""
+        if caches is None:
+            caches = self.new_caches(x.shape[0])
+        x_res = x.to(torch.float32).clone()
+        self.step_(x_res, caches)
+        return x_res, caches

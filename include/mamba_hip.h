@@ -25,10 +25,8 @@
  *   mamba1_scan_step    <- Mamba1::selective_scan_step (src/mamba1/mamba1.rs:666-674)
  *   mamba2_step_ssm     <- the body of Mamba2::step between in_proj and out_proj
  *                          (src/mamba2/mamba2.rs:857-995)
- *   mamba_linear_bf16   <- burn::nn::Linear::forward as used by in_proj/out_proj
- *                          (src/mamba2/mamba2.rs:850,1000)
  *   mamba_rmsnorm       <- RmsNorm::forward (src/modules/norm/rms_norm.rs:53-98), the
- *                          pre-norm of Layer::step_one (src/modules/layer.rs:224-232)
+ *                          pre-norm and residual of Layer::step_one (src/modules/layer.rs:224-232)
  */
 #ifndef MAMBA_HIP_H
 #define MAMBA_HIP_H
@@ -153,6 +151,71 @@ int mamba1_scan_fwd(const mamba1_scan_args* args, mamba_stream_t stream);
 /* kernel (benchmark timing; no counterpart in the reference).                */
 int mamba1_scan_fwd_timed(const mamba1_scan_args* args, mamba_stream_t stream, void* event_start,
                           void* event_stop);
+
+/* ------------------------------------------------------------------------- */
+/* Mamba-2 recurrent decode step: everything of Mamba2::step between in_proj  */
+/* and out_proj (src/mamba2/mamba2.rs:857-995), for one token per sequence:    */
+/*                                                                             */
+/*   zxbcdt = [z (d_inner) | xBC (conv_dim) | dt_raw (nheads)]  (in_proj out)  */
+/*   window[b,v,:] <- shift left, append xBC[b,v]      (conv_state, in place)  */
+/*   xBC' = silu(sum_k window[b,v,k] conv_w[v,k] + conv_b[v])                  */
+/*   dt   = clamp(softplus(dt_raw + dt_bias), dt_min, dt_max) ; dA = exp(dt A)  */
+/*   h[b,h,p,n] <- h dA + (dt B[g,n]) x[h,p]          (ssm_state, in place)    */
+/*   y = sum_n h C[g,n] + D x ; out = RmsNormGated(y, z)                       */
+/*                                                                             */
+/* conv_dim = d_inner + 2 ngroups dstate, d_inner = nheads headdim; head h     */
+/* reads group h / (nheads / ngroups).  RmsNormGated (norm/rms_norm_gated.rs:  */
+/* 70-135): norm_before_gate = 0 gives g = y silu(z), out = g / sqrt(mean(g^2) */
+/* + eps) w; 1 gives out = y / sqrt(mean(y^2) + eps) w silu(z); the mean runs  */
+/* over all d_inner channels of a row.  The caches keep the reference's        */
+/* Mamba2Cache layout (src/mamba2/cache.rs:98-122): conv_bvk [b, conv_dim, K]   */
+/* and ssm_bhpr [b, nheads, headdim, dstate], both f32 and contiguous.         */
+/* ------------------------------------------------------------------------- */
+typedef struct mamba2_step_args {
+    int32_t batch, nheads, headdim, ngroups, dstate, conv_kernel;
+    int32_t zxbcdt_dtype;             /* mamba_dtype of zxbcdt                  */
+    int32_t out_dtype;                /* mamba_dtype of out                     */
+    int32_t norm_before_gate;         /* 0 (reference default) or 1             */
+    const void* zxbcdt; int64_t zxbcdt_sb;  /* [b, d_inner + conv_dim + nheads] */
+    float* conv_state;                /* [b, conv_dim, conv_kernel], in/out     */
+    const float* conv_w;              /* [conv_dim, conv_kernel] (Conv1d [v,1,k]) */
+    const float* conv_b;              /* [conv_dim] or NULL                      */
+    const float* dt_bias;             /* [nheads] or NULL                        */
+    const float* A;                   /* [nheads], A = -exp(a_log)               */
+    const float* D;                   /* [nheads] or NULL (= 0)                  */
+    float dt_min, dt_max;             /* dt_limit (reference default 0, 65504)  */
+    const float* norm_w;              /* [d_inner] gated-RMSNorm gamma           */
+    float* ssm_state;                 /* [b, nheads, headdim, dstate], in/out   */
+    void* out; int64_t out_sb;        /* [b, d_inner]                            */
+} mamba2_step_args;
+
+size_t mamba2_step_workspace_size(const mamba2_step_args* args);
+/* Replaces Mamba2::step (src/mamba2/mamba2.rs:820-1004) from the in_proj      */
+/* split (:849-861) to the gated norm (:995); in_proj/out_proj stay dense      */
+/* products the caller runs.                                                   */
+int mamba2_step_ssm(const mamba2_step_args* args, void* workspace, size_t workspace_bytes,
+                    mamba_stream_t stream);
+/* As mamba2_step_ssm, recording the caller's HIP events around the state-     */
+/* update kernel (benchmark timing; no counterpart in the reference).          */
+int mamba2_step_ssm_timed(const mamba2_step_args* args, void* workspace, size_t workspace_bytes,
+                          mamba_stream_t stream, void* event_start, void* event_stop);
+
+/* ------------------------------------------------------------------------- */
+/* Residual add + RmsNorm over rows (src/modules/norm/rms_norm.rs:53-98), the  */
+/* pre-norm and residual of Layer::step_one (src/modules/layer.rs:224-232):    */
+/*   x[r,:] += add[r,:]                      (when add != NULL; x is f32)     */
+/*   out[r,:] = x[r,:] / sqrt(mean(x[r,:]^2) + eps) * weight   (when out)     */
+/* ------------------------------------------------------------------------- */
+typedef struct mamba_rmsnorm_args {
+    int32_t rows, cols;
+    int32_t add_dtype, out_dtype;     /* mamba_dtype of add and out             */
+    float* x;         int64_t x_sr;   /* [rows, cols] f32, updated when add     */
+    const void* add;  int64_t add_sr; /* [rows, cols] or NULL                    */
+    const float* weight;              /* [cols]; required when out != NULL       */
+    void* out;        int64_t out_sr; /* [rows, cols] or NULL                    */
+} mamba_rmsnorm_args;
+
+int mamba_rmsnorm(const mamba_rmsnorm_args* args, mamba_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -127,7 +127,8 @@ def mamba1_step(u, delta, A, B, C, state, D=None, z=None, delta_bias=None, delta
 # --------------------------------------------------------------------------
 
 def mamba2_step_ssm(zxbcdt, conv_state, conv_w, conv_b, dt_bias, A, D, norm_w, ssm_state,
-                    nheads, headdim, ngroups, dstate, dt_limit=(0.0, 65504.0), prec=64):
+                    nheads, headdim, ngroups, dstate, dt_limit=(0.0, 65504.0), norm_before_gate=False,
+                    prec=64):
     """Everything of Mamba2::step between in_proj and out_proj.
 
     Returns (out[b, d_inner], new_conv_state, new_ssm_state)."""
@@ -141,7 +142,7 @@ def mamba2_step_ssm(zxbcdt, conv_state, conv_w, conv_b, dt_bias, A, D, norm_w, s
     _fn("mamba2_step_ssm", prec)(b, nheads, headdim, ngroups, dstate, k, _ptr(zxbcdt), _ptr(cs),
                                  _ptr(conv_w), _ptr(conv_b), _ptr(dt_bias), _ptr(A), _ptr(D),
                                  ctypes.c_float(dt_limit[0]), ctypes.c_float(dt_limit[1]),
-                                 _ptr(norm_w), _ptr(ss), _ptr(out))
+                                 _ptr(norm_w), _ptr(ss), _ptr(out), int(bool(norm_before_gate)))
     return out, cs, ss
 
 

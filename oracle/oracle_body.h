@@ -357,8 +357,9 @@ void F(mamba1_step)(int batch, int dim, int dstate, const float* u, const float*
 /* out_proj: conv-window slide + depthwise dot + bias + SiLU (:865-902),      */
 /* split (:907-918), dt = softplus(dt_raw + dt_bias).clamp(lo,hi) (:924),     */
 /* dA = exp(dt*A) (:932), h = h*dA + dt*B*x (:940-966), y = sum_n h*C + D*x   */
-/* (:970-991), gated RMSNorm with norm_before_gate = false (:995,             */
-/* rms_norm_gated.rs:70-135: g = y*silu(z); g / sqrt(mean(g^2)+eps) * gamma). */
+/* (:970-991), gated RMSNorm (:995, rms_norm_gated.rs:70-135): with          */
+/* norm_before_gate = 0 (the default) g = y*silu(z), g/sqrt(mean(g^2)+eps)*w; */
+/* with 1, y/sqrt(mean(y^2)+eps)*w*silu(z).                                   */
 /*   zxbcdt[b, d_inner + conv_dim + H]  conv_state[b, conv_dim, K] (in/out)   */
 /*   conv_w[conv_dim, K] conv_b[conv_dim] (nullable) dt_bias[H] A[H] D[H]     */
 /*   norm_w[d_inner]  ssm_state[b,H,P,N] (in/out)  out[b, d_inner]            */
@@ -367,13 +368,14 @@ void F(mamba2_step_ssm)(int batch, int nheads, int headdim, int ngroups, int dst
                         const float* zxbcdt, float* conv_state, const float* conv_w,
                         const float* conv_b, const float* dt_bias, const float* A, const float* D,
                         float dt_lo, float dt_hi, const float* norm_w, float* ssm_state,
-                        float* out) {
+                        float* out, int norm_before_gate) {
     const int H = nheads, P = headdim, G = ngroups, N = dstate, K = conv_k;
     const int d_inner = H * P, conv_dim = d_inner + 2 * G * N, hpg = H / G;
     const int d_in_proj = d_inner + conv_dim + H;
-    REAL* xbc = (REAL*)malloc(sizeof(REAL) * conv_dim);
-    REAL* g = (REAL*)malloc(sizeof(REAL) * d_inner);
+#pragma omp parallel for schedule(static)
     for (int b = 0; b < batch; ++b) {
+        REAL* xbc = (REAL*)malloc(sizeof(REAL) * conv_dim);
+        REAL* g = (REAL*)malloc(sizeof(REAL) * d_inner);
         const float* row = zxbcdt + (size_t)b * d_in_proj;
         for (int v = 0; v < conv_dim; ++v) {
             float* cw = conv_state + ((size_t)b * conv_dim + v) * K;
@@ -403,16 +405,20 @@ void F(mamba2_step_ssm)(int batch, int nheads, int headdim, int ngroups, int dst
                     acc += sv * cg[n];
                 }
                 const REAL yv = acc + (D ? (REAL)D[h] : (REAL)0) * xh[p];
-                const REAL gv = yv * F(silu_)((REAL)row[(size_t)h * P + p]);
+                const REAL gv = norm_before_gate ? yv : yv * F(silu_)((REAL)row[(size_t)h * P + p]);
                 g[h * P + p] = gv;
                 ssq += gv * gv;
             }
         }
         const REAL rms = (REAL)sqrt((double)(ssq / (REAL)d_inner + F(div_eps_)()));
-        for (int i = 0; i < d_inner; ++i) out[(size_t)b * d_inner + i] = (float)((g[i] / rms) * (REAL)norm_w[i]);
+        for (int i = 0; i < d_inner; ++i) {
+            REAL v = (g[i] / rms) * (REAL)norm_w[i];
+            if (norm_before_gate) v *= F(silu_)((REAL)row[i]);
+            out[(size_t)b * d_inner + i] = (float)v;
+        }
+        free(xbc);
+        free(g);
     }
-    free(xbc);
-    free(g);
 }
 
 /* RmsNorm (src/modules/norm/rms_norm.rs:53-98): x / sqrt(mean(x^2)+eps) * w. */

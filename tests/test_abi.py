@@ -51,7 +51,9 @@ int main(void) {{ printf("%zu\\n", sizeof({struct_name})); {body} return 0; }}
 
 
 @pytest.mark.parametrize("cls_name,c_name", [("Ssd2Args", "mamba_ssd2_args"),
-                                             ("Mamba1ScanArgs", "mamba1_scan_args")])
+                                             ("Mamba1ScanArgs", "mamba1_scan_args"),
+                                             ("Mamba2StepArgs", "mamba2_step_args"),
+                                             ("RmsNormArgs", "mamba_rmsnorm_args")])
 def test_struct_layouts_match_header(cls_name, c_name):
     from mamba_hip import _lib
     cls = getattr(_lib, cls_name)
@@ -69,3 +71,25 @@ def test_invalid_args_need_no_gpu():
     rc = _lib.lib().mamba_ssd2_fwd(ctypes.byref(a), None, 0, None)
     assert rc == 1  # MAMBA_ERR_INVALID_ARG
     assert b"ngroups" in _lib.lib().mamba_last_error()
+
+
+def test_step_validation_needs_no_gpu():
+    """mamba2_step_ssm rejects bad groups and a short workspace before any HIP call."""
+    from mamba_hip import _lib
+    L = _lib.lib()
+    a = _lib.Mamba2StepArgs()
+    a.batch, a.nheads, a.headdim, a.ngroups, a.dstate, a.conv_kernel = 2, 3, 64, 2, 128, 4
+    assert L.mamba2_step_ssm(ctypes.byref(a), None, 0, None) == 1
+    assert b"ngroups" in L.mamba_last_error()
+    a.nheads = 4
+    for name in ("zxbcdt", "conv_state", "conv_w", "A", "norm_w", "ssm_state", "out"):
+        setattr(a, name, 4096)  # never dereferenced: validation fails first
+    a.zxbcdt_sb = 4 * 64 + 4 * 64 + 2 * 2 * 128 + 4
+    a.out_sb = 4 * 64
+    need = L.mamba2_step_workspace_size(ctypes.byref(a))
+    assert need >= 2 * 4 * 64 * 4
+    assert L.mamba2_step_ssm(ctypes.byref(a), ctypes.c_void_p(4096), need - 1, None) == 3  # WORKSPACE
+    assert b"workspace" in L.mamba_last_error()
+    r = _lib.RmsNormArgs()
+    r.rows, r.cols = 2, 8
+    assert L.mamba_rmsnorm(ctypes.byref(r), None) == 1

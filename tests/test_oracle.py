@@ -214,6 +214,12 @@ def test_mamba2_step_ssm_closed_form():
     gv = y.reshape(b, d_inner) * _silu(z.astype(np.float64))
     ref = gv / np.sqrt((gv ** 2).mean(-1, keepdims=True) + 8.1584695e-8) * nw
     np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-6)
+    # norm_before_gate = true: normalise y first, gate afterwards
+    out_nb, _, _ = oracle.mamba2_step_ssm(zx, conv_state, conv_w, conv_b, dt_bias, A, D, nw, ss, H, P, G, N,
+                                          norm_before_gate=True)
+    yb = y.reshape(b, d_inner)
+    ref_nb = yb / np.sqrt((yb ** 2).mean(-1, keepdims=True) + 8.1584695e-8) * nw * _silu(z.astype(np.float64))
+    np.testing.assert_allclose(out_nb, ref_nb, rtol=1e-5, atol=1e-6)
 
 
 def test_mamba2_step_unroll_equals_ssd():

@@ -1,0 +1,290 @@
+"""Mamba-2 decode step: libmamba_hip.so (C ABI) vs the CPU oracle.
+
+* mamba2_step_ssm (everything of Mamba2::step between in_proj and out_proj)
+  against oracle.mamba2_step_ssm over several consecutive steps, so the conv
+  window slide and the state recurrence are both exercised; f32 I/O at rtol
+  1e-4, bf16 I/O at rtol 2e-2 / atol 1e-2.
+* The pre-norm layer (RmsNorm -> in_proj -> step -> out_proj -> residual)
+  against oracle.mamba2_layer_step, with f32 weights (tight) and bf16 weights.
+* A stack captured in a HIP graph: every replay equals the eager step.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = dict(rtol=1e-4, atol=1e-5)
+BF16_TOL = dict(rtol=2e-2, atol=1e-2)
+
+
+def _t(a, dtype=None):
+    import torch
+    t = torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    return t if dtype is None else t.to(dtype)
+
+
+def _bf16_round(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(torch.bfloat16).float().numpy()
+
+
+def _ssm_inputs(seed, b, H, P, G, N, K):
+    rng = np.random.default_rng(seed)
+    d_inner, conv_dim = H * P, H * P + 2 * G * N
+    dt0 = np.exp(rng.uniform(np.log(1e-3), np.log(0.1), H))
+    return dict(
+        conv_w=rng.uniform(-0.5, 0.5, (conv_dim, K)).astype(np.float32),
+        conv_b=rng.uniform(-0.5, 0.5, conv_dim).astype(np.float32),
+        dt_bias=(dt0 + np.log(-np.expm1(-dt0))).astype(np.float32),
+        A=-rng.uniform(1, 16, H).astype(np.float32),
+        D=rng.standard_normal(H).astype(np.float32),
+        norm_w=(1 + 0.1 * rng.standard_normal(d_inner)).astype(np.float32),
+        conv=rng.standard_normal((b, conv_dim, K)).astype(np.float32),
+        ssm=(0.1 * rng.standard_normal((b, H, P, N))).astype(np.float32),
+        zx=[rng.standard_normal((b, d_inner + conv_dim + H)).astype(np.float32) for _ in range(3)],
+    )
+
+
+SSM_CASES = [
+    # (b, H, P, G, N, K, zx dtype, out dtype, norm_before_gate)
+    (3, 8, 64, 1, 128, 4, "f32", "f32", 0),     # fast kernel, dstate 128 (config-3 head shape)
+    (2, 6, 64, 2, 64, 4, "f32", "f32", 0),      # fast kernel, dstate 64, two groups
+    (2, 4, 64, 1, 128, 4, "bf16", "bf16", 0),   # bf16 in_proj output and out
+    (1, 4, 64, 2, 128, 4, "f32", "f32", 1),     # norm before gate
+    (2, 5, 16, 1, 24, 3, "f32", "f32", 0),      # generic kernel (headdim 16, dstate 24, width 3)
+    (2, 3, 8, 3, 6, 2, "bf16", "f32", 1),       # generic, per-head groups
+    (1, 2, 64, 1, 128, 1, "f32", "f32", 0),     # conv width 1 (no history)
+]
+
+
+@pytest.mark.parametrize("case", SSM_CASES)
+def test_step_ssm_matches_oracle(case):
+    import torch
+    import mamba_hip
+    import oracle
+    b, H, P, G, N, K, zxd, outd, nbg = case
+    dts = {"f32": torch.float32, "bf16": torch.bfloat16}
+    inp = _ssm_inputs(sum(case[:6]), b, H, P, G, N, K)
+    cfg = mamba_hip.Mamba2Config(d_model=H * P // 2, state_rank=N, conv_kernel=K, per_head_dim=P, ngroups=G,
+                                 is_norm_before_gate=bool(nbg))
+    assert cfg.nheads == H
+    cache = mamba_hip.Mamba2Cache(conv_bvk=_t(inp["conv"]), ssm_bhpr=_t(inp["ssm"]))
+    out = torch.empty(b, H * P, device="cuda", dtype=dts[outd])
+    ws = torch.empty(1 << 20, device="cuda", dtype=torch.uint8)
+    ref_conv, ref_ssm = inp["conv"], inp["ssm"]
+    tol = F32_TOL if outd == "f32" else BF16_TOL
+    for step, zx in enumerate(inp["zx"]):
+        zx_in = zx if zxd == "f32" else _bf16_round(zx)
+        zx_dev = _t(zx_in, dts[zxd])
+        args = mamba_hip.step_ssm_args(cfg, zx_dev, cache, _t(inp["conv_w"]), _t(inp["conv_b"]),
+                                       _t(inp["dt_bias"]), _t(inp["A"]), _t(inp["D"]), _t(inp["norm_w"]), out)
+        mamba_hip.step_ssm(args, ws)
+        torch.cuda.synchronize()
+        ref_out, ref_conv, ref_ssm = oracle.mamba2_step_ssm(
+            zx_in, ref_conv, inp["conv_w"], inp["conv_b"], inp["dt_bias"], inp["A"], inp["D"], inp["norm_w"],
+            ref_ssm, H, P, G, N, norm_before_gate=bool(nbg))
+        print(f"step {step}: case {case}", flush=True)
+        np.testing.assert_array_equal(cache.conv_bvk.cpu().numpy(), ref_conv)
+        np.testing.assert_allclose(cache.ssm_bhpr.cpu().numpy(), ref_ssm, **F32_TOL)
+        np.testing.assert_allclose(out.float().cpu().numpy(), ref_out, **tol)
+
+
+def test_step_ssm_without_optional_inputs():
+    """conv_b, dt_bias and D absent (NULL in the C ABI)."""
+    import torch
+    import mamba_hip
+    import oracle
+    b, H, P, G, N, K = 2, 4, 64, 1, 128, 4
+    inp = _ssm_inputs(77, b, H, P, G, N, K)
+    cfg = mamba_hip.Mamba2Config(d_model=128, state_rank=N, per_head_dim=P)
+    cache = mamba_hip.Mamba2Cache(conv_bvk=_t(inp["conv"]), ssm_bhpr=_t(inp["ssm"]))
+    out = torch.empty(b, H * P, device="cuda")
+    ws = torch.empty(1 << 20, device="cuda", dtype=torch.uint8)
+    args = mamba_hip.step_ssm_args(cfg, _t(inp["zx"][0]), cache, _t(inp["conv_w"]), None, None, _t(inp["A"]),
+                                   None, _t(inp["norm_w"]), out)
+    mamba_hip.step_ssm(args, ws)
+    torch.cuda.synchronize()
+    ref_out, ref_conv, ref_ssm = oracle.mamba2_step_ssm(
+        inp["zx"][0], inp["conv"], inp["conv_w"], None, np.zeros(H, np.float32), inp["A"], None, inp["norm_w"],
+        inp["ssm"], H, P, G, N)
+    np.testing.assert_allclose(cache.ssm_bhpr.cpu().numpy(), ref_ssm, **F32_TOL)
+    np.testing.assert_allclose(out.cpu().numpy(), ref_out, **F32_TOL)
+
+
+def test_step_ssm_dt_limit_clamp():
+    """dt is clamped to dt_limit after softplus (mamba2.rs:924)."""
+    import torch
+    import mamba_hip
+    import oracle
+    b, H, P, G, N, K = 1, 4, 64, 1, 64, 4
+    inp = _ssm_inputs(5, b, H, P, G, N, K)
+    cfg = mamba_hip.Mamba2Config(d_model=128, state_rank=N, per_head_dim=P, dt_limit=(0.02, 0.05))
+    cache = mamba_hip.Mamba2Cache(conv_bvk=_t(inp["conv"]), ssm_bhpr=_t(inp["ssm"]))
+    out = torch.empty(b, H * P, device="cuda")
+    ws = torch.empty(1 << 20, device="cuda", dtype=torch.uint8)
+    zx = inp["zx"][0]
+    zx[:, -H:] = np.array([-10.0, -1.0, 1.0, 25.0], np.float32)  # below, inside, above, softplus-linear
+    args = mamba_hip.step_ssm_args(cfg, _t(zx), cache, _t(inp["conv_w"]), _t(inp["conv_b"]), _t(inp["dt_bias"]),
+                                   _t(inp["A"]), _t(inp["D"]), _t(inp["norm_w"]), out)
+    mamba_hip.step_ssm(args, ws)
+    torch.cuda.synchronize()
+    ref_out, _, ref_ssm = oracle.mamba2_step_ssm(
+        zx, inp["conv"], inp["conv_w"], inp["conv_b"], inp["dt_bias"], inp["A"], inp["D"], inp["norm_w"],
+        inp["ssm"], H, P, G, N, dt_limit=(0.02, 0.05))
+    np.testing.assert_allclose(cache.ssm_bhpr.cpu().numpy(), ref_ssm, **F32_TOL)
+    np.testing.assert_allclose(out.cpu().numpy(), ref_out, **F32_TOL)
+
+
+def test_rmsnorm_residual():
+    import torch
+    import mamba_hip
+    import oracle
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((5, 2560)).astype(np.float32)
+    add = rng.standard_normal((5, 2560)).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(2560)).astype(np.float32)
+    xd, out = _t(x), torch.empty(5, 2560, device="cuda")
+    mamba_hip.rmsnorm(xd, _t(w), out=out, add=_t(add))
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(xd.cpu().numpy(), x + add, rtol=0, atol=0)
+    np.testing.assert_allclose(out.cpu().numpy(), oracle.rmsnorm(x + add, w), **F32_TOL)
+    outb = torch.empty(5, 2560, device="cuda", dtype=torch.bfloat16)
+    mamba_hip.rmsnorm(xd, _t(w), out=outb)  # no add: x unchanged
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(xd.cpu().numpy(), x + add, rtol=0, atol=0)
+    np.testing.assert_allclose(outb.float().cpu().numpy(), oracle.rmsnorm(x + add, w), **BF16_TOL)
+
+
+def _oracle_params(layer):
+    m = layer.mixer
+    f = lambda t: None if t is None else t.float().cpu().numpy()  # noqa: E731
+    return dict(pre_norm_w=f(layer.norm_w), w_in=f(m.in_proj_w), conv_w=f(m.conv_w), conv_b=f(m.conv_b),
+                dt_bias=f(m.dt_bias), A=f(m.A), D=f(m.d), norm_w=f(m.norm_w), w_out=f(m.out_proj_w))
+
+
+def _cfg_dict(cfg):
+    return dict(nheads=cfg.nheads, headdim=cfg.per_head_dim, ngroups=cfg.ngroups, dstate=cfg.state_rank)
+
+
+@pytest.mark.parametrize("wdtype", ["f32", "bf16"])
+def test_layer_steps_match_oracle(wdtype):
+    """Two pre-norm layers stepped three tokens: RmsNorm -> in_proj -> SSM step
+    -> gated norm -> out_proj -> residual, caches carried between tokens."""
+    import torch
+    import mamba_hip
+    import oracle
+    dt = torch.float32 if wdtype == "f32" else torch.bfloat16
+    cfg = mamba_hip.Mamba2Config(d_model=256, state_rank=128, per_head_dim=64)
+    gen = torch.Generator().manual_seed(11)
+    stack = mamba_hip.Mamba2Stack.init(cfg, 2, "cuda", dt, gen)
+    b = 3
+    rng = np.random.default_rng(12)
+    caches = stack.new_caches(b)
+    ref_caches = []
+    for c in caches:
+        c.conv_bvk.copy_(_t(rng.standard_normal(tuple(c.conv_bvk.shape)).astype(np.float32)))
+        c.ssm_bhpr.copy_(_t((0.1 * rng.standard_normal(tuple(c.ssm_bhpr.shape))).astype(np.float32)))
+        ref_caches.append([c.conv_bvk.cpu().numpy(), c.ssm_bhpr.cpu().numpy()])
+    params = [_oracle_params(l) for l in stack.layers]
+    tol = F32_TOL if wdtype == "f32" else BF16_TOL
+    for step in range(3):
+        x = rng.standard_normal((b, cfg.d_model)).astype(np.float32)
+        y, caches = stack.step(_t(x), caches)
+        torch.cuda.synchronize()
+        u = x
+        for i, p in enumerate(params):
+            u, ref_caches[i][0], ref_caches[i][1] = oracle.mamba2_layer_step(
+                u, p, ref_caches[i][0], ref_caches[i][1], _cfg_dict(cfg))
+        print(f"step {step} ({wdtype})", flush=True)
+        np.testing.assert_allclose(y.cpu().numpy(), u, **tol)
+        for i, c in enumerate(caches):
+            if wdtype == "f32":
+                np.testing.assert_allclose(c.conv_bvk.cpu().numpy(), ref_caches[i][0], **F32_TOL)
+                np.testing.assert_allclose(c.ssm_bhpr.cpu().numpy(), ref_caches[i][1], **F32_TOL)
+            else:  # states of a bf16 model: inputs carry bf16 rounding of in_proj
+                np.testing.assert_allclose(c.ssm_bhpr.cpu().numpy(), ref_caches[i][1], **BF16_TOL)
+
+
+def test_mamba2_step_signature():
+    """Mamba2::step(input_bm, None) allocates a zero cache like mamba2.rs:838-846."""
+    import torch
+    import mamba_hip
+    import oracle
+    cfg = mamba_hip.Mamba2Config(d_model=128, state_rank=64, per_head_dim=64)
+    m = cfg.init("cuda", torch.float32, torch.Generator().manual_seed(1))
+    x = np.random.default_rng(2).standard_normal((2, 128)).astype(np.float32)
+    out, cache = m.step(_t(x), None)
+    torch.cuda.synchronize()
+    zx = oracle.linear(x, m.in_proj_w.cpu().numpy())
+    ref, _, ref_ssm = oracle.mamba2_step_ssm(
+        zx, np.zeros((2, cfg.conv_dim, 4), np.float32), m.conv_w.cpu().numpy(), m.conv_b.cpu().numpy(),
+        m.dt_bias.cpu().numpy(), m.A.cpu().numpy(), m.d.cpu().numpy(), m.norm_w.cpu().numpy(),
+        np.zeros((2, cfg.nheads, 64, 64), np.float32), cfg.nheads, 64, 1, 64)
+    np.testing.assert_allclose(out.cpu().numpy(), oracle.linear(ref, m.out_proj_w.cpu().numpy()), **F32_TOL)
+    np.testing.assert_allclose(cache.ssm_bhpr.cpu().numpy(), ref_ssm, **F32_TOL)
+
+
+def test_stack_hip_graph_replays_equal_eager():
+    """Capture one stack step in a HIP graph; replay it several times with eager
+    work in between and check every replay against the eager result."""
+    import torch
+    import mamba_hip
+    cfg = mamba_hip.Mamba2Config(d_model=256, state_rank=128, per_head_dim=64)
+    stack = mamba_hip.Mamba2Stack.init(cfg, 3, "cuda", torch.bfloat16, torch.Generator().manual_seed(4))
+    b = 4
+    rng = np.random.default_rng(5)
+    base = stack.new_caches(b)
+    for c in base:
+        c.conv_bvk.copy_(_t(rng.standard_normal(tuple(c.conv_bvk.shape)).astype(np.float32)))
+        c.ssm_bhpr.copy_(_t((0.1 * rng.standard_normal(tuple(c.ssm_bhpr.shape))).astype(np.float32)))
+    x0 = _t(rng.standard_normal((b, cfg.d_model)).astype(np.float32))
+
+    def clone(cs):
+        return [mamba_hip.Mamba2Cache(c.conv_bvk.clone(), c.ssm_bhpr.clone()) for c in cs]
+
+    eager_caches = clone(base)
+    x_e = x0.clone()
+    stack.step_(x_e, eager_caches)
+    torch.cuda.synchronize()
+
+    gcaches = clone(base)
+    x_g = x0.clone()
+    stack.buffers(b, x_g.device)  # allocate outside the capture
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):  # warm up the BLAS handles on the capture stream
+        stack.step_(x_g.clone(), clone(base))
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        stack.step_(x_g, gcaches)
+    for rep in range(3):
+        x_g.copy_(x0)
+        for dst, src in zip(gcaches, base):
+            dst.conv_bvk.copy_(src.conv_bvk)
+            dst.ssm_bhpr.copy_(src.ssm_bhpr)
+        _ = (x0 * 2).sum().item()  # eager work and a sync between replays
+        g.replay()
+        torch.cuda.synchronize()
+        print(f"replay {rep}", flush=True)
+        np.testing.assert_array_equal(x_g.cpu().numpy(), x_e.cpu().numpy())
+        for a, e in zip(gcaches, eager_caches):
+            np.testing.assert_array_equal(a.ssm_bhpr.cpu().numpy(), e.ssm_bhpr.cpu().numpy())
+            np.testing.assert_array_equal(a.conv_bvk.cpu().numpy(), e.conv_bvk.cpu().numpy())
+
+
+def test_step_invalid_args_raise():
+    import torch
+    import mamba_hip
+    from mamba_hip import _lib
+    a = _lib.Mamba2StepArgs()
+    a.batch, a.nheads, a.headdim, a.ngroups, a.dstate, a.conv_kernel = 1, 4, 64, 1, 128, 4
+    ws = torch.empty(16, device="cuda", dtype=torch.uint8)
+    rc = _lib.lib().mamba2_step_ssm(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), 16, None)
+    assert rc == 1  # required pointers missing
+    with pytest.raises(mamba_hip.MambaHipError):
+        mamba_hip.rmsnorm(torch.zeros(2, 3, device="cuda", dtype=torch.float64), None)
