@@ -247,13 +247,25 @@ def bench_decode(args):
     with torch.cuda.graph(graph):
         eager()
 
-    def step(events=None):
-        if events is None:
-            graph.replay()
-        else:
-            eager(events)
-
-    ms_per_step, kern_ms = _time_steps(args, step)
+    log(f"warmup {args.warmup}")
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} graph replays")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    # state-update kernel: events around it in every layer of K eager steps
+    pairs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(cfg["n_layers"])] for _ in range(args.steps)]
+    for ev in pairs:
+        eager(ev)
+    torch.cuda.synchronize()
+    durs = [a.elapsed_time(b_) for ev in pairs for a, b_ in ev]
+    kern_ms = sum(durs) / len(durs)
+    log(f"ms/step {ms_per_step:.4f}, state-update kernel {kern_ms * 1e3:.2f} us (mean of {len(durs)})")
     t0 = time.perf_counter()
     for _ in range(args.steps):
         eager()
@@ -312,6 +324,33 @@ def cpu_baseline_decode(cfg, budget_s=10.0, seed=0):
     return {"value": us, "unit": "us/step", "cores": threads, "kind": "port",
             "sample": f"{layers} of {cfg['n_layers']} layers at batch {b} ({el:.1f} s), scaled to the full "
                       f"stack; f32 restatement of RmsNorm + Mamba2::step + residual"}
+
+
+COPY_BYTES = 1 << 30
+
+
+def calibrate_copy():
+    """A plain device-to-device copy of COPY_BYTES (read COPY_BYTES, write
+    COPY_BYTES): the reference kernel for scaling HBM byte counters."""
+    import torch
+    src = torch.ones(COPY_BYTES // 4, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copy calibration: 3 x {COPY_BYTES} bytes")
+
+
+def _profiled_traffic(workload):
+    """HBM bytes per launch of the dominant kernel, measured by rocprofv3
+    FETCH_SIZE + WRITE_SIZE and scaled by the copy calibration; stored in
+    profiles/traffic.json by the profiling run (None when absent)."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        entry = json.load(f).get(workload)
+    return None if entry is None else entry.get("bytes_per_launch")
 
 
 def _time_steps(args, step):
@@ -404,6 +443,9 @@ def main():
     ap.add_argument("--workload", default="ssd2", choices=["ssd2", "mamba1", "decode"])
     ap.add_argument("--batch", type=int, default=DECODE_CFG3["batch"], help="decode batch")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a plain 1 GiB device copy 3 times (known bytes) so that rocprofv3 "
+                         "FETCH_SIZE/WRITE_SIZE of the same run can be scaled to true HBM bytes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -419,6 +461,11 @@ def main():
     else:
         out = bench_ssd2(args)
         base = (lambda: cpu_baseline_ssd2(SSD2_CFG1))
+    if args.calibrate_copy:
+        calibrate_copy()
+    traffic = _profiled_traffic(out["config"]["workload"])
+    if traffic is not None:
+        out["roofline"]["traffic"] = traffic
     if not args.no_cpu_baseline:
         log("cpu baseline")
         out["cpu_baseline"] = base()

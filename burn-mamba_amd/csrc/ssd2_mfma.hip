@@ -5,10 +5,10 @@
 // src/mamba2/ssd/serial_recalculated/serial_recalculated.rs:98-155.
 //
 // Two launches per call:
-//   1. ssd2_cb_mfma / ssd2_bt_transpose (per batch, chunk, group): the
-//      group-shared C_c.B_c^T matrix in f32 (K2, computed once per group
-//      instead of once per head) and a time-major copy of B_c (so the chunk
-//      state contraction over time can read B directly as an MFMA operand).
+//   1. ssd2_prep_mfma (per batch, chunk, group): the group-shared causal
+//      C_c.B_c^T tiles in f32 (K2, computed once per group instead of once per
+//      head), and C_c and B_c in bf16, all three stored in MFMA operand order
+//      so that every wave load of them is one contiguous 1 KB.
 //   2. ssd2_scan_mfma: one workgroup per (batch, head[, half of headdim])
 //      walks the chunks in order.  The running state h[p, n] lives in MFMA
 //      accumulators for the whole sequence (K4 needs no HBM round trip); per

@@ -296,14 +296,14 @@ class Mamba2Stack:
     def step_(self, x_res: torch.Tensor, caches: List[Mamba2Cache], events=None):
         """In-place step of the whole stack: x_res [b, d_model] f32 becomes the stack output.
 
-        ``events`` (start, stop) raw hipEvent_t pair: recorded around the state
-        update kernel of the first layer (benchmark timing)."""
+        ``events``: optional list of one torch.cuda.Event pair per layer,
+        recorded around that layer's state-update kernel (benchmark timing)."""
         bufs = self.buffers(x_res.shape[0], x_res.device)
         prev = None
         for i, layer in enumerate(self.layers):
             rmsnorm(x_res, layer.norm_w, out=bufs["normed"], add=prev)
             layer.mixer.step_into(bufs["normed"], caches[i], bufs["zx"], bufs["y"], bufs["out"], bufs["ws"],
-                                  events if i == 0 else None)
+                                  None if events is None else events[i])
             prev = bufs["out"]
         rmsnorm(x_res, None, add=prev)
         return x_res

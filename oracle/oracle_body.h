@@ -33,9 +33,11 @@
 static inline REAL F(exp_)(REAL v) { return (REAL)exp((double)v); }
 
 /* src/modules/activation/softplus.rs:17-48 — x above the per-dtype threshold
- * passes through, else log1p(exp(min(x, thr))).  thr = 18 for f32, 38 for f64. */
+ * passes through, else log1p(exp(min(x, thr))).  Both precisions use the f32
+ * model's threshold (18): prec=64 evaluates the f32 model's formula in f64
+ * arithmetic, which is the truth the f32/bf16 GPU path is checked against. */
 static inline REAL F(softplus_)(REAL v) {
-    const REAL thr = (sizeof(REAL) == 4) ? (REAL)18 : (REAL)38;
+    const REAL thr = (REAL)18;
     if (v > thr) return v;
     return (REAL)log1p(exp((double)(v < thr ? v : thr)));
 }
@@ -43,10 +45,9 @@ static inline REAL F(softplus_)(REAL v) {
 /* src/modules/activation/silu.rs:24-27 — x / (1 + exp(-x)). */
 static inline REAL F(silu_)(REAL v) { return v / ((REAL)exp(-(double)v) + (REAL)1); }
 
-/* src/utils/mod.rs:59-65 — div_eps(F32) = 8.1584695e-8 (F64: 4.0693917e-16). */
-static inline REAL F(div_eps_)(void) {
-    return (sizeof(REAL) == 4) ? (REAL)8.1584695e-8f : (REAL)4.0693917e-16;
-}
+/* src/utils/mod.rs:59-65 — div_eps(F32) = 8.1584695e-8, the f32 model's
+ * constant, at both precisions (see softplus_ above). */
+static inline REAL F(div_eps_)(void) { return (REAL)8.1584695e-8f; }
 
 /* ------------------------------------------------------------------------- */
 /* Mamba-2 SSD, serial K1..K5 — src/mamba2/ssd/serial.rs:34-506 (identical to */

@@ -305,3 +305,25 @@ def test_ssd3_lambda_one_is_mamba2():
     y2, h2 = oracle.ssd2(x, d["dt"].astype(np.float32), d["A"].astype(np.float32), Bm, Cm, None, d["h0"], chunk=8)
     np.testing.assert_allclose(y3[:, :, 0], y2, rtol=1e-5, atol=1e-6)
     np.testing.assert_allclose(h3, h2, rtol=1e-5, atol=1e-6)
+
+
+def test_rmsnorm_and_linear_known_answers():
+    """RmsNorm of a constant row c is c / sqrt(c^2 + eps) * w (so +-w for
+    |c| >> sqrt(eps)); a row and its negation normalise to negated outputs;
+    scaling a row leaves its normalisation unchanged.  Linear is x @ W
+    (Burn's [d_in, d_out] weight layout), checked against numpy.matmul."""
+    w = np.linspace(0.5, 1.5, 16).astype(np.float32)
+    x = np.stack([np.full(16, 3.0), np.full(16, -0.25), np.full(16, 1e-5)]).astype(np.float32)
+    out = oracle.rmsnorm(x, w)
+    eps = 8.1584695e-8
+    for r, c in enumerate((3.0, -0.25, 1e-5)):
+        np.testing.assert_allclose(out[r], c / np.sqrt(c * c + eps) * w, rtol=1e-6)
+    rng = np.random.default_rng(0)
+    v = rng.standard_normal((2, 16)).astype(np.float32)
+    np.testing.assert_allclose(oracle.rmsnorm(-v, w), -oracle.rmsnorm(v, w), rtol=1e-6)
+    np.testing.assert_allclose(oracle.rmsnorm(7 * v, w), oracle.rmsnorm(v, w), rtol=1e-5)
+    X = rng.standard_normal((3, 5)).astype(np.float32)
+    W = rng.standard_normal((5, 4)).astype(np.float32)
+    bias = rng.standard_normal(4).astype(np.float32)
+    np.testing.assert_allclose(oracle.linear(X, W), X.astype(np.float64) @ W, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(oracle.linear(X, W, bias), X.astype(np.float64) @ W + bias, rtol=1e-6, atol=1e-6)
