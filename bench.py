@@ -286,7 +286,7 @@ def bench_decode(args):
                    "entry": "mamba_rmsnorm + torch.mm + mamba2_step_ssm + torch.mm per layer"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel_ms": kern_ms,
-                     "algorithmic_bytes": kernel_bytes, "kernel": "step2_ssm_fast<128> (layer 0)"},
+                     "algorithmic_bytes": kernel_bytes, "kernel": "step2_ssm_fast<128> (mean over all layers)"},
     }
 
 

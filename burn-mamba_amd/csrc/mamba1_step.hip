@@ -1,0 +1,201 @@
+// Mamba-1 recurrent decode step for gfx950 (f32), and the depthwise causal
+// conv-window step shared by the recurrent blocks.
+//
+// Reference: Mamba1::selective_scan_step (burn-mamba src/mamba1/mamba1.rs:666-733)
+// with the dt_proj bias + softplus of Mamba1::ssm_step (:646) and the silu(res)
+// gate of Mamba1::step (:603); the conv window roll + depthwise dot + bias +
+// SiLU of Mamba1::step (:558-597).
+//
+// One token per sequence: the state [b, d, n] is read and written once, so the
+// step is HBM-bound (8 bytes of state traffic per (channel, state) against
+// ~6 flops).  For dstate a multiple of 4 (up to 64) a channel is spread over
+// n/4 lanes holding 4 consecutive states each: consecutive lanes touch
+// consecutive 16 bytes, and y = sum_n h C is a butterfly over those lanes.
+#include "common.h"
+
+namespace mamba {
+
+struct M1StepParams {
+    int nb, D, N;
+    const float* u; int64_t u_sb;
+    const float* dl; int64_t dl_sb;
+    const float* A; int64_t A_sd, A_sn;
+    const float* Bm; int64_t B_sb, B_sn;
+    const float* Cm; int64_t C_sb, C_sn;
+    const float* Dv;
+    const float* z; int64_t z_sb;
+    const float* dbias; bool softplus;
+    float* h;  // [nb, D, N] contiguous, in place
+    float* y; int64_t y_sb;
+};
+
+// Same evaluation as the selective-scan kernel: x above 20 is returned as is.
+__device__ __forceinline__ float m1s_softplus(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
+
+__device__ __forceinline__ float m1s_delta(const M1StepParams& p, int b, int d) {
+    float dv = p.dl[(int64_t)b * p.dl_sb + d];
+    if (p.dbias) dv += p.dbias[d];
+    return p.softplus ? m1s_softplus(dv) : dv;
+}
+
+// grid (ceil(D / CPB), nb), 256 threads; LPC = N/4 lanes per channel.
+template <int N>
+__global__ __launch_bounds__(256) void mamba1_step_kernel(M1StepParams p) {
+    constexpr int LPC = N / 4;
+    constexpr int CPB = 256 / LPC;
+    const int b = blockIdx.y;
+    const int t = threadIdx.x;
+    const int q = t % LPC;
+    const int d_raw = blockIdx.x * CPB + t / LPC;
+    const bool live = d_raw < p.D;
+    const int d = live ? d_raw : p.D - 1;  // whole lane groups share d: shuffles stay inside a group
+    float4* hp = reinterpret_cast<float4*>(p.h + ((int64_t)b * p.D + d) * N) + q;
+    const float4 hv = *hp;
+    const float dv = m1s_delta(p, b, d);
+    const float uv = p.u[(int64_t)b * p.u_sb + d];
+    const int n0 = 4 * q;
+    float a[4], bb[4], cc[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        a[k] = p.A[(int64_t)d * p.A_sd + (int64_t)(n0 + k) * p.A_sn];
+        bb[k] = p.Bm[(int64_t)b * p.B_sb + (int64_t)(n0 + k) * p.B_sn];
+        cc[k] = p.Cm[(int64_t)b * p.C_sb + (int64_t)(n0 + k) * p.C_sn];
+    }
+    // h <- h exp(delta A) + (delta B) u ; y partial = sum of this lane's h C
+    float4 hn;
+    hn.x = hv.x * __expf(dv * a[0]) + (dv * bb[0]) * uv;
+    hn.y = hv.y * __expf(dv * a[1]) + (dv * bb[1]) * uv;
+    hn.z = hv.z * __expf(dv * a[2]) + (dv * bb[2]) * uv;
+    hn.w = hv.w * __expf(dv * a[3]) + (dv * bb[3]) * uv;
+    float acc = hn.x * cc[0] + hn.y * cc[1] + hn.z * cc[2] + hn.w * cc[3];
+#pragma unroll
+    for (int o = 1; o < LPC; o <<= 1) acc += __shfl_xor(acc, o, 64);
+    if (!live) return;
+    *hp = hn;
+    if (q == 0) {
+        float out = acc + (p.Dv ? p.Dv[d] : 0.f) * uv;
+        if (p.z) {
+            const float zv = p.z[(int64_t)b * p.z_sb + d];
+            out *= zv / (1.f + __expf(-zv));
+        }
+        p.y[(int64_t)b * p.y_sb + d] = out;
+    }
+}
+
+// Any dstate: one thread per channel.
+__global__ __launch_bounds__(256) void mamba1_step_generic(M1StepParams p) {
+    const int b = blockIdx.y;
+    const int d = blockIdx.x * 256 + threadIdx.x;
+    if (d >= p.D) return;
+    const float dv = m1s_delta(p, b, d);
+    const float uv = p.u[(int64_t)b * p.u_sb + d];
+    float* hrow = p.h + ((int64_t)b * p.D + d) * p.N;
+    float acc = 0.f;
+    for (int n = 0; n < p.N; ++n) {
+        const float a = p.A[(int64_t)d * p.A_sd + (int64_t)n * p.A_sn];
+        const float bv = p.Bm[(int64_t)b * p.B_sb + (int64_t)n * p.B_sn];
+        const float cv = p.Cm[(int64_t)b * p.C_sb + (int64_t)n * p.C_sn];
+        const float hn = hrow[n] * __expf(dv * a) + (dv * bv) * uv;
+        hrow[n] = hn;
+        acc += hn * cv;
+    }
+    float out = acc + (p.Dv ? p.Dv[d] : 0.f) * uv;
+    if (p.z) {
+        const float zv = p.z[(int64_t)b * p.z_sb + d];
+        out *= zv / (1.f + __expf(-zv));
+    }
+    p.y[(int64_t)b * p.y_sb + d] = out;
+}
+
+// ---------------------------------------------------------------------------
+// Depthwise causal conv, one step: window[b,c,:] <- (window[b,c,1:], x[b,c]);
+// out[b,c] = act(sum_k window[b,c,k] w[c,k] + bias[c]).
+// ---------------------------------------------------------------------------
+struct ConvStepParams {
+    int nb, C, K;
+    bool x_bf16, out_bf16, silu;
+    const void* x; int64_t x_sb;
+    float* state;
+    const float* w; const float* bias;
+    void* out; int64_t out_sb;
+};
+
+__global__ __launch_bounds__(256) void conv1d_step_kernel(ConvStepParams p) {
+    const int b = blockIdx.y;
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= p.C) return;
+    const int64_t xi = (int64_t)b * p.x_sb + c;
+    const float xin = p.x_bf16 ? bf16_to_f32(static_cast<const bf16_t*>(p.x)[xi]) : static_cast<const float*>(p.x)[xi];
+    float* win = p.state + ((int64_t)b * p.C + c) * p.K;
+    const float* w = p.w + (int64_t)c * p.K;
+    float acc = 0.f;
+    for (int k = 0; k + 1 < p.K; ++k) {
+        const float v = win[k + 1];
+        win[k] = v;
+        acc += v * w[k];
+    }
+    win[p.K - 1] = xin;
+    acc += xin * w[p.K - 1];
+    if (p.bias) acc += p.bias[c];
+    if (p.silu) acc = acc / (__expf(-acc) + 1.f);
+    const int64_t oi = (int64_t)b * p.out_sb + c;
+    if (p.out_bf16)
+        static_cast<bf16_t*>(p.out)[oi] = f32_to_bf16(acc);
+    else
+        static_cast<float*>(p.out)[oi] = acc;
+}
+
+}  // namespace mamba
+
+using namespace mamba;
+
+extern "C" int mamba1_scan_step(const mamba1_step_args* a, mamba_stream_t stream) {
+    MAMBA_CHECK_ARG(a != nullptr, "args is NULL");
+    MAMBA_CHECK_ARG(a->batch > 0 && a->dim > 0 && a->dstate > 0 && a->dstate <= 1024,
+                    "batch, dim >= 1 and dstate in [1, 1024] required");
+    MAMBA_CHECK_ARG(a->u && a->delta && a->A && a->B && a->C && a->state && a->y,
+                    "u, delta, A, B, C, state and y are required");
+    M1StepParams p;
+    p.nb = a->batch; p.D = a->dim; p.N = a->dstate;
+    p.u = a->u; p.u_sb = a->u_sb; p.dl = a->delta; p.dl_sb = a->delta_sb;
+    p.A = a->A; p.A_sd = a->A_sd; p.A_sn = a->A_sn;
+    p.Bm = a->B; p.B_sb = a->B_sb; p.B_sn = a->B_sn;
+    p.Cm = a->C; p.C_sb = a->C_sb; p.C_sn = a->C_sn;
+    p.Dv = a->D; p.z = a->z; p.z_sb = a->z_sb;
+    p.dbias = a->delta_bias; p.softplus = a->delta_softplus != 0;
+    p.h = a->state; p.y = a->y; p.y_sb = a->y_sb;
+    const bool aligned = ((uintptr_t)p.h & 15u) == 0;
+    hipStream_t s = (hipStream_t)stream;
+    switch (aligned ? p.N : 0) {
+        case 16:
+            hipLaunchKernelGGL(mamba1_step_kernel<16>, dim3(ceil_div(p.D, 64), p.nb), dim3(256), 0, s, p);
+            break;
+        case 32:
+            hipLaunchKernelGGL(mamba1_step_kernel<32>, dim3(ceil_div(p.D, 32), p.nb), dim3(256), 0, s, p);
+            break;
+        case 64:
+            hipLaunchKernelGGL(mamba1_step_kernel<64>, dim3(ceil_div(p.D, 16), p.nb), dim3(256), 0, s, p);
+            break;
+        default:
+            hipLaunchKernelGGL(mamba1_step_generic, dim3(ceil_div(p.D, 256), p.nb), dim3(256), 0, s, p);
+    }
+    MAMBA_CHECK_LAUNCH();
+    return MAMBA_OK;
+}
+
+extern "C" int mamba_conv1d_step(const mamba_conv1d_step_args* a, mamba_stream_t stream) {
+    MAMBA_CHECK_ARG(a != nullptr, "args is NULL");
+    MAMBA_CHECK_ARG(a->batch > 0 && a->channels > 0, "batch and channels must be >= 1");
+    MAMBA_CHECK_ARG(a->kernel >= 1 && a->kernel <= 64, "kernel must be in [1, 64]");
+    MAMBA_CHECK_ARG(a->x && a->state && a->w && a->out, "x, state, w and out are required");
+    MAMBA_CHECK_ARG(a->x_dtype == MAMBA_F32 || a->x_dtype == MAMBA_BF16, "bad x_dtype");
+    MAMBA_CHECK_ARG(a->out_dtype == MAMBA_F32 || a->out_dtype == MAMBA_BF16, "bad out_dtype");
+    ConvStepParams p;
+    p.nb = a->batch; p.C = a->channels; p.K = a->kernel;
+    p.x_bf16 = a->x_dtype == MAMBA_BF16; p.out_bf16 = a->out_dtype == MAMBA_BF16; p.silu = a->silu != 0;
+    p.x = a->x; p.x_sb = a->x_sb; p.state = a->state; p.w = a->w; p.bias = a->bias;
+    p.out = a->out; p.out_sb = a->out_sb;
+    hipLaunchKernelGGL(conv1d_step_kernel, dim3(ceil_div(p.C, 256), p.nb), dim3(256), 0, (hipStream_t)stream, p);
+    MAMBA_CHECK_LAUNCH();
+    return MAMBA_OK;
+}

@@ -59,6 +59,33 @@ class Mamba1ScanArgs(ctypes.Structure):
     ]
 
 
+class Mamba1StepArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", c_i32), ("dim", c_i32), ("dstate", c_i32),
+        ("u", c_vp), ("u_sb", c_i64),
+        ("delta", c_vp), ("delta_sb", c_i64),
+        ("A", c_vp), ("A_sd", c_i64), ("A_sn", c_i64),
+        ("B", c_vp), ("B_sb", c_i64), ("B_sn", c_i64),
+        ("C", c_vp), ("C_sb", c_i64), ("C_sn", c_i64),
+        ("D", c_vp),
+        ("z", c_vp), ("z_sb", c_i64),
+        ("delta_bias", c_vp), ("delta_softplus", c_i32),
+        ("state", c_vp),
+        ("y", c_vp), ("y_sb", c_i64),
+    ]
+
+
+class Conv1dStepArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", c_i32), ("channels", c_i32), ("kernel", c_i32),
+        ("x_dtype", c_i32), ("out_dtype", c_i32),
+        ("x", c_vp), ("x_sb", c_i64),
+        ("state", c_vp), ("w", c_vp), ("bias", c_vp),
+        ("silu", c_i32),
+        ("out", c_vp), ("out_sb", c_i64),
+    ]
+
+
 class Mamba2StepArgs(ctypes.Structure):
     _fields_ = [
         ("batch", c_i32), ("nheads", c_i32), ("headdim", c_i32), ("ngroups", c_i32),
@@ -95,6 +122,8 @@ _SIGNATURES = {
                              ctypes.c_int),
     "mamba1_scan_fwd": ([ctypes.POINTER(Mamba1ScanArgs), c_vp], ctypes.c_int),
     "mamba1_scan_fwd_timed": ([ctypes.POINTER(Mamba1ScanArgs), c_vp, c_vp, c_vp], ctypes.c_int),
+    "mamba1_scan_step": ([ctypes.POINTER(Mamba1StepArgs), c_vp], ctypes.c_int),
+    "mamba_conv1d_step": ([ctypes.POINTER(Conv1dStepArgs), c_vp], ctypes.c_int),
     "mamba2_step_workspace_size": ([ctypes.POINTER(Mamba2StepArgs)], ctypes.c_size_t),
     "mamba2_step_ssm": ([ctypes.POINTER(Mamba2StepArgs), c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),
     "mamba2_step_ssm_timed": ([ctypes.POINTER(Mamba2StepArgs), c_vp, ctypes.c_size_t, c_vp, c_vp, c_vp],

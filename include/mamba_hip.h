@@ -22,7 +22,8 @@
  *                          (src/mamba3/single_ssd/ssd/serial_recalculated/serial_recalculated.rs:86-114)
  *   mamba1_scan_fwd     <- Mamba1::selective_scan (src/mamba1/mamba1.rs:422-430)
  *                          plus the silu(z) gate of Mamba1::forward (mamba1.rs:348)
- *   mamba1_scan_step    <- Mamba1::selective_scan_step (src/mamba1/mamba1.rs:666-674)
+ *   mamba1_scan_step    <- Mamba1::selective_scan_step (src/mamba1/mamba1.rs:666-733)
+ *   mamba_conv1d_step   <- the conv-window step of Mamba1::step (src/mamba1/mamba1.rs:558-597)
  *   mamba2_step_ssm     <- the body of Mamba2::step between in_proj and out_proj
  *                          (src/mamba2/mamba2.rs:857-995)
  *   mamba_rmsnorm       <- RmsNorm::forward (src/modules/norm/rms_norm.rs:53-98), the
@@ -151,6 +152,56 @@ int mamba1_scan_fwd(const mamba1_scan_args* args, mamba_stream_t stream);
 /* kernel (benchmark timing; no counterpart in the reference).                */
 int mamba1_scan_fwd_timed(const mamba1_scan_args* args, mamba_stream_t stream, void* event_start,
                           void* event_stop);
+
+/* ------------------------------------------------------------------------- */
+/* Mamba-1 recurrent decode step (f32), one token per sequence:                */
+/*                                                                             */
+/*   dl = softplus(delta + delta_bias)  (or delta as given)                   */
+/*   state[b,d,n] <- exp(dl A[d,n]) state[b,d,n] + (dl B[b,n]) u[b,d]          */
+/*   y[b,d] = (sum_n state[b,d,n] C[b,n] + D[d] u[b,d]) * silu(z[b,d])          */
+/*                                                                             */
+/* Replaces Mamba1::selective_scan_step (src/mamba1/mamba1.rs:666-733); with   */
+/* delta_bias/delta_softplus/z it also covers the dt_proj bias + softplus of   */
+/* Mamba1::ssm_step (mamba1.rs:646) and the silu(res) gate of Mamba1::step     */
+/* (mamba1.rs:603).  state is Mamba1Cache::ssm_bir (src/mamba1/cache.rs:30-47),*/
+/* contiguous, updated in place.  softplus is evaluated as in mamba1_scan_fwd. */
+/* ------------------------------------------------------------------------- */
+typedef struct mamba1_step_args {
+    int32_t batch, dim, dstate;
+    const float* u;     int64_t u_sb;                /* [b, d]               */
+    const float* delta; int64_t delta_sb;            /* [b, d]               */
+    const float* A;     int64_t A_sd, A_sn;          /* [d, n]               */
+    const float* B;     int64_t B_sb, B_sn;          /* [b, n]               */
+    const float* C;     int64_t C_sb, C_sn;          /* [b, n]               */
+    const float* D;                                  /* [d] or NULL          */
+    const float* z;     int64_t z_sb;                /* [b, d] or NULL       */
+    const float* delta_bias;                         /* [d] or NULL          */
+    int32_t delta_softplus;                          /* 0 or 1               */
+    float* state;                                    /* [b, d, n], in/out    */
+    float* y;           int64_t y_sb;                /* [b, d]               */
+} mamba1_step_args;
+
+int mamba1_scan_step(const mamba1_step_args* args, mamba_stream_t stream);
+
+/* ------------------------------------------------------------------------- */
+/* Depthwise causal conv, one step (the conv-window roll of Mamba1::step,      */
+/* src/mamba1/mamba1.rs:558-597; Mamba-2's is fused into mamba2_step_ssm):     */
+/*   state[b,c,:] <- (state[b,c,1:], x[b,c])                                   */
+/*   out[b,c] = act(sum_k state[b,c,k] w[c,k] + bias[c]),  act = SiLU or id    */
+/* state is Mamba1Cache::conv_bik [b, c, K] f32, contiguous, in place.          */
+/* ------------------------------------------------------------------------- */
+typedef struct mamba_conv1d_step_args {
+    int32_t batch, channels, kernel;
+    int32_t x_dtype, out_dtype;        /* mamba_dtype                            */
+    const void* x;  int64_t x_sb;      /* [b, c] new column                      */
+    float* state;                      /* [b, c, K], in/out                      */
+    const float* w;                    /* [c, K] (Conv1d weight [c, 1, K])       */
+    const float* bias;                 /* [c] or NULL                            */
+    int32_t silu;                      /* 1: SiLU after the bias                 */
+    void* out;      int64_t out_sb;    /* [b, c]                                 */
+} mamba_conv1d_step_args;
+
+int mamba_conv1d_step(const mamba_conv1d_step_args* args, mamba_stream_t stream);
 
 /* ------------------------------------------------------------------------- */
 /* Mamba-2 recurrent decode step: everything of Mamba2::step between in_proj  */

@@ -42,7 +42,7 @@ def lib():
         _lib = ctypes.CDLL(_LIB_PATH)
         for prec in (32, 64):
             for name in ("ssd2_serial", "ssd2_minimal", "ssd2_recurrent", "mamba1_scan",
-                         "mamba1_step", "mamba2_step_ssm", "rmsnorm", "linear", "ssd3_serial",
+                         "mamba1_step", "mamba2_step_ssm", "rmsnorm", "linear", "ssd3_serial", "conv1d_step",
                          "ssd3_recurrent"):
                 getattr(_lib, f"orc{prec}_{name}").restype = None
     return _lib
@@ -144,6 +144,32 @@ def mamba2_step_ssm(zxbcdt, conv_state, conv_w, conv_b, dt_bias, A, D, norm_w, s
                                  ctypes.c_float(dt_limit[0]), ctypes.c_float(dt_limit[1]),
                                  _ptr(norm_w), _ptr(ss), _ptr(out), int(bool(norm_before_gate)))
     return out, cs, ss
+
+
+def conv1d_step(x, state, w, bias=None, silu=True, prec=64):
+    """One depthwise causal conv step: x[b,c], state[b,c,K] -> (out[b,c], new state)."""
+    x, w, bias = _f32(x), _f32(w), _f32(bias)
+    st = np.array(state, dtype=np.float32, copy=True)
+    b, c, k = st.shape
+    out = np.zeros((b, c), np.float32)
+    _fn("conv1d_step", prec)(b, c, k, _ptr(x), _ptr(st), _ptr(w), _ptr(bias), int(bool(silu)), _ptr(out))
+    return out, st
+
+
+def mamba1_block_step(x, p, conv_state, ssm_state, prec=64):
+    """Mamba1::step (src/mamba1/mamba1.rs:533-612): in_proj -> split (xs, res) ->
+    conv step + SiLU -> x_proj -> split (dt, B, C) -> dt_proj (+bias) -> softplus ->
+    selective_scan_step -> * silu(res) -> out_proj.  Returns (y, conv', ssm')."""
+    d_inner = p["conv_w"].shape[0]
+    r = p["dt_proj_w"].shape[0]
+    n = p["A"].shape[1]
+    xr = linear(x, p["in_proj_w"], None, prec)
+    u, cs = conv1d_step(xr[:, :d_inner], conv_state, p["conv_w"], p["conv_b"], True, prec)
+    x_dbl = linear(u, p["x_proj_w"], None, prec)
+    delta = linear(np.ascontiguousarray(x_dbl[:, :r]), p["dt_proj_w"], None, prec)
+    y, ss = mamba1_step(u, delta, p["A"], x_dbl[:, r:r + n], x_dbl[:, r + n:], ssm_state, p["D"],
+                        xr[:, d_inner:], p["dt_proj_b"], True, prec)
+    return linear(y, p["out_proj_w"], None, prec), cs, ss
 
 
 def rmsnorm(x, w, prec=64):

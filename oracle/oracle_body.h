@@ -422,6 +422,23 @@ void F(mamba2_step_ssm)(int batch, int nheads, int headdim, int ngroups, int dst
     }
 }
 
+/* Depthwise causal conv, one step: the window roll + dot + bias (+ SiLU) of   */
+/* Mamba1::step (src/mamba1/mamba1.rs:558-597).  x[b,c]; state[b,c,K] in place;*/
+/* w[c,K]; bias[c] (nullable); out[b,c].                                      */
+void F(conv1d_step)(int batch, int channels, int K, const float* x, float* state, const float* w,
+                    const float* bias, int silu, float* out) {
+    for (int b = 0; b < batch; ++b)
+        for (int c = 0; c < channels; ++c) {
+            float* win = state + ((size_t)b * channels + c) * K;
+            for (int k = 0; k + 1 < K; ++k) win[k] = win[k + 1];
+            win[K - 1] = x[(size_t)b * channels + c];
+            REAL acc = 0;
+            for (int k = 0; k < K; ++k) acc += (REAL)win[k] * (REAL)w[(size_t)c * K + k];
+            if (bias) acc += (REAL)bias[c];
+            out[(size_t)b * channels + c] = (float)(silu ? F(silu_)(acc) : acc);
+        }
+}
+
 /* RmsNorm (src/modules/norm/rms_norm.rs:53-98): x / sqrt(mean(x^2)+eps) * w. */
 void F(rmsnorm)(int rows, int cols, const float* x, const float* w, float* out) {
     for (int r = 0; r < rows; ++r) {

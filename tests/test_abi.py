@@ -52,6 +52,8 @@ int main(void) {{ printf("%zu\\n", sizeof({struct_name})); {body} return 0; }}
 
 @pytest.mark.parametrize("cls_name,c_name", [("Ssd2Args", "mamba_ssd2_args"),
                                              ("Mamba1ScanArgs", "mamba1_scan_args"),
+                                             ("Mamba1StepArgs", "mamba1_step_args"),
+                                             ("Conv1dStepArgs", "mamba_conv1d_step_args"),
                                              ("Mamba2StepArgs", "mamba2_step_args"),
                                              ("RmsNormArgs", "mamba_rmsnorm_args")])
 def test_struct_layouts_match_header(cls_name, c_name):

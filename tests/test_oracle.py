@@ -327,3 +327,26 @@ def test_rmsnorm_and_linear_known_answers():
     bias = rng.standard_normal(4).astype(np.float32)
     np.testing.assert_allclose(oracle.linear(X, W), X.astype(np.float64) @ W, rtol=1e-6, atol=1e-6)
     np.testing.assert_allclose(oracle.linear(X, W, bias), X.astype(np.float64) @ W + bias, rtol=1e-6, atol=1e-6)
+
+
+def test_conv1d_step_unroll_equals_convolution():
+    """Stepping the causal depthwise conv window token by token equals a full
+    causal convolution (numpy.convolve) of the sequence prefixed by the initial
+    window; plus bias and SiLU."""
+    rng = np.random.default_rng(21)
+    b, c, k, L = 2, 5, 4, 9
+    w = rng.standard_normal((c, k)).astype(np.float32)
+    bias = rng.standard_normal(c).astype(np.float32)
+    st0 = rng.standard_normal((b, c, k)).astype(np.float32)
+    xs = rng.standard_normal((L, b, c)).astype(np.float32)
+    st = st0
+    for t in range(L):
+        out, st = oracle.conv1d_step(xs[t], st, w, bias, silu=(t % 2 == 0))
+        for bi in range(b):
+            for ci in range(c):
+                seq = np.concatenate([st0[bi, ci], xs[:t + 1, bi, ci]]).astype(np.float64)
+                full = np.convolve(seq, w[ci, ::-1].astype(np.float64), mode="valid")  # correlation
+                v = full[t + 1] + bias[ci]
+                ref = v / (1 + np.exp(-v)) if t % 2 == 0 else v
+                np.testing.assert_allclose(out[bi, ci], ref, rtol=1e-5, atol=1e-6)
+    np.testing.assert_array_equal(st[:, :, -1], xs[-1])
