@@ -283,7 +283,8 @@ def bench_decode(args):
         "config": {"workload": "mamba2_decode_step_cfg3", **cfg, "weights": "bf16", "state": "f32",
                    "graph": "hip graph of the whole step", "eager_ms_per_step": eager_ms,
                    "step_bytes": step_bytes, "step_hbm_gbs": step_gbs, "step_hbm_frac": step_gbs / HBM_PEAK_GBS,
-                   "entry": "mamba_rmsnorm + torch.mm + mamba2_step_ssm + torch.mm per layer"},
+                   "entry": ("mamba2_layer_step per layer (packed products, fused norm/residual)" if stack.fused
+                             else "mamba_rmsnorm + torch.mm + mamba2_step_ssm + torch.mm per layer")},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel_ms": kern_ms,
                      "algorithmic_bytes": kernel_bytes, "kernel": "step2_ssm_fast<128> (mean over all layers)"},

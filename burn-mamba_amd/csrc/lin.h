@@ -1,0 +1,53 @@
+// Weight-streaming dense product for one-token-per-sequence steps (decode),
+// shared by the step entry points.
+#pragma once
+
+#include "common.h"
+
+namespace mamba {
+
+typedef __bf16 lin_bf16x8_t __attribute__((ext_vector_type(8)));
+
+// Packed operand formats (v_mfma_f32_32x32x16_bf16, lane l, r = l % 32, half = l / 32):
+//   weight W[k][n] (K x N):  block (j, s) = 32 columns x 16 k, lane l holds
+//                            W[16 s + 8 half + e][32 j + r], e = 0..7 (16 bytes);
+//                            blocks ordered j-major: offset (j * KS + s) * 64 lanes.
+//   activation A[m][k] (M x K): block (s, i) = 32 rows x 16 k, lane l holds
+//                            A[32 i + r][16 s + 8 half + e];
+//                            blocks ordered s-major: offset (s * MT + i) * 64 lanes.
+// KS = K / 16; MT = lin_mt(M), the number of 32-row tiles rounded up to 1, 2, 4
+// or 8 (the kernel is instantiated for those).  Rows m >= M of an activation
+// block are never written and never reach an output (row m of the product
+// depends on row m of A only).
+inline int lin_mt(int M) { return M <= 32 ? 1 : M <= 64 ? 2 : M <= 128 ? 4 : 8; }
+inline size_t lin_weight_elems(int K, int N) { return (size_t)((N + 31) / 32) * 32 * K; }
+inline size_t lin_act_elems(int M, int K) { return (size_t)lin_mt(M) * 32 * K; }
+
+__device__ __forceinline__ int64_t lin_act_offset(int m, int k, int MT) {
+    const int s = k >> 4, i = m >> 5, lane = (m & 31) + 32 * ((k >> 3) & 1);
+    return ((int64_t)(s * MT + i) * 64 + lane) * 8 + (k & 7);
+}
+
+enum LinEpilogue { LIN_STORE = 0, LIN_RESID_RMS = 1 };
+
+struct LinParams {
+    int M, N, K, MT;         // MT = lin_mt(M)
+    const lin_bf16x8_t* W;   // packed weight
+    const lin_bf16x8_t* A;   // packed activation
+    const float* bias;       // [N] or NULL
+    // LIN_STORE: out[m, n] = acc + bias
+    void* out; int64_t out_ld; bool out_bf16;
+    // LIN_RESID_RMS: xres[m, n] += acc / rms[m] + bias, rms[m] = sqrt(sum_h ssq[m, h] / rms_d + eps)
+    float* xres; int64_t xres_ld;
+    const float* ssq; int ssq_h; float rms_d;
+    // side job (may be empty): slide the conv windows of channels [c0, c0 + nc)
+    // of every row m < M, appending zx[m, zx_off + c]
+    float* conv; int conv_dim, conv_k, c0, nc;
+    const void* zx; int64_t zx_ld; bool zx_bf16; int zx_off;
+};
+
+// Launch the product on `stream`; the caller has validated the shapes
+// (K % 16 == 0, 1 <= M <= 256).
+void lin_launch(const LinParams& p, int epilogue, hipStream_t stream);
+
+}  // namespace mamba

@@ -1,0 +1,299 @@
+// Weight-streaming dense product Y[M, N] = A[M, K] W[K, N] for decode steps
+// (M = batch <= 256): the in_proj / out_proj of the recurrent blocks.
+//
+// At decode the product is bound by streaming W from HBM (every weight byte is
+// used M times, M small), so the design point is "each weight byte read once,
+// in whole 1 KB wave loads, with enough bytes in flight":
+//   * W is packed once (mamba_linear_pack) into v_mfma_f32_32x32x16_bf16
+//     B-operand order, 32-column tiles contiguous along K;
+//   * the activation arrives already in A-operand order (written that way by
+//     the producing kernel), so it too is read as contiguous 1 KB blocks (from
+//     L2: it is small and shared by every workgroup);
+//   * one workgroup owns one 32-column tile over all of K; its NW waves split
+//     K, each software-pipelines its loads two stages deep, and the partial
+//     accumulators are reduced through LDS, so there is no split-K traffic to
+//     HBM and no atomics;
+//   * epilogues: plain store (+bias), or the residual update
+//     x += acc / rms(row) (+bias) that finishes a gated RMSNorm whose per-row
+//     scale commutes with the product.
+#include <algorithm>
+
+#include "lin.h"
+
+namespace mamba {
+
+typedef float lin_f32x16_t __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ lin_f32x16_t lin_mfma(lin_bf16x8_t a, lin_bf16x8_t b, lin_f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+template <int MT>
+struct LinStage {
+    static constexpr int U = MT == 1 ? 8 : MT == 2 ? 4 : MT == 4 ? 2 : 1;  // k-steps per pipeline stage
+    lin_bf16x8_t w[U];
+    lin_bf16x8_t a[U][MT];
+};
+
+template <int MT>
+__device__ __forceinline__ void lin_load(LinStage<MT>& st, const lin_bf16x8_t* Wj, const lin_bf16x8_t* Ap, int s) {
+#pragma unroll
+    for (int u = 0; u < LinStage<MT>::U; ++u) {
+        st.w[u] = Wj[(int64_t)(s + u) * 64];
+#pragma unroll
+        for (int i = 0; i < MT; ++i) st.a[u][i] = Ap[((int64_t)(s + u) * MT + i) * 64];
+    }
+}
+
+template <int MT>
+__device__ __forceinline__ void lin_compute(const LinStage<MT>& st, lin_f32x16_t (&acc)[MT]) {
+#pragma unroll
+    for (int u = 0; u < LinStage<MT>::U; ++u)
+#pragma unroll
+        for (int i = 0; i < MT; ++i) acc[i] = lin_mfma(st.a[u][i], st.w[u], acc[i]);
+}
+
+__device__ void lin_side_job(const LinParams& p) {
+    if (p.conv == nullptr) return;
+    const int total = p.M * p.nc;
+    for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += gridDim.x * blockDim.x) {
+        const int m = idx / p.nc, c = idx - m * p.nc;
+        const int ch = p.c0 + c;
+        float* win = p.conv + ((int64_t)m * p.conv_dim + ch) * p.conv_k;
+        const int64_t zi = (int64_t)m * p.zx_ld + p.zx_off + ch;
+        const float xin = p.zx_bf16 ? bf16_to_f32(static_cast<const bf16_t*>(p.zx)[zi])
+                                    : static_cast<const float*>(p.zx)[zi];
+        for (int k = 0; k + 1 < p.conv_k; ++k) win[k] = win[k + 1];
+        win[p.conv_k - 1] = xin;
+    }
+}
+
+// grid: ceil(N / 32) workgroups of NW waves.
+template <int MT, int NW, int EPI>
+__global__ __launch_bounds__(64 * NW) void lin_stream(LinParams p) {
+    __shared__ float s_red[NW][2][16][64];
+    __shared__ float s_inv[256];
+    const int j = blockIdx.x;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int KS = p.K >> 4;
+    const int s0 = (KS * wave) / NW, s1 = (KS * (wave + 1)) / NW;
+
+    lin_side_job(p);
+
+    const lin_bf16x8_t* Wj = p.W + (int64_t)j * KS * 64 + lane;
+    const lin_bf16x8_t* Ap = p.A + lane;
+    lin_f32x16_t acc[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][v] = 0.f;
+
+    constexpr int U = LinStage<MT>::U;
+    const int nstage = (s1 - s0) / U;
+    int s = s0;
+    if (nstage > 0) {
+        LinStage<MT> sa, sb;
+        lin_load<MT>(sa, Wj, Ap, s);
+        for (int st = 0; st < nstage; st += 2) {
+            const bool more1 = st + 1 < nstage;
+            if (more1) lin_load<MT>(sb, Wj, Ap, s + U);
+            lin_compute<MT>(sa, acc);
+            if (more1) {
+                if (st + 2 < nstage) lin_load<MT>(sa, Wj, Ap, s + 2 * U);
+                lin_compute<MT>(sb, acc);
+            }
+            s += 2 * U;
+        }
+        s = s0 + nstage * U;
+    }
+    for (; s < s1; ++s) {
+        const lin_bf16x8_t w = Wj[(int64_t)s * 64];
+#pragma unroll
+        for (int i = 0; i < MT; ++i) acc[i] = lin_mfma(Ap[((int64_t)s * MT + i) * 64], w, acc[i]);
+    }
+
+    if (EPI == LIN_RESID_RMS) {
+        for (int m = threadIdx.x; m < p.M; m += 64 * NW) {
+            float ss = 0.f;
+            for (int h = 0; h < p.ssq_h; ++h) ss += p.ssq[(int64_t)m * p.ssq_h + h];
+            s_inv[m] = sqrtf(ss / p.rms_d + kDivEpsF32);
+        }
+    }
+
+    // cross-wave reduction through LDS, two 32-row tiles at a time
+#pragma unroll
+    for (int ig = 0; ig < MT; ig += 2) {
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2)
+            if (ig + t2 < MT)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) s_red[wave][t2][v][lane] = acc[ig + t2 < MT ? ig + t2 : 0][v];
+        __syncthreads();
+        for (int e = threadIdx.x; e < 2 * 1024; e += 64 * NW) {
+            const int t2 = e >> 10, v = (e >> 6) & 15, ln = e & 63;
+            if (ig + t2 >= MT) break;
+            const int m = 32 * (ig + t2) + 8 * (v >> 2) + 4 * (ln >> 5) + (v & 3);
+            const int n = 32 * j + (ln & 31);
+            if (m >= p.M || n >= p.N) continue;
+            float sum = 0.f;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) sum += s_red[w][t2][v][ln];
+            if (EPI == LIN_STORE) {
+                if (p.bias) sum += p.bias[n];
+                if (p.out_bf16)
+                    static_cast<bf16_t*>(p.out)[(int64_t)m * p.out_ld + n] = f32_to_bf16(sum);
+                else
+                    static_cast<float*>(p.out)[(int64_t)m * p.out_ld + n] = sum;
+            } else {
+                float v2 = sum / s_inv[m];
+                if (p.bias) v2 += p.bias[n];
+                p.xres[(int64_t)m * p.xres_ld + n] += v2;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+template <int MT>
+static void lin_launch_mt(const LinParams& p, int epi, hipStream_t stream) {
+    const dim3 grid((p.N + 31) / 32);
+    // waves per workgroup: enough to put ~40 k-steps (40 KB of weight) on each
+    const int KS = p.K / 16;
+    if (KS >= 256) {
+        if (epi == LIN_STORE) hipLaunchKernelGGL((lin_stream<MT, 8, LIN_STORE>), grid, dim3(512), 0, stream, p);
+        else hipLaunchKernelGGL((lin_stream<MT, 8, LIN_RESID_RMS>), grid, dim3(512), 0, stream, p);
+    } else {
+        if (epi == LIN_STORE) hipLaunchKernelGGL((lin_stream<MT, 4, LIN_STORE>), grid, dim3(256), 0, stream, p);
+        else hipLaunchKernelGGL((lin_stream<MT, 4, LIN_RESID_RMS>), grid, dim3(256), 0, stream, p);
+    }
+}
+
+void lin_launch(const LinParams& p, int epi, hipStream_t stream) {
+    switch (p.MT) {
+        case 1: lin_launch_mt<1>(p, epi, stream); break;
+        case 2: lin_launch_mt<2>(p, epi, stream); break;
+        case 4: lin_launch_mt<4>(p, epi, stream); break;
+        default: lin_launch_mt<8>(p, epi, stream); break;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Weight packing: W [K, N] row-major (Burn Linear layout [d_in, d_out]), f32 or
+// bf16, into the packed bf16 B-operand format; columns past N are zero.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void lin_pack_kernel(const void* W, int K, int N, int64_t ldw, bool w_bf16,
+                                                       lin_bf16x8_t* out) {
+    const int64_t KS = K / 16;
+    const int64_t nlanes = (int64_t)((N + 31) / 32) * KS * 64;
+    for (int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x; g < nlanes; g += (int64_t)gridDim.x * 256) {
+        const int lane = (int)(g & 63);
+        const int64_t blk = g >> 6;
+        const int j = (int)(blk / KS), s = (int)(blk % KS);
+        const int n = 32 * j + (lane & 31);
+        const int k0 = 16 * s + 8 * (lane >> 5);
+        lin_bf16x8_t v;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float f = 0.f;
+            if (n < N) {
+                const int64_t idx = (int64_t)(k0 + e) * ldw + n;
+                f = w_bf16 ? bf16_to_f32(static_cast<const bf16_t*>(W)[idx]) : static_cast<const float*>(W)[idx];
+            }
+            v[e] = (__bf16)f;
+        }
+        out[g] = v;
+    }
+}
+
+}  // namespace mamba
+
+using namespace mamba;
+
+extern "C" size_t mamba_linear_packed_size(int32_t d_in, int32_t d_out) {
+    if (d_in <= 0 || d_out <= 0 || d_in % 16 != 0) return 0;
+    return lin_weight_elems(d_in, d_out) * 2;
+}
+
+extern "C" int mamba_linear_pack(const void* weight, int32_t d_in, int32_t d_out, int64_t ld, int32_t dtype,
+                                 void* packed, mamba_stream_t stream) {
+    MAMBA_CHECK_ARG(weight && packed, "weight and packed are required");
+    MAMBA_CHECK_ARG(d_in > 0 && d_out > 0, "d_in and d_out must be >= 1");
+    MAMBA_CHECK_ARG(d_in % 16 == 0, "d_in must be a multiple of 16");
+    MAMBA_CHECK_ARG(ld >= d_out, "ld must be >= d_out");
+    MAMBA_CHECK_ARG(dtype == MAMBA_F32 || dtype == MAMBA_BF16, "bad dtype");
+    MAMBA_CHECK_ARG(((uintptr_t)packed & 15u) == 0, "packed must be 16-byte aligned");
+    const int64_t nlanes = (int64_t)((d_out + 31) / 32) * (d_in / 16) * 64;
+    const int grid = (int)std::min<int64_t>((nlanes + 255) / 256, 8192);
+    hipLaunchKernelGGL(lin_pack_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, weight, d_in, d_out, ld,
+                       dtype == MAMBA_BF16, static_cast<lin_bf16x8_t*>(packed));
+    MAMBA_CHECK_LAUNCH();
+    return MAMBA_OK;
+}
+
+// ---------------------------------------------------------------------------
+// General entry: y = x W (+bias) with x row-major; x is packed into the
+// workspace first (one 16-byte run of 8 consecutive k per thread).
+// ---------------------------------------------------------------------------
+namespace mamba {
+
+__global__ __launch_bounds__(256) void lin_act_pack_kernel(const void* x, int M, int K, int64_t ldx, bool x_bf16,
+                                                           bf16_t* a_out, int mt) {
+    const int groups = K / 8;
+    const int64_t total = (int64_t)M * groups;
+    for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
+        const int m = (int)(idx / groups), g = (int)(idx % groups);
+        uint32_t u[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int64_t i0 = (int64_t)m * ldx + 8 * g + 2 * e;
+            float f0, f1;
+            if (x_bf16) {
+                f0 = bf16_to_f32(static_cast<const bf16_t*>(x)[i0]);
+                f1 = bf16_to_f32(static_cast<const bf16_t*>(x)[i0 + 1]);
+            } else {
+                f0 = static_cast<const float*>(x)[i0];
+                f1 = static_cast<const float*>(x)[i0 + 1];
+            }
+            u[e] = (uint32_t)f32_to_bf16(f0) | ((uint32_t)f32_to_bf16(f1) << 16);
+        }
+        *reinterpret_cast<uint4*>(a_out + lin_act_offset(m, 8 * g, mt)) = make_uint4(u[0], u[1], u[2], u[3]);
+    }
+}
+
+}  // namespace mamba
+
+extern "C" size_t mamba_linear_workspace_size(const mamba_linear_args* a) {
+    if (a == nullptr || a->rows <= 0 || a->d_in <= 0) return 0;
+    return align_up(lin_act_elems(a->rows, a->d_in) * 2, 256);
+}
+
+extern "C" int mamba_linear_fwd(const mamba_linear_args* a, void* ws, size_t ws_bytes, mamba_stream_t stream) {
+    MAMBA_CHECK_ARG(a != nullptr, "args is NULL");
+    MAMBA_CHECK_ARG(a->rows >= 1 && a->rows <= 256, "rows must be in [1, 256]");
+    MAMBA_CHECK_ARG(a->d_in > 0 && a->d_in % 16 == 0 && a->d_out > 0, "d_in must be a positive multiple of 16");
+    MAMBA_CHECK_ARG(a->x && a->packed_w && a->y, "x, packed_w and y are required");
+    MAMBA_CHECK_ARG(a->x_dtype == MAMBA_F32 || a->x_dtype == MAMBA_BF16, "bad x_dtype");
+    MAMBA_CHECK_ARG(a->y_dtype == MAMBA_F32 || a->y_dtype == MAMBA_BF16, "bad y_dtype");
+    MAMBA_CHECK_ARG(a->x_ld >= a->d_in && a->y_ld >= a->d_out, "leading dimensions too small");
+    MAMBA_CHECK_ARG(((uintptr_t)a->packed_w & 15u) == 0, "packed_w must be 16-byte aligned");
+    const size_t need = mamba_linear_workspace_size(a);
+    if (ws == nullptr || ws_bytes < need || ((uintptr_t)ws & 15u) != 0) {
+        set_error("mamba_linear_fwd: a 16-byte aligned workspace of " + std::to_string(need) + " bytes is required");
+        return MAMBA_ERR_WORKSPACE;
+    }
+    const int mt = lin_mt(a->rows);
+    hipStream_t s = (hipStream_t)stream;
+    const int64_t total = (int64_t)a->rows * (a->d_in / 8);
+    hipLaunchKernelGGL(lin_act_pack_kernel, dim3((int)std::min<int64_t>((total + 255) / 256, 4096)), dim3(256), 0, s,
+                       a->x, a->rows, a->d_in, a->x_ld, a->x_dtype == MAMBA_BF16, static_cast<bf16_t*>(ws), mt);
+    MAMBA_CHECK_LAUNCH();
+    LinParams p = {};
+    p.M = a->rows; p.N = a->d_out; p.K = a->d_in; p.MT = mt;
+    p.W = static_cast<const lin_bf16x8_t*>(a->packed_w);
+    p.A = static_cast<const lin_bf16x8_t*>(ws);
+    p.bias = a->bias;
+    p.out = a->y; p.out_ld = a->y_ld; p.out_bf16 = a->y_dtype == MAMBA_BF16;
+    lin_launch(p, LIN_STORE, s);
+    MAMBA_CHECK_LAUNCH();
+    return MAMBA_OK;
+}

@@ -26,6 +26,7 @@
 // (conv_bvk [b, conv_dim, K] f32 and ssm_bhpr [b, H, P, N] f32, cache.rs:98-122),
 // so a state tile of one (b, h) is one contiguous P*N*4-byte block.
 #include "common.h"
+#include "lin.h"
 
 namespace mamba {
 
@@ -41,6 +42,11 @@ struct Step2Params {
     void* out; int64_t out_sb;
     float* g_ws;    // [nb, d_inner]  gated (or raw, if norm_before_gate) y
     float* ssq_ws;  // [nb, H]        sum of squares of g_ws per head
+    // packed mode (the fused layer step): instead of g_ws, write the out_proj
+    // operand g * norm_w (norm_before_gate: y * norm_w * silu(z)) in bf16, in
+    // the packed activation layout of lin.h with MT = a_mt; the 1/rms of the
+    // row is applied after the product (it is a per-row scalar).
+    bf16_t* a_out; int a_mt;
 };
 
 __device__ __forceinline__ float ld_act(const void* base, int64_t i, bool bf16) {
@@ -72,7 +78,7 @@ __device__ __forceinline__ float block_sum_256(float v, float* s_red) {
 // Fast path: headdim 64, dstate N in {64, 128}, conv width 4, 256 threads.
 // Thread t owns float4 column n4 = t % (N/4) of rows row0 + i*RPI, i < R.
 // ---------------------------------------------------------------------------
-template <int N>
+template <int N, bool PACK>
 __global__ __launch_bounds__(256) void step2_ssm_fast(Step2Params p) {
     constexpr int P = 64;
     constexpr int LPR = N / 4;      // lanes per state row
@@ -83,6 +89,7 @@ __global__ __launch_bounds__(256) void step2_ssm_fast(Step2Params p) {
     __shared__ __align__(16) float s_B[N];
     __shared__ __align__(16) float s_C[N];
     __shared__ float s_red[4];
+    __shared__ __align__(16) float s_pk[PACK ? P : 1];
 
     const int t = threadIdx.x;
     const int bh = blockIdx.x;
@@ -169,12 +176,52 @@ __global__ __launch_bounds__(256) void step2_ssm_fast(Step2Params p) {
         const int pr = row0 + (n4 >> 2) * RPI;
         const float y = ysum + Dh * s_x[pr];
         float gv = y;
-        if (!p.norm_before_gate) gv *= silu_fast(ld_act(zrow, h * P + pr, p.zx_bf16));
-        p.g_ws[(int64_t)b * p.d_inner + h * P + pr] = gv;
+        if (PACK) {
+            const float zg = silu_fast(ld_act(zrow, h * P + pr, p.zx_bf16));
+            if (!p.norm_before_gate) gv *= zg;
+            s_pk[pr] = p.norm_before_gate ? y * p.norm_w[h * P + pr] * zg : gv * p.norm_w[h * P + pr];
+        } else {
+            if (!p.norm_before_gate) gv *= silu_fast(ld_act(zrow, h * P + pr, p.zx_bf16));
+            p.g_ws[(int64_t)b * p.d_inner + h * P + pr] = gv;
+        }
         sq = gv * gv;
     }
-    sq = block_sum_256(sq, s_red);
+    sq = block_sum_256(sq, s_red);  // its barriers also publish s_pk
     if (t == 0) p.ssq_ws[bh] = sq;
+    if (PACK && t < P / 8) {
+        // 8 consecutive channels are one 16-byte run of the packed layout
+        const float4 lo = reinterpret_cast<const float4*>(s_pk)[2 * t];
+        const float4 hi = reinterpret_cast<const float4*>(s_pk)[2 * t + 1];
+        uint4 v;
+        v.x = (uint32_t)f32_to_bf16(lo.x) | ((uint32_t)f32_to_bf16(lo.y) << 16);
+        v.y = (uint32_t)f32_to_bf16(lo.z) | ((uint32_t)f32_to_bf16(lo.w) << 16);
+        v.z = (uint32_t)f32_to_bf16(hi.x) | ((uint32_t)f32_to_bf16(hi.y) << 16);
+        v.w = (uint32_t)f32_to_bf16(hi.z) | ((uint32_t)f32_to_bf16(hi.w) << 16);
+        *reinterpret_cast<uint4*>(p.a_out + lin_act_offset(b, h * P + 8 * t, p.a_mt)) = v;
+    }
+}
+
+// RmsNorm of one residual row into the packed activation layout (bf16):
+// out = x / sqrt(mean(x^2) + eps) * w  (rms_norm.rs:53-98).  grid (rows), 256 threads.
+__global__ __launch_bounds__(256) void rmsnorm_pack(const float* x, int64_t x_sr, int cols, const float* w,
+                                                    bf16_t* a_out, int a_mt) {
+    __shared__ float s_red[4];
+    const int r = blockIdx.x, t = threadIdx.x;
+    const float* xr = x + (int64_t)r * x_sr;
+    float ss = 0.f;
+    for (int c = t; c < cols; c += 256) ss += xr[c] * xr[c];
+    ss = block_sum_256(ss, s_red);
+    const float rms = sqrtf(ss / (float)cols + kDivEpsF32);
+    for (int g = t; g < cols / 8; g += 256) {
+        uint32_t u[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int c = 8 * g + 2 * e;
+            u[e] = (uint32_t)f32_to_bf16((xr[c] / rms) * w[c]) |
+                   ((uint32_t)f32_to_bf16((xr[c + 1] / rms) * w[c + 1]) << 16);
+        }
+        *reinterpret_cast<uint4*>(a_out + lin_act_offset(r, 8 * g, a_mt)) = make_uint4(u[0], u[1], u[2], u[3]);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -359,6 +406,7 @@ static int step2_make_params(const mamba2_step_args* a, void* ws, size_t ws_byte
     p.out = a->out; p.out_sb = a->out_sb;
     p.g_ws = static_cast<float*>(ws);
     p.ssq_ws = reinterpret_cast<float*>(static_cast<char*>(ws) + align_up((size_t)p.nb * d_inner * 4, 256));
+    p.a_out = nullptr; p.a_mt = 0;
     return MAMBA_OK;
 }
 
@@ -372,9 +420,9 @@ static int step2_dispatch(const mamba2_step_args* a, void* ws, size_t ws_bytes, 
     const dim3 grid(p.nb * p.H);
     if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, stream));
     if (fast && p.N == 128)
-        hipLaunchKernelGGL(step2_ssm_fast<128>, grid, dim3(256), 0, stream, p);
+        hipLaunchKernelGGL((step2_ssm_fast<128, false>), grid, dim3(256), 0, stream, p);
     else if (fast)
-        hipLaunchKernelGGL(step2_ssm_fast<64>, grid, dim3(256), 0, stream, p);
+        hipLaunchKernelGGL((step2_ssm_fast<64, false>), grid, dim3(256), 0, stream, p);
     else
         hipLaunchKernelGGL(step2_ssm_generic, grid, dim3(256), (p.P + 2 * p.N) * sizeof(float), stream, p);
     MAMBA_CHECK_LAUNCH();
@@ -423,4 +471,131 @@ extern "C" int mamba_rmsnorm(const mamba_rmsnorm_args* a, mamba_stream_t stream)
     hipLaunchKernelGGL(rmsnorm_residual, dim3(p.rows), dim3(256), 0, (hipStream_t)stream, p);
     MAMBA_CHECK_LAUNCH();
     return MAMBA_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Fused pre-norm layer step: x += out_proj(RmsNormGated(ssm(in_proj(RmsNorm(x)))))
+// ---------------------------------------------------------------------------
+namespace mamba {
+
+struct LayerWs {
+    bf16_t* a_in; void* zx; bf16_t* a_out; float* ssq; size_t total;
+};
+
+static LayerWs layer_ws_layout(const mamba2_layer_args* a, void* base) {
+    const int d_inner = a->nheads * a->headdim;
+    const int conv_dim = d_inner + 2 * a->ngroups * a->dstate;
+    const int d_in_proj = d_inner + conv_dim + a->nheads;
+    char* p = static_cast<char*>(base);
+    LayerWs w;
+    size_t off = 0;
+    w.a_in = reinterpret_cast<bf16_t*>(p + off);
+    off += align_up(lin_act_elems(a->batch, a->d_model) * 2, 256);
+    w.zx = p + off;
+    off += align_up((size_t)a->batch * d_in_proj * (a->zxbcdt_dtype == MAMBA_BF16 ? 2 : 4), 256);
+    w.a_out = reinterpret_cast<bf16_t*>(p + off);
+    off += align_up(lin_act_elems(a->batch, d_inner) * 2, 256);
+    w.ssq = reinterpret_cast<float*>(p + off);
+    off += align_up((size_t)a->batch * a->nheads * 4, 256);
+    w.total = off;
+    return w;
+}
+
+static int layer_dispatch(const mamba2_layer_args* a, void* ws, size_t ws_bytes, hipStream_t stream,
+                          hipEvent_t ev0, hipEvent_t ev1) {
+    MAMBA_CHECK_ARG(a != nullptr, "args is NULL");
+    MAMBA_CHECK_ARG(a->batch >= 1 && a->batch <= 256, "batch must be in [1, 256]");
+    MAMBA_CHECK_ARG(a->d_model > 0 && a->d_model % 16 == 0, "d_model must be a positive multiple of 16");
+    MAMBA_CHECK_ARG(a->x && a->pre_norm_w && a->in_proj && a->out_proj, "x, pre_norm_w, in_proj, out_proj required");
+    MAMBA_CHECK_ARG(a->x_sb >= a->d_model, "x_sb shorter than a row");
+    if (!(a->headdim == 64 && (a->dstate == 64 || a->dstate == 128) && a->conv_kernel == 4)) {
+        set_error("mamba2_layer_step: needs headdim 64, dstate 64 or 128 and conv_kernel 4 "
+                  "(use mamba2_step_ssm with a separate product otherwise)");
+        return MAMBA_ERR_UNSUPPORTED;
+    }
+    MAMBA_CHECK_ARG(((uintptr_t)a->in_proj & 15u) == 0 && ((uintptr_t)a->out_proj & 15u) == 0,
+                    "packed weights must be 16-byte aligned");
+    // the state-update part: reuse the mamba2_step_ssm validation
+    mamba2_step_args sa;
+    sa.batch = a->batch; sa.nheads = a->nheads; sa.headdim = a->headdim; sa.ngroups = a->ngroups;
+    sa.dstate = a->dstate; sa.conv_kernel = a->conv_kernel;
+    sa.zxbcdt_dtype = a->zxbcdt_dtype; sa.out_dtype = MAMBA_BF16; sa.norm_before_gate = a->norm_before_gate;
+    const int d_inner = a->nheads * a->headdim;
+    const int conv_dim = d_inner + 2 * a->ngroups * a->dstate;
+    const int d_in_proj = d_inner + conv_dim + a->nheads;
+    const LayerWs w = layer_ws_layout(a, ws);
+    if (ws == nullptr || ws_bytes < w.total) {
+        set_error("mamba2_layer_step: workspace of " + std::to_string(w.total) + " bytes required");
+        return MAMBA_ERR_WORKSPACE;
+    }
+    sa.zxbcdt = w.zx; sa.zxbcdt_sb = d_in_proj;
+    sa.conv_state = a->conv_state; sa.conv_w = a->conv_w; sa.conv_b = a->conv_b;
+    sa.dt_bias = a->dt_bias; sa.A = a->A; sa.D = a->D; sa.dt_min = a->dt_min; sa.dt_max = a->dt_max;
+    sa.norm_w = a->norm_w; sa.ssm_state = a->ssm_state;
+    sa.out = w.a_out; sa.out_sb = d_inner;  // validated only; the packed path writes a_out itself
+    Step2Params p;
+    // the step-ssm workspace is not used in packed mode: hand it the ssq slot
+    int st = step2_make_params(&sa, w.ssq, (size_t)-1 >> 1, &p);
+    if (st != MAMBA_OK) return st;
+    const bool aligned = aligned16(p.ssm) && aligned16(p.conv) && aligned16(p.conv_w);
+    MAMBA_CHECK_ARG(aligned, "ssm_state, conv_state and conv_w must be 16-byte aligned");
+    p.g_ws = nullptr; p.ssq_ws = w.ssq;
+    const int mt = lin_mt(a->batch);
+    p.a_out = w.a_out; p.a_mt = mt;
+
+    // 1. pre-norm into the packed in_proj operand
+    hipLaunchKernelGGL(rmsnorm_pack, dim3(a->batch), dim3(256), 0, stream, a->x, a->x_sb, a->d_model,
+                       a->pre_norm_w, w.a_in, mt);
+    MAMBA_CHECK_LAUNCH();
+    // 2. in_proj -> zxbcdt
+    LinParams li = {};
+    li.M = a->batch; li.N = d_in_proj; li.K = a->d_model; li.MT = mt;
+    li.W = static_cast<const lin_bf16x8_t*>(a->in_proj);
+    li.A = reinterpret_cast<const lin_bf16x8_t*>(w.a_in);
+    li.bias = a->in_proj_b;
+    li.out = w.zx; li.out_ld = d_in_proj; li.out_bf16 = a->zxbcdt_dtype == MAMBA_BF16;
+    lin_launch(li, LIN_STORE, stream);
+    MAMBA_CHECK_LAUNCH();
+    // 3. conv + state update + gate, packed out_proj operand + per-head sums of squares
+    if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, stream));
+    if (p.N == 128)
+        hipLaunchKernelGGL((step2_ssm_fast<128, true>), dim3(p.nb * p.H), dim3(256), 0, stream, p);
+    else
+        hipLaunchKernelGGL((step2_ssm_fast<64, true>), dim3(p.nb * p.H), dim3(256), 0, stream, p);
+    MAMBA_CHECK_LAUNCH();
+    if (ev1) MAMBA_CHECK_HIP(hipEventRecord(ev1, stream));
+    // 4. out_proj with the gated-norm 1/rms and the residual in its epilogue; its
+    //    side job slides the B/C conv windows (every head has read them by now)
+    LinParams lo = {};
+    lo.M = a->batch; lo.N = a->d_model; lo.K = d_inner; lo.MT = mt;
+    lo.W = static_cast<const lin_bf16x8_t*>(a->out_proj);
+    lo.A = reinterpret_cast<const lin_bf16x8_t*>(w.a_out);
+    lo.bias = a->out_proj_b;
+    lo.xres = a->x; lo.xres_ld = a->x_sb;
+    lo.ssq = w.ssq; lo.ssq_h = a->nheads; lo.rms_d = (float)d_inner;
+    lo.conv = a->conv_state; lo.conv_dim = conv_dim; lo.conv_k = a->conv_kernel;
+    lo.c0 = d_inner; lo.nc = 2 * a->ngroups * a->dstate;
+    lo.zx = w.zx; lo.zx_ld = d_in_proj; lo.zx_bf16 = a->zxbcdt_dtype == MAMBA_BF16; lo.zx_off = d_inner;
+    lin_launch(lo, LIN_RESID_RMS, stream);
+    MAMBA_CHECK_LAUNCH();
+    return MAMBA_OK;
+}
+
+}  // namespace mamba
+
+extern "C" size_t mamba2_layer_workspace_size(const mamba2_layer_args* a) {
+    return a ? layer_ws_layout(a, nullptr).total : 0;
+}
+
+extern "C" int mamba2_layer_step(const mamba2_layer_args* a, void* ws, size_t ws_bytes, mamba_stream_t stream) {
+    return layer_dispatch(a, ws, ws_bytes, (hipStream_t)stream, nullptr, nullptr);
+}
+
+extern "C" int mamba2_layer_step_timed(const mamba2_layer_args* a, void* ws, size_t ws_bytes, mamba_stream_t stream,
+                                       void* ev_start, void* ev_stop) {
+    if (ev_start == nullptr || ev_stop == nullptr) {
+        set_error("mamba2_layer_step_timed: both events are required");
+        return MAMBA_ERR_INVALID_ARG;
+    }
+    return layer_dispatch(a, ws, ws_bytes, (hipStream_t)stream, (hipEvent_t)ev_start, (hipEvent_t)ev_stop);
 }

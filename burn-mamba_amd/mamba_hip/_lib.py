@@ -110,6 +110,28 @@ class RmsNormArgs(ctypes.Structure):
     ]
 
 
+class LinearArgs(ctypes.Structure):
+    _fields_ = [
+        ("rows", c_i32), ("d_in", c_i32), ("d_out", c_i32), ("x_dtype", c_i32), ("y_dtype", c_i32),
+        ("x", c_vp), ("x_ld", c_i64),
+        ("packed_w", c_vp), ("bias", c_vp),
+        ("y", c_vp), ("y_ld", c_i64),
+    ]
+
+
+class Mamba2LayerArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", c_i32), ("d_model", c_i32), ("nheads", c_i32), ("headdim", c_i32), ("ngroups", c_i32),
+        ("dstate", c_i32), ("conv_kernel", c_i32), ("norm_before_gate", c_i32), ("zxbcdt_dtype", c_i32),
+        ("x", c_vp), ("x_sb", c_i64),
+        ("pre_norm_w", c_vp), ("in_proj", c_vp), ("in_proj_b", c_vp), ("out_proj", c_vp), ("out_proj_b", c_vp),
+        ("conv_state", c_vp), ("conv_w", c_vp), ("conv_b", c_vp),
+        ("dt_bias", c_vp), ("A", c_vp), ("D", c_vp),
+        ("dt_min", ctypes.c_float), ("dt_max", ctypes.c_float),
+        ("norm_w", c_vp), ("ssm_state", c_vp),
+    ]
+
+
 # name -> (argtypes, restype); the exported symbol set of include/mamba_hip.h
 _SIGNATURES = {
     "mamba_last_error": ([], ctypes.c_char_p),
@@ -129,6 +151,14 @@ _SIGNATURES = {
     "mamba2_step_ssm_timed": ([ctypes.POINTER(Mamba2StepArgs), c_vp, ctypes.c_size_t, c_vp, c_vp, c_vp],
                               ctypes.c_int),
     "mamba_rmsnorm": ([ctypes.POINTER(RmsNormArgs), c_vp], ctypes.c_int),
+    "mamba_linear_packed_size": ([c_i32, c_i32], ctypes.c_size_t),
+    "mamba_linear_pack": ([c_vp, c_i32, c_i32, c_i64, c_i32, c_vp, c_vp], ctypes.c_int),
+    "mamba_linear_workspace_size": ([ctypes.POINTER(LinearArgs)], ctypes.c_size_t),
+    "mamba_linear_fwd": ([ctypes.POINTER(LinearArgs), c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),
+    "mamba2_layer_workspace_size": ([ctypes.POINTER(Mamba2LayerArgs)], ctypes.c_size_t),
+    "mamba2_layer_step": ([ctypes.POINTER(Mamba2LayerArgs), c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),
+    "mamba2_layer_step_timed": ([ctypes.POINTER(Mamba2LayerArgs), c_vp, ctypes.c_size_t, c_vp, c_vp, c_vp],
+                                ctypes.c_int),
 }
 
 _lib = None

@@ -25,7 +25,7 @@ from typing import List, Optional, Tuple
 import torch
 
 from . import _lib
-from ._lib import Mamba2StepArgs, RmsNormArgs, check
+from ._lib import LinearArgs, Mamba2LayerArgs, Mamba2StepArgs, RmsNormArgs, check
 from .ssd import _dtype_code, _raw_events, _stream
 
 
@@ -185,6 +185,47 @@ def rmsnorm(x: torch.Tensor, weight: Optional[torch.Tensor], out: Optional[torch
     check(_lib.lib().mamba_rmsnorm(ctypes.byref(a), _stream(x.device)), "mamba_rmsnorm")
 
 
+def pack_linear(weight: torch.Tensor) -> torch.Tensor:
+    """Pack a Linear weight [d_in, d_out] (f32/bf16) for mamba_linear_fwd and the
+    fused layer step (done once, at model load).  Returns a uint8 device buffer."""
+    d_in, d_out = weight.shape
+    if weight.stride(1) != 1:
+        raise _lib.MambaHipError("weight needs a contiguous d_out axis")
+    L = _lib.lib()
+    n = L.mamba_linear_packed_size(d_in, d_out)
+    if n == 0:
+        raise _lib.MambaHipError(f"unsupported Linear shape {d_in} x {d_out} (d_in must be a multiple of 16)")
+    out = torch.empty(n, dtype=torch.uint8, device=weight.device)
+    check(L.mamba_linear_pack(ctypes.c_void_p(weight.data_ptr()), d_in, d_out, weight.stride(0),
+                              _dtype_code(weight), ctypes.c_void_p(out.data_ptr()), _stream(weight.device)),
+          "mamba_linear_pack")
+    return out
+
+
+def linear(x: torch.Tensor, packed_w: torch.Tensor, d_out: int, bias: Optional[torch.Tensor] = None,
+           out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y = x W (+bias) through mamba_linear_fwd (rows <= 256, W packed by pack_linear)."""
+    if x.dim() != 2 or x.stride(1) != 1:
+        raise _lib.MambaHipError("x must be 2-d with a contiguous last axis")
+    rows, d_in = x.shape
+    if out is None:
+        out = torch.empty(rows, d_out, dtype=torch.float32, device=x.device)
+    a = LinearArgs()
+    a.rows, a.d_in, a.d_out = rows, d_in, d_out
+    a.x_dtype, a.y_dtype = _dtype_code(x), _dtype_code(out)
+    a.x, a.x_ld = x.data_ptr(), x.stride(0)
+    a.packed_w = packed_w.data_ptr()
+    a.bias = None if bias is None else bias.data_ptr()
+    a.y, a.y_ld = out.data_ptr(), out.stride(0)
+    L = _lib.lib()
+    need = L.mamba_linear_workspace_size(ctypes.byref(a))
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=x.device)
+    check(L.mamba_linear_fwd(ctypes.byref(a), ctypes.c_void_p(workspace.data_ptr()), workspace.numel(),
+                             _stream(x.device)), "mamba_linear_fwd")
+    return out
+
+
 @dataclass
 class Mamba2:
     """Decode-side Mamba2 block (parameters of src/mamba2/mamba2.rs:391-505)."""
@@ -256,23 +297,66 @@ class Mamba2Layer:
 class Mamba2Stack:
     """A stack of pre-norm Mamba2 layers stepped one token at a time.
 
-    The residual stream is kept in f32.  The residual add of layer l is fused
-    with the RmsNorm of layer l+1 (one mamba_rmsnorm call), so a layer is five
-    launches: rmsnorm, in_proj, mamba2_step_ssm (two kernels), out_proj.  All
-    activations live in buffers allocated once per batch size, so ``step_``
-    allocates nothing and can be captured in a HIP graph."""
+    The residual stream is kept in f32.  With ``fused`` (the default where the
+    shape allows: headdim 64, dstate 64/128, conv width 4, batch <= 256) each
+    layer is one mamba2_layer_step call: four kernels (pre-norm into the packed
+    product operand, in_proj, state update, out_proj with the gated norm's
+    1/rms and the residual in its epilogue) on weights packed once at
+    construction.  Otherwise the residual add of layer l is fused with the
+    RmsNorm of layer l+1 (one mamba_rmsnorm call) around torch.mm products and
+    mamba2_step_ssm.  All activations live in buffers allocated once per batch
+    size, so ``step_`` allocates nothing and can be captured in a HIP graph."""
 
-    def __init__(self, layers: List[Mamba2Layer]):
+    def __init__(self, layers: List[Mamba2Layer], fused: bool = True):
         assert layers
         self.layers = layers
         self.cfg = layers[0].mixer.cfg
         self._bufs = {}
+        self._args = {}
+        c = self.cfg
+        self.fused = fused and c.per_head_dim == 64 and c.state_rank in (64, 128) and c.conv_kernel == 4 \
+            and c.d_model % 16 == 0
+        # packed in_proj / out_proj per layer (mamba_linear_pack), built once
+        self._packed = [(pack_linear(l.mixer.in_proj_w), pack_linear(l.mixer.out_proj_w)) for l in layers] \
+            if self.fused else None
+        self._bias_f32 = [tuple(None if t is None else t.float().contiguous()
+                                for t in (l.mixer.in_proj_b, l.mixer.out_proj_b)) for l in layers]
 
     @staticmethod
     def init(cfg: Mamba2Config, n_layers: int, device, dtype=torch.bfloat16,
-             generator: Optional[torch.Generator] = None) -> "Mamba2Stack":
+             generator: Optional[torch.Generator] = None, fused: bool = True) -> "Mamba2Stack":
         return Mamba2Stack([Mamba2Layer(norm_w=torch.ones(cfg.d_model, device=device, dtype=torch.float32),
-                                        mixer=cfg.init(device, dtype, generator)) for _ in range(n_layers)])
+                                        mixer=cfg.init(device, dtype, generator)) for _ in range(n_layers)],
+                           fused=fused)
+
+    def _layer_args(self, i: int, x_res: torch.Tensor, cache: Mamba2Cache) -> Mamba2LayerArgs:
+        key = (i, x_res.data_ptr(), x_res.shape[0], cache.conv_bvk.data_ptr(), cache.ssm_bhpr.data_ptr())
+        a = self._args.get(key)
+        if a is not None:
+            return a
+        c, m = self.cfg, self.layers[i].mixer
+        b = x_res.shape[0]
+        if tuple(cache.ssm_bhpr.shape) != (b, c.nheads, c.per_head_dim, c.state_rank) or \
+                tuple(cache.conv_bvk.shape) != (b, c.conv_dim, c.conv_kernel):
+            raise _lib.MambaHipError("cache shapes do not match the config / batch")
+        a = Mamba2LayerArgs()
+        a.batch, a.d_model, a.nheads, a.headdim = b, c.d_model, c.nheads, c.per_head_dim
+        a.ngroups, a.dstate, a.conv_kernel = c.ngroups, c.state_rank, c.conv_kernel
+        a.norm_before_gate = int(c.is_norm_before_gate)
+        a.zxbcdt_dtype = _lib.MAMBA_BF16 if m.dtype == torch.bfloat16 else _lib.MAMBA_F32
+        a.x, a.x_sb = x_res.data_ptr(), x_res.stride(0)
+        a.pre_norm_w = self.layers[i].norm_w.data_ptr()
+        a.in_proj, a.out_proj = self._packed[i][0].data_ptr(), self._packed[i][1].data_ptr()
+        ib, ob = self._bias_f32[i]
+        a.in_proj_b = None if ib is None else ib.data_ptr()
+        a.out_proj_b = None if ob is None else ob.data_ptr()
+        a.conv_state, a.conv_w = cache.conv_bvk.data_ptr(), m.conv_w.data_ptr()
+        a.conv_b = None if m.conv_b is None else m.conv_b.data_ptr()
+        a.dt_bias, a.A, a.D = m.dt_bias.data_ptr(), m.A.data_ptr(), m.d.data_ptr()
+        a.dt_min, a.dt_max = float(c.dt_limit[0]), float(c.dt_limit[1])
+        a.norm_w, a.ssm_state = m.norm_w.data_ptr(), cache.ssm_bhpr.data_ptr()
+        self._args[key] = a
+        return a
 
     def new_caches(self, batch: int) -> List[Mamba2Cache]:
         return [l.mixer.new_cache(batch) for l in self.layers]
@@ -289,6 +373,12 @@ class Mamba2Stack:
             probe = Mamba2StepArgs()
             probe.batch, probe.nheads, probe.headdim = batch, c.nheads, c.per_head_dim
             n = _lib.lib().mamba2_step_workspace_size(ctypes.byref(probe))
+            if self.fused:
+                la = Mamba2LayerArgs()
+                la.batch, la.d_model, la.nheads, la.headdim = batch, c.d_model, c.nheads, c.per_head_dim
+                la.ngroups, la.dstate, la.conv_kernel = c.ngroups, c.state_rank, c.conv_kernel
+                la.zxbcdt_dtype = _lib.MAMBA_BF16 if dt == torch.bfloat16 else _lib.MAMBA_F32
+                n = max(n, _lib.lib().mamba2_layer_workspace_size(ctypes.byref(la)))
             bufs["ws"] = torch.empty(n, device=device, dtype=torch.uint8)
             self._bufs[key] = bufs
         return self._bufs[key]
@@ -299,6 +389,19 @@ class Mamba2Stack:
         ``events``: optional list of one torch.cuda.Event pair per layer,
         recorded around that layer's state-update kernel (benchmark timing)."""
         bufs = self.buffers(x_res.shape[0], x_res.device)
+        if self.fused and x_res.shape[0] <= 256:
+            L = _lib.lib()
+            ws = bufs["ws"]
+            wsp, stream = ctypes.c_void_p(ws.data_ptr()), _stream(x_res.device)
+            for i in range(len(self.layers)):
+                a = self._layer_args(i, x_res, caches[i])
+                if events is None:
+                    check(L.mamba2_layer_step(ctypes.byref(a), wsp, ws.numel(), stream), "mamba2_layer_step")
+                else:
+                    e0, e1 = _raw_events(events[i], x_res.device)
+                    check(L.mamba2_layer_step_timed(ctypes.byref(a), wsp, ws.numel(), stream, e0, e1),
+                          "mamba2_layer_step_timed")
+            return x_res
         prev = None
         for i, layer in enumerate(self.layers):
             rmsnorm(x_res, layer.norm_w, out=bufs["normed"], add=prev)

@@ -26,6 +26,9 @@
  *   mamba_conv1d_step   <- the conv-window step of Mamba1::step (src/mamba1/mamba1.rs:558-597)
  *   mamba2_step_ssm     <- the body of Mamba2::step between in_proj and out_proj
  *                          (src/mamba2/mamba2.rs:857-995)
+ *   mamba_linear_fwd    <- burn::nn::Linear::forward in the decode steps (packed weights)
+ *   mamba2_layer_step   <- Layer::step_one around Mamba2::step (src/modules/layer.rs:224-232,
+ *                          src/mamba2/mamba2.rs:820-1004), with packed in_proj/out_proj
  *   mamba_rmsnorm       <- RmsNorm::forward (src/modules/norm/rms_norm.rs:53-98), the
  *                          pre-norm and residual of Layer::step_one (src/modules/layer.rs:224-232)
  */
@@ -250,6 +253,79 @@ int mamba2_step_ssm(const mamba2_step_args* args, void* workspace, size_t worksp
 /* update kernel (benchmark timing; no counterpart in the reference).          */
 int mamba2_step_ssm_timed(const mamba2_step_args* args, void* workspace, size_t workspace_bytes,
                           mamba_stream_t stream, void* event_start, void* event_stop);
+
+/* ------------------------------------------------------------------------- */
+/* Dense-product weight packing for the fused decode entry points.            */
+/* A Burn Linear weight [d_in, d_out] (row-major, leading dimension ld, f32 or */
+/* bf16) is repacked once, at model load, into bf16 tiles in MFMA operand      */
+/* order; d_in must be a multiple of 16.  mamba_linear_packed_size returns the */
+/* bytes of the packed copy (0 for unsupported shapes).  No counterpart in the */
+/* reference (Burn multiplies its stored layout directly).                     */
+/* ------------------------------------------------------------------------- */
+size_t mamba_linear_packed_size(int32_t d_in, int32_t d_out);
+int mamba_linear_pack(const void* weight, int32_t d_in, int32_t d_out, int64_t ld, int32_t dtype,
+                      void* packed, mamba_stream_t stream);
+
+/* y[r, :] = x[r, :] W (+ bias) for 1 <= rows <= 256 (one token per sequence), */
+/* W packed by mamba_linear_pack: burn::nn::Linear::forward as the decode      */
+/* steps use it (in_proj/x_proj/dt_proj/out_proj, src/mamba1/mamba1.rs:551,    */
+/* 633-644,609; src/mamba2/mamba2.rs:850,1000).  bf16 operands, f32            */
+/* accumulation; x is repacked into the workspace.                            */
+typedef struct mamba_linear_args {
+    int32_t rows, d_in, d_out;
+    int32_t x_dtype, y_dtype;         /* mamba_dtype                            */
+    const void* x; int64_t x_ld;      /* [rows, d_in]                           */
+    const void* packed_w;             /* mamba_linear_pack output               */
+    const float* bias;                /* [d_out] or NULL                        */
+    void* y; int64_t y_ld;            /* [rows, d_out]                          */
+} mamba_linear_args;
+
+size_t mamba_linear_workspace_size(const mamba_linear_args* args);
+int mamba_linear_fwd(const mamba_linear_args* args, void* workspace, size_t workspace_bytes,
+                     mamba_stream_t stream);
+
+/* ------------------------------------------------------------------------- */
+/* Fused pre-norm Mamba-2 layer decode step (Layer::step_one around           */
+/* Mamba2::step, src/modules/layer.rs:224-232 + src/mamba2/mamba2.rs:820-1004): */
+/*                                                                             */
+/*   x += out_proj(RmsNormGated(ssm_step(in_proj(RmsNorm(x)))))                */
+/*                                                                             */
+/* with the same state update as mamba2_step_ssm and the caches updated in     */
+/* place.  in_proj / out_proj are the packed weights of mamba_linear_pack.     */
+/* Four kernels: RmsNorm into the product's operand layout, in_proj, the state */
+/* update (writing the out_proj operand), out_proj whose epilogue applies the  */
+/* gated norm's 1/rms and the residual add.  Supports headdim 64, dstate 64 or */
+/* 128, conv_kernel 4, batch <= 256, d_model % 16 == 0; other shapes return    */
+/* MAMBA_ERR_UNSUPPORTED (use mamba2_step_ssm with a separate product).        */
+/* ------------------------------------------------------------------------- */
+typedef struct mamba2_layer_args {
+    int32_t batch, d_model, nheads, headdim, ngroups, dstate, conv_kernel;
+    int32_t norm_before_gate;
+    int32_t zxbcdt_dtype;             /* precision of the in_proj result (bf16 like a bf16 model) */
+    float* x; int64_t x_sb;           /* [b, d_model] f32 residual stream, in/out */
+    const float* pre_norm_w;          /* [d_model] RmsNorm gamma of the layer   */
+    const void* in_proj;              /* packed [d_model, d_in_proj]            */
+    const float* in_proj_b;           /* [d_in_proj] or NULL                    */
+    const void* out_proj;             /* packed [d_inner, d_model]              */
+    const float* out_proj_b;          /* [d_model] or NULL                      */
+    float* conv_state;                /* [b, conv_dim, conv_kernel], in/out     */
+    const float* conv_w;              /* [conv_dim, conv_kernel]                */
+    const float* conv_b;              /* [conv_dim] or NULL                     */
+    const float* dt_bias;             /* [nheads] or NULL                       */
+    const float* A;                   /* [nheads]                               */
+    const float* D;                   /* [nheads] or NULL                       */
+    float dt_min, dt_max;
+    const float* norm_w;              /* [d_inner] gated-RMSNorm gamma          */
+    float* ssm_state;                 /* [b, nheads, headdim, dstate], in/out   */
+} mamba2_layer_args;
+
+size_t mamba2_layer_workspace_size(const mamba2_layer_args* args);
+int mamba2_layer_step(const mamba2_layer_args* args, void* workspace, size_t workspace_bytes,
+                      mamba_stream_t stream);
+/* As mamba2_layer_step, recording the caller's HIP events around the state-  */
+/* update kernel (benchmark timing; no counterpart in the reference).          */
+int mamba2_layer_step_timed(const mamba2_layer_args* args, void* workspace, size_t workspace_bytes,
+                            mamba_stream_t stream, void* event_start, void* event_stop);
 
 /* ------------------------------------------------------------------------- */
 /* Residual add + RmsNorm over rows (src/modules/norm/rms_norm.rs:53-98), the  */

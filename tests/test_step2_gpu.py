@@ -172,14 +172,15 @@ def _cfg_dict(cfg):
 @pytest.mark.parametrize("wdtype", ["f32", "bf16"])
 def test_layer_steps_match_oracle(wdtype):
     """Two pre-norm layers stepped three tokens: RmsNorm -> in_proj -> SSM step
-    -> gated norm -> out_proj -> residual, caches carried between tokens."""
+    -> gated norm -> out_proj -> residual, caches carried between tokens
+    (torch.mm products around mamba2_step_ssm)."""
     import torch
     import mamba_hip
     import oracle
     dt = torch.float32 if wdtype == "f32" else torch.bfloat16
     cfg = mamba_hip.Mamba2Config(d_model=256, state_rank=128, per_head_dim=64)
     gen = torch.Generator().manual_seed(11)
-    stack = mamba_hip.Mamba2Stack.init(cfg, 2, "cuda", dt, gen)
+    stack = mamba_hip.Mamba2Stack.init(cfg, 2, "cuda", dt, gen, fused=False)
     b = 3
     rng = np.random.default_rng(12)
     caches = stack.new_caches(b)
@@ -227,14 +228,15 @@ def test_mamba2_step_signature():
     np.testing.assert_allclose(cache.ssm_bhpr.cpu().numpy(), ref_ssm, **F32_TOL)
 
 
-def test_stack_hip_graph_replays_equal_eager():
+@pytest.mark.parametrize("fused", [False, True])
+def test_stack_hip_graph_replays_equal_eager(fused):
     """Capture one stack step in a HIP graph; replay it several times with eager
     work in between and check every replay against the eager result."""
     import torch
     import mamba_hip
     cfg = mamba_hip.Mamba2Config(d_model=256, state_rank=128, per_head_dim=64)
-    stack = mamba_hip.Mamba2Stack.init(cfg, 3, "cuda", torch.bfloat16, torch.Generator().manual_seed(4))
-    b = 4
+    stack = mamba_hip.Mamba2Stack.init(cfg, 3, "cuda", torch.bfloat16, torch.Generator().manual_seed(4), fused=fused)
+    b = 4 if not fused else 40
     rng = np.random.default_rng(5)
     base = stack.new_caches(b)
     for c in base:
@@ -288,3 +290,120 @@ def test_step_invalid_args_raise():
     assert rc == 1  # required pointers missing
     with pytest.raises(mamba_hip.MambaHipError):
         mamba_hip.rmsnorm(torch.zeros(2, 3, device="cuda", dtype=torch.float64), None)
+
+
+# ------------------------------------------------------------- fused path --
+
+LIN_CASES = [
+    # (rows, d_in, d_out, x dtype, y dtype, bias)
+    (1, 256, 1000, "f32", "f32", False),     # MT 1, 4 waves, tail loop only, ragged last tile
+    (3, 1024, 96, "bf16", "f32", True),      # MT 1, two pipeline stages per wave
+    (40, 512, 320, "bf16", "bf16", False),   # MT 2
+    (100, 2048, 64, "f32", "f32", True),     # MT 4
+    (200, 4096, 200, "bf16", "f32", False),  # MT 8, 8 waves per workgroup
+    (256, 64, 33, "f32", "f32", True),       # full 256 rows, K smaller than one stage
+]
+
+
+@pytest.mark.parametrize("case", LIN_CASES)
+def test_linear_fwd_matches_oracle(case):
+    """mamba_linear_fwd (packed bf16 weight, bf16 operand, f32 accumulation)
+    against the oracle's f64 product of the same bf16-rounded operands."""
+    import torch
+    import mamba_hip
+    import oracle
+    rows, d_in, d_out, xd, yd, has_b = case
+    dts = {"f32": torch.float32, "bf16": torch.bfloat16}
+    rng = np.random.default_rng(rows + d_in)
+    W = (rng.standard_normal((d_in, d_out)) / np.sqrt(d_in)).astype(np.float32)
+    x = rng.standard_normal((rows, d_in)).astype(np.float32)
+    bias = rng.standard_normal(d_out).astype(np.float32) if has_b else None
+    Wd = _t(W, torch.bfloat16)
+    packed = mamba_hip.pack_linear(Wd)
+    xdev = _t(x, dts[xd])
+    y = torch.empty(rows, d_out, device="cuda", dtype=dts[yd])
+    mamba_hip.linear(xdev, packed, d_out, None if bias is None else _t(bias), out=y)
+    torch.cuda.synchronize()
+    ref = oracle.linear(_bf16_round(x), Wd.float().cpu().numpy(), bias)
+    scale = np.abs(ref).max()
+    tol = dict(rtol=2e-3, atol=2e-3 * scale) if yd == "f32" else dict(rtol=1e-2, atol=1e-2 * scale)
+    np.testing.assert_allclose(y.float().cpu().numpy(), ref, **tol)
+
+
+def _randomize_caches(caches, rng):
+    refs = []
+    for c in caches:
+        c.conv_bvk.copy_(_t(rng.standard_normal(tuple(c.conv_bvk.shape)).astype(np.float32)))
+        c.ssm_bhpr.copy_(_t((0.1 * rng.standard_normal(tuple(c.ssm_bhpr.shape))).astype(np.float32)))
+        refs.append([c.conv_bvk.cpu().numpy(), c.ssm_bhpr.cpu().numpy()])
+    return refs
+
+
+@pytest.mark.parametrize("b,d_model,nbg", [(3, 256, 0), (40, 512, 0), (100, 256, 1), (200, 256, 0), (2, 2048, 0)])
+def test_fused_layer_steps_match_oracle(b, d_model, nbg):
+    """mamba2_layer_step (packed products, 1/rms and residual in the out_proj
+    epilogue, B/C window slide as its side job) over two layers and two tokens
+    against the oracle's pre-norm layer step on the same bf16 weights."""
+    import torch
+    import mamba_hip
+    import oracle
+    cfg = mamba_hip.Mamba2Config(d_model=d_model, state_rank=128, per_head_dim=64, is_norm_before_gate=bool(nbg))
+    stack = mamba_hip.Mamba2Stack.init(cfg, 2, "cuda", torch.bfloat16, torch.Generator().manual_seed(b), fused=True)
+    assert stack.fused
+    rng = np.random.default_rng(b)
+    caches = stack.new_caches(b)
+    refs = _randomize_caches(caches, rng)
+    params = [_oracle_params(l) for l in stack.layers]
+    for step in range(2):
+        x = rng.standard_normal((b, d_model)).astype(np.float32)
+        y, caches = stack.step(_t(x), caches)
+        torch.cuda.synchronize()
+        u = x
+        for i, p in enumerate(params):
+            u, refs[i][0], refs[i][1] = oracle.mamba2_layer_step(u, p, refs[i][0], refs[i][1], _cfg_dict(cfg),
+                                                                 ) if not nbg else _layer_step_nbg(u, p, refs[i], cfg)
+        print(f"b={b} d_model={d_model} step {step}", flush=True)
+        np.testing.assert_allclose(y.cpu().numpy(), u, **BF16_TOL)
+        for i, c in enumerate(caches):
+            np.testing.assert_allclose(c.conv_bvk.cpu().numpy(), refs[i][0], **BF16_TOL)
+            np.testing.assert_allclose(c.ssm_bhpr.cpu().numpy(), refs[i][1], **BF16_TOL)
+
+
+def _layer_step_nbg(u, p, ref, cfg):
+    """oracle.mamba2_layer_step with norm_before_gate (composed from the same
+    oracle pieces)."""
+    import oracle
+    normed = oracle.rmsnorm(u, p["pre_norm_w"])
+    zx = oracle.linear(normed, p["w_in"])
+    out, cs, ss = oracle.mamba2_step_ssm(zx, ref[0], p["conv_w"], p["conv_b"], p["dt_bias"], p["A"], p["D"],
+                                         p["norm_w"], ref[1], cfg.nheads, cfg.per_head_dim, cfg.ngroups,
+                                         cfg.state_rank, norm_before_gate=True)
+    return u + oracle.linear(out, p["w_out"]), cs, ss
+
+
+def test_fused_and_unfused_stacks_agree():
+    """The fused layer step and the torch.mm + mamba2_step_ssm path compute the
+    same function (bf16 weights)."""
+    import torch
+    import mamba_hip
+    cfg = mamba_hip.Mamba2Config(d_model=512, state_rank=64, per_head_dim=64)
+    fused = mamba_hip.Mamba2Stack.init(cfg, 3, "cuda", torch.bfloat16, torch.Generator().manual_seed(6))
+    plain = mamba_hip.Mamba2Stack(fused.layers, fused=False)
+    b = 16
+    rng = np.random.default_rng(7)
+    c1 = fused.new_caches(b)
+    _randomize_caches(c1, rng)
+    c2 = [mamba_hip.Mamba2Cache(c.conv_bvk.clone(), c.ssm_bhpr.clone()) for c in c1]
+    for _ in range(3):
+        x = _t(rng.standard_normal((b, 512)).astype(np.float32))
+        y1, c1 = fused.step(x, c1)
+        y2, c2 = plain.step(x, c2)
+    torch.cuda.synchronize()
+    # two bf16 approximations of the same f32 function (each within BF16_TOL of
+    # the oracle, see above): their difference gets twice the absolute budget
+    tol = dict(rtol=2e-2, atol=2e-2)
+    np.testing.assert_allclose(y1.cpu().numpy(), y2.cpu().numpy(), **tol)
+    for a, e in zip(c1, c2):
+        np.testing.assert_allclose(a.ssm_bhpr.cpu().numpy(), e.ssm_bhpr.cpu().numpy(), **tol)
+        # windows hold raw bf16 in_proj outputs: a different accumulation order can move them by one bf16 ulp
+        np.testing.assert_allclose(a.conv_bvk.cpu().numpy(), e.conv_bvk.cpu().numpy(), **tol)
