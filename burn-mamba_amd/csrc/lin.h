@@ -28,23 +28,31 @@ __device__ __forceinline__ int64_t lin_act_offset(int m, int k, int MT) {
     return ((int64_t)(s * MT + i) * 64 + lane) * 8 + (k & 7);
 }
 
-enum LinEpilogue { LIN_STORE = 0, LIN_RESID_RMS = 1 };
+enum LinEpilogue { LIN_STORE = 0, LIN_PARTIAL = 1 };
 
 struct LinParams {
     int M, N, K, MT;         // MT = lin_mt(M)
+    int S;                   // k-splits across workgroups (grid.y)
     const lin_bf16x8_t* W;   // packed weight
     const lin_bf16x8_t* A;   // packed activation
+    // LIN_STORE (S == 1): out[m, n] = acc + bias
     const float* bias;       // [N] or NULL
-    // LIN_STORE: out[m, n] = acc + bias
     void* out; int64_t out_ld; bool out_bf16;
-    // LIN_RESID_RMS: xres[m, n] += acc / rms[m] + bias, rms[m] = sqrt(sum_h ssq[m, h] / rms_d + eps)
-    float* xres; int64_t xres_ld;
-    const float* ssq; int ssq_h; float rms_d;
-    // side job (may be empty): slide the conv windows of channels [c0, c0 + nc)
-    // of every row m < M, appending zx[m, zx_off + c]
-    float* conv; int conv_dim, conv_k, c0, nc;
-    const void* zx; int64_t zx_ld; bool zx_bf16; int zx_off;
+    // LIN_PARTIAL: part[z][m][n] = acc over k-split z (f32, planes of M x N);
+    // the consumer sums the S planes in a fixed order
+    float* part;
 };
+
+// k-splits for a product: enough workgroups (~1300 of 4 waves, ~10 weight
+// blocks per wave) to stream the weight at full HBM rate, fewer for large M
+// where the partial planes grow.
+inline int lin_splits(int M, int K, int N) {
+    const int ks = K / 16, tiles = (N + 31) / 32;
+    int s = 1;
+    while (s < 16 && ks / (2 * s) >= 40 && tiles * s < 1024 && (M <= 64 || s < 2)) s *= 2;
+    return s;
+}
+inline size_t lin_part_elems(int M, int N, int S) { return (size_t)S * M * N; }
 
 // Launch the product on `stream`; the caller has validated the shapes
 // (K % 16 == 0, 1 <= M <= 256).

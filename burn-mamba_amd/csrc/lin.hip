@@ -9,13 +9,14 @@
 //   * the activation arrives already in A-operand order (written that way by
 //     the producing kernel), so it too is read as contiguous 1 KB blocks (from
 //     L2: it is small and shared by every workgroup);
-//   * one workgroup owns one 32-column tile over all of K; its NW waves split
-//     K, each software-pipelines its loads two stages deep, and the partial
-//     accumulators are reduced through LDS, so there is no split-K traffic to
-//     HBM and no atomics;
-//   * epilogues: plain store (+bias), or the residual update
-//     x += acc / rms(row) (+bias) that finishes a gated RMSNorm whose per-row
-//     scale commutes with the product.
+//   * one workgroup owns one 32-column tile over a 1/S slice of K (grid.y =
+//     S); its NW waves split that slice again, each software-pipelines its
+//     loads two stages deep, and the wave accumulators are reduced through
+//     LDS.  Small slices on many workgroups (~1300) is what streams a weight
+//     at full HBM rate (a workgroup's ramp-up and tail are then short);
+//   * epilogues: plain store (+bias) when S = 1, else one f32 partial plane
+//     per k-slice, summed in a fixed order by the consumer (deterministic, no
+//     atomics).
 #include <algorithm>
 
 #include "lin.h"
@@ -28,9 +29,26 @@ __device__ __forceinline__ lin_f32x16_t lin_mfma(lin_bf16x8_t a, lin_bf16x8_t b,
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// Tuning constants (compile-time; defaults measured on MI355X).
+#ifndef MAMBA_LIN_NW
+#define MAMBA_LIN_NW 4          // waves per workgroup
+#endif
+#ifndef MAMBA_LIN_U1
+#define MAMBA_LIN_U1 5          // k-steps per pipeline stage for one 32-row tile
+#endif
+#ifndef MAMBA_LIN_U2
+#define MAMBA_LIN_U2 5          // k-steps per pipeline stage for two 32-row tiles
+#endif
+#ifndef MAMBA_LIN_NT
+#define MAMBA_LIN_NT 0          // 1: weight loads carry the non-temporal hint (read once)
+#endif
+#ifndef MAMBA_LIN_ROTATE
+#define MAMBA_LIN_ROTATE 0      // 1: each workgroup starts its k walk at a different stage
+#endif
+
 template <int MT>
 struct LinStage {
-    static constexpr int U = MT == 1 ? 8 : MT == 2 ? 4 : MT == 4 ? 2 : 1;  // k-steps per pipeline stage
+    static constexpr int U = MT == 1 ? MAMBA_LIN_U1 : MT == 2 ? MAMBA_LIN_U2 : MT == 4 ? 2 : 1;  // k-steps per stage
     lin_bf16x8_t w[U];
     lin_bf16x8_t a[U][MT];
 };
@@ -39,7 +57,11 @@ template <int MT>
 __device__ __forceinline__ void lin_load(LinStage<MT>& st, const lin_bf16x8_t* Wj, const lin_bf16x8_t* Ap, int s) {
 #pragma unroll
     for (int u = 0; u < LinStage<MT>::U; ++u) {
+#if MAMBA_LIN_NT
+        st.w[u] = __builtin_nontemporal_load(Wj + (int64_t)(s + u) * 64);
+#else
         st.w[u] = Wj[(int64_t)(s + u) * 64];
+#endif
 #pragma unroll
         for (int i = 0; i < MT; ++i) st.a[u][i] = Ap[((int64_t)(s + u) * MT + i) * 64];
     }
@@ -53,32 +75,15 @@ __device__ __forceinline__ void lin_compute(const LinStage<MT>& st, lin_f32x16_t
         for (int i = 0; i < MT; ++i) acc[i] = lin_mfma(st.a[u][i], st.w[u], acc[i]);
 }
 
-__device__ void lin_side_job(const LinParams& p) {
-    if (p.conv == nullptr) return;
-    const int total = p.M * p.nc;
-    for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += gridDim.x * blockDim.x) {
-        const int m = idx / p.nc, c = idx - m * p.nc;
-        const int ch = p.c0 + c;
-        float* win = p.conv + ((int64_t)m * p.conv_dim + ch) * p.conv_k;
-        const int64_t zi = (int64_t)m * p.zx_ld + p.zx_off + ch;
-        const float xin = p.zx_bf16 ? bf16_to_f32(static_cast<const bf16_t*>(p.zx)[zi])
-                                    : static_cast<const float*>(p.zx)[zi];
-        for (int k = 0; k + 1 < p.conv_k; ++k) win[k] = win[k + 1];
-        win[p.conv_k - 1] = xin;
-    }
-}
-
-// grid: ceil(N / 32) workgroups of NW waves.
+// grid: (ceil(N / 32), S) workgroups of NW waves.
 template <int MT, int NW, int EPI>
 __global__ __launch_bounds__(64 * NW) void lin_stream(LinParams p) {
     __shared__ float s_red[NW][2][16][64];
-    __shared__ float s_inv[256];
-    const int j = blockIdx.x;
+    const int j = blockIdx.x, z = blockIdx.y;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int KS = p.K >> 4;
-    const int s0 = (KS * wave) / NW, s1 = (KS * (wave + 1)) / NW;
-
-    lin_side_job(p);
+    const int z0 = (KS * z) / p.S, z1 = (KS * (z + 1)) / p.S;
+    const int s0 = z0 + ((z1 - z0) * wave) / NW, s1 = z0 + ((z1 - z0) * (wave + 1)) / NW;
 
     const lin_bf16x8_t* Wj = p.W + (int64_t)j * KS * 64 + lane;
     const lin_bf16x8_t* Ap = p.A + lane;
@@ -92,17 +97,21 @@ __global__ __launch_bounds__(64 * NW) void lin_stream(LinParams p) {
     const int nstage = (s1 - s0) / U;
     int s = s0;
     if (nstage > 0) {
+        // stage st covers k-steps s0 + U * ((st + rot) % nstage) .. + U - 1: with
+        // rot varying over workgroups, concurrent waves read different blocks of
+        // the (shared, L2-resident) activation instead of the same one
+        const int rot = MAMBA_LIN_ROTATE ? (int)(blockIdx.x % (unsigned)nstage) : 0;
+        auto kstep = [&](int st) { int q = st + rot; q -= q >= nstage ? nstage : 0; return s0 + U * q; };
         LinStage<MT> sa, sb;
-        lin_load<MT>(sa, Wj, Ap, s);
+        lin_load<MT>(sa, Wj, Ap, kstep(0));
         for (int st = 0; st < nstage; st += 2) {
             const bool more1 = st + 1 < nstage;
-            if (more1) lin_load<MT>(sb, Wj, Ap, s + U);
+            if (more1) lin_load<MT>(sb, Wj, Ap, kstep(st + 1));
             lin_compute<MT>(sa, acc);
             if (more1) {
-                if (st + 2 < nstage) lin_load<MT>(sa, Wj, Ap, s + 2 * U);
+                if (st + 2 < nstage) lin_load<MT>(sa, Wj, Ap, kstep(st + 2));
                 lin_compute<MT>(sb, acc);
             }
-            s += 2 * U;
         }
         s = s0 + nstage * U;
     }
@@ -110,14 +119,6 @@ __global__ __launch_bounds__(64 * NW) void lin_stream(LinParams p) {
         const lin_bf16x8_t w = Wj[(int64_t)s * 64];
 #pragma unroll
         for (int i = 0; i < MT; ++i) acc[i] = lin_mfma(Ap[((int64_t)s * MT + i) * 64], w, acc[i]);
-    }
-
-    if (EPI == LIN_RESID_RMS) {
-        for (int m = threadIdx.x; m < p.M; m += 64 * NW) {
-            float ss = 0.f;
-            for (int h = 0; h < p.ssq_h; ++h) ss += p.ssq[(int64_t)m * p.ssq_h + h];
-            s_inv[m] = sqrtf(ss / p.rms_d + kDivEpsF32);
-        }
     }
 
     // cross-wave reduction through LDS, two 32-row tiles at a time
@@ -145,9 +146,7 @@ __global__ __launch_bounds__(64 * NW) void lin_stream(LinParams p) {
                 else
                     static_cast<float*>(p.out)[(int64_t)m * p.out_ld + n] = sum;
             } else {
-                float v2 = sum / s_inv[m];
-                if (p.bias) v2 += p.bias[n];
-                p.xres[(int64_t)m * p.xres_ld + n] += v2;
+                p.part[((int64_t)z * p.M + m) * p.N + n] = sum;
             }
         }
         __syncthreads();
@@ -156,16 +155,10 @@ __global__ __launch_bounds__(64 * NW) void lin_stream(LinParams p) {
 
 template <int MT>
 static void lin_launch_mt(const LinParams& p, int epi, hipStream_t stream) {
-    const dim3 grid((p.N + 31) / 32);
-    // waves per workgroup: enough to put ~40 k-steps (40 KB of weight) on each
-    const int KS = p.K / 16;
-    if (KS >= 256) {
-        if (epi == LIN_STORE) hipLaunchKernelGGL((lin_stream<MT, 8, LIN_STORE>), grid, dim3(512), 0, stream, p);
-        else hipLaunchKernelGGL((lin_stream<MT, 8, LIN_RESID_RMS>), grid, dim3(512), 0, stream, p);
-    } else {
-        if (epi == LIN_STORE) hipLaunchKernelGGL((lin_stream<MT, 4, LIN_STORE>), grid, dim3(256), 0, stream, p);
-        else hipLaunchKernelGGL((lin_stream<MT, 4, LIN_RESID_RMS>), grid, dim3(256), 0, stream, p);
-    }
+    const dim3 grid((p.N + 31) / 32, p.S);
+    constexpr int NW = MAMBA_LIN_NW;
+    if (epi == LIN_STORE) hipLaunchKernelGGL((lin_stream<MT, NW, LIN_STORE>), grid, dim3(64 * NW), 0, stream, p);
+    else hipLaunchKernelGGL((lin_stream<MT, NW, LIN_PARTIAL>), grid, dim3(64 * NW), 0, stream, p);
 }
 
 void lin_launch(const LinParams& p, int epi, hipStream_t stream) {
@@ -288,7 +281,7 @@ extern "C" int mamba_linear_fwd(const mamba_linear_args* a, void* ws, size_t ws_
                        a->x, a->rows, a->d_in, a->x_ld, a->x_dtype == MAMBA_BF16, static_cast<bf16_t*>(ws), mt);
     MAMBA_CHECK_LAUNCH();
     LinParams p = {};
-    p.M = a->rows; p.N = a->d_out; p.K = a->d_in; p.MT = mt;
+    p.M = a->rows; p.N = a->d_out; p.K = a->d_in; p.MT = mt; p.S = 1;
     p.W = static_cast<const lin_bf16x8_t*>(a->packed_w);
     p.A = static_cast<const lin_bf16x8_t*>(ws);
     p.bias = a->bias;

@@ -47,7 +47,19 @@ struct Step2Params {
     // the packed activation layout of lin.h with MT = a_mt; the 1/rms of the
     // row is applied after the product (it is a per-row scalar).
     bf16_t* a_out; int a_mt;
+    // zxbcdt as zx_S f32 partial planes [zx_S][nb][zx_ld] (+ zx_bias), summed on
+    // read; zx_S = 0 reads the single buffer zx (bf16/f32) instead
+    const float* zx_part; int zx_S; int64_t zx_ld; const float* zx_bias;
 };
+
+// zxbcdt[b, i]: the single buffer, or the sum of the in_proj partial planes
+__device__ __forceinline__ float zx_at(const Step2Params& p, const char* zrow, int b, int i) {
+    if (p.zx_S == 0) return p.zx_bf16 ? bf16_to_f32(reinterpret_cast<const bf16_t*>(zrow)[i])
+                                      : reinterpret_cast<const float*>(zrow)[i];
+    float v = p.zx_bias ? p.zx_bias[i] : 0.f;
+    for (int s = 0; s < p.zx_S; ++s) v += p.zx_part[((int64_t)s * p.nb + b) * p.zx_ld + i];
+    return v;
+}
 
 __device__ __forceinline__ float ld_act(const void* base, int64_t i, bool bf16) {
     return bf16 ? bf16_to_f32(static_cast<const bf16_t*>(base)[i]) : static_cast<const float*>(base)[i];
@@ -57,8 +69,8 @@ __device__ __forceinline__ float silu_fast(float x) { return x / (__expf(-x) + 1
 
 // dt = clamp(softplus(dt_raw + dt_bias), lo, hi), mamba2.rs:924 with the f32
 // softplus threshold of src/modules/activation/softplus.rs:21-47.
-__device__ __forceinline__ float step_dt(const Step2Params& p, const void* zrow, int h) {
-    float v = ld_act(zrow, p.d_inner + p.conv_dim + h, p.zx_bf16);
+__device__ __forceinline__ float step_dt(const Step2Params& p, const char* zrow, int b, int h) {
+    float v = zx_at(p, zrow, b, p.d_inner + p.conv_dim + h);
     if (p.dt_bias) v += p.dt_bias[h];
     float dt = v > 18.f ? v : log1pf(__expf(v));
     return fminf(fmaxf(dt, p.dt_lo), p.dt_hi);
@@ -114,7 +126,7 @@ __global__ __launch_bounds__(256) void step2_ssm_fast(Step2Params p) {
         else ch = p.d_inner + (p.G + g) * N + (c - P - N);
         const float4 win = win_base[ch];
         const float4 w = cw[ch];
-        const float xin = ld_act(zrow, p.d_inner + ch, p.zx_bf16);
+        const float xin = zx_at(p, zrow, b, p.d_inner + ch);
         float acc = win.y * w.x;
         acc += win.z * w.y;
         acc += win.w * w.z;
@@ -130,7 +142,7 @@ __global__ __launch_bounds__(256) void step2_ssm_fast(Step2Params p) {
             s_C[c - P - N] = v;
         }
     }
-    const float dt = step_dt(p, zrow, h);
+    const float dt = step_dt(p, zrow, b, h);
     const float dA = __expf(dt * p.A[h]);
     const float Dh = p.Dv ? p.Dv[h] : 0.f;
     __syncthreads();
@@ -177,11 +189,11 @@ __global__ __launch_bounds__(256) void step2_ssm_fast(Step2Params p) {
         const float y = ysum + Dh * s_x[pr];
         float gv = y;
         if (PACK) {
-            const float zg = silu_fast(ld_act(zrow, h * P + pr, p.zx_bf16));
+            const float zg = silu_fast(zx_at(p, zrow, b, h * P + pr));
             if (!p.norm_before_gate) gv *= zg;
             s_pk[pr] = p.norm_before_gate ? y * p.norm_w[h * P + pr] * zg : gv * p.norm_w[h * P + pr];
         } else {
-            if (!p.norm_before_gate) gv *= silu_fast(ld_act(zrow, h * P + pr, p.zx_bf16));
+            if (!p.norm_before_gate) gv *= silu_fast(zx_at(p, zrow, b, h * P + pr));
             p.g_ws[(int64_t)b * p.d_inner + h * P + pr] = gv;
         }
         sq = gv * gv;
@@ -198,29 +210,6 @@ __global__ __launch_bounds__(256) void step2_ssm_fast(Step2Params p) {
         v.z = (uint32_t)f32_to_bf16(hi.x) | ((uint32_t)f32_to_bf16(hi.y) << 16);
         v.w = (uint32_t)f32_to_bf16(hi.z) | ((uint32_t)f32_to_bf16(hi.w) << 16);
         *reinterpret_cast<uint4*>(p.a_out + lin_act_offset(b, h * P + 8 * t, p.a_mt)) = v;
-    }
-}
-
-// RmsNorm of one residual row into the packed activation layout (bf16):
-// out = x / sqrt(mean(x^2) + eps) * w  (rms_norm.rs:53-98).  grid (rows), 256 threads.
-__global__ __launch_bounds__(256) void rmsnorm_pack(const float* x, int64_t x_sr, int cols, const float* w,
-                                                    bf16_t* a_out, int a_mt) {
-    __shared__ float s_red[4];
-    const int r = blockIdx.x, t = threadIdx.x;
-    const float* xr = x + (int64_t)r * x_sr;
-    float ss = 0.f;
-    for (int c = t; c < cols; c += 256) ss += xr[c] * xr[c];
-    ss = block_sum_256(ss, s_red);
-    const float rms = sqrtf(ss / (float)cols + kDivEpsF32);
-    for (int g = t; g < cols / 8; g += 256) {
-        uint32_t u[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int c = 8 * g + 2 * e;
-            u[e] = (uint32_t)f32_to_bf16((xr[c] / rms) * w[c]) |
-                   ((uint32_t)f32_to_bf16((xr[c + 1] / rms) * w[c + 1]) << 16);
-        }
-        *reinterpret_cast<uint4*>(a_out + lin_act_offset(r, 8 * g, a_mt)) = make_uint4(u[0], u[1], u[2], u[3]);
     }
 }
 
@@ -247,7 +236,7 @@ __global__ __launch_bounds__(256) void step2_ssm_generic(Step2Params p) {
         else ch = p.d_inner + (p.G + g) * N + (c - P - N);
         float* win = p.conv + ((int64_t)b * p.conv_dim + ch) * K;
         const float* w = p.conv_w + (int64_t)ch * K;
-        const float xin = ld_act(zrow, p.d_inner + ch, p.zx_bf16);
+        const float xin = zx_at(p, zrow, b, p.d_inner + ch);
         float acc = 0.f;
         for (int k = 0; k + 1 < K; ++k) acc += win[k + 1] * w[k];
         acc += xin * w[K - 1];
@@ -263,7 +252,7 @@ __global__ __launch_bounds__(256) void step2_ssm_generic(Step2Params p) {
             s_C[c - P - N] = v;
         }
     }
-    const float dt = step_dt(p, zrow, h);
+    const float dt = step_dt(p, zrow, b, h);
     const float dA = __expf(dt * p.A[h]);
     const float Dh = p.Dv ? p.Dv[h] : 0.f;
     __syncthreads();
@@ -281,7 +270,7 @@ __global__ __launch_bounds__(256) void step2_ssm_generic(Step2Params p) {
         if (lane == 0) {
             const float y = acc + Dh * xv;
             float gv = y;
-            if (!p.norm_before_gate) gv *= silu_fast(ld_act(zrow, h * P + pr, p.zx_bf16));
+            if (!p.norm_before_gate) gv *= silu_fast(zx_at(p, zrow, b, h * P + pr));
             p.g_ws[(int64_t)b * p.d_inner + h * P + pr] = gv;
             sq += gv * gv;
         }
@@ -407,6 +396,7 @@ static int step2_make_params(const mamba2_step_args* a, void* ws, size_t ws_byte
     p.g_ws = static_cast<float*>(ws);
     p.ssq_ws = reinterpret_cast<float*>(static_cast<char*>(ws) + align_up((size_t)p.nb * d_inner * 4, 256));
     p.a_out = nullptr; p.a_mt = 0;
+    p.zx_part = nullptr; p.zx_S = 0; p.zx_ld = 0; p.zx_bias = nullptr;
     return MAMBA_OK;
 }
 
@@ -475,88 +465,215 @@ extern "C" int mamba_rmsnorm(const mamba_rmsnorm_args* a, mamba_stream_t stream)
 
 // ---------------------------------------------------------------------------
 // Fused pre-norm layer step: x += out_proj(RmsNormGated(ssm(in_proj(RmsNorm(x)))))
+// and the whole stack of them.
 // ---------------------------------------------------------------------------
 namespace mamba {
 
-struct LayerWs {
-    bf16_t* a_in; void* zx; bf16_t* a_out; float* ssq; size_t total;
+// One workgroup per row m of the residual stream x[m, 0:cols):
+//   S > 0:  x += (sum of the S out_proj planes) / rms_ssq(m) (+ bias), where
+//           rms_ssq(m) = sqrt(sum_h ssq[m, h] / d_inner + eps) finishes the
+//           gated RMSNorm of the layer just computed, and the shared B/C conv
+//           windows of row m slide (every head has read them by now);
+//   PACK:   write RmsNorm(x)[m, :] * w (rms_norm.rs:53-98) in bf16, packed as
+//           the next in_proj operand.
+// Every thread keeps its columns in registers between the two parts.
+struct RowsParams {
+    int M, cols, H, d_inner, conv_dim, conv_k, nbc;  // nbc: B/C channels (2 G N)
+    float* x; int64_t x_ld;
+    const float* part; const float* bias; const float* ssq;
+    float* conv; const float* zx_part; int zx_S; int64_t zx_ld; const float* zx_bias;
+    const float* w; bf16_t* a_out; int a_mt;
 };
 
-static LayerWs layer_ws_layout(const mamba2_layer_args* a, void* base) {
-    const int d_inner = a->nheads * a->headdim;
-    const int conv_dim = d_inner + 2 * a->ngroups * a->dstate;
-    const int d_in_proj = d_inner + conv_dim + a->nheads;
+constexpr int kRowsThreads = 256;
+constexpr int kRowsMaxVec = 4;  // float4 per thread: cols <= 4096
+
+template <int S, bool PACK>
+__global__ __launch_bounds__(kRowsThreads) void layer_rows(RowsParams p) {
+    __shared__ float s_red[4];
+    const int m = blockIdx.x, t = threadIdx.x;
+    const int nv = p.cols / 4;
+    float4* xr = reinterpret_cast<float4*>(p.x + (int64_t)m * p.x_ld);
+    float4 v[kRowsMaxVec];
+#pragma unroll
+    for (int i = 0; i < kRowsMaxVec; ++i) {
+        const int c4 = t + i * kRowsThreads;
+        if (c4 < nv) v[i] = xr[c4];
+    }
+    if (S > 0) {
+        float4 acc[kRowsMaxVec];
+#pragma unroll
+        for (int i = 0; i < kRowsMaxVec; ++i) acc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int z = 0; z < S; ++z) {
+            const float4* pl = reinterpret_cast<const float4*>(p.part + ((int64_t)z * p.M + m) * p.cols);
+#pragma unroll
+            for (int i = 0; i < kRowsMaxVec; ++i) {
+                const int c4 = t + i * kRowsThreads;
+                if (c4 < nv) {
+                    const float4 q = pl[c4];
+                    acc[i].x += q.x; acc[i].y += q.y; acc[i].z += q.z; acc[i].w += q.w;
+                }
+            }
+        }
+        // rms of the gated values of this row (per-head partial sums of squares)
+        float ss = 0.f;
+        for (int h = t; h < p.H; h += kRowsThreads) ss += p.ssq[(int64_t)m * p.H + h];
+        ss = block_sum_256(ss, s_red);
+        const float rms = sqrtf(ss / (float)p.d_inner + kDivEpsF32);
+#pragma unroll
+        for (int i = 0; i < kRowsMaxVec; ++i) {
+            const int c4 = t + i * kRowsThreads;
+            if (c4 < nv) {
+                float4 o = make_float4(acc[i].x / rms, acc[i].y / rms, acc[i].z / rms, acc[i].w / rms);
+                if (p.bias) {
+                    const float4 bb = reinterpret_cast<const float4*>(p.bias)[c4];
+                    o.x += bb.x; o.y += bb.y; o.z += bb.z; o.w += bb.w;
+                }
+                v[i].x += o.x; v[i].y += o.y; v[i].z += o.z; v[i].w += o.w;
+                xr[c4] = v[i];
+            }
+        }
+        // B/C conv windows of row m
+        for (int c = t; c < p.nbc; c += kRowsThreads) {
+            const int ch = p.d_inner + c;
+            float* win = p.conv + ((int64_t)m * p.conv_dim + ch) * p.conv_k;
+            const int zi = p.d_inner + ch;
+            float xin = p.zx_bias ? p.zx_bias[zi] : 0.f;
+            for (int z = 0; z < p.zx_S; ++z) xin += p.zx_part[((int64_t)z * p.M + m) * p.zx_ld + zi];
+            for (int k = 0; k + 1 < p.conv_k; ++k) win[k] = win[k + 1];
+            win[p.conv_k - 1] = xin;
+        }
+    }
+    if (PACK) {
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < kRowsMaxVec; ++i)
+            if (t + i * kRowsThreads < nv) ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
+        ss = block_sum_256(ss, s_red);
+        const float rms = sqrtf(ss / (float)p.cols + kDivEpsF32);
+        // pairs of float4 (8 consecutive columns) form one 16-byte run of the packed layout;
+        // thread t owns columns 4t.. of each slab, so exchange halves through LDS-free
+        // shuffles: lanes 2q and 2q+1 hold columns 8q..8q+7 of a slab
+#pragma unroll
+        for (int i = 0; i < kRowsMaxVec; ++i) {
+            const int c4 = t + i * kRowsThreads;
+            const float4 w4 = c4 < nv ? reinterpret_cast<const float4*>(p.w)[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
+            const uint32_t lo = (uint32_t)f32_to_bf16((v[i].x / rms) * w4.x) |
+                                ((uint32_t)f32_to_bf16((v[i].y / rms) * w4.y) << 16);
+            const uint32_t hi = (uint32_t)f32_to_bf16((v[i].z / rms) * w4.z) |
+                                ((uint32_t)f32_to_bf16((v[i].w / rms) * w4.w) << 16);
+            const uint32_t lo_n = __shfl_xor(lo, 1, 64), hi_n = __shfl_xor(hi, 1, 64);
+            if (c4 < nv && (c4 & 1) == 0) {
+                *reinterpret_cast<uint4*>(p.a_out + lin_act_offset(m, 4 * c4, p.a_mt)) = make_uint4(lo, hi, lo_n, hi_n);
+            }
+        }
+    }
+}
+
+template <bool PACK>
+static void rows_launch(const RowsParams& rp, int S, hipStream_t stream) {
+    const dim3 g(rp.M), b(kRowsThreads);
+    switch (S) {
+        case 0: hipLaunchKernelGGL((layer_rows<0, PACK>), g, b, 0, stream, rp); break;
+        case 1: hipLaunchKernelGGL((layer_rows<1, PACK>), g, b, 0, stream, rp); break;
+        case 2: hipLaunchKernelGGL((layer_rows<2, PACK>), g, b, 0, stream, rp); break;
+        case 4: hipLaunchKernelGGL((layer_rows<4, PACK>), g, b, 0, stream, rp); break;
+        case 8: hipLaunchKernelGGL((layer_rows<8, PACK>), g, b, 0, stream, rp); break;
+        default: hipLaunchKernelGGL((layer_rows<16, PACK>), g, b, 0, stream, rp); break;
+    }
+}
+
+struct LayerGeom {
+    int M, d_model, H, d_inner, conv_dim, d_in_proj, nbc, mt, S_in, S_out;
+};
+
+struct LayerWs {
+    bf16_t* a_in; float* zx_part; bf16_t* a_out; float* ssq; float* out_part; size_t total;
+};
+
+static LayerGeom layer_geom(const mamba2_layer_args* a) {
+    LayerGeom g;
+    g.M = a->batch; g.d_model = a->d_model; g.H = a->nheads;
+    g.d_inner = a->nheads * a->headdim;
+    g.nbc = 2 * a->ngroups * a->dstate;
+    g.conv_dim = g.d_inner + g.nbc;
+    g.d_in_proj = g.d_inner + g.conv_dim + g.H;
+    g.mt = lin_mt(g.M);
+    g.S_in = lin_splits(g.M, g.d_model, g.d_in_proj);
+    g.S_out = lin_splits(g.M, g.d_inner, g.d_model);
+    return g;
+}
+
+static LayerWs layer_ws_layout(const LayerGeom& g, void* base) {
     char* p = static_cast<char*>(base);
     LayerWs w;
     size_t off = 0;
-    w.a_in = reinterpret_cast<bf16_t*>(p + off);
-    off += align_up(lin_act_elems(a->batch, a->d_model) * 2, 256);
-    w.zx = p + off;
-    off += align_up((size_t)a->batch * d_in_proj * (a->zxbcdt_dtype == MAMBA_BF16 ? 2 : 4), 256);
-    w.a_out = reinterpret_cast<bf16_t*>(p + off);
-    off += align_up(lin_act_elems(a->batch, d_inner) * 2, 256);
-    w.ssq = reinterpret_cast<float*>(p + off);
-    off += align_up((size_t)a->batch * a->nheads * 4, 256);
+    auto take = [&](size_t bytes) { char* q = p + off; off += align_up(bytes, 256); return q; };
+    w.a_in = reinterpret_cast<bf16_t*>(take(lin_act_elems(g.M, g.d_model) * 2));
+    w.zx_part = reinterpret_cast<float*>(take(lin_part_elems(g.M, g.d_in_proj, g.S_in) * 4));
+    w.a_out = reinterpret_cast<bf16_t*>(take(lin_act_elems(g.M, g.d_inner) * 2));
+    w.ssq = reinterpret_cast<float*>(take((size_t)g.M * g.H * 4));
+    w.out_part = reinterpret_cast<float*>(take(lin_part_elems(g.M, g.d_model, g.S_out) * 4));
     w.total = off;
     return w;
 }
 
-static int layer_dispatch(const mamba2_layer_args* a, void* ws, size_t ws_bytes, hipStream_t stream,
-                          hipEvent_t ev0, hipEvent_t ev1) {
+// Validates one layer's arguments against the geometry of the first.
+static int layer_check(const mamba2_layer_args* a, const mamba2_layer_args* first) {
     MAMBA_CHECK_ARG(a != nullptr, "args is NULL");
     MAMBA_CHECK_ARG(a->batch >= 1 && a->batch <= 256, "batch must be in [1, 256]");
-    MAMBA_CHECK_ARG(a->d_model > 0 && a->d_model % 16 == 0, "d_model must be a positive multiple of 16");
+    MAMBA_CHECK_ARG(a->d_model > 0 && a->d_model % 16 == 0 && a->d_model <= 4 * 4 * kRowsThreads,
+                    "d_model must be a positive multiple of 16, at most 4096");
     MAMBA_CHECK_ARG(a->x && a->pre_norm_w && a->in_proj && a->out_proj, "x, pre_norm_w, in_proj, out_proj required");
-    MAMBA_CHECK_ARG(a->x_sb >= a->d_model, "x_sb shorter than a row");
+    MAMBA_CHECK_ARG(a->x_sb >= a->d_model && a->x_sb % 4 == 0, "x_sb must be >= d_model and a multiple of 4");
     if (!(a->headdim == 64 && (a->dstate == 64 || a->dstate == 128) && a->conv_kernel == 4)) {
         set_error("mamba2_layer_step: needs headdim 64, dstate 64 or 128 and conv_kernel 4 "
                   "(use mamba2_step_ssm with a separate product otherwise)");
         return MAMBA_ERR_UNSUPPORTED;
     }
-    MAMBA_CHECK_ARG(((uintptr_t)a->in_proj & 15u) == 0 && ((uintptr_t)a->out_proj & 15u) == 0,
-                    "packed weights must be 16-byte aligned");
-    // the state-update part: reuse the mamba2_step_ssm validation
-    mamba2_step_args sa;
+    MAMBA_CHECK_ARG(aligned16(a->in_proj) && aligned16(a->out_proj) && aligned16(a->x) && aligned16(a->pre_norm_w) &&
+                    (!a->out_proj_b || aligned16(a->out_proj_b)),
+                    "packed weights, x, pre_norm_w and out_proj_b must be 16-byte aligned");
+    MAMBA_CHECK_ARG(aligned16(a->ssm_state) && aligned16(a->conv_state) && aligned16(a->conv_w),
+                    "ssm_state, conv_state and conv_w must be 16-byte aligned");
+    if (first && a != first) {
+        MAMBA_CHECK_ARG(a->batch == first->batch && a->d_model == first->d_model && a->nheads == first->nheads &&
+                            a->headdim == first->headdim && a->ngroups == first->ngroups &&
+                            a->dstate == first->dstate && a->conv_kernel == first->conv_kernel &&
+                            a->x == first->x && a->x_sb == first->x_sb,
+                        "every layer of a stack must share the shapes and the residual stream x");
+    }
+    return MAMBA_OK;
+}
+
+// in_proj, state update, out_proj of one layer; a_in must hold the packed
+// normed input.  Leaves the out_proj planes and ssq in the workspace.
+static int layer_core(const mamba2_layer_args* a, const LayerGeom& g, const LayerWs& w, hipStream_t stream,
+                      hipEvent_t ev0, hipEvent_t ev1) {
+    LinParams li = {};
+    li.M = g.M; li.N = g.d_in_proj; li.K = g.d_model; li.MT = g.mt; li.S = g.S_in;
+    li.W = static_cast<const lin_bf16x8_t*>(a->in_proj);
+    li.A = reinterpret_cast<const lin_bf16x8_t*>(w.a_in);
+    li.part = w.zx_part;
+    lin_launch(li, LIN_PARTIAL, stream);
+    MAMBA_CHECK_LAUNCH();
+
+    mamba2_step_args sa = {};
     sa.batch = a->batch; sa.nheads = a->nheads; sa.headdim = a->headdim; sa.ngroups = a->ngroups;
     sa.dstate = a->dstate; sa.conv_kernel = a->conv_kernel;
-    sa.zxbcdt_dtype = a->zxbcdt_dtype; sa.out_dtype = MAMBA_BF16; sa.norm_before_gate = a->norm_before_gate;
-    const int d_inner = a->nheads * a->headdim;
-    const int conv_dim = d_inner + 2 * a->ngroups * a->dstate;
-    const int d_in_proj = d_inner + conv_dim + a->nheads;
-    const LayerWs w = layer_ws_layout(a, ws);
-    if (ws == nullptr || ws_bytes < w.total) {
-        set_error("mamba2_layer_step: workspace of " + std::to_string(w.total) + " bytes required");
-        return MAMBA_ERR_WORKSPACE;
-    }
-    sa.zxbcdt = w.zx; sa.zxbcdt_sb = d_in_proj;
+    sa.zxbcdt_dtype = MAMBA_F32; sa.out_dtype = MAMBA_BF16; sa.norm_before_gate = a->norm_before_gate;
+    sa.zxbcdt = w.zx_part; sa.zxbcdt_sb = g.d_in_proj;
     sa.conv_state = a->conv_state; sa.conv_w = a->conv_w; sa.conv_b = a->conv_b;
     sa.dt_bias = a->dt_bias; sa.A = a->A; sa.D = a->D; sa.dt_min = a->dt_min; sa.dt_max = a->dt_max;
     sa.norm_w = a->norm_w; sa.ssm_state = a->ssm_state;
-    sa.out = w.a_out; sa.out_sb = d_inner;  // validated only; the packed path writes a_out itself
+    sa.out = w.a_out; sa.out_sb = g.d_inner;  // validated only: the packed path writes a_out itself
     Step2Params p;
-    // the step-ssm workspace is not used in packed mode: hand it the ssq slot
-    int st = step2_make_params(&sa, w.ssq, (size_t)-1 >> 1, &p);
+    int st = step2_make_params(&sa, w.ssq, (size_t)-1 >> 1, &p);  // no step workspace in packed mode
     if (st != MAMBA_OK) return st;
-    const bool aligned = aligned16(p.ssm) && aligned16(p.conv) && aligned16(p.conv_w);
-    MAMBA_CHECK_ARG(aligned, "ssm_state, conv_state and conv_w must be 16-byte aligned");
     p.g_ws = nullptr; p.ssq_ws = w.ssq;
-    const int mt = lin_mt(a->batch);
-    p.a_out = w.a_out; p.a_mt = mt;
-
-    // 1. pre-norm into the packed in_proj operand
-    hipLaunchKernelGGL(rmsnorm_pack, dim3(a->batch), dim3(256), 0, stream, a->x, a->x_sb, a->d_model,
-                       a->pre_norm_w, w.a_in, mt);
-    MAMBA_CHECK_LAUNCH();
-    // 2. in_proj -> zxbcdt
-    LinParams li = {};
-    li.M = a->batch; li.N = d_in_proj; li.K = a->d_model; li.MT = mt;
-    li.W = static_cast<const lin_bf16x8_t*>(a->in_proj);
-    li.A = reinterpret_cast<const lin_bf16x8_t*>(w.a_in);
-    li.bias = a->in_proj_b;
-    li.out = w.zx; li.out_ld = d_in_proj; li.out_bf16 = a->zxbcdt_dtype == MAMBA_BF16;
-    lin_launch(li, LIN_STORE, stream);
-    MAMBA_CHECK_LAUNCH();
-    // 3. conv + state update + gate, packed out_proj operand + per-head sums of squares
+    p.a_out = w.a_out; p.a_mt = g.mt;
+    p.zx_part = w.zx_part; p.zx_S = g.S_in; p.zx_ld = g.d_in_proj; p.zx_bias = a->in_proj_b;
     if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, stream));
     if (p.N == 128)
         hipLaunchKernelGGL((step2_ssm_fast<128, true>), dim3(p.nb * p.H), dim3(256), 0, stream, p);
@@ -564,31 +681,76 @@ static int layer_dispatch(const mamba2_layer_args* a, void* ws, size_t ws_bytes,
         hipLaunchKernelGGL((step2_ssm_fast<64, true>), dim3(p.nb * p.H), dim3(256), 0, stream, p);
     MAMBA_CHECK_LAUNCH();
     if (ev1) MAMBA_CHECK_HIP(hipEventRecord(ev1, stream));
-    // 4. out_proj with the gated-norm 1/rms and the residual in its epilogue; its
-    //    side job slides the B/C conv windows (every head has read them by now)
+
     LinParams lo = {};
-    lo.M = a->batch; lo.N = a->d_model; lo.K = d_inner; lo.MT = mt;
+    lo.M = g.M; lo.N = g.d_model; lo.K = g.d_inner; lo.MT = g.mt; lo.S = g.S_out;
     lo.W = static_cast<const lin_bf16x8_t*>(a->out_proj);
     lo.A = reinterpret_cast<const lin_bf16x8_t*>(w.a_out);
-    lo.bias = a->out_proj_b;
-    lo.xres = a->x; lo.xres_ld = a->x_sb;
-    lo.ssq = w.ssq; lo.ssq_h = a->nheads; lo.rms_d = (float)d_inner;
-    lo.conv = a->conv_state; lo.conv_dim = conv_dim; lo.conv_k = a->conv_kernel;
-    lo.c0 = d_inner; lo.nc = 2 * a->ngroups * a->dstate;
-    lo.zx = w.zx; lo.zx_ld = d_in_proj; lo.zx_bf16 = a->zxbcdt_dtype == MAMBA_BF16; lo.zx_off = d_inner;
-    lin_launch(lo, LIN_RESID_RMS, stream);
+    lo.part = w.out_part;
+    lin_launch(lo, LIN_PARTIAL, stream);
     MAMBA_CHECK_LAUNCH();
+    return MAMBA_OK;
+}
+
+static RowsParams rows_params(const mamba2_layer_args* a, const LayerGeom& g, const LayerWs& w) {
+    RowsParams rp = {};
+    rp.M = g.M; rp.cols = g.d_model; rp.H = g.H; rp.d_inner = g.d_inner; rp.conv_dim = g.conv_dim;
+    rp.conv_k = a->conv_kernel; rp.nbc = g.nbc;
+    rp.x = a->x; rp.x_ld = a->x_sb;
+    rp.part = w.out_part; rp.bias = a->out_proj_b; rp.ssq = w.ssq;
+    rp.conv = a->conv_state; rp.zx_part = w.zx_part; rp.zx_S = g.S_in; rp.zx_ld = g.d_in_proj;
+    rp.zx_bias = a->in_proj_b;
+    rp.a_out = w.a_in; rp.a_mt = g.mt;
+    return rp;
+}
+
+// n_layers consecutive layers on one residual stream; events (optional) are
+// per-layer arrays recorded around each state-update kernel.
+static int stack_dispatch(const mamba2_layer_args* layers, int n_layers, void* ws, size_t ws_bytes,
+                          hipStream_t stream, void* const* ev0, void* const* ev1) {
+    MAMBA_CHECK_ARG(layers != nullptr && n_layers >= 1, "at least one layer is required");
+    for (int l = 0; l < n_layers; ++l) {
+        const int st = layer_check(&layers[l], &layers[0]);
+        if (st != MAMBA_OK) return st;
+    }
+    const LayerGeom g = layer_geom(&layers[0]);
+    const LayerWs w = layer_ws_layout(g, ws);
+    if (ws == nullptr || ws_bytes < w.total) {
+        set_error("mamba2 layer step: workspace of " + std::to_string(w.total) + " bytes required");
+        return MAMBA_ERR_WORKSPACE;
+    }
+    // pre-norm of the first layer
+    RowsParams rp = rows_params(&layers[0], g, w);
+    rp.w = layers[0].pre_norm_w;
+    rows_launch<true>(rp, 0, stream);
+    MAMBA_CHECK_LAUNCH();
+    for (int l = 0; l < n_layers; ++l) {
+        const mamba2_layer_args* a = &layers[l];
+        const int st = layer_core(a, g, w, stream, ev0 ? (hipEvent_t)ev0[l] : nullptr,
+                                  ev1 ? (hipEvent_t)ev1[l] : nullptr);
+        if (st != MAMBA_OK) return st;
+        // residual of layer l, fused with the pre-norm of layer l + 1
+        rp = rows_params(a, g, w);
+        if (l + 1 < n_layers) {
+            rp.w = layers[l + 1].pre_norm_w;
+            rows_launch<true>(rp, g.S_out, stream);
+        } else {
+            rows_launch<false>(rp, g.S_out, stream);
+        }
+        MAMBA_CHECK_LAUNCH();
+    }
     return MAMBA_OK;
 }
 
 }  // namespace mamba
 
 extern "C" size_t mamba2_layer_workspace_size(const mamba2_layer_args* a) {
-    return a ? layer_ws_layout(a, nullptr).total : 0;
+    if (a == nullptr || a->batch < 1 || a->nheads < 1 || a->headdim < 1) return 0;
+    return layer_ws_layout(layer_geom(a), nullptr).total;
 }
 
 extern "C" int mamba2_layer_step(const mamba2_layer_args* a, void* ws, size_t ws_bytes, mamba_stream_t stream) {
-    return layer_dispatch(a, ws, ws_bytes, (hipStream_t)stream, nullptr, nullptr);
+    return stack_dispatch(a, 1, ws, ws_bytes, (hipStream_t)stream, nullptr, nullptr);
 }
 
 extern "C" int mamba2_layer_step_timed(const mamba2_layer_args* a, void* ws, size_t ws_bytes, mamba_stream_t stream,
@@ -597,5 +759,19 @@ extern "C" int mamba2_layer_step_timed(const mamba2_layer_args* a, void* ws, siz
         set_error("mamba2_layer_step_timed: both events are required");
         return MAMBA_ERR_INVALID_ARG;
     }
-    return layer_dispatch(a, ws, ws_bytes, (hipStream_t)stream, (hipEvent_t)ev_start, (hipEvent_t)ev_stop);
+    return stack_dispatch(a, 1, ws, ws_bytes, (hipStream_t)stream, &ev_start, &ev_stop);
+}
+
+extern "C" int mamba2_stack_step(const mamba2_layer_args* layers, int32_t n_layers, void* ws, size_t ws_bytes,
+                                 mamba_stream_t stream) {
+    return stack_dispatch(layers, n_layers, ws, ws_bytes, (hipStream_t)stream, nullptr, nullptr);
+}
+
+extern "C" int mamba2_stack_step_timed(const mamba2_layer_args* layers, int32_t n_layers, void* ws, size_t ws_bytes,
+                                       mamba_stream_t stream, void* const* ev_start, void* const* ev_stop) {
+    if (ev_start == nullptr || ev_stop == nullptr) {
+        set_error("mamba2_stack_step_timed: both event arrays are required");
+        return MAMBA_ERR_INVALID_ARG;
+    }
+    return stack_dispatch(layers, n_layers, ws, ws_bytes, (hipStream_t)stream, ev_start, ev_stop);
 }

@@ -159,6 +159,9 @@ _SIGNATURES = {
     "mamba2_layer_step": ([ctypes.POINTER(Mamba2LayerArgs), c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),
     "mamba2_layer_step_timed": ([ctypes.POINTER(Mamba2LayerArgs), c_vp, ctypes.c_size_t, c_vp, c_vp, c_vp],
                                 ctypes.c_int),
+    "mamba2_stack_step": ([ctypes.POINTER(Mamba2LayerArgs), c_i32, c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),
+    "mamba2_stack_step_timed": ([ctypes.POINTER(Mamba2LayerArgs), c_i32, c_vp, ctypes.c_size_t, c_vp,
+                                 ctypes.POINTER(c_vp), ctypes.POINTER(c_vp)], ctypes.c_int),
 }
 
 _lib = None

@@ -298,11 +298,11 @@ class Mamba2Stack:
     """A stack of pre-norm Mamba2 layers stepped one token at a time.
 
     The residual stream is kept in f32.  With ``fused`` (the default where the
-    shape allows: headdim 64, dstate 64/128, conv width 4, batch <= 256) each
-    layer is one mamba2_layer_step call: four kernels (pre-norm into the packed
-    product operand, in_proj, state update, out_proj with the gated norm's
-    1/rms and the residual in its epilogue) on weights packed once at
-    construction.  Otherwise the residual add of layer l is fused with the
+    shape allows: headdim 64, dstate 64/128, conv width 4, batch <= 256) the
+    whole stack is one mamba2_stack_step call: per layer four kernels (in_proj,
+    state update, out_proj, and a per-row pass doing the residual, the gated
+    norm's 1/rms, the B/C window slide and the next layer's pre-norm) on
+    weights packed once at construction.  Otherwise the residual add of layer l is fused with the
     RmsNorm of layer l+1 (one mamba_rmsnorm call) around torch.mm products and
     mamba2_step_ssm.  All activations live in buffers allocated once per batch
     size, so ``step_`` allocates nothing and can be captured in a HIP graph."""
@@ -389,18 +389,24 @@ class Mamba2Stack:
         ``events``: optional list of one torch.cuda.Event pair per layer,
         recorded around that layer's state-update kernel (benchmark timing)."""
         bufs = self.buffers(x_res.shape[0], x_res.device)
-        if self.fused and x_res.shape[0] <= 256:
+        if self.fused and x_res.shape[0] <= 256 and x_res.data_ptr() % 16 == 0 and x_res.stride(0) % 4 == 0:
             L = _lib.lib()
             ws = bufs["ws"]
             wsp, stream = ctypes.c_void_p(ws.data_ptr()), _stream(x_res.device)
-            for i in range(len(self.layers)):
-                a = self._layer_args(i, x_res, caches[i])
-                if events is None:
-                    check(L.mamba2_layer_step(ctypes.byref(a), wsp, ws.numel(), stream), "mamba2_layer_step")
-                else:
-                    e0, e1 = _raw_events(events[i], x_res.device)
-                    check(L.mamba2_layer_step_timed(ctypes.byref(a), wsp, ws.numel(), stream, e0, e1),
-                          "mamba2_layer_step_timed")
+            key = ("stack", x_res.data_ptr(), x_res.shape[0]) + tuple(c.ssm_bhpr.data_ptr() for c in caches)
+            arr = self._args.get(key)
+            if arr is None:
+                arr = (Mamba2LayerArgs * len(self.layers))(
+                    *[self._layer_args(i, x_res, caches[i]) for i in range(len(self.layers))])
+                self._args[key] = arr
+            if events is None:
+                check(L.mamba2_stack_step(arr, len(self.layers), wsp, ws.numel(), stream), "mamba2_stack_step")
+            else:
+                raw = [_raw_events(ev, x_res.device) for ev in events]
+                e0 = (ctypes.c_void_p * len(raw))(*[r[0] for r in raw])
+                e1 = (ctypes.c_void_p * len(raw))(*[r[1] for r in raw])
+                check(L.mamba2_stack_step_timed(arr, len(self.layers), wsp, ws.numel(), stream, e0, e1),
+                      "mamba2_stack_step_timed")
             return x_res
         prev = None
         for i, layer in enumerate(self.layers):

@@ -29,6 +29,8 @@
  *   mamba_linear_fwd    <- burn::nn::Linear::forward in the decode steps (packed weights)
  *   mamba2_layer_step   <- Layer::step_one around Mamba2::step (src/modules/layer.rs:224-232,
  *                          src/mamba2/mamba2.rs:820-1004), with packed in_proj/out_proj
+ *   mamba2_stack_step   <- Layers::step over such layers, without class latents
+ *                          (src/modules/layers.rs:427)
  *   mamba_rmsnorm       <- RmsNorm::forward (src/modules/norm/rms_norm.rs:53-98), the
  *                          pre-norm and residual of Layer::step_one (src/modules/layer.rs:224-232)
  */
@@ -292,11 +294,16 @@ int mamba_linear_fwd(const mamba_linear_args* args, void* workspace, size_t work
 /*                                                                             */
 /* with the same state update as mamba2_step_ssm and the caches updated in     */
 /* place.  in_proj / out_proj are the packed weights of mamba_linear_pack.     */
-/* Four kernels: RmsNorm into the product's operand layout, in_proj, the state */
-/* update (writing the out_proj operand), out_proj whose epilogue applies the  */
-/* gated norm's 1/rms and the residual add.  Supports headdim 64, dstate 64 or */
-/* 128, conv_kernel 4, batch <= 256, d_model % 16 == 0; other shapes return    */
-/* MAMBA_ERR_UNSUPPORTED (use mamba2_step_ssm with a separate product).        */
+/* Kernels: RmsNorm into the product's operand layout, in_proj (k-split f32    */
+/* partial planes), the state update (sums the in_proj planes, writes the      */
+/* out_proj operand g * norm_w), out_proj (planes), and a per-row pass that    */
+/* sums those planes, applies the gated norm's 1/rms (a per-row scalar, so it  */
+/* commutes with the product), the bias and the residual add, and slides the  */
+/* B/C conv windows.  The projections stay in f32 (zxbcdt_dtype is ignored).  */
+/* Supports headdim 64, dstate 64 or 128, conv_kernel 4, batch <= 256,         */
+/* d_model % 16 == 0 and <= 4096; other shapes return MAMBA_ERR_UNSUPPORTED    */
+/* (use mamba2_step_ssm with a separate product).  x, the packed weights,      */
+/* pre_norm_w, out_proj_b and the caches must be 16-byte aligned.              */
 /* ------------------------------------------------------------------------- */
 typedef struct mamba2_layer_args {
     int32_t batch, d_model, nheads, headdim, ngroups, dstate, conv_kernel;
@@ -326,6 +333,19 @@ int mamba2_layer_step(const mamba2_layer_args* args, void* workspace, size_t wor
 /* update kernel (benchmark timing; no counterpart in the reference).          */
 int mamba2_layer_step_timed(const mamba2_layer_args* args, void* workspace, size_t workspace_bytes,
                             mamba_stream_t stream, void* event_start, void* event_stop);
+
+/* n_layers pre-norm layers on one residual stream, one token per sequence:    */
+/* the decode side of Layers::step without class latents                       */
+/* (src/modules/layers.rs:427-…).  Every layer shares the shapes and x; the    */
+/* residual pass of layer l also writes the normed operand of layer l + 1, so  */
+/* a layer is four kernels.  Workspace: mamba2_layer_workspace_size of any one */
+/* layer.  The _timed variant records event_start[l] / event_stop[l] around    */
+/* layer l's state-update kernel (benchmark timing).                           */
+int mamba2_stack_step(const mamba2_layer_args* layers, int32_t n_layers, void* workspace,
+                      size_t workspace_bytes, mamba_stream_t stream);
+int mamba2_stack_step_timed(const mamba2_layer_args* layers, int32_t n_layers, void* workspace,
+                            size_t workspace_bytes, mamba_stream_t stream, void* const* event_start,
+                            void* const* event_stop);
 
 /* ------------------------------------------------------------------------- */
 /* Residual add + RmsNorm over rows (src/modules/norm/rms_norm.rs:53-98), the  */
