@@ -46,10 +46,14 @@ struct LinParams {
 // k-splits for a product: enough workgroups (~1300 of 4 waves, ~10 weight
 // blocks per wave) to stream the weight at full HBM rate, fewer for large M
 // where the partial planes grow.
+#ifndef MAMBA_LIN_MAXS_MID
+#define MAMBA_LIN_MAXS_MID 2   // k-split cap for 32 < M <= 64 (fewer partial planes)
+#endif
 inline int lin_splits(int M, int K, int N) {
     const int ks = K / 16, tiles = (N + 31) / 32;
+    const int cap = M <= 32 ? 16 : M <= 64 ? MAMBA_LIN_MAXS_MID : 2;
     int s = 1;
-    while (s < 16 && ks / (2 * s) >= 40 && tiles * s < 1024 && (M <= 64 || s < 2)) s *= 2;
+    while (s < cap && ks / (2 * s) >= 40 && tiles * s < 1024) s *= 2;
     return s;
 }
 inline size_t lin_part_elems(int M, int N, int S) { return (size_t)S * M * N; }

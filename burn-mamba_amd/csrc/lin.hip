@@ -31,7 +31,10 @@ __device__ __forceinline__ lin_f32x16_t lin_mfma(lin_bf16x8_t a, lin_bf16x8_t b,
 
 // Tuning constants (compile-time; defaults measured on MI355X).
 #ifndef MAMBA_LIN_NW
-#define MAMBA_LIN_NW 4          // waves per workgroup
+#define MAMBA_LIN_NW 4          // waves per workgroup for up to two 32-row tiles
+#endif
+#ifndef MAMBA_LIN_NW_BIGM
+#define MAMBA_LIN_NW_BIGM 8     // waves per workgroup for four or eight 32-row tiles
 #endif
 #ifndef MAMBA_LIN_U1
 #define MAMBA_LIN_U1 5          // k-steps per pipeline stage for one 32-row tile
@@ -156,7 +159,7 @@ __global__ __launch_bounds__(64 * NW) void lin_stream(LinParams p) {
 template <int MT>
 static void lin_launch_mt(const LinParams& p, int epi, hipStream_t stream) {
     const dim3 grid((p.N + 31) / 32, p.S);
-    constexpr int NW = MAMBA_LIN_NW;
+    constexpr int NW = MT <= 2 ? MAMBA_LIN_NW : MAMBA_LIN_NW_BIGM;
     if (epi == LIN_STORE) hipLaunchKernelGGL((lin_stream<MT, NW, LIN_STORE>), grid, dim3(64 * NW), 0, stream, p);
     else hipLaunchKernelGGL((lin_stream<MT, NW, LIN_PARTIAL>), grid, dim3(64 * NW), 0, stream, p);
 }
@@ -255,9 +258,36 @@ __global__ __launch_bounds__(256) void lin_act_pack_kernel(const void* x, int M,
 
 }  // namespace mamba
 
+namespace mamba {
+
+// y[m, n] = sum_z part[z][m][n] (+ bias[n]), planes summed in order.
+__global__ __launch_bounds__(256) void lin_reduce_kernel(const float* part, int S, int M, int N, const float* bias,
+                                                         void* y, int64_t y_ld, bool y_bf16) {
+    const int64_t total = (int64_t)M * N;
+    for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * 256) {
+        const int m = (int)(idx / N), n = (int)(idx % N);
+        float v = bias ? bias[n] : 0.f;
+        for (int z = 0; z < S; ++z) v += part[(int64_t)z * total + idx];
+        if (y_bf16)
+            static_cast<bf16_t*>(y)[(int64_t)m * y_ld + n] = f32_to_bf16(v);
+        else
+            static_cast<float*>(y)[(int64_t)m * y_ld + n] = v;
+    }
+}
+
+static size_t linear_ws(const mamba_linear_args* a, size_t* part_off) {
+    const size_t act = align_up(lin_act_elems(a->rows, a->d_in) * 2, 256);
+    const int S = lin_splits(a->rows, a->d_in, a->d_out);
+    *part_off = act;
+    return act + (S > 1 ? align_up(lin_part_elems(a->rows, a->d_out, S) * 4, 256) : 0);
+}
+
+}  // namespace mamba
+
 extern "C" size_t mamba_linear_workspace_size(const mamba_linear_args* a) {
-    if (a == nullptr || a->rows <= 0 || a->d_in <= 0) return 0;
-    return align_up(lin_act_elems(a->rows, a->d_in) * 2, 256);
+    if (a == nullptr || a->rows <= 0 || a->d_in <= 0 || a->d_out <= 0) return 0;
+    size_t off;
+    return linear_ws(a, &off);
 }
 
 extern "C" int mamba_linear_fwd(const mamba_linear_args* a, void* ws, size_t ws_bytes, mamba_stream_t stream) {
@@ -269,7 +299,8 @@ extern "C" int mamba_linear_fwd(const mamba_linear_args* a, void* ws, size_t ws_
     MAMBA_CHECK_ARG(a->y_dtype == MAMBA_F32 || a->y_dtype == MAMBA_BF16, "bad y_dtype");
     MAMBA_CHECK_ARG(a->x_ld >= a->d_in && a->y_ld >= a->d_out, "leading dimensions too small");
     MAMBA_CHECK_ARG(((uintptr_t)a->packed_w & 15u) == 0, "packed_w must be 16-byte aligned");
-    const size_t need = mamba_linear_workspace_size(a);
+    size_t part_off;
+    const size_t need = linear_ws(a, &part_off);
     if (ws == nullptr || ws_bytes < need || ((uintptr_t)ws & 15u) != 0) {
         set_error("mamba_linear_fwd: a 16-byte aligned workspace of " + std::to_string(need) + " bytes is required");
         return MAMBA_ERR_WORKSPACE;
@@ -281,12 +312,22 @@ extern "C" int mamba_linear_fwd(const mamba_linear_args* a, void* ws, size_t ws_
                        a->x, a->rows, a->d_in, a->x_ld, a->x_dtype == MAMBA_BF16, static_cast<bf16_t*>(ws), mt);
     MAMBA_CHECK_LAUNCH();
     LinParams p = {};
-    p.M = a->rows; p.N = a->d_out; p.K = a->d_in; p.MT = mt; p.S = 1;
+    p.M = a->rows; p.N = a->d_out; p.K = a->d_in; p.MT = mt; p.S = lin_splits(a->rows, a->d_in, a->d_out);
     p.W = static_cast<const lin_bf16x8_t*>(a->packed_w);
     p.A = static_cast<const lin_bf16x8_t*>(ws);
-    p.bias = a->bias;
-    p.out = a->y; p.out_ld = a->y_ld; p.out_bf16 = a->y_dtype == MAMBA_BF16;
-    lin_launch(p, LIN_STORE, s);
+    if (p.S == 1) {
+        p.bias = a->bias;
+        p.out = a->y; p.out_ld = a->y_ld; p.out_bf16 = a->y_dtype == MAMBA_BF16;
+        lin_launch(p, LIN_STORE, s);
+        MAMBA_CHECK_LAUNCH();
+        return MAMBA_OK;
+    }
+    p.part = reinterpret_cast<float*>(static_cast<char*>(ws) + part_off);
+    lin_launch(p, LIN_PARTIAL, s);
+    MAMBA_CHECK_LAUNCH();
+    const int64_t nout = (int64_t)a->rows * a->d_out;
+    hipLaunchKernelGGL(lin_reduce_kernel, dim3((int)std::min<int64_t>((nout + 255) / 256, 4096)), dim3(256), 0, s,
+                       p.part, p.S, a->rows, a->d_out, a->bias, a->y, a->y_ld, a->y_dtype == MAMBA_BF16);
     MAMBA_CHECK_LAUNCH();
     return MAMBA_OK;
 }

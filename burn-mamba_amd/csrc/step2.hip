@@ -52,12 +52,22 @@ struct Step2Params {
     const float* zx_part; int zx_S; int64_t zx_ld; const float* zx_bias;
 };
 
-// zxbcdt[b, i]: the single buffer, or the sum of the in_proj partial planes
+// zxbcdt[b, i]: the single buffer, or the sum of the in_proj partial planes.
+// ZS > 0: exactly ZS planes, their loads issued together; ZS = 0: p.zx_S at run time.
+template <int ZS = 0>
 __device__ __forceinline__ float zx_at(const Step2Params& p, const char* zrow, int b, int i) {
-    if (p.zx_S == 0) return p.zx_bf16 ? bf16_to_f32(reinterpret_cast<const bf16_t*>(zrow)[i])
-                                      : reinterpret_cast<const float*>(zrow)[i];
+    if (ZS == 0 && p.zx_S == 0)
+        return p.zx_bf16 ? bf16_to_f32(reinterpret_cast<const bf16_t*>(zrow)[i]) : reinterpret_cast<const float*>(zrow)[i];
     float v = p.zx_bias ? p.zx_bias[i] : 0.f;
-    for (int s = 0; s < p.zx_S; ++s) v += p.zx_part[((int64_t)s * p.nb + b) * p.zx_ld + i];
+    if (ZS > 0) {
+        float q[ZS > 0 ? ZS : 1];
+#pragma unroll
+        for (int s = 0; s < ZS; ++s) q[s] = p.zx_part[((int64_t)s * p.nb + b) * p.zx_ld + i];
+#pragma unroll
+        for (int s = 0; s < ZS; ++s) v += q[s];
+    } else {
+        for (int s = 0; s < p.zx_S; ++s) v += p.zx_part[((int64_t)s * p.nb + b) * p.zx_ld + i];
+    }
     return v;
 }
 
@@ -69,8 +79,9 @@ __device__ __forceinline__ float silu_fast(float x) { return x / (__expf(-x) + 1
 
 // dt = clamp(softplus(dt_raw + dt_bias), lo, hi), mamba2.rs:924 with the f32
 // softplus threshold of src/modules/activation/softplus.rs:21-47.
+template <int ZS = 0>
 __device__ __forceinline__ float step_dt(const Step2Params& p, const char* zrow, int b, int h) {
-    float v = zx_at(p, zrow, b, p.d_inner + p.conv_dim + h);
+    float v = zx_at<ZS>(p, zrow, b, p.d_inner + p.conv_dim + h);
     if (p.dt_bias) v += p.dt_bias[h];
     float dt = v > 18.f ? v : log1pf(__expf(v));
     return fminf(fmaxf(dt, p.dt_lo), p.dt_hi);
@@ -90,7 +101,7 @@ __device__ __forceinline__ float block_sum_256(float v, float* s_red) {
 // Fast path: headdim 64, dstate N in {64, 128}, conv width 4, 256 threads.
 // Thread t owns float4 column n4 = t % (N/4) of rows row0 + i*RPI, i < R.
 // ---------------------------------------------------------------------------
-template <int N, bool PACK>
+template <int N, bool PACK, int ZS = 0>
 __global__ __launch_bounds__(256) void step2_ssm_fast(Step2Params p) {
     constexpr int P = 64;
     constexpr int LPR = N / 4;      // lanes per state row
@@ -126,7 +137,7 @@ __global__ __launch_bounds__(256) void step2_ssm_fast(Step2Params p) {
         else ch = p.d_inner + (p.G + g) * N + (c - P - N);
         const float4 win = win_base[ch];
         const float4 w = cw[ch];
-        const float xin = zx_at(p, zrow, b, p.d_inner + ch);
+        const float xin = zx_at<ZS>(p, zrow, b, p.d_inner + ch);
         float acc = win.y * w.x;
         acc += win.z * w.y;
         acc += win.w * w.z;
@@ -142,7 +153,7 @@ __global__ __launch_bounds__(256) void step2_ssm_fast(Step2Params p) {
             s_C[c - P - N] = v;
         }
     }
-    const float dt = step_dt(p, zrow, b, h);
+    const float dt = step_dt<ZS>(p, zrow, b, h);
     const float dA = __expf(dt * p.A[h]);
     const float Dh = p.Dv ? p.Dv[h] : 0.f;
     __syncthreads();
@@ -189,11 +200,11 @@ __global__ __launch_bounds__(256) void step2_ssm_fast(Step2Params p) {
         const float y = ysum + Dh * s_x[pr];
         float gv = y;
         if (PACK) {
-            const float zg = silu_fast(zx_at(p, zrow, b, h * P + pr));
+            const float zg = silu_fast(zx_at<ZS>(p, zrow, b, h * P + pr));
             if (!p.norm_before_gate) gv *= zg;
             s_pk[pr] = p.norm_before_gate ? y * p.norm_w[h * P + pr] * zg : gv * p.norm_w[h * P + pr];
         } else {
-            if (!p.norm_before_gate) gv *= silu_fast(zx_at(p, zrow, b, h * P + pr));
+            if (!p.norm_before_gate) gv *= silu_fast(zx_at<ZS>(p, zrow, b, h * P + pr));
             p.g_ws[(int64_t)b * p.d_inner + h * P + pr] = gv;
         }
         sq = gv * gv;
@@ -488,92 +499,101 @@ struct RowsParams {
 constexpr int kRowsThreads = 256;
 constexpr int kRowsMaxVec = 4;  // float4 per thread: cols <= 4096
 
+// Workgroups past the M row workgroups slide the shared B/C conv windows of
+// the layer just computed (every head has read them by now): one thread per
+// (row, B/C channel), all of its loads issued together.
+__device__ __forceinline__ void bc_window_slide(const RowsParams& p, int idx) {
+    if (idx >= p.M * p.nbc) return;
+    const int m = idx / p.nbc, c = idx - m * p.nbc;
+    const int ch = p.d_inner + c;
+    float4* win = reinterpret_cast<float4*>(p.conv + ((int64_t)m * p.conv_dim + ch) * 4);
+    const float4 old = *win;
+    const int zi = p.d_inner + ch;
+    float zs[16];
+#pragma unroll
+    for (int z = 0; z < 16; ++z) zs[z] = z < p.zx_S ? p.zx_part[((int64_t)z * p.M + m) * p.zx_ld + zi] : 0.f;
+    float xin = p.zx_bias ? p.zx_bias[zi] : 0.f;
+#pragma unroll
+    for (int z = 0; z < 16; ++z) xin += zs[z];
+    *win = make_float4(old.y, old.z, old.w, xin);
+}
+
 template <int S, bool PACK>
 __global__ __launch_bounds__(kRowsThreads) void layer_rows(RowsParams p) {
     __shared__ float s_red[4];
+    if (S > 0 && (int)blockIdx.x >= p.M) {
+        bc_window_slide(p, ((int)blockIdx.x - p.M) * kRowsThreads + (int)threadIdx.x);
+        return;
+    }
     const int m = blockIdx.x, t = threadIdx.x;
     const int nv = p.cols / 4;
     float4* xr = reinterpret_cast<float4*>(p.x + (int64_t)m * p.x_ld);
-    float4 v[kRowsMaxVec];
+    // ---- every load of this row first (one memory round trip) ----
+    float4 v[kRowsMaxVec], acc[kRowsMaxVec], bb[kRowsMaxVec], w4[kRowsMaxVec];
 #pragma unroll
     for (int i = 0; i < kRowsMaxVec; ++i) {
         const int c4 = t + i * kRowsThreads;
-        if (c4 < nv) v[i] = xr[c4];
+        const bool in = c4 < nv;
+        v[i] = in ? xr[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
+        acc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        bb[i] = (S > 0 && in && p.bias) ? reinterpret_cast<const float4*>(p.bias)[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
+        w4[i] = (PACK && in) ? reinterpret_cast<const float4*>(p.w)[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    if (S > 0) {
-        float4 acc[kRowsMaxVec];
+    float4 q[S > 0 ? S : 1][kRowsMaxVec];
 #pragma unroll
-        for (int i = 0; i < kRowsMaxVec; ++i) acc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-        for (int z = 0; z < S; ++z) {
-            const float4* pl = reinterpret_cast<const float4*>(p.part + ((int64_t)z * p.M + m) * p.cols);
-#pragma unroll
-            for (int i = 0; i < kRowsMaxVec; ++i) {
-                const int c4 = t + i * kRowsThreads;
-                if (c4 < nv) {
-                    const float4 q = pl[c4];
-                    acc[i].x += q.x; acc[i].y += q.y; acc[i].z += q.z; acc[i].w += q.w;
-                }
-            }
-        }
-        // rms of the gated values of this row (per-head partial sums of squares)
-        float ss = 0.f;
-        for (int h = t; h < p.H; h += kRowsThreads) ss += p.ssq[(int64_t)m * p.H + h];
-        ss = block_sum_256(ss, s_red);
-        const float rms = sqrtf(ss / (float)p.d_inner + kDivEpsF32);
+    for (int z = 0; z < S; ++z) {
+        const float4* pl = reinterpret_cast<const float4*>(p.part + ((int64_t)z * p.M + m) * p.cols);
 #pragma unroll
         for (int i = 0; i < kRowsMaxVec; ++i) {
             const int c4 = t + i * kRowsThreads;
-            if (c4 < nv) {
-                float4 o = make_float4(acc[i].x / rms, acc[i].y / rms, acc[i].z / rms, acc[i].w / rms);
-                if (p.bias) {
-                    const float4 bb = reinterpret_cast<const float4*>(p.bias)[c4];
-                    o.x += bb.x; o.y += bb.y; o.z += bb.z; o.w += bb.w;
-                }
-                v[i].x += o.x; v[i].y += o.y; v[i].z += o.z; v[i].w += o.w;
-                xr[c4] = v[i];
-            }
+            q[z][i] = c4 < nv ? pl[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-        // B/C conv windows of row m
-        for (int c = t; c < p.nbc; c += kRowsThreads) {
-            const int ch = p.d_inner + c;
-            float* win = p.conv + ((int64_t)m * p.conv_dim + ch) * p.conv_k;
-            const int zi = p.d_inner + ch;
-            float xin = p.zx_bias ? p.zx_bias[zi] : 0.f;
-            for (int z = 0; z < p.zx_S; ++z) xin += p.zx_part[((int64_t)z * p.M + m) * p.zx_ld + zi];
-            for (int k = 0; k + 1 < p.conv_k; ++k) win[k] = win[k + 1];
-            win[p.conv_k - 1] = xin;
+    }
+    float ss_h = 0.f;
+    if (S > 0 && t < p.H) ss_h = p.ssq[(int64_t)m * p.H + t];
+    if (S > 0) {
+        // ---- residual of the layer just computed ----
+        const float rms = sqrtf(block_sum_256(ss_h, s_red) / (float)p.d_inner + kDivEpsF32);
+#pragma unroll
+        for (int z = 0; z < S; ++z)
+#pragma unroll
+            for (int i = 0; i < kRowsMaxVec; ++i) {
+                acc[i].x += q[z][i].x; acc[i].y += q[z][i].y; acc[i].z += q[z][i].z; acc[i].w += q[z][i].w;
+            }
+#pragma unroll
+        for (int i = 0; i < kRowsMaxVec; ++i) {
+            const int c4 = t + i * kRowsThreads;
+            v[i].x += acc[i].x / rms + bb[i].x;
+            v[i].y += acc[i].y / rms + bb[i].y;
+            v[i].z += acc[i].z / rms + bb[i].z;
+            v[i].w += acc[i].w / rms + bb[i].w;
+            if (c4 < nv) xr[c4] = v[i];
         }
     }
     if (PACK) {
         float ss = 0.f;
 #pragma unroll
-        for (int i = 0; i < kRowsMaxVec; ++i)
-            if (t + i * kRowsThreads < nv) ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
-        ss = block_sum_256(ss, s_red);
-        const float rms = sqrtf(ss / (float)p.cols + kDivEpsF32);
-        // pairs of float4 (8 consecutive columns) form one 16-byte run of the packed layout;
-        // thread t owns columns 4t.. of each slab, so exchange halves through LDS-free
-        // shuffles: lanes 2q and 2q+1 hold columns 8q..8q+7 of a slab
+        for (int i = 0; i < kRowsMaxVec; ++i) ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
+        const float rms = sqrtf(block_sum_256(ss, s_red) / (float)p.cols + kDivEpsF32);
+        // lanes 2q and 2q+1 hold columns 8q..8q+7 of a slab: one 16-byte run of
+        // the packed operand, written by the even lane
 #pragma unroll
         for (int i = 0; i < kRowsMaxVec; ++i) {
             const int c4 = t + i * kRowsThreads;
-            const float4 w4 = c4 < nv ? reinterpret_cast<const float4*>(p.w)[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
-            const uint32_t lo = (uint32_t)f32_to_bf16((v[i].x / rms) * w4.x) |
-                                ((uint32_t)f32_to_bf16((v[i].y / rms) * w4.y) << 16);
-            const uint32_t hi = (uint32_t)f32_to_bf16((v[i].z / rms) * w4.z) |
-                                ((uint32_t)f32_to_bf16((v[i].w / rms) * w4.w) << 16);
+            const uint32_t lo = (uint32_t)f32_to_bf16((v[i].x / rms) * w4[i].x) |
+                                ((uint32_t)f32_to_bf16((v[i].y / rms) * w4[i].y) << 16);
+            const uint32_t hi = (uint32_t)f32_to_bf16((v[i].z / rms) * w4[i].z) |
+                                ((uint32_t)f32_to_bf16((v[i].w / rms) * w4[i].w) << 16);
             const uint32_t lo_n = __shfl_xor(lo, 1, 64), hi_n = __shfl_xor(hi, 1, 64);
-            if (c4 < nv && (c4 & 1) == 0) {
+            if (c4 < nv && (c4 & 1) == 0)
                 *reinterpret_cast<uint4*>(p.a_out + lin_act_offset(m, 4 * c4, p.a_mt)) = make_uint4(lo, hi, lo_n, hi_n);
-            }
         }
     }
 }
 
 template <bool PACK>
 static void rows_launch(const RowsParams& rp, int S, hipStream_t stream) {
-    const dim3 g(rp.M), b(kRowsThreads);
+    const dim3 g(rp.M + (S > 0 ? (rp.M * rp.nbc + kRowsThreads - 1) / kRowsThreads : 0)), b(kRowsThreads);
     switch (S) {
         case 0: hipLaunchKernelGGL((layer_rows<0, PACK>), g, b, 0, stream, rp); break;
         case 1: hipLaunchKernelGGL((layer_rows<1, PACK>), g, b, 0, stream, rp); break;
@@ -675,10 +695,20 @@ static int layer_core(const mamba2_layer_args* a, const LayerGeom& g, const Laye
     p.a_out = w.a_out; p.a_mt = g.mt;
     p.zx_part = w.zx_part; p.zx_S = g.S_in; p.zx_ld = g.d_in_proj; p.zx_bias = a->in_proj_b;
     if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, stream));
-    if (p.N == 128)
-        hipLaunchKernelGGL((step2_ssm_fast<128, true>), dim3(p.nb * p.H), dim3(256), 0, stream, p);
-    else
-        hipLaunchKernelGGL((step2_ssm_fast<64, true>), dim3(p.nb * p.H), dim3(256), 0, stream, p);
+    const dim3 kg(p.nb * p.H), kb(256);
+#define MAMBA_STEP2_PACKED(NN)                                                                        \
+    switch (g.S_in) {                                                                                  \
+        case 1: hipLaunchKernelGGL((step2_ssm_fast<NN, true, 1>), kg, kb, 0, stream, p); break;        \
+        case 2: hipLaunchKernelGGL((step2_ssm_fast<NN, true, 2>), kg, kb, 0, stream, p); break;        \
+        case 4: hipLaunchKernelGGL((step2_ssm_fast<NN, true, 4>), kg, kb, 0, stream, p); break;        \
+        default: hipLaunchKernelGGL((step2_ssm_fast<NN, true, 0>), kg, kb, 0, stream, p); break;       \
+    }
+    if (p.N == 128) {
+        MAMBA_STEP2_PACKED(128)
+    } else {
+        MAMBA_STEP2_PACKED(64)
+    }
+#undef MAMBA_STEP2_PACKED
     MAMBA_CHECK_LAUNCH();
     if (ev1) MAMBA_CHECK_HIP(hipEventRecord(ev1, stream));
 
