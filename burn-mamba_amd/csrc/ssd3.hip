@@ -1,0 +1,301 @@
+// Mamba-3 single-pass ("single-SSD") chunked SSD forward for gfx950.
+//
+// Reference: Mamba3SingleSsdBackendExt::single_ssd_serial_recalculated
+// (burn-mamba src/mamba3/single_ssd/ssd/serial_recalculated/serial_recalculated.rs:86-164):
+// K1 cumsum of da, K2 C.B^T on the fused (time, mimo) axis, K3 chunk state on
+// scale * B, K4 state passing (double_ssd/ssd/serial.rs:118-286) and the
+// single-SSD K5 (:192-291) with its gamma same-step correction
+// (single_ssd/ssd/diag.rs:50-100).  For output step t, MIMO row mo:
+//
+//   y[t,mo,:] = exp(cs_t) C[t,mo].h_in
+//             + sum_{t' < t, mi} (C[t,mo].B[t',mi]) exp(cs_t - cs_t') scale_t' v[t',mi,:]
+//             + gamma_t sum_mi (C[t,mo].B[t,mi]) v[t,mi,:]
+//   h_out     = exp(cs_end) h_in + sum_{t, mi} exp(cs_end - cs_t) scale_t v[t,mi,:] (x) B[t,mi,:]
+//
+// cs is the within-chunk cumulative sum of da (= dt A); positions past seqlen
+// read as zero.  This file holds the shape-generic path: three SIMT kernels
+// (chunk state, state passing, chunk scan) with f32 arithmetic and f32 or bf16
+// I/O; chunk_len counts base time steps.
+#include "common.h"
+
+namespace mamba {
+
+struct Ssd3Params {
+    int nb, L, M, H, P, G, N, Q, nch;
+    int io_dtype;
+    const void* v; int64_t v_sb, v_sl, v_sm, v_sh;
+    const float* da; int64_t da_sb, da_sl, da_sh;
+    const float* gm; int64_t gm_sb, gm_sl, gm_sh;
+    const float* sc; int64_t sc_sb, sc_sl, sc_sh;
+    const void* Bm; int64_t B_sb, B_sl, B_sm, B_sg;
+    const void* Cm; int64_t C_sb, C_sl, C_sm, C_sg;
+    const float* h0;
+    void* y; int64_t y_sb, y_sl, y_sm, y_sh;
+    float* hT;
+};
+
+__device__ __forceinline__ float ld_io(const void* base, int64_t i, bool bf16) {
+    return bf16 ? bf16_to_f32(static_cast<const bf16_t*>(base)[i]) : static_cast<const float*>(base)[i];
+}
+
+// cs[l] = sum_{l' <= l} da over the chunk's base steps; also scale and gamma
+// tables.  Steps past seqlen contribute da = scale = gamma = 0.
+__device__ void ssd3_chunk_tables(const Ssd3Params& p, int b, int c, int h, float* cs, float* scl, float* gmm,
+                                  float* sh4) {
+    float carry = 0.f;
+    for (int base = 0; base < p.Q; base += 256) {
+        const int l = base + threadIdx.x;
+        const int t = c * p.Q + l;
+        const bool ok = l < p.Q && t < p.L;
+        const float dav = ok ? p.da[(int64_t)b * p.da_sb + (int64_t)t * p.da_sl + (int64_t)h * p.da_sh] : 0.f;
+        // inclusive block scan of 256 values
+        const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+        float v = wave_incl_scan(dav);
+        if (lane == 63) sh4[wid] = v;
+        __syncthreads();
+        float off = 0.f;
+        for (int w = 0; w < wid; ++w) off += sh4[w];
+        __syncthreads();
+        if (l < p.Q) {
+            cs[l] = v + off + carry;
+            scl[l] = ok ? p.sc[(int64_t)b * p.sc_sb + (int64_t)t * p.sc_sl + (int64_t)h * p.sc_sh] : 0.f;
+            gmm[l] = ok ? p.gm[(int64_t)b * p.gm_sb + (int64_t)t * p.gm_sl + (int64_t)h * p.gm_sh] : 0.f;
+        }
+        __syncthreads();
+        carry = cs[min(base + 256, p.Q) - 1];
+        __syncthreads();
+    }
+}
+
+// ------------------------------------------------------------ K1 + K3 --
+// S[b,c,h,p,n] = sum_{l, m} v[l,m,p] * B[l,m,n] * scale_l * exp(cs_end - cs_l)
+__global__ __launch_bounds__(256) void ssd3_chunk_state_generic(Ssd3Params p, float* states, float* da_end) {
+    extern __shared__ float smem[];
+    const int h = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
+    const int g = h / (p.H / p.G);
+    const int Q = p.Q, P = p.P, N = p.N, M = p.M;
+    const bool bf = p.io_dtype == MAMBA_BF16;
+    float* cs = smem;
+    float* scl = cs + Q;
+    float* gmm = scl + Q;
+    float* sh4 = gmm + Q;
+    constexpr int TL = 16;  // fused rows staged per pass
+    float* vt = sh4 + 4;    // [TL][P]
+    float* bt = vt + TL * P;  // [TL][N]
+    ssd3_chunk_tables(p, b, c, h, cs, scl, gmm, sh4);
+    const float cs_end = cs[Q - 1];
+    if (threadIdx.x == 0) da_end[((int64_t)b * p.H + h) * p.nch + c] = cs_end;
+    float* Sout = states + (((int64_t)b * p.nch + c) * p.H + h) * P * N;
+    const int QM = Q * M;
+    constexpr int OPT = 32;
+    for (int e0 = 0; e0 < P * N; e0 += 256 * OPT) {
+        float acc[OPT];
+#pragma unroll
+        for (int k = 0; k < OPT; ++k) acc[k] = 0.f;
+        for (int f0 = 0; f0 < QM; f0 += TL) {
+            __syncthreads();
+            for (int i = threadIdx.x; i < TL * P; i += 256) {
+                const int f = f0 + i / P, pp = i % P, l = f / M, m = f % M, t = c * Q + l;
+                vt[i] = (f < QM && t < p.L)
+                            ? ld_io(p.v, (int64_t)b * p.v_sb + (int64_t)t * p.v_sl + (int64_t)m * p.v_sm +
+                                             (int64_t)h * p.v_sh + pp, bf)
+                            : 0.f;
+            }
+            for (int i = threadIdx.x; i < TL * N; i += 256) {
+                const int f = f0 + i / N, n = i % N, l = f / M, m = f % M, t = c * Q + l;
+                float w = 0.f;
+                if (f < QM && t < p.L) {
+                    const float k = __expf(cs_end - cs[l]) * scl[l];
+                    w = ld_io(p.Bm, (int64_t)b * p.B_sb + (int64_t)t * p.B_sl + (int64_t)m * p.B_sm +
+                                        (int64_t)g * p.B_sg + n, bf) * k;
+                }
+                bt[i] = w;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int k = 0; k < OPT; ++k) {
+                const int e = e0 + k * 256 + threadIdx.x;
+                if (e < P * N) {
+                    const int pp = e / N, n = e % N;
+                    float a = acc[k];
+                    for (int r = 0; r < TL; ++r) a += vt[r * P + pp] * bt[r * N + n];
+                    acc[k] = a;
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < OPT; ++k) {
+            const int e = e0 + k * 256 + threadIdx.x;
+            if (e < P * N) Sout[e] = acc[k];
+        }
+    }
+}
+
+// ------------------------------------------------------------------ K4 --
+__global__ __launch_bounds__(256) void ssd3_state_pass_generic(Ssd3Params p, float* states, const float* da_end) {
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int PN = p.P * p.N;
+    const int e = blockIdx.x * 256 + threadIdx.x;
+    if (e >= PN) return;
+    float run = p.h0 ? p.h0[((int64_t)b * p.H + h) * PN + e] : 0.f;
+    const float* de = da_end + ((int64_t)b * p.H + h) * p.nch;
+    for (int c = 0; c < p.nch; ++c) {
+        float* s = states + (((int64_t)b * p.nch + c) * p.H + h) * PN + e;
+        const float tmp = *s;
+        *s = run;
+        run = __expf(de[c]) * run + tmp;
+    }
+    p.hT[((int64_t)b * p.H + h) * PN + e] = run;
+}
+
+// ------------------------------------------------------------ K2 + K5 --
+// One workgroup per (head, chunk, batch); R fused output rows per pass with
+// their C.B^T row segments staged in LDS.
+__global__ __launch_bounds__(256) void ssd3_chunk_scan_generic(Ssd3Params p, const float* states) {
+    extern __shared__ float smem[];
+    const int h = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
+    const int g = h / (p.H / p.G);
+    const int Q = p.Q, P = p.P, N = p.N, M = p.M;
+    const bool bf = p.io_dtype == MAMBA_BF16;
+    float* cs = smem;
+    float* scl = cs + Q;
+    float* gmm = scl + Q;
+    float* sh4 = gmm + Q;
+    float* cb = sh4 + 4;  // [R][Q*M]
+    ssd3_chunk_tables(p, b, c, h, cs, scl, gmm, sh4);
+    const float* hin = states + (((int64_t)b * p.nch + c) * p.H + h) * P * N;
+    const int QM = Q * M;
+    const int R = P >= 256 ? 1 : 256 / P;
+    const int qvalid = min(Q, p.L - c * Q);
+    const int fvalid = qvalid * M;
+    auto cptr = [&](int t, int m) { return (int64_t)b * p.C_sb + (int64_t)t * p.C_sl + (int64_t)m * p.C_sm + (int64_t)g * p.C_sg; };
+    auto bptr = [&](int t, int m) { return (int64_t)b * p.B_sb + (int64_t)t * p.B_sl + (int64_t)m * p.B_sm + (int64_t)g * p.B_sg; };
+    for (int f0 = 0; f0 < fvalid; f0 += R) {
+        __syncthreads();
+        // C.B^T for rows f0..f0+R against every source up to the row's step
+        for (int k = threadIdx.x; k < R * QM; k += 256) {
+            const int fi = f0 + k / QM, fj = k % QM;
+            const int li = fi / M, lj = fj / M;
+            float v = 0.f;
+            if (fi < fvalid && lj <= li) {
+                const int64_t ci = cptr(c * Q + li, fi % M), bj = bptr(c * Q + lj, fj % M);
+                for (int n = 0; n < N; ++n) v += ld_io(p.Cm, ci + n, bf) * ld_io(p.Bm, bj + n, bf);
+            }
+            cb[k] = v;
+        }
+        __syncthreads();
+        for (int k = threadIdx.x; k < R * P; k += 256) {
+            const int fi = f0 + k / P, pp = k % P;
+            if (fi >= fvalid) continue;
+            const int li = fi / M, mo = fi % M, ti = c * Q + li;
+            const int64_t ci = cptr(ti, mo);
+            float blue = 0.f;
+            for (int n = 0; n < N; ++n) blue += ld_io(p.Cm, ci + n, bf) * hin[pp * N + n];
+            blue *= __expf(cs[li]);
+            const float* cbr = cb + (k / P) * QM;
+            float lower = 0.f;
+            for (int fj = 0; fj < li * M; ++fj) {
+                const int lj = fj / M, tj = c * Q + lj;
+                const float vv = ld_io(p.v, (int64_t)b * p.v_sb + (int64_t)tj * p.v_sl + (int64_t)(fj % M) * p.v_sm +
+                                                (int64_t)h * p.v_sh + pp, bf);
+                lower += (cbr[fj] * (__expf(cs[li] - cs[lj]) * scl[lj])) * vv;
+            }
+            float diag = 0.f;
+            for (int mi = 0; mi < M; ++mi) {
+                const float vv = ld_io(p.v, (int64_t)b * p.v_sb + (int64_t)ti * p.v_sl + (int64_t)mi * p.v_sm +
+                                                (int64_t)h * p.v_sh + pp, bf);
+                diag += cbr[li * M + mi] * vv;
+            }
+            const float out = (blue + lower) + diag * gmm[li];
+            const int64_t yi = (int64_t)b * p.y_sb + (int64_t)ti * p.y_sl + (int64_t)mo * p.y_sm + (int64_t)h * p.y_sh + pp;
+            if (bf)
+                static_cast<bf16_t*>(p.y)[yi] = f32_to_bf16(out);
+            else
+                static_cast<float*>(p.y)[yi] = out;
+        }
+    }
+}
+
+// ------------------------------------------------------------ host side --
+static int ssd3_make_params(const mamba_ssd3_args* a, Ssd3Params* out) {
+    MAMBA_CHECK_ARG(a != nullptr, "args is NULL");
+    MAMBA_CHECK_ARG(a->batch > 0 && a->seqlen > 0 && a->mimo > 0, "batch, seqlen and mimo must be >= 1");
+    MAMBA_CHECK_ARG(a->nheads > 0 && a->headdim > 0 && a->dstate > 0, "nheads/headdim/dstate must be >= 1");
+    MAMBA_CHECK_ARG(a->headdim <= 256 && a->dstate <= 256 && a->mimo <= 64, "headdim, dstate <= 256, mimo <= 64");
+    MAMBA_CHECK_ARG(a->ngroups > 0 && a->nheads % a->ngroups == 0, "nheads must be a multiple of ngroups");
+    MAMBA_CHECK_ARG(a->chunk_len > 0 && a->chunk_len * a->mimo <= 4096, "chunk_len * mimo must be in [1, 4096]");
+    MAMBA_CHECK_ARG(a->io_dtype == MAMBA_F32 || a->io_dtype == MAMBA_BF16, "io_dtype must be MAMBA_F32 or MAMBA_BF16");
+    MAMBA_CHECK_ARG(a->v && a->da && a->gamma && a->scale && a->B && a->C && a->y && a->final_state,
+                    "v, da, gamma, scale, B, C, y and final_state are required");
+    Ssd3Params& p = *out;
+    p.nb = a->batch; p.L = a->seqlen; p.M = a->mimo; p.H = a->nheads; p.P = a->headdim; p.G = a->ngroups;
+    p.N = a->dstate; p.Q = a->chunk_len; p.nch = (a->seqlen + a->chunk_len - 1) / a->chunk_len;
+    p.io_dtype = a->io_dtype;
+    p.v = a->v; p.v_sb = a->v_sb; p.v_sl = a->v_sl; p.v_sm = a->v_sm; p.v_sh = a->v_sh;
+    p.da = a->da; p.da_sb = a->da_sb; p.da_sl = a->da_sl; p.da_sh = a->da_sh;
+    p.gm = a->gamma; p.gm_sb = a->gamma_sb; p.gm_sl = a->gamma_sl; p.gm_sh = a->gamma_sh;
+    p.sc = a->scale; p.sc_sb = a->scale_sb; p.sc_sl = a->scale_sl; p.sc_sh = a->scale_sh;
+    p.Bm = a->B; p.B_sb = a->B_sb; p.B_sl = a->B_sl; p.B_sm = a->B_sm; p.B_sg = a->B_sg;
+    p.Cm = a->C; p.C_sb = a->C_sb; p.C_sl = a->C_sl; p.C_sm = a->C_sm; p.C_sg = a->C_sg;
+    p.h0 = a->initial_state;
+    p.y = a->y; p.y_sb = a->y_sb; p.y_sl = a->y_sl; p.y_sm = a->y_sm; p.y_sh = a->y_sh;
+    p.hT = a->final_state;
+    return MAMBA_OK;
+}
+
+static size_t ssd3_ws_bytes(const Ssd3Params& p) {
+    return align_up((size_t)p.nb * p.nch * p.H * p.P * p.N * 4, 256) + align_up((size_t)p.nb * p.H * p.nch * 4, 256);
+}
+
+static int ssd3_dispatch(const mamba_ssd3_args* a, void* ws, size_t ws_bytes, hipStream_t stream, hipEvent_t ev0,
+                         hipEvent_t ev1) {
+    Ssd3Params p;
+    int st = ssd3_make_params(a, &p);
+    if (st != MAMBA_OK) return st;
+    const size_t need = ssd3_ws_bytes(p);
+    if (ws == nullptr || ws_bytes < need) {
+        set_error("mamba_ssd3_fwd: workspace of " + std::to_string(need) + " bytes required");
+        return MAMBA_ERR_WORKSPACE;
+    }
+    const int R = p.P >= 256 ? 1 : 256 / p.P;
+    const size_t sm_state = (3 * (size_t)p.Q + 4 + 16 * (size_t)p.P + 16 * (size_t)p.N) * 4;
+    const size_t sm_scan = (3 * (size_t)p.Q + 4 + (size_t)R * p.Q * p.M) * 4;
+    MAMBA_CHECK_ARG(sm_scan <= 160 * 1024 && sm_state <= 160 * 1024, "chunk_len * mimo too large for the generic path");
+    float* states = static_cast<float*>(ws);
+    float* daend = reinterpret_cast<float*>(static_cast<char*>(ws) +
+                                            align_up((size_t)p.nb * p.nch * p.H * p.P * p.N * 4, 256));
+    const dim3 grid(p.H, p.nch, p.nb);
+    hipLaunchKernelGGL(ssd3_chunk_state_generic, grid, dim3(256), sm_state, stream, p, states, daend);
+    MAMBA_CHECK_LAUNCH();
+    hipLaunchKernelGGL(ssd3_state_pass_generic, dim3(ceil_div(p.P * p.N, 256), p.H, p.nb), dim3(256), 0, stream, p,
+                       states, daend);
+    MAMBA_CHECK_LAUNCH();
+    if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, stream));
+    hipLaunchKernelGGL(ssd3_chunk_scan_generic, grid, dim3(256), sm_scan, stream, p, states);
+    MAMBA_CHECK_LAUNCH();
+    if (ev1) MAMBA_CHECK_HIP(hipEventRecord(ev1, stream));
+    return MAMBA_OK;
+}
+
+}  // namespace mamba
+
+using namespace mamba;
+
+extern "C" size_t mamba_ssd3_workspace_size(const mamba_ssd3_args* a) {
+    Ssd3Params p;
+    if (ssd3_make_params(a, &p) != MAMBA_OK) return 0;
+    return ssd3_ws_bytes(p);
+}
+
+extern "C" int mamba_ssd3_fwd(const mamba_ssd3_args* a, void* ws, size_t ws_bytes, mamba_stream_t stream) {
+    return ssd3_dispatch(a, ws, ws_bytes, (hipStream_t)stream, nullptr, nullptr);
+}
+
+extern "C" int mamba_ssd3_fwd_timed(const mamba_ssd3_args* a, void* ws, size_t ws_bytes, mamba_stream_t stream,
+                                    void* ev_start, void* ev_stop) {
+    if (ev_start == nullptr || ev_stop == nullptr) {
+        set_error("mamba_ssd3_fwd_timed: both events are required");
+        return MAMBA_ERR_INVALID_ARG;
+    }
+    return ssd3_dispatch(a, ws, ws_bytes, (hipStream_t)stream, (hipEvent_t)ev_start, (hipEvent_t)ev_stop);
+}

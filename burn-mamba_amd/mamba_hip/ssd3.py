@@ -1,0 +1,94 @@
+"""Mamba-3 single-pass SSD host interface over the C ABI (``mamba_ssd3_fwd``).
+
+Reference: ``Mamba3SingleSsdInput`` / ``run`` (src/mamba3/single_ssd/ssd/ssd_path/mod.rs:25-133)
+and ``Mamba3SingleSsdBackendExt::single_ssd_serial_recalculated``
+(src/mamba3/single_ssd/ssd/serial_recalculated/serial_recalculated.rs:86-164).
+The reference's chunked [b, n, l, ...] tensors are the [b, n*l, ...] tensors
+here with chunk_len = l.  Tensors are PyTorch device tensors used as memory.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import Ssd3Args, check
+from .ssd import _dtype_code, _raw_events, _stream, workspace
+
+
+def ssd3_fwd(v, da, B, C, gamma, scale, initial_state=None, chunk_len=64, y=None, final_state=None,
+             events=None):
+    """v [b, l, m, h, p]; da, gamma, scale [b, l, h] f32; B, C [b, l, m, g, n] (g = h for
+    per-head B/C); initial_state [b, h, p, n] f32.  Returns (y [b, l, m, h, p], final_state)."""
+    b, l, m, h, p = v.shape
+    g, n = B.shape[3], B.shape[4]
+    if B.shape != C.shape or B.shape[:3] != (b, l, m):
+        raise _lib.MambaHipError("B and C must be [b, l, m, g, n] matching v")
+    for t, nm in ((v, "v"), (B, "B"), (C, "C")):
+        if t.stride(-1) != 1:
+            raise _lib.MambaHipError(f"{nm}: innermost axis must be contiguous")
+    for t, nm in ((da, "da"), (gamma, "gamma"), (scale, "scale")):
+        if t.dtype != torch.float32 or t.shape != (b, l, h):
+            raise _lib.MambaHipError(f"{nm} must be float32 [b, l, h]")
+    if y is None:
+        y = torch.empty((b, l, m, h, p), dtype=v.dtype, device=v.device)
+    if final_state is None:
+        final_state = torch.empty((b, h, p, n), dtype=torch.float32, device=v.device)
+    for t in (initial_state, final_state):
+        if t is not None and (t.dtype != torch.float32 or not t.is_contiguous()):
+            raise _lib.MambaHipError("states must be contiguous float32")
+    a = Ssd3Args()
+    a.batch, a.seqlen, a.mimo, a.nheads, a.headdim, a.ngroups, a.dstate = b, l, m, h, p, g, n
+    a.chunk_len, a.io_dtype = int(chunk_len), _dtype_code(v)
+    a.v = v.data_ptr(); a.v_sb, a.v_sl, a.v_sm, a.v_sh = v.stride()[:4]
+    a.da = da.data_ptr(); a.da_sb, a.da_sl, a.da_sh = da.stride()
+    a.gamma = gamma.data_ptr(); a.gamma_sb, a.gamma_sl, a.gamma_sh = gamma.stride()
+    a.scale = scale.data_ptr(); a.scale_sb, a.scale_sl, a.scale_sh = scale.stride()
+    a.B = B.data_ptr(); a.B_sb, a.B_sl, a.B_sm, a.B_sg = B.stride()[:4]
+    a.C = C.data_ptr(); a.C_sb, a.C_sl, a.C_sm, a.C_sg = C.stride()[:4]
+    a.initial_state = None if initial_state is None else initial_state.data_ptr()
+    a.y = y.data_ptr(); a.y_sb, a.y_sl, a.y_sm, a.y_sh = y.stride()[:4]
+    a.final_state = final_state.data_ptr()
+    L = _lib.lib()
+    need = L.mamba_ssd3_workspace_size(ctypes.byref(a))
+    if need == 0:
+        check(L.mamba_ssd3_fwd(ctypes.byref(a), None, 0, _stream(v.device)), "mamba_ssd3_fwd")
+    ws = workspace(v.device, need)
+    st, wsp = _stream(v.device), ctypes.c_void_p(ws.data_ptr())
+    if events is not None:
+        e0, e1 = _raw_events(events, v.device)
+        check(L.mamba_ssd3_fwd_timed(ctypes.byref(a), wsp, ws.numel(), st, e0, e1), "mamba_ssd3_fwd_timed")
+    else:
+        check(L.mamba_ssd3_fwd(ctypes.byref(a), wsp, ws.numel(), st), "mamba_ssd3_fwd")
+    return y, final_state
+
+
+@dataclass
+class Mamba3SingleSsdInput:
+    """The reference's input bundle with [b, l, ...] tensors (the chunk axis folded into l).
+
+    ``init_state_hpr`` (the learnable initial state) is added to
+    ``initial_state_bhpr``; ``siso_specialization`` is a reference-side
+    performance switch with no effect on the result."""
+    v_blmhp: torch.Tensor
+    b_blmhr: torch.Tensor
+    c_blmhr: torch.Tensor
+    da_blh: torch.Tensor
+    gamma_blh: torch.Tensor
+    scale_blh: torch.Tensor
+    initial_state_bhpr: Optional[torch.Tensor] = None
+    init_state_hpr: Optional[torch.Tensor] = None
+    siso_specialization: bool = False
+
+    def run(self, chunk_len: int = 64):
+        h0 = self.initial_state_bhpr
+        if self.init_state_hpr is not None:
+            base = h0 if h0 is not None else torch.zeros(
+                (self.v_blmhp.shape[0],) + tuple(self.init_state_hpr.shape), device=self.v_blmhp.device)
+            h0 = (base + self.init_state_hpr.unsqueeze(0)).contiguous()
+        return ssd3_fwd(self.v_blmhp, self.da_blh, self.b_blmhr, self.c_blmhr, self.gamma_blh, self.scale_blh,
+                        h0, chunk_len)

@@ -120,6 +120,44 @@ int mamba_ssd2_fwd_timed(const mamba_ssd2_args* args, void* workspace, size_t wo
                          mamba_stream_t stream, void* event_start, void* event_stop);
 
 /* ------------------------------------------------------------------------- */
+/* Mamba-3 single-pass chunked SSD forward (trapezoidal discretisation, MIMO   */
+/* rank M fused into the time axis):                                           */
+/*                                                                             */
+/*   y[t,mo] = exp(cs_t) C[t,mo].h_in                                          */
+/*           + sum_{t'<t, mi} (C[t,mo].B[t',mi]) exp(cs_t - cs_t') scale_t' v[t',mi] */
+/*           + gamma_t sum_mi (C[t,mo].B[t,mi]) v[t,mi]                        */
+/*   h_out   = exp(cs_end) h_in + sum_{t,mi} exp(cs_end - cs_t) scale_t v[t,mi] (x) B[t,mi] */
+/*                                                                             */
+/* with cs the within-chunk cumulative sum of da = dt A.  Replaces            */
+/* Mamba3SingleSsdBackendExt::single_ssd_serial_recalculated                   */
+/* (src/mamba3/single_ssd/ssd/serial_recalculated/serial_recalculated.rs:86-114),*/
+/* whose [b, n, l, ...] chunked tensors are the [b, l, ...] tensors here       */
+/* (chunk_len = l); B/C are per head there (ngroups = nheads).  Strides are    */
+/* element strides; the innermost axis (headdim, dstate) is contiguous.  The   */
+/* reference has no D term in this seam.                                       */
+/* ------------------------------------------------------------------------- */
+typedef struct mamba_ssd3_args {
+    int32_t batch, seqlen, mimo, nheads, headdim, ngroups, dstate, chunk_len;
+    int32_t io_dtype;                                      /* v, B, C, y           */
+    const void* v;      int64_t v_sb, v_sl, v_sm, v_sh;      /* [b, l, m, h, p]      */
+    const float* da;    int64_t da_sb, da_sl, da_sh;         /* [b, l, h]  dt * A    */
+    const float* gamma; int64_t gamma_sb, gamma_sl, gamma_sh; /* [b, l, h]           */
+    const float* scale; int64_t scale_sb, scale_sl, scale_sh; /* [b, l, h]           */
+    const void* B;      int64_t B_sb, B_sl, B_sm, B_sg;      /* [b, l, m, g, n]      */
+    const void* C;      int64_t C_sb, C_sl, C_sm, C_sg;      /* [b, l, m, g, n]      */
+    const float* initial_state;                              /* [b, h, p, n] or NULL */
+    void* y;            int64_t y_sb, y_sl, y_sm, y_sh;      /* [b, l, m, h, p]      */
+    float* final_state;                                      /* [b, h, p, n] f32     */
+} mamba_ssd3_args;
+
+size_t mamba_ssd3_workspace_size(const mamba_ssd3_args* args);
+int mamba_ssd3_fwd(const mamba_ssd3_args* args, void* workspace, size_t workspace_bytes, mamba_stream_t stream);
+/* As mamba_ssd3_fwd, recording the caller's HIP events around the chunk-scan  */
+/* kernel (benchmark timing; no counterpart in the reference).                 */
+int mamba_ssd3_fwd_timed(const mamba_ssd3_args* args, void* workspace, size_t workspace_bytes,
+                         mamba_stream_t stream, void* event_start, void* event_stop);
+
+/* ------------------------------------------------------------------------- */
 /* Mamba-1 selective scan (f32), with the optional dt bias + softplus of       */
 /* Mamba1::ssm and the silu(z) gate of Mamba1::forward:                        */
 /*                                                                             */

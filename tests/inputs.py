@@ -71,3 +71,24 @@ def mamba1_inputs(seed, b, d, l, n, h0=False):
     z = rng.standard_normal((b, d, l), dtype=np.float32)
     hs = (0.1 * rng.standard_normal((b, d, n))).astype(np.float32) if h0 else None
     return dict(u=u, delta=delta, A=A, B=B, C=C, D=D, z=z, h0=hs)
+
+
+def ssd3_inputs(seed, b, l, m, h, p, n, lam=None):
+    """Mamba-3 single-SSD inputs: v, per-head B/C, da = dt A, gamma = lam dt,
+    scale = gamma_t + (1 - lam_{t+1}) dt_{t+1} (0 past the end,
+    single_ssd/single_ssd/mod.rs:129-150), beta = (1 - lam) dt exp(da), h0."""
+    rng = np.random.default_rng(seed)
+    v = rng.standard_normal((b, l, m, h, p)).astype(np.float32)
+    B = (rng.standard_normal((b, l, m, h, n)) / np.sqrt(n)).astype(np.float32)
+    C = (rng.standard_normal((b, l, m, h, n)) / np.sqrt(n)).astype(np.float32)
+    dt = rng.uniform(0.01, 0.3, (b, l, h))
+    A = -rng.uniform(0.5, 2.0, h)
+    lam = 1.0 / (1.0 + np.exp(-rng.standard_normal((b, l, h)))) if lam is None else np.full((b, l, h), lam)
+    da = dt * A
+    gamma = lam * dt
+    nxt = np.concatenate([(1 - lam[:, 1:]) * dt[:, 1:], np.zeros((b, 1, h))], 1)
+    scale = gamma + nxt
+    beta = (1 - lam) * dt * np.exp(da)
+    h0 = (0.1 * rng.standard_normal((b, h, p, n))).astype(np.float32)
+    f = lambda a: np.asarray(a, np.float32)
+    return dict(v=v, B=B, C=C, da=f(da), gamma=f(gamma), scale=f(scale), beta=beta, dt=dt, A=A, lam=lam, h0=h0)

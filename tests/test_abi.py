@@ -50,7 +50,7 @@ int main(void) {{ printf("%zu\\n", sizeof({struct_name})); {body} return 0; }}
     return [int(v) for v in out]
 
 
-@pytest.mark.parametrize("cls_name,c_name", [("Ssd2Args", "mamba_ssd2_args"),
+@pytest.mark.parametrize("cls_name,c_name", [("Ssd2Args", "mamba_ssd2_args"), ("Ssd3Args", "mamba_ssd3_args"),
                                              ("Mamba1ScanArgs", "mamba1_scan_args"),
                                              ("Mamba1StepArgs", "mamba1_step_args"),
                                              ("Conv1dStepArgs", "mamba_conv1d_step_args"),

@@ -22,7 +22,7 @@ import numpy as np
 import pytest
 
 import oracle
-from inputs import mamba1_inputs, softplus, ssd2_inputs, ssd2_test_inputs
+from inputs import mamba1_inputs, softplus, ssd2_inputs, ssd2_test_inputs, ssd3_inputs
 
 SHAPES = [(2, 12, 2, 8, 2, 8, 4), (2, 12, 4, 8, 4, 8, 4), (2, 4, 2, 8, 1, 8, 4), (1, 37, 4, 8, 2, 8, 8)]
 
@@ -242,22 +242,7 @@ def test_mamba2_step_unroll_equals_ssd():
 
 # ----------------------------------------------------------------- Mamba-3 --
 
-def _m3_inputs(seed, b, l, m, h, p, n, lam=None):
-    rng = np.random.default_rng(seed)
-    v = rng.standard_normal((b, l, m, h, p)).astype(np.float32)
-    B = (rng.standard_normal((b, l, m, h, n)) / np.sqrt(n)).astype(np.float32)
-    C = (rng.standard_normal((b, l, m, h, n)) / np.sqrt(n)).astype(np.float32)
-    dt = rng.uniform(0.01, 0.3, (b, l, h))
-    A = -rng.uniform(0.5, 2.0, h)
-    lam = 1.0 / (1.0 + np.exp(-rng.standard_normal((b, l, h)))) if lam is None else np.full((b, l, h), lam)
-    da = dt * A
-    gamma = lam * dt
-    nxt = np.concatenate([(1 - lam[:, 1:]) * dt[:, 1:], np.zeros((b, 1, h))], 1)
-    scale = gamma + nxt
-    beta = (1 - lam) * dt * np.exp(da)
-    h0 = (0.1 * rng.standard_normal((b, h, p, n))).astype(np.float32)
-    f = lambda a: np.asarray(a, np.float32)
-    return dict(v=v, B=B, C=C, da=f(da), gamma=f(gamma), scale=f(scale), beta=beta, dt=dt, A=A, lam=lam, h0=h0)
+_m3_inputs = ssd3_inputs
 
 
 def _trapezoid_loop(d, h0_boundary):
