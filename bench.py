@@ -178,6 +178,97 @@ def bench_mamba1(args):
     }
 
 
+SSD3_CFG4 = dict(batch=4, seqlen=8192, mimo=4, nheads=32, headdim=64, dstate=128, ngroups=32, chunk=128)
+
+
+def ssd3_algorithmic(cfg):
+    """Compulsory HBM bytes and FLOPs of one Mamba-3 single-SSD call at the
+    reference seam (per-head B/C, single_ssd/ssd/serial_recalculated.rs:86-114):
+    v, B, C read and y written in bf16, da/gamma/scale f32, final state f32.
+    FLOPs (causal-exact, fused L*M axis, per token per head):
+    Q M^2 (N + P) + 4 M P N + 2 M^2 (N + P)."""
+    b, l, m, h, p, n, q = (cfg[k] for k in ("batch", "seqlen", "mimo", "nheads", "headdim", "dstate", "chunk"))
+    tok = b * l
+    bytes_ = tok * m * h * (p * 2 * 2 + n * 2 * 2) + tok * h * 3 * 4 + b * h * p * n * 4
+    flops = tok * h * (q * m * m * (n + p) + 4 * m * p * n + 2 * m * m * (n + p))
+    return bytes_, flops
+
+
+def make_ssd3_inputs(cfg, dev, seed=0):
+    """BASELINE.json configs[4] at the SSD seam: v ~ N(0,1); dt = softplus(N(0,1) + b_h)
+    as in config 0; A = -exp(U(ln1, ln16)); da = dt A; lam = sigmoid(N(0,1));
+    gamma = lam dt, scale = gamma + (1 - lam_{t+1}) dt_{t+1}; B, C ~ N(0,1)/sqrt(N)
+    per head and MIMO rank (the rotation/normalisation upstream of the seam is
+    not part of this call)."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    b, l, m, h, p, n = (cfg[k] for k in ("batch", "seqlen", "mimo", "nheads", "headdim", "dstate"))
+    v = torch.randn((b, l, m, h, p), generator=g, device=dev).to(torch.bfloat16)
+    Bm = (torch.randn((b, l, m, h, n), generator=g, device=dev) / n ** 0.5).to(torch.bfloat16)
+    Cm = (torch.randn((b, l, m, h, n), generator=g, device=dev) / n ** 0.5).to(torch.bfloat16)
+    dt_target = torch.exp(torch.empty(h, device=dev).uniform_(float(torch.log(torch.tensor(1e-3))),
+                                                              float(torch.log(torch.tensor(0.1))), generator=g))
+    bias = dt_target + torch.log(-torch.expm1(-dt_target))
+    dt = torch.nn.functional.softplus(torch.randn((b, l, h), generator=g, device=dev) + bias)
+    A = -torch.exp(torch.empty(h, device=dev).uniform_(0.0, float(torch.log(torch.tensor(16.0))), generator=g))
+    lam = torch.sigmoid(torch.randn((b, l, h), generator=g, device=dev))
+    gamma = lam * dt
+    nxt = torch.cat([(1 - lam[:, 1:]) * dt[:, 1:], torch.zeros((b, 1, h), device=dev)], 1)
+    return dict(v=v, B=Bm, C=Cm, da=(dt * A).contiguous(), gamma=gamma.contiguous(),
+                scale=(gamma + nxt).contiguous())
+
+
+def bench_ssd3(args):
+    import torch
+
+    import mamba_hip
+    cfg = dict(SSD3_CFG4)
+    dev = torch.device("cuda:0")
+    inp = make_ssd3_inputs(cfg, dev)
+    y = torch.empty_like(inp["v"])
+    hT = torch.empty((cfg["batch"], cfg["nheads"], cfg["headdim"], cfg["dstate"]), device=dev)
+
+    def step(events=None):
+        mamba_hip.ssd3_fwd(inp["v"], inp["da"], inp["B"], inp["C"], inp["gamma"], inp["scale"], None,
+                           chunk_len=cfg["chunk"], y=y, final_state=hT, events=events)
+
+    ms_per_step, kern_ms = _time_steps(args, step)
+    nbytes, flops = ssd3_algorithmic(cfg)
+    tokens = cfg["batch"] * cfg["seqlen"]
+    achieved = flops / (kern_ms * 1e-3) / 1e12
+    return {
+        "metric": "Mamba-3 SSD prefill tokens/s (B=4 L=8192 H=32 P=64 N=128 MIMO 4) + % MFMA roofline",
+        "value": tokens / (ms_per_step * 1e-3), "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (BASELINE.json configs[4] distributions at the SSD seam, seed 0)",
+        "config": {"workload": "mamba3_ssd_prefill_cfg4", **cfg, "io": "v/B/C/y bf16 (per-head B/C), da/gamma/scale f32",
+                   "entry": "mamba_ssd3_fwd", "algorithmic_bytes": nbytes,
+                   "hbm_gbs": nbytes / (kern_ms * 1e-3) / 1e9},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / BF16_PEAK_TFLOPS, "traffic": None, "kernel_ms": kern_ms,
+                     "algorithmic_flops": flops},
+    }
+
+
+def cpu_baseline_ssd3(cfg, seed=0):
+    """The f32 CPU restatement of the reference's single-SSD K1-K5 (oracle/,
+    OpenMP over (batch, head)) on one sequence of 4096 steps, scaled to tokens/s."""
+    import oracle
+    from inputs import ssd3_inputs
+    oracle.build()
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    L = 4096
+    d = ssd3_inputs(seed, 1, L, cfg["mimo"], cfg["nheads"], cfg["headdim"], cfg["dstate"])
+    t0 = time.perf_counter()
+    oracle.ssd3(d["v"], d["da"], d["B"], d["C"], d["gamma"], d["scale"], None, chunk=cfg["chunk"], prec=32)
+    el = time.perf_counter() - t0
+    return {"value": L / el, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"1 x {L} tokens, {cfg['nheads']} heads, MIMO {cfg['mimo']} ({el:.1f} s), f32 serial "
+                      f"single-SSD K1-K5 restatement of the reference"}
+
+
 DECODE_CFG3 = dict(n_layers=64, d_model=2560, expand=2, headdim=64, dstate=128, ngroups=1, conv_kernel=4,
                    batch=64)
 
@@ -441,7 +532,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="ssd2", choices=["ssd2", "mamba1", "decode"])
+    ap.add_argument("--workload", default="ssd2", choices=["ssd2", "mamba1", "decode", "ssd3"])
     ap.add_argument("--batch", type=int, default=DECODE_CFG3["batch"], help="decode batch")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -453,7 +544,10 @@ def main():
               "(the hot path shards by batch/head with no communication; see DESIGN.md)",
               file=sys.stderr)
         sys.exit(2)
-    if args.workload == "decode":
+    if args.workload == "ssd3":
+        out = bench_ssd3(args)
+        base = (lambda: cpu_baseline_ssd3(SSD3_CFG4))
+    elif args.workload == "decode":
         out = bench_decode(args)
         base = (lambda: cpu_baseline_decode(dict(DECODE_CFG3, batch=args.batch)))
     elif args.workload == "mamba1":

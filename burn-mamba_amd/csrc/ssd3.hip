@@ -15,7 +15,11 @@
 // cs is the within-chunk cumulative sum of da (= dt A); positions past seqlen
 // read as zero.  This file holds the shape-generic path: three SIMT kernels
 // (chunk state, state passing, chunk scan) with f32 arithmetic and f32 or bf16
-// I/O; chunk_len counts base time steps.
+// I/O; chunk_len counts base time steps.  bf16 calls with headdim 64, dstate
+// 128 and a MIMO rank dividing 32 take the single-kernel MFMA path
+// (ssd3_mfma.hip), which chunks on 128 fused positions whatever chunk_len
+// says: the chunked form is exact for any chunk length, so only rounding
+// differs.
 #include "common.h"
 
 namespace mamba {
@@ -247,11 +251,15 @@ static size_t ssd3_ws_bytes(const Ssd3Params& p) {
     return align_up((size_t)p.nb * p.nch * p.H * p.P * p.N * 4, 256) + align_up((size_t)p.nb * p.H * p.nch * 4, 256);
 }
 
+bool ssd3_mfma_supported(const mamba_ssd3_args* a);
+int ssd3_mfma_launch(const mamba_ssd3_args* a, hipStream_t stream, hipEvent_t ev0, hipEvent_t ev1);
+
 static int ssd3_dispatch(const mamba_ssd3_args* a, void* ws, size_t ws_bytes, hipStream_t stream, hipEvent_t ev0,
-                         hipEvent_t ev1) {
+                         hipEvent_t ev1, bool allow_fast) {
     Ssd3Params p;
     int st = ssd3_make_params(a, &p);
     if (st != MAMBA_OK) return st;
+    if (allow_fast && ssd3_mfma_supported(a)) return ssd3_mfma_launch(a, stream, ev0, ev1);
     const size_t need = ssd3_ws_bytes(p);
     if (ws == nullptr || ws_bytes < need) {
         set_error("mamba_ssd3_fwd: workspace of " + std::to_string(need) + " bytes required");
@@ -284,11 +292,21 @@ using namespace mamba;
 extern "C" size_t mamba_ssd3_workspace_size(const mamba_ssd3_args* a) {
     Ssd3Params p;
     if (ssd3_make_params(a, &p) != MAMBA_OK) return 0;
-    return ssd3_ws_bytes(p);
+    return ssd3_ws_bytes(p);  // the MFMA path needs none; this covers both paths
+}
+
+extern "C" int mamba_ssd3_fast_path(const mamba_ssd3_args* a) {
+    Ssd3Params p;
+    if (ssd3_make_params(a, &p) != MAMBA_OK) return -1;
+    return ssd3_mfma_supported(a) ? 1 : 0;
 }
 
 extern "C" int mamba_ssd3_fwd(const mamba_ssd3_args* a, void* ws, size_t ws_bytes, mamba_stream_t stream) {
-    return ssd3_dispatch(a, ws, ws_bytes, (hipStream_t)stream, nullptr, nullptr);
+    return ssd3_dispatch(a, ws, ws_bytes, (hipStream_t)stream, nullptr, nullptr, true);
+}
+
+extern "C" int mamba_ssd3_fwd_generic(const mamba_ssd3_args* a, void* ws, size_t ws_bytes, mamba_stream_t stream) {
+    return ssd3_dispatch(a, ws, ws_bytes, (hipStream_t)stream, nullptr, nullptr, false);
 }
 
 extern "C" int mamba_ssd3_fwd_timed(const mamba_ssd3_args* a, void* ws, size_t ws_bytes, mamba_stream_t stream,
@@ -297,5 +315,5 @@ extern "C" int mamba_ssd3_fwd_timed(const mamba_ssd3_args* a, void* ws, size_t w
         set_error("mamba_ssd3_fwd_timed: both events are required");
         return MAMBA_ERR_INVALID_ARG;
     }
-    return ssd3_dispatch(a, ws, ws_bytes, (hipStream_t)stream, (hipEvent_t)ev_start, (hipEvent_t)ev_stop);
+    return ssd3_dispatch(a, ws, ws_bytes, (hipStream_t)stream, (hipEvent_t)ev_start, (hipEvent_t)ev_stop, true);
 }

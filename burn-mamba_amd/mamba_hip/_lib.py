@@ -159,7 +159,9 @@ _SIGNATURES = {
     "mamba_ssd2_fwd_timed": ([ctypes.POINTER(Ssd2Args), c_vp, ctypes.c_size_t, c_vp, c_vp, c_vp],
                              ctypes.c_int),
     "mamba_ssd3_workspace_size": ([ctypes.POINTER(Ssd3Args)], ctypes.c_size_t),
+    "mamba_ssd3_fast_path": ([ctypes.POINTER(Ssd3Args)], ctypes.c_int),
     "mamba_ssd3_fwd": ([ctypes.POINTER(Ssd3Args), c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),
+    "mamba_ssd3_fwd_generic": ([ctypes.POINTER(Ssd3Args), c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),
     "mamba_ssd3_fwd_timed": ([ctypes.POINTER(Ssd3Args), c_vp, ctypes.c_size_t, c_vp, c_vp, c_vp], ctypes.c_int),
     "mamba1_scan_fwd": ([ctypes.POINTER(Mamba1ScanArgs), c_vp], ctypes.c_int),
     "mamba1_scan_fwd_timed": ([ctypes.POINTER(Mamba1ScanArgs), c_vp, c_vp, c_vp], ctypes.c_int),

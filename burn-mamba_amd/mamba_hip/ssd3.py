@@ -20,10 +20,7 @@ from ._lib import Ssd3Args, check
 from .ssd import _dtype_code, _raw_events, _stream, workspace
 
 
-def ssd3_fwd(v, da, B, C, gamma, scale, initial_state=None, chunk_len=64, y=None, final_state=None,
-             events=None):
-    """v [b, l, m, h, p]; da, gamma, scale [b, l, h] f32; B, C [b, l, m, g, n] (g = h for
-    per-head B/C); initial_state [b, h, p, n] f32.  Returns (y [b, l, m, h, p], final_state)."""
+def _args(v, da, B, C, gamma, scale, initial_state, chunk_len, y, final_state) -> Ssd3Args:
     b, l, m, h, p = v.shape
     g, n = B.shape[3], B.shape[4]
     if B.shape != C.shape or B.shape[:3] != (b, l, m):
@@ -34,10 +31,6 @@ def ssd3_fwd(v, da, B, C, gamma, scale, initial_state=None, chunk_len=64, y=None
     for t, nm in ((da, "da"), (gamma, "gamma"), (scale, "scale")):
         if t.dtype != torch.float32 or t.shape != (b, l, h):
             raise _lib.MambaHipError(f"{nm} must be float32 [b, l, h]")
-    if y is None:
-        y = torch.empty((b, l, m, h, p), dtype=v.dtype, device=v.device)
-    if final_state is None:
-        final_state = torch.empty((b, h, p, n), dtype=torch.float32, device=v.device)
     for t in (initial_state, final_state):
         if t is not None and (t.dtype != torch.float32 or not t.is_contiguous()):
             raise _lib.MambaHipError("states must be contiguous float32")
@@ -53,6 +46,35 @@ def ssd3_fwd(v, da, B, C, gamma, scale, initial_state=None, chunk_len=64, y=None
     a.initial_state = None if initial_state is None else initial_state.data_ptr()
     a.y = y.data_ptr(); a.y_sb, a.y_sl, a.y_sm, a.y_sh = y.stride()[:4]
     a.final_state = final_state.data_ptr()
+    return a
+
+
+def _outputs(v, B, y, final_state):
+    b, l, m, h, p = v.shape
+    if y is None:
+        y = torch.empty((b, l, m, h, p), dtype=v.dtype, device=v.device)
+    if final_state is None:
+        final_state = torch.empty((b, h, p, B.shape[4]), dtype=torch.float32, device=v.device)
+    return y, final_state
+
+
+def ssd3_fast_path(v, da, B, C, gamma, scale, chunk_len=64) -> bool:
+    """True when ``ssd3_fwd`` takes the single-kernel MFMA path for these tensors."""
+    y, hT = _outputs(v, B, None, None)
+    a = _args(v, da, B, C, gamma, scale, None, chunk_len, y, hT)
+    r = _lib.lib().mamba_ssd3_fast_path(ctypes.byref(a))
+    if r < 0:
+        check(1, "mamba_ssd3_fast_path")
+    return r == 1
+
+
+def ssd3_fwd(v, da, B, C, gamma, scale, initial_state=None, chunk_len=64, y=None, final_state=None,
+             events=None, generic=False):
+    """v [b, l, m, h, p]; da, gamma, scale [b, l, h] f32; B, C [b, l, m, g, n] (g = h for
+    per-head B/C); initial_state [b, h, p, n] f32.  Returns (y [b, l, m, h, p], final_state).
+    ``generic`` forces the shape-generic kernels (cross-checks of the fast path)."""
+    y, final_state = _outputs(v, B, y, final_state)
+    a = _args(v, da, B, C, gamma, scale, initial_state, chunk_len, y, final_state)
     L = _lib.lib()
     need = L.mamba_ssd3_workspace_size(ctypes.byref(a))
     if need == 0:
@@ -60,8 +82,12 @@ def ssd3_fwd(v, da, B, C, gamma, scale, initial_state=None, chunk_len=64, y=None
     ws = workspace(v.device, need)
     st, wsp = _stream(v.device), ctypes.c_void_p(ws.data_ptr())
     if events is not None:
+        if generic:
+            raise _lib.MambaHipError("events time the default path only")
         e0, e1 = _raw_events(events, v.device)
         check(L.mamba_ssd3_fwd_timed(ctypes.byref(a), wsp, ws.numel(), st, e0, e1), "mamba_ssd3_fwd_timed")
+    elif generic:
+        check(L.mamba_ssd3_fwd_generic(ctypes.byref(a), wsp, ws.numel(), st), "mamba_ssd3_fwd_generic")
     else:
         check(L.mamba_ssd3_fwd(ctypes.byref(a), wsp, ws.numel(), st), "mamba_ssd3_fwd")
     return y, final_state

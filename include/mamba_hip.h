@@ -151,7 +151,18 @@ typedef struct mamba_ssd3_args {
 } mamba_ssd3_args;
 
 size_t mamba_ssd3_workspace_size(const mamba_ssd3_args* args);
+/* 1 if mamba_ssd3_fwd takes the single-kernel MFMA fast path (bf16 I/O,       */
+/* headdim 64, dstate 128, mimo dividing 32, fused (l, m) axis of uniform      */
+/* stride, 16-byte aligned rows), 0 for the shape-generic path, -1 if the      */
+/* arguments are invalid.  The fast path chunks on 128 fused positions         */
+/* whatever chunk_len says (the chunked form is exact for any chunk length)    */
+/* and needs no workspace.  No counterpart in the reference.                   */
+int mamba_ssd3_fast_path(const mamba_ssd3_args* args);
 int mamba_ssd3_fwd(const mamba_ssd3_args* args, void* workspace, size_t workspace_bytes, mamba_stream_t stream);
+/* Same contract, forced onto the shape-generic kernels; used to cross-check   */
+/* the fast path.                                                              */
+int mamba_ssd3_fwd_generic(const mamba_ssd3_args* args, void* workspace, size_t workspace_bytes,
+                           mamba_stream_t stream);
 /* As mamba_ssd3_fwd, recording the caller's HIP events around the chunk-scan  */
 /* kernel (benchmark timing; no counterpart in the reference).                 */
 int mamba_ssd3_fwd_timed(const mamba_ssd3_args* args, void* workspace, size_t workspace_bytes,

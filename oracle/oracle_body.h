@@ -524,13 +524,22 @@ void F(ssd3_serial)(int batch, int seqlen, int mimo, int nheads, int headdim, in
                 for (size_t i = 0; i < PN; ++i) run[i] = dec * run[i] + S[(size_t)c * PN + i];
             }
             for (size_t i = 0; i < PN; ++i) hT[((size_t)b * H + h) * PN + i] = (float)run[i];
-            /* K5 single (single_ssd/ssd/serial.rs:156-268). */
+            /* K5 single (single_ssd/ssd/serial.rs:156-268); the C.B^T row of each
+             * output (K2, computed once per chunk as the reference does) is
+             * formed before the headdim loop. */
+            REAL* cbrow = (REAL*)malloc(sizeof(REAL) * (size_t)Q * M);
             for (int c = 0; c < nch; ++c) {
                 const REAL* hc = hin + (size_t)c * PN;
                 for (int i = 0; i < Q; ++i) {
                     const int ti = T_OF(c, i);
                     if (ti >= seqlen) break;
-                    for (int mo = 0; mo < M; ++mo)
+                    for (int mo = 0; mo < M; ++mo) {
+                        for (int j = 0; j <= i; ++j)
+                            for (int mi = 0; mi < M; ++mi) {
+                                REAL cbv = 0;
+                                for (int n = 0; n < N; ++n) cbv += CV(ti, mo, n) * BV(T_OF(c, j), mi, n);
+                                cbrow[j * M + mi] = cbv;
+                            }
                         for (int p = 0; p < P; ++p) {
                             REAL ch = 0;
                             for (int n = 0; n < N; ++n) ch += CV(ti, mo, n) * hc[p * N + n];
@@ -539,23 +548,17 @@ void F(ssd3_serial)(int batch, int seqlen, int mimo, int nheads, int headdim, in
                             for (int j = 0; j < i; ++j) {
                                 const int tj = T_OF(c, j);
                                 const REAL ker = F(exp_)(cs[ti] - cs[tj]) * SC(tj);
-                                for (int mi = 0; mi < M; ++mi) {
-                                    REAL cbv = 0;
-                                    for (int n = 0; n < N; ++n) cbv += CV(ti, mo, n) * BV(tj, mi, n);
-                                    ylow += (cbv * ker) * VV(tj, mi, p);
-                                }
+                                for (int mi = 0; mi < M; ++mi) ylow += (cbrow[j * M + mi] * ker) * VV(tj, mi, p);
                             }
                             REAL ydiag = 0;
-                            for (int mi = 0; mi < M; ++mi) {
-                                REAL qk = 0;
-                                for (int n = 0; n < N; ++n) qk += CV(ti, mo, n) * BV(ti, mi, n);
-                                ydiag += qk * VV(ti, mi, p);
-                            }
+                            for (int mi = 0; mi < M; ++mi) ydiag += cbrow[i * M + mi] * VV(ti, mi, p);
                             ydiag *= GM(ti);
                             y[((((size_t)b * seqlen + ti) * M + mo) * H + h) * P + p] = (float)((yoff + ylow) + ydiag);
                         }
+                    }
                 }
             }
+            free(cbrow);
 #undef T_OF
 #undef DA
 #undef GM
