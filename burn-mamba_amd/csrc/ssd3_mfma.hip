@@ -60,41 +60,124 @@ __device__ __forceinline__ s3_f32x16_t s3_zero() {
     return z;
 }
 
-__device__ __forceinline__ uint4 s3_ld16(const void* ptr, bool ok) {
-    return ok ? *(const uint4*)ptr : make_uint4(0u, 0u, 0u, 0u);
+// Raw buffer access (gfx9 descriptor word 3): offsets at or past `bytes`
+// read as zero and drop on store, which clips chunks at the sequence end.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t s3_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 s3_bld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ float s3_bld4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
 }
 
 __device__ __forceinline__ float s3_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float s3_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
+// LDS of one workgroup (about 83 KB at QF = 128).
+template <int QF>
+struct __align__(16) Ssd3Lds {
+    bf16_t xT[32][QF + 8];      // v^T of the chunk (headdim half x positions)
+    bf16_t xTw[32][QF + 8];     // w_j v^T[p][j], the state GEMM's A operand
+    bf16_t B[QF][136];          // B rows of the chunk (positions x dstate)
+    bf16_t h[2][32][136];       // state entering the chunk (bf16 MFMA operand), double-buffered
+    bf16_t y[4][32][40];        // per-wave y tile staging
+    float cs2[QF];              // within-chunk cumulative da, log2 units
+    float sc[QF], gm[QF];       // scale and gamma per position
+    float st[QF];               // step index of each position (read per chunk: keeps the
+                                // diagonal masks in the loop rather than hoisted to SGPRs)
+    float w[QF];                // scale_j exp(cs_end - cs_j)
+    float f[QF / 32 - 1][QF];   // scale_j exp(cs_r0 - cs_j) for tile starts r0 = 32, 64, ..
+    float red[4], anc[QF / 32];
+};
+
+// y of output tile IT (positions 32 IT .. 32 IT + 31 of the chunk) for this
+// wave's headdim half, in one accumulator (lane = column i, so the per-i
+// factors are per-lane scalars applied between the MFMA chains):
+//   y  = C_i.h_in;  y *= exp(cs_r0);  y += lower tiles (f_IT[j]);
+//   y *= exp(cs_i - cs_r0);  y += diagonal tile (exact per-(j, i) factor)
+template <int QF, int IT>
+__device__ __forceinline__ void ssd3_y_tile(Ssd3Lds<QF>& S, const s3_bf16x8_t (&cfr)[8], int cur, int r, int half,
+                                            s3_f32x16_t& y) {
+    constexpr int NK = 8;
+    const int il = IT * 32 + r;
+    const float cs_i = S.cs2[il];
+    const float cs_r0 = S.cs2[IT * 32];
+    const float gm_i = S.gm[il];
+    const float ti = S.st[il];  // chunks and tiles start on step boundaries
+    y = s3_zero();
+#pragma unroll
+    for (int kn = 0; kn < NK; ++kn)
+        y = s3_mfma(*(const s3_bf16x8_t*)&S.h[cur][r][kn * 16 + 8 * half], cfr[kn], y);
+    {
+        const float e0 = __builtin_amdgcn_exp2f(cs_r0);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) y[v] *= e0;
+    }
+#pragma unroll
+    for (int jt = 0; jt <= IT; ++jt) {
+        s3_f32x16_t d = s3_zero();
+#pragma unroll
+        for (int kn = 0; kn < NK; ++kn)
+            d = s3_mfma(*(const s3_bf16x8_t*)&S.B[jt * 32 + r][kn * 16 + 8 * half], cfr[kn], d);
+        // d[v] = C_i . B_j for j = 32 jt + 8 (v / 4) + 4 half + v % 4
+        float fac[16];
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+            const int j0 = jt * 32 + 8 * gq + 4 * half;
+            if (jt < IT) {
+                const float4 fv = *(const float4*)&S.f[IT - 1][j0];
+                fac[4 * gq] = fv.x; fac[4 * gq + 1] = fv.y; fac[4 * gq + 2] = fv.z; fac[4 * gq + 3] = fv.w;
+            } else {
+                const float4 sv = *(const float4*)&S.sc[j0];
+                const float4 cv = *(const float4*)&S.cs2[j0];
+                const float4 tv = *(const float4*)&S.st[j0];
+                const float sa[4] = {sv.x, sv.y, sv.z, sv.w}, ca[4] = {cv.x, cv.y, cv.z, cv.w};
+                const float ta[4] = {tv.x, tv.y, tv.z, tv.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float tj = ta[e];
+                    // exponent clamped at 0: only the tj < ti entries are kept
+                    const float k = sa[e] * __builtin_amdgcn_exp2f(fminf(cs_i - ca[e], 0.f));
+                    fac[4 * gq + e] = tj < ti ? k : (tj == ti ? gm_i : 0.f);
+                }
+            }
+        }
+        if (jt == IT) {
+            const float el = __builtin_amdgcn_exp2f(cs_i - cs_r0);
+#pragma unroll
+            for (int v = 0; v < 16; ++v) y[v] *= el;
+        }
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            s3_bf16x8_t bop;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) bop[e] = (__bf16)(d[8 * kk + e] * fac[8 * kk + e]);
+            // v^T[p][j] in the same permuted k order: j = 32 jt + 16 kk + 4 half + {0..3, 8..11}
+            const int j0 = jt * 32 + 16 * kk + 4 * half;
+            const s3_bf16x4_t lo = *(const s3_bf16x4_t*)&S.xT[r][j0];
+            const s3_bf16x4_t hi = *(const s3_bf16x4_t*)&S.xT[r][j0 + 8];
+            const s3_bf16x8_t a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            y = s3_mfma(a, bop, y);
+        }
+    }
+}
+
 template <int QF>
 __global__ __launch_bounds__(256, 1) void ssd3_scan_mfma(Ssd3MfmaParams p) {
     constexpr int N = 128;
-    constexpr int T = QF / 32;            // i-tiles per chunk (one per wave)
+    constexpr int T = QF / 32;            // output tiles per chunk (one per wave)
     static_assert(T == 4, "one output tile per wave");
-    constexpr int XP = QF + 8;            // s_xT / s_BT row pitch (bf16)
-    constexpr int RP = N + 8;             // s_B / s_C / s_h row pitch (bf16)
     constexpr int NK = N / 16;            // k-steps over dstate
     constexpr int KS = QF / 16;           // k-steps over the chunk
-    constexpr int XI = (QF / 2) * 4;      // v staging items: (row pair, 8-wide headdim chunk)
-    constexpr int BI = (QF / 2) * (N / 8);  // B staging items: (row pair, 8-wide dstate chunk)
-    constexpr int CI = QF * (N / 8);        // C staging items: (row, 8-wide dstate chunk)
-    constexpr int XPT = (XI + 255) / 256, BPT = BI / 256, CPT = CI / 256;
-    __shared__ __align__(16) bf16_t s_xT[32][XP];
-    __shared__ __align__(16) bf16_t s_B[QF][RP];
-    __shared__ __align__(16) bf16_t s_C[QF][RP];
-    __shared__ __align__(16) bf16_t s_BT[N][XP];
-    __shared__ __align__(16) bf16_t s_h[32][RP];
-    __shared__ __align__(16) bf16_t s_y[4][32][40];
-    __shared__ __align__(16) float s_cs2[QF];
-    __shared__ __align__(16) float s_sc[QF];
-    __shared__ __align__(16) float s_gm[QF];
-    __shared__ __align__(16) float s_w[QF];
-    __shared__ __align__(16) float s_f[T - 1][QF];
-    __shared__ float s_red[4];
+    constexpr int XI = (QF / 2) * 4;      // v staging items: (position pair, 8-wide headdim piece)
+    constexpr int BI = (QF / 2) * (N / 8);  // B staging items: (position pair, 8-wide dstate piece)
+    constexpr int XPT = (XI + 255) / 256, BPT = BI / 256;
+    __shared__ Ssd3Lds<QF> S;
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 31, half = lane >> 5;
-    // XCD-aware mapping: the two headdim halves of a head (sharing B/C) and
+    // XCD-aware mapping: the two headdim halves of a head (same B/C rows) and
     // neighbouring heads of a batch row land on one XCD
     const int nwg = p.nb * p.H * 2;
     int w = blockIdx.x;
@@ -114,215 +197,176 @@ __global__ __launch_bounds__(256, 1) void ssd3_scan_mfma(Ssd3MfmaParams p) {
     }
 #pragma unroll
     for (int v = 0; v < 16; ++v)
-        s_h[8 * (v >> 2) + 4 * half + (v & 3)][wave * 32 + r] = __builtin_bit_cast(bf16_t, (__bf16)hacc[v]);
+        S.h[0][8 * (v >> 2) + 4 * half + (v & 3)][wave * 32 + r] = __builtin_bit_cast(bf16_t, (__bf16)hacc[v]);
 
     const bf16_t* vhead = p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh + p0;
     const bf16_t* bhead = p.Bm + (int64_t)b * p.B_sb + (int64_t)g * p.B_sg;
     const bf16_t* chead = p.Cm + (int64_t)b * p.C_sb + (int64_t)g * p.C_sg;
     bf16_t* yhead = p.y + (int64_t)b * p.y_sb + (int64_t)h * p.y_sh + p0;
+    const float* dahead = p.da + (int64_t)b * p.da_sb + (int64_t)h * p.da_sh;
+    const float* schead = p.sc + (int64_t)b * p.sc_sb + (int64_t)h * p.sc_sh;
+    const float* gmhead = p.gm + (int64_t)b * p.gm_sb + (int64_t)h * p.gm_sh;
 
-    // ---- register prefetch of one chunk
-    uint4 xq[XPT][2], bq[BPT][2], cq[CPT];
+    // per-thread byte offsets within a chunk (the host bounds a chunk's span below 2^31 bytes)
+    const uint32_t v_rs = (uint32_t)p.v_sf * 2, b_rs = (uint32_t)p.B_sf * 2, c_rs = (uint32_t)p.C_sf * 2;
+    const uint32_t vo = (uint32_t)(threadIdx.x >> 2) * 2 * v_rs + (threadIdx.x & 3) * 16;
+    const uint32_t bo = (uint32_t)(threadIdx.x >> 4) * 2 * b_rs + (threadIdx.x & 15) * 16;
+    const uint32_t co = (uint32_t)(wave * 32 + r) * c_rs + 16 * half;
+    const int tpos = threadIdx.x >> lgM;  // step of this thread's position within the chunk
+    const uint32_t dao = (uint32_t)tpos * (uint32_t)p.da_sl * 4, sco = (uint32_t)tpos * (uint32_t)p.sc_sl * 4,
+                   gmo = (uint32_t)tpos * (uint32_t)p.gm_sl * 4;
+    const bool first_m = (threadIdx.x & ((1 << lgM) - 1)) == 0;
+
+    // ---- register prefetch of one chunk: v and B pieces for the LDS commit,
+    // this wave's C fragments (MFMA B operand of its output tile), tables
+    static_assert(XPT == 1, "one v item per thread");
+    uint4 xq[XPT][2], bq[BPT][2], cn[NK];
     float daq = 0.f, scq = 0.f, gmq = 0.f;
     auto fetch = [&](int c) {
-#pragma unroll
-        for (int k = 0; k < XPT; ++k) {
-            const int item = threadIdx.x + 256 * k;
-            const int fp = item >> 2, pv = item & 3;
-            const int f0 = c * QF + 2 * fp;
-            const bool ok = item < XI;
-            xq[k][0] = s3_ld16(vhead + (int64_t)f0 * p.v_sf + pv * 8, ok && f0 < p.L);
-            xq[k][1] = s3_ld16(vhead + (int64_t)(f0 + 1) * p.v_sf + pv * 8, ok && f0 + 1 < p.L);
-        }
+        const int rows = min(QF, p.L - c * QF);  // valid positions of the chunk
+        const int steps = rows >> lgM;
+        const int64_t f0 = (int64_t)c * QF;
+        const __amdgpu_buffer_rsrc_t rv = s3_rsrc(vhead + f0 * p.v_sf, (uint32_t)rows * v_rs);
+        const __amdgpu_buffer_rsrc_t rb = s3_rsrc(bhead + f0 * p.B_sf, (uint32_t)rows * b_rs);
+        const __amdgpu_buffer_rsrc_t rc = s3_rsrc(chead + f0 * p.C_sf, (uint32_t)rows * c_rs);
+        xq[0][0] = s3_bld16(rv, vo);
+        xq[0][1] = s3_bld16(rv, vo + v_rs);
 #pragma unroll
         for (int k = 0; k < BPT; ++k) {
-            const int item = threadIdx.x + 256 * k;
-            const int fp = item >> 4, nv = item & 15;
-            const int f0 = c * QF + 2 * fp;
-            bq[k][0] = s3_ld16(bhead + (int64_t)f0 * p.B_sf + nv * 8, f0 < p.L);
-            bq[k][1] = s3_ld16(bhead + (int64_t)(f0 + 1) * p.B_sf + nv * 8, f0 + 1 < p.L);
+            bq[k][0] = s3_bld16(rb, bo + (uint32_t)k * 32 * b_rs);
+            bq[k][1] = s3_bld16(rb, bo + (uint32_t)k * 32 * b_rs + b_rs);
         }
 #pragma unroll
-        for (int k = 0; k < CPT; ++k) {
-            const int item = threadIdx.x + 256 * k;
-            const int f = c * QF + (item >> 4), nv = item & 15;
-            cq[k] = s3_ld16(chead + (int64_t)f * p.C_sf + nv * 8, f < p.L);
-        }
-        daq = scq = gmq = 0.f;
-        const int f = c * QF + threadIdx.x;
-        if (threadIdx.x < QF && f < p.L) {
-            const int t = f >> lgM;
-            if (f - (t << lgM) == 0) daq = p.da[(int64_t)b * p.da_sb + (int64_t)t * p.da_sl + (int64_t)h * p.da_sh];
-            scq = p.sc[(int64_t)b * p.sc_sb + (int64_t)t * p.sc_sl + (int64_t)h * p.sc_sh];
-            gmq = p.gm[(int64_t)b * p.gm_sb + (int64_t)t * p.gm_sl + (int64_t)h * p.gm_sh];
-        }
+        for (int kn = 0; kn < NK; ++kn) cn[kn] = s3_bld16(rc, co + 32 * kn);
+        const int64_t t0 = f0 >> lgM;
+        const __amdgpu_buffer_rsrc_t rda = s3_rsrc(dahead + t0 * p.da_sl, (uint32_t)steps * (uint32_t)p.da_sl * 4);
+        const __amdgpu_buffer_rsrc_t rsc = s3_rsrc(schead + t0 * p.sc_sl, (uint32_t)steps * (uint32_t)p.sc_sl * 4);
+        const __amdgpu_buffer_rsrc_t rgm = s3_rsrc(gmhead + t0 * p.gm_sl, (uint32_t)steps * (uint32_t)p.gm_sl * 4);
+        const float dav = s3_bld4(rda, dao);
+        daq = first_m ? dav : 0.f;  // da enters the cumulative sum once per step
+        scq = s3_bld4(rsc, sco);
+        gmq = s3_bld4(rgm, gmo);
     };
     fetch(0);
 
     for (int c = 0; c < p.nch; ++c) {
-        // ---- commit v (time-major), B and C (row-major), per-position tables
+        const int cur = c & 1;
+        // ---- per-position tables: one block scan of da (log2 units); the
+        // wave totals and the local values at tile starts go through LDS
+        const float loc = wave_incl_scan(daq * kLog2eS3);
+        if (lane == 63) S.red[wave] = loc;
+        if ((threadIdx.x & 31) == 0 && threadIdx.x < QF) S.anc[threadIdx.x >> 5] = loc;
+        __syncthreads();
+        const float cs_end = (S.red[0] + S.red[1]) + (S.red[2] + S.red[3]);
+        if (threadIdx.x < QF) {
+            const int j = threadIdx.x;
+            float off = 0.f;
+#pragma unroll
+            for (int k = 0; k < 3; ++k)
+                if (k < wave) off += S.red[k];
+            const float csj = loc + off;
+            S.cs2[j] = csj;
+            S.st[j] = (float)(j >> lgM);
+            S.sc[j] = scq;
+            S.gm[j] = gmq;
+            S.w[j] = scq * __builtin_amdgcn_exp2f(cs_end - csj);
+#pragma unroll
+            for (int it = 1; it < T; ++it) {
+                if (j < it * 32) {
+                    float anchor = S.anc[it];
+#pragma unroll
+                    for (int k = 0; k < 3; ++k)
+                        if (k < (it >> 1)) anchor += S.red[k];
+                    S.f[it - 1][j] = scq * __builtin_amdgcn_exp2f(anchor - csj);
+                }
+            }
+        }
+        // ---- commit B (row-major) to LDS
+#pragma unroll
+        for (int k = 0; k < BPT; ++k) {
+            const int item = threadIdx.x + 256 * k;
+            const int fp = item >> 4, nv = item & 15;
+            *(uint4*)&S.B[2 * fp][nv * 8] = bq[k][0];
+            *(uint4*)&S.B[2 * fp + 1][nv * 8] = bq[k][1];
+        }
+        __syncthreads();  // w table ready
+        // ---- commit v^T and w-scaled v^T
 #pragma unroll
         for (int k = 0; k < XPT; ++k) {
             const int item = threadIdx.x + 256 * k;
             if (item < XI) {
                 const int fp = item >> 2, pv = item & 3;
+                const float w0 = S.w[2 * fp], w1 = S.w[2 * fp + 1];
                 const uint32_t a0[4] = {xq[k][0].x, xq[k][0].y, xq[k][0].z, xq[k][0].w};
                 const uint32_t a1[4] = {xq[k][1].x, xq[k][1].y, xq[k][1].z, xq[k][1].w};
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    *(uint32_t*)&s_xT[pv * 8 + 2 * e][2 * fp] = (a0[e] & 0xffffu) | (a1[e] << 16);
-                    *(uint32_t*)&s_xT[pv * 8 + 2 * e + 1][2 * fp] = (a0[e] >> 16) | (a1[e] & 0xffff0000u);
+                    *(uint32_t*)&S.xT[pv * 8 + 2 * e][2 * fp] = (a0[e] & 0xffffu) | (a1[e] << 16);
+                    *(uint32_t*)&S.xT[pv * 8 + 2 * e + 1][2 * fp] = (a0[e] >> 16) | (a1[e] & 0xffff0000u);
+                    const s3_bf16x4_t q = {(__bf16)(s3_lo(a0[e]) * w0), (__bf16)(s3_lo(a1[e]) * w1),
+                                           (__bf16)(s3_hi(a0[e]) * w0), (__bf16)(s3_hi(a1[e]) * w1)};
+                    const uint2 qq = __builtin_bit_cast(uint2, q);
+                    *(uint32_t*)&S.xTw[pv * 8 + 2 * e][2 * fp] = qq.x;
+                    *(uint32_t*)&S.xTw[pv * 8 + 2 * e + 1][2 * fp] = qq.y;
                 }
             }
         }
+        s3_bf16x8_t cfr[NK];
 #pragma unroll
-        for (int k = 0; k < BPT; ++k) {
-            const int item = threadIdx.x + 256 * k;
-            const int fp = item >> 4, nv = item & 15;
-            *(uint4*)&s_B[2 * fp][nv * 8] = bq[k][0];
-            *(uint4*)&s_B[2 * fp + 1][nv * 8] = bq[k][1];
-        }
-#pragma unroll
-        for (int k = 0; k < CPT; ++k) {
-            const int item = threadIdx.x + 256 * k;
-            *(uint4*)&s_C[item >> 4][(item & 15) * 8] = cq[k];
-        }
-        {
-            float vsum = wave_incl_scan(daq * kLog2eS3);
-            if (lane == 63) s_red[wave] = vsum;
-            __syncthreads();
-#pragma unroll
-            for (int k = 0; k < 3; ++k)
-                if (k < wave) vsum += s_red[k];
-            if (threadIdx.x < QF) {
-                s_cs2[threadIdx.x] = vsum;
-                s_sc[threadIdx.x] = scq;
-                s_gm[threadIdx.x] = gmq;
-            }
-        }
-        __syncthreads();
-        const float cs2_end = s_cs2[QF - 1];
-        if (threadIdx.x < QF) {
-            const int j = threadIdx.x;
-            const float csj = s_cs2[j];
-            s_w[j] = scq * __builtin_amdgcn_exp2f(cs2_end - csj);
-#pragma unroll
-            for (int it = 1; it < T; ++it)
-                if (j < it * 32) s_f[it - 1][j] = scq * __builtin_amdgcn_exp2f(s_cs2[it * 32] - csj);
-        }
-        __syncthreads();
-        // w-scaled transposed B (the state GEMM's B operand): s_BT[n][j] = w_j B[j][n]
-#pragma unroll
-        for (int k = 0; k < BPT; ++k) {
-            const int item = threadIdx.x + 256 * k;
-            const int fp = item >> 4, nv = item & 15;
-            const float w0 = s_w[2 * fp], w1 = s_w[2 * fp + 1];
-            const uint32_t a0[4] = {bq[k][0].x, bq[k][0].y, bq[k][0].z, bq[k][0].w};
-            const uint32_t a1[4] = {bq[k][1].x, bq[k][1].y, bq[k][1].z, bq[k][1].w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const uint32_t lo = (uint32_t)f32_to_bf16(s3_lo(a0[e]) * w0) | ((uint32_t)f32_to_bf16(s3_lo(a1[e]) * w1) << 16);
-                const uint32_t hi = (uint32_t)f32_to_bf16(s3_hi(a0[e]) * w0) | ((uint32_t)f32_to_bf16(s3_hi(a1[e]) * w1) << 16);
-                *(uint32_t*)&s_BT[nv * 8 + 2 * e][2 * fp] = lo;
-                *(uint32_t*)&s_BT[nv * 8 + 2 * e + 1][2 * fp] = hi;
-            }
-        }
-
-        // ---- y for output tile it = wave
-        {
-            const int it = wave;
-            const int il = it * 32 + r;  // this lane's output position (B-operand column)
-            s3_bf16x8_t cfr[NK];
-#pragma unroll
-            for (int kn = 0; kn < NK; ++kn) cfr[kn] = *(const s3_bf16x8_t*)&s_C[il][kn * 16 + 8 * half];
-            const float cs2_i = s_cs2[il], cs2_r0 = s_cs2[it * 32];
-            s3_f32x16_t yacc = s3_zero();
-            // inter-chunk term h_in . C_i^T
-#pragma unroll
-            for (int kn = 0; kn < NK; ++kn) {
-                const s3_bf16x8_t a = *(const s3_bf16x8_t*)&s_h[r][kn * 16 + 8 * half];
-                yacc = s3_mfma(a, cfr[kn], yacc);
-            }
-            {
-                const float sc0 = __builtin_amdgcn_exp2f(cs2_r0);
-#pragma unroll
-                for (int v = 0; v < 16; ++v) yacc[v] *= sc0;
-            }
-            // C.B^T tile jt -> scaled bf16 B operand -> two y k-steps
-            auto ytile = [&](int jt, auto factor) {
-                s3_f32x16_t d = s3_zero();
-#pragma unroll
-                for (int kn = 0; kn < NK; ++kn) {
-                    const s3_bf16x8_t a = *(const s3_bf16x8_t*)&s_B[jt * 32 + r][kn * 16 + 8 * half];
-                    d = s3_mfma(a, cfr[kn], d);
-                }
-#pragma unroll
-                for (int kk = 0; kk < 2; ++kk) {
-                    s3_bf16x8_t bop;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const int v = 8 * kk + e;
-                        const int j = jt * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-                        bop[e] = (__bf16)(d[v] * factor(j));
-                    }
-                    // v^T[p][j] in the same (permuted) k order: j = jt*32 + 16 kk + {0..3, 8..11} + 4 half
-                    const int j0 = jt * 32 + 16 * kk + 4 * half;
-                    const s3_bf16x4_t lo = *(const s3_bf16x4_t*)&s_xT[r][j0];
-                    const s3_bf16x4_t hi = *(const s3_bf16x4_t*)&s_xT[r][j0 + 8];
-                    s3_bf16x8_t a;
-                    a[0] = lo[0]; a[1] = lo[1]; a[2] = lo[2]; a[3] = lo[3];
-                    a[4] = hi[0]; a[5] = hi[1]; a[6] = hi[2]; a[7] = hi[3];
-                    yacc = s3_mfma(a, bop, yacc);
-                }
-            };
-            for (int jt = 0; jt < it; ++jt) ytile(jt, [&](int j) { return s_f[it - 1][j]; });
-            {
-                const float ei = __builtin_amdgcn_exp2f(cs2_i - cs2_r0);
-#pragma unroll
-                for (int v = 0; v < 16; ++v) yacc[v] *= ei;
-            }
-            const int ti = il >> lgM;  // chunks and tiles start on step boundaries
-            const float gmi = s_gm[il];
-            ytile(it, [&](int j) {
-                const int tj = j >> lgM;
-                return tj < ti ? s_sc[j] * __builtin_amdgcn_exp2f(cs2_i - s_cs2[j]) : (tj == ti ? gmi : 0.f);
-            });
-            // stage the 32 (p) x 32 (time) tile: lane holds y[il][p = 8(v/4) + 4 half + v%4]
-#pragma unroll
-            for (int gq = 0; gq < 4; ++gq) {
-                uint2 pk;
-                pk.x = (uint32_t)f32_to_bf16(yacc[4 * gq]) | ((uint32_t)f32_to_bf16(yacc[4 * gq + 1]) << 16);
-                pk.y = (uint32_t)f32_to_bf16(yacc[4 * gq + 2]) | ((uint32_t)f32_to_bf16(yacc[4 * gq + 3]) << 16);
-                *(uint2*)&s_y[wave][r][8 * gq + 4 * half] = pk;
-            }
-            __builtin_amdgcn_wave_barrier();  // LDS ops of one wave complete in order
-            // 32 rows x 64 bytes: 4 lanes per row, 16 rows per instruction
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                const int row = q * 16 + (lane >> 2), ch = lane & 3;
-                const int f = c * QF + it * 32 + row;
-                if (f < p.L) *(uint4*)(yhead + (int64_t)f * p.y_sf + ch * 8) = *(const uint4*)&s_y[wave][row][ch * 8];
-            }
-        }
-        __syncthreads();  // s_B / s_C / s_h / s_xT reads of the y phase done
-        // ---- next chunk's loads land during the state GEMM
+        for (int kn = 0; kn < NK; ++kn) cfr[kn] = __builtin_bit_cast(s3_bf16x8_t, cn[kn]);
+        // ---- the next chunk's loads land during this chunk's MFMA work
         if (c + 1 < p.nch) fetch(c + 1);
-        // ---- state: h <- exp(cs_end) h + sum_j v^T[p][j] (w_j B[j][n]) for n tile = wave
+        __syncthreads();
+        // ---- state: h <- exp(cs_end) h + sum_j (w_j v^T[p][j]) B[j][n], n tile = wave;
+        // the B operand is read column-wise from the row-major B tile
         {
-            const float dec = __builtin_amdgcn_exp2f(cs2_end);
+            const float dec = __builtin_amdgcn_exp2f(cs_end);
 #pragma unroll
             for (int v = 0; v < 16; ++v) hacc[v] *= dec;
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
-                const s3_bf16x8_t a = *(const s3_bf16x8_t*)&s_xT[r][ks * 16 + 8 * half];
-                const s3_bf16x8_t bo = *(const s3_bf16x8_t*)&s_BT[wave * 32 + r][ks * 16 + 8 * half];
+                const int j0 = ks * 16 + 8 * half;
+                const s3_bf16x8_t a = *(const s3_bf16x8_t*)&S.xTw[r][j0];
+                s3_bf16x8_t bo;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) bo[e] = __builtin_bit_cast(__bf16, S.B[j0 + e][wave * 32 + r]);
                 hacc = s3_mfma(a, bo, hacc);
             }
 #pragma unroll
             for (int v = 0; v < 16; ++v)
-                s_h[8 * (v >> 2) + 4 * half + (v & 3)][wave * 32 + r] = __builtin_bit_cast(bf16_t, (__bf16)hacc[v]);
+                S.h[cur ^ 1][8 * (v >> 2) + 4 * half + (v & 3)][wave * 32 + r] =
+                    __builtin_bit_cast(bf16_t, (__bf16)hacc[v]);
         }
-        __syncthreads();  // s_h / s_xT / s_BT consumed before the next commit
+        // ---- y for output tile = wave
+        {
+            s3_f32x16_t yacc;
+            switch (wave) {
+                case 0: ssd3_y_tile<QF, 0>(S, cfr, cur, r, half, yacc); break;
+                case 1: ssd3_y_tile<QF, 1>(S, cfr, cur, r, half, yacc); break;
+                case 2: ssd3_y_tile<QF, 2>(S, cfr, cur, r, half, yacc); break;
+                default: ssd3_y_tile<QF, 3>(S, cfr, cur, r, half, yacc); break;
+            }
+            // stage the 32 (time) x 32 (p) tile: lane holds y[i][p = 8(v/4) + 4 half + v%4]
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq) {
+                const s3_bf16x4_t q = {(__bf16)yacc[4 * gq], (__bf16)yacc[4 * gq + 1], (__bf16)yacc[4 * gq + 2],
+                                       (__bf16)yacc[4 * gq + 3]};
+                *(s3_bf16x4_t*)&S.y[wave][r][8 * gq + 4 * half] = q;
+            }
+            __builtin_amdgcn_wave_barrier();  // LDS ops of one wave complete in order
+            // 32 rows x 64 bytes: 4 lanes per row, 16 rows per instruction
+            const int rows = min(QF, p.L - c * QF);
+            const uint32_t y_rs = (uint32_t)p.y_sf * 2;
+            const __amdgpu_buffer_rsrc_t ry = s3_rsrc(yhead + (int64_t)c * QF * p.y_sf, (uint32_t)rows * y_rs);
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const int row = q * 16 + (lane >> 2), ch = lane & 3;
+                const uint4 val = *(const uint4*)&S.y[wave][row][ch * 8];
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(decltype(__builtin_amdgcn_raw_buffer_load_b128(ry, 0, 0, 0)), val),
+                                                       ry, (uint32_t)(wave * 32 + row) * y_rs + ch * 16, 0, 0);
+            }
+        }
+        __syncthreads();  // LDS reads of this chunk done before the next commit
     }
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
