@@ -29,6 +29,11 @@ CFLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-I", os.path.join(HERE, "..", "include"),
 ]
+# per-file additions: MFMA results kept in VGPRs (no AGPR round trips for
+# kernels that post-process accumulators with VALU work)
+FILE_FLAGS = {
+    "ssd3_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
 
 
 def _deps_newer(obj: str, src: str) -> bool:
@@ -42,7 +47,7 @@ def _deps_newer(obj: str, src: str) -> bool:
 def _compile(src: str, force: bool) -> str:
     obj = os.path.join(OBJDIR, os.path.basename(src).replace(".hip", ".o"))
     if force or _deps_newer(obj, src):
-        cmd = [HIPCC, *CFLAGS, "-c", src, "-o", obj]
+        cmd = [HIPCC, *CFLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
         r = subprocess.run(cmd, capture_output=True, text=True)
         if r.returncode != 0:
             raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")

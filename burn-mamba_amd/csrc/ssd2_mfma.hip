@@ -57,6 +57,9 @@ constexpr int kMaxQ = 256;
 #ifndef MAMBA_SSD2_DIAG_FACTORED
 #define MAMBA_SSD2_DIAG_FACTORED 0  // tabulated diagonal-block decay when its span allows
 #endif
+#ifndef MAMBA_SSD2_CB_BF16
+#define MAMBA_SSD2_CB_BF16 1  // C.B^T fragments stored in bf16 (else f32)
+#endif
 
 __device__ __forceinline__ f32x16_t mfma32x32x16(bf16x8_t a, bf16x8_t b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -94,6 +97,23 @@ __device__ __forceinline__ f32x16_t zero16() {
     return z;
 }
 
+// One lane's C.B^T fragment (8 consecutive k) in the workspace
+#if MAMBA_SSD2_CB_BF16
+typedef bf16_t cb_t;
+constexpr int kCbLane = 8;  // elements per lane in a fragment block
+struct CbFrag { uint4 v; };
+__device__ __forceinline__ CbFrag cb_load(const cb_t* q) { return {*(const uint4*)q}; }
+__device__ __forceinline__ void cb_unpack(const CbFrag& f, float* o) { unpack8(f.v, o); }
+#else
+typedef float cb_t;
+constexpr int kCbLane = 4;
+struct CbFrag { float4 a, b; };
+__device__ __forceinline__ CbFrag cb_load(const cb_t* q) { return {*(const float4*)q, *(const float4*)(q + 256)}; }
+__device__ __forceinline__ void cb_unpack(const CbFrag& f, float* o) {
+    o[0] = f.a.x; o[1] = f.a.y; o[2] = f.a.z; o[3] = f.a.w; o[4] = f.b.x; o[5] = f.b.y; o[6] = f.b.z; o[7] = f.b.w;
+}
+#endif
+
 // ------------------------------------------------ per-group operand prep --
 // Per (batch, chunk, group) -- shared by every head of the group -- write the
 // MFMA B operands of the scan kernel in fragment order, so that each wave
@@ -106,7 +126,7 @@ __device__ __forceinline__ f32x16_t zero16() {
 // fragments of cbf are written (K2, src/mamba2/ssd/serial.rs:170-185), and
 // inside the diagonal 32x32 blocks the entries with j > i are stored as 0.
 template <int N, int Q>
-__global__ __launch_bounds__(256) void ssd2_prep_mfma(Ssd2Params p, float* cbf, bf16_t* cf, void* bfr) {
+__global__ __launch_bounds__(256) void ssd2_prep_mfma(Ssd2Params p, cb_t* cbf, bf16_t* cf, void* bfr) {
     constexpr int T = Q / 32, NK = N / 16, KS = Q / 16, NTN = N / 32;
     constexpr int NTILE = T * (T + 1) / 2;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 31, half = lane >> 5;
@@ -117,7 +137,7 @@ __global__ __launch_bounds__(256) void ssd2_prep_mfma(Ssd2Params p, float* cbf, 
     const bf16_t* Bg = (const bf16_t*)p.Bm + (int64_t)b * p.B_sb + (int64_t)g * p.B_sg;
     // (C.B^T)^T tiles: D[j][i] = sum_n B[j][n] C[i][n]; the lane then holds
     // column i = 32 it + r at rows j = 32 jt + 8 q + 4 half + u (v = 4 q + u)
-    float* cbase = cbf + grp * Q * Q;
+    cb_t* cbase = cbf + grp * Q * Q;
     for (int tile = s + S * wave; tile < NTILE; tile += 4 * S) {
         int it = 0;
         while ((it + 1) * (it + 2) / 2 <= tile) ++it;
@@ -139,8 +159,18 @@ __global__ __launch_bounds__(256) void ssd2_prep_mfma(Ssd2Params p, float* cbf, 
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int ks = 2 * jt + (q >> 1), lp = r + 32 * (q & 1);
+#if MAMBA_SSD2_CB_BF16
+            // fragment (it, ks), lane lp, elements 4 half .. 4 half + 3
+            uint2 pk;
+            pk.x = (uint32_t)__builtin_bit_cast(bf16_t, (__bf16)acc[4 * q]) |
+                   ((uint32_t)__builtin_bit_cast(bf16_t, (__bf16)acc[4 * q + 1]) << 16);
+            pk.y = (uint32_t)__builtin_bit_cast(bf16_t, (__bf16)acc[4 * q + 2]) |
+                   ((uint32_t)__builtin_bit_cast(bf16_t, (__bf16)acc[4 * q + 3]) << 16);
+            *(uint2*)(cbase + ((int64_t)(it * KS + ks) * 64 + lp) * 8 + 4 * half) = pk;
+#else
             const float4 val = make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
             *(float4*)(cbase + (((int64_t)(it * KS + ks) * 2 + half) * 64 + lp) * 4) = val;
+#endif
         }
     }
     bf16_t* cbase2 = cf + grp * (int64_t)Q * N;
@@ -201,7 +231,7 @@ __device__ __forceinline__ int itile_owner(int it) {
 // both bounded (< 2^60); otherwise it falls back to the exact exponent
 // exp(cs_i - cs_j), accumulated after the e_i scaling.
 template <int N, int Q, int PT>
-__global__ __launch_bounds__(256, 2) void ssd2_scan_mfma(Ssd2Params p, const float* cbf,
+__global__ __launch_bounds__(256, 2) void ssd2_scan_mfma(Ssd2Params p, const cb_t* cbf,
                                                          const bf16_t* cf, const void* bfr) {
     constexpr int T = Q / 32;                 // i-tiles per chunk
     constexpr int NTN = N / 32;               // n tiles of the state
@@ -217,6 +247,7 @@ __global__ __launch_bounds__(256, 2) void ssd2_scan_mfma(Ssd2Params p, const flo
     __shared__ __align__(16) float s_cs2[Q];
     __shared__ __align__(16) float s_w[Q];
     __shared__ __align__(16) float s_fd[Q];
+    __shared__ __align__(16) float s_dt[Q];
     __shared__ float s_red[4];
     __shared__ __align__(16) float s_f[T > 1 ? T - 1 : 1][Q];
     __shared__ __align__(16) bf16_t s_xT[PT * 32][XP];
@@ -297,7 +328,8 @@ __global__ __launch_bounds__(256, 2) void ssd2_scan_mfma(Ssd2Params p, const flo
     // L2 warm-up of the next chunk's group operands: the H/G heads (x headdim
     // splits) of a group share them and sit on one XCD, so each workgroup
     // touches one slice of the group's lines, one dword per line
-    constexpr int CB_LINES = 16 * T * (T + 1);  // causal C.B^T fragments
+    constexpr int FL = 512 * (int)sizeof(cb_t) / 128;  // 128-byte lines per C.B^T fragment
+    constexpr int CB_LINES = FL * T * (T + 1);  // causal C.B^T fragments (row it: 2 it + 2 of them)
     constexpr int FR_LINES = Q * N * 2 / 128;   // C fragments (bf16)
     constexpr int GRP_LINES = CB_LINES + (MAMBA_SSD2_B_F32 ? 3 : 2) * FR_LINES;  // + B fragments
     const int nslice = (p.H / p.G) * splits;
@@ -307,8 +339,8 @@ __global__ __launch_bounds__(256, 2) void ssd2_scan_mfma(Ssd2Params p, const flo
     int64_t pf_off = 0;  // byte offset of the line inside the group's block
     if (pf_line < CB_LINES) {
         int it = 0;
-        while (16 * (it + 1) * (it + 2) <= pf_line) ++it;
-        pf_off = ((int64_t)it * KS * 16 + (pf_line - 16 * it * (it + 1))) * 128;
+        while (FL * (it + 1) * (it + 2) <= pf_line) ++it;
+        pf_off = ((int64_t)it * KS * FL + (pf_line - FL * it * (it + 1))) * 128;
     } else if (pf_line < CB_LINES + FR_LINES) {
         pf_off = (int64_t)(pf_line - CB_LINES) * 128;
     } else {
@@ -352,6 +384,7 @@ __global__ __launch_bounds__(256, 2) void ssd2_scan_mfma(Ssd2Params p, const flo
             const float csj = s_cs2[j];
             s_w[j] = dtv * __builtin_amdgcn_exp2f(cs2_end - csj);
             s_fd[j] = dtv * __builtin_amdgcn_exp2f(s_cs2[j & ~31] - csj);
+            s_dt[j] = dtv;
             // decay table of the strictly-lower blocks: row block it > j / 32
 #pragma unroll
             for (int it = 1; it < T; ++it)
@@ -363,7 +396,7 @@ __global__ __launch_bounds__(256, 2) void ssd2_scan_mfma(Ssd2Params p, const flo
 
         // ---- K2 + K5: y^T for the i-tiles this wave owns
         const int64_t grp = ((int64_t)b * p.nch + c) * p.G + g;
-        const float* cbg = cbf + grp * Q * Q + lane * 4;
+        const cb_t* cbg = cbf + grp * Q * Q + lane * kCbLane;
         const bf16_t* cfg = cf + grp * (int64_t)Q * N + lane * 8;
 #pragma unroll 1
         for (int it = 0; it < T; ++it) {
@@ -374,17 +407,14 @@ __global__ __launch_bounds__(256, 2) void ssd2_scan_mfma(Ssd2Params p, const flo
             uint4 craw[NK];
 #pragma unroll
             for (int kn = 0; kn < NK; ++kn) craw[kn] = *(const uint4*)(cfg + (int64_t)(it * NK + kn) * 512);
-            const float* cbt = cbg + (int64_t)it * KS * 512;  // fragment (it, ks) at + ks * 512
+            const cb_t* cbt = cbg + (int64_t)it * KS * 512;  // fragment (it, ks) at + ks * 512
             const int nb = 2 * it;    // strictly-lower k-steps (even)
             const int ntot = nb + 2;  // + the diagonal block
             constexpr int RD = MAMBA_SSD2_CB_RING;  // CB fragment ring depth
-            float4 ring[RD][2];
+            CbFrag ring[RD];
 #pragma unroll
             for (int k = 0; k < RD; ++k)
-                if (k < ntot) {
-                    ring[k][0] = *(const float4*)(cbt + k * 512);
-                    ring[k][1] = *(const float4*)(cbt + k * 512 + 256);
-                }
+                if (k < ntot) ring[k] = cb_load(cbt + k * 512);
             const float cs2_i = s_cs2[il];
             const float cs2_r0 = s_cs2[it * 32];
             f32x16_t yacc[PT];
@@ -414,15 +444,13 @@ __global__ __launch_bounds__(256, 2) void ssd2_scan_mfma(Ssd2Params p, const flo
                     const int ks = ks0 + k;
                     if (ks < nb) {
                         const int j0 = ks * 16 + 8 * half;
-                        const float4 c0 = ring[k][0], c1 = ring[k][1];
-                        if (ks + RD < ntot) {
-                            ring[k][0] = *(const float4*)(cbt + (ks + RD) * 512);
-                            ring[k][1] = *(const float4*)(cbt + (ks + RD) * 512 + 256);
-                        }
+                        float cv[8];
+                        cb_unpack(ring[k], cv);
+                        if (ks + RD < ntot) ring[k] = cb_load(cbt + (ks + RD) * 512);
                         const float4 f0 = *(const float4*)&s_f[it - 1][j0];
                         const float4 f1 = *(const float4*)&s_f[it - 1][j0 + 4];
-                        const float m[8] = {c0.x * f0.x, c0.y * f0.y, c0.z * f0.z, c0.w * f0.w,
-                                            c1.x * f1.x, c1.y * f1.y, c1.z * f1.z, c1.w * f1.w};
+                        const float m[8] = {cv[0] * f0.x, cv[1] * f0.y, cv[2] * f0.z, cv[3] * f0.w,
+                                            cv[4] * f1.x, cv[5] * f1.y, cv[6] * f1.z, cv[7] * f1.w};
                         const bf16x8_t bop = pack8(m);
 #pragma unroll
                         for (int pt = 0; pt < PT; ++pt) {
@@ -435,12 +463,11 @@ __global__ __launch_bounds__(256, 2) void ssd2_scan_mfma(Ssd2Params p, const flo
             // diagonal block: its two CB fragments sit in ring slots nb % RD and
             // nb % RD + 1 (nb is even).  The prep stored its upper triangle as 0.
             static_assert(RD == 2 || RD == 4, "ring depth 2 or 4");
-            float4 dg[2][2];
+            CbFrag dg[2];
             if (RD == 2 || (nb & 3) == 0) {
-                dg[0][0] = ring[0][0]; dg[0][1] = ring[0][1]; dg[1][0] = ring[1][0]; dg[1][1] = ring[1][1];
+                dg[0] = ring[0]; dg[1] = ring[1];
             } else {
-                dg[0][0] = ring[RD - 2][0]; dg[0][1] = ring[RD - 2][1];
-                dg[1][0] = ring[RD - 1][0]; dg[1][1] = ring[RD - 1][1];
+                dg[0] = ring[RD - 2]; dg[1] = ring[RD - 1];
             }
             const float ei = __builtin_amdgcn_exp2f(cs2_i - cs2_r0);
             const float span = cs2_r0 - s_cs2[it * 32 + 31];
@@ -450,12 +477,13 @@ __global__ __launch_bounds__(256, 2) void ssd2_scan_mfma(Ssd2Params p, const flo
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk) {
                     const int j0 = it * 32 + kk * 16 + 8 * half;
-                    const float4 c0 = dg[kk][0], c1 = dg[kk][1];
+                    float cv[8];
+                    cb_unpack(dg[kk], cv);
                     const float4 f0 = *(const float4*)&s_fd[j0];
                     const float4 f1 = *(const float4*)&s_fd[j0 + 4];
                     const int d = il - j0;  // position of the diagonal in this fragment
-                    float m[8] = {c0.x * f0.x, c0.y * f0.y, c0.z * f0.z, c0.w * f0.w,
-                                  c1.x * f1.x, c1.y * f1.y, c1.z * f1.z, c1.w * f1.w};
+                    float m[8] = {cv[0] * f0.x, cv[1] * f0.y, cv[2] * f0.z, cv[3] * f0.w,
+                                  cv[4] * f1.x, cv[5] * f1.y, cv[6] * f1.z, cv[7] * f1.w};
 #pragma unroll
                     for (int e = 0; e < 8; ++e) m[e] += (e == d) ? dei : 0.f;
                     const bf16x8_t bop = pack8(m);
@@ -478,14 +506,13 @@ __global__ __launch_bounds__(256, 2) void ssd2_scan_mfma(Ssd2Params p, const flo
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk) {
                     const int j0 = it * 32 + kk * 16 + 8 * half;
-                    const float4 c0 = dg[kk][0], c1 = dg[kk][1];
-                    const float cbv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+                    float cbv[8];
+                    cb_unpack(dg[kk], cbv);
                     float m[8];
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         const int j = j0 + e;
-                        const int tj = c * Q + j;
-                        const float dtj = tj < p.L ? dthead[(int64_t)tj * p.dt_sl] : 0.f;
+                        const float dtj = s_dt[j];  // 0 past seqlen
                         const float val = cbv[e] * dtj * __builtin_amdgcn_exp2f(cs2_i - s_cs2[j]);
                         m[e] = (j < il) ? val : ((j == il) ? val + Dh : 0.f);
                     }
@@ -624,7 +651,7 @@ bool ssd2_mfma_supported(const Ssd2Params& p) {
 
 // workspace: cbf (Q*Q f32) + cf (Q*N bf16) + bf (Q*N f32 or bf16) per (batch, chunk, group)
 static size_t cbf_bytes(const Ssd2Params& p) {
-    return align_up((size_t)p.nb * p.nch * p.G * p.Q * p.Q * sizeof(float), 256);
+    return align_up((size_t)p.nb * p.nch * p.G * p.Q * p.Q * sizeof(cb_t), 256);
 }
 static size_t frag_bytes(const Ssd2Params& p) {
     return align_up((size_t)p.nb * p.nch * p.G * p.N * p.Q * sizeof(bf16_t), 256);
@@ -648,7 +675,7 @@ static int choose_pt(const Ssd2Params& p) {
 
 template <int N, int Q>
 static int launch_q(const Ssd2Params& p, void* ws, hipStream_t stream, hipEvent_t ev0, hipEvent_t ev1) {
-    float* cbf = (float*)ws;
+    cb_t* cbf = (cb_t*)ws;
     bf16_t* cf = (bf16_t*)((char*)ws + cbf_bytes(p));
     void* bfr = (void*)((char*)ws + cbf_bytes(p) + frag_bytes(p));
     const int S = 4;  // prep workgroups per (batch, chunk, group)
@@ -658,10 +685,10 @@ static int launch_q(const Ssd2Params& p, void* ws, hipStream_t stream, hipEvent_
     if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, stream));
     if (choose_pt(p) == 2) {
         hipLaunchKernelGGL((ssd2_scan_mfma<N, Q, 2>), dim3(p.nb * p.H), dim3(256), 0, stream, p,
-                           (const float*)cbf, (const bf16_t*)cf, (const void*)bfr);
+                           (const cb_t*)cbf, (const bf16_t*)cf, (const void*)bfr);
     } else {
         hipLaunchKernelGGL((ssd2_scan_mfma<N, Q, 1>), dim3(p.nb * p.H * 2), dim3(256), 0, stream, p,
-                           (const float*)cbf, (const bf16_t*)cf, (const void*)bfr);
+                           (const cb_t*)cbf, (const bf16_t*)cf, (const void*)bfr);
     }
     MAMBA_CHECK_LAUNCH();
     if (ev1) MAMBA_CHECK_HIP(hipEventRecord(ev1, stream));

@@ -210,15 +210,16 @@ __global__ __launch_bounds__(256, 1) void ssd3_scan_mfma(Ssd3MfmaParams p) {
     // per-thread byte offsets within a chunk (the host bounds a chunk's span below 2^31 bytes)
     const uint32_t v_rs = (uint32_t)p.v_sf * 2, b_rs = (uint32_t)p.B_sf * 2, c_rs = (uint32_t)p.C_sf * 2;
     const uint32_t vo = (uint32_t)(threadIdx.x >> 2) * 2 * v_rs + (threadIdx.x & 3) * 16;
-    const uint32_t bo = (uint32_t)(threadIdx.x >> 4) * 2 * b_rs + (threadIdx.x & 15) * 16;
+    // B items: position pair fp = tid / 16 (+16 per k), 8-wide dstate piece nv
+    const int b_fp = threadIdx.x >> 4, b_nv = threadIdx.x & 15;
+    const uint32_t bo = (uint32_t)b_fp * 2 * b_rs + b_nv * 16;
     const uint32_t co = (uint32_t)(wave * 32 + r) * c_rs + 16 * half;
     const int tpos = threadIdx.x >> lgM;  // step of this thread's position within the chunk
     const uint32_t dao = (uint32_t)tpos * (uint32_t)p.da_sl * 4, sco = (uint32_t)tpos * (uint32_t)p.sc_sl * 4,
                    gmo = (uint32_t)tpos * (uint32_t)p.gm_sl * 4;
     const bool first_m = (threadIdx.x & ((1 << lgM) - 1)) == 0;
 
-    // ---- register prefetch of one chunk: v and B pieces for the LDS commit,
-    // this wave's C fragments (MFMA B operand of its output tile), tables
+    // ---- register prefetch of one chunk: v and B pieces for the LDS commit, tables
     static_assert(XPT == 1, "one v item per thread");
     uint4 xq[XPT][2], bq[BPT][2], cn[NK];
     float daq = 0.f, scq = 0.f, gmq = 0.f;
@@ -228,7 +229,6 @@ __global__ __launch_bounds__(256, 1) void ssd3_scan_mfma(Ssd3MfmaParams p) {
         const int64_t f0 = (int64_t)c * QF;
         const __amdgpu_buffer_rsrc_t rv = s3_rsrc(vhead + f0 * p.v_sf, (uint32_t)rows * v_rs);
         const __amdgpu_buffer_rsrc_t rb = s3_rsrc(bhead + f0 * p.B_sf, (uint32_t)rows * b_rs);
-        const __amdgpu_buffer_rsrc_t rc = s3_rsrc(chead + f0 * p.C_sf, (uint32_t)rows * c_rs);
         xq[0][0] = s3_bld16(rv, vo);
         xq[0][1] = s3_bld16(rv, vo + v_rs);
 #pragma unroll
@@ -236,8 +236,6 @@ __global__ __launch_bounds__(256, 1) void ssd3_scan_mfma(Ssd3MfmaParams p) {
             bq[k][0] = s3_bld16(rb, bo + (uint32_t)k * 32 * b_rs);
             bq[k][1] = s3_bld16(rb, bo + (uint32_t)k * 32 * b_rs + b_rs);
         }
-#pragma unroll
-        for (int kn = 0; kn < NK; ++kn) cn[kn] = s3_bld16(rc, co + 32 * kn);
         const int64_t t0 = f0 >> lgM;
         const __amdgpu_buffer_rsrc_t rda = s3_rsrc(dahead + t0 * p.da_sl, (uint32_t)steps * (uint32_t)p.da_sl * 4);
         const __amdgpu_buffer_rsrc_t rsc = s3_rsrc(schead + t0 * p.sc_sl, (uint32_t)steps * (uint32_t)p.sc_sl * 4);
@@ -247,7 +245,16 @@ __global__ __launch_bounds__(256, 1) void ssd3_scan_mfma(Ssd3MfmaParams p) {
         scq = s3_bld4(rsc, sco);
         gmq = s3_bld4(rgm, gmo);
     };
+    // this wave's C fragments of a chunk: issued a chunk ahead, after the
+    // current fragments are dead, so only one set is held in registers
+    auto fetch_c = [&](int c) {
+        const int rows = min(QF, p.L - c * QF);
+        const __amdgpu_buffer_rsrc_t rc = s3_rsrc(chead + (int64_t)c * QF * p.C_sf, (uint32_t)rows * c_rs);
+#pragma unroll
+        for (int kn = 0; kn < NK; ++kn) cn[kn] = s3_bld16(rc, co + 32 * kn);
+    };
     fetch(0);
+    fetch_c(0);
 
     for (int c = 0; c < p.nch; ++c) {
         const int cur = c & 1;
@@ -284,10 +291,9 @@ __global__ __launch_bounds__(256, 1) void ssd3_scan_mfma(Ssd3MfmaParams p) {
         // ---- commit B (row-major) to LDS
 #pragma unroll
         for (int k = 0; k < BPT; ++k) {
-            const int item = threadIdx.x + 256 * k;
-            const int fp = item >> 4, nv = item & 15;
-            *(uint4*)&S.B[2 * fp][nv * 8] = bq[k][0];
-            *(uint4*)&S.B[2 * fp + 1][nv * 8] = bq[k][1];
+            const int fp = b_fp + 16 * k;
+            *(uint4*)&S.B[2 * fp][b_nv * 8] = bq[k][0];
+            *(uint4*)&S.B[2 * fp + 1][b_nv * 8] = bq[k][1];
         }
         __syncthreads();  // w table ready
         // ---- commit v^T and w-scaled v^T
@@ -318,7 +324,7 @@ __global__ __launch_bounds__(256, 1) void ssd3_scan_mfma(Ssd3MfmaParams p) {
         if (c + 1 < p.nch) fetch(c + 1);
         __syncthreads();
         // ---- state: h <- exp(cs_end) h + sum_j (w_j v^T[p][j]) B[j][n], n tile = wave;
-        // the B operand is read column-wise from the row-major B tile
+        // the B operand is gathered column-wise from the row-major B tile
         {
             const float dec = __builtin_amdgcn_exp2f(cs_end);
 #pragma unroll
@@ -354,6 +360,7 @@ __global__ __launch_bounds__(256, 1) void ssd3_scan_mfma(Ssd3MfmaParams p) {
                 *(s3_bf16x4_t*)&S.y[wave][r][8 * gq + 4 * half] = q;
             }
             __builtin_amdgcn_wave_barrier();  // LDS ops of one wave complete in order
+            if (c + 1 < p.nch) fetch_c(c + 1);
             // 32 rows x 64 bytes: 4 lanes per row, 16 rows per instruction
             const int rows = min(QF, p.L - c * QF);
             const uint32_t y_rs = (uint32_t)p.y_sf * 2;
