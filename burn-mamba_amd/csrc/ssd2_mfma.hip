@@ -661,16 +661,36 @@ size_t ssd2_mfma_workspace(const Ssd2Params& p) {
     return cbf_bytes(p) + (MAMBA_SSD2_B_F32 ? 3 : 2) * frag_bytes(p);
 }
 
-// Headdim split: 2 workgroups per (batch, head) doubles the workgroup count
-// (better balance over 256 CUs) at the price of re-building the decay matrix
-// in both halves.  The environment variable MAMBA_SSD2_PSPLIT=0/1 (read on
-// every call) overrides the heuristic.
+// Headdim split.  PT = 2: one workgroup per (batch, head); PT = 1: two (one
+// per 32-wide headdim half).  Every workgroup walks the whole sequence, so the
+// launch runs in ceil(workgroups / resident slots) rounds; the per-workgroup
+// time barely depends on PT (the C.B^T decay work per chunk is the same),
+// measured at 0.94x for PT = 1 against PT = 2 at the 2.7B-layer shape.  The
+// choice minimises rounds x that relative time, with resident slots from the
+// runtime occupancy query.  MAMBA_SSD2_PSPLIT=0/1 (read on every call) forces it.
+template <int N, int Q>
 static int choose_pt(const Ssd2Params& p) {
     const char* e = getenv("MAMBA_SSD2_PSPLIT");
     const int forced = e ? atoi(e) : -1;
     if (forced == 0) return 2;
     if (forced == 1) return 1;
-    return (int64_t)p.nb * p.H < 320 ? 1 : 2;
+    static int slots1 = -1, slots2 = -1;  // resident workgroups on the device, per PT
+    if (slots1 < 0) {
+        int dev = 0, cus = 0, b1 = 0, b2 = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&b1, ssd2_scan_mfma<N, Q, 1>, 256, 0) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&b2, ssd2_scan_mfma<N, Q, 2>, 256, 0) != hipSuccess) {
+            (void)hipGetLastError();
+            return (int64_t)p.nb * p.H < 320 ? 1 : 2;
+        }
+        slots1 = (b1 > 0 ? b1 : 1) * cus;
+        slots2 = (b2 > 0 ? b2 : 1) * cus;
+    }
+    const int64_t items = (int64_t)p.nb * p.H;
+    const double cost1 = 0.94 * (double)((2 * items + slots1 - 1) / slots1);
+    const double cost2 = (double)((items + slots2 - 1) / slots2);
+    return cost1 <= cost2 ? 1 : 2;
 }
 
 template <int N, int Q>
@@ -683,7 +703,7 @@ static int launch_q(const Ssd2Params& p, void* ws, hipStream_t stream, hipEvent_
                        cf, bfr);
     MAMBA_CHECK_LAUNCH();
     if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, stream));
-    if (choose_pt(p) == 2) {
+    if (choose_pt<N, Q>(p) == 2) {
         hipLaunchKernelGGL((ssd2_scan_mfma<N, Q, 2>), dim3(p.nb * p.H), dim3(256), 0, stream, p,
                            (const cb_t*)cbf, (const bf16_t*)cf, (const void*)bfr);
     } else {
