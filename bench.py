@@ -178,6 +178,127 @@ def bench_mamba1(args):
     }
 
 
+MAMBA1_STEP_CFG = dict(n_layers=64, dim=5120, dstate=16, conv_kernel=4)
+
+
+def mamba1_step_algorithmic(cfg, batch):
+    """Compulsory HBM bytes of one decode token through the SSM part of
+    Mamba1::step (mamba1.rs:533-733) for every layer: conv window and state
+    read + written (f32), x in, conv out, delta, z in, y out (f32), B and C,
+    A, D, conv weight/bias.  Returns (all kernels, scan-step kernel) per step."""
+    L, d, n, k = cfg["n_layers"], cfg["dim"], cfg["dstate"], cfg["conv_kernel"]
+    conv = batch * d * k * 4 * 2 + batch * d * 4 * 2 + d * k * 4 + d * 4
+    scan = batch * d * n * 4 * 2 + batch * d * 4 * 4 + batch * n * 4 * 2 + d * n * 4 + d * 4
+    return L * (conv + scan), scan
+
+
+def bench_mamba1_step(args):
+    """64 layers of the Mamba-1 decode SSM step (conv window step + selective
+    scan step) at the 2.8B layer shape, captured in one HIP graph; every layer
+    owns its caches, so the states stream from HBM."""
+    import torch
+
+    import mamba_hip
+    cfg = dict(MAMBA1_STEP_CFG)
+    b = args.batch
+    L, d, n, k = cfg["n_layers"], cfg["dim"], cfg["dstate"], cfg["conv_kernel"]
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    A = -torch.arange(1, n + 1, device=dev, dtype=torch.float32).repeat(d, 1).contiguous()
+    D = torch.ones(d, device=dev)
+    conv_w = torch.randn((d, k), generator=g, device=dev) / k ** 0.5
+    conv_b = torch.randn(d, generator=g, device=dev) * 0.1
+    states = [torch.randn((b, d, n), generator=g, device=dev) * 0.1 for _ in range(L)]
+    convs = [torch.randn((b, d, k), generator=g, device=dev) for _ in range(L)]
+    x = torch.randn((b, d), generator=g, device=dev)
+    delta = torch.nn.functional.softplus(torch.randn((b, d), generator=g, device=dev) - 4.0)
+    z = torch.randn((b, d), generator=g, device=dev)
+    Bm = torch.randn((b, n), generator=g, device=dev)
+    Cm = torch.randn((b, n), generator=g, device=dev)
+    xc = torch.empty((b, d), device=dev)
+    y = torch.empty((b, d), device=dev)
+
+    def eager(events=None):
+        for i in range(L):
+            mamba_hip.conv1d_step(x, convs[i], conv_w, conv_b, silu=True, out=xc)
+            mamba_hip.scan_step(xc, delta, A, Bm, Cm, states[i], D=D, z=z, y=y,
+                                events=None if events is None else events[i])
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        eager()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        eager()
+    log(f"warmup {args.warmup}")
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} graph replays")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    pairs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(L)]
+             for _ in range(args.steps)]
+    for ev in pairs:
+        eager(ev)
+    torch.cuda.synchronize()
+    durs = [a.elapsed_time(b_) for ev in pairs for a, b_ in ev]
+    kern_ms = sum(durs) / len(durs)
+    log(f"ms/step {ms_per_step:.4f}, scan-step kernel {kern_ms * 1e3:.2f} us (mean of {len(durs)})")
+    step_bytes, kernel_bytes = mamba1_step_algorithmic(cfg, b)
+    achieved = kernel_bytes / (kern_ms * 1e-3) / 1e9
+    return {
+        "metric": f"Mamba-1 decode SSM step us at batch {b} (64 layers, D=5120 N=16 K=4, 1 GPU) + % HBM roofline",
+        "value": ms_per_step * 1e3, "unit": "us/step",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (config-2 shapes, states ~N(0,0.1), seed 0)",
+        "config": {"workload": "mamba1_decode_step", **cfg, "batch": b, "graph": "hip graph of the 64-layer step",
+                   "step_bytes": step_bytes, "step_hbm_gbs": step_bytes / (ms_per_step * 1e-3) / 1e9,
+                   "entry": "mamba_conv1d_step + mamba1_scan_step per layer"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel_ms": kern_ms,
+                     "algorithmic_bytes": kernel_bytes, "kernel": "mamba1_step_kernel (mean over all layers)"},
+    }
+
+
+def cpu_baseline_mamba1_step(cfg, batch, budget_s=10.0, seed=0):
+    """oracle.conv1d_step + oracle.mamba1_step (f32 restatement) per layer,
+    as many layers as fit in the budget, scaled to the 64-layer step."""
+    import numpy as np
+
+    import oracle
+    rng = np.random.default_rng(seed)
+    d, n, k = cfg["dim"], cfg["dstate"], cfg["conv_kernel"]
+    A = -np.tile(np.arange(1, n + 1, dtype=np.float32), (d, 1))
+    D = np.ones(d, np.float32)
+    w = (rng.standard_normal((d, k)) / k ** 0.5).astype(np.float32)
+    bias = (0.1 * rng.standard_normal(d)).astype(np.float32)
+    x = rng.standard_normal((batch, d)).astype(np.float32)
+    delta = np.log1p(np.exp(rng.standard_normal((batch, d)) - 4.0)).astype(np.float32)
+    z = rng.standard_normal((batch, d)).astype(np.float32)
+    Bm = rng.standard_normal((batch, n)).astype(np.float32)
+    Cm = rng.standard_normal((batch, n)).astype(np.float32)
+    st = (0.1 * rng.standard_normal((batch, d, n))).astype(np.float32)
+    cs = rng.standard_normal((batch, d, k)).astype(np.float32)
+    done, t0 = 0, time.perf_counter()
+    while done < cfg["n_layers"] and (done == 0 or time.perf_counter() - t0 < budget_s):
+        xc, cs = oracle.conv1d_step(x, cs, w, bias, silu=True, prec=32)
+        _, st = oracle.mamba1_step(xc, delta, A, Bm, Cm, st, D=D, z=z, prec=32)
+        done += 1
+    sec = (time.perf_counter() - t0) / done * cfg["n_layers"]
+    return {"value": sec * 1e6, "unit": "us/step", "cores": int(os.environ.get("OMP_NUM_THREADS", os.cpu_count())),
+            "kind": "port", "sample": f"{done} of {cfg['n_layers']} layers at batch {batch} ({sec * done / cfg['n_layers']:.1f} s), "
+                                      "scaled to 64 layers; f32 conv-step + scan-step restatement"}
+
+
 SSD3_CFG4 = dict(batch=4, seqlen=8192, mimo=4, nheads=32, headdim=64, dstate=128, ngroups=32, chunk=128)
 
 
@@ -541,7 +662,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="ssd2", choices=["ssd2", "mamba1", "decode", "ssd3"])
+    ap.add_argument("--workload", default="ssd2", choices=["ssd2", "mamba1", "decode", "ssd3", "mamba1_step"])
     ap.add_argument("--batch", type=int, default=DECODE_CFG3["batch"], help="decode batch")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -553,7 +674,10 @@ def main():
               "(the hot path shards by batch/head with no communication; see DESIGN.md)",
               file=sys.stderr)
         sys.exit(2)
-    if args.workload == "ssd3":
+    if args.workload == "mamba1_step":
+        out = bench_mamba1_step(args)
+        base = (lambda: cpu_baseline_mamba1_step(MAMBA1_STEP_CFG, args.batch))
+    elif args.workload == "ssd3":
         out = bench_ssd3(args)
         base = (lambda: cpu_baseline_ssd3(SSD3_CFG4))
     elif args.workload == "decode":

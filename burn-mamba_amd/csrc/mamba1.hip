@@ -67,7 +67,7 @@ __global__ __launch_bounds__(16 * N, N <= 16 ? 3 : 1) void mamba1_scan_kernel(Ma
     __shared__ __align__(16) float s_B[kTT][N];
     __shared__ __align__(16) float s_C[kTT][N];
 
-    const int tid = threadIdx.x, lane = tid & 63;
+    const int tid = threadIdx.x;
     const int nblk_d = (p.D + CPB - 1) / CPB;
     const int b = blockIdx.x / nblk_d, d0 = (blockIdx.x % nblk_d) * CPB;
     // compute mapping: channel c of this block, states 4*ng .. 4*ng+3

@@ -38,47 +38,68 @@ __device__ __forceinline__ float m1s_delta(const M1StepParams& p, int b, int d) 
     return p.softplus ? m1s_softplus(dv) : dv;
 }
 
-// grid (ceil(D / CPB), nb), 256 threads; LPC = N/4 lanes per channel.
-template <int N>
+// grid (ceil(D / (CPB CPT)), nb), 256 threads; LPC = N/4 lanes per channel,
+// CPB channels per round, CPT rounds per thread (all loads of the CPT rounds
+// are issued before any arithmetic, for memory-level parallelism).
+template <int N, int CPT>
 __global__ __launch_bounds__(256) void mamba1_step_kernel(M1StepParams p) {
     constexpr int LPC = N / 4;
     constexpr int CPB = 256 / LPC;
     const int b = blockIdx.y;
     const int t = threadIdx.x;
     const int q = t % LPC;
-    const int d_raw = blockIdx.x * CPB + t / LPC;
-    const bool live = d_raw < p.D;
-    const int d = live ? d_raw : p.D - 1;  // whole lane groups share d: shuffles stay inside a group
-    float4* hp = reinterpret_cast<float4*>(p.h + ((int64_t)b * p.D + d) * N) + q;
-    const float4 hv = *hp;
-    const float dv = m1s_delta(p, b, d);
-    const float uv = p.u[(int64_t)b * p.u_sb + d];
     const int n0 = 4 * q;
-    float a[4], bb[4], cc[4];
+    const int dbase = blockIdx.x * CPB * CPT + t / LPC;
+    // a lane group shares d (and so its live flag): shuffles stay inside a group
+    int dd[CPT];
+    bool live[CPT];
+    float4 hv[CPT], av[CPT];
+    float dv[CPT], uv[CPT];
+    const bool a_vec = p.A_sn == 1 && (p.A_sd & 3) == 0 && ((uintptr_t)p.A & 15u) == 0;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        a[k] = p.A[(int64_t)d * p.A_sd + (int64_t)(n0 + k) * p.A_sn];
-        bb[k] = p.Bm[(int64_t)b * p.B_sb + (int64_t)(n0 + k) * p.B_sn];
-        cc[k] = p.Cm[(int64_t)b * p.C_sb + (int64_t)(n0 + k) * p.C_sn];
-    }
-    // h <- h exp(delta A) + (delta B) u ; y partial = sum of this lane's h C
-    float4 hn;
-    hn.x = hv.x * __expf(dv * a[0]) + (dv * bb[0]) * uv;
-    hn.y = hv.y * __expf(dv * a[1]) + (dv * bb[1]) * uv;
-    hn.z = hv.z * __expf(dv * a[2]) + (dv * bb[2]) * uv;
-    hn.w = hv.w * __expf(dv * a[3]) + (dv * bb[3]) * uv;
-    float acc = hn.x * cc[0] + hn.y * cc[1] + hn.z * cc[2] + hn.w * cc[3];
-#pragma unroll
-    for (int o = 1; o < LPC; o <<= 1) acc += __shfl_xor(acc, o, 64);
-    if (!live) return;
-    *hp = hn;
-    if (q == 0) {
-        float out = acc + (p.Dv ? p.Dv[d] : 0.f) * uv;
-        if (p.z) {
-            const float zv = p.z[(int64_t)b * p.z_sb + d];
-            out *= zv / (1.f + __expf(-zv));
+    for (int k = 0; k < CPT; ++k) {
+        const int d_raw = dbase + k * CPB;
+        live[k] = d_raw < p.D;
+        dd[k] = live[k] ? d_raw : p.D - 1;
+        hv[k] = *(reinterpret_cast<const float4*>(p.h + ((int64_t)b * p.D + dd[k]) * N) + q);
+        if (a_vec) {
+            av[k] = *reinterpret_cast<const float4*>(p.A + (int64_t)dd[k] * p.A_sd + n0);
+        } else {
+            const float* ar = p.A + (int64_t)dd[k] * p.A_sd;
+            av[k] = make_float4(ar[(int64_t)n0 * p.A_sn], ar[(int64_t)(n0 + 1) * p.A_sn],
+                                ar[(int64_t)(n0 + 2) * p.A_sn], ar[(int64_t)(n0 + 3) * p.A_sn]);
         }
-        p.y[(int64_t)b * p.y_sb + d] = out;
+        dv[k] = m1s_delta(p, b, dd[k]);
+        uv[k] = p.u[(int64_t)b * p.u_sb + dd[k]];
+    }
+    float bb[4], cc[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        bb[e] = p.Bm[(int64_t)b * p.B_sb + (int64_t)(n0 + e) * p.B_sn];
+        cc[e] = p.Cm[(int64_t)b * p.C_sb + (int64_t)(n0 + e) * p.C_sn];
+    }
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+        // h <- h exp(delta A) + (delta B) u ; y partial = sum of this lane's h C
+        const float d_ = dv[k], u_ = uv[k];
+        float4 hn;
+        hn.x = hv[k].x * __expf(d_ * av[k].x) + (d_ * bb[0]) * u_;
+        hn.y = hv[k].y * __expf(d_ * av[k].y) + (d_ * bb[1]) * u_;
+        hn.z = hv[k].z * __expf(d_ * av[k].z) + (d_ * bb[2]) * u_;
+        hn.w = hv[k].w * __expf(d_ * av[k].w) + (d_ * bb[3]) * u_;
+        float acc = hn.x * cc[0] + hn.y * cc[1] + hn.z * cc[2] + hn.w * cc[3];
+#pragma unroll
+        for (int o = 1; o < LPC; o <<= 1) acc += __shfl_xor(acc, o, 64);
+        if (!live[k]) continue;
+        *(reinterpret_cast<float4*>(p.h + ((int64_t)b * p.D + dd[k]) * N) + q) = hn;
+        if (q == 0) {
+            float out = acc + (p.Dv ? p.Dv[dd[k]] : 0.f) * u_;
+            if (p.z) {
+                const float zv = p.z[(int64_t)b * p.z_sb + dd[k]];
+                out *= zv / (1.f + __expf(-zv));
+            }
+            p.y[(int64_t)b * p.y_sb + dd[k]] = out;
+        }
     }
 }
 
@@ -120,6 +141,7 @@ struct ConvStepParams {
     void* out; int64_t out_sb;
 };
 
+template <bool K4>
 __global__ __launch_bounds__(256) void conv1d_step_kernel(ConvStepParams p) {
     const int b = blockIdx.y;
     const int c = blockIdx.x * 256 + threadIdx.x;
@@ -129,13 +151,21 @@ __global__ __launch_bounds__(256) void conv1d_step_kernel(ConvStepParams p) {
     float* win = p.state + ((int64_t)b * p.C + c) * p.K;
     const float* w = p.w + (int64_t)c * p.K;
     float acc = 0.f;
-    for (int k = 0; k + 1 < p.K; ++k) {
-        const float v = win[k + 1];
-        win[k] = v;
-        acc += v * w[k];
+    if (K4) {  // one 16-byte window and weight row per channel
+        const float4 wv = *reinterpret_cast<const float4*>(win);
+        const float4 ww = *reinterpret_cast<const float4*>(w);
+        const float4 nw = make_float4(wv.y, wv.z, wv.w, xin);
+        *reinterpret_cast<float4*>(win) = nw;
+        acc = nw.x * ww.x + nw.y * ww.y + nw.z * ww.z + nw.w * ww.w;
+    } else {
+        for (int k = 0; k + 1 < p.K; ++k) {
+            const float v = win[k + 1];
+            win[k] = v;
+            acc += v * w[k];
+        }
+        win[p.K - 1] = xin;
+        acc += xin * w[p.K - 1];
     }
-    win[p.K - 1] = xin;
-    acc += xin * w[p.K - 1];
     if (p.bias) acc += p.bias[c];
     if (p.silu) acc = acc / (__expf(-acc) + 1.f);
     const int64_t oi = (int64_t)b * p.out_sb + c;
@@ -149,7 +179,7 @@ __global__ __launch_bounds__(256) void conv1d_step_kernel(ConvStepParams p) {
 
 using namespace mamba;
 
-extern "C" int mamba1_scan_step(const mamba1_step_args* a, mamba_stream_t stream) {
+static int m1_step_dispatch(const mamba1_step_args* a, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
     MAMBA_CHECK_ARG(a != nullptr, "args is NULL");
     MAMBA_CHECK_ARG(a->batch > 0 && a->dim > 0 && a->dstate > 0 && a->dstate <= 1024,
                     "batch, dim >= 1 and dstate in [1, 1024] required");
@@ -165,22 +195,37 @@ extern "C" int mamba1_scan_step(const mamba1_step_args* a, mamba_stream_t stream
     p.dbias = a->delta_bias; p.softplus = a->delta_softplus != 0;
     p.h = a->state; p.y = a->y; p.y_sb = a->y_sb;
     const bool aligned = ((uintptr_t)p.h & 15u) == 0;
-    hipStream_t s = (hipStream_t)stream;
+    constexpr int CPT = 4;
+    if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, s));
     switch (aligned ? p.N : 0) {
         case 16:
-            hipLaunchKernelGGL(mamba1_step_kernel<16>, dim3(ceil_div(p.D, 64), p.nb), dim3(256), 0, s, p);
+            hipLaunchKernelGGL((mamba1_step_kernel<16, CPT>), dim3(ceil_div(p.D, 64 * CPT), p.nb), dim3(256), 0, s, p);
             break;
         case 32:
-            hipLaunchKernelGGL(mamba1_step_kernel<32>, dim3(ceil_div(p.D, 32), p.nb), dim3(256), 0, s, p);
+            hipLaunchKernelGGL((mamba1_step_kernel<32, CPT>), dim3(ceil_div(p.D, 32 * CPT), p.nb), dim3(256), 0, s, p);
             break;
         case 64:
-            hipLaunchKernelGGL(mamba1_step_kernel<64>, dim3(ceil_div(p.D, 16), p.nb), dim3(256), 0, s, p);
+            hipLaunchKernelGGL((mamba1_step_kernel<64, CPT>), dim3(ceil_div(p.D, 16 * CPT), p.nb), dim3(256), 0, s, p);
             break;
         default:
             hipLaunchKernelGGL(mamba1_step_generic, dim3(ceil_div(p.D, 256), p.nb), dim3(256), 0, s, p);
     }
     MAMBA_CHECK_LAUNCH();
+    if (ev1) MAMBA_CHECK_HIP(hipEventRecord(ev1, s));
     return MAMBA_OK;
+}
+
+extern "C" int mamba1_scan_step(const mamba1_step_args* a, mamba_stream_t stream) {
+    return m1_step_dispatch(a, (hipStream_t)stream, nullptr, nullptr);
+}
+
+extern "C" int mamba1_scan_step_timed(const mamba1_step_args* a, mamba_stream_t stream, void* ev_start,
+                                      void* ev_stop) {
+    if (ev_start == nullptr || ev_stop == nullptr) {
+        set_error("mamba1_scan_step_timed: both events are required");
+        return MAMBA_ERR_INVALID_ARG;
+    }
+    return m1_step_dispatch(a, (hipStream_t)stream, (hipEvent_t)ev_start, (hipEvent_t)ev_stop);
 }
 
 extern "C" int mamba_conv1d_step(const mamba_conv1d_step_args* a, mamba_stream_t stream) {
@@ -195,7 +240,11 @@ extern "C" int mamba_conv1d_step(const mamba_conv1d_step_args* a, mamba_stream_t
     p.x_bf16 = a->x_dtype == MAMBA_BF16; p.out_bf16 = a->out_dtype == MAMBA_BF16; p.silu = a->silu != 0;
     p.x = a->x; p.x_sb = a->x_sb; p.state = a->state; p.w = a->w; p.bias = a->bias;
     p.out = a->out; p.out_sb = a->out_sb;
-    hipLaunchKernelGGL(conv1d_step_kernel, dim3(ceil_div(p.C, 256), p.nb), dim3(256), 0, (hipStream_t)stream, p);
+    const bool k4 = p.K == 4 && ((uintptr_t)p.state & 15u) == 0 && ((uintptr_t)p.w & 15u) == 0;
+    if (k4)
+        hipLaunchKernelGGL(conv1d_step_kernel<true>, dim3(ceil_div(p.C, 256), p.nb), dim3(256), 0, (hipStream_t)stream, p);
+    else
+        hipLaunchKernelGGL(conv1d_step_kernel<false>, dim3(ceil_div(p.C, 256), p.nb), dim3(256), 0, (hipStream_t)stream, p);
     MAMBA_CHECK_LAUNCH();
     return MAMBA_OK;
 }

@@ -166,6 +166,7 @@ _SIGNATURES = {
     "mamba1_scan_fwd": ([ctypes.POINTER(Mamba1ScanArgs), c_vp], ctypes.c_int),
     "mamba1_scan_fwd_timed": ([ctypes.POINTER(Mamba1ScanArgs), c_vp, c_vp, c_vp], ctypes.c_int),
     "mamba1_scan_step": ([ctypes.POINTER(Mamba1StepArgs), c_vp], ctypes.c_int),
+    "mamba1_scan_step_timed": ([ctypes.POINTER(Mamba1StepArgs), c_vp, c_vp, c_vp], ctypes.c_int),
     "mamba_conv1d_step": ([ctypes.POINTER(Conv1dStepArgs), c_vp], ctypes.c_int),
     "mamba2_step_workspace_size": ([ctypes.POINTER(Mamba2StepArgs)], ctypes.c_size_t),
     "mamba2_step_ssm": ([ctypes.POINTER(Mamba2StepArgs), c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),

@@ -89,9 +89,11 @@ def selective_scan(delta, a, b, c, d, u, init_ssm):
 # Recurrent decode step
 # --------------------------------------------------------------------------
 
-def scan_step(u, delta, A, B, C, state, D=None, z=None, delta_bias=None, delta_softplus=False, y=None):
+def scan_step(u, delta, A, B, C, state, D=None, z=None, delta_bias=None, delta_softplus=False, y=None,
+              events=None):
     """mamba1_scan_step: u, delta, z [b, d]; A [d, n]; B, C [b, n] (any strides);
-    state [b, d, n] contiguous f32, updated in place.  Returns y [b, d]."""
+    state [b, d, n] contiguous f32, updated in place.  Returns y [b, d].
+    ``events`` (start, stop) are recorded by the library around the kernel."""
     for t, nm in ((u, "u"), (delta, "delta"), (A, "A"), (B, "B"), (C, "C"), (D, "D"), (z, "z"),
                   (delta_bias, "delta_bias"), (state, "state")):
         _f32(t, nm)
@@ -120,7 +122,12 @@ def scan_step(u, delta, A, B, C, state, D=None, z=None, delta_bias=None, delta_s
     a.delta_softplus = int(bool(delta_softplus))
     a.state = state.data_ptr()
     a.y, a.y_sb = y.data_ptr(), y.stride(0)
-    check(_lib.lib().mamba1_scan_step(ctypes.byref(a), _stream(u.device)), "mamba1_scan_step")
+    if events is not None:
+        e0, e1 = _raw_events(events, u.device)
+        check(_lib.lib().mamba1_scan_step_timed(ctypes.byref(a), _stream(u.device), e0, e1),
+              "mamba1_scan_step_timed")
+    else:
+        check(_lib.lib().mamba1_scan_step(ctypes.byref(a), _stream(u.device)), "mamba1_scan_step")
     return y
 
 

@@ -236,6 +236,11 @@ typedef struct mamba1_step_args {
 } mamba1_step_args;
 
 int mamba1_scan_step(const mamba1_step_args* args, mamba_stream_t stream);
+/* As mamba1_scan_step, recording the caller's HIP events (already created)    */
+/* on `stream` immediately around the kernel, for benchmark timing.  No       */
+/* counterpart in the reference.                                              */
+int mamba1_scan_step_timed(const mamba1_step_args* args, mamba_stream_t stream, void* event_start,
+                           void* event_stop);
 
 /* ------------------------------------------------------------------------- */
 /* Depthwise causal conv, one step (the conv-window roll of Mamba1::step,      */
