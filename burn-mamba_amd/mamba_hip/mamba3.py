@@ -1,0 +1,210 @@
+"""Mamba-3 recurrent decode step, mirroring the reference's block signatures.
+
+Reference:
+  * ``Mamba3::step(input_bd, Option<cache>) -> (out_bd, cache)``: the double-SSD
+    step (src/mamba3/double_ssd/double_ssd/mod.rs:634-760), which single-SSD
+    decoding also uses (single_ssd/single_ssd/mod.rs:383-397).
+  * ``Mamba3DoubleSsdCache { ssm_bhpr, k_state_bmhr, v_state_bhp, rotation }``
+    (double_ssd/cache.rs:81-106) with the Complex2D ``RotationState::Angle``.
+  * ``Mamba3Config`` defaults and ``init`` (src/mamba3/mamba3.rs:355-780).
+
+in_proj / out_proj run through ``torch.mm`` (plain library GEMMs); everything
+between them is one ``mamba3_step_ssm`` call into libmamba_hip.so.  Nothing
+here computes on the CPU; a missing library raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import Mamba3StepArgs, check
+from .ssd import _dtype_code, _raw_events, _stream
+
+
+@dataclass
+class Mamba3Cache:
+    """ssm_bhpr [b, H, P, N], k_state_bmhr [b, M, H, N] (previous rotated B),
+    v_state_bhp [b, H, P] (previous x), angle_bha [b, H, A] (cumulative angle); f32."""
+    ssm_bhpr: torch.Tensor
+    k_state_bmhr: torch.Tensor
+    v_state_bhp: torch.Tensor
+    angle_bha: torch.Tensor
+
+
+@dataclass
+class Mamba3Config:
+    """Mamba3Config (src/mamba3/mamba3.rs:355-470) with the reference defaults
+    (Complex2D rotation only)."""
+    d_model: int
+    state_rank: int = 128
+    expand: int = 2
+    per_head_dim: int = 64
+    ngroups: int = 1
+    mimo_rank: int = 1
+    a_floor: float = 1e-4
+    dt_min: float = 1e-3
+    dt_max: float = 0.1
+    dt_init_floor: float = 1e-4
+    dt_limit: tuple = (0.0, 6.5504e4)
+    has_proj_bias: bool = False
+    rope_fraction: float = 1.0
+    has_outproj_norm: bool = False
+    rotation_range: float = 2.0
+
+    @property
+    def d_inner(self) -> int:
+        return self.expand * self.d_model
+
+    @property
+    def nheads(self) -> int:
+        return self.d_inner // self.per_head_dim
+
+    @property
+    def rope_dim(self) -> int:
+        """rope_dim (mamba3.rs:550-556): state_rank * rope_fraction rounded down to even."""
+        d = int(self.state_rank * self.rope_fraction)
+        return d - 1 if d % 2 else d
+
+    @property
+    def num_rope_angles(self) -> int:
+        return max(self.rope_dim // 2, 1)
+
+    @property
+    def d_in_proj(self) -> int:
+        """d_in_proj (mamba3.rs:600-605)."""
+        return (2 * self.d_inner + 2 * self.ngroups * self.state_rank * self.mimo_rank + 3 * self.nheads
+                + self.num_rope_angles)
+
+    def init(self, device, dtype=torch.float32, generator: Optional[torch.Generator] = None) -> "Mamba3":
+        """Mamba3Config::init (mamba3.rs:632-780): in/out_proj U(+-1/sqrt(fan_in)),
+        dt_bias = softplus^-1 of a log-uniform dt, D = 1, norm gammas = 1,
+        B/C biases = 1, mimo_x = mimo_o = 1/M, mimo_z = 1."""
+        H, M, N, P = self.nheads, self.mimo_rank, self.state_rank, self.per_head_dim
+
+        def uni(shape, bound):
+            return (torch.rand(shape, generator=generator, device=device) * 2 - 1) * bound
+
+        in_w = uni((self.d_model, self.d_in_proj), 1 / math.sqrt(self.d_model)).to(dtype)
+        out_w = uni((self.d_inner, self.d_model), 1 / math.sqrt(self.d_inner)).to(dtype)
+        u = torch.rand(H, generator=generator, device=device)
+        dt = torch.exp(u * (math.log(self.dt_max) - math.log(self.dt_min)) + math.log(self.dt_min))
+        dt = dt.clamp(min=self.dt_init_floor)
+        dt_bias = dt + torch.log(-torch.expm1(-dt))
+        ones = lambda *s: torch.ones(s, device=device)  # noqa: E731
+        mimo = (M > 1)
+        return Mamba3(
+            cfg=self, in_proj_w=in_w, out_proj_w=out_w,
+            in_proj_b=torch.zeros(self.d_in_proj, device=device) if self.has_proj_bias else None,
+            out_proj_b=torch.zeros(self.d_model, device=device) if self.has_proj_bias else None,
+            dt_bias=dt_bias.contiguous(), D=ones(H), b_norm_w=ones(N), c_norm_w=ones(N),
+            b_bias=ones(H, M, N), c_bias=ones(H, M, N),
+            mimo_x=torch.full((H, M, P), 1.0 / M, device=device) if mimo else None,
+            mimo_z=ones(H, M, P) if mimo else None,
+            mimo_o=torch.full((H, M, P), 1.0 / M, device=device) if mimo else None,
+            out_norm_w=ones(P) if self.has_outproj_norm else None)
+
+
+def _f32c(t, name):
+    if t is None:
+        return None
+    if t.dtype != torch.float32 or not t.is_contiguous():
+        raise _lib.MambaHipError(f"{name} must be a contiguous float32 tensor")
+    return t
+
+
+def step_ssm_args(cfg: Mamba3Config, proj: torch.Tensor, cache: Mamba3Cache, *, dt_bias, b_norm_w, c_norm_w,
+                  b_bias, c_bias, D=None, mimo_x=None, mimo_z=None, mimo_o=None, out_norm_w=None,
+                  out: torch.Tensor) -> Mamba3StepArgs:
+    """Fill mamba3_step_args for proj [b, d_in_proj] (f32 or bf16, unit inner stride)."""
+    b = proj.shape[0]
+    H, P, N, M, G = cfg.nheads, cfg.per_head_dim, cfg.state_rank, cfg.mimo_rank, cfg.ngroups
+    A = cfg.num_rope_angles
+    if proj.dim() != 2 or proj.shape[1] != cfg.d_in_proj or proj.stride(1) != 1:
+        raise _lib.MambaHipError(f"proj must be [b, {cfg.d_in_proj}] with a unit inner stride")
+    shapes = dict(ssm_bhpr=(b, H, P, N), k_state_bmhr=(b, M, H, N), v_state_bhp=(b, H, P), angle_bha=(b, H, A))
+    for name, shp in shapes.items():
+        t = _f32c(getattr(cache, name), name)
+        if tuple(t.shape) != shp:
+            raise _lib.MambaHipError(f"cache.{name} shape {tuple(t.shape)} != {shp}")
+    if out.stride(1) != 1 or tuple(out.shape) != (b, H * P):
+        raise _lib.MambaHipError("out must be [b, d_inner] with a unit inner stride")
+    a = Mamba3StepArgs()
+    a.batch, a.nheads, a.headdim, a.ngroups, a.dstate, a.mimo, a.rope_dim = b, H, P, G, N, M, cfg.rope_dim
+    a.proj_dtype, a.out_dtype = _dtype_code(proj), _dtype_code(out)
+    a.proj, a.proj_sb = proj.data_ptr(), proj.stride(0)
+    a.ssm_state, a.k_state = cache.ssm_bhpr.data_ptr(), cache.k_state_bmhr.data_ptr()
+    a.v_state, a.angle = cache.v_state_bhp.data_ptr(), cache.angle_bha.data_ptr()
+    a.dt_bias = _f32c(dt_bias, "dt_bias").data_ptr()
+    a.a_floor, a.dt_min, a.dt_max = cfg.a_floor, cfg.dt_limit[0], cfg.dt_limit[1]
+    a.rotation_range = cfg.rotation_range
+    a.b_norm_w, a.c_norm_w = _f32c(b_norm_w, "b_norm_w").data_ptr(), _f32c(c_norm_w, "c_norm_w").data_ptr()
+    a.b_bias, a.c_bias = _f32c(b_bias, "b_bias").data_ptr(), _f32c(c_bias, "c_bias").data_ptr()
+    for nm, t in (("mimo_x", mimo_x), ("mimo_z", mimo_z), ("mimo_o", mimo_o), ("D", D), ("out_norm_w", out_norm_w)):
+        setattr(a, nm, None if t is None else _f32c(t, nm).data_ptr())
+    a.out, a.out_sb = out.data_ptr(), out.stride(0)
+    return a
+
+
+def step_ssm(args: Mamba3StepArgs, device, events=None):
+    """One mamba3_step_ssm launch on the current stream (events: optional (start, stop))."""
+    L = _lib.lib()
+    st = _stream(device)
+    if events is not None:
+        e0, e1 = _raw_events(events, device)
+        check(L.mamba3_step_ssm_timed(ctypes.byref(args), st, e0, e1), "mamba3_step_ssm_timed")
+    else:
+        check(L.mamba3_step_ssm(ctypes.byref(args), st), "mamba3_step_ssm")
+
+
+@dataclass
+class Mamba3:
+    """One Mamba-3 block's parameters (Burn Linear layout [d_in, d_out])."""
+    cfg: Mamba3Config
+    in_proj_w: torch.Tensor
+    out_proj_w: torch.Tensor
+    in_proj_b: Optional[torch.Tensor]
+    out_proj_b: Optional[torch.Tensor]
+    dt_bias: torch.Tensor
+    D: torch.Tensor
+    b_norm_w: torch.Tensor
+    c_norm_w: torch.Tensor
+    b_bias: torch.Tensor
+    c_bias: torch.Tensor
+    mimo_x: Optional[torch.Tensor] = None
+    mimo_z: Optional[torch.Tensor] = None
+    mimo_o: Optional[torch.Tensor] = None
+    out_norm_w: Optional[torch.Tensor] = None
+
+    def new_cache(self, batch: int) -> Mamba3Cache:
+        """The reference's fresh cache: zero state, K, v_state and angle
+        (double_ssd/double_ssd/mod.rs:649-669)."""
+        c, dev = self.cfg, self.in_proj_w.device
+        z = lambda *s: torch.zeros(s, device=dev)  # noqa: E731
+        return Mamba3Cache(z(batch, c.nheads, c.per_head_dim, c.state_rank),
+                           z(batch, c.mimo_rank, c.nheads, c.state_rank),
+                           z(batch, c.nheads, c.per_head_dim), z(batch, c.nheads, c.num_rope_angles))
+
+    def step(self, x: torch.Tensor, cache: Optional[Mamba3Cache] = None, events=None):
+        """Mamba3::step: x [b, d_model] -> (out [b, d_model], cache updated in place)."""
+        if cache is None:
+            cache = self.new_cache(x.shape[0])
+        wdt = self.in_proj_w.dtype
+        proj = torch.mm(x.to(wdt), self.in_proj_w)
+        if self.in_proj_b is not None:
+            proj = proj + self.in_proj_b.to(wdt)
+        y = torch.empty((x.shape[0], self.cfg.d_inner), dtype=wdt, device=x.device)
+        args = step_ssm_args(self.cfg, proj, cache, dt_bias=self.dt_bias, b_norm_w=self.b_norm_w,
+                             c_norm_w=self.c_norm_w, b_bias=self.b_bias, c_bias=self.c_bias, D=self.D,
+                             mimo_x=self.mimo_x, mimo_z=self.mimo_z, mimo_o=self.mimo_o,
+                             out_norm_w=self.out_norm_w, out=y)
+        step_ssm(args, x.device, events)
+        out = torch.mm(y, self.out_proj_w)
+        if self.out_proj_b is not None:
+            out = out + self.out_proj_b.to(wdt)
+        return out.to(x.dtype), cache

@@ -24,6 +24,8 @@
  *                          plus the silu(z) gate of Mamba1::forward (mamba1.rs:348)
  *   mamba1_scan_step    <- Mamba1::selective_scan_step (src/mamba1/mamba1.rs:666-733)
  *   mamba_conv1d_step   <- the conv-window step of Mamba1::step (src/mamba1/mamba1.rs:558-597)
+ *   mamba3_step_ssm     <- Mamba3::step between in_proj and out_proj
+ *                          (src/mamba3/double_ssd/double_ssd/mod.rs:634-760)
  *   mamba2_step_ssm     <- the body of Mamba2::step between in_proj and out_proj
  *                          (src/mamba2/mamba2.rs:857-995)
  *   mamba_linear_fwd    <- burn::nn::Linear::forward in the decode steps (packed weights)
@@ -261,6 +263,49 @@ typedef struct mamba_conv1d_step_args {
 } mamba_conv1d_step_args;
 
 int mamba_conv1d_step(const mamba_conv1d_step_args* args, mamba_stream_t stream);
+
+/* ------------------------------------------------------------------------- */
+/* Mamba-3 decode step: everything of Mamba3::step between in_proj and         */
+/* out_proj, per token (Complex2D rotation).  Replaces Mamba3::step_double_ssd */
+/* (src/mamba3/double_ssd/double_ssd/mod.rs:634-760; single-SSD decoding uses  */
+/* the same step, single_ssd/single_ssd/mod.rs:383-397) from the split of the  */
+/* in_proj row to the MIMO merge: trapezoid coefficients (helpers.rs:42-73),   */
+/* QK-norm + GQA + bias (helpers.rs:82-95), the cumulative-angle RoPE of B/C   */
+/* (rotation/mod.rs:729-763, rope.rs:23-170), the state update                 */
+/*   h = alpha h + sum_m gamma (x mimo_x[m]) (x) B[m] + sum_m beta (x_prev mimo_x[m]) (x) K[m] */
+/* the readout sum_n C h + D v, and step_finish's gate / gated RMSNorm and     */
+/* mimo_o merge (mod.rs:556-628).  The in_proj row is                          */
+/*   [z (H P) | x (H P) | b_raw (M, G, N) | c_raw (M, G, N) | dd_dt (H) |      */
+/*    dd_a (H) | lambda (H) | rot (A)],  A = max(rope_dim / 2, 1).             */
+/* The four cache tensors (Mamba3DoubleSsdCache / Mamba3SingleSsdCache,        */
+/* double_ssd/cache.rs:81-106) are updated in place: ssm, k_state = the        */
+/* rotated B, v_state = x, angle = the wrapped cumulative angle.               */
+/* dstate in {8, 16, 32, 64, 128, 256}, headdim * dstate <= 8192,              */
+/* mimo in {1, 2, 4, 8}.                                                       */
+/* ------------------------------------------------------------------------- */
+typedef struct mamba3_step_args {
+    int32_t batch, nheads, headdim, ngroups, dstate, mimo, rope_dim;
+    int32_t proj_dtype, out_dtype;
+    const void* proj;   int64_t proj_sb;             /* [b, row] in_proj output   */
+    float* ssm_state;                                /* [b, H, P, N] in/out       */
+    float* k_state;                                  /* [b, M, H, N] in/out       */
+    float* v_state;                                  /* [b, H, P]    in/out       */
+    float* angle;                                    /* [b, H, A]    in/out       */
+    const float* dt_bias;                            /* [H]                       */
+    float a_floor, dt_min, dt_max, rotation_range;
+    const float* b_norm_w; const float* c_norm_w;    /* [N] QK-norm gammas        */
+    const float* b_bias;   const float* c_bias;      /* [H, M, N]                 */
+    const float* mimo_x; const float* mimo_z; const float* mimo_o; /* [H, M, P]; NULL if mimo == 1 */
+    const float* D;                                  /* [H] or NULL               */
+    const float* out_norm_w;                         /* [P] or NULL: gated RMSNorm instead of the silu gate */
+    void* out;          int64_t out_sb;              /* [b, H P] (before out_proj) */
+} mamba3_step_args;
+
+int mamba3_step_ssm(const mamba3_step_args* args, mamba_stream_t stream);
+/* As mamba3_step_ssm, recording the caller's HIP events around the kernel     */
+/* (benchmark timing; no counterpart in the reference).                        */
+int mamba3_step_ssm_timed(const mamba3_step_args* args, mamba_stream_t stream, void* event_start,
+                          void* event_stop);
 
 /* ------------------------------------------------------------------------- */
 /* Mamba-2 recurrent decode step: everything of Mamba2::step between in_proj  */

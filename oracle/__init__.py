@@ -220,3 +220,77 @@ def ssd3(v, da, B, C, gamma, scale, h0=None, chunk=64, form="serial", prec=64):
     return y, hT
 
 
+# --------------------------------------------------------------------------
+# Mamba-3 block step (src/mamba3/double_ssd/double_ssd/mod.rs:407-760)
+# --------------------------------------------------------------------------
+
+def mamba3_num_angles(rope_dim):
+    """num_rope_angles (mamba3.rs:565-567): max(rope_dim / 2, 1)."""
+    return max(rope_dim // 2, 1)
+
+
+def mamba3_step_prep(proj, p, angle, prec=64):
+    """step_project + rotate_bc_step (Complex2D) for one token.
+
+    proj [b, 2 d_inner + 2 M G N + 3 H + A]; p: dict of heads/headdim/ngroups/dstate/
+    mimo/rope_dim, dt_bias[H], a_floor, dt_limit, rotation_range, b_norm_w/c_norm_w[N],
+    b_bias/c_bias[H, M, N]; angle [b, H, A] (not modified).
+    Returns dict(B, C [b, M, H, N], dt, alpha, beta, gamma [b, H], angle [b, H, A])."""
+    H, P, G, N, M, R = (p[k] for k in ("nheads", "headdim", "ngroups", "dstate", "mimo", "rope_dim"))
+    proj = _f32(proj)
+    b = proj.shape[0]
+    ang = np.array(angle, dtype=np.float32, copy=True)
+    Bo = np.zeros((b, M, H, N), np.float32)
+    Co = np.zeros((b, M, H, N), np.float32)
+    dt, al, be, ga = (np.zeros((b, H), np.float32) for _ in range(4))
+    lo, hi = p.get("dt_limit", (0.0, 65504.0))
+    _fn("mamba3_step_prep", prec)(b, H, P, G, N, M, R, _ptr(proj), _ptr(_f32(p["dt_bias"])),
+                                  ctypes.c_float(p.get("a_floor", 1e-4)), ctypes.c_float(lo), ctypes.c_float(hi),
+                                  ctypes.c_float(p.get("rotation_range", 2.0)), _ptr(_f32(p["b_norm_w"])),
+                                  _ptr(_f32(p["c_norm_w"])), _ptr(_f32(p["b_bias"])), _ptr(_f32(p["c_bias"])),
+                                  _ptr(ang), _ptr(Bo), _ptr(Co), _ptr(dt), _ptr(al), _ptr(be), _ptr(ga))
+    return dict(B=Bo, C=Co, dt=dt, alpha=al, beta=be, gamma=ga, angle=ang)
+
+
+def mamba3_step_core(x, v_state, B, K, C, alpha, beta, gamma, state, mimo_x=None, D=None, prec=64):
+    """The token state update + readout: x, v_state [b, H, P]; B, K, C [b, M, H, N];
+    alpha/beta/gamma [b, H]; state [b, H, P, N]; mimo_x [H, M, P] or None (M == 1).
+    Returns (out [b, M, H, P] with the D skip, new state)."""
+    x, v_state, B, K, C, alpha, beta, gamma, mimo_x, D = map(
+        _f32, (x, v_state, B, K, C, alpha, beta, gamma, mimo_x, D))
+    st = np.array(state, dtype=np.float32, copy=True)
+    b, H, P, N = st.shape
+    M = B.shape[1]
+    out = np.zeros((b, M, H, P), np.float32)
+    _fn("mamba3_step_core", prec)(b, H, P, N, M, _ptr(x), _ptr(v_state), _ptr(B), _ptr(K), _ptr(C),
+                                  _ptr(alpha), _ptr(beta), _ptr(gamma), _ptr(mimo_x), _ptr(D), _ptr(st),
+                                  _ptr(out))
+    return out, st
+
+
+def mamba3_step_finish(out, z, mimo_z=None, mimo_o=None, norm_w=None, prec=64):
+    """step_finish before out_proj: out [b, M, H, P]; z [b, H*P] -> y [b, H*P]."""
+    out, z, mimo_z, mimo_o, norm_w = map(_f32, (out, z, mimo_z, mimo_o, norm_w))
+    b, M, H, P = out.shape
+    y = np.zeros((b, H * P), np.float32)
+    _fn("mamba3_step_finish", prec)(b, H, P, M, _ptr(out), _ptr(z), _ptr(mimo_z), _ptr(mimo_o),
+                                    _ptr(norm_w), _ptr(y))
+    return y
+
+
+def mamba3_step(proj, p, cache, prec=64):
+    """Mamba3::step between in_proj and out_proj (double_ssd/double_ssd/mod.rs:634-760).
+    cache: dict(ssm [b,H,P,N], k_state [b,M,H,N], v_state [b,H,P], angle [b,H,A]).
+    Returns (y [b, H*P], new cache); the new k_state is the rotated B, v_state the raw x."""
+    H, P = p["nheads"], p["headdim"]
+    proj = _f32(proj)
+    b = proj.shape[0]
+    d_inner = H * P
+    z = proj[:, :d_inner]
+    x = proj[:, d_inner:2 * d_inner].reshape(b, H, P)
+    pr = mamba3_step_prep(proj, p, cache["angle"], prec)
+    out, st = mamba3_step_core(x, cache["v_state"], pr["B"], cache["k_state"], pr["C"], pr["alpha"],
+                               pr["beta"], pr["gamma"], cache["ssm"], p.get("mimo_x"), p.get("D"), prec)
+    y = mamba3_step_finish(out, z, p.get("mimo_z"), p.get("mimo_o"), p.get("out_norm_w"), prec)
+    return y, dict(ssm=st, k_state=pr["B"], v_state=np.ascontiguousarray(x), angle=pr["angle"])
+

@@ -620,6 +620,187 @@ void F(ssd3_recurrent)(int batch, int seqlen, int mimo, int nheads, int headdim,
         }
 }
 
+/* ------------------------------------------------------------------------- */
+/* Mamba-3 per-token prep — Mamba3::step_project (src/mamba3/double_ssd/      */
+/* double_ssd/mod.rs:407-496) and rotate_bc_step for Complex2D                 */
+/* (src/mamba3/rotation/mod.rs:729-763).  The in_proj row splits as           */
+/* [z | x | b_raw (M,G,N) | c_raw (M,G,N) | dd_dt (H) | dd_a (H) | lambda (H) | */
+/*  rot (A)] (:430-447), A = max(rope_dim/2, 1) angles (mamba3.rs:565-567).   */
+/* trapezoidal_coefficients (helpers.rs:42-73):                               */
+/*   dt = clamp(softplus(dd_dt + dt_bias)), a = -max(softplus(dd_a), a_floor), */
+/*   alpha = exp(dt a), beta = (1 - sigmoid(lambda)) dt alpha,                */
+/*   gamma = sigmoid(lambda) dt.                                              */
+/* qk_norm_expand_bias (helpers.rs:82-95): RmsNorm over N, group h/(H/G),     */
+/* + bias[h,m,n].  angle_increment (rotation/mod.rs:559-567):                 */
+/*   angle[b,h,a] = wrap(angle + dt range pi tanh(rot[a])), wrap_angle        */
+/* (rope.rs:23-27) subtracting round(x / 2pi) 2pi; apply_rope_partial         */
+/* (rope.rs:118-170): pairs (2a, 2a+1) when M == 1, (a, a + N/2) otherwise,   */
+/* for a < rope_dim/2; rope_dim == 0 rotates nothing.                          */
+/*   proj[b, *]; angle[b,H,A] in/out; Bo, Co[b,M,H,N]; dt/alpha/beta/gamma[b,H] */
+/* ------------------------------------------------------------------------- */
+static inline REAL F(wrap_)(REAL a) {
+    const REAL two_pi = (REAL)(2.0f * 3.14159265358979323846f);
+    const REAL k = (REAL)nearbyint((double)(a * ((REAL)1 / two_pi)));
+    return a - k * two_pi;
+}
+
+void F(mamba3_step_prep)(int batch, int nheads, int headdim, int ngroups, int dstate, int mimo,
+                         int rope_dim, const float* proj, const float* dt_bias, float a_floor,
+                         float dt_lo, float dt_hi, float rot_range, const float* b_norm_w,
+                         const float* c_norm_w, const float* b_bias, const float* c_bias,
+                         float* angle, float* Bo, float* Co, float* dt_o, float* alpha_o,
+                         float* beta_o, float* gamma_o) {
+    const int H = nheads, P = headdim, G = ngroups, N = dstate, M = mimo, hpg = H / G;
+    const int A = rope_dim / 2 > 1 ? rope_dim / 2 : 1;
+    const int d_inner = H * P, bc = M * G * N;
+    const size_t row_len = (size_t)2 * d_inner + 2 * bc + 3 * H + A;
+    const REAL span = (REAL)((double)rot_range * 3.14159265358979323846);  /* range * pi */
+    for (int b = 0; b < batch; ++b) {
+        const float* row = proj + (size_t)b * row_len;
+        const float* braw = row + 2 * d_inner;
+        const float* craw = braw + bc;
+        const float* dd_dt = craw + bc;
+        const float* dd_a = dd_dt + H;
+        const float* lam = dd_a + H;
+        const float* rot = lam + H;
+        for (int h = 0; h < H; ++h) {
+            REAL dt = F(softplus_)((REAL)dd_dt[h] + (REAL)dt_bias[h]);
+            if (dt < (REAL)dt_lo) dt = (REAL)dt_lo;
+            if (dt > (REAL)dt_hi) dt = (REAL)dt_hi;
+            REAL sa = F(softplus_)((REAL)dd_a[h]);
+            if (sa < (REAL)a_floor) sa = (REAL)a_floor;
+            const REAL a = -sa;
+            const REAL l = (REAL)1 / ((REAL)1 + F(exp_)(-(REAL)lam[h]));
+            const REAL al = F(exp_)(dt * a);
+            const size_t bh = (size_t)b * H + h;
+            dt_o[bh] = (float)dt;
+            alpha_o[bh] = (float)al;
+            beta_o[bh] = (float)(((REAL)1 - l) * dt * al);
+            gamma_o[bh] = (float)(l * dt);
+            /* cumulative angle of this head */
+            float* ang = angle + bh * A;
+            for (int k = 0; k < A; ++k) {
+                const REAL inc = dt * ((REAL)tanh((double)rot[k]) * span);
+                ang[k] = (float)F(wrap_)((REAL)ang[k] + inc);
+            }
+            const int g = h / hpg;
+            for (int m = 0; m < M; ++m)
+                for (int which = 0; which < 2; ++which) {
+                    const float* src = (which ? craw : braw) + ((size_t)m * G + g) * N;
+                    const float* nw = which ? c_norm_w : b_norm_w;
+                    const float* bias = (which ? c_bias : b_bias) + ((size_t)h * M + m) * N;
+                    float* dst = (which ? Co : Bo) + (((size_t)b * M + m) * H + h) * N;
+                    REAL ssq = 0;
+                    for (int n = 0; n < N; ++n) ssq += (REAL)src[n] * (REAL)src[n];
+                    const REAL rms = (REAL)sqrt((double)(ssq / (REAL)N + F(div_eps_)()));
+                    REAL* tmp = (REAL*)malloc(sizeof(REAL) * N);
+                    for (int n = 0; n < N; ++n) tmp[n] = ((REAL)src[n] / rms) * (REAL)nw[n] + (REAL)bias[n];
+                    if (rope_dim > 0)
+                        for (int k = 0; k < rope_dim / 2; ++k) {
+                            const int i0 = M == 1 ? 2 * k : k, i1 = M == 1 ? 2 * k + 1 : k + N / 2;
+                            const REAL th = F(wrap_)((REAL)ang[k]);
+                            const REAL cs = (REAL)cos((double)th), sn = (REAL)sin((double)th);
+                            const REAL x0 = tmp[i0], x1 = tmp[i1];
+                            tmp[i0] = cs * x0 - sn * x1;
+                            tmp[i1] = sn * x0 + cs * x1;
+                        }
+                    for (int n = 0; n < N; ++n) dst[n] = (float)tmp[n];
+                    free(tmp);
+                }
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------- */
+/* Mamba-3 token state update + readout — Mamba3::step_double_ssd             */
+/* (src/mamba3/double_ssd/double_ssd/mod.rs:699-733), build_v_with_mimo       */
+/* (helpers.rs:152-168), mimo_outer_sum (:113-140), step_readout (mod.rs:516-  */
+/* 550) and the D skip of step_finish (:565-573):                             */
+/*   v[m,p] = x[p] mimo_x[h,m,p]      xs[m,p] = v_state[p] mimo_x[h,m,p]      */
+/*   h      = alpha h + sum_m gamma v[m] (x) B[m] + sum_m beta xs[m] (x) K[m]  */
+/*   out    = sum_n C[m,n] h[p,n] + D v[m,p]                                  */
+/* mimo_x NULL means M == 1 with v = x.  x, v_state[b,H,P]; B, K, C[b,M,H,N];  */
+/* alpha/beta/gamma[b,H]; state[b,H,P,N] in/out; out[b,M,H,P].                */
+/* ------------------------------------------------------------------------- */
+void F(mamba3_step_core)(int batch, int nheads, int headdim, int dstate, int mimo, const float* x,
+                         const float* v_state, const float* Bm, const float* K, const float* Cm,
+                         const float* alpha, const float* beta, const float* gamma,
+                         const float* mimo_x, const float* D, float* state, float* out) {
+    const int H = nheads, P = headdim, N = dstate, M = mimo;
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int b = 0; b < batch; ++b)
+        for (int h = 0; h < H; ++h) {
+            const size_t bh = (size_t)b * H + h;
+            const REAL al = alpha[bh], be = beta[bh], ga = gamma[bh];
+            REAL* v = (REAL*)malloc(sizeof(REAL) * M * P);
+            REAL* xs = (REAL*)malloc(sizeof(REAL) * M * P);
+            for (int m = 0; m < M; ++m)
+                for (int p = 0; p < P; ++p) {
+                    const REAL mx = mimo_x ? (REAL)mimo_x[((size_t)h * M + m) * P + p] : (REAL)1;
+                    v[m * P + p] = (REAL)x[bh * P + p] * mx;
+                    xs[m * P + p] = (REAL)v_state[bh * P + p] * mx;
+                }
+            for (int p = 0; p < P; ++p) {
+                float* sp = state + (bh * P + p) * N;
+                for (int n = 0; n < N; ++n) {
+                    REAL acc = al * (REAL)sp[n];
+                    for (int m = 0; m < M; ++m) {
+                        const size_t bi = (((size_t)b * M + m) * H + h) * N + n;
+                        acc += (ga * v[m * P + p]) * (REAL)Bm[bi] + (be * xs[m * P + p]) * (REAL)K[bi];
+                    }
+                    sp[n] = (float)acc;
+                }
+                for (int m = 0; m < M; ++m) {
+                    const float* cr = Cm + (((size_t)b * M + m) * H + h) * N;
+                    REAL acc = 0;
+                    for (int n = 0; n < N; ++n) acc += (REAL)cr[n] * (REAL)sp[n];
+                    out[(((size_t)b * M + m) * H + h) * P + p] =
+                        (float)(acc + (D ? (REAL)D[h] : (REAL)0) * v[m * P + p]);
+                }
+            }
+            free(v);
+            free(xs);
+        }
+}
+
+/* ------------------------------------------------------------------------- */
+/* Mamba-3 step_finish without out_proj (double_ssd/double_ssd/mod.rs:556-628):*/
+/*   M > 1: y[p] = sum_m mimo_o[h,m,p] G(out[m,p], z[p] mimo_z[h,m,p])         */
+/*   M = 1: y[p] = G(out[0,p], z[p])                                          */
+/* G(y, z) = y silu(z), or with norm_w (has_outproj_norm, RmsNormGated with   */
+/* norm_before_gate = true over the P entries of one (m, head), mamba3.rs:744- */
+/* 748, rms_norm_gated.rs:70-135): y / sqrt(mean_p(y^2) + eps) w[p] silu(z).  */
+/* out[b,M,H,P]; z[b,H*P]; y[b,H*P].                                          */
+/* ------------------------------------------------------------------------- */
+void F(mamba3_step_finish)(int batch, int nheads, int headdim, int mimo, const float* out,
+                           const float* z, const float* mimo_z, const float* mimo_o,
+                           const float* norm_w, float* y) {
+    const int H = nheads, P = headdim, M = mimo;
+    for (int b = 0; b < batch; ++b)
+        for (int h = 0; h < H; ++h) {
+            REAL* acc = (REAL*)calloc(P, sizeof(REAL));
+            for (int m = 0; m < M; ++m) {
+                const float* o = out + (((size_t)b * M + m) * H + h) * P;
+                REAL rms = 1;
+                if (norm_w) {
+                    REAL ssq = 0;
+                    for (int p = 0; p < P; ++p) ssq += (REAL)o[p] * (REAL)o[p];
+                    rms = (REAL)sqrt((double)(ssq / (REAL)P + F(div_eps_)()));
+                }
+                for (int p = 0; p < P; ++p) {
+                    REAL zv = (REAL)z[((size_t)b * H + h) * P + p];
+                    if (M > 1) zv *= (REAL)mimo_z[((size_t)h * M + m) * P + p];
+                    REAL gv = norm_w ? ((REAL)o[p] / rms) * (REAL)norm_w[p] * F(silu_)(zv)
+                                     : (REAL)o[p] * F(silu_)(zv);
+                    if (M > 1) gv *= (REAL)mimo_o[((size_t)h * M + m) * P + p];
+                    acc[p] += gv;
+                }
+            }
+            for (int p = 0; p < P; ++p) y[((size_t)b * H + h) * P + p] = (float)acc[p];
+            free(acc);
+        }
+}
+
 #undef F
 #undef CAT
 #undef CAT2

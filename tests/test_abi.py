@@ -55,6 +55,7 @@ int main(void) {{ printf("%zu\\n", sizeof({struct_name})); {body} return 0; }}
                                              ("Mamba1StepArgs", "mamba1_step_args"),
                                              ("Conv1dStepArgs", "mamba_conv1d_step_args"),
                                              ("Mamba2StepArgs", "mamba2_step_args"),
+                                             ("Mamba3StepArgs", "mamba3_step_args"),
                                              ("LinearArgs", "mamba_linear_args"),
                                              ("Mamba2LayerArgs", "mamba2_layer_args"),
                                              ("RmsNormArgs", "mamba_rmsnorm_args")])

@@ -335,3 +335,149 @@ def test_conv1d_step_unroll_equals_convolution():
                 ref = v / (1 + np.exp(-v)) if t % 2 == 0 else v
                 np.testing.assert_allclose(out[bi, ci], ref, rtol=1e-5, atol=1e-6)
     np.testing.assert_array_equal(st[:, :, -1], xs[-1])
+
+
+# ------------------------------------------------------------- Mamba-3 step --
+
+def _mamba3_seq(seed, b, L, M, H, P, N):
+    rng = np.random.default_rng(seed)
+    dt = rng.uniform(0.01, 0.3, (b, L, H))
+    A = -rng.uniform(0.5, 2.0, H)
+    lam = 1.0 / (1.0 + np.exp(-rng.standard_normal((b, L, H))))
+    da = dt * A
+    alpha, beta, gamma = np.exp(da), (1 - lam) * dt * np.exp(da), lam * dt
+    x = rng.standard_normal((b, L, H, P)).astype(np.float32)
+    B = (rng.standard_normal((b, L, M, H, N)) / np.sqrt(N)).astype(np.float32)
+    C = (rng.standard_normal((b, L, M, H, N)) / np.sqrt(N)).astype(np.float32)
+    mimo_x = None if M == 1 else rng.standard_normal((H, M, P)).astype(np.float32)
+    D = rng.standard_normal(H).astype(np.float32)
+    return dict(dt=dt, lam=lam, da=da, alpha=alpha, beta=beta, gamma=gamma, x=x, B=B, C=C, mimo_x=mimo_x, D=D)
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_mamba3_step_core_unroll_equals_chunked_ssd3(M):
+    """Token steps from an empty cache (double-SSD recurrence, the beta term
+    built from the previous token's B and x) equal the pinned chunked
+    single-SSD forward with scale_t = gamma_t + (1 - lambda_{t+1}) dt_{t+1}
+    (single_ssd/single_ssd/mod.rs:129-150), plus the D skip on v."""
+    b, L, H, P, N = 2, 13, 2, 8, 8
+    d = _mamba3_seq(3 + M, b, L, M, H, P, N)
+    st = np.zeros((b, H, P, N), np.float32)
+    K = np.zeros((b, M, H, N), np.float32)
+    vs = np.zeros((b, H, P), np.float32)
+    outs = []
+    for t in range(L):
+        o, st = oracle.mamba3_step_core(d["x"][:, t], vs, d["B"][:, t], K, d["C"][:, t], d["alpha"][:, t],
+                                        d["beta"][:, t], d["gamma"][:, t], st, d["mimo_x"], d["D"])
+        outs.append(o)
+        K, vs = d["B"][:, t], d["x"][:, t]
+    out = np.stack(outs, 1)  # [b, L, M, H, P]
+    mx = np.ones((H, M, P), np.float32) if d["mimo_x"] is None else d["mimo_x"]
+    v = d["x"][:, :, None] * mx.transpose(1, 0, 2)[None, None]  # [b, L, M, H, P]
+    nxt = np.concatenate([(1 - d["lam"][:, 1:]) * d["dt"][:, 1:], np.zeros((b, 1, H))], 1)
+    scale = (d["gamma"] + nxt).astype(np.float32)
+    y, hT = oracle.ssd3(v, d["da"].astype(np.float32), d["B"], d["C"], d["gamma"].astype(np.float32), scale,
+                        None, chunk=4)
+    # the step's state round-trips through f32 between tokens (as the cache does)
+    np.testing.assert_allclose(out, y + d["D"][None, None, None, :, None] * v, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(st, hT, rtol=1e-5, atol=1e-6)
+
+
+def _mamba3_params(seed, H, P, G, N, M, rope_dim, rng=None):
+    rng = rng or np.random.default_rng(seed)
+    return dict(nheads=H, headdim=P, ngroups=G, dstate=N, mimo=M, rope_dim=rope_dim,
+                dt_bias=rng.uniform(-3, -1, H).astype(np.float32), a_floor=1e-4, dt_limit=(0.0, 65504.0),
+                rotation_range=2.0, b_norm_w=rng.uniform(0.5, 1.5, N).astype(np.float32),
+                c_norm_w=rng.uniform(0.5, 1.5, N).astype(np.float32),
+                b_bias=(0.1 * rng.standard_normal((H, M, N))).astype(np.float32),
+                c_bias=(0.1 * rng.standard_normal((H, M, N))).astype(np.float32))
+
+
+def _mamba3_proj(rng, b, p):
+    H, P, G, N, M = (p[k] for k in ("nheads", "headdim", "ngroups", "dstate", "mimo"))
+    A = oracle.mamba3_num_angles(p["rope_dim"])
+    return rng.standard_normal((b, 2 * H * P + 2 * M * G * N + 3 * H + A)).astype(np.float32)
+
+
+@pytest.mark.parametrize("M,rope_frac", [(1, 1.0), (4, 1.0), (1, 0.5), (4, 0.5)])
+def test_mamba3_step_prep_rotation_closed_form(M, rope_frac):
+    """The rotation equals a complex multiply by exp(i theta) on each pair
+    ((2a, 2a+1) for M = 1, (a, a + N/2) otherwise, rope.rs:34-170), preserves
+    norms, leaves the unrotated entries alone, and theta is the wrapped
+    cumulative angle prev + dt range pi tanh(rot)."""
+    H, P, G, N, b = 4, 8, 2, 16, 3
+    rope_dim = int(N * rope_frac)
+    p = _mamba3_params(5, H, P, G, N, M, rope_dim)
+    rng = np.random.default_rng(7)
+    proj = _mamba3_proj(rng, b, p)
+    A = oracle.mamba3_num_angles(rope_dim)
+    ang0 = rng.uniform(-3, 3, (b, H, A)).astype(np.float32)
+    r = oracle.mamba3_step_prep(proj, p, ang0)
+    p0 = dict(p, rope_dim=0)
+    r0 = oracle.mamba3_step_prep(proj[:, :proj.shape[1] - A + 1] if A != 1 else proj, p0,
+                                 np.zeros((b, H, 1), np.float32))  # unrotated B/C (rot channel ignored)
+    rot = proj[:, -A:]
+    inc = r["dt"][:, :, None] * np.tanh(rot)[:, None, :] * (2.0 * np.pi)
+    theta = np.angle(np.exp(1j * (ang0 + inc)))
+    # outputs are f32 arrays: f32-level tolerances
+    np.testing.assert_allclose(np.cos(r["angle"]), np.cos(theta), atol=2e-6)
+    np.testing.assert_allclose(np.sin(r["angle"]), np.sin(theta), atol=2e-6)
+    assert np.all(np.abs(r["angle"]) <= np.pi + 1e-6)
+    i0 = np.arange(rope_dim // 2) * (2 if M == 1 else 1)
+    i1 = i0 + (1 if M == 1 else N // 2)
+    for key in ("B", "C"):
+        u, w = r0[key], r[key]
+        z = (u[..., i0] + 1j * u[..., i1]) * np.exp(1j * r["angle"][:, None, :, :rope_dim // 2])
+        np.testing.assert_allclose(w[..., i0], z.real, rtol=1e-6, atol=1e-6)
+        np.testing.assert_allclose(w[..., i1], z.imag, rtol=1e-6, atol=1e-6)
+        rest = np.setdiff1d(np.arange(N), np.concatenate([i0, i1]))
+        np.testing.assert_allclose(w[..., rest], u[..., rest], rtol=0, atol=0)
+
+
+def test_mamba3_step_prep_coefficients_and_norm():
+    """Trapezoid coefficients: beta/alpha + gamma = dt (the two endpoint
+    weights share dt), lambda -> 1 gives beta -> 0, the a_floor clamp and the
+    dt clamp; QK-norm: a constant raw row normalises to sign(c) w (+ bias)."""
+    H, P, G, N, M, b = 2, 4, 1, 8, 2, 2
+    p = _mamba3_params(9, H, P, G, N, M, 0)
+    rng = np.random.default_rng(11)
+    proj = _mamba3_proj(rng, b, p)
+    d_inner, bc = H * P, M * G * N
+    o_dt, o_a, o_l = 2 * d_inner + 2 * bc, 2 * d_inner + 2 * bc + H, 2 * d_inner + 2 * bc + 2 * H
+    r = oracle.mamba3_step_prep(proj, p, np.zeros((b, H, 1), np.float32))
+    np.testing.assert_allclose(r["beta"] / r["alpha"] + r["gamma"], r["dt"], rtol=1e-6)
+    softplus = lambda v: np.log1p(np.exp(v))  # noqa: E731
+    dt = softplus(proj[:, o_dt:o_dt + H] + p["dt_bias"])
+    np.testing.assert_allclose(r["dt"], dt, rtol=1e-6)
+    a = -np.maximum(softplus(proj[:, o_a:o_a + H]), p["a_floor"])
+    np.testing.assert_allclose(r["alpha"], np.exp(dt * a), rtol=1e-6)
+    pr = proj.copy()
+    pr[:, o_l:o_l + H] = 40.0          # lambda -> 1
+    pr[:, o_a:o_a + H] = -60.0         # softplus below a_floor
+    pr[:, 2 * d_inner:2 * d_inner + bc] = -2.5  # constant B rows
+    r2 = oracle.mamba3_step_prep(pr, dict(p, dt_limit=(0.0, 0.05)), np.zeros((b, H, 1), np.float32))
+    assert np.all(r2["beta"] < 1e-17) and np.all(r2["dt"] <= 0.05)
+    np.testing.assert_allclose(r2["alpha"], np.exp(-r2["dt"] * p["a_floor"]), rtol=1e-6)
+    want = -p["b_norm_w"][None, None, None, :] / np.sqrt(1 + 8.1584695e-8 / 6.25) + p["b_bias"].transpose(1, 0, 2)[None]
+    np.testing.assert_allclose(r2["B"], np.broadcast_to(want, r2["B"].shape), rtol=1e-7)
+
+
+def test_mamba3_step_finish_known_answers():
+    """z = 0 closes the gate; a one-hot mimo_o selects one rank; the gated
+    norm of a constant row is sign(c) w silu(z)."""
+    rng = np.random.default_rng(13)
+    b, M, H, P = 2, 3, 2, 4
+    out = rng.standard_normal((b, M, H, P)).astype(np.float32)
+    z = rng.standard_normal((b, H * P)).astype(np.float32)
+    silu = lambda v: v / (1 + np.exp(-v))  # noqa: E731
+    y1 = oracle.mamba3_step_finish(out[:, :1], np.zeros_like(z))
+    np.testing.assert_array_equal(y1, 0)
+    mo = np.zeros((H, M, P), np.float32)
+    mo[:, 1] = 1.0
+    y = oracle.mamba3_step_finish(out, z, np.ones((H, M, P), np.float32), mo)
+    np.testing.assert_allclose(y, (out[:, 1] * silu(z.reshape(b, H, P))).reshape(b, -1), rtol=1e-6)
+    const = np.full((b, 1, H, P), -0.7, np.float32)
+    w = rng.uniform(0.5, 1.5, P).astype(np.float32)
+    yn = oracle.mamba3_step_finish(const, z, norm_w=w)
+    want = -w[None, None] / np.sqrt(1 + 8.1584695e-8 / 0.49) * silu(z.reshape(b, H, P))
+    np.testing.assert_allclose(yn, want.reshape(b, -1), rtol=1e-7)
