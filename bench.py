@@ -299,6 +299,145 @@ def cpu_baseline_mamba1_step(cfg, batch, budget_s=10.0, seed=0):
                                       "scaled to 64 layers; f32 conv-step + scan-step restatement"}
 
 
+MAMBA3_STEP_CFG = dict(n_layers=64, d_model=1024, state_rank=128, per_head_dim=64, ngroups=1, mimo_rank=4)
+
+
+def mamba3_step_algorithmic(cfg, batch):
+    """Compulsory HBM bytes of one Mamba-3 decode token (Mamba3::step,
+    double_ssd/double_ssd/mod.rs:634-760) per layer: in_proj/out_proj weights
+    (bf16) once; the SSM kernel's cache read + written (state, K, v_state,
+    angle; f32), its in_proj row in (bf16) and y out (bf16).
+    Returns (step bytes, SSM-kernel bytes per launch)."""
+    import mamba_hip
+    c = mamba_hip.Mamba3Config(d_model=cfg["d_model"], state_rank=cfg["state_rank"],
+                               per_head_dim=cfg["per_head_dim"], ngroups=cfg["ngroups"], mimo_rank=cfg["mimo_rank"])
+    H, P, N, M, A = c.nheads, c.per_head_dim, c.state_rank, c.mimo_rank, c.num_rope_angles
+    cache = batch * (H * P * N + M * H * N + H * P + H * A) * 4 * 2
+    kern = cache + batch * c.d_in_proj * 2 + batch * c.d_inner * 2
+    weights = (c.d_model * c.d_in_proj + c.d_inner * c.d_model) * 2
+    step = cfg["n_layers"] * (weights + kern) + batch * c.d_model * 4 * 2
+    return step, kern
+
+
+def bench_mamba3_step(args):
+    """64 Mamba-3 blocks stepping one token (in_proj on hipBLASLt ->
+    mamba3_step_ssm -> out_proj), config-4 block shapes with the reference's
+    init, every layer with its own weights and cache, captured in one HIP graph."""
+    import torch
+
+    import mamba_hip
+    cfg = dict(MAMBA3_STEP_CFG)
+    b = args.batch
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    c = mamba_hip.Mamba3Config(d_model=cfg["d_model"], state_rank=cfg["state_rank"],
+                               per_head_dim=cfg["per_head_dim"], ngroups=cfg["ngroups"], mimo_rank=cfg["mimo_rank"])
+    blocks = [c.init(dev, torch.bfloat16, gen) for _ in range(cfg["n_layers"])]
+    caches = []
+    for m in blocks:
+        cc = m.new_cache(b)
+        cc.ssm_bhpr.normal_(0.0, 0.1, generator=gen)
+        cc.k_state_bmhr.normal_(0.0, 0.1, generator=gen)
+        cc.v_state_bhp.normal_(0.0, 1.0, generator=gen)
+        caches.append(cc)
+    x0 = torch.randn((b, c.d_model), generator=gen, device=dev)
+    projs = [torch.empty((b, c.d_in_proj), device=dev, dtype=torch.bfloat16) for _ in range(2)]
+    ys = torch.empty((b, c.d_inner), device=dev, dtype=torch.bfloat16)
+    xs = [torch.empty((b, c.d_model), device=dev, dtype=torch.bfloat16) for _ in range(2)]
+    argl = [mamba_hip.mamba3_step_ssm_args(c, projs[i % 2], caches[i], dt_bias=m.dt_bias, b_norm_w=m.b_norm_w,
+                                           c_norm_w=m.c_norm_w, b_bias=m.b_bias, c_bias=m.c_bias, D=m.D,
+                                           mimo_x=m.mimo_x, mimo_z=m.mimo_z, mimo_o=m.mimo_o, out=ys)
+            for i, m in enumerate(blocks)]
+
+    # every block reads the same input row (no norm/residual between blocks
+    # here, so chaining 64 of them would only grow or shrink the activations)
+    def eager(events=None):
+        xs[0].copy_(x0)
+        for i, m in enumerate(blocks):
+            torch.mm(xs[0], m.in_proj_w, out=projs[i % 2])
+            mamba_hip.mamba3_step_ssm(argl[i], dev, None if events is None else events[i])
+            torch.mm(ys, m.out_proj_w, out=xs[1])
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        eager()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        eager()
+    log(f"warmup {args.warmup}")
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} graph replays")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    L = cfg["n_layers"]
+    pairs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(L)]
+             for _ in range(args.steps)]
+    for ev in pairs:
+        eager(ev)
+    torch.cuda.synchronize()
+    durs = [a.elapsed_time(b_) for ev in pairs for a, b_ in ev]
+    kern_ms = sum(durs) / len(durs)
+    log(f"ms/step {ms_per_step:.4f}, SSM-step kernel {kern_ms * 1e3:.2f} us (mean of {len(durs)})")
+    step_bytes, kernel_bytes = mamba3_step_algorithmic(cfg, b)
+    achieved = kernel_bytes / (kern_ms * 1e-3) / 1e9
+    return {
+        "metric": f"Mamba-3 decode step us at batch {b} (64 layers, H=32 P=64 N=128 MIMO 4, 1 GPU) + % HBM roofline",
+        "value": ms_per_step * 1e3, "unit": "us/step",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (config-4 block shapes, reference init, states ~N(0,0.1), seed 0)",
+        "config": {"workload": "mamba3_decode_step", **cfg, "batch": b, "graph": "hip graph of the 64-layer step",
+                   "step_bytes": step_bytes, "step_hbm_gbs": step_bytes / (ms_per_step * 1e-3) / 1e9,
+                   "entry": "torch.mm in_proj + mamba3_step_ssm + torch.mm out_proj per layer"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel_ms": kern_ms,
+                     "algorithmic_bytes": kernel_bytes, "kernel": "mamba3_step_kernel (mean over all layers)"},
+    }
+
+
+def cpu_baseline_mamba3_step(cfg, batch, budget_s=10.0, seed=0):
+    """oracle.mamba3_step (f32 restatement) plus numpy products per layer, as
+    many layers as fit in the budget, scaled to the 64-layer step."""
+    import numpy as np
+
+    import mamba_hip
+    import oracle
+    rng = np.random.default_rng(seed)
+    c = mamba_hip.Mamba3Config(d_model=cfg["d_model"], state_rank=cfg["state_rank"],
+                               per_head_dim=cfg["per_head_dim"], ngroups=cfg["ngroups"], mimo_rank=cfg["mimo_rank"])
+    H, P, N, M, A = c.nheads, c.per_head_dim, c.state_rank, c.mimo_rank, c.num_rope_angles
+    f = lambda *s: rng.standard_normal(s).astype(np.float32)  # noqa: E731
+    prm = dict(nheads=H, headdim=P, ngroups=c.ngroups, dstate=N, mimo=M, rope_dim=c.rope_dim,
+               dt_bias=np.full(H, -2.0, np.float32), a_floor=c.a_floor, dt_limit=c.dt_limit,
+               rotation_range=c.rotation_range, b_norm_w=np.ones(N, np.float32), c_norm_w=np.ones(N, np.float32),
+               b_bias=np.ones((H, M, N), np.float32), c_bias=np.ones((H, M, N), np.float32),
+               D=np.ones(H, np.float32), mimo_x=np.full((H, M, P), 1 / M, np.float32),
+               mimo_z=np.ones((H, M, P), np.float32), mimo_o=np.full((H, M, P), 1 / M, np.float32))
+    W = (f(c.d_model, c.d_in_proj) / np.sqrt(c.d_model)).astype(np.float32)
+    Wo = (f(c.d_inner, c.d_model) / np.sqrt(c.d_inner)).astype(np.float32)
+    cache = dict(ssm=0.1 * f(batch, H, P, N), k_state=0.1 * f(batch, M, H, N), v_state=f(batch, H, P),
+                 angle=np.zeros((batch, H, A), np.float32))
+    x = f(batch, c.d_model)
+    done, t0 = 0, time.perf_counter()
+    while done < cfg["n_layers"] and (done == 0 or time.perf_counter() - t0 < budget_s):
+        y, cache = oracle.mamba3_step(x @ W, prm, cache, prec=32)
+        _ = y @ Wo  # every block reads the same input row, as on the GPU
+        done += 1
+    sec = (time.perf_counter() - t0) / done * cfg["n_layers"]
+    return {"value": sec * 1e6, "unit": "us/step", "cores": int(os.environ.get("OMP_NUM_THREADS", os.cpu_count())),
+            "kind": "port", "sample": f"{done} of {cfg['n_layers']} layers at batch {batch} ({sec * done / cfg['n_layers']:.1f} s), "
+                                      "scaled to 64 layers; f32 Mamba-3 step restatement + numpy products"}
+
+
 SSD3_CFG4 = dict(batch=4, seqlen=8192, mimo=4, nheads=32, headdim=64, dstate=128, ngroups=32, chunk=128)
 
 
@@ -662,7 +801,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="ssd2", choices=["ssd2", "mamba1", "decode", "ssd3", "mamba1_step"])
+    ap.add_argument("--workload", default="ssd2",
+                    choices=["ssd2", "mamba1", "decode", "ssd3", "mamba1_step", "mamba3_step"])
     ap.add_argument("--batch", type=int, default=DECODE_CFG3["batch"], help="decode batch")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -674,7 +814,10 @@ def main():
               "(the hot path shards by batch/head with no communication; see DESIGN.md)",
               file=sys.stderr)
         sys.exit(2)
-    if args.workload == "mamba1_step":
+    if args.workload == "mamba3_step":
+        out = bench_mamba3_step(args)
+        base = (lambda: cpu_baseline_mamba3_step(MAMBA3_STEP_CFG, args.batch))
+    elif args.workload == "mamba1_step":
         out = bench_mamba1_step(args)
         base = (lambda: cpu_baseline_mamba1_step(MAMBA1_STEP_CFG, args.batch))
     elif args.workload == "ssd3":
