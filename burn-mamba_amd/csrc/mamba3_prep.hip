@@ -1,0 +1,326 @@
+// Mamba-3 prefill around the single-SSD seam, gfx950: the prologue that turns
+// the in_proj output into the seam's inputs, and the epilogue after it.
+//
+// Reference: Mamba3::forward_single_ssd (burn-mamba
+// src/mamba3/single_ssd/single_ssd/mod.rs:44-360).
+//  * mamba3_prep_fwd (steps 2-6, :86-262): trapezoidal_coefficients
+//    (helpers.rs:42-73); scale_t = gamma_t + (1 - lambda_{t+1}) dt_{t+1}
+//    (:129-150); qk_norm_expand_bias (helpers.rs:82-95); rotate_bc_forward
+//    Complex2D (rotation/mod.rs:653-679: cumulative angle prev +
+//    cumsum_s(dt range pi tanh(rot)), apply_rope_partial rope.rs:118-170);
+//    v = x mimo_x (helpers.rs:152-168); the beta seed
+//    h0 = ssm + (dt_0 - gamma_0) sum_m (v_prev mimo_x[m]) (x) K_prev[m]
+//    (:195-225); the cache tail (last token's rotated B and x, wrapped angle;
+//    the angle goes to a separate buffer because every (b, h, m) workgroup
+//    reads the starting angle).
+//  * mamba3_finish_fwd (step 9 before out_proj, :288-332): y += D v, the silu
+//    gate (or per-head gated RMSNorm) with mimo_z, and the mimo_o merge.
+// The cumulative angle is carried wrapped to [-pi, pi] at every position (the
+// same cos/sin as the reference's unwrapped f32 cumsum, without its drift on
+// long sequences).
+#include "common.h"
+
+namespace mamba {
+
+struct M3PrepParams {
+    int nb, L, H, P, G, N, M, R, A;
+    bool proj_bf16, io_bf16;
+    const void* proj; int64_t proj_sb, proj_sl;
+    const float* ssm; float* kst; float* vst; const float* ang; float* ang_out;
+    const float* dt_bias; float a_floor, dt_lo, dt_hi, span;
+    const float* bnw; const float* cnw; const float* bbias; const float* cbias; const float* mx;
+    void* v; void* Bo; void* Co;
+    float* da; float* gm; float* sc;
+    float* h0;
+};
+
+__device__ __forceinline__ float m3p_softplus(float x) { return x > 18.f ? x : log1pf(__expf(x)); }
+__device__ __forceinline__ float m3p_wrap(float a) {
+    const float two_pi = 6.28318530717958647692f;
+    return a - rintf(a * (1.f / two_pi)) * two_pi;
+}
+__device__ __forceinline__ float m3p_ld(const M3PrepParams& p, int b, int l, int i) {
+    const int64_t off = (int64_t)b * p.proj_sb + (int64_t)l * p.proj_sl + i;
+    return p.proj_bf16 ? bf16_to_f32(static_cast<const bf16_t*>(p.proj)[off]) : static_cast<const float*>(p.proj)[off];
+}
+__device__ __forceinline__ void m3p_st(bool bf, void* base, int64_t i, float v) {
+    if (bf)
+        static_cast<bf16_t*>(base)[i] = f32_to_bf16(v);
+    else
+        static_cast<float*>(base)[i] = v;
+}
+
+// dt, lambda of (b, l, h); l past the end gives dt = lambda = 0 (scale's shift)
+__device__ __forceinline__ void m3p_coef(const M3PrepParams& p, int b, int l, int h, float& dt, float& da,
+                                         float& lam) {
+    if (l >= p.L) {
+        dt = da = lam = 0.f;
+        return;
+    }
+    const int o = 2 * p.H * p.P + 2 * p.M * p.G * p.N;
+    dt = fminf(fmaxf(m3p_softplus(m3p_ld(p, b, l, o + h) + p.dt_bias[h]), p.dt_lo), p.dt_hi);
+    da = dt * -fmaxf(m3p_softplus(m3p_ld(p, b, l, o + p.H + h)), p.a_floor);
+    lam = 1.f / (1.f + __expf(-m3p_ld(p, b, l, o + 2 * p.H + h)));
+}
+
+// Beta seed of the initial state, one workgroup per (b, h): reads the previous
+// token's K / v_state before mamba3_prep_kernel replaces them.
+__global__ __launch_bounds__(256) void mamba3_seed_kernel(M3PrepParams p) {
+    const int b = blockIdx.x / p.H, h = blockIdx.x % p.H;
+    float dt, da, lam;
+    m3p_coef(p, b, 0, h, dt, da, lam);
+    const float f = dt - lam * dt;  // dt_0 - gamma_0
+    const int64_t bh = (int64_t)b * p.H + h;
+    for (int i = threadIdx.x; i < p.P * p.N; i += 256) {
+        const int pp = i / p.N, n = i % p.N;
+        float acc = 0.f;
+        for (int m = 0; m < p.M; ++m) {
+            const float mxv = p.mx ? p.mx[((int64_t)h * p.M + m) * p.P + pp] : 1.f;
+            acc += (p.vst[bh * p.P + pp] * mxv) * p.kst[(((int64_t)b * p.M + m) * p.H + h) * p.N + n];
+        }
+        p.h0[bh * p.P * p.N + i] = p.ssm[bh * p.P * p.N + i] + f * acc;
+    }
+}
+
+// One workgroup per (b, h, m): positions in tiles of TS; the angle scan of
+// (b, h) is carried by threads a < A (recomputed by every m of the head).
+template <int TS>
+__global__ __launch_bounds__(256) void mamba3_prep_kernel(M3PrepParams p) {
+    const int m = blockIdx.x % p.M, h = (blockIdx.x / p.M) % p.H, b = blockIdx.x / (p.M * p.H);
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int N = p.N, P = p.P, g = h / (p.H / p.G);
+    const int64_t bh = (int64_t)b * p.H + h;
+    const int d_inner = p.H * P, bc = p.M * p.G * N;
+    const int o_b = 2 * d_inner + (m * p.G + g) * N, o_c = o_b + bc;
+    const int o_rot = 2 * d_inner + 2 * bc + 3 * p.H;
+    const int npair = p.R / 2;
+    extern __shared__ __align__(16) float s_dyn[];
+    float* s_raw = s_dyn;                  // [2][TS][N]
+    float* s_cs = s_raw + 2 * TS * N;      // [TS][npair]
+    float* s_sn = s_cs + TS * npair;       // [TS][npair]
+    __shared__ float s_dt[TS + 1], s_lam[TS + 1], s_da[TS], s_rms[2 * TS];
+
+    float theta = (t < p.A) ? p.ang[bh * p.A + t] : 0.f;
+    for (int l0 = 0; l0 < p.L; l0 += TS) {
+        const int nt = min(TS, p.L - l0);
+        // coefficients of the tile (+ the next position for scale)
+        if (t <= TS) {
+            float dt, da, lam;
+            m3p_coef(p, b, l0 + t, h, dt, da, lam);
+            s_dt[t] = dt;
+            s_lam[t] = lam;
+            if (t < TS) s_da[t] = da;
+        }
+        // raw B/C rows of (m, g)
+        for (int i = t; i < 2 * TS * N; i += 256) {
+            const int which = i / (TS * N), r = (i / N) % TS, n = i % N;
+            s_raw[i] = r < nt ? m3p_ld(p, b, l0 + r, (which ? o_c : o_b) + n) : 0.f;
+        }
+        __syncthreads();
+        // cumulative angle: sequential over the tile, wrapped at every position
+        if (t < p.A) {
+            for (int r = 0; r < nt; ++r) {
+                theta = m3p_wrap(theta + s_dt[r] * (tanhf(m3p_ld(p, b, l0 + r, o_rot + t)) * p.span));
+                if (t < npair) {
+                    s_cs[r * npair + t] = cosf(theta);
+                    s_sn[r * npair + t] = sinf(theta);
+                }
+            }
+        }
+        // QK-norm sums of squares: 2 TS rows, one wave per row (strided)
+        for (int rr = wave; rr < 2 * TS; rr += 4) {
+            const float* src = s_raw + rr * N;
+            float ss = 0.f;
+            for (int n = lane; n < N; n += 64) ss += src[n] * src[n];
+            ss = wave_sum(ss);
+            if (lane == 0) s_rms[rr] = 1.f / sqrtf(ss / (float)N + 8.1584695e-8f);
+        }
+        __syncthreads();
+        for (int i = t; i < 2 * TS * N; i += 256) {
+            const int which = i / (TS * N), n = i % N;
+            const float w = which ? p.cnw[n] : p.bnw[n];
+            const float bb = (which ? p.cbias : p.bbias)[((int64_t)h * p.M + m) * N + n];
+            s_raw[i] = (s_raw[i] * s_rms[i / N]) * w + bb;
+        }
+        __syncthreads();
+        // rotation: pairs (2k, 2k+1) for M == 1, (k, k + N/2) otherwise, k < R/2
+        for (int i = t; i < 2 * TS * npair; i += 256) {
+            const int which = i / (TS * npair), r = (i / npair) % TS, k = i % npair;
+            if (r >= nt) continue;
+            const int i0 = p.M == 1 ? 2 * k : k, i1 = p.M == 1 ? 2 * k + 1 : k + N / 2;
+            float* vv = s_raw + (which * TS + r) * N;
+            const float cs = s_cs[r * npair + k], sn = s_sn[r * npair + k];
+            const float x0 = vv[i0], x1 = vv[i1];
+            vv[i0] = cs * x0 - sn * x1;
+            vv[i1] = sn * x0 + cs * x1;
+        }
+        __syncthreads();
+        // outputs: B, C [b, l, m, h, n]; v [b, l, m, h, p]; da/gamma/scale (m == 0)
+        for (int i = t; i < 2 * nt * N; i += 256) {
+            const int which = i / (nt * N), r = (i / N) % nt, n = i % N;
+            const int64_t o = ((((int64_t)b * p.L + l0 + r) * p.M + m) * p.H + h) * N + n;
+            m3p_st(p.io_bf16, which ? p.Co : p.Bo, o, s_raw[(which * TS + r) * N + n]);
+        }
+        for (int i = t; i < nt * P; i += 256) {
+            const int r = i / P, pp = i % P;
+            const float mxv = p.mx ? p.mx[((int64_t)h * p.M + m) * P + pp] : 1.f;
+            const int64_t o = ((((int64_t)b * p.L + l0 + r) * p.M + m) * p.H + h) * P + pp;
+            m3p_st(p.io_bf16, p.v, o, m3p_ld(p, b, l0 + r, d_inner + h * P + pp) * mxv);
+        }
+        if (m == 0 && t < nt) {
+            const int64_t o = ((int64_t)b * p.L + l0 + t) * p.H + h;
+            const float gmv = s_lam[t] * s_dt[t];
+            p.da[o] = s_da[t];
+            p.gm[o] = gmv;
+            p.sc[o] = gmv + (1.f - s_lam[t + 1]) * s_dt[t + 1];
+        }
+        // the cache tail: the last token's rotated B (per m), x and angle (m == 0)
+        if (l0 + nt == p.L) {
+            for (int n = t; n < N; n += 256)
+                p.kst[(((int64_t)b * p.M + m) * p.H + h) * N + n] = s_raw[(nt - 1) * N + n];
+            if (m == 0) {
+                for (int pp = t; pp < P; pp += 256) p.vst[bh * P + pp] = m3p_ld(p, b, p.L - 1, d_inner + h * P + pp);
+                if (t < p.A) p.ang_out[bh * p.A + t] = theta;
+            }
+        }
+        __syncthreads();  // LDS reuse by the next tile
+    }
+}
+
+// ---- epilogue ------------------------------------------------------------
+struct M3FinishParams {
+    int nb, L, H, P, M;
+    bool io_bf16, z_bf16, out_bf16;
+    const void* y; const void* v;
+    const void* z; int64_t z_sb, z_sl;
+    const float* Dh; const float* mz; const float* mo; const float* onw;
+    void* out; int64_t out_sb, out_sl;
+};
+
+__device__ __forceinline__ float m3f_ld(bool bf, const void* base, int64_t i) {
+    return bf ? bf16_to_f32(static_cast<const bf16_t*>(base)[i]) : static_cast<const float*>(base)[i];
+}
+
+// one wave per (b, l, h); lanes over headdim (P <= 256, up to 4 per lane)
+__global__ __launch_bounds__(256) void mamba3_finish_kernel(M3FinishParams p) {
+    const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (item >= (int64_t)p.nb * p.L * p.H) return;  // whole waves exit together
+    const int h = (int)(item % p.H);
+    const int64_t bl = item / p.H;
+    const int l = (int)(bl % p.L), b = (int)(bl / p.L);
+    const float Dv = p.Dh ? p.Dh[h] : 0.f;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int m = 0; m < p.M; ++m) {
+        float o[4];
+        float ss = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int pp = lane + 64 * k;
+            o[k] = 0.f;
+            if (pp < p.P) {
+                const int64_t yi = (((bl * p.M + m) * p.H + h) * p.P) + pp;
+                o[k] = m3f_ld(p.io_bf16, p.y, yi) + Dv * m3f_ld(p.io_bf16, p.v, yi);
+                ss += o[k] * o[k];
+            }
+        }
+        float inv = 1.f;
+        if (p.onw) inv = 1.f / sqrtf(wave_sum(ss) / (float)p.P + 8.1584695e-8f);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int pp = lane + 64 * k;
+            if (pp >= p.P) continue;
+            float zv = m3f_ld(p.z_bf16, p.z, (int64_t)b * p.z_sb + (int64_t)l * p.z_sl + h * p.P + pp);
+            if (p.M > 1) zv *= p.mz[((int64_t)h * p.M + m) * p.P + pp];
+            const float sz = zv / (1.f + __expf(-zv));
+            float gv = p.onw ? (o[k] * inv) * p.onw[pp] * sz : o[k] * sz;
+            if (p.M > 1) gv *= p.mo[((int64_t)h * p.M + m) * p.P + pp];
+            acc[k] += gv;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int pp = lane + 64 * k;
+        if (pp < p.P)
+            m3p_st(p.out_bf16, p.out, (int64_t)b * p.out_sb + (int64_t)l * p.out_sl + h * p.P + pp, acc[k]);
+    }
+}
+
+constexpr int kM3PrepTS = 16;
+
+static int m3_prep_params(const mamba3_prep_args* a, M3PrepParams* out) {
+    MAMBA_CHECK_ARG(a != nullptr, "args is NULL");
+    MAMBA_CHECK_ARG(a->batch > 0 && a->seqlen > 0 && a->nheads > 0 && a->headdim > 0 && a->ngroups > 0,
+                    "sizes must be >= 1");
+    MAMBA_CHECK_ARG(a->nheads % a->ngroups == 0, "nheads must be a multiple of ngroups");
+    MAMBA_CHECK_ARG(a->dstate >= 2 && a->dstate <= 256 && a->dstate % 2 == 0, "dstate must be even, <= 256");
+    MAMBA_CHECK_ARG(a->headdim <= 1024, "headdim <= 1024 required");
+    MAMBA_CHECK_ARG(a->mimo >= 1 && a->mimo <= 16, "mimo must be in [1, 16]");
+    MAMBA_CHECK_ARG(a->rope_dim >= 0 && a->rope_dim <= a->dstate && a->rope_dim % 2 == 0,
+                    "rope_dim must be even and in [0, dstate]");
+    MAMBA_CHECK_ARG(a->angle_out && a->angle_out != a->angle, "angle_out is required and must not alias angle");
+    MAMBA_CHECK_ARG(a->proj && a->ssm_state && a->k_state && a->v_state && a->angle && a->dt_bias &&
+                        a->b_norm_w && a->c_norm_w && a->b_bias && a->c_bias && a->v && a->B && a->C &&
+                        a->da && a->gamma && a->scale && a->initial_state,
+                    "proj, cache, parameters and every output are required");
+    MAMBA_CHECK_ARG(a->mimo == 1 || a->mimo_x, "mimo_x is required when mimo > 1");
+    MAMBA_CHECK_ARG(a->proj_dtype == MAMBA_F32 || a->proj_dtype == MAMBA_BF16, "bad proj_dtype");
+    MAMBA_CHECK_ARG(a->io_dtype == MAMBA_F32 || a->io_dtype == MAMBA_BF16, "bad io_dtype");
+    M3PrepParams& p = *out;
+    p.nb = a->batch; p.L = a->seqlen; p.H = a->nheads; p.P = a->headdim; p.G = a->ngroups; p.N = a->dstate;
+    p.M = a->mimo; p.R = a->rope_dim; p.A = a->rope_dim / 2 > 1 ? a->rope_dim / 2 : 1;
+    MAMBA_CHECK_ARG(p.A <= 256, "too many angles");
+    const int64_t row = 2LL * p.H * p.P + 2LL * p.M * p.G * p.N + 3LL * p.H + p.A;
+    MAMBA_CHECK_ARG(a->proj_sl >= row && (a->seqlen == 1 || a->proj_sb >= a->proj_sl), "proj strides too small");
+    p.proj_bf16 = a->proj_dtype == MAMBA_BF16; p.io_bf16 = a->io_dtype == MAMBA_BF16;
+    p.proj = a->proj; p.proj_sb = a->proj_sb; p.proj_sl = a->proj_sl;
+    p.ssm = a->ssm_state; p.kst = a->k_state; p.vst = a->v_state; p.ang = a->angle; p.ang_out = a->angle_out;
+    p.dt_bias = a->dt_bias; p.a_floor = a->a_floor; p.dt_lo = a->dt_min; p.dt_hi = a->dt_max;
+    p.span = (float)((double)a->rotation_range * 3.14159265358979323846);
+    p.bnw = a->b_norm_w; p.cnw = a->c_norm_w; p.bbias = a->b_bias; p.cbias = a->c_bias; p.mx = a->mimo_x;
+    p.v = a->v; p.Bo = a->B; p.Co = a->C; p.da = a->da; p.gm = a->gamma; p.sc = a->scale; p.h0 = a->initial_state;
+    return MAMBA_OK;
+}
+
+}  // namespace mamba
+
+using namespace mamba;
+
+extern "C" int mamba3_prep_fwd(const mamba3_prep_args* a, mamba_stream_t stream) {
+    M3PrepParams p;
+    const int st = m3_prep_params(a, &p);
+    if (st != MAMBA_OK) return st;
+    hipStream_t s = (hipStream_t)stream;
+    hipLaunchKernelGGL(mamba3_seed_kernel, dim3(p.nb * p.H), dim3(256), 0, s, p);
+    MAMBA_CHECK_LAUNCH();
+    constexpr int TS = kM3PrepTS;
+    const int npair = p.R / 2;
+    const size_t lds = (size_t)(2 * TS * p.N + 2 * TS * npair) * sizeof(float);
+    hipLaunchKernelGGL(mamba3_prep_kernel<TS>, dim3(p.nb * p.H * p.M), dim3(256), lds, s, p);
+    MAMBA_CHECK_LAUNCH();
+    return MAMBA_OK;
+}
+
+extern "C" int mamba3_finish_fwd(const mamba3_finish_args* a, mamba_stream_t stream) {
+    MAMBA_CHECK_ARG(a != nullptr, "args is NULL");
+    MAMBA_CHECK_ARG(a->batch > 0 && a->seqlen > 0 && a->nheads > 0 && a->headdim > 0 && a->headdim <= 256,
+                    "sizes must be >= 1 and headdim <= 256");
+    MAMBA_CHECK_ARG(a->mimo >= 1 && a->mimo <= 16, "mimo must be in [1, 16]");
+    MAMBA_CHECK_ARG(a->mimo == 1 || (a->mimo_z && a->mimo_o), "mimo_z and mimo_o are required when mimo > 1");
+    MAMBA_CHECK_ARG(a->y_ssd && a->v && a->z && a->out, "y_ssd, v, z and out are required");
+    MAMBA_CHECK_ARG((a->io_dtype == MAMBA_F32 || a->io_dtype == MAMBA_BF16) &&
+                        (a->z_dtype == MAMBA_F32 || a->z_dtype == MAMBA_BF16) &&
+                        (a->out_dtype == MAMBA_F32 || a->out_dtype == MAMBA_BF16),
+                    "bad dtype");
+    M3FinishParams p;
+    p.nb = a->batch; p.L = a->seqlen; p.H = a->nheads; p.P = a->headdim; p.M = a->mimo;
+    p.io_bf16 = a->io_dtype == MAMBA_BF16; p.z_bf16 = a->z_dtype == MAMBA_BF16; p.out_bf16 = a->out_dtype == MAMBA_BF16;
+    p.y = a->y_ssd; p.v = a->v; p.z = a->z; p.z_sb = a->z_sb; p.z_sl = a->z_sl;
+    p.Dh = a->D; p.mz = a->mimo_z; p.mo = a->mimo_o; p.onw = a->out_norm_w;
+    p.out = a->out; p.out_sb = a->out_sb; p.out_sl = a->out_sl;
+    const int64_t items = (int64_t)p.nb * p.L * p.H;
+    MAMBA_CHECK_ARG((items + 3) / 4 < (1ll << 31), "too many (batch, position, head) items");
+    hipLaunchKernelGGL(mamba3_finish_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, (hipStream_t)stream, p);
+    MAMBA_CHECK_LAUNCH();
+    return MAMBA_OK;
+}

@@ -119,6 +119,33 @@ class Mamba3StepArgs(ctypes.Structure):
     ]
 
 
+class Mamba3PrepArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", c_i32), ("seqlen", c_i32), ("nheads", c_i32), ("headdim", c_i32),
+        ("ngroups", c_i32), ("dstate", c_i32), ("mimo", c_i32), ("rope_dim", c_i32),
+        ("proj_dtype", c_i32), ("io_dtype", c_i32),
+        ("proj", c_vp), ("proj_sb", c_i64), ("proj_sl", c_i64),
+        ("ssm_state", c_vp), ("k_state", c_vp), ("v_state", c_vp), ("angle", c_vp), ("angle_out", c_vp),
+        ("dt_bias", c_vp),
+        ("a_floor", ctypes.c_float), ("dt_min", ctypes.c_float), ("dt_max", ctypes.c_float),
+        ("rotation_range", ctypes.c_float),
+        ("b_norm_w", c_vp), ("c_norm_w", c_vp), ("b_bias", c_vp), ("c_bias", c_vp), ("mimo_x", c_vp),
+        ("v", c_vp), ("B", c_vp), ("C", c_vp),
+        ("da", c_vp), ("gamma", c_vp), ("scale", c_vp), ("initial_state", c_vp),
+    ]
+
+
+class Mamba3FinishArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", c_i32), ("seqlen", c_i32), ("nheads", c_i32), ("headdim", c_i32), ("mimo", c_i32),
+        ("io_dtype", c_i32), ("z_dtype", c_i32), ("out_dtype", c_i32),
+        ("y_ssd", c_vp), ("v", c_vp),
+        ("z", c_vp), ("z_sb", c_i64), ("z_sl", c_i64),
+        ("D", c_vp), ("mimo_z", c_vp), ("mimo_o", c_vp), ("out_norm_w", c_vp),
+        ("out", c_vp), ("out_sb", c_i64), ("out_sl", c_i64),
+    ]
+
+
 class Mamba2StepArgs(ctypes.Structure):
     _fields_ = [
         ("batch", c_i32), ("nheads", c_i32), ("headdim", c_i32), ("ngroups", c_i32),
@@ -184,6 +211,8 @@ _SIGNATURES = {
     "mamba1_scan_fwd_timed": ([ctypes.POINTER(Mamba1ScanArgs), c_vp, c_vp, c_vp], ctypes.c_int),
     "mamba1_scan_step": ([ctypes.POINTER(Mamba1StepArgs), c_vp], ctypes.c_int),
     "mamba3_step_ssm": ([ctypes.POINTER(Mamba3StepArgs), c_vp], ctypes.c_int),
+    "mamba3_prep_fwd": ([ctypes.POINTER(Mamba3PrepArgs), c_vp], ctypes.c_int),
+    "mamba3_finish_fwd": ([ctypes.POINTER(Mamba3FinishArgs), c_vp], ctypes.c_int),
     "mamba3_step_ssm_timed": ([ctypes.POINTER(Mamba3StepArgs), c_vp, c_vp, c_vp], ctypes.c_int),
     "mamba1_scan_step_timed": ([ctypes.POINTER(Mamba1StepArgs), c_vp, c_vp, c_vp], ctypes.c_int),
     "mamba_conv1d_step": ([ctypes.POINTER(Conv1dStepArgs), c_vp], ctypes.c_int),

@@ -23,7 +23,7 @@ from typing import Optional
 import torch
 
 from . import _lib
-from ._lib import Mamba3StepArgs, check
+from ._lib import Mamba3FinishArgs, Mamba3PrepArgs, Mamba3StepArgs, check
 from .ssd import _dtype_code, _raw_events, _stream
 
 
@@ -162,6 +162,63 @@ def step_ssm(args: Mamba3StepArgs, device, events=None):
         check(L.mamba3_step_ssm(ctypes.byref(args), st), "mamba3_step_ssm")
 
 
+def prep_fwd(cfg: Mamba3Config, proj: torch.Tensor, cache: Mamba3Cache, *, dt_bias, b_norm_w, c_norm_w, b_bias,
+             c_bias, mimo_x=None, io_dtype=None):
+    """mamba3_prep_fwd: proj [b, l, d_in_proj] -> dict(v [b,l,M,H,P], B, C [b,l,M,H,N],
+    da, gamma, scale [b,l,H], h0 [b,H,P,N]).  The cache's k_state / v_state are
+    replaced in place by the last token's; its angle by the new cumulative angle."""
+    b, L, row = proj.shape
+    H, P, N, M, G = cfg.nheads, cfg.per_head_dim, cfg.state_rank, cfg.mimo_rank, cfg.ngroups
+    if row != cfg.d_in_proj or proj.stride(2) != 1:
+        raise _lib.MambaHipError(f"proj must be [b, l, {cfg.d_in_proj}] with a unit inner stride")
+    dev, iod = proj.device, io_dtype or proj.dtype
+    out = dict(v=torch.empty((b, L, M, H, P), device=dev, dtype=iod),
+               B=torch.empty((b, L, M, H, N), device=dev, dtype=iod),
+               C=torch.empty((b, L, M, H, N), device=dev, dtype=iod),
+               da=torch.empty((b, L, H), device=dev), gamma=torch.empty((b, L, H), device=dev),
+               scale=torch.empty((b, L, H), device=dev), h0=torch.empty((b, H, P, N), device=dev))
+    angle_out = torch.empty_like(cache.angle_bha)
+    a = Mamba3PrepArgs()
+    a.batch, a.seqlen, a.nheads, a.headdim, a.ngroups, a.dstate, a.mimo = b, L, H, P, G, N, M
+    a.rope_dim, a.proj_dtype, a.io_dtype = cfg.rope_dim, _dtype_code(proj), _dtype_code(out["v"])
+    a.proj, a.proj_sb, a.proj_sl = proj.data_ptr(), proj.stride(0), proj.stride(1)
+    a.ssm_state = _f32c(cache.ssm_bhpr, "ssm_bhpr").data_ptr()
+    a.k_state = _f32c(cache.k_state_bmhr, "k_state_bmhr").data_ptr()
+    a.v_state = _f32c(cache.v_state_bhp, "v_state_bhp").data_ptr()
+    a.angle, a.angle_out = _f32c(cache.angle_bha, "angle_bha").data_ptr(), angle_out.data_ptr()
+    a.dt_bias = _f32c(dt_bias, "dt_bias").data_ptr()
+    a.a_floor, a.dt_min, a.dt_max, a.rotation_range = cfg.a_floor, cfg.dt_limit[0], cfg.dt_limit[1], cfg.rotation_range
+    a.b_norm_w, a.c_norm_w = _f32c(b_norm_w, "b_norm_w").data_ptr(), _f32c(c_norm_w, "c_norm_w").data_ptr()
+    a.b_bias, a.c_bias = _f32c(b_bias, "b_bias").data_ptr(), _f32c(c_bias, "c_bias").data_ptr()
+    a.mimo_x = None if mimo_x is None else _f32c(mimo_x, "mimo_x").data_ptr()
+    a.v, a.B, a.C = out["v"].data_ptr(), out["B"].data_ptr(), out["C"].data_ptr()
+    a.da, a.gamma, a.scale = out["da"].data_ptr(), out["gamma"].data_ptr(), out["scale"].data_ptr()
+    a.initial_state = out["h0"].data_ptr()
+    check(_lib.lib().mamba3_prep_fwd(ctypes.byref(a), _stream(dev)), "mamba3_prep_fwd")
+    cache.angle_bha = angle_out
+    return out
+
+
+def finish_fwd(cfg: Mamba3Config, y_ssd: torch.Tensor, v: torch.Tensor, z: torch.Tensor, *, D=None, mimo_z=None,
+               mimo_o=None, out_norm_w=None, out: Optional[torch.Tensor] = None):
+    """mamba3_finish_fwd: y_ssd, v [b, l, M, H, P] (contiguous); z [b, l, H*P] -> [b, l, H*P]."""
+    b, L, M, H, P = y_ssd.shape
+    if not (y_ssd.is_contiguous() and v.is_contiguous() and y_ssd.dtype == v.dtype) or z.stride(2) != 1:
+        raise _lib.MambaHipError("y_ssd / v must be contiguous with one dtype; z needs a unit inner stride")
+    if out is None:
+        out = torch.empty((b, L, H * P), device=y_ssd.device, dtype=y_ssd.dtype)
+    a = Mamba3FinishArgs()
+    a.batch, a.seqlen, a.nheads, a.headdim, a.mimo = b, L, H, P, M
+    a.io_dtype, a.z_dtype, a.out_dtype = _dtype_code(y_ssd), _dtype_code(z), _dtype_code(out)
+    a.y_ssd, a.v = y_ssd.data_ptr(), v.data_ptr()
+    a.z, a.z_sb, a.z_sl = z.data_ptr(), z.stride(0), z.stride(1)
+    for nm, t in (("D", D), ("mimo_z", mimo_z), ("mimo_o", mimo_o), ("out_norm_w", out_norm_w)):
+        setattr(a, nm, None if t is None else _f32c(t, nm).data_ptr())
+    a.out, a.out_sb, a.out_sl = out.data_ptr(), out.stride(0), out.stride(1)
+    check(_lib.lib().mamba3_finish_fwd(ctypes.byref(a), _stream(y_ssd.device)), "mamba3_finish_fwd")
+    return out
+
+
 @dataclass
 class Mamba3:
     """One Mamba-3 block's parameters (Burn Linear layout [d_in, d_out])."""
@@ -189,6 +246,30 @@ class Mamba3:
         return Mamba3Cache(z(batch, c.nheads, c.per_head_dim, c.state_rank),
                            z(batch, c.mimo_rank, c.nheads, c.state_rank),
                            z(batch, c.nheads, c.per_head_dim), z(batch, c.nheads, c.num_rope_angles))
+
+    def forward(self, x: torch.Tensor, cache: Optional[Mamba3Cache] = None, chunk_len: int = 64):
+        """Mamba3::forward_single_ssd (single_ssd/single_ssd/mod.rs:44-360):
+        x [b, l, d_model] -> (out [b, l, d_model], cache).  in_proj / out_proj on
+        torch.mm; prep -> mamba_ssd3_fwd -> finish in between."""
+        from .ssd3 import ssd3_fwd
+        b, L, _ = x.shape
+        if cache is None:
+            cache = self.new_cache(b)
+        wdt = self.in_proj_w.dtype
+        proj = torch.mm(x.reshape(b * L, -1).to(wdt), self.in_proj_w).reshape(b, L, -1)
+        if self.in_proj_b is not None:
+            proj = proj + self.in_proj_b.to(wdt)
+        pr = prep_fwd(self.cfg, proj, cache, dt_bias=self.dt_bias, b_norm_w=self.b_norm_w, c_norm_w=self.c_norm_w,
+                      b_bias=self.b_bias, c_bias=self.c_bias, mimo_x=self.mimo_x)
+        y_ssd, hT = ssd3_fwd(pr["v"], pr["da"], pr["B"], pr["C"], pr["gamma"], pr["scale"], pr["h0"],
+                             chunk_len=chunk_len)
+        cache.ssm_bhpr = hT
+        y = finish_fwd(self.cfg, y_ssd, pr["v"], proj[:, :, :self.cfg.d_inner], D=self.D, mimo_z=self.mimo_z,
+                       mimo_o=self.mimo_o, out_norm_w=self.out_norm_w)
+        out = torch.mm(y.reshape(b * L, -1), self.out_proj_w).reshape(b, L, -1)
+        if self.out_proj_b is not None:
+            out = out + self.out_proj_b.to(wdt)
+        return out.to(x.dtype), cache
 
     def step(self, x: torch.Tensor, cache: Optional[Mamba3Cache] = None, events=None):
         """Mamba3::step: x [b, d_model] -> (out [b, d_model], cache updated in place)."""

@@ -26,6 +26,9 @@
  *   mamba_conv1d_step   <- the conv-window step of Mamba1::step (src/mamba1/mamba1.rs:558-597)
  *   mamba3_step_ssm     <- Mamba3::step between in_proj and out_proj
  *                          (src/mamba3/double_ssd/double_ssd/mod.rs:634-760)
+ *   mamba3_prep_fwd     <- Mamba3::forward_single_ssd steps 2-6, before the SSD seam
+ *                          (src/mamba3/single_ssd/single_ssd/mod.rs:86-262)
+ *   mamba3_finish_fwd   <- the same forward's step 9 before out_proj (:288-332)
  *   mamba2_step_ssm     <- the body of Mamba2::step between in_proj and out_proj
  *                          (src/mamba2/mamba2.rs:857-995)
  *   mamba_linear_fwd    <- burn::nn::Linear::forward in the decode steps (packed weights)
@@ -306,6 +309,58 @@ int mamba3_step_ssm(const mamba3_step_args* args, mamba_stream_t stream);
 /* (benchmark timing; no counterpart in the reference).                        */
 int mamba3_step_ssm_timed(const mamba3_step_args* args, mamba_stream_t stream, void* event_start,
                           void* event_stop);
+
+/* ------------------------------------------------------------------------- */
+/* Mamba-3 prefill prologue: forward_single_ssd steps 2-6                      */
+/* (src/mamba3/single_ssd/single_ssd/mod.rs:86-262) from the in_proj output to */
+/* the inputs of mamba_ssd3_fwd: trapezoid coefficients (helpers.rs:42-73),    */
+/* scale_t = gamma_t + (1 - lambda_{t+1}) dt_{t+1} (:129-150), QK-norm + GQA + */
+/* bias (helpers.rs:82-95), the cumulative-angle RoPE of B and C               */
+/* (rotate_bc_forward Complex2D, rotation/mod.rs:653-679), v = x mimo_x, and   */
+/* the beta-seeded initial state ssm + (dt_0 - gamma_0) sum_m v_prev[m] (x)    */
+/* K_prev[m] (:195-225).  The cache's k_state / v_state are replaced by this   */
+/* call's last token (rotated B, x); the wrapped last angle goes to angle_out  */
+/* (not aliasing angle).  The cache's ssm_state is read only: mamba_ssd3_fwd's */
+/* final state is the new one.  proj row layout as for mamba3_step_ssm.        */
+/* ------------------------------------------------------------------------- */
+typedef struct mamba3_prep_args {
+    int32_t batch, seqlen, nheads, headdim, ngroups, dstate, mimo, rope_dim;
+    int32_t proj_dtype, io_dtype;                    /* io: v, B, C                */
+    const void* proj;   int64_t proj_sb, proj_sl;    /* [b, l, row]                */
+    const float* ssm_state;                          /* [b, H, P, N] (read)        */
+    float* k_state;                                  /* [b, M, H, N] in/out        */
+    float* v_state;                                  /* [b, H, P]    in/out        */
+    const float* angle;                              /* [b, H, A]    in            */
+    float* angle_out;                                /* [b, H, A]    out           */
+    const float* dt_bias;                            /* [H]                        */
+    float a_floor, dt_min, dt_max, rotation_range;
+    const float* b_norm_w; const float* c_norm_w;    /* [N]                        */
+    const float* b_bias;   const float* c_bias;      /* [H, M, N]                  */
+    const float* mimo_x;                             /* [H, M, P]; NULL if mimo == 1 */
+    void* v;                                         /* [b, l, M, H, P] out        */
+    void* B;            void* C;                     /* [b, l, M, H, N] out        */
+    float* da;          float* gamma;  float* scale; /* [b, l, H] out              */
+    float* initial_state;                            /* [b, H, P, N] out           */
+} mamba3_prep_args;
+
+int mamba3_prep_fwd(const mamba3_prep_args* args, mamba_stream_t stream);
+
+/* Mamba-3 prefill epilogue: forward_single_ssd step 9 before out_proj         */
+/* (single_ssd/single_ssd/mod.rs:288-332): y += D v, the silu gate (or the     */
+/* per-head gated RMSNorm) with z mimo_z[m], and the mimo_o merge over ranks.  */
+typedef struct mamba3_finish_args {
+    int32_t batch, seqlen, nheads, headdim, mimo;
+    int32_t io_dtype, z_dtype, out_dtype;
+    const void* y_ssd;                               /* [b, l, M, H, P] contiguous */
+    const void* v;                                   /* [b, l, M, H, P] contiguous */
+    const void* z;      int64_t z_sb, z_sl;          /* [b, l, H P]                */
+    const float* D;                                  /* [H] or NULL                */
+    const float* mimo_z; const float* mimo_o;        /* [H, M, P]; NULL if mimo == 1 */
+    const float* out_norm_w;                         /* [P] or NULL                */
+    void* out;          int64_t out_sb, out_sl;      /* [b, l, H P]                */
+} mamba3_finish_args;
+
+int mamba3_finish_fwd(const mamba3_finish_args* args, mamba_stream_t stream);
 
 /* ------------------------------------------------------------------------- */
 /* Mamba-2 recurrent decode step: everything of Mamba2::step between in_proj  */

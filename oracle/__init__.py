@@ -294,3 +294,82 @@ def mamba3_step(proj, p, cache, prec=64):
     y = mamba3_step_finish(out, z, p.get("mimo_z"), p.get("mimo_o"), p.get("out_norm_w"), prec)
     return y, dict(ssm=st, k_state=pr["B"], v_state=np.ascontiguousarray(x), angle=pr["angle"])
 
+
+
+# --------------------------------------------------------------------------
+# Mamba-3 prefill around the single-SSD seam (single_ssd/single_ssd/mod.rs:44-360)
+# --------------------------------------------------------------------------
+
+def mamba3_prep_fwd(proj, p, cache):
+    """forward_single_ssd steps 2-6 (single_ssd/single_ssd/mod.rs:86-262) in
+    float64 numpy: trapezoidal_coefficients (helpers.rs:42-73), scale_t =
+    gamma_t + (1 - lambda_{t+1}) dt_{t+1} (:129-150), qk_norm_expand_bias
+    (helpers.rs:82-95), rotate_bc_forward Complex2D (rotation/mod.rs:653-679:
+    cumulative angle = prev + cumsum_s(dt range pi tanh(rot)), wrapped only for
+    cos/sin and for the cache), v = x mimo_x (helpers.rs:152-168) and the beta
+    seed h0 = ssm + (dt_0 - gamma_0) sum_m (v_prev mimo_x[m]) (x) K_prev[m]
+    (:195-225).  proj [b, s, row]; cache: ssm/k_state/v_state/angle.
+    Returns dict(v [b,s,M,H,P], B, C [b,s,M,H,N], da, gamma, scale [b,s,H], h0, and
+    the new k_state / v_state / angle)."""
+    H, P, G, N, M, R = (p[k] for k in ("nheads", "headdim", "ngroups", "dstate", "mimo", "rope_dim"))
+    proj = np.asarray(proj, np.float64)
+    b, s, _ = proj.shape
+    A = mamba3_num_angles(R)
+    d_inner, bc = H * P, M * G * N
+    x = proj[..., d_inner:2 * d_inner].reshape(b, s, H, P)
+    braw = proj[..., 2 * d_inner:2 * d_inner + bc].reshape(b, s, M, G, N)
+    craw = proj[..., 2 * d_inner + bc:2 * d_inner + 2 * bc].reshape(b, s, M, G, N)
+    o = 2 * d_inner + 2 * bc
+    dd_dt, dd_a, lam_raw, rot = proj[..., o:o + H], proj[..., o + H:o + 2 * H], proj[..., o + 2 * H:o + 3 * H], \
+        proj[..., o + 3 * H:o + 3 * H + A]
+
+    def softplus(v):
+        return np.where(v > 18.0, v, np.log1p(np.exp(np.minimum(v, 18.0))))
+    lo, hi = p.get("dt_limit", (0.0, 65504.0))
+    dt = np.clip(softplus(dd_dt + np.asarray(p["dt_bias"], np.float64)), lo, hi)
+    a = -np.maximum(softplus(dd_a), p.get("a_floor", 1e-4))
+    da = dt * a
+    lam = 1.0 / (1.0 + np.exp(-lam_raw))
+    gamma = lam * dt
+    nxt = np.concatenate([(1 - lam[:, 1:]) * dt[:, 1:], np.zeros((b, 1, H))], 1)
+    scale = gamma + nxt
+
+    def qk(raw, w, bias):
+        rms = np.sqrt((raw * raw).mean(-1, keepdims=True) + 8.1584695e-8)
+        normed = raw / rms * np.asarray(w, np.float64)                      # [b, s, M, G, N]
+        exp = np.repeat(normed, H // G, axis=3)                              # group h // (H/G)
+        return exp + np.asarray(bias, np.float64).transpose(1, 0, 2)[None, None]  # [b, s, M, H, N]
+    Bq, Cq = qk(braw, p["b_norm_w"], p["b_bias"]), qk(craw, p["c_norm_w"], p["c_bias"])
+    inc = dt[..., None] * (np.tanh(rot)[:, :, None, :] * (p.get("rotation_range", 2.0) * np.pi))  # [b,s,H,A]
+    theta = np.asarray(cache["angle"], np.float64)[:, None] + np.cumsum(inc, axis=1)
+    if R > 0:
+        k = np.arange(R // 2)
+        i0 = 2 * k if M == 1 else k
+        i1 = i0 + (1 if M == 1 else N // 2)
+        th = theta[:, :, None, :, :R // 2]
+        cs, sn = np.cos(th), np.sin(th)
+        for Z in (Bq, Cq):
+            x0, x1 = Z[..., i0].copy(), Z[..., i1].copy()
+            Z[..., i0] = cs * x0 - sn * x1
+            Z[..., i1] = sn * x0 + cs * x1
+    mx = np.ones((H, M, P)) if p.get("mimo_x") is None else np.asarray(p["mimo_x"], np.float64)
+    v = x[:, :, None] * mx.transpose(1, 0, 2)[None, None]                   # [b, s, M, H, P]
+    vprev = np.asarray(cache["v_state"], np.float64)[:, None] * mx.transpose(1, 0, 2)[None]  # [b, M, H, P]
+    seed = np.einsum("bmhp,bmhn->bhpn", vprev, np.asarray(cache["k_state"], np.float64))
+    h0 = np.asarray(cache["ssm"], np.float64) + (dt[:, 0] - gamma[:, 0])[:, :, None, None] * seed
+    wrap = lambda t: t - np.round(t / (2 * np.pi)) * (2 * np.pi)  # noqa: E731
+    f = lambda t: np.ascontiguousarray(t, np.float32)  # noqa: E731
+    return dict(v=f(v), B=f(Bq), C=f(Cq), da=f(da), gamma=f(gamma), scale=f(scale), dt=f(dt), h0=f(h0),
+                k_state=f(Bq[:, -1]), v_state=f(x[:, -1]), angle=f(wrap(theta[:, -1])))
+
+
+def mamba3_finish_fwd(y_ssd, v, z, p):
+    """forward_single_ssd step 9 before out_proj (single_ssd/single_ssd/mod.rs:288-332):
+    y += D v, then the gate (or per-head gated norm) and the mimo_o merge per
+    position.  y_ssd, v [b, s, M, H, P]; z [b, s, H*P] -> [b, s, H*P]."""
+    y_ssd, v, z = (np.asarray(t, np.float32) for t in (y_ssd, v, z))
+    b, s, M, H, P = y_ssd.shape
+    D = np.zeros(H, np.float32) if p.get("D") is None else np.asarray(p["D"], np.float32)
+    out = (y_ssd + D[None, None, None, :, None] * v).reshape(b * s, M, H, P)
+    y = mamba3_step_finish(out, z.reshape(b * s, H * P), p.get("mimo_z"), p.get("mimo_o"), p.get("out_norm_w"))
+    return y.reshape(b, s, H * P)

@@ -56,6 +56,8 @@ int main(void) {{ printf("%zu\\n", sizeof({struct_name})); {body} return 0; }}
                                              ("Conv1dStepArgs", "mamba_conv1d_step_args"),
                                              ("Mamba2StepArgs", "mamba2_step_args"),
                                              ("Mamba3StepArgs", "mamba3_step_args"),
+                                             ("Mamba3PrepArgs", "mamba3_prep_args"),
+                                             ("Mamba3FinishArgs", "mamba3_finish_args"),
                                              ("LinearArgs", "mamba_linear_args"),
                                              ("Mamba2LayerArgs", "mamba2_layer_args"),
                                              ("RmsNormArgs", "mamba_rmsnorm_args")])

@@ -481,3 +481,68 @@ def test_mamba3_step_finish_known_answers():
     yn = oracle.mamba3_step_finish(const, z, norm_w=w)
     want = -w[None, None] / np.sqrt(1 + 8.1584695e-8 / 0.49) * silu(z.reshape(b, H, P))
     np.testing.assert_allclose(yn, want.reshape(b, -1), rtol=1e-7)
+
+
+def test_mamba3_prep_fwd_equals_step_prep():
+    """The prefill prep over a sequence equals the pinned per-token prep run
+    token by token (angles compared on the circle), and its cache tail is the
+    last token's."""
+    H, P, G, N, M, b, s = 4, 8, 2, 16, 4, 2, 9
+    p = _mamba3_params(41, H, P, G, N, M, 16)
+    p.update(mimo_x=np.random.default_rng(1).standard_normal((H, M, P)).astype(np.float32))
+    rng = np.random.default_rng(43)
+    A = oracle.mamba3_num_angles(16)
+    proj = np.stack([_mamba3_proj(rng, b, p) for _ in range(s)], 1)
+    cache = dict(ssm=np.zeros((b, H, P, N), np.float32), k_state=np.zeros((b, M, H, N), np.float32),
+                 v_state=np.zeros((b, H, P), np.float32), angle=rng.uniform(-3, 3, (b, H, A)).astype(np.float32))
+    r = oracle.mamba3_prep_fwd(proj, p, cache)
+    ang = cache["angle"]
+    for t in range(s):
+        st = oracle.mamba3_step_prep(proj[:, t], p, ang)
+        ang = st["angle"]
+        np.testing.assert_allclose(r["B"][:, t], st["B"], rtol=2e-5, atol=2e-6)
+        np.testing.assert_allclose(r["C"][:, t], st["C"], rtol=2e-5, atol=2e-6)
+        np.testing.assert_allclose(r["gamma"][:, t], st["gamma"], rtol=1e-6)
+        np.testing.assert_allclose(np.exp(r["da"][:, t]), st["alpha"], rtol=1e-6)
+    np.testing.assert_allclose(np.cos(r["angle"]), np.cos(ang), atol=2e-6)
+    np.testing.assert_allclose(np.sin(r["angle"]), np.sin(ang), atol=2e-6)
+    np.testing.assert_allclose(r["k_state"], r["B"][:, -1])
+
+
+@pytest.mark.parametrize("M,out_norm", [(1, False), (4, True)])
+def test_mamba3_prefill_then_steps_equals_steps(M, out_norm):
+    """A prefill (prep -> pinned chunked SSD -> finish) of the first s1 tokens,
+    then per-token steps from its cache, equals per-token steps from an empty
+    cache for every token (the reference's split-prefill/step parity,
+    single_ssd/single_ssd/tests.rs) -- this pins the beta seed, scale and the
+    cache handover."""
+    H, P, G, N, b, s1, s2 = 2, 8, 1, 16, 2, 7, 3
+    p = _mamba3_params(47 + M, H, P, G, N, M, 16)
+    rng = np.random.default_rng(53)
+    if M > 1:
+        p.update(mimo_x=rng.standard_normal((H, M, P)).astype(np.float32),
+                 mimo_z=rng.standard_normal((H, M, P)).astype(np.float32),
+                 mimo_o=rng.standard_normal((H, M, P)).astype(np.float32))
+    if out_norm:
+        p.update(out_norm_w=rng.uniform(0.5, 1.5, P).astype(np.float32))
+    p.update(D=rng.standard_normal(H).astype(np.float32))
+    A = oracle.mamba3_num_angles(16)
+    proj = np.stack([_mamba3_proj(rng, b, p) for _ in range(s1 + s2)], 1)
+    zero = dict(ssm=np.zeros((b, H, P, N), np.float32), k_state=np.zeros((b, M, H, N), np.float32),
+                v_state=np.zeros((b, H, P), np.float32), angle=np.zeros((b, H, A), np.float32))
+    # reference: token steps from the empty cache
+    ys, c = [], zero
+    for t in range(s1 + s2):
+        y, c = oracle.mamba3_step(proj[:, t], p, c)
+        ys.append(y)
+    # prefill of the first s1 tokens
+    r = oracle.mamba3_prep_fwd(proj[:, :s1], p, zero)
+    yssd, hT = oracle.ssd3(r["v"], r["da"], r["B"], r["C"], r["gamma"], r["scale"], r["h0"], chunk=4)
+    d_inner = H * P
+    yp = oracle.mamba3_finish_fwd(yssd, r["v"], proj[:, :s1, :d_inner], p)
+    for t in range(s1):
+        np.testing.assert_allclose(yp[:, t], ys[t], rtol=2e-4, atol=2e-5)
+    c = dict(ssm=hT, k_state=r["k_state"], v_state=r["v_state"], angle=r["angle"])
+    for t in range(s1, s1 + s2):
+        y, c = oracle.mamba3_step(proj[:, t], p, c)
+        np.testing.assert_allclose(y, ys[t], rtol=2e-4, atol=2e-5)
