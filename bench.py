@@ -438,6 +438,99 @@ def cpu_baseline_mamba3_step(cfg, batch, budget_s=10.0, seed=0):
                                       "scaled to 64 layers; f32 Mamba-3 step restatement + numpy products"}
 
 
+def mamba3_prep_algorithmic(cfg):
+    """Compulsory HBM bytes of one mamba3_prep_fwd call at config 4: the in_proj
+    rows read (bf16), v / B / C written per head and rank (bf16), da / gamma /
+    scale (f32), the initial state read + written (f32) and the small cache tail."""
+    import mamba_hip
+    c = mamba_hip.Mamba3Config(d_model=cfg["nheads"] * cfg["headdim"] // 2, state_rank=cfg["dstate"],
+                               per_head_dim=cfg["headdim"], ngroups=1, mimo_rank=cfg["mimo"])
+    b, L, H, P, N, M = cfg["batch"], cfg["seqlen"], c.nheads, c.per_head_dim, c.state_rank, c.mimo_rank
+    tok = b * L
+    return (tok * c.d_in_proj * 2 + tok * M * H * (P + 2 * N) * 2 + tok * H * 3 * 4 + 2 * b * H * P * N * 4
+            + 2 * b * (M * H * N + H * P + H * c.num_rope_angles) * 4)
+
+
+def bench_mamba3_prep(args):
+    """mamba3_prep_fwd at config 4 (B=4 L=8192 H=32 P=64 N=128 MIMO 4, full
+    rotation): the prologue from in_proj rows to the SSD seam's inputs."""
+    import torch
+
+    import mamba_hip
+    cfg = dict(SSD3_CFG4)
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    c = mamba_hip.Mamba3Config(d_model=cfg["nheads"] * cfg["headdim"] // 2, state_rank=cfg["dstate"],
+                               per_head_dim=cfg["headdim"], ngroups=1, mimo_rank=cfg["mimo"])
+    m = c.init(dev, torch.bfloat16, gen)
+    b, L = cfg["batch"], cfg["seqlen"]
+    proj = (torch.randn((b, L, c.d_in_proj), generator=gen, device=dev)).to(torch.bfloat16)
+    cache = m.new_cache(b)
+
+    def step():
+        mamba_hip.mamba3_prep_fwd(c, proj, cache, dt_bias=m.dt_bias, b_norm_w=m.b_norm_w, c_norm_w=m.c_norm_w,
+                                  b_bias=m.b_bias, c_bias=m.c_bias, mimo_x=m.mimo_x)
+
+    log(f"warmup {args.warmup}")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} steps")
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    kern_ms = e0.elapsed_time(e1) / args.steps
+    nbytes = mamba3_prep_algorithmic(cfg)
+    gbs = nbytes / (kern_ms * 1e-3) / 1e9
+    tokens = b * L
+    return {
+        "metric": "Mamba-3 prefill prologue tokens/s (B=4 L=8192 H=32 P=64 N=128 MIMO 4) + % HBM roofline",
+        "value": tokens / (ms_per_step * 1e-3), "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (config-4 shapes, reference init, in_proj rows ~N(0,1), seed 0)",
+        "config": {"workload": "mamba3_prep_cfg4", **cfg, "io": "proj/v/B/C bf16, coefficients and states f32",
+                   "entry": "mamba3_prep_fwd (seed + prep kernels)"},
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": gbs / HBM_PEAK_GBS, "traffic": None, "kernel_ms": kern_ms,
+                     "algorithmic_bytes": nbytes,
+                     "timing": "HIP events around the back-to-back calls on the launch stream, per call"},
+    }
+
+
+def cpu_baseline_mamba3_prep(cfg, seed=0):
+    """oracle.mamba3_prep_fwd (float64 numpy restatement) on one batch row's
+    first 1024 tokens, scaled to the whole call."""
+    import numpy as np
+
+    import mamba_hip
+    import oracle
+    c = mamba_hip.Mamba3Config(d_model=cfg["nheads"] * cfg["headdim"] // 2, state_rank=cfg["dstate"],
+                               per_head_dim=cfg["headdim"], ngroups=1, mimo_rank=cfg["mimo"])
+    H, P, N, M, A = c.nheads, c.per_head_dim, c.state_rank, c.mimo_rank, c.num_rope_angles
+    rng = np.random.default_rng(seed)
+    L = 1024
+    prm = dict(nheads=H, headdim=P, ngroups=1, dstate=N, mimo=M, rope_dim=c.rope_dim,
+               dt_bias=np.full(H, -2.0, np.float32), b_norm_w=np.ones(N, np.float32), c_norm_w=np.ones(N, np.float32),
+               b_bias=np.ones((H, M, N), np.float32), c_bias=np.ones((H, M, N), np.float32),
+               mimo_x=np.full((H, M, P), 1 / M, np.float32))
+    proj = rng.standard_normal((1, L, c.d_in_proj)).astype(np.float32)
+    z = lambda *s: np.zeros(s, np.float32)  # noqa: E731
+    cache = dict(ssm=z(1, H, P, N), k_state=z(1, M, H, N), v_state=z(1, H, P), angle=z(1, H, A))
+    t0 = time.perf_counter()
+    oracle.mamba3_prep_fwd(proj, prm, cache)
+    sec = time.perf_counter() - t0
+    total = cfg["batch"] * cfg["seqlen"]
+    return {"value": L / sec, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"1 x {L} tokens ({sec:.1f} s) of {total}; float64 numpy restatement of the prologue"}
+
+
 SSD3_CFG4 = dict(batch=4, seqlen=8192, mimo=4, nheads=32, headdim=64, dstate=128, ngroups=32, chunk=128)
 
 
@@ -802,7 +895,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="ssd2",
-                    choices=["ssd2", "mamba1", "decode", "ssd3", "mamba1_step", "mamba3_step"])
+                    choices=["ssd2", "mamba1", "decode", "ssd3", "mamba1_step", "mamba3_step", "mamba3_prep"])
     ap.add_argument("--batch", type=int, default=DECODE_CFG3["batch"], help="decode batch")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -814,7 +907,10 @@ def main():
               "(the hot path shards by batch/head with no communication; see DESIGN.md)",
               file=sys.stderr)
         sys.exit(2)
-    if args.workload == "mamba3_step":
+    if args.workload == "mamba3_prep":
+        out = bench_mamba3_prep(args)
+        base = (lambda: cpu_baseline_mamba3_prep(SSD3_CFG4))
+    elif args.workload == "mamba3_step":
         out = bench_mamba3_step(args)
         base = (lambda: cpu_baseline_mamba3_step(MAMBA3_STEP_CFG, args.batch))
     elif args.workload == "mamba1_step":

@@ -84,23 +84,43 @@ __global__ __launch_bounds__(256) void mamba3_seed_kernel(M3PrepParams p) {
 
 // One workgroup per (b, h, m): positions in tiles of TS; the angle scan of
 // (b, h) is carried by threads a < A (recomputed by every m of the head).
-template <int TS>
+// N (dstate, a power of two) is a template parameter so the per-element loops
+// are (row, column) walks with shifts, not runtime divisions.
+template <int TS, int N>
 __global__ __launch_bounds__(256) void mamba3_prep_kernel(M3PrepParams p) {
+    constexpr int RS = N >= 256 ? 1 : 256 / N;  // rows per pass of a [rows][N] walk
     const int m = blockIdx.x % p.M, h = (blockIdx.x / p.M) % p.H, b = blockIdx.x / (p.M * p.H);
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int N = p.N, P = p.P, g = h / (p.H / p.G);
+    const int P = p.P, g = h / (p.H / p.G);
+    const int col = t % N, row0 = t / N;  // N <= 256: every thread owns one column
     const int64_t bh = (int64_t)b * p.H + h;
     const int d_inner = p.H * P, bc = p.M * p.G * N;
     const int o_b = 2 * d_inner + (m * p.G + g) * N, o_c = o_b + bc;
     const int o_rot = 2 * d_inner + 2 * bc + 3 * p.H;
-    const int npair = p.R / 2;
+    const int npair = p.R / 2, A = p.A;
     extern __shared__ __align__(16) float s_dyn[];
-    float* s_raw = s_dyn;                  // [2][TS][N]
+    float* s_raw = s_dyn;                  // [2 TS][N]: B rows, then C rows
     float* s_cs = s_raw + 2 * TS * N;      // [TS][npair]
     float* s_sn = s_cs + TS * npair;       // [TS][npair]
+    float* s_th = s_sn + TS * npair;       // [TS][A]: angle increments, then cumulative angles
+    float* s_x = s_th + TS * A;            // [TS][P]: x rows of the tile
     __shared__ float s_dt[TS + 1], s_lam[TS + 1], s_da[TS], s_rms[2 * TS];
+    const float bnw = p.bnw[col], cnw = p.cnw[col];
+    const float bbias = p.bbias[((int64_t)h * p.M + m) * N + col], cbias = p.cbias[((int64_t)h * p.M + m) * N + col];
+    // rotation partner of this column: pairs (2k, 2k+1) for M == 1, (k, k + N/2) otherwise
+    const bool pw = p.M == 1;
+    const int k_of = pw ? col >> 1 : (col < N / 2 ? col : col - N / 2);
+    const bool first = pw ? (col & 1) == 0 : col < N / 2;
+    const int partner = pw ? (col ^ 1) : (first ? col + N / 2 : col - N / 2);
+    const bool rotated = k_of < npair;
+    // 2-D walks over the tile for the runtime widths A (angles), npair and P:
+    // this thread's column and row offset, and the row step, computed once
+    const int ca = t % A, ra0 = t / A, rsa = A >= 256 ? 1 : 256 / A;
+    const int np1 = npair > 0 ? npair : 1;
+    const int cp = t % np1, rp0 = t / np1, rsp = np1 >= 256 ? 1 : 256 / np1;
+    const int cx = t % P, rx0 = t / P, rsx = P >= 256 ? 1 : 256 / P;
 
-    float theta = (t < p.A) ? p.ang[bh * p.A + t] : 0.f;
+    float theta = (t < A) ? p.ang[bh * A + t] : 0.f;
     for (int l0 = 0; l0 < p.L; l0 += TS) {
         const int nt = min(TS, p.L - l0);
         // coefficients of the tile (+ the next position for scale)
@@ -111,21 +131,34 @@ __global__ __launch_bounds__(256) void mamba3_prep_kernel(M3PrepParams p) {
             s_lam[t] = lam;
             if (t < TS) s_da[t] = da;
         }
-        // raw B/C rows of (m, g)
-        for (int i = t; i < 2 * TS * N; i += 256) {
-            const int which = i / (TS * N), r = (i / N) % TS, n = i % N;
-            s_raw[i] = r < nt ? m3p_ld(p, b, l0 + r, (which ? o_c : o_b) + n) : 0.f;
+        // raw B/C rows of (m, g): row r < TS is B, r >= TS is C; the tile's x rows.
+        // Everything the tile reads from HBM is staged here, before any global
+        // store (proj and the outputs are untyped pointers the compiler must
+        // assume may alias, which would serialise load -> store pairs).
+        for (int r = row0; r < 2 * TS; r += RS) {
+            const int rr = r < TS ? r : r - TS;
+            s_raw[r * N + col] = rr < nt ? m3p_ld(p, b, l0 + rr, (r < TS ? o_b : o_c) + col) : 0.f;
+        }
+        if (P <= 256) {
+            for (int r = rx0; r < nt; r += rsx) s_x[r * P + cx] = m3p_ld(p, b, l0 + r, d_inner + h * P + cx);
+        } else {
+            for (int r = 0; r < nt; ++r)
+                for (int pp = t; pp < P; pp += 256) s_x[r * P + pp] = m3p_ld(p, b, l0 + r, d_inner + h * P + pp);
+        }
+        // raw rotation channels of the tile
+        if (A <= 256) {
+            for (int r = ra0; r < nt; r += rsa) s_th[r * A + ca] = m3p_ld(p, b, l0 + r, o_rot + ca);
+        } else {
+            for (int r = 0; r < nt; ++r)
+                for (int k = t; k < A; k += 256) s_th[r * A + k] = m3p_ld(p, b, l0 + r, o_rot + k);
         }
         __syncthreads();
-        // cumulative angle: sequential over the tile, wrapped at every position
-        if (t < p.A) {
-            for (int r = 0; r < nt; ++r) {
-                theta = m3p_wrap(theta + s_dt[r] * (tanhf(m3p_ld(p, b, l0 + r, o_rot + t)) * p.span));
-                if (t < npair) {
-                    s_cs[r * npair + t] = cosf(theta);
-                    s_sn[r * npair + t] = sinf(theta);
-                }
-            }
+        // angle increments dt range pi tanh(rot), spread over all threads
+        if (A <= 256) {
+            for (int r = ra0; r < nt; r += rsa) s_th[r * A + ca] = s_dt[r] * (tanhf(s_th[r * A + ca]) * p.span);
+        } else {
+            for (int r = 0; r < nt; ++r)
+                for (int k = t; k < A; k += 256) s_th[r * A + k] = s_dt[r] * (tanhf(s_th[r * A + k]) * p.span);
         }
         // QK-norm sums of squares: 2 TS rows, one wave per row (strided)
         for (int rr = wave; rr < 2 * TS; rr += 4) {
@@ -136,36 +169,53 @@ __global__ __launch_bounds__(256) void mamba3_prep_kernel(M3PrepParams p) {
             if (lane == 0) s_rms[rr] = 1.f / sqrtf(ss / (float)N + 8.1584695e-8f);
         }
         __syncthreads();
-        for (int i = t; i < 2 * TS * N; i += 256) {
-            const int which = i / (TS * N), n = i % N;
-            const float w = which ? p.cnw[n] : p.bnw[n];
-            const float bb = (which ? p.cbias : p.bbias)[((int64_t)h * p.M + m) * N + n];
-            s_raw[i] = (s_raw[i] * s_rms[i / N]) * w + bb;
+        // cumulative angle: sequential per angle over the tile (LDS only), wrapped at every position
+        if (t < A)
+            for (int r = 0; r < nt; ++r) {
+                theta = m3p_wrap(theta + s_th[r * A + t]);
+                s_th[r * A + t] = theta;
+            }
+        // normalise + bias in place
+        for (int r = row0; r < 2 * TS; r += RS)
+            s_raw[r * N + col] = (s_raw[r * N + col] * s_rms[r]) * (r < TS ? bnw : cnw) + (r < TS ? bbias : cbias);
+        __syncthreads();
+        // cos / sin of the rotated pairs' angles, spread over all threads
+        if (npair > 0 && npair <= 256) {
+            for (int r = rp0; r < nt; r += rsp) {
+                const float th = s_th[r * A + cp];
+                s_cs[r * npair + cp] = cosf(th);
+                s_sn[r * npair + cp] = sinf(th);
+            }
+        } else if (npair > 256) {
+            for (int r = 0; r < nt; ++r)
+                for (int k = t; k < npair; k += 256) {
+                    s_cs[r * npair + k] = cosf(s_th[r * A + k]);
+                    s_sn[r * npair + k] = sinf(s_th[r * A + k]);
+                }
         }
         __syncthreads();
-        // rotation: pairs (2k, 2k+1) for M == 1, (k, k + N/2) otherwise, k < R/2
-        for (int i = t; i < 2 * TS * npair; i += 256) {
-            const int which = i / (TS * npair), r = (i / npair) % TS, k = i % npair;
-            if (r >= nt) continue;
-            const int i0 = p.M == 1 ? 2 * k : k, i1 = p.M == 1 ? 2 * k + 1 : k + N / 2;
-            float* vv = s_raw + (which * TS + r) * N;
-            const float cs = s_cs[r * npair + k], sn = s_sn[r * npair + k];
-            const float x0 = vv[i0], x1 = vv[i1];
-            vv[i0] = cs * x0 - sn * x1;
-            vv[i1] = sn * x0 + cs * x1;
+        // rotate and store: each thread owns column col of its rows, reading its partner
+        for (int r = row0; r < 2 * TS; r += RS) {
+            const int rr = r < TS ? r : r - TS;
+            if (rr >= nt) continue;
+            float v = s_raw[r * N + col];
+            if (rotated) {
+                const float cs = s_cs[rr * npair + k_of], sn = s_sn[rr * npair + k_of];
+                const float o = s_raw[r * N + partner];
+                v = first ? cs * v - sn * o : sn * o + cs * v;
+            }
+            const int64_t oi = ((((int64_t)b * p.L + l0 + rr) * p.M + m) * p.H + h) * N + col;
+            m3p_st(p.io_bf16, r < TS ? p.Bo : p.Co, oi, v);
+            // the cache tail: the last token's rotated B
+            if (r < TS && l0 + rr == p.L - 1) p.kst[(((int64_t)b * p.M + m) * p.H + h) * N + col] = v;
         }
-        __syncthreads();
-        // outputs: B, C [b, l, m, h, n]; v [b, l, m, h, p]; da/gamma/scale (m == 0)
-        for (int i = t; i < 2 * nt * N; i += 256) {
-            const int which = i / (nt * N), r = (i / N) % nt, n = i % N;
-            const int64_t o = ((((int64_t)b * p.L + l0 + r) * p.M + m) * p.H + h) * N + n;
-            m3p_st(p.io_bf16, which ? p.Co : p.Bo, o, s_raw[(which * TS + r) * N + n]);
-        }
-        for (int i = t; i < nt * P; i += 256) {
-            const int r = i / P, pp = i % P;
+        // v = x mimo_x [b, l, m, h, p]; da / gamma / scale (m == 0)
+        for (int pp = t; pp < P; pp += 256) {
             const float mxv = p.mx ? p.mx[((int64_t)h * p.M + m) * P + pp] : 1.f;
-            const int64_t o = ((((int64_t)b * p.L + l0 + r) * p.M + m) * p.H + h) * P + pp;
-            m3p_st(p.io_bf16, p.v, o, m3p_ld(p, b, l0 + r, d_inner + h * P + pp) * mxv);
+            for (int r = 0; r < nt; ++r) {
+                const int64_t oi = ((((int64_t)b * p.L + l0 + r) * p.M + m) * p.H + h) * P + pp;
+                m3p_st(p.io_bf16, p.v, oi, s_x[r * P + pp] * mxv);
+            }
         }
         if (m == 0 && t < nt) {
             const int64_t o = ((int64_t)b * p.L + l0 + t) * p.H + h;
@@ -174,14 +224,10 @@ __global__ __launch_bounds__(256) void mamba3_prep_kernel(M3PrepParams p) {
             p.gm[o] = gmv;
             p.sc[o] = gmv + (1.f - s_lam[t + 1]) * s_dt[t + 1];
         }
-        // the cache tail: the last token's rotated B (per m), x and angle (m == 0)
-        if (l0 + nt == p.L) {
-            for (int n = t; n < N; n += 256)
-                p.kst[(((int64_t)b * p.M + m) * p.H + h) * N + n] = s_raw[(nt - 1) * N + n];
-            if (m == 0) {
-                for (int pp = t; pp < P; pp += 256) p.vst[bh * P + pp] = m3p_ld(p, b, p.L - 1, d_inner + h * P + pp);
-                if (t < p.A) p.ang_out[bh * p.A + t] = theta;
-            }
+        // the rest of the cache tail (m == 0): the last x and the wrapped angle
+        if (l0 + nt == p.L && m == 0) {
+            for (int pp = t; pp < P; pp += 256) p.vst[bh * P + pp] = s_x[(nt - 1) * P + pp];
+            if (t < A) p.ang_out[bh * A + t] = theta;
         }
         __syncthreads();  // LDS reuse by the next tile
     }
@@ -246,14 +292,16 @@ __global__ __launch_bounds__(256) void mamba3_finish_kernel(M3FinishParams p) {
     }
 }
 
-constexpr int kM3PrepTS = 16;
+constexpr int kM3PrepTS = 32;
 
 static int m3_prep_params(const mamba3_prep_args* a, M3PrepParams* out) {
     MAMBA_CHECK_ARG(a != nullptr, "args is NULL");
     MAMBA_CHECK_ARG(a->batch > 0 && a->seqlen > 0 && a->nheads > 0 && a->headdim > 0 && a->ngroups > 0,
                     "sizes must be >= 1");
     MAMBA_CHECK_ARG(a->nheads % a->ngroups == 0, "nheads must be a multiple of ngroups");
-    MAMBA_CHECK_ARG(a->dstate >= 2 && a->dstate <= 256 && a->dstate % 2 == 0, "dstate must be even, <= 256");
+    MAMBA_CHECK_ARG(a->dstate == 8 || a->dstate == 16 || a->dstate == 32 || a->dstate == 64 || a->dstate == 128 ||
+                        a->dstate == 256,
+                    "dstate must be one of 8, 16, 32, 64, 128, 256");
     MAMBA_CHECK_ARG(a->headdim <= 1024, "headdim <= 1024 required");
     MAMBA_CHECK_ARG(a->mimo >= 1 && a->mimo <= 16, "mimo must be in [1, 16]");
     MAMBA_CHECK_ARG(a->rope_dim >= 0 && a->rope_dim <= a->dstate && a->rope_dim % 2 == 0,
@@ -293,10 +341,27 @@ extern "C" int mamba3_prep_fwd(const mamba3_prep_args* a, mamba_stream_t stream)
     hipStream_t s = (hipStream_t)stream;
     hipLaunchKernelGGL(mamba3_seed_kernel, dim3(p.nb * p.H), dim3(256), 0, s, p);
     MAMBA_CHECK_LAUNCH();
-    constexpr int TS = kM3PrepTS;
     const int npair = p.R / 2;
-    const size_t lds = (size_t)(2 * TS * p.N + 2 * TS * npair) * sizeof(float);
-    hipLaunchKernelGGL(mamba3_prep_kernel<TS>, dim3(p.nb * p.H * p.M), dim3(256), lds, s, p);
+    auto lds_of = [&](int ts) {
+        return (size_t)(2 * ts * p.N + 2 * ts * npair + ts * p.A + ts * p.P) * sizeof(float);
+    };
+    // wide tiles while the dynamic LDS stays within 64 KB
+    const bool wide = lds_of(kM3PrepTS) <= 64 * 1024;
+    const dim3 grid(p.nb * p.H * p.M), block(256);
+#define MAMBA3_PREP_N(NN)                                                                                        \
+    if (wide)                                                                                                    \
+        hipLaunchKernelGGL((mamba3_prep_kernel<kM3PrepTS, NN>), grid, block, lds_of(kM3PrepTS), s, p);          \
+    else                                                                                                         \
+        hipLaunchKernelGGL((mamba3_prep_kernel<8, NN>), grid, block, lds_of(8), s, p);
+    switch (p.N) {
+        case 8: MAMBA3_PREP_N(8) break;
+        case 16: MAMBA3_PREP_N(16) break;
+        case 32: MAMBA3_PREP_N(32) break;
+        case 64: MAMBA3_PREP_N(64) break;
+        case 128: MAMBA3_PREP_N(128) break;
+        default: MAMBA3_PREP_N(256) break;
+    }
+#undef MAMBA3_PREP_N
     MAMBA_CHECK_LAUNCH();
     return MAMBA_OK;
 }
