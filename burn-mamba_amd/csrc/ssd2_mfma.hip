@@ -37,28 +37,8 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kMaxQ = 256;
 
-// Tuning constants of the scan kernel (compile-time; the defaults are the
-// measured best on MI355X for the 2.7B-layer shape).
-#ifndef MAMBA_SSD2_CB_RING
-#define MAMBA_SSD2_CB_RING 4  // in-flight C.B^T fragments per wave (2 or 4)
-#endif
-#ifndef MAMBA_SSD2_B_RING
-#define MAMBA_SSD2_B_RING 4   // in-flight B fragments per wave in the state GEMM
-#endif
-#ifndef MAMBA_SSD2_STATE_UNROLL
-#define MAMBA_SSD2_STATE_UNROLL 16  // must be a multiple of MAMBA_SSD2_B_RING
-#endif
 #ifndef MAMBA_SSD2_L2_WARM
 #define MAMBA_SSD2_L2_WARM 1  // touch the next chunk's group operands ahead of use
-#endif
-#ifndef MAMBA_SSD2_B_F32
-#define MAMBA_SSD2_B_F32 0    // B fragments of the state GEMM stored in f32 (else bf16)
-#endif
-#ifndef MAMBA_SSD2_DIAG_FACTORED
-#define MAMBA_SSD2_DIAG_FACTORED 0  // tabulated diagonal-block decay when its span allows
-#endif
-#ifndef MAMBA_SSD2_CB_BF16
-#define MAMBA_SSD2_CB_BF16 1  // C.B^T fragments stored in bf16 (else f32)
 #endif
 
 __device__ __forceinline__ f32x16_t mfma32x32x16(bf16x8_t a, bf16x8_t b, f32x16_t c) {
@@ -97,39 +77,22 @@ __device__ __forceinline__ f32x16_t zero16() {
     return z;
 }
 
-// One lane's C.B^T fragment (8 consecutive k) in the workspace
-#if MAMBA_SSD2_CB_BF16
-typedef bf16_t cb_t;
-constexpr int kCbLane = 8;  // elements per lane in a fragment block
-struct CbFrag { uint4 v; };
-__device__ __forceinline__ CbFrag cb_load(const cb_t* q) { return {*(const uint4*)q}; }
-__device__ __forceinline__ void cb_unpack(const CbFrag& f, float* o) { unpack8(f.v, o); }
-#else
-typedef float cb_t;
-constexpr int kCbLane = 4;
-struct CbFrag { float4 a, b; };
-__device__ __forceinline__ CbFrag cb_load(const cb_t* q) { return {*(const float4*)q, *(const float4*)(q + 256)}; }
-__device__ __forceinline__ void cb_unpack(const CbFrag& f, float* o) {
-    o[0] = f.a.x; o[1] = f.a.y; o[2] = f.a.z; o[3] = f.a.w; o[4] = f.b.x; o[5] = f.b.y; o[6] = f.b.z; o[7] = f.b.w;
-}
-#endif
-
 // ------------------------------------------------ per-group operand prep --
 // Per (batch, chunk, group) -- shared by every head of the group -- write the
 // MFMA B operands of the scan kernel in fragment order, so that each wave
 // load there is one contiguous 1 KB read:
-//   cbf[it][ks][plane][lane][4] f32 : (C.B^T)[i = 32 it + lane%32][j = 16 ks + 8 (lane/32) + 4 plane + e]
-//   cf [it][kn][lane][8]     bf16   : C[i = 32 it + lane%32][n = 16 kn + 8 (lane/32) + e]
-//   bf [nt][ks][plane][lane][4] f32 : B[j = 16 ks + 8 (lane/32) + 4 plane + e][n = 32 nt + lane%32]
-//      (or [nt][ks][lane][8] bf16 when MAMBA_SSD2_B_F32 is 0)
+//   cbf[it][ks][lane][8] : (C.B^T)[i = 32 it + lane%32][j = 16 ks + 8 (lane/32) + e]
+//   cf [it][kn][lane][8] : C[i = 32 it + lane%32][n = 16 kn + 8 (lane/32) + e]
+//   bf [nt][ks][lane][8] : B[j = 16 ks + 8 (lane/32) + e][n = 32 nt + lane%32]
+// all bf16 (the C.B^T products rounded from their f32 accumulation).
 // Positions past seqlen read as zero.  Only the causal (ks <= 2 it + 1)
 // fragments of cbf are written (K2, src/mamba2/ssd/serial.rs:170-185), and
 // inside the diagonal 32x32 blocks the entries with j > i are stored as 0.
 template <int N, int Q>
-__global__ __launch_bounds__(256) void ssd2_prep_mfma(Ssd2Params p, cb_t* cbf, bf16_t* cf, void* bfr) {
+__global__ __launch_bounds__(256) void ssd2_prep_mfma(Ssd2Params p, bf16_t* cbf, bf16_t* cf, bf16_t* bfr) {
     constexpr int T = Q / 32, NK = N / 16, KS = Q / 16, NTN = N / 32;
     constexpr int NTILE = T * (T + 1) / 2;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 31, half = lane >> 5;
+    const int wave = wave_id(), lane = threadIdx.x & 63, r = lane & 31, half = lane >> 5;
     const int s = blockIdx.x, S = gridDim.x;
     const int cg = blockIdx.y, c = cg / p.G, g = cg % p.G, b = blockIdx.z;
     const int64_t grp = ((int64_t)b * p.nch + c) * p.G + g;
@@ -137,7 +100,7 @@ __global__ __launch_bounds__(256) void ssd2_prep_mfma(Ssd2Params p, cb_t* cbf, b
     const bf16_t* Bg = (const bf16_t*)p.Bm + (int64_t)b * p.B_sb + (int64_t)g * p.B_sg;
     // (C.B^T)^T tiles: D[j][i] = sum_n B[j][n] C[i][n]; the lane then holds
     // column i = 32 it + r at rows j = 32 jt + 8 q + 4 half + u (v = 4 q + u)
-    cb_t* cbase = cbf + grp * Q * Q;
+    bf16_t* cbase = cbf + grp * Q * Q;
     for (int tile = s + S * wave; tile < NTILE; tile += 4 * S) {
         int it = 0;
         while ((it + 1) * (it + 2) / 2 <= tile) ++it;
@@ -159,7 +122,6 @@ __global__ __launch_bounds__(256) void ssd2_prep_mfma(Ssd2Params p, cb_t* cbf, b
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int ks = 2 * jt + (q >> 1), lp = r + 32 * (q & 1);
-#if MAMBA_SSD2_CB_BF16
             // fragment (it, ks), lane lp, elements 4 half .. 4 half + 3
             uint2 pk;
             pk.x = (uint32_t)__builtin_bit_cast(bf16_t, (__bf16)acc[4 * q]) |
@@ -167,10 +129,6 @@ __global__ __launch_bounds__(256) void ssd2_prep_mfma(Ssd2Params p, cb_t* cbf, b
             pk.y = (uint32_t)__builtin_bit_cast(bf16_t, (__bf16)acc[4 * q + 2]) |
                    ((uint32_t)__builtin_bit_cast(bf16_t, (__bf16)acc[4 * q + 3]) << 16);
             *(uint2*)(cbase + ((int64_t)(it * KS + ks) * 64 + lp) * 8 + 4 * half) = pk;
-#else
-            const float4 val = make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
-            *(float4*)(cbase + (((int64_t)(it * KS + ks) * 2 + half) * 64 + lp) * 4) = val;
-#endif
         }
     }
     bf16_t* cbase2 = cf + grp * (int64_t)Q * N;
@@ -180,11 +138,7 @@ __global__ __launch_bounds__(256) void ssd2_prep_mfma(Ssd2Params p, cb_t* cbf, b
         *(uint4*)(cbase2 + ((int64_t)f * 64 + lane) * 8) =
             ld16(Cg + (int64_t)t * p.C_sl + kn * 16 + 8 * half, t < p.L);
     }
-#if MAMBA_SSD2_B_F32
-    float* bbase = (float*)bfr + grp * (int64_t)Q * N;
-#else
-    bf16_t* bbase = (bf16_t*)bfr + grp * (int64_t)Q * N;
-#endif
+    bf16_t* bbase = bfr + grp * (int64_t)Q * N;
     for (int f = s + S * wave; f < NTN * KS; f += 4 * S) {
         const int nt = f / KS, ks = f % KS;
         const int n = nt * 32 + r;
@@ -194,17 +148,9 @@ __global__ __launch_bounds__(256) void ssd2_prep_mfma(Ssd2Params p, cb_t* cbf, b
             const int t = c * Q + ks * 16 + 8 * half + e;
             raw[e] = t < p.L ? (uint32_t)Bg[(int64_t)t * p.B_sl + n] : 0u;
         }
-#if MAMBA_SSD2_B_F32
-        float* dst = bbase + (int64_t)f * 512 + lane * 4;
-        *(float4*)dst = make_float4(__uint_as_float(raw[0] << 16), __uint_as_float(raw[1] << 16),
-                                    __uint_as_float(raw[2] << 16), __uint_as_float(raw[3] << 16));
-        *(float4*)(dst + 256) = make_float4(__uint_as_float(raw[4] << 16), __uint_as_float(raw[5] << 16),
-                                            __uint_as_float(raw[6] << 16), __uint_as_float(raw[7] << 16));
-#else
         *(uint4*)(bbase + ((int64_t)f * 64 + lane) * 8) =
             make_uint4(raw[0] | (raw[1] << 16), raw[2] | (raw[3] << 16), raw[4] | (raw[5] << 16),
                        raw[6] | (raw[7] << 16));
-#endif
     }
 }
 
@@ -216,45 +162,60 @@ __device__ __forceinline__ int itile_owner(int it) {
 // ----------------------------------------------- K1 + K3 + K4 + K5 fused --
 // One workgroup (4 waves) per (batch, head[, headdim half]); chunks in order.
 // N = dstate, Q = chunk length (multiple of 32, <= 256), PT = 32-wide headdim
-// tiles per workgroup (2: the whole headdim 64; 1: one half).
+// tiles per workgroup (2: the whole headdim 64; 1: one half).  Every
+// group-shared fragment a wave loads feeds PT MFMAs.
+//
+// The chunk is cut into 32-position blocks k = 0 .. T-1 ending at e_k = 32k+31
+// (cs_{e_-1} = 0 is the chunk start).  Every decay is carried by x and by a
+// scalar recurrence, so that the group-shared fragments (C.B^T, C, B) enter
+// the MFMAs exactly as the prep stored them, with no per-element work:
+//   xg_j = x_j dt_j exp(cs_{e_k} - cs_j)          (j in block k; factor <= 1)
+//   F_k  = exp(cs_{e_k} - cs_{e_{k-1}})           (block decay; <= 1)
+//   S_k[i] = sum_{j in k} (C_i.B_j) xg_j           (raw C.B^T fragments)
+// Output block `it` is then a Horner recurrence over the blocks before it,
+//   acc = C_i.h_in;  acc = acc F_k + S_k  (k = 0 .. it)
+//   y_i = exp(cs_i - cs_{e_it}) acc + D x_i
+// and the chunk state is the same recurrence over all T blocks with the raw B
+// fragments,  h <- h F_k + sum_{j in k} xg_j (x) B_j.
+// Only xg is kept in LDS.  D x_i is taken from it as D xg_i / g_i (g_i =
+// dt_i exp(cs_{e_it} - cs_i)) when every g_i of the tile is at least 2^-100,
+// and from the raw x rows otherwise (dt = 0 included).  The output's last
+// factor exp(cs_i - cs_{e_it}) is >= 1 and xg_j of the diagonal block can be
+// as small as exp(cs_{e_it} - cs_{e_{it-1}}); when that block decay exceeds
+// 2^-64 (a steep block) the diagonal block instead uses the exact per-element
+// weight dt_j exp(cs_i - cs_j) on the raw x rows, after scaling acc by
+// exp(cs_i - cs_{e_{it-1}}) <= 1.  Raw x is read back from global memory
+// (the chunk was just streamed through L2) on those rare paths only.
 //
 // Outputs are computed transposed, y^T[p, i] (i = time along MFMA columns),
 // so every per-time factor is a per-lane scalar and the four consecutive
-// headdim values a lane holds are stored as one 8-byte write.  For output
-// time i in 32-row block it (r0 = 32*it), with e_i = exp(cs_i - cs_r0) <= 1:
-//   y_i = e_i [ exp(cs_r0) (h_in . C_i) + sum_{j < r0} x_j (C_i.B_j) f_it[j] ]
-//         + sum_{r0 <= j <= i} x_j (C_i.B_j) dt_j exp(cs_i - cs_j) + D x_i
-// where f_it[j] = dt_j exp(cs_r0 - cs_j) <= dt_j is tabulated per chunk in
-// LDS (s_f); all these factors are <= 1.  The diagonal block uses the same
-// form, with fd[j] = dt_j exp(cs_r0 - cs_j) for r0 <= j (now >= dt_j) and D/e_i
-// on its diagonal, whenever the block's decay span cs_r0 - cs_{r0+31} keeps
-// both bounded (< 2^60); otherwise it falls back to the exact exponent
-// exp(cs_i - cs_j), accumulated after the e_i scaling.
+// headdim values a lane holds are stored as one 8-byte write.
 template <int N, int Q, int PT>
-__global__ __launch_bounds__(256, 2) void ssd2_scan_mfma(Ssd2Params p, const cb_t* cbf,
-                                                         const bf16_t* cf, const void* bfr) {
-    constexpr int T = Q / 32;                 // i-tiles per chunk
+__global__ __launch_bounds__(256, 3) void ssd2_scan_mfma(Ssd2Params p, const bf16_t* cbf, const bf16_t* cf,
+                                                         const bf16_t* bfr) {
+    constexpr int T = Q / 32;                 // 32-position blocks per chunk
     constexpr int NTN = N / 32;               // n tiles of the state
     constexpr int NST = PT * NTN;             // state tiles per workgroup
     constexpr int SPW = NST >= 4 ? NST / 4 : 1;  // state tiles per wave
-    constexpr int XP = Q + 8;                 // s_xT row pitch (bf16)
+    constexpr int XP = Q + 8;                 // s_xg row pitch (bf16)
     constexpr int HP = N + 8;                 // s_h row pitch (bf16)
     constexpr int PV = PT * 4;                // 8-wide headdim vectors per time row
     constexpr int XITEMS = (Q / 2) * PV;      // x staging items (2 time rows each)
     constexpr int XPT = (XITEMS + 255) / 256; // items per thread
+    constexpr int JPM = 256 / PV;             // time-row pairs between a thread's items
+    static_assert(256 % PV == 0, "a thread's items share its headdim vector");
     constexpr int NK = N / 16, KS = Q / 16;
-    constexpr int YP = PT * 32 + 8;           // s_y row pitch (bf16)
+    constexpr int CR = NK < 4 ? NK : 4;       // C fragment ring depth
+    constexpr float kSteep = 64.f;            // log2 of the largest block decay factored
+    constexpr float kTinyG = 0x1p-100f;       // smallest g_i for D x from xg
     __shared__ __align__(16) float s_cs2[Q];
-    __shared__ __align__(16) float s_w[Q];
-    __shared__ __align__(16) float s_fd[Q];
     __shared__ __align__(16) float s_dt[Q];
+    __shared__ __align__(16) float s_F[T];
     __shared__ float s_red[4];
-    __shared__ __align__(16) float s_f[T > 1 ? T - 1 : 1][Q];
-    __shared__ __align__(16) bf16_t s_xT[PT * 32][XP];
+    __shared__ __align__(16) bf16_t s_xg[PT * 32][XP];  // xg^T (block-scaled x)
     __shared__ __align__(16) bf16_t s_h[PT * 32][HP];
-    __shared__ __align__(16) bf16_t s_y[4][32][YP];  // per-wave y tile staging
 
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 31, half = lane >> 5;
+    const int wave = wave_id(), lane = threadIdx.x & 63, r = lane & 31, half = lane >> 5;
     // XCD-aware work mapping: consecutive work items (same batch, neighbouring
     // heads, sharing B/C/CB) land on the same XCD and its L2.
     constexpr int splits = 2 / PT;
@@ -277,18 +238,23 @@ __global__ __launch_bounds__(256, 2) void ssd2_scan_mfma(Ssd2Params p, const cb_
         st_pt[k] = s / NTN;
         st_nt[k] = s % NTN;
     }
+    // state element (p, n) of this lane's register v in tile k sits at
+    // (p0 + 32 st_pt + 4 half + r_v, 32 st_nt + r) with r_v = 8 (v / 4) + v % 4:
+    // one row offset per tile plus compile-time offsets
     f32x16_t hacc[SPW];
     const int64_t hbase = ((int64_t)b * p.H + h) * 64 * N;
+    auto hoff = [&](int k) { return (int64_t)(p0 + st_pt[k] * 32 + 4 * half) * N + st_nt[k] * 32 + r; };
 #pragma unroll
     for (int k = 0; k < SPW; ++k) {
+        const float* h0t = p.h0 ? p.h0 + hbase + hoff(k) : nullptr;
+        const float* hit = p.init_hpr ? p.init_hpr + (int64_t)h * 64 * N + hoff(k) : nullptr;
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-            const int pp = p0 + st_pt[k] * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-            const int n = st_nt[k] * 32 + r;
+            const int rv = (8 * (v >> 2) + (v & 3)) * N;
             float val = 0.f;
             if (st_ok[k]) {
-                if (p.h0) val = p.h0[hbase + pp * N + n];
-                if (p.init_hpr) val += p.init_hpr[(int64_t)h * 64 * N + pp * N + n];
+                if (h0t) val = h0t[rv];
+                if (hit) val += hit[rv];
             }
             hacc[k][v] = val;
         }
@@ -307,31 +273,37 @@ __global__ __launch_bounds__(256, 2) void ssd2_scan_mfma(Ssd2Params p, const cb_
     const bf16_t* xhead = X + (int64_t)b * p.x_sb + (int64_t)h * p.x_sh + p0;
     const float* dthead = p.dt + (int64_t)b * p.dt_sb + (int64_t)h * p.dt_sh;
     bf16_t* yhead = Y + (int64_t)b * p.y_sb + (int64_t)h * p.y_sh + p0;
+    const uint32_t xrow = (uint32_t)p.x_sl * 2u;
+    // x staging item m of this thread: time rows 2 (jpt + JPM m) + {0, 1}, headdim vector pv
+    const int jpt = threadIdx.x / PV, pvt = threadIdx.x % PV;
 
-    // register prefetch of the next chunk's x rows and dt
+    // register prefetch of the next chunk's x rows and dt; buffer loads past
+    // the sequence end read as zero
     uint4 xq[XPT][2];
     float dtq = 0.f;
     auto fetch = [&](int c) {
+        const uint32_t rows = (uint32_t)max(0, min(Q, p.L - c * Q));
+        const __amdgpu_buffer_rsrc_t rx = buf_rsrc(xhead + (int64_t)c * Q * p.x_sl, rows * xrow);
+        const uint32_t off0 = (uint32_t)(2 * jpt) * xrow + pvt * 16;
 #pragma unroll
         for (int m = 0; m < XPT; ++m) {
-            const int item = threadIdx.x + 256 * m;
-            const int jp = item / PV, pv = item % PV;
-            const int t0 = c * Q + 2 * jp;
-            const bool ok = item < XITEMS;
-            xq[m][0] = ld16(xhead + (int64_t)t0 * p.x_sl + pv * 8, ok && t0 < p.L);
-            xq[m][1] = ld16(xhead + (int64_t)(t0 + 1) * p.x_sl + pv * 8, ok && t0 + 1 < p.L);
+            if (XITEMS % 256 == 0 || (int)threadIdx.x + 256 * m < XITEMS) {
+                xq[m][0] = buf_ld16(rx, off0, (uint32_t)(2 * JPM * m) * xrow);
+                xq[m][1] = buf_ld16(rx, off0, (uint32_t)(2 * JPM * m + 1) * xrow);
+            }
         }
-        const int tt = c * Q + threadIdx.x;
-        dtq = (threadIdx.x < Q && tt < p.L) ? dthead[(int64_t)tt * p.dt_sl] : 0.f;
+        const __amdgpu_buffer_rsrc_t rd =
+            buf_rsrc(dthead + (int64_t)c * Q * p.dt_sl, rows * (uint32_t)p.dt_sl * 4u);
+        dtq = threadIdx.x < Q ? buf_ld4(rd, threadIdx.x * (uint32_t)p.dt_sl * 4u) : 0.f;
     };
     fetch(0);
     // L2 warm-up of the next chunk's group operands: the H/G heads (x headdim
     // splits) of a group share them and sit on one XCD, so each workgroup
     // touches one slice of the group's lines, one dword per line
-    constexpr int FL = 512 * (int)sizeof(cb_t) / 128;  // 128-byte lines per C.B^T fragment
+    constexpr int FL = 512 * 2 / 128;           // 128-byte lines per fragment
     constexpr int CB_LINES = FL * T * (T + 1);  // causal C.B^T fragments (row it: 2 it + 2 of them)
-    constexpr int FR_LINES = Q * N * 2 / 128;   // C fragments (bf16)
-    constexpr int GRP_LINES = CB_LINES + (MAMBA_SSD2_B_F32 ? 3 : 2) * FR_LINES;  // + B fragments
+    constexpr int FR_LINES = Q * N * 2 / 128;   // C (or B) fragments
+    constexpr int GRP_LINES = CB_LINES + 2 * FR_LINES;
     const int nslice = (p.H / p.G) * splits;
     const int slice = (h % (p.H / p.G)) * splits + ph;
     const int pf_line = (int)(((int64_t)GRP_LINES * slice) / nslice) + threadIdx.x;
@@ -350,23 +322,10 @@ __global__ __launch_bounds__(256, 2) void ssd2_scan_mfma(Ssd2Params p, const cb_
     uint32_t pf = 0u, pf_sink = 0u;
 
     for (int c = 0; c < p.nch; ++c) {
-        // ---- commit prefetched x -> s_xT[p][j] (time-major) and K1 cumsum
-#pragma unroll
-        for (int m = 0; m < XPT; ++m) {
-            const int item = threadIdx.x + 256 * m;
-            if (item < XITEMS) {
-                const int jp = item / PV, pv = item % PV;
-                const uint32_t a0[4] = {xq[m][0].x, xq[m][0].y, xq[m][0].z, xq[m][0].w};
-                const uint32_t a1[4] = {xq[m][1].x, xq[m][1].y, xq[m][1].z, xq[m][1].w};
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    *(uint32_t*)&s_xT[pv * 8 + 2 * k][2 * jp] = (a0[k] & 0xffffu) | (a1[k] << 16);
-                    *(uint32_t*)&s_xT[pv * 8 + 2 * k + 1][2 * jp] =
-                        (a0[k] >> 16) | (a1[k] & 0xffff0000u);
-                }
-            }
-        }
+        pf_sink += pf;  // the previous chunk's warm-up load, long complete
+        // ---- dt and the K1 cumsum (log2 units) of this chunk
         const float dtv = dtq;  // dt of position threadIdx.x of this chunk
+        if (threadIdx.x < Q) s_dt[threadIdx.x] = dtv;
         {
             float v = wave_incl_scan(dtv * A2);
             if (lane == 63) s_red[wave] = v;
@@ -377,242 +336,250 @@ __global__ __launch_bounds__(256, 2) void ssd2_scan_mfma(Ssd2Params p, const cb_
             if (threadIdx.x < Q) s_cs2[threadIdx.x] = v;
         }
         __syncthreads();
-        const float cs2_end = s_cs2[Q - 1];
-        // chunk-state weights dt_j exp(cs_end - cs_j) and the decay table
-        if (threadIdx.x < Q) {
-            const int j = threadIdx.x;
-            const float csj = s_cs2[j];
-            s_w[j] = dtv * __builtin_amdgcn_exp2f(cs2_end - csj);
-            s_fd[j] = dtv * __builtin_amdgcn_exp2f(s_cs2[j & ~31] - csj);
-            s_dt[j] = dtv;
-            // decay table of the strictly-lower blocks: row block it > j / 32
+        // ---- block-scaled x -> s_xg[p][j] (time-major), block decays -> s_F
 #pragma unroll
-            for (int it = 1; it < T; ++it)
-                if (j < it * 32) s_f[it - 1][j] = dtv * __builtin_amdgcn_exp2f(s_cs2[it * 32] - csj);
+        for (int m = 0; m < XPT; ++m) {
+            if (XITEMS % 256 == 0 || (int)threadIdx.x + 256 * m < XITEMS) {
+                const int pv = pvt, j0 = 2 * (jpt + JPM * m);
+                const float ce = s_cs2[j0 | 31];
+                const float g0 = s_dt[j0] * __builtin_amdgcn_exp2f(ce - s_cs2[j0]);
+                const float g1 = s_dt[j0 + 1] * __builtin_amdgcn_exp2f(ce - s_cs2[j0 + 1]);
+                const uint32_t a0[4] = {xq[m][0].x, xq[m][0].y, xq[m][0].z, xq[m][0].w};
+                const uint32_t a1[4] = {xq[m][1].x, xq[m][1].y, xq[m][1].z, xq[m][1].w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    *(uint32_t*)&s_xg[pv * 8 + 2 * k][j0] =
+                        pack_bf16x2(__uint_as_float(a0[k] << 16) * g0, __uint_as_float(a1[k] << 16) * g1);
+                    *(uint32_t*)&s_xg[pv * 8 + 2 * k + 1][j0] =
+                        pack_bf16x2(__uint_as_float(a0[k] & 0xffff0000u) * g0,
+                                    __uint_as_float(a1[k] & 0xffff0000u) * g1);
+                }
+            }
+        }
+        if (threadIdx.x < T) {
+            const int k = threadIdx.x;
+            s_F[k] = __builtin_amdgcn_exp2f(s_cs2[32 * k + 31] - (k ? s_cs2[32 * k - 1] : 0.f));
         }
         __syncthreads();
 
-        pf_sink += pf;
-
-        // ---- K2 + K5: y^T for the i-tiles this wave owns
+        // ---- K2 + K5: y^T for the i-tiles this wave owns.  No global access
+        // of a tile sits under a branch except on the rare raw-x paths: the
+        // C.B^T ring is refilled through a buffer clipped at the tile's last
+        // strictly-lower fragment (reads past it return zero without a memory
+        // access) and only the arithmetic of a block is skipped, on a scalar
+        // condition.  The waits on the rings are therefore exact counts.
         const int64_t grp = ((int64_t)b * p.nch + c) * p.G + g;
-        const cb_t* cbg = cbf + grp * Q * Q + lane * kCbLane;
         const bf16_t* cfg = cf + grp * (int64_t)Q * N + lane * 8;
+        const uint32_t rows_c = (uint32_t)min(Q, p.L - c * Q);
+        const __amdgpu_buffer_rsrc_t ry = buf_rsrc(yhead + (int64_t)c * Q * p.y_sl, rows_c * (uint32_t)p.y_sl * 2u);
+        const __amdgpu_buffer_rsrc_t rxc = buf_rsrc(xhead + (int64_t)c * Q * p.x_sl, rows_c * xrow);
 #pragma unroll 1
-        for (int it = 0; it < T; ++it) {
-            if (itile_owner(it) != wave) continue;
+        for (int q = 0; q < 2; ++q) {
+            const int it = q ? 7 - wave : wave;  // the snake pair {w, 7 - w}
+            if (it >= T || (q && it == wave)) continue;
             const int il = it * 32 + r;  // this lane's output time (B-operand column)
-            // issue every global load of this tile before the first wait:
-            // the C fragments (inter-chunk term) and a ring of CB fragments
-            uint4 craw[NK];
+            // issue the first global loads of this tile before the first wait:
+            // a ring of C fragments (inter-chunk term), the diagonal block and
+            // two blocks of strictly-lower C.B^T fragments
+            const bf16_t* ctile = cfg + (int64_t)it * NK * 512;
+            uint4 cr[CR];
 #pragma unroll
-            for (int kn = 0; kn < NK; ++kn) craw[kn] = *(const uint4*)(cfg + (int64_t)(it * NK + kn) * 512);
-            const cb_t* cbt = cbg + (int64_t)it * KS * 512;  // fragment (it, ks) at + ks * 512
-            const int nb = 2 * it;    // strictly-lower k-steps (even)
-            const int ntot = nb + 2;  // + the diagonal block
-            constexpr int RD = MAMBA_SSD2_CB_RING;  // CB fragment ring depth
-            CbFrag ring[RD];
+            for (int k = 0; k < CR; ++k) cr[k] = *(const uint4*)(ctile + k * 512);
+            const bf16_t* cbrow = cbf + grp * Q * Q + (int64_t)it * KS * 512;
+            const uint32_t loff = lane * 16u;
+            const uint4 dg0 = *(const uint4*)(cbrow + (2 * it) * 512 + lane * 8);
+            const uint4 dg1 = *(const uint4*)(cbrow + (2 * it + 1) * 512 + lane * 8);
+            const __amdgpu_buffer_rsrc_t rcb = buf_rsrc(cbrow, (uint32_t)(2 * it) * 1024u);
+            uint4 ring[4];
 #pragma unroll
-            for (int k = 0; k < RD; ++k)
-                if (k < ntot) ring[k] = cb_load(cbt + k * 512);
-            const float cs2_i = s_cs2[il];
-            const float cs2_r0 = s_cs2[it * 32];
+            for (int k = 0; k < 4; ++k) ring[k] = buf_ld16(rcb, k * 1024u + loff);
             f32x16_t yacc[PT];
 #pragma unroll
             for (int pt = 0; pt < PT; ++pt) yacc[pt] = zero16();
             // inter-chunk term h_in . C_i^T with raw C rows as the B operand
 #pragma unroll
             for (int ks = 0; ks < NK; ++ks) {
-                const bf16x8_t bop = as_bf16x8(craw[ks]);
+                const bf16x8_t bop = as_bf16x8(cr[ks % CR]);
+                if (ks + CR < NK) cr[ks % CR] = *(const uint4*)(ctile + (ks + CR) * 512);
 #pragma unroll
                 for (int pt = 0; pt < PT; ++pt) {
                     const bf16x8_t a = *(const bf16x8_t*)&s_h[pt * 32 + r][ks * 16 + 8 * half];
                     yacc[pt] = mfma32x32x16(a, bop, yacc[pt]);
                 }
             }
-            {
-                const float sc = __builtin_amdgcn_exp2f(cs2_r0);
+            // Horner over the strictly-lower blocks: acc <- acc F_jt + S_jt;
+            // block jt's fragments sit in ring slots 2 (jt % 2), refilled two
+            // blocks ahead.  A block's LDS reads are issued before its scaling,
+            // which covers their latency.
+#pragma unroll
+            for (int jt = 0; jt < T - 1; ++jt) {
+                if (jt < it) {
+                    const float F = s_F[jt];
+                    bf16x8_t a[2][PT];
+#pragma unroll
+                    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                        for (int pt = 0; pt < PT; ++pt)
+                            a[kk][pt] = *(const bf16x8_t*)&s_xg[pt * 32 + r][(2 * jt + kk) * 16 + 8 * half];
+#pragma unroll
+                    for (int pt = 0; pt < PT; ++pt)
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) yacc[pt][v] *= F;
+#pragma unroll
+                    for (int kk = 0; kk < 2; ++kk) {
+                        const bf16x8_t bop = as_bf16x8(ring[(2 * jt + kk) % 4]);
+#pragma unroll
+                        for (int pt = 0; pt < PT; ++pt) yacc[pt] = mfma32x32x16(a[kk][pt], bop, yacc[pt]);
+                    }
+                }
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+                    const int ks = 2 * jt + kk;
+                    if (ks + 4 < KS) ring[ks % 4] = buf_ld16(rcb, (ks + 4) * 1024u + loff);
+                }
+            }
+            // diagonal block: the prep stored its upper triangle as 0
+            const float cs2_i = s_cs2[il];
+            const float cse_prev = it ? s_cs2[it * 32 - 1] : 0.f;
+            const float cse = s_cs2[it * 32 + 31];
+            const float span = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(cse_prev - cse)));
+            if (span <= kSteep) {
+                const float F = s_F[it];
+                bf16x8_t a[2][PT];
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                    for (int pt = 0; pt < PT; ++pt)
+                        a[kk][pt] = *(const bf16x8_t*)&s_xg[pt * 32 + r][it * 32 + kk * 16 + 8 * half];
+#pragma unroll
+                for (int pt = 0; pt < PT; ++pt)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) yacc[pt][v] *= F;
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+                    const bf16x8_t bop = as_bf16x8(kk ? dg1 : dg0);
+#pragma unroll
+                    for (int pt = 0; pt < PT; ++pt) yacc[pt] = mfma32x32x16(a[kk][pt], bop, yacc[pt]);
+                }
+                // y_i = exp(cs_i - cs_e) (acc + D xg_i / g_i) with exp(cs_i - cs_e) / g_i = 1 / dt_i
+                const float colf = __builtin_amdgcn_exp2f(cs2_i - cse);
+                const float dti = s_dt[il];
+                const float gi = dti * __builtin_amdgcn_exp2f(cse - cs2_i);
+                if (__all(gi >= kTinyG)) {
+                    const float dinv = Dh / dti;
+#pragma unroll
+                    for (int pt = 0; pt < PT; ++pt)
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) {
+                            const float xv = __uint_as_float(
+                                (uint32_t)s_xg[pt * 32 + 8 * (v >> 2) + 4 * half + (v & 3)][il] << 16);
+                            yacc[pt][v] = (yacc[pt][v] + dinv * xv) * colf;
+                        }
+                } else {
+                    // raw x of the lane's output row, four headdim values per load
+#pragma unroll
+                    for (int pt = 0; pt < PT; ++pt)
+#pragma unroll
+                        for (int gq = 0; gq < 4; ++gq) {
+                            const uint2 xr =
+                                buf_ld8(rxc, ((uint32_t)il * (uint32_t)p.x_sl + pt * 32 + 8 * gq + 4 * half) * 2u);
+                            const float xv[4] = {__uint_as_float(xr.x << 16), __uint_as_float(xr.x & 0xffff0000u),
+                                                 __uint_as_float(xr.y << 16), __uint_as_float(xr.y & 0xffff0000u)};
+#pragma unroll
+                            for (int u = 0; u < 4; ++u)
+                                yacc[pt][4 * gq + u] = yacc[pt][4 * gq + u] * colf + Dh * xv[u];
+                        }
+                }
+            } else {
+                // steep block: bring acc to position i (factor <= 1), then the
+                // exact weights dt_j exp(cs_i - cs_j) (+ D on the diagonal) on raw x
+                const float sc = __builtin_amdgcn_exp2f(cs2_i - cse_prev);
 #pragma unroll
                 for (int pt = 0; pt < PT; ++pt)
 #pragma unroll
                     for (int v = 0; v < 16; ++v) yacc[pt][v] *= sc;
-            }
-            // strictly-lower blocks: B operand (C_i.B_j) f_it[j]
-            for (int ks0 = 0; ks0 < nb; ks0 += RD) {
-#pragma unroll
-                for (int k = 0; k < RD; ++k) {
-                    const int ks = ks0 + k;
-                    if (ks < nb) {
-                        const int j0 = ks * 16 + 8 * half;
-                        float cv[8];
-                        cb_unpack(ring[k], cv);
-                        if (ks + RD < ntot) ring[k] = cb_load(cbt + (ks + RD) * 512);
-                        const float4 f0 = *(const float4*)&s_f[it - 1][j0];
-                        const float4 f1 = *(const float4*)&s_f[it - 1][j0 + 4];
-                        const float m[8] = {cv[0] * f0.x, cv[1] * f0.y, cv[2] * f0.z, cv[3] * f0.w,
-                                            cv[4] * f1.x, cv[5] * f1.y, cv[6] * f1.z, cv[7] * f1.w};
-                        const bf16x8_t bop = pack8(m);
-#pragma unroll
-                        for (int pt = 0; pt < PT; ++pt) {
-                            const bf16x8_t a = *(const bf16x8_t*)&s_xT[pt * 32 + r][j0];
-                            yacc[pt] = mfma32x32x16(a, bop, yacc[pt]);
-                        }
-                    }
-                }
-            }
-            // diagonal block: its two CB fragments sit in ring slots nb % RD and
-            // nb % RD + 1 (nb is even).  The prep stored its upper triangle as 0.
-            static_assert(RD == 2 || RD == 4, "ring depth 2 or 4");
-            CbFrag dg[2];
-            if (RD == 2 || (nb & 3) == 0) {
-                dg[0] = ring[0]; dg[1] = ring[1];
-            } else {
-                dg[0] = ring[RD - 2]; dg[1] = ring[RD - 1];
-            }
-            const float ei = __builtin_amdgcn_exp2f(cs2_i - cs2_r0);
-            const float span = cs2_r0 - s_cs2[it * 32 + 31];
-            if (MAMBA_SSD2_DIAG_FACTORED && span < 60.f) {
-                // bounded: (C_i.B_j) fd[j] (+ D / e_i on the diagonal), then scale by e_i
-                const float dei = Dh / ei;
-#pragma unroll
-                for (int kk = 0; kk < 2; ++kk) {
-                    const int j0 = it * 32 + kk * 16 + 8 * half;
-                    float cv[8];
-                    cb_unpack(dg[kk], cv);
-                    const float4 f0 = *(const float4*)&s_fd[j0];
-                    const float4 f1 = *(const float4*)&s_fd[j0 + 4];
-                    const int d = il - j0;  // position of the diagonal in this fragment
-                    float m[8] = {cv[0] * f0.x, cv[1] * f0.y, cv[2] * f0.z, cv[3] * f0.w,
-                                  cv[4] * f1.x, cv[5] * f1.y, cv[6] * f1.z, cv[7] * f1.w};
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) m[e] += (e == d) ? dei : 0.f;
-                    const bf16x8_t bop = pack8(m);
-#pragma unroll
-                    for (int pt = 0; pt < PT; ++pt) {
-                        const bf16x8_t a = *(const bf16x8_t*)&s_xT[pt * 32 + r][j0];
-                        yacc[pt] = mfma32x32x16(a, bop, yacc[pt]);
-                    }
-                }
-#pragma unroll
-                for (int pt = 0; pt < PT; ++pt)
-#pragma unroll
-                    for (int v = 0; v < 16; ++v) yacc[pt][v] *= ei;
-            } else {
-                // steep decay inside the block: exact exponent, after the e_i scaling
-#pragma unroll
-                for (int pt = 0; pt < PT; ++pt)
-#pragma unroll
-                    for (int v = 0; v < 16; ++v) yacc[pt][v] *= ei;
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk) {
                     const int j0 = it * 32 + kk * 16 + 8 * half;
                     float cbv[8];
-                    cb_unpack(dg[kk], cbv);
+                    unpack8(kk ? dg1 : dg0, cbv);
                     float m[8];
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         const int j = j0 + e;
-                        const float dtj = s_dt[j];  // 0 past seqlen
-                        const float val = cbv[e] * dtj * __builtin_amdgcn_exp2f(cs2_i - s_cs2[j]);
+                        const float val = cbv[e] * s_dt[j] * __builtin_amdgcn_exp2f(cs2_i - s_cs2[j]);
                         m[e] = (j < il) ? val : ((j == il) ? val + Dh : 0.f);
                     }
                     const bf16x8_t bop = pack8(m);
 #pragma unroll
                     for (int pt = 0; pt < PT; ++pt) {
-                        const bf16x8_t a = *(const bf16x8_t*)&s_xT[pt * 32 + r][j0];
+                        // A operand x^T[p][j0 .. j0 + 7] for p = pt * 32 + r, from the raw rows
+                        uint32_t xw[4];
+#pragma unroll
+                        for (int e2 = 0; e2 < 4; ++e2) {
+                            const uint32_t lo = buf_ld2(rxc, ((uint32_t)(j0 + 2 * e2) * (uint32_t)p.x_sl + pt * 32 + r) * 2u);
+                            const uint32_t hi =
+                                buf_ld2(rxc, ((uint32_t)(j0 + 2 * e2 + 1) * (uint32_t)p.x_sl + pt * 32 + r) * 2u);
+                            xw[e2] = lo | (hi << 16);
+                        }
+                        const bf16x8_t a = as_bf16x8(make_uint4(xw[0], xw[1], xw[2], xw[3]));
                         yacc[pt] = mfma32x32x16(a, bop, yacc[pt]);
                     }
                 }
             }
             // store: the lane holds y[il][4 consecutive p] per group of 4
-            // registers; stage the 32 x (32 PT) tile in LDS, then write whole rows
+            // registers; rows past the sequence end are dropped by the buffer
 #pragma unroll
             for (int pt = 0; pt < PT; ++pt)
 #pragma unroll
-                for (int gq = 0; gq < 4; ++gq) {
-                    uint2 pk;
-                    pk.x = (uint32_t)__builtin_bit_cast(bf16_t, (__bf16)yacc[pt][4 * gq]) |
-                           ((uint32_t)__builtin_bit_cast(bf16_t, (__bf16)yacc[pt][4 * gq + 1]) << 16);
-                    pk.y = (uint32_t)__builtin_bit_cast(bf16_t, (__bf16)yacc[pt][4 * gq + 2]) |
-                           ((uint32_t)__builtin_bit_cast(bf16_t, (__bf16)yacc[pt][4 * gq + 3]) << 16);
-                    *(uint2*)&s_y[wave][r][pt * 32 + 8 * gq + 4 * half] = pk;
-                }
-            {
-                constexpr int CPR = PT * 4;       // 16-byte chunks per row
-                constexpr int RPI = 64 / CPR;     // rows per wave instruction
-#pragma unroll
-                for (int q = 0; q < 32 / RPI; ++q) {
-                    const int row = q * RPI + lane / CPR, ch = lane % CPR;
-                    const uint4 v = *(const uint4*)&s_y[wave][row][ch * 8];
-                    const int to = c * Q + it * 32 + row;
-                    if (to < p.L) *(uint4*)(yhead + (int64_t)to * p.y_sl + ch * 8) = v;
-                }
-            }
+                for (int gq = 0; gq < 4; ++gq)
+                    buf_st8(ry, ((uint32_t)il * (uint32_t)p.y_sl + pt * 32 + 8 * gq + 4 * half) * 2u,
+                            make_uint2(pack_bf16x2(yacc[pt][4 * gq], yacc[pt][4 * gq + 1]),
+                                       pack_bf16x2(yacc[pt][4 * gq + 2], yacc[pt][4 * gq + 3])));
         }
 
         // ---- prefetch the next chunk's x / dt (lands during the state GEMM)
-        if (c + 1 < p.nch) fetch(c + 1);
+        fetch(c + 1);  // past the last chunk every load reads zero
 
-        // ---- K3 + K4: h <- exp(cs_end) h + x^T (B o w), B fragments in a small ring
-        if (wave < NST) {  // every state tile of this wave is valid (SPW > 1 iff NST >= 8)
-            const float dec = __builtin_amdgcn_exp2f(cs2_end);
-#pragma unroll
-            for (int k = 0; k < SPW; ++k)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) hacc[k][v] *= dec;
+        // ---- K3 + K4: h <- h F_k + xg_k^T B_k over the blocks, B fragments in a ring
+        if (NST >= 4 || wave < NST) {  // every state tile of this wave is valid (SPW > 1 iff NST >= 8)
             // all state tiles of a wave share one n tile (st_nt[0]) when SPW > 1
-            constexpr int BD = MAMBA_SSD2_B_RING;  // B fragment ring depth
-#if MAMBA_SSD2_B_F32
-            const float* btf = (const float*)bfr + grp * (int64_t)Q * N + (int64_t)st_nt[0] * KS * 512 + lane * 4;
-            float4 bring[BD][2];
-#pragma unroll
-            for (int k = 0; k < BD; ++k) {
-                bring[k][0] = *(const float4*)(btf + k * 512);
-                bring[k][1] = *(const float4*)(btf + k * 512 + 256);
-            }
-#else
-            const bf16_t* btf = (const bf16_t*)bfr + grp * (int64_t)Q * N + ((int64_t)st_nt[0] * KS * 64 + lane) * 8;
+            constexpr int BD = 4;  // B fragment ring depth (two blocks)
+            const bf16_t* btf = bfr + grp * (int64_t)Q * N + ((int64_t)st_nt[0] * KS * 64 + lane) * 8;
             uint4 bring[BD];
 #pragma unroll
-            for (int k = 0; k < BD; ++k) bring[k] = *(const uint4*)(btf + k * 512);
-#endif
-#pragma unroll MAMBA_SSD2_STATE_UNROLL
-            for (int ks = 0; ks < KS; ++ks) {
-                const int j0 = ks * 16 + 8 * half;
-#if MAMBA_SSD2_B_F32
-                const float4 b0 = bring[ks % BD][0], b1 = bring[ks % BD][1];
-                if (ks + BD < KS) {
-                    bring[ks % BD][0] = *(const float4*)(btf + (ks + BD) * 512);
-                    bring[ks % BD][1] = *(const float4*)(btf + (ks + BD) * 512 + 256);
-                }
-#else
-                float bu[8];
-                unpack8(bring[ks % BD], bu);
-                if (ks + BD < KS) bring[ks % BD] = *(const uint4*)(btf + (ks + BD) * 512);
-                const float4 b0 = make_float4(bu[0], bu[1], bu[2], bu[3]);
-                const float4 b1 = make_float4(bu[4], bu[5], bu[6], bu[7]);
-#endif
-                const float4 w0 = *(const float4*)&s_w[j0];
-                const float4 w1 = *(const float4*)&s_w[j0 + 4];
-                const float bv[8] = {b0.x * w0.x, b0.y * w0.y, b0.z * w0.z, b0.w * w0.w,
-                                     b1.x * w1.x, b1.y * w1.y, b1.z * w1.z, b1.w * w1.w};
-                const bf16x8_t bop = pack8(bv);
+            for (int k = 0; k < BD; ++k)
+                if (k < KS) bring[k] = *(const uint4*)(btf + k * 512);
 #pragma unroll
-                for (int k = 0; k < SPW; ++k) {
-                    const bf16x8_t a = *(const bf16x8_t*)&s_xT[st_pt[k] * 32 + r][j0];
-                    hacc[k] = mfma32x32x16(a, bop, hacc[k]);
+            for (int jt = 0; jt < T; ++jt) {
+                const float F = s_F[jt];
+#pragma unroll
+                for (int k = 0; k < SPW; ++k)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) hacc[k][v] *= F;
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+                    const int ks = 2 * jt + kk;
+                    const bf16x8_t bop = as_bf16x8(bring[ks % BD]);
+                    if (ks + BD < KS) bring[ks % BD] = *(const uint4*)(btf + (ks + BD) * 512);
+#pragma unroll
+                    for (int k = 0; k < SPW; ++k) {
+                        const bf16x8_t a = *(const bf16x8_t*)&s_xg[st_pt[k] * 32 + r][ks * 16 + 8 * half];
+                        hacc[k] = mfma32x32x16(a, bop, hacc[k]);
+                    }
                 }
             }
         }
         // ---- warm L2 with the next chunk's group operands while the WG syncs and scans
-        if (MAMBA_SSD2_L2_WARM && c + 1 < p.nch && pf_on) {
+        if (MAMBA_SSD2_L2_WARM) {  // one unconditional load per thread
             const int64_t g1 = grp + p.G;  // (b, c + 1, g)
-            const char* blk = pf_kind == 0 ? (const char*)(cbf + g1 * Q * Q)
-                            : pf_kind == 1 ? (const char*)(cf + g1 * (int64_t)Q * N)
-                                           : (const char*)bfr + g1 * (int64_t)Q * N * (MAMBA_SSD2_B_F32 ? 4 : 2);
-            pf = *(const uint32_t*)(blk + pf_off);
+            const bf16_t* blk = pf_kind == 0 ? cbf + g1 * Q * Q
+                              : pf_kind == 1 ? cf + g1 * (int64_t)Q * N
+                                             : bfr + g1 * (int64_t)Q * N;
+            const bool warm = c + 1 < p.nch && pf_on;  // else re-touch a line of this chunk
+            pf = *(const uint32_t*)(warm ? (const char*)blk + pf_off : (const char*)(cbf + grp * Q * Q));
         }
-        __syncthreads();  // all reads of s_h / s_xT / s_cs2 / s_dt / s_w / s_f done
+        __syncthreads();  // all reads of s_h / s_xg / s_cs2 / s_dt / s_F done
 #pragma unroll
         for (int k = 0; k < SPW; ++k)
             if (st_ok[k])
@@ -627,11 +594,9 @@ __global__ __launch_bounds__(256, 2) void ssd2_scan_mfma(Ssd2Params p, const cb_
 #pragma unroll
     for (int k = 0; k < SPW; ++k) {
         if (!st_ok[k]) continue;
+        float* hTt = p.hT + hbase + hoff(k);
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int pp = p0 + st_pt[k] * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-            p.hT[hbase + pp * N + st_nt[k] * 32 + r] = hacc[k][v];
-        }
+        for (int v = 0; v < 16; ++v) hTt[(8 * (v >> 2) + (v & 3)) * N] = hacc[k][v];
     }
 }
 
@@ -646,58 +611,42 @@ bool ssd2_mfma_supported(const Ssd2Params& p) {
     const int64_t s[] = {p.x_sb, p.x_sl, p.x_sh, p.B_sb, p.B_sl, p.B_sg, p.C_sb, p.C_sl, p.C_sg};
     for (int64_t v : s)
         if (v % 8 != 0) return false;
+    // x and y rows are addressed through 32-bit buffer offsets inside one
+    // chunk, and a row must hold the whole headdim
+    if (p.x_sl < p.P || p.y_sl < p.P || p.dt_sl < 1 || (int64_t)p.Q * p.x_sl * 2 >= (1ll << 31) ||
+        (int64_t)p.Q * p.y_sl * 2 >= (1ll << 31) || (int64_t)p.Q * p.dt_sl * 4 >= (1ll << 31))
+        return false;
     return true;
 }
 
-// workspace: cbf (Q*Q f32) + cf (Q*N bf16) + bf (Q*N f32 or bf16) per (batch, chunk, group)
+// workspace: cbf (Q*Q), cf (Q*N) and bf (Q*N), all bf16, per (batch, chunk, group)
 static size_t cbf_bytes(const Ssd2Params& p) {
-    return align_up((size_t)p.nb * p.nch * p.G * p.Q * p.Q * sizeof(cb_t), 256);
+    return align_up((size_t)p.nb * p.nch * p.G * p.Q * p.Q * sizeof(bf16_t), 256);
 }
 static size_t frag_bytes(const Ssd2Params& p) {
     return align_up((size_t)p.nb * p.nch * p.G * p.N * p.Q * sizeof(bf16_t), 256);
 }
 
 size_t ssd2_mfma_workspace(const Ssd2Params& p) {
-    return cbf_bytes(p) + (MAMBA_SSD2_B_F32 ? 3 : 2) * frag_bytes(p);
+    return cbf_bytes(p) + 2 * frag_bytes(p);
 }
 
-// Headdim split.  PT = 2: one workgroup per (batch, head); PT = 1: two (one
-// per 32-wide headdim half).  Every workgroup walks the whole sequence, so the
-// launch runs in ceil(workgroups / resident slots) rounds; the per-workgroup
-// time barely depends on PT (the C.B^T decay work per chunk is the same),
-// measured at 0.94x for PT = 1 against PT = 2 at the 2.7B-layer shape.  The
-// choice minimises rounds x that relative time, with resident slots from the
-// runtime occupancy query.  MAMBA_SSD2_PSPLIT=0/1 (read on every call) forces it.
+// Headdim split.  PT = 1 (two workgroups per head, one per 32-wide headdim
+// half) measured faster than PT = 2 at every shape tried on MI355X: at the
+// 2.7B-layer shape 460 us against 535 us, both at three workgroups per CU;
+// PT = 2 needs the whole register budget and spills.  PT = 2 stays available
+// as MAMBA_SSD2_PSPLIT=0 (read on every call; 1 forces PT = 1).
 template <int N, int Q>
-static int choose_pt(const Ssd2Params& p) {
+static int choose_pt(const Ssd2Params&) {
     const char* e = getenv("MAMBA_SSD2_PSPLIT");
-    const int forced = e ? atoi(e) : -1;
-    if (forced == 0) return 2;
-    if (forced == 1) return 1;
-    static int slots1 = -1, slots2 = -1;  // resident workgroups on the device, per PT
-    if (slots1 < 0) {
-        int dev = 0, cus = 0, b1 = 0, b2 = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&b1, ssd2_scan_mfma<N, Q, 1>, 256, 0) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&b2, ssd2_scan_mfma<N, Q, 2>, 256, 0) != hipSuccess) {
-            (void)hipGetLastError();
-            return (int64_t)p.nb * p.H < 320 ? 1 : 2;
-        }
-        slots1 = (b1 > 0 ? b1 : 1) * cus;
-        slots2 = (b2 > 0 ? b2 : 1) * cus;
-    }
-    const int64_t items = (int64_t)p.nb * p.H;
-    const double cost1 = 0.94 * (double)((2 * items + slots1 - 1) / slots1);
-    const double cost2 = (double)((items + slots2 - 1) / slots2);
-    return cost1 <= cost2 ? 1 : 2;
+    return (e && atoi(e) == 0) ? 2 : 1;
 }
 
 template <int N, int Q>
 static int launch_q(const Ssd2Params& p, void* ws, hipStream_t stream, hipEvent_t ev0, hipEvent_t ev1) {
-    cb_t* cbf = (cb_t*)ws;
+    bf16_t* cbf = (bf16_t*)ws;
     bf16_t* cf = (bf16_t*)((char*)ws + cbf_bytes(p));
-    void* bfr = (void*)((char*)ws + cbf_bytes(p) + frag_bytes(p));
+    bf16_t* bfr = (bf16_t*)((char*)ws + cbf_bytes(p) + frag_bytes(p));
     const int S = 4;  // prep workgroups per (batch, chunk, group)
     hipLaunchKernelGGL((ssd2_prep_mfma<N, Q>), dim3(S, p.nch * p.G, p.nb), dim3(256), 0, stream, p, cbf,
                        cf, bfr);
@@ -705,10 +654,10 @@ static int launch_q(const Ssd2Params& p, void* ws, hipStream_t stream, hipEvent_
     if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, stream));
     if (choose_pt<N, Q>(p) == 2) {
         hipLaunchKernelGGL((ssd2_scan_mfma<N, Q, 2>), dim3(p.nb * p.H), dim3(256), 0, stream, p,
-                           (const cb_t*)cbf, (const bf16_t*)cf, (const void*)bfr);
+                           (const bf16_t*)cbf, (const bf16_t*)cf, (const bf16_t*)bfr);
     } else {
         hipLaunchKernelGGL((ssd2_scan_mfma<N, Q, 1>), dim3(p.nb * p.H * 2), dim3(256), 0, stream, p,
-                           (const cb_t*)cbf, (const bf16_t*)cf, (const void*)bfr);
+                           (const bf16_t*)cbf, (const bf16_t*)cf, (const bf16_t*)bfr);
     }
     MAMBA_CHECK_LAUNCH();
     if (ev1) MAMBA_CHECK_HIP(hipEventRecord(ev1, stream));

@@ -203,3 +203,28 @@ def test_ssd2_mfma_matches_generic_closely():
     torch.cuda.synchronize()
     np.testing.assert_allclose(yf.float().cpu().numpy(), yg.float().cpu().numpy(), **BF16_TOL)
     np.testing.assert_allclose(hf.cpu().numpy(), hg.cpu().numpy(), **BF16_TOL)
+
+
+@pytest.mark.parametrize("dt_range", [(0.02, 1.5), (0.5, 4.0)])
+def test_ssd2_mfma_steep_blocks(dt_range):
+    """Strong decay.  A 32-position block whose total decay exp(sum dt A) is
+    below 2^-64 takes the exact per-element diagonal path; the others take the
+    factored one.  Both kinds occur in these inputs (checked below) and both
+    must match the oracle, outputs and final states."""
+    import torch
+    import mamba_hip
+    b, l, h, g, q = 2, 700, 8, 2, 256
+    inp = ssd2_inputs(seed=31, b=b, l=l, h=h, p=64, g=g, n=128, h0=True, dt_range=dt_range)
+    lp = -(-l // 32) * 32
+    da2 = np.zeros((b, lp, h))
+    da2[:, :l] = inp["dt"] * inp["A"][None, None, :] * np.log2(np.e)
+    span = -da2.reshape(b, lp // 32, 32, h).sum(axis=2)
+    assert (span > 64).any()
+    if dt_range[0] < 0.1:
+        assert (span <= 64).any()
+    t = _to_dev(inp)
+    y, hT = mamba_hip.ssd2_fwd(t["x"], t["dt"], t["A"], t["B"], t["C"], t["D"], t["h0"], chunk_len=q)
+    torch.cuda.synchronize()
+    yr, hr = _oracle(inp, q, "bf16")
+    np.testing.assert_allclose(y.float().cpu().numpy(), yr, **BF16_TOL)
+    np.testing.assert_allclose(hT.cpu().numpy(), hr, **BF16_TOL)
