@@ -205,7 +205,6 @@ __global__ __launch_bounds__(256, 3) void ssd2_scan_mfma(Ssd2Params p, const bf1
     constexpr int JPM = 256 / PV;             // time-row pairs between a thread's items
     static_assert(256 % PV == 0, "a thread's items share its headdim vector");
     constexpr int NK = N / 16, KS = Q / 16;
-    constexpr int CR = NK < 4 ? NK : 4;       // C fragment ring depth
     constexpr float kSteep = 64.f;            // log2 of the largest block decay factored
     constexpr float kTinyG = 0x1p-100f;       // smallest g_i for D x from xg
     __shared__ __align__(16) float s_cs2[Q];
@@ -321,8 +320,25 @@ __global__ __launch_bounds__(256, 3) void ssd2_scan_mfma(Ssd2Params p, const bf1
     const int pf_kind = pf_line < CB_LINES ? 0 : (pf_line < CB_LINES + FR_LINES ? 1 : 2);
     uint32_t pf = 0u, pf_sink = 0u;
 
+    static_assert(NK >= 4, "the C and B fragment rings are four deep");
     for (int c = 0; c < p.nch; ++c) {
         pf_sink += pf;  // the previous chunk's warm-up load, long complete
+        // Group operands of this chunk.  `cr` carries the first four fragments
+        // of the wave's next phase, loaded one phase ahead: here those of its
+        // first tile's C (or, with no tile, of its state GEMM's B); then, from
+        // a tile's inter-chunk term, those of the following tile or of the
+        // state GEMM.  Fragment indices are clamped inside the operand.
+        const int64_t grp = ((int64_t)b * p.nch + c) * p.G + g;
+        const bf16_t* cfg = cf + grp * (int64_t)Q * N + lane * 8;
+        const bf16_t* btf = bfr + grp * (int64_t)Q * N + ((int64_t)st_nt[0] * KS * 64 + lane) * 8;
+        uint4 cr[4];
+        {
+            const bool has_tile = wave < T;
+            const bf16_t* nxt = has_tile ? cfg + (int64_t)wave * NK * 512 : btf;
+            const int lim = has_tile ? NK : KS;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) cr[k] = *(const uint4*)(nxt + min(k, lim - 1) * 512);
+        }
         // ---- dt and the K1 cumsum (log2 units) of this chunk
         const float dtv = dtq;  // dt of position threadIdx.x of this chunk
         if (threadIdx.x < Q) s_dt[threadIdx.x] = dtv;
@@ -368,8 +384,6 @@ __global__ __launch_bounds__(256, 3) void ssd2_scan_mfma(Ssd2Params p, const bf1
         // strictly-lower fragment (reads past it return zero without a memory
         // access) and only the arithmetic of a block is skipped, on a scalar
         // condition.  The waits on the rings are therefore exact counts.
-        const int64_t grp = ((int64_t)b * p.nch + c) * p.G + g;
-        const bf16_t* cfg = cf + grp * (int64_t)Q * N + lane * 8;
         const uint32_t rows_c = (uint32_t)min(Q, p.L - c * Q);
         const __amdgpu_buffer_rsrc_t ry = buf_rsrc(yhead + (int64_t)c * Q * p.y_sl, rows_c * (uint32_t)p.y_sl * 2u);
         const __amdgpu_buffer_rsrc_t rxc = buf_rsrc(xhead + (int64_t)c * Q * p.x_sl, rows_c * xrow);
@@ -378,13 +392,14 @@ __global__ __launch_bounds__(256, 3) void ssd2_scan_mfma(Ssd2Params p, const bf1
             const int it = q ? 7 - wave : wave;  // the snake pair {w, 7 - w}
             if (it >= T || (q && it == wave)) continue;
             const int il = it * 32 + r;  // this lane's output time (B-operand column)
-            // issue the first global loads of this tile before the first wait:
-            // a ring of C fragments (inter-chunk term), the diagonal block and
-            // two blocks of strictly-lower C.B^T fragments
+            // issue the first global loads of this tile before the first wait
+            // (its first C fragments are already in `cr`): the diagonal block
+            // and two blocks of strictly-lower C.B^T fragments
             const bf16_t* ctile = cfg + (int64_t)it * NK * 512;
-            uint4 cr[CR];
-#pragma unroll
-            for (int k = 0; k < CR; ++k) cr[k] = *(const uint4*)(ctile + k * 512);
+            const int it2 = 7 - wave;  // the wave's next tile, if any
+            const bool next_tile = q == 0 && it2 < T && it2 != wave;
+            const bf16_t* nxt = next_tile ? cfg + (int64_t)it2 * NK * 512 : btf;
+            const int lim = next_tile ? NK : KS;
             const bf16_t* cbrow = cbf + grp * Q * Q + (int64_t)it * KS * 512;
             const uint32_t loff = lane * 16u;
             const uint4 dg0 = *(const uint4*)(cbrow + (2 * it) * 512 + lane * 8);
@@ -399,8 +414,11 @@ __global__ __launch_bounds__(256, 3) void ssd2_scan_mfma(Ssd2Params p, const bf1
             // inter-chunk term h_in . C_i^T with raw C rows as the B operand
 #pragma unroll
             for (int ks = 0; ks < NK; ++ks) {
-                const bf16x8_t bop = as_bf16x8(cr[ks % CR]);
-                if (ks + CR < NK) cr[ks % CR] = *(const uint4*)(ctile + (ks + CR) * 512);
+                const bf16x8_t bop = as_bf16x8(cr[ks % 4]);
+                if (ks + 4 < NK)
+                    cr[ks % 4] = *(const uint4*)(ctile + (ks + 4) * 512);
+                else  // the slot is free: the next phase's fragment ks + 4 - NK
+                    cr[ks % 4] = *(const uint4*)(nxt + min(ks + 4 - NK, lim - 1) * 512);
 #pragma unroll
                 for (int pt = 0; pt < PT; ++pt) {
                     const bf16x8_t a = *(const bf16x8_t*)&s_h[pt * 32 + r][ks * 16 + 8 * half];
@@ -544,12 +562,10 @@ __global__ __launch_bounds__(256, 3) void ssd2_scan_mfma(Ssd2Params p, const bf1
         // ---- K3 + K4: h <- h F_k + xg_k^T B_k over the blocks, B fragments in a ring
         if (NST >= 4 || wave < NST) {  // every state tile of this wave is valid (SPW > 1 iff NST >= 8)
             // all state tiles of a wave share one n tile (st_nt[0]) when SPW > 1
-            constexpr int BD = 4;  // B fragment ring depth (two blocks)
-            const bf16_t* btf = bfr + grp * (int64_t)Q * N + ((int64_t)st_nt[0] * KS * 64 + lane) * 8;
+            constexpr int BD = 4;  // B fragment ring depth (two blocks), primed in `cr`
             uint4 bring[BD];
 #pragma unroll
-            for (int k = 0; k < BD; ++k)
-                if (k < KS) bring[k] = *(const uint4*)(btf + k * 512);
+            for (int k = 0; k < BD; ++k) bring[k] = cr[k];
 #pragma unroll
             for (int jt = 0; jt < T; ++jt) {
                 const float F = s_F[jt];
