@@ -233,6 +233,298 @@ __global__ __launch_bounds__(256) void mamba3_prep_kernel(M3PrepParams p) {
     }
 }
 
+// ---- segment-parallel fast path -------------------------------------------
+// The sequence is cut into segments of kM3Seg positions.  A first kernel sums
+// each segment's angle increments dt range pi tanh(rot) per (head, angle) in
+// f64; the main kernel then runs one workgroup per (b, h, segment) over every
+// MIMO rank, starting from the wrapped sum of the earlier segments' totals, and
+// carries the angle wrapped at every position inside its segment.  Loads and
+// stores of proj rows, B, C and v are 8- or 4-wide vectors; proj and the
+// outputs are typed by template parameters.
+constexpr int kM3Seg = 256, kM3Tile = 32;
+
+template <typename T> __device__ __forceinline__ float m3_ld1(const T* q);
+template <> __device__ __forceinline__ float m3_ld1<float>(const float* q) { return *q; }
+template <> __device__ __forceinline__ float m3_ld1<bf16_t>(const bf16_t* q) { return bf16_to_f32(*q); }
+
+// 8 consecutive elements, 16-byte aligned start
+template <typename T> __device__ __forceinline__ void m3_ld8(const T* q, float* o);
+template <> __device__ __forceinline__ void m3_ld8<float>(const float* q, float* o) {
+    const float4 a = *(const float4*)q, c = *(const float4*)(q + 4);
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; o[4] = c.x; o[5] = c.y; o[6] = c.z; o[7] = c.w;
+}
+template <> __device__ __forceinline__ void m3_ld8<bf16_t>(const bf16_t* q, float* o) {
+    const uint4 u = *(const uint4*)q;
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        o[2 * k] = __uint_as_float(w[k] << 16);
+        o[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+    }
+}
+// 4 consecutive elements, aligned to their size
+template <typename T> __device__ __forceinline__ void m3_ld4(const T* q, float* o);
+template <> __device__ __forceinline__ void m3_ld4<float>(const float* q, float* o) {
+    const float4 a = *(const float4*)q;
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+}
+template <> __device__ __forceinline__ void m3_ld4<bf16_t>(const bf16_t* q, float* o) {
+    const uint2 u = *(const uint2*)q;
+    o[0] = __uint_as_float(u.x << 16); o[1] = __uint_as_float(u.x & 0xffff0000u);
+    o[2] = __uint_as_float(u.y << 16); o[3] = __uint_as_float(u.y & 0xffff0000u);
+}
+template <typename T> __device__ __forceinline__ void m3_st8(T* q, const float* v);
+template <> __device__ __forceinline__ void m3_st8<float>(float* q, const float* v) {
+    *(float4*)q = make_float4(v[0], v[1], v[2], v[3]);
+    *(float4*)(q + 4) = make_float4(v[4], v[5], v[6], v[7]);
+}
+template <> __device__ __forceinline__ void m3_st8<bf16_t>(bf16_t* q, const float* v) {
+    *(uint4*)q = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                            pack_bf16x2(v[6], v[7]));
+}
+template <typename T> __device__ __forceinline__ void m3_st4(T* q, const float* v);
+template <> __device__ __forceinline__ void m3_st4<float>(float* q, const float* v) {
+    *(float4*)q = make_float4(v[0], v[1], v[2], v[3]);
+}
+template <> __device__ __forceinline__ void m3_st4<bf16_t>(bf16_t* q, const float* v) {
+    *(uint2*)q = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+}
+
+// tanh from one exponential: sign(x) (1 - e) / (1 + e), e = exp(-2 |x|) <= 1
+__device__ __forceinline__ float m3_tanh(float x) {
+    const float e = __expf(-2.f * fabsf(x));
+    return copysignf((1.f - e) / (1.f + e), x);
+}
+__device__ __forceinline__ double m3_wrap_d(double a) {
+    const double two_pi = 6.283185307179586476925286766559;
+    return a - rint(a / two_pi) * two_pi;
+}
+
+template <typename TP>
+__device__ __forceinline__ void m3_coef_t(const M3PrepParams& p, const TP* proj, int b, int l, int h, float& dt,
+                                          float& da, float& lam) {
+    if (l >= p.L) {
+        dt = da = lam = 0.f;
+        return;
+    }
+    const TP* row = proj + (int64_t)b * p.proj_sb + (int64_t)l * p.proj_sl + 2 * p.H * p.P + 2 * p.M * p.G * p.N;
+    dt = fminf(fmaxf(m3p_softplus(m3_ld1(row + h) + p.dt_bias[h]), p.dt_lo), p.dt_hi);
+    da = dt * -fmaxf(m3p_softplus(m3_ld1(row + p.H + h)), p.a_floor);
+    lam = 1.f / (1.f + __expf(-m3_ld1(row + 2 * p.H + h)));
+}
+
+// Per (b, segment): tot[b][seg][h][a] = sum over the segment's positions of
+// dt[b, l, h] * (tanh(rot[b, l, a]) * span), each term rounded to f32 exactly
+// as the main kernel forms it, the sum in f64.  Dynamic LDS: [tile][H] dt and
+// [tile][A] tanh(rot) * span.
+template <typename TP>
+__global__ __launch_bounds__(256) void mamba3_angle_tot_kernel(M3PrepParams p, int nseg, double* tot) {
+    const int b = blockIdx.x / nseg, seg = blockIdx.x % nseg, t = threadIdx.x;
+    const TP* proj = static_cast<const TP*>(p.proj);
+    const int H = p.H, A = p.A, HA = H * A;
+    const int l_begin = seg * kM3Seg, l_end = min(p.L, l_begin + kM3Seg);
+    const int o_rot = 2 * H * p.P + 2 * p.M * p.G * p.N + 3 * H;
+    extern __shared__ __align__(16) float s_dyn[];
+    float* s_dtt = s_dyn;                 // [kM3Tile][H]
+    float* s_tr = s_dtt + kM3Tile * H;    // [kM3Tile][A]
+    constexpr int KP = 16;                // (h, a) pairs per thread and pass
+    for (int pb = 0; pb < HA; pb += 256 * KP) {
+        double acc[KP];
+#pragma unroll
+        for (int k = 0; k < KP; ++k) acc[k] = 0.0;
+        for (int l0 = l_begin; l0 < l_end; l0 += kM3Tile) {
+            const int nt = min(kM3Tile, l_end - l0);
+            for (int i = t; i < kM3Tile * H; i += 256) {
+                const int r = i / H, h = i % H;
+                float dt = 0.f, da, lam;
+                if (r < nt) m3_coef_t(p, proj, b, l0 + r, h, dt, da, lam);
+                s_dtt[i] = dt;
+            }
+            for (int i = t; i < kM3Tile * A; i += 256) {
+                const int r = i / A, a = i % A;
+                s_tr[i] = r < nt ? m3_tanh(m3_ld1(proj + (int64_t)b * p.proj_sb + (int64_t)(l0 + r) * p.proj_sl +
+                                                  o_rot + a)) * p.span
+                                 : 0.f;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int k = 0; k < KP; ++k) {
+                const int i = pb + t + 256 * k;
+                if (i < HA) {
+                    const int h = i / A, a = i % A;
+                    double sacc = acc[k];
+                    for (int r = 0; r < nt; ++r) sacc += (double)(s_dtt[r * H + h] * s_tr[r * A + a]);
+                    acc[k] = sacc;
+                }
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int k = 0; k < KP; ++k) {
+            const int i = pb + t + 256 * k;
+            if (i < HA) tot[((int64_t)b * nseg + seg) * HA + i] = acc[k];
+        }
+    }
+}
+
+// One workgroup per (b, h, segment), every MIMO rank.  Dynamic LDS: three
+// [kM3Tile][A] arrays (angle increments / cumulative angles, cos, sin).
+template <typename TP, typename TO, int N>
+__global__ __launch_bounds__(256) void mamba3_prep_seg_kernel(M3PrepParams p, int nseg, const double* tot) {
+    constexpr int TPR = N / 8;         // threads per B/C row (8 columns each)
+    constexpr int RPP = 256 / TPR;     // rows per pass
+    const int seg = blockIdx.x % nseg, h = (blockIdx.x / nseg) % p.H, b = blockIdx.x / (nseg * p.H);
+    const int t = threadIdx.x;
+    const TP* proj = static_cast<const TP*>(p.proj);
+    const int P = p.P, M = p.M, A = p.A, npair = p.R / 2, g = h / (p.H / p.G);
+    const int d_inner = p.H * P, bc = M * p.G * N;
+    const int o_rot = 2 * d_inner + 2 * bc + 3 * p.H;
+    const int64_t bh = (int64_t)b * p.H + h;
+    const int l_begin = seg * kM3Seg, l_end = min(p.L, l_begin + kM3Seg);
+    extern __shared__ __align__(16) float s_dyn[];
+    float* s_th = s_dyn;                   // [kM3Tile][A]
+    float* s_cs = s_th + kM3Tile * A;      // [kM3Tile][A]
+    float* s_sn = s_cs + kM3Tile * A;      // [kM3Tile][A]
+    __shared__ float s_dt[kM3Tile + 1], s_lam[kM3Tile + 1], s_da[kM3Tile];
+
+    // starting angle of the segment: the cache's angle plus the earlier segments' totals
+    float theta = 0.f;
+    if (t < A) {
+        double acc = p.ang[bh * A + t];
+        for (int s2 = 0; s2 < seg; ++s2) acc += tot[((int64_t)b * nseg + s2) * p.H * A + (int64_t)h * A + t];
+        theta = (float)m3_wrap_d(acc);
+    }
+    // this thread's 8 columns of every B/C row, their norm weights, rotation partners
+    const int col0 = (t % TPR) * 8, rsub = t / TPR;
+    float bw[8], cw[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        bw[e] = p.bnw[col0 + e];
+        cw[e] = p.cnw[col0 + e];
+    }
+    const bool pairwise = M == 1;            // pairs (2k, 2k+1); else (k, k + N/2)
+    const bool first_half = col0 < N / 2;
+    const int kbase = pairwise ? col0 / 2 : (first_half ? col0 : col0 - N / 2);
+
+    for (int l0 = l_begin; l0 < l_end; l0 += kM3Tile) {
+        const int nt = min(kM3Tile, l_end - l0);
+        // coefficients of the tile and of the position after it (scale's shift)
+        if (t <= kM3Tile) {
+            float dt = 0.f, da = 0.f, lam = 0.f;  // past the tile's next position: unused
+            if (t <= nt) m3_coef_t(p, proj, b, l0 + t, h, dt, da, lam);
+            s_dt[t] = dt;
+            s_lam[t] = lam;
+            if (t < kM3Tile) s_da[t] = da;
+        }
+        __syncthreads();
+        // angle increments dt range pi tanh(rot)
+        for (int i = t; i < nt * A; i += 256) {
+            const int r = i / A, a = i % A;
+            s_th[i] = s_dt[r] * (m3_tanh(m3_ld1(proj + (int64_t)b * p.proj_sb + (int64_t)(l0 + r) * p.proj_sl +
+                                                o_rot + a)) * p.span);
+        }
+        __syncthreads();
+        // cumulative angle, wrapped at every position
+        if (t < A)
+            for (int r = 0; r < nt; ++r) {
+                theta = m3p_wrap(theta + s_th[r * A + t]);
+                s_th[r * A + t] = theta;
+            }
+        __syncthreads();
+        for (int i = t; i < nt * A; i += 256) sincosf(s_th[i], &s_sn[i], &s_cs[i]);
+        __syncthreads();
+        // B / C rows: row index ((r * 2 + which) * M + m)
+        for (int rb = rsub; rb < nt * 2 * M; rb += RPP) {
+            const int m = rb % M, which = (rb / M) & 1, r = rb / (2 * M);
+            const int64_t prow = (int64_t)b * p.proj_sb + (int64_t)(l0 + r) * p.proj_sl;
+            float y[8];
+            m3_ld8(proj + prow + 2 * d_inner + which * bc + (m * p.G + g) * N + col0, y);
+            float ss = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss += y[e] * y[e];
+#pragma unroll
+            for (int o = 1; o < TPR; o <<= 1) ss += __shfl_xor(ss, o, 64);
+            const float rms = 1.f / sqrtf(ss / (float)N + 8.1584695e-8f);
+            const float* bias = (which ? p.cbias : p.bbias) + ((int64_t)h * M + m) * N + col0;
+            const float4 b0 = *(const float4*)bias, b1 = *(const float4*)(bias + 4);
+            const float bv[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) y[e] = (y[e] * rms) * (which ? cw[e] : bw[e]) + bv[e];
+            if (pairwise) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int k = kbase + j;
+                    if (k < npair) {
+                        const float c = s_cs[r * A + k], sn = s_sn[r * A + k];
+                        const float y0 = y[2 * j], y1 = y[2 * j + 1];
+                        y[2 * j] = c * y0 - sn * y1;
+                        y[2 * j + 1] = sn * y0 + c * y1;
+                    }
+                }
+            } else if (TPR == 1) {  // N == 8: the pairs (k, k + 4) are both in this thread
+                float o[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] = y[e ^ 4];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int k = e & 3;
+                    if (k < npair) {
+                        const float c = s_cs[r * A + k], sn = s_sn[r * A + k];
+                        y[e] = e < 4 ? c * y[e] - sn * o[e] : sn * o[e] + c * y[e];
+                    }
+                }
+            } else {
+                float o[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] = __shfl_xor(y[e], TPR / 2, 64);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int k = kbase + e;
+                    if (k < npair) {
+                        const float c = s_cs[r * A + k], sn = s_sn[r * A + k];
+                        y[e] = first_half ? c * y[e] - sn * o[e] : sn * o[e] + c * y[e];
+                    }
+                }
+            }
+            const int64_t oi = ((((int64_t)b * p.L + l0 + r) * M + m) * p.H + h) * N + col0;
+            m3_st8(static_cast<TO*>(which ? p.Co : p.Bo) + oi, y);
+            // the cache tail: the last token's rotated B
+            if (!which && l0 + r == p.L - 1) {
+                float* kq = p.kst + (((int64_t)b * M + m) * p.H + h) * N + col0;
+                *(float4*)kq = make_float4(y[0], y[1], y[2], y[3]);
+                *(float4*)(kq + 4) = make_float4(y[4], y[5], y[6], y[7]);
+            }
+        }
+        // v = x mimo_x [b, l, m, h, p], four headdim values per item
+        const int PQ = P / 4;
+        for (int i = t; i < nt * M * PQ; i += 256) {
+            const int pq = i % PQ, m = (i / PQ) % M, r = i / (PQ * M);
+            float x[4];
+            m3_ld4(proj + (int64_t)b * p.proj_sb + (int64_t)(l0 + r) * p.proj_sl + d_inner + h * P + 4 * pq, x);
+            if (p.mx) {
+                const float4 mv = *(const float4*)(p.mx + ((int64_t)h * M + m) * P + 4 * pq);
+                x[0] *= mv.x; x[1] *= mv.y; x[2] *= mv.z; x[3] *= mv.w;
+            }
+            m3_st4(static_cast<TO*>(p.v) + ((((int64_t)b * p.L + l0 + r) * M + m) * p.H + h) * P + 4 * pq, x);
+        }
+        if (t < nt) {
+            const int64_t o = ((int64_t)b * p.L + l0 + t) * p.H + h;
+            const float gmv = s_lam[t] * s_dt[t];
+            p.da[o] = s_da[t];
+            p.gm[o] = gmv;
+            p.sc[o] = gmv + (1.f - s_lam[t + 1]) * s_dt[t + 1];
+        }
+        // the rest of the cache tail: the last x and the wrapped angle
+        if (l0 + nt == p.L) {
+            for (int pp = t; pp < P; pp += 256)
+                p.vst[bh * P + pp] = m3_ld1(proj + (int64_t)b * p.proj_sb + (int64_t)(p.L - 1) * p.proj_sl + d_inner +
+                                            h * P + pp);
+            if (t < A) p.ang_out[bh * A + t] = theta;
+        }
+        __syncthreads();  // LDS reuse by the next tile
+    }
+}
+
 // ---- epilogue ------------------------------------------------------------
 struct M3FinishParams {
     int nb, L, H, P, M;
@@ -334,13 +626,80 @@ static int m3_prep_params(const mamba3_prep_args* a, M3PrepParams* out) {
 
 using namespace mamba;
 
-extern "C" int mamba3_prep_fwd(const mamba3_prep_args* a, mamba_stream_t stream) {
+// The fast path needs 16-byte aligned vector access to proj rows (B/C and x
+// slices) and 4-wide headdim.
+static bool m3_prep_fast(const M3PrepParams& p) {
+    if (((uintptr_t)p.proj & 15u) != 0) return false;
+    if (p.proj_sl % 8 != 0 || (p.nb > 1 && p.proj_sb % 8 != 0)) return false;
+    if ((2 * p.H * p.P) % 8 != 0 || p.P % 4 != 0 || (p.H * p.P) % 4 != 0) return false;
+    if (p.mx && ((uintptr_t)p.mx & 15u) != 0) return false;
+    if (((uintptr_t)p.bbias & 15u) != 0 || ((uintptr_t)p.cbias & 15u) != 0) return false;
+    if (((uintptr_t)p.kst & 15u) != 0) return false;
+    if (((uintptr_t)p.v & 15u) != 0 || ((uintptr_t)p.Bo & 15u) != 0 || ((uintptr_t)p.Co & 15u) != 0) return false;
+    // dynamic LDS of both kernels within 64 KB
+    if ((size_t)3 * kM3Tile * p.A * sizeof(float) > 64 * 1024) return false;
+    if ((size_t)kM3Tile * (p.H + p.A) * sizeof(float) > 64 * 1024) return false;
+    return true;
+}
+static int m3_nseg(const M3PrepParams& p) { return (p.L + kM3Seg - 1) / kM3Seg; }
+
+extern "C" int mamba3_prep_fast_path(const mamba3_prep_args* a) {
+    M3PrepParams p;
+    if (m3_prep_params(a, &p) != MAMBA_OK) return -1;
+    return m3_prep_fast(p) ? 1 : 0;
+}
+
+extern "C" size_t mamba3_prep_workspace_size(const mamba3_prep_args* a) {
+    M3PrepParams p;
+    if (m3_prep_params(a, &p) != MAMBA_OK) return 0;
+    const int nseg = m3_nseg(p);
+    if (!m3_prep_fast(p) || nseg == 1) return 0;
+    return (size_t)p.nb * nseg * p.H * p.A * sizeof(double);
+}
+
+template <typename TP, typename TO>
+static void m3_launch_fast(const M3PrepParams& p, double* tot, hipStream_t s) {
+    const int nseg = m3_nseg(p);
+    if (nseg > 1)
+        hipLaunchKernelGGL((mamba3_angle_tot_kernel<TP>), dim3(p.nb * nseg), dim3(256),
+                           (size_t)kM3Tile * (p.H + p.A) * sizeof(float), s, p, nseg, tot);
+    const dim3 grid(p.nb * p.H * nseg), block(256);
+    const size_t lds = (size_t)3 * kM3Tile * p.A * sizeof(float);
+#define MAMBA3_SEG_N(NN) \
+    hipLaunchKernelGGL((mamba3_prep_seg_kernel<TP, TO, NN>), grid, block, lds, s, p, nseg, (const double*)tot);
+    switch (p.N) {
+        case 8: MAMBA3_SEG_N(8) break;
+        case 16: MAMBA3_SEG_N(16) break;
+        case 32: MAMBA3_SEG_N(32) break;
+        case 64: MAMBA3_SEG_N(64) break;
+        case 128: MAMBA3_SEG_N(128) break;
+        default: MAMBA3_SEG_N(256) break;
+    }
+#undef MAMBA3_SEG_N
+}
+
+extern "C" int mamba3_prep_fwd(const mamba3_prep_args* a, void* workspace, size_t workspace_bytes,
+                               mamba_stream_t stream) {
     M3PrepParams p;
     const int st = m3_prep_params(a, &p);
     if (st != MAMBA_OK) return st;
     hipStream_t s = (hipStream_t)stream;
+    const size_t need = mamba3_prep_workspace_size(a);
+    MAMBA_CHECK_ARG(workspace_bytes >= need && (need == 0 || workspace != nullptr),
+                    "workspace too small: mamba3_prep_workspace_size() bytes are required");
+    MAMBA_CHECK_ARG(need == 0 || ((uintptr_t)workspace & 7u) == 0, "workspace must be 8-byte aligned");
+    MAMBA_CHECK_ARG((int64_t)p.nb * p.H * m3_nseg(p) < (1ll << 31), "too many (batch, head, segment) items");
     hipLaunchKernelGGL(mamba3_seed_kernel, dim3(p.nb * p.H), dim3(256), 0, s, p);
     MAMBA_CHECK_LAUNCH();
+    if (m3_prep_fast(p)) {
+        double* tot = (double*)workspace;
+        if (p.proj_bf16 && p.io_bf16) m3_launch_fast<bf16_t, bf16_t>(p, tot, s);
+        else if (p.proj_bf16) m3_launch_fast<bf16_t, float>(p, tot, s);
+        else if (p.io_bf16) m3_launch_fast<float, bf16_t>(p, tot, s);
+        else m3_launch_fast<float, float>(p, tot, s);
+        MAMBA_CHECK_LAUNCH();
+        return MAMBA_OK;
+    }
     const int npair = p.R / 2;
     auto lds_of = [&](int ts) {
         return (size_t)(2 * ts * p.N + 2 * ts * npair + ts * p.A + ts * p.P) * sizeof(float);

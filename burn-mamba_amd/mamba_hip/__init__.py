@@ -15,3 +15,4 @@ from .ssd3 import Mamba3SingleSsdInput, ssd3_fast_path, ssd3_fwd  # noqa: F401
 from .mamba3 import Mamba3, Mamba3Cache, Mamba3Config  # noqa: F401
 from .mamba3 import step_ssm as mamba3_step_ssm, step_ssm_args as mamba3_step_ssm_args  # noqa: F401
 from .mamba3 import finish_fwd as mamba3_finish_fwd, prep_fwd as mamba3_prep_fwd  # noqa: F401
+from .mamba3 import prep_args as mamba3_prep_args, prep_fast_path as mamba3_prep_fast_path  # noqa: F401

@@ -211,7 +211,9 @@ _SIGNATURES = {
     "mamba1_scan_fwd_timed": ([ctypes.POINTER(Mamba1ScanArgs), c_vp, c_vp, c_vp], ctypes.c_int),
     "mamba1_scan_step": ([ctypes.POINTER(Mamba1StepArgs), c_vp], ctypes.c_int),
     "mamba3_step_ssm": ([ctypes.POINTER(Mamba3StepArgs), c_vp], ctypes.c_int),
-    "mamba3_prep_fwd": ([ctypes.POINTER(Mamba3PrepArgs), c_vp], ctypes.c_int),
+    "mamba3_prep_fast_path": ([ctypes.POINTER(Mamba3PrepArgs)], ctypes.c_int),
+    "mamba3_prep_workspace_size": ([ctypes.POINTER(Mamba3PrepArgs)], ctypes.c_size_t),
+    "mamba3_prep_fwd": ([ctypes.POINTER(Mamba3PrepArgs), c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),
     "mamba3_finish_fwd": ([ctypes.POINTER(Mamba3FinishArgs), c_vp], ctypes.c_int),
     "mamba3_step_ssm_timed": ([ctypes.POINTER(Mamba3StepArgs), c_vp, c_vp, c_vp], ctypes.c_int),
     "mamba1_scan_step_timed": ([ctypes.POINTER(Mamba1StepArgs), c_vp, c_vp, c_vp], ctypes.c_int),

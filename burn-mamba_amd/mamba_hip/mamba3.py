@@ -162,11 +162,10 @@ def step_ssm(args: Mamba3StepArgs, device, events=None):
         check(L.mamba3_step_ssm(ctypes.byref(args), st), "mamba3_step_ssm")
 
 
-def prep_fwd(cfg: Mamba3Config, proj: torch.Tensor, cache: Mamba3Cache, *, dt_bias, b_norm_w, c_norm_w, b_bias,
-             c_bias, mimo_x=None, io_dtype=None):
-    """mamba3_prep_fwd: proj [b, l, d_in_proj] -> dict(v [b,l,M,H,P], B, C [b,l,M,H,N],
-    da, gamma, scale [b,l,H], h0 [b,H,P,N]).  The cache's k_state / v_state are
-    replaced in place by the last token's; its angle by the new cumulative angle."""
+def prep_args(cfg: Mamba3Config, proj: torch.Tensor, cache: Mamba3Cache, *, dt_bias, b_norm_w, c_norm_w, b_bias,
+              c_bias, mimo_x=None, io_dtype=None) -> Mamba3PrepArgs:
+    """The mamba3_prep_args of one call, with its outputs allocated (kept on
+    the struct as `outputs` and `angle_out`)."""
     b, L, row = proj.shape
     H, P, N, M, G = cfg.nheads, cfg.per_head_dim, cfg.state_rank, cfg.mimo_rank, cfg.ngroups
     if row != cfg.d_in_proj or proj.stride(2) != 1:
@@ -194,9 +193,31 @@ def prep_fwd(cfg: Mamba3Config, proj: torch.Tensor, cache: Mamba3Cache, *, dt_bi
     a.v, a.B, a.C = out["v"].data_ptr(), out["B"].data_ptr(), out["C"].data_ptr()
     a.da, a.gamma, a.scale = out["da"].data_ptr(), out["gamma"].data_ptr(), out["scale"].data_ptr()
     a.initial_state = out["h0"].data_ptr()
-    check(_lib.lib().mamba3_prep_fwd(ctypes.byref(a), _stream(dev)), "mamba3_prep_fwd")
-    cache.angle_bha = angle_out
-    return out
+    a.outputs, a.angle_out_t = out, angle_out
+    return a
+
+
+def prep_fast_path(args: Mamba3PrepArgs) -> int:
+    """1 if mamba3_prep_fwd runs the segment-parallel kernels for these
+    arguments, 0 for the per-(batch, head, rank) kernel, -1 if invalid."""
+    return int(_lib.lib().mamba3_prep_fast_path(ctypes.byref(args)))
+
+
+def prep_fwd(cfg: Mamba3Config, proj: torch.Tensor, cache: Mamba3Cache, *, dt_bias, b_norm_w, c_norm_w, b_bias,
+             c_bias, mimo_x=None, io_dtype=None):
+    """mamba3_prep_fwd: proj [b, l, d_in_proj] -> dict(v [b,l,M,H,P], B, C [b,l,M,H,N],
+    da, gamma, scale [b,l,H], h0 [b,H,P,N]).  The cache's k_state / v_state are
+    replaced in place by the last token's; its angle by the new cumulative angle."""
+    a = prep_args(cfg, proj, cache, dt_bias=dt_bias, b_norm_w=b_norm_w, c_norm_w=c_norm_w, b_bias=b_bias,
+                  c_bias=c_bias, mimo_x=mimo_x, io_dtype=io_dtype)
+    dev = proj.device
+    L_ = _lib.lib()
+    nws = L_.mamba3_prep_workspace_size(ctypes.byref(a))
+    ws = torch.empty(max(int(nws), 1), device=dev, dtype=torch.uint8) if nws else None
+    check(L_.mamba3_prep_fwd(ctypes.byref(a), None if ws is None else ws.data_ptr(), int(nws), _stream(dev)),
+          "mamba3_prep_fwd")
+    cache.angle_bha = a.angle_out_t
+    return a.outputs
 
 
 def finish_fwd(cfg: Mamba3Config, y_ssd: torch.Tensor, v: torch.Tensor, z: torch.Tensor, *, D=None, mimo_z=None,

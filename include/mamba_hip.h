@@ -343,7 +343,16 @@ typedef struct mamba3_prep_args {
     float* initial_state;                            /* [b, H, P, N] out           */
 } mamba3_prep_args;
 
-int mamba3_prep_fwd(const mamba3_prep_args* args, mamba_stream_t stream);
+/* 1 if mamba3_prep_fwd runs the segment-parallel kernels (proj rows of 8k    */
+/* elements at a 16-byte aligned base, headdim a multiple of 4, aligned        */
+/* parameter and output buffers), 0 for the per-(batch, head, rank) kernel,    */
+/* -1 if the arguments are invalid.                                            */
+int mamba3_prep_fast_path(const mamba3_prep_args* args);
+/* Workspace bytes mamba3_prep_fwd needs: per-segment angle totals (f64) when */
+/* the sequence spans more than one 256-position segment, else 0.             */
+size_t mamba3_prep_workspace_size(const mamba3_prep_args* args);
+int mamba3_prep_fwd(const mamba3_prep_args* args, void* workspace, size_t workspace_bytes,
+                    mamba_stream_t stream);
 
 /* Mamba-3 prefill epilogue: forward_single_ssd step 9 before out_proj         */
 /* (single_ssd/single_ssd/mod.rs:288-332): y += D v, the silu gate (or the     */

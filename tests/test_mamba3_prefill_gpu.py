@@ -171,3 +171,57 @@ def test_mamba3_forward_then_step(M):
     c1 = dict(ssm=hT, k_state=r["k_state"], v_state=r["v_state"], angle=r["angle"])
     y2, _ = oracle.mamba3_step(xt.cpu().numpy() @ W, prm, c1)
     np.testing.assert_allclose(out2.cpu().numpy(), y2 @ Wo, rtol=1e-3, atol=1e-4)
+
+
+FAST_CASES = [
+    # (b, L, H, P, G, N, M, rope_dim): proj rows padded to a multiple of 8 elements,
+    # which selects the segment-parallel kernels (256-position segments)
+    (2, 37, 4, 16, 2, 16, 1, 16),     # SISO, one segment
+    (2, 300, 4, 16, 1, 32, 4, 32),    # MIMO 4, two segments
+    (1, 700, 2, 8, 1, 16, 2, 8),      # partial rotation, three segments, ragged tail
+    (2, 512, 4, 32, 2, 64, 1, 0),     # rotation off, exactly two segments
+    (1, 270, 2, 8, 1, 8, 2, 8),       # dstate 8 with MIMO: both pair members in one thread
+]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("case", FAST_CASES)
+def test_mamba3_prep_fwd_segments(case, dtype):
+    """The segment-parallel prep (aligned proj rows): the angle carried across
+    segments through the f64 segment totals, every output and the cache tail
+    against the oracle."""
+    import torch
+    import mamba_hip
+    import oracle
+    b, L, H, P, G, N, M, R = case
+    prm = _params(sum(case) + 5, H, P, G, N, M, R)
+    cfg = _cfg(prm)
+    A = cfg.num_rope_angles
+    rng = np.random.default_rng(sum(case) + 6)
+    proj = rng.standard_normal((b, L, cfg.d_in_proj)).astype(np.float32)
+    pad = -(-cfg.d_in_proj // 8) * 8 + 8
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    wide = torch.zeros((b, L, pad), dtype=tdt, device="cuda")
+    wide[:, :, :cfg.d_in_proj] = torch.from_numpy(proj).to(tdt).cuda()
+    pin = wide[:, :, :cfg.d_in_proj]
+    cache = _cache(sum(case) + 7, b, prm, A)
+    cg = _gpu_cache(cache)
+    a = mamba_hip.mamba3_prep_args(cfg, pin, cg, dt_bias=_g(prm, "dt_bias"), b_norm_w=_g(prm, "b_norm_w"),
+                                   c_norm_w=_g(prm, "c_norm_w"), b_bias=_g(prm, "b_bias"),
+                                   c_bias=_g(prm, "c_bias"), mimo_x=_g(prm, "mimo_x"))
+    assert mamba_hip.mamba3_prep_fast_path(a) == 1
+    out = mamba_hip.mamba3_prep_fwd(cfg, pin, cg, dt_bias=_g(prm, "dt_bias"), b_norm_w=_g(prm, "b_norm_w"),
+                                    c_norm_w=_g(prm, "c_norm_w"), b_bias=_g(prm, "b_bias"),
+                                    c_bias=_g(prm, "c_bias"), mimo_x=_g(prm, "mimo_x"))
+    torch.cuda.synchronize()
+    r = oracle.mamba3_prep_fwd(pin.float().cpu().numpy(), prm, cache)
+    io_tol = dict(rtol=2e-2, atol=1e-2) if dtype == "bf16" else F32_TOL
+    for k in ("v", "B", "C"):
+        np.testing.assert_allclose(out[k].float().cpu().numpy(), r[k], **io_tol, err_msg=k)
+    for k in ("da", "gamma", "scale", "h0"):
+        np.testing.assert_allclose(out[k].cpu().numpy(), r[k], **F32_TOL, err_msg=k)
+    np.testing.assert_allclose(cg.k_state_bmhr.cpu().numpy(), r["k_state"], **F32_TOL)
+    np.testing.assert_allclose(cg.v_state_bhp.cpu().numpy(), r["v_state"], **F32_TOL)
+    ag = cg.angle_bha.cpu().numpy()
+    np.testing.assert_allclose(np.cos(ag), np.cos(r["angle"]), atol=5e-5)
+    np.testing.assert_allclose(np.sin(ag), np.sin(r["angle"]), atol=5e-5)
