@@ -290,6 +290,31 @@ template <> __device__ __forceinline__ void m3_st4<bf16_t>(bf16_t* q, const floa
     *(uint2*)q = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
 }
 
+// Lane exchanges inside aligned groups of a wave, without LDS addressing:
+// DPP for the quad and 16-lane-row patterns, ds_swizzle (bit-mask mode) for
+// the other xor distances below 32.
+template <int CTRL>
+__device__ __forceinline__ float m3_dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+template <int K>
+__device__ __forceinline__ float m3_xor(float x) {  // value of lane (lane ^ K), K < 32
+    if constexpr (K == 1) return m3_dpp<0xB1>(x);   // quad_perm [1, 0, 3, 2]
+    else if constexpr (K == 2) return m3_dpp<0x4E>(x);  // quad_perm [2, 3, 0, 1]
+    else if constexpr (K == 8) return m3_dpp<0x128>(x);  // row_ror:8 (lane ^ 8 inside a 16-lane row)
+    else return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x1F | (K << 10)));
+}
+// sum over an aligned group of G lanes (G a power of two <= 32), in every lane
+template <int G>
+__device__ __forceinline__ float m3_group_sum(float x) {
+    if constexpr (G >= 32) x += m3_xor<16>(x);
+    if constexpr (G >= 16) x += m3_dpp<0x140>(x);  // row_mirror: i <-> 15 - i
+    if constexpr (G >= 8) x += m3_dpp<0x141>(x);   // row_half_mirror: i <-> 7 - i (per 8)
+    if constexpr (G >= 4) x += m3_dpp<0x1B>(x);    // quad_perm [3, 2, 1, 0]
+    if constexpr (G >= 2) x += m3_dpp<0xB1>(x);    // quad_perm [1, 0, 3, 2]
+    return x;
+}
+
 // tanh from one exponential: sign(x) (1 - e) / (1 + e), e = exp(-2 |x|) <= 1
 __device__ __forceinline__ float m3_tanh(float x) {
     const float e = __expf(-2.f * fabsf(x));
@@ -367,24 +392,32 @@ __global__ __launch_bounds__(256) void mamba3_angle_tot_kernel(M3PrepParams p, i
     }
 }
 
-// One workgroup per (b, h, segment), every MIMO rank.  Dynamic LDS: three
-// [kM3Tile][A] arrays (angle increments / cumulative angles, cos, sin).
+// One workgroup per (b, h, segment), every MIMO rank.  Dynamic LDS: the
+// angle increments / cumulative angles [kM3Tile][A4] (A4 = A rounded up to 4)
+// and cos / sin tables [kM3Tile][N/2] over every pair index k, with the
+// identity (1, 0) for the pairs past the rotated ones, so a thread reads its
+// columns' factors as aligned vectors and rotates without selects.  When 2 M
+// divides the rows of a pass (256 / (N / 8)), every thread keeps one (B or C,
+// rank) and its column block for the whole segment; otherwise the rows are
+// decomposed per pass.
 template <typename TP, typename TO, int N>
 __global__ __launch_bounds__(256) void mamba3_prep_seg_kernel(M3PrepParams p, int nseg, const double* tot) {
     constexpr int TPR = N / 8;         // threads per B/C row (8 columns each)
     constexpr int RPP = 256 / TPR;     // rows per pass
+    constexpr int W = N / 2;           // pair indices
     const int seg = blockIdx.x % nseg, h = (blockIdx.x / nseg) % p.H, b = blockIdx.x / (nseg * p.H);
     const int t = threadIdx.x;
     const TP* proj = static_cast<const TP*>(p.proj);
-    const int P = p.P, M = p.M, A = p.A, npair = p.R / 2, g = h / (p.H / p.G);
+    const int P = p.P, M = p.M, A = p.A, A4 = (p.A + 3) & ~3, npair = p.R / 2, g = h / (p.H / p.G);
     const int d_inner = p.H * P, bc = M * p.G * N;
     const int o_rot = 2 * d_inner + 2 * bc + 3 * p.H;
     const int64_t bh = (int64_t)b * p.H + h;
     const int l_begin = seg * kM3Seg, l_end = min(p.L, l_begin + kM3Seg);
+    const TP* projb = proj + (int64_t)b * p.proj_sb;
     extern __shared__ __align__(16) float s_dyn[];
-    float* s_th = s_dyn;                   // [kM3Tile][A]
-    float* s_cs = s_th + kM3Tile * A;      // [kM3Tile][A]
-    float* s_sn = s_cs + kM3Tile * A;      // [kM3Tile][A]
+    float* s_th = s_dyn;                   // [kM3Tile][A4]
+    float* s_cs = s_th + kM3Tile * A4;     // [kM3Tile][W]
+    float* s_sn = s_cs + kM3Tile * W;      // [kM3Tile][W]
     __shared__ float s_dt[kM3Tile + 1], s_lam[kM3Tile + 1], s_da[kM3Tile];
 
     // starting angle of the segment: the cache's angle plus the earlier segments' totals
@@ -394,17 +427,82 @@ __global__ __launch_bounds__(256) void mamba3_prep_seg_kernel(M3PrepParams p, in
         for (int s2 = 0; s2 < seg; ++s2) acc += tot[((int64_t)b * nseg + s2) * p.H * A + (int64_t)h * A + t];
         theta = (float)m3_wrap_d(acc);
     }
-    // this thread's 8 columns of every B/C row, their norm weights, rotation partners
+    // this thread's 8 columns of every B/C row, their pair indices and rotation sign
     const int col0 = (t % TPR) * 8, rsub = t / TPR;
-    float bw[8], cw[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        bw[e] = p.bnw[col0 + e];
-        cw[e] = p.cnw[col0 + e];
-    }
     const bool pairwise = M == 1;            // pairs (2k, 2k+1); else (k, k + N/2)
-    const bool first_half = col0 < N / 2;
-    const int kbase = pairwise ? col0 / 2 : (first_half ? col0 : col0 - N / 2);
+    const int kbase = pairwise ? col0 / 2 : (TPR == 1 ? 0 : (col0 < N / 2 ? col0 : col0 - N / 2));
+    const float sgn = col0 < N / 2 ? -1.f : 1.f;  // y' = c y + sgn s y_partner (M > 1)
+    const bool fixed = RPP % (2 * M) == 0;   // one (B or C, rank) per thread
+    const int which_f = (rsub % (2 * M)) / M, m_f = rsub % M, dpos = RPP / (2 * M);
+    float w8[8], bias8[8];
+    if (fixed) {
+        const float* wsrc = which_f ? p.cnw : p.bnw;
+        const float* bsrc = (which_f ? p.cbias : p.bbias) + ((int64_t)h * M + m_f) * N + col0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            w8[e] = wsrc[col0 + e];
+            bias8[e] = bsrc[e];
+        }
+    }
+
+    const int PQ = P / 4;
+    const bool vfixed = 256 % (M * PQ) == 0;
+    const int vpq = t % PQ, vm = (t / PQ) % M, vr0 = t / (M * PQ), vdr = vfixed ? 256 / (M * PQ) : 1;
+    float4 vmx = make_float4(1.f, 1.f, 1.f, 1.f);
+    if (vfixed && p.mx) vmx = *(const float4*)(p.mx + ((int64_t)h * M + vm) * P + 4 * vpq);
+
+    // one B/C row: norm, weight, bias, rotation, store (and the cache tail)
+    auto bc_row = [&](int l0, int r, int which, int m, const float* w, const float* bias) {
+        const int l = l0 + r;
+        float y[8];
+        m3_ld8(projb + (int64_t)l * p.proj_sl + 2 * d_inner + which * bc + (m * p.G + g) * N + col0, y);
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += y[e] * y[e];
+        ss = m3_group_sum<TPR>(ss);
+        const float rms = 1.f / sqrtf(ss / (float)N + 8.1584695e-8f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = (y[e] * rms) * w[e] + bias[e];
+        const float* csr = (const float*)__builtin_assume_aligned(s_cs + r * W + kbase, 16);
+        const float* snr = (const float*)__builtin_assume_aligned(s_sn + r * W + kbase, 16);
+        if (pairwise) {
+            const float4 c4 = *(const float4*)csr, s4 = *(const float4*)snr;
+            const float cv[4] = {c4.x, c4.y, c4.z, c4.w}, sv[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float y0 = y[2 * j], y1 = y[2 * j + 1];
+                y[2 * j] = cv[j] * y0 - sv[j] * y1;
+                y[2 * j + 1] = sv[j] * y0 + cv[j] * y1;
+            }
+        } else if (TPR == 1) {  // N == 8: the pairs (k, k + 4) are both in this thread
+            const float4 c4 = *(const float4*)csr, s4 = *(const float4*)snr;
+            const float cv[4] = {c4.x, c4.y, c4.z, c4.w}, sv[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float y0 = y[j], y1 = y[j + 4];
+                y[j] = cv[j] * y0 - sv[j] * y1;
+                y[j + 4] = sv[j] * y0 + cv[j] * y1;
+            }
+        } else {
+            float o[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = m3_xor<TPR / 2>(y[e]);
+            const float4 c0 = *(const float4*)csr, c1 = *(const float4*)(csr + 4);
+            const float4 s0 = *(const float4*)snr, s1 = *(const float4*)(snr + 4);
+            const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+            const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) y[e] = cv[e] * y[e] + (sgn * sv[e]) * o[e];
+        }
+        const int64_t oi = ((((int64_t)b * p.L + l) * M + m) * p.H + h) * N + col0;
+        m3_st8(static_cast<TO*>(which ? p.Co : p.Bo) + oi, y);
+        // the cache tail: the last token's rotated B
+        if (!which && l == p.L - 1) {
+            float* kq = p.kst + (((int64_t)b * M + m) * p.H + h) * N + col0;
+            *(float4*)kq = make_float4(y[0], y[1], y[2], y[3]);
+            *(float4*)(kq + 4) = make_float4(y[4], y[5], y[6], y[7]);
+        }
+    };
 
     for (int l0 = l_begin; l0 < l_end; l0 += kM3Tile) {
         const int nt = min(kM3Tile, l_end - l0);
@@ -419,93 +517,71 @@ __global__ __launch_bounds__(256) void mamba3_prep_seg_kernel(M3PrepParams p, in
         __syncthreads();
         // angle increments dt range pi tanh(rot)
         for (int i = t; i < nt * A; i += 256) {
-            const int r = i / A, a = i % A;
-            s_th[i] = s_dt[r] * (m3_tanh(m3_ld1(proj + (int64_t)b * p.proj_sb + (int64_t)(l0 + r) * p.proj_sl +
-                                                o_rot + a)) * p.span);
+            const int r = i / A, a = i - r * A;
+            s_th[r * A4 + a] =
+                s_dt[r] * (m3_tanh(m3_ld1(projb + (int64_t)(l0 + r) * p.proj_sl + o_rot + a)) * p.span);
         }
         __syncthreads();
         // cumulative angle, wrapped at every position
         if (t < A)
             for (int r = 0; r < nt; ++r) {
-                theta = m3p_wrap(theta + s_th[r * A + t]);
-                s_th[r * A + t] = theta;
+                theta = m3p_wrap(theta + s_th[r * A4 + t]);
+                s_th[r * A4 + t] = theta;
             }
         __syncthreads();
-        for (int i = t; i < nt * A; i += 256) sincosf(s_th[i], &s_sn[i], &s_cs[i]);
-        __syncthreads();
-        // B / C rows: row index ((r * 2 + which) * M + m)
-        for (int rb = rsub; rb < nt * 2 * M; rb += RPP) {
-            const int m = rb % M, which = (rb / M) & 1, r = rb / (2 * M);
-            const int64_t prow = (int64_t)b * p.proj_sb + (int64_t)(l0 + r) * p.proj_sl;
-            float y[8];
-            m3_ld8(proj + prow + 2 * d_inner + which * bc + (m * p.G + g) * N + col0, y);
-            float ss = 0.f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) ss += y[e] * y[e];
-#pragma unroll
-            for (int o = 1; o < TPR; o <<= 1) ss += __shfl_xor(ss, o, 64);
-            const float rms = 1.f / sqrtf(ss / (float)N + 8.1584695e-8f);
-            const float* bias = (which ? p.cbias : p.bbias) + ((int64_t)h * M + m) * N + col0;
-            const float4 b0 = *(const float4*)bias, b1 = *(const float4*)(bias + 4);
-            const float bv[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-#pragma unroll
-            for (int e = 0; e < 8; ++e) y[e] = (y[e] * rms) * (which ? cw[e] : bw[e]) + bv[e];
-            if (pairwise) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int k = kbase + j;
-                    if (k < npair) {
-                        const float c = s_cs[r * A + k], sn = s_sn[r * A + k];
-                        const float y0 = y[2 * j], y1 = y[2 * j + 1];
-                        y[2 * j] = c * y0 - sn * y1;
-                        y[2 * j + 1] = sn * y0 + c * y1;
-                    }
-                }
-            } else if (TPR == 1) {  // N == 8: the pairs (k, k + 4) are both in this thread
-                float o[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) o[e] = y[e ^ 4];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const int k = e & 3;
-                    if (k < npair) {
-                        const float c = s_cs[r * A + k], sn = s_sn[r * A + k];
-                        y[e] = e < 4 ? c * y[e] - sn * o[e] : sn * o[e] + c * y[e];
-                    }
-                }
-            } else {
-                float o[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) o[e] = __shfl_xor(y[e], TPR / 2, 64);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const int k = kbase + e;
-                    if (k < npair) {
-                        const float c = s_cs[r * A + k], sn = s_sn[r * A + k];
-                        y[e] = first_half ? c * y[e] - sn * o[e] : sn * o[e] + c * y[e];
-                    }
-                }
+        // cos / sin of the wrapped angles (|angle| <= pi); identity past the rotated pairs
+        for (int i = t; i < nt * W; i += 256) {
+            const int r = i / W, k = i % W;
+            float c = 1.f, sn = 0.f;
+            if (k < npair) {
+                const float th = s_th[r * A4 + k];
+                c = __cosf(th);
+                sn = __sinf(th);
             }
-            const int64_t oi = ((((int64_t)b * p.L + l0 + r) * M + m) * p.H + h) * N + col0;
-            m3_st8(static_cast<TO*>(which ? p.Co : p.Bo) + oi, y);
-            // the cache tail: the last token's rotated B
-            if (!which && l0 + r == p.L - 1) {
-                float* kq = p.kst + (((int64_t)b * M + m) * p.H + h) * N + col0;
-                *(float4*)kq = make_float4(y[0], y[1], y[2], y[3]);
-                *(float4*)(kq + 4) = make_float4(y[4], y[5], y[6], y[7]);
+            s_cs[i] = c;
+            s_sn[i] = sn;
+        }
+        __syncthreads();
+        // B / C rows
+        if (fixed) {
+            for (int r = rsub / (2 * M); r < nt; r += dpos) bc_row(l0, r, which_f, m_f, w8, bias8);
+        } else {
+            for (int rb = rsub; rb < nt * 2 * M; rb += RPP) {
+                const int m = rb % M, which = (rb / M) & 1, r = rb / (2 * M);
+                float w[8], bias[8];
+                const float* bsrc = (which ? p.cbias : p.bbias) + ((int64_t)h * M + m) * N + col0;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    w[e] = (which ? p.cnw : p.bnw)[col0 + e];
+                    bias[e] = bsrc[e];
+                }
+                bc_row(l0, r, which, m, w, bias);
             }
         }
-        // v = x mimo_x [b, l, m, h, p], four headdim values per item
-        const int PQ = P / 4;
-        for (int i = t; i < nt * M * PQ; i += 256) {
-            const int pq = i % PQ, m = (i / PQ) % M, r = i / (PQ * M);
-            float x[4];
-            m3_ld4(proj + (int64_t)b * p.proj_sb + (int64_t)(l0 + r) * p.proj_sl + d_inner + h * P + 4 * pq, x);
-            if (p.mx) {
-                const float4 mv = *(const float4*)(p.mx + ((int64_t)h * M + m) * P + 4 * pq);
-                x[0] *= mv.x; x[1] *= mv.y; x[2] *= mv.z; x[3] *= mv.w;
+        // v = x mimo_x [b, l, m, h, p], four headdim values per item; with
+        // 256 % (M P / 4) == 0 each thread keeps one (rank, quad) of the head
+        if (vfixed) {
+            const TP* xs = projb + (int64_t)(l0 + vr0) * p.proj_sl + d_inner + h * P + 4 * vpq;
+            TO* vd = static_cast<TO*>(p.v) + ((((int64_t)b * p.L + l0 + vr0) * M + vm) * p.H + h) * P + 4 * vpq;
+            for (int r = vr0; r < nt; r += vdr) {
+                float x[4];
+                m3_ld4(xs, x);
+                x[0] *= vmx.x; x[1] *= vmx.y; x[2] *= vmx.z; x[3] *= vmx.w;
+                m3_st4(vd, x);
+                xs += (int64_t)vdr * p.proj_sl;
+                vd += (int64_t)vdr * M * p.H * P;
             }
-            m3_st4(static_cast<TO*>(p.v) + ((((int64_t)b * p.L + l0 + r) * M + m) * p.H + h) * P + 4 * pq, x);
+        } else {
+            for (int i = t; i < nt * M * PQ; i += 256) {
+                const int pq = i % PQ, m = (i / PQ) % M, r = i / (PQ * M);
+                float x[4];
+                m3_ld4(projb + (int64_t)(l0 + r) * p.proj_sl + d_inner + h * P + 4 * pq, x);
+                if (p.mx) {
+                    const float4 mv = *(const float4*)(p.mx + ((int64_t)h * M + m) * P + 4 * pq);
+                    x[0] *= mv.x; x[1] *= mv.y; x[2] *= mv.z; x[3] *= mv.w;
+                }
+                m3_st4(static_cast<TO*>(p.v) + ((((int64_t)b * p.L + l0 + r) * M + m) * p.H + h) * P + 4 * pq, x);
+            }
         }
         if (t < nt) {
             const int64_t o = ((int64_t)b * p.L + l0 + t) * p.H + h;
@@ -517,8 +593,7 @@ __global__ __launch_bounds__(256) void mamba3_prep_seg_kernel(M3PrepParams p, in
         // the rest of the cache tail: the last x and the wrapped angle
         if (l0 + nt == p.L) {
             for (int pp = t; pp < P; pp += 256)
-                p.vst[bh * P + pp] = m3_ld1(proj + (int64_t)b * p.proj_sb + (int64_t)(p.L - 1) * p.proj_sl + d_inner +
-                                            h * P + pp);
+                p.vst[bh * P + pp] = m3_ld1(projb + (int64_t)(p.L - 1) * p.proj_sl + d_inner + h * P + pp);
             if (t < A) p.ang_out[bh * A + t] = theta;
         }
         __syncthreads();  // LDS reuse by the next tile
@@ -637,7 +712,7 @@ static bool m3_prep_fast(const M3PrepParams& p) {
     if (((uintptr_t)p.kst & 15u) != 0) return false;
     if (((uintptr_t)p.v & 15u) != 0 || ((uintptr_t)p.Bo & 15u) != 0 || ((uintptr_t)p.Co & 15u) != 0) return false;
     // dynamic LDS of both kernels within 64 KB
-    if ((size_t)3 * kM3Tile * p.A * sizeof(float) > 64 * 1024) return false;
+    if ((size_t)kM3Tile * (((p.A + 3) & ~3) + p.N) * sizeof(float) > 64 * 1024) return false;
     if ((size_t)kM3Tile * (p.H + p.A) * sizeof(float) > 64 * 1024) return false;
     return true;
 }
@@ -664,7 +739,7 @@ static void m3_launch_fast(const M3PrepParams& p, double* tot, hipStream_t s) {
         hipLaunchKernelGGL((mamba3_angle_tot_kernel<TP>), dim3(p.nb * nseg), dim3(256),
                            (size_t)kM3Tile * (p.H + p.A) * sizeof(float), s, p, nseg, tot);
     const dim3 grid(p.nb * p.H * nseg), block(256);
-    const size_t lds = (size_t)3 * kM3Tile * p.A * sizeof(float);
+    const size_t lds = (size_t)kM3Tile * (((p.A + 3) & ~3) + p.N) * sizeof(float);
 #define MAMBA3_SEG_N(NN) \
     hipLaunchKernelGGL((mamba3_prep_seg_kernel<TP, TO, NN>), grid, block, lds, s, p, nseg, (const double*)tot);
     switch (p.N) {
