@@ -170,6 +170,31 @@ class RmsNormArgs(ctypes.Structure):
     ]
 
 
+class Mamba2ConvArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", c_i32), ("seqlen", c_i32), ("channels", c_i32), ("kernel", c_i32), ("nheads", c_i32),
+        ("in_dtype", c_i32), ("out_dtype", c_i32),
+        ("proj", c_vp), ("proj_sb", c_i64), ("proj_sl", c_i64),
+        ("xbc_offset", c_i32), ("dt_offset", c_i32),
+        ("conv_w", c_vp), ("conv_b", c_vp), ("conv_state", c_vp), ("dt_bias", c_vp),
+        ("dt_min", ctypes.c_float), ("dt_max", ctypes.c_float),
+        ("xbc", c_vp), ("xbc_sb", c_i64), ("xbc_sl", c_i64),
+        ("dt", c_vp),
+    ]
+
+
+class Mamba2GatedNormArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", c_i32), ("seqlen", c_i32), ("width", c_i32), ("norm_before_gate", c_i32),
+        ("y_dtype", c_i32), ("z_dtype", c_i32), ("out_dtype", c_i32),
+        ("eps", ctypes.c_float),
+        ("y", c_vp), ("y_sb", c_i64), ("y_sl", c_i64),
+        ("z", c_vp), ("z_sb", c_i64), ("z_sl", c_i64),
+        ("gamma", c_vp),
+        ("out", c_vp), ("out_sb", c_i64), ("out_sl", c_i64),
+    ]
+
+
 class LinearArgs(ctypes.Structure):
     _fields_ = [
         ("rows", c_i32), ("d_in", c_i32), ("d_out", c_i32), ("x_dtype", c_i32), ("y_dtype", c_i32),
@@ -211,6 +236,8 @@ _SIGNATURES = {
     "mamba1_scan_fwd_timed": ([ctypes.POINTER(Mamba1ScanArgs), c_vp, c_vp, c_vp], ctypes.c_int),
     "mamba1_scan_step": ([ctypes.POINTER(Mamba1StepArgs), c_vp], ctypes.c_int),
     "mamba3_step_ssm": ([ctypes.POINTER(Mamba3StepArgs), c_vp], ctypes.c_int),
+    "mamba2_conv_fwd": ([ctypes.POINTER(Mamba2ConvArgs), c_vp], ctypes.c_int),
+    "mamba2_gated_rmsnorm": ([ctypes.POINTER(Mamba2GatedNormArgs), c_vp], ctypes.c_int),
     "mamba3_prep_fast_path": ([ctypes.POINTER(Mamba3PrepArgs)], ctypes.c_int),
     "mamba3_prep_workspace_size": ([ctypes.POINTER(Mamba3PrepArgs)], ctypes.c_size_t),
     "mamba3_prep_fwd": ([ctypes.POINTER(Mamba3PrepArgs), c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),

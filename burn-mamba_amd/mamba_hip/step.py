@@ -226,9 +226,69 @@ def linear(x: torch.Tensor, packed_w: torch.Tensor, d_out: int, bias: Optional[t
     return out
 
 
+def div_eps(dtype: torch.dtype) -> float:
+    """div_eps (src/utils/mod.rs:50-95) of the reference's tensor dtype."""
+    return {torch.float64: 4.0693917e-16, torch.float32: 8.1584695e-8, torch.float16: 7.1209995e-4,
+            torch.bfloat16: 2.0885676e-5}[dtype]
+
+
+def conv_fwd(cfg: Mamba2Config, zxbcdt: torch.Tensor, cache: Mamba2Cache, conv_w, conv_b, dt_bias,
+             io_dtype=None):
+    """mamba2_conv_fwd (Mamba2::forward steps 2 and 4, src/mamba2/mamba2.rs:618-699):
+    zxbcdt [b, l, d_in_proj] (unit inner stride) -> (xbc [b, l, conv_dim], dt [b, l, nheads] f32).
+    cache.conv_bvk is updated in place."""
+    b, L, row = zxbcdt.shape
+    if row != cfg.d_in_proj or zxbcdt.stride(2) != 1:
+        raise _lib.MambaHipError(f"zxbcdt must be [b, l, {cfg.d_in_proj}] with a unit inner stride")
+    dev = zxbcdt.device
+    xbc = torch.empty((b, L, cfg.conv_dim), device=dev, dtype=io_dtype or zxbcdt.dtype)
+    dt = torch.empty((b, L, cfg.nheads), device=dev, dtype=torch.float32)
+    cs = cache.conv_bvk
+    if cs.dtype != torch.float32 or not cs.is_contiguous() or tuple(cs.shape) != (b, cfg.conv_dim, cfg.conv_kernel):
+        raise _lib.MambaHipError("conv_bvk must be a contiguous f32 [b, conv_dim, conv_kernel] tensor")
+    a = _lib.Mamba2ConvArgs()
+    a.batch, a.seqlen, a.channels, a.kernel, a.nheads = b, L, cfg.conv_dim, cfg.conv_kernel, cfg.nheads
+    a.in_dtype, a.out_dtype = _dtype_code(zxbcdt), _dtype_code(xbc)
+    a.proj, a.proj_sb, a.proj_sl = zxbcdt.data_ptr(), zxbcdt.stride(0), zxbcdt.stride(1)
+    a.xbc_offset, a.dt_offset = cfg.d_inner, cfg.d_inner + cfg.conv_dim
+    a.conv_w = conv_w.contiguous().float().data_ptr()
+    a.conv_b = None if conv_b is None else conv_b.contiguous().float().data_ptr()
+    a.conv_state = cs.data_ptr()
+    a.dt_bias = dt_bias.contiguous().float().data_ptr()
+    a.dt_min, a.dt_max = cfg.dt_limit
+    a.xbc, a.xbc_sb, a.xbc_sl = xbc.data_ptr(), xbc.stride(0), xbc.stride(1)
+    a.dt = dt.data_ptr()
+    check(_lib.lib().mamba2_conv_fwd(ctypes.byref(a), _stream(dev)), "mamba2_conv_fwd")
+    return xbc, dt
+
+
+def gated_rmsnorm(y: torch.Tensor, z: torch.Tensor, gamma: torch.Tensor, eps: Optional[float] = None,
+                  norm_before_gate: bool = False, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """mamba2_gated_rmsnorm (RmsNormGated::forward, src/modules/norm/rms_norm_gated.rs:70-135):
+    y, z [b, l, width] (unit inner stride) -> [b, l, width] in y's dtype.  eps defaults
+    to div_eps of y's dtype, as the reference computes in that dtype."""
+    b, L, W = y.shape
+    if tuple(z.shape) != (b, L, W) or y.stride(2) != 1 or z.stride(2) != 1:
+        raise _lib.MambaHipError("y and z must be [b, l, width] with a unit inner stride")
+    if out is None:
+        out = torch.empty((b, L, W), device=y.device, dtype=y.dtype)
+    g = gamma.contiguous().float()
+    a = _lib.Mamba2GatedNormArgs()
+    a.batch, a.seqlen, a.width, a.norm_before_gate = b, L, W, int(bool(norm_before_gate))
+    a.y_dtype, a.z_dtype, a.out_dtype = _dtype_code(y), _dtype_code(z), _dtype_code(out)
+    a.eps = div_eps(y.dtype) if eps is None else eps
+    a.y, a.y_sb, a.y_sl = y.data_ptr(), y.stride(0), y.stride(1)
+    a.z, a.z_sb, a.z_sl = z.data_ptr(), z.stride(0), z.stride(1)
+    a.gamma = g.data_ptr()
+    a.out, a.out_sb, a.out_sl = out.data_ptr(), out.stride(0), out.stride(1)
+    check(_lib.lib().mamba2_gated_rmsnorm(ctypes.byref(a), _stream(y.device)), "mamba2_gated_rmsnorm")
+    return out
+
+
 @dataclass
 class Mamba2:
-    """Decode-side Mamba2 block (parameters of src/mamba2/mamba2.rs:391-505)."""
+    """Mamba2 block (parameters of src/mamba2/mamba2.rs:391-505): the prefill
+    forward and the decode step."""
     cfg: Mamba2Config
     in_proj_w: torch.Tensor            # [d_model, d_in_proj]
     in_proj_b: Optional[torch.Tensor]
@@ -257,6 +317,37 @@ class Mamba2:
         return Mamba2Cache(
             conv_bvk=torch.zeros(batch, c.conv_dim, c.conv_kernel, device=dev, dtype=torch.float32),
             ssm_bhpr=torch.zeros(batch, c.nheads, c.per_head_dim, c.state_rank, device=dev, dtype=torch.float32))
+
+    def forward(self, input_bsm: torch.Tensor, cache: Optional[Mamba2Cache] = None,
+                chunk_len: Optional[int] = None, init_state_hpr: Optional[torch.Tensor] = None):
+        """Mamba2::forward (src/mamba2/mamba2.rs:546-786): input [b, s, d_model] ->
+        (out [b, s, d_model], cache).  in_proj and out_proj are library GEMMs;
+        the conv prologue (mamba2_conv_fwd), the SSD (mamba_ssd2_fwd on strided
+        views of the conv output, B/C in group form) and the gated RMSNorm
+        (mamba2_gated_rmsnorm) are this library's kernels.  chunk_len None is
+        the reference's optimal chunk (ssd_path.rs:20-163).  The cache is
+        updated: conv window in place, the SSM state replaced."""
+        from .ssd import ssd2_fwd
+        c = self.cfg
+        b, L, _ = input_bsm.shape
+        if cache is None:
+            cache = self.new_cache(b)
+        x = input_bsm.to(self.dtype)
+        zxbcdt = torch.matmul(x, self.in_proj_w)
+        if self.in_proj_b is not None:
+            zxbcdt = zxbcdt + self.in_proj_b
+        xbc, dt = conv_fwd(c, zxbcdt, cache, self.conv_w, self.conv_b, self.dt_bias)
+        H, P, G, N, di = c.nheads, c.per_head_dim, c.ngroups, c.state_rank, c.d_inner
+        xs = xbc[:, :, :di].unflatten(2, (H, P))
+        Bm = xbc[:, :, di:di + G * N].unflatten(2, (G, N))
+        Cm = xbc[:, :, di + G * N:].unflatten(2, (G, N))
+        y, hT = ssd2_fwd(xs, dt, self.A, Bm, Cm, self.d, cache.ssm_bhpr, init_state_hpr, chunk_len=chunk_len)
+        cache.ssm_bhpr = hT
+        yn = gated_rmsnorm(y.flatten(2), zxbcdt[:, :, :di], self.norm_w, norm_before_gate=c.is_norm_before_gate)
+        out = torch.matmul(yn, self.out_proj_w)
+        if self.out_proj_b is not None:
+            out = out + self.out_proj_b
+        return out, cache
 
     def step_into(self, x: torch.Tensor, cache: Mamba2Cache, zx: torch.Tensor, y: torch.Tensor,
                   out: torch.Tensor, workspace: torch.Tensor, events=None):

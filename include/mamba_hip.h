@@ -38,6 +38,10 @@
  *                          (src/modules/layers.rs:427)
  *   mamba_rmsnorm       <- RmsNorm::forward (src/modules/norm/rms_norm.rs:53-98), the
  *                          pre-norm and residual of Layer::step_one (src/modules/layer.rs:224-232)
+ *   mamba2_conv_fwd     <- Mamba2::forward steps 2 and 4 (src/mamba2/mamba2.rs:618-699): causal
+ *                          depthwise conv1d + SiLU over xBC, dt softplus/clamp, conv-cache update
+ *   mamba2_gated_rmsnorm <- RmsNormGated::forward (src/modules/norm/rms_norm_gated.rs:70-135),
+ *                          step 7 of Mamba2::forward (src/mamba2/mamba2.rs:776)
  */
 #ifndef MAMBA_HIP_H
 #define MAMBA_HIP_H
@@ -526,6 +530,50 @@ typedef struct mamba_rmsnorm_args {
 } mamba_rmsnorm_args;
 
 int mamba_rmsnorm(const mamba_rmsnorm_args* args, mamba_stream_t stream);
+
+/* ------------------------------------------------------------------------- */
+/* Mamba-2 prefill prologue: Mamba2::forward steps 2 and 4                     */
+/* (src/mamba2/mamba2.rs:618-699).  From the in_proj rows [b, l, row]:         */
+/*   xbc[b,l,c] = silu(conv_b[c] + sum_k conv_w[c,k] xpad[b,c,l+k])            */
+/* with xpad = [conv_state[b,c,1:] | proj[b,:,xbc_offset + c]] (causal, valid), */
+/*   dt[b,l,h] = clamp(softplus(proj[b,l,dt_offset + h] + dt_bias[h]),         */
+/*                     dt_min, dt_max),                                         */
+/* then conv_state[b,c,:] = the last `kernel` columns of xpad (:652-655),      */
+/* updated in place after the outputs are computed.                            */
+/* ------------------------------------------------------------------------- */
+typedef struct mamba2_conv_args {
+    int32_t batch, seqlen, channels, kernel, nheads; /* channels = conv_dim; kernel <= 8 */
+    int32_t in_dtype, out_dtype;                     /* proj; xbc                  */
+    const void* proj;   int64_t proj_sb, proj_sl;    /* [b, l, row]                */
+    int32_t xbc_offset, dt_offset;                   /* column offsets in a row    */
+    const float* conv_w;                             /* [channels, kernel]         */
+    const float* conv_b;                             /* [channels] or NULL         */
+    float* conv_state;                               /* [b, channels, kernel] in/out */
+    const float* dt_bias;                            /* [nheads]                   */
+    float dt_min, dt_max;
+    void* xbc;          int64_t xbc_sb, xbc_sl;      /* [b, l, channels] out       */
+    float* dt;                                       /* [b, l, nheads] out         */
+} mamba2_conv_args;
+
+int mamba2_conv_fwd(const mamba2_conv_args* args, mamba_stream_t stream);
+
+/* Gated RMSNorm over rows of `width` (RmsNormGated::forward,                  */
+/* src/modules/norm/rms_norm_gated.rs:70-135; Mamba2::forward step 7,         */
+/* src/mamba2/mamba2.rs:776):                                                  */
+/*   norm_before_gate == 0:  g = y silu(z);  out = g / sqrt(mean(g^2) + eps) gamma */
+/*   norm_before_gate != 0:  out = y / sqrt(mean(y^2) + eps) gamma silu(z)    */
+/* eps is the reference's div_eps of its dtype (src/utils/mod.rs:50-95).       */
+typedef struct mamba2_gated_norm_args {
+    int32_t batch, seqlen, width, norm_before_gate;
+    int32_t y_dtype, z_dtype, out_dtype;
+    float eps;
+    const void* y;      int64_t y_sb, y_sl;          /* [b, l, width]              */
+    const void* z;      int64_t z_sb, z_sl;          /* [b, l, width]              */
+    const float* gamma;                              /* [width]                    */
+    void* out;          int64_t out_sb, out_sl;      /* [b, l, width]              */
+} mamba2_gated_norm_args;
+
+int mamba2_gated_rmsnorm(const mamba2_gated_norm_args* args, mamba_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -373,3 +373,64 @@ def mamba3_finish_fwd(y_ssd, v, z, p):
     out = (y_ssd + D[None, None, None, :, None] * v).reshape(b * s, M, H, P)
     y = mamba3_step_finish(out, z.reshape(b * s, H * P), p.get("mimo_z"), p.get("mimo_o"), p.get("out_norm_w"))
     return y.reshape(b, s, H * P)
+
+
+def mamba2_conv_fwd(proj, conv_w, conv_b, conv_state, dt_bias, xbc_offset, dt_offset, channels, nheads,
+                    dt_limit=(0.0, 65504.0)):
+    """Mamba2::forward steps 2 and 4 (src/mamba2/mamba2.rs:618-699) in float64.
+
+    The causal depthwise conv over xpad = [conv_state[:, :, 1:] | xBC] (valid,
+    :634-645, Conv1d cross-correlation) + bias, then SiLU; dt = clamp(softplus(
+    dt_raw + dt_bias)) (:695, softplus threshold 18 as for f32).  The new conv
+    window is the last `kernel` columns of xpad (:652-655).
+    proj [b, l, row] -> (xbc [b, l, channels], dt [b, l, nheads], conv_state' [b, channels, K])."""
+    proj = np.asarray(proj, np.float64)
+    w = np.asarray(conv_w, np.float64)
+    b, L, _ = proj.shape
+    K = w.shape[1]
+    x = proj[:, :, xbc_offset:xbc_offset + channels]
+    tail = np.asarray(conv_state, np.float64)[:, :, 1:].transpose(0, 2, 1)
+    pad = np.concatenate([tail, x], axis=1)  # [b, K - 1 + L, channels]
+    acc = np.zeros((b, L, channels))
+    if conv_b is not None:
+        acc += np.asarray(conv_b, np.float64)
+    for k in range(K):
+        acc += pad[:, k:k + L, :] * w[:, k]
+    xbc = acc / (1.0 + np.exp(-acc))
+    new_state = np.ascontiguousarray(pad[:, L - 1:L - 1 + K, :].transpose(0, 2, 1))
+    raw = proj[:, :, dt_offset:dt_offset + nheads] + np.asarray(dt_bias, np.float64)
+    sp = np.where(raw > 18.0, raw, np.log1p(np.exp(np.minimum(raw, 18.0))))
+    dt = np.clip(sp, dt_limit[0], dt_limit[1])
+    return xbc, dt, new_state
+
+
+def mamba2_gated_rmsnorm(y, z, gamma, eps, norm_before_gate=False):
+    """RmsNormGated::forward (src/modules/norm/rms_norm_gated.rs:70-135) over the
+    last axis in float64: gate-then-norm (default) or norm-then-gate."""
+    y = np.asarray(y, np.float64)
+    z = np.asarray(z, np.float64)
+    sz = z / (1.0 + np.exp(-z))
+    g = y if norm_before_gate else y * sz
+    out = g / np.sqrt(np.mean(g * g, axis=-1, keepdims=True) + eps) * np.asarray(gamma, np.float64)
+    return out * sz if norm_before_gate else out
+
+
+def mamba2_block_fwd(proj, p, conv_state, ssm_state, chunk, cfg, eps=8.1584695e-8):
+    """Mamba2::forward between in_proj and out_proj (src/mamba2/mamba2.rs:546-786):
+    conv prologue -> SSD (ssd2, f64) -> gated RMSNorm with z.  proj [b, l, row];
+    p has conv_w, conv_b, dt_bias, A, D, norm_w.  Returns (y [b, l, d_inner],
+    conv_state', ssm_state')."""
+    H, P, G, N = cfg["nheads"], cfg["headdim"], cfg["ngroups"], cfg["dstate"]
+    d_inner = H * P
+    conv_dim = d_inner + 2 * G * N
+    b, L, _ = proj.shape
+    xbc, dt, cs = mamba2_conv_fwd(proj, p["conv_w"], p.get("conv_b"), conv_state, p["dt_bias"], d_inner,
+                                  d_inner + conv_dim, conv_dim, H, cfg.get("dt_limit", (0.0, 65504.0)))
+    x = xbc[:, :, :d_inner].reshape(b, L, H, P)
+    Bm = xbc[:, :, d_inner:d_inner + G * N].reshape(b, L, G, N)
+    Cm = xbc[:, :, d_inner + G * N:].reshape(b, L, G, N)
+    y, hT = ssd2(x, dt, p["A"], Bm, Cm, p.get("D"), ssm_state, chunk=chunk)
+    z = np.asarray(proj, np.float64)[:, :, :d_inner]
+    yn = mamba2_gated_rmsnorm(np.asarray(y, np.float64).reshape(b, L, d_inner), z, p["norm_w"], eps,
+                              cfg.get("norm_before_gate", False))
+    return yn, cs, hT

@@ -60,7 +60,9 @@ int main(void) {{ printf("%zu\\n", sizeof({struct_name})); {body} return 0; }}
                                              ("Mamba3FinishArgs", "mamba3_finish_args"),
                                              ("LinearArgs", "mamba_linear_args"),
                                              ("Mamba2LayerArgs", "mamba2_layer_args"),
-                                             ("RmsNormArgs", "mamba_rmsnorm_args")])
+                                             ("RmsNormArgs", "mamba_rmsnorm_args"),
+                                             ("Mamba2ConvArgs", "mamba2_conv_args"),
+                                             ("Mamba2GatedNormArgs", "mamba2_gated_norm_args")])
 def test_struct_layouts_match_header(cls_name, c_name):
     from mamba_hip import _lib
     cls = getattr(_lib, cls_name)

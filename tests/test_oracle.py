@@ -546,3 +546,81 @@ def test_mamba3_prefill_then_steps_equals_steps(M, out_norm):
     for t in range(s1, s1 + s2):
         y, c = oracle.mamba3_step(proj[:, t], p, c)
         np.testing.assert_allclose(y, ys[t], rtol=2e-4, atol=2e-5)
+
+
+# ---------------------------------------------------------- Mamba-2 block forward --
+
+@pytest.mark.parametrize("K,L", [(4, 9), (4, 2), (1, 5), (3, 3)])
+def test_mamba2_conv_fwd_equals_conv_steps(K, L):
+    """The prefill conv (mamba2.rs:618-699) over L tokens equals L single conv
+    steps of the C oracle (conv1d_step, the decode window of mamba2.rs:870-905)
+    from the same cache, outputs and final window (also when L < K)."""
+    rng = np.random.default_rng(K * 10 + L)
+    b, c = 2, 12
+    proj = rng.standard_normal((b, L, c + 9)).astype(np.float32)
+    w = rng.standard_normal((c, K)).astype(np.float32)
+    bias = rng.standard_normal(c).astype(np.float32)
+    st = rng.standard_normal((b, c, K)).astype(np.float32)
+    xbc, _, ns = oracle.mamba2_conv_fwd(proj, w, bias, st, np.zeros(3, np.float32), 4, 4 + c, c, 3)
+    s = st.copy()
+    for l in range(L):
+        o, s = oracle.conv1d_step(proj[:, l, 4:4 + c], s, w, bias, True)
+        np.testing.assert_allclose(xbc[:, l], o, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(ns, s, rtol=0, atol=0)
+
+
+def test_mamba2_conv_fwd_dt_closed_form():
+    """dt = clamp(softplus(raw + bias)): log(2) at zero, the identity above the
+    threshold, and the clamp limits."""
+    proj = np.array([[[0.0, 30.0, -40.0]]], np.float32)
+    _, dt, _ = oracle.mamba2_conv_fwd(proj, np.ones((1, 1), np.float32), None, np.zeros((1, 1, 1), np.float32),
+                                      np.zeros(3, np.float32), 0, 0, 1, 3, dt_limit=(1e-3, 25.0))
+    np.testing.assert_allclose(dt[0, 0], [np.log(2.0), 25.0, 1e-3], rtol=1e-12)
+
+
+def test_mamba2_gated_rmsnorm_closed_forms():
+    """A constant row normalises to sign * gamma (up to eps); the norm is scale
+    invariant; norm-then-gate multiplies the normalised row by silu(z)."""
+    W = 16
+    gamma = np.linspace(0.5, 1.5, W)
+    z = np.full((1, W), 0.7)
+    y = np.full((1, W), -3.0)
+    out = oracle.mamba2_gated_rmsnorm(y, z, gamma, 1e-12)
+    np.testing.assert_allclose(out[0], -gamma, rtol=1e-9)
+    rng = np.random.default_rng(3)
+    y2, z2 = rng.standard_normal((4, W)), rng.standard_normal((4, W))
+    np.testing.assert_allclose(oracle.mamba2_gated_rmsnorm(5.0 * y2, z2, gamma, 1e-14),
+                               oracle.mamba2_gated_rmsnorm(y2, z2, gamma, 1e-14), rtol=1e-9)
+    sz = 0.7 / (1 + np.exp(-0.7))
+    np.testing.assert_allclose(oracle.mamba2_gated_rmsnorm(y, z, gamma, 1e-12, norm_before_gate=True)[0],
+                               -gamma * sz, rtol=1e-9)
+
+
+@pytest.mark.parametrize("norm_before_gate", [False, True])
+def test_mamba2_block_fwd_equals_steps(norm_before_gate):
+    """Mamba2::forward between the projections over L tokens (conv prologue ->
+    SSD -> gated norm) equals L decode steps (the C oracle's mamba2_step_ssm,
+    pinned against its own closed forms) from the same caches: every token's
+    output and both final caches."""
+    rng = np.random.default_rng(11 + norm_before_gate)
+    b, L, H, P, G, N, K = 2, 10, 4, 8, 2, 8, 4
+    d_inner = H * P
+    conv_dim = d_inner + 2 * G * N
+    row = d_inner + conv_dim + H
+    cfg = dict(nheads=H, headdim=P, ngroups=G, dstate=N, norm_before_gate=norm_before_gate)
+    p = dict(conv_w=(rng.standard_normal((conv_dim, K)) / 2).astype(np.float32),
+             conv_b=(0.1 * rng.standard_normal(conv_dim)).astype(np.float32),
+             dt_bias=rng.uniform(-3, -1, H).astype(np.float32),
+             A=(-np.exp(rng.uniform(0, np.log(8), H))).astype(np.float32),
+             D=rng.standard_normal(H).astype(np.float32), norm_w=rng.uniform(0.5, 1.5, d_inner).astype(np.float32))
+    proj = rng.standard_normal((b, L, row)).astype(np.float32)
+    cs0 = rng.standard_normal((b, conv_dim, K)).astype(np.float32)
+    ss0 = (0.1 * rng.standard_normal((b, H, P, N))).astype(np.float32)
+    y, cs, ss = oracle.mamba2_block_fwd(proj, p, cs0, ss0, chunk=4, cfg=cfg)
+    c_s, s_s = cs0, ss0
+    for l in range(L):
+        o, c_s, s_s = oracle.mamba2_step_ssm(proj[:, l], c_s, p["conv_w"], p["conv_b"], p["dt_bias"], p["A"], p["D"],
+                                             p["norm_w"], s_s, H, P, G, N, norm_before_gate=norm_before_gate)
+        np.testing.assert_allclose(y[:, l], o, rtol=2e-4, atol=2e-5)
+    np.testing.assert_allclose(cs, c_s, rtol=0, atol=0)
+    np.testing.assert_allclose(ss, s_s, rtol=1e-4, atol=1e-6)
