@@ -496,7 +496,7 @@ def bench_mamba3_prep(args):
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": "synthetic (config-4 shapes, reference init, in_proj rows ~N(0,1), seed 0)",
         "config": {"workload": "mamba3_prep_cfg4", **cfg, "io": "proj/v/B/C bf16, coefficients and states f32",
-                   "entry": "mamba3_prep_fwd (seed + prep kernels)"},
+                   "entry": "mamba3_prep_fwd (seed, angle-total and segment prep kernels)"},
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": gbs / HBM_PEAK_GBS, "traffic": None, "kernel_ms": kern_ms,
                      "algorithmic_bytes": nbytes,
@@ -889,13 +889,159 @@ def bench_ssd2(args):
     return out
 
 
+MAMBA2_BLOCK_CFG1 = dict(batch=8, seqlen=4096, d_model=2560, chunk=256)
+
+
+def mamba2_block_algorithmic(cfg):
+    """Per-phase compulsory HBM bytes and FLOPs of one Mamba2.forward at the
+    config-1 block shape (d_model 2560: 80 heads x 64, d_state 128, one group,
+    conv width 4), all activations bf16, states f32:
+      in_proj  x read, weight read, zxbcdt written; 2*tok*d_model*d_in_proj flops
+      conv     xBC + dt columns read, xbc (bf16) and dt (f32) written, conv window r+w
+      ssd      as the SSD workload, plus the initial state read from the cache
+      norm     y and z read, normed output written
+      out_proj normed output read, weight read, out written; 2*tok*d_inner*d_model flops"""
+    import mamba_hip
+    c = mamba_hip.Mamba2Config(d_model=cfg["d_model"])
+    b, L = cfg["batch"], cfg["seqlen"]
+    tok = b * L
+    dm, di, dip, cd, H, P, N, K = (c.d_model, c.d_inner, c.d_in_proj, c.conv_dim, c.nheads, c.per_head_dim,
+                                   c.state_rank, c.conv_kernel)
+    ssd_cfg = dict(batch=b, seqlen=L, nheads=H, headdim=P, dstate=N, ngroups=c.ngroups, chunk=cfg["chunk"])
+    ssd_bytes, ssd_flops = ssd2_algorithmic(ssd_cfg)
+    return {
+        "in_proj": (tok * dm * 2 + dm * dip * 2 + tok * dip * 2, 2 * tok * dm * dip),
+        "conv": (tok * (cd + H) * 2 + tok * cd * 2 + tok * H * 4 + 2 * b * cd * K * 4 + cd * (K + 1) * 4 + H * 4,
+                 tok * cd * (2 * K + 4)),
+        "ssd": (ssd_bytes + b * H * P * N * 4, ssd_flops),
+        "norm": (3 * tok * di * 2 + di * 4, 6 * tok * di),
+        "out_proj": (tok * di * 2 + di * dm * 2 + tok * dm * 2, 2 * tok * di * dm),
+    }
+
+
+def bench_mamba2_block(args):
+    """Mamba2.forward (full block prefill: in_proj -> conv prologue -> SSD ->
+    gated RMSNorm -> out_proj) at the config-1 shape, B=8 L=4096, bf16."""
+    import torch
+
+    import mamba_hip
+    cfg = dict(MAMBA2_BLOCK_CFG1)
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    c = mamba_hip.Mamba2Config(d_model=cfg["d_model"])
+    m = c.init(dev, torch.bfloat16, gen)
+    b, L = cfg["batch"], cfg["seqlen"]
+    x = torch.randn((b, L, c.d_model), generator=gen, device=dev).to(torch.bfloat16)
+    cache = m.new_cache(b)
+    # the SSD inside the block takes the MFMA path on the conv output's views
+    xbc = torch.empty((b, L, c.conv_dim), device=dev, dtype=torch.bfloat16)
+    di, N = c.d_inner, c.state_rank
+    assert mamba_hip.ssd2_fast_path(xbc[:, :, :di].unflatten(2, (c.nheads, c.per_head_dim)),
+                                    torch.empty((b, L, c.nheads), device=dev), m.A,
+                                    xbc[:, :, di:di + N].unflatten(2, (1, N)),
+                                    xbc[:, :, di + N:].unflatten(2, (1, N)), chunk_len=cfg["chunk"])
+    del xbc
+
+    def step(events=None):
+        m.forward(x, cache, chunk_len=cfg["chunk"], events=events)
+
+    log(f"warmup {args.warmup}")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} steps")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    marks = []
+    for _ in range(args.steps):
+        ev = []
+        step(events=ev)
+        marks.append(ev)
+    torch.cuda.synchronize()
+    names = [n for n, _ in marks[0]][1:]
+    phase_ms = {n: sum(ev[i][1].elapsed_time(ev[i + 1][1]) for ev in marks) / len(marks)
+                for i, n in enumerate(names)}
+    alg = mamba2_block_algorithmic(cfg)
+    phases = {}
+    for n in names:
+        nbytes, flops = alg[n]
+        t = phase_ms[n] * 1e-3
+        hbm_s, mfma_s = nbytes / (HBM_PEAK_GBS * 1e9), flops / (BF16_PEAK_TFLOPS * 1e12)
+        bound = "hbm" if hbm_s >= mfma_s else "mfma"
+        achieved = nbytes / t / 1e9 if bound == "hbm" else flops / t / 1e12
+        peak = HBM_PEAK_GBS if bound == "hbm" else BF16_PEAK_TFLOPS
+        phases[n] = {"ms": phase_ms[n], "bound": bound, "achieved": achieved, "peak": peak,
+                     "unit": "GB/s" if bound == "hbm" else "TFLOP/s", "frac": achieved / peak,
+                     "algorithmic_bytes": nbytes, "flops": flops}
+    log("phases " + ", ".join(f"{n} {phase_ms[n]:.3f} ms ({phases[n]['frac']:.3f})" for n in names))
+    dom = max(names, key=lambda n: phase_ms[n])
+    d = phases[dom]
+    ideal_ms = sum(max(alg[n][0] / (HBM_PEAK_GBS * 1e9), alg[n][1] / (BF16_PEAK_TFLOPS * 1e12)) for n in names) * 1e3
+    tokens = b * L
+    return {
+        "metric": "Mamba-2 block prefill tokens/s (2.7B-shaped layer, B=8 L=4096 d_model 2560) + % roofline",
+        "value": tokens / (ms_per_step * 1e-3), "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (reference init of the block, input ~N(0,1), seed 0)",
+        "config": {"workload": "mamba2_block_prefill_cfg1", **cfg, "nheads": c.nheads, "headdim": c.per_head_dim,
+                   "dstate": c.state_rank, "ngroups": c.ngroups, "conv_kernel": c.conv_kernel,
+                   "entry": "Mamba2.forward: torch matmul in_proj/out_proj, mamba2_conv_fwd, mamba_ssd2_fwd, "
+                            "mamba2_gated_rmsnorm"},
+        "roofline": {"bound": d["bound"], "achieved": d["achieved"], "peak": d["peak"], "unit": d["unit"],
+                     "frac": d["frac"], "traffic": None, "kernel": dom, "kernel_ms": d["ms"],
+                     "timing": "HIP events on the launch stream between the block's phases, mean over steps",
+                     "block_ideal_ms": ideal_ms, "block_frac": ideal_ms / sum(phase_ms.values()),
+                     "phases": phases},
+    }
+
+
+def cpu_baseline_mamba2_block(cfg, seed=0):
+    """The block on the CPU: in_proj and out_proj as numpy f32 products and
+    oracle.mamba2_block_fwd (conv prologue, the f64 serial SSD, gated norm) on
+    one batch row of the full length, scaled per token."""
+    import numpy as np
+
+    import mamba_hip
+    import oracle
+    oracle.build()
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    c = mamba_hip.Mamba2Config(d_model=cfg["d_model"])
+    rng = np.random.default_rng(seed)
+    L = cfg["seqlen"]
+    H, P, N, K = c.nheads, c.per_head_dim, c.state_rank, c.conv_kernel
+    win = (rng.uniform(-1, 1, (c.d_model, c.d_in_proj)) / np.sqrt(c.d_model)).astype(np.float32)
+    wout = (rng.uniform(-1, 1, (c.d_inner, c.d_model)) / np.sqrt(c.d_inner)).astype(np.float32)
+    p = dict(conv_w=(rng.uniform(-0.5, 0.5, (c.conv_dim, K))).astype(np.float32),
+             conv_b=np.zeros(c.conv_dim, np.float32), dt_bias=np.full(H, -3.0, np.float32),
+             A=-np.arange(1, H + 1, dtype=np.float32), D=np.ones(H, np.float32),
+             norm_w=np.ones(c.d_inner, np.float32))
+    cfgd = dict(nheads=H, headdim=P, ngroups=c.ngroups, dstate=N, norm_before_gate=c.is_norm_before_gate,
+                dt_limit=c.dt_limit)
+    x = rng.standard_normal((1, L, c.d_model)).astype(np.float32)
+    t0 = time.perf_counter()
+    proj = x @ win
+    yn, _, _ = oracle.mamba2_block_fwd(proj, p, np.zeros((1, c.conv_dim, K), np.float32),
+                                       np.zeros((1, H, P, N), np.float32), cfg["chunk"], cfgd)
+    _ = yn.astype(np.float32) @ wout
+    el = time.perf_counter() - t0
+    return {"value": L / el, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"one batch row of {cfg['batch']} ({L} tokens): numpy f32 in/out products and the "
+                      f"oracle's conv, f64 serial SSD and gated norm, {el:.2f} s, per token"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="ssd2",
-                    choices=["ssd2", "mamba1", "decode", "ssd3", "mamba1_step", "mamba3_step", "mamba3_prep"])
+                    choices=["ssd2", "mamba1", "decode", "ssd3", "mamba1_step", "mamba3_step", "mamba3_prep",
+                             "mamba2_block"])
     ap.add_argument("--batch", type=int, default=DECODE_CFG3["batch"], help="decode batch")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -907,7 +1053,10 @@ def main():
               "(the hot path shards by batch/head with no communication; see DESIGN.md)",
               file=sys.stderr)
         sys.exit(2)
-    if args.workload == "mamba3_prep":
+    if args.workload == "mamba2_block":
+        out = bench_mamba2_block(args)
+        base = (lambda: cpu_baseline_mamba2_block(MAMBA2_BLOCK_CFG1))
+    elif args.workload == "mamba3_prep":
         out = bench_mamba3_prep(args)
         base = (lambda: cpu_baseline_mamba3_prep(SSD3_CFG4))
     elif args.workload == "mamba3_step":

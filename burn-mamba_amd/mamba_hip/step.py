@@ -319,34 +319,52 @@ class Mamba2:
             ssm_bhpr=torch.zeros(batch, c.nheads, c.per_head_dim, c.state_rank, device=dev, dtype=torch.float32))
 
     def forward(self, input_bsm: torch.Tensor, cache: Optional[Mamba2Cache] = None,
-                chunk_len: Optional[int] = None, init_state_hpr: Optional[torch.Tensor] = None):
+                chunk_len: Optional[int] = None, init_state_hpr: Optional[torch.Tensor] = None,
+                events: Optional[list] = None):
         """Mamba2::forward (src/mamba2/mamba2.rs:546-786): input [b, s, d_model] ->
         (out [b, s, d_model], cache).  in_proj and out_proj are library GEMMs;
         the conv prologue (mamba2_conv_fwd), the SSD (mamba_ssd2_fwd on strided
         views of the conv output, B/C in group form) and the gated RMSNorm
         (mamba2_gated_rmsnorm) are this library's kernels.  chunk_len None is
         the reference's optimal chunk (ssd_path.rs:20-163).  The cache is
-        updated: conv window in place, the SSM state replaced."""
+        updated: conv window in place, the SSM state replaced.
+
+        events: if a list, a timing event is recorded on the current stream
+        before the first phase and after each phase, and appended as (phase,
+        event) with phase in start, in_proj, conv, ssd, norm, out_proj."""
         from .ssd import ssd2_fwd
+
+        def mark(phase):
+            if events is not None:
+                ev = torch.cuda.Event(enable_timing=True)
+                ev.record()
+                events.append((phase, ev))
+
         c = self.cfg
         b, L, _ = input_bsm.shape
         if cache is None:
             cache = self.new_cache(b)
         x = input_bsm.to(self.dtype)
+        mark("start")
         zxbcdt = torch.matmul(x, self.in_proj_w)
         if self.in_proj_b is not None:
             zxbcdt = zxbcdt + self.in_proj_b
+        mark("in_proj")
         xbc, dt = conv_fwd(c, zxbcdt, cache, self.conv_w, self.conv_b, self.dt_bias)
+        mark("conv")
         H, P, G, N, di = c.nheads, c.per_head_dim, c.ngroups, c.state_rank, c.d_inner
         xs = xbc[:, :, :di].unflatten(2, (H, P))
         Bm = xbc[:, :, di:di + G * N].unflatten(2, (G, N))
         Cm = xbc[:, :, di + G * N:].unflatten(2, (G, N))
         y, hT = ssd2_fwd(xs, dt, self.A, Bm, Cm, self.d, cache.ssm_bhpr, init_state_hpr, chunk_len=chunk_len)
         cache.ssm_bhpr = hT
+        mark("ssd")
         yn = gated_rmsnorm(y.flatten(2), zxbcdt[:, :, :di], self.norm_w, norm_before_gate=c.is_norm_before_gate)
+        mark("norm")
         out = torch.matmul(yn, self.out_proj_w)
         if self.out_proj_b is not None:
             out = out + self.out_proj_b
+        mark("out_proj")
         return out, cache
 
     def step_into(self, x: torch.Tensor, cache: Mamba2Cache, zx: torch.Tensor, y: torch.Tensor,
