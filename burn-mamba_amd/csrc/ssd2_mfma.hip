@@ -6,8 +6,9 @@
 //
 // Two launches per call:
 //   1. ssd2_prep_mfma (per batch, chunk, group): the group-shared causal
-//      C_c.B_c^T tiles in f32 (K2, computed once per group instead of once per
-//      head), and C_c and B_c in bf16, all three stored in MFMA operand order
+//      C_c.B_c^T tiles (K2, computed once per group instead of once per head,
+//      f32 accumulation rounded to bf16), and C_c and B_c in bf16, all three
+//      stored in MFMA operand order
 //      so that every wave load of them is one contiguous 1 KB.
 //   2. ssd2_scan_mfma: one workgroup per (batch, head[, half of headdim])
 //      walks the chunks in order.  The running state h[p, n] lives in MFMA
