@@ -62,8 +62,9 @@ __device__ void ssd3_chunk_tables(const Ssd3Params& p, int b, int c, int h, floa
         __syncthreads();
         if (l < p.Q) {
             cs[l] = v + off + carry;
-            scl[l] = ok ? p.sc[(int64_t)b * p.sc_sb + (int64_t)t * p.sc_sl + (int64_t)h * p.sc_sh] : 0.f;
-            gmm[l] = ok ? p.gm[(int64_t)b * p.gm_sb + (int64_t)t * p.gm_sl + (int64_t)h * p.gm_sh] : 0.f;
+            // NULL scale / gamma: unit coefficients (the double-SSD seam)
+            scl[l] = !ok ? 0.f : p.sc ? p.sc[(int64_t)b * p.sc_sb + (int64_t)t * p.sc_sl + (int64_t)h * p.sc_sh] : 1.f;
+            gmm[l] = !ok ? 0.f : p.gm ? p.gm[(int64_t)b * p.gm_sb + (int64_t)t * p.gm_sl + (int64_t)h * p.gm_sh] : 1.f;
         }
         __syncthreads();
         carry = cs[min(base + 256, p.Q) - 1];
@@ -221,7 +222,8 @@ __global__ __launch_bounds__(256) void ssd3_chunk_scan_generic(Ssd3Params p, con
 }
 
 // ------------------------------------------------------------ host side --
-static int ssd3_make_params(const mamba_ssd3_args* a, Ssd3Params* out) {
+// unit: the double-SSD seam, whose gamma and scale are NULL (unit coefficients)
+static int ssd3_make_params(const mamba_ssd3_args* a, Ssd3Params* out, bool unit = false) {
     MAMBA_CHECK_ARG(a != nullptr, "args is NULL");
     MAMBA_CHECK_ARG(a->batch > 0 && a->seqlen > 0 && a->mimo > 0, "batch, seqlen and mimo must be >= 1");
     MAMBA_CHECK_ARG(a->nheads > 0 && a->headdim > 0 && a->dstate > 0, "nheads/headdim/dstate must be >= 1");
@@ -229,8 +231,10 @@ static int ssd3_make_params(const mamba_ssd3_args* a, Ssd3Params* out) {
     MAMBA_CHECK_ARG(a->ngroups > 0 && a->nheads % a->ngroups == 0, "nheads must be a multiple of ngroups");
     MAMBA_CHECK_ARG(a->chunk_len > 0 && a->chunk_len * a->mimo <= 4096, "chunk_len * mimo must be in [1, 4096]");
     MAMBA_CHECK_ARG(a->io_dtype == MAMBA_F32 || a->io_dtype == MAMBA_BF16, "io_dtype must be MAMBA_F32 or MAMBA_BF16");
-    MAMBA_CHECK_ARG(a->v && a->da && a->gamma && a->scale && a->B && a->C && a->y && a->final_state,
-                    "v, da, gamma, scale, B, C, y and final_state are required");
+    MAMBA_CHECK_ARG(a->v && a->da && a->B && a->C && a->y && a->final_state,
+                    "v, da, B, C, y and final_state are required");
+    MAMBA_CHECK_ARG(unit ? (a->gamma == nullptr && a->scale == nullptr) : (a->gamma && a->scale),
+                    "gamma and scale are required");
     Ssd3Params& p = *out;
     p.nb = a->batch; p.L = a->seqlen; p.M = a->mimo; p.H = a->nheads; p.P = a->headdim; p.G = a->ngroups;
     p.N = a->dstate; p.Q = a->chunk_len; p.nch = (a->seqlen + a->chunk_len - 1) / a->chunk_len;
@@ -255,9 +259,9 @@ bool ssd3_mfma_supported(const mamba_ssd3_args* a);
 int ssd3_mfma_launch(const mamba_ssd3_args* a, hipStream_t stream, hipEvent_t ev0, hipEvent_t ev1);
 
 static int ssd3_dispatch(const mamba_ssd3_args* a, void* ws, size_t ws_bytes, hipStream_t stream, hipEvent_t ev0,
-                         hipEvent_t ev1, bool allow_fast) {
+                         hipEvent_t ev1, bool allow_fast, bool unit = false) {
     Ssd3Params p;
-    int st = ssd3_make_params(a, &p);
+    int st = ssd3_make_params(a, &p, unit);
     if (st != MAMBA_OK) return st;
     if (allow_fast && ssd3_mfma_supported(a)) return ssd3_mfma_launch(a, stream, ev0, ev1);
     const size_t need = ssd3_ws_bytes(p);
@@ -283,6 +287,22 @@ static int ssd3_dispatch(const mamba_ssd3_args* a, void* ws, size_t ws_bytes, hi
     MAMBA_CHECK_LAUNCH();
     if (ev1) MAMBA_CHECK_HIP(hipEventRecord(ev1, stream));
     return MAMBA_OK;
+}
+
+// The double-SSD seam's arguments as single-SSD arguments with unit coefficients.
+static mamba_ssd3_args ssd3_from_double(const mamba_ssd3_double_args* d) {
+    mamba_ssd3_args a{};
+    a.batch = d->batch; a.seqlen = d->seqlen; a.mimo = d->mimo; a.nheads = d->nheads; a.headdim = d->headdim;
+    a.ngroups = d->ngroups; a.dstate = d->dstate; a.chunk_len = d->chunk_len; a.io_dtype = d->io_dtype;
+    a.v = d->v; a.v_sb = d->v_sb; a.v_sl = d->v_sl; a.v_sm = d->v_sm; a.v_sh = d->v_sh;
+    a.da = d->da; a.da_sb = d->da_sb; a.da_sl = d->da_sl; a.da_sh = d->da_sh;
+    a.gamma = nullptr; a.scale = nullptr;
+    a.B = d->B; a.B_sb = d->B_sb; a.B_sl = d->B_sl; a.B_sm = d->B_sm; a.B_sg = d->B_sg;
+    a.C = d->C; a.C_sb = d->C_sb; a.C_sl = d->C_sl; a.C_sm = d->C_sm; a.C_sg = d->C_sg;
+    a.initial_state = d->initial_state;
+    a.y = d->y; a.y_sb = d->y_sb; a.y_sl = d->y_sl; a.y_sm = d->y_sm; a.y_sh = d->y_sh;
+    a.final_state = d->final_state;
+    return a;
 }
 
 }  // namespace mamba
@@ -316,4 +336,40 @@ extern "C" int mamba_ssd3_fwd_timed(const mamba_ssd3_args* a, void* ws, size_t w
         return MAMBA_ERR_INVALID_ARG;
     }
     return ssd3_dispatch(a, ws, ws_bytes, (hipStream_t)stream, (hipEvent_t)ev_start, (hipEvent_t)ev_stop, true);
+}
+
+extern "C" size_t mamba_ssd3_double_workspace_size(const mamba_ssd3_double_args* d) {
+    if (d == nullptr) return 0;
+    const mamba_ssd3_args a = ssd3_from_double(d);
+    Ssd3Params p;
+    if (ssd3_make_params(&a, &p, true) != MAMBA_OK) return 0;
+    return ssd3_ws_bytes(p);
+}
+
+extern "C" int mamba_ssd3_double_fast_path(const mamba_ssd3_double_args* d) {
+    if (d == nullptr) return -1;
+    const mamba_ssd3_args a = ssd3_from_double(d);
+    Ssd3Params p;
+    if (ssd3_make_params(&a, &p, true) != MAMBA_OK) return -1;
+    return ssd3_mfma_supported(&a) ? 1 : 0;
+}
+
+extern "C" int mamba_ssd3_double_fwd(const mamba_ssd3_double_args* d, void* ws, size_t ws_bytes,
+                                     mamba_stream_t stream) {
+    if (d == nullptr) {
+        set_error("args is NULL");
+        return MAMBA_ERR_INVALID_ARG;
+    }
+    const mamba_ssd3_args a = ssd3_from_double(d);
+    return ssd3_dispatch(&a, ws, ws_bytes, (hipStream_t)stream, nullptr, nullptr, true, true);
+}
+
+extern "C" int mamba_ssd3_double_fwd_generic(const mamba_ssd3_double_args* d, void* ws, size_t ws_bytes,
+                                             mamba_stream_t stream) {
+    if (d == nullptr) {
+        set_error("args is NULL");
+        return MAMBA_ERR_INVALID_ARG;
+    }
+    const mamba_ssd3_args a = ssd3_from_double(d);
+    return ssd3_dispatch(&a, ws, ws_bytes, (hipStream_t)stream, nullptr, nullptr, false, true);
 }

@@ -164,7 +164,8 @@ __device__ __forceinline__ void ssd3_y_tile(Ssd3Lds<QF>& S, const s3_bf16x8_t (&
     }
 }
 
-template <int QF>
+// UNIT: the double-SSD seam, scale = gamma = 1 at every position (no tables read)
+template <int QF, bool UNIT>
 __global__ __launch_bounds__(256, 1) void ssd3_scan_mfma(Ssd3MfmaParams p) {
     constexpr int N = 128;
     constexpr int T = QF / 32;            // output tiles per chunk (one per wave)
@@ -238,12 +239,18 @@ __global__ __launch_bounds__(256, 1) void ssd3_scan_mfma(Ssd3MfmaParams p) {
         }
         const int64_t t0 = f0 >> lgM;
         const __amdgpu_buffer_rsrc_t rda = s3_rsrc(dahead + t0 * p.da_sl, (uint32_t)steps * (uint32_t)p.da_sl * 4);
-        const __amdgpu_buffer_rsrc_t rsc = s3_rsrc(schead + t0 * p.sc_sl, (uint32_t)steps * (uint32_t)p.sc_sl * 4);
-        const __amdgpu_buffer_rsrc_t rgm = s3_rsrc(gmhead + t0 * p.gm_sl, (uint32_t)steps * (uint32_t)p.gm_sl * 4);
         const float dav = s3_bld4(rda, dao);
         daq = first_m ? dav : 0.f;  // da enters the cumulative sum once per step
-        scq = s3_bld4(rsc, sco);
-        gmq = s3_bld4(rgm, gmo);
+        if constexpr (UNIT) {
+            // positions past the end carry v = B = 0, so their unit factor is inert
+            scq = 1.f;
+            gmq = 1.f;
+        } else {
+            const __amdgpu_buffer_rsrc_t rsc = s3_rsrc(schead + t0 * p.sc_sl, (uint32_t)steps * (uint32_t)p.sc_sl * 4);
+            const __amdgpu_buffer_rsrc_t rgm = s3_rsrc(gmhead + t0 * p.gm_sl, (uint32_t)steps * (uint32_t)p.gm_sl * 4);
+            scq = s3_bld4(rsc, sco);
+            gmq = s3_bld4(rgm, gmo);
+        }
     };
     // this wave's C fragments of a chunk: issued a chunk ahead, after the
     // current fragments are dead, so only one set is held in registers
@@ -411,7 +418,11 @@ int ssd3_mfma_launch(const mamba_ssd3_args* a, hipStream_t stream, hipEvent_t ev
     p.y = static_cast<bf16_t*>(a->y); p.y_sb = a->y_sb; p.y_sf = a->y_sm; p.y_sh = a->y_sh;
     p.hT = a->final_state;
     if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, stream));
-    hipLaunchKernelGGL(ssd3_scan_mfma<QF>, dim3(p.nb * p.H * 2), dim3(256), 0, stream, p);
+    // gamma and scale are NULL only for the double-SSD seam (unit coefficients)
+    if (a->gamma == nullptr)
+        hipLaunchKernelGGL((ssd3_scan_mfma<QF, true>), dim3(p.nb * p.H * 2), dim3(256), 0, stream, p);
+    else
+        hipLaunchKernelGGL((ssd3_scan_mfma<QF, false>), dim3(p.nb * p.H * 2), dim3(256), 0, stream, p);
     MAMBA_CHECK_LAUNCH();
     if (ev1) MAMBA_CHECK_HIP(hipEventRecord(ev1, stream));
     return MAMBA_OK;

@@ -58,6 +58,20 @@ class Ssd3Args(ctypes.Structure):
     ]
 
 
+class Ssd3DoubleArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", c_i32), ("seqlen", c_i32), ("mimo", c_i32), ("nheads", c_i32), ("headdim", c_i32),
+        ("ngroups", c_i32), ("dstate", c_i32), ("chunk_len", c_i32), ("io_dtype", c_i32),
+        ("v", c_vp), ("v_sb", c_i64), ("v_sl", c_i64), ("v_sm", c_i64), ("v_sh", c_i64),
+        ("da", c_vp), ("da_sb", c_i64), ("da_sl", c_i64), ("da_sh", c_i64),
+        ("B", c_vp), ("B_sb", c_i64), ("B_sl", c_i64), ("B_sm", c_i64), ("B_sg", c_i64),
+        ("C", c_vp), ("C_sb", c_i64), ("C_sl", c_i64), ("C_sm", c_i64), ("C_sg", c_i64),
+        ("initial_state", c_vp),
+        ("y", c_vp), ("y_sb", c_i64), ("y_sl", c_i64), ("y_sm", c_i64), ("y_sh", c_i64),
+        ("final_state", c_vp),
+    ]
+
+
 class Mamba1ScanArgs(ctypes.Structure):
     _fields_ = [
         ("batch", c_i32), ("dim", c_i32), ("seqlen", c_i32), ("dstate", c_i32),
@@ -232,6 +246,10 @@ _SIGNATURES = {
     "mamba_ssd3_fwd": ([ctypes.POINTER(Ssd3Args), c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),
     "mamba_ssd3_fwd_generic": ([ctypes.POINTER(Ssd3Args), c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),
     "mamba_ssd3_fwd_timed": ([ctypes.POINTER(Ssd3Args), c_vp, ctypes.c_size_t, c_vp, c_vp, c_vp], ctypes.c_int),
+    "mamba_ssd3_double_workspace_size": ([ctypes.POINTER(Ssd3DoubleArgs)], ctypes.c_size_t),
+    "mamba_ssd3_double_fast_path": ([ctypes.POINTER(Ssd3DoubleArgs)], ctypes.c_int),
+    "mamba_ssd3_double_fwd": ([ctypes.POINTER(Ssd3DoubleArgs), c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),
+    "mamba_ssd3_double_fwd_generic": ([ctypes.POINTER(Ssd3DoubleArgs), c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),
     "mamba1_scan_fwd": ([ctypes.POINTER(Mamba1ScanArgs), c_vp], ctypes.c_int),
     "mamba1_scan_fwd_timed": ([ctypes.POINTER(Mamba1ScanArgs), c_vp, c_vp, c_vp], ctypes.c_int),
     "mamba1_scan_step": ([ctypes.POINTER(Mamba1StepArgs), c_vp], ctypes.c_int),

@@ -1,8 +1,12 @@
-"""Mamba-3 single-pass SSD host interface over the C ABI (``mamba_ssd3_fwd``).
+"""Mamba-3 SSD host interfaces over the C ABI: the single-pass SSD
+(``mamba_ssd3_fwd``) and the double-SSD seam (``mamba_ssd3_double_fwd``).
 
-Reference: ``Mamba3SingleSsdInput`` / ``run`` (src/mamba3/single_ssd/ssd/ssd_path/mod.rs:25-133)
+References: ``Mamba3SingleSsdInput`` / ``run`` (src/mamba3/single_ssd/ssd/ssd_path/mod.rs:25-133)
 and ``Mamba3SingleSsdBackendExt::single_ssd_serial_recalculated``
-(src/mamba3/single_ssd/ssd/serial_recalculated/serial_recalculated.rs:86-164).
+(src/mamba3/single_ssd/ssd/serial_recalculated/serial_recalculated.rs:86-164);
+``Mamba3DoubleSsdInput`` (src/mamba3/double_ssd/ssd/ssd_path/mod.rs) and
+``Mamba3DoubleSsdBackendExt::double_ssd_serial_recalculated``
+(src/mamba3/double_ssd/ssd/serial_recalculated/serial_recalculated.rs:76-94).
 The reference's chunked [b, n, l, ...] tensors are the [b, n*l, ...] tensors
 here with chunk_len = l.  Tensors are PyTorch device tensors used as memory.
 """
@@ -16,7 +20,7 @@ from typing import Optional
 import torch
 
 from . import _lib
-from ._lib import Ssd3Args, check
+from ._lib import Ssd3Args, Ssd3DoubleArgs, check
 from .ssd import _dtype_code, _raw_events, _stream, workspace
 
 
@@ -78,6 +82,7 @@ def ssd3_fwd(v, da, B, C, gamma, scale, initial_state=None, chunk_len=64, y=None
     L = _lib.lib()
     need = L.mamba_ssd3_workspace_size(ctypes.byref(a))
     if need == 0:
+        # invalid arguments: the call reports why
         check(L.mamba_ssd3_fwd(ctypes.byref(a), None, 0, _stream(v.device)), "mamba_ssd3_fwd")
     ws = workspace(v.device, need)
     st, wsp = _stream(v.device), ctypes.c_void_p(ws.data_ptr())
@@ -118,3 +123,78 @@ class Mamba3SingleSsdInput:
             h0 = (base + self.init_state_hpr.unsqueeze(0)).contiguous()
         return ssd3_fwd(self.v_blmhp, self.da_blh, self.b_blmhr, self.c_blmhr, self.gamma_blh, self.scale_blh,
                         h0, chunk_len)
+
+
+def _double_args(v, da, B, C, initial_state, chunk_len, y, final_state) -> Ssd3DoubleArgs:
+    b, l, m, h, p = v.shape
+    if B.shape != C.shape or B.shape[:3] != (b, l, m):
+        raise _lib.MambaHipError("B and C must be [b, l, m, g, n] matching v")
+    for t, nm in ((v, "v"), (B, "B"), (C, "C")):
+        if t.stride(-1) != 1:
+            raise _lib.MambaHipError(f"{nm}: innermost axis must be contiguous")
+    if da.dtype != torch.float32 or da.shape != (b, l, h):
+        raise _lib.MambaHipError("da must be float32 [b, l, h]")
+    for t in (initial_state, final_state):
+        if t is not None and (t.dtype != torch.float32 or not t.is_contiguous()):
+            raise _lib.MambaHipError("states must be contiguous float32")
+    a = Ssd3DoubleArgs()
+    a.batch, a.seqlen, a.mimo, a.nheads, a.headdim, a.ngroups, a.dstate = b, l, m, h, p, B.shape[3], B.shape[4]
+    a.chunk_len, a.io_dtype = int(chunk_len), _dtype_code(v)
+    a.v = v.data_ptr(); a.v_sb, a.v_sl, a.v_sm, a.v_sh = v.stride()[:4]
+    a.da = da.data_ptr(); a.da_sb, a.da_sl, a.da_sh = da.stride()
+    a.B = B.data_ptr(); a.B_sb, a.B_sl, a.B_sm, a.B_sg = B.stride()[:4]
+    a.C = C.data_ptr(); a.C_sb, a.C_sl, a.C_sm, a.C_sg = C.stride()[:4]
+    a.initial_state = None if initial_state is None else initial_state.data_ptr()
+    a.y = y.data_ptr(); a.y_sb, a.y_sl, a.y_sm, a.y_sh = y.stride()[:4]
+    a.final_state = final_state.data_ptr()
+    return a
+
+
+def ssd3_double_fast_path(v, da, B, C, chunk_len=64) -> bool:
+    """True when ``ssd3_double_fwd`` takes the single-kernel MFMA path for these tensors."""
+    y, hT = _outputs(v, B, None, None)
+    a = _double_args(v, da, B, C, None, chunk_len, y, hT)
+    r = _lib.lib().mamba_ssd3_double_fast_path(ctypes.byref(a))
+    if r < 0:
+        check(1, "mamba_ssd3_double_fast_path")
+    return r == 1
+
+
+def ssd3_double_fwd(v, da, B, C, initial_state=None, chunk_len=64, y=None, final_state=None, generic=False):
+    """The double-SSD seam: v (pre-scaled) [b, l, m, h, p]; da [b, l, h] f32; B, C
+    [b, l, m, g, n]; initial_state [b, h, p, n] f32.  Returns (y, final_state)
+    with y[t, m] = C[t, m] . h_t, h_t = exp(da_t) h_{t-1} + sum_m' v[t, m'] (x) B[t, m'].
+    ``generic`` forces the shape-generic kernels."""
+    y, final_state = _outputs(v, B, y, final_state)
+    a = _double_args(v, da, B, C, initial_state, chunk_len, y, final_state)
+    L = _lib.lib()
+    st = _stream(v.device)
+    need = L.mamba_ssd3_double_workspace_size(ctypes.byref(a))
+    if need == 0:
+        # invalid arguments: the call reports why
+        check(L.mamba_ssd3_double_fwd(ctypes.byref(a), None, 0, st), "mamba_ssd3_double_fwd")
+    ws = workspace(v.device, need)
+    fn = L.mamba_ssd3_double_fwd_generic if generic else L.mamba_ssd3_double_fwd
+    check(fn(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), ws.numel(), st), "mamba_ssd3_double_fwd")
+    return y, final_state
+
+
+@dataclass
+class Mamba3DoubleSsdInput:
+    """The double-SSD seam's input bundle (src/mamba3/double_ssd/ssd/ssd_path/mod.rs)
+    with [b, l, ...] tensors (the chunk axis folded into l).  ``init_state_hpr``
+    (the learnable initial state) is added to ``initial_state_bhpr``."""
+    v_blmhp: torch.Tensor
+    da_blh: torch.Tensor
+    b_blmhr: torch.Tensor
+    c_blmhr: torch.Tensor
+    initial_state_bhpr: Optional[torch.Tensor] = None
+    init_state_hpr: Optional[torch.Tensor] = None
+
+    def run(self, chunk_len: int = 64):
+        h0 = self.initial_state_bhpr
+        if self.init_state_hpr is not None:
+            base = h0 if h0 is not None else torch.zeros(
+                (self.v_blmhp.shape[0],) + tuple(self.init_state_hpr.shape), device=self.v_blmhp.device)
+            h0 = (base + self.init_state_hpr.unsqueeze(0)).contiguous()
+        return ssd3_double_fwd(self.v_blmhp, self.da_blh, self.b_blmhr, self.c_blmhr, h0, chunk_len)

@@ -20,6 +20,8 @@
  *                          reached from Mamba2SsdInput::run (src/mamba2/ssd/ssd_path.rs:149-155)
  *   mamba_ssd3_fwd      <- Mamba3SingleSsdBackendExt::single_ssd_serial_recalculated
  *                          (src/mamba3/single_ssd/ssd/serial_recalculated/serial_recalculated.rs:86-114)
+ *   mamba_ssd3_double_fwd <- Mamba3DoubleSsdBackendExt::double_ssd_serial_recalculated
+ *                          (src/mamba3/double_ssd/ssd/serial_recalculated/serial_recalculated.rs:76-94)
  *   mamba1_scan_fwd     <- Mamba1::selective_scan (src/mamba1/mamba1.rs:422-430)
  *                          plus the silu(z) gate of Mamba1::forward (mamba1.rs:348)
  *   mamba1_scan_step    <- Mamba1::selective_scan_step (src/mamba1/mamba1.rs:666-733)
@@ -176,6 +178,37 @@ int mamba_ssd3_fwd_generic(const mamba_ssd3_args* args, void* workspace, size_t 
 /* kernel (benchmark timing; no counterpart in the reference).                 */
 int mamba_ssd3_fwd_timed(const mamba_ssd3_args* args, void* workspace, size_t workspace_bytes,
                          mamba_stream_t stream, void* event_start, void* event_stop);
+
+/* ---- Mamba-3 double SSD (the Mamba3DoubleSsdBackendExt seam) ------------- */
+/* Mamba3DoubleSsdBackendExt::double_ssd_serial_recalculated                   */
+/* (src/mamba3/double_ssd/ssd/serial_recalculated/serial_recalculated.rs:76-94; */
+/* K1-K5 in src/mamba3/double_ssd/ssd/serial.rs:118-409): v, da, B, C, h0 ->  */
+/* y, final state, with the same chunk axis folding and strides as            */
+/* mamba_ssd3_args.  v arrives pre-scaled (no scale or gamma column), and the */
+/* fused-rank causal mask keeps every rank pair of the same step (triu(1) on  */
+/* steps): y[t, m] = C[t, m] . h_t with h_t = exp(da_t) h_{t-1} +             */
+/* sum_m' v[t, m'] (x) B[t, m'].  The single-SSD kernels run it with unit     */
+/* coefficients; the fast-path conditions are those of mamba_ssd3_fwd.        */
+typedef struct mamba_ssd3_double_args {
+    int32_t batch, seqlen, mimo, nheads, headdim, ngroups, dstate, chunk_len;
+    int32_t io_dtype;                                      /* v, B, C, y           */
+    const void* v;      int64_t v_sb, v_sl, v_sm, v_sh;      /* [b, l, m, h, p]      */
+    const float* da;    int64_t da_sb, da_sl, da_sh;         /* [b, l, h]  dt * A    */
+    const void* B;      int64_t B_sb, B_sl, B_sm, B_sg;      /* [b, l, m, g, n]      */
+    const void* C;      int64_t C_sb, C_sl, C_sm, C_sg;      /* [b, l, m, g, n]      */
+    const float* initial_state;                              /* [b, h, p, n] or NULL */
+    void* y;            int64_t y_sb, y_sl, y_sm, y_sh;      /* [b, l, m, h, p]      */
+    float* final_state;                                      /* [b, h, p, n] f32     */
+} mamba_ssd3_double_args;
+
+size_t mamba_ssd3_double_workspace_size(const mamba_ssd3_double_args* args);
+/* 1 / 0 / -1 as mamba_ssd3_fast_path.  No counterpart in the reference.       */
+int mamba_ssd3_double_fast_path(const mamba_ssd3_double_args* args);
+int mamba_ssd3_double_fwd(const mamba_ssd3_double_args* args, void* workspace, size_t workspace_bytes,
+                          mamba_stream_t stream);
+/* Same contract, forced onto the shape-generic kernels (cross-checks).        */
+int mamba_ssd3_double_fwd_generic(const mamba_ssd3_double_args* args, void* workspace,
+                                  size_t workspace_bytes, mamba_stream_t stream);
 
 /* ------------------------------------------------------------------------- */
 /* Mamba-1 selective scan (f32), with the optional dt bias + softplus of       */

@@ -204,6 +204,52 @@ def mamba2_layer_step(u, params, conv_state, ssm_state, cfg, prec=64):
 # Mamba-3 single-pass SSD (src/mamba3/single_ssd/ssd/serial.rs:56-268)
 # --------------------------------------------------------------------------
 
+def ssd3_double(v, da, B, C, h0=None, chunk=64):
+    """Mamba3DoubleSsdBackendExt::double_ssd_serial_recalculated, f64 numpy,
+    following its K1-K5 (src/mamba3/double_ssd/ssd/serial.rs:118-409):
+    v[b,l,m,h,p] (pre-scaled) da[b,l,h] B,C[b,l,m,h,n] h0[b,h,p,n] -> (y, hT).
+    The sequence is zero-padded to whole chunks (double_ssd/double_ssd/mod.rs:215-245);
+    K1 cumsum of da per chunk; K2 C.B^T on the fused (step, rank) axis; K3
+    chunk states with exp(cs_end - cs) v (x) B; K4 the serial state passing;
+    K5 exp(cs_i) C_i h_in + (C.B^T * exp(cs_i - cs_j), kept where step(j) <=
+    step(i): the triu(1) step mask of serial.rs:366-398) @ v."""
+    v, da, B, C = (np.asarray(t, np.float64) for t in (v, da, B, C))
+    b, l, m, h, p = v.shape
+    n = B.shape[-1]
+    assert B.shape == C.shape == (b, l, m, h, n) and da.shape == (b, l, h)
+    Q = int(chunk)
+    nch = -(-l // Q)
+    L = nch * Q
+    pad = L - l
+
+    def padl(t):
+        return np.concatenate([t, np.zeros((b, pad) + t.shape[2:])], 1) if pad else t
+
+    v, da, B, C = map(padl, (v, da, B, C))
+    # fused index f = step * m + rank inside a chunk
+    vf = v.reshape(b, nch, Q * m, h, p).transpose(0, 1, 3, 2, 4)     # [b, c, h, QM, p]
+    Bf = B.reshape(b, nch, Q * m, h, n).transpose(0, 1, 3, 2, 4)     # [b, c, h, QM, n]
+    Cf = C.reshape(b, nch, Q * m, h, n).transpose(0, 1, 3, 2, 4)
+    cs = np.cumsum(da.reshape(b, nch, Q, h), axis=2).transpose(0, 1, 3, 2)   # K1 [b, c, h, Q]
+    end = cs[..., -1]                                                  # [b, c, h]
+    csf = np.repeat(cs, m, axis=3)                                     # [b, c, h, QM]
+    cb = Cf @ Bf.transpose(0, 1, 2, 4, 3)                              # K2 [b, c, h, QM, QM]
+    states = (np.exp(end[..., None] - csf)[..., None] * vf).transpose(0, 1, 2, 4, 3) @ Bf  # K3 [b,c,h,p,n]
+    hin = np.zeros((b, nch, h, p, n))                                  # K4
+    run = np.zeros((b, h, p, n)) if h0 is None else np.asarray(h0, np.float64)
+    for c in range(nch):
+        hin[:, c] = run
+        run = np.exp(end[:, c])[..., None, None] * run + states[:, c]
+    step = np.repeat(np.arange(Q), m)
+    keep = step[None, :] <= step[:, None]                              # [QM target, QM source]
+    diff = csf[..., :, None] - csf[..., None, :]
+    decay = np.where(keep, np.exp(np.where(keep, diff, 0.0)), 0.0)
+    blue = np.exp(csf)[..., None] * (Cf @ hin.transpose(0, 1, 2, 4, 3))  # [b, c, h, QM, p]
+    orange = (cb * decay) @ vf
+    y = (blue + orange).transpose(0, 1, 3, 2, 4).reshape(b, L, m, h, p)[:, :l]
+    return y, run
+
+
 def ssd3(v, da, B, C, gamma, scale, h0=None, chunk=64, form="serial", prec=64):
     """v[b,l,m,h,p] da,gamma,scale[b,l,h] B,C[b,l,m,h,n] h0[b,h,p,n] -> (y[b,l,m,h,p], hT)."""
     v, da, B, C, gamma, scale, h0 = map(_f32, (v, da, B, C, gamma, scale, h0))

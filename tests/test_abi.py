@@ -51,6 +51,7 @@ int main(void) {{ printf("%zu\\n", sizeof({struct_name})); {body} return 0; }}
 
 
 @pytest.mark.parametrize("cls_name,c_name", [("Ssd2Args", "mamba_ssd2_args"), ("Ssd3Args", "mamba_ssd3_args"),
+                                             ("Ssd3DoubleArgs", "mamba_ssd3_double_args"),
                                              ("Mamba1ScanArgs", "mamba1_scan_args"),
                                              ("Mamba1StepArgs", "mamba1_step_args"),
                                              ("Conv1dStepArgs", "mamba_conv1d_step_args"),

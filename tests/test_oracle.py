@@ -279,6 +279,66 @@ def test_ssd3_serial_equals_recurrent_and_trapezoid(m):
     np.testing.assert_allclose(y0, yt, rtol=1e-5, atol=1e-6)
 
 
+def _double_recurrence(v, da, B, C, h0):
+    """The double-SSD seam as a token loop (the textbook SSM recurrence the
+    chunked K1-K5 factor): h_t = exp(da_t) h_{t-1} + sum_m v[t, m] (x) B[t, m],
+    y[t, m] = C[t, m] . h_t."""
+    b, l, m, h, p = v.shape
+    hs = np.asarray(h0, np.float64).copy()
+    y = np.zeros((b, l, m, h, p))
+    for t in range(l):
+        hs = np.exp(da[:, t].astype(np.float64))[:, :, None, None] * hs + np.einsum(
+            "bmhp,bmhn->bhpn", v[:, t].astype(np.float64), B[:, t].astype(np.float64))
+        y[:, t] = np.einsum("bmhn,bhpn->bmhp", C[:, t].astype(np.float64), hs)
+    return y, hs
+
+
+@pytest.mark.parametrize("m,chunk", [(1, 4), (2, 5), (4, 8)])
+def test_ssd3_double_equals_recurrence(m, chunk):
+    """K1-K5 of the double seam (ragged last chunk included) equal the token
+    recurrence, from a non-zero initial state."""
+    d = _m3_inputs(17 + m, b=2, l=19, m=m, h=3, p=4, n=6)
+    yd, hd = oracle.ssd3_double(d["v"], d["da"], d["B"], d["C"], d["h0"], chunk=chunk)
+    yr, hr = _double_recurrence(d["v"], d["da"], d["B"], d["C"], d["h0"])
+    np.testing.assert_allclose(yd, yr, rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(hd, hr, rtol=1e-10, atol=1e-12)
+
+
+def test_ssd3_double_is_single_with_unit_coefficients():
+    """The double seam is the (pinned) single-SSD seam with scale = gamma = 1:
+    weight 1 on every earlier step and on the same step's rank pairs."""
+    d = _m3_inputs(23, b=1, l=21, m=2, h=2, p=4, n=5)
+    one = np.ones_like(d["gamma"])
+    ys, hs = oracle.ssd3(d["v"], d["da"], d["B"], d["C"], one, one, d["h0"], chunk=8)
+    yd, hd = oracle.ssd3_double(d["v"], d["da"], d["B"], d["C"], d["h0"], chunk=6)
+    np.testing.assert_allclose(yd, ys, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(hd, hs, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("m", [1, 2, 4])
+def test_single_ssd_equals_double_ssd_pathway(m):
+    """The reference's single == double relation (Mamba-3 forward, single_ssd
+    vs double_ssd pathways): the gamma call (gamma_t v_t, B_t, cached state)
+    plus the beta call (beta_t v_{t-1}, B_{t-1}, cache's v_prev / K_prev at
+    t = 0, zero state) of the double seam equal one single-SSD call from the
+    seeded state h0 + (dt_0 - gamma_0) sum_m v_prev (x) K_prev."""
+    b, l, h, p, n = 2, 23, 2, 4, 6
+    d = _m3_inputs(60 + m, b=b, l=l, m=m, h=h, p=p, n=n)
+    rng = np.random.default_rng(61 + m)
+    v_prev = rng.standard_normal((b, m, h, p))
+    k_prev = rng.standard_normal((b, m, h, n)) / np.sqrt(n)
+    v, B, C = d["v"], d["B"], d["C"]
+    gamma = d["gamma"].astype(np.float64)
+    vs = np.concatenate([v_prev[:, None], v[:, :-1]], 1)
+    bs = np.concatenate([k_prev[:, None], B[:, :-1]], 1)
+    yg, hg = oracle.ssd3_double(gamma[:, :, None, :, None] * v, d["da"], B, C, d["h0"], chunk=8)
+    yb, hb = oracle.ssd3_double(d["beta"][:, :, None, :, None] * vs, d["da"], bs, C, None, chunk=8)
+    seed = (d["dt"][:, 0] - gamma[:, 0])[:, :, None, None] * np.einsum("bmhp,bmhn->bhpn", v_prev, k_prev)
+    ys, hs = oracle.ssd3(v, d["da"], B, C, d["gamma"], d["scale"], (d["h0"] + seed).astype(np.float32), chunk=8)
+    np.testing.assert_allclose(yg + yb, ys, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(hg + hb, hs, rtol=1e-5, atol=1e-6)
+
+
 def test_ssd3_lambda_one_is_mamba2():
     """lam = 1 removes the beta term: gamma = scale = dt and the single-SSD is
     the Mamba-2 SSD without D (src/mamba3/mamba3.rs:28)."""
