@@ -24,6 +24,10 @@ template <typename T> __device__ __forceinline__ void m2_st1(T* q, float v);
 template <> __device__ __forceinline__ void m2_st1<float>(float* q, float v) { *q = v; }
 template <> __device__ __forceinline__ void m2_st1<bf16_t>(bf16_t* q, float v) { *q = f32_to_bf16(v); }
 
+// SiLU x / (1 + e^-x) (silu.rs:24-27) with the hardware reciprocal (1 ulp)
+// in place of an IEEE division; x -> -inf gives x * rcp(inf) = -0.
+__device__ __forceinline__ float m2_silu(float x) { return x * __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
+
 // 8 consecutive elements at a 16-byte aligned address
 template <typename T> __device__ __forceinline__ void m2_ld8(const T* q, float* o);
 template <> __device__ __forceinline__ void m2_ld8<float>(const float* q, float* o) {
@@ -61,13 +65,14 @@ struct M2ConvParams {
 };
 
 constexpr int kM2ConvTile = 64;  // positions per workgroup
+constexpr int kM2ConvRows = 8;   // input rows in flight per thread
 constexpr int kM2MaxK = 8;
 
 // One thread per VW consecutive channels over a tile of kM2ConvTile positions:
 // the last K - 1 inputs stay in registers, so every input is read once.
 // Channels c of position l: sum_k w[c][k] xpad[l + k] with xpad = [the
-// window's last K - 1 columns | the new inputs].  Blocks with blockIdx.y == 0
-// also write the tile's dt.
+// window's last K - 1 columns | the new inputs].  The channel blocks of a
+// tile also share out the tile's dt.
 template <typename TI, typename TO, int VW, int K>
 __global__ __launch_bounds__(256) void mamba2_conv_kernel(M2ConvParams p) {
     const int tile = blockIdx.x, b = blockIdx.z;
@@ -86,27 +91,29 @@ __global__ __launch_bounds__(256) void mamba2_conv_kernel(M2ConvParams p) {
         float win[K > 1 ? K - 1 : 1][VW];
 #pragma unroll
         for (int j = 0; j < K - 1; ++j) {
-            const int l = l0 - (K - 1) + j;
+            const int l = l0 - (K - 1) + j;  // uniform over the workgroup
+            bool done = false;
+            if constexpr (VW == 8) {
+                if (l >= 0) {
+                    m2_ld8(proj + (int64_t)l * p.proj_sl + p.xbc_off + c0, win[j]);
+                    done = true;
+                }
+            }
+            if (!done) {
 #pragma unroll
-            for (int e = 0; e < VW; ++e) {
-                float v;
-                if (l >= 0)
-                    v = m2_ld1(proj + (int64_t)l * p.proj_sl + p.xbc_off + c0 + e);
-                else  // cache column (K + l): the window's last K - 1 columns end at column K - 1
-                    v = p.state[((int64_t)b * p.V + c0 + e) * K + K + l];
-                win[j][e] = v;
+                for (int e = 0; e < VW; ++e) {
+                    float v;
+                    if (l >= 0)
+                        v = m2_ld1(proj + (int64_t)l * p.proj_sl + p.xbc_off + c0 + e);
+                    else  // cache column (K + l): the window's last K - 1 columns end at column K - 1
+                        v = p.state[((int64_t)b * p.V + c0 + e) * K + K + l];
+                    win[j][e] = v;
+                }
             }
         }
         TO* out = static_cast<TO*>(p.out) + (int64_t)b * p.out_sb;
-        for (int l = l0; l < l1; ++l) {
-            float x[VW];
-            const TI* src = proj + (int64_t)l * p.proj_sl + p.xbc_off + c0;
-            if constexpr (VW == 8) {
-                m2_ld8(src, x);
-            } else {
-#pragma unroll
-                for (int e = 0; e < VW; ++e) x[e] = m2_ld1(src + e);
-            }
+        // one position: convolve, slide the window, store
+        auto emit = [&](int l, const float* x) {
             float y[VW];
 #pragma unroll
             for (int e = 0; e < VW; ++e) {
@@ -114,7 +121,7 @@ __global__ __launch_bounds__(256) void mamba2_conv_kernel(M2ConvParams p) {
 #pragma unroll
                 for (int k = 0; k < K - 1; ++k) acc += w[e][k] * win[k][e];
                 acc += w[e][K - 1] * x[e];
-                y[e] = acc / (1.f + __expf(-acc));  // SiLU
+                y[e] = m2_silu(acc);
             }
 #pragma unroll
             for (int j = 0; j + 1 < K - 1; ++j)
@@ -131,14 +138,55 @@ __global__ __launch_bounds__(256) void mamba2_conv_kernel(M2ConvParams p) {
 #pragma unroll
                 for (int e = 0; e < VW; ++e) m2_st1(dst + e, y[e]);
             }
+        };
+        auto load = [&](int l, float* x) {
+            const TI* src = proj + (int64_t)l * p.proj_sl + p.xbc_off + c0;
+            if constexpr (VW == 8) {
+                m2_ld8(src, x);
+            } else {
+#pragma unroll
+                for (int e = 0; e < VW; ++e) x[e] = m2_ld1(src + e);
+            }
+        };
+        // kM2ConvRows rows are loaded before any is used, so their HBM
+        // latencies overlap instead of adding up row by row
+        int l = l0;
+        for (; l + kM2ConvRows <= l1; l += kM2ConvRows) {
+            float xs[kM2ConvRows][VW];
+#pragma unroll
+            for (int u = 0; u < kM2ConvRows; ++u) load(l + u, xs[u]);
+#pragma unroll
+            for (int u = 0; u < kM2ConvRows; ++u) emit(l + u, xs[u]);
+        }
+        for (; l < l1; ++l) {
+            float x[VW];
+            load(l, x);
+            emit(l, x);
         }
     }
-    if (blockIdx.y == 0) {
-        for (int i = threadIdx.x; i < (l1 - l0) * p.H; i += 256) {
-            const int l = l0 + i / p.H, h = i % p.H;
-            const float raw = m2_ld1(proj + (int64_t)l * p.proj_sl + p.dt_off + h) + p.dt_bias[h];
-            const float sp = raw > 18.f ? raw : log1pf(__expf(raw));
-            p.dt[((int64_t)b * p.L + l) * p.H + h] = fminf(fmaxf(sp, p.dt_lo), p.dt_hi);
+    // the tile's dt, its (position, head) pairs split over the channel blocks;
+    // each thread issues all its loads before its stores
+    {
+        const int n = (l1 - l0) * p.H, per = (n + gridDim.y - 1) / gridDim.y;
+        const int i0 = blockIdx.y * per, i1 = min(n, i0 + per);
+        constexpr int kU = 4;
+        for (int ib = i0 + (int)threadIdx.x; ib < i1; ib += 256 * kU) {
+            float raw[kU];
+#pragma unroll
+            for (int u = 0; u < kU; ++u) {
+                const int i = ib + 256 * u;
+                raw[u] = i < i1 ? m2_ld1(proj + (int64_t)(l0 + i / p.H) * p.proj_sl + p.dt_off + i % p.H) : 0.f;
+            }
+#pragma unroll
+            for (int u = 0; u < kU; ++u) {
+                const int i = ib + 256 * u;
+                if (i < i1) {
+                    const int l = l0 + i / p.H, h = i % p.H;
+                    const float v = raw[u] + p.dt_bias[h];
+                    const float sp = v > 18.f ? v : log1pf(__expf(v));
+                    p.dt[((int64_t)b * p.L + l) * p.H + h] = fminf(fmaxf(sp, p.dt_lo), p.dt_hi);
+                }
+            }
         }
     }
 }
@@ -200,7 +248,7 @@ __global__ __launch_bounds__(256) void mamba2_gated_norm_kernel(M2NormParams p) 
         load(c, yv, zv);
 #pragma unroll
         for (int e = 0; e < VW; ++e) {
-            const float g = p.before ? yv[e] : yv[e] * (zv[e] / (1.f + __expf(-zv[e])));
+            const float g = p.before ? yv[e] : yv[e] * m2_silu(zv[e]);
             ss += g * g;
         }
     }
@@ -211,7 +259,7 @@ __global__ __launch_bounds__(256) void mamba2_gated_norm_kernel(M2NormParams p) 
         load(c, yv, zv);
 #pragma unroll
         for (int e = 0; e < VW; ++e) {
-            const float sz = zv[e] / (1.f + __expf(-zv[e]));
+            const float sz = m2_silu(zv[e]);
             const float g = p.before ? yv[e] : yv[e] * sz;
             o[e] = (g * inv) * p.gamma[c + e];
             if (p.before) o[e] *= sz;
@@ -220,6 +268,76 @@ __global__ __launch_bounds__(256) void mamba2_gated_norm_kernel(M2NormParams p) 
             m2_st8(out + c, o);
         } else {
             m2_st1(out + c, o[0]);
+        }
+    }
+}
+
+// bf16 y and z with the whole row held in registers (packed, 8 per uint4):
+// every load of a row is issued before its reduction, and the output pass
+// reads nothing from memory again but gamma.  One wave per row (a wave that
+// finishes frees its slot for a new row at once; a grid-stride walk over rows
+// with gamma in LDS measured slower).  NI = vectors of 8 per lane, the row
+// width is at most 512 NI.
+__device__ __forceinline__ void m2_unpack8(const uint4 u, float* o) {
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        o[2 * k] = __uint_as_float(w[k] << 16);
+        o[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+    }
+}
+
+template <typename TO, int NI>
+__global__ __launch_bounds__(256) void mamba2_gated_norm_res_kernel(M2NormParams p) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= (int64_t)p.nb * p.L) return;  // whole waves exit together
+    const int b = (int)(row / p.L), l = (int)(row % p.L);
+    const bf16_t* y = static_cast<const bf16_t*>(p.y) + (int64_t)b * p.y_sb + (int64_t)l * p.y_sl;
+    const bf16_t* z = static_cast<const bf16_t*>(p.z) + (int64_t)b * p.z_sb + (int64_t)l * p.z_sl;
+    TO* out = static_cast<TO*>(p.out) + (int64_t)b * p.out_sb + (int64_t)l * p.out_sl;
+    uint4 yr[NI], zr[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const int c = (i * 64 + lane) * 8;
+        if (c < p.W) {
+            yr[i] = *(const uint4*)(y + c);
+            zr[i] = *(const uint4*)(z + c);
+        }
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const int c = (i * 64 + lane) * 8;
+        if (c < p.W) {
+            float yv[8], zv[8];
+            m2_unpack8(yr[i], yv);
+            m2_unpack8(zr[i], zv);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float g = p.before ? yv[e] : yv[e] * m2_silu(zv[e]);
+                ss += g * g;
+            }
+        }
+    }
+    ss = wave_sum(ss);
+    const float inv = 1.f / sqrtf(ss / (float)p.W + p.eps);
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const int c = (i * 64 + lane) * 8;
+        if (c < p.W) {
+            float yv[8], zv[8], gm[8], o[8];
+            m2_unpack8(yr[i], yv);
+            m2_unpack8(zr[i], zv);
+            m2_ld8(p.gamma + c, gm);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float sz = m2_silu(zv[e]);
+                const float g = p.before ? yv[e] : yv[e] * sz;
+                o[e] = (g * inv) * gm[e];
+                if (p.before) o[e] *= sz;
+            }
+            m2_st8(out + c, o);
         }
     }
 }
@@ -326,7 +444,27 @@ extern "C" int mamba2_gated_rmsnorm(const mamba2_gated_norm_args* a, mamba_strea
     hipStream_t s = (hipStream_t)stream;
     const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
     const bool yb = a->y_dtype == MAMBA_BF16, zb = a->z_dtype == MAMBA_BF16, ob = a->out_dtype == MAMBA_BF16;
-#define M2N(TY, TZ, TO)                                                                       \
+    if (vec && yb && zb && p.W <= 512 * 16) {
+        // rows held in registers: ceil(W / 512) vectors of 8 per lane, rounded up to even
+        const int ni = ((p.W + 1023) / 1024) * 2;
+#define M2R1(TO, NI) \
+    case NI: hipLaunchKernelGGL((mamba2_gated_norm_res_kernel<TO, NI>), grid, block, 0, s, p); break;
+#define M2R(TO)                                                                            \
+    switch (ni) {                                                                          \
+        M2R1(TO, 2) M2R1(TO, 4) M2R1(TO, 6) M2R1(TO, 8) M2R1(TO, 10) M2R1(TO, 12) M2R1(TO, 14) \
+        default: hipLaunchKernelGGL((mamba2_gated_norm_res_kernel<TO, 16>), grid, block, 0, s, p); \
+    }
+        if (ob) {
+            M2R(bf16_t)
+        } else {
+            M2R(float)
+        }
+#undef M2R
+#undef M2R1
+        MAMBA_CHECK_LAUNCH();
+        return MAMBA_OK;
+    }
+#define M2N(TY, TZ, TO)                                                                     \
     if (vec)                                                                                  \
         hipLaunchKernelGGL((mamba2_gated_norm_kernel<TY, TZ, TO, 8>), grid, block, 0, s, p); \
     else                                                                                      \

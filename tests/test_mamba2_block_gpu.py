@@ -72,7 +72,8 @@ def test_mamba2_conv_fwd_matches_oracle(case, dtype):
 
 
 @pytest.mark.parametrize("before", [False, True])
-@pytest.mark.parametrize("dtype,W", [("f32", 96), ("bf16", 5120), ("f32", 37)])
+@pytest.mark.parametrize("dtype,W", [("f32", 96), ("bf16", 5120), ("f32", 37), ("bf16", 1000), ("bf16", 3072),
+                                     ("bf16", 37), ("bf16-f32out", 2048)])
 def test_mamba2_gated_rmsnorm_matches_oracle(dtype, W, before):
     import torch
     import mamba_hip
@@ -82,13 +83,16 @@ def test_mamba2_gated_rmsnorm_matches_oracle(dtype, W, before):
     y = rng.standard_normal((b, L, W)).astype(np.float32)
     zw = rng.standard_normal((b, L, W + 24)).astype(np.float32)  # z as a slice of a wider row
     gamma = rng.uniform(0.5, 1.5, W).astype(np.float32)
-    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    tdt = torch.float32 if dtype == "f32" else torch.bfloat16
     yt, zt = _t(y, tdt), _t(zw, tdt)[:, :, 8:8 + W]
-    out = mamba_hip.mamba2_gated_rmsnorm(yt, zt, _t(gamma), norm_before_gate=before)
+    # bf16 rows of 8-multiple width take the register-resident kernel, the rest the streaming one
+    out = None if dtype != "bf16-f32out" else torch.empty((b, L, W), device="cuda")
+    out = mamba_hip.mamba2_gated_rmsnorm(yt, zt, _t(gamma), norm_before_gate=before, out=out)
     torch.cuda.synchronize()
     want = oracle.mamba2_gated_rmsnorm(yt.float().cpu().numpy(), zt.float().cpu().numpy(), gamma,
                                        mamba_hip.div_eps(tdt), before)
-    np.testing.assert_allclose(out.float().cpu().numpy(), want, **(BF16_TOL if dtype == "bf16" else F32_TOL))
+    tol = {"f32": F32_TOL, "bf16": BF16_TOL, "bf16-f32out": F32_TOL}[dtype]
+    np.testing.assert_allclose(out.float().cpu().numpy(), want, **tol)
 
 
 def _model(cfg, seed, dtype):
