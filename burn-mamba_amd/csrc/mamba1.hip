@@ -10,7 +10,7 @@
 // decay, so the work is VALU-bound (one exp, two multiplies and two FMAs per
 // state per token).  A workgroup owns 64 channels of one batch row; each
 // channel is spread over N/4 lanes holding 4 states each, so for dstate 16 the
-// per-token y reduction is a quad DPP sum.  Time is processed in tiles of 32 tokens that
+// per-token y reduction is a quad DPP sum.  Time is processed in tiles of 16 tokens that
 // are staged through LDS with coalesced loads (the next tile's loads are issued
 // into registers before the current tile is computed); softplus, delta*u, D*u
 // and silu(z) are evaluated once per element in the staging pass.
@@ -36,7 +36,7 @@ struct Mamba1Params {
 };
 
 constexpr float kLog2eM1 = 1.4426950408889634f;
-constexpr int kTT = 16;  // tokens per staged tile
+constexpr int kTT = 16;  // tokens per staged tile (32 measured slower: the staging registers spill)
 
 // softplus(x) = log(1 + e^x); above 20 it equals x to f32 precision (the
 // reference's Burn softplus overflows to inf above ~88.7 instead).
@@ -85,12 +85,14 @@ __global__ __launch_bounds__(16 * N, N <= 16 ? 3 : 1) void mamba1_scan_kernel(Ma
     // tile, read along time when the inputs are time-contiguous (TM) and along
     // channels otherwise.  u, delta, z and y share one stride pair (checked on
     // the host), so one loop-invariant 32-bit offset addresses all four.
-    auto e_lc = [&](int e) { const int idx = tid + NT * e; return TM ? idx / kTT : idx % CPB; };
-    auto e_lt = [&](int e) { const int idx = tid + NT * e; return TM ? idx % kTT : idx / CPB; };
-    int e_off[EPT];
-#pragma unroll
-    for (int e = 0; e < EPT; ++e)
-        e_off[e] = (int)((int64_t)(d0 + e_lc(e)) * p.u_sd + (int64_t)e_lt(e) * p.u_sl);
+    // NT is a multiple of kTT and of CPB, so element e of a thread sits a
+    // fixed step from its element 0: e_off(e) = e_base + e * e_step.
+    static_assert(NT % kTT == 0 && NT % CPB == 0, "element steps must be uniform");
+    auto e_lc = [&](int e) { return TM ? tid / kTT + (NT / kTT) * e : tid % CPB; };
+    auto e_lt = [&](int e) { return TM ? tid % kTT : tid / CPB + (NT / CPB) * e; };
+    const int e_base = (int)((int64_t)(d0 + e_lc(0)) * p.u_sd + (int64_t)e_lt(0) * p.u_sl);
+    const int e_step = (int)(TM ? (int64_t)(NT / kTT) * p.u_sd : (int64_t)(NT / CPB) * p.u_sl);
+    auto e_off = [&](int e) { return e_base + e * e_step; };
     const float* ub = p.u + (int64_t)b * p.u_sb;
     const float* db = p.dl + (int64_t)b * p.dl_sb;
     const float* zb = p.z ? p.z + (int64_t)b * p.z_sb : nullptr;
@@ -103,9 +105,9 @@ __global__ __launch_bounds__(16 * N, N <= 16 ? 3 : 1) void mamba1_scan_kernel(Ma
 #pragma unroll
         for (int e = 0; e < EPT; ++e) {
             const bool ok = d0 + e_lc(e) < p.D && t0 + e_lt(e) < p.L;
-            ru[e] = ok ? ub[tb + e_off[e]] : 0.f;
-            rd[e] = ok ? db[tb + e_off[e]] : 0.f;
-            rz[e] = (ok && zb) ? zb[tb + e_off[e]] : 0.f;
+            ru[e] = ok ? ub[tb + e_off(e)] : 0.f;
+            rd[e] = ok ? db[tb + e_off(e)] : 0.f;
+            rz[e] = (ok && zb) ? zb[tb + e_off(e)] : 0.f;
         }
 #pragma unroll
         for (int e = 0; e < BPT; ++e) {
@@ -192,7 +194,7 @@ __global__ __launch_bounds__(16 * N, N <= 16 ? 3 : 1) void mamba1_scan_kernel(Ma
             const int lc = e_lc(e), lt = e_lt(e);
             if (d0 + lc < p.D && t0 + lt < p.L) {
                 const float2 ep = s_epi[lc][lt];
-                yb[(int64_t)t0 * p.u_sl + e_off[e]] = (s_y[lc][lt] + ep.x) * ep.y;
+                yb[(int64_t)t0 * p.u_sl + e_off(e)] = (s_y[lc][lt] + ep.x) * ep.y;
             }
         }
         __syncthreads();
