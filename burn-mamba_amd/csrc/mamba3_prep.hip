@@ -340,30 +340,33 @@ __device__ __forceinline__ void m3_coef_t(const M3PrepParams& p, const TP* proj,
 
 // Per (b, segment): tot[b][seg][h][a] = sum over the segment's positions of
 // dt[b, l, h] * (tanh(rot[b, l, a]) * span), each term rounded to f32 exactly
-// as the main kernel forms it, the sum in f64.  Dynamic LDS: [tile][H] dt and
-// [tile][A] tanh(rot) * span.
+// as the main kernel forms it, the sum in f64.  Grid (b * nseg, head groups):
+// a workgroup takes hpw heads (hpw * A <= 256 where possible, one (h, a) pair
+// per thread) so that b * nseg * H / hpw workgroups share the segments.
+// Dynamic LDS: [tile][hpw] dt and [tile][A] tanh(rot) * span.
 template <typename TP>
-__global__ __launch_bounds__(256) void mamba3_angle_tot_kernel(M3PrepParams p, int nseg, double* tot) {
+__global__ __launch_bounds__(256) void mamba3_angle_tot_kernel(M3PrepParams p, int nseg, int hpw, double* tot) {
     const int b = blockIdx.x / nseg, seg = blockIdx.x % nseg, t = threadIdx.x;
     const TP* proj = static_cast<const TP*>(p.proj);
     const int H = p.H, A = p.A, HA = H * A;
+    const int h0 = blockIdx.y * hpw, nh = min(hpw, H - h0), np = nh * A;  // this group's pairs
     const int l_begin = seg * kM3Seg, l_end = min(p.L, l_begin + kM3Seg);
     const int o_rot = 2 * H * p.P + 2 * p.M * p.G * p.N + 3 * H;
     extern __shared__ __align__(16) float s_dyn[];
-    float* s_dtt = s_dyn;                 // [kM3Tile][H]
-    float* s_tr = s_dtt + kM3Tile * H;    // [kM3Tile][A]
-    constexpr int KP = 16;                // (h, a) pairs per thread and pass
-    for (int pb = 0; pb < HA; pb += 256 * KP) {
+    float* s_dtt = s_dyn;                  // [kM3Tile][hpw]
+    float* s_tr = s_dtt + kM3Tile * hpw;   // [kM3Tile][A]
+    constexpr int KP = 4;                  // (h, a) pairs per thread and pass
+    for (int pb = 0; pb < np; pb += 256 * KP) {
         double acc[KP];
 #pragma unroll
         for (int k = 0; k < KP; ++k) acc[k] = 0.0;
         for (int l0 = l_begin; l0 < l_end; l0 += kM3Tile) {
             const int nt = min(kM3Tile, l_end - l0);
-            for (int i = t; i < kM3Tile * H; i += 256) {
-                const int r = i / H, h = i % H;
+            for (int i = t; i < kM3Tile * nh; i += 256) {
+                const int r = i / nh, hl = i % nh;
                 float dt = 0.f, da, lam;
-                if (r < nt) m3_coef_t(p, proj, b, l0 + r, h, dt, da, lam);
-                s_dtt[i] = dt;
+                if (r < nt) m3_coef_t(p, proj, b, l0 + r, h0 + hl, dt, da, lam);
+                s_dtt[r * hpw + hl] = dt;
             }
             for (int i = t; i < kM3Tile * A; i += 256) {
                 const int r = i / A, a = i % A;
@@ -375,10 +378,10 @@ __global__ __launch_bounds__(256) void mamba3_angle_tot_kernel(M3PrepParams p, i
 #pragma unroll
             for (int k = 0; k < KP; ++k) {
                 const int i = pb + t + 256 * k;
-                if (i < HA) {
-                    const int h = i / A, a = i % A;
+                if (i < np) {
+                    const int hl = i / A, a = i % A;
                     double sacc = acc[k];
-                    for (int r = 0; r < nt; ++r) sacc += (double)(s_dtt[r * H + h] * s_tr[r * A + a]);
+                    for (int r = 0; r < nt; ++r) sacc += (double)(s_dtt[r * hpw + hl] * s_tr[r * A + a]);
                     acc[k] = sacc;
                 }
             }
@@ -387,7 +390,7 @@ __global__ __launch_bounds__(256) void mamba3_angle_tot_kernel(M3PrepParams p, i
 #pragma unroll
         for (int k = 0; k < KP; ++k) {
             const int i = pb + t + 256 * k;
-            if (i < HA) tot[((int64_t)b * nseg + seg) * HA + i] = acc[k];
+            if (i < np) tot[((int64_t)b * nseg + seg) * HA + (int64_t)h0 * A + i] = acc[k];
         }
     }
 }
@@ -735,9 +738,11 @@ extern "C" size_t mamba3_prep_workspace_size(const mamba3_prep_args* a) {
 template <typename TP, typename TO>
 static void m3_launch_fast(const M3PrepParams& p, double* tot, hipStream_t s) {
     const int nseg = m3_nseg(p);
-    if (nseg > 1)
-        hipLaunchKernelGGL((mamba3_angle_tot_kernel<TP>), dim3(p.nb * nseg), dim3(256),
-                           (size_t)kM3Tile * (p.H + p.A) * sizeof(float), s, p, nseg, tot);
+    if (nseg > 1) {
+        const int hpw = p.A >= 256 ? 1 : (256 / p.A < p.H ? 256 / p.A : p.H);  // heads per workgroup
+        hipLaunchKernelGGL((mamba3_angle_tot_kernel<TP>), dim3(p.nb * nseg, (p.H + hpw - 1) / hpw), dim3(256),
+                           (size_t)kM3Tile * (hpw + p.A) * sizeof(float), s, p, nseg, hpw, tot);
+    }
     const dim3 grid(p.nb * p.H * nseg), block(256);
     const size_t lds = (size_t)kM3Tile * (((p.A + 3) & ~3) + p.N) * sizeof(float);
 #define MAMBA3_SEG_N(NN) \
