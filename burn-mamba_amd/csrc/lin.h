@@ -49,11 +49,19 @@ struct LinParams {
 #ifndef MAMBA_LIN_MAXS_MID
 #define MAMBA_LIN_MAXS_MID 2   // k-split cap for 32 < M <= 64 (fewer partial planes)
 #endif
+#ifndef MAMBA_LIN_PART_BYTES
+#define MAMBA_LIN_PART_BYTES (6 << 20)  // partial planes small enough to split further
+#endif
 inline int lin_splits(int M, int K, int N) {
     const int ks = K / 16, tiles = (N + 31) / 32;
     const int cap = M <= 32 ? 16 : M <= 64 ? MAMBA_LIN_MAXS_MID : 2;
+    auto more = [&](int s) { return ks / (2 * s) >= 40 && tiles * s < 1024; };
     int s = 1;
-    while (s < cap && ks / (2 * s) >= 40 && tiles * s < 1024) s *= 2;
+    while (s < cap && more(s)) s *= 2;
+    // products with few column tiles (out_proj: N = d_model) have small
+    // planes: keep splitting while they stay small, so that enough workgroups
+    // stream the weight
+    while (s < 16 && more(s) && (size_t)2 * s * M * N * 4 <= (size_t)MAMBA_LIN_PART_BYTES) s *= 2;
     return s;
 }
 inline size_t lin_part_elems(int M, int N, int S) { return (size_t)S * M * N; }
