@@ -62,15 +62,6 @@ __global__ __launch_bounds__(256) void mamba3_step_kernel(M3StepParams p) {
     const int64_t bh = (int64_t)b * p.H + h;
     float* st = p.ssm + bh * P * N;
 
-    // ---- state tile loads first: they land during the prep
-    float4 hv[MAXPASS];
-#pragma unroll
-    for (int k = 0; k < MAXPASS; ++k) {
-        const int pr = row0 + k * RPP;
-        hv[k] = (k < npass && pr < P) ? *(reinterpret_cast<const float4*>(st + (int64_t)pr * N) + q)
-                                      : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-
     __shared__ __align__(16) float s_B[MM][N], s_C[MM][N], s_K[MM][N];
     __shared__ float s_gv[MM][256], s_bx[MM][256], s_v[MM][256], s_out[MM][256];
     __shared__ float s_cs[128], s_sn[128], s_rms[2 * MM];
@@ -79,19 +70,60 @@ __global__ __launch_bounds__(256) void mamba3_step_kernel(M3StepParams p) {
     const int d_inner = p.H * P, bc = MM * p.G * N;
     const int o_b = 2 * d_inner, o_c = o_b + bc, o_dt = o_c + bc, o_a = o_dt + p.H, o_l = o_a + p.H,
               o_rot = o_l + p.H;
+    const int g = h / (p.H / p.G);
+    // ---- this row's inputs first, into registers: the prep below waits for
+    // them only, while the state tile (issued next) is still in flight
+    constexpr int RBC = (2 * MM * N + 255) / 256, RK = (MM * N + 255) / 256;
+    const float raw_dt = m3_proj(p, row, o_dt + h), raw_a = m3_proj(p, row, o_a + h),
+                raw_l = m3_proj(p, row, o_l + h), dtb = p.dt_bias[h];
+    float raw_rot = 0.f, ang0 = 0.f;
+    if (t < p.A) {
+        raw_rot = m3_proj(p, row, o_rot + t);
+        ang0 = p.ang[bh * p.A + t];
+    }
+    float rbc[RBC], rk[RK];
+#pragma unroll
+    for (int j = 0; j < RBC; ++j) {
+        const int i = t + 256 * j, which = i / (MM * N), m = (i / N) % MM, n = i % N;
+        rbc[j] = i < 2 * MM * N ? m3_proj(p, row, (which ? o_c : o_b) + (m * p.G + g) * N + n) : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < RK; ++j) {
+        const int i = t + 256 * j, m = i / N, n = i % N;
+        rk[j] = i < MM * N ? p.kst[(((int64_t)b * MM + m) * p.H + h) * N + n] : 0.f;
+    }
+    float xv = 0.f, xo = 0.f, mxv[MM];
+#pragma unroll
+    for (int m = 0; m < MM; ++m) mxv[m] = 1.f;
+    if (t < P) {
+        xv = m3_proj(p, row, d_inner + h * P + t);
+        xo = p.vst[bh * P + t];
+        if (p.mx)
+#pragma unroll
+            for (int m = 0; m < MM; ++m) mxv[m] = p.mx[((int64_t)h * MM + m) * P + t];
+    }
+
+    // ---- the state tile: unconditional loads (rows clamped into the tile, the
+    // duplicates unused), so the waits on the inputs above are exact counts
+    float4 hv[MAXPASS];
+#pragma unroll
+    for (int k = 0; k < MAXPASS; ++k) {
+        const int pr = min(row0 + k * RPP, P - 1);
+        hv[k] = *(reinterpret_cast<const float4*>(st + (int64_t)pr * N) + q);
+    }
+
     // ---- trapezoid coefficients (every thread; three proj values)
-    float dt = m3_softplus(m3_proj(p, row, o_dt + h) + p.dt_bias[h]);
+    float dt = m3_softplus(raw_dt + dtb);
     dt = fminf(fmaxf(dt, p.dt_lo), p.dt_hi);
-    const float a = -fmaxf(m3_softplus(m3_proj(p, row, o_a + h)), p.a_floor);
-    const float lam = 1.f / (1.f + __expf(-m3_proj(p, row, o_l + h)));
+    const float a = -fmaxf(m3_softplus(raw_a), p.a_floor);
+    const float lam = 1.f / (1.f + __expf(-raw_l));
     const float alpha = __expf(dt * a);
     const float beta = (1.f - lam) * dt * alpha, gamma = lam * dt;
 
     // ---- cumulative angle of this head, cos/sin of the rotated pairs
     if (t < p.A) {
-        float* ap = p.ang + bh * p.A + t;
-        const float th = m3_wrap(*ap + dt * (tanhf(m3_proj(p, row, o_rot + t)) * p.span));
-        *ap = th;
+        const float th = m3_wrap(ang0 + dt * (tanhf(raw_rot) * p.span));
+        p.ang[bh * p.A + t] = th;
         const float tw = m3_wrap(th);
         if (t < 128) {
             s_cs[t] = cosf(tw);
@@ -99,25 +131,22 @@ __global__ __launch_bounds__(256) void mamba3_step_kernel(M3StepParams p) {
         }
     }
     // ---- raw B/C of this head's group, the previous token's K, v / xs
-    const int g = h / (p.H / p.G);
-    for (int i = t; i < 2 * MM * N; i += 256) {
-        const int which = i / (MM * N), m = (i / N) % MM, n = i % N;
-        const float v = m3_proj(p, row, (which ? o_c : o_b) + (m * p.G + g) * N + n);
-        (which ? s_C : s_B)[m][n] = v;
+#pragma unroll
+    for (int j = 0; j < RBC; ++j) {
+        const int i = t + 256 * j, which = i / (MM * N), m = (i / N) % MM, n = i % N;
+        if (i < 2 * MM * N) (which ? s_C : s_B)[m][n] = rbc[j];
     }
-    for (int i = t; i < MM * N; i += 256) {
-        const int m = i / N, n = i % N;
-        s_K[m][n] = p.kst[(((int64_t)b * MM + m) * p.H + h) * N + n];
+#pragma unroll
+    for (int j = 0; j < RK; ++j) {
+        const int i = t + 256 * j, m = i / N, n = i % N;
+        if (i < MM * N) s_K[m][n] = rk[j];
     }
-    for (int i = t; i < P; i += 256) {
-        const float xv = m3_proj(p, row, d_inner + h * P + i);
-        const float xo = p.vst[bh * P + i];
+    if (t < P) {
 #pragma unroll
         for (int m = 0; m < MM; ++m) {
-            const float mxv = p.mx ? p.mx[((int64_t)h * MM + m) * P + i] : 1.f;
-            s_v[m][i] = xv * mxv;
-            s_gv[m][i] = gamma * (xv * mxv);
-            s_bx[m][i] = beta * (xo * mxv);
+            s_v[m][t] = xv * mxv[m];
+            s_gv[m][t] = gamma * (xv * mxv[m]);
+            s_bx[m][t] = beta * (xo * mxv[m]);
         }
     }
     __syncthreads();
