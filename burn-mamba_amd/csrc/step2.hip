@@ -75,7 +75,8 @@ __device__ __forceinline__ float ld_act(const void* base, int64_t i, bool bf16) 
     return bf16 ? bf16_to_f32(static_cast<const bf16_t*>(base)[i]) : static_cast<const float*>(base)[i];
 }
 
-__device__ __forceinline__ float silu_fast(float x) { return x / (__expf(-x) + 1.f); }
+// SiLU with the hardware reciprocal (1 ulp) in place of an IEEE division
+__device__ __forceinline__ float silu_fast(float x) { return x * __builtin_amdgcn_rcpf(__expf(-x) + 1.f); }
 
 // dt = clamp(softplus(dt_raw + dt_bias), lo, hi), mamba2.rs:924 with the f32
 // softplus threshold of src/modules/activation/softplus.rs:21-47.
@@ -120,29 +121,50 @@ __global__ __launch_bounds__(256) void step2_ssm_fast(Step2Params p) {
     const int g = h / p.hpg;
     const int n4 = t % LPR, row0 = t / LPR;
 
-    // 1. state tile loads first: they are the bytes that matter
+    // 1. this row's inputs first, into registers: conv windows, weights, the new
+    //    inputs (summed in_proj partial planes) and the raw dt.  The conv below
+    //    waits for them only, while the state tile (issued next) is in flight.
+    const char* zrow = static_cast<const char*>(p.zx) + b * p.zx_sb * (p.zx_bf16 ? 2 : 4);
+    float4* win_base = reinterpret_cast<float4*>(p.conv) + (int64_t)b * p.conv_dim;
+    const float4* cw = reinterpret_cast<const float4*>(p.conv_w);
+    constexpr int CI = (P + 2 * N + 255) / 256;  // conv channels per thread
+    int chs[CI];
+    float4 cwin[CI], cwt[CI];
+    float cxin[CI], cbias[CI];
+#pragma unroll
+    for (int j = 0; j < CI; ++j) {
+        const int c = min(t + 256 * j, P + 2 * N - 1);  // clamped: the duplicate is not used
+        int ch;
+        if (c < P) ch = h * P + c;
+        else if (c < P + N) ch = p.d_inner + g * N + (c - P);
+        else ch = p.d_inner + (p.G + g) * N + (c - P - N);
+        chs[j] = ch;
+        cwin[j] = win_base[ch];
+        cwt[j] = cw[ch];
+        cxin[j] = zx_at<ZS>(p, zrow, b, p.d_inner + ch);
+        cbias[j] = p.conv_b ? p.conv_b[ch] : 0.f;
+    }
+    const float dt_raw = zx_at<ZS>(p, zrow, b, p.d_inner + p.conv_dim + h) + (p.dt_bias ? p.dt_bias[h] : 0.f);
+
+    // 2. the state tile: the bytes that matter
     float4* st = reinterpret_cast<float4*>(p.ssm) + (int64_t)bh * (P * LPR);
     float4 hv[R];
 #pragma unroll
     for (int i = 0; i < R; ++i) hv[i] = st[(row0 + i * RPI) * LPR + n4];
 
-    // 2. causal conv, one channel per thread (mamba2.rs:865-902)
-    const char* zrow = static_cast<const char*>(p.zx) + b * p.zx_sb * (p.zx_bf16 ? 2 : 4);
-    float4* win_base = reinterpret_cast<float4*>(p.conv) + (int64_t)b * p.conv_dim;
-    const float4* cw = reinterpret_cast<const float4*>(p.conv_w);
-    for (int c = t; c < P + 2 * N; c += 256) {
-        int ch;
-        if (c < P) ch = h * P + c;
-        else if (c < P + N) ch = p.d_inner + g * N + (c - P);
-        else ch = p.d_inner + (p.G + g) * N + (c - P - N);
-        const float4 win = win_base[ch];
-        const float4 w = cw[ch];
-        const float xin = zx_at<ZS>(p, zrow, b, p.d_inner + ch);
+    // 3. causal conv, one channel per thread (mamba2.rs:865-902)
+#pragma unroll
+    for (int j = 0; j < CI; ++j) {
+        const int c = t + 256 * j;
+        if (c >= P + 2 * N) break;
+        const int ch = chs[j];
+        const float4 win = cwin[j], w = cwt[j];
+        const float xin = cxin[j];
         float acc = win.y * w.x;
         acc += win.z * w.y;
         acc += win.w * w.z;
         acc += xin * w.w;
-        if (p.conv_b) acc += p.conv_b[ch];
+        acc += cbias[j];
         const float v = silu_fast(acc);
         if (c < P) {
             s_x[c] = v;
@@ -153,7 +175,9 @@ __global__ __launch_bounds__(256) void step2_ssm_fast(Step2Params p) {
             s_C[c - P - N] = v;
         }
     }
-    const float dt = step_dt<ZS>(p, zrow, b, h);
+    // dt = clamp(softplus(dt_raw + dt_bias), lo, hi), mamba2.rs:924 with the f32
+    // softplus threshold of src/modules/activation/softplus.rs:21-47
+    const float dt = fminf(fmaxf(dt_raw > 18.f ? dt_raw : log1pf(__expf(dt_raw)), p.dt_lo), p.dt_hi);
     const float dA = __expf(dt * p.A[h]);
     const float Dh = p.Dv ? p.Dv[h] : 0.f;
     __syncthreads();
