@@ -273,6 +273,27 @@ template <> __device__ __forceinline__ void m3_ld4<bf16_t>(const bf16_t* q, floa
     o[0] = __uint_as_float(u.x << 16); o[1] = __uint_as_float(u.x & 0xffff0000u);
     o[2] = __uint_as_float(u.y << 16); o[3] = __uint_as_float(u.y & 0xffff0000u);
 }
+// Raw 8 consecutive elements, converted where used: a group of loads is
+// issued together and its elements unpacked only when consumed.
+template <typename T> struct M3Raw8;
+template <> struct M3Raw8<bf16_t> { uint4 u; };
+template <> struct M3Raw8<float> { float4 a, c; };
+__device__ __forceinline__ M3Raw8<bf16_t> m3_raw8(const bf16_t* q) { return {*(const uint4*)q}; }
+__device__ __forceinline__ M3Raw8<float> m3_raw8(const float* q) {
+    return {*(const float4*)q, *(const float4*)(q + 4)};
+}
+__device__ __forceinline__ void m3_cvt8(const M3Raw8<bf16_t>& r, float* o) {
+    const uint32_t w[4] = {r.u.x, r.u.y, r.u.z, r.u.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        o[2 * k] = __uint_as_float(w[k] << 16);
+        o[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+    }
+}
+__device__ __forceinline__ void m3_cvt8(const M3Raw8<float>& r, float* o) {
+    o[0] = r.a.x; o[1] = r.a.y; o[2] = r.a.z; o[3] = r.a.w; o[4] = r.c.x; o[5] = r.c.y; o[6] = r.c.z; o[7] = r.c.w;
+}
+
 template <typename T> __device__ __forceinline__ void m3_st8(T* q, const float* v);
 template <> __device__ __forceinline__ void m3_st8<float>(float* q, const float* v) {
     *(float4*)q = make_float4(v[0], v[1], v[2], v[3]);
@@ -455,10 +476,11 @@ __global__ __launch_bounds__(256) void mamba3_prep_seg_kernel(M3PrepParams p, in
     if (vfixed && p.mx) vmx = *(const float4*)(p.mx + ((int64_t)h * M + vm) * P + 4 * vpq);
 
     // one B/C row: norm, weight, bias, rotation, store (and the cache tail)
-    auto bc_row = [&](int l0, int r, int which, int m, const float* w, const float* bias) {
+    auto bc_src = [&](int l, int which, int m) {
+        return projb + (int64_t)l * p.proj_sl + 2 * d_inner + which * bc + (m * p.G + g) * N + col0;
+    };
+    auto bc_finish = [&](int l0, int r, int which, int m, const float* w, const float* bias, float* y) {
         const int l = l0 + r;
-        float y[8];
-        m3_ld8(projb + (int64_t)l * p.proj_sl + 2 * d_inner + which * bc + (m * p.G + g) * N + col0, y);
         float ss = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) ss += y[e] * y[e];
@@ -506,6 +528,12 @@ __global__ __launch_bounds__(256) void mamba3_prep_seg_kernel(M3PrepParams p, in
             *(float4*)(kq + 4) = make_float4(y[4], y[5], y[6], y[7]);
         }
     };
+    auto bc_row = [&](int l0, int r, int which, int m, const float* w, const float* bias) {
+        float y[8];
+        m3_ld8(bc_src(l0 + r, which, m), y);
+        bc_finish(l0, r, which, m, w, bias, y);
+    };
+    constexpr int kBCG = 2;  // B/C rows whose loads are issued together (fixed path)
 
     for (int l0 = l_begin; l0 < l_end; l0 += kM3Tile) {
         const int nt = min(kM3Tile, l_end - l0);
@@ -547,7 +575,21 @@ __global__ __launch_bounds__(256) void mamba3_prep_seg_kernel(M3PrepParams p, in
         __syncthreads();
         // B / C rows
         if (fixed) {
-            for (int r = rsub / (2 * M); r < nt; r += dpos) bc_row(l0, r, which_f, m_f, w8, bias8);
+            // kBCG rows per group, their loads issued before the first is used (rows
+            // clamped into the tile so that the loads are unconditional)
+            for (int r0 = rsub / (2 * M); r0 < nt; r0 += kBCG * dpos) {
+                M3Raw8<TP> q[kBCG];
+#pragma unroll
+                for (int j = 0; j < kBCG; ++j) q[j] = m3_raw8(bc_src(l0 + min(r0 + j * dpos, nt - 1), which_f, m_f));
+#pragma unroll
+                for (int j = 0; j < kBCG; ++j) {
+                    if (r0 + j * dpos < nt) {
+                        float y[8];
+                        m3_cvt8(q[j], y);
+                        bc_finish(l0, r0 + j * dpos, which_f, m_f, w8, bias8, y);
+                    }
+                }
+            }
         } else {
             for (int rb = rsub; rb < nt * 2 * M; rb += RPP) {
                 const int m = rb % M, which = (rb / M) & 1, r = rb / (2 * M);
