@@ -606,15 +606,22 @@ __global__ __launch_bounds__(256) void mamba3_prep_seg_kernel(M3PrepParams p, in
         // v = x mimo_x [b, l, m, h, p], four headdim values per item; with
         // 256 % (M P / 4) == 0 each thread keeps one (rank, quad) of the head
         if (vfixed) {
-            const TP* xs = projb + (int64_t)(l0 + vr0) * p.proj_sl + d_inner + h * P + 4 * vpq;
-            TO* vd = static_cast<TO*>(p.v) + ((((int64_t)b * p.L + l0 + vr0) * M + vm) * p.H + h) * P + 4 * vpq;
-            for (int r = vr0; r < nt; r += vdr) {
-                float x[4];
-                m3_ld4(xs, x);
-                x[0] *= vmx.x; x[1] *= vmx.y; x[2] *= vmx.z; x[3] *= vmx.w;
-                m3_st4(vd, x);
-                xs += (int64_t)vdr * p.proj_sl;
-                vd += (int64_t)vdr * M * p.H * P;
+            // kVG rows per group, their loads issued before the first is used
+            constexpr int kVG = 4;
+            const TP* xs = projb + d_inner + h * P + 4 * vpq;
+            for (int r0 = vr0; r0 < nt; r0 += kVG * vdr) {
+                float x[kVG][4];
+#pragma unroll
+                for (int j = 0; j < kVG; ++j) m3_ld4(xs + (int64_t)(l0 + min(r0 + j * vdr, nt - 1)) * p.proj_sl, x[j]);
+#pragma unroll
+                for (int j = 0; j < kVG; ++j) {
+                    const int r = r0 + j * vdr;
+                    if (r < nt) {
+                        x[j][0] *= vmx.x; x[j][1] *= vmx.y; x[j][2] *= vmx.z; x[j][3] *= vmx.w;
+                        m3_st4(static_cast<TO*>(p.v) + ((((int64_t)b * p.L + l0 + r) * M + vm) * p.H + h) * P + 4 * vpq,
+                               x[j]);
+                    }
+                }
             }
         } else {
             for (int i = t; i < nt * M * PQ; i += 256) {
