@@ -54,7 +54,11 @@ __global__ __launch_bounds__(256) void mamba1_step_kernel(M1StepParams p) {
     int dd[CPT];
     bool live[CPT];
     float4 hv[CPT], av[CPT];
-    float dv[CPT], uv[CPT];
+    float dv[CPT], uv[CPT], dbv[CPT], Dvv[CPT], zvv[CPT];
+    // optional inputs read through a selected pointer (a real element when
+    // absent, its value then dropped), so that no load sits under a branch and
+    // every load of the CPT rounds is in flight before the first is used
+    const bool has_db = p.dbias != nullptr, has_D = p.Dv != nullptr, has_z = p.z != nullptr;
     const bool a_vec = p.A_sn == 1 && (p.A_sd & 3) == 0 && ((uintptr_t)p.A & 15u) == 0;
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
@@ -69,8 +73,17 @@ __global__ __launch_bounds__(256) void mamba1_step_kernel(M1StepParams p) {
             av[k] = make_float4(ar[(int64_t)n0 * p.A_sn], ar[(int64_t)(n0 + 1) * p.A_sn],
                                 ar[(int64_t)(n0 + 2) * p.A_sn], ar[(int64_t)(n0 + 3) * p.A_sn]);
         }
-        dv[k] = m1s_delta(p, b, dd[k]);
+        dv[k] = p.dl[(int64_t)b * p.dl_sb + dd[k]];
         uv[k] = p.u[(int64_t)b * p.u_sb + dd[k]];
+        dbv[k] = *(has_db ? p.dbias + dd[k] : p.dl + (int64_t)b * p.dl_sb + dd[k]);
+        Dvv[k] = *(has_D ? p.Dv + dd[k] : p.dl + (int64_t)b * p.dl_sb + dd[k]);
+        zvv[k] = *(has_z ? p.z + (int64_t)b * p.z_sb + dd[k] : p.dl + (int64_t)b * p.dl_sb + dd[k]);
+    }
+    // delta = softplus(delta + bias) (Mamba1::ssm_step, mamba1.rs:646) once every load is issued
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+        float v = dv[k] + (has_db ? dbv[k] : 0.f);
+        dv[k] = p.softplus ? m1s_softplus(v) : v;
     }
     float bb[4], cc[4];
 #pragma unroll
@@ -93,10 +106,10 @@ __global__ __launch_bounds__(256) void mamba1_step_kernel(M1StepParams p) {
         if (!live[k]) continue;
         *(reinterpret_cast<float4*>(p.h + ((int64_t)b * p.D + dd[k]) * N) + q) = hn;
         if (q == 0) {
-            float out = acc + (p.Dv ? p.Dv[dd[k]] : 0.f) * u_;
-            if (p.z) {
-                const float zv = p.z[(int64_t)b * p.z_sb + dd[k]];
-                out *= zv / (1.f + __expf(-zv));
+            float out = acc + (has_D ? Dvv[k] : 0.f) * u_;
+            if (has_z) {
+                const float zv = zvv[k];
+                out *= zv * __builtin_amdgcn_rcpf(1.f + __expf(-zv));
             }
             p.y[(int64_t)b * p.y_sb + dd[k]] = out;
         }
