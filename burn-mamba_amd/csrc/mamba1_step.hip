@@ -163,6 +163,8 @@ __global__ __launch_bounds__(256) void conv1d_step_kernel(ConvStepParams p) {
     const float xin = p.x_bf16 ? bf16_to_f32(static_cast<const bf16_t*>(p.x)[xi]) : static_cast<const float*>(p.x)[xi];
     float* win = p.state + ((int64_t)b * p.C + c) * p.K;
     const float* w = p.w + (int64_t)c * p.K;
+    // the bias with the other loads (a selected pointer: no load under a branch)
+    const float bv = *(p.bias ? p.bias + c : w);
     float acc = 0.f;
     if (K4) {  // one 16-byte window and weight row per channel
         const float4 wv = *reinterpret_cast<const float4*>(win);
@@ -179,8 +181,8 @@ __global__ __launch_bounds__(256) void conv1d_step_kernel(ConvStepParams p) {
         win[p.K - 1] = xin;
         acc += xin * w[p.K - 1];
     }
-    if (p.bias) acc += p.bias[c];
-    if (p.silu) acc = acc / (__expf(-acc) + 1.f);
+    if (p.bias) acc += bv;
+    if (p.silu) acc = acc * __builtin_amdgcn_rcpf(__expf(-acc) + 1.f);
     const int64_t oi = (int64_t)b * p.out_sb + c;
     if (p.out_bf16)
         static_cast<bf16_t*>(p.out)[oi] = f32_to_bf16(acc);
