@@ -63,22 +63,50 @@ __device__ __forceinline__ void m3p_coef(const M3PrepParams& p, int b, int l, in
     lam = 1.f / (1.f + __expf(-m3p_ld(p, b, l, o + 2 * p.H + h)));
 }
 
-// Beta seed of the initial state, one workgroup per (b, h): reads the previous
-// token's K / v_state before mamba3_prep_kernel replaces them.
-__global__ __launch_bounds__(256) void mamba3_seed_kernel(M3PrepParams p) {
-    const int b = blockIdx.x / p.H, h = blockIdx.x % p.H;
+// Beta seed of the initial state: reads the previous token's K / v_state
+// before the prep kernels replace them.  Grid (b * H, row blocks): a
+// workgroup seeds rows_per rows of one (b, h) state, with v_state mimo_x and
+// K staged in LDS and its (at most kSeedE) state loads per thread issued
+// before the first is used.  Dynamic LDS: [M][rows_per] + [M][N] floats.
+constexpr int kSeedE = 8;
+__global__ __launch_bounds__(256) void mamba3_seed_kernel(M3PrepParams p, int rows_per) {
+    extern __shared__ float s_seed[];
+    const int b = blockIdx.x / p.H, h = blockIdx.x % p.H, t = threadIdx.x;
+    const int p0 = blockIdx.y * rows_per, nr = min(rows_per, p.P - p0);
+    if (nr <= 0) return;  // uniform over the workgroup
+    float* s_vx = s_seed;                  // [M][rows_per]
+    float* s_k = s_seed + p.M * rows_per;  // [M][N]
+    const int64_t bh = (int64_t)b * p.H + h;
+    const int64_t base = bh * p.P * p.N + (int64_t)p0 * p.N;
+    const int ne = nr * p.N;
+    float hv[kSeedE];
+#pragma unroll
+    for (int j = 0; j < kSeedE; ++j) {
+        const int e = t + 256 * j;
+        hv[j] = e < ne ? p.ssm[base + e] : 0.f;
+    }
+    for (int i = t; i < p.M * nr; i += 256) {
+        const int m = i / nr, r = i % nr;
+        const float mxv = p.mx ? p.mx[((int64_t)h * p.M + m) * p.P + p0 + r] : 1.f;
+        s_vx[m * rows_per + r] = p.vst[bh * p.P + p0 + r] * mxv;
+    }
+    for (int i = t; i < p.M * p.N; i += 256) {
+        const int m = i / p.N, n = i % p.N;
+        s_k[i] = p.kst[(((int64_t)b * p.M + m) * p.H + h) * p.N + n];
+    }
     float dt, da, lam;
     m3p_coef(p, b, 0, h, dt, da, lam);
     const float f = dt - lam * dt;  // dt_0 - gamma_0
-    const int64_t bh = (int64_t)b * p.H + h;
-    for (int i = threadIdx.x; i < p.P * p.N; i += 256) {
-        const int pp = i / p.N, n = i % p.N;
-        float acc = 0.f;
-        for (int m = 0; m < p.M; ++m) {
-            const float mxv = p.mx ? p.mx[((int64_t)h * p.M + m) * p.P + pp] : 1.f;
-            acc += (p.vst[bh * p.P + pp] * mxv) * p.kst[(((int64_t)b * p.M + m) * p.H + h) * p.N + n];
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kSeedE; ++j) {
+        const int e = t + 256 * j;
+        if (e < ne) {
+            const int r = e / p.N, n = e % p.N;
+            float acc = 0.f;
+            for (int m = 0; m < p.M; ++m) acc += s_vx[m * rows_per + r] * s_k[m * p.N + n];
+            p.h0[base + e] = hv[j] + f * acc;
         }
-        p.h0[bh * p.P * p.N + i] = p.ssm[bh * p.P * p.N + i] + f * acc;
     }
 }
 
@@ -818,7 +846,14 @@ extern "C" int mamba3_prep_fwd(const mamba3_prep_args* a, void* workspace, size_
                     "workspace too small: mamba3_prep_workspace_size() bytes are required");
     MAMBA_CHECK_ARG(need == 0 || ((uintptr_t)workspace & 7u) == 0, "workspace must be 8-byte aligned");
     MAMBA_CHECK_ARG((int64_t)p.nb * p.H * m3_nseg(p) < (1ll << 31), "too many (batch, head, segment) items");
-    hipLaunchKernelGGL(mamba3_seed_kernel, dim3(p.nb * p.H), dim3(256), 0, s, p);
+    {
+        // rows per workgroup: at most kSeedE state elements per thread, at most P rows
+        // (LDS <= M (P + N) floats, 32 KB at the limits M = 16, P = N = 256)
+        int rows_per = (256 * kSeedE) / p.N > 0 ? (256 * kSeedE) / p.N : 1;
+        rows_per = rows_per < p.P ? rows_per : p.P;
+        hipLaunchKernelGGL(mamba3_seed_kernel, dim3(p.nb * p.H, (p.P + rows_per - 1) / rows_per), dim3(256),
+                           (size_t)p.M * (rows_per + p.N) * sizeof(float), s, p, rows_per);
+    }
     MAMBA_CHECK_LAUNCH();
     if (m3_prep_fast(p)) {
         double* tot = (double*)workspace;
