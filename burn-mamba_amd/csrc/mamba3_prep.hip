@@ -682,7 +682,7 @@ __global__ __launch_bounds__(256) void mamba3_prep_seg_kernel(M3PrepParams p, in
 
 // ---- epilogue ------------------------------------------------------------
 struct M3FinishParams {
-    int nb, L, H, P, M;
+    int nb, L, H, P, M, YM;  // YM: ranks in y's rank axis (the first M are read)
     bool io_bf16, z_bf16, out_bf16;
     const void* y; const void* v;
     const void* z; int64_t z_sb, z_sl;
@@ -692,6 +692,50 @@ struct M3FinishParams {
 
 __device__ __forceinline__ float m3f_ld(bool bf, const void* base, int64_t i) {
     return bf ? bf16_to_f32(static_cast<const bf16_t*>(base)[i]) : static_cast<const float*>(base)[i];
+}
+
+// ---- double-SSD pathway inputs -------------------------------------------
+// One wave per (b, t, h): ranks m < M of the 2M-rank call carry gamma_t v_t
+// with B_t, ranks M + m carry beta_t v_{t-1} with B_{t-1} (the cache's x_prev
+// mimo_x and K_prev at t = 0); both carry C_t.  gamma = lambda dt and
+// beta = (1 - lambda) dt exp(da) (trapezoidal_coefficients, helpers.rs:42-73).
+struct M3DoubleParams {
+    const void* v; const void* B; const void* C;
+    const float* xp; const float* kp; const float* mx;
+    void* v2; void* B2; void* C2;
+};
+
+__global__ __launch_bounds__(256) void mamba3_double_inputs_kernel(M3PrepParams p, M3DoubleParams d) {
+    const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (item >= (int64_t)p.nb * p.L * p.H) return;  // whole waves exit together
+    const int h = (int)(item % p.H);
+    const int64_t bl = item / p.H;
+    const int t = (int)(bl % p.L), b = (int)(bl / p.L);
+    const int M = p.M, H = p.H, P = p.P, N = p.N;
+    float dt, da, lam;
+    m3p_coef(p, b, t, h, dt, da, lam);
+    const float gamma = lam * dt, beta = (1.f - lam) * dt * __expf(da);
+    for (int m = 0; m < M; ++m) {
+        const int64_t cur = ((bl * M + m) * H + h), prv = (((bl - 1) * M + m) * H + h);
+        const int64_t o0 = ((bl * 2 * M + m) * H + h), o1 = ((bl * 2 * M + M + m) * H + h);
+        for (int pp = lane; pp < P; pp += 64) {
+            const float vt = m3f_ld(p.io_bf16, d.v, cur * P + pp);
+            const float vp = t > 0 ? m3f_ld(p.io_bf16, d.v, prv * P + pp)
+                                   : d.xp[((int64_t)b * H + h) * P + pp] * (d.mx ? d.mx[((int64_t)h * M + m) * P + pp] : 1.f);
+            m3p_st(p.io_bf16, d.v2, o0 * P + pp, gamma * vt);
+            m3p_st(p.io_bf16, d.v2, o1 * P + pp, beta * vp);
+        }
+        for (int n = lane; n < N; n += 64) {
+            const float bt = m3f_ld(p.io_bf16, d.B, cur * N + n);
+            const float bp = t > 0 ? m3f_ld(p.io_bf16, d.B, prv * N + n) : d.kp[(((int64_t)b * M + m) * H + h) * N + n];
+            const float ct = m3f_ld(p.io_bf16, d.C, cur * N + n);
+            m3p_st(p.io_bf16, d.B2, o0 * N + n, bt);
+            m3p_st(p.io_bf16, d.B2, o1 * N + n, bp);
+            m3p_st(p.io_bf16, d.C2, o0 * N + n, ct);
+            m3p_st(p.io_bf16, d.C2, o1 * N + n, ct);
+        }
+    }
 }
 
 // one wave per (b, l, h); lanes over headdim (P <= 256, up to 4 per lane)
@@ -712,8 +756,9 @@ __global__ __launch_bounds__(256) void mamba3_finish_kernel(M3FinishParams p) {
             const int pp = lane + 64 * k;
             o[k] = 0.f;
             if (pp < p.P) {
-                const int64_t yi = (((bl * p.M + m) * p.H + h) * p.P) + pp;
-                o[k] = m3f_ld(p.io_bf16, p.y, yi) + Dv * m3f_ld(p.io_bf16, p.v, yi);
+                const int64_t yi = (((bl * p.YM + m) * p.H + h) * p.P) + pp;
+                const int64_t vi = (((bl * p.M + m) * p.H + h) * p.P) + pp;
+                o[k] = m3f_ld(p.io_bf16, p.y, yi) + Dv * m3f_ld(p.io_bf16, p.v, vi);
                 ss += o[k] * o[k];
             }
         }
@@ -900,8 +945,11 @@ extern "C" int mamba3_finish_fwd(const mamba3_finish_args* a, mamba_stream_t str
                         (a->z_dtype == MAMBA_F32 || a->z_dtype == MAMBA_BF16) &&
                         (a->out_dtype == MAMBA_F32 || a->out_dtype == MAMBA_BF16),
                     "bad dtype");
+    MAMBA_CHECK_ARG(a->y_ranks == 0 || (a->y_ranks >= a->mimo && a->y_ranks <= 32),
+                    "y_ranks must be 0 or in [mimo, 32]");
     M3FinishParams p;
     p.nb = a->batch; p.L = a->seqlen; p.H = a->nheads; p.P = a->headdim; p.M = a->mimo;
+    p.YM = a->y_ranks > 0 ? a->y_ranks : a->mimo;
     p.io_bf16 = a->io_dtype == MAMBA_BF16; p.z_bf16 = a->z_dtype == MAMBA_BF16; p.out_bf16 = a->out_dtype == MAMBA_BF16;
     p.y = a->y_ssd; p.v = a->v; p.z = a->z; p.z_sb = a->z_sb; p.z_sl = a->z_sl;
     p.Dh = a->D; p.mz = a->mimo_z; p.mo = a->mimo_o; p.onw = a->out_norm_w;
@@ -909,6 +957,35 @@ extern "C" int mamba3_finish_fwd(const mamba3_finish_args* a, mamba_stream_t str
     const int64_t items = (int64_t)p.nb * p.L * p.H;
     MAMBA_CHECK_ARG((items + 3) / 4 < (1ll << 31), "too many (batch, position, head) items");
     hipLaunchKernelGGL(mamba3_finish_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, (hipStream_t)stream, p);
+    MAMBA_CHECK_LAUNCH();
+    return MAMBA_OK;
+}
+
+extern "C" int mamba3_double_inputs(const mamba3_double_inputs_args* a, mamba_stream_t stream) {
+    MAMBA_CHECK_ARG(a != nullptr, "args is NULL");
+    MAMBA_CHECK_ARG(a->batch > 0 && a->seqlen > 0 && a->nheads > 0 && a->headdim > 0 && a->dstate > 0,
+                    "sizes must be >= 1");
+    MAMBA_CHECK_ARG(a->ngroups > 0 && a->nheads % a->ngroups == 0, "nheads must be a multiple of ngroups");
+    MAMBA_CHECK_ARG(a->mimo >= 1 && a->mimo <= 16, "mimo must be in [1, 16]");
+    MAMBA_CHECK_ARG(a->mimo == 1 || a->mimo_x, "mimo_x is required when mimo > 1");
+    MAMBA_CHECK_ARG(a->proj && a->dt_bias && a->v && a->B && a->C && a->x_prev && a->k_prev && a->v2 && a->B2 && a->C2,
+                    "proj, dt_bias, v, B, C, x_prev, k_prev, v2, B2 and C2 are required");
+    MAMBA_CHECK_ARG((a->proj_dtype == MAMBA_F32 || a->proj_dtype == MAMBA_BF16) &&
+                        (a->io_dtype == MAMBA_F32 || a->io_dtype == MAMBA_BF16),
+                    "bad dtype");
+    M3PrepParams p{};
+    p.nb = a->batch; p.L = a->seqlen; p.H = a->nheads; p.P = a->headdim; p.G = a->ngroups; p.N = a->dstate;
+    p.M = a->mimo;
+    p.proj_bf16 = a->proj_dtype == MAMBA_BF16; p.io_bf16 = a->io_dtype == MAMBA_BF16;
+    p.proj = a->proj; p.proj_sb = a->proj_sb; p.proj_sl = a->proj_sl;
+    p.dt_bias = a->dt_bias; p.a_floor = a->a_floor; p.dt_lo = a->dt_min; p.dt_hi = a->dt_max;
+    M3DoubleParams d;
+    d.v = a->v; d.B = a->B; d.C = a->C; d.xp = a->x_prev; d.kp = a->k_prev; d.mx = a->mimo_x;
+    d.v2 = a->v2; d.B2 = a->B2; d.C2 = a->C2;
+    const int64_t items = (int64_t)p.nb * p.L * p.H;
+    MAMBA_CHECK_ARG((items + 3) / 4 < (1ll << 31), "too many (batch, position, head) items");
+    hipLaunchKernelGGL(mamba3_double_inputs_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0,
+                       (hipStream_t)stream, p, d);
     MAMBA_CHECK_LAUNCH();
     return MAMBA_OK;
 }

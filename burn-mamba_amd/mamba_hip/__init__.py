@@ -18,3 +18,4 @@ from .mamba3 import Mamba3, Mamba3Cache, Mamba3Config  # noqa: F401
 from .mamba3 import step_ssm as mamba3_step_ssm, step_ssm_args as mamba3_step_ssm_args  # noqa: F401
 from .mamba3 import finish_fwd as mamba3_finish_fwd, prep_fwd as mamba3_prep_fwd  # noqa: F401
 from .mamba3 import prep_args as mamba3_prep_args, prep_fast_path as mamba3_prep_fast_path  # noqa: F401
+from .mamba3 import double_inputs as mamba3_double_inputs  # noqa: F401

@@ -157,6 +157,19 @@ class Mamba3FinishArgs(ctypes.Structure):
         ("z", c_vp), ("z_sb", c_i64), ("z_sl", c_i64),
         ("D", c_vp), ("mimo_z", c_vp), ("mimo_o", c_vp), ("out_norm_w", c_vp),
         ("out", c_vp), ("out_sb", c_i64), ("out_sl", c_i64),
+        ("y_ranks", c_i32),
+    ]
+
+
+class Mamba3DoubleInputsArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", c_i32), ("seqlen", c_i32), ("nheads", c_i32), ("headdim", c_i32), ("ngroups", c_i32),
+        ("dstate", c_i32), ("mimo", c_i32), ("proj_dtype", c_i32), ("io_dtype", c_i32),
+        ("proj", c_vp), ("proj_sb", c_i64), ("proj_sl", c_i64),
+        ("dt_bias", c_vp), ("a_floor", ctypes.c_float), ("dt_min", ctypes.c_float), ("dt_max", ctypes.c_float),
+        ("v", c_vp), ("B", c_vp), ("C", c_vp),
+        ("x_prev", c_vp), ("k_prev", c_vp), ("mimo_x", c_vp),
+        ("v2", c_vp), ("B2", c_vp), ("C2", c_vp),
     ]
 
 
@@ -260,6 +273,7 @@ _SIGNATURES = {
     "mamba3_prep_workspace_size": ([ctypes.POINTER(Mamba3PrepArgs)], ctypes.c_size_t),
     "mamba3_prep_fwd": ([ctypes.POINTER(Mamba3PrepArgs), c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),
     "mamba3_finish_fwd": ([ctypes.POINTER(Mamba3FinishArgs), c_vp], ctypes.c_int),
+    "mamba3_double_inputs": ([ctypes.POINTER(Mamba3DoubleInputsArgs), c_vp], ctypes.c_int),
     "mamba3_step_ssm_timed": ([ctypes.POINTER(Mamba3StepArgs), c_vp, c_vp, c_vp], ctypes.c_int),
     "mamba1_scan_step_timed": ([ctypes.POINTER(Mamba1StepArgs), c_vp, c_vp, c_vp], ctypes.c_int),
     "mamba_conv1d_step": ([ctypes.POINTER(Conv1dStepArgs), c_vp], ctypes.c_int),

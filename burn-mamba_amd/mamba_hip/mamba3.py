@@ -30,11 +30,15 @@ from .ssd import _dtype_code, _raw_events, _stream
 @dataclass
 class Mamba3Cache:
     """ssm_bhpr [b, H, P, N], k_state_bmhr [b, M, H, N] (previous rotated B),
-    v_state_bhp [b, H, P] (previous x), angle_bha [b, H, A] (cumulative angle); f32."""
+    v_state_bhp [b, H, P] (previous x), angle_bha [b, H, A] (cumulative angle); f32.
+    pathway: "single" or "double", the variant of the reference's Mamba3Cache
+    (src/mamba3/cache.rs:41-47) that selects the forward pathway; both
+    variants hold the same tensors."""
     ssm_bhpr: torch.Tensor
     k_state_bmhr: torch.Tensor
     v_state_bhp: torch.Tensor
     angle_bha: torch.Tensor
+    pathway: str = "single"
 
 
 @dataclass
@@ -222,14 +226,20 @@ def prep_fwd(cfg: Mamba3Config, proj: torch.Tensor, cache: Mamba3Cache, *, dt_bi
 
 def finish_fwd(cfg: Mamba3Config, y_ssd: torch.Tensor, v: torch.Tensor, z: torch.Tensor, *, D=None, mimo_z=None,
                mimo_o=None, out_norm_w=None, out: Optional[torch.Tensor] = None):
-    """mamba3_finish_fwd: y_ssd, v [b, l, M, H, P] (contiguous); z [b, l, H*P] -> [b, l, H*P]."""
-    b, L, M, H, P = y_ssd.shape
+    """mamba3_finish_fwd: y_ssd [b, l, Y, H, P] whose first M ranks are read (Y = M, or 2M
+    for the double pathway's call), v [b, l, M, H, P] (both contiguous); z [b, l, H*P] ->
+    [b, l, H*P]."""
+    b, L, M, H, P = v.shape
+    Y = y_ssd.shape[2]
+    if tuple(y_ssd.shape) != (b, L, Y, H, P) or Y < M:
+        raise _lib.MambaHipError("y_ssd must be [b, l, Y >= M, H, P] matching v")
     if not (y_ssd.is_contiguous() and v.is_contiguous() and y_ssd.dtype == v.dtype) or z.stride(2) != 1:
         raise _lib.MambaHipError("y_ssd / v must be contiguous with one dtype; z needs a unit inner stride")
     if out is None:
         out = torch.empty((b, L, H * P), device=y_ssd.device, dtype=y_ssd.dtype)
     a = Mamba3FinishArgs()
     a.batch, a.seqlen, a.nheads, a.headdim, a.mimo = b, L, H, P, M
+    a.y_ranks = Y
     a.io_dtype, a.z_dtype, a.out_dtype = _dtype_code(y_ssd), _dtype_code(z), _dtype_code(out)
     a.y_ssd, a.v = y_ssd.data_ptr(), v.data_ptr()
     a.z, a.z_sb, a.z_sl = z.data_ptr(), z.stride(0), z.stride(1)
@@ -238,6 +248,34 @@ def finish_fwd(cfg: Mamba3Config, y_ssd: torch.Tensor, v: torch.Tensor, z: torch
     a.out, a.out_sb, a.out_sl = out.data_ptr(), out.stride(0), out.stride(1)
     check(_lib.lib().mamba3_finish_fwd(ctypes.byref(a), _stream(y_ssd.device)), "mamba3_finish_fwd")
     return out
+
+
+def double_inputs(cfg: Mamba3Config, proj: torch.Tensor, prep: dict, x_prev: torch.Tensor, k_prev: torch.Tensor,
+                  *, dt_bias, mimo_x=None):
+    """mamba3_double_inputs: the 2M-rank inputs (v2, B2, C2) [b, l, 2M, H, P|N] of
+    forward_double_ssd's gamma + beta SSD calls, from the prep's v, B, C and the
+    cache's x_prev [b, H, P] / K_prev [b, M, H, N] as they were before the prep."""
+    v, B, C = prep["v"], prep["B"], prep["C"]
+    b, L, M, H, P = v.shape
+    N = B.shape[-1]
+    if proj.stride(2) != 1 or tuple(proj.shape[:2]) != (b, L):
+        raise _lib.MambaHipError("proj must be [b, l, d_in_proj] with a unit inner stride")
+    dev = v.device
+    v2 = torch.empty((b, L, 2 * M, H, P), device=dev, dtype=v.dtype)
+    B2 = torch.empty((b, L, 2 * M, H, N), device=dev, dtype=v.dtype)
+    C2 = torch.empty((b, L, 2 * M, H, N), device=dev, dtype=v.dtype)
+    a = _lib.Mamba3DoubleInputsArgs()
+    a.batch, a.seqlen, a.nheads, a.headdim, a.ngroups, a.dstate, a.mimo = b, L, H, P, cfg.ngroups, N, M
+    a.proj_dtype, a.io_dtype = _dtype_code(proj), _dtype_code(v)
+    a.proj, a.proj_sb, a.proj_sl = proj.data_ptr(), proj.stride(0), proj.stride(1)
+    a.dt_bias = _f32c(dt_bias, "dt_bias").data_ptr()
+    a.a_floor, a.dt_min, a.dt_max = cfg.a_floor, cfg.dt_limit[0], cfg.dt_limit[1]
+    a.v, a.B, a.C = v.data_ptr(), B.data_ptr(), C.data_ptr()
+    a.x_prev, a.k_prev = _f32c(x_prev, "x_prev").data_ptr(), _f32c(k_prev, "k_prev").data_ptr()
+    a.mimo_x = None if mimo_x is None else _f32c(mimo_x, "mimo_x").data_ptr()
+    a.v2, a.B2, a.C2 = v2.data_ptr(), B2.data_ptr(), C2.data_ptr()
+    check(_lib.lib().mamba3_double_inputs(ctypes.byref(a), _stream(dev)), "mamba3_double_inputs")
+    return v2, B2, C2
 
 
 @dataclass
@@ -259,27 +297,46 @@ class Mamba3:
     mimo_o: Optional[torch.Tensor] = None
     out_norm_w: Optional[torch.Tensor] = None
 
-    def new_cache(self, batch: int) -> Mamba3Cache:
+    def new_cache(self, batch: int, pathway: str = "single") -> Mamba3Cache:
         """The reference's fresh cache: zero state, K, v_state and angle
-        (double_ssd/double_ssd/mod.rs:649-669)."""
+        (double_ssd/double_ssd/mod.rs:649-669); a missing cache is the
+        single-ssd variant (mamba3.rs:825-826)."""
         c, dev = self.cfg, self.in_proj_w.device
         z = lambda *s: torch.zeros(s, device=dev)  # noqa: E731
         return Mamba3Cache(z(batch, c.nheads, c.per_head_dim, c.state_rank),
                            z(batch, c.mimo_rank, c.nheads, c.state_rank),
-                           z(batch, c.nheads, c.per_head_dim), z(batch, c.nheads, c.num_rope_angles))
+                           z(batch, c.nheads, c.per_head_dim), z(batch, c.nheads, c.num_rope_angles), pathway)
 
-    def forward(self, x: torch.Tensor, cache: Optional[Mamba3Cache] = None, chunk_len: int = 64):
-        """Mamba3::forward_single_ssd (single_ssd/single_ssd/mod.rs:44-360):
-        x [b, l, d_model] -> (out [b, l, d_model], cache).  in_proj / out_proj on
-        torch.mm; prep -> mamba_ssd3_fwd -> finish in between."""
-        from .ssd3 import ssd3_fwd
+    def _in_proj(self, x: torch.Tensor):
         b, L, _ = x.shape
-        if cache is None:
-            cache = self.new_cache(b)
         wdt = self.in_proj_w.dtype
         proj = torch.mm(x.reshape(b * L, -1).to(wdt), self.in_proj_w).reshape(b, L, -1)
         if self.in_proj_b is not None:
             proj = proj + self.in_proj_b.to(wdt)
+        return proj
+
+    def _out_proj(self, y: torch.Tensor, x: torch.Tensor):
+        b, L, _ = y.shape
+        out = torch.mm(y.reshape(b * L, -1), self.out_proj_w).reshape(b, L, -1)
+        if self.out_proj_b is not None:
+            out = out + self.out_proj_b.to(self.in_proj_w.dtype)
+        return out.to(x.dtype)
+
+    def forward(self, x: torch.Tensor, cache: Optional[Mamba3Cache] = None, chunk_len: int = 64):
+        """Mamba3::forward (mamba3.rs:805-840): x [b, l, d_model] -> (out [b, l, d_model],
+        cache), the pathway chosen by the cache's variant (a missing cache is the
+        single-ssd one).  Both pathways compute the same function."""
+        if cache is not None and cache.pathway == "double":
+            return self.forward_double_ssd(x, cache, chunk_len)
+        return self.forward_single_ssd(x, cache, chunk_len)
+
+    def forward_single_ssd(self, x: torch.Tensor, cache: Optional[Mamba3Cache] = None, chunk_len: int = 64):
+        """Mamba3::forward_single_ssd (single_ssd/single_ssd/mod.rs:44-360): in_proj /
+        out_proj on torch.mm; prep -> mamba_ssd3_fwd -> finish in between."""
+        from .ssd3 import ssd3_fwd
+        if cache is None:
+            cache = self.new_cache(x.shape[0])
+        proj = self._in_proj(x)
         pr = prep_fwd(self.cfg, proj, cache, dt_bias=self.dt_bias, b_norm_w=self.b_norm_w, c_norm_w=self.c_norm_w,
                       b_bias=self.b_bias, c_bias=self.c_bias, mimo_x=self.mimo_x)
         y_ssd, hT = ssd3_fwd(pr["v"], pr["da"], pr["B"], pr["C"], pr["gamma"], pr["scale"], pr["h0"],
@@ -287,10 +344,28 @@ class Mamba3:
         cache.ssm_bhpr = hT
         y = finish_fwd(self.cfg, y_ssd, pr["v"], proj[:, :, :self.cfg.d_inner], D=self.D, mimo_z=self.mimo_z,
                        mimo_o=self.mimo_o, out_norm_w=self.out_norm_w)
-        out = torch.mm(y.reshape(b * L, -1), self.out_proj_w).reshape(b, L, -1)
-        if self.out_proj_b is not None:
-            out = out + self.out_proj_b.to(wdt)
-        return out.to(x.dtype), cache
+        return self._out_proj(y, x), cache
+
+    def forward_double_ssd(self, x: torch.Tensor, cache: Optional[Mamba3Cache] = None, chunk_len: int = 64):
+        """Mamba3::forward_double_ssd (double_ssd/double_ssd/mod.rs:40-369): the same
+        prep (QK-norm, bias, rotation, coefficients), then the gamma and beta SSD
+        calls of :254-283 as one 2M-rank mamba_ssd3_double_fwd (they share da and
+        C, so the first M ranks of its y are y_gamma + y_beta and its final state
+        is their sum), then the D skip / gate / merge and out_proj."""
+        from .ssd3 import ssd3_double_fwd
+        if cache is None:
+            cache = self.new_cache(x.shape[0], "double")
+        proj = self._in_proj(x)
+        # the beta term's t = 0 inputs: x_prev and K_prev before the prep replaces them
+        x_prev, k_prev = cache.v_state_bhp.clone(), cache.k_state_bmhr.clone()
+        pr = prep_fwd(self.cfg, proj, cache, dt_bias=self.dt_bias, b_norm_w=self.b_norm_w, c_norm_w=self.c_norm_w,
+                      b_bias=self.b_bias, c_bias=self.c_bias, mimo_x=self.mimo_x)
+        v2, B2, C2 = double_inputs(self.cfg, proj, pr, x_prev, k_prev, dt_bias=self.dt_bias, mimo_x=self.mimo_x)
+        y2, hT = ssd3_double_fwd(v2, pr["da"], B2, C2, cache.ssm_bhpr, chunk_len=chunk_len)
+        cache.ssm_bhpr = hT
+        y = finish_fwd(self.cfg, y2, pr["v"], proj[:, :, :self.cfg.d_inner], D=self.D, mimo_z=self.mimo_z,
+                       mimo_o=self.mimo_o, out_norm_w=self.out_norm_w)
+        return self._out_proj(y, x), cache
 
     def step(self, x: torch.Tensor, cache: Optional[Mamba3Cache] = None, events=None):
         """Mamba3::step: x [b, d_model] -> (out [b, d_model], cache updated in place)."""

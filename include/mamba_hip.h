@@ -31,6 +31,9 @@
  *   mamba3_prep_fwd     <- Mamba3::forward_single_ssd steps 2-6, before the SSD seam
  *                          (src/mamba3/single_ssd/single_ssd/mod.rs:86-262)
  *   mamba3_finish_fwd   <- the same forward's step 9 before out_proj (:288-332)
+ *   mamba3_double_inputs <- the gamma / beta inputs of Mamba3::forward_double_ssd
+ *                          (src/mamba3/double_ssd/double_ssd/mod.rs:179-283), as one
+ *                          2M-rank call of mamba_ssd3_double_fwd
  *   mamba2_step_ssm     <- the body of Mamba2::step between in_proj and out_proj
  *                          (src/mamba2/mamba2.rs:857-995)
  *   mamba_linear_fwd    <- burn::nn::Linear::forward in the decode steps (packed weights)
@@ -404,9 +407,37 @@ typedef struct mamba3_finish_args {
     const float* mimo_z; const float* mimo_o;        /* [H, M, P]; NULL if mimo == 1 */
     const float* out_norm_w;                         /* [P] or NULL                */
     void* out;          int64_t out_sb, out_sl;      /* [b, l, H P]                */
+    int32_t y_ranks;    /* ranks in y_ssd's rank axis, of which the first mimo are */
+                        /* read (0 = mimo; 2 mimo for the double pathway's call)   */
 } mamba3_finish_args;
 
 int mamba3_finish_fwd(const mamba3_finish_args* args, mamba_stream_t stream);
+
+/* Mamba-3 double-SSD pathway (Mamba3::forward_double_ssd,                     */
+/* src/mamba3/double_ssd/double_ssd/mod.rs:40-369): its gamma call (gamma_t v_t, */
+/* B_t, the cached state) and its beta call (beta_t v_{t-1}, B_{t-1}, with the  */
+/* cache's x_prev mimo_x and K_prev at t = 0, zero state) share da and C, so   */
+/* their sum is one mamba_ssd3_double_fwd over 2M ranks:                       */
+/*   v2 = [gamma v | beta v_prev], B2 = [B | B_prev], C2 = [C | C]             */
+/* whose first M ranks of y are y_gamma + y_beta and whose final state is the  */
+/* sum of both.  This entry builds v2, B2, C2 from the prep's v, B, C (the    */
+/* single-pathway prep computes the same normed, biased, rotated B/C) and the */
+/* cache tail as it was before the prep; gamma and beta come from the in_proj */
+/* row (trapezoidal_coefficients, helpers.rs:42-73).                           */
+typedef struct mamba3_double_inputs_args {
+    int32_t batch, seqlen, nheads, headdim, ngroups, dstate, mimo;
+    int32_t proj_dtype, io_dtype;                    /* proj; v/B/C and outputs  */
+    const void* proj;   int64_t proj_sb, proj_sl;    /* [b, l, d_in_proj]        */
+    const float* dt_bias;                            /* [H]                      */
+    float a_floor, dt_min, dt_max;
+    const void* v; const void* B; const void* C;     /* [b, l, M, H, P|N] contig. */
+    const float* x_prev;                             /* [b, H, P] before the prep */
+    const float* k_prev;                             /* [b, M, H, N] before the prep */
+    const float* mimo_x;                             /* [H, M, P] or NULL (M = 1) */
+    void* v2; void* B2; void* C2;                    /* [b, l, 2M, H, P|N] contig. */
+} mamba3_double_inputs_args;
+
+int mamba3_double_inputs(const mamba3_double_inputs_args* args, mamba_stream_t stream);
 
 /* ------------------------------------------------------------------------- */
 /* Mamba-2 recurrent decode step: everything of Mamba2::step between in_proj  */

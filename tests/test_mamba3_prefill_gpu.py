@@ -173,6 +173,45 @@ def test_mamba3_forward_then_step(M):
     np.testing.assert_allclose(out2.cpu().numpy(), y2 @ Wo, rtol=1e-3, atol=1e-4)
 
 
+@pytest.mark.parametrize("dtype,M", [("f32", 1), ("f32", 4), ("bf16", 4)])
+def test_mamba3_forward_double_equals_single(dtype, M):
+    """Mamba3::forward with a double-ssd cache (forward_double_ssd: its gamma and
+    beta SSD calls as one 2M-rank mamba_ssd3_double_fwd) equals the single-ssd
+    pathway from the same cache (the reference's single == double relation):
+    outputs and every cache tensor, over a prompt and then a continuation whose
+    beta term starts from the cache's x_prev / K_prev.  bf16 runs the config-4
+    head shape (P 64, N 128, MIMO 4) on the MFMA paths."""
+    import torch
+    import mamba_hip
+    if dtype == "f32":
+        cfg = mamba_hip.Mamba3Config(d_model=64, state_rank=32, per_head_dim=16, mimo_rank=M, rope_fraction=0.5)
+        tdt, tol, stol = torch.float32, dict(rtol=1e-3, atol=1e-4), dict(rtol=1e-3, atol=1e-4)
+    else:
+        cfg = mamba_hip.Mamba3Config(d_model=128, state_rank=128, per_head_dim=64, mimo_rank=M)
+        tdt, tol, stol = torch.bfloat16, dict(rtol=0, atol=3e-2), dict(rtol=2e-2, atol=1e-2)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(40 + M)
+    m = cfg.init("cuda", tdt, gen)
+    m.b_bias.normal_(0, 0.1, generator=gen)
+    m.D.normal_(0, 1, generator=gen)
+    b = 2
+    x1 = torch.randn((b, 150, cfg.d_model), generator=gen, device="cuda").to(tdt)
+    x2 = torch.randn((b, 70, cfg.d_model), generator=gen, device="cuda").to(tdt)
+    cs, cd = m.new_cache(b, "single"), m.new_cache(b, "double")
+    outs = []
+    for x in (x1, x2):
+        o_s, cs = m.forward(x, cs, chunk_len=32)
+        o_d, cd = m.forward(x, cd, chunk_len=32)
+        outs.append((o_s, o_d))
+    torch.cuda.synchronize()
+    assert cs.pathway == "single" and cd.pathway == "double"
+    for o_s, o_d in outs:
+        scale = float(o_s.float().abs().max())
+        np.testing.assert_allclose(o_d.float().cpu().numpy() / scale, o_s.float().cpu().numpy() / scale, **tol)
+    for nm in ("ssm_bhpr", "k_state_bmhr", "v_state_bhp", "angle_bha"):
+        np.testing.assert_allclose(getattr(cd, nm).cpu().numpy(), getattr(cs, nm).cpu().numpy(), **stol)
+
+
 FAST_CASES = [
     # (b, L, H, P, G, N, M, rope_dim): proj rows padded to a multiple of 8 elements,
     # which selects the segment-parallel kernels (256-position segments)
