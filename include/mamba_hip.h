@@ -32,7 +32,7 @@
  *                          (src/mamba3/single_ssd/single_ssd/mod.rs:86-262)
  *   mamba3_finish_fwd   <- the same forward's step 9 before out_proj (:288-332)
  *   mamba3_double_inputs <- the gamma / beta inputs of Mamba3::forward_double_ssd
- *                          (src/mamba3/double_ssd/double_ssd/mod.rs:179-283), as one
+ *                          (src/mamba3/double_ssd/double_ssd/mod.rs:174-282), as one
  *                          2M-rank call of mamba_ssd3_double_fwd
  *   mamba2_step_ssm     <- the body of Mamba2::step between in_proj and out_proj
  *                          (src/mamba2/mamba2.rs:857-995)
