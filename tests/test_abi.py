@@ -104,3 +104,22 @@ def test_step_validation_needs_no_gpu():
     r = _lib.RmsNormArgs()
     r.rows, r.cols = 2, 8
     assert L.mamba_rmsnorm(ctypes.byref(r), None) == 1
+
+
+def test_missing_library_raises_no_fallback():
+    """The product path has no CPU fallback: with libmamba_hip.so absent, the
+    first library call raises MambaHipError (checked in a fresh interpreter,
+    so the library already loaded by this process is not reused)."""
+    import sys
+    code = (
+        "import sys; sys.path[:0] = [%r]\n"
+        "from mamba_hip import _lib\n"
+        "_lib.LIB_PATH = '/nonexistent/libmamba_hip.so'\n"
+        "try:\n"
+        "    _lib.lib()\n"
+        "except _lib.MambaHipError as e:\n"
+        "    print('raised', e)\n"
+        "    sys.exit(0)\n"
+        "sys.exit(3)\n" % os.path.join(ROOT, "burn-mamba_amd"))
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and "raised" in r.stdout, r.stdout + r.stderr
