@@ -25,6 +25,7 @@ import torch
 from . import _lib
 from ._lib import Mamba3FinishArgs, Mamba3PrepArgs, Mamba3StepArgs, check
 from .ssd import _dtype_code, _raw_events, _stream
+from .step import prefill_mm
 
 
 @dataclass
@@ -310,14 +311,14 @@ class Mamba3:
     def _in_proj(self, x: torch.Tensor):
         b, L, _ = x.shape
         wdt = self.in_proj_w.dtype
-        proj = torch.mm(x.reshape(b * L, -1).to(wdt), self.in_proj_w).reshape(b, L, -1)
+        proj = prefill_mm(x.reshape(b * L, -1).to(wdt), self.in_proj_w).reshape(b, L, -1)
         if self.in_proj_b is not None:
             proj = proj + self.in_proj_b.to(wdt)
         return proj
 
     def _out_proj(self, y: torch.Tensor, x: torch.Tensor):
         b, L, _ = y.shape
-        out = torch.mm(y.reshape(b * L, -1), self.out_proj_w).reshape(b, L, -1)
+        out = prefill_mm(y.reshape(b * L, -1), self.out_proj_w).reshape(b, L, -1)
         if self.out_proj_b is not None:
             out = out + self.out_proj_b.to(self.in_proj_w.dtype)
         return out.to(x.dtype)
