@@ -320,9 +320,10 @@ def mamba3_step_algorithmic(cfg, batch):
 
 
 def bench_mamba3_step(args):
-    """64 Mamba-3 blocks stepping one token (in_proj on hipBLASLt ->
-    mamba3_step_ssm -> out_proj), config-4 block shapes with the reference's
-    init, every layer with its own weights and cache, captured in one HIP graph."""
+    """64 Mamba-3 blocks stepping one token (in_proj -> mamba3_step_ssm ->
+    out_proj, the products on the packed streaming kernel as Mamba3.step runs
+    them), config-4 block shapes with the reference's init, every layer with its
+    own weights and cache, captured in one HIP graph."""
     import torch
 
     import mamba_hip
@@ -345,6 +346,7 @@ def bench_mamba3_step(args):
     projs = [torch.empty((b, c.d_in_proj), device=dev, dtype=torch.bfloat16) for _ in range(2)]
     ys = torch.empty((b, c.d_inner), device=dev, dtype=torch.bfloat16)
     xs = [torch.empty((b, c.d_model), device=dev, dtype=torch.bfloat16) for _ in range(2)]
+    lin_ws = torch.empty(8 << 20, device=dev, dtype=torch.uint8)  # product workspace, shared in order
     argl = [mamba_hip.mamba3_step_ssm_args(c, projs[i % 2], caches[i], dt_bias=m.dt_bias, b_norm_w=m.b_norm_w,
                                            c_norm_w=m.c_norm_w, b_bias=m.b_bias, c_bias=m.c_bias, D=m.D,
                                            mimo_x=m.mimo_x, mimo_z=m.mimo_z, mimo_o=m.mimo_o, out=ys)
@@ -355,9 +357,9 @@ def bench_mamba3_step(args):
     def eager(events=None):
         xs[0].copy_(x0)
         for i, m in enumerate(blocks):
-            torch.mm(xs[0], m.in_proj_w, out=projs[i % 2])
+            mamba_hip.step_mm(xs[0], m.in_proj_w, out=projs[i % 2], workspace=lin_ws)
             mamba_hip.mamba3_step_ssm(argl[i], dev, None if events is None else events[i])
-            torch.mm(ys, m.out_proj_w, out=xs[1])
+            mamba_hip.step_mm(ys, m.out_proj_w, out=xs[1], workspace=lin_ws)
 
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -397,7 +399,7 @@ def bench_mamba3_step(args):
         "dtype": "bf16", "data": "synthetic (config-4 block shapes, reference init, states ~N(0,0.1), seed 0)",
         "config": {"workload": "mamba3_decode_step", **cfg, "batch": b, "graph": "hip graph of the 64-layer step",
                    "step_bytes": step_bytes, "step_hbm_gbs": step_bytes / (ms_per_step * 1e-3) / 1e9,
-                   "entry": "torch.mm in_proj + mamba3_step_ssm + torch.mm out_proj per layer"},
+                   "entry": "mamba_linear_fwd in_proj + mamba3_step_ssm + mamba_linear_fwd out_proj per layer"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel_ms": kern_ms,
                      "algorithmic_bytes": kernel_bytes, "kernel": "mamba3_step_kernel (mean over all layers)"},

@@ -25,7 +25,7 @@ import torch
 from . import _lib
 from ._lib import Mamba3FinishArgs, Mamba3PrepArgs, Mamba3StepArgs, check
 from .ssd import _dtype_code, _raw_events, _stream
-from .step import prefill_mm
+from .step import prefill_mm, step_mm
 
 
 @dataclass
@@ -373,16 +373,18 @@ class Mamba3:
         if cache is None:
             cache = self.new_cache(x.shape[0])
         wdt = self.in_proj_w.dtype
-        proj = torch.mm(x.to(wdt), self.in_proj_w)
+        # the packed streaming product: bf16 weights, at most 256 rows
+        small = x.shape[0] <= 256 and wdt == torch.bfloat16
+        proj = step_mm(x.to(wdt), self.in_proj_w) if small else torch.mm(x.to(wdt), self.in_proj_w)
         if self.in_proj_b is not None:
-            proj = proj + self.in_proj_b.to(wdt)
+            proj = proj + self.in_proj_b.to(proj.dtype)
         y = torch.empty((x.shape[0], self.cfg.d_inner), dtype=wdt, device=x.device)
         args = step_ssm_args(self.cfg, proj, cache, dt_bias=self.dt_bias, b_norm_w=self.b_norm_w,
                              c_norm_w=self.c_norm_w, b_bias=self.b_bias, c_bias=self.c_bias, D=self.D,
                              mimo_x=self.mimo_x, mimo_z=self.mimo_z, mimo_o=self.mimo_o,
                              out_norm_w=self.out_norm_w, out=y)
         step_ssm(args, x.device, events)
-        out = torch.mm(y, self.out_proj_w)
+        out = step_mm(y, self.out_proj_w) if small else torch.mm(y, self.out_proj_w)
         if self.out_proj_b is not None:
-            out = out + self.out_proj_b.to(wdt)
+            out = out + self.out_proj_b.to(out.dtype)
         return out.to(x.dtype), cache

@@ -241,6 +241,23 @@ def prefill_mm(x2d: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     return torch.mm(x2d, hit[1].t())
 
 
+def step_mm(x2d: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = None,
+            workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """x2d [rows, d_in] @ w [d_in, d_out] for decode-sized rows (<= 256) through
+    mamba_linear_fwd on a packed copy of w, made once and kept on the weight
+    tensor (remade after an in-place update).  Measured faster than hipBLASLt's
+    skinny products at the Mamba-3 block shapes; `out` f32 (default) or bf16.
+    The packed operands are bf16, so w must be bf16 (an f32 weight would be
+    rounded)."""
+    if w.dtype != torch.bfloat16:
+        raise _lib.MambaHipError("step_mm packs bf16 weights only")
+    hit = getattr(w, "_mamba_packed", None)
+    if hit is None or hit[0] != w._version:
+        hit = (w._version, pack_linear(w))
+        w._mamba_packed = hit
+    return linear(x2d, hit[1], w.shape[1], out=out, workspace=workspace)
+
+
 def div_eps(dtype: torch.dtype) -> float:
     """div_eps (src/utils/mod.rs:50-95) of the reference's tensor dtype."""
     return {torch.float64: 4.0693917e-16, torch.float32: 8.1584695e-8, torch.float16: 7.1209995e-4,
