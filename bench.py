@@ -1046,6 +1046,8 @@ def main():
                              "mamba2_block"])
     ap.add_argument("--batch", type=int, default=DECODE_CFG3["batch"], help="decode batch")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true",
+                    help="ssd2 only: leave out the decode_b64 half of the headline metric")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 1 GiB device copy 3 times (known bytes) so that rocprofv3 "
                          "FETCH_SIZE/WRITE_SIZE of the same run can be scaled to true HBM bytes")
@@ -1087,7 +1089,38 @@ def main():
     if not args.no_cpu_baseline:
         log("cpu baseline")
         out["cpu_baseline"] = base()
+    if args.workload == "ssd2" and not args.no_decode:
+        out["decode_b64"] = decode_b64_summary(args)
     print(json.dumps(out), flush=True)
+
+
+def decode_b64_summary(args):
+    """The second half of BASELINE.json's headline metric: the recurrent
+    decode step of the 64-layer config-3 stack at batch 64 (bench_decode, the
+    whole step replayed as one HIP graph, the step methodology of the
+    reference's benches/layer.rs:362-395: each step's caches feed the next),
+    with the step's HBM fraction, the state-update kernel's roofline and its
+    own CPU baseline."""
+    import torch
+    d = bench_decode(argparse.Namespace(batch=64, steps=args.steps, warmup=args.warmup))
+    traffic = _profiled_traffic(d["config"]["workload"])
+    if traffic is not None:
+        d["roofline"]["traffic"] = traffic
+    cfg = d["config"]
+    s = {"metric": "decode step us at batch 64 (64-layer Mamba-2 2.7B-shaped stack) + % HBM roofline",
+         "value": d["value"], "unit": "us/step", "higher_is_better": False, "steps": args.steps,
+         "warmup": args.warmup, "step_bytes": cfg["step_bytes"], "step_hbm_gbs": cfg["step_hbm_gbs"],
+         "step_hbm_frac": cfg["step_hbm_frac"],
+         "target_us": cfg["step_bytes"] / (0.6 * HBM_PEAK_GBS * 1e9) * 1e6,
+         "config": {k: cfg[k] for k in ("workload", "batch", "n_layers", "d_model", "nheads", "headdim", "dstate",
+                                        "weights", "state", "graph", "eager_ms_per_step", "entry")
+                    if k in cfg},
+         "roofline": d["roofline"]}
+    if not args.no_cpu_baseline:
+        log("decode cpu baseline")
+        s["cpu_baseline"] = cpu_baseline_decode(dict(DECODE_CFG3, batch=64))
+    del torch
+    return s
 
 
 if __name__ == "__main__":

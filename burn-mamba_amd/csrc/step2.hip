@@ -669,6 +669,8 @@ static int layer_check(const mamba2_layer_args* a, const mamba2_layer_args* firs
     MAMBA_CHECK_ARG(a->batch >= 1 && a->batch <= 256, "batch must be in [1, 256]");
     MAMBA_CHECK_ARG(a->d_model > 0 && a->d_model % 16 == 0 && a->d_model <= 4 * 4 * kRowsThreads,
                     "d_model must be a positive multiple of 16, at most 4096");
+    // layer_rows reduces the per-head sums of squares with one thread per head
+    MAMBA_CHECK_ARG(a->nheads >= 1 && a->nheads <= kRowsThreads, "nheads must be in [1, 256]");
     MAMBA_CHECK_ARG(a->x && a->pre_norm_w && a->in_proj && a->out_proj, "x, pre_norm_w, in_proj, out_proj required");
     MAMBA_CHECK_ARG(a->x_sb >= a->d_model && a->x_sb % 4 == 0, "x_sb must be >= d_model and a multiple of 4");
     if (!(a->headdim == 64 && (a->dstate == 64 || a->dstate == 128) && a->conv_kernel == 4)) {

@@ -25,7 +25,7 @@ import torch
 from . import _lib
 from ._lib import Mamba3FinishArgs, Mamba3PrepArgs, Mamba3StepArgs, check
 from .ssd import _dtype_code, _raw_events, _stream
-from .step import prefill_mm, step_mm
+from .step import packed_weight, prefill_mm, step_mm, step_mm_ok
 
 
 @dataclass
@@ -373,18 +373,35 @@ class Mamba3:
         if cache is None:
             cache = self.new_cache(x.shape[0])
         wdt = self.in_proj_w.dtype
-        # the packed streaming product: bf16 weights, at most 256 rows
-        small = x.shape[0] <= 256 and wdt == torch.bfloat16
-        proj = step_mm(x.to(wdt), self.in_proj_w) if small else torch.mm(x.to(wdt), self.in_proj_w)
+        xw = x.to(wdt)
+        b = x.shape[0]
+        # the packed streaming product where it applies (bf16 weights, d_in a
+        # multiple of 16, at most 256 rows); its outputs are rounded to the
+        # weight dtype, as the library GEMM's are
+        if step_mm_ok(xw, self.in_proj_w):
+            proj = step_mm(xw, self.in_proj_w, out=torch.empty((b, self.cfg.d_in_proj), dtype=wdt, device=x.device))
+        else:
+            proj = torch.mm(xw, self.in_proj_w)
         if self.in_proj_b is not None:
             proj = proj + self.in_proj_b.to(proj.dtype)
-        y = torch.empty((x.shape[0], self.cfg.d_inner), dtype=wdt, device=x.device)
+        y = torch.empty((b, self.cfg.d_inner), dtype=wdt, device=x.device)
         args = step_ssm_args(self.cfg, proj, cache, dt_bias=self.dt_bias, b_norm_w=self.b_norm_w,
                              c_norm_w=self.c_norm_w, b_bias=self.b_bias, c_bias=self.c_bias, D=self.D,
                              mimo_x=self.mimo_x, mimo_z=self.mimo_z, mimo_o=self.mimo_o,
                              out_norm_w=self.out_norm_w, out=y)
         step_ssm(args, x.device, events)
-        out = step_mm(y, self.out_proj_w) if small else torch.mm(y, self.out_proj_w)
+        if step_mm_ok(y, self.out_proj_w):
+            out = step_mm(y, self.out_proj_w, out=torch.empty((b, self.cfg.d_model), dtype=wdt, device=x.device))
+        else:
+            out = torch.mm(y, self.out_proj_w)
         if self.out_proj_b is not None:
             out = out + self.out_proj_b.to(out.dtype)
         return out.to(x.dtype), cache
+
+    def pack_products(self) -> None:
+        """Make the packed copies of in_proj / out_proj that step() streams
+        (bf16 weights only), so that no packing happens inside a captured HIP
+        graph.  step() packs on first use otherwise."""
+        for w in (self.in_proj_w, self.out_proj_w):
+            if w.dtype == torch.bfloat16 and w.shape[0] % 16 == 0:
+                packed_weight(w)

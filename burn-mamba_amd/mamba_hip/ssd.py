@@ -164,6 +164,12 @@ class Mamba2SsdPath:
     def chunk_len(self) -> Optional[int]:
         return self._chunk_len
 
+    @classmethod
+    def default_optimal_from_block(cls, block) -> "Mamba2SsdPath":
+        """SerialRecalculated at the block's optimal chunk length (ssd_path.rs:129-134)."""
+        c = block.cfg
+        return cls(cls.SERIAL_RECALCULATED, cls.optimal_chunk_len(c.state_rank, c.per_head_dim))
+
     def chunk_len_or_optimal(self, state_rank: int, per_head_dim: int) -> int:
         return self._chunk_len if self._chunk_len is not None else self.optimal_chunk_len(
             state_rank, per_head_dim)

@@ -226,19 +226,54 @@ def linear(x: torch.Tensor, packed_w: torch.Tensor, d_out: int, bias: Optional[t
     return out
 
 
+_DERIVED_ATTRS = ("_mamba_prefill_wt", "_mamba_packed")
+
+
+def _weight_key(w: torch.Tensor):
+    """What identifies a weight's current values for the derived-copy caches
+    below: its version counter, which every in-place update bumps.  Tensors
+    made under torch.inference_mode have no version counter; for them the key
+    is the storage address and layout, so an in-place update of such a weight
+    must be followed by drop_derived(w)."""
+    try:
+        return ("version", w._version)
+    except RuntimeError:
+        return ("storage", w.data_ptr(), tuple(w.shape), tuple(w.stride()))
+
+
+def drop_derived(w: torch.Tensor) -> None:
+    """Forget the transposed and packed copies made from ``w`` (needed only
+    after an in-place update of an inference-mode weight)."""
+    for a in _DERIVED_ATTRS:
+        if hasattr(w, a):
+            delattr(w, a)
+
+
+def _derived(w: torch.Tensor, attr: str, make):
+    """The copy of ``w`` that ``make`` builds, made once and kept on the weight
+    tensor itself (so it lives exactly as long) and remade when the weight
+    changes.  Making it launches device work, which must not be recorded into
+    a captured HIP graph: a capture that finds no current copy raises, and the
+    caller derives the copies before capturing (``Mamba3.pack_products``)."""
+    key = _weight_key(w)
+    hit = getattr(w, attr, None)
+    if hit is None or hit[0] != key:
+        if w.is_cuda and torch.cuda.is_current_stream_capturing():
+            raise _lib.MambaHipError(f"{attr[1:]}: the weight copy must be made before HIP graph capture")
+        hit = (key, make(w))
+        setattr(w, attr, hit)
+    return hit[1]
+
+
 def prefill_mm(x2d: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     """x2d [M, d_in] @ w [d_in, d_out] (Burn's Linear layout) for prefill-sized M.
     The product runs on a [d_out, d_in] contiguous copy of w through its
     transposed view: hipBLASLt's kernels for that layout measured 9-19 % faster
     at the 2.7B-layer shapes.  The copy is made once per weight and kept on the
-    weight tensor itself (so it lives exactly as long), remade when the weight
-    is updated in place; it doubles that weight's memory for callers that
-    prefill."""
-    hit = getattr(w, "_mamba_prefill_wt", None)
-    if hit is None or hit[0] != w._version:
-        hit = (w._version, w.t().contiguous())
-        w._mamba_prefill_wt = hit
-    return torch.mm(x2d, hit[1].t())
+    weight tensor itself, remade when the weight is updated in place; it
+    doubles that weight's memory for callers that prefill."""
+    wt = _derived(w, "_mamba_prefill_wt", lambda t: t.t().contiguous())
+    return torch.mm(x2d, wt.t())
 
 
 def step_mm(x2d: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = None,
@@ -248,14 +283,23 @@ def step_mm(x2d: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = No
     tensor (remade after an in-place update).  Measured faster than hipBLASLt's
     skinny products at the Mamba-3 block shapes; `out` f32 (default) or bf16.
     The packed operands are bf16, so w must be bf16 (an f32 weight would be
-    rounded)."""
+    rounded), and d_in a multiple of 16 with x2d's rows contiguous."""
+    return linear(x2d, packed_weight(w), w.shape[1], out=out, workspace=workspace)
+
+
+def packed_weight(w: torch.Tensor) -> torch.Tensor:
+    """The packed copy of a bf16 Linear weight that step_mm streams, made once
+    and kept on the weight tensor (remade after an in-place update)."""
     if w.dtype != torch.bfloat16:
         raise _lib.MambaHipError("step_mm packs bf16 weights only")
-    hit = getattr(w, "_mamba_packed", None)
-    if hit is None or hit[0] != w._version:
-        hit = (w._version, pack_linear(w))
-        w._mamba_packed = hit
-    return linear(x2d, hit[1], w.shape[1], out=out, workspace=workspace)
+    return _derived(w, "_mamba_packed", pack_linear)
+
+
+def step_mm_ok(x2d: torch.Tensor, w: torch.Tensor) -> bool:
+    """True where step_mm applies: a bf16 weight whose d_in is a multiple of
+    16, at most 256 rows and a unit inner stride of x2d."""
+    return (w.dtype == torch.bfloat16 and x2d.dim() == 2 and x2d.shape[0] <= 256 and x2d.stride(1) == 1
+            and w.shape[0] % 16 == 0)
 
 
 def div_eps(dtype: torch.dtype) -> float:
@@ -456,7 +500,7 @@ class Mamba2Stack:
         self._args = {}
         c = self.cfg
         self.fused = fused and c.per_head_dim == 64 and c.state_rank in (64, 128) and c.conv_kernel == 4 \
-            and c.d_model % 16 == 0
+            and c.d_model % 16 == 0 and c.d_model <= 4096 and c.nheads <= 256
         # packed in_proj / out_proj per layer (mamba_linear_pack), built once
         self._packed = [(pack_linear(l.mixer.in_proj_w), pack_linear(l.mixer.out_proj_w)) for l in layers] \
             if self.fused else None

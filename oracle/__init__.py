@@ -461,22 +461,27 @@ def mamba2_gated_rmsnorm(y, z, gamma, eps, norm_before_gate=False):
     return out * sz if norm_before_gate else out
 
 
-def mamba2_block_fwd(proj, p, conv_state, ssm_state, chunk, cfg, eps=8.1584695e-8):
+def mamba2_block_fwd(proj, p, conv_state, ssm_state, chunk, cfg, eps=8.1584695e-8, io_round=None):
     """Mamba2::forward between in_proj and out_proj (src/mamba2/mamba2.rs:546-786):
     conv prologue -> SSD (ssd2, f64) -> gated RMSNorm with z.  proj [b, l, row];
     p has conv_w, conv_b, dt_bias, A, D, norm_w.  Returns (y [b, l, d_inner],
-    conv_state', ssm_state')."""
+    conv_state', ssm_state').  ``io_round`` (e.g. a bf16 rounding) is applied
+    where a model of that dtype stores a tensor: the conv output, the SSD's y
+    and the normed output."""
+    rnd = io_round if io_round is not None else (lambda a: a)
     H, P, G, N = cfg["nheads"], cfg["headdim"], cfg["ngroups"], cfg["dstate"]
     d_inner = H * P
     conv_dim = d_inner + 2 * G * N
     b, L, _ = proj.shape
     xbc, dt, cs = mamba2_conv_fwd(proj, p["conv_w"], p.get("conv_b"), conv_state, p["dt_bias"], d_inner,
                                   d_inner + conv_dim, conv_dim, H, cfg.get("dt_limit", (0.0, 65504.0)))
+    xbc = rnd(xbc)
     x = xbc[:, :, :d_inner].reshape(b, L, H, P)
     Bm = xbc[:, :, d_inner:d_inner + G * N].reshape(b, L, G, N)
     Cm = xbc[:, :, d_inner + G * N:].reshape(b, L, G, N)
     y, hT = ssd2(x, dt, p["A"], Bm, Cm, p.get("D"), ssm_state, chunk=chunk)
+    y = rnd(y)
     z = np.asarray(proj, np.float64)[:, :, :d_inner]
     yn = mamba2_gated_rmsnorm(np.asarray(y, np.float64).reshape(b, L, d_inner), z, p["norm_w"], eps,
                               cfg.get("norm_before_gate", False))
-    return yn, cs, hT
+    return rnd(yn), cs, hT

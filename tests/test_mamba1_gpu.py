@@ -114,3 +114,22 @@ def test_mamba1_split_equals_full():
     torch.cuda.synchronize()
     np.testing.assert_allclose(torch.cat([ya, yb], -1).cpu().numpy(), y.cpu().numpy(), rtol=1e-5, atol=1e-6)
     np.testing.assert_allclose(hb.cpu().numpy(), hT.cpu().numpy(), rtol=1e-5, atol=1e-6)
+
+
+def test_mamba1_config2_full_size():
+    """BASELINE.json configs[2] at its full size (8 x 5120 channels x 2048
+    tokens, dstate 16, f32, z gate, D = 1): the benched kernel against the f64
+    oracle at north_star's f32 bar, outputs and final states."""
+    import torch
+    import mamba_hip
+    b, d, l, n = 8, 5120, 2048, 16
+    print(f"mamba1 config 2 full size {b}x{d}x{l}", flush=True)
+    inp = mamba1_inputs(seed=2048, b=b, d=d, l=l, n=n)
+    y, hT = mamba_hip.mamba1_scan(_dev(inp["u"]), _dev(inp["delta"]), _dev(inp["A"]), _dev(inp["B"]),
+                                  _dev(inp["C"]), _dev(inp["D"]), _dev(inp["z"]))
+    torch.cuda.synchronize()
+    y, hT = y.cpu().numpy(), hT.cpu().numpy()
+    yr, hr = _oracle(inp)
+    for i in range(b):
+        np.testing.assert_allclose(y[i], yr[i], err_msg=f"y[{i}]", **TOL)
+    np.testing.assert_allclose(hT, hr, **TOL)

@@ -106,19 +106,24 @@ def _model(cfg, seed, dtype):
     return m
 
 
-def _oracle_forward(m, x, cs0, ss0, chunk):
-    """Oracle composition: in_proj (f64) -> mamba2_block_fwd -> out_proj (f64)."""
+def _oracle_forward(m, x, cs0, ss0, chunk, io_round=None):
+    """Oracle composition: in_proj (f64) -> mamba2_block_fwd -> out_proj (f64).
+    ``io_round`` rounds where the bf16 model stores a tensor: the in_proj
+    output, the conv output, the SSD's y, the normed output and the block
+    output."""
     import oracle
+    rnd = io_round if io_round is not None else (lambda a: a)
     c = m.cfg
-    proj = x.astype(np.float64) @ m.in_proj_w.float().cpu().numpy().astype(np.float64)
+    proj = rnd(x.astype(np.float64) @ m.in_proj_w.float().cpu().numpy().astype(np.float64))
     p = dict(conv_w=m.conv_w.cpu().numpy(), conv_b=None if m.conv_b is None else m.conv_b.cpu().numpy(),
              dt_bias=m.dt_bias.cpu().numpy(), A=m.A.cpu().numpy(), D=m.d.cpu().numpy(),
              norm_w=m.norm_w.cpu().numpy())
     cfgd = dict(nheads=c.nheads, headdim=c.per_head_dim, ngroups=c.ngroups, dstate=c.state_rank,
                 norm_before_gate=c.is_norm_before_gate, dt_limit=c.dt_limit)
     yn, cs, ss = oracle.mamba2_block_fwd(proj.astype(np.float32), p, cs0, ss0, chunk, cfgd,
-                                         eps=8.1584695e-8)
-    out = yn @ m.out_proj_w.float().cpu().numpy().astype(np.float64)
+                                         eps=2.0885676e-5 if io_round is not None else 8.1584695e-8,
+                                         io_round=io_round)
+    out = rnd(yn @ m.out_proj_w.float().cpu().numpy().astype(np.float64))
     return out, cs, ss
 
 
@@ -186,10 +191,16 @@ def test_mamba2_forward_bf16_config1_heads():
     assert mamba_hip.ssd2_fast_path(xbc[:, :, :di].unflatten(2, (cfg.nheads, 64)), dt, m.A,
                                     xbc[:, :, di:di + N].unflatten(2, (1, N)), xbc[:, :, di + N:].unflatten(2, (1, N)),
                                     chunk_len=256)
+    # the oracle rounds to bf16 where the bf16 model stores a tensor (in_proj,
+    # conv and SSD outputs, normed values, block output), so the bars are
+    # north_star's absolute ones
     want, _, ss = _oracle_forward(m, xt.float().cpu().numpy(), np.zeros((b, cfg.conv_dim, 4), np.float32),
-                                  np.zeros((b, cfg.nheads, 64, N), np.float32), 256)
+                                  np.zeros((b, cfg.nheads, 64, N), np.float32), 256, io_round=_bf16)
     got = out.float().cpu().numpy()
-    # out = yn @ W_out sums 5120 bf16 products: compare relative to the output scale
-    scale = np.abs(want).max()
-    np.testing.assert_allclose(got / scale, want / scale, rtol=0, atol=2e-2)
+    np.testing.assert_allclose(got, want, **BF16_TOL)
     np.testing.assert_allclose(cache.ssm_bhpr.cpu().numpy(), ss, **BF16_TOL)
+
+
+def _bf16(a):
+    from inputs import bf16_round
+    return bf16_round(np.asarray(a, np.float32)).astype(np.float64)

@@ -220,6 +220,10 @@ FAST_CASES = [
     (1, 700, 2, 8, 1, 16, 2, 8),      # partial rotation, three segments, ragged tail
     (2, 512, 4, 32, 2, 64, 1, 0),     # rotation off, exactly two segments
     (1, 270, 2, 8, 1, 8, 2, 8),       # dstate 8 with MIMO: both pair members in one thread
+    # the benched config-4 instantiation (dstate 128: 16 threads per row, (k, k + 64)
+    # partners by xor-8 lane exchange, the fixed (B/C, rank) mapping of MIMO 4),
+    # full rotation, three segments with a ragged tail
+    (1, 600, 8, 64, 1, 128, 4, 128),
 ]
 
 
@@ -255,8 +259,18 @@ def test_mamba3_prep_fwd_segments(case, dtype):
     torch.cuda.synchronize()
     r = oracle.mamba3_prep_fwd(pin.float().cpu().numpy(), prm, cache)
     io_tol = dict(rtol=2e-2, atol=1e-2) if dtype == "bf16" else F32_TOL
-    for k in ("v", "B", "C"):
-        np.testing.assert_allclose(out[k].float().cpu().numpy(), r[k], **io_tol, err_msg=k)
+    np.testing.assert_allclose(out["v"].float().cpu().numpy(), r["v"], **io_tol, err_msg="v")
+    for k in ("B", "C"):
+        # rotated rows: an angle error d moves each rotated pair by d times the
+        # pair's length, so the f32 bar is relative to each row's scale (f32
+        # angles carried over hundreds of positions err by ~1e-6 rad)
+        got, want = out[k].float().cpu().numpy(), r[k]
+        if dtype == "bf16":
+            np.testing.assert_allclose(got, want, **io_tol, err_msg=k)
+        else:
+            row = np.abs(want).max(axis=-1, keepdims=True)
+            bad = np.abs(got - want) > F32_TOL["atol"] + F32_TOL["rtol"] * row
+            assert not bad.any(), f"{k}: {int(bad.sum())} elements beyond rtol 1e-4 of their row's scale"
     for k in ("da", "gamma", "scale", "h0"):
         np.testing.assert_allclose(out[k].cpu().numpy(), r[k], **F32_TOL, err_msg=k)
     np.testing.assert_allclose(cg.k_state_bmhr.cpu().numpy(), r["k_state"], **F32_TOL)

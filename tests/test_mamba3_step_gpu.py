@@ -151,39 +151,48 @@ def test_mamba3_block_step_and_fresh_cache():
     np.testing.assert_allclose(out2.cpu().numpy(), y2 @ Wo, rtol=1e-3, atol=1e-4)
 
 
-def test_mamba3_block_step_bf16_packed_products():
-    """Mamba3.step on a bf16 block at the config-4 head shape (P 64, N 128,
-    MIMO 4): in_proj and out_proj run on the packed streaming product
-    (mamba_linear_fwd), against the oracle with the same bf16 weight values;
-    the bf16 bar relative to the output scale, two steps from a fresh cache."""
+@pytest.mark.parametrize("d_model,P,N,M,b,packed", [
+    (128, 64, 128, 4, 3, True),     # config-4 head shape, MT 1 product tiles
+    (128, 64, 128, 4, 40, True),    # MT 2
+    (128, 64, 128, 4, 130, True),   # MT 8
+    (40, 16, 32, 2, 5, False),      # d_model 40: not a multiple of 16, the library GEMM
+])
+def test_mamba3_block_step_bf16(d_model, P, N, M, b, packed):
+    """Mamba3.step on a bf16 block, two steps from a fresh cache, against the
+    oracle with the same bf16 weight values.  in_proj and out_proj run on the
+    packed streaming product (mamba_linear_fwd) where its shape rules allow,
+    else on the library GEMM; both round their outputs to bf16 as the bf16
+    model stores them, which the oracle repeats, so the bars are north_star's
+    absolute ones."""
     import torch
     import mamba_hip
     import oracle
-    cfg = mamba_hip.Mamba3Config(d_model=128, state_rank=128, per_head_dim=64, mimo_rank=4)
+    from inputs import bf16_round
+    cfg = mamba_hip.Mamba3Config(d_model=d_model, state_rank=N, per_head_dim=P, mimo_rank=M)
     gen = torch.Generator(device="cuda")
-    gen.manual_seed(13)
+    gen.manual_seed(13 + b)
     m = cfg.init("cuda", torch.bfloat16, gen)
-    b = 3
-    x = torch.randn((b, 128), generator=gen, device="cuda").to(torch.bfloat16)
+    x = torch.randn((b, d_model), generator=gen, device="cuda").to(torch.bfloat16)
+    assert mamba_hip.step_mm_ok(x, m.in_proj_w) == packed
     out, cache = m.step(x, None)
     out2, cache = m.step((x.float() * 0.5).to(torch.bfloat16), cache)
     torch.cuda.synchronize()
+    assert out.dtype == torch.bfloat16
     f = lambda t: None if t is None else t.float().cpu().numpy()  # noqa: E731
-    prm = dict(nheads=cfg.nheads, headdim=64, ngroups=1, dstate=128, mimo=4, rope_dim=cfg.rope_dim,
+    prm = dict(nheads=cfg.nheads, headdim=P, ngroups=1, dstate=N, mimo=M, rope_dim=cfg.rope_dim,
                dt_bias=f(m.dt_bias), a_floor=cfg.a_floor, dt_limit=cfg.dt_limit, rotation_range=cfg.rotation_range,
                b_norm_w=f(m.b_norm_w), c_norm_w=f(m.c_norm_w), b_bias=f(m.b_bias), c_bias=f(m.c_bias), D=f(m.D),
                mimo_x=f(m.mimo_x), mimo_z=f(m.mimo_z), mimo_o=f(m.mimo_o))
     W, Wo = f(m.in_proj_w), f(m.out_proj_w)
     c0 = {k: np.zeros(sh, np.float32) for k, sh in
-          dict(ssm=(b, cfg.nheads, 64, 128), k_state=(b, 4, cfg.nheads, 128), v_state=(b, cfg.nheads, 64),
+          dict(ssm=(b, cfg.nheads, P, N), k_state=(b, M, cfg.nheads, N), v_state=(b, cfg.nheads, P),
                angle=(b, cfg.nheads, cfg.num_rope_angles)).items()}
     xs = f(x)
-    y1, c1 = oracle.mamba3_step(xs @ W, prm, c0)
-    y2, _ = oracle.mamba3_step(f((x.float() * 0.5).to(torch.bfloat16)) @ W, prm, c1)
+    y1, c1 = oracle.mamba3_step(bf16_round(xs @ W), prm, c0)
+    y2, _ = oracle.mamba3_step(bf16_round(f((x.float() * 0.5).to(torch.bfloat16)) @ W), prm, c1)
     for got, y in ((out, y1), (out2, y2)):
-        want = y @ Wo
-        scale = np.abs(want).max()
-        np.testing.assert_allclose(f(got) / scale, want / scale, rtol=0, atol=2e-2)
+        want = bf16_round(bf16_round(y) @ Wo)
+        np.testing.assert_allclose(f(got), want, rtol=2e-2, atol=1e-2)
 
 
 def test_mamba3_step_validation():

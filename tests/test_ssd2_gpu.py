@@ -228,3 +228,88 @@ def test_ssd2_mfma_steep_blocks(dt_range):
     yr, hr = _oracle(inp, q, "bf16")
     np.testing.assert_allclose(y.float().cpu().numpy(), yr, **BF16_TOL)
     np.testing.assert_allclose(hT.cpu().numpy(), hr, **BF16_TOL)
+
+
+def _assert_close_rows(got, want, rtol, atol, what):
+    """assert_allclose over the leading axis, one slice at a time (the
+    full-size arrays are hundreds of MB)."""
+    for i in range(got.shape[0]):
+        np.testing.assert_allclose(got[i], want[i], rtol=rtol, atol=atol, err_msg=f"{what}[{i}]")
+
+
+def test_ssd2_config1_full_size():
+    """BASELINE.json configs[1] at its full size (8 x 4096 tokens, 80 heads,
+    headdim 64, dstate 128, one group, chunk 256, bf16 x/B/C/y): the benched
+    MFMA path (16-chunk state carry, XCD-remapped workgroups) against the f32
+    serial oracle on the same bf16-rounded inputs; y and the final state at
+    north_star's bf16 bars."""
+    import torch
+    import mamba_hip
+    import oracle
+    b, l, h, p, g, n, q = 8, 4096, 80, 64, 1, 128, 256
+    print(f"ssd2 config 1 full size {b}x{l}x{h}", flush=True)
+    inp = ssd2_inputs(seed=2024, b=b, l=l, h=h, p=p, g=g, n=n, h0=False)
+    t = _to_dev(inp)
+    assert mamba_hip.ssd2_fast_path(t["x"], t["dt"], t["A"], t["B"], t["C"], chunk_len=q)
+    y, hT = mamba_hip.ssd2_fwd(t["x"], t["dt"], t["A"], t["B"], t["C"], t["D"], None, chunk_len=q)
+    torch.cuda.synchronize()
+    y = y.float().cpu().numpy()
+    hT = hT.cpu().numpy()
+    del t
+    for k in ("x", "B", "C"):
+        inp[k] = bf16_round(inp[k])
+    yr, hr = oracle.ssd2(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"], None, chunk=q,
+                         form="serial", prec=32)
+    _assert_close_rows(y, yr, what="y", **BF16_TOL)
+    _assert_close_rows(hT, hr, what="final_state", **BF16_TOL)
+
+
+def test_mamba2_ssd_input_run_chunked():
+    """Mamba2SsdInput.run on the reference's 5-d chunked tensors
+    (ssd_path.rs:58-87, 149-155): x [b, n, l, h, p], dt [b, n, l, h], per-head
+    B/C [b, n, l, h, r] as the reference's GQA expand leaves them
+    (mamba2.rs:733-734), and a learnable init_state_hpr; y comes back chunked."""
+    import torch
+    import mamba_hip
+    import oracle
+    b, nch, q, h, p, n = 2, 3, 64, 4, 64, 128
+    inp = ssd2_inputs(seed=17, b=b, l=nch * q, h=h, p=p, g=1, n=n, h0=True)
+    init = (0.1 * np.random.default_rng(18).standard_normal((h, p, n))).astype(np.float32)
+    t = _to_dev(inp)
+    exp = lambda a: a.repeat_interleave(h, dim=2).reshape(b, nch, q, h, n)  # noqa: E731
+    si = mamba_hip.Mamba2SsdInput(
+        x_bnlhp=t["x"].reshape(b, nch, q, h, p), dt_bnlh=t["dt"].reshape(b, nch, q, h), a_decay_h=t["A"],
+        b_bnlhr=exp(t["B"]), c_bnlhr=exp(t["C"]), d_h=t["D"], initial_state_bhpr=t["h0"],
+        init_state_hpr=torch.from_numpy(init).cuda())
+    path = mamba_hip.Mamba2SsdPath(mamba_hip.Mamba2SsdPath.SERIAL_RECALCULATED, q)
+    y, hT = si.run(path)
+    torch.cuda.synchronize()
+    assert tuple(y.shape) == (b, nch, q, h, p) and tuple(hT.shape) == (b, h, p, n)
+    xr, Br, Cr = bf16_round(inp["x"]), bf16_round(inp["B"]), bf16_round(inp["C"])
+    yr, hr = oracle.ssd2(xr, inp["dt"], inp["A"], Br, Cr, inp["D"], inp["h0"], init, chunk=q)
+    np.testing.assert_allclose(y.float().cpu().numpy().reshape(b, nch * q, h, p), yr, **BF16_TOL)
+    np.testing.assert_allclose(hT.cpu().numpy(), hr, **BF16_TOL)
+
+
+def test_mamba2_ssd_path_default_chunk():
+    """Mamba2SsdPath with no chunk length takes optimal_chunk_len
+    (ssd_path.rs:109-114, 139-155): 96 for r=128, p=64 and 64 for r=p=64.  The
+    SSD called with chunk_len=None chunks at that length, and the result is
+    the oracle's at chunk 96."""
+    import torch
+    import mamba_hip
+    P = mamba_hip.Mamba2SsdPath
+    path = P()
+    assert path.kind == P.SERIAL_RECALCULATED and path.chunk_len() is None
+    assert path.chunk_len_or_optimal(128, 64) == 96 == P.optimal_chunk_len(128, 64)
+    assert path.chunk_len_or_optimal(64, 64) == 64
+    assert P.optimal_chunk_len(16, 16) == 32 and P.optimal_chunk_len(4096, 4096) == 512
+    assert P(P.MINIMAL, 48).chunk_len_or_optimal(128, 64) == 48
+    inp = ssd2_inputs(seed=19, b=1, l=300, h=4, p=64, g=1, n=128, h0=True)
+    t = _to_dev(inp)
+    assert mamba_hip.ssd2_fast_path(t["x"], t["dt"], t["A"], t["B"], t["C"], chunk_len=None)
+    y, hT = mamba_hip.ssd2_fwd(t["x"], t["dt"], t["A"], t["B"], t["C"], t["D"], t["h0"], chunk_len=None)
+    torch.cuda.synchronize()
+    yr, hr = _oracle(inp, 96, "bf16")
+    np.testing.assert_allclose(y.float().cpu().numpy(), yr, **BF16_TOL)
+    np.testing.assert_allclose(hT.cpu().numpy(), hr, **BF16_TOL)

@@ -407,3 +407,36 @@ def test_fused_and_unfused_stacks_agree():
         np.testing.assert_allclose(a.ssm_bhpr.cpu().numpy(), e.ssm_bhpr.cpu().numpy(), **tol)
         # windows hold raw bf16 in_proj outputs: a different accumulation order can move them by one bf16 ulp
         np.testing.assert_allclose(a.conv_bvk.cpu().numpy(), e.conv_bvk.cpu().numpy(), **tol)
+
+
+def test_fused_stack_config3_layer_shape():
+    """BASELINE.json configs[3]'s layer shape at batch 64: d_model 2560, 80
+    heads x 64, dstate 128, conv width 4, in_proj 2560 -> 10576 and out_proj
+    5120 -> 2560 (the split-K products the benchmark runs).  Two fused layers
+    (one mamba2_stack_step call) step two tokens from random caches, against
+    the oracle's pre-norm layer step (src/modules/layer.rs:224-228) on the same
+    bf16 weights: outputs and both caches of every layer."""
+    import torch
+    import mamba_hip
+    import oracle
+    b, d_model = 64, 2560
+    cfg = mamba_hip.Mamba2Config(d_model=d_model)
+    assert (cfg.nheads, cfg.d_in_proj, cfg.state_rank) == (80, 10576, 128)
+    stack = mamba_hip.Mamba2Stack.init(cfg, 2, "cuda", torch.bfloat16, torch.Generator().manual_seed(64), fused=True)
+    assert stack.fused
+    rng = np.random.default_rng(64)
+    caches = stack.new_caches(b)
+    refs = _randomize_caches(caches, rng)
+    params = [_oracle_params(l) for l in stack.layers]
+    for step in range(2):
+        x = rng.standard_normal((b, d_model)).astype(np.float32)
+        y, caches = stack.step(_t(x), caches)
+        torch.cuda.synchronize()
+        u = x
+        for i, p in enumerate(params):
+            u, refs[i][0], refs[i][1] = oracle.mamba2_layer_step(u, p, refs[i][0], refs[i][1], _cfg_dict(cfg))
+        print(f"config-3 layer shape, batch {b}, step {step}", flush=True)
+        np.testing.assert_allclose(y.cpu().numpy(), u, **BF16_TOL)
+        for i, c in enumerate(caches):
+            np.testing.assert_allclose(c.conv_bvk.cpu().numpy(), refs[i][0], **BF16_TOL)
+            np.testing.assert_allclose(c.ssm_bhpr.cpu().numpy(), refs[i][1], **BF16_TOL)
