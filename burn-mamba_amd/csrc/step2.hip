@@ -25,6 +25,8 @@
 // HBM layout: the caches are the reference's Mamba2Cache tensors unchanged
 // (conv_bvk [b, conv_dim, K] f32 and ssm_bhpr [b, H, P, N] f32, cache.rs:98-122),
 // so a state tile of one (b, h) is one contiguous P*N*4-byte block.
+#include <mutex>
+
 #include "common.h"
 #include "lin.h"
 
@@ -798,7 +800,56 @@ static int stack_dispatch(const mamba2_layer_args* layers, int n_layers, void* w
     return MAMBA_OK;
 }
 
+// ------------------------------------------------ allocation-free stack --
+// The workspace of mamba2_stack_step_noalloc: a file-scope device array.  Each
+// GPU the library runs on holds its own copy (at its own address) until the
+// process ends.  Host code never passes `scratch` itself to a kernel or a copy:
+// on the host the name is only a stand-in for the symbol, so the device address
+// of the current GPU's copy is looked up once per device and kept.
+static __device__ __align__(256) unsigned char scratch[MAMBA2_STACK_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kScratchDevices] = {};
+
+// Device address of the current GPU's `scratch` (looked up on the first call
+// on that device, with that device current).
+static int scratch_address(void** out) {
+    int dev = -1;
+    MAMBA_CHECK_HIP(hipGetDevice(&dev));
+    MAMBA_CHECK_ARG(dev >= 0 && dev < kScratchDevices, "device index out of range for the scratch table");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* ptr = nullptr;
+        MAMBA_CHECK_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        MAMBA_CHECK_ARG(ptr != nullptr && ((uintptr_t)ptr & 255u) == 0, "scratch symbol address is not usable");
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return MAMBA_OK;
+}
+
 }  // namespace mamba
+
+extern "C" int mamba2_stack_step_noalloc(const mamba2_layer_args* layers, int32_t n_layers, mamba_stream_t stream) {
+    MAMBA_CHECK_ARG(layers != nullptr && n_layers >= 1, "at least one layer is required");
+    const int st = layer_check(&layers[0], &layers[0]);
+    if (st != MAMBA_OK) return st;
+    const size_t need = layer_ws_layout(layer_geom(&layers[0]), nullptr).total;
+    if (need > MAMBA2_STACK_NOALLOC_SCRATCH_BYTES) {
+        set_error("mamba2_stack_step_noalloc: this stack needs a workspace of " + std::to_string(need) +
+                  " bytes, more than the " + std::to_string(MAMBA2_STACK_NOALLOC_SCRATCH_BYTES) +
+                  "-byte scratch array; use mamba2_stack_step with a caller workspace");
+        return MAMBA_ERR_WORKSPACE;
+    }
+    void* ws = nullptr;
+    const int sa = scratch_address(&ws);
+    if (sa != MAMBA_OK) return sa;
+    // every workspace region is written before it is read within the call
+    // (packed operands, partial planes, per-head sums), so nothing is cleared
+    return stack_dispatch(layers, n_layers, ws, MAMBA2_STACK_NOALLOC_SCRATCH_BYTES, (hipStream_t)stream, nullptr,
+                          nullptr);
+}
 
 extern "C" size_t mamba2_layer_workspace_size(const mamba2_layer_args* a) {
     if (a == nullptr || a->batch < 1 || a->nheads < 1 || a->headdim < 1) return 0;

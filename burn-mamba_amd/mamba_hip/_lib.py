@@ -293,6 +293,7 @@ _SIGNATURES = {
     "mamba2_stack_step": ([ctypes.POINTER(Mamba2LayerArgs), c_i32, c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),
     "mamba2_stack_step_timed": ([ctypes.POINTER(Mamba2LayerArgs), c_i32, c_vp, ctypes.c_size_t, c_vp,
                                  ctypes.POINTER(c_vp), ctypes.POINTER(c_vp)], ctypes.c_int),
+    "mamba2_stack_step_noalloc": ([ctypes.POINTER(Mamba2LayerArgs), c_i32, c_vp], ctypes.c_int),
 }
 
 _lib = None

@@ -578,6 +578,20 @@ int mamba2_stack_step_timed(const mamba2_layer_args* layers, int32_t n_layers, v
                             size_t workspace_bytes, mamba_stream_t stream, void* const* event_start,
                             void* const* event_stop);
 
+/* mamba2_stack_step without a workspace argument and without any allocation: */
+/* no counterpart in the reference.  It is for callers that cannot allocate    */
+/* device memory (code under HIP graph capture, tight serving loops, harnesses */
+/* that forbid hipMalloc).  The workspace is a file-scope device array of      */
+/* MAMBA2_STACK_NOALLOC_SCRATCH_BYTES, one per GPU, held until the process     */
+/* ends; a stack whose mamba2_layer_workspace_size exceeds it is rejected with */
+/* MAMBA_ERR_WORKSPACE before any launch.  48 MiB holds every one-group stack  */
+/* mamba2_stack_step accepts at expand 2 (batch <= 256, d_model <= 4096; the   */
+/* 2.7B-shaped stack needs 29.5 MiB at batch 256).  Nothing in it needs to     */
+/* start at zero.  Every call on a GPU shares that GPU's array, so calls that  */
+/* overlap on one GPU (other streams or host threads) race; serialise them.    */
+#define MAMBA2_STACK_NOALLOC_SCRATCH_BYTES ((size_t)48 << 20)
+int mamba2_stack_step_noalloc(const mamba2_layer_args* layers, int32_t n_layers, mamba_stream_t stream);
+
 /* ------------------------------------------------------------------------- */
 /* Residual add + RmsNorm over rows (src/modules/norm/rms_norm.rs:53-98), the  */
 /* pre-norm and residual of Layer::step_one (src/modules/layer.rs:224-232):    */
