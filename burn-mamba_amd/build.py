@@ -32,6 +32,7 @@ CFLAGS = [
 # per-file additions: MFMA results kept in VGPRs (no AGPR round trips for
 # kernels that post-process accumulators with VALU work)
 FILE_FLAGS = {
+    "ssd2_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "ssd3_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 

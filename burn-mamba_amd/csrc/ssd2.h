@@ -26,6 +26,8 @@ int ssd2_generic_launch(const Ssd2Params& p, void* ws, hipStream_t stream, hipEv
                         hipEvent_t ev1 = nullptr);
 
 bool ssd2_mfma_supported(const Ssd2Params& p);
+// heads per workgroup the MFMA scan kernel would use for p
+int ssd2_mfma_hpw(const Ssd2Params& p);
 size_t ssd2_mfma_workspace(const Ssd2Params& p);
 int ssd2_mfma_launch(const Ssd2Params& p, void* ws, hipStream_t stream, hipEvent_t ev0 = nullptr,
                      hipEvent_t ev1 = nullptr);

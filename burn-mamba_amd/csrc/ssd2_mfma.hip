@@ -5,26 +5,28 @@
 // src/mamba2/ssd/serial_recalculated/serial_recalculated.rs:98-155.
 //
 // Two launches per call:
-//   1. ssd2_prep_mfma (per batch, chunk, group): the group-shared causal
+//   1. ssd2_prep_pack (per batch, chunk, group): the group-shared causal
 //      C_c.B_c^T tiles (K2, computed once per group instead of once per head,
-//      f32 accumulation rounded to bf16), and C_c and B_c in bf16, all three
-//      stored in MFMA operand order
-//      so that every wave load of them is one contiguous 1 KB.
-//   2. ssd2_scan_mfma: one workgroup per (batch, head[, half of headdim])
-//      walks the chunks in order.  The running state h[p, n] lives in MFMA
-//      accumulators for the whole sequence (K4 needs no HBM round trip); per
-//      chunk it computes K1 in registers/LDS, then
+//      f32 accumulation rounded to bf16), C_c and B_c in bf16, written as one
+//      packed run of 1 KB MFMA operand fragments per (batch, chunk, group).
+//   2. ssd2_scan_wu: one wave per (batch, head, 32-wide headdim half) walks
+//      the chunks in order, with the running state in its MFMA accumulators
+//      for the whole sequence (K4 needs no HBM round trip).  The HPW waves of
+//      a workgroup are HPW heads of one group: the only thing they share is
+//      the group's fragments, which the workgroup stages once per chunk into
+//      LDS with direct-to-LDS loads (double-buffered, one barrier per chunk).
+//      Per chunk a wave computes K1 in its lanes, then
 //        y = exp(cs_i) C_i . h_in + sum_{j<=i} (C_i.B_j) dt_j exp(cs_i-cs_j) x_j + D x_i
-//        h_out = exp(cs_end) h_in + sum_j x_j^T (B_j dt_j exp(cs_end - cs_j))
+//        h_out = exp(cs_end) h_in + sum_j (B_j dt_j exp(cs_end - cs_j)) (x) x_j
 //      with every contraction on v_mfma_f32_32x32x16_bf16.  x is read from
-//      HBM once (staged time-major in LDS), y is written once.
+//      HBM once, y is written once.
 //
 // MFMA 32x32x16 operand/result layout (lane l, r = l % 32, half = l / 32):
 //   A[m][k]: lane holds row m = r, k = 8*half .. 8*half+7
 //   B[k][n]: lane holds col n = r, k = 8*half .. 8*half+7
 //   D[m][n]: lane holds col n = r, rows 8*(v/4) + 4*half + (v%4), v = 0..15
-// (Any permutation of k that A and B share leaves the product unchanged; the
-// row/col mappings and the D layout are what the indexing below relies on.)
+// Any permutation of k that A and B share leaves the product unchanged; the
+// row/col mappings and the D layout are what the indexing below relies on.
 
 #include <cstdlib>
 
@@ -39,15 +41,15 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kMaxQ = 256;
 
 #ifndef MAMBA_SSD2_L2_WARM
-#define MAMBA_SSD2_L2_WARM 1  // touch the next chunk's group operands ahead of use
+#define MAMBA_SSD2_L2_WARM 1  // touch the chunk after next's fragments ahead of use
 #endif
 
 __device__ __forceinline__ f32x16_t mfma32x32x16(bf16x8_t a, bf16x8_t b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ uint4 ld16(const void* ptr, bool ok) {
-    return ok ? *(const uint4*)ptr : make_uint4(0u, 0u, 0u, 0u);
+__device__ __forceinline__ uint2 ld8(const void* ptr, bool ok) {
+    return ok ? *(const uint2*)ptr : make_uint2(0u, 0u);
 }
 
 // 8 packed bf16 (one uint4) -> 8 floats
@@ -78,20 +80,31 @@ __device__ __forceinline__ f32x16_t zero16() {
     return z;
 }
 
+// Fragments per (batch, chunk, group), in the order the scan kernel stages them:
+//   CB  it*(it+1) + ks         (C.B^T)[i = 32 it + lane%32][j = 16 ks + 8 (lane/32) + e],
+//                              ks <= 2 it + 1 (the causal ones)
+//   C   NCB + it*NK + kn       C[i = 32 it + lane%32][n = 16 kn + perm(lane/32, e)]
+//   B   NCB + T*NK + nt*KS+ks  B[j = 16 ks + 8 (lane/32) + e][n = 32 nt + lane%32]
+// each 64 lanes x 8 bf16 = 1 KB.  perm(half, e) = e < 4 ? 4 half + e : 8 + 4 half + e - 4
+// is the k order in which a wave's state accumulator rows (D layout) sit in its
+// lanes, so the state enters h . C^T as the A operand straight from registers.
+template <int N, int Q>
+struct FragLayout {
+    static constexpr int T = Q / 32, NK = N / 16, KS = Q / 16, NTN = N / 32;
+    static constexpr int NCB = T * (T + 1);
+    static constexpr int C0 = NCB, B0 = NCB + T * NK;
+    static constexpr int NF = B0 + NTN * KS;
+};
+
 // ------------------------------------------------ per-group operand prep --
 // Per (batch, chunk, group) -- shared by every head of the group -- write the
-// MFMA B operands of the scan kernel in fragment order, so that each wave
-// load there is one contiguous 1 KB read:
-//   cbf[it][ks][lane][8] : (C.B^T)[i = 32 it + lane%32][j = 16 ks + 8 (lane/32) + e]
-//   cf [it][kn][lane][8] : C[i = 32 it + lane%32][n = 16 kn + 8 (lane/32) + e]
-//   bf [nt][ks][lane][8] : B[j = 16 ks + 8 (lane/32) + e][n = 32 nt + lane%32]
-// all bf16 (the C.B^T products rounded from their f32 accumulation).
-// Positions past seqlen read as zero.  Only the causal (ks <= 2 it + 1)
-// fragments of cbf are written (K2, src/mamba2/ssd/serial.rs:170-185), and
-// inside the diagonal 32x32 blocks the entries with j > i are stored as 0.
+// fragments above.  Positions past seqlen read as zero.  Only the causal
+// (ks <= 2 it + 1) C.B^T fragments are written (K2, src/mamba2/ssd/serial.rs:170-185),
+// and inside the diagonal 32x32 blocks the entries with j > i are stored as 0.
 template <int N, int Q>
-__global__ __launch_bounds__(256) void ssd2_prep_mfma(Ssd2Params p, bf16_t* cbf, bf16_t* cf, bf16_t* bfr) {
-    constexpr int T = Q / 32, NK = N / 16, KS = Q / 16, NTN = N / 32;
+__global__ __launch_bounds__(256) void ssd2_prep_pack(Ssd2Params p, bf16_t* frag) {
+    using FL = FragLayout<N, Q>;
+    constexpr int T = FL::T, NK = FL::NK, KS = FL::KS, NTN = FL::NTN, NF = FL::NF;
     constexpr int NTILE = T * (T + 1) / 2;
     const int wave = wave_id(), lane = threadIdx.x & 63, r = lane & 31, half = lane >> 5;
     const int s = blockIdx.x, S = gridDim.x;
@@ -99,9 +112,9 @@ __global__ __launch_bounds__(256) void ssd2_prep_mfma(Ssd2Params p, bf16_t* cbf,
     const int64_t grp = ((int64_t)b * p.nch + c) * p.G + g;
     const bf16_t* Cg = (const bf16_t*)p.Cm + (int64_t)b * p.C_sb + (int64_t)g * p.C_sg;
     const bf16_t* Bg = (const bf16_t*)p.Bm + (int64_t)b * p.B_sb + (int64_t)g * p.B_sg;
+    bf16_t* base = frag + grp * NF * 512;
     // (C.B^T)^T tiles: D[j][i] = sum_n B[j][n] C[i][n]; the lane then holds
     // column i = 32 it + r at rows j = 32 jt + 8 q + 4 half + u (v = 4 q + u)
-    bf16_t* cbase = cbf + grp * Q * Q;
     for (int tile = s + S * wave; tile < NTILE; tile += 4 * S) {
         int it = 0;
         while ((it + 1) * (it + 2) / 2 <= tile) ++it;
@@ -111,8 +124,10 @@ __global__ __launch_bounds__(256) void ssd2_prep_mfma(Ssd2Params p, bf16_t* cbf,
 #pragma unroll
         for (int kn = 0; kn < NK; ++kn) {
             const int n0 = kn * 16 + 8 * half;
-            const bf16x8_t a = as_bf16x8(ld16(Bg + (int64_t)tj * p.B_sl + n0, tj < p.L));
-            const bf16x8_t bb = as_bf16x8(ld16(Cg + (int64_t)ti * p.C_sl + n0, ti < p.L));
+            const bf16x8_t a = as_bf16x8(tj < p.L ? *(const uint4*)(Bg + (int64_t)tj * p.B_sl + n0)
+                                                  : make_uint4(0u, 0u, 0u, 0u));
+            const bf16x8_t bb = as_bf16x8(ti < p.L ? *(const uint4*)(Cg + (int64_t)ti * p.C_sl + n0)
+                                                   : make_uint4(0u, 0u, 0u, 0u));
             acc = mfma32x32x16(a, bb, acc);
         }
         if (jt == it) {  // causal mask of the diagonal block: row j = 8 q + 4 half + u, column i = r
@@ -125,21 +140,18 @@ __global__ __launch_bounds__(256) void ssd2_prep_mfma(Ssd2Params p, bf16_t* cbf,
             const int ks = 2 * jt + (q >> 1), lp = r + 32 * (q & 1);
             // fragment (it, ks), lane lp, elements 4 half .. 4 half + 3
             uint2 pk;
-            pk.x = (uint32_t)__builtin_bit_cast(bf16_t, (__bf16)acc[4 * q]) |
-                   ((uint32_t)__builtin_bit_cast(bf16_t, (__bf16)acc[4 * q + 1]) << 16);
-            pk.y = (uint32_t)__builtin_bit_cast(bf16_t, (__bf16)acc[4 * q + 2]) |
-                   ((uint32_t)__builtin_bit_cast(bf16_t, (__bf16)acc[4 * q + 3]) << 16);
-            *(uint2*)(cbase + ((int64_t)(it * KS + ks) * 64 + lp) * 8 + 4 * half) = pk;
+            pk.x = pack_bf16x2(acc[4 * q], acc[4 * q + 1]);
+            pk.y = pack_bf16x2(acc[4 * q + 2], acc[4 * q + 3]);
+            *(uint2*)(base + ((int64_t)(it * (it + 1) + ks) * 64 + lp) * 8 + 4 * half) = pk;
         }
     }
-    bf16_t* cbase2 = cf + grp * (int64_t)Q * N;
     for (int f = s + S * wave; f < T * NK; f += 4 * S) {
         const int it = f / NK, kn = f % NK;
         const int t = c * Q + it * 32 + r;
-        *(uint4*)(cbase2 + ((int64_t)f * 64 + lane) * 8) =
-            ld16(Cg + (int64_t)t * p.C_sl + kn * 16 + 8 * half, t < p.L);
+        const bf16_t* row = Cg + (int64_t)t * p.C_sl + kn * 16 + 4 * half;
+        const uint2 lo = ld8(row, t < p.L), hi = ld8(row + 8, t < p.L);  // k order perm(half, .)
+        *(uint4*)(base + ((int64_t)(FL::C0 + f) * 64 + lane) * 8) = make_uint4(lo.x, lo.y, hi.x, hi.y);
     }
-    bf16_t* bbase = bfr + grp * (int64_t)Q * N;
     for (int f = s + S * wave; f < NTN * KS; f += 4 * S) {
         const int nt = f / KS, ks = f % KS;
         const int n = nt * 32 + r;
@@ -149,22 +161,23 @@ __global__ __launch_bounds__(256) void ssd2_prep_mfma(Ssd2Params p, bf16_t* cbf,
             const int t = c * Q + ks * 16 + 8 * half + e;
             raw[e] = t < p.L ? (uint32_t)Bg[(int64_t)t * p.B_sl + n] : 0u;
         }
-        *(uint4*)(bbase + ((int64_t)f * 64 + lane) * 8) =
+        *(uint4*)(base + ((int64_t)(FL::B0 + f) * 64 + lane) * 8) =
             make_uint4(raw[0] | (raw[1] << 16), raw[2] | (raw[3] << 16), raw[4] | (raw[5] << 16),
                        raw[6] | (raw[7] << 16));
     }
 }
 
-// Owner wave of i-tile `it` (snake order, balances the causal triangle).
-__device__ __forceinline__ int itile_owner(int it) {
-    return ((it >> 2) & 1) ? 3 - (it & 3) : (it & 3);
-}
-
 // ----------------------------------------------- K1 + K3 + K4 + K5 fused --
-// One workgroup (4 waves) per (batch, head[, headdim half]); chunks in order.
-// N = dstate, Q = chunk length (multiple of 32, <= 256), PT = 32-wide headdim
-// tiles per workgroup (2: the whole headdim 64; 1: one half).  Every
-// group-shared fragment a wave loads feeds PT MFMAs.
+// One wave per (batch, head, 32-wide headdim half), HPW waves (HPW heads of
+// one group) per workgroup; chunks in order.  N = dstate, Q = chunk length
+// (32 or 64: a chunk's positions are the wave's lanes).
+//
+// The state is carried transposed, h^T[n, p] (n along MFMA rows, p along
+// columns), in NTN accumulator tiles: the state GEMM is h^T += B^T . xg with
+// the B fragments as the A operand and xg from LDS as the B operand, and the
+// accumulator registers of h^T, converted to bf16 eight at a time, are the A
+// operand of y^T = h . C^T (the C fragments carry the matching k order).  So
+// nothing of the state leaves the registers between chunks.
 //
 // The chunk is cut into 32-position blocks k = 0 .. T-1 ending at e_k = 32k+31
 // (cs_{e_-1} = 0 is the chunk start).  Every decay is carried by x and by a
@@ -177,7 +190,7 @@ __device__ __forceinline__ int itile_owner(int it) {
 //   acc = C_i.h_in;  acc = acc F_k + S_k  (k = 0 .. it)
 //   y_i = exp(cs_i - cs_{e_it}) acc + D x_i
 // and the chunk state is the same recurrence over all T blocks with the raw B
-// fragments,  h <- h F_k + sum_{j in k} xg_j (x) B_j.
+// fragments,  h <- h F_k + sum_{j in k} B_j (x) xg_j.
 // Only xg is kept in LDS.  D x_i is taken from it as D xg_i / g_i (g_i =
 // dt_i exp(cs_{e_it} - cs_i)) when every g_i of the tile is at least 2^-100,
 // and from the raw x rows otherwise (dt = 0 included).  The output's last
@@ -191,332 +204,255 @@ __device__ __forceinline__ int itile_owner(int it) {
 // Outputs are computed transposed, y^T[p, i] (i = time along MFMA columns),
 // so every per-time factor is a per-lane scalar and the four consecutive
 // headdim values a lane holds are stored as one 8-byte write.
-template <int N, int Q, int PT>
-__global__ __launch_bounds__(256, 3) void ssd2_scan_mfma(Ssd2Params p, const bf16_t* cbf, const bf16_t* cf,
-                                                         const bf16_t* bfr) {
-    constexpr int T = Q / 32;                 // 32-position blocks per chunk
-    constexpr int NTN = N / 32;               // n tiles of the state
-    constexpr int NST = PT * NTN;             // state tiles per workgroup
-    constexpr int SPW = NST >= 4 ? NST / 4 : 1;  // state tiles per wave
+//
+// Per chunk c a wave: issues the direct-to-LDS loads of its share of chunk
+// c + 1's fragments (into the other buffer); scans dt; stages xg; issues its
+// register prefetch of chunk c + 1's x rows and dt; computes its output tiles
+// and its state; then waits for its loads and meets the others at the chunk's
+// one barrier, after which chunk c + 1's fragments are complete and chunk c's
+// buffer is free.
+// The launch bound caps a wave at 256 registers (two waves per SIMD), which
+// keeps the accumulators in VGPRs next to the VALU work that scales them.
+template <int N, int Q, int HPW>
+__global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu(Ssd2Params p, const bf16_t* frag) {
+    using FL = FragLayout<N, Q>;
+    constexpr int T = FL::T, NK = FL::NK, KS = FL::KS, NTN = FL::NTN, NF = FL::NF;
     constexpr int XP = Q + 8;                 // s_xg row pitch (bf16)
-    constexpr int HP = N + 8;                 // s_h row pitch (bf16)
-    constexpr int PV = PT * 4;                // 8-wide headdim vectors per time row
-    constexpr int XITEMS = (Q / 2) * PV;      // x staging items (2 time rows each)
-    constexpr int XPT = (XITEMS + 255) / 256; // items per thread
-    constexpr int JPM = 256 / PV;             // time-row pairs between a thread's items
-    static_assert(256 % PV == 0, "a thread's items share its headdim vector");
-    constexpr int NK = N / 16, KS = Q / 16;
+    constexpr int XPT = Q / 32;               // x staging items per lane: (2 rows x 8 headdim) each
+    constexpr int FPW = (NF + HPW - 1) / HPW; // fragments each wave stages per chunk
     constexpr float kSteep = 64.f;            // log2 of the largest block decay factored
     constexpr float kTinyG = 0x1p-100f;       // smallest g_i for D x from xg
-    __shared__ __align__(16) float s_cs2[Q];
-    __shared__ __align__(16) float s_dt[Q];
-    __shared__ __align__(16) float s_F[T];
-    __shared__ float s_red[4];
-    __shared__ __align__(16) bf16_t s_xg[PT * 32][XP];  // xg^T (block-scaled x)
-    __shared__ __align__(16) bf16_t s_h[PT * 32][HP];
+    static_assert(Q == 32 || Q == 64, "a chunk's positions are the wave's lanes");
+    __shared__ __align__(16) bf16_t s_frag[2][NF][512];  // the group's fragments, two chunks
+    __shared__ __align__(16) bf16_t s_xg[HPW][32][XP];   // per wave: xg^T [p][j]
+    __shared__ __align__(16) float s_cs[HPW][Q];         // per wave: cumsum (log2 units)
+    __shared__ __align__(16) float s_dt[HPW][Q];         // per wave: dt
 
-    const int wave = wave_id(), lane = threadIdx.x & 63, r = lane & 31, half = lane >> 5;
-    // XCD-aware work mapping: consecutive work items (same batch, neighbouring
-    // heads, sharing B/C/CB) land on the same XCD and its L2.
-    constexpr int splits = 2 / PT;
-    const int nwg = p.nb * p.H * splits;
+    const int wave = wave_id(), lane0 = threadIdx.x & 63;
+    // XCD-aware work mapping: consecutive workgroups (same batch row, sharing
+    // its group fragments through L2) land on the same XCD
+    const int nhq = p.H / HPW;                // head sets per batch row
+    const int nwg = p.nb * nhq * 2;
     int w = blockIdx.x;
     if ((nwg & 7) == 0) w = (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3);
-    const int ph = w % splits, h = (w / splits) % p.H, b = w / (splits * p.H);
-    const int g = h / (p.H / p.G);
-    const int p0 = ph * 32 * PT;
+    const int ph = w & 1, hq = (w >> 1) % nhq, b = (w >> 1) / nhq;
+    const int hpg = p.H / p.G;
+    const int g = (hq * HPW) / hpg;           // all HPW heads of the workgroup are in group g
+    const int h = hq * HPW + wave;            // this wave's head
+    const int p0 = ph * 32;
     const float A2 = p.A[h] * kLog2e;
     const float Dh = p.D ? p.D[h] : 0.f;
 
-    // state tiles owned by this wave
-    int st_pt[SPW], st_nt[SPW];
-    bool st_ok[SPW];
+    // ---- the state h^T: tile nt, register v holds (n = 32 nt + 8 (v/4) + 4 half + v%4, p = p0 + r)
+    f32x16_t hacc[NTN];
+    {
+        const int r = lane0 & 31, half = lane0 >> 5;
+        const int64_t hrow = (((int64_t)b * p.H + h) * 64 + p0 + r) * N;
+        const float* hin = p.h0 ? p.h0 + hrow : nullptr;
+        const float* hid = p.init_hpr ? p.init_hpr + ((int64_t)h * 64 + p0 + r) * N : nullptr;
 #pragma unroll
-    for (int k = 0; k < SPW; ++k) {
-        const int s = wave + 4 * k;
-        st_ok[k] = s < NST;
-        st_pt[k] = s / NTN;
-        st_nt[k] = s % NTN;
-    }
-    // state element (p, n) of this lane's register v in tile k sits at
-    // (p0 + 32 st_pt + 4 half + r_v, 32 st_nt + r) with r_v = 8 (v / 4) + v % 4:
-    // one row offset per tile plus compile-time offsets
-    f32x16_t hacc[SPW];
-    const int64_t hbase = ((int64_t)b * p.H + h) * 64 * N;
-    auto hoff = [&](int k) { return (int64_t)(p0 + st_pt[k] * 32 + 4 * half) * N + st_nt[k] * 32 + r; };
+        for (int nt = 0; nt < NTN; ++nt)
 #pragma unroll
-    for (int k = 0; k < SPW; ++k) {
-        const float* h0t = p.h0 ? p.h0 + hbase + hoff(k) : nullptr;
-        const float* hit = p.init_hpr ? p.init_hpr + (int64_t)h * 64 * N + hoff(k) : nullptr;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int rv = (8 * (v >> 2) + (v & 3)) * N;
-            float val = 0.f;
-            if (st_ok[k]) {
-                if (h0t) val = h0t[rv];
-                if (hit) val += hit[rv];
+            for (int q = 0; q < 4; ++q) {
+                const int n = 32 * nt + 8 * q + 4 * half;
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (hin) v = *(const float4*)(hin + n);
+                if (hid) {
+                    const float4 u = *(const float4*)(hid + n);
+                    v.x += u.x; v.y += u.y; v.z += u.z; v.w += u.w;
+                }
+                hacc[nt][4 * q] = v.x; hacc[nt][4 * q + 1] = v.y;
+                hacc[nt][4 * q + 2] = v.z; hacc[nt][4 * q + 3] = v.w;
             }
-            hacc[k][v] = val;
-        }
     }
-    // bf16 copy of the state: the A operand of h . C^T
-#pragma unroll
-    for (int k = 0; k < SPW; ++k)
-        if (st_ok[k])
-#pragma unroll
-            for (int v = 0; v < 16; ++v)
-                s_h[st_pt[k] * 32 + 8 * (v >> 2) + 4 * half + (v & 3)][st_nt[k] * 32 + r] =
-                    __builtin_bit_cast(bf16_t, (__bf16)hacc[k][v]);
 
-    const bf16_t* X = (const bf16_t*)p.x;
-    bf16_t* Y = (bf16_t*)p.y;
-    const bf16_t* xhead = X + (int64_t)b * p.x_sb + (int64_t)h * p.x_sh + p0;
+    const bf16_t* xhead = (const bf16_t*)p.x + (int64_t)b * p.x_sb + (int64_t)h * p.x_sh + p0;
     const float* dthead = p.dt + (int64_t)b * p.dt_sb + (int64_t)h * p.dt_sh;
-    bf16_t* yhead = Y + (int64_t)b * p.y_sb + (int64_t)h * p.y_sh + p0;
+    bf16_t* yhead = (bf16_t*)p.y + (int64_t)b * p.y_sb + (int64_t)h * p.y_sh + p0;
     const uint32_t xrow = (uint32_t)p.x_sl * 2u;
-    // x staging item m of this thread: time rows 2 (jpt + JPM m) + {0, 1}, headdim vector pv
-    const int jpt = threadIdx.x / PV, pvt = threadIdx.x % PV;
+    const int64_t grp_stride = (int64_t)p.G * NF * 512;       // bf16 elements per chunk step
+    const bf16_t* gfrag = frag + ((int64_t)b * p.nch * p.G + g) * NF * 512;  // chunk 0 of (b, g)
 
-    // register prefetch of the next chunk's x rows and dt; buffer loads past
-    // the sequence end read as zero
+    // direct-to-LDS loads of chunk cc's fragments f = wave + HPW k into buffer `buf`
+    auto stage = [&](int cc, int buf, int lane) {
+        const __amdgpu_buffer_rsrc_t rf = buf_rsrc(gfrag + (int64_t)cc * grp_stride, (uint32_t)NF * 1024u);
+#pragma unroll
+        for (int k = 0; k < FPW; ++k) {
+            const int f = wave + HPW * k;
+            if (FPW * HPW == NF || f < NF)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rf, (__attribute__((address_space(3))) void*)&s_frag[buf][f][0], 16, lane * 16u,
+                    (uint32_t)__builtin_amdgcn_readfirstlane(f * 1024), 0, 0);
+        }
+    };
+    // register prefetch of chunk cc's x rows (item m: rows 2 (lane/4 + 16 m) + {0, 1},
+    // headdim vector lane % 4) and dt (lane = position); loads past the end read zero
     uint4 xq[XPT][2];
-    float dtq = 0.f;
-    auto fetch = [&](int c) {
-        const uint32_t rows = (uint32_t)max(0, min(Q, p.L - c * Q));
-        const __amdgpu_buffer_rsrc_t rx = buf_rsrc(xhead + (int64_t)c * Q * p.x_sl, rows * xrow);
-        const uint32_t off0 = (uint32_t)(2 * jpt) * xrow + pvt * 16;
+    float dtq;
+    auto fetch = [&](int cc, int lane) {
+        const int jp = lane >> 2, pv = lane & 3;
+        const uint32_t rows = (uint32_t)max(0, min(Q, p.L - cc * Q));
+        const __amdgpu_buffer_rsrc_t rx = buf_rsrc(xhead + (int64_t)cc * Q * p.x_sl, rows * xrow);
+        const uint32_t off0 = (uint32_t)(2 * jp) * xrow + pv * 16;
 #pragma unroll
         for (int m = 0; m < XPT; ++m) {
-            if (XITEMS % 256 == 0 || (int)threadIdx.x + 256 * m < XITEMS) {
-                xq[m][0] = buf_ld16(rx, off0, (uint32_t)(2 * JPM * m) * xrow);
-                xq[m][1] = buf_ld16(rx, off0, (uint32_t)(2 * JPM * m + 1) * xrow);
-            }
+            xq[m][0] = buf_ld16(rx, off0, (uint32_t)(32 * m) * xrow);
+            xq[m][1] = buf_ld16(rx, off0, (uint32_t)(32 * m + 1) * xrow);
         }
         const __amdgpu_buffer_rsrc_t rd =
-            buf_rsrc(dthead + (int64_t)c * Q * p.dt_sl, rows * (uint32_t)p.dt_sl * 4u);
-        dtq = threadIdx.x < Q ? buf_ld4(rd, threadIdx.x * (uint32_t)p.dt_sl * 4u) : 0.f;
+            buf_rsrc(dthead + (int64_t)cc * Q * p.dt_sl, rows * (uint32_t)p.dt_sl * 4u);
+        dtq = lane < Q ? buf_ld4(rd, lane * (uint32_t)p.dt_sl * 4u) : 0.f;
     };
-    fetch(0);
-    // L2 warm-up of the next chunk's group operands: the H/G heads (x headdim
-    // splits) of a group share them and sit on one XCD, so each workgroup
-    // touches one slice of the group's lines, one dword per line
-    constexpr int FL = 512 * 2 / 128;           // 128-byte lines per fragment
-    constexpr int CB_LINES = FL * T * (T + 1);  // causal C.B^T fragments (row it: 2 it + 2 of them)
-    constexpr int FR_LINES = Q * N * 2 / 128;   // C (or B) fragments
-    constexpr int GRP_LINES = CB_LINES + 2 * FR_LINES;
-    const int nslice = (p.H / p.G) * splits;
-    const int slice = (h % (p.H / p.G)) * splits + ph;
-    const int pf_line = (int)(((int64_t)GRP_LINES * slice) / nslice) + threadIdx.x;
-    const bool pf_on = pf_line < (int)(((int64_t)GRP_LINES * (slice + 1)) / nslice);
-    int64_t pf_off = 0;  // byte offset of the line inside the group's block
-    if (pf_line < CB_LINES) {
-        int it = 0;
-        while (FL * (it + 1) * (it + 2) <= pf_line) ++it;
-        pf_off = ((int64_t)it * KS * FL + (pf_line - FL * it * (it + 1))) * 128;
-    } else if (pf_line < CB_LINES + FR_LINES) {
-        pf_off = (int64_t)(pf_line - CB_LINES) * 128;
-    } else {
-        pf_off = (int64_t)(pf_line - CB_LINES - FR_LINES) * 128;
-    }
-    const int pf_kind = pf_line < CB_LINES ? 0 : (pf_line < CB_LINES + FR_LINES ? 1 : 2);
+
+    stage(0, 0, lane0);
+    fetch(0, lane0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
     uint32_t pf = 0u, pf_sink = 0u;
 
-    static_assert(NK >= 4, "the C and B fragment rings are four deep");
     for (int c = 0; c < p.nch; ++c) {
-        pf_sink += pf;  // the previous chunk's warm-up load, long complete
-        // Group operands of this chunk.  `cr` carries the first four fragments
-        // of the wave's next phase, loaded one phase ahead: here those of its
-        // first tile's C (or, with no tile, of its state GEMM's B); then, from
-        // a tile's inter-chunk term, those of the following tile or of the
-        // state GEMM.  Fragment indices are clamped inside the operand.
-        const int64_t grp = ((int64_t)b * p.nch + c) * p.G + g;
-        const bf16_t* cfg = cf + grp * (int64_t)Q * N + lane * 8;
-        const bf16_t* btf = bfr + grp * (int64_t)Q * N + ((int64_t)st_nt[0] * KS * 64 + lane) * 8;
-        uint4 cr[4];
-        {
-            const bool has_tile = wave < T;
-            const bf16_t* nxt = has_tile ? cfg + (int64_t)wave * NK * 512 : btf;
-            const int lim = has_tile ? NK : KS;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) cr[k] = *(const uint4*)(nxt + min(k, lim - 1) * 512);
+        const int buf = c & 1;
+        const bf16_t* F0 = &s_frag[buf][0][0];
+        pf_sink += pf;
+        // the lane index as an opaque value: the many per-lane LDS addresses
+        // below are loop-invariant, and hoisted out of the chunk loop they
+        // would hold ~60 registers; recomputed here they cost a few adds
+        int lane = lane0;
+        asm volatile("" : "+v"(lane));
+        const int r = lane & 31, half = lane >> 5;
+        // ---- chunk c + 1's fragments into the other buffer (free since the
+        // last barrier)
+        if (c + 1 < p.nch) stage(c + 1, buf ^ 1, lane);
+        // ---- K1: dt and its cumsum (log2 units), one position per lane
+        const float cs2 = wave_incl_scan(dtq * A2);
+        if (lane < Q) {
+            s_cs[wave][lane] = cs2;
+            s_dt[wave][lane] = dtq;
         }
-        // ---- dt and the K1 cumsum (log2 units) of this chunk
-        const float dtv = dtq;  // dt of position threadIdx.x of this chunk
-        if (threadIdx.x < Q) s_dt[threadIdx.x] = dtv;
-        {
-            float v = wave_incl_scan(dtv * A2);
-            if (lane == 63) s_red[wave] = v;
-            __syncthreads();
+        float cse[T];  // block ends, wave-uniform
 #pragma unroll
-            for (int k = 0; k < 3; ++k)
-                if (k < wave) v += s_red[k];
-            if (threadIdx.x < Q) s_cs2[threadIdx.x] = v;
-        }
-        __syncthreads();
-        // ---- block-scaled x -> s_xg[p][j] (time-major), block decays -> s_F
+        for (int k = 0; k < T; ++k)
+            cse[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cs2), 32 * k + 31));
+        // ---- block-scaled x -> s_xg[wave][p][j] (time-major)
+        const int jp = lane >> 2, pv = lane & 3;
 #pragma unroll
         for (int m = 0; m < XPT; ++m) {
-            if (XITEMS % 256 == 0 || (int)threadIdx.x + 256 * m < XITEMS) {
-                const int pv = pvt, j0 = 2 * (jpt + JPM * m);
-                const float ce = s_cs2[j0 | 31];
-                const float g0 = s_dt[j0] * __builtin_amdgcn_exp2f(ce - s_cs2[j0]);
-                const float g1 = s_dt[j0 + 1] * __builtin_amdgcn_exp2f(ce - s_cs2[j0 + 1]);
-                const uint32_t a0[4] = {xq[m][0].x, xq[m][0].y, xq[m][0].z, xq[m][0].w};
-                const uint32_t a1[4] = {xq[m][1].x, xq[m][1].y, xq[m][1].z, xq[m][1].w};
+            const int j0 = 2 * (jp + 16 * m);
+            const float ce = cse[m];  // rows j0, j0 + 1 sit in block m
+            const float g0 = __shfl(dtq, j0, 64) * __builtin_amdgcn_exp2f(ce - __shfl(cs2, j0, 64));
+            const float g1 = __shfl(dtq, j0 + 1, 64) * __builtin_amdgcn_exp2f(ce - __shfl(cs2, j0 + 1, 64));
+            const uint32_t a0[4] = {xq[m][0].x, xq[m][0].y, xq[m][0].z, xq[m][0].w};
+            const uint32_t a1[4] = {xq[m][1].x, xq[m][1].y, xq[m][1].z, xq[m][1].w};
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    *(uint32_t*)&s_xg[pv * 8 + 2 * k][j0] =
-                        pack_bf16x2(__uint_as_float(a0[k] << 16) * g0, __uint_as_float(a1[k] << 16) * g1);
-                    *(uint32_t*)&s_xg[pv * 8 + 2 * k + 1][j0] =
-                        pack_bf16x2(__uint_as_float(a0[k] & 0xffff0000u) * g0,
-                                    __uint_as_float(a1[k] & 0xffff0000u) * g1);
-                }
+            for (int k = 0; k < 4; ++k) {
+                *(uint32_t*)&s_xg[wave][pv * 8 + 2 * k][j0] =
+                    pack_bf16x2(__uint_as_float(a0[k] << 16) * g0, __uint_as_float(a1[k] << 16) * g1);
+                *(uint32_t*)&s_xg[wave][pv * 8 + 2 * k + 1][j0] =
+                    pack_bf16x2(__uint_as_float(a0[k] & 0xffff0000u) * g0,
+                                __uint_as_float(a1[k] & 0xffff0000u) * g1);
             }
         }
-        if (threadIdx.x < T) {
-            const int k = threadIdx.x;
-            s_F[k] = __builtin_amdgcn_exp2f(s_cs2[32 * k + 31] - (k ? s_cs2[32 * k - 1] : 0.f));
+        // ---- chunk c + 1's x rows and dt into registers (they land during
+        // this chunk's MFMA work)
+        if (c + 1 < p.nch) fetch(c + 1, lane);
+        // L2 warm-up of chunk c + 2's fragments: the workgroups of a group
+        // share them and sit on one XCD; one dword per 128-byte line, spread
+        // over the workgroups of the group
+        if (MAMBA_SSD2_L2_WARM && c + 2 < p.nch) {
+            const int nslice = (hpg / HPW) * 2, slice = (hq % (hpg / HPW)) * 2 + ph;
+            const int line = threadIdx.x * nslice + slice;  // 128-byte lines of the NF KB block
+            if (line < NF * 8)
+                pf = *(const uint32_t*)((const char*)(gfrag + (int64_t)(c + 2) * grp_stride) + line * 128);
         }
-        __syncthreads();
 
-        // ---- K2 + K5: y^T for the i-tiles this wave owns.  No global access
-        // of a tile sits under a branch except on the rare raw-x paths: the
-        // C.B^T ring is refilled through a buffer clipped at the tile's last
-        // strictly-lower fragment (reads past it return zero without a memory
-        // access) and only the arithmetic of a block is skipped, on a scalar
-        // condition.  The waits on the rings are therefore exact counts.
         const uint32_t rows_c = (uint32_t)min(Q, p.L - c * Q);
-        const __amdgpu_buffer_rsrc_t ry = buf_rsrc(yhead + (int64_t)c * Q * p.y_sl, rows_c * (uint32_t)p.y_sl * 2u);
-        const __amdgpu_buffer_rsrc_t rxc = buf_rsrc(xhead + (int64_t)c * Q * p.x_sl, rows_c * xrow);
-#pragma unroll 1
-        for (int q = 0; q < 2; ++q) {
-            const int it = q ? 7 - wave : wave;  // the snake pair {w, 7 - w}
-            if (it >= T || (q && it == wave)) continue;
-            const int il = it * 32 + r;  // this lane's output time (B-operand column)
-            // issue the first global loads of this tile before the first wait
-            // (its first C fragments are already in `cr`): the diagonal block
-            // and two blocks of strictly-lower C.B^T fragments
-            const bf16_t* ctile = cfg + (int64_t)it * NK * 512;
-            const int it2 = 7 - wave;  // the wave's next tile, if any
-            const bool next_tile = q == 0 && it2 < T && it2 != wave;
-            const bf16_t* nxt = next_tile ? cfg + (int64_t)it2 * NK * 512 : btf;
-            const int lim = next_tile ? NK : KS;
-            const bf16_t* cbrow = cbf + grp * Q * Q + (int64_t)it * KS * 512;
-            const uint32_t loff = lane * 16u;
-            const uint4 dg0 = *(const uint4*)(cbrow + (2 * it) * 512 + lane * 8);
-            const uint4 dg1 = *(const uint4*)(cbrow + (2 * it + 1) * 512 + lane * 8);
-            const __amdgpu_buffer_rsrc_t rcb = buf_rsrc(cbrow, (uint32_t)(2 * it) * 1024u);
-            uint4 ring[4];
+        // ---- K2 + K5: y^T for the chunk's row tiles.  Inter-chunk term
+        // h_in . C_i^T first, for every tile, with A from the state registers
+        f32x16_t yacc[T];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) ring[k] = buf_ld16(rcb, k * 1024u + loff);
-            f32x16_t yacc[PT];
+        for (int it = 0; it < T; ++it) yacc[it] = zero16();
 #pragma unroll
-            for (int pt = 0; pt < PT; ++pt) yacc[pt] = zero16();
-            // inter-chunk term h_in . C_i^T with raw C rows as the B operand
+        for (int kn = 0; kn < NK; ++kn) {
+            const int nt = kn >> 1, q = kn & 1;
+            float hv[8];
 #pragma unroll
-            for (int ks = 0; ks < NK; ++ks) {
-                const bf16x8_t bop = as_bf16x8(cr[ks % 4]);
-                if (ks + 4 < NK)
-                    cr[ks % 4] = *(const uint4*)(ctile + (ks + 4) * 512);
-                else  // the slot is free: the next phase's fragment ks + 4 - NK
-                    cr[ks % 4] = *(const uint4*)(nxt + min(ks + 4 - NK, lim - 1) * 512);
+            for (int e = 0; e < 8; ++e) hv[e] = hacc[nt][8 * q + e];
+            const bf16x8_t a = pack8(hv);
 #pragma unroll
-                for (int pt = 0; pt < PT; ++pt) {
-                    const bf16x8_t a = *(const bf16x8_t*)&s_h[pt * 32 + r][ks * 16 + 8 * half];
-                    yacc[pt] = mfma32x32x16(a, bop, yacc[pt]);
-                }
+            for (int it = 0; it < T; ++it) {
+                const bf16x8_t bop = *(const bf16x8_t*)(F0 + ((FL::C0 + it * NK + kn) * 64 + lane) * 8);
+                yacc[it] = mfma32x32x16(a, bop, yacc[it]);
             }
-            // Horner over the strictly-lower blocks: acc <- acc F_jt + S_jt;
-            // block jt's fragments sit in ring slots 2 (jt % 2), refilled two
-            // blocks ahead.  A block's LDS reads are issued before its scaling,
-            // which covers their latency.
+        }
 #pragma unroll
-            for (int jt = 0; jt < T - 1; ++jt) {
-                if (jt < it) {
-                    const float F = s_F[jt];
-                    bf16x8_t a[2][PT];
+        for (int it = 0; it < T; ++it) {
+            const int il = it * 32 + r;  // this lane's output time (B-operand column)
+            f32x16_t acc = yacc[it];
+            // Horner over the strictly-lower blocks: acc <- acc F_jt + S_jt
 #pragma unroll
-                    for (int kk = 0; kk < 2; ++kk)
+            for (int jt = 0; jt < it; ++jt) {
+                const float F = __builtin_amdgcn_exp2f(cse[jt] - (jt ? cse[jt - 1] : 0.f));
 #pragma unroll
-                        for (int pt = 0; pt < PT; ++pt)
-                            a[kk][pt] = *(const bf16x8_t*)&s_xg[pt * 32 + r][(2 * jt + kk) * 16 + 8 * half];
-#pragma unroll
-                    for (int pt = 0; pt < PT; ++pt)
-#pragma unroll
-                        for (int v = 0; v < 16; ++v) yacc[pt][v] *= F;
-#pragma unroll
-                    for (int kk = 0; kk < 2; ++kk) {
-                        const bf16x8_t bop = as_bf16x8(ring[(2 * jt + kk) % 4]);
-#pragma unroll
-                        for (int pt = 0; pt < PT; ++pt) yacc[pt] = mfma32x32x16(a[kk][pt], bop, yacc[pt]);
-                    }
-                }
+                for (int v = 0; v < 16; ++v) acc[v] *= F;
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk) {
                     const int ks = 2 * jt + kk;
-                    if (ks + 4 < KS) ring[ks % 4] = buf_ld16(rcb, (ks + 4) * 1024u + loff);
+                    const bf16x8_t a = *(const bf16x8_t*)&s_xg[wave][r][ks * 16 + 8 * half];
+                    const bf16x8_t bop = *(const bf16x8_t*)(F0 + ((it * (it + 1) + ks) * 64 + lane) * 8);
+                    acc = mfma32x32x16(a, bop, acc);
                 }
             }
-            // diagonal block: the prep stored its upper triangle as 0
-            const float cs2_i = s_cs2[il];
-            const float cse_prev = it ? s_cs2[it * 32 - 1] : 0.f;
-            const float cse = s_cs2[it * 32 + 31];
-            const float span = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(cse_prev - cse)));
-            if (span <= kSteep) {
-                const float F = s_F[it];
-                bf16x8_t a[2][PT];
+            // diagonal block (the prep stored its upper triangle as 0)
+            const float cs2_i = s_cs[wave][il];
+            const float cse_prev = it ? cse[it - 1] : 0.f;
+            const float cs_e = cse[it];
+            const uint4 dg0 = *(const uint4*)(F0 + ((it * (it + 1) + 2 * it) * 64 + lane) * 8);
+            const uint4 dg1 = *(const uint4*)(F0 + ((it * (it + 1) + 2 * it + 1) * 64 + lane) * 8);
+            if (cse_prev - cs_e <= kSteep) {
+                const float F = __builtin_amdgcn_exp2f(cs_e - cse_prev);
 #pragma unroll
-                for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-                    for (int pt = 0; pt < PT; ++pt)
-                        a[kk][pt] = *(const bf16x8_t*)&s_xg[pt * 32 + r][it * 32 + kk * 16 + 8 * half];
-#pragma unroll
-                for (int pt = 0; pt < PT; ++pt)
-#pragma unroll
-                    for (int v = 0; v < 16; ++v) yacc[pt][v] *= F;
+                for (int v = 0; v < 16; ++v) acc[v] *= F;
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk) {
-                    const bf16x8_t bop = as_bf16x8(kk ? dg1 : dg0);
-#pragma unroll
-                    for (int pt = 0; pt < PT; ++pt) yacc[pt] = mfma32x32x16(a[kk][pt], bop, yacc[pt]);
+                    const bf16x8_t a = *(const bf16x8_t*)&s_xg[wave][r][it * 32 + kk * 16 + 8 * half];
+                    acc = mfma32x32x16(a, as_bf16x8(kk ? dg1 : dg0), acc);
                 }
                 // y_i = exp(cs_i - cs_e) (acc + D xg_i / g_i) with exp(cs_i - cs_e) / g_i = 1 / dt_i
-                const float colf = __builtin_amdgcn_exp2f(cs2_i - cse);
-                const float dti = s_dt[il];
-                const float gi = dti * __builtin_amdgcn_exp2f(cse - cs2_i);
+                const float colf = __builtin_amdgcn_exp2f(cs2_i - cs_e);
+                const float dti = s_dt[wave][il];
+                const float gi = dti * __builtin_amdgcn_exp2f(cs_e - cs2_i);
                 if (__all(gi >= kTinyG)) {
-                    const float dinv = Dh / dti;
+                    const float dinv = Dh * __builtin_amdgcn_rcpf(dti);  // 1 ulp
 #pragma unroll
-                    for (int pt = 0; pt < PT; ++pt)
-#pragma unroll
-                        for (int v = 0; v < 16; ++v) {
-                            const float xv = __uint_as_float(
-                                (uint32_t)s_xg[pt * 32 + 8 * (v >> 2) + 4 * half + (v & 3)][il] << 16);
-                            yacc[pt][v] = (yacc[pt][v] + dinv * xv) * colf;
-                        }
+                    for (int v = 0; v < 16; ++v) {
+                        const float xv = __uint_as_float(
+                            (uint32_t)s_xg[wave][8 * (v >> 2) + 4 * half + (v & 3)][il] << 16);
+                        acc[v] = (acc[v] + dinv * xv) * colf;
+                    }
                 } else {
                     // raw x of the lane's output row, four headdim values per load
+                    const __amdgpu_buffer_rsrc_t rxc = buf_rsrc(xhead + (int64_t)c * Q * p.x_sl, rows_c * xrow);
 #pragma unroll
-                    for (int pt = 0; pt < PT; ++pt)
+                    for (int gq = 0; gq < 4; ++gq) {
+                        const uint2 xr = buf_ld8(rxc, ((uint32_t)il * (uint32_t)p.x_sl + 8 * gq + 4 * half) * 2u);
+                        const float xv[4] = {__uint_as_float(xr.x << 16), __uint_as_float(xr.x & 0xffff0000u),
+                                             __uint_as_float(xr.y << 16), __uint_as_float(xr.y & 0xffff0000u)};
 #pragma unroll
-                        for (int gq = 0; gq < 4; ++gq) {
-                            const uint2 xr =
-                                buf_ld8(rxc, ((uint32_t)il * (uint32_t)p.x_sl + pt * 32 + 8 * gq + 4 * half) * 2u);
-                            const float xv[4] = {__uint_as_float(xr.x << 16), __uint_as_float(xr.x & 0xffff0000u),
-                                                 __uint_as_float(xr.y << 16), __uint_as_float(xr.y & 0xffff0000u)};
-#pragma unroll
-                            for (int u = 0; u < 4; ++u)
-                                yacc[pt][4 * gq + u] = yacc[pt][4 * gq + u] * colf + Dh * xv[u];
-                        }
+                        for (int u = 0; u < 4; ++u) acc[4 * gq + u] = acc[4 * gq + u] * colf + Dh * xv[u];
+                    }
                 }
             } else {
                 // steep block: bring acc to position i (factor <= 1), then the
                 // exact weights dt_j exp(cs_i - cs_j) (+ D on the diagonal) on raw x
+                const __amdgpu_buffer_rsrc_t rxc = buf_rsrc(xhead + (int64_t)c * Q * p.x_sl, rows_c * xrow);
                 const float sc = __builtin_amdgcn_exp2f(cs2_i - cse_prev);
 #pragma unroll
-                for (int pt = 0; pt < PT; ++pt)
-#pragma unroll
-                    for (int v = 0; v < 16; ++v) yacc[pt][v] *= sc;
+                for (int v = 0; v < 16; ++v) acc[v] *= sc;
+                // the lane's row as an opaque value: its compares below are
+                // loop-invariant, and hoisted out of the chunk loop they would
+                // hold scalar registers for this rare path
+                int ilo = il;
+                asm volatile("" : "+v"(ilo));
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk) {
                     const int j0 = it * 32 + kk * 16 + 8 * half;
@@ -526,94 +462,67 @@ __global__ __launch_bounds__(256, 3) void ssd2_scan_mfma(Ssd2Params p, const bf1
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         const int j = j0 + e;
-                        const float val = cbv[e] * s_dt[j] * __builtin_amdgcn_exp2f(cs2_i - s_cs2[j]);
-                        m[e] = (j < il) ? val : ((j == il) ? val + Dh : 0.f);
+                        const float val = cbv[e] * s_dt[wave][j] * __builtin_amdgcn_exp2f(cs2_i - s_cs[wave][j]);
+                        m[e] = (j < ilo) ? val : ((j == ilo) ? val + Dh : 0.f);
                     }
-                    const bf16x8_t bop = pack8(m);
+                    // A operand x^T[p][j0 .. j0 + 7] for p = r, from the raw rows
+                    uint32_t xw[4];
 #pragma unroll
-                    for (int pt = 0; pt < PT; ++pt) {
-                        // A operand x^T[p][j0 .. j0 + 7] for p = pt * 32 + r, from the raw rows
-                        uint32_t xw[4];
-#pragma unroll
-                        for (int e2 = 0; e2 < 4; ++e2) {
-                            const uint32_t lo = buf_ld2(rxc, ((uint32_t)(j0 + 2 * e2) * (uint32_t)p.x_sl + pt * 32 + r) * 2u);
-                            const uint32_t hi =
-                                buf_ld2(rxc, ((uint32_t)(j0 + 2 * e2 + 1) * (uint32_t)p.x_sl + pt * 32 + r) * 2u);
-                            xw[e2] = lo | (hi << 16);
-                        }
-                        const bf16x8_t a = as_bf16x8(make_uint4(xw[0], xw[1], xw[2], xw[3]));
-                        yacc[pt] = mfma32x32x16(a, bop, yacc[pt]);
+                    for (int e2 = 0; e2 < 4; ++e2) {
+                        const uint32_t lo = buf_ld2(rxc, ((uint32_t)(j0 + 2 * e2) * (uint32_t)p.x_sl + r) * 2u);
+                        const uint32_t hi = buf_ld2(rxc, ((uint32_t)(j0 + 2 * e2 + 1) * (uint32_t)p.x_sl + r) * 2u);
+                        xw[e2] = lo | (hi << 16);
                     }
+                    acc = mfma32x32x16(as_bf16x8(make_uint4(xw[0], xw[1], xw[2], xw[3])), pack8(m), acc);
                 }
             }
             // store: the lane holds y[il][4 consecutive p] per group of 4
             // registers; rows past the sequence end are dropped by the buffer
+            const __amdgpu_buffer_rsrc_t ry = buf_rsrc(yhead + (int64_t)c * Q * p.y_sl, rows_c * (uint32_t)p.y_sl * 2u);
 #pragma unroll
-            for (int pt = 0; pt < PT; ++pt)
-#pragma unroll
-                for (int gq = 0; gq < 4; ++gq)
-                    buf_st8(ry, ((uint32_t)il * (uint32_t)p.y_sl + pt * 32 + 8 * gq + 4 * half) * 2u,
-                            make_uint2(pack_bf16x2(yacc[pt][4 * gq], yacc[pt][4 * gq + 1]),
-                                       pack_bf16x2(yacc[pt][4 * gq + 2], yacc[pt][4 * gq + 3])));
+            for (int gq = 0; gq < 4; ++gq)
+                buf_st8(ry, ((uint32_t)il * (uint32_t)p.y_sl + 8 * gq + 4 * half) * 2u,
+                        make_uint2(pack_bf16x2(acc[4 * gq], acc[4 * gq + 1]),
+                                   pack_bf16x2(acc[4 * gq + 2], acc[4 * gq + 3])));
         }
 
-        // ---- prefetch the next chunk's x / dt (lands during the state GEMM)
-        fetch(c + 1);  // past the last chunk every load reads zero
-
-        // ---- K3 + K4: h <- h F_k + xg_k^T B_k over the blocks, B fragments in a ring
-        if (NST >= 4 || wave < NST) {  // every state tile of this wave is valid (SPW > 1 iff NST >= 8)
-            // all state tiles of a wave share one n tile (st_nt[0]) when SPW > 1
-            constexpr int BD = 4;  // B fragment ring depth (two blocks), primed in `cr`
-            uint4 bring[BD];
+        // ---- K3 + K4: h^T <- h^T F_k + B_k^T . xg_k over the blocks
 #pragma unroll
-            for (int k = 0; k < BD; ++k) bring[k] = cr[k];
+        for (int jt = 0; jt < T; ++jt) {
+            const float F = __builtin_amdgcn_exp2f(cse[jt] - (jt ? cse[jt - 1] : 0.f));
 #pragma unroll
-            for (int jt = 0; jt < T; ++jt) {
-                const float F = s_F[jt];
+            for (int nt = 0; nt < NTN; ++nt)
 #pragma unroll
-                for (int k = 0; k < SPW; ++k)
+                for (int v = 0; v < 16; ++v) hacc[nt][v] *= F;
 #pragma unroll
-                    for (int v = 0; v < 16; ++v) hacc[k][v] *= F;
+            for (int kk = 0; kk < 2; ++kk) {
+                const int ks = 2 * jt + kk;
+                const bf16x8_t bx = *(const bf16x8_t*)&s_xg[wave][r][ks * 16 + 8 * half];
 #pragma unroll
-                for (int kk = 0; kk < 2; ++kk) {
-                    const int ks = 2 * jt + kk;
-                    const bf16x8_t bop = as_bf16x8(bring[ks % BD]);
-                    if (ks + BD < KS) bring[ks % BD] = *(const uint4*)(btf + (ks + BD) * 512);
-#pragma unroll
-                    for (int k = 0; k < SPW; ++k) {
-                        const bf16x8_t a = *(const bf16x8_t*)&s_xg[st_pt[k] * 32 + r][ks * 16 + 8 * half];
-                        hacc[k] = mfma32x32x16(a, bop, hacc[k]);
-                    }
+                for (int nt = 0; nt < NTN; ++nt) {
+                    const bf16x8_t a = *(const bf16x8_t*)(F0 + ((FL::B0 + nt * KS + ks) * 64 + lane) * 8);
+                    hacc[nt] = mfma32x32x16(a, bx, hacc[nt]);
                 }
             }
         }
-        // ---- warm L2 with the next chunk's group operands while the WG syncs and scans
-        if (MAMBA_SSD2_L2_WARM) {  // one unconditional load per thread
-            const int64_t g1 = grp + p.G;  // (b, c + 1, g)
-            const bf16_t* blk = pf_kind == 0 ? cbf + g1 * Q * Q
-                              : pf_kind == 1 ? cf + g1 * (int64_t)Q * N
-                                             : bfr + g1 * (int64_t)Q * N;
-            const bool warm = c + 1 < p.nch && pf_on;  // else re-touch a line of this chunk
-            pf = *(const uint32_t*)(warm ? (const char*)blk + pf_off : (const char*)(cbf + grp * Q * Q));
-        }
-        __syncthreads();  // all reads of s_h / s_xg / s_cs2 / s_dt / s_F done
-#pragma unroll
-        for (int k = 0; k < SPW; ++k)
-            if (st_ok[k])
-#pragma unroll
-                for (int v = 0; v < 16; ++v)
-                    s_h[st_pt[k] * 32 + 8 * (v >> 2) + 4 * half + (v & 3)][st_nt[k] * 32 + r] =
-                        __builtin_bit_cast(bf16_t, (__bf16)hacc[k][v]);
+        // ---- this wave's loads done (chunk c + 1's fragments and x), then
+        // the chunk's barrier: every wave's fragments for c + 1 have landed and
+        // every wave is done with chunk c's buffer
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
     }
     // keeps the L2 warm-up loads alive (the condition never holds: L >= 1)
     if (p.L < 0 && pf_sink == 0x9e3779b9u) p.hT[0] = 0.f;
-    // final state (f32)
+    // final state (f32): h[p = p0 + r][n] from h^T
+    {
+        const int r = lane0 & 31, half = lane0 >> 5;
+        float* hTr = p.hT + (((int64_t)b * p.H + h) * 64 + p0 + r) * N;
 #pragma unroll
-    for (int k = 0; k < SPW; ++k) {
-        if (!st_ok[k]) continue;
-        float* hTt = p.hT + hbase + hoff(k);
+        for (int nt = 0; nt < NTN; ++nt)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) hTt[(8 * (v >> 2) + (v & 3)) * N] = hacc[k][v];
+            for (int q = 0; q < 4; ++q)
+                *(float4*)(hTr + 32 * nt + 8 * q + 4 * half) =
+                    make_float4(hacc[nt][4 * q], hacc[nt][4 * q + 1], hacc[nt][4 * q + 2], hacc[nt][4 * q + 3]);
     }
 }
 
@@ -636,68 +545,88 @@ bool ssd2_mfma_supported(const Ssd2Params& p) {
     return true;
 }
 
-// workspace: cbf (Q*Q), cf (Q*N) and bf (Q*N), all bf16, per (batch, chunk, group)
-static size_t cbf_bytes(const Ssd2Params& p) {
-    return align_up((size_t)p.nb * p.nch * p.G * p.Q * p.Q * sizeof(bf16_t), 256);
-}
-static size_t frag_bytes(const Ssd2Params& p) {
-    return align_up((size_t)p.nb * p.nch * p.G * p.N * p.Q * sizeof(bf16_t), 256);
+// The MFMA path chunks at min(chunk_len, 64) positions, a chunk's positions
+// being a wave's lanes: the chunked form is exact for any chunk length, so
+// only rounding differs.
+constexpr int kFastQ = 64;
+
+static Ssd2Params fast_params(const Ssd2Params& p) {
+    Ssd2Params q = p;
+    q.Q = p.Q < kFastQ ? p.Q : kFastQ;
+    q.nch = (p.L + q.Q - 1) / q.Q;
+    return q;
 }
 
-size_t ssd2_mfma_workspace(const Ssd2Params& p) {
-    return cbf_bytes(p) + 2 * frag_bytes(p);
+static size_t frag_count(const Ssd2Params& p) {
+    const int T = p.Q / 32, NK = p.N / 16, KS = p.Q / 16, NTN = p.N / 32;
+    return (size_t)(T * (T + 1) + T * NK + NTN * KS);
 }
 
-// Headdim split.  PT = 1 (two workgroups per head, one per 32-wide headdim
-// half) measured faster than PT = 2 at every shape tried on MI355X: at the
-// 2.7B-layer shape 460 us against 535 us, both at three workgroups per CU;
-// PT = 2 needs the whole register budget and spills.  PT = 2 stays available
-// as MAMBA_SSD2_PSPLIT=0 (read on every call; 1 forces PT = 1).
-template <int N, int Q>
-static int choose_pt(const Ssd2Params&) {
-    const char* e = getenv("MAMBA_SSD2_PSPLIT");
-    return (e && atoi(e) == 0) ? 2 : 1;
+size_t ssd2_mfma_workspace(const Ssd2Params& p0) {
+    const Ssd2Params p = fast_params(p0);
+    return align_up((size_t)p.nb * p.nch * p.G * frag_count(p) * 1024, 256);
+}
+
+// Heads per workgroup (waves per workgroup): one of 5, 4, 2, 1 dividing the
+// heads of a group.  The scan kernel's LDS (two chunks of group fragments)
+// allows one workgroup per CU, so a launch of nwg workgroups takes
+// ceil(nwg / 256) rounds on MI355X's 256 CUs, each as long as the busiest
+// SIMD's ceil(HPW / 4) waves.  Ties go to the larger set, which stages each
+// fragment for more heads.  MAMBA_SSD2_HPW (read on every call) forces a
+// valid choice.
+static int choose_hpw(const Ssd2Params& p) {
+    const int hpg = p.H / p.G;
+    const char* e = getenv("MAMBA_SSD2_HPW");
+    if (e) {
+        const int v = atoi(e);
+        if ((v == 1 || v == 2 || v == 4 || v == 5) && hpg % v == 0) return v;
+    }
+    constexpr int kCUs = 256;
+    int best = 1;
+    int64_t best_cost = INT64_MAX;
+    for (int hpw : {5, 4, 2, 1}) {
+        if (hpg % hpw != 0) continue;
+        const int64_t nwg = (int64_t)p.nb * (p.H / hpw) * 2;
+        const int64_t cost = (nwg + kCUs - 1) / kCUs * ((hpw + 3) / 4);
+        if (cost < best_cost) {
+            best_cost = cost;
+            best = hpw;
+        }
+    }
+    return best;
+}
+
+template <int N, int Q, int HPW>
+static void launch_scan(const Ssd2Params& p, const bf16_t* frag, hipStream_t stream) {
+    const int nwg = p.nb * (p.H / HPW) * 2;
+    hipLaunchKernelGGL((ssd2_scan_wu<N, Q, HPW>), dim3(nwg), dim3(64 * HPW), 0, stream, p, frag);
 }
 
 template <int N, int Q>
 static int launch_q(const Ssd2Params& p, void* ws, hipStream_t stream, hipEvent_t ev0, hipEvent_t ev1) {
-    bf16_t* cbf = (bf16_t*)ws;
-    bf16_t* cf = (bf16_t*)((char*)ws + cbf_bytes(p));
-    bf16_t* bfr = (bf16_t*)((char*)ws + cbf_bytes(p) + frag_bytes(p));
+    bf16_t* frag = (bf16_t*)ws;
     const int S = 4;  // prep workgroups per (batch, chunk, group)
-    hipLaunchKernelGGL((ssd2_prep_mfma<N, Q>), dim3(S, p.nch * p.G, p.nb), dim3(256), 0, stream, p, cbf,
-                       cf, bfr);
+    hipLaunchKernelGGL((ssd2_prep_pack<N, Q>), dim3(S, p.nch * p.G, p.nb), dim3(256), 0, stream, p, frag);
     MAMBA_CHECK_LAUNCH();
     if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, stream));
-    if (choose_pt<N, Q>(p) == 2) {
-        hipLaunchKernelGGL((ssd2_scan_mfma<N, Q, 2>), dim3(p.nb * p.H), dim3(256), 0, stream, p,
-                           (const bf16_t*)cbf, (const bf16_t*)cf, (const bf16_t*)bfr);
-    } else {
-        hipLaunchKernelGGL((ssd2_scan_mfma<N, Q, 1>), dim3(p.nb * p.H * 2), dim3(256), 0, stream, p,
-                           (const bf16_t*)cbf, (const bf16_t*)cf, (const bf16_t*)bfr);
+    switch (choose_hpw(p)) {
+        case 5: launch_scan<N, Q, 5>(p, frag, stream); break;
+        case 4: launch_scan<N, Q, 4>(p, frag, stream); break;
+        case 2: launch_scan<N, Q, 2>(p, frag, stream); break;
+        default: launch_scan<N, Q, 1>(p, frag, stream); break;
     }
     MAMBA_CHECK_LAUNCH();
     if (ev1) MAMBA_CHECK_HIP(hipEventRecord(ev1, stream));
     return MAMBA_OK;
 }
 
-template <int N>
-static int launch_n(const Ssd2Params& p, void* ws, hipStream_t stream, hipEvent_t ev0, hipEvent_t ev1) {
-    switch (p.Q) {
-        case 32: return launch_q<N, 32>(p, ws, stream, ev0, ev1);
-        case 64: return launch_q<N, 64>(p, ws, stream, ev0, ev1);
-        case 96: return launch_q<N, 96>(p, ws, stream, ev0, ev1);
-        case 128: return launch_q<N, 128>(p, ws, stream, ev0, ev1);
-        case 160: return launch_q<N, 160>(p, ws, stream, ev0, ev1);
-        case 192: return launch_q<N, 192>(p, ws, stream, ev0, ev1);
-        case 224: return launch_q<N, 224>(p, ws, stream, ev0, ev1);
-        default: return launch_q<N, 256>(p, ws, stream, ev0, ev1);
-    }
+int ssd2_mfma_launch(const Ssd2Params& p0, void* ws, hipStream_t stream, hipEvent_t ev0, hipEvent_t ev1) {
+    const Ssd2Params p = fast_params(p0);
+    if (p.N == 64)
+        return p.Q == 32 ? launch_q<64, 32>(p, ws, stream, ev0, ev1) : launch_q<64, 64>(p, ws, stream, ev0, ev1);
+    return p.Q == 32 ? launch_q<128, 32>(p, ws, stream, ev0, ev1) : launch_q<128, 64>(p, ws, stream, ev0, ev1);
 }
 
-int ssd2_mfma_launch(const Ssd2Params& p, void* ws, hipStream_t stream, hipEvent_t ev0, hipEvent_t ev1) {
-    if (p.N == 64) return launch_n<64>(p, ws, stream, ev0, ev1);
-    return launch_n<128>(p, ws, stream, ev0, ev1);
-}
+int ssd2_mfma_hpw(const Ssd2Params& p) { return choose_hpw(fast_params(p)); }
 
 }  // namespace mamba

@@ -133,9 +133,15 @@ FAST_CASES = [
     (2, 1000, 4, 64, 2, 128, 256),   # ragged tail, 2 groups
     (2, 333, 6, 64, 3, 64, 64),      # dstate 64, ragged
     (1, 77, 2, 64, 1, 128, 32),      # smallest chunk
-    (1, 512, 4, 64, 1, 64, 160),     # 5 row tiles per chunk
-    (3, 256, 80, 64, 1, 128, 256),   # all 80 heads of config 1, one chunk
+    (1, 512, 4, 64, 1, 64, 160),     # chunk 160 (the kernel chunks at 128)
+    (3, 256, 80, 64, 1, 128, 256),   # all 80 heads of config 1
+    (2, 700, 10, 64, 1, 128, 96),    # 10 heads: sets of 5, eight chunks of 96, ragged
+    (1, 450, 20, 64, 2, 64, 128),    # dstate 64 with sets of 5 per group
 ]
+
+
+def _hpw_ok(h, g, hpw):
+    return (h // g) % hpw == 0
 
 
 def _to_dev(inp, dtype="bf16"):
@@ -150,13 +156,17 @@ def _to_dev(inp, dtype="bf16"):
         h0=None if inp["h0"] is None else torch.from_numpy(inp["h0"]).to(dev))
 
 
-@pytest.mark.parametrize("psplit", ["0", "1"])
+@pytest.mark.parametrize("hpw", [1, 2, 4, 5])
 @pytest.mark.parametrize("case", FAST_CASES)
-def test_ssd2_mfma_bf16(case, psplit, monkeypatch):
+def test_ssd2_mfma_bf16(case, hpw, monkeypatch):
+    """The MFMA path at every head-set size it can run a shape with
+    (MAMBA_SSD2_HPW forces the choice)."""
     import torch
     import mamba_hip
-    monkeypatch.setenv("MAMBA_SSD2_PSPLIT", psplit)
     b, l, h, p, g, n, q = case
+    if not _hpw_ok(h, g, hpw):
+        pytest.skip(f"{h // g} heads per group do not split into sets of {hpw}")
+    monkeypatch.setenv("MAMBA_SSD2_HPW", str(hpw))
     inp = ssd2_inputs(seed=100 + sum(case), b=b, l=l, h=h, p=p, g=g, n=n, h0=True)
     t = _to_dev(inp)
     assert mamba_hip.ssd2_fast_path(t["x"], t["dt"], t["A"], t["B"], t["C"], chunk_len=q)
