@@ -223,10 +223,15 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
     constexpr float kSteep = 64.f;            // log2 of the largest block decay factored
     constexpr float kTinyG = 0x1p-100f;       // smallest g_i for D x from xg
     static_assert(Q == 32 || Q == 64, "a chunk's positions are the wave's lanes");
-    __shared__ __align__(16) bf16_t s_frag[2][NF][512];  // the group's fragments, two chunks
+    // the group's fragments of two chunks, as two arrays: the reads of one and
+    // the direct-to-LDS loads into the other are then provably disjoint, so no
+    // wait for those loads is placed before the reads
+    __shared__ __align__(16) bf16_t s_fragA[NF][512];
+    __shared__ __align__(16) bf16_t s_fragB[NF][512];
     __shared__ __align__(16) bf16_t s_xg[HPW][32][XP];   // per wave: xg^T [p][j]
     __shared__ __align__(16) float s_cs[HPW][Q];         // per wave: cumsum (log2 units)
     __shared__ __align__(16) float s_dt[HPW][Q];         // per wave: dt
+    __shared__ __align__(16) bf16_t s_yt[HPW][T][32][40];  // per wave: a chunk's output tiles, row-major
 
     const int wave = wave_id(), lane0 = threadIdx.x & 63;
     // XCD-aware work mapping: consecutive workgroups (same batch row, sharing
@@ -273,15 +278,15 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
     const int64_t grp_stride = (int64_t)p.G * NF * 512;       // bf16 elements per chunk step
     const bf16_t* gfrag = frag + ((int64_t)b * p.nch * p.G + g) * NF * 512;  // chunk 0 of (b, g)
 
-    // direct-to-LDS loads of chunk cc's fragments f = wave + HPW k into buffer `buf`
-    auto stage = [&](int cc, int buf, int lane) {
+    // direct-to-LDS loads of chunk cc's fragments f = wave + HPW k into `dst`
+    auto stage = [&](int cc, bf16_t (&dst)[NF][512], int lane) __attribute__((always_inline)) {
         const __amdgpu_buffer_rsrc_t rf = buf_rsrc(gfrag + (int64_t)cc * grp_stride, (uint32_t)NF * 1024u);
 #pragma unroll
         for (int k = 0; k < FPW; ++k) {
             const int f = wave + HPW * k;
             if (FPW * HPW == NF || f < NF)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    rf, (__attribute__((address_space(3))) void*)&s_frag[buf][f][0], 16, lane * 16u,
+                    rf, (__attribute__((address_space(3))) void*)&dst[f][0], 16, lane * 16u,
                     (uint32_t)__builtin_amdgcn_readfirstlane(f * 1024), 0, 0);
         }
     };
@@ -304,15 +309,34 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
         dtq = lane < Q ? buf_ld4(rd, lane * (uint32_t)p.dt_sl * 4u) : 0.f;
     };
 
-    stage(0, 0, lane0);
+    // chunk cc's output tiles from the wave's LDS scratch: four lanes cover a
+    // row's 64 bytes, a store instruction 16 whole rows (storing straight from
+    // the MFMA layout, every instruction would touch 32 rows).  Rows past the
+    // sequence end are dropped by the buffer.
+    auto store_tiles = [&](int cc, int lane) {
+        const uint32_t rows = (uint32_t)min(Q, p.L - cc * Q);
+        const __amdgpu_buffer_rsrc_t ry = buf_rsrc(yhead + (int64_t)cc * Q * p.y_sl, rows * (uint32_t)p.y_sl * 2u);
+#pragma unroll
+        for (int it = 0; it < T; ++it)
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const int row = (lane >> 2) + 16 * t, pc = (lane & 3) * 8;
+                const uint4 v = *(const uint4*)&s_yt[wave][it][row][pc];
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    __builtin_bit_cast(decltype(__builtin_amdgcn_raw_buffer_load_b128(ry, 0, 0, 0)), v), ry,
+                    ((uint32_t)(it * 32 + row) * (uint32_t)p.y_sl + pc) * 2u, 0, 0);
+            }
+    };
+
+    stage(0, s_fragA, lane0);
     fetch(0, lane0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     uint32_t pf = 0u, pf_sink = 0u;
 
-    for (int c = 0; c < p.nch; ++c) {
-        const int buf = c & 1;
-        const bf16_t* F0 = &s_frag[buf][0][0];
+    // chunk c, its fragments in `cur`; chunk c + 1's go to `nxt`
+    auto chunk = [&](int c, bf16_t (&cur)[NF][512], bf16_t (&nxt)[NF][512]) __attribute__((always_inline)) {
+        const bf16_t* F0 = &cur[0][0];
         pf_sink += pf;
         // the lane index as an opaque value: the many per-lane LDS addresses
         // below are loop-invariant, and hoisted out of the chunk loop they
@@ -322,7 +346,10 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
         const int r = lane & 31, half = lane >> 5;
         // ---- chunk c + 1's fragments into the other buffer (free since the
         // last barrier)
-        if (c + 1 < p.nch) stage(c + 1, buf ^ 1, lane);
+        if (c + 1 < p.nch) stage(c + 1, nxt, lane);
+        // ---- the previous chunk's outputs: issued here, they have this whole
+        // chunk to complete before the barrier's wait
+        if (c > 0) store_tiles(c - 1, lane);
         // ---- K1: dt and its cumsum (log2 units), one position per lane
         const float cs2 = wave_incl_scan(dtq * A2);
         if (lane < Q) {
@@ -476,14 +503,12 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
                     acc = mfma32x32x16(as_bf16x8(make_uint4(xw[0], xw[1], xw[2], xw[3])), pack8(m), acc);
                 }
             }
-            // store: the lane holds y[il][4 consecutive p] per group of 4
-            // registers; rows past the sequence end are dropped by the buffer
-            const __amdgpu_buffer_rsrc_t ry = buf_rsrc(yhead + (int64_t)c * Q * p.y_sl, rows_c * (uint32_t)p.y_sl * 2u);
+            // the tile goes to the wave's LDS scratch, row-major; it is stored
+            // at the start of the next chunk (store_tiles)
 #pragma unroll
             for (int gq = 0; gq < 4; ++gq)
-                buf_st8(ry, ((uint32_t)il * (uint32_t)p.y_sl + 8 * gq + 4 * half) * 2u,
-                        make_uint2(pack_bf16x2(acc[4 * gq], acc[4 * gq + 1]),
-                                   pack_bf16x2(acc[4 * gq + 2], acc[4 * gq + 3])));
+                *(uint2*)&s_yt[wave][it][r][8 * gq + 4 * half] =
+                    make_uint2(pack_bf16x2(acc[4 * gq], acc[4 * gq + 1]), pack_bf16x2(acc[4 * gq + 2], acc[4 * gq + 3]));
         }
 
         // ---- K3 + K4: h^T <- h^T F_k + B_k^T . xg_k over the blocks
@@ -510,7 +535,12 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
         // every wave is done with chunk c's buffer
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+    };
+    for (int c = 0; c < p.nch; c += 2) {
+        chunk(c, s_fragA, s_fragB);
+        if (c + 1 < p.nch) chunk(c + 1, s_fragB, s_fragA);
     }
+    store_tiles(p.nch - 1, lane0);
     // keeps the L2 warm-up loads alive (the condition never holds: L >= 1)
     if (p.L < 0 && pf_sink == 0x9e3779b9u) p.hT[0] = 0.f;
     // final state (f32): h[p = p0 + r][n] from h^T
