@@ -81,14 +81,27 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-// Inclusive prefix sum over a wave (64 lanes).
-__device__ __forceinline__ float wave_incl_scan(float v) {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        float t = __shfl_up(v, o, 64);
-        if (lane >= o) v += t;
+// Inclusive prefix sum over a wave (64 lanes), on DPP lane moves (no LDS
+// round trips): shifts by 1, 2, 4, 8 inside each 16-lane row, then lane 15 of
+// each row broadcast into the next row and lane 31 into the upper half.
+// Lanes with no source add 0 (bound_ctrl / masked rows keep the old value 0).
+__device__ __forceinline__ float dpp_term(float v, int ctrl, int row_mask) {
+    switch (ctrl) {  // the DPP control is an immediate
+        case 0x111: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x111, 0xf, 0xf, false));
+        case 0x112: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x112, 0xf, 0xf, false));
+        case 0x114: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x114, 0xf, 0xf, false));
+        case 0x118: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x118, 0xf, 0xf, false));
+        case 0x142: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xa, 0xf, false));
+        default: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xc, 0xf, false));
     }
+}
+__device__ __forceinline__ float wave_incl_scan(float v) {
+    v += dpp_term(v, 0x111, 0xf);  // row_shr:1
+    v += dpp_term(v, 0x112, 0xf);  // row_shr:2
+    v += dpp_term(v, 0x114, 0xf);  // row_shr:4
+    v += dpp_term(v, 0x118, 0xf);  // row_shr:8
+    v += dpp_term(v, 0x142, 0xa);  // row_bcast:15 into rows 1 and 3
+    v += dpp_term(v, 0x143, 0xc);  // row_bcast:31 into rows 2 and 3
     return v;
 }
 

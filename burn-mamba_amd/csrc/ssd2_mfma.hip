@@ -395,21 +395,29 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
         const uint32_t rows_c = (uint32_t)min(Q, p.L - c * Q);
         // ---- K2 + K5: y^T for the chunk's row tiles.  Inter-chunk term
         // h_in . C_i^T first, for every tile, with A from the state registers
+        // (each step's C fragments are read one step ahead, so the LDS
+        // latency of a read overlaps the previous step's MFMAs)
         f32x16_t yacc[T];
 #pragma unroll
         for (int it = 0; it < T; ++it) yacc[it] = zero16();
+        bf16x8_t cnext[T];
+#pragma unroll
+        for (int it = 0; it < T; ++it) cnext[it] = *(const bf16x8_t*)(F0 + ((FL::C0 + it * NK) * 64 + lane) * 8);
 #pragma unroll
         for (int kn = 0; kn < NK; ++kn) {
             const int nt = kn >> 1, q = kn & 1;
+            bf16x8_t cop[T];
+#pragma unroll
+            for (int it = 0; it < T; ++it) {
+                cop[it] = cnext[it];
+                if (kn + 1 < NK) cnext[it] = *(const bf16x8_t*)(F0 + ((FL::C0 + it * NK + kn + 1) * 64 + lane) * 8);
+            }
             float hv[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) hv[e] = hacc[nt][8 * q + e];
             const bf16x8_t a = pack8(hv);
 #pragma unroll
-            for (int it = 0; it < T; ++it) {
-                const bf16x8_t bop = *(const bf16x8_t*)(F0 + ((FL::C0 + it * NK + kn) * 64 + lane) * 8);
-                yacc[it] = mfma32x32x16(a, bop, yacc[it]);
-            }
+            for (int it = 0; it < T; ++it) yacc[it] = mfma32x32x16(a, cop[it], yacc[it]);
         }
 #pragma unroll
         for (int it = 0; it < T; ++it) {
@@ -511,7 +519,11 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
                     make_uint2(pack_bf16x2(acc[4 * gq], acc[4 * gq + 1]), pack_bf16x2(acc[4 * gq + 2], acc[4 * gq + 3]));
         }
 
-        // ---- K3 + K4: h^T <- h^T F_k + B_k^T . xg_k over the blocks
+        // ---- K3 + K4: h^T <- h^T F_k + B_k^T . xg_k over the blocks (each
+        // k step's operands read one step ahead)
+        bf16x8_t bnext[NTN], xnext = *(const bf16x8_t*)&s_xg[wave][r][8 * half];
+#pragma unroll
+        for (int nt = 0; nt < NTN; ++nt) bnext[nt] = *(const bf16x8_t*)(F0 + ((FL::B0 + nt * KS) * 64 + lane) * 8);
 #pragma unroll
         for (int jt = 0; jt < T; ++jt) {
             const float F = __builtin_amdgcn_exp2f(cse[jt] - (jt ? cse[jt - 1] : 0.f));
@@ -522,12 +534,18 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) {
                 const int ks = 2 * jt + kk;
-                const bf16x8_t bx = *(const bf16x8_t*)&s_xg[wave][r][ks * 16 + 8 * half];
+                const bf16x8_t bx = xnext;
+                bf16x8_t bop[NTN];
 #pragma unroll
-                for (int nt = 0; nt < NTN; ++nt) {
-                    const bf16x8_t a = *(const bf16x8_t*)(F0 + ((FL::B0 + nt * KS + ks) * 64 + lane) * 8);
-                    hacc[nt] = mfma32x32x16(a, bx, hacc[nt]);
+                for (int nt = 0; nt < NTN; ++nt) bop[nt] = bnext[nt];
+                if (ks + 1 < KS) {
+                    xnext = *(const bf16x8_t*)&s_xg[wave][r][(ks + 1) * 16 + 8 * half];
+#pragma unroll
+                    for (int nt = 0; nt < NTN; ++nt)
+                        bnext[nt] = *(const bf16x8_t*)(F0 + ((FL::B0 + nt * KS + ks + 1) * 64 + lane) * 8);
                 }
+#pragma unroll
+                for (int nt = 0; nt < NTN; ++nt) hacc[nt] = mfma32x32x16(bop[nt], bx, hacc[nt]);
             }
         }
         // ---- this wave's loads done (chunk c + 1's fragments and x), then
