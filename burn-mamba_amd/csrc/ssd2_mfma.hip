@@ -191,15 +191,14 @@ __global__ __launch_bounds__(256) void ssd2_prep_pack(Ssd2Params p, bf16_t* frag
 //   y_i = exp(cs_i - cs_{e_it}) acc + D x_i
 // and the chunk state is the same recurrence over all T blocks with the raw B
 // fragments,  h <- h F_k + sum_{j in k} B_j (x) xg_j.
-// Only xg is kept in LDS.  D x_i is taken from it as D xg_i / g_i (g_i =
-// dt_i exp(cs_{e_it} - cs_i)) when every g_i of the tile is at least 2^-100,
-// and from the raw x rows otherwise (dt = 0 included).  The output's last
-// factor exp(cs_i - cs_{e_it}) is >= 1 and xg_j of the diagonal block can be
-// as small as exp(cs_{e_it} - cs_{e_{it-1}}); when that block decay exceeds
-// 2^-64 (a steep block) the diagonal block instead uses the exact per-element
-// weight dt_j exp(cs_i - cs_j) on the raw x rows, after scaling acc by
-// exp(cs_i - cs_{e_{it-1}}) <= 1.  Raw x is read back from global memory
-// (the chunk was just streamed through L2) on those rare paths only.
+// xg^T is kept in LDS as the MFMA operand, and the raw x rows (time-major)
+// for the D x_i term.  The output's last factor exp(cs_i - cs_{e_it}) is >= 1
+// and xg_j of the diagonal block can be as small as exp(cs_{e_it} -
+// cs_{e_{it-1}}); when that block decay exceeds 2^-64 (a steep block) the
+// tile is recomputed with the exact per-element weight dt_j exp(cs_i - cs_j)
+// on the diagonal block, after scaling acc by exp(cs_i - cs_{e_{it-1}}) <= 1.
+// Raw x is read back from global memory (the chunk was just streamed through
+// L2) on that rare path only.
 //
 // Outputs are computed transposed, y^T[p, i] (i = time along MFMA columns),
 // so every per-time factor is a per-lane scalar and the four consecutive
@@ -221,7 +220,6 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
     constexpr int XPT = Q / 32;               // x staging items per lane: (2 rows x 8 headdim) each
     constexpr int FPW = (NF + HPW - 1) / HPW; // fragments each wave stages per chunk
     constexpr float kSteep = 64.f;            // log2 of the largest block decay factored
-    constexpr float kTinyG = 0x1p-100f;       // smallest g_i for D x from xg
     static_assert(Q == 32 || Q == 64, "a chunk's positions are the wave's lanes");
     // the group's fragments of two chunks, as two arrays: the reads of one and
     // the direct-to-LDS loads into the other are then provably disjoint, so no
@@ -231,7 +229,9 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
     __shared__ __align__(16) bf16_t s_xg[HPW][32][XP];   // per wave: xg^T [p][j]
     __shared__ __align__(16) float s_cs[HPW][Q];         // per wave: cumsum (log2 units)
     __shared__ __align__(16) float s_dt[HPW][Q];         // per wave: dt
-    __shared__ __align__(16) bf16_t s_yt[HPW][T][32][40];  // per wave: a chunk's output tiles, row-major
+    // per wave: the chunk's raw x rows, time-major, overwritten in place by
+    // its output rows (stored to global memory at the start of the next chunk)
+    __shared__ __align__(16) bf16_t s_io[HPW][T][32][40];
 
     const int wave = wave_id(), lane0 = threadIdx.x & 63;
     // XCD-aware work mapping: consecutive workgroups (same batch row, sharing
@@ -321,7 +321,7 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 const int row = (lane >> 2) + 16 * t, pc = (lane & 3) * 8;
-                const uint4 v = *(const uint4*)&s_yt[wave][it][row][pc];
+                const uint4 v = *(const uint4*)&s_io[wave][it][row][pc];
                 __builtin_amdgcn_raw_buffer_store_b128(
                     __builtin_bit_cast(decltype(__builtin_amdgcn_raw_buffer_load_b128(ry, 0, 0, 0)), v), ry,
                     ((uint32_t)(it * 32 + row) * (uint32_t)p.y_sl + pc) * 2u, 0, 0);
@@ -378,6 +378,9 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
                     pack_bf16x2(__uint_as_float(a0[k] & 0xffff0000u) * g0,
                                 __uint_as_float(a1[k] & 0xffff0000u) * g1);
             }
+            // the raw rows, time-major, for D x
+            *(uint4*)&s_io[wave][m][2 * jp][pv * 8] = xq[m][0];
+            *(uint4*)&s_io[wave][m][2 * jp + 1][pv * 8] = xq[m][1];
         }
         // ---- chunk c + 1's x rows and dt into registers (they land during
         // this chunk's MFMA work)
@@ -419,86 +422,107 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
 #pragma unroll
             for (int it = 0; it < T; ++it) yacc[it] = mfma32x32x16(a, cop[it], yacc[it]);
         }
+        // block decays F_k = exp(cs_{e_k} - cs_{e_{k-1}}) <= 1 (shared by the
+        // output tiles and the state)
+        float Fb[T];
+#pragma unroll
+        for (int k = 0; k < T; ++k) Fb[k] = __builtin_amdgcn_exp2f(cse[k] - (k ? cse[k - 1] : 0.f));
+        // ---- every tile as if no block were steep, the tiles' chains side by
+        // side and branch-free: block jt's xg operands serve all tiles it >= jt
+        //   acc_it <- acc_it F_jt + S_jt   (jt = it: the diagonal C.B^T block,
+        //   its upper triangle stored as 0 by the prep)
+#pragma unroll
+        for (int jt = 0; jt < T; ++jt) {
+#pragma unroll
+            for (int it = jt; it < T; ++it)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) yacc[it][v] *= Fb[jt];
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                const int ks = 2 * jt + kk;
+                const bf16x8_t a = *(const bf16x8_t*)&s_xg[wave][r][ks * 16 + 8 * half];
+#pragma unroll
+                for (int it = jt; it < T; ++it)
+                    yacc[it] = mfma32x32x16(
+                        a, *(const bf16x8_t*)(F0 + ((it * (it + 1) + ks) * 64 + lane) * 8), yacc[it]);
+            }
+        }
+        // y_i = exp(cs_i - cs_{e_it}) acc + D x_i, x_i raw from the chunk's
+        // time-major rows; the output overwrites them in place (the same lane
+        // reads and writes each of its 8-byte pieces)
 #pragma unroll
         for (int it = 0; it < T; ++it) {
-            const int il = it * 32 + r;  // this lane's output time (B-operand column)
-            f32x16_t acc = yacc[it];
-            // Horner over the strictly-lower blocks: acc <- acc F_jt + S_jt
+            const float colf = __builtin_amdgcn_exp2f(s_cs[wave][it * 32 + r] - cse[it]);
 #pragma unroll
-            for (int jt = 0; jt < it; ++jt) {
-                const float F = __builtin_amdgcn_exp2f(cse[jt] - (jt ? cse[jt - 1] : 0.f));
+            for (int gq = 0; gq < 4; ++gq) {
+                const uint2 xr = *(const uint2*)&s_io[wave][it][r][8 * gq + 4 * half];
+                const float xv[4] = {__uint_as_float(xr.x << 16), __uint_as_float(xr.x & 0xffff0000u),
+                                     __uint_as_float(xr.y << 16), __uint_as_float(xr.y & 0xffff0000u)};
+                float o[4];
 #pragma unroll
-                for (int v = 0; v < 16; ++v) acc[v] *= F;
-#pragma unroll
-                for (int kk = 0; kk < 2; ++kk) {
-                    const int ks = 2 * jt + kk;
-                    const bf16x8_t a = *(const bf16x8_t*)&s_xg[wave][r][ks * 16 + 8 * half];
-                    const bf16x8_t bop = *(const bf16x8_t*)(F0 + ((it * (it + 1) + ks) * 64 + lane) * 8);
-                    acc = mfma32x32x16(a, bop, acc);
-                }
+                for (int u = 0; u < 4; ++u) o[u] = yacc[it][4 * gq + u] * colf + Dh * xv[u];
+                *(uint2*)&s_io[wave][it][r][8 * gq + 4 * half] =
+                    make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
             }
-            // diagonal block (the prep stored its upper triangle as 0)
-            const float cs2_i = s_cs[wave][il];
-            const float cse_prev = it ? cse[it - 1] : 0.f;
-            const float cs_e = cse[it];
-            const uint4 dg0 = *(const uint4*)(F0 + ((it * (it + 1) + 2 * it) * 64 + lane) * 8);
-            const uint4 dg1 = *(const uint4*)(F0 + ((it * (it + 1) + 2 * it + 1) * 64 + lane) * 8);
-            if (cse_prev - cs_e <= kSteep) {
-                const float F = __builtin_amdgcn_exp2f(cs_e - cse_prev);
+        }
+        // ---- steep diagonal blocks (decay beyond 2^-64 inside the block: the
+        // factor exp(cs_i - cs_{e_it}) above may overflow) are recomputed: acc
+        // from the state again, brought to position i (factor <= 1), then the
+        // exact weights dt_j exp(cs_i - cs_j) (+ D on the diagonal) on raw x
+        // rows read back from global memory (the chunk was just streamed
+        // through L2)
+        bool steep = false;
 #pragma unroll
-                for (int v = 0; v < 16; ++v) acc[v] *= F;
+        for (int it = 0; it < T; ++it) steep |= (it ? cse[it - 1] : 0.f) - cse[it] > kSteep;
+        if (steep) {
+            // block end by a wave-uniform index, as selects (no indexed registers)
+            auto cse_at = [&](int k) {
+                float v = cse[0];
 #pragma unroll
-                for (int kk = 0; kk < 2; ++kk) {
-                    const bf16x8_t a = *(const bf16x8_t*)&s_xg[wave][r][it * 32 + kk * 16 + 8 * half];
-                    acc = mfma32x32x16(a, as_bf16x8(kk ? dg1 : dg0), acc);
+                for (int q = 1; q < T; ++q) v = k == q ? cse[q] : v;
+                return v;
+            };
+#pragma unroll 1
+            for (int it = 0; it < T; ++it) {
+                const float cse_prev = it ? cse_at(it - 1) : 0.f;
+                if (cse_prev - cse_at(it) <= kSteep) continue;
+                const int il = it * 32 + r;
+                f32x16_t acc = zero16();
+#pragma unroll
+                for (int kn = 0; kn < NK; ++kn) {
+                    float hv[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) hv[e] = hacc[kn >> 1][8 * (kn & 1) + e];
+                    acc = mfma32x32x16(pack8(hv),
+                                       *(const bf16x8_t*)(F0 + ((FL::C0 + it * NK + kn) * 64 + lane) * 8), acc);
                 }
-                // y_i = exp(cs_i - cs_e) (acc + D xg_i / g_i) with exp(cs_i - cs_e) / g_i = 1 / dt_i
-                const float colf = __builtin_amdgcn_exp2f(cs2_i - cs_e);
-                const float dti = s_dt[wave][il];
-                const float gi = dti * __builtin_amdgcn_exp2f(cs_e - cs2_i);
-                if (__all(gi >= kTinyG)) {
-                    const float dinv = Dh * __builtin_amdgcn_rcpf(dti);  // 1 ulp
+#pragma unroll 1
+                for (int jt = 0; jt < it; ++jt) {
 #pragma unroll
-                    for (int v = 0; v < 16; ++v) {
-                        const float xv = __uint_as_float(
-                            (uint32_t)s_xg[wave][8 * (v >> 2) + 4 * half + (v & 3)][il] << 16);
-                        acc[v] = (acc[v] + dinv * xv) * colf;
-                    }
-                } else {
-                    // raw x of the lane's output row, four headdim values per load
-                    const __amdgpu_buffer_rsrc_t rxc = buf_rsrc(xhead + (int64_t)c * Q * p.x_sl, rows_c * xrow);
+                    for (int v = 0; v < 16; ++v) acc[v] *= __builtin_amdgcn_exp2f(cse_at(jt) - (jt ? cse_at(jt - 1) : 0.f));
 #pragma unroll
-                    for (int gq = 0; gq < 4; ++gq) {
-                        const uint2 xr = buf_ld8(rxc, ((uint32_t)il * (uint32_t)p.x_sl + 8 * gq + 4 * half) * 2u);
-                        const float xv[4] = {__uint_as_float(xr.x << 16), __uint_as_float(xr.x & 0xffff0000u),
-                                             __uint_as_float(xr.y << 16), __uint_as_float(xr.y & 0xffff0000u)};
-#pragma unroll
-                        for (int u = 0; u < 4; ++u) acc[4 * gq + u] = acc[4 * gq + u] * colf + Dh * xv[u];
+                    for (int kk = 0; kk < 2; ++kk) {
+                        const int ks = 2 * jt + kk;
+                        acc = mfma32x32x16(*(const bf16x8_t*)&s_xg[wave][r][ks * 16 + 8 * half],
+                                           *(const bf16x8_t*)(F0 + ((it * (it + 1) + ks) * 64 + lane) * 8), acc);
                     }
                 }
-            } else {
-                // steep block: bring acc to position i (factor <= 1), then the
-                // exact weights dt_j exp(cs_i - cs_j) (+ D on the diagonal) on raw x
                 const __amdgpu_buffer_rsrc_t rxc = buf_rsrc(xhead + (int64_t)c * Q * p.x_sl, rows_c * xrow);
+                const float cs2_i = s_cs[wave][il];
                 const float sc = __builtin_amdgcn_exp2f(cs2_i - cse_prev);
 #pragma unroll
                 for (int v = 0; v < 16; ++v) acc[v] *= sc;
-                // the lane's row as an opaque value: its compares below are
-                // loop-invariant, and hoisted out of the chunk loop they would
-                // hold scalar registers for this rare path
-                int ilo = il;
-                asm volatile("" : "+v"(ilo));
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk) {
                     const int j0 = it * 32 + kk * 16 + 8 * half;
                     float cbv[8];
-                    unpack8(kk ? dg1 : dg0, cbv);
+                    unpack8(*(const uint4*)(F0 + ((it * (it + 1) + 2 * it + kk) * 64 + lane) * 8), cbv);
                     float m[8];
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         const int j = j0 + e;
                         const float val = cbv[e] * s_dt[wave][j] * __builtin_amdgcn_exp2f(cs2_i - s_cs[wave][j]);
-                        m[e] = (j < ilo) ? val : ((j == ilo) ? val + Dh : 0.f);
+                        m[e] = (j < il) ? val : ((j == il) ? val + Dh : 0.f);
                     }
                     // A operand x^T[p][j0 .. j0 + 7] for p = r, from the raw rows
                     uint32_t xw[4];
@@ -510,13 +534,11 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
                     }
                     acc = mfma32x32x16(as_bf16x8(make_uint4(xw[0], xw[1], xw[2], xw[3])), pack8(m), acc);
                 }
-            }
-            // the tile goes to the wave's LDS scratch, row-major; it is stored
-            // at the start of the next chunk (store_tiles)
 #pragma unroll
-            for (int gq = 0; gq < 4; ++gq)
-                *(uint2*)&s_yt[wave][it][r][8 * gq + 4 * half] =
-                    make_uint2(pack_bf16x2(acc[4 * gq], acc[4 * gq + 1]), pack_bf16x2(acc[4 * gq + 2], acc[4 * gq + 3]));
+                for (int gq = 0; gq < 4; ++gq)
+                    *(uint2*)&s_io[wave][it][r][8 * gq + 4 * half] = make_uint2(
+                        pack_bf16x2(acc[4 * gq], acc[4 * gq + 1]), pack_bf16x2(acc[4 * gq + 2], acc[4 * gq + 3]));
+            }
         }
 
         // ---- K3 + K4: h^T <- h^T F_k + B_k^T . xg_k over the blocks (each
@@ -526,11 +548,10 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
         for (int nt = 0; nt < NTN; ++nt) bnext[nt] = *(const bf16x8_t*)(F0 + ((FL::B0 + nt * KS) * 64 + lane) * 8);
 #pragma unroll
         for (int jt = 0; jt < T; ++jt) {
-            const float F = __builtin_amdgcn_exp2f(cse[jt] - (jt ? cse[jt - 1] : 0.f));
 #pragma unroll
             for (int nt = 0; nt < NTN; ++nt)
 #pragma unroll
-                for (int v = 0; v < 16; ++v) hacc[nt][v] *= F;
+                for (int v = 0; v < 16; ++v) hacc[nt][v] *= Fb[jt];
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) {
                 const int ks = 2 * jt + kk;
