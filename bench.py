@@ -1039,8 +1039,8 @@ def cpu_baseline_mamba2_block(cfg, seed=0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", default="ssd2",
                     choices=["ssd2", "mamba1", "decode", "ssd3", "mamba1_step", "mamba3_step", "mamba3_prep",
                              "mamba2_block"])

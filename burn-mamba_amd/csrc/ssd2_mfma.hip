@@ -48,6 +48,36 @@ __device__ __forceinline__ f32x16_t mfma32x32x16(bf16x8_t a, bf16x8_t b, f32x16_
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// Raw buffer resource words (base, num_records, the flags buf_rsrc uses), in
+// scalar registers: `base` and `bytes` must be wave-uniform.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x4_t buf_words(const void* base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)base;
+    u32x4_t w;
+    w.x = __builtin_amdgcn_readfirstlane((uint32_t)a);
+    w.y = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) & 0xffffu;  // stride 0
+    w.z = __builtin_amdgcn_readfirstlane(bytes);
+    w.w = 0x00020000u;
+    return w;
+}
+
+// One direct-to-LDS load of 16 bytes per lane: bytes [soff + voff, +16) of
+// the buffer (zero past its end) land at LDS address lds + 16 * lane.  `lds`
+// and `soff` are wave-uniform.  Written as inline assembly so that the
+// compiler's memory-counter bookkeeping does not see it: its own LDS
+// accesses are then never held back by these loads (it cannot always prove
+// them disjoint), and the caller waits for them (s_waitcnt vmcnt(0), then a
+// barrier) before anything reads the destination.
+__device__ __forceinline__ void dma16(u32x4_t rsrc, uint32_t lds, uint32_t voff, uint32_t soff) {
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %1, %2, %3 offen lds"
+        :
+        : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(rsrc), "s"(soff)
+        : "m0");
+}
+
 __device__ __forceinline__ uint2 ld8(const void* ptr, bool ok) {
     return ok ? *(const uint2*)ptr : make_uint2(0u, 0u);
 }
@@ -205,11 +235,11 @@ __global__ __launch_bounds__(256) void ssd2_prep_pack(Ssd2Params p, bf16_t* frag
 // headdim values a lane holds are stored as one 8-byte write.
 //
 // Per chunk c a wave: issues the direct-to-LDS loads of its share of chunk
-// c + 1's fragments (into the other buffer); scans dt; stages xg; issues its
-// register prefetch of chunk c + 1's x rows and dt; computes its output tiles
-// and its state; then waits for its loads and meets the others at the chunk's
-// one barrier, after which chunk c + 1's fragments are complete and chunk c's
-// buffer is free.
+// c + 1's fragments (into the other buffer); stores chunk c - 1's outputs;
+// scans dt; stages xg and the raw x rows; issues its register prefetch of
+// chunk c + 1's x rows and dt; computes its output tiles and its state; then
+// waits for its loads and meets the others at the chunk's one barrier, after
+// which chunk c + 1's fragments are complete and chunk c's buffer is free.
 // The launch bound caps a wave at 256 registers (two waves per SIMD), which
 // keeps the accumulators in VGPRs next to the VALU work that scales them.
 template <int N, int Q, int HPW>
@@ -230,7 +260,10 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
     __shared__ __align__(16) float s_cs[HPW][Q];         // per wave: cumsum (log2 units)
     __shared__ __align__(16) float s_dt[HPW][Q];         // per wave: dt
     // per wave: the chunk's raw x rows, time-major, overwritten in place by
-    // its output rows (stored to global memory at the start of the next chunk)
+    // its output rows (stored to global memory at the start of the next
+    // chunk).  A row's 32 headdim values sit in MFMA-result order, headdim
+    // p at 16 ((p / 4) % 2) + 4 (p / 8) + p % 4, so that the 16 values a
+    // lane holds of a row are contiguous (two 16-byte accesses)
     __shared__ __align__(16) bf16_t s_io[HPW][T][32][40];
 
     const int wave = wave_id(), lane0 = threadIdx.x & 63;
@@ -280,14 +313,13 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
 
     // direct-to-LDS loads of chunk cc's fragments f = wave + HPW k into `dst`
     auto stage = [&](int cc, bf16_t (&dst)[NF][512], int lane) __attribute__((always_inline)) {
-        const __amdgpu_buffer_rsrc_t rf = buf_rsrc(gfrag + (int64_t)cc * grp_stride, (uint32_t)NF * 1024u);
+        const u32x4_t rf = buf_words(gfrag + (int64_t)cc * grp_stride, (uint32_t)NF * 1024u);
 #pragma unroll
         for (int k = 0; k < FPW; ++k) {
             const int f = wave + HPW * k;
             if (FPW * HPW == NF || f < NF)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    rf, (__attribute__((address_space(3))) void*)&dst[f][0], 16, lane * 16u,
-                    (uint32_t)__builtin_amdgcn_readfirstlane(f * 1024), 0, 0);
+                dma16(rf, (uint32_t)(uintptr_t)&dst[f][0], lane * 16u,
+                      (uint32_t)__builtin_amdgcn_readfirstlane(f * 1024));
         }
     };
     // register prefetch of chunk cc's x rows (item m: rows 2 (lane/4 + 16 m) + {0, 1},
@@ -321,7 +353,9 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 const int row = (lane >> 2) + 16 * t, pc = (lane & 3) * 8;
-                const uint4 v = *(const uint4*)&s_io[wave][it][row][pc];
+                const uint2 lo = *(const uint2*)&s_io[wave][it][row][(lane & 3) * 4];
+                const uint2 hi = *(const uint2*)&s_io[wave][it][row][16 + (lane & 3) * 4];
+                const uint4 v = make_uint4(lo.x, lo.y, hi.x, hi.y);
                 __builtin_amdgcn_raw_buffer_store_b128(
                     __builtin_bit_cast(decltype(__builtin_amdgcn_raw_buffer_load_b128(ry, 0, 0, 0)), v), ry,
                     ((uint32_t)(it * 32 + row) * (uint32_t)p.y_sl + pc) * 2u, 0, 0);
@@ -379,8 +413,11 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
                                 __uint_as_float(a1[k] & 0xffff0000u) * g1);
             }
             // the raw rows, time-major, for D x
-            *(uint4*)&s_io[wave][m][2 * jp][pv * 8] = xq[m][0];
-            *(uint4*)&s_io[wave][m][2 * jp + 1][pv * 8] = xq[m][1];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                *(uint2*)&s_io[wave][m][2 * jp + e][pv * 4] = make_uint2(xq[m][e].x, xq[m][e].y);
+                *(uint2*)&s_io[wave][m][2 * jp + e][16 + pv * 4] = make_uint2(xq[m][e].z, xq[m][e].w);
+            }
         }
         // ---- chunk c + 1's x rows and dt into registers (they land during
         // this chunk's MFMA work)
@@ -449,21 +486,20 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
         }
         // y_i = exp(cs_i - cs_{e_it}) acc + D x_i, x_i raw from the chunk's
         // time-major rows; the output overwrites them in place (the same lane
-        // reads and writes each of its 8-byte pieces)
+        // reads and writes its 32 bytes of the row, accumulator order)
 #pragma unroll
         for (int it = 0; it < T; ++it) {
             const float colf = __builtin_amdgcn_exp2f(s_cs[wave][it * 32 + r] - cse[it]);
+            bf16_t* io = &s_io[wave][it][r][16 * half];
+            const uint4 xa = *(const uint4*)io, xb = *(const uint4*)(io + 8);
+            const uint32_t xw[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+            uint32_t ow[8];
 #pragma unroll
-            for (int gq = 0; gq < 4; ++gq) {
-                const uint2 xr = *(const uint2*)&s_io[wave][it][r][8 * gq + 4 * half];
-                const float xv[4] = {__uint_as_float(xr.x << 16), __uint_as_float(xr.x & 0xffff0000u),
-                                     __uint_as_float(xr.y << 16), __uint_as_float(xr.y & 0xffff0000u)};
-                float o[4];
-#pragma unroll
-                for (int u = 0; u < 4; ++u) o[u] = yacc[it][4 * gq + u] * colf + Dh * xv[u];
-                *(uint2*)&s_io[wave][it][r][8 * gq + 4 * half] =
-                    make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
-            }
+            for (int k = 0; k < 8; ++k)
+                ow[k] = pack_bf16x2(yacc[it][2 * k] * colf + Dh * __uint_as_float(xw[k] << 16),
+                                    yacc[it][2 * k + 1] * colf + Dh * __uint_as_float(xw[k] & 0xffff0000u));
+            *(uint4*)io = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+            *(uint4*)(io + 8) = make_uint4(ow[4], ow[5], ow[6], ow[7]);
         }
         // ---- steep diagonal blocks (decay beyond 2^-64 inside the block: the
         // factor exp(cs_i - cs_{e_it}) above may overflow) are recomputed: acc
@@ -534,10 +570,12 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
                     }
                     acc = mfma32x32x16(as_bf16x8(make_uint4(xw[0], xw[1], xw[2], xw[3])), pack8(m), acc);
                 }
+                uint32_t ow[8];
 #pragma unroll
-                for (int gq = 0; gq < 4; ++gq)
-                    *(uint2*)&s_io[wave][it][r][8 * gq + 4 * half] = make_uint2(
-                        pack_bf16x2(acc[4 * gq], acc[4 * gq + 1]), pack_bf16x2(acc[4 * gq + 2], acc[4 * gq + 3]));
+                for (int k = 0; k < 8; ++k) ow[k] = pack_bf16x2(acc[2 * k], acc[2 * k + 1]);
+                bf16_t* io = &s_io[wave][it][r][16 * half];
+                *(uint4*)io = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+                *(uint4*)(io + 8) = make_uint4(ow[4], ow[5], ow[6], ow[7]);
             }
         }
 
