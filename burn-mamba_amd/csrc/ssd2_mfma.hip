@@ -221,6 +221,13 @@ __global__ __launch_bounds__(256) void ssd2_prep_pack(Ssd2Params p, bf16_t* frag
 //   y_i = exp(cs_i - cs_{e_it}) acc + D x_i
 // and the chunk state is the same recurrence over all T blocks with the raw B
 // fragments,  h <- h F_k + sum_{j in k} B_j (x) xg_j.
+// The decays are applied lazily: the registers hold h-hat with h = phi h-hat
+// for a wave-uniform phi (kept as log2), so that h <- h F_k is phi <- phi F_k
+// and S_k enters as S_k / phi (1 / phi folded into xg, the Horner
+// accumulators likewise in phi units, phi folded into the output factor).
+// Only when phi would drop below 2^-64 is it applied to the registers (an
+// "event": h-hat and the live accumulators times phi, phi = 1), which bounds
+// xg / phi and h-hat by 2^64 times their true size.
 // xg^T is kept in LDS as the MFMA operand, and the raw x rows (time-major)
 // for the D x_i term.  The output's last factor exp(cs_i - cs_{e_it}) is >= 1
 // and xg_j of the diagonal block can be as small as exp(cs_{e_it} -
@@ -250,6 +257,7 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
     constexpr int XPT = Q / 32;               // x staging items per lane: (2 rows x 8 headdim) each
     constexpr int FPW = (NF + HPW - 1) / HPW; // fragments each wave stages per chunk
     constexpr float kSteep = 64.f;            // log2 of the largest block decay factored
+    constexpr float kLazy = 64.f;             // log2 of the smallest pending state factor
     static_assert(Q == 32 || Q == 64, "a chunk's positions are the wave's lanes");
     // the group's fragments of two chunks, as two arrays: the reads of one and
     // the direct-to-LDS loads into the other are then provably disjoint, so no
@@ -367,6 +375,7 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     uint32_t pf = 0u, pf_sink = 0u;
+    float lphi = 0.f;  // log2 of the state's pending factor: h = 2^lphi * hacc
 
     // chunk c, its fragments in `cur`; chunk c + 1's go to `nxt`
     auto chunk = [&](int c, bf16_t (&cur)[NF][512], bf16_t (&nxt)[NF][512]) __attribute__((always_inline)) {
@@ -394,12 +403,25 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
 #pragma unroll
         for (int k = 0; k < T; ++k)
             cse[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cs2), 32 * k + 31));
+        // lazy decay (wave-uniform): phi after block k (log2), whether block k
+        // applies it to the registers first (event) and by what factor
+        const float lphi_in = lphi;
+        float lph[T], rho[T];
+        bool ev[T];
+#pragma unroll
+        for (int k = 0; k < T; ++k) {
+            const float lk = lphi + (cse[k] - (k ? cse[k - 1] : 0.f));
+            ev[k] = lk < -kLazy;
+            rho[k] = __builtin_amdgcn_exp2f(lk);
+            lphi = ev[k] ? 0.f : lk;
+            lph[k] = lphi;
+        }
         // ---- block-scaled x -> s_xg[wave][p][j] (time-major)
         const int jp = lane >> 2, pv = lane & 3;
 #pragma unroll
         for (int m = 0; m < XPT; ++m) {
             const int j0 = 2 * (jp + 16 * m);
-            const float ce = cse[m];  // rows j0, j0 + 1 sit in block m
+            const float ce = cse[m] - lph[m];  // rows j0, j0 + 1 sit in block m; xg / phi
             const float g0 = __shfl(dtq, j0, 64) * __builtin_amdgcn_exp2f(ce - __shfl(cs2, j0, 64));
             const float g1 = __shfl(dtq, j0 + 1, 64) * __builtin_amdgcn_exp2f(ce - __shfl(cs2, j0 + 1, 64));
             const uint32_t a0[4] = {xq[m][0].x, xq[m][0].y, xq[m][0].z, xq[m][0].w};
@@ -459,21 +481,18 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
 #pragma unroll
             for (int it = 0; it < T; ++it) yacc[it] = mfma32x32x16(a, cop[it], yacc[it]);
         }
-        // block decays F_k = exp(cs_{e_k} - cs_{e_{k-1}}) <= 1 (shared by the
-        // output tiles and the state)
-        float Fb[T];
-#pragma unroll
-        for (int k = 0; k < T; ++k) Fb[k] = __builtin_amdgcn_exp2f(cse[k] - (k ? cse[k - 1] : 0.f));
         // ---- every tile as if no block were steep, the tiles' chains side by
-        // side and branch-free: block jt's xg operands serve all tiles it >= jt
-        //   acc_it <- acc_it F_jt + S_jt   (jt = it: the diagonal C.B^T block,
-        //   its upper triangle stored as 0 by the prep)
+        // side: block jt's xg operands serve all tiles it >= jt
+        //   acc_it <- acc_it + S_jt / phi_jt   (jt = it: the diagonal C.B^T
+        //   block, its upper triangle stored as 0 by the prep)
 #pragma unroll
         for (int jt = 0; jt < T; ++jt) {
+            if (ev[jt]) {
 #pragma unroll
-            for (int it = jt; it < T; ++it)
+                for (int it = jt; it < T; ++it)
 #pragma unroll
-                for (int v = 0; v < 16; ++v) yacc[it][v] *= Fb[jt];
+                    for (int v = 0; v < 16; ++v) yacc[it][v] *= rho[jt];
+            }
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) {
                 const int ks = 2 * jt + kk;
@@ -484,12 +503,12 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
                         a, *(const bf16x8_t*)(F0 + ((it * (it + 1) + ks) * 64 + lane) * 8), yacc[it]);
             }
         }
-        // y_i = exp(cs_i - cs_{e_it}) acc + D x_i, x_i raw from the chunk's
+        // y_i = exp(cs_i - cs_{e_it}) phi_it acc + D x_i, x_i raw from the chunk's
         // time-major rows; the output overwrites them in place (the same lane
         // reads and writes its 32 bytes of the row, accumulator order)
 #pragma unroll
         for (int it = 0; it < T; ++it) {
-            const float colf = __builtin_amdgcn_exp2f(s_cs[wave][it * 32 + r] - cse[it]);
+            const float colf = __builtin_amdgcn_exp2f(s_cs[wave][it * 32 + r] - cse[it] + lph[it]);
             bf16_t* io = &s_io[wave][it][r][16 * half];
             const uint4 xa = *(const uint4*)io, xb = *(const uint4*)(io + 8);
             const uint32_t xw[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
@@ -518,11 +537,19 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
                 for (int q = 1; q < T; ++q) v = k == q ? cse[q] : v;
                 return v;
             };
+            auto lph_at = [&](int k) {
+                float v = lph[0];
+#pragma unroll
+                for (int q = 1; q < T; ++q) v = k == q ? lph[q] : v;
+                return v;
+            };
 #pragma unroll 1
             for (int it = 0; it < T; ++it) {
                 const float cse_prev = it ? cse_at(it - 1) : 0.f;
                 if (cse_prev - cse_at(it) <= kSteep) continue;
                 const int il = it * 32 + r;
+                // true units here: acc = C_i.h_in = phi_in C_i.h-hat_in, and
+                // each lower block's S_k / phi_k times phi_k
                 f32x16_t acc = zero16();
 #pragma unroll
                 for (int kn = 0; kn < NK; ++kn) {
@@ -532,16 +559,22 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
                     acc = mfma32x32x16(pack8(hv),
                                        *(const bf16x8_t*)(F0 + ((FL::C0 + it * NK + kn) * 64 + lane) * 8), acc);
                 }
+                const float phin = __builtin_amdgcn_exp2f(lphi_in);
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[v] *= phin;
 #pragma unroll 1
                 for (int jt = 0; jt < it; ++jt) {
-#pragma unroll
-                    for (int v = 0; v < 16; ++v) acc[v] *= __builtin_amdgcn_exp2f(cse_at(jt) - (jt ? cse_at(jt - 1) : 0.f));
+                    const float F = __builtin_amdgcn_exp2f(cse_at(jt) - (jt ? cse_at(jt - 1) : 0.f));
+                    const float ph = __builtin_amdgcn_exp2f(lph_at(jt));
+                    f32x16_t t = zero16();
 #pragma unroll
                     for (int kk = 0; kk < 2; ++kk) {
                         const int ks = 2 * jt + kk;
-                        acc = mfma32x32x16(*(const bf16x8_t*)&s_xg[wave][r][ks * 16 + 8 * half],
-                                           *(const bf16x8_t*)(F0 + ((it * (it + 1) + ks) * 64 + lane) * 8), acc);
+                        t = mfma32x32x16(*(const bf16x8_t*)&s_xg[wave][r][ks * 16 + 8 * half],
+                                         *(const bf16x8_t*)(F0 + ((it * (it + 1) + ks) * 64 + lane) * 8), t);
                     }
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) acc[v] = acc[v] * F + t[v] * ph;
                 }
                 const __amdgpu_buffer_rsrc_t rxc = buf_rsrc(xhead + (int64_t)c * Q * p.x_sl, rows_c * xrow);
                 const float cs2_i = s_cs[wave][il];
@@ -579,17 +612,20 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
             }
         }
 
-        // ---- K3 + K4: h^T <- h^T F_k + B_k^T . xg_k over the blocks (each
-        // k step's operands read one step ahead)
+        // ---- K3 + K4: h-hat^T <- h-hat^T + B_k^T . (xg_k / phi_k) over the
+        // blocks (phi applied on events only; each k step's operands read one
+        // step ahead)
         bf16x8_t bnext[NTN], xnext = *(const bf16x8_t*)&s_xg[wave][r][8 * half];
 #pragma unroll
         for (int nt = 0; nt < NTN; ++nt) bnext[nt] = *(const bf16x8_t*)(F0 + ((FL::B0 + nt * KS) * 64 + lane) * 8);
 #pragma unroll
         for (int jt = 0; jt < T; ++jt) {
+            if (ev[jt]) {
 #pragma unroll
-            for (int nt = 0; nt < NTN; ++nt)
+                for (int nt = 0; nt < NTN; ++nt)
 #pragma unroll
-                for (int v = 0; v < 16; ++v) hacc[nt][v] *= Fb[jt];
+                    for (int v = 0; v < 16; ++v) hacc[nt][v] *= rho[jt];
+            }
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) {
                 const int ks = 2 * jt + kk;
@@ -620,9 +656,14 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
     store_tiles(p.nch - 1, lane0);
     // keeps the L2 warm-up loads alive (the condition never holds: L >= 1)
     if (p.L < 0 && pf_sink == 0x9e3779b9u) p.hT[0] = 0.f;
-    // final state (f32): h[p = p0 + r][n] from h^T
+    // final state (f32): h[p = p0 + r][n] = phi h-hat^T[n][p]
     {
         const int r = lane0 & 31, half = lane0 >> 5;
+        const float ph = __builtin_amdgcn_exp2f(lphi);
+#pragma unroll
+        for (int nt = 0; nt < NTN; ++nt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) hacc[nt][v] *= ph;
         float* hTr = p.hT + (((int64_t)b * p.H + h) * 64 + p0 + r) * N;
 #pragma unroll
         for (int nt = 0; nt < NTN; ++nt)
