@@ -8,7 +8,10 @@
 //    clamped to dt_limit (:695, softplus.rs:17-48).  The conv window of the
 //    cache becomes the last `kernel` columns of the padded input
 //    (mamba2.rs:652-655); it is updated in place by a second kernel that runs
-//    after the first has read the old window.
+//    after the first has read the old window.  With nheads = 0 there is no dt
+//    and this is the Mamba-1 prefill conv (Mamba1::forward layer 2,
+//    src/mamba1/mamba1.rs:300-340: the same padded causal conv, SiLU and
+//    window update over the x half of the in_proj rows).
 //  * mamba2_gated_rmsnorm (step 7, :776; RmsNormGated, rms_norm_gated.rs:70-135):
 //    gate-then-norm (default) or norm-then-gate over a row of `width`,
 //    rms = sqrt(mean(x^2) + eps) with the caller's eps (div_eps of the
@@ -350,10 +353,11 @@ using namespace mamba;
 
 extern "C" int mamba2_conv_fwd(const mamba2_conv_args* a, mamba_stream_t stream) {
     MAMBA_CHECK_ARG(a != nullptr, "args is NULL");
-    MAMBA_CHECK_ARG(a->batch > 0 && a->seqlen > 0 && a->channels > 0 && a->nheads > 0, "sizes must be >= 1");
+    MAMBA_CHECK_ARG(a->batch > 0 && a->seqlen > 0 && a->channels > 0 && a->nheads >= 0,
+                    "batch, seqlen and channels must be >= 1, nheads >= 0");
     MAMBA_CHECK_ARG(a->kernel >= 1 && a->kernel <= kM2MaxK, "kernel must be in [1, 8]");
-    MAMBA_CHECK_ARG(a->proj && a->conv_w && a->conv_state && a->dt_bias && a->xbc && a->dt,
-                    "proj, conv_w, conv_state, dt_bias, xbc and dt are required");
+    MAMBA_CHECK_ARG(a->proj && a->conv_w && a->conv_state && a->xbc, "proj, conv_w, conv_state and xbc are required");
+    MAMBA_CHECK_ARG(a->nheads == 0 || (a->dt_bias && a->dt), "dt_bias and dt are required when nheads > 0");
     MAMBA_CHECK_ARG((a->in_dtype == MAMBA_F32 || a->in_dtype == MAMBA_BF16) &&
                         (a->out_dtype == MAMBA_F32 || a->out_dtype == MAMBA_BF16),
                     "bad dtype");

@@ -1,12 +1,15 @@
-"""Mamba-1 over the C ABI: the selective scan (``mamba1_scan_fwd``) and the
-recurrent decode step (``mamba1_scan_step``, ``mamba_conv1d_step``).
+"""Mamba-1 over the C ABI: the block forward (prefill conv on
+``mamba2_conv_fwd`` with no dt heads, then ``mamba1_scan_fwd``), the selective
+scan (``mamba1_scan_fwd``) and the recurrent decode step (``mamba1_scan_step``,
+``mamba_conv1d_step``).
 
 Reference: ``Mamba1::selective_scan`` (src/mamba1/mamba1.rs:422-523) and, with
 ``delta_bias``/``delta_softplus``/``z``, the scan part of ``Mamba1::ssm`` plus
-the ``silu(z)`` gate of ``Mamba1::forward`` (mamba1.rs:348, 391-394);
+the ``silu(z)`` gate of ``Mamba1::forward`` (mamba1.rs:348, 391-394); the block
+``Mamba1::forward`` (mamba1.rs:278-352);
 ``Mamba1::step`` / ``ssm_step`` / ``selective_scan_step`` (mamba1.rs:533-733).
-The x_proj / dt_proj / in_proj / out_proj products of the step run on the ROCm
-BLAS through ``torch.mm``.
+The x_proj / dt_proj / in_proj / out_proj products run on the ROCm BLAS
+through ``torch.mm``.
 """
 
 from __future__ import annotations
@@ -163,6 +166,34 @@ def conv1d_step(x, state, w, bias=None, silu=True, out=None):
     return out
 
 
+def conv1d_fwd(x, state, w, bias=None):
+    """Layer 2 of Mamba1::forward (src/mamba1/mamba1.rs:300-340) on the
+    ``mamba2_conv_fwd`` kernel with no dt heads: x [b, l, c] (unit inner stride)
+    -> silu(causal depthwise conv of [state[:, :, 1:] | x] + bias) [b, l, c] f32;
+    state [b, c, K] (contiguous f32) becomes the last K columns of that padded
+    input, in place."""
+    b, L, ch = x.shape
+    k = w.shape[1]
+    if x.dtype != torch.float32 or x.stride(2) != 1:
+        raise _lib.MambaHipError("x must be f32 with a unit inner stride")
+    if state.dtype != torch.float32 or not state.is_contiguous() or tuple(state.shape) != (b, ch, k):
+        raise _lib.MambaHipError("conv state must be a contiguous f32 [b, channels, K] tensor")
+    out = torch.empty((b, L, ch), device=x.device, dtype=torch.float32)
+    wc, bc = w.contiguous().float(), None if bias is None else bias.contiguous().float()
+    a = _lib.Mamba2ConvArgs()
+    a.batch, a.seqlen, a.channels, a.kernel, a.nheads = b, L, ch, k, 0
+    a.in_dtype = a.out_dtype = _lib.MAMBA_F32
+    a.proj, a.proj_sb, a.proj_sl = x.data_ptr(), x.stride(0), x.stride(1)
+    a.xbc_offset = a.dt_offset = 0
+    a.conv_w = wc.data_ptr()
+    a.conv_b = None if bc is None else bc.data_ptr()
+    a.conv_state = state.data_ptr()
+    a.dt_bias, a.dt = None, None
+    a.xbc, a.xbc_sb, a.xbc_sl = out.data_ptr(), out.stride(0), out.stride(1)
+    check(_lib.lib().mamba2_conv_fwd(ctypes.byref(a), _stream(x.device)), "mamba2_conv_fwd")
+    return out
+
+
 @dataclass
 class Mamba1Cache:
     """conv_bik [batch, d_inner, conv_kernel] and ssm_bir [batch, d_inner, state_rank], f32
@@ -226,8 +257,8 @@ class Mamba1Config:
 
 @dataclass
 class Mamba1:
-    """Decode-side Mamba1 block (parameters of src/mamba1/mamba1.rs:124-227); Linear
-    weights in Burn's [d_in, d_out] layout."""
+    """Mamba1 block, forward and step (parameters of src/mamba1/mamba1.rs:124-227);
+    Linear weights in Burn's [d_in, d_out] layout."""
     cfg: Mamba1Config
     in_proj_w: torch.Tensor      # [d_model, 2 d_inner]
     conv_w: torch.Tensor         # [d_inner, K]
@@ -247,6 +278,39 @@ class Mamba1:
         c, dev = self.cfg, self.in_proj_w.device
         return Mamba1Cache(conv_bik=torch.zeros(batch, c.d_inner, c.conv_kernel, device=dev),
                            ssm_bir=torch.zeros(batch, c.d_inner, c.state_rank, device=dev))
+
+    def forward(self, x: torch.Tensor, cache: Optional[Mamba1Cache] = None):
+        """Mamba1::forward (src/mamba1/mamba1.rs:278-352): x [b, l, d_model] ->
+        (y [b, l, d_model], cache).  The cache (zero when None) supplies the
+        initial conv window and SSM state and is updated in place, so a
+        sequence can be run in segments (chunked prefill, then step)."""
+        c = self.cfg
+        b, L, dm = x.shape
+        if L < 1:
+            raise _lib.MambaHipError("sequence length must be at least 1")
+        if cache is None:
+            cache = self.new_cache(b)
+        di, r, n = c.d_inner, c.dt_rank, c.state_rank
+        x2 = x.reshape(b * L, dm).float()
+        # layer 1, in_proj, as its two halves so each is a dense [b, l, d_inner]
+        xs = torch.mm(x2, self.in_proj_w[:, :di]).view(b, L, di)
+        res = torch.mm(x2, self.in_proj_w[:, di:]).view(b, L, di)
+        # layer 2: causal conv over [cached window | xs] + SiLU; window updated
+        u = conv1d_fwd(xs, cache.conv_bik, self.conv_w, self.conv_b)
+        # ssm (mamba1.rs:366-399): x_proj, dt_proj (its bias and the softplus go
+        # to the scan), then the selective scan with D u and the silu(res) gate
+        x_dbl = torch.mm(u.view(b * L, di), self.x_proj_w).view(b, L, r + 2 * n)
+        delta = torch.mm(x_dbl.view(b * L, r + 2 * n)[:, :r], self.dt_proj_w).view(b, L, di)
+        y = torch.empty((b, L, di), device=x.device, dtype=torch.float32)
+        final = torch.empty_like(cache.ssm_bir)
+        # [b, l, *] tensors as the scan's [b, d, l] views: u, delta, z and y
+        # share one stride pair
+        mamba1_scan(u.transpose(1, 2), delta.transpose(1, 2), self.A,
+                    x_dbl[:, :, r:r + n].transpose(1, 2), x_dbl[:, :, r + n:].transpose(1, 2),
+                    D=self.d, z=res.transpose(1, 2), delta_bias=self.dt_proj_b, delta_softplus=True,
+                    initial_state=cache.ssm_bir, y=y.transpose(1, 2), final_state=final)
+        cache.ssm_bir.copy_(final)
+        return torch.mm(y.view(b * L, di), self.out_proj_w).view(b, L, dm), cache
 
     def step(self, x: torch.Tensor, cache: Optional[Mamba1Cache] = None):
         """Mamba1::step (mamba1.rs:533-612): returns (y [b, d_model], cache); the cache

@@ -327,10 +327,12 @@ def conv_fwd(cfg: Mamba2Config, zxbcdt: torch.Tensor, cache: Mamba2Cache, conv_w
     a.in_dtype, a.out_dtype = _dtype_code(zxbcdt), _dtype_code(xbc)
     a.proj, a.proj_sb, a.proj_sl = zxbcdt.data_ptr(), zxbcdt.stride(0), zxbcdt.stride(1)
     a.xbc_offset, a.dt_offset = cfg.d_inner, cfg.d_inner + cfg.conv_dim
-    a.conv_w = conv_w.contiguous().float().data_ptr()
-    a.conv_b = None if conv_b is None else conv_b.contiguous().float().data_ptr()
+    # converted copies held until the launch is queued
+    w, bias, dtb = (None if t is None else t.contiguous().float() for t in (conv_w, conv_b, dt_bias))
+    a.conv_w = w.data_ptr()
+    a.conv_b = None if bias is None else bias.data_ptr()
     a.conv_state = cs.data_ptr()
-    a.dt_bias = dt_bias.contiguous().float().data_ptr()
+    a.dt_bias = dtb.data_ptr()
     a.dt_min, a.dt_max = cfg.dt_limit
     a.xbc, a.xbc_sb, a.xbc_sl = xbc.data_ptr(), xbc.stride(0), xbc.stride(1)
     a.dt = dt.data_ptr()

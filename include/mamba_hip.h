@@ -617,10 +617,13 @@ int mamba_rmsnorm(const mamba_rmsnorm_args* args, mamba_stream_t stream);
 /*   dt[b,l,h] = clamp(softplus(proj[b,l,dt_offset + h] + dt_bias[h]),         */
 /*                     dt_min, dt_max),                                         */
 /* then conv_state[b,c,:] = the last `kernel` columns of xpad (:652-655),      */
-/* updated in place after the outputs are computed.                            */
+/* updated in place after the outputs are computed.  nheads = 0 skips dt      */
+/* (dt_bias and dt may then be NULL): the Mamba-1 prefill conv, layer 2 of    */
+/* Mamba1::forward (src/mamba1/mamba1.rs:300-340), over the x half of the     */
+/* in_proj rows.                                                               */
 /* ------------------------------------------------------------------------- */
 typedef struct mamba2_conv_args {
-    int32_t batch, seqlen, channels, kernel, nheads; /* channels = conv_dim; kernel <= 8 */
+    int32_t batch, seqlen, channels, kernel, nheads; /* channels = conv_dim; kernel <= 8; nheads >= 0 */
     int32_t in_dtype, out_dtype;                     /* proj; xbc                  */
     const void* proj;   int64_t proj_sb, proj_sl;    /* [b, l, row]                */
     int32_t xbc_offset, dt_offset;                   /* column offsets in a row    */

@@ -172,6 +172,36 @@ def mamba1_block_step(x, p, conv_state, ssm_state, prec=64):
     return linear(y, p["out_proj_w"], None, prec), cs, ss
 
 
+def mamba1_block_fwd(x, p, conv_state, ssm_state, prec=64):
+    """Mamba1::forward (src/mamba1/mamba1.rs:278-352): in_proj -> split (xs, res)
+    -> causal depthwise conv over [cached window[:, :, 1:] | xs] + bias, SiLU
+    (:300-340; the window becomes the padded input's last K columns) -> ssm
+    (:366-399: x_proj -> split (dt, B, C) -> dt_proj (+bias) -> softplus ->
+    selective_scan with D u) -> * silu(res) -> out_proj.
+    x [b, l, d_model] -> (y [b, l, d_model], conv' [b, d_inner, K], ssm' [b, d_inner, n])."""
+    x = np.asarray(x, np.float32)
+    b, L, dm = x.shape
+    di = p["conv_w"].shape[0]
+    r = p["dt_proj_w"].shape[0]
+    n = p["A"].shape[1]
+    xr = linear(x.reshape(b * L, dm), p["in_proj_w"], None, prec).reshape(b, L, 2 * di)
+    # the conv of the Mamba-2 prologue with no dt heads is the same padded
+    # causal conv + SiLU + window update
+    u, _, cs = mamba2_conv_fwd(xr, p["conv_w"], p["conv_b"], conv_state, np.zeros(0), 0, 0, di, 0)
+    u = u.astype(np.float32)
+    x_dbl = linear(u.reshape(b * L, di), p["x_proj_w"], None, prec)
+    delta = linear(np.ascontiguousarray(x_dbl[:, :r]), p["dt_proj_w"], None, prec).reshape(b, L, di)
+    x_dbl = x_dbl.reshape(b, L, r + 2 * n)
+
+    def bdl(t):  # [b, l, c] -> [b, c, l]
+        return np.ascontiguousarray(np.asarray(t).transpose(0, 2, 1))
+
+    y, ss = mamba1_scan(bdl(u), bdl(delta), p["A"], bdl(x_dbl[..., r:r + n]), bdl(x_dbl[..., r + n:]), p["D"],
+                        bdl(xr[..., di:]), p["dt_proj_b"], True, ssm_state, prec)
+    out = linear(bdl(y).reshape(b * L, di), p["out_proj_w"], None, prec)
+    return out.reshape(b, L, dm), cs.astype(np.float32), ss
+
+
 def rmsnorm(x, w, prec=64):
     x, w = _f32(x), _f32(w)
     out = np.zeros_like(x)

@@ -12,7 +12,9 @@ sign, off-by-one in the causal mask, transposed operand) would break:
     y = D u; N = 1 with constant delta is a first-order IIR filter
     (scipy.signal.lfilter);
   * invariants: chunk-length independence; zero-dt padding is an identity
-    (src/mamba2/mamba2.rs:703-706); split == full (cache continuity);
+    (src/mamba2/mamba2.rs:703-706); split == full (cache continuity); the
+    Mamba-1 block forward equals its step unrolled token by token, from zero
+    and from random caches (src/mamba1/mamba1/tests.rs:216-372);
   * Mamba-3: the merged single-SSD equals the explicit two-term trapezoid
     recurrence (src/mamba3/mamba3.rs:14-26), and lambda = 1 collapses it to
     Mamba-2.
@@ -684,3 +686,90 @@ def test_mamba2_block_fwd_equals_steps(norm_before_gate):
         np.testing.assert_allclose(y[:, l], o, rtol=2e-4, atol=2e-5)
     np.testing.assert_allclose(cs, c_s, rtol=0, atol=0)
     np.testing.assert_allclose(ss, s_s, rtol=1e-4, atol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# Mamba-1 block forward (src/mamba1/mamba1.rs:278-352) against the block step
+# unrolled token by token, and prefix + suffix forward against one forward:
+# the reference's own relations (src/mamba1/mamba1/tests.rs:216-372, 384-429)
+# ---------------------------------------------------------------------------
+
+def _m1_params(seed, d_model, n, k, expand, dt_rank=None):
+    """Random Mamba-1 parameters with the reference init's scales
+    (src/mamba1/mamba1.rs:124-227); Linear weights [d_in, d_out]."""
+    rng = np.random.default_rng(seed)
+    di = expand * d_model
+    r = dt_rank or -(-d_model // n)
+
+    def uni(shape, bound):
+        return ((rng.random(shape) * 2 - 1) * bound).astype(np.float32)
+
+    dt = np.exp(rng.random(di) * (np.log(0.1) - np.log(1e-3)) + np.log(1e-3))
+    return dict(in_proj_w=uni((d_model, 2 * di), d_model ** -0.5), conv_w=uni((di, k), k ** -0.5),
+                conv_b=uni((di,), k ** -0.5), x_proj_w=uni((di, r + 2 * n), di ** -0.5),
+                dt_proj_w=uni((r, di), r ** -0.5), dt_proj_b=(dt + np.log(-np.expm1(-dt))).astype(np.float32),
+                A=-np.tile(np.arange(1, n + 1, dtype=np.float32), (di, 1)), D=np.ones(di, np.float32),
+                out_proj_w=uni((di, d_model), di ** -0.5))
+
+
+def _m1_cache(seed, b, di, k, n, random):
+    rng = np.random.default_rng(seed)
+    if not random:
+        return np.zeros((b, di, k), np.float32), np.zeros((b, di, n), np.float32)
+    return (rng.standard_normal((b, di, k)).astype(np.float32),
+            rng.standard_normal((b, di, n)).astype(np.float32))
+
+
+# (d_model, state_rank, conv_kernel, expand, dt_rank): the reference's small
+# config and its d_state 16, d_conv 2, expand 1 and custom dt_rank variants
+M1_CFGS = [(32, 8, 4, 2, None), (32, 16, 4, 2, None), (32, 8, 2, 2, None), (32, 8, 4, 1, None), (32, 8, 4, 2, 8)]
+
+
+@pytest.mark.parametrize("cfg", M1_CFGS)
+@pytest.mark.parametrize("random_init", [False, True])
+def test_mamba1_block_forward_equals_step_unroll(cfg, random_init):
+    dm, n, k, ex, r = cfg
+    p = _m1_params(1, dm, n, k, ex, r)
+    b, L = 2, 5
+    x = np.random.default_rng(2).standard_normal((b, L, dm)).astype(np.float32)
+    conv0, ssm0 = _m1_cache(3, b, ex * dm, k, n, random_init)
+    y, conv, ssm = oracle.mamba1_block_fwd(x, p, conv0, ssm0)
+    cs, ss, ys = conv0, ssm0, []
+    for t in range(L):
+        yt, cs, ss = oracle.mamba1_block_step(np.ascontiguousarray(x[:, t]), p, cs, ss)
+        ys.append(yt)
+    np.testing.assert_allclose(y, np.stack(ys, 1), rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(conv, cs, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(ssm, ss, rtol=1e-5, atol=1e-6)
+    if random_init:
+        # the initial state is consumed: a zero cache gives a clearly different output
+        y0, _, _ = oracle.mamba1_block_fwd(x, p, *_m1_cache(3, b, ex * dm, k, n, False))
+        assert np.abs(y - y0).max() > 1e-3
+
+
+def test_mamba1_block_split_equals_full():
+    dm, n, k, ex, r = M1_CFGS[0]
+    p = _m1_params(4, dm, n, k, ex, r)
+    b, L, split = 2, 6, 2
+    x = np.random.default_rng(5).standard_normal((b, L, dm)).astype(np.float32)
+    conv0, ssm0 = _m1_cache(6, b, ex * dm, k, n, True)
+    y, conv, ssm = oracle.mamba1_block_fwd(x, p, conv0, ssm0)
+    ya, ca, sa = oracle.mamba1_block_fwd(x[:, :split], p, conv0, ssm0)
+    yb, cb, sb = oracle.mamba1_block_fwd(x[:, split:], p, ca, sa)
+    np.testing.assert_allclose(y, np.concatenate([ya, yb], 1), rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(conv, cb, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(ssm, sb, rtol=1e-5, atol=1e-6)
+
+
+def test_mamba1_block_forward_short_sequence_window():
+    """A sequence shorter than the conv kernel: the new window keeps the old
+    window's tail (mamba1.rs:317-325), checked by hand against the padded input."""
+    dm, n, k, ex, r = 16, 4, 4, 2, None
+    p = _m1_params(7, dm, n, k, ex, r)
+    b, L = 1, 2
+    x = np.random.default_rng(8).standard_normal((b, L, dm)).astype(np.float32)
+    conv0, ssm0 = _m1_cache(9, b, ex * dm, k, n, True)
+    _, conv, _ = oracle.mamba1_block_fwd(x, p, conv0, ssm0)
+    xs = oracle.linear(x.reshape(b * L, dm), p["in_proj_w"])[:, :ex * dm].reshape(b, L, ex * dm)
+    pad = np.concatenate([conv0[:, :, 1:], xs.transpose(0, 2, 1)], axis=2)
+    np.testing.assert_allclose(conv, pad[:, :, L - 1:L - 1 + k], rtol=1e-6, atol=1e-6)
