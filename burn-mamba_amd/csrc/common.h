@@ -143,6 +143,38 @@ __device__ __forceinline__ void buf_st8(__amdgpu_buffer_rsrc_t r, uint32_t off, 
         __builtin_bit_cast(decltype(__builtin_amdgcn_raw_buffer_load_b64(r, 0, 0, 0)), v), r, off, 0, 0);
 }
 
+// Raw buffer resource words (base, num_records, the flags buf_rsrc uses), in
+// scalar registers: `base` and `bytes` must be wave-uniform.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x4_t buf_words(const void* base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)base;
+    u32x4_t w;
+    w.x = __builtin_amdgcn_readfirstlane((uint32_t)a);
+    w.y = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) & 0xffffu;  // stride 0
+    w.z = __builtin_amdgcn_readfirstlane(bytes);
+    w.w = 0x00020000u;
+    return w;
+}
+
+// One direct-to-LDS load of 16 bytes per lane: bytes [soff + voff, +16) of
+// the buffer (zero past its end) land at LDS address lds + 16 * lane.  `lds`
+// and `soff` are wave-uniform.  Written as inline assembly so that the
+// compiler's memory-counter bookkeeping does not see it: its own LDS
+// accesses are then never held back by these loads (it cannot always prove
+// them disjoint), and the caller waits for them (an s_waitcnt on the vector
+// memory counter that covers them, then a barrier) before anything reads the
+// destination.  The compiler's own vmcnt waits stay correct: the counter
+// drains in issue order, so an uncounted load can only make them wait longer.
+__device__ __forceinline__ void dma16(u32x4_t rsrc, uint32_t lds, uint32_t voff, uint32_t soff) {
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %1, %2, %3 offen lds"
+        :
+        : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(rsrc), "s"(soff)
+        : "m0");
+}
+
 // two floats -> two bf16 (round to nearest even) in one dword, lo first
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));

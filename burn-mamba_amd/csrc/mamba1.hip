@@ -16,6 +16,7 @@
 // and silu(z) are evaluated once per element in the staging pass.
 
 #include <cstdlib>
+#include <type_traits>
 
 #include "common.h"
 
@@ -205,6 +206,229 @@ __global__ __launch_bounds__(16 * N, N <= 16 ? 3 : 1) void mamba1_scan_kernel(Ma
     }
 }
 
+// ---------------------------------------------------------------------------
+// Time-major path for dstate 16 (u, delta, z and y contiguous along time, rows
+// 16-byte aligned): 64 channels x 32-token tiles, 4 lanes per channel holding 4
+// states each, as above.  A tile spans whole 128-byte lines of every row it
+// touches, so each line is read from HBM once (16-token tiles read half lines
+// and HBM fetched many lines twice) and y is written in whole lines.
+//  * u and delta arrive by direct-to-LDS loads, one 16-byte piece (4 tokens)
+//    of all 64 rows per instruction, into [t/4][channel][t%4]: the scan's
+//    float4 reads of 4 tokens of 16 channels then cover all banks.  They are
+//    double-buffered (tile k+1 streams in while tile k is scanned), with no
+//    staging registers.
+//  * B and C (16 x 32 per tile) are transposed through registers into [t][n].
+//  * z is prefetched into registers in the store mapping (8 tokens of one row
+//    per thread, two 16-byte pieces).
+//  * The scan writes y + D u over u in place; after a barrier the epilogue
+//    multiplies by silu(z) and stores.
+// Per tile: a barrier once the tile's loads have landed, one after the scan
+// (and one after the in-place softplus of delta when a bias or softplus is
+// requested).
+constexpr int kTm16Tile = 32;
+
+template <bool GATE>
+__global__ __launch_bounds__(256, 3) void mamba1_scan_tm16(Mamba1Params p) {
+    constexpr int N = 16, CPB = 64, TT = kTm16Tile, NQ = TT / 4;
+    __shared__ __align__(16) float s_u[2][NQ][CPB][4];  // u, then y + D u in place
+    __shared__ __align__(16) float s_d[2][NQ][CPB][4];  // delta (softplus'd in place)
+    __shared__ __align__(16) float s_B[2][TT][N];
+    __shared__ __align__(16) float s_C[2][TT][N];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    const int nblk_d = (p.D + CPB - 1) / CPB;
+    const int b = blockIdx.x / nblk_d, d0 = (blockIdx.x % nblk_d) * CPB;
+    // scan mapping: channel c, states 4 ng .. 4 ng + 3
+    const int c = tid >> 2, ng = tid & 3, d = d0 + c;
+    const bool dvalid = d < p.D;
+    float A2[4], h[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int n = 4 * ng + k;
+        A2[k] = dvalid ? p.A[(int64_t)d * p.A_sd + (int64_t)n * p.A_sn] * kLog2eM1 : 0.f;
+        h[k] = (dvalid && p.h0) ? p.h0[((int64_t)b * p.D + d) * N + n] : 0.f;
+    }
+    const float Dd = (p.Dv && dvalid) ? p.Dv[d] : 0.f;
+    const int ntile = (p.L + TT - 1) / TT;
+    // byte extents of the batch row's u / delta / z / y (u's strides for all);
+    // lanes with nothing to move get an offset past the end (loads read zero,
+    // stores are dropped)
+    const uint32_t row_bytes = (uint32_t)((((int64_t)p.D - 1) * p.u_sd + p.L) * 4);
+    constexpr uint32_t kOut = 0x80000000u;
+    const u32x4_t ru = buf_words(p.u + (int64_t)b * p.u_sb, row_bytes);
+    const u32x4_t rd = buf_words(p.dl + (int64_t)b * p.dl_sb, row_bytes);
+    const __amdgpu_buffer_rsrc_t rz = buf_rsrc(GATE ? p.z + (int64_t)b * p.z_sb : p.u, row_bytes);
+    const __amdgpu_buffer_rsrc_t ry = buf_rsrc(p.y + (int64_t)b * p.y_sb, row_bytes);
+    // DMA mapping: wave w moves pieces q = 2 w, 2 w + 1 of u and delta; lane i
+    // is channel d0 + i
+    const bool lvalid = d0 + lane < p.D;
+    // a byte offset, or kOut where `ok` fails, as a plain select: kept opaque
+    // so that the compiler neither branches around the access nor duplicates
+    // it (each access below is one instruction on every path)
+    auto sel = [](bool ok, uint32_t off) {
+        uint32_t r = ok ? off : kOut;
+        asm volatile("" : "+v"(r));
+        return r;
+    };
+    const uint32_t sd = (uint32_t)p.u_sd;
+    auto dma_tile = [&](int tk, int buf) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int q = 2 * wave + k, t = tk * TT + 4 * q;
+            const uint32_t off = sel(lvalid && t < p.L, ((uint32_t)(d0 + lane) * sd + (uint32_t)t) * 4u);
+            dma16(ru, (uint32_t)(uintptr_t)&s_u[buf][q][0][0], off, 0u);
+            dma16(rd, (uint32_t)(uintptr_t)&s_d[buf][q][0][0], off, 0u);
+        }
+    };
+    // B/C mapping: thread -> state tid / 16, tokens 2 (tid % 16) + {0, 1}
+    const int bn = tid >> 4, bt = (tid & 15) * 2;
+    const uint32_t bc_bytes = (uint32_t)(((int64_t)(N - 1) * p.B_sn + ((int64_t)p.L - 1) * p.B_sl + 1) * 4);
+    const uint32_t cc_bytes = (uint32_t)(((int64_t)(N - 1) * p.C_sn + ((int64_t)p.L - 1) * p.C_sl + 1) * 4);
+    const __amdgpu_buffer_rsrc_t rb = buf_rsrc(p.Bm + (int64_t)b * p.B_sb, bc_bytes);
+    const __amdgpu_buffer_rsrc_t rc = buf_rsrc(p.Cm + (int64_t)b * p.C_sb, cc_bytes);
+    float rB[2], rC[2];
+    // every load and store below is issued unconditionally (past-the-end
+    // offsets read zero / drop), so that the compiler's counts of outstanding
+    // memory operations are exact at the top of each tile
+    auto load_bc = [&](int tk) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int t = tk * TT + bt + e;
+            rB[e] = buf_ld4(rb, sel(t < p.L, ((uint32_t)bn * (uint32_t)p.B_sn + (uint32_t)t * (uint32_t)p.B_sl) * 4u));
+            rC[e] = buf_ld4(rc, sel(t < p.L, ((uint32_t)bn * (uint32_t)p.C_sn + (uint32_t)t * (uint32_t)p.C_sl) * 4u));
+        }
+    };
+    // store mapping: thread -> channel tid / 4, tokens 8 (tid % 4) .. + 7
+    const int ec = tid >> 2, et = (tid & 3) * 8;
+    const bool evalid = d0 + ec < p.D;
+    // the in-place softplus touches channel tid / 4 only (8 elements per thread)
+    const float sbias = (p.dbias && evalid) ? p.dbias[d0 + ec] : 0.f;
+    uint4 rzv[2];
+    auto eoff = [&](int tk, int k) {
+        const int t = tk * TT + et + 4 * k;
+        return sel(evalid && t < p.L, ((uint32_t)(d0 + ec) * sd + (uint32_t)t) * 4u);
+    };
+    auto load_z = [&](int tk) {
+        if (GATE) {
+#pragma unroll
+            for (int k = 0; k < 2; ++k) rzv[k] = buf_ld16(rz, eoff(tk, k));
+        }
+    };
+
+    auto tile = [&](int tk, auto partial_tag) __attribute__((always_inline)) {
+        constexpr bool partial = decltype(partial_tag)::value;
+        const int buf = tk & 1, t0 = tk * TT;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            s_B[buf][bt + e][bn] = rB[e];
+            s_C[buf][bt + e][bn] = rC[e];
+        }
+        // this tile's direct-to-LDS loads: at most the previous tile's two
+        // stores and this tile's two z loads were issued after them (tile 0's
+        // were waited for before the first tile)
+        if (GATE)
+            __builtin_amdgcn_s_waitcnt(0xF74);  // vmcnt(4) expcnt(7) lgkmcnt(15)
+        else
+            __builtin_amdgcn_s_waitcnt(0xF72);  // vmcnt(2)
+        __syncthreads();
+        load_bc(tk + 1);
+        if (tk + 1 < ntile) dma_tile(tk + 1, buf ^ 1);
+        if (p.dbias || p.softplus) {
+            // delta <- softplus(delta + bias), in place
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int e = tid + 256 * j, q = e >> 8;
+                float v = s_d[buf][q][ec][e & 3] + sbias;
+                if (p.softplus) v = m1_softplus(v);
+                s_d[buf][q][ec][e & 3] = v;
+            }
+            __syncthreads();
+        }
+        // ---- the recurrence, 4 tokens per LDS read of delta and u
+#pragma unroll 2
+        for (int q = 0; q < NQ; ++q) {
+            const float4 dv4 = *(const float4*)&s_d[buf][q][c][0];
+            const float4 uv4 = *(const float4*)&s_u[buf][q][c][0];
+            float4 bq[4], cq[4];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                bq[g] = *(const float4*)&s_B[buf][4 * q + g][4 * ng];
+                cq[g] = *(const float4*)&s_C[buf][4 * q + g][4 * ng];
+            }
+            float dv[4] = {dv4.x, dv4.y, dv4.z, dv4.w}, uv[4] = {uv4.x, uv4.y, uv4.z, uv4.w};
+            if (partial) {
+                // past the end: identity steps (the loaded values are another
+                // row's or zero), outputs not stored
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const bool ok = t0 + 4 * q + g < p.L;
+                    dv[g] = ok ? dv[g] : 0.f;
+                    uv[g] = ok ? uv[g] : 0.f;
+                }
+            }
+            float yq[4];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const float du = dv[g] * uv[g];
+                const float a0 = __builtin_amdgcn_exp2f(dv[g] * A2[0]);
+                const float a1 = __builtin_amdgcn_exp2f(dv[g] * A2[1]);
+                const float a2 = __builtin_amdgcn_exp2f(dv[g] * A2[2]);
+                const float a3 = __builtin_amdgcn_exp2f(dv[g] * A2[3]);
+                h[0] = __builtin_fmaf(h[0], a0, du * bq[g].x);
+                h[1] = __builtin_fmaf(h[1], a1, du * bq[g].y);
+                h[2] = __builtin_fmaf(h[2], a2, du * bq[g].z);
+                h[3] = __builtin_fmaf(h[3], a3, du * bq[g].w);
+                yq[g] = __builtin_fmaf(cq[g].x, h[0], cq[g].y * h[1]) + __builtin_fmaf(cq[g].z, h[2], cq[g].w * h[3]);
+            }
+#pragma unroll
+            for (int g = 0; g < 4; ++g) yq[g] = quad_sum(yq[g]);
+            // every lane of the channel holds the sums: y + D u over u
+            *(float4*)&s_u[buf][q][c][0] = make_float4(__builtin_fmaf(Dd, uv[0], yq[0]), __builtin_fmaf(Dd, uv[1], yq[1]),
+                                                       __builtin_fmaf(Dd, uv[2], yq[2]), __builtin_fmaf(Dd, uv[3], yq[3]));
+        }
+        __syncthreads();
+        // ---- epilogue: y = (y + D u) silu(z), two 16-byte stores per thread
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            float4 o = *(const float4*)&s_u[buf][(et >> 2) + k][ec][0];
+            if (GATE) {
+                const uint4 zw = rzv[k];
+                const float zv[4] = {__uint_as_float(zw.x), __uint_as_float(zw.y), __uint_as_float(zw.z),
+                                     __uint_as_float(zw.w)};
+                float* ov = &o.x;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) ov[e] *= zv[e] * __builtin_amdgcn_rcpf(1.f + __expf(-zv[e]));
+            }
+            const uint32_t off = eoff(tk, k);
+            if (partial) {
+                // a piece may straddle the end: element by element
+                const float ov[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const bool ok = off != kOut && t0 + et + 4 * k + e < p.L;
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(ov[e]), ry, sel(ok, off + 4 * e), 0, 0);
+                }
+            } else {
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    __builtin_bit_cast(decltype(__builtin_amdgcn_raw_buffer_load_b128(ry, 0, 0, 0)), o), ry, off, 0, 0);
+            }
+        }
+        load_z(tk + 1);
+    };
+
+    load_bc(0);
+    dma_tile(0, 0);
+    load_z(0);
+    __builtin_amdgcn_s_waitcnt(0);
+    const int nfull = p.L / TT;
+    for (int tk = 0; tk < nfull; ++tk) tile(tk, std::false_type{});
+    if (nfull < ntile) tile(nfull, std::true_type{});
+    if (dvalid && p.hT) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) p.hT[((int64_t)b * p.D + d) * N + 4 * ng + k] = h[k];
+    }
+}
+
 // Shape-generic fallback (any dstate <= 256): one thread per channel, states in
 // LDS.  Used when dstate is not 16, 32 or 64 or the strides do not allow the
 // tiled kernel.
@@ -260,6 +484,18 @@ static int m1_make_params(const mamba1_scan_args* a, Mamba1Params* out) {
     return MAMBA_OK;
 }
 
+// the time-major tile path: dstate 16, time-contiguous rows at 16-byte
+// aligned addresses, byte offsets inside a batch row below 2^31
+static bool tm16_ok(const Mamba1Params& p) {
+    auto al16 = [](const void* q) { return ((uintptr_t)q & 15u) == 0; };
+    return p.N == 16 && p.u_sl == 1 && p.u_sd % 4 == 0 && p.u_sd >= p.L && al16(p.u) && al16(p.dl) &&
+           al16(p.y) && (!p.z || al16(p.z)) && p.u_sb % 4 == 0 && p.dl_sb % 4 == 0 && p.y_sb % 4 == 0 &&
+           (!p.z || p.z_sb % 4 == 0) && (((int64_t)p.D - 1) * p.u_sd + p.L) * 4 < (1ll << 31) &&
+           p.B_sn >= 0 && p.B_sl >= 0 && p.C_sn >= 0 && p.C_sl >= 0 &&
+           ((int64_t)(p.N - 1) * p.B_sn + ((int64_t)p.L - 1) * p.B_sl + 1) * 4 < (1ll << 31) &&
+           ((int64_t)(p.N - 1) * p.C_sn + ((int64_t)p.L - 1) * p.C_sl + 1) * 4 < (1ll << 31);
+}
+
 template <int N>
 static void launch_m1(const Mamba1Params& p, hipStream_t stream) {
     constexpr int CPB = 64;
@@ -277,9 +513,18 @@ static int m1_dispatch(const mamba1_scan_args* a, hipStream_t stream, hipEvent_t
     const bool same_strides = p.dl_sd == p.u_sd && p.dl_sl == p.u_sl && p.y_sd == p.u_sd &&
                               p.y_sl == p.u_sl && (!p.z || (p.z_sd == p.u_sd && p.z_sl == p.u_sl));
     const bool fits32 = (int64_t)p.D * std::abs(p.u_sd) + (int64_t)p.L * std::abs(p.u_sl) < (1ll << 31);
-    const int nfast = (same_strides && fits32) ? p.N : 0;
+    int nfast = (same_strides && fits32) ? p.N : 0;
     if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, stream));
+    if (nfast == 16 && tm16_ok(p)) {
+        const int nblk = p.nb * ((p.D + 63) / 64);
+        if (p.z)
+            hipLaunchKernelGGL((mamba1_scan_tm16<true>), dim3(nblk), dim3(256), 0, stream, p);
+        else
+            hipLaunchKernelGGL((mamba1_scan_tm16<false>), dim3(nblk), dim3(256), 0, stream, p);
+        nfast = -1;
+    }
     switch (nfast) {
+        case -1: break;
         case 16: launch_m1<16>(p, stream); break;
         case 32: launch_m1<32>(p, stream); break;
         case 64: launch_m1<64>(p, stream); break;

@@ -48,36 +48,6 @@ __device__ __forceinline__ f32x16_t mfma32x32x16(bf16x8_t a, bf16x8_t b, f32x16_
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// Raw buffer resource words (base, num_records, the flags buf_rsrc uses), in
-// scalar registers: `base` and `bytes` must be wave-uniform.
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ u32x4_t buf_words(const void* base, uint32_t bytes) {
-    const uint64_t a = (uint64_t)base;
-    u32x4_t w;
-    w.x = __builtin_amdgcn_readfirstlane((uint32_t)a);
-    w.y = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) & 0xffffu;  // stride 0
-    w.z = __builtin_amdgcn_readfirstlane(bytes);
-    w.w = 0x00020000u;
-    return w;
-}
-
-// One direct-to-LDS load of 16 bytes per lane: bytes [soff + voff, +16) of
-// the buffer (zero past its end) land at LDS address lds + 16 * lane.  `lds`
-// and `soff` are wave-uniform.  Written as inline assembly so that the
-// compiler's memory-counter bookkeeping does not see it: its own LDS
-// accesses are then never held back by these loads (it cannot always prove
-// them disjoint), and the caller waits for them (s_waitcnt vmcnt(0), then a
-// barrier) before anything reads the destination.
-__device__ __forceinline__ void dma16(u32x4_t rsrc, uint32_t lds, uint32_t voff, uint32_t soff) {
-    asm volatile(
-        "s_mov_b32 m0, %0\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %1, %2, %3 offen lds"
-        :
-        : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(rsrc), "s"(soff)
-        : "m0");
-}
-
 __device__ __forceinline__ uint2 ld8(const void* ptr, bool ok) {
     return ok ? *(const uint2*)ptr : make_uint2(0u, 0u);
 }

@@ -67,6 +67,37 @@ def test_mamba1_delta_bias_softplus_no_gate():
     np.testing.assert_allclose(hT.cpu().numpy(), hr, **TOL)
 
 
+@pytest.mark.parametrize("l,pad", [(37, 40), (61, 64), (32, 36)])
+def test_mamba1_padded_rows(l, pad):
+    """Time-contiguous rows with a padded row stride (16-byte aligned) and a
+    sequence that ends inside a 16-byte piece: the tiled path's last-tile
+    masking.  Bias + softplus + gate + D; y's padding must stay untouched."""
+    import torch
+    import mamba_hip
+    import oracle
+    b, d, n = 2, 130, 16
+    inp = mamba1_inputs(seed=l, b=b, d=d, l=l, n=n, h0=True)
+    raw = (np.random.default_rng(l).standard_normal((b, d, l)) - 2.0).astype(np.float32)
+    bias = (0.5 * np.random.default_rng(l + 1).standard_normal(d)).astype(np.float32)
+
+    def padded(a, fill=0.0):
+        t = torch.full((b, d, pad), fill, device="cuda")
+        t[:, :, :l] = _dev(a)
+        return t[:, :, :l]
+
+    y = padded(np.zeros((b, d, l), np.float32), fill=7.0)
+    _, hT = mamba_hip.mamba1_scan(padded(inp["u"]), padded(raw), _dev(inp["A"]), _dev(inp["B"]), _dev(inp["C"]),
+                                  _dev(inp["D"]), padded(inp["z"]), delta_bias=_dev(bias), delta_softplus=True,
+                                  initial_state=_dev(inp["h0"]), y=y)
+    torch.cuda.synchronize()
+    yr, hr = oracle.mamba1_scan(inp["u"], raw, inp["A"], inp["B"], inp["C"], inp["D"], inp["z"], delta_bias=bias,
+                                delta_softplus=True, h0=inp["h0"])
+    np.testing.assert_allclose(y.cpu().numpy(), yr, **TOL)
+    np.testing.assert_allclose(hT.cpu().numpy(), hr, **TOL)
+    full = y.as_strided((b, d, pad), y.stride()).cpu().numpy()
+    assert (full[:, :, l:] == 7.0).all()
+
+
 def test_mamba1_reference_signature_and_layouts():
     """Mamba1::selective_scan(delta [s,b,d], a, b [b,s,r], c [s,b,r], d, u [b,s,d], init)
     (mamba1.rs:422-430) gives the channel-major result transposed."""
