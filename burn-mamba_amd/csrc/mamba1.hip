@@ -212,11 +212,14 @@ __global__ __launch_bounds__(16 * N, N <= 16 ? 3 : 1) void mamba1_scan_kernel(Ma
 // states each, as above.  A tile spans whole 128-byte lines of every row it
 // touches, so each line is read from HBM once (16-token tiles read half lines
 // and HBM fetched many lines twice) and y is written in whole lines.
-//  * u and delta arrive by direct-to-LDS loads, one 16-byte piece (4 tokens)
-//    of all 64 rows per instruction, into [t/4][channel][t%4]: the scan's
-//    float4 reads of 4 tokens of 16 channels then cover all banks.  They are
-//    double-buffered (tile k+1 streams in while tile k is scanned), with no
-//    staging registers.
+//  * u and delta arrive by direct-to-LDS loads, 8 whole 128-byte row pieces
+//    per instruction (8 lanes per line, so the memory requests are whole
+//    lines), double-buffered (tile k+1 streams in while tile k is scanned),
+//    with no staging registers.  Rows are [channel][32 tokens] with the eight
+//    16-byte pieces of row c swizzled (piece k in slot k ^ (c % 8)): a lane
+//    loads the piece its slot holds, and the scan's float4 reads of one piece
+//    across 16 channels then spread over the banks.  Each wave loads the rows
+//    of its own 16 channels.
 //  * B and C (16 x 32 per tile) are transposed through registers into [t][n].
 //  * z is prefetched into registers in the store mapping (8 tokens of one row
 //    per thread, two 16-byte pieces).
@@ -230,8 +233,8 @@ constexpr int kTm16Tile = 32;
 template <bool GATE>
 __global__ __launch_bounds__(256, 3) void mamba1_scan_tm16(Mamba1Params p) {
     constexpr int N = 16, CPB = 64, TT = kTm16Tile, NQ = TT / 4;
-    __shared__ __align__(16) float s_u[2][NQ][CPB][4];  // u, then y + D u in place
-    __shared__ __align__(16) float s_d[2][NQ][CPB][4];  // delta (softplus'd in place)
+    __shared__ __align__(16) float s_u[2][CPB][TT];  // u, then y + D u in place (swizzled pieces)
+    __shared__ __align__(16) float s_d[2][CPB][TT];  // delta (softplus'd in place)
     __shared__ __align__(16) float s_B[2][TT][N];
     __shared__ __align__(16) float s_C[2][TT][N];
 
@@ -259,9 +262,8 @@ __global__ __launch_bounds__(256, 3) void mamba1_scan_tm16(Mamba1Params p) {
     const u32x4_t rd = buf_words(p.dl + (int64_t)b * p.dl_sb, row_bytes);
     const __amdgpu_buffer_rsrc_t rz = buf_rsrc(GATE ? p.z + (int64_t)b * p.z_sb : p.u, row_bytes);
     const __amdgpu_buffer_rsrc_t ry = buf_rsrc(p.y + (int64_t)b * p.y_sb, row_bytes);
-    // DMA mapping: wave w moves pieces q = 2 w, 2 w + 1 of u and delta; lane i
-    // is channel d0 + i
-    const bool lvalid = d0 + lane < p.D;
+    // 16-byte piece q of row r sits at float offset 4 (q ^ (r % 8)) of the row
+    auto slot = [](int r, int q) { return 4 * (q ^ (r & 7)); };
     // a byte offset, or kOut where `ok` fails, as a plain select: kept opaque
     // so that the compiler neither branches around the access nor duplicates
     // it (each access below is one instruction on every path)
@@ -271,13 +273,16 @@ __global__ __launch_bounds__(256, 3) void mamba1_scan_tm16(Mamba1Params p) {
         return r;
     };
     const uint32_t sd = (uint32_t)p.u_sd;
+    // DMA mapping: wave w moves rows 16 w .. 16 w + 15 (its own channels) in
+    // two instructions of 8 rows; lane i -> row + i / 8, slot i % 8
     auto dma_tile = [&](int tk, int buf) {
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
-            const int q = 2 * wave + k, t = tk * TT + 4 * q;
-            const uint32_t off = sel(lvalid && t < p.L, ((uint32_t)(d0 + lane) * sd + (uint32_t)t) * 4u);
-            dma16(ru, (uint32_t)(uintptr_t)&s_u[buf][q][0][0], off, 0u);
-            dma16(rd, (uint32_t)(uintptr_t)&s_d[buf][q][0][0], off, 0u);
+            const int r0 = 16 * wave + 8 * k, r = r0 + (lane >> 3);
+            const int piece = (lane & 7) ^ (r & 7), t = tk * TT + 4 * piece;
+            const uint32_t off = sel(d0 + r < p.D && t < p.L, ((uint32_t)(d0 + r) * sd + (uint32_t)t) * 4u);
+            dma16(ru, (uint32_t)(uintptr_t)&s_u[buf][r0][0], off, 0u);
+            dma16(rd, (uint32_t)(uintptr_t)&s_d[buf][r0][0], off, 0u);
         }
     };
     // B/C mapping: thread -> state tid / 16, tokens 2 (tid % 16) + {0, 1}
@@ -336,19 +341,18 @@ __global__ __launch_bounds__(256, 3) void mamba1_scan_tm16(Mamba1Params p) {
         if (p.dbias || p.softplus) {
             // delta <- softplus(delta + bias), in place
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int e = tid + 256 * j, q = e >> 8;
-                float v = s_d[buf][q][ec][e & 3] + sbias;
-                if (p.softplus) v = m1_softplus(v);
-                s_d[buf][q][ec][e & 3] = v;
+            for (int k = 0; k < 2; ++k) {
+                float* v = &s_d[buf][ec][slot(ec, (et >> 2) + k)];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = p.softplus ? m1_softplus(v[e] + sbias) : v[e] + sbias;
             }
             __syncthreads();
         }
         // ---- the recurrence, 4 tokens per LDS read of delta and u
 #pragma unroll 2
         for (int q = 0; q < NQ; ++q) {
-            const float4 dv4 = *(const float4*)&s_d[buf][q][c][0];
-            const float4 uv4 = *(const float4*)&s_u[buf][q][c][0];
+            const float4 dv4 = *(const float4*)&s_d[buf][c][slot(c, q)];
+            const float4 uv4 = *(const float4*)&s_u[buf][c][slot(c, q)];
             float4 bq[4], cq[4];
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
@@ -383,14 +387,14 @@ __global__ __launch_bounds__(256, 3) void mamba1_scan_tm16(Mamba1Params p) {
 #pragma unroll
             for (int g = 0; g < 4; ++g) yq[g] = quad_sum(yq[g]);
             // every lane of the channel holds the sums: y + D u over u
-            *(float4*)&s_u[buf][q][c][0] = make_float4(__builtin_fmaf(Dd, uv[0], yq[0]), __builtin_fmaf(Dd, uv[1], yq[1]),
-                                                       __builtin_fmaf(Dd, uv[2], yq[2]), __builtin_fmaf(Dd, uv[3], yq[3]));
+            *(float4*)&s_u[buf][c][slot(c, q)] = make_float4(__builtin_fmaf(Dd, uv[0], yq[0]), __builtin_fmaf(Dd, uv[1], yq[1]),
+                                                             __builtin_fmaf(Dd, uv[2], yq[2]), __builtin_fmaf(Dd, uv[3], yq[3]));
         }
         __syncthreads();
         // ---- epilogue: y = (y + D u) silu(z), two 16-byte stores per thread
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
-            float4 o = *(const float4*)&s_u[buf][(et >> 2) + k][ec][0];
+            float4 o = *(const float4*)&s_u[buf][ec][slot(ec, (et >> 2) + k)];
             if (GATE) {
                 const uint4 zw = rzv[k];
                 const float zv[4] = {__uint_as_float(zw.x), __uint_as_float(zw.y), __uint_as_float(zw.z),
