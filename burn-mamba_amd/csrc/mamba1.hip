@@ -225,9 +225,8 @@ __global__ __launch_bounds__(16 * N, N <= 16 ? 3 : 1) void mamba1_scan_kernel(Ma
 //    per thread, two 16-byte pieces).
 //  * The scan writes y + D u over u in place; after a barrier the epilogue
 //    multiplies by silu(z) and stores.
-// Per tile: a barrier once the tile's loads have landed, one after the scan
-// (and one after the in-place softplus of delta when a bias or softplus is
-// requested).
+// Per tile one barrier, for the B/C tiles the waves share; everything else a
+// wave touches belongs to its own 16 channels.
 constexpr int kTm16Tile = 32;
 
 template <bool GATE>
@@ -328,9 +327,14 @@ __global__ __launch_bounds__(256, 3) void mamba1_scan_tm16(Mamba1Params p) {
             s_B[buf][bt + e][bn] = rB[e];
             s_C[buf][bt + e][bn] = rC[e];
         }
-        // this tile's direct-to-LDS loads: at most the previous tile's two
-        // stores and this tile's two z loads were issued after them (tile 0's
-        // were waited for before the first tile)
+        // this wave's direct-to-LDS loads of the tile: at most the previous
+        // tile's two stores and this tile's two z loads were issued after them
+        // (tile 0's were waited for before the first tile).  u, delta and the
+        // outputs of a channel are touched by its own wave only (DMA rows,
+        // scan lanes and store threads of wave w are channels 16 w .. 16 w +
+        // 15), so the one barrier per tile is for B/C: every wave's writes of
+        // this tile's B/C are visible, and every wave is done with the buffer
+        // the next tile's B/C will overwrite
         if (GATE)
             __builtin_amdgcn_s_waitcnt(0xF74);  // vmcnt(4) expcnt(7) lgkmcnt(15)
         else
@@ -346,7 +350,6 @@ __global__ __launch_bounds__(256, 3) void mamba1_scan_tm16(Mamba1Params p) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) v[e] = p.softplus ? m1_softplus(v[e] + sbias) : v[e] + sbias;
             }
-            __syncthreads();
         }
         // ---- the recurrence, 4 tokens per LDS read of delta and u
 #pragma unroll 2
@@ -390,8 +393,8 @@ __global__ __launch_bounds__(256, 3) void mamba1_scan_tm16(Mamba1Params p) {
             *(float4*)&s_u[buf][c][slot(c, q)] = make_float4(__builtin_fmaf(Dd, uv[0], yq[0]), __builtin_fmaf(Dd, uv[1], yq[1]),
                                                              __builtin_fmaf(Dd, uv[2], yq[2]), __builtin_fmaf(Dd, uv[3], yq[3]));
         }
-        __syncthreads();
         // ---- epilogue: y = (y + D u) silu(z), two 16-byte stores per thread
+        // (the wave's own rows: its LDS accesses complete in program order)
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
             float4 o = *(const float4*)&s_u[buf][ec][slot(ec, (et >> 2) + k)];
