@@ -385,7 +385,7 @@ __global__ __launch_bounds__(256, 3) void mamba1_scan_tm16(Mamba1Params p) {
                 h[1] = __builtin_fmaf(h[1], a1, du * bq[g].y);
                 h[2] = __builtin_fmaf(h[2], a2, du * bq[g].z);
                 h[3] = __builtin_fmaf(h[3], a3, du * bq[g].w);
-                yq[g] = __builtin_fmaf(cq[g].x, h[0], cq[g].y * h[1]) + __builtin_fmaf(cq[g].z, h[2], cq[g].w * h[3]);
+                yq[g] = __builtin_fmaf(cq[g].w, h[3], __builtin_fmaf(cq[g].z, h[2], __builtin_fmaf(cq[g].y, h[1], cq[g].x * h[0])));
             }
 #pragma unroll
             for (int g = 0; g < 4; ++g) yq[g] = quad_sum(yq[g]);
