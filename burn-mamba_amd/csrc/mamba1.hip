@@ -352,7 +352,7 @@ __global__ __launch_bounds__(256, 3) void mamba1_scan_tm16(Mamba1Params p) {
             }
         }
         // ---- the recurrence, 4 tokens per LDS read of delta and u
-#pragma unroll 2
+#pragma unroll
         for (int q = 0; q < NQ; ++q) {
             const float4 dv4 = *(const float4*)&s_d[buf][c][slot(c, q)];
             const float4 uv4 = *(const float4*)&s_u[buf][c][slot(c, q)];
