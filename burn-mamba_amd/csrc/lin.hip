@@ -37,10 +37,10 @@ __device__ __forceinline__ lin_f32x16_t lin_mfma(lin_bf16x8_t a, lin_bf16x8_t b,
 #define MAMBA_LIN_NW_BIGM 8     // waves per workgroup for four or eight 32-row tiles
 #endif
 #ifndef MAMBA_LIN_U1
-#define MAMBA_LIN_U1 5          // k-steps per pipeline stage for one 32-row tile
+#define MAMBA_LIN_U1 3          // k-steps per pipeline stage for one 32-row tile
 #endif
 #ifndef MAMBA_LIN_U2
-#define MAMBA_LIN_U2 5          // k-steps per pipeline stage for two 32-row tiles
+#define MAMBA_LIN_U2 3          // k-steps per pipeline stage for two 32-row tiles
 #endif
 #ifndef MAMBA_LIN_NT
 #define MAMBA_LIN_NT 0          // 1: weight loads carry the non-temporal hint (read once)
@@ -56,17 +56,21 @@ struct LinStage {
     lin_bf16x8_t a[U][MT];
 };
 
+// Operand blocks through buffer resources (scalar base, 32-bit byte offsets):
+// a load's address costs no 64-bit VGPR pair, which keeps the wave within the
+// register budget of four waves per SIMD.
+__device__ __forceinline__ lin_bf16x8_t lin_ld(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(lin_bf16x8_t, buf_ld16(r, off));
+}
+
 template <int MT>
-__device__ __forceinline__ void lin_load(LinStage<MT>& st, const lin_bf16x8_t* Wj, const lin_bf16x8_t* Ap, int s) {
+__device__ __forceinline__ void lin_load(LinStage<MT>& st, __amdgpu_buffer_rsrc_t rw, __amdgpu_buffer_rsrc_t ra,
+                                         uint32_t lo, int s) {
 #pragma unroll
     for (int u = 0; u < LinStage<MT>::U; ++u) {
-#if MAMBA_LIN_NT
-        st.w[u] = __builtin_nontemporal_load(Wj + (int64_t)(s + u) * 64);
-#else
-        st.w[u] = Wj[(int64_t)(s + u) * 64];
-#endif
+        st.w[u] = lin_ld(rw, (uint32_t)(s + u) * 1024u + lo);
 #pragma unroll
-        for (int i = 0; i < MT; ++i) st.a[u][i] = Ap[((int64_t)(s + u) * MT + i) * 64];
+        for (int i = 0; i < MT; ++i) st.a[u][i] = lin_ld(ra, ((uint32_t)(s + u) * MT + i) * 1024u + lo);
     }
 }
 
@@ -88,8 +92,10 @@ __global__ __launch_bounds__(64 * NW) void lin_stream(LinParams p) {
     const int z0 = (KS * z) / p.S, z1 = (KS * (z + 1)) / p.S;
     const int s0 = z0 + ((z1 - z0) * wave) / NW, s1 = z0 + ((z1 - z0) * (wave + 1)) / NW;
 
-    const lin_bf16x8_t* Wj = p.W + (int64_t)j * KS * 64 + lane;
-    const lin_bf16x8_t* Ap = p.A + lane;
+    // this tile's column of weight blocks, and the activation blocks
+    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(p.W + (int64_t)j * KS * 64, (uint32_t)KS * 1024u);
+    const __amdgpu_buffer_rsrc_t ra = buf_rsrc(p.A, (uint32_t)KS * MT * 1024u);
+    const uint32_t lo = (uint32_t)lane * 16u;
     lin_f32x16_t acc[MT];
 #pragma unroll
     for (int i = 0; i < MT; ++i)
@@ -106,22 +112,22 @@ __global__ __launch_bounds__(64 * NW) void lin_stream(LinParams p) {
         const int rot = MAMBA_LIN_ROTATE ? (int)(blockIdx.x % (unsigned)nstage) : 0;
         auto kstep = [&](int st) { int q = st + rot; q -= q >= nstage ? nstage : 0; return s0 + U * q; };
         LinStage<MT> sa, sb;
-        lin_load<MT>(sa, Wj, Ap, kstep(0));
+        lin_load<MT>(sa, rw, ra, lo, kstep(0));
         for (int st = 0; st < nstage; st += 2) {
             const bool more1 = st + 1 < nstage;
-            if (more1) lin_load<MT>(sb, Wj, Ap, kstep(st + 1));
+            if (more1) lin_load<MT>(sb, rw, ra, lo, kstep(st + 1));
             lin_compute<MT>(sa, acc);
             if (more1) {
-                if (st + 2 < nstage) lin_load<MT>(sa, Wj, Ap, kstep(st + 2));
+                if (st + 2 < nstage) lin_load<MT>(sa, rw, ra, lo, kstep(st + 2));
                 lin_compute<MT>(sb, acc);
             }
         }
         s = s0 + nstage * U;
     }
     for (; s < s1; ++s) {
-        const lin_bf16x8_t w = Wj[(int64_t)s * 64];
+        const lin_bf16x8_t w = lin_ld(rw, (uint32_t)s * 1024u + lo);
 #pragma unroll
-        for (int i = 0; i < MT; ++i) acc[i] = lin_mfma(Ap[((int64_t)s * MT + i) * 64], w, acc[i]);
+        for (int i = 0; i < MT; ++i) acc[i] = lin_mfma(lin_ld(ra, ((uint32_t)s * MT + i) * 1024u + lo), w, acc[i]);
     }
 
     // cross-wave reduction through LDS, two 32-row tiles at a time
