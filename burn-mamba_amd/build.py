@@ -34,6 +34,7 @@ CFLAGS = [
 FILE_FLAGS = {
     "ssd2_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "ssd3_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "mamba3_fused.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     # the decode products: accumulators in VGPRs keep a wave within 128
     # registers (four waves per SIMD)
     "lin.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],

@@ -18,27 +18,10 @@
 // The cumulative angle is carried wrapped to [-pi, pi] at every position (the
 // same cos/sin as the reference's unwrapped f32 cumsum, without its drift on
 // long sequences).
-#include "common.h"
+#include "mamba3_internal.h"
 
 namespace mamba {
 
-struct M3PrepParams {
-    int nb, L, H, P, G, N, M, R, A;
-    bool proj_bf16, io_bf16;
-    const void* proj; int64_t proj_sb, proj_sl;
-    const float* ssm; float* kst; float* vst; const float* ang; float* ang_out;
-    const float* dt_bias; float a_floor, dt_lo, dt_hi, span;
-    const float* bnw; const float* cnw; const float* bbias; const float* cbias; const float* mx;
-    void* v; void* Bo; void* Co;
-    float* da; float* gm; float* sc;
-    float* h0;
-};
-
-__device__ __forceinline__ float m3p_softplus(float x) { return x > 18.f ? x : log1pf(__expf(x)); }
-__device__ __forceinline__ float m3p_wrap(float a) {
-    const float two_pi = 6.28318530717958647692f;
-    return a - rintf(a * (1.f / two_pi)) * two_pi;
-}
 __device__ __forceinline__ float m3p_ld(const M3PrepParams& p, int b, int l, int i) {
     const int64_t off = (int64_t)b * p.proj_sb + (int64_t)l * p.proj_sl + i;
     return p.proj_bf16 ? bf16_to_f32(static_cast<const bf16_t*>(p.proj)[off]) : static_cast<const float*>(p.proj)[off];
@@ -339,36 +322,6 @@ template <> __device__ __forceinline__ void m3_st4<bf16_t>(bf16_t* q, const floa
     *(uint2*)q = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
 }
 
-// Lane exchanges inside aligned groups of a wave, without LDS addressing:
-// DPP for the quad and 16-lane-row patterns, ds_swizzle (bit-mask mode) for
-// the other xor distances below 32.
-template <int CTRL>
-__device__ __forceinline__ float m3_dpp(float x) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
-}
-template <int K>
-__device__ __forceinline__ float m3_xor(float x) {  // value of lane (lane ^ K), K < 32
-    if constexpr (K == 1) return m3_dpp<0xB1>(x);   // quad_perm [1, 0, 3, 2]
-    else if constexpr (K == 2) return m3_dpp<0x4E>(x);  // quad_perm [2, 3, 0, 1]
-    else if constexpr (K == 8) return m3_dpp<0x128>(x);  // row_ror:8 (lane ^ 8 inside a 16-lane row)
-    else return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x1F | (K << 10)));
-}
-// sum over an aligned group of G lanes (G a power of two <= 32), in every lane
-template <int G>
-__device__ __forceinline__ float m3_group_sum(float x) {
-    if constexpr (G >= 32) x += m3_xor<16>(x);
-    if constexpr (G >= 16) x += m3_dpp<0x140>(x);  // row_mirror: i <-> 15 - i
-    if constexpr (G >= 8) x += m3_dpp<0x141>(x);   // row_half_mirror: i <-> 7 - i (per 8)
-    if constexpr (G >= 4) x += m3_dpp<0x1B>(x);    // quad_perm [3, 2, 1, 0]
-    if constexpr (G >= 2) x += m3_dpp<0xB1>(x);    // quad_perm [1, 0, 3, 2]
-    return x;
-}
-
-// tanh from one exponential: sign(x) (1 - e) / (1 + e), e = exp(-2 |x|) <= 1
-__device__ __forceinline__ float m3_tanh(float x) {
-    const float e = __expf(-2.f * fabsf(x));
-    return copysignf((1.f - e) / (1.f + e), x);
-}
 __device__ __forceinline__ double m3_wrap_d(double a) {
     const double two_pi = 6.283185307179586476925286766559;
     return a - rint(a / two_pi) * two_pi;
@@ -758,7 +711,8 @@ __global__ __launch_bounds__(256) void mamba3_finish_kernel(M3FinishParams p) {
             if (pp < p.P) {
                 const int64_t yi = (((bl * p.YM + m) * p.H + h) * p.P) + pp;
                 const int64_t vi = (((bl * p.M + m) * p.H + h) * p.P) + pp;
-                o[k] = m3f_ld(p.io_bf16, p.y, yi) + Dv * m3f_ld(p.io_bf16, p.v, vi);
+                o[k] = m3f_ld(p.io_bf16, p.y, yi);
+                if (p.v) o[k] += Dv * m3f_ld(p.io_bf16, p.v, vi);
                 ss += o[k] * o[k];
             }
         }
@@ -786,7 +740,7 @@ __global__ __launch_bounds__(256) void mamba3_finish_kernel(M3FinishParams p) {
 
 constexpr int kM3PrepTS = 32;
 
-static int m3_prep_params(const mamba3_prep_args* a, M3PrepParams* out) {
+int m3_prep_params(const mamba3_prep_args* a, M3PrepParams* out, bool need_outputs) {
     MAMBA_CHECK_ARG(a != nullptr, "args is NULL");
     MAMBA_CHECK_ARG(a->batch > 0 && a->seqlen > 0 && a->nheads > 0 && a->headdim > 0 && a->ngroups > 0,
                     "sizes must be >= 1");
@@ -800,9 +754,10 @@ static int m3_prep_params(const mamba3_prep_args* a, M3PrepParams* out) {
                     "rope_dim must be even and in [0, dstate]");
     MAMBA_CHECK_ARG(a->angle_out && a->angle_out != a->angle, "angle_out is required and must not alias angle");
     MAMBA_CHECK_ARG(a->proj && a->ssm_state && a->k_state && a->v_state && a->angle && a->dt_bias &&
-                        a->b_norm_w && a->c_norm_w && a->b_bias && a->c_bias && a->v && a->B && a->C &&
-                        a->da && a->gamma && a->scale && a->initial_state,
-                    "proj, cache, parameters and every output are required");
+                        a->b_norm_w && a->c_norm_w && a->b_bias && a->c_bias && a->initial_state,
+                    "proj, cache, parameters and initial_state are required");
+    MAMBA_CHECK_ARG(!need_outputs || (a->v && a->B && a->C && a->da && a->gamma && a->scale),
+                    "v, B, C, da, gamma and scale are required");
     MAMBA_CHECK_ARG(a->mimo == 1 || a->mimo_x, "mimo_x is required when mimo > 1");
     MAMBA_CHECK_ARG(a->proj_dtype == MAMBA_F32 || a->proj_dtype == MAMBA_BF16, "bad proj_dtype");
     MAMBA_CHECK_ARG(a->io_dtype == MAMBA_F32 || a->io_dtype == MAMBA_BF16, "bad io_dtype");
@@ -828,6 +783,15 @@ using namespace mamba;
 
 // The fast path needs 16-byte aligned vector access to proj rows (B/C and x
 // slices) and 4-wide headdim.
+void mamba::m3_launch_seed(const M3PrepParams& p, hipStream_t s) {
+    // rows per workgroup: at most kSeedE state elements per thread, at most P rows
+    // (LDS <= M (P + N) floats, 32 KB at the limits M = 16, P = N = 256)
+    int rows_per = (256 * kSeedE) / p.N > 0 ? (256 * kSeedE) / p.N : 1;
+    rows_per = rows_per < p.P ? rows_per : p.P;
+    hipLaunchKernelGGL(mamba3_seed_kernel, dim3(p.nb * p.H, (p.P + rows_per - 1) / rows_per), dim3(256),
+                       (size_t)p.M * (rows_per + p.N) * sizeof(float), s, p, rows_per);
+}
+
 static bool m3_prep_fast(const M3PrepParams& p) {
     if (((uintptr_t)p.proj & 15u) != 0) return false;
     if (p.proj_sl % 8 != 0 || (p.nb > 1 && p.proj_sb % 8 != 0)) return false;
@@ -845,13 +809,13 @@ static int m3_nseg(const M3PrepParams& p) { return (p.L + kM3Seg - 1) / kM3Seg; 
 
 extern "C" int mamba3_prep_fast_path(const mamba3_prep_args* a) {
     M3PrepParams p;
-    if (m3_prep_params(a, &p) != MAMBA_OK) return -1;
+    if (m3_prep_params(a, &p, true) != MAMBA_OK) return -1;
     return m3_prep_fast(p) ? 1 : 0;
 }
 
 extern "C" size_t mamba3_prep_workspace_size(const mamba3_prep_args* a) {
     M3PrepParams p;
-    if (m3_prep_params(a, &p) != MAMBA_OK) return 0;
+    if (m3_prep_params(a, &p, true) != MAMBA_OK) return 0;
     const int nseg = m3_nseg(p);
     if (!m3_prep_fast(p) || nseg == 1) return 0;
     return (size_t)p.nb * nseg * p.H * p.A * sizeof(double);
@@ -883,7 +847,7 @@ static void m3_launch_fast(const M3PrepParams& p, double* tot, hipStream_t s) {
 extern "C" int mamba3_prep_fwd(const mamba3_prep_args* a, void* workspace, size_t workspace_bytes,
                                mamba_stream_t stream) {
     M3PrepParams p;
-    const int st = m3_prep_params(a, &p);
+    const int st = m3_prep_params(a, &p, true);
     if (st != MAMBA_OK) return st;
     hipStream_t s = (hipStream_t)stream;
     const size_t need = mamba3_prep_workspace_size(a);
@@ -891,14 +855,7 @@ extern "C" int mamba3_prep_fwd(const mamba3_prep_args* a, void* workspace, size_
                     "workspace too small: mamba3_prep_workspace_size() bytes are required");
     MAMBA_CHECK_ARG(need == 0 || ((uintptr_t)workspace & 7u) == 0, "workspace must be 8-byte aligned");
     MAMBA_CHECK_ARG((int64_t)p.nb * p.H * m3_nseg(p) < (1ll << 31), "too many (batch, head, segment) items");
-    {
-        // rows per workgroup: at most kSeedE state elements per thread, at most P rows
-        // (LDS <= M (P + N) floats, 32 KB at the limits M = 16, P = N = 256)
-        int rows_per = (256 * kSeedE) / p.N > 0 ? (256 * kSeedE) / p.N : 1;
-        rows_per = rows_per < p.P ? rows_per : p.P;
-        hipLaunchKernelGGL(mamba3_seed_kernel, dim3(p.nb * p.H, (p.P + rows_per - 1) / rows_per), dim3(256),
-                           (size_t)p.M * (rows_per + p.N) * sizeof(float), s, p, rows_per);
-    }
+    m3_launch_seed(p, s);
     MAMBA_CHECK_LAUNCH();
     if (m3_prep_fast(p)) {
         double* tot = (double*)workspace;
@@ -940,7 +897,8 @@ extern "C" int mamba3_finish_fwd(const mamba3_finish_args* a, mamba_stream_t str
                     "sizes must be >= 1 and headdim <= 256");
     MAMBA_CHECK_ARG(a->mimo >= 1 && a->mimo <= 16, "mimo must be in [1, 16]");
     MAMBA_CHECK_ARG(a->mimo == 1 || (a->mimo_z && a->mimo_o), "mimo_z and mimo_o are required when mimo > 1");
-    MAMBA_CHECK_ARG(a->y_ssd && a->v && a->z && a->out, "y_ssd, v, z and out are required");
+    MAMBA_CHECK_ARG(a->y_ssd && a->z && a->out, "y_ssd, z and out are required");
+    MAMBA_CHECK_ARG(a->v || !a->D, "v is required when D is given");
     MAMBA_CHECK_ARG((a->io_dtype == MAMBA_F32 || a->io_dtype == MAMBA_BF16) &&
                         (a->z_dtype == MAMBA_F32 || a->z_dtype == MAMBA_BF16) &&
                         (a->out_dtype == MAMBA_F32 || a->out_dtype == MAMBA_BF16),

@@ -1,0 +1,133 @@
+// Shared pieces of the Mamba-3 single-SSD MFMA scans (bf16 operands, f32
+// accumulators, headdim 64 in two 32-wide halves, dstate 128, 128 fused
+// positions per chunk): the MFMA helpers, the per-workgroup LDS layout and the
+// y tile of one wave.  Included by the SSD-seam kernel and by the fused
+// prologue + SSD kernel.
+#pragma once
+
+#include "common.h"
+
+namespace mamba {
+
+typedef __bf16 s3_bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 s3_bf16x4_t __attribute__((ext_vector_type(4)));
+typedef float s3_f32x16_t __attribute__((ext_vector_type(16)));
+
+constexpr float kLog2eS3 = 1.4426950408889634f;
+
+__device__ __forceinline__ s3_f32x16_t s3_mfma(s3_bf16x8_t a, s3_bf16x8_t b, s3_f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ s3_f32x16_t s3_zero() {
+    s3_f32x16_t z;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) z[v] = 0.f;
+    return z;
+}
+
+// Raw buffer access (gfx9 descriptor word 3): offsets at or past `bytes`
+// read as zero and drop on store, which clips chunks at the sequence end.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t s3_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 s3_bld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ float s3_bld4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+
+__device__ __forceinline__ float s3_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float s3_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// LDS of one workgroup (about 83 KB at QF = 128).
+template <int QF>
+struct __align__(16) Ssd3Lds {
+    bf16_t xT[32][QF + 8];      // v^T of the chunk (headdim half x positions)
+    bf16_t xTw[32][QF + 8];     // w_j v^T[p][j], the state GEMM's A operand
+    bf16_t B[QF][136];          // B rows of the chunk (positions x dstate)
+    bf16_t h[2][32][136];       // state entering the chunk (bf16 MFMA operand), double-buffered
+    bf16_t y[4][32][40];        // per-wave y tile staging
+    float cs2[QF];              // within-chunk cumulative da, log2 units
+    float sc[QF], gm[QF];       // scale and gamma per position
+    float st[QF];               // step index of each position (read per chunk: keeps the
+                                // diagonal masks in the loop rather than hoisted to SGPRs)
+    float w[QF];                // scale_j exp(cs_end - cs_j)
+    float f[QF / 32 - 1][QF];   // scale_j exp(cs_r0 - cs_j) for tile starts r0 = 32, 64, ..
+    float red[4], anc[QF / 32];
+};
+
+// y of output tile IT (positions 32 IT .. 32 IT + 31 of the chunk) for this
+// wave's headdim half, in one accumulator (lane = column i, so the per-i
+// factors are per-lane scalars applied between the MFMA chains):
+//   y  = C_i.h_in;  y *= exp(cs_r0);  y += lower tiles (f_IT[j]);
+//   y *= exp(cs_i - cs_r0);  y += diagonal tile (exact per-(j, i) factor)
+template <int QF, int IT>
+__device__ __forceinline__ void ssd3_y_tile(Ssd3Lds<QF>& S, const s3_bf16x8_t (&cfr)[8], int cur, int r, int half,
+                                            s3_f32x16_t& y) {
+    constexpr int NK = 8;
+    const int il = IT * 32 + r;
+    const float cs_i = S.cs2[il];
+    const float cs_r0 = S.cs2[IT * 32];
+    const float gm_i = S.gm[il];
+    const float ti = S.st[il];  // chunks and tiles start on step boundaries
+    y = s3_zero();
+#pragma unroll
+    for (int kn = 0; kn < NK; ++kn)
+        y = s3_mfma(*(const s3_bf16x8_t*)&S.h[cur][r][kn * 16 + 8 * half], cfr[kn], y);
+    {
+        const float e0 = __builtin_amdgcn_exp2f(cs_r0);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) y[v] *= e0;
+    }
+#pragma unroll
+    for (int jt = 0; jt <= IT; ++jt) {
+        s3_f32x16_t d = s3_zero();
+#pragma unroll
+        for (int kn = 0; kn < NK; ++kn)
+            d = s3_mfma(*(const s3_bf16x8_t*)&S.B[jt * 32 + r][kn * 16 + 8 * half], cfr[kn], d);
+        // d[v] = C_i . B_j for j = 32 jt + 8 (v / 4) + 4 half + v % 4
+        float fac[16];
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+            const int j0 = jt * 32 + 8 * gq + 4 * half;
+            if (jt < IT) {
+                const float4 fv = *(const float4*)&S.f[IT - 1][j0];
+                fac[4 * gq] = fv.x; fac[4 * gq + 1] = fv.y; fac[4 * gq + 2] = fv.z; fac[4 * gq + 3] = fv.w;
+            } else {
+                const float4 sv = *(const float4*)&S.sc[j0];
+                const float4 cv = *(const float4*)&S.cs2[j0];
+                const float4 tv = *(const float4*)&S.st[j0];
+                const float sa[4] = {sv.x, sv.y, sv.z, sv.w}, ca[4] = {cv.x, cv.y, cv.z, cv.w};
+                const float ta[4] = {tv.x, tv.y, tv.z, tv.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float tj = ta[e];
+                    // exponent clamped at 0: only the tj < ti entries are kept
+                    const float k = sa[e] * __builtin_amdgcn_exp2f(fminf(cs_i - ca[e], 0.f));
+                    fac[4 * gq + e] = tj < ti ? k : (tj == ti ? gm_i : 0.f);
+                }
+            }
+        }
+        if (jt == IT) {
+            const float el = __builtin_amdgcn_exp2f(cs_i - cs_r0);
+#pragma unroll
+            for (int v = 0; v < 16; ++v) y[v] *= el;
+        }
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            s3_bf16x8_t bop;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) bop[e] = (__bf16)(d[8 * kk + e] * fac[8 * kk + e]);
+            // v^T[p][j] in the same permuted k order: j = 32 jt + 16 kk + 4 half + {0..3, 8..11}
+            const int j0 = jt * 32 + 16 * kk + 4 * half;
+            const s3_bf16x4_t lo = *(const s3_bf16x4_t*)&S.xT[r][j0];
+            const s3_bf16x4_t hi = *(const s3_bf16x4_t*)&S.xT[r][j0 + 8];
+            const s3_bf16x8_t a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            y = s3_mfma(a, bop, y);
+        }
+    }
+}
+
+}  // namespace mamba

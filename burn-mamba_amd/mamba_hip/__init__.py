@@ -20,3 +20,5 @@ from .mamba3 import step_ssm as mamba3_step_ssm, step_ssm_args as mamba3_step_ss
 from .mamba3 import finish_fwd as mamba3_finish_fwd, prep_fwd as mamba3_prep_fwd  # noqa: F401
 from .mamba3 import prep_args as mamba3_prep_args, prep_fast_path as mamba3_prep_fast_path  # noqa: F401
 from .mamba3 import double_inputs as mamba3_double_inputs  # noqa: F401
+from .mamba3 import fused_args as mamba3_fused_args, fused_supported as mamba3_fused_supported  # noqa: F401
+from .mamba3 import fused_run as mamba3_fused_run, ssd_fused_fwd as mamba3_ssd_fused_fwd  # noqa: F401

@@ -149,6 +149,10 @@ class Mamba3PrepArgs(ctypes.Structure):
     ]
 
 
+class Mamba3FusedArgs(ctypes.Structure):
+    _fields_ = [("prep", Mamba3PrepArgs), ("D", c_vp), ("y", c_vp), ("final_state", c_vp)]
+
+
 class Mamba3FinishArgs(ctypes.Structure):
     _fields_ = [
         ("batch", c_i32), ("seqlen", c_i32), ("nheads", c_i32), ("headdim", c_i32), ("mimo", c_i32),
@@ -273,6 +277,9 @@ _SIGNATURES = {
     "mamba3_prep_workspace_size": ([ctypes.POINTER(Mamba3PrepArgs)], ctypes.c_size_t),
     "mamba3_prep_fwd": ([ctypes.POINTER(Mamba3PrepArgs), c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),
     "mamba3_finish_fwd": ([ctypes.POINTER(Mamba3FinishArgs), c_vp], ctypes.c_int),
+    "mamba3_ssd_fused_supported": ([ctypes.POINTER(Mamba3FusedArgs)], ctypes.c_int),
+    "mamba3_ssd_fused_fwd": ([ctypes.POINTER(Mamba3FusedArgs), c_vp], ctypes.c_int),
+    "mamba3_ssd_fused_fwd_timed": ([ctypes.POINTER(Mamba3FusedArgs), c_vp, c_vp, c_vp], ctypes.c_int),
     "mamba3_double_inputs": ([ctypes.POINTER(Mamba3DoubleInputsArgs), c_vp], ctypes.c_int),
     "mamba3_step_ssm_timed": ([ctypes.POINTER(Mamba3StepArgs), c_vp, c_vp, c_vp], ctypes.c_int),
     "mamba1_scan_step_timed": ([ctypes.POINTER(Mamba1StepArgs), c_vp, c_vp, c_vp], ctypes.c_int),

@@ -23,9 +23,9 @@ from typing import Optional
 import torch
 
 from . import _lib
-from ._lib import Mamba3FinishArgs, Mamba3PrepArgs, Mamba3StepArgs, check
+from ._lib import Mamba3FinishArgs, Mamba3FusedArgs, Mamba3PrepArgs, Mamba3StepArgs, check
 from .ssd import _dtype_code, _raw_events, _stream
-from .step import packed_weight, prefill_mm, step_mm, step_mm_ok
+from .step import packed_weight, prefill_mm, prefill_mm_rows, step_mm, step_mm_ok
 
 
 @dataclass
@@ -168,23 +168,27 @@ def step_ssm(args: Mamba3StepArgs, device, events=None):
 
 
 def prep_args(cfg: Mamba3Config, proj: torch.Tensor, cache: Mamba3Cache, *, dt_bias, b_norm_w, c_norm_w, b_bias,
-              c_bias, mimo_x=None, io_dtype=None) -> Mamba3PrepArgs:
+              c_bias, mimo_x=None, io_dtype=None, outputs: bool = True) -> Mamba3PrepArgs:
     """The mamba3_prep_args of one call, with its outputs allocated (kept on
-    the struct as `outputs` and `angle_out`)."""
+    the struct as `outputs` and `angle_out`); outputs=False allocates only the
+    initial state (the fused scan's prologue arguments)."""
     b, L, row = proj.shape
     H, P, N, M, G = cfg.nheads, cfg.per_head_dim, cfg.state_rank, cfg.mimo_rank, cfg.ngroups
     if row != cfg.d_in_proj or proj.stride(2) != 1:
         raise _lib.MambaHipError(f"proj must be [b, l, {cfg.d_in_proj}] with a unit inner stride")
     dev, iod = proj.device, io_dtype or proj.dtype
-    out = dict(v=torch.empty((b, L, M, H, P), device=dev, dtype=iod),
-               B=torch.empty((b, L, M, H, N), device=dev, dtype=iod),
-               C=torch.empty((b, L, M, H, N), device=dev, dtype=iod),
-               da=torch.empty((b, L, H), device=dev), gamma=torch.empty((b, L, H), device=dev),
-               scale=torch.empty((b, L, H), device=dev), h0=torch.empty((b, H, P, N), device=dev))
+    out = dict(h0=torch.empty((b, H, P, N), device=dev))
+    if outputs:
+        out.update(v=torch.empty((b, L, M, H, P), device=dev, dtype=iod),
+                   B=torch.empty((b, L, M, H, N), device=dev, dtype=iod),
+                   C=torch.empty((b, L, M, H, N), device=dev, dtype=iod),
+                   da=torch.empty((b, L, H), device=dev), gamma=torch.empty((b, L, H), device=dev),
+                   scale=torch.empty((b, L, H), device=dev))
     angle_out = torch.empty_like(cache.angle_bha)
     a = Mamba3PrepArgs()
     a.batch, a.seqlen, a.nheads, a.headdim, a.ngroups, a.dstate, a.mimo = b, L, H, P, G, N, M
-    a.rope_dim, a.proj_dtype, a.io_dtype = cfg.rope_dim, _dtype_code(proj), _dtype_code(out["v"])
+    a.rope_dim, a.proj_dtype = cfg.rope_dim, _dtype_code(proj)
+    a.io_dtype = _dtype_code(out["v"]) if outputs else _dtype_code(torch.empty(0, dtype=iod))
     a.proj, a.proj_sb, a.proj_sl = proj.data_ptr(), proj.stride(0), proj.stride(1)
     a.ssm_state = _f32c(cache.ssm_bhpr, "ssm_bhpr").data_ptr()
     a.k_state = _f32c(cache.k_state_bmhr, "k_state_bmhr").data_ptr()
@@ -195,8 +199,9 @@ def prep_args(cfg: Mamba3Config, proj: torch.Tensor, cache: Mamba3Cache, *, dt_b
     a.b_norm_w, a.c_norm_w = _f32c(b_norm_w, "b_norm_w").data_ptr(), _f32c(c_norm_w, "c_norm_w").data_ptr()
     a.b_bias, a.c_bias = _f32c(b_bias, "b_bias").data_ptr(), _f32c(c_bias, "c_bias").data_ptr()
     a.mimo_x = None if mimo_x is None else _f32c(mimo_x, "mimo_x").data_ptr()
-    a.v, a.B, a.C = out["v"].data_ptr(), out["B"].data_ptr(), out["C"].data_ptr()
-    a.da, a.gamma, a.scale = out["da"].data_ptr(), out["gamma"].data_ptr(), out["scale"].data_ptr()
+    if outputs:
+        a.v, a.B, a.C = out["v"].data_ptr(), out["B"].data_ptr(), out["C"].data_ptr()
+        a.da, a.gamma, a.scale = out["da"].data_ptr(), out["gamma"].data_ptr(), out["scale"].data_ptr()
     a.initial_state = out["h0"].data_ptr()
     a.outputs, a.angle_out_t = out, angle_out
     return a
@@ -225,16 +230,69 @@ def prep_fwd(cfg: Mamba3Config, proj: torch.Tensor, cache: Mamba3Cache, *, dt_bi
     return a.outputs
 
 
-def finish_fwd(cfg: Mamba3Config, y_ssd: torch.Tensor, v: torch.Tensor, z: torch.Tensor, *, D=None, mimo_z=None,
-               mimo_o=None, out_norm_w=None, out: Optional[torch.Tensor] = None):
+def fused_args(cfg: Mamba3Config, proj: torch.Tensor, cache: Mamba3Cache, *, dt_bias, b_norm_w, c_norm_w, b_bias,
+               c_bias, mimo_x=None, D=None) -> Mamba3FusedArgs:
+    """The mamba3_fused_args of one call: the prologue's arguments (without its
+    per-head outputs) and y [b, l, M, H, P] bf16 + the final state, allocated
+    and kept on the struct as `y_t`, `final_t`, `angle_out_t`."""
+    b, L, _ = proj.shape
+    H, P, N, M = cfg.nheads, cfg.per_head_dim, cfg.state_rank, cfg.mimo_rank
+    pa = prep_args(cfg, proj, cache, dt_bias=dt_bias, b_norm_w=b_norm_w, c_norm_w=c_norm_w, b_bias=b_bias,
+                   c_bias=c_bias, mimo_x=mimo_x, io_dtype=torch.bfloat16, outputs=False)
+    a = Mamba3FusedArgs()
+    a.prep = pa
+    y = torch.empty((b, L, M, H, P), device=proj.device, dtype=torch.bfloat16)
+    hT = torch.empty((b, H, P, N), device=proj.device)
+    a.D = None if D is None else _f32c(D, "D").data_ptr()
+    a.y, a.final_state = y.data_ptr(), hT.data_ptr()
+    a.y_t, a.final_t, a.angle_out_t, a.h0_t = y, hT, pa.angle_out_t, pa.outputs["h0"]
+    return a
+
+
+def fused_supported(args: Mamba3FusedArgs) -> int:
+    """1 if mamba3_ssd_fused_fwd runs for these arguments, 0 if the shape or
+    layout is outside the fused kernel, -1 if invalid."""
+    return int(_lib.lib().mamba3_ssd_fused_supported(ctypes.byref(args)))
+
+
+def fused_run(args: Mamba3FusedArgs, cache: Mamba3Cache, events=None):
+    """Launch mamba3_ssd_fused_fwd on the current stream; returns (y, final
+    state) and points the cache's angle at the new one."""
+    dev = args.y_t.device
+    L_ = _lib.lib()
+    if events is not None:
+        e0, e1 = _raw_events(events, dev)
+        check(L_.mamba3_ssd_fused_fwd_timed(ctypes.byref(args), _stream(dev), e0, e1), "mamba3_ssd_fused_fwd_timed")
+    else:
+        check(L_.mamba3_ssd_fused_fwd(ctypes.byref(args), _stream(dev)), "mamba3_ssd_fused_fwd")
+    cache.angle_bha = args.angle_out_t
+    return args.y_t, args.final_t
+
+
+def ssd_fused_fwd(cfg: Mamba3Config, proj: torch.Tensor, cache: Mamba3Cache, *, dt_bias, b_norm_w, c_norm_w,
+                  b_bias, c_bias, mimo_x=None, D=None, events=None):
+    """mamba3_ssd_fused_fwd: proj [b, l, d_in_proj] (bf16) -> (y [b, l, M, H, P]
+    bf16 = y_ssd + D v, final state [b, H, P, N] f32), the prologue fused into
+    the scan.  The cache's k_state / v_state / angle are replaced as by
+    prep_fwd; its ssm_bhpr is read (the caller stores the final state)."""
+    a = fused_args(cfg, proj, cache, dt_bias=dt_bias, b_norm_w=b_norm_w, c_norm_w=c_norm_w, b_bias=b_bias,
+                   c_bias=c_bias, mimo_x=mimo_x, D=D)
+    return fused_run(a, cache, events)
+
+
+def finish_fwd(cfg: Mamba3Config, y_ssd: torch.Tensor, v: Optional[torch.Tensor], z: torch.Tensor, *, D=None,
+               mimo_z=None, mimo_o=None, out_norm_w=None, out: Optional[torch.Tensor] = None):
     """mamba3_finish_fwd: y_ssd [b, l, Y, H, P] whose first M ranks are read (Y = M, or 2M
-    for the double pathway's call), v [b, l, M, H, P] (both contiguous); z [b, l, H*P] ->
-    [b, l, H*P]."""
-    b, L, M, H, P = v.shape
-    Y = y_ssd.shape[2]
-    if tuple(y_ssd.shape) != (b, L, Y, H, P) or Y < M:
+    for the double pathway's call), v [b, l, M, H, P] (both contiguous; v may be None
+    without D, as after the fused scan); z [b, l, H*P] -> [b, l, H*P]."""
+    b, L, Y, H, P = y_ssd.shape
+    M = cfg.mimo_rank
+    if Y < M or (v is not None and tuple(v.shape) != (b, L, M, H, P)):
         raise _lib.MambaHipError("y_ssd must be [b, l, Y >= M, H, P] matching v")
-    if not (y_ssd.is_contiguous() and v.is_contiguous() and y_ssd.dtype == v.dtype) or z.stride(2) != 1:
+    if v is None and D is not None:
+        raise _lib.MambaHipError("v is required with D")
+    if not (y_ssd.is_contiguous() and (v is None or (v.is_contiguous() and y_ssd.dtype == v.dtype))) \
+            or z.stride(2) != 1:
         raise _lib.MambaHipError("y_ssd / v must be contiguous with one dtype; z needs a unit inner stride")
     if out is None:
         out = torch.empty((b, L, H * P), device=y_ssd.device, dtype=y_ssd.dtype)
@@ -242,7 +300,7 @@ def finish_fwd(cfg: Mamba3Config, y_ssd: torch.Tensor, v: torch.Tensor, z: torch
     a.batch, a.seqlen, a.nheads, a.headdim, a.mimo = b, L, H, P, M
     a.y_ranks = Y
     a.io_dtype, a.z_dtype, a.out_dtype = _dtype_code(y_ssd), _dtype_code(z), _dtype_code(out)
-    a.y_ssd, a.v = y_ssd.data_ptr(), v.data_ptr()
+    a.y_ssd, a.v = y_ssd.data_ptr(), None if v is None else v.data_ptr()
     a.z, a.z_sb, a.z_sl = z.data_ptr(), z.stride(0), z.stride(1)
     for nm, t in (("D", D), ("mimo_z", mimo_z), ("mimo_o", mimo_o), ("out_norm_w", out_norm_w)):
         setattr(a, nm, None if t is None else _f32c(t, nm).data_ptr())
@@ -309,11 +367,13 @@ class Mamba3:
                            z(batch, c.nheads, c.per_head_dim), z(batch, c.nheads, c.num_rope_angles), pathway)
 
     def _in_proj(self, x: torch.Tensor):
+        """in_proj into rows padded to 8 elements (a strided [b, l, d_in_proj]
+        view), the layout the prologue's fast kernels read."""
         b, L, _ = x.shape
         wdt = self.in_proj_w.dtype
-        proj = prefill_mm(x.reshape(b * L, -1).to(wdt), self.in_proj_w).reshape(b, L, -1)
+        proj = prefill_mm_rows(x.reshape(b * L, -1).to(wdt), self.in_proj_w).reshape(b, L, -1)
         if self.in_proj_b is not None:
-            proj = proj + self.in_proj_b.to(wdt)
+            proj.add_(self.in_proj_b.to(wdt))
         return proj
 
     def _out_proj(self, y: torch.Tensor, x: torch.Tensor):
@@ -333,11 +393,23 @@ class Mamba3:
 
     def forward_single_ssd(self, x: torch.Tensor, cache: Optional[Mamba3Cache] = None, chunk_len: int = 64):
         """Mamba3::forward_single_ssd (single_ssd/single_ssd/mod.rs:44-360): in_proj /
-        out_proj on torch.mm; prep -> mamba_ssd3_fwd -> finish in between."""
+        out_proj on torch.mm; in between, the fused prologue + scan
+        (mamba3_ssd_fused_fwd) where its shape applies, else prep ->
+        mamba_ssd3_fwd; then finish."""
         from .ssd3 import ssd3_fwd
         if cache is None:
             cache = self.new_cache(x.shape[0])
         proj = self._in_proj(x)
+        if proj.dtype == torch.bfloat16:
+            fa = fused_args(self.cfg, proj, cache, dt_bias=self.dt_bias, b_norm_w=self.b_norm_w,
+                            c_norm_w=self.c_norm_w, b_bias=self.b_bias, c_bias=self.c_bias, mimo_x=self.mimo_x,
+                            D=self.D)
+            if fused_supported(fa) == 1:
+                y_ssd, hT = fused_run(fa, cache)
+                cache.ssm_bhpr = hT
+                y = finish_fwd(self.cfg, y_ssd, None, proj[:, :, :self.cfg.d_inner], mimo_z=self.mimo_z,
+                               mimo_o=self.mimo_o, out_norm_w=self.out_norm_w)
+                return self._out_proj(y, x), cache
         pr = prep_fwd(self.cfg, proj, cache, dt_bias=self.dt_bias, b_norm_w=self.b_norm_w, c_norm_w=self.c_norm_w,
                       b_bias=self.b_bias, c_bias=self.c_bias, mimo_x=self.mimo_x)
         y_ssd, hT = ssd3_fwd(pr["v"], pr["da"], pr["B"], pr["C"], pr["gamma"], pr["scale"], pr["h0"],

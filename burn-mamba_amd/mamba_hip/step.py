@@ -276,6 +276,21 @@ def prefill_mm(x2d: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     return torch.mm(x2d, wt.t())
 
 
+def prefill_mm_rows(x2d: torch.Tensor, w: torch.Tensor, align: int = 8) -> torch.Tensor:
+    """prefill_mm with each output row padded to a multiple of `align`
+    elements: the [M, d_out] view of an [M, d_pad] product whose weight copy
+    carries d_pad - d_out zero rows, so that every row of the result starts
+    16-byte aligned (the vector loads of the Mamba-3 prologue kernels need it).
+    Equal to prefill_mm when d_out is already a multiple of `align`."""
+    d_out = w.shape[1]
+    d_pad = -(-d_out // align) * align
+    if d_pad == d_out:
+        return prefill_mm(x2d, w)
+    wt = _derived(w, "_mamba_prefill_wt_pad",
+                  lambda t: torch.cat([t.t(), t.new_zeros((d_pad - d_out, t.shape[0]))]).contiguous())
+    return torch.mm(x2d, wt.t())[:, :d_out]
+
+
 def step_mm(x2d: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = None,
             workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
     """x2d [rows, d_in] @ w [d_in, d_out] for decode-sized rows (<= 256) through

@@ -401,7 +401,8 @@ typedef struct mamba3_finish_args {
     int32_t batch, seqlen, nheads, headdim, mimo;
     int32_t io_dtype, z_dtype, out_dtype;
     const void* y_ssd;                               /* [b, l, M, H, P] contiguous */
-    const void* v;                                   /* [b, l, M, H, P] contiguous */
+    const void* v;                                   /* [b, l, M, H, P] contiguous; */
+                                                     /* may be NULL when D is NULL  */
     const void* z;      int64_t z_sb, z_sl;          /* [b, l, H P]                */
     const float* D;                                  /* [H] or NULL                */
     const float* mimo_z; const float* mimo_o;        /* [H, M, P]; NULL if mimo == 1 */
@@ -412,6 +413,40 @@ typedef struct mamba3_finish_args {
 } mamba3_finish_args;
 
 int mamba3_finish_fwd(const mamba3_finish_args* args, mamba_stream_t stream);
+
+/* Mamba-3 prefill prologue fused into the single SSD: forward_single_ssd      */
+/* steps 2-7 and the D skip of step 9 (single_ssd/single_ssd/mod.rs:86-290) in */
+/* one scan kernel (after the beta-seed kernel of mamba3_prep_fwd).  The scan  */
+/* reads the raw in_proj row (x, group-form B / C, dd_dt, dd_A, lambda, the    */
+/* rotation channels) and forms, in its B / C tile loaders, the trapezoid      */
+/* coefficients, the QK-norm + bias, the cumulative-angle rotation and         */
+/* v = x mimo_x; no per-head v / B / C / coefficient tensor reaches HBM.       */
+/* Its output is y_ssd + D v per rank, for mamba3_finish_fwd with D = NULL.    */
+/* prep: the prologue's arguments as for mamba3_prep_fwd, except that its v,   */
+/* B, C, da, gamma and scale outputs are not used (may be NULL); its          */
+/* initial_state receives the seeded state; the cache tail (k_state, v_state, */
+/* angle_out) is written as by mamba3_prep_fwd.  Only the fast shape is       */
+/* provided (bf16 proj and y, headdim 64, dstate 128, mimo 2 / 4 / 8, 16-byte */
+/* aligned proj rows): mamba3_ssd_fused_supported says whether it applies;    */
+/* otherwise run mamba3_prep_fwd -> mamba_ssd3_fwd -> mamba3_finish_fwd.  No   */
+/* single counterpart in the reference (it replaces that sequence).           */
+typedef struct mamba3_fused_args {
+    mamba3_prep_args prep;
+    const float* D;                                  /* [H] or NULL                */
+    void* y;                                         /* [b, l, M, H, P] bf16 out,  */
+                                                     /* contiguous                 */
+    float* final_state;                              /* [b, H, P, N] f32 out; may  */
+                                                     /* alias prep.ssm_state       */
+} mamba3_fused_args;
+
+/* 1 if mamba3_ssd_fused_fwd runs for these arguments, 0 if the shape or      */
+/* layout is not the fused kernel's, -1 if the arguments are invalid.         */
+int mamba3_ssd_fused_supported(const mamba3_fused_args* args);
+int mamba3_ssd_fused_fwd(const mamba3_fused_args* args, mamba_stream_t stream);
+/* As mamba3_ssd_fused_fwd, recording the caller's HIP events around the      */
+/* seed and scan kernels (benchmark timing).                                   */
+int mamba3_ssd_fused_fwd_timed(const mamba3_fused_args* args, mamba_stream_t stream, void* event_start,
+                               void* event_stop);
 
 /* Mamba-3 double-SSD pathway (Mamba3::forward_double_ssd,                     */
 /* src/mamba3/double_ssd/double_ssd/mod.rs:40-369): its gamma call (gamma_t v_t, */

@@ -59,6 +59,7 @@ int main(void) {{ printf("%zu\\n", sizeof({struct_name})); {body} return 0; }}
                                              ("Mamba3StepArgs", "mamba3_step_args"),
                                              ("Mamba3PrepArgs", "mamba3_prep_args"),
                                              ("Mamba3FinishArgs", "mamba3_finish_args"),
+                                             ("Mamba3FusedArgs", "mamba3_fused_args"),
                                              ("Mamba3DoubleInputsArgs", "mamba3_double_inputs_args"),
                                              ("LinearArgs", "mamba_linear_args"),
                                              ("Mamba2LayerArgs", "mamba2_layer_args"),
@@ -104,6 +105,38 @@ def test_step_validation_needs_no_gpu():
     r = _lib.RmsNormArgs()
     r.rows, r.cols = 2, 8
     assert L.mamba_rmsnorm(ctypes.byref(r), None) == 1
+
+
+def test_fused_predicate_needs_no_gpu():
+    """mamba3_ssd_fused_supported validates and classifies host-side: 1 at the
+    config-4 shape, 0 outside the fused kernel's shapes / layouts, -1 for
+    invalid arguments (no pointer is dereferenced)."""
+    from mamba_hip import _lib
+    L = _lib.lib()
+    a = _lib.Mamba3FusedArgs()
+    p = a.prep
+    p.batch, p.seqlen, p.nheads, p.headdim, p.ngroups, p.dstate, p.mimo, p.rope_dim = 4, 8192, 32, 64, 1, 128, 4, 128
+    p.proj_dtype = p.io_dtype = 1  # MAMBA_BF16
+    p.proj_sl = 2 * 32 * 64 + 2 * 4 * 128 + 3 * 32 + 64
+    p.proj_sb = 8192 * p.proj_sl
+    ptrs = ("proj", "ssm_state", "k_state", "v_state", "angle", "angle_out", "dt_bias", "b_norm_w", "c_norm_w",
+            "b_bias", "c_bias", "mimo_x", "initial_state")
+    for i, name in enumerate(ptrs):
+        setattr(p, name, 4096 * (i + 1))  # never dereferenced
+    a.y, a.final_state = 4096 * 20, 4096 * 21
+    assert L.mamba3_ssd_fused_supported(ctypes.byref(a)) == 1
+    for field, bad in (("headdim", 32), ("mimo", 1), ("proj_dtype", 0)):
+        old = getattr(p, field)
+        setattr(p, field, bad)
+        assert L.mamba3_ssd_fused_supported(ctypes.byref(a)) == 0, field
+        setattr(p, field, old)
+    p.proj_sl += 4  # rows no longer 16-byte aligned
+    p.proj_sb = 8192 * p.proj_sl
+    assert L.mamba3_ssd_fused_supported(ctypes.byref(a)) == 0
+    a.y = None
+    assert L.mamba3_ssd_fused_supported(ctypes.byref(a)) == -1
+    assert L.mamba3_ssd_fused_fwd(ctypes.byref(a), None) == 1
+    assert b"y and final_state" in L.mamba_last_error()
 
 
 def test_missing_library_raises_no_fallback():
