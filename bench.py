@@ -616,6 +616,108 @@ def bench_ssd3(args):
     }
 
 
+def mamba3_fused_algorithmic(cfg):
+    """Compulsory HBM bytes and the algorithmic FLOPs of the config-4 prefill
+    from the in_proj rows to y per rank (mamba3_ssd_fused_fwd): the rows' x,
+    raw group-form B / C, dd_dt / dd_A / lambda and rotation columns read once
+    (bf16), y per rank written (bf16), the state read and written (f32).
+    FLOPs as the SSD seam's (ssd3_algorithmic, chunk 128 steps)."""
+    import mamba_hip
+    c = mamba_hip.Mamba3Config(d_model=cfg["nheads"] * cfg["headdim"] // 2, state_rank=cfg["dstate"],
+                               per_head_dim=cfg["headdim"], ngroups=1, mimo_rank=cfg["mimo"])
+    b, L, H, P, N, M, G, A = (cfg["batch"], cfg["seqlen"], c.nheads, c.per_head_dim, c.state_rank, c.mimo_rank,
+                              c.ngroups, c.num_rope_angles)
+    tok = b * L
+    bytes_ = tok * (H * P + 2 * M * G * N + 3 * H + A) * 2 + tok * M * H * P * 2 + 2 * b * H * P * N * 4
+    _, flops = ssd3_algorithmic(cfg)
+    return bytes_, flops
+
+
+def bench_mamba3_fused(args):
+    """The config-4 Mamba-3 prefill from the in_proj rows to y per rank
+    (B=4 L=8192 H=32 P=64 N=128 MIMO 4, full rotation): mamba3_ssd_fused_fwd
+    (beta-seed kernel + the fused prologue / SSD scan), reference init."""
+    import torch
+
+    import mamba_hip
+    cfg = dict(SSD3_CFG4)
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    c = mamba_hip.Mamba3Config(d_model=cfg["nheads"] * cfg["headdim"] // 2, state_rank=cfg["dstate"],
+                               per_head_dim=cfg["headdim"], ngroups=1, mimo_rank=cfg["mimo"])
+    m = c.init(dev, torch.bfloat16, gen)
+    b, L = cfg["batch"], cfg["seqlen"]
+    proj = torch.randn((b, L, c.d_in_proj), generator=gen, device=dev).to(torch.bfloat16)
+    cache = m.new_cache(b)
+    a = mamba_hip.mamba3_fused_args(c, proj, cache, dt_bias=m.dt_bias, b_norm_w=m.b_norm_w, c_norm_w=m.c_norm_w,
+                                    b_bias=m.b_bias, c_bias=m.c_bias, mimo_x=m.mimo_x, D=m.D)
+    if mamba_hip.mamba3_fused_supported(a) != 1:
+        raise RuntimeError("config 4 is outside the fused kernel")
+
+    def step(events=None):
+        mamba_hip.mamba3_fused_run(a, cache, events)
+
+    ms_per_step, kern_ms = _time_steps(args, step)
+    nbytes, flops = mamba3_fused_algorithmic(cfg)
+    tokens = b * L
+    gbs = nbytes / (kern_ms * 1e-3) / 1e9
+    tflops = flops / (kern_ms * 1e-3) / 1e12
+    hbm_bound = nbytes / (HBM_PEAK_GBS * 1e9) >= flops / (BF16_PEAK_TFLOPS * 1e12)
+    if hbm_bound:
+        roof = {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS}
+    else:
+        roof = {"bound": "mfma", "achieved": tflops, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": tflops / BF16_PEAK_TFLOPS}
+    roof.update({"traffic": _profiled_traffic("mamba3_fused_prefill_cfg4"), "kernel_ms": kern_ms,
+                 "algorithmic_bytes": nbytes, "algorithmic_flops": flops, "hbm_gbs": gbs,
+                 "timing": "HIP events around the seed and fused scan kernels on their stream, per call"})
+    return {
+        "metric": "Mamba-3 prefill tokens/s, in_proj rows -> y per rank (B=4 L=8192 H=32 P=64 N=128 MIMO 4) "
+                  "+ % MFMA roofline",
+        "value": tokens / (ms_per_step * 1e-3), "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (config-4 shapes, reference init, in_proj rows ~N(0,1), seed 0)",
+        "config": {"workload": "mamba3_fused_prefill_cfg4", **cfg, "rope_dim": c.rope_dim,
+                   "io": "proj and y bf16, state f32",
+                   "entry": "mamba3_ssd_fused_fwd (mamba3_seed_kernel + mamba3_ssd_fused<4>)"},
+        "roofline": roof,
+    }
+
+
+def cpu_baseline_mamba3_fused(cfg, seed=0):
+    """oracle.mamba3_prep_fwd then oracle.ssd3 (the f32 C restatement of the
+    reference's single-SSD K1-K5) on one sequence of 1024 tokens, scaled to
+    tokens/s."""
+    import numpy as np
+
+    import mamba_hip
+    import oracle
+    oracle.build()
+    c = mamba_hip.Mamba3Config(d_model=cfg["nheads"] * cfg["headdim"] // 2, state_rank=cfg["dstate"],
+                               per_head_dim=cfg["headdim"], ngroups=1, mimo_rank=cfg["mimo"])
+    H, P, N, M, A = c.nheads, c.per_head_dim, c.state_rank, c.mimo_rank, c.num_rope_angles
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    rng = np.random.default_rng(seed)
+    L = 1024
+    prm = dict(nheads=H, headdim=P, ngroups=1, dstate=N, mimo=M, rope_dim=c.rope_dim,
+               dt_bias=np.full(H, -2.0, np.float32), b_norm_w=np.ones(N, np.float32), c_norm_w=np.ones(N, np.float32),
+               b_bias=np.ones((H, M, N), np.float32), c_bias=np.ones((H, M, N), np.float32),
+               mimo_x=np.full((H, M, P), 1 / M, np.float32))
+    proj = rng.standard_normal((1, L, c.d_in_proj)).astype(np.float32)
+    z = lambda *s: np.zeros(s, np.float32)  # noqa: E731
+    cache = dict(ssm=z(1, H, P, N), k_state=z(1, M, H, N), v_state=z(1, H, P), angle=z(1, H, A))
+    t0 = time.perf_counter()
+    r = oracle.mamba3_prep_fwd(proj, prm, cache)
+    oracle.ssd3(r["v"], r["da"], r["B"], r["C"], r["gamma"], r["scale"], r["h0"], chunk=cfg["chunk"], prec=32)
+    sec = time.perf_counter() - t0
+    total = cfg["batch"] * cfg["seqlen"]
+    return {"value": L / sec, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"1 x {L} tokens ({sec:.1f} s) of {total}; float64 numpy prologue + f32 serial single-SSD "
+                      f"K1-K5 restatement (OpenMP over heads)"}
+
+
 def cpu_baseline_ssd3(cfg, seed=0):
     """The f32 CPU restatement of the reference's single-SSD K1-K5 (oracle/,
     OpenMP over (batch, head)) on one sequence of 4096 steps, scaled to tokens/s."""
@@ -1042,7 +1144,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", default="ssd2",
-                    choices=["ssd2", "mamba1", "decode", "ssd3", "mamba1_step", "mamba3_step", "mamba3_prep",
+                    choices=["ssd2", "mamba1", "decode", "ssd3", "mamba3_fused", "mamba1_step", "mamba3_step",
+                             "mamba3_prep",
                              "mamba2_block"])
     ap.add_argument("--batch", type=int, default=DECODE_CFG3["batch"], help="decode batch")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -1069,6 +1172,9 @@ def main():
     elif args.workload == "mamba1_step":
         out = bench_mamba1_step(args)
         base = (lambda: cpu_baseline_mamba1_step(MAMBA1_STEP_CFG, args.batch))
+    elif args.workload == "mamba3_fused":
+        out = bench_mamba3_fused(args)
+        base = (lambda: cpu_baseline_mamba3_fused(SSD3_CFG4))
     elif args.workload == "ssd3":
         out = bench_ssd3(args)
         base = (lambda: cpu_baseline_ssd3(SSD3_CFG4))

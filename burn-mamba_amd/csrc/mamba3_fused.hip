@@ -48,13 +48,91 @@ struct M3FusedParams {
 template <int M>
 struct __align__(16) M3FusedLds {
     Ssd3Lds<128> core;
-    float cs[128 / M][64], sn[128 / M][64];  // cos / sin per step of the chunk and pair index
-    float2 bwb[M][128], cwb[M][128];         // (norm weight, bias) of B and C per rank and column
+    bf16_t C[128][136];                      // C rows of the chunk (the y tiles' MFMA B operand)
+    float cs[128 / M][64], sn[128 / M][64];  // cos / sin per step and pair index k, at m3f_pos(k)
+    float4 bwb[M][4][16], cwb[M][4][16];     // (w, bias, w, bias) of columns 8 nv + 2 e2 (+1) of B / C
+                                             // per rank, at [m][e2][nv]
     float mx[M][32];                         // mimo_x of this headdim half
     float dt[128 / M];                       // dt per step of the chunk (0 past the end)
 };
 
 __device__ __forceinline__ float m3f_bf(uint32_t u) { return __uint_as_float(u << 16); }
+// Position of pair index k in a cos / sin table row: the four entries 8 j .. 8 j + 3
+// at 4 j, the four 8 j + 4 .. 8 j + 7 at 32 + 4 j.  A thread whose columns hold the
+// pairs 8 j .. 8 j + 7 reads them as two 16-byte vectors, and the 8 threads j = 0..7
+// of a row read 32 consecutive dwords per instruction (no bank conflicts).
+__device__ __forceinline__ int m3f_pos(int k) { return ((k & 4) << 3) + ((k >> 3) << 2) + (k & 3); }
+// tanh and sigmoid through the hardware reciprocal (1 ulp)
+__device__ __forceinline__ float m3f_tanh(float x) {
+    const float e = __expf(-2.f * fabsf(x));
+    return copysignf((1.f - e) * __builtin_amdgcn_rcpf(1.f + e), x);
+}
+__device__ __forceinline__ float m3f_sigmoid(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
+// value of lane ^ 8 inside a 16-lane row (row_ror:8; every lane is written)
+__device__ __forceinline__ float m3f_xor8(float x) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x128, 0xf, 0xf, false));
+}
+// value of lane - K inside a 16-lane row (row_shr:K), 0 where that leaves the row
+template <int K>
+__device__ __forceinline__ float m3f_shr(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x110 + K, 0xf, 0xf, false));
+}
+// value of lane 8 (lane / 8) + 7: the last lane of each aligned group of 8 (ds_swizzle bit masks)
+__device__ __forceinline__ float m3f_last8(float x) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x18 | (0x7 << 5)));
+}
+
+// Two rows (ranks m0 and m0 + 1 of one step) x 8 columns (8 nv ..) of raw
+// group-form B or C: the RMS over the row's 16 lanes, norm weight and bias,
+// the (k, k + N/2) rotation with the partner columns from lane ^ 8 (k = n mod
+// N/2; cs / sn point at the step's table entries for this thread's first four
+// pairs, the next four 32 entries on: the m3f_pos layout).
+// Writes the bf16 rows to the LDS tile and leaves the f32 rows in y0 / y1.
+__device__ __forceinline__ void m3f_rows(uint4 r0, uint4 r1, const float (&w)[8], const float (&b0)[8],
+                                         const float (&b1)[8], const float* cs, const float* sn, float sgn,
+                                         bf16_t* dst0, bf16_t* dst1, float (&y0)[8], float (&y1)[8]) {
+    const uint32_t a0[4] = {r0.x, r0.y, r0.z, r0.w}, a1[4] = {r1.x, r1.y, r1.z, r1.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        y0[2 * e] = s3_lo(a0[e]); y0[2 * e + 1] = s3_hi(a0[e]);
+        y1[2 * e] = s3_lo(a1[e]); y1[2 * e + 1] = s3_hi(a1[e]);
+    }
+    float ss0 = 0.f, ss1 = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        ss0 += y0[e] * y0[e];
+        ss1 += y1[e] * y1[e];
+    }
+    ss0 = m3_group_sum<16>(ss0);
+    ss1 = m3_group_sum<16>(ss1);
+    // 1 / sqrt(mean + eps) (the argument is >= eps, a normal number)
+    const float rms0 = __builtin_amdgcn_rsqf(ss0 * (1.f / 128.f) + kDivEpsF32);
+    const float rms1 = __builtin_amdgcn_rsqf(ss1 * (1.f / 128.f) + kDivEpsF32);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        y0[e] = (y0[e] * rms0) * w[e] + b0[e];
+        y1[e] = (y1[e] * rms1) * w[e] + b1[e];
+    }
+    float o0[8], o1[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        o0[e] = m3f_xor8(y0[e]);
+        o1[e] = m3f_xor8(y1[e]);
+    }
+    const float4 c0 = *(const float4*)cs, c1 = *(const float4*)(cs + 32);
+    const float4 s0 = *(const float4*)sn, s1 = *(const float4*)(sn + 32);
+    const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+    const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        y0[e] = cv[e] * y0[e] + (sgn * sv[e]) * o0[e];
+        y1[e] = cv[e] * y1[e] + (sgn * sv[e]) * o1[e];
+    }
+    *(uint4*)dst0 = make_uint4(pack_bf16x2(y0[0], y0[1]), pack_bf16x2(y0[2], y0[3]), pack_bf16x2(y0[4], y0[5]),
+                               pack_bf16x2(y0[6], y0[7]));
+    *(uint4*)dst1 = make_uint4(pack_bf16x2(y1[0], y1[1]), pack_bf16x2(y1[2], y1[3]), pack_bf16x2(y1[4], y1[5]),
+                               pack_bf16x2(y1[6], y1[7]));
+}
 
 // M bf16 values to LDS as one store (2 M bytes, aligned to its size)
 template <int M>
@@ -69,19 +147,23 @@ __device__ __forceinline__ void m3f_st(bf16_t* dst, const float* v) {
     }
 }
 
+// 8 waves, two per SIMD: all take part in the chunk's prologue (coefficients,
+// angles, B and C rows, v^T); then waves 0-3 compute the y tiles (tile =
+// wave) while waves 4-7 update the state (dstate columns 32 (wave - 4) ..).
 template <int M>
-__global__ __launch_bounds__(256, 1) void mamba3_ssd_fused(M3FusedParams p) {
-    constexpr int QF = 128, N = 128, NK = N / 16, KS = QF / 16;
+__global__ __launch_bounds__(512, 1) void mamba3_ssd_fused(M3FusedParams p) {
+    constexpr int QF = 128, N = 128, KS = QF / 16;
     constexpr int TS = QF / M;                    // steps per chunk
     constexpr int lgM = M == 2 ? 1 : (M == 4 ? 2 : 3);
     static_assert(M == 2 || M == 4 || M == 8, "MIMO rank 2, 4 or 8");
-    constexpr int JA = TS / 4;                    // steps per angle thread
-    constexpr int XI = TS * 8, XPT = (XI + 255) / 256;  // x items: (step, 4-wide headdim piece)
-    constexpr int BPT = 4;                        // B items: (row pair, 8-wide column piece)
+    constexpr int JA = TS / 8;                    // steps per angle thread (8 threads per angle)
+    constexpr int XI = TS * 8, XPT = (XI + 511) / 512;  // x items: (step, 4-wide headdim piece)
+    constexpr int RP = 2;                         // B row pairs and C row pairs per thread
     __shared__ M3FusedLds<M> SF;
     Ssd3Lds<QF>& S = SF.core;
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r = lane & 31, half = lane >> 5;
+    const int tid_ = threadIdx.x, r_ = tid_ & 31, half_ = (tid_ >> 5) & 1;
+    const int wv = wave_id(), w4 = wv & 3;
     // XCD-aware mapping: the two headdim halves of a head and neighbouring heads on one XCD
     const int nwg = p.nb * p.H * 2;
     int w = blockIdx.x;
@@ -92,27 +174,30 @@ __global__ __launch_bounds__(256, 1) void mamba3_ssd_fused(M3FusedParams p) {
     const int64_t bh = (int64_t)b * p.H + h;
 
     // per-head constants
-    for (int i = tid; i < M * N; i += 256) {
-        const int m = i / N, n = i % N;
-        const int64_t o = ((int64_t)h * M + m) * N + n;
-        SF.bwb[m][n] = make_float2(p.bnw[n], p.bbias[o]);
-        SF.cwb[m][n] = make_float2(p.cnw[n], p.cbias[o]);
+    for (int i = tid_; i < M * 64; i += 512) {
+        const int m = i >> 6, nv = (i >> 2) & 15, e2 = i & 3, n = nv * 8 + 2 * e2;
+        const float* bb = p.bbias + ((int64_t)h * M + m) * N;
+        const float* cb = p.cbias + ((int64_t)h * M + m) * N;
+        SF.bwb[m][e2][nv] = make_float4(p.bnw[n], bb[n], p.bnw[n + 1], bb[n + 1]);
+        SF.cwb[m][e2][nv] = make_float4(p.cnw[n], cb[n], p.cnw[n + 1], cb[n + 1]);
     }
-    if (tid < M * 32) {
-        const int m = tid >> 5, pp = tid & 31;
+    if (tid_ < M * 32) {
+        const int m = tid_ >> 5, pp = tid_ & 31;
         SF.mx[m][pp] = p.mx ? p.mx[((int64_t)h * M + m) * 64 + p0 + pp] : 1.f;
     }
-    // state tile of this wave: headdim rows p0..p0+31, dstate columns 32 wave..
+    // state tile of waves 4-7: headdim rows p0..p0+31, dstate columns 32 w4..
     s3_f32x16_t hacc;
     const int64_t hbase = bh * 64 * N;
+    if (wv >= 4) {
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-        const int pp = p0 + 8 * (v >> 2) + 4 * half + (v & 3);
-        hacc[v] = p.h0[hbase + pp * N + wave * 32 + r];
+        for (int v = 0; v < 16; ++v) {
+            const int pp = p0 + 8 * (v >> 2) + 4 * half_ + (v & 3);
+            hacc[v] = p.h0[hbase + pp * N + w4 * 32 + r_];
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+            S.h[0][8 * (v >> 2) + 4 * half_ + (v & 3)][w4 * 32 + r_] = __builtin_bit_cast(bf16_t, (__bf16)hacc[v]);
     }
-#pragma unroll
-    for (int v = 0; v < 16; ++v)
-        S.h[0][8 * (v >> 2) + 4 * half + (v & 3)][wave * 32 + r] = __builtin_bit_cast(bf16_t, (__bf16)hacc[v]);
 
     const float dtb = p.dt_bias[h];
     const float Dv = p.Dh ? p.Dh[h] : 0.f;
@@ -123,82 +208,107 @@ __global__ __launch_bounds__(256, 1) void mamba3_ssd_fused(M3FusedParams p) {
 
     // ---- thread roles and their byte offsets within a chunk's proj rows
     // coefficients: fused position f = tid (< QF) of step f >> lgM
-    const int cf_tl = (tid & (QF - 1)) >> lgM;
-    const bool cf_first = (tid & (M - 1)) == 0;
-    const uint32_t co_dt = (uint32_t)cf_tl * rs + (uint32_t)(p.o_dt + h) * 2;
+    const uint32_t co_dt = (uint32_t)((tid_ & (QF - 1)) >> lgM) * rs + (uint32_t)(p.o_dt + h) * 2;
     const uint32_t co_da = co_dt + (uint32_t)p.H * 2, co_lam = co_dt + (uint32_t)p.H * 4;
-    // angles: a = tid / 4 over steps q JA .. q JA + JA - 1, q = tid % 4
-    const int ang_a = tid >> 2, ang_q = tid & 3;
-    const uint32_t ao = (uint32_t)(ang_q * JA) * rs + (uint32_t)(p.o_dt + 3 * p.H + min(ang_a, p.A - 1)) * 2;
-    // B items: rows f0 = 2 (b_fp + 16 k) and f0 + 1 (ranks bm0, bm0 + 1 of one step), columns 8 b_nv..
-    const int b_fp = tid >> 4, b_nv = tid & 15;
-    const int bm0 = (2 * b_fp) & (M - 1);
-    const uint32_t bo = (uint32_t)((2 * b_fp) >> lgM) * rs + (uint32_t)(p.o_b + (bm0 * p.G + g) * N + b_nv * 8) * 2;
-    const uint32_t b_r2 = (uint32_t)p.G * N * 2;
-    // C fragments: row i = 32 wave + r, columns 16 kn + 8 half .. (+8) for kn = 0..7
-    const int c_i = wave * 32 + r, c_tl = c_i >> lgM, c_m = c_i & (M - 1);
-    const uint32_t cofs = (uint32_t)c_tl * rs + (uint32_t)(p.o_c + (c_m * p.G + g) * N + 8 * half) * 2;
+    // angles: a = tid / 8 over steps q JA .. q JA + JA - 1, q = tid % 8
+    const uint32_t ao = (uint32_t)((tid_ & 7) * JA) * rs + (uint32_t)(p.o_dt + 3 * p.H + min(tid_ >> 3, p.A - 1)) * 2;
+    // B and C rows: pairs fp = tid / 16 + 32 k (rows 2 fp, 2 fp + 1: ranks bm0, bm0 + 1 of one
+    // step), columns 8 nv .. 8 nv + 7
+    const uint32_t bro = (uint32_t)((2 * (tid_ >> 4)) >> lgM) * rs +
+                         (uint32_t)((((2 * (tid_ >> 4)) & (M - 1)) * p.G + g) * N + (tid_ & 15) * 8) * 2;
+    const uint32_t bo = bro + (uint32_t)p.o_b * 2, cofs = bro + (uint32_t)p.o_c * 2;
+    const uint32_t r2 = (uint32_t)p.G * N * 2;  // the pair's second row (rank bm0 + 1)
 
     // ---- register prefetch of one chunk's raw proj data
     uint2 xq[XPT];
-    uint4 bq[BPT][2], cn[NK];
-    uint32_t cq[5] = {0u, 0u, 0u, 0u, 0u};
+    uint4 bq[RP][2], cq[RP][2];
+    uint32_t kq[5] = {0u, 0u, 0u, 0u, 0u};
     uint32_t rq[JA];
     // rows of chunk c and the step after it (scale's shift); zero past the end
     auto chunk_rsrc = [&](int c) {
-        const int steps = min(TS + 1, p.L - c * TS);
+        const int steps = max(0, min(TS + 1, p.L - c * TS));  // none past the last chunk
         return buf_rsrc(projb + (int64_t)c * TS * p.proj_sl, (uint32_t)steps * rs);
+    };
+    auto fetch_rows = [&](int c) {
+        const __amdgpu_buffer_rsrc_t rp = chunk_rsrc(c);
+#pragma unroll
+        for (int k = 0; k < RP; ++k) {
+            const uint32_t o = (uint32_t)((64 * k) >> lgM) * rs;
+            bq[k][0] = buf_ld16(rp, bo + o);
+            bq[k][1] = buf_ld16(rp, bo + o + r2);
+            cq[k][0] = buf_ld16(rp, cofs + o);
+            cq[k][1] = buf_ld16(rp, cofs + o + r2);
+        }
     };
     auto fetch = [&](int c) {
         const __amdgpu_buffer_rsrc_t rp = chunk_rsrc(c);
+        // every load is issued by every thread on every chunk (the threads past
+        // the x items and positions load duplicates; past the last chunk the
+        // resource is empty): the compiler's waits then count the same loads on
+        // every path
 #pragma unroll
         for (int k = 0; k < XPT; ++k) {
-            const int item = tid + 256 * k;
-            if (XI % 256 == 0 || item < XI)
-                xq[k] = buf_ld8(rp, (uint32_t)(item >> 3) * rs + (uint32_t)(p.o_x + h * 64 + p0 + (item & 7) * 4) * 2);
+            const int item = (tid_ + 512 * k) % XI;
+            xq[k] = buf_ld8(rp, (uint32_t)(item >> 3) * rs + (uint32_t)(p.o_x + h * 64 + p0 + (item & 7) * 4) * 2);
         }
-#pragma unroll
-        for (int k = 0; k < BPT; ++k) {
-            const uint32_t o = bo + (uint32_t)((32 * k) >> lgM) * rs;
-            bq[k][0] = buf_ld16(rp, o);
-            bq[k][1] = buf_ld16(rp, o + b_r2);
-        }
-        if (tid < QF) {
-            cq[0] = buf_ld2(rp, co_dt);
-            cq[1] = buf_ld2(rp, co_da);
-            cq[2] = buf_ld2(rp, co_lam);
-            cq[3] = buf_ld2(rp, co_dt + rs);
-            cq[4] = buf_ld2(rp, co_lam + rs);
-        }
+        kq[0] = buf_ld2(rp, co_dt);
+        kq[1] = buf_ld2(rp, co_da);
+        kq[2] = buf_ld2(rp, co_lam);
+        kq[3] = buf_ld2(rp, co_dt + rs);
+        kq[4] = buf_ld2(rp, co_lam + rs);
 #pragma unroll
         for (int j = 0; j < JA; ++j) rq[j] = buf_ld2(rp, ao + (uint32_t)j * rs);
     };
-    auto fetch_c = [&](int c) {
-        const __amdgpu_buffer_rsrc_t rp = chunk_rsrc(c);
+    // y tile of chunk c (waves 0-3) from its LDS staging: 32 rows x 64 bytes, 4 lanes per row
+    auto store_y = [&](int c, int lane) {
+        const int t0 = c * TS;
+        const int rows = min(QF, (p.L - t0) * M);
+        const __amdgpu_buffer_rsrc_t ry = buf_rsrc(yhead + (int64_t)t0 * M * p.H * 64, (uint32_t)rows * y_rs);
 #pragma unroll
-        for (int kn = 0; kn < NK; ++kn) cn[kn] = buf_ld16(rp, cofs + 32 * kn);
+        for (int q = 0; q < 2; ++q) {
+            const int row = q * 16 + (lane >> 2), ch = lane & 3;
+            const uint4 val = *(const uint4*)&S.y[wv][row][ch * 8];
+            __builtin_amdgcn_raw_buffer_store_b128(
+                __builtin_bit_cast(decltype(__builtin_amdgcn_raw_buffer_load_b128(ry, 0, 0, 0)), val), ry,
+                (uint32_t)(wv * 32 + row) * y_rs + ch * 16, 0, 0);
+        }
     };
+    // the same issue order as inside the loop (small loads, then rows): the
+    // waits at the loop head then count the same way on entry and on the back-edge
+    float theta = (tid_ >> 3) < p.A ? p.ang[bh * p.A + (tid_ >> 3)] : 0.f;  // loaded before the prefetch
     fetch(0);
-    fetch_c(0);
-    float theta = ang_a < p.A ? p.ang[bh * p.A + ang_a] : 0.f;
+    __builtin_amdgcn_sched_barrier(0);
+    fetch_rows(0);
+    __builtin_amdgcn_sched_barrier(0);
 
     for (int c = 0; c < p.nch; ++c) {
         const int cur = c & 1;
         const int t0 = c * TS;
+        // thread coordinates redefined per chunk: LDS addresses derived from them are
+        // formed inside the loop instead of being hoisted (and spilled) as invariants
+        int tid = tid_;
+        asm volatile("" : "+v"(tid));
+        const int lane = tid & 63, r = lane & 31, half = lane >> 5;
+        const int cf_tl = (tid & (QF - 1)) >> lgM;
+        const bool cf_first = (tid & (M - 1)) == 0;
+        const int ang_a = tid >> 3, ang_q = tid & 7;
+        const int b_fp = tid >> 4, b_nv = tid & 15;
+        const int bm0 = (2 * b_fp) & (M - 1);
+        const int kq4 = (b_nv & 7) * 4;  // m3f_pos of the thread's first pair index 8 (nv & 7)
+        const float sgn = b_nv < 8 ? -1.f : 1.f;
         // ---- A: coefficients of this thread's position; the block scan of da
         float daq = 0.f, scq = 0.f, gmq = 0.f;
         if (tid < QF) {
             const int t = t0 + cf_tl;
             float dt = 0.f;
             if (t < p.L) {
-                dt = fminf(fmaxf(m3p_softplus(m3f_bf(cq[0]) + dtb), p.dt_lo), p.dt_hi);
-                const float da = dt * -fmaxf(m3p_softplus(m3f_bf(cq[1])), p.a_floor);
-                const float lam = 1.f / (1.f + __expf(-m3f_bf(cq[2])));
+                dt = fminf(fmaxf(m3p_softplus(m3f_bf(kq[0]) + dtb), p.dt_lo), p.dt_hi);
+                const float da = dt * -fmaxf(m3p_softplus(m3f_bf(kq[1])), p.a_floor);
+                const float lam = m3f_sigmoid(m3f_bf(kq[2]));
                 float nxt = 0.f;
                 if (t + 1 < p.L) {
-                    const float dt1 = fminf(fmaxf(m3p_softplus(m3f_bf(cq[3]) + dtb), p.dt_lo), p.dt_hi);
-                    const float lam1 = 1.f / (1.f + __expf(-m3f_bf(cq[4])));
-                    nxt = (1.f - lam1) * dt1;
+                    const float dt1 = fminf(fmaxf(m3p_softplus(m3f_bf(kq[3]) + dtb), p.dt_lo), p.dt_hi);
+                    nxt = (1.f - m3f_sigmoid(m3f_bf(kq[4]))) * dt1;
                 }
                 gmq = lam * dt;
                 scq = gmq + nxt;
@@ -206,19 +316,15 @@ __global__ __launch_bounds__(256, 1) void mamba3_ssd_fused(M3FusedParams p) {
             }
             if (cf_first) SF.dt[cf_tl] = dt;
         }
-        const float loc = wave_incl_scan(daq * kLog2eS3);
-        if (lane == 63) S.red[wave] = loc;
+        const float loc = wave_incl_scan(daq * kLog2eS3);  // waves 0 and 1 hold the chunk's positions
+        if (lane == 63 && wv < 2) S.red[wv] = loc;
         if ((tid & 31) == 0 && tid < QF) S.anc[tid >> 5] = loc;
         __syncthreads();
         // ---- B: per-position tables; angles and their cos / sin
-        const float cs_end = (S.red[0] + S.red[1]) + (S.red[2] + S.red[3]);
+        const float cs_end = S.red[0] + S.red[1];
         if (tid < QF) {
             const int j = tid;
-            float off = 0.f;
-#pragma unroll
-            for (int k = 0; k < 3; ++k)
-                if (k < wave) off += S.red[k];
-            const float csj = loc + off;
+            const float csj = loc + (wv == 1 ? S.red[0] : 0.f);
             S.cs2[j] = csj;
             S.st[j] = (float)(j >> lgM);
             S.sc[j] = scq;
@@ -227,10 +333,7 @@ __global__ __launch_bounds__(256, 1) void mamba3_ssd_fused(M3FusedParams p) {
 #pragma unroll
             for (int it = 1; it < 4; ++it) {
                 if (j < it * 32) {
-                    float anchor = S.anc[it];
-#pragma unroll
-                    for (int k = 0; k < 3; ++k)
-                        if (k < (it >> 1)) anchor += S.red[k];
+                    const float anchor = S.anc[it] + (it >= 2 ? S.red[0] : 0.f);
                     S.f[it - 1][j] = scq * __builtin_amdgcn_exp2f(anchor - csj);
                 }
             }
@@ -240,95 +343,36 @@ __global__ __launch_bounds__(256, 1) void mamba3_ssd_fused(M3FusedParams p) {
             float run = 0.f;
 #pragma unroll
             for (int j = 0; j < JA; ++j) {
-                run += SF.dt[ang_q * JA + j] * (m3_tanh(m3f_bf(rq[j])) * p.span);
+                run += SF.dt[ang_q * JA + j] * (m3f_tanh(m3f_bf(rq[j])) * p.span);
                 cum[j] = run;
             }
-            // exclusive prefix of the quarters' totals inside the quad (lanes 4 a .. 4 a + 3)
-            const float q0 = m3_dpp<0x00>(run), q1 = m3_dpp<0x55>(run), q2 = m3_dpp<0xAA>(run);
-            const float base = theta + ((ang_q >= 1 ? q0 : 0.f) + (ang_q >= 2 ? q1 : 0.f) + (ang_q >= 3 ? q2 : 0.f));
+            // inclusive scan of the 8 parts' totals inside each aligned group of 8 lanes
+            float incl = run;
+            {
+                const float t1 = m3f_shr<1>(incl);
+                incl += ang_q >= 1 ? t1 : 0.f;
+                const float t2 = m3f_shr<2>(incl);
+                incl += ang_q >= 2 ? t2 : 0.f;
+                const float t4 = m3f_shr<4>(incl);
+                incl += ang_q >= 4 ? t4 : 0.f;
+            }
+            const float base = theta + (incl - run);
+            const float total = m3f_last8(incl);
             const bool rot_on = ang_a < p.npair;
 #pragma unroll
             for (int j = 0; j < JA; ++j) {
                 const float th = m3p_wrap(base + cum[j]);
-                SF.cs[ang_q * JA + j][ang_a] = rot_on ? __cosf(th) : 1.f;
-                SF.sn[ang_q * JA + j][ang_a] = rot_on ? __sinf(th) : 0.f;
+                SF.cs[ang_q * JA + j][m3f_pos(ang_a)] = rot_on ? __cosf(th) : 1.f;
+                SF.sn[ang_q * JA + j][m3f_pos(ang_a)] = rot_on ? __sinf(th) : 0.f;
             }
-            // the chunk's last angle (quarter 3's), carried wrapped
-            theta = m3p_wrap(m3_dpp<0xFF>(base + cum[JA - 1]));
+            theta = m3p_wrap(theta + total);  // the chunk's last angle, carried wrapped
         }
         __syncthreads();
-        // ---- C: B rows to LDS; v^T and w-scaled v^T; this wave's C fragments
-        {
-            const int kb = (b_nv & 7) * 8;  // pair index of this thread's first column
-            const float sgn = b_nv < 8 ? -1.f : 1.f;
-            float bw[8], bb0[8], bb1[8];
-#pragma unroll
-            for (int e = 0; e < 8; e += 2) {
-                const float4 u0 = *(const float4*)&SF.bwb[bm0][b_nv * 8 + e];
-                const float4 u1 = *(const float4*)&SF.bwb[bm0 + 1][b_nv * 8 + e];
-                bw[e] = u0.x; bb0[e] = u0.y; bw[e + 1] = u0.z; bb0[e + 1] = u0.w;
-                bb1[e] = u1.y; bb1[e + 1] = u1.w;
-            }
-#pragma unroll
-            for (int k = 0; k < BPT; ++k) {
-                const int f0 = 2 * (b_fp + 16 * k), tl = f0 >> lgM;
-                float y0[8], y1[8];
-                const uint32_t a0[4] = {bq[k][0].x, bq[k][0].y, bq[k][0].z, bq[k][0].w};
-                const uint32_t a1[4] = {bq[k][1].x, bq[k][1].y, bq[k][1].z, bq[k][1].w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    y0[2 * e] = s3_lo(a0[e]); y0[2 * e + 1] = s3_hi(a0[e]);
-                    y1[2 * e] = s3_lo(a1[e]); y1[2 * e + 1] = s3_hi(a1[e]);
-                }
-                float ss0 = 0.f, ss1 = 0.f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    ss0 += y0[e] * y0[e];
-                    ss1 += y1[e] * y1[e];
-                }
-                ss0 = m3_group_sum<16>(ss0);
-                ss1 = m3_group_sum<16>(ss1);
-                const float rms0 = 1.f / sqrtf(ss0 / (float)N + kDivEpsF32);
-                const float rms1 = 1.f / sqrtf(ss1 / (float)N + kDivEpsF32);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    y0[e] = (y0[e] * rms0) * bw[e] + bb0[e];
-                    y1[e] = (y1[e] * rms1) * bw[e] + bb1[e];
-                }
-                float o0[8], o1[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    o0[e] = m3_xor<8>(y0[e]);
-                    o1[e] = m3_xor<8>(y1[e]);
-                }
-                const float4 c0 = *(const float4*)&SF.cs[tl][kb], c1 = *(const float4*)&SF.cs[tl][kb + 4];
-                const float4 s0 = *(const float4*)&SF.sn[tl][kb], s1 = *(const float4*)&SF.sn[tl][kb + 4];
-                const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-                const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    y0[e] = cv[e] * y0[e] + (sgn * sv[e]) * o0[e];
-                    y1[e] = cv[e] * y1[e] + (sgn * sv[e]) * o1[e];
-                }
-                *(uint4*)&S.B[f0][b_nv * 8] = make_uint4(pack_bf16x2(y0[0], y0[1]), pack_bf16x2(y0[2], y0[3]),
-                                                        pack_bf16x2(y0[4], y0[5]), pack_bf16x2(y0[6], y0[7]));
-                *(uint4*)&S.B[f0 + 1][b_nv * 8] = make_uint4(pack_bf16x2(y1[0], y1[1]), pack_bf16x2(y1[2], y1[3]),
-                                                            pack_bf16x2(y1[4], y1[5]), pack_bf16x2(y1[6], y1[7]));
-                // the cache tail: the last step's rotated B (f32)
-                if (ph == 0 && t0 + tl == p.L - 1) {
-                    float* k0 = p.kst + (((int64_t)b * M + bm0) * p.H + h) * N + b_nv * 8;
-                    float* k1 = p.kst + (((int64_t)b * M + bm0 + 1) * p.H + h) * N + b_nv * 8;
-                    *(float4*)k0 = make_float4(y0[0], y0[1], y0[2], y0[3]);
-                    *(float4*)(k0 + 4) = make_float4(y0[4], y0[5], y0[6], y0[7]);
-                    *(float4*)k1 = make_float4(y1[0], y1[1], y1[2], y1[3]);
-                    *(float4*)(k1 + 4) = make_float4(y1[4], y1[5], y1[6], y1[7]);
-                }
-            }
-        }
+        if (c > 0 && wv < 4) store_y(c - 1, lane);
 #pragma unroll
         for (int k = 0; k < XPT; ++k) {
-            const int item = tid + 256 * k;
-            if (XI % 256 == 0 || item < XI) {
+            const int item = tid + 512 * k;
+            if (XI % 512 == 0 || item < XI) {
                 const int tl = item >> 3, pv = item & 7;
                 const float xv[4] = {s3_lo(xq[k].x), s3_hi(xq[k].x), s3_lo(xq[k].y), s3_hi(xq[k].y)};
                 if (t0 + tl == p.L - 1)  // the cache tail: the last step's x
@@ -353,54 +397,48 @@ __global__ __launch_bounds__(256, 1) void mamba3_ssd_fused(M3FusedParams p) {
                 }
             }
         }
-        s3_bf16x8_t cfr[NK];
+        // the next chunk's coefficient, angle and x columns (their registers are free now)
+        __builtin_amdgcn_sched_barrier(0);
+        fetch(c + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        // ---- C: B and C rows to LDS; v^T and w-scaled v^T
         {
-            float cv[NK][8];
+            float bw[8], bb0[8], bb1[8], cw[8], cb0[8], cb1[8];
 #pragma unroll
-            for (int kn = 0; kn < NK; ++kn) {
-                const uint32_t a[4] = {cn[kn].x, cn[kn].y, cn[kn].z, cn[kn].w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    cv[kn][2 * e] = s3_lo(a[e]);
-                    cv[kn][2 * e + 1] = s3_hi(a[e]);
-                }
+            for (int e = 0; e < 8; e += 2) {
+                const float4 u0 = SF.bwb[bm0][e >> 1][b_nv], u1 = SF.bwb[bm0 + 1][e >> 1][b_nv];
+                const float4 v0 = SF.cwb[bm0][e >> 1][b_nv], v1 = SF.cwb[bm0 + 1][e >> 1][b_nv];
+                bw[e] = u0.x; bb0[e] = u0.y; bw[e + 1] = u0.z; bb0[e + 1] = u0.w;
+                bb1[e] = u1.y; bb1[e + 1] = u1.w;
+                cw[e] = v0.x; cb0[e] = v0.y; cw[e + 1] = v0.z; cb0[e + 1] = v0.w;
+                cb1[e] = v1.y; cb1[e + 1] = v1.w;
             }
-            float ss = 0.f;
 #pragma unroll
-            for (int kn = 0; kn < NK; ++kn)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) ss += cv[kn][e] * cv[kn][e];
-            ss += __shfl_xor(ss, 32, 64);  // the row's other 64 columns
-            const float rms = 1.f / sqrtf(ss / (float)N + kDivEpsF32);
-#pragma unroll
-            for (int kn = 0; kn < NK / 2; ++kn) {
-                const int n0 = 16 * kn + 8 * half;  // columns n0 .. n0 + 7 and their partners n0 + 64 ..
-                float lo[8], hi[8];
-#pragma unroll
-                for (int e = 0; e < 8; e += 2) {
-                    const float4 u = *(const float4*)&SF.cwb[c_m][n0 + e];
-                    const float4 v = *(const float4*)&SF.cwb[c_m][n0 + 64 + e];
-                    lo[e] = (cv[kn][e] * rms) * u.x + u.y;
-                    lo[e + 1] = (cv[kn][e + 1] * rms) * u.z + u.w;
-                    hi[e] = (cv[kn + 4][e] * rms) * v.x + v.y;
-                    hi[e + 1] = (cv[kn + 4][e + 1] * rms) * v.z + v.w;
+            for (int k = 0; k < RP; ++k) {
+                const int f0 = 2 * (b_fp + 32 * k), tl = f0 >> lgM;
+                float y0[8], y1[8];
+                m3f_rows(bq[k][0], bq[k][1], bw, bb0, bb1, &SF.cs[tl][kq4], &SF.sn[tl][kq4], sgn,
+                         &S.B[f0][b_nv * 8], &S.B[f0 + 1][b_nv * 8], y0, y1);
+                // the cache tail: the last step's rotated B (f32)
+                if (ph == 0 && t0 + tl == p.L - 1) {
+                    float* k0 = p.kst + (((int64_t)b * M + bm0) * p.H + h) * N + b_nv * 8;
+                    float* k1 = p.kst + (((int64_t)b * M + bm0 + 1) * p.H + h) * N + b_nv * 8;
+                    *(float4*)k0 = make_float4(y0[0], y0[1], y0[2], y0[3]);
+                    *(float4*)(k0 + 4) = make_float4(y0[4], y0[5], y0[6], y0[7]);
+                    *(float4*)k1 = make_float4(y1[0], y1[1], y1[2], y1[3]);
+                    *(float4*)(k1 + 4) = make_float4(y1[4], y1[5], y1[6], y1[7]);
                 }
-                const float4 c0 = *(const float4*)&SF.cs[c_tl][n0], c1 = *(const float4*)&SF.cs[c_tl][n0 + 4];
-                const float4 s0 = *(const float4*)&SF.sn[c_tl][n0], s1 = *(const float4*)&SF.sn[c_tl][n0 + 4];
-                const float ca[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-                const float sa[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    cfr[kn][e] = (__bf16)(ca[e] * lo[e] + (-sa[e]) * hi[e]);
-                    cfr[kn + 4][e] = (__bf16)(ca[e] * hi[e] + sa[e] * lo[e]);
-                }
+                m3f_rows(cq[k][0], cq[k][1], cw, cb0, cb1, &SF.cs[tl][kq4], &SF.sn[tl][kq4], sgn,
+                         &SF.C[f0][b_nv * 8], &SF.C[f0 + 1][b_nv * 8], y0, y1);
             }
         }
-        // ---- the next chunk's loads land during this chunk's MFMA work
-        if (c + 1 < p.nch) fetch(c + 1);
+        // ---- the next chunk's rows land during this chunk's MFMA work
+        __builtin_amdgcn_sched_barrier(0);
+        fetch_rows(c + 1);
+        __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
-        // ---- D: state h <- exp(cs_end) h + sum_j (w_j v^T[p][j]) B[j][n], n tile = wave
-        {
+        if (wv >= 4) {
+            // ---- D (waves 4-7): h <- exp(cs_end) h + sum_j (w_j v^T[p][j]) B[j][n], n tile = w4
             const float dec = __builtin_amdgcn_exp2f(cs_end);
 #pragma unroll
             for (int v = 0; v < 16; ++v) hacc[v] *= dec;
@@ -410,28 +448,30 @@ __global__ __launch_bounds__(256, 1) void mamba3_ssd_fused(M3FusedParams p) {
                 const s3_bf16x8_t a = *(const s3_bf16x8_t*)&S.xTw[r][j0];
                 s3_bf16x8_t bo8;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) bo8[e] = __builtin_bit_cast(__bf16, S.B[j0 + e][wave * 32 + r]);
+                for (int e = 0; e < 8; ++e) bo8[e] = __builtin_bit_cast(__bf16, S.B[j0 + e][w4 * 32 + r]);
                 hacc = s3_mfma(a, bo8, hacc);
             }
 #pragma unroll
             for (int v = 0; v < 16; ++v)
-                S.h[cur ^ 1][8 * (v >> 2) + 4 * half + (v & 3)][wave * 32 + r] =
+                S.h[cur ^ 1][8 * (v >> 2) + 4 * half + (v & 3)][w4 * 32 + r] =
                     __builtin_bit_cast(bf16_t, (__bf16)hacc[v]);
-        }
-        // ---- y for output tile = wave, plus D v
-        {
+        } else {
+            // ---- D (waves 0-3): y for output tile = wave, plus D v
+            s3_bf16x8_t cfr[8];
+#pragma unroll
+            for (int kn = 0; kn < 8; ++kn) cfr[kn] = *(const s3_bf16x8_t*)&SF.C[wv * 32 + r][kn * 16 + 8 * half];
             s3_f32x16_t yacc;
-            switch (wave) {
-                case 0: ssd3_y_tile<QF, 0>(S, cfr, cur, r, half, yacc); break;
-                case 1: ssd3_y_tile<QF, 1>(S, cfr, cur, r, half, yacc); break;
-                case 2: ssd3_y_tile<QF, 2>(S, cfr, cur, r, half, yacc); break;
-                default: ssd3_y_tile<QF, 3>(S, cfr, cur, r, half, yacc); break;
+            switch (wv) {
+                case 0: ssd3_y_tile<QF, 0, true>(S, cfr, cur, r, half, yacc); break;
+                case 1: ssd3_y_tile<QF, 1, true>(S, cfr, cur, r, half, yacc); break;
+                case 2: ssd3_y_tile<QF, 2, true>(S, cfr, cur, r, half, yacc); break;
+                default: ssd3_y_tile<QF, 3, true>(S, cfr, cur, r, half, yacc); break;
             }
             if (p.Dh) {
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
                     const int pp = 8 * (v >> 2) + 4 * half + (v & 3);
-                    yacc[v] += Dv * bf16_to_f32(S.xT[pp][wave * 32 + r]);
+                    yacc[v] += Dv * bf16_to_f32(S.xT[pp][wv * 32 + r]);
                 }
             }
             // stage the 32 (position) x 32 (p) tile: lane holds y[i][p = 8(v/4) + 4 half + v%4]
@@ -439,30 +479,23 @@ __global__ __launch_bounds__(256, 1) void mamba3_ssd_fused(M3FusedParams p) {
             for (int gq = 0; gq < 4; ++gq) {
                 const s3_bf16x4_t q = {(__bf16)yacc[4 * gq], (__bf16)yacc[4 * gq + 1], (__bf16)yacc[4 * gq + 2],
                                        (__bf16)yacc[4 * gq + 3]};
-                *(s3_bf16x4_t*)&S.y[wave][r][8 * gq + 4 * half] = q;
+                *(s3_bf16x4_t*)&S.y[wv][r][8 * gq + 4 * half] = q;
             }
-            __builtin_amdgcn_wave_barrier();  // LDS ops of one wave complete in order
-            if (c + 1 < p.nch) fetch_c(c + 1);
-            // 32 rows x 64 bytes: 4 lanes per row, 16 rows per instruction
-            const int rows = min(QF, (p.L - t0) * M);
-            const __amdgpu_buffer_rsrc_t ry = buf_rsrc(yhead + (int64_t)t0 * M * p.H * 64, (uint32_t)rows * y_rs);
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                const int row = q * 16 + (lane >> 2), ch = lane & 3;
-                const uint4 val = *(const uint4*)&S.y[wave][row][ch * 8];
-                __builtin_amdgcn_raw_buffer_store_b128(
-                    __builtin_bit_cast(decltype(__builtin_amdgcn_raw_buffer_load_b128(ry, 0, 0, 0)), val), ry,
-                    (uint32_t)(wave * 32 + row) * y_rs + ch * 16, 0, 0);
-            }
+            // stored from the staging tile during the next chunk (store_y), after that
+            // chunk's waits on its prefetched loads, which then never wait on these stores
         }
         __syncthreads();  // LDS reads of this chunk done before the next commit
     }
+    if (wv < 4) store_y(p.nch - 1, tid_ & 63);
+    if (wv < 4) store_y(p.nch - 1, tid_ & 63);
+    if (wv >= 4) {
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-        const int pp = p0 + 8 * (v >> 2) + 4 * half + (v & 3);
-        p.hT[hbase + pp * N + wave * 32 + r] = hacc[v];
+        for (int v = 0; v < 16; ++v) {
+            const int pp = p0 + 8 * (v >> 2) + 4 * half_ + (v & 3);
+            p.hT[hbase + pp * N + w4 * 32 + r_] = hacc[v];
+        }
     }
-    if (ph == 0 && ang_q == 0 && ang_a < p.A) p.ang_out[bh * p.A + ang_a] = theta;
+    if (ph == 0 && (tid_ & 7) == 0 && (tid_ >> 3) < p.A) p.ang_out[bh * p.A + (tid_ >> 3)] = theta;
 }
 
 // Validates the arguments (-1 with the error set when invalid), fills the
@@ -504,7 +537,7 @@ static int m3_fused_run(const mamba3_fused_args* a, hipStream_t s, hipEvent_t ev
     if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, s));
     m3_launch_seed(pp, s);
     MAMBA_CHECK_LAUNCH();
-    const dim3 grid(fp.nb * fp.H * 2), block(256);
+    const dim3 grid(fp.nb * fp.H * 2), block(512);
     switch (pp.M) {
         case 2: hipLaunchKernelGGL(mamba3_ssd_fused<2>, grid, block, 0, s, fp); break;
         case 4: hipLaunchKernelGGL(mamba3_ssd_fused<4>, grid, block, 0, s, fp); break;

@@ -63,7 +63,10 @@ struct __align__(16) Ssd3Lds {
 // factors are per-lane scalars applied between the MFMA chains):
 //   y  = C_i.h_in;  y *= exp(cs_r0);  y += lower tiles (f_IT[j]);
 //   y *= exp(cs_i - cs_r0);  y += diagonal tile (exact per-(j, i) factor)
-template <int QF, int IT>
+// LEAN: a scheduling barrier between the lower-tile blocks, so that the
+// compiler does not hoist every block's LDS operands at once (for callers
+// that run two waves per SIMD within 256 registers).
+template <int QF, int IT, bool LEAN = false>
 __device__ __forceinline__ void ssd3_y_tile(Ssd3Lds<QF>& S, const s3_bf16x8_t (&cfr)[8], int cur, int r, int half,
                                             s3_f32x16_t& y) {
     constexpr int NK = 8;
@@ -83,6 +86,7 @@ __device__ __forceinline__ void ssd3_y_tile(Ssd3Lds<QF>& S, const s3_bf16x8_t (&
     }
 #pragma unroll
     for (int jt = 0; jt <= IT; ++jt) {
+        if constexpr (LEAN) __builtin_amdgcn_sched_barrier(0);
         s3_f32x16_t d = s3_zero();
 #pragma unroll
         for (int kn = 0; kn < NK; ++kn)
