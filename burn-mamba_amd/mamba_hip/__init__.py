@@ -9,6 +9,7 @@ from ._lib import MambaHipError, exported_symbols, lib  # noqa: F401
 from .mamba1 import (Mamba1, Mamba1Cache, Mamba1Config, conv1d_fwd, conv1d_step, mamba1_scan, scan_step,  # noqa: F401
                      selective_scan, selective_scan_step)
 from .ssd import Mamba2SsdInput, Mamba2SsdPath, ssd2_fast_path, ssd2_fwd  # noqa: F401
+from .ssd import ssd2_autograd, ssd2_bwd  # noqa: F401
 from .step import (Mamba2, Mamba2Cache, Mamba2Config, Mamba2Layer, Mamba2Stack, linear, pack_linear,  # noqa: F401
                    rmsnorm, step_ssm, step_ssm_args)
 from .step import conv_fwd as mamba2_conv_fwd, div_eps, gated_rmsnorm as mamba2_gated_rmsnorm  # noqa: F401

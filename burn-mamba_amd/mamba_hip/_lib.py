@@ -149,6 +149,23 @@ class Mamba3PrepArgs(ctypes.Structure):
     ]
 
 
+class Ssd2BwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", c_i32), ("seqlen", c_i32), ("nheads", c_i32), ("headdim", c_i32), ("ngroups", c_i32),
+        ("dstate", c_i32),
+        ("x", c_vp), ("x_sb", c_i64), ("x_sl", c_i64), ("x_sh", c_i64),
+        ("dt", c_vp), ("dt_sb", c_i64), ("dt_sl", c_i64), ("dt_sh", c_i64),
+        ("A", c_vp),
+        ("B", c_vp), ("B_sb", c_i64), ("B_sl", c_i64), ("B_sg", c_i64),
+        ("C", c_vp), ("C_sb", c_i64), ("C_sl", c_i64), ("C_sg", c_i64),
+        ("D", c_vp), ("initial_state", c_vp),
+        ("dy", c_vp), ("dy_sb", c_i64), ("dy_sl", c_i64), ("dy_sh", c_i64),
+        ("d_final_state", c_vp),
+        ("dx", c_vp), ("ddt", c_vp), ("dA", c_vp), ("dB", c_vp), ("dC", c_vp), ("dD", c_vp),
+        ("d_initial_state", c_vp),
+    ]
+
+
 class Mamba3FusedArgs(ctypes.Structure):
     _fields_ = [("prep", Mamba3PrepArgs), ("D", c_vp), ("y", c_vp), ("final_state", c_vp)]
 
@@ -258,6 +275,8 @@ _SIGNATURES = {
     "mamba_ssd2_fwd_generic": ([ctypes.POINTER(Ssd2Args), c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),
     "mamba_ssd2_fwd_timed": ([ctypes.POINTER(Ssd2Args), c_vp, ctypes.c_size_t, c_vp, c_vp, c_vp],
                              ctypes.c_int),
+    "mamba_ssd2_bwd_workspace_size": ([ctypes.POINTER(Ssd2BwdArgs)], ctypes.c_size_t),
+    "mamba_ssd2_bwd": ([ctypes.POINTER(Ssd2BwdArgs), c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),
     "mamba_ssd3_workspace_size": ([ctypes.POINTER(Ssd3Args)], ctypes.c_size_t),
     "mamba_ssd3_fast_path": ([ctypes.POINTER(Ssd3Args)], ctypes.c_int),
     "mamba_ssd3_fwd": ([ctypes.POINTER(Ssd3Args), c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),

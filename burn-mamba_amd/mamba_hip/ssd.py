@@ -21,7 +21,7 @@ from typing import Optional
 import torch
 
 from . import _lib
-from ._lib import MAMBA_BF16, MAMBA_F32, Ssd2Args, check
+from ._lib import MAMBA_BF16, MAMBA_F32, Ssd2Args, Ssd2BwdArgs, check
 
 
 def _dtype_code(t: torch.Tensor) -> int:
@@ -132,6 +132,83 @@ def ssd2_fwd(x, dt, A, B, C, D=None, initial_state=None, init_state_hpr=None, ch
         fn = L.mamba_ssd2_fwd_generic if generic else L.mamba_ssd2_fwd
         check(fn(ctypes.byref(a), wsp, ws.numel(), st), "mamba_ssd2_fwd")
     return y, final_state
+
+
+def ssd2_bwd(dy, x, dt, A, B, C, D=None, initial_state=None, d_final_state=None):
+    """The SSD forward's gradients through ``mamba_ssd2_bwd``: the Autodiff arm
+    of Mamba2BackendExt::ssd_serial_recalculated
+    (src/mamba2/ssd/serial_recalculated/backward.rs:29-321; gradient math
+    combined_backward.rs:126-593).  Inputs as ``ssd2_fwd`` (bf16 ones are read
+    as f32), dy[b,l,h,p], d_final_state[b,h,p,n] or None.  Returns a dict of f32
+    gradients: dx[b,l,h,p], ddt[b,l,h], dA[h], dB / dC[b,l,g,n] (summed over
+    each group's heads), dD[h] (None without D), d_initial_state[b,h,p,n]."""
+    b, l, h, p = x.shape
+    g, n = B.shape[2], B.shape[3]
+    f = lambda t: None if t is None else (t if t.dtype == torch.float32 else t.float())  # noqa: E731
+    x, dy, B, C, dt, A, D, initial_state, d_final_state = map(f, (x, dy, B, C, dt, A, D, initial_state,
+                                                                d_final_state))
+    for t, nm in ((x, "x"), (B, "B"), (C, "C"), (dy, "dy")):
+        _check_inner(t, nm)
+    for t in (A, D, initial_state, d_final_state):
+        if t is not None and not t.is_contiguous():
+            raise _lib.MambaHipError("A, D and the states must be contiguous")
+    dev = x.device
+    out = dict(dx=torch.empty((b, l, h, p), device=dev), ddt=torch.empty((b, l, h), device=dev),
+               dA=torch.empty(h, device=dev), dB=torch.empty((b, l, g, n), device=dev),
+               dC=torch.empty((b, l, g, n), device=dev), dD=None if D is None else torch.empty(h, device=dev),
+               d_initial_state=torch.empty((b, h, p, n), device=dev))
+    a = Ssd2BwdArgs()
+    a.batch, a.seqlen, a.nheads, a.headdim, a.ngroups, a.dstate = b, l, h, p, g, n
+    a.x = x.data_ptr(); a.x_sb, a.x_sl, a.x_sh = x.stride(0), x.stride(1), x.stride(2)
+    a.dt = dt.data_ptr(); a.dt_sb, a.dt_sl, a.dt_sh = dt.stride(0), dt.stride(1), dt.stride(2)
+    a.A = A.data_ptr()
+    a.B = B.data_ptr(); a.B_sb, a.B_sl, a.B_sg = B.stride(0), B.stride(1), B.stride(2)
+    a.C = C.data_ptr(); a.C_sb, a.C_sl, a.C_sg = C.stride(0), C.stride(1), C.stride(2)
+    a.D = None if D is None else D.data_ptr()
+    a.initial_state = None if initial_state is None else initial_state.data_ptr()
+    a.dy = dy.data_ptr(); a.dy_sb, a.dy_sl, a.dy_sh = dy.stride(0), dy.stride(1), dy.stride(2)
+    a.d_final_state = None if d_final_state is None else d_final_state.data_ptr()
+    for k in ("dx", "ddt", "dA", "dB", "dC", "dD"):
+        setattr(a, k, None if out[k] is None else out[k].data_ptr())
+    a.d_initial_state = out["d_initial_state"].data_ptr()
+    L = _lib.lib()
+    nbytes = L.mamba_ssd2_bwd_workspace_size(ctypes.byref(a))
+    if nbytes == 0:
+        check(L.mamba_ssd2_bwd(ctypes.byref(a), None, 0, _stream(dev)), "mamba_ssd2_bwd")
+    ws = workspace(dev, nbytes)
+    check(L.mamba_ssd2_bwd(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(dev)),
+          "mamba_ssd2_bwd")
+    return out
+
+
+class _Ssd2Function(torch.autograd.Function):
+    """The SSD as one differentiable node: ``mamba_ssd2_fwd`` forward,
+    ``mamba_ssd2_bwd`` backward from the saved leaf inputs (the reference's
+    Autodiff arm, backward.rs:29-321: one node for both outputs, intermediates
+    recomputed rather than kept)."""
+
+    @staticmethod
+    def forward(ctx, x, dt, A, B, C, D, initial_state, chunk_len):
+        y, hT = ssd2_fwd(x, dt, A, B, C, D, initial_state, chunk_len=chunk_len)
+        ctx.save_for_backward(x, dt, A, B, C, D, initial_state)
+        return y, hT
+
+    @staticmethod
+    def backward(ctx, dy, dhT):
+        x, dt, A, B, C, D, h0 = ctx.saved_tensors
+        if dy is None:
+            dy = torch.zeros(x.shape, device=x.device)
+        gr = ssd2_bwd(dy.contiguous(), x, dt, A, B, C, D, h0, None if dhT is None else dhT.contiguous())
+        cast = lambda t, like: None if t is None else t.to(like.dtype)  # noqa: E731
+        return (cast(gr["dx"], x), gr["ddt"], gr["dA"], cast(gr["dB"], B), cast(gr["dC"], C), gr["dD"],
+                None if h0 is None else gr["d_initial_state"], None)
+
+
+def ssd2_autograd(x, dt, A, B, C, D=None, initial_state=None, chunk_len=None):
+    """``ssd2_fwd`` as a differentiable op (torch.autograd), returning
+    (y, final_state); gradients flow to x, dt, A, B, C, D and initial_state
+    through ``mamba_ssd2_bwd``."""
+    return _Ssd2Function.apply(x, dt, A, B, C, D, initial_state, chunk_len)
 
 
 def _raw_events(events, device):

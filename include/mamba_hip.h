@@ -134,6 +134,47 @@ int mamba_ssd2_fwd_timed(const mamba_ssd2_args* args, void* workspace, size_t wo
                          mamba_stream_t stream, void* event_start, void* event_stop);
 
 /* ------------------------------------------------------------------------- */
+/* Mamba-2 SSD backward (recompute form): the gradients of mamba_ssd2_fwd's    */
+/* y and final state with respect to x, dt, A, B, C, D and the initial state,  */
+/* given dy and d(final state).  Replaces the Autodiff arm of                  */
+/* Mamba2BackendExt::ssd_serial_recalculated                                   */
+/* (src/mamba2/ssd/serial_recalculated/backward.rs:29-321) and its gradient   */
+/* math, combined_backward (combined_backward.rs:126-593): the forward's chunk */
+/* states are recomputed into the workspace, then a reverse chunk loop         */
+/* carries the state gradient.  f32 inputs and gradients; layouts and strides  */
+/* as mamba_ssd2_args; dB / dC are per group (summed over the group's heads in */
+/* head order; with ngroups = nheads they are per head, as the reference's    */
+/* expanded B / C).  init_state_hpr is not supported (the reference's serial  */
+/* path asserts it absent, src/mamba2/ssd/serial.rs:48-51).  headdim x dstate */
+/* <= 8192.  Deterministic (no atomics).                                       */
+/* ------------------------------------------------------------------------- */
+typedef struct mamba_ssd2_bwd_args {
+    int32_t batch, seqlen, nheads, headdim, ngroups, dstate;
+    const float* x;  int64_t x_sb, x_sl, x_sh;      /* [b, l, h, p]           */
+    const float* dt; int64_t dt_sb, dt_sl, dt_sh;   /* [b, l, h]              */
+    const float* A;                                  /* [h]                    */
+    const float* B;  int64_t B_sb, B_sl, B_sg;      /* [b, l, g, n]           */
+    const float* C;  int64_t C_sb, C_sl, C_sg;      /* [b, l, g, n]           */
+    const float* D;                                  /* [h] or NULL (= 0)      */
+    const float* initial_state;                      /* [b, h, p, n] or NULL   */
+    const float* dy; int64_t dy_sb, dy_sl, dy_sh;   /* [b, l, h, p]           */
+    const float* d_final_state;                      /* [b, h, p, n] or NULL   */
+    float* dx;                                       /* [b, l, h, p] contiguous */
+    float* ddt;                                      /* [b, l, h] contiguous   */
+    float* dA;                                       /* [h]                    */
+    float* dB;                                       /* [b, l, g, n] contiguous */
+    float* dC;                                       /* [b, l, g, n] contiguous */
+    float* dD;                                       /* [h] or NULL            */
+    float* d_initial_state;                          /* [b, h, p, n]           */
+} mamba_ssd2_bwd_args;
+
+/* Workspace bytes (chunk states, per-head dB / dC when ngroups < nheads,     */
+/* per-(batch, head) partial sums); 0 if the arguments are invalid.            */
+size_t mamba_ssd2_bwd_workspace_size(const mamba_ssd2_bwd_args* args);
+int mamba_ssd2_bwd(const mamba_ssd2_bwd_args* args, void* workspace, size_t workspace_bytes,
+                   mamba_stream_t stream);
+
+/* ------------------------------------------------------------------------- */
 /* Mamba-3 single-pass chunked SSD forward (trapezoidal discretisation, MIMO   */
 /* rank M fused into the time axis):                                           */
 /*                                                                             */

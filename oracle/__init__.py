@@ -90,6 +90,59 @@ def ssd2(x, dt, A, B, C, D=None, h0=None, init_hpr=None, chunk=64, form="serial"
     return y, hT
 
 
+def ssd2_bwd(dy, dfinal, x, dt, A, B, C, D=None, h0=None):
+    """Gradients of the Mamba-2 SSD forward (oracle.ssd2) in float64 numpy, by
+    the per-token reverse recurrence: the analytic backward of
+    Mamba2BackendExt::ssd_serial_recalculated that
+    src/mamba2/ssd/serial_recalculated/combined_backward.rs:126-593 computes
+    chunk-wise (its Autodiff arm, backward.rs:29-321), here token by token.
+
+    Forward per (b, head): h_t = exp(dt_t A) h_{t-1} + dt_t x_t B_t^T,
+    y_t = h_t C_t + D x_t, final state h_L.  With L = sum dy.y + sum dfinal.h_L
+    and G_t = dL/dh_t (G_L = dfinal + dy_L C_L^T, G_{t-1} = exp(dt_t A) G_t +
+    dy_{t-1} C_{t-1}^T):
+      dC_t = h_t^T dy_t, dx_t = D dy_t + dt_t G_t B_t, dB_t = dt_t G_t^T x_t,
+      d(dt_t A) = exp(dt_t A) <G_t, h_{t-1}>, ddt_t = A d(dt_t A) + x_t^T G_t B_t,
+      dA = sum_t dt_t d(dt_t A), dD = sum_t x_t . dy_t, dh0 = exp(dt_1 A) G_1.
+    x, dy [b,l,h,p]; dt [b,l,h]; A [h]; B, C [b,l,g,n] (group form, dB / dC
+    summed over the group's heads); D [h] or None; h0 [b,h,p,n] or None;
+    dfinal [b,h,p,n] or None.  Returns a dict of float64 gradients."""
+    f = lambda t: None if t is None else np.asarray(t, np.float64)  # noqa: E731
+    dy, dfinal, x, dt, A, B, C, D, h0 = map(f, (dy, dfinal, x, dt, A, B, C, D, h0))
+    b, l, h, p = x.shape
+    g, n = B.shape[2], B.shape[3]
+    rep = h // g
+    Bh = np.repeat(B, rep, axis=2)   # [b, l, h, n]
+    Ch = np.repeat(C, rep, axis=2)
+    Dv = np.zeros(h) if D is None else D
+    da = dt * A[None, None, :]       # [b, l, h]
+    hs = np.zeros((l + 1, b, h, p, n))
+    hs[0] = 0.0 if h0 is None else h0
+    for t in range(l):
+        hs[t + 1] = np.exp(da[:, t])[:, :, None, None] * hs[t] + \
+            (dt[:, t][:, :, None] * x[:, t])[..., None] * Bh[:, t][:, :, None, :]
+    G = np.zeros((b, h, p, n)) if dfinal is None else dfinal.copy()
+    dx = np.zeros_like(x)
+    ddt = np.zeros_like(dt)
+    dBh = np.zeros_like(Bh)
+    dCh = np.zeros_like(Ch)
+    dA = np.zeros(h)
+    for t in range(l - 1, -1, -1):
+        G = G + dy[:, t][..., None] * Ch[:, t][:, :, None, :]
+        dCh[:, t] = np.einsum("bhpn,bhp->bhn", hs[t + 1], dy[:, t])
+        GB = np.einsum("bhpn,bhn->bhp", G, Bh[:, t])
+        dx[:, t] = Dv[None, :, None] * dy[:, t] + dt[:, t][..., None] * GB
+        dBh[:, t] = dt[:, t][..., None] * np.einsum("bhpn,bhp->bhn", G, x[:, t])
+        dda = np.exp(da[:, t]) * np.einsum("bhpn,bhpn->bh", G, hs[t])
+        xGB = np.einsum("bhp,bhp->bh", x[:, t], GB)
+        ddt[:, t] = A[None, :] * dda + xGB
+        dA += (dt[:, t] * dda).sum(0)
+        G = np.exp(da[:, t])[:, :, None, None] * G
+    dD = np.einsum("blhp,blhp->h", x, dy)
+    return dict(dx=dx, ddt=ddt, dA=dA, dB=dBh.reshape(b, l, g, rep, n).sum(3),
+                dC=dCh.reshape(b, l, g, rep, n).sum(3), dD=dD, dh0=G)
+
+
 # --------------------------------------------------------------------------
 # Mamba-1 selective scan (src/mamba1/mamba1.rs:422-523, :666-733)
 # --------------------------------------------------------------------------

@@ -60,6 +60,7 @@ int main(void) {{ printf("%zu\\n", sizeof({struct_name})); {body} return 0; }}
                                              ("Mamba3PrepArgs", "mamba3_prep_args"),
                                              ("Mamba3FinishArgs", "mamba3_finish_args"),
                                              ("Mamba3FusedArgs", "mamba3_fused_args"),
+                                             ("Ssd2BwdArgs", "mamba_ssd2_bwd_args"),
                                              ("Mamba3DoubleInputsArgs", "mamba3_double_inputs_args"),
                                              ("LinearArgs", "mamba_linear_args"),
                                              ("Mamba2LayerArgs", "mamba2_layer_args"),

@@ -773,3 +773,82 @@ def test_mamba1_block_forward_short_sequence_window():
     xs = oracle.linear(x.reshape(b * L, dm), p["in_proj_w"])[:, :ex * dm].reshape(b, L, ex * dm)
     pad = np.concatenate([conv0[:, :, 1:], xs.transpose(0, 2, 1)], axis=2)
     np.testing.assert_allclose(conv, pad[:, :, L - 1:L - 1 + k], rtol=1e-6, atol=1e-6)
+
+
+# --------------------------------------------------------------------------
+# Mamba-2 SSD backward (oracle.ssd2_bwd): pinned by finite differences of an
+# independent float64 forward in the segsum (matrix) form, itself tied to
+# oracle.ssd2, and by closed forms.
+# --------------------------------------------------------------------------
+
+def _ssd2_fwd64(x, dt, A, B, C, D, h0):
+    """Whole-sequence segsum form (ssd_minimal with one chunk, minimal.rs:95-496)
+    in float64: y = (L o C B^T)(dt x) + exp(cs) C h0^T + D x, h_L from the same
+    weights.  Independent of the recurrence the backward oracle runs."""
+    b, l, h, p = x.shape
+    g = B.shape[2]
+    rep = h // g
+    Bh, Ch = np.repeat(B, rep, axis=2), np.repeat(C, rep, axis=2)
+    cs = np.cumsum(dt * A[None, None, :], axis=1)                     # [b, l, h]
+    seg = cs[:, :, None, :] - cs[:, None, :, :]                      # [b, t, s, h]
+    tri = np.tril(np.ones((l, l), bool))[None, :, :, None]
+    Lm = np.where(tri, np.exp(np.where(tri, seg, 0.0)), 0.0)
+    CB = np.einsum("bthn,bshn->btsh", Ch, Bh)
+    y = np.einsum("btsh,bsh,bshp->bthp", Lm * CB, dt, x)
+    y += np.exp(cs)[..., None] * np.einsum("bthn,bhpn->bthp", Ch, h0)
+    y += D[None, None, :, None] * x
+    wend = np.exp(cs[:, -1:, :] - cs) * dt                            # [b, s, h]
+    hT = np.exp(cs[:, -1])[:, :, None, None] * h0 + np.einsum("bsh,bshp,bshn->bhpn", wend, x, Bh)
+    return y, hT
+
+
+def _ssd2_bwd_case(seed, b=1, l=6, h=2, p=3, g=1, n=4):
+    rng = np.random.default_rng(seed)
+    r = lambda *s: rng.standard_normal(s)  # noqa: E731
+    return dict(x=r(b, l, h, p), dt=rng.uniform(0.05, 0.6, (b, l, h)), A=-rng.uniform(0.3, 2.0, h),
+                B=r(b, l, g, n), C=r(b, l, g, n), D=r(h), h0=r(b, h, p, n)), r(b, l, h, p), r(b, h, p, n)
+
+
+def test_ssd2_fwd64_matches_oracle_forward():
+    """The float64 matrix form used for the finite differences equals oracle.ssd2."""
+    inp, _, _ = _ssd2_bwd_case(3, b=2, l=9, h=4, p=5, g=2, n=6)
+    y, hT = _ssd2_fwd64(**inp)
+    yo, ho = oracle.ssd2(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"], inp["h0"], form="recurrent")
+    np.testing.assert_allclose(y, yo, rtol=2e-6, atol=2e-6)
+    np.testing.assert_allclose(hT, ho, rtol=2e-6, atol=2e-6)
+
+
+@pytest.mark.parametrize("g", [1, 2])
+def test_ssd2_bwd_equals_finite_differences(g):
+    """Every gradient of oracle.ssd2_bwd equals the central difference of
+    L = sum dy.y + sum dfinal.h_L through the float64 forward, at every
+    coordinate (tiny shapes; dB/dC in group form sum the group's heads)."""
+    inp, dy, dF = _ssd2_bwd_case(11 + g, b=2, l=5, h=2, p=3, g=g, n=4)
+    grads = oracle.ssd2_bwd(dy, dF, **inp)
+
+    def loss(a):
+        y, hT = _ssd2_fwd64(**a)
+        return float((y * dy).sum() + (hT * dF).sum())
+    eps = 1e-6
+    names = dict(x="dx", dt="ddt", A="dA", B="dB", C="dC", D="dD", h0="dh0")
+    for k, gk in names.items():
+        fd = np.zeros_like(inp[k])
+        for idx in np.ndindex(inp[k].shape):
+            a = {kk: vv.copy() for kk, vv in inp.items()}
+            a[k][idx] += eps
+            lp = loss(a)
+            a[k][idx] -= 2 * eps
+            fd[idx] = (lp - loss(a)) / (2 * eps)
+        np.testing.assert_allclose(grads[gk], fd, rtol=1e-6, atol=1e-7, err_msg=k)
+
+
+def test_ssd2_bwd_closed_forms():
+    """With dy = 0 only the final state carries gradient: dh0 = exp(A sum dt)
+    dfinal and dC = 0; dD = sum x.dy for any dy."""
+    inp, dy, dF = _ssd2_bwd_case(21, b=2, l=7, h=3, p=2, g=1, n=3)
+    gz = oracle.ssd2_bwd(np.zeros_like(dy), dF, **inp)
+    decay = np.exp(inp["A"][None, :] * inp["dt"].sum(1))              # [b, h]
+    np.testing.assert_allclose(gz["dh0"], decay[:, :, None, None] * dF, rtol=1e-12)
+    np.testing.assert_allclose(gz["dC"], 0.0, atol=0)
+    gd = oracle.ssd2_bwd(dy, None, **inp)
+    np.testing.assert_allclose(gd["dD"], np.einsum("blhp,blhp->h", inp["x"], dy), rtol=1e-12)
