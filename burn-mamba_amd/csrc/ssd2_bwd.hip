@@ -282,6 +282,454 @@ __global__ __launch_bounds__(kBwdT) void ssd2_bwd_chunks(Ssd2BwdParams p) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// MFMA path for headdim 64 x dstate 128 (the config-1 head shape): the same
+// recurrences with every P x N x Q and Q x Q x (P | N) contraction on
+// v_mfma_f32_32x32x2_f32 (f32 operands and accumulation).  For that
+// instruction lane l supplies A[l % 32][k0 + l / 32] and B[k0 + l / 32][l % 32],
+// and accumulator r of lane l holds D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32].
+// LDS rows are padded to an odd number of words, so that both the K-major
+// reads (32 rows, one column) and the row-major reads (32 consecutive words)
+// of a half-wave fall in 32 distinct banks.
+typedef float bwd_f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kFP = 64, kFN = 128;                 // headdim, dstate of this path
+constexpr int kSX = 65, kSB = 129, kSQ = 33;       // padded row lengths (words)
+
+__device__ __forceinline__ bwd_f32x16 bwd_mfma(float a, float b, bwd_f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+// the accumulator row of register r for a lane in wave half hf
+__device__ __forceinline__ int bwd_row(int r, int hf) { return 8 * (r >> 2) + 4 * hf + (r & 3); }
+
+// Sum of 16 per-lane values over the 32 lanes of a wave half, scattered: lane
+// i32 returns the total of value (i32 >> 1) (both lanes of a pair hold it).
+__device__ __forceinline__ float bwd_half_sum16(const float (&v)[16], int i32) {
+    float w[8], x[4], y[2];
+    const bool b4 = (i32 >> 4) & 1, b3 = (i32 >> 3) & 1, b2 = (i32 >> 2) & 1, b1 = (i32 >> 1) & 1;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) w[q] = (b4 ? v[8 + q] : v[q]) + __shfl_xor(b4 ? v[q] : v[8 + q], 16, 64);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) x[q] = (b3 ? w[4 + q] : w[q]) + __shfl_xor(b3 ? w[q] : w[4 + q], 8, 64);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) y[q] = (b2 ? x[2 + q] : x[q]) + __shfl_xor(b2 ? x[q] : x[2 + q], 4, 64);
+    float z = (b1 ? y[1] : y[0]) + __shfl_xor(b1 ? y[0] : y[1], 2, 64);
+    return z + __shfl_xor(z, 1, 64);
+}
+// Sum over the 32 lanes of a wave half (every lane of the half gets it).
+__device__ __forceinline__ float bwd_half_sum(float v) {
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// One chunk's inputs in registers (loaded ahead, written to LDS later).
+struct BwdRows {
+    float4 x, dy, B0, B1, C0, C1;
+    float dt;
+};
+
+struct BwdFastLds {
+    float g[kFP * kSB];      // [p][n] gradient of the state leaving the chunk
+    float x[32 * kSX];       // [j][p]
+    float dy[32 * kSX];      // [j][p]
+    float B[32 * kSB];       // [j][n]
+    float C[32 * kSB];       // [j][n]
+    float E1[32 * kSQ];      // [k][i] C_k . B_i, then e_ki C_k . B_i (0 above the diagonal)
+    float DX[32 * kSQ];      // [k][i] dy_k . x_i
+    float E2[32 * kSQ];      // [k][i] e_ki dy_k . x_i
+    float E3T[32 * kSQ];     // [i][k] e_ki dt_i dy_k . x_i
+    float dt[32], cs[32], av[32], bv[32];
+    float xu[2][32];         // x_j . g B_j, per 32-row half of p
+    float dv[4][32];         // C_k . h_c^T dy_k, per 32-column quarter of n
+    float ghc[4];            // <g, h_c>, per quarter of n
+    float cpart[2][8][32];   // per-wave column sums: s2, then sum_k e_kj (C_k.B_j) (dy_k.x_j)
+    float rs1[32], rrow[32]; // row sums: s1_j, and the row sums of M
+};
+
+// Loads chunk c's rows of x, dy, B, C, dt for a 512-thread block (rows past
+// the sequence end read as zero; their loads are clamped to the last row).
+__device__ __forceinline__ void bwd_fetch(const Ssd2BwdParams& p, const float* xb, const float* yb, const float* Bb,
+                                          const float* Cb, const float* db, int c, int tid, BwdRows& f) {
+    const int t0 = c * 32;
+    const int ix = tid >> 4, cx = (tid & 15) * 4;
+    const int ib = tid >> 5, cb = (tid & 31) * 4;
+    const float4 z = {0.f, 0.f, 0.f, 0.f};
+    const int tx = t0 + ix, tb0 = t0 + ib, tb1 = t0 + ib + 16, tt = t0 + (tid & 31);
+    const float4 vx = *reinterpret_cast<const float4*>(xb + (int64_t)min(tx, p.L - 1) * p.x_sl + cx);
+    const float4 vy = *reinterpret_cast<const float4*>(yb + (int64_t)min(tx, p.L - 1) * p.dy_sl + cx);
+    const float4 vb0 = *reinterpret_cast<const float4*>(Bb + (int64_t)min(tb0, p.L - 1) * p.B_sl + cb);
+    const float4 vb1 = *reinterpret_cast<const float4*>(Bb + (int64_t)min(tb1, p.L - 1) * p.B_sl + cb);
+    const float4 vc0 = *reinterpret_cast<const float4*>(Cb + (int64_t)min(tb0, p.L - 1) * p.C_sl + cb);
+    const float4 vc1 = *reinterpret_cast<const float4*>(Cb + (int64_t)min(tb1, p.L - 1) * p.C_sl + cb);
+    const float vt = db[(int64_t)min(tt, p.L - 1) * p.dt_sl];
+    f.x = tx < p.L ? vx : z;
+    f.dy = tx < p.L ? vy : z;
+    f.B0 = tb0 < p.L ? vb0 : z;
+    f.B1 = tb1 < p.L ? vb1 : z;
+    f.C0 = tb0 < p.L ? vc0 : z;
+    f.C1 = tb1 < p.L ? vc1 : z;
+    f.dt = tt < p.L ? vt : 0.f;
+}
+
+__device__ __forceinline__ void bwd_put4(float* dst, float4 v) {
+    dst[0] = v.x;
+    dst[1] = v.y;
+    dst[2] = v.z;
+    dst[3] = v.w;
+}
+
+// Writes fetched rows to LDS; wave 0 also forms cs, a = exp(cs_end - cs),
+// b = exp(cs) from dt.
+__device__ __forceinline__ void bwd_commit(BwdFastLds& S, const BwdRows& f, float A, int tid) {
+    const int ix = tid >> 4, cx = (tid & 15) * 4;
+    const int ib = tid >> 5, cb = (tid & 31) * 4;
+    bwd_put4(&S.x[ix * kSX + cx], f.x);
+    bwd_put4(&S.dy[ix * kSX + cx], f.dy);
+    bwd_put4(&S.B[ib * kSB + cb], f.B0);
+    bwd_put4(&S.B[(ib + 16) * kSB + cb], f.B1);
+    bwd_put4(&S.C[ib * kSB + cb], f.C0);
+    bwd_put4(&S.C[(ib + 16) * kSB + cb], f.C1);
+    if (tid < 64) {
+        const int lane = tid;
+        const float cs = wave_incl_scan(lane < 32 ? f.dt * A : 0.f);
+        const float tot = __shfl(cs, 31, 64);
+        if (lane < 32) {
+            S.dt[lane] = f.dt;
+            S.cs[lane] = cs;
+            S.av[lane] = __expf(tot - cs);
+            S.bv[lane] = __expf(cs);
+        }
+    }
+}
+
+// The reverse chunk loop on MFMA.  One 512-thread workgroup per (batch, head),
+// eight waves with fixed roles per phase:
+//   phase 1  waves 0-1: u = g B_j (one 32-column half of p each, K = n)
+//            waves 2-5: g^T x_j and h_c^T dy_j (one quarter of n each, K = p;
+//                       h_c's columns for the wave sit in registers)
+//            wave 6: C_k . B_i;  wave 7: dy_k . x_i
+//   then the Q x Q decay-weighted matrices and their row / column sums on
+//   every thread, and
+//   phase 2  waves 0-1: G_j B_j = a_j g B_j + sum_k e_kj (C_k.B_j) dy_k -> dx
+//            waves 2-5: dB_j, dC_j (continuing the phase-1 accumulators)
+//            waves 0, 1, 6, 7: the update of g (two 32 x 32 tiles each)
+//            wave 7: the per-position scalars (d(da_j), ddt_j, dA / dD partials).
+// The next chunk's rows (and h_c columns) are loaded during the two phases.
+__global__ __launch_bounds__(512, 1) void ssd2_bwd_chunks_mfma(Ssd2BwdParams p) {
+    __shared__ BwdFastLds S;
+    const int tid = threadIdx.x, wv = wave_id(), lane = tid & 63, i32 = lane & 31, hf = lane >> 5;
+    const int b = blockIdx.x / p.H, h = blockIdx.x % p.H, grp = h / (p.H / p.G);
+    const int64_t bh = (int64_t)b * p.H + h;
+    const float A = p.A[h], Dh = p.D ? p.D[h] : 0.f;
+    const float* xb = p.x + (int64_t)b * p.x_sb + (int64_t)h * p.x_sh;
+    const float* yb = p.dy + (int64_t)b * p.dy_sb + (int64_t)h * p.dy_sh;
+    const float* Bb = p.B + (int64_t)b * p.B_sb + (int64_t)grp * p.B_sg;
+    const float* Cb = p.C + (int64_t)b * p.C_sb + (int64_t)grp * p.C_sg;
+    const float* db = p.dt + (int64_t)b * p.dt_sb + (int64_t)h * p.dt_sh;
+    const int tq = wv - 2;  // n quarter of waves 2-5
+    // h_c columns of waves 2-5: hreg[m] = h_c[2 m + hf][32 tq + i32]; reloaded
+    // with the next chunk's as soon as the current chunk's last use is done
+    float hreg[32];
+    auto fetch_h = [&](int c, float (&dst)[32]) {
+        const float* src = p.hs + (bh * p.nch + c) * (kFP * kFN) + hf * kFN + 32 * tq + i32;
+#pragma unroll
+        for (int m = 0; m < 32; ++m) dst[m] = src[m * 2 * kFN];
+    };
+    for (int e = tid; e < kFP * kFN; e += 512) S.g[(e >> 7) * kSB + (e & 127)] = p.dfin ? p.dfin[bh * (kFP * kFN) + e] : 0.f;
+    BwdRows pre;
+    bwd_fetch(p, xb, yb, Bb, Cb, db, p.nch - 1, tid, pre);
+    if (wv >= 2 && wv < 6) fetch_h(p.nch - 1, hreg);
+    bwd_commit(S, pre, A, tid);
+    float accA = 0.f, accD = 0.f;
+    __syncthreads();
+    for (int c = p.nch - 1; c >= 0; --c) {
+        const int t0 = c * 32;
+        const int cn = c > 0 ? c - 1 : 0;  // the next chunk (reloads chunk 0 at the end; unused)
+        // per-chunk opaque copy of the thread index: the LDS addresses derived
+        // from it are then formed inside the loop instead of being hoisted out
+        // of it (dozens of loop-invariant addresses would not fit in registers)
+        int tid = threadIdx.x;
+        asm volatile("" : "+v"(tid));
+        const int lane = tid & 63, i32 = lane & 31, hf = lane >> 5;
+        bwd_fetch(p, xb, yb, Bb, Cb, db, cn, tid, pre);
+        // ---- phase 1
+        bwd_f32x16 acc0 = {}, acc1 = {};
+        if (wv < 2) {
+            const float* Ap = S.B + i32 * kSB + hf;
+            const float* Bp = S.g + (32 * wv + i32) * kSB + hf;
+#pragma unroll 16
+            for (int n0 = 0; n0 < kFN; n0 += 2) acc0 = bwd_mfma(Ap[n0], Bp[n0], acc0);
+        } else if (wv < 6) {
+            const float* Ax = S.x + i32 * kSX + hf;
+            const float* Ay = S.dy + i32 * kSX + hf;
+            const float* Bg = S.g + hf * kSB + 32 * tq + i32;
+#pragma unroll
+            for (int m = 0; m < 32; ++m) {
+                acc0 = bwd_mfma(Ax[2 * m], Bg[2 * m * kSB], acc0);
+                acc1 = bwd_mfma(Ay[2 * m], hreg[m], acc1);
+                if ((m & 7) == 7) __builtin_amdgcn_sched_barrier(0);  // bounds the operand prefetch
+            }
+        } else if (wv == 6) {
+            const float* Ap = S.C + i32 * kSB + hf;
+            const float* Bp = S.B + i32 * kSB + hf;
+#pragma unroll 16
+            for (int n0 = 0; n0 < kFN; n0 += 2) acc0 = bwd_mfma(Ap[n0], Bp[n0], acc0);
+        } else {
+            const float* Ap = S.dy + i32 * kSX + hf;
+            const float* Bp = S.x + i32 * kSX + hf;
+#pragma unroll 16
+            for (int p0 = 0; p0 < kFP; p0 += 2) acc0 = bwd_mfma(Ap[p0], Bp[p0], acc0);
+        }
+        // ---- per-wave reductions of the phase-1 products
+        {
+            float v[16];
+            if (wv < 2) {  // x_j . g B_j over this half of p
+#pragma unroll
+                for (int r = 0; r < 16; ++r) v[r] = acc0[r] * S.x[bwd_row(r, hf) * kSX + 32 * wv + i32];
+                const float s = bwd_half_sum16(v, i32);
+                if ((i32 & 1) == 0) S.xu[wv][bwd_row(i32 >> 1, hf)] = s;
+            } else if (wv < 6) {  // C_k . h_c^T dy_k over this quarter of n; <g, h_c>
+#pragma unroll
+                for (int r = 0; r < 16; ++r) v[r] = acc1[r] * S.C[bwd_row(r, hf) * kSB + 32 * tq + i32];
+                const float s = bwd_half_sum16(v, i32);
+                if ((i32 & 1) == 0) S.dv[tq][bwd_row(i32 >> 1, hf)] = s;
+                float gh = 0.f;
+#pragma unroll
+                for (int m = 0; m < 32; ++m) gh += hreg[m] * S.g[(2 * m + hf) * kSB + 32 * tq + i32];
+                gh = wave_sum(gh);
+                if (lane == 0) S.ghc[tq] = gh;
+                fetch_h(cn, hreg);
+            } else {
+                float* dst = wv == 6 ? S.E1 : S.DX;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) dst[bwd_row(r, hf) * kSQ + i32] = acc0[r];
+            }
+        }
+        __syncthreads();
+        // ---- the decay-weighted Q x Q matrices; row sums s1 and M, column sums s2 and xg2
+        {
+            const int i = i32, k0 = 4 * wv + 2 * hf;
+            const float cs_i = S.cs[i], dt_i = S.dt[i];
+            const float xu_i = S.xu[0][i] + S.xu[1][i];
+            float rsum[4], s2c = 0.f, xgc = 0.f;
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const int k = k0 + q;
+                const float e = k >= i ? __expf(S.cs[k] - cs_i) : 0.f;
+                const float e1 = e * S.E1[k * kSQ + i];
+                const float dx = S.DX[k * kSQ + i];
+                S.E1[k * kSQ + i] = e1;
+                S.E2[k * kSQ + i] = e * dx;
+                S.E3T[i * kSQ + k] = e * dt_i * dx;
+                rsum[q] = e * dt_i * xu_i;
+                rsum[2 + q] = e1 * dt_i * dx;
+                s2c += e * ((S.dv[0][k] + S.dv[1][k]) + (S.dv[2][k] + S.dv[3][k]));
+                xgc += e1 * dx;
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) rsum[q] = bwd_half_sum(rsum[q]);
+            if (i32 < 2) {
+                S.rs1[k0 + i32] = rsum[i32];
+                S.rrow[k0 + i32] = rsum[2 + i32];
+            }
+            s2c += __shfl_xor(s2c, 32, 64);
+            xgc += __shfl_xor(xgc, 32, 64);
+            if (hf == 0) {
+                S.cpart[0][wv][i] = s2c;
+                S.cpart[1][wv][i] = xgc;
+            }
+        }
+        __syncthreads();
+        // ---- phase 2
+        if (wv < 2) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc0[r] *= S.av[bwd_row(r, hf)];
+            const float* Ap = S.E1 + hf * kSQ + i32;
+            const float* Bp = S.dy + hf * kSX + 32 * wv + i32;
+#pragma unroll
+            for (int k0 = 0; k0 < 32; k0 += 2) acc0 = bwd_mfma(Ap[k0 * kSQ], Bp[k0 * kSX], acc0);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int j = bwd_row(r, hf);
+                if (t0 + j < p.L)
+                    p.dx[(((int64_t)b * p.L + t0 + j) * p.H + h) * kFP + 32 * wv + i32] =
+                        Dh * S.dy[j * kSX + 32 * wv + i32] + S.dt[j] * acc0[r];
+            }
+        } else if (wv < 6) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                acc0[r] *= S.av[bwd_row(r, hf)];
+                acc1[r] *= S.bv[bwd_row(r, hf)];
+            }
+            const float* A2 = S.E2 + hf * kSQ + i32;
+            const float* A3 = S.E3T + hf * kSQ + i32;
+            const float* Bc = S.C + hf * kSB + 32 * tq + i32;
+            const float* Bbp = S.B + hf * kSB + 32 * tq + i32;
+#pragma unroll
+            for (int k0 = 0; k0 < 32; k0 += 2) {
+                acc0 = bwd_mfma(A2[k0 * kSQ], Bc[k0 * kSB], acc0);
+                acc1 = bwd_mfma(A3[k0 * kSQ], Bbp[k0 * kSB], acc1);
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int j = bwd_row(r, hf);
+                if (t0 + j < p.L) {
+                    const int64_t o = (((int64_t)b * p.L + t0 + j) * p.H + h) * kFN + 32 * tq + i32;
+                    p.dBh[o] = S.dt[j] * acc0[r];
+                    p.dCh[o] = acc1[r];
+                }
+            }
+        } else if (wv == 7) {
+            // per position j (lanes 0-31): <G_j, H_j>, d(da_j), ddt_j
+            const int j = i32;
+            const bool live = lane < 32;
+            float s2 = 0.f, xg2 = 0.f;
+#pragma unroll
+            for (int w = 0; w < 8; ++w) {
+                s2 += S.cpart[0][w][j];
+                xg2 += S.cpart[1][w][j];
+            }
+            const float dtj = S.dt[j], avj = S.av[j], bvj = S.bv[j];
+            const float xu = S.xu[0][j] + S.xu[1][j];
+            const float ghc = (S.ghc[0] + S.ghc[1]) + (S.ghc[2] + S.ghc[3]);
+            const float colm = live ? dtj * xg2 : 0.f, rowm = live ? S.rrow[j] : 0.f;
+            const float pc = wave_incl_scan(colm);
+            const float pr = wave_incl_scan(rowm) - rowm;
+            const float gh = avj * bvj * ghc + avj * S.rs1[j] + bvj * s2 + (pc - pr);
+            const float xgb = avj * xu + xg2;
+            const float dda = gh - dtj * xgb;
+            if (live && t0 + j < p.L) {
+                p.ddt[(int64_t)b * p.L * p.H + (int64_t)(t0 + j) * p.H + h] = A * dda + xgb;
+                accA += dtj * dda;
+                accD += S.DX[j * kSQ + j];
+            }
+        }
+        // the gradient entering this chunk: exp(cs_end) g + sum_k b_k dy_k C_k^T
+        if (wv < 2 || wv >= 6) {
+            const float dec = __expf(S.cs[31]);
+            const int gt0 = wv < 2 ? 2 * wv : 2 * wv - 8;
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                const int tile = gt0 + tt, tp = tile >> 2, tn = tile & 3;
+                float* gp = S.g + (32 * tp) * kSB + 32 * tn + i32;
+                bwd_f32x16 a;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) a[r] = dec * gp[bwd_row(r, hf) * kSB];
+                const float* Ap = S.dy + hf * kSX + 32 * tp + i32;
+                const float* Bp = S.C + hf * kSB + 32 * tn + i32;
+#pragma unroll
+                for (int k0 = 0; k0 < 32; k0 += 2) a = bwd_mfma(S.bv[k0 + hf] * Ap[k0 * kSX], Bp[k0 * kSB], a);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) gp[bwd_row(r, hf) * kSB] = a[r];
+            }
+        }
+        __syncthreads();
+        bwd_commit(S, pre, A, tid);
+        __syncthreads();
+    }
+    for (int e = tid; e < kFP * kFN; e += 512) p.dh0[bh * (kFP * kFN) + e] = S.g[(e >> 7) * kSB + (e & 127)];
+    if (wv == 7) {
+        const float sA = wave_sum(accA), sD = wave_sum(accD);
+        if (lane == 0) {
+            p.pA[bh] = sA;
+            p.pD[bh] = sD;
+        }
+    }
+}
+
+// Chunk-entry states on MFMA (headdim 64 x dstate 128): one 256-thread
+// workgroup per (batch, head); wave w keeps two 32 x 32 tiles of the state
+// (rows 32 (w / 2).., columns 64 (w % 2)..) as accumulators across chunks,
+// stores them as chunk c's entry state, then adds
+//   exp(cs_end) h + sum_i exp(cs_end - cs_i) dt_i x_i B_i^T.
+struct BwdStatesLds {
+    float x[32 * kSX];
+    float B[32 * kSB];
+    float w[32];
+    float dec;
+};
+
+__global__ __launch_bounds__(256, 3) void ssd2_bwd_states_mfma(Ssd2BwdParams p) {
+    __shared__ BwdStatesLds S;
+    const int tid = threadIdx.x, wv = wave_id(), lane = tid & 63, i32 = lane & 31, hf = lane >> 5;
+    const int b = blockIdx.x / p.H, h = blockIdx.x % p.H, grp = h / (p.H / p.G);
+    const int64_t bh = (int64_t)b * p.H + h;
+    const float A = p.A[h];
+    const float* xb = p.x + (int64_t)b * p.x_sb + (int64_t)h * p.x_sh;
+    const float* Bb = p.B + (int64_t)b * p.B_sb + (int64_t)grp * p.B_sg;
+    const float* db = p.dt + (int64_t)b * p.dt_sb + (int64_t)h * p.dt_sh;
+    const int tp = wv >> 1, tn0 = 2 * (wv & 1);
+    bwd_f32x16 acc[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            acc[q][r] = p.h0 ? p.h0[bh * (kFP * kFN) + (32 * tp + bwd_row(r, hf)) * kFN + 32 * (tn0 + q) + i32] : 0.f;
+    // loads of one chunk: x rows (tid >> 4) and + 16; B rows (tid >> 5) + 8 q
+    const int ix = tid >> 4, cx = (tid & 15) * 4, ib = tid >> 5, cb = (tid & 31) * 4;
+    float4 fx[2], fb[4];
+    float fdt;
+    auto fetch = [&](int c) {
+        const int t0 = c * 32;
+        const float4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int t = t0 + ix + 16 * q;
+            const float4 v = *reinterpret_cast<const float4*>(xb + (int64_t)min(t, p.L - 1) * p.x_sl + cx);
+            fx[q] = t < p.L ? v : z;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int t = t0 + ib + 8 * q;
+            const float4 v = *reinterpret_cast<const float4*>(Bb + (int64_t)min(t, p.L - 1) * p.B_sl + cb);
+            fb[q] = t < p.L ? v : z;
+        }
+        const int t = t0 + (tid & 31);
+        const float v = db[(int64_t)min(t, p.L - 1) * p.dt_sl];
+        fdt = t < p.L ? v : 0.f;
+    };
+    auto commit = [&]() {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) bwd_put4(&S.x[(ix + 16 * q) * kSX + cx], fx[q]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) bwd_put4(&S.B[(ib + 8 * q) * kSB + cb], fb[q]);
+        if (wv == 0) {
+            const float cs = wave_incl_scan(lane < 32 ? fdt * A : 0.f);
+            const float tot = __shfl(cs, 31, 64);
+            if (lane < 32) S.w[lane] = __expf(tot - cs) * fdt;
+            if (lane == 31) S.dec = __expf(tot);
+        }
+    };
+    fetch(0);
+    commit();
+    __syncthreads();
+    for (int c = 0; c < p.nch; ++c) {
+        fetch(c + 1 < p.nch ? c + 1 : c);
+        float* dst = p.hs + (bh * p.nch + c) * (kFP * kFN) + (32 * tp) * kFN + i32;
+        const float dec = S.dec;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                dst[bwd_row(r, hf) * kFN + 32 * (tn0 + q)] = acc[q][r];
+                acc[q][r] *= dec;
+            }
+        }
+        const float* Ap = S.x + hf * kSX + 32 * tp + i32;
+        const float* Bp = S.B + hf * kSB + 32 * tn0 + i32;
+#pragma unroll
+        for (int k0 = 0; k0 < 32; k0 += 2) {
+            const float a = S.w[k0 + hf] * Ap[k0 * kSX];
+            acc[0] = bwd_mfma(a, Bp[k0 * kSB], acc[0]);
+            acc[1] = bwd_mfma(a, Bp[k0 * kSB + 32], acc[1]);
+        }
+        __syncthreads();
+        commit();
+        __syncthreads();
+    }
+}
+
 // dA[h], dD[h] = sum over the batch of the (b, h) partials; dB / dC summed over
 // the heads of each group (in head order) when ngroups < nheads.
 __global__ __launch_bounds__(256) void ssd2_bwd_finish(Ssd2BwdParams p, float* dA, float* dD, float* dB, float* dC) {
@@ -322,6 +770,15 @@ static size_t bwd_chunks_lds(int P, int N) {
 struct BwdLayout {
     size_t hs, dbh, pa, total;
 };
+
+// The MFMA path: headdim 64, dstate 128, and float4-aligned rows of x, dy, B, C.
+static bool bwd_mfma_ok(const mamba_ssd2_bwd_args* a) {
+    auto al = [](const void* q) { return ((uintptr_t)q & 15u) == 0; };
+    auto m4 = [](int64_t s0, int64_t s1, int64_t s2) { return s0 % 4 == 0 && s1 % 4 == 0 && s2 % 4 == 0; };
+    return a->headdim == kFP && a->dstate == kFN && al(a->x) && al(a->dy) && al(a->B) && al(a->C) &&
+           m4(a->x_sb, a->x_sl, a->x_sh) && m4(a->dy_sb, a->dy_sl, a->dy_sh) && m4(a->B_sb, a->B_sl, a->B_sg) &&
+           m4(a->C_sb, a->C_sl, a->C_sg);
+}
 
 static int bwd_validate(const mamba_ssd2_bwd_args* a, BwdLayout* lay) {
     MAMBA_CHECK_ARG(a != nullptr, "args is NULL");
@@ -391,15 +848,22 @@ extern "C" int mamba_ssd2_bwd(const mamba_ssd2_bwd_args* a, void* workspace, siz
     p.pD = p.pA + align_up((size_t)a->batch * a->nheads * sizeof(float), 256) / sizeof(float);
     hipStream_t s = (hipStream_t)stream;
     const dim3 grid(a->batch * a->nheads);
-    // dynamic LDS above the 64 KB default (up to the CU's 160 KB)
-    MAMBA_CHECK_HIP(hipFuncSetAttribute((const void*)ssd2_bwd_states, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        (int)bwd_states_lds(p.P, p.N)));
-    MAMBA_CHECK_HIP(hipFuncSetAttribute((const void*)ssd2_bwd_chunks, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        (int)bwd_chunks_lds(p.P, p.N)));
-    hipLaunchKernelGGL(ssd2_bwd_states, grid, dim3(kBwdT), bwd_states_lds(p.P, p.N), s, p);
-    MAMBA_CHECK_LAUNCH();
-    hipLaunchKernelGGL(ssd2_bwd_chunks, grid, dim3(kBwdT), bwd_chunks_lds(p.P, p.N), s, p);
-    MAMBA_CHECK_LAUNCH();
+    if (bwd_mfma_ok(a)) {
+        hipLaunchKernelGGL(ssd2_bwd_states_mfma, grid, dim3(256), 0, s, p);
+        MAMBA_CHECK_LAUNCH();
+        hipLaunchKernelGGL(ssd2_bwd_chunks_mfma, grid, dim3(512), 0, s, p);
+        MAMBA_CHECK_LAUNCH();
+    } else {
+        // dynamic LDS above the 64 KB default (up to the CU's 160 KB)
+        MAMBA_CHECK_HIP(hipFuncSetAttribute((const void*)ssd2_bwd_states, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            (int)bwd_states_lds(p.P, p.N)));
+        MAMBA_CHECK_HIP(hipFuncSetAttribute((const void*)ssd2_bwd_chunks, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            (int)bwd_chunks_lds(p.P, p.N)));
+        hipLaunchKernelGGL(ssd2_bwd_states, grid, dim3(kBwdT), bwd_states_lds(p.P, p.N), s, p);
+        MAMBA_CHECK_LAUNCH();
+        hipLaunchKernelGGL(ssd2_bwd_chunks, grid, dim3(kBwdT), bwd_chunks_lds(p.P, p.N), s, p);
+        MAMBA_CHECK_LAUNCH();
+    }
     const int64_t fin = a->ngroups == a->nheads ? 0 : (int64_t)a->batch * a->seqlen * a->ngroups * a->dstate;
     const int fgrid = (int)std::max<int64_t>((a->nheads + 255) / 256, std::min<int64_t>((fin + 255) / 256, 4096));
     hipLaunchKernelGGL(ssd2_bwd_finish, dim3(fgrid), dim3(256), 0, s, p, a->dA, a->dD, a->dB, a->dC);

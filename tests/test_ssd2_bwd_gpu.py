@@ -20,6 +20,9 @@ CASES = [
     (1, 100, 2, 64, 1, 128, True, True, True),   # config-1 head shape (P 64, N 128)
     (2, 64, 4, 32, 4, 64, False, False, True),   # per-head B / C (ngroups = nheads), no D / h0
     (1, 45, 3, 8, 1, 32, True, False, False),    # no d(final state)
+    # headdim 64 x dstate 128 with float4-aligned rows: the MFMA kernels
+    (2, 200, 4, 64, 2, 128, True, True, True),   # seven chunks, ragged tail, two groups
+    (1, 64, 2, 64, 2, 128, False, False, False), # per-head B / C, nothing optional
 ]
 
 
@@ -62,13 +65,16 @@ def test_ssd2_bwd_matches_oracle(case):
         assert out["dD"] is None
 
 
-def test_ssd2_bwd_strided_inputs():
+@pytest.mark.parametrize("p,n", [(16, 32), (64, 128)])
+def test_ssd2_bwd_strided_inputs(p, n):
     """The seam's layouts through strides: x and dy as [b, l, h, p] views of a
     wider row, dt as a [b, h, l] tensor viewed [b, l, h] (the reference's
-    dt_bhnl), B / C as slices of one xBC row."""
+    dt_bhnl), B / C as slices of one xBC row (an odd row length, so at
+    headdim 64 x dstate 128 the unaligned rows take the SIMT kernels)."""
     import torch
     import mamba_hip
-    b, l, h, p, g, n = 2, 50, 4, 16, 2, 32
+    print("ssd2 bwd strided", p, n, flush=True)
+    b, l, h, g = 2, 50, 4, 2
     d, dy, dF = _inputs(5, b, l, h, p, g, n, True, True, True)
     wide = torch.zeros((b, l, h, p + 8), device="cuda")
     wide[..., :p] = _t(d["x"])
