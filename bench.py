@@ -686,6 +686,90 @@ def bench_mamba3_fused(args):
     }
 
 
+def ssd2_bwd_algorithmic(cfg):
+    """Causal-exact FLOPs of the Mamba-2 SSD backward at chunk Q = 32, per
+    token and head: the reverse chunk loop's four P x N products per position
+    (g B_j, g^T x_j, h_c^T dy_j and the state-gradient update) and its five
+    lower-triangular Q x Q products (C.B, dy.x, then the dy, C and B
+    contractions with them); the chunk-entry states' P x N product.  Bytes: the
+    compulsory HBM traffic of the whole call (x, dy, dt, B, C read, f32; dx, ddt,
+    dB, dC, d(initial state) written)."""
+    b, l, h, p, n, g = (cfg[k] for k in ("batch", "seqlen", "nheads", "headdim", "dstate", "ngroups"))
+    q = 32
+    th = b * l * h
+    chunk_flops = th * 2 * (4 * p * n + (q + 1) / 2 * (3 * n + 2 * p))
+    state_flops = th * 2 * p * n
+    bytes_ = 4 * (b * l * h * p * 2 + b * l * h + 2 * b * l * g * n) + 4 * (b * l * h * p + b * l * h + 2 * b * l * g * n
+                                                                            + b * h * p * n)
+    return bytes_, chunk_flops, state_flops
+
+
+F32_MFMA_PEAK_TFLOPS = 157.3   # MI355X dense f32 MFMA, published
+
+
+def bench_ssd2_bwd(args):
+    """The Mamba-2 SSD backward at the config-1 head shape (B=8 L=4096 H=80
+    P=64 N=128, one group), f32: mamba_ssd2_bwd from dy (no initial state, no
+    d(final state): a whole-sequence training step)."""
+    import torch
+
+    import mamba_hip
+    cfg = dict(SSD2_CFG1)
+    dev = torch.device("cuda:0")
+    inp = make_ssd2_inputs(cfg, dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    x, B, C = (inp[k].float() for k in ("x", "B", "C"))
+    dy = torch.randn(x.shape, generator=g, device=dev)
+
+    def step(events=None):
+        mamba_hip.ssd2_bwd(dy, x, inp["dt"], inp["A"], B, C, inp["D"], None, None, events=events)
+
+    ms_per_step, kern_ms = _time_steps(args, step)
+    nbytes, flops, state_flops = ssd2_bwd_algorithmic(cfg)
+    tokens = cfg["batch"] * cfg["seqlen"]
+    tflops = flops / (kern_ms * 1e-3) / 1e12
+    roof = {"bound": "mfma", "achieved": tflops, "peak": F32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": tflops / F32_MFMA_PEAK_TFLOPS, "traffic": _profiled_traffic("mamba2_ssd_bwd_cfg1"),
+            "kernel_ms": kern_ms, "algorithmic_flops": flops, "kernel": "ssd2_bwd_chunks (reverse chunk loop)",
+            "timing": "HIP events around the reverse chunk-loop kernel on its stream, per call",
+            "call_tflops": (flops + state_flops) / (ms_per_step * 1e-3) / 1e12,
+            "call_compulsory_bytes": nbytes}
+    return {
+        "metric": "Mamba-2 SSD backward tokens/s (B=8 L=4096 H=80 P=64 N=128, f32) + % f32 MFMA roofline",
+        "value": tokens / (ms_per_step * 1e-3), "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (BASELINE.json configs[1] distributions, dy ~ N(0,1), seeds 0 / 1)",
+        "config": {"workload": "mamba2_ssd_bwd_cfg1", **cfg, "chunk": 32, "io": "all f32",
+                   "entry": "mamba_ssd2_bwd (chunk states, reverse chunk loop, group sums)"},
+        "roofline": roof,
+    }
+
+
+def cpu_baseline_ssd2_bwd(cfg, seed=0):
+    """The oracle's float64 token-by-token reverse recurrence (oracle.ssd2_bwd)
+    on one sequence of 8192 tokens with every head, scaled to tokens/s."""
+    import numpy as np
+
+    import oracle
+    rng = np.random.default_rng(seed)
+    L, h, p, n = 8192, cfg["nheads"], cfg["headdim"], cfg["dstate"]
+    x = rng.standard_normal((1, L, h, p)).astype(np.float32)
+    dy = rng.standard_normal((1, L, h, p)).astype(np.float32)
+    dt = rng.uniform(1e-3, 0.1, (1, L, h)).astype(np.float32)
+    A = -rng.uniform(1.0, 16.0, h).astype(np.float32)
+    B = (rng.standard_normal((1, L, 1, n)) / np.sqrt(n)).astype(np.float32)
+    C = (rng.standard_normal((1, L, 1, n)) / np.sqrt(n)).astype(np.float32)
+    D = rng.standard_normal(h).astype(np.float32)
+    t0 = time.perf_counter()
+    oracle.ssd2_bwd(dy, None, x, dt, A, B, C, D, None)
+    el = time.perf_counter() - t0
+    return {"value": L / el, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"1 x {L} tokens, {h} heads ({el:.1f} s), float64 numpy token-by-token reverse "
+                      f"recurrence of the reference's backward"}
+
+
 def cpu_baseline_mamba3_fused(cfg, seed=0):
     """oracle.mamba3_prep_fwd then oracle.ssd3 (the f32 C restatement of the
     reference's single-SSD K1-K5) on one sequence of 1024 tokens, scaled to
@@ -1145,8 +1229,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", default="ssd2",
                     choices=["ssd2", "mamba1", "decode", "ssd3", "mamba3_fused", "mamba1_step", "mamba3_step",
-                             "mamba3_prep",
-                             "mamba2_block"])
+                             "mamba3_prep", "mamba2_block", "ssd2_bwd"])
     ap.add_argument("--batch", type=int, default=DECODE_CFG3["batch"], help="decode batch")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true",
@@ -1160,7 +1243,10 @@ def main():
               "(the hot path shards by batch/head with no communication; see DESIGN.md)",
               file=sys.stderr)
         sys.exit(2)
-    if args.workload == "mamba2_block":
+    if args.workload == "ssd2_bwd":
+        out = bench_ssd2_bwd(args)
+        base = (lambda: cpu_baseline_ssd2_bwd(SSD2_CFG1))
+    elif args.workload == "mamba2_block":
         out = bench_mamba2_block(args)
         base = (lambda: cpu_baseline_mamba2_block(MAMBA2_BLOCK_CFG1))
     elif args.workload == "mamba3_prep":

@@ -814,8 +814,8 @@ extern "C" size_t mamba_ssd2_bwd_workspace_size(const mamba_ssd2_bwd_args* a) {
     return lay.total;
 }
 
-extern "C" int mamba_ssd2_bwd(const mamba_ssd2_bwd_args* a, void* workspace, size_t workspace_bytes,
-                              mamba_stream_t stream) {
+static int ssd2_bwd_run(const mamba_ssd2_bwd_args* a, void* workspace, size_t workspace_bytes,
+                        mamba_stream_t stream, hipEvent_t ev0, hipEvent_t ev1) {
     BwdLayout lay;
     const int st = bwd_validate(a, &lay);
     if (st != MAMBA_OK) return st;
@@ -851,8 +851,10 @@ extern "C" int mamba_ssd2_bwd(const mamba_ssd2_bwd_args* a, void* workspace, siz
     if (bwd_mfma_ok(a)) {
         hipLaunchKernelGGL(ssd2_bwd_states_mfma, grid, dim3(256), 0, s, p);
         MAMBA_CHECK_LAUNCH();
+        if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, s));
         hipLaunchKernelGGL(ssd2_bwd_chunks_mfma, grid, dim3(512), 0, s, p);
         MAMBA_CHECK_LAUNCH();
+        if (ev1) MAMBA_CHECK_HIP(hipEventRecord(ev1, s));
     } else {
         // dynamic LDS above the 64 KB default (up to the CU's 160 KB)
         MAMBA_CHECK_HIP(hipFuncSetAttribute((const void*)ssd2_bwd_states, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -861,12 +863,24 @@ extern "C" int mamba_ssd2_bwd(const mamba_ssd2_bwd_args* a, void* workspace, siz
                                             (int)bwd_chunks_lds(p.P, p.N)));
         hipLaunchKernelGGL(ssd2_bwd_states, grid, dim3(kBwdT), bwd_states_lds(p.P, p.N), s, p);
         MAMBA_CHECK_LAUNCH();
+        if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, s));
         hipLaunchKernelGGL(ssd2_bwd_chunks, grid, dim3(kBwdT), bwd_chunks_lds(p.P, p.N), s, p);
         MAMBA_CHECK_LAUNCH();
+        if (ev1) MAMBA_CHECK_HIP(hipEventRecord(ev1, s));
     }
     const int64_t fin = a->ngroups == a->nheads ? 0 : (int64_t)a->batch * a->seqlen * a->ngroups * a->dstate;
     const int fgrid = (int)std::max<int64_t>((a->nheads + 255) / 256, std::min<int64_t>((fin + 255) / 256, 4096));
     hipLaunchKernelGGL(ssd2_bwd_finish, dim3(fgrid), dim3(256), 0, s, p, a->dA, a->dD, a->dB, a->dC);
     MAMBA_CHECK_LAUNCH();
     return MAMBA_OK;
+}
+
+extern "C" int mamba_ssd2_bwd(const mamba_ssd2_bwd_args* a, void* workspace, size_t workspace_bytes,
+                              mamba_stream_t stream) {
+    return ssd2_bwd_run(a, workspace, workspace_bytes, stream, nullptr, nullptr);
+}
+
+extern "C" int mamba_ssd2_bwd_timed(const mamba_ssd2_bwd_args* a, void* workspace, size_t workspace_bytes,
+                                    mamba_stream_t stream, void* event_start, void* event_stop) {
+    return ssd2_bwd_run(a, workspace, workspace_bytes, stream, (hipEvent_t)event_start, (hipEvent_t)event_stop);
 }

@@ -277,6 +277,7 @@ _SIGNATURES = {
                              ctypes.c_int),
     "mamba_ssd2_bwd_workspace_size": ([ctypes.POINTER(Ssd2BwdArgs)], ctypes.c_size_t),
     "mamba_ssd2_bwd": ([ctypes.POINTER(Ssd2BwdArgs), c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),
+    "mamba_ssd2_bwd_timed": ([ctypes.POINTER(Ssd2BwdArgs), c_vp, ctypes.c_size_t, c_vp, c_vp, c_vp], ctypes.c_int),
     "mamba_ssd3_workspace_size": ([ctypes.POINTER(Ssd3Args)], ctypes.c_size_t),
     "mamba_ssd3_fast_path": ([ctypes.POINTER(Ssd3Args)], ctypes.c_int),
     "mamba_ssd3_fwd": ([ctypes.POINTER(Ssd3Args), c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),

@@ -134,14 +134,16 @@ def ssd2_fwd(x, dt, A, B, C, D=None, initial_state=None, init_state_hpr=None, ch
     return y, final_state
 
 
-def ssd2_bwd(dy, x, dt, A, B, C, D=None, initial_state=None, d_final_state=None):
+def ssd2_bwd(dy, x, dt, A, B, C, D=None, initial_state=None, d_final_state=None, events=None):
     """The SSD forward's gradients through ``mamba_ssd2_bwd``: the Autodiff arm
     of Mamba2BackendExt::ssd_serial_recalculated
     (src/mamba2/ssd/serial_recalculated/backward.rs:29-321; gradient math
     combined_backward.rs:126-593).  Inputs as ``ssd2_fwd`` (bf16 ones are read
     as f32), dy[b,l,h,p], d_final_state[b,h,p,n] or None.  Returns a dict of f32
     gradients: dx[b,l,h,p], ddt[b,l,h], dA[h], dB / dC[b,l,g,n] (summed over
-    each group's heads), dD[h] (None without D), d_initial_state[b,h,p,n]."""
+    each group's heads), dD[h] (None without D), d_initial_state[b,h,p,n].
+    events: optional (start, stop) torch events recorded around the reverse
+    chunk-loop kernel (mamba_ssd2_bwd_timed)."""
     b, l, h, p = x.shape
     g, n = B.shape[2], B.shape[3]
     f = lambda t: None if t is None else (t if t.dtype == torch.float32 else t.float())  # noqa: E731
@@ -176,8 +178,13 @@ def ssd2_bwd(dy, x, dt, A, B, C, D=None, initial_state=None, d_final_state=None)
     if nbytes == 0:
         check(L.mamba_ssd2_bwd(ctypes.byref(a), None, 0, _stream(dev)), "mamba_ssd2_bwd")
     ws = workspace(dev, nbytes)
-    check(L.mamba_ssd2_bwd(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(dev)),
-          "mamba_ssd2_bwd")
+    if events is None:
+        check(L.mamba_ssd2_bwd(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(dev)),
+              "mamba_ssd2_bwd")
+    else:
+        e0, e1 = _raw_events(events, dev)
+        check(L.mamba_ssd2_bwd_timed(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(dev),
+                                     e0, e1), "mamba_ssd2_bwd_timed")
     return out
 
 

@@ -173,6 +173,10 @@ typedef struct mamba_ssd2_bwd_args {
 size_t mamba_ssd2_bwd_workspace_size(const mamba_ssd2_bwd_args* args);
 int mamba_ssd2_bwd(const mamba_ssd2_bwd_args* args, void* workspace, size_t workspace_bytes,
                    mamba_stream_t stream);
+/* Same, recording the caller's HIP events immediately before and after the   */
+/* dominant kernel (the reverse chunk loop).  No counterpart in the reference. */
+int mamba_ssd2_bwd_timed(const mamba_ssd2_bwd_args* args, void* workspace, size_t workspace_bytes,
+                         mamba_stream_t stream, void* event_start, void* event_stop);
 
 /* ------------------------------------------------------------------------- */
 /* Mamba-3 single-pass chunked SSD forward (trapezoidal discretisation, MIMO   */
