@@ -166,6 +166,24 @@ class Ssd2BwdArgs(ctypes.Structure):
     ]
 
 
+class Ssd3BwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", c_i32), ("seqlen", c_i32), ("mimo", c_i32), ("nheads", c_i32), ("headdim", c_i32),
+        ("ngroups", c_i32), ("dstate", c_i32),
+        ("v", c_vp), ("v_sb", c_i64), ("v_sl", c_i64), ("v_sm", c_i64), ("v_sh", c_i64),
+        ("da", c_vp), ("da_sb", c_i64), ("da_sl", c_i64), ("da_sh", c_i64),
+        ("gamma", c_vp), ("gamma_sb", c_i64), ("gamma_sl", c_i64), ("gamma_sh", c_i64),
+        ("scale", c_vp), ("scale_sb", c_i64), ("scale_sl", c_i64), ("scale_sh", c_i64),
+        ("B", c_vp), ("B_sb", c_i64), ("B_sl", c_i64), ("B_sm", c_i64), ("B_sg", c_i64),
+        ("C", c_vp), ("C_sb", c_i64), ("C_sl", c_i64), ("C_sm", c_i64), ("C_sg", c_i64),
+        ("initial_state", c_vp),
+        ("dy", c_vp), ("dy_sb", c_i64), ("dy_sl", c_i64), ("dy_sm", c_i64), ("dy_sh", c_i64),
+        ("d_final_state", c_vp),
+        ("dv", c_vp), ("dda", c_vp), ("dgamma", c_vp), ("dscale", c_vp), ("dB", c_vp), ("dC", c_vp),
+        ("d_initial_state", c_vp),
+    ]
+
+
 class Mamba3FusedArgs(ctypes.Structure):
     _fields_ = [("prep", Mamba3PrepArgs), ("D", c_vp), ("y", c_vp), ("final_state", c_vp)]
 
@@ -278,6 +296,9 @@ _SIGNATURES = {
     "mamba_ssd2_bwd_workspace_size": ([ctypes.POINTER(Ssd2BwdArgs)], ctypes.c_size_t),
     "mamba_ssd2_bwd": ([ctypes.POINTER(Ssd2BwdArgs), c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),
     "mamba_ssd2_bwd_timed": ([ctypes.POINTER(Ssd2BwdArgs), c_vp, ctypes.c_size_t, c_vp, c_vp, c_vp], ctypes.c_int),
+    "mamba_ssd3_bwd_workspace_size": ([ctypes.POINTER(Ssd3BwdArgs)], ctypes.c_size_t),
+    "mamba_ssd3_bwd": ([ctypes.POINTER(Ssd3BwdArgs), c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),
+    "mamba_ssd3_bwd_timed": ([ctypes.POINTER(Ssd3BwdArgs), c_vp, ctypes.c_size_t, c_vp, c_vp, c_vp], ctypes.c_int),
     "mamba_ssd3_workspace_size": ([ctypes.POINTER(Ssd3Args)], ctypes.c_size_t),
     "mamba_ssd3_fast_path": ([ctypes.POINTER(Ssd3Args)], ctypes.c_int),
     "mamba_ssd3_fwd": ([ctypes.POINTER(Ssd3Args), c_vp, ctypes.c_size_t, c_vp], ctypes.c_int),

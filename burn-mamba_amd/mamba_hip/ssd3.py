@@ -20,7 +20,7 @@ from typing import Optional
 import torch
 
 from . import _lib
-from ._lib import Ssd3Args, Ssd3DoubleArgs, check
+from ._lib import Ssd3Args, Ssd3BwdArgs, Ssd3DoubleArgs, check
 from .ssd import _dtype_code, _raw_events, _stream, workspace
 
 
@@ -177,6 +177,100 @@ def ssd3_double_fwd(v, da, B, C, initial_state=None, chunk_len=64, y=None, final
     fn = L.mamba_ssd3_double_fwd_generic if generic else L.mamba_ssd3_double_fwd
     check(fn(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), ws.numel(), st), "mamba_ssd3_double_fwd")
     return y, final_state
+
+
+def ssd3_bwd(dy, v, da, B, C, gamma=None, scale=None, initial_state=None, d_final_state=None, events=None):
+    """The single-SSD forward's gradients through ``mamba_ssd3_bwd``: the
+    Autodiff arm of Mamba3SingleSsdBackendExt::single_ssd_serial_recalculated
+    (src/mamba3/single_ssd/ssd/serial_recalculated/backward.rs:27-299; gradient
+    math combined_backward.rs:74-536).  gamma = scale = None is the double-SSD
+    seam's backward (double_ssd/ssd/serial_recalculated/backward.rs:27-275).
+    Inputs as ``ssd3_fwd`` (bf16 ones are read as f32), dy [b, l, m, h, p],
+    d_final_state [b, h, p, n] or None.  Returns a dict of f32 gradients: dv,
+    dda, dgamma / dscale (None without the weights), dB / dC [b, l, m, g, n]
+    (summed over each group's heads), d_initial_state [b, h, p, n].  events:
+    optional (start, stop) torch events around the reverse chunk-loop kernel."""
+    b, l, m, h, p = v.shape
+    g, n = B.shape[3], B.shape[4]
+    f = lambda t: None if t is None else (t if t.dtype == torch.float32 else t.float())  # noqa: E731
+    v, dy, B, C, da, gamma, scale, initial_state, d_final_state = map(
+        f, (v, dy, B, C, da, gamma, scale, initial_state, d_final_state))
+    if B.shape != C.shape or B.shape[:3] != (b, l, m) or dy.shape != v.shape:
+        raise _lib.MambaHipError("B and C must be [b, l, m, g, n] and dy [b, l, m, h, p] matching v")
+    for t, nm in ((v, "v"), (B, "B"), (C, "C"), (dy, "dy")):
+        if t.stride(-1) != 1:
+            raise _lib.MambaHipError(f"{nm}: innermost axis must be contiguous")
+    for t, nm in ((da, "da"), (gamma, "gamma"), (scale, "scale")):
+        if t is not None and t.shape != (b, l, h):
+            raise _lib.MambaHipError(f"{nm} must be [b, l, h]")
+    for t in (initial_state, d_final_state):
+        if t is not None and not t.is_contiguous():
+            raise _lib.MambaHipError("the states must be contiguous")
+    dev = v.device
+    out = dict(dv=torch.empty((b, l, m, h, p), device=dev), dda=torch.empty((b, l, h), device=dev),
+               dgamma=None if gamma is None else torch.empty((b, l, h), device=dev),
+               dscale=None if scale is None else torch.empty((b, l, h), device=dev),
+               dB=torch.empty((b, l, m, g, n), device=dev), dC=torch.empty((b, l, m, g, n), device=dev),
+               d_initial_state=torch.empty((b, h, p, n), device=dev))
+    a = Ssd3BwdArgs()
+    a.batch, a.seqlen, a.mimo, a.nheads, a.headdim, a.ngroups, a.dstate = b, l, m, h, p, g, n
+    a.v = v.data_ptr(); a.v_sb, a.v_sl, a.v_sm, a.v_sh = v.stride()[:4]
+    a.da = da.data_ptr(); a.da_sb, a.da_sl, a.da_sh = da.stride()
+    if gamma is not None:
+        a.gamma = gamma.data_ptr(); a.gamma_sb, a.gamma_sl, a.gamma_sh = gamma.stride()
+    if scale is not None:
+        a.scale = scale.data_ptr(); a.scale_sb, a.scale_sl, a.scale_sh = scale.stride()
+    a.B = B.data_ptr(); a.B_sb, a.B_sl, a.B_sm, a.B_sg = B.stride()[:4]
+    a.C = C.data_ptr(); a.C_sb, a.C_sl, a.C_sm, a.C_sg = C.stride()[:4]
+    a.initial_state = None if initial_state is None else initial_state.data_ptr()
+    a.dy = dy.data_ptr(); a.dy_sb, a.dy_sl, a.dy_sm, a.dy_sh = dy.stride()[:4]
+    a.d_final_state = None if d_final_state is None else d_final_state.data_ptr()
+    for k in ("dv", "dda", "dgamma", "dscale", "dB", "dC", "d_initial_state"):
+        setattr(a, k, None if out[k] is None else out[k].data_ptr())
+    L = _lib.lib()
+    need = L.mamba_ssd3_bwd_workspace_size(ctypes.byref(a))
+    st = _stream(dev)
+    if need == 0:
+        # invalid arguments: the call reports why
+        check(L.mamba_ssd3_bwd(ctypes.byref(a), None, 0, st), "mamba_ssd3_bwd")
+    ws = workspace(dev, need)
+    if events is None:
+        check(L.mamba_ssd3_bwd(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), ws.numel(), st), "mamba_ssd3_bwd")
+    else:
+        e0, e1 = _raw_events(events, dev)
+        check(L.mamba_ssd3_bwd_timed(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), ws.numel(), st, e0, e1),
+              "mamba_ssd3_bwd_timed")
+    return out
+
+
+class _Ssd3Function(torch.autograd.Function):
+    """The single-SSD seam as one differentiable node: ``mamba_ssd3_fwd``
+    forward, ``mamba_ssd3_bwd`` backward from the saved leaf inputs (the
+    reference's Autodiff arm, single_ssd/ssd/serial_recalculated/
+    backward.rs:27-299: one node for both outputs, intermediates recomputed)."""
+
+    @staticmethod
+    def forward(ctx, v, da, B, C, gamma, scale, initial_state, chunk_len):
+        y, hT = ssd3_fwd(v, da, B, C, gamma, scale, initial_state, chunk_len=chunk_len)
+        ctx.save_for_backward(v, da, B, C, gamma, scale, initial_state)
+        return y, hT
+
+    @staticmethod
+    def backward(ctx, dy, dhT):
+        v, da, B, C, gamma, scale, h0 = ctx.saved_tensors
+        if dy is None:
+            dy = torch.zeros(v.shape, device=v.device)
+        gr = ssd3_bwd(dy.contiguous(), v, da, B, C, gamma, scale, h0, None if dhT is None else dhT.contiguous())
+        cast = lambda t, like: t.to(like.dtype)  # noqa: E731
+        return (cast(gr["dv"], v), gr["dda"], cast(gr["dB"], B), cast(gr["dC"], C), gr["dgamma"], gr["dscale"],
+                None if h0 is None else gr["d_initial_state"], None)
+
+
+def ssd3_autograd(v, da, B, C, gamma, scale, initial_state=None, chunk_len=64):
+    """``ssd3_fwd`` as a differentiable op (torch.autograd), returning
+    (y, final_state); gradients flow to v, da, B, C, gamma, scale and
+    initial_state through ``mamba_ssd3_bwd``."""
+    return _Ssd3Function.apply(v, da, B, C, gamma, scale, initial_state, chunk_len)
 
 
 @dataclass

@@ -259,6 +259,51 @@ int mamba_ssd3_double_fwd_generic(const mamba_ssd3_double_args* args, void* work
                                   size_t workspace_bytes, mamba_stream_t stream);
 
 /* ------------------------------------------------------------------------- */
+/* Mamba-3 SSD backward (recompute form): the gradients of mamba_ssd3_fwd's    */
+/* y and final state with respect to v, da, B, C, gamma, scale and the        */
+/* initial state, given dy and d(final state).  Replaces the Autodiff arm of  */
+/* Mamba3SingleSsdBackendExt::single_ssd_serial_recalculated                   */
+/* (src/mamba3/single_ssd/ssd/serial_recalculated/backward.rs:27-299; its      */
+/* gradient math combined_backward.rs:74-536).  With gamma = scale = NULL     */
+/* (unit weights; dgamma / dscale NULL) it is the Autodiff arm of             */
+/* Mamba3DoubleSsdBackendExt::double_ssd_serial_recalculated                   */
+/* (double_ssd/ssd/serial_recalculated/backward.rs:27-275, combined_backward.rs:98-542), */
+/* whose forward (mamba_ssd3_double_fwd) is the single one with unit weights.  */
+/* f32; element strides with the innermost axis contiguous; B / C in group    */
+/* form (dB / dC summed over each group's heads).  mimo must divide 32.       */
+/* headdim x dstate <= 8192.  Deterministic (no atomics).                      */
+/* ------------------------------------------------------------------------- */
+typedef struct mamba_ssd3_bwd_args {
+    int32_t batch, seqlen, mimo, nheads, headdim, ngroups, dstate;
+    const float* v;     int64_t v_sb, v_sl, v_sm, v_sh;           /* [b, l, m, h, p]      */
+    const float* da;    int64_t da_sb, da_sl, da_sh;              /* [b, l, h]            */
+    const float* gamma; int64_t gamma_sb, gamma_sl, gamma_sh;     /* [b, l, h] or NULL    */
+    const float* scale; int64_t scale_sb, scale_sl, scale_sh;     /* [b, l, h] or NULL    */
+    const float* B;     int64_t B_sb, B_sl, B_sm, B_sg;           /* [b, l, m, g, n]      */
+    const float* C;     int64_t C_sb, C_sl, C_sm, C_sg;           /* [b, l, m, g, n]      */
+    const float* initial_state;                                   /* [b, h, p, n] or NULL */
+    const float* dy;    int64_t dy_sb, dy_sl, dy_sm, dy_sh;       /* [b, l, m, h, p]      */
+    const float* d_final_state;                                   /* [b, h, p, n] or NULL */
+    float* dv;                                                    /* [b, l, m, h, p] contiguous */
+    float* dda;                                                   /* [b, l, h] contiguous */
+    float* dgamma;                                                /* [b, l, h] or NULL    */
+    float* dscale;                                                /* [b, l, h] or NULL    */
+    float* dB;                                                    /* [b, l, m, g, n] contiguous */
+    float* dC;                                                    /* [b, l, m, g, n] contiguous */
+    float* d_initial_state;                                       /* [b, h, p, n]         */
+} mamba_ssd3_bwd_args;
+
+/* Workspace bytes (chunk states; per-head dB / dC when ngroups < nheads);     */
+/* 0 if the arguments are invalid.                                             */
+size_t mamba_ssd3_bwd_workspace_size(const mamba_ssd3_bwd_args* args);
+int mamba_ssd3_bwd(const mamba_ssd3_bwd_args* args, void* workspace, size_t workspace_bytes,
+                   mamba_stream_t stream);
+/* Same, recording the caller's HIP events immediately before and after the   */
+/* dominant kernel (the reverse chunk loop).  No counterpart in the reference. */
+int mamba_ssd3_bwd_timed(const mamba_ssd3_bwd_args* args, void* workspace, size_t workspace_bytes,
+                         mamba_stream_t stream, void* event_start, void* event_stop);
+
+/* ------------------------------------------------------------------------- */
 /* Mamba-1 selective scan (f32), with the optional dt bias + softplus of       */
 /* Mamba1::ssm and the silu(z) gate of Mamba1::forward:                        */
 /*                                                                             */

@@ -143,6 +143,72 @@ def ssd2_bwd(dy, dfinal, x, dt, A, B, C, D=None, h0=None):
                 dC=dCh.reshape(b, l, g, rep, n).sum(3), dD=dD, dh0=G)
 
 
+def ssd3_bwd(dy, dfinal, v, da, B, C, gamma=None, scale=None, h0=None):
+    """Gradients of the Mamba-3 single-SSD forward (oracle.ssd3) in float64
+    numpy by the per-token reverse recurrence: the analytic backward that
+    src/mamba3/single_ssd/ssd/serial_recalculated/combined_backward.rs:74-536
+    computes chunk-wise (its Autodiff arm, single_ssd/ssd/serial_recalculated/
+    backward.rs:27-299), here token by token.  With gamma = scale = None (both
+    1) it is the double-SSD seam's backward (double_ssd/ssd/serial_recalculated/
+    combined_backward.rs:98-542, backward.rs:27-275), whose forward is the
+    single one with unit weights.
+
+    Forward per (b, head), K_t = sum_m v[t,m] B[t,m]^T (P x N):
+      S_t = exp(da_t) h_{t-1},  h_t = S_t + scale_t K_t,
+      y[t,mo] = S_t C[t,mo] + gamma_t sum_mi (C[t,mo].B[t,mi]) v[t,mi],
+    final state h_L.  With G_t = dL/dh_t (G_L = dfinal) and
+    Q_t = sum_mo dy[t,mo] C[t,mo]^T:
+      dC[t,mo] = S_t^T dy[t,mo] + gamma_t sum_mi (dy[t,mo].v[t,mi]) B[t,mi]
+      dB[t,mi] = scale_t G_t^T v[t,mi] + gamma_t sum_mo (dy[t,mo].v[t,mi]) C[t,mo]
+      dv[t,mi] = scale_t G_t B[t,mi] + gamma_t sum_mo (C[t,mo].B[t,mi]) dy[t,mo]
+      dscale_t = sum_mi v[t,mi]^T G_t B[t,mi]
+      dgamma_t = sum_{mo,mi} (C[t,mo].B[t,mi]) (dy[t,mo].v[t,mi])
+      dda_t = <G_t + Q_t, S_t>,  G_{t-1} = exp(da_t) (G_t + Q_t),  dh0 = G_0.
+    v, dy [b,l,m,h,p]; da, gamma, scale [b,l,h]; B, C [b,l,m,g,n] (group form,
+    dB / dC summed over the group's heads); h0, dfinal [b,h,p,n] or None.
+    Returns a dict of float64 gradients (dgamma / dscale None when the weight
+    is None)."""
+    f = lambda t: None if t is None else np.asarray(t, np.float64)  # noqa: E731
+    dy, dfinal, v, da, B, C, gamma, scale, h0 = map(f, (dy, dfinal, v, da, B, C, gamma, scale, h0))
+    b, l, m, h, p = v.shape
+    g, n = B.shape[3], B.shape[4]
+    rep = h // g
+    Bh = np.repeat(B, rep, axis=3)   # [b, l, m, h, n]
+    Ch = np.repeat(C, rep, axis=3)
+    gam = np.ones((b, l, h)) if gamma is None else gamma
+    scl = np.ones((b, l, h)) if scale is None else scale
+    S = np.zeros((l, b, h, p, n))
+    hc = np.zeros((b, h, p, n)) if h0 is None else h0.copy()
+    for t in range(l):
+        S[t] = np.exp(da[:, t])[:, :, None, None] * hc
+        hc = S[t] + scl[:, t][:, :, None, None] * np.einsum("bmhp,bmhn->bhpn", v[:, t], Bh[:, t])
+    G = np.zeros((b, h, p, n)) if dfinal is None else dfinal.copy()
+    dv = np.zeros_like(v)
+    dBh = np.zeros_like(Bh)
+    dCh = np.zeros_like(Ch)
+    dda = np.zeros_like(da)
+    dgam = np.zeros_like(da)
+    dscl = np.zeros_like(da)
+    for t in range(l - 1, -1, -1):
+        vt, Bt, Ct, yt = v[:, t], Bh[:, t], Ch[:, t], dy[:, t]        # [b, m, h, .]
+        Qt = np.einsum("bohp,bohn->bhpn", yt, Ct)
+        yv = np.einsum("bohp,bihp->bhoi", yt, vt)                      # dy[mo] . v[mi]
+        cb = np.einsum("bohn,bihn->bhoi", Ct, Bt)                      # C[mo] . B[mi]
+        dCh[:, t] = np.einsum("bhpn,bohp->bohn", S[t], yt) + \
+            np.einsum("bh,bhoi,bihn->bohn", gam[:, t], yv, Bt)
+        GB = np.einsum("bhpn,bihn->bihp", G, Bt)                       # G_t B[t,mi]
+        dBh[:, t] = np.einsum("bh,bhpn,bihp->bihn", scl[:, t], G, vt) + \
+            np.einsum("bh,bhoi,bohn->bihn", gam[:, t], yv, Ct)
+        dv[:, t] = scl[:, t][:, None, :, None] * GB + np.einsum("bh,bhoi,bohp->bihp", gam[:, t], cb, yt)
+        dscl[:, t] = np.einsum("bihp,bihp->bh", vt, GB)
+        dgam[:, t] = np.einsum("bhoi,bhoi->bh", cb, yv)
+        dda[:, t] = np.einsum("bhpn,bhpn->bh", G + Qt, S[t])
+        G = np.exp(da[:, t])[:, :, None, None] * (G + Qt)
+    return dict(dv=dv, dda=dda, dB=dBh.reshape(b, l, m, g, rep, n).sum(4),
+                dC=dCh.reshape(b, l, m, g, rep, n).sum(4), dgamma=None if gamma is None else dgam,
+                dscale=None if scale is None else dscl, dh0=G)
+
+
 # --------------------------------------------------------------------------
 # Mamba-1 selective scan (src/mamba1/mamba1.rs:422-523, :666-733)
 # --------------------------------------------------------------------------

@@ -61,6 +61,7 @@ int main(void) {{ printf("%zu\\n", sizeof({struct_name})); {body} return 0; }}
                                              ("Mamba3FinishArgs", "mamba3_finish_args"),
                                              ("Mamba3FusedArgs", "mamba3_fused_args"),
                                              ("Ssd2BwdArgs", "mamba_ssd2_bwd_args"),
+                                             ("Ssd3BwdArgs", "mamba_ssd3_bwd_args"),
                                              ("Mamba3DoubleInputsArgs", "mamba3_double_inputs_args"),
                                              ("LinearArgs", "mamba_linear_args"),
                                              ("Mamba2LayerArgs", "mamba2_layer_args"),

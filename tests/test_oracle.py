@@ -852,3 +852,108 @@ def test_ssd2_bwd_closed_forms():
     np.testing.assert_allclose(gz["dC"], 0.0, atol=0)
     gd = oracle.ssd2_bwd(dy, None, **inp)
     np.testing.assert_allclose(gd["dD"], np.einsum("blhp,blhp->h", inp["x"], dy), rtol=1e-12)
+
+
+def _ssd3_fwd64(v, da, B, C, gamma, scale, h0):
+    """Whole-sequence matrix form of the Mamba-3 single-SSD forward in float64
+    (the fused-axis K5 of single_ssd/ssd/serial.rs:56-268 with one chunk): y =
+    (W o C B^T) v + exp(cs) C h0^T with W = exp(cs_t - cs_s) scale_s for s < t
+    and gamma_t for s = t; h_L from the same weights.  gamma / scale None = 1.
+    Group-form B / C [b, l, m, g, n].  Independent of the backward oracle's
+    recurrence."""
+    b, l, m, h, p = v.shape
+    g = B.shape[3]
+    rep = h // g
+    Bh, Ch = np.repeat(B, rep, axis=3), np.repeat(C, rep, axis=3)
+    gam = np.ones((b, l, h)) if gamma is None else gamma
+    scl = np.ones((b, l, h)) if scale is None else scale
+    cs = np.cumsum(da, axis=1)                                         # [b, l, h]
+    seg = cs[:, :, None, :] - cs[:, None, :, :]                        # [b, t, s, h]
+    lower = np.tril(np.ones((l, l), bool), -1)[None, :, :, None]
+    eye = np.eye(l, dtype=bool)[None, :, :, None]
+    W = np.where(lower, np.exp(np.where(lower, seg, 0.0)) * scl[:, None, :, :], 0.0)
+    W = W + np.where(eye, gam[:, :, None, :], 0.0)
+    y = np.einsum("btsh,btohn,bsihn,bsihp->btohp", W, Ch, Bh, v)
+    y += np.exp(cs)[:, :, None, :, None] * np.einsum("btohn,bhpn->btohp", Ch, h0)
+    wend = np.exp(cs[:, -1:, :] - cs) * scl                            # [b, s, h]
+    hT = np.exp(cs[:, -1])[:, :, None, None] * h0 + np.einsum("bsh,bsihp,bsihn->bhpn", wend, v, Bh)
+    return y, hT
+
+
+def _ssd3_bwd_case(seed, b=2, l=4, m=2, h=2, p=2, g=1, n=3, weights=True):
+    rng = np.random.default_rng(seed)
+    r = lambda *s: rng.standard_normal(s)  # noqa: E731
+    inp = dict(v=r(b, l, m, h, p), da=-rng.uniform(0.05, 0.8, (b, l, h)), B=r(b, l, m, g, n), C=r(b, l, m, g, n),
+               gamma=rng.uniform(0.05, 0.6, (b, l, h)) if weights else None,
+               scale=rng.uniform(0.1, 0.9, (b, l, h)) if weights else None, h0=r(b, h, p, n))
+    return inp, r(b, l, m, h, p), r(b, h, p, n)
+
+
+def test_ssd3_fwd64_matches_oracle_forward():
+    """The float64 matrix form used for the finite differences equals the C
+    oracle's single-SSD forward (per-head B / C, f32-representable inputs)."""
+    inp, _, _ = _ssd3_bwd_case(5, b=2, l=9, m=3, h=2, p=4, g=2, n=5)
+    inp = {k: v.astype(np.float32).astype(np.float64) for k, v in inp.items()}
+    y, hT = _ssd3_fwd64(**inp)
+    yo, ho = oracle.ssd3(inp["v"], inp["da"], inp["B"], inp["C"], inp["gamma"], inp["scale"], inp["h0"], chunk=4)
+    np.testing.assert_allclose(y, yo, rtol=2e-6, atol=2e-6)
+    np.testing.assert_allclose(hT, ho, rtol=2e-6, atol=2e-6)
+
+
+@pytest.mark.parametrize("g,weights", [(1, True), (2, True), (1, False)])
+def test_ssd3_bwd_equals_finite_differences(g, weights):
+    """Every gradient of oracle.ssd3_bwd equals the central difference of
+    L = sum dy.y + sum dfinal.h_L through the float64 forward at every
+    coordinate: the single seam (gamma, scale given) and the double seam
+    (unit weights); dB / dC in group form sum the group's heads."""
+    inp, dy, dF = _ssd3_bwd_case(31 + g + 2 * weights, g=g, weights=weights)
+    grads = oracle.ssd3_bwd(dy, dF, **inp)
+
+    def loss(a):
+        y, hT = _ssd3_fwd64(**a)
+        return float((y * dy).sum() + (hT * dF).sum())
+    eps = 1e-6
+    names = dict(v="dv", da="dda", B="dB", C="dC", h0="dh0")
+    if weights:
+        names.update(gamma="dgamma", scale="dscale")
+    else:
+        assert grads["dgamma"] is None and grads["dscale"] is None
+    for k, gk in names.items():
+        fd = np.zeros_like(inp[k])
+        for idx in np.ndindex(inp[k].shape):
+            a = {kk: (None if vv is None else vv.copy()) for kk, vv in inp.items()}
+            a[k][idx] += eps
+            lp = loss(a)
+            a[k][idx] -= 2 * eps
+            fd[idx] = (lp - loss(a)) / (2 * eps)
+        np.testing.assert_allclose(grads[gk], fd, rtol=1e-6, atol=1e-7, err_msg=k)
+
+
+def test_ssd3_bwd_reduces_to_mamba2():
+    """MIMO rank 1 with v = x, da = dt A, scale = gamma = dt is the Mamba-2 SSD
+    (no D): the gradients equal oracle.ssd2_bwd's, with ddt = A dda + dscale +
+    dgamma and dA = sum dt dda."""
+    inp, dy, dF = _ssd2_bwd_case(41, b=2, l=6, h=4, p=3, g=2, n=5)
+    x, dt, A = inp["x"], inp["dt"], inp["A"]
+    g2 = oracle.ssd2_bwd(dy, dF, x, dt, A, inp["B"], inp["C"], None, inp["h0"])
+    g3 = oracle.ssd3_bwd(dy[:, :, None], dF, x[:, :, None], dt * A[None, None, :], inp["B"][:, :, None],
+                         inp["C"][:, :, None], dt, dt, inp["h0"])
+    np.testing.assert_allclose(g3["dv"][:, :, 0], g2["dx"], rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(g3["dB"][:, :, 0], g2["dB"], rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(g3["dC"][:, :, 0], g2["dC"], rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(g3["dh0"], g2["dh0"], rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(A[None, None, :] * g3["dda"] + g3["dscale"] + g3["dgamma"], g2["ddt"],
+                               rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose((dt * g3["dda"]).sum((0, 1)), g2["dA"], rtol=1e-12, atol=1e-12)
+
+
+def test_ssd3_bwd_closed_forms():
+    """With dy = 0 only the final state carries gradient: dh0 = exp(sum da)
+    dfinal, dC = 0 and dgamma = 0."""
+    inp, dy, dF = _ssd3_bwd_case(51, b=2, l=5, m=2, h=3, p=2, g=1, n=3)
+    gz = oracle.ssd3_bwd(np.zeros_like(dy), dF, **inp)
+    decay = np.exp(inp["da"].sum(1))                                    # [b, h]
+    np.testing.assert_allclose(gz["dh0"], decay[:, :, None, None] * dF, rtol=1e-12)
+    np.testing.assert_allclose(gz["dC"], 0.0, atol=0)
+    np.testing.assert_allclose(gz["dgamma"], 0.0, atol=0)
+
