@@ -30,6 +30,7 @@
 // live in LDS, so any headdim x dstate up to 64 x 128 runs.
 #include <algorithm>
 
+#include "bwd_core.h"
 #include "common.h"
 
 namespace mamba {
@@ -285,44 +286,7 @@ __global__ __launch_bounds__(kBwdT) void ssd2_bwd_chunks(Ssd2BwdParams p) {
 // ---------------------------------------------------------------------------
 // MFMA path for headdim 64 x dstate 128 (the config-1 head shape): the same
 // recurrences with every P x N x Q and Q x Q x (P | N) contraction on
-// v_mfma_f32_32x32x2_f32 (f32 operands and accumulation).  For that
-// instruction lane l supplies A[l % 32][k0 + l / 32] and B[k0 + l / 32][l % 32],
-// and accumulator r of lane l holds D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32].
-// LDS rows are padded to an odd number of words, so that both the K-major
-// reads (32 rows, one column) and the row-major reads (32 consecutive words)
-// of a half-wave fall in 32 distinct banks.
-typedef float bwd_f32x16 __attribute__((ext_vector_type(16)));
-
-constexpr int kFP = 64, kFN = 128;                 // headdim, dstate of this path
-constexpr int kSX = 65, kSB = 129, kSQ = 33;       // padded row lengths (words)
-
-__device__ __forceinline__ bwd_f32x16 bwd_mfma(float a, float b, bwd_f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
-}
-// the accumulator row of register r for a lane in wave half hf
-__device__ __forceinline__ int bwd_row(int r, int hf) { return 8 * (r >> 2) + 4 * hf + (r & 3); }
-
-// Sum of 16 per-lane values over the 32 lanes of a wave half, scattered: lane
-// i32 returns the total of value (i32 >> 1) (both lanes of a pair hold it).
-__device__ __forceinline__ float bwd_half_sum16(const float (&v)[16], int i32) {
-    float w[8], x[4], y[2];
-    const bool b4 = (i32 >> 4) & 1, b3 = (i32 >> 3) & 1, b2 = (i32 >> 2) & 1, b1 = (i32 >> 1) & 1;
-#pragma unroll
-    for (int q = 0; q < 8; ++q) w[q] = (b4 ? v[8 + q] : v[q]) + __shfl_xor(b4 ? v[q] : v[8 + q], 16, 64);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) x[q] = (b3 ? w[4 + q] : w[q]) + __shfl_xor(b3 ? w[q] : w[4 + q], 8, 64);
-#pragma unroll
-    for (int q = 0; q < 2; ++q) y[q] = (b2 ? x[2 + q] : x[q]) + __shfl_xor(b2 ? x[q] : x[2 + q], 4, 64);
-    float z = (b1 ? y[1] : y[0]) + __shfl_xor(b1 ? y[0] : y[1], 2, 64);
-    return z + __shfl_xor(z, 1, 64);
-}
-// Sum over the 32 lanes of a wave half (every lane of the half gets it).
-__device__ __forceinline__ float bwd_half_sum(float v) {
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-
+// v_mfma_f32_32x32x2_f32 (helpers in bwd_core.h).
 // One chunk's inputs in registers (loaded ahead, written to LDS later).
 struct BwdRows {
     float4 x, dy, B0, B1, C0, C1;
@@ -370,13 +334,6 @@ __device__ __forceinline__ void bwd_fetch(const Ssd2BwdParams& p, const float* x
     f.C0 = tb0 < p.L ? vc0 : z;
     f.C1 = tb1 < p.L ? vc1 : z;
     f.dt = tt < p.L ? vt : 0.f;
-}
-
-__device__ __forceinline__ void bwd_put4(float* dst, float4 v) {
-    dst[0] = v.x;
-    dst[1] = v.y;
-    dst[2] = v.z;
-    dst[3] = v.w;
 }
 
 // Writes fetched rows to LDS; wave 0 also forms cs, a = exp(cs_end - cs),

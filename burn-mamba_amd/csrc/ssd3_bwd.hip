@@ -33,6 +33,7 @@
 // exp(cs_end) g + sum_k b_t(k) dy_k C_k^T.  f32 throughout.
 #include <algorithm>
 
+#include "bwd_core.h"
 #include "common.h"
 
 namespace mamba {
@@ -316,9 +317,433 @@ __global__ __launch_bounds__(256) void ssd3_bwd_finish(Ssd3BwdParams p, float* d
     }
 }
 
+// ---------------------------------------------------------------------------
+// MFMA path for headdim 64 x dstate 128 (the config-4 head shape): the Mamba-2
+// backward's f32 MFMA structure (bwd_core.h) on 32 fused rows per chunk.  The
+// per-step scalars are expanded over the step's M rows in LDS.
+
+// One chunk's fused rows and per-step scalars in registers.
+struct B3Rows {
+    float4 v, dy, B0, B1, C0, C1;
+    float da, gm, sc;
+};
+
+struct B3FastLds {
+    float g[kFP * kSB];      // [p][n] gradient of the state leaving the chunk
+    float v[32 * kSX];       // [j][p] fused rows
+    float dy[32 * kSX];      // [j][p]
+    float B[32 * kSB];       // [j][n]
+    float C[32 * kSB];       // [j][n]
+    float E1[32 * kSQ];      // [k][i] C_k . B_i, then W[k][i] C_k . B_i
+    float DX[32 * kSQ];      // [k][i] dy_k . v_i
+    float E2[32 * kSQ];      // [k][i] W[k][i] dy_k . v_i
+    float E3T[32 * kSQ];     // [i][k] W[k][i] dy_k . v_i
+    float cs[32], av[32], bv[32], sc[32], gm[32];   // per fused row (its step's values)
+    float xu[2][32];         // v_j . g B_j, per 32-row half of p
+    float qh[4][32];         // C_k . h_c^T dy_k, per quarter of n
+    float ghc[4];            // <g, h_c>, per quarter of n
+    float cpart[8][32];      // per-wave column sums of e (C_k.B_i)(dy_k.v_i) over later steps
+    float rrow[32], rdg[32]; // row sums: M over earlier steps, (C_k.B_i)(dy_k.v_i) over the same step
+};
+
+__device__ __forceinline__ int b3_lg(int M) { return 31 - __builtin_clz(M); }
+
+// Loads chunk c's fused rows (row j = step t0 + j / M, rank j % M) of v, dy, B,
+// C, and lane (tid & 31)'s step scalars; rows past the end read as zero.
+__device__ __forceinline__ void b3m_fetch(const Ssd3BwdParams& p, const float* vb, const float* yb, const float* Bb,
+                                          const float* Cb, int b, int h, int c, int tid, int lg, B3Rows& f) {
+    const int t0 = c * p.QS, mk = p.M - 1;
+    const int ix = tid >> 4, cx = (tid & 15) * 4;
+    const int ib = tid >> 5, cb = (tid & 31) * 4, ib2 = ib + 16;
+    const float4 z = {0.f, 0.f, 0.f, 0.f};
+    const int tx = t0 + (ix >> lg), tb0 = t0 + (ib >> lg), tb1 = t0 + (ib2 >> lg);
+    const int64_t ox = (int64_t)min(tx, p.L - 1), o0 = (int64_t)min(tb0, p.L - 1), o1 = (int64_t)min(tb1, p.L - 1);
+    const float4 vv = *reinterpret_cast<const float4*>(vb + ox * p.v_sl + (int64_t)(ix & mk) * p.v_sm + cx);
+    const float4 vy = *reinterpret_cast<const float4*>(yb + ox * p.dy_sl + (int64_t)(ix & mk) * p.dy_sm + cx);
+    const float4 vb0 = *reinterpret_cast<const float4*>(Bb + o0 * p.B_sl + (int64_t)(ib & mk) * p.B_sm + cb);
+    const float4 vb1 = *reinterpret_cast<const float4*>(Bb + o1 * p.B_sl + (int64_t)(ib2 & mk) * p.B_sm + cb);
+    const float4 vc0 = *reinterpret_cast<const float4*>(Cb + o0 * p.C_sl + (int64_t)(ib & mk) * p.C_sm + cb);
+    const float4 vc1 = *reinterpret_cast<const float4*>(Cb + o1 * p.C_sl + (int64_t)(ib2 & mk) * p.C_sm + cb);
+    const int tt = t0 + ((tid & 31) >> lg);
+    const int64_t ot = (int64_t)min(tt, p.L - 1);
+    const float da = p.da[(int64_t)b * p.da_sb + ot * p.da_sl + (int64_t)h * p.da_sh];
+    const float gm = p.gam ? p.gam[(int64_t)b * p.gam_sb + ot * p.gam_sl + (int64_t)h * p.gam_sh] : 1.f;
+    const float sc = p.scl ? p.scl[(int64_t)b * p.scl_sb + ot * p.scl_sl + (int64_t)h * p.scl_sh] : 1.f;
+    f.v = tx < p.L ? vv : z;
+    f.dy = tx < p.L ? vy : z;
+    f.B0 = tb0 < p.L ? vb0 : z;
+    f.B1 = tb1 < p.L ? vb1 : z;
+    f.C0 = tb0 < p.L ? vc0 : z;
+    f.C1 = tb1 < p.L ? vc1 : z;
+    f.da = tt < p.L ? da : 0.f;
+    f.gm = tt < p.L ? gm : 0.f;
+    f.sc = tt < p.L ? sc : 0.f;
+}
+
+// Writes fetched rows to LDS; wave 0 forms each fused row's cs (the inclusive
+// sum of da over the chunk's steps), a, b, scale and gamma.
+__device__ __forceinline__ void b3m_commit(B3FastLds& S, const B3Rows& f, int tid, int lg) {
+    const int ix = tid >> 4, cx = (tid & 15) * 4;
+    const int ib = tid >> 5, cb = (tid & 31) * 4;
+    bwd_put4(&S.v[ix * kSX + cx], f.v);
+    bwd_put4(&S.dy[ix * kSX + cx], f.dy);
+    bwd_put4(&S.B[ib * kSB + cb], f.B0);
+    bwd_put4(&S.B[(ib + 16) * kSB + cb], f.B1);
+    bwd_put4(&S.C[ib * kSB + cb], f.C0);
+    bwd_put4(&S.C[(ib + 16) * kSB + cb], f.C1);
+    if (tid < 64) {
+        const int lane = tid;
+        // the first row of each step carries its da, so the scan gives every row its step's cs
+        const bool first = (lane & ((1 << lg) - 1)) == 0;
+        const float cs = wave_incl_scan(lane < 32 && first ? f.da : 0.f);
+        const float tot = __shfl(cs, 31, 64);
+        if (lane < 32) {
+            S.cs[lane] = cs;
+            S.av[lane] = __expf(tot - cs);
+            S.bv[lane] = __expf(cs);
+            S.sc[lane] = f.sc;
+            S.gm[lane] = f.gm;
+        }
+    }
+}
+
+// The reverse chunk loop on MFMA: one 512-thread workgroup per (batch, head),
+// eight waves with the roles of the Mamba-2 kernel (ssd2_bwd.hip), on fused rows:
+//   phase 1  waves 0-1: u = g B_j; waves 2-5: g^T v_j, h_c^T dy_j; wave 6: C.B; wave 7: dy.v
+//   then W o (C.B), W o (dy.v), their transposes, and the row / column sums of
+//   M and of the same-step products on every thread;
+//   phase 2  waves 0-1: dv; waves 2-5: dB, dC; waves 0, 1, 6, 7: the update of g;
+//            wave 7: the per-step scalars (dda, dscale, dgamma).
+__global__ __launch_bounds__(512, 1) void ssd3_bwd_chunks_mfma(Ssd3BwdParams p) {
+    __shared__ B3FastLds S;
+    const int tid = threadIdx.x, wv = wave_id(), lane = tid & 63, i32 = lane & 31, hf = lane >> 5;
+    const int b = blockIdx.x / p.H, h = blockIdx.x % p.H, grp = h / (p.H / p.G);
+    const int lg = b3_lg(p.M), QS = p.QS;
+    const int64_t bh = (int64_t)b * p.H + h;
+    const float* vb = p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh;
+    const float* yb = p.dy + (int64_t)b * p.dy_sb + (int64_t)h * p.dy_sh;
+    const float* Bb = p.B + (int64_t)b * p.B_sb + (int64_t)grp * p.B_sg;
+    const float* Cb = p.C + (int64_t)b * p.C_sb + (int64_t)grp * p.C_sg;
+    const int tq = wv - 2;  // n quarter of waves 2-5
+    // h_c columns of waves 2-5: hreg[m] = h_c[2 m + hf][32 tq + i32]; reloaded
+    // with the next chunk's as soon as the current chunk's last use is done
+    float hreg[32];
+    auto fetch_h = [&](int c, float (&dst)[32]) {
+        const float* src = p.hs + (bh * p.nch + c) * (kFP * kFN) + hf * kFN + 32 * tq + i32;
+#pragma unroll
+        for (int m = 0; m < 32; ++m) dst[m] = src[m * 2 * kFN];
+    };
+    for (int e = tid; e < kFP * kFN; e += 512) S.g[(e >> 7) * kSB + (e & 127)] = p.dfin ? p.dfin[bh * (kFP * kFN) + e] : 0.f;
+    B3Rows pre;
+    b3m_fetch(p, vb, yb, Bb, Cb, b, h, p.nch - 1, tid, lg, pre);
+    if (wv >= 2 && wv < 6) fetch_h(p.nch - 1, hreg);
+    b3m_commit(S, pre, tid, lg);
+    __syncthreads();
+    for (int c = p.nch - 1; c >= 0; --c) {
+        const int t0 = c * QS;
+        const int cn = c > 0 ? c - 1 : 0;  // the next chunk (reloads chunk 0 at the end; unused)
+        // per-chunk opaque copy of the thread index (keeps the LDS addresses in the loop)
+        int tid = threadIdx.x;
+        asm volatile("" : "+v"(tid));
+        const int lane = tid & 63, i32 = lane & 31, hf = lane >> 5;
+        b3m_fetch(p, vb, yb, Bb, Cb, b, h, cn, tid, lg, pre);
+        // ---- phase 1
+        bwd_f32x16 acc0 = {}, acc1 = {};
+        if (wv < 2) {
+            const float* Ap = S.B + i32 * kSB + hf;
+            const float* Bp = S.g + (32 * wv + i32) * kSB + hf;
+#pragma unroll 16
+            for (int n0 = 0; n0 < kFN; n0 += 2) acc0 = bwd_mfma(Ap[n0], Bp[n0], acc0);
+        } else if (wv < 6) {
+            const float* Ax = S.v + i32 * kSX + hf;
+            const float* Ay = S.dy + i32 * kSX + hf;
+            const float* Bg = S.g + hf * kSB + 32 * tq + i32;
+#pragma unroll
+            for (int m = 0; m < 32; ++m) {
+                acc0 = bwd_mfma(Ax[2 * m], Bg[2 * m * kSB], acc0);
+                acc1 = bwd_mfma(Ay[2 * m], hreg[m], acc1);
+                if ((m & 7) == 7) __builtin_amdgcn_sched_barrier(0);  // bounds the operand prefetch
+            }
+        } else if (wv == 6) {
+            const float* Ap = S.C + i32 * kSB + hf;
+            const float* Bp = S.B + i32 * kSB + hf;
+#pragma unroll 16
+            for (int n0 = 0; n0 < kFN; n0 += 2) acc0 = bwd_mfma(Ap[n0], Bp[n0], acc0);
+        } else {
+            const float* Ap = S.dy + i32 * kSX + hf;
+            const float* Bp = S.v + i32 * kSX + hf;
+#pragma unroll 16
+            for (int p0 = 0; p0 < kFP; p0 += 2) acc0 = bwd_mfma(Ap[p0], Bp[p0], acc0);
+        }
+        // ---- per-wave reductions of the phase-1 products
+        {
+            float w[16];
+            if (wv < 2) {  // v_j . g B_j over this half of p
+#pragma unroll
+                for (int r = 0; r < 16; ++r) w[r] = acc0[r] * S.v[bwd_row(r, hf) * kSX + 32 * wv + i32];
+                const float s = bwd_half_sum16(w, i32);
+                if ((i32 & 1) == 0) S.xu[wv][bwd_row(i32 >> 1, hf)] = s;
+            } else if (wv < 6) {  // C_k . h_c^T dy_k over this quarter of n; <g, h_c>
+#pragma unroll
+                for (int r = 0; r < 16; ++r) w[r] = acc1[r] * S.C[bwd_row(r, hf) * kSB + 32 * tq + i32];
+                const float s = bwd_half_sum16(w, i32);
+                if ((i32 & 1) == 0) S.qh[tq][bwd_row(i32 >> 1, hf)] = s;
+                float gh = 0.f;
+#pragma unroll
+                for (int m = 0; m < 32; ++m) gh += hreg[m] * S.g[(2 * m + hf) * kSB + 32 * tq + i32];
+                gh = wave_sum(gh);
+                if (lane == 0) S.ghc[tq] = gh;
+                fetch_h(cn, hreg);
+            } else {
+                float* dst = wv == 6 ? S.E1 : S.DX;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) dst[bwd_row(r, hf) * kSQ + i32] = acc0[r];
+            }
+        }
+        __syncthreads();
+        // ---- the weighted fused Q x Q matrices; row sums of M and of the
+        // same-step products, column sums of e (C.B)(dy.v) over later steps
+        {
+            const int i = i32, k0 = 4 * wv + 2 * hf, ti = i >> lg;
+            const float cs_i = S.cs[i], sc_i = S.sc[i];
+            float rsum[4], xgc = 0.f;
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const int k = k0 + q, tk = k >> lg;
+                const bool lower = tk > ti, same = tk == ti;
+                const float e = lower ? __expf(S.cs[k] - cs_i) : 0.f;
+                const float W = lower ? e * sc_i : (same ? S.gm[k] : 0.f);
+                const float cb = S.E1[k * kSQ + i];
+                const float dx = S.DX[k * kSQ + i];
+                S.E1[k * kSQ + i] = W * cb;
+                S.E2[k * kSQ + i] = W * dx;
+                S.E3T[i * kSQ + k] = W * dx;
+                rsum[q] = lower ? W * dx * cb : 0.f;
+                rsum[2 + q] = same ? cb * dx : 0.f;
+                xgc += e * cb * dx;
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) rsum[q] = bwd_half_sum(rsum[q]);
+            if (i32 < 2) {
+                S.rrow[k0 + i32] = rsum[i32];
+                S.rdg[k0 + i32] = rsum[2 + i32];
+            }
+            xgc += __shfl_xor(xgc, 32, 64);
+            if (hf == 0) S.cpart[wv][i] = xgc;
+        }
+        __syncthreads();
+        // ---- phase 2
+        if (wv < 2) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc0[r] *= S.sc[bwd_row(r, hf)] * S.av[bwd_row(r, hf)];
+            const float* Ap = S.E1 + hf * kSQ + i32;
+            const float* Bp = S.dy + hf * kSX + 32 * wv + i32;
+#pragma unroll
+            for (int k0 = 0; k0 < 32; k0 += 2) acc0 = bwd_mfma(Ap[k0 * kSQ], Bp[k0 * kSX], acc0);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int j = bwd_row(r, hf), t = t0 + (j >> lg);
+                if (t < p.L)
+                    p.dv[((((int64_t)b * p.L + t) * p.M + (j & (p.M - 1))) * p.H + h) * kFP + 32 * wv + i32] = acc0[r];
+            }
+        } else if (wv < 6) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int j = bwd_row(r, hf);
+                acc0[r] *= S.sc[j] * S.av[j];
+                acc1[r] *= S.bv[j];
+            }
+            const float* A2 = S.E2 + hf * kSQ + i32;
+            const float* A3 = S.E3T + hf * kSQ + i32;
+            const float* Bc = S.C + hf * kSB + 32 * tq + i32;
+            const float* Bbp = S.B + hf * kSB + 32 * tq + i32;
+#pragma unroll
+            for (int k0 = 0; k0 < 32; k0 += 2) {
+                acc0 = bwd_mfma(A2[k0 * kSQ], Bc[k0 * kSB], acc0);
+                acc1 = bwd_mfma(A3[k0 * kSQ], Bbp[k0 * kSB], acc1);
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int j = bwd_row(r, hf), t = t0 + (j >> lg);
+                if (t < p.L) {
+                    const int64_t o = ((((int64_t)b * p.L + t) * p.M + (j & (p.M - 1))) * p.H + h) * kFN + 32 * tq + i32;
+                    p.dBh[o] = acc0[r];
+                    p.dCh[o] = acc1[r];
+                }
+            }
+        } else if (wv == 7) {
+            // per step t (lanes 0 .. QS-1): the sums over its rows, then dda, dscale, dgamma
+            const int t = lane;
+            const bool live = t < QS;
+            const int r0 = live ? t << lg : 0;
+            float xu = 0.f, qh = 0.f, xg2 = 0.f, rowm = 0.f, dg = 0.f;
+            for (int m = 0; m < p.M; ++m) {
+                const int j = r0 + m;
+                xu += S.xu[0][j] + S.xu[1][j];
+                qh += (S.qh[0][j] + S.qh[1][j]) + (S.qh[2][j] + S.qh[3][j]);
+#pragma unroll
+                for (int w = 0; w < 8; ++w) xg2 += S.cpart[w][j];
+                rowm += S.rrow[j];
+                dg += S.rdg[j];
+            }
+            if (!live) xu = qh = xg2 = rowm = dg = 0.f;
+            const float cst = S.cs[r0], avt = S.av[r0], bvt = S.bv[r0], sct = live ? S.sc[r0] : 0.f;
+            const float ghc = (S.ghc[0] + S.ghc[1]) + (S.ghc[2] + S.ghc[3]);
+            const float scxu = sct * xu;
+            float s1 = 0.f, s2 = 0.f;
+            for (int u = 0; u < QS; ++u) {  // u is wave-uniform: the other step's values by lane read
+                const float cu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cst), u));
+                const float xuu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(scxu), u));
+                const float qhu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qh), u));
+                if (u < t) s1 += __expf(cst - cu) * xuu;
+                if (u >= t) s2 += __expf(cu - cst) * qhu;
+            }
+            const float colm = sct * xg2;
+            const float pc = wave_incl_scan(colm) - colm;
+            const float pr = wave_incl_scan(rowm) - rowm;
+            if (live && t0 + t < p.L) {
+                const int64_t o = (int64_t)b * p.L * p.H + (int64_t)(t0 + t) * p.H + h;
+                p.dda[o] = avt * bvt * ghc + avt * s1 + bvt * s2 + (pc - pr);
+                if (p.dscl) p.dscl[o] = avt * xu + xg2;
+                if (p.dgam) p.dgam[o] = dg;
+            }
+        }
+        // the gradient entering this chunk: exp(cs_end) g + sum_k b_k dy_k C_k^T
+        if (wv < 2 || wv >= 6) {
+            const float dec = __expf(S.cs[31]);
+            const int gt0 = wv < 2 ? 2 * wv : 2 * wv - 8;
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                const int tile = gt0 + tt, tp = tile >> 2, tn = tile & 3;
+                float* gp = S.g + (32 * tp) * kSB + 32 * tn + i32;
+                bwd_f32x16 a;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) a[r] = dec * gp[bwd_row(r, hf) * kSB];
+                const float* Ap = S.dy + hf * kSX + 32 * tp + i32;
+                const float* Bp = S.C + hf * kSB + 32 * tn + i32;
+#pragma unroll
+                for (int k0 = 0; k0 < 32; k0 += 2) a = bwd_mfma(S.bv[k0 + hf] * Ap[k0 * kSX], Bp[k0 * kSB], a);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) gp[bwd_row(r, hf) * kSB] = a[r];
+            }
+        }
+        __syncthreads();
+        b3m_commit(S, pre, tid, lg);
+        __syncthreads();
+    }
+    for (int e = tid; e < kFP * kFN; e += 512) p.dh0[bh * (kFP * kFN) + e] = S.g[(e >> 7) * kSB + (e & 127)];
+}
+
+// Chunk-entry states on MFMA (headdim 64 x dstate 128), as the Mamba-2 one:
+// wave w keeps two 32 x 32 state tiles as accumulators across chunks, stores
+// them as chunk c's entry state, then adds
+//   exp(cs_end) h + sum_j exp(cs_end - cs_t(j)) scale_t(j) v_j B_j^T.
+struct B3StatesLds {
+    float v[32 * kSX];
+    float B[32 * kSB];
+    float w[32];
+    float dec;
+};
+
+__global__ __launch_bounds__(256, 3) void ssd3_bwd_states_mfma(Ssd3BwdParams p) {
+    __shared__ B3StatesLds S;
+    const int tid = threadIdx.x, wv = wave_id(), lane = tid & 63, i32 = lane & 31, hf = lane >> 5;
+    const int b = blockIdx.x / p.H, h = blockIdx.x % p.H, grp = h / (p.H / p.G);
+    const int lg = b3_lg(p.M), mk = p.M - 1;
+    const int64_t bh = (int64_t)b * p.H + h;
+    const float* vb = p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh;
+    const float* Bb = p.B + (int64_t)b * p.B_sb + (int64_t)grp * p.B_sg;
+    const int tp = wv >> 1, tn0 = 2 * (wv & 1);
+    bwd_f32x16 acc[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            acc[q][r] = p.h0 ? p.h0[bh * (kFP * kFN) + (32 * tp + bwd_row(r, hf)) * kFN + 32 * (tn0 + q) + i32] : 0.f;
+    // loads of one chunk: v rows (tid >> 4) and + 16; B rows (tid >> 5) + 8 q
+    const int ix = tid >> 4, cx = (tid & 15) * 4, ib = tid >> 5, cb = (tid & 31) * 4;
+    float4 fv[2], fb[4];
+    float fda, fsc;
+    auto fetch = [&](int c) {
+        const int t0 = c * p.QS;
+        const float4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int j = ix + 16 * q, t = t0 + (j >> lg);
+            const float4 v = *reinterpret_cast<const float4*>(vb + (int64_t)min(t, p.L - 1) * p.v_sl +
+                                                              (int64_t)(j & mk) * p.v_sm + cx);
+            fv[q] = t < p.L ? v : z;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int j = ib + 8 * q, t = t0 + (j >> lg);
+            const float4 v = *reinterpret_cast<const float4*>(Bb + (int64_t)min(t, p.L - 1) * p.B_sl +
+                                                              (int64_t)(j & mk) * p.B_sm + cb);
+            fb[q] = t < p.L ? v : z;
+        }
+        const int t = t0 + ((tid & 31) >> lg);
+        const int64_t ot = (int64_t)min(t, p.L - 1);
+        const float da = p.da[(int64_t)b * p.da_sb + ot * p.da_sl + (int64_t)h * p.da_sh];
+        const float sc = p.scl ? p.scl[(int64_t)b * p.scl_sb + ot * p.scl_sl + (int64_t)h * p.scl_sh] : 1.f;
+        fda = t < p.L ? da : 0.f;
+        fsc = t < p.L ? sc : 0.f;
+    };
+    auto commit = [&]() {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) bwd_put4(&S.v[(ix + 16 * q) * kSX + cx], fv[q]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) bwd_put4(&S.B[(ib + 8 * q) * kSB + cb], fb[q]);
+        if (wv == 0) {
+            const bool first = (lane & mk) == 0;
+            const float cs = wave_incl_scan(lane < 32 && first ? fda : 0.f);
+            const float tot = __shfl(cs, 31, 64);
+            if (lane < 32) S.w[lane] = __expf(tot - cs) * fsc;
+            if (lane == 31) S.dec = __expf(tot);
+        }
+    };
+    fetch(0);
+    commit();
+    __syncthreads();
+    for (int c = 0; c < p.nch; ++c) {
+        fetch(c + 1 < p.nch ? c + 1 : c);
+        float* dst = p.hs + (bh * p.nch + c) * (kFP * kFN) + (32 * tp) * kFN + i32;
+        const float dec = S.dec;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                dst[bwd_row(r, hf) * kFN + 32 * (tn0 + q)] = acc[q][r];
+                acc[q][r] *= dec;
+            }
+        }
+        const float* Ap = S.v + hf * kSX + 32 * tp + i32;
+        const float* Bp = S.B + hf * kSB + 32 * tn0 + i32;
+#pragma unroll
+        for (int k0 = 0; k0 < 32; k0 += 2) {
+            const float a = S.w[k0 + hf] * Ap[k0 * kSX];
+            acc[0] = bwd_mfma(a, Bp[k0 * kSB], acc[0]);
+            acc[1] = bwd_mfma(a, Bp[k0 * kSB + 32], acc[1]);
+        }
+        __syncthreads();
+        commit();
+        __syncthreads();
+    }
+}
+
 static size_t b3_states_lds(int P, int N) { return ((size_t)P * N + (size_t)kB3F * (P + N)) * sizeof(float); }
 static size_t b3_chunks_lds(int P, int N) {
     return ((size_t)2 * P * N + (size_t)3 * kB3F * P + (size_t)2 * kB3F * N + (size_t)3 * kB3F * kB3F) * sizeof(float);
+}
+
+// The MFMA path: headdim 64, dstate 128, and float4-aligned rows of v, dy, B, C.
+static bool b3_mfma_ok(const mamba_ssd3_bwd_args* a) {
+    auto al = [](const void* q) { return ((uintptr_t)q & 15u) == 0; };
+    auto m4 = [](int64_t s0, int64_t s1, int64_t s2, int64_t s3) {
+        return s0 % 4 == 0 && s1 % 4 == 0 && s2 % 4 == 0 && s3 % 4 == 0;
+    };
+    return a->headdim == kFP && a->dstate == kFN && al(a->v) && al(a->dy) && al(a->B) && al(a->C) &&
+           m4(a->v_sb, a->v_sl, a->v_sm, a->v_sh) && m4(a->dy_sb, a->dy_sl, a->dy_sm, a->dy_sh) &&
+           m4(a->B_sb, a->B_sl, a->B_sm, a->B_sg) && m4(a->C_sb, a->C_sl, a->C_sm, a->C_sg);
 }
 
 struct B3Layout {
@@ -385,16 +810,25 @@ static int ssd3_bwd_run(const mamba_ssd3_bwd_args* a, void* workspace, size_t wo
     }
     hipStream_t s = (hipStream_t)stream;
     const dim3 grid(a->batch * a->nheads);
-    MAMBA_CHECK_HIP(hipFuncSetAttribute((const void*)ssd3_bwd_states, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        (int)b3_states_lds(p.P, p.N)));
-    MAMBA_CHECK_HIP(hipFuncSetAttribute((const void*)ssd3_bwd_chunks, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        (int)b3_chunks_lds(p.P, p.N)));
-    hipLaunchKernelGGL(ssd3_bwd_states, grid, dim3(kB3T), b3_states_lds(p.P, p.N), s, p);
-    MAMBA_CHECK_LAUNCH();
-    if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, s));
-    hipLaunchKernelGGL(ssd3_bwd_chunks, grid, dim3(kB3T), b3_chunks_lds(p.P, p.N), s, p);
-    MAMBA_CHECK_LAUNCH();
-    if (ev1) MAMBA_CHECK_HIP(hipEventRecord(ev1, s));
+    if (b3_mfma_ok(a)) {
+        hipLaunchKernelGGL(ssd3_bwd_states_mfma, grid, dim3(256), 0, s, p);
+        MAMBA_CHECK_LAUNCH();
+        if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, s));
+        hipLaunchKernelGGL(ssd3_bwd_chunks_mfma, grid, dim3(512), 0, s, p);
+        MAMBA_CHECK_LAUNCH();
+        if (ev1) MAMBA_CHECK_HIP(hipEventRecord(ev1, s));
+    } else {
+        MAMBA_CHECK_HIP(hipFuncSetAttribute((const void*)ssd3_bwd_states, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            (int)b3_states_lds(p.P, p.N)));
+        MAMBA_CHECK_HIP(hipFuncSetAttribute((const void*)ssd3_bwd_chunks, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            (int)b3_chunks_lds(p.P, p.N)));
+        hipLaunchKernelGGL(ssd3_bwd_states, grid, dim3(kB3T), b3_states_lds(p.P, p.N), s, p);
+        MAMBA_CHECK_LAUNCH();
+        if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, s));
+        hipLaunchKernelGGL(ssd3_bwd_chunks, grid, dim3(kB3T), b3_chunks_lds(p.P, p.N), s, p);
+        MAMBA_CHECK_LAUNCH();
+        if (ev1) MAMBA_CHECK_HIP(hipEventRecord(ev1, s));
+    }
     if (a->ngroups != a->nheads) {
         const int64_t fin = (int64_t)a->batch * a->seqlen * a->mimo * a->ngroups * a->dstate;
         const int fgrid = (int)std::max<int64_t>(1, std::min<int64_t>((fin + 255) / 256, 4096));

@@ -21,7 +21,11 @@ CASES = [
     (1, 40, 2, 4, 16, 1, 16, True, False, True),    # MIMO 2, one group
     (2, 13, 1, 3, 8, 3, 32, True, True, False),     # SISO, no d(final state)
     (1, 19, 8, 2, 16, 1, 32, False, True, True),    # MIMO 8, unit weights (the double seam)
-    (1, 70, 4, 2, 64, 2, 128, True, True, True),    # config-4 head shape
+    # headdim 64 x dstate 128 with float4-aligned rows: the MFMA kernels
+    (1, 70, 4, 2, 64, 2, 128, True, True, True),    # config-4 head shape, per-head B / C
+    (2, 37, 2, 4, 64, 1, 128, True, True, True),    # MIMO 2, one group, ragged
+    (1, 40, 1, 2, 64, 1, 128, True, False, True),   # SISO (32 steps per chunk)
+    (1, 21, 8, 2, 64, 2, 128, False, True, True),   # MIMO 8, unit weights (the double seam)
 ]
 
 
@@ -65,14 +69,16 @@ def test_ssd3_bwd_matches_oracle(case):
         assert out["dgamma"] is None and out["dscale"] is None
 
 
-def test_ssd3_bwd_strided_inputs():
+@pytest.mark.parametrize("p,n", [(16, 32), (64, 128)])
+def test_ssd3_bwd_strided_inputs(p, n):
     """The seam's layouts through strides: v and dy as views of a wider row,
     da / gamma / scale as [b, h, l] tensors viewed [b, l, h], B / C as slices
-    of one wider row."""
+    of one wider row (an odd row length, so at headdim 64 x dstate 128 the
+    unaligned rows take the SIMT kernels)."""
     import torch
     import mamba_hip
-    b, l, m, h, p, g, n = 2, 30, 2, 2, 16, 1, 32
-    print("ssd3 bwd strided", flush=True)
+    b, l, m, h, g = 2, 30, 2, 2, 1
+    print("ssd3 bwd strided", p, n, flush=True)
     d, dy, dF = _inputs(7, b, l, m, h, p, g, n, True, True, True)
     wide = torch.zeros((b, l, m, h, p + 4), device="cuda")
     wide[..., :p] = _t(d["v"])
