@@ -33,6 +33,7 @@ for _p in (ROOT, os.path.join(ROOT, "burn-mamba_amd"), os.path.join(ROOT, "tests
 
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, published
 BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA, published
+F32_MFMA_PEAK_TFLOPS = 157.3   # MI355X dense f32 MFMA, published
 
 
 def log(msg):
@@ -704,9 +705,6 @@ def ssd2_bwd_algorithmic(cfg):
     return bytes_, chunk_flops, state_flops
 
 
-F32_MFMA_PEAK_TFLOPS = 157.3   # MI355X dense f32 MFMA, published
-
-
 def bench_ssd2_bwd(args):
     """The Mamba-2 SSD backward at the config-1 head shape (B=8 L=4096 H=80
     P=64 N=128, one group), f32: mamba_ssd2_bwd from dy (no initial state, no
@@ -767,6 +765,86 @@ def cpu_baseline_ssd2_bwd(cfg, seed=0):
     el = time.perf_counter() - t0
     return {"value": L / el, "unit": "tokens/s", "cores": 1, "kind": "port",
             "sample": f"1 x {L} tokens, {h} heads ({el:.1f} s), float64 numpy token-by-token reverse "
+                      f"recurrence of the reference's backward"}
+
+
+def ssd3_bwd_algorithmic(cfg):
+    """Causal-exact FLOPs of the Mamba-3 single-SSD backward at 32 fused
+    positions (32 / M steps) per chunk, per (batch, head): the reverse chunk
+    loop's four P x N products per fused position (g B_j, g^T v_j, h_c^T dy_j,
+    the state-gradient update) and its five fused Q x Q products (C.B, dy.v,
+    then the dy, C and B contractions with them) over the pairs whose step is
+    not later, M^2 QS (QS + 1) / 2 per chunk; the chunk-entry states' P x N
+    product per fused position."""
+    b, l, m, h, p, n = (cfg[k] for k in ("batch", "seqlen", "mimo", "nheads", "headdim", "dstate"))
+    qs = 32 // m
+    nch = -(-l // qs)
+    pairs = m * m * qs * (qs + 1) // 2
+    chunk_flops = b * h * nch * 2 * (4 * 32 * p * n + pairs * (3 * n + 2 * p))
+    state_flops = b * h * l * m * 2 * p * n
+    return chunk_flops, state_flops
+
+
+def bench_ssd3_bwd(args):
+    """The Mamba-3 single-SSD backward at config 4 (B=4 L=8192 H=32 P=64 N=128
+    MIMO 4, per-head B / C), f32: mamba_ssd3_bwd from dy (no initial state, no
+    d(final state))."""
+    import torch
+
+    import mamba_hip
+    cfg = dict(SSD3_CFG4)
+    dev = torch.device("cuda:0")
+    inp = make_ssd3_inputs(cfg, dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    v, B, C = (inp[k].float() for k in ("v", "B", "C"))
+    dy = torch.randn(v.shape, generator=g, device=dev)
+
+    def step(events=None):
+        mamba_hip.ssd3_bwd(dy, v, inp["da"], B, C, inp["gamma"], inp["scale"], None, None, events=events)
+
+    ms_per_step, kern_ms = _time_steps(args, step)
+    flops, state_flops = ssd3_bwd_algorithmic(cfg)
+    tokens = cfg["batch"] * cfg["seqlen"]
+    tflops = flops / (kern_ms * 1e-3) / 1e12
+    roof = {"bound": "mfma", "achieved": tflops, "peak": F32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": tflops / F32_MFMA_PEAK_TFLOPS, "traffic": _profiled_traffic("mamba3_ssd_bwd_cfg4"),
+            "kernel_ms": kern_ms, "algorithmic_flops": flops, "kernel": "ssd3_bwd_chunks (reverse chunk loop)",
+            "timing": "HIP events around the reverse chunk-loop kernel on its stream, per call",
+            "call_tflops": (flops + state_flops) / (ms_per_step * 1e-3) / 1e12,
+            "grid": f"{cfg['batch'] * cfg['nheads']} workgroups (one per batch row and head) on 256 CUs"}
+    return {
+        "metric": "Mamba-3 SSD backward tokens/s (B=4 L=8192 H=32 P=64 N=128 MIMO 4, f32) + % f32 MFMA roofline",
+        "value": tokens / (ms_per_step * 1e-3), "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (BASELINE.json configs[4] distributions at the SSD seam, dy ~ N(0,1), "
+                                "seeds 0 / 1)",
+        "config": {"workload": "mamba3_ssd_bwd_cfg4", **cfg, "io": "all f32, per-head B / C",
+                   "entry": "mamba_ssd3_bwd (chunk states, reverse chunk loop; 32 fused positions per chunk)"},
+        "roofline": roof,
+    }
+
+
+def cpu_baseline_ssd3_bwd(cfg, seed=0):
+    """The oracle's float64 token-by-token reverse recurrence (oracle.ssd3_bwd)
+    on one sequence of 512 tokens with every head, scaled to tokens/s."""
+    import numpy as np
+
+    import oracle
+    rng = np.random.default_rng(seed)
+    L, m, h, p, n = 512, cfg["mimo"], cfg["nheads"], cfg["headdim"], cfg["dstate"]
+    r = lambda *s: rng.standard_normal(s).astype(np.float32)  # noqa: E731
+    v, dy = r(1, L, m, h, p), r(1, L, m, h, p)
+    B, C = (r(1, L, m, h, n) / np.sqrt(n)).astype(np.float32), (r(1, L, m, h, n) / np.sqrt(n)).astype(np.float32)
+    da = (-rng.uniform(1e-3, 0.5, (1, L, h))).astype(np.float32)
+    gam = rng.uniform(1e-3, 0.1, (1, L, h)).astype(np.float32)
+    scl = rng.uniform(1e-3, 0.2, (1, L, h)).astype(np.float32)
+    t0 = time.perf_counter()
+    oracle.ssd3_bwd(dy, None, v, da, B, C, gam, scl, None)
+    el = time.perf_counter() - t0
+    return {"value": L / el, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"1 x {L} tokens, {h} heads, MIMO {m} ({el:.1f} s), float64 numpy token-by-token reverse "
                       f"recurrence of the reference's backward"}
 
 
@@ -1229,7 +1307,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", default="ssd2",
                     choices=["ssd2", "mamba1", "decode", "ssd3", "mamba3_fused", "mamba1_step", "mamba3_step",
-                             "mamba3_prep", "mamba2_block", "ssd2_bwd"])
+                             "mamba3_prep", "mamba2_block", "ssd2_bwd", "ssd3_bwd"])
     ap.add_argument("--batch", type=int, default=DECODE_CFG3["batch"], help="decode batch")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true",
@@ -1243,7 +1321,10 @@ def main():
               "(the hot path shards by batch/head with no communication; see DESIGN.md)",
               file=sys.stderr)
         sys.exit(2)
-    if args.workload == "ssd2_bwd":
+    if args.workload == "ssd3_bwd":
+        out = bench_ssd3_bwd(args)
+        base = (lambda: cpu_baseline_ssd3_bwd(SSD3_CFG4))
+    elif args.workload == "ssd2_bwd":
         out = bench_ssd2_bwd(args)
         base = (lambda: cpu_baseline_ssd2_bwd(SSD2_CFG1))
     elif args.workload == "mamba2_block":

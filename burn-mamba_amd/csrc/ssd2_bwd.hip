@@ -595,10 +595,11 @@ __global__ __launch_bounds__(512, 1) void ssd2_bwd_chunks_mfma(Ssd2BwdParams p) 
     }
 }
 
-// Chunk-entry states on MFMA (headdim 64 x dstate 128): one 256-thread
-// workgroup per (batch, head); wave w keeps two 32 x 32 tiles of the state
-// (rows 32 (w / 2).., columns 64 (w % 2)..) as accumulators across chunks,
-// stores them as chunk c's entry state, then adds
+// Chunk-entry states on MFMA (headdim 64 x dstate 128): two 256-thread
+// workgroups per (batch, head), one per 64-column half of the state (the
+// columns evolve independently); wave w keeps one 32 x 32 tile (rows
+// 32 (w / 2).., columns 32 (2 half + w % 2)..) as an accumulator across
+// chunks, stores it as chunk c's entry state, then adds
 //   exp(cs_end) h + sum_i exp(cs_end - cs_i) dt_i x_i B_i^T.
 struct BwdStatesLds {
     float x[32 * kSX];
@@ -610,22 +611,21 @@ struct BwdStatesLds {
 __global__ __launch_bounds__(256, 3) void ssd2_bwd_states_mfma(Ssd2BwdParams p) {
     __shared__ BwdStatesLds S;
     const int tid = threadIdx.x, wv = wave_id(), lane = tid & 63, i32 = lane & 31, hf = lane >> 5;
-    const int b = blockIdx.x / p.H, h = blockIdx.x % p.H, grp = h / (p.H / p.G);
+    const int ns = blockIdx.x & 1;  // 64-column half of the state
+    const int b = (blockIdx.x >> 1) / p.H, h = (blockIdx.x >> 1) % p.H, grp = h / (p.H / p.G);
     const int64_t bh = (int64_t)b * p.H + h;
     const float A = p.A[h];
     const float* xb = p.x + (int64_t)b * p.x_sb + (int64_t)h * p.x_sh;
     const float* Bb = p.B + (int64_t)b * p.B_sb + (int64_t)grp * p.B_sg;
     const float* db = p.dt + (int64_t)b * p.dt_sb + (int64_t)h * p.dt_sh;
-    const int tp = wv >> 1, tn0 = 2 * (wv & 1);
-    bwd_f32x16 acc[2];
+    const int tp = wv >> 1, tn = 2 * ns + (wv & 1);
+    bwd_f32x16 acc;
 #pragma unroll
-    for (int q = 0; q < 2; ++q)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-            acc[q][r] = p.h0 ? p.h0[bh * (kFP * kFN) + (32 * tp + bwd_row(r, hf)) * kFN + 32 * (tn0 + q) + i32] : 0.f;
+    for (int r = 0; r < 16; ++r)
+        acc[r] = p.h0 ? p.h0[bh * (kFP * kFN) + (32 * tp + bwd_row(r, hf)) * kFN + 32 * tn + i32] : 0.f;
     // loads of one chunk: x rows (tid >> 4) and + 16; B rows (tid >> 5) + 8 q
-    const int ix = tid >> 4, cx = (tid & 15) * 4, ib = tid >> 5, cb = (tid & 31) * 4;
-    float4 fx[2], fb[4];
+    const int ix = tid >> 4, cx = (tid & 15) * 4, ib = tid >> 4, cb = 64 * ns + (tid & 15) * 4;
+    float4 fx[2], fb[2];
     float fdt;
     auto fetch = [&](int c) {
         const int t0 = c * 32;
@@ -637,8 +637,8 @@ __global__ __launch_bounds__(256, 3) void ssd2_bwd_states_mfma(Ssd2BwdParams p) 
             fx[q] = t < p.L ? v : z;
         }
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int t = t0 + ib + 8 * q;
+        for (int q = 0; q < 2; ++q) {
+            const int t = t0 + ib + 16 * q;
             const float4 v = *reinterpret_cast<const float4*>(Bb + (int64_t)min(t, p.L - 1) * p.B_sl + cb);
             fb[q] = t < p.L ? v : z;
         }
@@ -650,7 +650,7 @@ __global__ __launch_bounds__(256, 3) void ssd2_bwd_states_mfma(Ssd2BwdParams p) 
 #pragma unroll
         for (int q = 0; q < 2; ++q) bwd_put4(&S.x[(ix + 16 * q) * kSX + cx], fx[q]);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) bwd_put4(&S.B[(ib + 8 * q) * kSB + cb], fb[q]);
+        for (int q = 0; q < 2; ++q) bwd_put4(&S.B[(ib + 16 * q) * kSB + cb], fb[q]);
         if (wv == 0) {
             const float cs = wave_incl_scan(lane < 32 ? fdt * A : 0.f);
             const float tot = __shfl(cs, 31, 64);
@@ -666,20 +666,16 @@ __global__ __launch_bounds__(256, 3) void ssd2_bwd_states_mfma(Ssd2BwdParams p) 
         float* dst = p.hs + (bh * p.nch + c) * (kFP * kFN) + (32 * tp) * kFN + i32;
         const float dec = S.dec;
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                dst[bwd_row(r, hf) * kFN + 32 * (tn0 + q)] = acc[q][r];
-                acc[q][r] *= dec;
-            }
+        for (int r = 0; r < 16; ++r) {
+            dst[bwd_row(r, hf) * kFN + 32 * tn] = acc[r];
+            acc[r] *= dec;
         }
         const float* Ap = S.x + hf * kSX + 32 * tp + i32;
-        const float* Bp = S.B + hf * kSB + 32 * tn0 + i32;
+        const float* Bp = S.B + hf * kSB + 32 * tn + i32;
 #pragma unroll
         for (int k0 = 0; k0 < 32; k0 += 2) {
             const float a = S.w[k0 + hf] * Ap[k0 * kSX];
-            acc[0] = bwd_mfma(a, Bp[k0 * kSB], acc[0]);
-            acc[1] = bwd_mfma(a, Bp[k0 * kSB + 32], acc[1]);
+            acc = bwd_mfma(a, Bp[k0 * kSB], acc);
         }
         __syncthreads();
         commit();
@@ -806,7 +802,7 @@ static int ssd2_bwd_run(const mamba_ssd2_bwd_args* a, void* workspace, size_t wo
     hipStream_t s = (hipStream_t)stream;
     const dim3 grid(a->batch * a->nheads);
     if (bwd_mfma_ok(a)) {
-        hipLaunchKernelGGL(ssd2_bwd_states_mfma, grid, dim3(256), 0, s, p);
+        hipLaunchKernelGGL(ssd2_bwd_states_mfma, dim3(2 * grid.x), dim3(256), 0, s, p);
         MAMBA_CHECK_LAUNCH();
         if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, s));
         hipLaunchKernelGGL(ssd2_bwd_chunks_mfma, grid, dim3(512), 0, s, p);

@@ -635,8 +635,9 @@ __global__ __launch_bounds__(512, 1) void ssd3_bwd_chunks_mfma(Ssd3BwdParams p) 
 }
 
 // Chunk-entry states on MFMA (headdim 64 x dstate 128), as the Mamba-2 one:
-// wave w keeps two 32 x 32 state tiles as accumulators across chunks, stores
-// them as chunk c's entry state, then adds
+// two workgroups per (batch, head), one per 64-column half of the state; wave
+// w keeps one 32 x 32 state tile as an accumulator across chunks, stores it as
+// chunk c's entry state, then adds
 //   exp(cs_end) h + sum_j exp(cs_end - cs_t(j)) scale_t(j) v_j B_j^T.
 struct B3StatesLds {
     float v[32 * kSX];
@@ -648,21 +649,20 @@ struct B3StatesLds {
 __global__ __launch_bounds__(256, 3) void ssd3_bwd_states_mfma(Ssd3BwdParams p) {
     __shared__ B3StatesLds S;
     const int tid = threadIdx.x, wv = wave_id(), lane = tid & 63, i32 = lane & 31, hf = lane >> 5;
-    const int b = blockIdx.x / p.H, h = blockIdx.x % p.H, grp = h / (p.H / p.G);
+    const int ns = blockIdx.x & 1;  // 64-column half of the state
+    const int b = (blockIdx.x >> 1) / p.H, h = (blockIdx.x >> 1) % p.H, grp = h / (p.H / p.G);
     const int lg = b3_lg(p.M), mk = p.M - 1;
     const int64_t bh = (int64_t)b * p.H + h;
     const float* vb = p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh;
     const float* Bb = p.B + (int64_t)b * p.B_sb + (int64_t)grp * p.B_sg;
-    const int tp = wv >> 1, tn0 = 2 * (wv & 1);
-    bwd_f32x16 acc[2];
+    const int tp = wv >> 1, tn = 2 * ns + (wv & 1);
+    bwd_f32x16 acc;
 #pragma unroll
-    for (int q = 0; q < 2; ++q)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-            acc[q][r] = p.h0 ? p.h0[bh * (kFP * kFN) + (32 * tp + bwd_row(r, hf)) * kFN + 32 * (tn0 + q) + i32] : 0.f;
+    for (int r = 0; r < 16; ++r)
+        acc[r] = p.h0 ? p.h0[bh * (kFP * kFN) + (32 * tp + bwd_row(r, hf)) * kFN + 32 * tn + i32] : 0.f;
     // loads of one chunk: v rows (tid >> 4) and + 16; B rows (tid >> 5) + 8 q
-    const int ix = tid >> 4, cx = (tid & 15) * 4, ib = tid >> 5, cb = (tid & 31) * 4;
-    float4 fv[2], fb[4];
+    const int ix = tid >> 4, cx = (tid & 15) * 4, ib = tid >> 4, cb = 64 * ns + (tid & 15) * 4;
+    float4 fv[2], fb[2];
     float fda, fsc;
     auto fetch = [&](int c) {
         const int t0 = c * p.QS;
@@ -675,8 +675,8 @@ __global__ __launch_bounds__(256, 3) void ssd3_bwd_states_mfma(Ssd3BwdParams p) 
             fv[q] = t < p.L ? v : z;
         }
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int j = ib + 8 * q, t = t0 + (j >> lg);
+        for (int q = 0; q < 2; ++q) {
+            const int j = ib + 16 * q, t = t0 + (j >> lg);
             const float4 v = *reinterpret_cast<const float4*>(Bb + (int64_t)min(t, p.L - 1) * p.B_sl +
                                                               (int64_t)(j & mk) * p.B_sm + cb);
             fb[q] = t < p.L ? v : z;
@@ -692,7 +692,7 @@ __global__ __launch_bounds__(256, 3) void ssd3_bwd_states_mfma(Ssd3BwdParams p) 
 #pragma unroll
         for (int q = 0; q < 2; ++q) bwd_put4(&S.v[(ix + 16 * q) * kSX + cx], fv[q]);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) bwd_put4(&S.B[(ib + 8 * q) * kSB + cb], fb[q]);
+        for (int q = 0; q < 2; ++q) bwd_put4(&S.B[(ib + 16 * q) * kSB + cb], fb[q]);
         if (wv == 0) {
             const bool first = (lane & mk) == 0;
             const float cs = wave_incl_scan(lane < 32 && first ? fda : 0.f);
@@ -709,20 +709,16 @@ __global__ __launch_bounds__(256, 3) void ssd3_bwd_states_mfma(Ssd3BwdParams p) 
         float* dst = p.hs + (bh * p.nch + c) * (kFP * kFN) + (32 * tp) * kFN + i32;
         const float dec = S.dec;
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                dst[bwd_row(r, hf) * kFN + 32 * (tn0 + q)] = acc[q][r];
-                acc[q][r] *= dec;
-            }
+        for (int r = 0; r < 16; ++r) {
+            dst[bwd_row(r, hf) * kFN + 32 * tn] = acc[r];
+            acc[r] *= dec;
         }
         const float* Ap = S.v + hf * kSX + 32 * tp + i32;
-        const float* Bp = S.B + hf * kSB + 32 * tn0 + i32;
+        const float* Bp = S.B + hf * kSB + 32 * tn + i32;
 #pragma unroll
         for (int k0 = 0; k0 < 32; k0 += 2) {
             const float a = S.w[k0 + hf] * Ap[k0 * kSX];
-            acc[0] = bwd_mfma(a, Bp[k0 * kSB], acc[0]);
-            acc[1] = bwd_mfma(a, Bp[k0 * kSB + 32], acc[1]);
+            acc = bwd_mfma(a, Bp[k0 * kSB], acc);
         }
         __syncthreads();
         commit();
@@ -811,7 +807,7 @@ static int ssd3_bwd_run(const mamba_ssd3_bwd_args* a, void* workspace, size_t wo
     hipStream_t s = (hipStream_t)stream;
     const dim3 grid(a->batch * a->nheads);
     if (b3_mfma_ok(a)) {
-        hipLaunchKernelGGL(ssd3_bwd_states_mfma, grid, dim3(256), 0, s, p);
+        hipLaunchKernelGGL(ssd3_bwd_states_mfma, dim3(2 * grid.x), dim3(256), 0, s, p);
         MAMBA_CHECK_LAUNCH();
         if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, s));
         hipLaunchKernelGGL(ssd3_bwd_chunks_mfma, grid, dim3(512), 0, s, p);
