@@ -56,6 +56,8 @@ struct Ssd3BwdParams {
     float* dBh; float* dCh;                               // [b, l, m, h, n] per head
     float* dh0;
     float* hs;                                            // [b, h, nch, P, N] chunk-entry states
+    float* dvp;                                           // [2][b, l, m, h, p] partial dv (half-dstate kernel)
+    float* sp;                                            // [3][2][b, l, h] partial dda, dscale, dgamma
 };
 
 // Per-step scalars of chunk c for threads 0..QS-1: da, gamma, scale (0 past the end).
@@ -319,81 +321,83 @@ __global__ __launch_bounds__(256) void ssd3_bwd_finish(Ssd3BwdParams p, float* d
 
 // ---------------------------------------------------------------------------
 // MFMA path for headdim 64 x dstate 128 (the config-4 head shape): the Mamba-2
-// backward's f32 MFMA structure (bwd_core.h) on 32 fused rows per chunk.  The
-// per-step scalars are expanded over the step's M rows in LDS.
-
-// One chunk's fused rows and per-step scalars in registers.
-struct B3Rows {
-    float4 v, dy, B0, B1, C0, C1;
-    float da, gm, sc;
-};
-
-struct B3FastLds {
-    float g[kFP * kSB];      // [p][n] gradient of the state leaving the chunk
-    float v[32 * kSX];       // [j][p] fused rows
-    float dy[32 * kSX];      // [j][p]
-    float B[32 * kSB];       // [j][n]
-    float C[32 * kSB];       // [j][n]
-    float E1[32 * kSQ];      // [k][i] C_k . B_i, then W[k][i] C_k . B_i
-    float DX[32 * kSQ];      // [k][i] dy_k . v_i
-    float E2[32 * kSQ];      // [k][i] W[k][i] dy_k . v_i
-    float E3T[32 * kSQ];     // [i][k] W[k][i] dy_k . v_i
-    float cs[32], av[32], bv[32], sc[32], gm[32];   // per fused row (its step's values)
-    float xu[2][32];         // v_j . g B_j, per 32-row half of p
-    float qh[4][32];         // C_k . h_c^T dy_k, per quarter of n
-    float ghc[4];            // <g, h_c>, per quarter of n
-    float cpart[8][32];      // per-wave column sums of e (C_k.B_i)(dy_k.v_i) over later steps
-    float rrow[32], rdg[32]; // row sums: M over earlier steps, (C_k.B_i)(dy_k.v_i) over the same step
-};
+// backward's f32 MFMA structure (bwd_core.h) on 32 fused rows per chunk, split
+// over the two halves of dstate.  The per-step scalars are expanded over the
+// step's M rows in LDS.
 
 __device__ __forceinline__ int b3_lg(int M) { return 31 - __builtin_clz(M); }
 
-// Loads chunk c's fused rows (row j = step t0 + j / M, rank j % M) of v, dy, B,
-// C, and lane (tid & 31)'s step scalars; rows past the end read as zero.
-__device__ __forceinline__ void b3m_fetch(const Ssd3BwdParams& p, const float* vb, const float* yb, const float* Bb,
-                                          const float* Cb, int b, int h, int c, int tid, int lg, B3Rows& f) {
+// The reverse chunk loop over one half of dstate: two 512-thread workgroups
+// per (batch, head), 69 KB of LDS each (every CU is busy at config 4's 128
+// heads x batch rows).  The state columns split exactly: g, h_c, dB, dC and
+// d(initial state) of a half are the half's own.  Sums over dstate (C.B,
+// g B_j, C.h_c^T dy, <g, h_c>) are partial, and every gradient linear in them
+// (dv, dda, dscale, dgamma) is written as one partial plane per half, summed
+// in a fixed order by ssd3_bwd_half_finish.  Eight waves, 32 MFMAs each in
+// phase 1 (waves w and w + 4 share a SIMD):
+//   phase 1  w0, w1: g B_j (one 32-row half of p each, K = the half's 64 columns)
+//            w2, w3: g^T v_j; w6, w7: h_c^T dy_j (one 32-column quarter each,
+//            h_c's columns in registers); w4: C.B over the half; w5: dy.v
+//   phase 2  w0, w1: dv; w2, w3: dB; w6, w7: dC; w4, w5: the update of g (two
+//            tiles each); w3: the per-step scalars.
+struct B3HalfLds {
+    float g[kFP * kSX];      // [p][n] this half's columns of the state gradient
+    float v[32 * kSX];       // [j][p]
+    float dy[32 * kSX];      // [j][p]
+    float B[32 * kSX];       // [j][n] this half's columns
+    float C[32 * kSX];       // [j][n]
+    float E1[32 * kSQ];      // [k][i] C_k . B_i over the half, then W o that
+    float DX[32 * kSQ];      // [k][i] dy_k . v_i
+    float E2[32 * kSQ];      // [k][i] W[k][i] dy_k . v_i
+    float E3T[32 * kSQ];     // [i][k] W[k][i] dy_k . v_i
+    float cs[32], av[32], bv[32], sc[32], gm[32];
+    float xu[2][32];         // v_j . g B_j (this half of dstate), per 32-row half of p
+    float qh[2][32];         // C_k . h_c^T dy_k, per 32-column quarter
+    float ghc[2];
+    float cpart[8][32];      // per-wave column sums of e (C.B)(dy.v) over later steps
+    float rrow[32], rdg[32];
+};
+
+// One chunk's fused rows (v, dy full; B, C this half) and step scalars.
+struct B3HalfRows {
+    float4 v, dy, B, C;
+    float da, gm, sc;
+};
+
+__device__ __forceinline__ void b3h_fetch(const Ssd3BwdParams& p, const float* vb, const float* yb, const float* Bb,
+                                          const float* Cb, int b, int h, int c, int tid, int lg, int ns,
+                                          B3HalfRows& f) {
     const int t0 = c * p.QS, mk = p.M - 1;
-    const int ix = tid >> 4, cx = (tid & 15) * 4;
-    const int ib = tid >> 5, cb = (tid & 31) * 4, ib2 = ib + 16;
+    const int j = tid >> 4, cx = (tid & 15) * 4;  // row j, a float4 of 64 columns
     const float4 z = {0.f, 0.f, 0.f, 0.f};
-    const int tx = t0 + (ix >> lg), tb0 = t0 + (ib >> lg), tb1 = t0 + (ib2 >> lg);
-    const int64_t ox = (int64_t)min(tx, p.L - 1), o0 = (int64_t)min(tb0, p.L - 1), o1 = (int64_t)min(tb1, p.L - 1);
-    const float4 vv = *reinterpret_cast<const float4*>(vb + ox * p.v_sl + (int64_t)(ix & mk) * p.v_sm + cx);
-    const float4 vy = *reinterpret_cast<const float4*>(yb + ox * p.dy_sl + (int64_t)(ix & mk) * p.dy_sm + cx);
-    const float4 vb0 = *reinterpret_cast<const float4*>(Bb + o0 * p.B_sl + (int64_t)(ib & mk) * p.B_sm + cb);
-    const float4 vb1 = *reinterpret_cast<const float4*>(Bb + o1 * p.B_sl + (int64_t)(ib2 & mk) * p.B_sm + cb);
-    const float4 vc0 = *reinterpret_cast<const float4*>(Cb + o0 * p.C_sl + (int64_t)(ib & mk) * p.C_sm + cb);
-    const float4 vc1 = *reinterpret_cast<const float4*>(Cb + o1 * p.C_sl + (int64_t)(ib2 & mk) * p.C_sm + cb);
+    const int t = t0 + (j >> lg), m = j & mk;
+    const int64_t ot = (int64_t)min(t, p.L - 1);
+    const float4 a = *reinterpret_cast<const float4*>(vb + ot * p.v_sl + (int64_t)m * p.v_sm + cx);
+    const float4 y = *reinterpret_cast<const float4*>(yb + ot * p.dy_sl + (int64_t)m * p.dy_sm + cx);
+    const float4 bb = *reinterpret_cast<const float4*>(Bb + ot * p.B_sl + (int64_t)m * p.B_sm + 64 * ns + cx);
+    const float4 cc = *reinterpret_cast<const float4*>(Cb + ot * p.C_sl + (int64_t)m * p.C_sm + 64 * ns + cx);
     const int tt = t0 + ((tid & 31) >> lg);
-    const int64_t ot = (int64_t)min(tt, p.L - 1);
-    const float da = p.da[(int64_t)b * p.da_sb + ot * p.da_sl + (int64_t)h * p.da_sh];
-    const float gm = p.gam ? p.gam[(int64_t)b * p.gam_sb + ot * p.gam_sl + (int64_t)h * p.gam_sh] : 1.f;
-    const float sc = p.scl ? p.scl[(int64_t)b * p.scl_sb + ot * p.scl_sl + (int64_t)h * p.scl_sh] : 1.f;
-    f.v = tx < p.L ? vv : z;
-    f.dy = tx < p.L ? vy : z;
-    f.B0 = tb0 < p.L ? vb0 : z;
-    f.B1 = tb1 < p.L ? vb1 : z;
-    f.C0 = tb0 < p.L ? vc0 : z;
-    f.C1 = tb1 < p.L ? vc1 : z;
+    const int64_t os = (int64_t)min(tt, p.L - 1);
+    const float da = p.da[(int64_t)b * p.da_sb + os * p.da_sl + (int64_t)h * p.da_sh];
+    const float gm = p.gam ? p.gam[(int64_t)b * p.gam_sb + os * p.gam_sl + (int64_t)h * p.gam_sh] : 1.f;
+    const float sc = p.scl ? p.scl[(int64_t)b * p.scl_sb + os * p.scl_sl + (int64_t)h * p.scl_sh] : 1.f;
+    f.v = t < p.L ? a : z;
+    f.dy = t < p.L ? y : z;
+    f.B = t < p.L ? bb : z;
+    f.C = t < p.L ? cc : z;
     f.da = tt < p.L ? da : 0.f;
     f.gm = tt < p.L ? gm : 0.f;
     f.sc = tt < p.L ? sc : 0.f;
 }
 
-// Writes fetched rows to LDS; wave 0 forms each fused row's cs (the inclusive
-// sum of da over the chunk's steps), a, b, scale and gamma.
-__device__ __forceinline__ void b3m_commit(B3FastLds& S, const B3Rows& f, int tid, int lg) {
-    const int ix = tid >> 4, cx = (tid & 15) * 4;
-    const int ib = tid >> 5, cb = (tid & 31) * 4;
-    bwd_put4(&S.v[ix * kSX + cx], f.v);
-    bwd_put4(&S.dy[ix * kSX + cx], f.dy);
-    bwd_put4(&S.B[ib * kSB + cb], f.B0);
-    bwd_put4(&S.B[(ib + 16) * kSB + cb], f.B1);
-    bwd_put4(&S.C[ib * kSB + cb], f.C0);
-    bwd_put4(&S.C[(ib + 16) * kSB + cb], f.C1);
+__device__ __forceinline__ void b3h_commit(B3HalfLds& S, const B3HalfRows& f, int tid, int lg) {
+    const int o = (tid >> 4) * kSX + (tid & 15) * 4;
+    bwd_put4(&S.v[o], f.v);
+    bwd_put4(&S.dy[o], f.dy);
+    bwd_put4(&S.B[o], f.B);
+    bwd_put4(&S.C[o], f.C);
     if (tid < 64) {
         const int lane = tid;
-        // the first row of each step carries its da, so the scan gives every row its step's cs
         const bool first = (lane & ((1 << lg) - 1)) == 0;
         const float cs = wave_incl_scan(lane < 32 && first ? f.da : 0.f);
         const float tot = __shfl(cs, 31, 64);
@@ -407,106 +411,101 @@ __device__ __forceinline__ void b3m_commit(B3FastLds& S, const B3Rows& f, int ti
     }
 }
 
-// The reverse chunk loop on MFMA: one 512-thread workgroup per (batch, head),
-// eight waves with the roles of the Mamba-2 kernel (ssd2_bwd.hip), on fused rows:
-//   phase 1  waves 0-1: u = g B_j; waves 2-5: g^T v_j, h_c^T dy_j; wave 6: C.B; wave 7: dy.v
-//   then W o (C.B), W o (dy.v), their transposes, and the row / column sums of
-//   M and of the same-step products on every thread;
-//   phase 2  waves 0-1: dv; waves 2-5: dB, dC; waves 0, 1, 6, 7: the update of g;
-//            wave 7: the per-step scalars (dda, dscale, dgamma).
-__global__ __launch_bounds__(512, 1) void ssd3_bwd_chunks_mfma(Ssd3BwdParams p) {
-    __shared__ B3FastLds S;
+__global__ __launch_bounds__(512, 1) void ssd3_bwd_chunks_half(Ssd3BwdParams p) {
+    __shared__ B3HalfLds S;
     const int tid = threadIdx.x, wv = wave_id(), lane = tid & 63, i32 = lane & 31, hf = lane >> 5;
-    const int b = blockIdx.x / p.H, h = blockIdx.x % p.H, grp = h / (p.H / p.G);
+    const int ns = blockIdx.x & 1;
+    const int b = (blockIdx.x >> 1) / p.H, h = (blockIdx.x >> 1) % p.H, grp = h / (p.H / p.G);
     const int lg = b3_lg(p.M), QS = p.QS;
     const int64_t bh = (int64_t)b * p.H + h;
     const float* vb = p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh;
     const float* yb = p.dy + (int64_t)b * p.dy_sb + (int64_t)h * p.dy_sh;
     const float* Bb = p.B + (int64_t)b * p.B_sb + (int64_t)grp * p.B_sg;
     const float* Cb = p.C + (int64_t)b * p.C_sb + (int64_t)grp * p.C_sg;
-    const int tq = wv - 2;  // n quarter of waves 2-5
-    // h_c columns of waves 2-5: hreg[m] = h_c[2 m + hf][32 tq + i32]; reloaded
-    // with the next chunk's as soon as the current chunk's last use is done
+    const int64_t nbl = (int64_t)p.nb * p.L;
+    const int tq = wv & 1;  // 32-column quarter of waves 2, 3, 6, 7 within the half
+    // h_c columns of waves 6-7: hreg[m] = h_c[2 m + hf][64 ns + 32 tq + i32]
     float hreg[32];
     auto fetch_h = [&](int c, float (&dst)[32]) {
-        const float* src = p.hs + (bh * p.nch + c) * (kFP * kFN) + hf * kFN + 32 * tq + i32;
+        const float* src = p.hs + (bh * p.nch + c) * (kFP * kFN) + hf * kFN + 64 * ns + 32 * tq + i32;
 #pragma unroll
         for (int m = 0; m < 32; ++m) dst[m] = src[m * 2 * kFN];
     };
-    for (int e = tid; e < kFP * kFN; e += 512) S.g[(e >> 7) * kSB + (e & 127)] = p.dfin ? p.dfin[bh * (kFP * kFN) + e] : 0.f;
-    B3Rows pre;
-    b3m_fetch(p, vb, yb, Bb, Cb, b, h, p.nch - 1, tid, lg, pre);
-    if (wv >= 2 && wv < 6) fetch_h(p.nch - 1, hreg);
-    b3m_commit(S, pre, tid, lg);
+    for (int e = tid; e < kFP * 64; e += 512)
+        S.g[(e >> 6) * kSX + (e & 63)] = p.dfin ? p.dfin[bh * (kFP * kFN) + (e >> 6) * kFN + 64 * ns + (e & 63)] : 0.f;
+    B3HalfRows pre;
+    b3h_fetch(p, vb, yb, Bb, Cb, b, h, p.nch - 1, tid, lg, ns, pre);
+    if (wv >= 6) fetch_h(p.nch - 1, hreg);
+    b3h_commit(S, pre, tid, lg);
     __syncthreads();
     for (int c = p.nch - 1; c >= 0; --c) {
         const int t0 = c * QS;
-        const int cn = c > 0 ? c - 1 : 0;  // the next chunk (reloads chunk 0 at the end; unused)
-        // per-chunk opaque copy of the thread index (keeps the LDS addresses in the loop)
-        int tid = threadIdx.x;
+        const int cn = c > 0 ? c - 1 : 0;
+        int tid = threadIdx.x;  // opaque per chunk: keeps the LDS addresses in the loop
         asm volatile("" : "+v"(tid));
         const int lane = tid & 63, i32 = lane & 31, hf = lane >> 5;
-        b3m_fetch(p, vb, yb, Bb, Cb, b, h, cn, tid, lg, pre);
-        // ---- phase 1
-        bwd_f32x16 acc0 = {}, acc1 = {};
-        if (wv < 2) {
-            const float* Ap = S.B + i32 * kSB + hf;
-            const float* Bp = S.g + (32 * wv + i32) * kSB + hf;
+        b3h_fetch(p, vb, yb, Bb, Cb, b, h, cn, tid, lg, ns, pre);
+        // ---- phase 1: 32 MFMAs on every wave
+        bwd_f32x16 acc = {};
+        if (wv < 2) {  // u = g B_j for p rows 32 wv .., K = the half's 64 columns
+            const float* Ap = S.B + i32 * kSX + hf;
+            const float* Bp = S.g + (32 * wv + i32) * kSX + hf;
 #pragma unroll 16
-            for (int n0 = 0; n0 < kFN; n0 += 2) acc0 = bwd_mfma(Ap[n0], Bp[n0], acc0);
-        } else if (wv < 6) {
+            for (int n0 = 0; n0 < 64; n0 += 2) acc = bwd_mfma(Ap[n0], Bp[n0], acc);
+        } else if (wv < 4) {  // g^T v_j for this quarter, K = p
             const float* Ax = S.v + i32 * kSX + hf;
+            const float* Bg = S.g + hf * kSX + 32 * tq + i32;
+#pragma unroll 16
+            for (int p0 = 0; p0 < kFP; p0 += 2) acc = bwd_mfma(Ax[p0], Bg[p0 * kSX], acc);
+        } else if (wv == 4) {  // C.B over the half
+            const float* Ac = S.C + i32 * kSX + hf;
+            const float* Bbp = S.B + i32 * kSX + hf;
+#pragma unroll 16
+            for (int k0 = 0; k0 < 64; k0 += 2) acc = bwd_mfma(Ac[k0], Bbp[k0], acc);
+        } else if (wv == 5) {  // dy.v
             const float* Ay = S.dy + i32 * kSX + hf;
-            const float* Bg = S.g + hf * kSB + 32 * tq + i32;
+            const float* Bv = S.v + i32 * kSX + hf;
+#pragma unroll 16
+            for (int k0 = 0; k0 < 64; k0 += 2) acc = bwd_mfma(Ay[k0], Bv[k0], acc);
+        } else {  // h_c^T dy_j for this quarter, h_c from registers
+            const float* Ay = S.dy + i32 * kSX + hf;
 #pragma unroll
             for (int m = 0; m < 32; ++m) {
-                acc0 = bwd_mfma(Ax[2 * m], Bg[2 * m * kSB], acc0);
-                acc1 = bwd_mfma(Ay[2 * m], hreg[m], acc1);
-                if ((m & 7) == 7) __builtin_amdgcn_sched_barrier(0);  // bounds the operand prefetch
+                acc = bwd_mfma(Ay[2 * m], hreg[m], acc);
+                if ((m & 7) == 7) __builtin_amdgcn_sched_barrier(0);
             }
-        } else if (wv == 6) {
-            const float* Ap = S.C + i32 * kSB + hf;
-            const float* Bp = S.B + i32 * kSB + hf;
-#pragma unroll 16
-            for (int n0 = 0; n0 < kFN; n0 += 2) acc0 = bwd_mfma(Ap[n0], Bp[n0], acc0);
-        } else {
-            const float* Ap = S.dy + i32 * kSX + hf;
-            const float* Bp = S.v + i32 * kSX + hf;
-#pragma unroll 16
-            for (int p0 = 0; p0 < kFP; p0 += 2) acc0 = bwd_mfma(Ap[p0], Bp[p0], acc0);
         }
-        // ---- per-wave reductions of the phase-1 products
+        // ---- per-wave reductions
         {
             float w[16];
             if (wv < 2) {  // v_j . g B_j over this half of p
 #pragma unroll
-                for (int r = 0; r < 16; ++r) w[r] = acc0[r] * S.v[bwd_row(r, hf) * kSX + 32 * wv + i32];
+                for (int r = 0; r < 16; ++r) w[r] = acc[r] * S.v[bwd_row(r, hf) * kSX + 32 * wv + i32];
                 const float s = bwd_half_sum16(w, i32);
                 if ((i32 & 1) == 0) S.xu[wv][bwd_row(i32 >> 1, hf)] = s;
-            } else if (wv < 6) {  // C_k . h_c^T dy_k over this quarter of n; <g, h_c>
+            } else if (wv >= 6) {  // C_k . h_c^T dy_k over this quarter; <g, h_c>
 #pragma unroll
-                for (int r = 0; r < 16; ++r) w[r] = acc1[r] * S.C[bwd_row(r, hf) * kSB + 32 * tq + i32];
+                for (int r = 0; r < 16; ++r) w[r] = acc[r] * S.C[bwd_row(r, hf) * kSX + 32 * tq + i32];
                 const float s = bwd_half_sum16(w, i32);
                 if ((i32 & 1) == 0) S.qh[tq][bwd_row(i32 >> 1, hf)] = s;
                 float gh = 0.f;
 #pragma unroll
-                for (int m = 0; m < 32; ++m) gh += hreg[m] * S.g[(2 * m + hf) * kSB + 32 * tq + i32];
+                for (int m = 0; m < 32; ++m) gh += hreg[m] * S.g[(2 * m + hf) * kSX + 32 * tq + i32];
                 gh = wave_sum(gh);
                 if (lane == 0) S.ghc[tq] = gh;
                 fetch_h(cn, hreg);
-            } else {
-                float* dst = wv == 6 ? S.E1 : S.DX;
+            } else if (wv >= 4) {
+                float* dst = wv == 4 ? S.E1 : S.DX;
 #pragma unroll
-                for (int r = 0; r < 16; ++r) dst[bwd_row(r, hf) * kSQ + i32] = acc0[r];
+                for (int r = 0; r < 16; ++r) dst[bwd_row(r, hf) * kSQ + i32] = acc[r];
             }
         }
         __syncthreads();
-        // ---- the weighted fused Q x Q matrices; row sums of M and of the
-        // same-step products, column sums of e (C.B)(dy.v) over later steps
+        // ---- weighted fused Q x Q matrices: wave w takes rows 4 w .. 4 w + 3
         {
             const int i = i32, k0 = 4 * wv + 2 * hf, ti = i >> lg;
             const float cs_i = S.cs[i], sc_i = S.sc[i];
-            float rsum[4], xgc = 0.f;
+            float rs[4], xgc = 0.f;
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
                 const int k = k0 + q, tk = k >> lg;
@@ -518,61 +517,73 @@ __global__ __launch_bounds__(512, 1) void ssd3_bwd_chunks_mfma(Ssd3BwdParams p) 
                 S.E1[k * kSQ + i] = W * cb;
                 S.E2[k * kSQ + i] = W * dx;
                 S.E3T[i * kSQ + k] = W * dx;
-                rsum[q] = lower ? W * dx * cb : 0.f;
-                rsum[2 + q] = same ? cb * dx : 0.f;
+                rs[q] = lower ? W * dx * cb : 0.f;
+                rs[2 + q] = same ? cb * dx : 0.f;
                 xgc += e * cb * dx;
             }
 #pragma unroll
-            for (int q = 0; q < 4; ++q) rsum[q] = bwd_half_sum(rsum[q]);
+            for (int q = 0; q < 4; ++q) rs[q] = bwd_half_sum(rs[q]);
             if (i32 < 2) {
-                S.rrow[k0 + i32] = rsum[i32];
-                S.rdg[k0 + i32] = rsum[2 + i32];
+                S.rrow[k0 + i32] = rs[i32];
+                S.rdg[k0 + i32] = rs[2 + i32];
             }
             xgc += __shfl_xor(xgc, 32, 64);
             if (hf == 0) S.cpart[wv][i] = xgc;
         }
         __syncthreads();
         // ---- phase 2
-        if (wv < 2) {
+        if (wv < 2) {  // dv (this half's share), p rows 32 wv ..
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc0[r] *= S.sc[bwd_row(r, hf)] * S.av[bwd_row(r, hf)];
+            for (int r = 0; r < 16; ++r) acc[r] *= S.sc[bwd_row(r, hf)] * S.av[bwd_row(r, hf)];
             const float* Ap = S.E1 + hf * kSQ + i32;
             const float* Bp = S.dy + hf * kSX + 32 * wv + i32;
 #pragma unroll
-            for (int k0 = 0; k0 < 32; k0 += 2) acc0 = bwd_mfma(Ap[k0 * kSQ], Bp[k0 * kSX], acc0);
+            for (int k0 = 0; k0 < 32; k0 += 2) acc = bwd_mfma(Ap[k0 * kSQ], Bp[k0 * kSX], acc);
+            float* dvp = p.dvp + (int64_t)ns * nbl * p.M * p.H * kFP;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int j = bwd_row(r, hf), t = t0 + (j >> lg);
                 if (t < p.L)
-                    p.dv[((((int64_t)b * p.L + t) * p.M + (j & (p.M - 1))) * p.H + h) * kFP + 32 * wv + i32] = acc0[r];
+                    dvp[((((int64_t)b * p.L + t) * p.M + (j & (p.M - 1))) * p.H + h) * kFP + 32 * wv + i32] = acc[r];
             }
-        } else if (wv < 6) {
+        } else if (wv < 4 || wv >= 6) {  // dB (waves 2, 3) or dC (waves 6, 7) for this quarter
+            const bool isB = wv < 4;
+            const float* Ap = (isB ? S.E2 : S.E3T) + hf * kSQ + i32;
+            const float* Bp = (isB ? S.C : S.B) + hf * kSX + 32 * tq + i32;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int j = bwd_row(r, hf);
-                acc0[r] *= S.sc[j] * S.av[j];
-                acc1[r] *= S.bv[j];
+                acc[r] *= isB ? S.sc[j] * S.av[j] : S.bv[j];
             }
-            const float* A2 = S.E2 + hf * kSQ + i32;
-            const float* A3 = S.E3T + hf * kSQ + i32;
-            const float* Bc = S.C + hf * kSB + 32 * tq + i32;
-            const float* Bbp = S.B + hf * kSB + 32 * tq + i32;
 #pragma unroll
-            for (int k0 = 0; k0 < 32; k0 += 2) {
-                acc0 = bwd_mfma(A2[k0 * kSQ], Bc[k0 * kSB], acc0);
-                acc1 = bwd_mfma(A3[k0 * kSQ], Bbp[k0 * kSB], acc1);
-            }
+            for (int k0 = 0; k0 < 32; k0 += 2) acc = bwd_mfma(Ap[k0 * kSQ], Bp[k0 * kSX], acc);
+            float* dst = isB ? p.dBh : p.dCh;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int j = bwd_row(r, hf), t = t0 + (j >> lg);
-                if (t < p.L) {
-                    const int64_t o = ((((int64_t)b * p.L + t) * p.M + (j & (p.M - 1))) * p.H + h) * kFN + 32 * tq + i32;
-                    p.dBh[o] = acc0[r];
-                    p.dCh[o] = acc1[r];
-                }
+                if (t < p.L)
+                    dst[((((int64_t)b * p.L + t) * p.M + (j & (p.M - 1))) * p.H + h) * kFN + 64 * ns + 32 * tq + i32] =
+                        acc[r];
             }
-        } else if (wv == 7) {
-            // per step t (lanes 0 .. QS-1): the sums over its rows, then dda, dscale, dgamma
+        } else {  // waves 4, 5: two tiles each of this half's g: exp(cs_end) g + sum_k b_k dy_k C_k^T
+            const float dec = __expf(S.cs[31]);
+            const int tp = wv - 4;
+#pragma unroll
+            for (int tn = 0; tn < 2; ++tn) {
+                float* gp = S.g + (32 * tp) * kSX + 32 * tn + i32;
+                bwd_f32x16 a;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) a[r] = dec * gp[bwd_row(r, hf) * kSX];
+                const float* Ap = S.dy + hf * kSX + 32 * tp + i32;
+                const float* Bp = S.C + hf * kSX + 32 * tn + i32;
+#pragma unroll
+                for (int k0 = 0; k0 < 32; k0 += 2) a = bwd_mfma(S.bv[k0 + hf] * Ap[k0 * kSX], Bp[k0 * kSX], a);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) gp[bwd_row(r, hf) * kSX] = a[r];
+            }
+        }
+        if (wv == 3) {
+            // per step t (lanes 0 .. QS-1): this half's share of dda, dscale, dgamma
             const int t = lane;
             const bool live = t < QS;
             const int r0 = live ? t << lg : 0;
@@ -580,7 +591,7 @@ __global__ __launch_bounds__(512, 1) void ssd3_bwd_chunks_mfma(Ssd3BwdParams p) 
             for (int m = 0; m < p.M; ++m) {
                 const int j = r0 + m;
                 xu += S.xu[0][j] + S.xu[1][j];
-                qh += (S.qh[0][j] + S.qh[1][j]) + (S.qh[2][j] + S.qh[3][j]);
+                qh += S.qh[0][j] + S.qh[1][j];
 #pragma unroll
                 for (int w = 0; w < 8; ++w) xg2 += S.cpart[w][j];
                 rowm += S.rrow[j];
@@ -588,7 +599,7 @@ __global__ __launch_bounds__(512, 1) void ssd3_bwd_chunks_mfma(Ssd3BwdParams p) 
             }
             if (!live) xu = qh = xg2 = rowm = dg = 0.f;
             const float cst = S.cs[r0], avt = S.av[r0], bvt = S.bv[r0], sct = live ? S.sc[r0] : 0.f;
-            const float ghc = (S.ghc[0] + S.ghc[1]) + (S.ghc[2] + S.ghc[3]);
+            const float ghc = S.ghc[0] + S.ghc[1];
             const float scxu = sct * xu;
             float s1 = 0.f, s2 = 0.f;
             for (int u = 0; u < QS; ++u) {  // u is wave-uniform: the other step's values by lane read
@@ -603,35 +614,30 @@ __global__ __launch_bounds__(512, 1) void ssd3_bwd_chunks_mfma(Ssd3BwdParams p) 
             const float pr = wave_incl_scan(rowm) - rowm;
             if (live && t0 + t < p.L) {
                 const int64_t o = (int64_t)b * p.L * p.H + (int64_t)(t0 + t) * p.H + h;
-                p.dda[o] = avt * bvt * ghc + avt * s1 + bvt * s2 + (pc - pr);
-                if (p.dscl) p.dscl[o] = avt * xu + xg2;
-                if (p.dgam) p.dgam[o] = dg;
-            }
-        }
-        // the gradient entering this chunk: exp(cs_end) g + sum_k b_k dy_k C_k^T
-        if (wv < 2 || wv >= 6) {
-            const float dec = __expf(S.cs[31]);
-            const int gt0 = wv < 2 ? 2 * wv : 2 * wv - 8;
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-                const int tile = gt0 + tt, tp = tile >> 2, tn = tile & 3;
-                float* gp = S.g + (32 * tp) * kSB + 32 * tn + i32;
-                bwd_f32x16 a;
-#pragma unroll
-                for (int r = 0; r < 16; ++r) a[r] = dec * gp[bwd_row(r, hf) * kSB];
-                const float* Ap = S.dy + hf * kSX + 32 * tp + i32;
-                const float* Bp = S.C + hf * kSB + 32 * tn + i32;
-#pragma unroll
-                for (int k0 = 0; k0 < 32; k0 += 2) a = bwd_mfma(S.bv[k0 + hf] * Ap[k0 * kSX], Bp[k0 * kSB], a);
-#pragma unroll
-                for (int r = 0; r < 16; ++r) gp[bwd_row(r, hf) * kSB] = a[r];
+                const int64_t plane = nbl * p.H;
+                p.sp[(0 * 2 + ns) * plane + o] = avt * bvt * ghc + avt * s1 + bvt * s2 + (pc - pr);
+                p.sp[(1 * 2 + ns) * plane + o] = avt * xu + xg2;
+                p.sp[(2 * 2 + ns) * plane + o] = dg;
             }
         }
         __syncthreads();
-        b3m_commit(S, pre, tid, lg);
+        b3h_commit(S, pre, tid, lg);
         __syncthreads();
     }
-    for (int e = tid; e < kFP * kFN; e += 512) p.dh0[bh * (kFP * kFN) + e] = S.g[(e >> 7) * kSB + (e & 127)];
+    for (int e = tid; e < kFP * 64; e += 512)
+        p.dh0[bh * (kFP * kFN) + (e >> 6) * kFN + 64 * ns + (e & 63)] = S.g[(e >> 6) * kSX + (e & 63)];
+}
+
+// Sums of the half-dstate kernel's two partial planes (half 0 + half 1).
+__global__ __launch_bounds__(256) void ssd3_bwd_half_finish(Ssd3BwdParams p) {
+    const int64_t nv = (int64_t)p.nb * p.L * p.M * p.H * kFP, ns = (int64_t)p.nb * p.L * p.H;
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < nv; e += stride) p.dv[e] = p.dvp[e] + p.dvp[nv + e];
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < ns; e += stride) {
+        p.dda[e] = p.sp[e] + p.sp[ns + e];
+        if (p.dscl) p.dscl[e] = p.sp[2 * ns + e] + p.sp[3 * ns + e];
+        if (p.dgam) p.dgam[e] = p.sp[4 * ns + e] + p.sp[5 * ns + e];
+    }
 }
 
 // Chunk-entry states on MFMA (headdim 64 x dstate 128), as the Mamba-2 one:
@@ -743,7 +749,7 @@ static bool b3_mfma_ok(const mamba_ssd3_bwd_args* a) {
 }
 
 struct B3Layout {
-    size_t hs, dbh, total;
+    size_t hs, dbh, part, total;
 };
 
 static int b3_validate(const mamba_ssd3_bwd_args* a, B3Layout* lay) {
@@ -768,6 +774,10 @@ static int b3_validate(const mamba_ssd3_bwd_args* a, B3Layout* lay) {
     lay->dbh = off;
     if (a->ngroups != a->nheads)
         off += 2 * align_up((size_t)a->batch * a->seqlen * a->mimo * a->nheads * a->dstate * sizeof(float), 256);
+    lay->part = off;
+    if (b3_mfma_ok(a))  // the half-dstate kernel's partial planes
+        off += align_up(2 * (size_t)a->batch * a->seqlen * a->mimo * a->nheads * a->headdim * sizeof(float), 256) +
+               align_up(6 * (size_t)a->batch * a->seqlen * a->nheads * sizeof(float), 256);
     lay->total = off;
     return MAMBA_OK;
 }
@@ -796,6 +806,8 @@ static int ssd3_bwd_run(const mamba_ssd3_bwd_args* a, void* workspace, size_t wo
     p.dv = a->dv; p.dda = a->dda; p.dgam = a->dgamma; p.dscl = a->dscale; p.dh0 = a->d_initial_state;
     char* ws = static_cast<char*>(workspace);
     p.hs = reinterpret_cast<float*>(ws + lay.hs);
+    p.dvp = nullptr;
+    p.sp = nullptr;
     if (a->ngroups == a->nheads) {
         p.dBh = a->dB;
         p.dCh = a->dC;
@@ -807,12 +819,18 @@ static int ssd3_bwd_run(const mamba_ssd3_bwd_args* a, void* workspace, size_t wo
     hipStream_t s = (hipStream_t)stream;
     const dim3 grid(a->batch * a->nheads);
     if (b3_mfma_ok(a)) {
+        p.dvp = reinterpret_cast<float*>(ws + lay.part);
+        p.sp = p.dvp + align_up(2 * (size_t)a->batch * a->seqlen * a->mimo * a->nheads * a->headdim * sizeof(float), 256) /
+                           sizeof(float);
         hipLaunchKernelGGL(ssd3_bwd_states_mfma, dim3(2 * grid.x), dim3(256), 0, s, p);
         MAMBA_CHECK_LAUNCH();
         if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, s));
-        hipLaunchKernelGGL(ssd3_bwd_chunks_mfma, grid, dim3(512), 0, s, p);
+        hipLaunchKernelGGL(ssd3_bwd_chunks_half, dim3(2 * grid.x), dim3(512), 0, s, p);
         MAMBA_CHECK_LAUNCH();
         if (ev1) MAMBA_CHECK_HIP(hipEventRecord(ev1, s));
+        const int64_t nv = (int64_t)a->batch * a->seqlen * a->mimo * a->nheads * a->headdim;
+        hipLaunchKernelGGL(ssd3_bwd_half_finish, dim3((int)std::min<int64_t>((nv + 255) / 256, 8192)), dim3(256), 0, s, p);
+        MAMBA_CHECK_LAUNCH();
     } else {
         MAMBA_CHECK_HIP(hipFuncSetAttribute((const void*)ssd3_bwd_states, hipFuncAttributeMaxDynamicSharedMemorySize,
                                             (int)b3_states_lds(p.P, p.N)));
