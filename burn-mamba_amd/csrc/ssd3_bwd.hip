@@ -411,7 +411,11 @@ __device__ __forceinline__ void b3h_commit(B3HalfLds& S, const B3HalfRows& f, in
     }
 }
 
-__global__ __launch_bounds__(512, 1) void ssd3_bwd_chunks_half(Ssd3BwdParams p) {
+// WPE = 1 gives the kernel 162 registers (one workgroup per CU); WPE = 4 holds
+// it to 128 (a few spills) so that two workgroups share a CU, which pays once
+// the grid has at least two workgroups per CU (21 % at batch 8 of config 4).
+template <int WPE>
+__global__ __launch_bounds__(512, WPE) void ssd3_bwd_chunks_half(Ssd3BwdParams p) {
     __shared__ B3HalfLds S;
     const int tid = threadIdx.x, wv = wave_id(), lane = tid & 63, i32 = lane & 31, hf = lane >> 5;
     const int ns = blockIdx.x & 1;
@@ -825,7 +829,13 @@ static int ssd3_bwd_run(const mamba_ssd3_bwd_args* a, void* workspace, size_t wo
         hipLaunchKernelGGL(ssd3_bwd_states_mfma, dim3(2 * grid.x), dim3(256), 0, s, p);
         MAMBA_CHECK_LAUNCH();
         if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, s));
-        hipLaunchKernelGGL(ssd3_bwd_chunks_half, dim3(2 * grid.x), dim3(512), 0, s, p);
+        int dev = 0, cus = 256;
+        MAMBA_CHECK_HIP(hipGetDevice(&dev));
+        MAMBA_CHECK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        if (2 * (int64_t)grid.x >= 2 * (int64_t)cus)
+            hipLaunchKernelGGL(ssd3_bwd_chunks_half<4>, dim3(2 * grid.x), dim3(512), 0, s, p);
+        else
+            hipLaunchKernelGGL(ssd3_bwd_chunks_half<1>, dim3(2 * grid.x), dim3(512), 0, s, p);
         MAMBA_CHECK_LAUNCH();
         if (ev1) MAMBA_CHECK_HIP(hipEventRecord(ev1, s));
         const int64_t nv = (int64_t)a->batch * a->seqlen * a->mimo * a->nheads * a->headdim;

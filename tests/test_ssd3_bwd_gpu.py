@@ -26,6 +26,7 @@ CASES = [
     (2, 37, 2, 4, 64, 1, 128, True, True, True),    # MIMO 2, one group, ragged
     (1, 40, 1, 2, 64, 1, 128, True, False, True),   # SISO (32 steps per chunk)
     (1, 21, 8, 2, 64, 2, 128, False, True, True),   # MIMO 8, unit weights (the double seam)
+    (8, 20, 4, 32, 64, 32, 128, True, True, True),  # 512 workgroups: the two-per-CU (128-register) build
 ]
 
 
