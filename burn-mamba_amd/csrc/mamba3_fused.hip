@@ -487,7 +487,6 @@ __global__ __launch_bounds__(512, 1) void mamba3_ssd_fused(M3FusedParams p) {
         __syncthreads();  // LDS reads of this chunk done before the next commit
     }
     if (wv < 4) store_y(p.nch - 1, tid_ & 63);
-    if (wv < 4) store_y(p.nch - 1, tid_ & 63);
     if (wv >= 4) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
