@@ -95,6 +95,23 @@ __device__ __forceinline__ float dpp_term(float v, int ctrl, int row_mask) {
         default: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xc, 0xf, false));
     }
 }
+// Sum over aligned groups of G lanes (G a power of two, <= 64) into each
+// group's last lane, on the same DPP moves: after the row shifts by 1 .. G/2
+// lane i holds the sum of lanes i - G + 1 .. i of its row, which for the last
+// lane of a group is the group; groups of 32 and 64 add the row broadcasts.
+// The other lanes hold partial sums.  (A __shfl_xor butterfly gives every
+// lane the sum but costs one LDS permute per step.)
+template <int G>
+__device__ __forceinline__ float group_sum_last(float v) {
+    static_assert(G >= 1 && G <= 64 && (G & (G - 1)) == 0, "group size must be a power of two <= 64");
+    if (G >= 2) v += dpp_term(v, 0x111, 0xf);   // row_shr:1
+    if (G >= 4) v += dpp_term(v, 0x112, 0xf);   // row_shr:2
+    if (G >= 8) v += dpp_term(v, 0x114, 0xf);   // row_shr:4
+    if (G >= 16) v += dpp_term(v, 0x118, 0xf);  // row_shr:8
+    if (G >= 32) v += dpp_term(v, 0x142, 0xa);  // row_bcast:15 into rows 1 and 3
+    if (G >= 64) v += dpp_term(v, 0x143, 0xc);  // row_bcast:31 into rows 2 and 3
+    return v;
+}
 __device__ __forceinline__ float wave_incl_scan(float v) {
     v += dpp_term(v, 0x111, 0xf);  // row_shr:1
     v += dpp_term(v, 0x112, 0xf);  // row_shr:2

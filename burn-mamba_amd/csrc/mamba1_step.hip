@@ -100,12 +100,11 @@ __global__ __launch_bounds__(256) void mamba1_step_kernel(M1StepParams p) {
         hn.y = hv[k].y * __expf(d_ * av[k].y) + (d_ * bb[1]) * u_;
         hn.z = hv[k].z * __expf(d_ * av[k].z) + (d_ * bb[2]) * u_;
         hn.w = hv[k].w * __expf(d_ * av[k].w) + (d_ * bb[3]) * u_;
-        float acc = hn.x * cc[0] + hn.y * cc[1] + hn.z * cc[2] + hn.w * cc[3];
-#pragma unroll
-        for (int o = 1; o < LPC; o <<= 1) acc += __shfl_xor(acc, o, 64);
+        // the channel's sum over its LPC lanes, in the group's last lane
+        const float acc = group_sum_last<LPC>(hn.x * cc[0] + hn.y * cc[1] + hn.z * cc[2] + hn.w * cc[3]);
         if (!live[k]) continue;
         *(reinterpret_cast<float4*>(p.h + ((int64_t)b * p.D + dd[k]) * N) + q) = hn;
-        if (q == 0) {
+        if (q == LPC - 1) {
             float out = acc + (has_D ? Dvv[k] : 0.f) * u_;
             if (has_z) {
                 const float zv = zvv[k];

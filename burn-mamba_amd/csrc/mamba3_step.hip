@@ -214,13 +214,12 @@ __global__ __launch_bounds__(256) void mamba3_step_kernel(M3StepParams p) {
         }
 #pragma unroll
         for (int m = 0; m < MM; ++m) acc[m] = cq[m].x * hn.x + cq[m].y * hn.y + cq[m].z * hn.z + cq[m].w * hn.w;
+        // the row's sum over its N4 lanes, in the row's last lane
 #pragma unroll
-        for (int o = 1; o < N4; o <<= 1)
-#pragma unroll
-            for (int m = 0; m < MM; ++m) acc[m] += __shfl_xor(acc[m], o, 64);
+        for (int m = 0; m < MM; ++m) acc[m] = group_sum_last<N4>(acc[m]);
         if (live) {
             *(reinterpret_cast<float4*>(st + (int64_t)pr * N) + q) = hn;
-            if (q == 0)
+            if (q == N4 - 1)
 #pragma unroll
                 for (int m = 0; m < MM; ++m) s_out[m][pr] = acc[m] + Dv * s_v[m][pr];
         }
