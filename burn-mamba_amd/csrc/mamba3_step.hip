@@ -64,16 +64,22 @@ __global__ __launch_bounds__(256) void mamba3_step_kernel(M3StepParams p) {
 
     __shared__ __align__(16) float s_B[MM][N], s_C[MM][N], s_K[MM][N];
     __shared__ float s_gv[MM][256], s_bx[MM][256], s_v[MM][256], s_out[MM][256];
-    __shared__ float s_cs[128], s_sn[128], s_rms[2 * MM];
+    __shared__ float s_cs[128], s_sn[128], s_rms[2 * MM], s_coef[3];
 
     const void* row = static_cast<const char*>(p.proj) + (int64_t)b * p.proj_sb * (p.proj_bf16 ? 2 : 4);
     const int d_inner = p.H * P, bc = MM * p.G * N;
     const int o_b = 2 * d_inner, o_c = o_b + bc, o_dt = o_c + bc, o_a = o_dt + p.H, o_l = o_a + p.H,
               o_rot = o_l + p.H;
     const int g = h / (p.H / p.G);
+    // B/C rows in rotation pairs, (k, k + N/2) for MIMO > 1 and (2k, 2k + 1)
+    // for MIMO 1 (rotate_bc_step): a row's N/2 pairs over a group of GS lanes
+    // (PPL pairs per lane), RPI rows per pass of the workgroup, JR passes
+    constexpr int NP = N / 2, GS = NP < 64 ? NP : 64, PPL = NP / GS;
+    constexpr int NROW = 2 * MM, RPI = 256 / GS, JR = (NROW + RPI - 1) / RPI;
+    const int gl = t % GS, rsub = t / GS;
     // ---- this row's inputs first, into registers: the prep below waits for
     // them only, while the state tile (issued next) is still in flight
-    constexpr int RBC = (2 * MM * N + 255) / 256, RK = (MM * N + 255) / 256;
+    constexpr int RK = (MM * N + 255) / 256;
     const float raw_dt = m3_proj(p, row, o_dt + h), raw_a = m3_proj(p, row, o_a + h),
                 raw_l = m3_proj(p, row, o_l + h), dtb = p.dt_bias[h];
     float raw_rot = 0.f, ang0 = 0.f;
@@ -81,12 +87,26 @@ __global__ __launch_bounds__(256) void mamba3_step_kernel(M3StepParams p) {
         raw_rot = m3_proj(p, row, o_rot + t);
         ang0 = p.ang[bh * p.A + t];
     }
-    float rbc[RBC], rk[RK];
+    // raw B/C pair values, their norm weights and this head's biases
+    float x0[JR][PPL], x1[JR][PPL], w0[JR][PPL], w1[JR][PPL], c0[JR][PPL], c1[JR][PPL];
 #pragma unroll
-    for (int j = 0; j < RBC; ++j) {
-        const int i = t + 256 * j, which = i / (MM * N), m = (i / N) % MM, n = i % N;
-        rbc[j] = i < 2 * MM * N ? m3_proj(p, row, (which ? o_c : o_b) + (m * p.G + g) * N + n) : 0.f;
+    for (int j = 0; j < JR; ++j) {
+        const int r = rsub + RPI * j;
+        const bool in = r < NROW;
+        const int rr = in ? r : 0, wh = rr / MM, mm = rr % MM;
+        const int src = (wh ? o_c : o_b) + (mm * p.G + g) * N;
+        const float* nw = wh ? p.cnw : p.bnw;
+        const float* bias = (wh ? p.cbias : p.bbias) + ((int64_t)h * MM + mm) * N;
+#pragma unroll
+        for (int e = 0; e < PPL; ++e) {
+            const int k = gl * PPL + e, i0 = MM == 1 ? 2 * k : k, i1 = MM == 1 ? 2 * k + 1 : k + NP;
+            x0[j][e] = in ? m3_proj(p, row, src + i0) : 0.f;
+            x1[j][e] = in ? m3_proj(p, row, src + i1) : 0.f;
+            w0[j][e] = nw[i0]; w1[j][e] = nw[i1];
+            c0[j][e] = bias[i0]; c1[j][e] = bias[i1];
+        }
     }
+    float rk[RK];
 #pragma unroll
     for (int j = 0; j < RK; ++j) {
         const int i = t + 256 * j, m = i / N, n = i % N;
@@ -111,36 +131,92 @@ __global__ __launch_bounds__(256) void mamba3_step_kernel(M3StepParams p) {
         const int pr = min(row0 + k * RPP, P - 1);
         hv[k] = *(reinterpret_cast<const float4*>(st + (int64_t)pr * N) + q);
     }
+    // the gate's inputs, issued after the tile (first used after the update)
+    float zq = 0.f, onq = 0.f, mzq[MM], moq[MM];
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+        mzq[m] = 1.f;
+        moq[m] = 1.f;
+    }
+    if (t < P) {
+        zq = m3_proj(p, row, h * P + t);
+        if (p.onw) onq = p.onw[t];
+        if (MM > 1)
+#pragma unroll
+            for (int m = 0; m < MM; ++m) {
+                mzq[m] = p.mz[((int64_t)h * MM + m) * P + t];
+                moq[m] = p.mo[((int64_t)h * MM + m) * P + t];
+            }
+    }
 
-    // ---- trapezoid coefficients (every thread; three proj values)
-    float dt = m3_softplus(raw_dt + dtb);
-    dt = fminf(fmaxf(dt, p.dt_lo), p.dt_hi);
-    const float a = -fmaxf(m3_softplus(raw_a), p.a_floor);
-    const float lam = 1.f / (1.f + __expf(-raw_l));
-    const float alpha = __expf(dt * a);
-    const float beta = (1.f - lam) * dt * alpha, gamma = lam * dt;
-
-    // ---- cumulative angle of this head, cos/sin of the rotated pairs
-    if (t < p.A) {
-        const float th = m3_wrap(ang0 + dt * (tanhf(raw_rot) * p.span));
-        p.ang[bh * p.A + t] = th;
-        const float tw = m3_wrap(th);
-        if (t < 128) {
-            s_cs[t] = cosf(tw);
-            s_sn[t] = sinf(tw);
+    // ---- trapezoid coefficients and the cumulative angle, on the waves that
+    // hold angles (wave 0 at least); the others read the coefficients from LDS
+    if (wave * 64 < (p.A > 64 ? p.A : 64)) {
+        float dt = m3_softplus(raw_dt + dtb);
+        dt = fminf(fmaxf(dt, p.dt_lo), p.dt_hi);
+        if (t == 0) {
+            const float a = -fmaxf(m3_softplus(raw_a), p.a_floor);
+            const float lam = 1.f / (1.f + __expf(-raw_l));
+            const float alpha = __expf(dt * a);
+            s_coef[0] = alpha;
+            s_coef[1] = (1.f - lam) * dt * alpha;  // beta
+            s_coef[2] = lam * dt;                  // gamma
+        }
+        if (t < p.A) {
+            const float th = m3_wrap(ang0 + dt * (tanhf(raw_rot) * p.span));
+            p.ang[bh * p.A + t] = th;
+            const float tw = m3_wrap(th);
+            if (t < 128) {
+                s_cs[t] = cosf(tw);
+                s_sn[t] = sinf(tw);
+            }
         }
     }
-    // ---- raw B/C of this head's group, the previous token's K, v / xs
-#pragma unroll
-    for (int j = 0; j < RBC; ++j) {
-        const int i = t + 256 * j, which = i / (MM * N), m = (i / N) % MM, n = i % N;
-        if (i < 2 * MM * N) (which ? s_C : s_B)[m][n] = rbc[j];
-    }
+    // ---- the previous token's K; QK-norm of the B/C rows (sum of squares over
+    // the row's lane group), weight and bias, in registers
 #pragma unroll
     for (int j = 0; j < RK; ++j) {
         const int i = t + 256 * j, m = i / N, n = i % N;
         if (i < MM * N) s_K[m][n] = rk[j];
     }
+#pragma unroll
+    for (int j = 0; j < JR; ++j) {
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < PPL; ++e) ss += x0[j][e] * x0[j][e] + x1[j][e] * x1[j][e];
+        ss = group_sum_last<GS>(ss);
+        ss = __shfl(ss, (lane & ~(GS - 1)) + GS - 1, 64);
+        const float rms = 1.f / sqrtf(ss / (float)N + 8.1584695e-8f);
+#pragma unroll
+        for (int e = 0; e < PPL; ++e) {
+            x0[j][e] = (x0[j][e] * rms) * w0[j][e] + c0[j][e];
+            x1[j][e] = (x1[j][e] * rms) * w1[j][e] + c1[j][e];
+        }
+    }
+    __syncthreads();
+    // ---- rotation of the first R/2 pairs by the angle's cos/sin, into LDS
+    const int npair = p.R / 2;
+#pragma unroll
+    for (int j = 0; j < JR; ++j) {
+        const int r = rsub + RPI * j;
+        if (r < NROW) {
+            const int which = r / MM, m = r % MM;
+            float* vv = which ? s_C[m] : s_B[m];
+#pragma unroll
+            for (int e = 0; e < PPL; ++e) {
+                const int k = gl * PPL + e, i0 = MM == 1 ? 2 * k : k, i1 = MM == 1 ? 2 * k + 1 : k + NP;
+                float r0 = x0[j][e], r1 = x1[j][e];
+                if (k < npair) {
+                    const float cs = s_cs[k], sn = s_sn[k];
+                    r0 = cs * x0[j][e] - sn * x1[j][e];
+                    r1 = sn * x0[j][e] + cs * x1[j][e];
+                }
+                vv[i0] = r0;
+                vv[i1] = r1;
+            }
+        }
+    }
+    const float alpha = s_coef[0], beta = s_coef[1], gamma = s_coef[2];
     if (t < P) {
 #pragma unroll
         for (int m = 0; m < MM; ++m) {
@@ -150,40 +226,12 @@ __global__ __launch_bounds__(256) void mamba3_step_kernel(M3StepParams p) {
         }
     }
     __syncthreads();
-    // ---- QK-norm: sum of squares of the 2 MM rows (one wave per row, strided)
-    for (int r = wave; r < 2 * MM; r += 4) {
-        const float* src = (r < MM ? s_B[r] : s_C[r - MM]);
-        float ss = 0.f;
-        for (int n = lane; n < N; n += 64) ss += src[n] * src[n];
-        ss = wave_sum(ss);
-        if (lane == 0) s_rms[r] = 1.f / sqrtf(ss / (float)N + 8.1584695e-8f);
-    }
-    __syncthreads();
-    for (int i = t; i < 2 * MM * N; i += 256) {
-        const int which = i / (MM * N), m = (i / N) % MM, n = i % N;
-        float* dst = which ? &s_C[m][n] : &s_B[m][n];
-        const float w = which ? p.cnw[n] : p.bnw[n];
-        const float bb = (which ? p.cbias : p.bbias)[((int64_t)h * MM + m) * N + n];
-        *dst = (*dst * s_rms[which * MM + m]) * w + bb;
-    }
-    __syncthreads();
-    // ---- rotation: pairs (2a, 2a+1) for M == 1, (a, a + N/2) otherwise, a < R/2
-    const int npair = p.R / 2;
-    for (int i = t; i < 2 * MM * npair; i += 256) {
-        const int which = i / (MM * npair), m = (i / npair) % MM, k = i % npair;
-        const int i0 = MM == 1 ? 2 * k : k, i1 = MM == 1 ? 2 * k + 1 : k + N / 2;
-        float* vv = which ? s_C[m] : s_B[m];
-        const float x0 = vv[i0], x1 = vv[i1];
-        vv[i0] = s_cs[k] * x0 - s_sn[k] * x1;
-        vv[i1] = s_sn[k] * x0 + s_cs[k] * x1;
-    }
-    __syncthreads();
     // ---- new cache entries: K <- rotated B, v_state <- x (old ones are in LDS)
     for (int i = t; i < MM * N; i += 256) {
         const int m = i / N, n = i % N;
         p.kst[(((int64_t)b * MM + m) * p.H + h) * N + n] = s_B[m][n];
     }
-    for (int i = t; i < P; i += 256) p.vst[bh * P + i] = m3_proj(p, row, d_inner + h * P + i);
+    if (t < P) p.vst[bh * P + t] = xv;
 
     // ---- state update and readout, N4 lanes per row
     const int n0 = 4 * q;
@@ -235,14 +283,14 @@ __global__ __launch_bounds__(256) void mamba3_step_kernel(M3StepParams p) {
         }
         __syncthreads();
     }
-    for (int i = t; i < P; i += 256) {
-        const float zv = m3_proj(p, row, h * P + i);
+    if (t < P) {
+        const int i = t;
         float y = 0.f;
 #pragma unroll
         for (int m = 0; m < MM; ++m) {
-            const float zm = MM > 1 ? zv * p.mz[((int64_t)h * MM + m) * P + i] : zv;
-            float gv = p.onw ? (s_out[m][i] * s_rms[m]) * p.onw[i] * m3_silu(zm) : s_out[m][i] * m3_silu(zm);
-            if (MM > 1) gv *= p.mo[((int64_t)h * MM + m) * P + i];
+            const float zm = MM > 1 ? zq * mzq[m] : zq;
+            float gv = p.onw ? (s_out[m][i] * s_rms[m]) * onq * m3_silu(zm) : s_out[m][i] * m3_silu(zm);
+            if (MM > 1) gv *= moq[m];
             y += gv;
         }
         const int64_t oi = (int64_t)b * p.out_sb + h * P + i;

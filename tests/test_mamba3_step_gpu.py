@@ -78,6 +78,9 @@ CASES = [
     (2, 2, 8, 1, 8, 2, 0.5, True),      # partial rotation, gated norm
     (2, 4, 32, 2, 64, 1, 0.0, True),    # rotation off (angle still advances)
     (2, 4, 64, 1, 128, 4, 1.0, False),  # config-4 head shape
+    (2, 4, 64, 2, 128, 1, 1.0, True),   # dstate 128 SISO pairs, two groups, gated norm
+    (3, 4, 64, 1, 128, 2, 0.5, True),   # dstate 128 MIMO 2, partial rotation, gated norm
+    (2, 2, 32, 1, 256, 8, 0.5, False),  # dstate 256: two rotation pairs per lane, MIMO 8
 ]
 
 
