@@ -112,6 +112,11 @@ __device__ __forceinline__ float group_sum_last(float v) {
     if (G >= 64) v += dpp_term(v, 0x143, 0xc);  // row_bcast:31 into rows 2 and 3
     return v;
 }
+// Wave sum as a wave-uniform value: the DPP group sum into lane 63, read
+// back as a scalar.  Every lane of the wave must be active.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(group_sum_last<64>(v)), 63));
+}
 __device__ __forceinline__ float wave_incl_scan(float v) {
     v += dpp_term(v, 0x111, 0xf);  // row_shr:1
     v += dpp_term(v, 0x112, 0xf);  // row_shr:2

@@ -92,7 +92,7 @@ __device__ __forceinline__ float step_dt(const Step2Params& p, const char* zrow,
 
 // Sum over the 256 threads of a workgroup; every thread gets the result.
 __device__ __forceinline__ float block_sum_256(float v, float* s_red) {
-    v = wave_sum(v);
+    v = wave_sum_dpp(v);  // every thread of the workgroup calls this
     const int wave = threadIdx.x >> 6;
     __syncthreads();  // s_red may still be read by a previous call
     if ((threadIdx.x & 63) == 0) s_red[wave] = v;
