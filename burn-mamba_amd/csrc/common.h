@@ -131,6 +131,20 @@ __device__ __forceinline__ float wave_incl_scan(float v) {
 // and loops on it stay scalar, so waits on memory counters remain exact.
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
+// --------------------------------------------------- streamed state tiles ---
+// 16-byte loads and stores with the non-temporal hint, for data touched once
+// per launch (a decode state tile read and written back): it then does not
+// displace the caches' reusable lines (weights, partial planes, activations).
+typedef float nt_f32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ld_nt4(const float4* p) {
+    const nt_f32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const nt_f32x4_t*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void st_nt4(float4* p, float4 h) {
+    const nt_f32x4_t v = {h.x, h.y, h.z, h.w};
+    __builtin_nontemporal_store(v, reinterpret_cast<nt_f32x4_t*>(p));
+}
+
 // ------------------------------------------------------- buffer access ---
 // Raw buffer resources (gfx9 descriptor word 3): loads at or past `bytes` read
 // as zero and stores there are dropped, which clips tiles at a sequence end

@@ -148,11 +148,11 @@ __global__ __launch_bounds__(256) void step2_ssm_fast(Step2Params p) {
     }
     const float dt_raw = zx_at<ZS>(p, zrow, b, p.d_inner + p.conv_dim + h) + (p.dt_bias ? p.dt_bias[h] : 0.f);
 
-    // 2. the state tile: the bytes that matter
+    // 2. the state tile: the bytes that matter (read and written once: non-temporal)
     float4* st = reinterpret_cast<float4*>(p.ssm) + (int64_t)bh * (P * LPR);
     float4 hv[R];
 #pragma unroll
-    for (int i = 0; i < R; ++i) hv[i] = st[(row0 + i * RPI) * LPR + n4];
+    for (int i = 0; i < R; ++i) hv[i] = ld_nt4(&st[(row0 + i * RPI) * LPR + n4]);
 
     // 3. causal conv, one channel per thread (mamba2.rs:865-902)
 #pragma unroll
@@ -197,7 +197,7 @@ __global__ __launch_bounds__(256) void step2_ssm_fast(Step2Params p) {
         hn.y = hv[i].y * dA + dB.y * xv;
         hn.z = hv[i].z * dA + dB.z * xv;
         hn.w = hv[i].w * dA + dB.w * xv;
-        st[(row0 + i * RPI) * LPR + n4] = hn;
+        st_nt4(&st[(row0 + i * RPI) * LPR + n4], hn);
         v[i] = hn.x * C4.x + hn.y * C4.y + hn.z * C4.z + hn.w * C4.w;
     }
 
