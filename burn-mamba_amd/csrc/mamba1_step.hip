@@ -65,7 +65,7 @@ __global__ __launch_bounds__(256) void mamba1_step_kernel(M1StepParams p) {
         const int d_raw = dbase + k * CPB;
         live[k] = d_raw < p.D;
         dd[k] = live[k] ? d_raw : p.D - 1;
-        hv[k] = *(reinterpret_cast<const float4*>(p.h + ((int64_t)b * p.D + dd[k]) * N) + q);
+        hv[k] = ld_nt4(reinterpret_cast<const float4*>(p.h + ((int64_t)b * p.D + dd[k]) * N) + q);
         if (a_vec) {
             av[k] = *reinterpret_cast<const float4*>(p.A + (int64_t)dd[k] * p.A_sd + n0);
         } else {
@@ -103,7 +103,7 @@ __global__ __launch_bounds__(256) void mamba1_step_kernel(M1StepParams p) {
         // the channel's sum over its LPC lanes, in the group's last lane
         const float acc = group_sum_last<LPC>(hn.x * cc[0] + hn.y * cc[1] + hn.z * cc[2] + hn.w * cc[3]);
         if (!live[k]) continue;
-        *(reinterpret_cast<float4*>(p.h + ((int64_t)b * p.D + dd[k]) * N) + q) = hn;
+        st_nt4(reinterpret_cast<float4*>(p.h + ((int64_t)b * p.D + dd[k]) * N) + q, hn);
         if (q == LPC - 1) {
             float out = acc + (has_D ? Dvv[k] : 0.f) * u_;
             if (has_z) {

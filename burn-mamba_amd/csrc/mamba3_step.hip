@@ -129,7 +129,7 @@ __global__ __launch_bounds__(256) void mamba3_step_kernel(M3StepParams p) {
 #pragma unroll
     for (int k = 0; k < MAXPASS; ++k) {
         const int pr = min(row0 + k * RPP, P - 1);
-        hv[k] = *(reinterpret_cast<const float4*>(st + (int64_t)pr * N) + q);
+        hv[k] = ld_nt4(reinterpret_cast<const float4*>(st + (int64_t)pr * N) + q);
     }
     // the gate's inputs, issued after the tile (first used after the update)
     float zq = 0.f, onq = 0.f, mzq[MM], moq[MM];
@@ -266,7 +266,7 @@ __global__ __launch_bounds__(256) void mamba3_step_kernel(M3StepParams p) {
 #pragma unroll
         for (int m = 0; m < MM; ++m) acc[m] = group_sum_last<N4>(acc[m]);
         if (live) {
-            *(reinterpret_cast<float4*>(st + (int64_t)pr * N) + q) = hn;
+            st_nt4(reinterpret_cast<float4*>(st + (int64_t)pr * N) + q, hn);
             if (q == N4 - 1)
 #pragma unroll
                 for (int m = 0; m < MM; ++m) s_out[m][pr] = acc[m] + Dv * s_v[m][pr];
