@@ -165,6 +165,11 @@ __device__ __forceinline__ uint4 buf_ld16(__amdgpu_buffer_rsrc_t r, uint32_t off
     return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
                                          r, off, (int)__builtin_amdgcn_readfirstlane(soff), 0));
 }
+// the same with the non-temporal hint (data streamed once)
+__device__ __forceinline__ uint4 buf_ld16_nt(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t soff) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                         r, off, (int)__builtin_amdgcn_readfirstlane(soff), 2));
+}
 __device__ __forceinline__ float buf_ld4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
 }

@@ -204,8 +204,7 @@ __global__ __launch_bounds__(256) void ssd2_prep_pack(Ssd2Params p, bf16_t* frag
 // cs_{e_{it-1}}); when that block decay exceeds 2^-64 (a steep block) the
 // tile is recomputed with the exact per-element weight dt_j exp(cs_i - cs_j)
 // on the diagonal block, after scaling acc by exp(cs_i - cs_{e_{it-1}}) <= 1.
-// Raw x is read back from global memory (the chunk was just streamed through
-// L2) on that rare path only.
+// Raw x is read back from global memory on that rare path only.
 //
 // Outputs are computed transposed, y^T[p, i] (i = time along MFMA columns),
 // so every per-time factor is a per-lane scalar and the four consecutive
@@ -301,7 +300,9 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
         }
     };
     // register prefetch of chunk cc's x rows (item m: rows 2 (lane/4 + 16 m) + {0, 1},
-    // headdim vector lane % 4) and dt (lane = position); loads past the end read zero
+    // headdim vector lane % 4) and dt (lane = position); loads past the end read zero.
+    // x is read once: its loads carry the non-temporal hint, which keeps the
+    // group fragments (shared by every workgroup of the group) resident in L2
     uint4 xq[XPT][2];
     float dtq;
     auto fetch = [&](int cc, int lane) {
@@ -311,8 +312,8 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
         const uint32_t off0 = (uint32_t)(2 * jp) * xrow + pv * 16;
 #pragma unroll
         for (int m = 0; m < XPT; ++m) {
-            xq[m][0] = buf_ld16(rx, off0, (uint32_t)(32 * m) * xrow);
-            xq[m][1] = buf_ld16(rx, off0, (uint32_t)(32 * m + 1) * xrow);
+            xq[m][0] = buf_ld16_nt(rx, off0, (uint32_t)(32 * m) * xrow);
+            xq[m][1] = buf_ld16_nt(rx, off0, (uint32_t)(32 * m + 1) * xrow);
         }
         const __amdgpu_buffer_rsrc_t rd =
             buf_rsrc(dthead + (int64_t)cc * Q * p.dt_sl, rows * (uint32_t)p.dt_sl * 4u);
@@ -494,8 +495,7 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
         // factor exp(cs_i - cs_{e_it}) above may overflow) are recomputed: acc
         // from the state again, brought to position i (factor <= 1), then the
         // exact weights dt_j exp(cs_i - cs_j) (+ D on the diagonal) on raw x
-        // rows read back from global memory (the chunk was just streamed
-        // through L2)
+        // rows read back from global memory
         bool steep = false;
 #pragma unroll
         for (int it = 0; it < T; ++it) steep |= (it ? cse[it - 1] : 0.f) - cse[it] > kSteep;
