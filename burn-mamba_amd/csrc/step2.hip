@@ -522,8 +522,19 @@ struct RowsParams {
     const float* w; bf16_t* a_out; int a_mt;
 };
 
-constexpr int kRowsThreads = 256;
-constexpr int kRowsMaxVec = 4;  // float4 per thread: cols <= 4096
+constexpr int kRowsThreads = 1024;  // a row per workgroup: one float4 per thread, more loads in flight
+constexpr int kRowsMaxVec = 1;      // float4 per thread: cols <= 4096
+constexpr int kRowsMaxHeads = 256;
+__device__ __forceinline__ float block_sum_rows(float v, float* s_red) {
+    v = wave_sum_dpp(v);  // every thread of the workgroup calls this
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < kRowsThreads / 64; ++w) s += s_red[w];
+    return s;
+}
 
 // Workgroups past the M row workgroups slide the shared B/C conv windows of
 // the layer just computed (every head has read them by now): one thread per
@@ -546,7 +557,7 @@ __device__ __forceinline__ void bc_window_slide(const RowsParams& p, int idx) {
 
 template <int S, bool PACK>
 __global__ __launch_bounds__(kRowsThreads) void layer_rows(RowsParams p) {
-    __shared__ float s_red[4];
+    __shared__ float s_red[kRowsThreads / 64];
     if (S > 0 && (int)blockIdx.x >= p.M) {
         bc_window_slide(p, ((int)blockIdx.x - p.M) * kRowsThreads + (int)threadIdx.x);
         return;
@@ -579,7 +590,7 @@ __global__ __launch_bounds__(kRowsThreads) void layer_rows(RowsParams p) {
     if (S > 0 && t < p.H) ss_h = p.ssq[(int64_t)m * p.H + t];
     if (S > 0) {
         // ---- residual of the layer just computed ----
-        const float rms = sqrtf(block_sum_256(ss_h, s_red) / (float)p.d_inner + kDivEpsF32);
+        const float rms = sqrtf(block_sum_rows(ss_h, s_red) / (float)p.d_inner + kDivEpsF32);
 #pragma unroll
         for (int z = 0; z < S; ++z)
 #pragma unroll
@@ -600,7 +611,7 @@ __global__ __launch_bounds__(kRowsThreads) void layer_rows(RowsParams p) {
         float ss = 0.f;
 #pragma unroll
         for (int i = 0; i < kRowsMaxVec; ++i) ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
-        const float rms = sqrtf(block_sum_256(ss, s_red) / (float)p.cols + kDivEpsF32);
+        const float rms = sqrtf(block_sum_rows(ss, s_red) / (float)p.cols + kDivEpsF32);
         // lanes 2q and 2q+1 hold columns 8q..8q+7 of a slab: one 16-byte run of
         // the packed operand, written by the even lane
 #pragma unroll
@@ -669,10 +680,10 @@ static LayerWs layer_ws_layout(const LayerGeom& g, void* base) {
 static int layer_check(const mamba2_layer_args* a, const mamba2_layer_args* first) {
     MAMBA_CHECK_ARG(a != nullptr, "args is NULL");
     MAMBA_CHECK_ARG(a->batch >= 1 && a->batch <= 256, "batch must be in [1, 256]");
-    MAMBA_CHECK_ARG(a->d_model > 0 && a->d_model % 16 == 0 && a->d_model <= 4 * 4 * kRowsThreads,
+    MAMBA_CHECK_ARG(a->d_model > 0 && a->d_model % 16 == 0 && a->d_model <= 4 * kRowsMaxVec * kRowsThreads,
                     "d_model must be a positive multiple of 16, at most 4096");
     // layer_rows reduces the per-head sums of squares with one thread per head
-    MAMBA_CHECK_ARG(a->nheads >= 1 && a->nheads <= kRowsThreads, "nheads must be in [1, 256]");
+    MAMBA_CHECK_ARG(a->nheads >= 1 && a->nheads <= kRowsMaxHeads, "nheads must be in [1, 256]");
     MAMBA_CHECK_ARG(a->x && a->pre_norm_w && a->in_proj && a->out_proj, "x, pre_norm_w, in_proj, out_proj required");
     MAMBA_CHECK_ARG(a->x_sb >= a->d_model && a->x_sb % 4 == 0, "x_sb must be >= d_model and a multiple of 4");
     if (!(a->headdim == 64 && (a->dstate == 64 || a->dstate == 128) && a->conv_kernel == 4)) {
