@@ -48,10 +48,6 @@ __device__ __forceinline__ f32x16_t mfma32x32x16(bf16x8_t a, bf16x8_t b, f32x16_
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ uint2 ld8(const void* ptr, bool ok) {
-    return ok ? *(const uint2*)ptr : make_uint2(0u, 0u);
-}
-
 // 8 packed bf16 (one uint4) -> 8 floats
 __device__ __forceinline__ void unpack8(uint4 v, float* f) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -101,34 +97,51 @@ struct FragLayout {
 // fragments above.  Positions past seqlen read as zero.  Only the causal
 // (ks <= 2 it + 1) C.B^T fragments are written (K2, src/mamba2/ssd/serial.rs:170-185),
 // and inside the diagonal 32x32 blocks the entries with j > i are stored as 0.
+// One workgroup per (chunk, group, batch): the chunk's B and C rows are read
+// once into LDS with 16-byte loads (rows padded by 16 bytes, so that the
+// transposed reads of the B fragments and the row reads of the C.B^T
+// operands spread over the banks), then every fragment is formed from LDS
+// and written as one contiguous 1 KB run.
 template <int N, int Q>
 __global__ __launch_bounds__(256) void ssd2_prep_pack(Ssd2Params p, bf16_t* frag) {
     using FL = FragLayout<N, Q>;
     constexpr int T = FL::T, NK = FL::NK, KS = FL::KS, NTN = FL::NTN, NF = FL::NF;
     constexpr int NTILE = T * (T + 1) / 2;
-    const int wave = wave_id(), lane = threadIdx.x & 63, r = lane & 31, half = lane >> 5;
-    const int s = blockIdx.x, S = gridDim.x;
-    const int cg = blockIdx.y, c = cg / p.G, g = cg % p.G, b = blockIdx.z;
+    constexpr int RP = N + 8;                  // LDS row pitch (bf16)
+    constexpr int PR = N / 8;                  // 16-byte pieces per row
+    __shared__ __align__(16) bf16_t sB[Q][RP];
+    __shared__ __align__(16) bf16_t sC[Q][RP];
+    const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63, r = lane & 31, half = lane >> 5;
+    const int cg = blockIdx.x, c = cg / p.G, g = cg % p.G, b = blockIdx.y;
     const int64_t grp = ((int64_t)b * p.nch + c) * p.G + g;
     const bf16_t* Cg = (const bf16_t*)p.Cm + (int64_t)b * p.C_sb + (int64_t)g * p.C_sg;
     const bf16_t* Bg = (const bf16_t*)p.Bm + (int64_t)b * p.B_sb + (int64_t)g * p.B_sg;
     bf16_t* base = frag + grp * NF * 512;
-    // (C.B^T)^T tiles: D[j][i] = sum_n B[j][n] C[i][n]; the lane then holds
+    // ---- the chunk's B and C rows into LDS (rows past seqlen as zero)
+#pragma unroll
+    for (int k = 0; k < (2 * Q * PR + 255) / 256; ++k) {
+        const int pi = tid + 256 * k;
+        if (pi < 2 * Q * PR) {
+            const int arr = pi / (Q * PR), row = (pi / PR) % Q, col = (pi % PR) * 8;
+            const int t = c * Q + row;
+            const bf16_t* src = (arr ? Cg + (int64_t)t * p.C_sl : Bg + (int64_t)t * p.B_sl) + col;
+            const uint4 v = t < p.L ? *(const uint4*)src : make_uint4(0u, 0u, 0u, 0u);
+            *(uint4*)(arr ? &sC[row][col] : &sB[row][col]) = v;
+        }
+    }
+    __syncthreads();
+    // ---- (C.B^T)^T tiles: D[j][i] = sum_n B[j][n] C[i][n]; the lane then holds
     // column i = 32 it + r at rows j = 32 jt + 8 q + 4 half + u (v = 4 q + u)
-    for (int tile = s + S * wave; tile < NTILE; tile += 4 * S) {
+    for (int tile = wave; tile < NTILE; tile += 4) {
         int it = 0;
         while ((it + 1) * (it + 2) / 2 <= tile) ++it;
         const int jt = tile - it * (it + 1) / 2;
-        const int tj = c * Q + jt * 32 + r, ti = c * Q + it * 32 + r;
         f32x16_t acc = zero16();
 #pragma unroll
         for (int kn = 0; kn < NK; ++kn) {
             const int n0 = kn * 16 + 8 * half;
-            const bf16x8_t a = as_bf16x8(tj < p.L ? *(const uint4*)(Bg + (int64_t)tj * p.B_sl + n0)
-                                                  : make_uint4(0u, 0u, 0u, 0u));
-            const bf16x8_t bb = as_bf16x8(ti < p.L ? *(const uint4*)(Cg + (int64_t)ti * p.C_sl + n0)
-                                                   : make_uint4(0u, 0u, 0u, 0u));
-            acc = mfma32x32x16(a, bb, acc);
+            acc = mfma32x32x16(as_bf16x8(*(const uint4*)&sB[jt * 32 + r][n0]),
+                               as_bf16x8(*(const uint4*)&sC[it * 32 + r][n0]), acc);
         }
         if (jt == it) {  // causal mask of the diagonal block: row j = 8 q + 4 half + u, column i = r
 #pragma unroll
@@ -145,25 +158,24 @@ __global__ __launch_bounds__(256) void ssd2_prep_pack(Ssd2Params p, bf16_t* frag
             *(uint2*)(base + ((int64_t)(it * (it + 1) + ks) * 64 + lp) * 8 + 4 * half) = pk;
         }
     }
-    for (int f = s + S * wave; f < T * NK; f += 4 * S) {
-        const int it = f / NK, kn = f % NK;
-        const int t = c * Q + it * 32 + r;
-        const bf16_t* row = Cg + (int64_t)t * p.C_sl + kn * 16 + 4 * half;
-        const uint2 lo = ld8(row, t < p.L), hi = ld8(row + 8, t < p.L);  // k order perm(half, .)
-        *(uint4*)(base + ((int64_t)(FL::C0 + f) * 64 + lane) * 8) = make_uint4(lo.x, lo.y, hi.x, hi.y);
-    }
-    for (int f = s + S * wave; f < NTN * KS; f += 4 * S) {
-        const int nt = f / KS, ks = f % KS;
-        const int n = nt * 32 + r;
-        uint32_t raw[8];
+    // ---- C fragments (k order perm(half, .)) and B fragments (transposed)
+    for (int f = wave; f < T * NK + NTN * KS; f += 4) {
+        uint4 v;
+        if (f < T * NK) {
+            const int it = f / NK, kn = f % NK;
+            const bf16_t* row = &sC[it * 32 + r][kn * 16 + 4 * half];
+            const uint2 lo = *(const uint2*)row, hi = *(const uint2*)(row + 8);
+            v = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        } else {
+            const int fb = f - T * NK, nt = fb / KS, ks = fb % KS;
+            const int n = nt * 32 + r, j0 = ks * 16 + 8 * half;
+            uint32_t raw[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int t = c * Q + ks * 16 + 8 * half + e;
-            raw[e] = t < p.L ? (uint32_t)Bg[(int64_t)t * p.B_sl + n] : 0u;
+            for (int e = 0; e < 8; ++e) raw[e] = (uint32_t)sB[j0 + e][n];
+            v = make_uint4(raw[0] | (raw[1] << 16), raw[2] | (raw[3] << 16), raw[4] | (raw[5] << 16),
+                           raw[6] | (raw[7] << 16));
         }
-        *(uint4*)(base + ((int64_t)(FL::B0 + f) * 64 + lane) * 8) =
-            make_uint4(raw[0] | (raw[1] << 16), raw[2] | (raw[3] << 16), raw[4] | (raw[5] << 16),
-                       raw[6] | (raw[7] << 16));
+        *(uint4*)(base + ((int64_t)(FL::C0 + f) * 64 + lane) * 8) = v;
     }
 }
 
@@ -723,8 +735,7 @@ static void launch_scan(const Ssd2Params& p, const bf16_t* frag, hipStream_t str
 template <int N, int Q>
 static int launch_q(const Ssd2Params& p, void* ws, hipStream_t stream, hipEvent_t ev0, hipEvent_t ev1) {
     bf16_t* frag = (bf16_t*)ws;
-    const int S = 4;  // prep workgroups per (batch, chunk, group)
-    hipLaunchKernelGGL((ssd2_prep_pack<N, Q>), dim3(S, p.nch * p.G, p.nb), dim3(256), 0, stream, p, frag);
+    hipLaunchKernelGGL((ssd2_prep_pack<N, Q>), dim3(p.nch * p.G, p.nb), dim3(256), 0, stream, p, frag);
     MAMBA_CHECK_LAUNCH();
     if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, stream));
     switch (choose_hpw(p)) {
