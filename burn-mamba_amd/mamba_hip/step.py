@@ -507,14 +507,20 @@ class Mamba2Stack:
     weights packed once at construction.  Otherwise the residual add of layer l is fused with the
     RmsNorm of layer l+1 (one mamba_rmsnorm call) around torch.mm products and
     mamba2_step_ssm.  All activations live in buffers allocated once per batch
-    size, so ``step_`` allocates nothing and can be captured in a HIP graph."""
+    size, so ``step_`` allocates nothing and can be captured in a HIP graph.
+    With ``split_batch`` (the default), a fused step of an even batch of 64 to
+    256 rows runs as two half batches on two streams: the rows never interact,
+    and one half's weight-streaming products overlap the other half's state
+    kernel (each half reads the weights once)."""
 
-    def __init__(self, layers: List[Mamba2Layer], fused: bool = True):
+    def __init__(self, layers: List[Mamba2Layer], fused: bool = True, split_batch: bool = True):
         assert layers
         self.layers = layers
         self.cfg = layers[0].mixer.cfg
         self._bufs = {}
         self._args = {}
+        self.split_batch = split_batch
+        self._side = None  # the two streams of the half-batch schedule, made on first use
         c = self.cfg
         self.fused = fused and c.per_head_dim == 64 and c.state_rank in (64, 128) and c.conv_kernel == 4 \
             and c.d_model % 16 == 0 and c.d_model <= 4096 and c.nheads <= 256
@@ -563,8 +569,8 @@ class Mamba2Stack:
     def new_caches(self, batch: int) -> List[Mamba2Cache]:
         return [l.mixer.new_cache(batch) for l in self.layers]
 
-    def buffers(self, batch: int, device):
-        key = (batch, str(device))
+    def buffers(self, batch: int, device, slot: int = 0):
+        key = (batch, str(device), slot)
         if key not in self._bufs:
             c, dt = self.cfg, self.layers[0].mixer.dtype
             bufs = dict(
@@ -590,26 +596,28 @@ class Mamba2Stack:
 
         ``events``: optional list of one torch.cuda.Event pair per layer,
         recorded around that layer's state-update kernel (benchmark timing)."""
-        bufs = self.buffers(x_res.shape[0], x_res.device)
-        if self.fused and x_res.shape[0] <= 256 and x_res.data_ptr() % 16 == 0 and x_res.stride(0) % 4 == 0:
-            L = _lib.lib()
-            ws = bufs["ws"]
-            wsp, stream = ctypes.c_void_p(ws.data_ptr()), _stream(x_res.device)
-            key = ("stack", x_res.data_ptr(), x_res.shape[0]) + tuple(c.ssm_bhpr.data_ptr() for c in caches)
-            arr = self._args.get(key)
-            if arr is None:
-                arr = (Mamba2LayerArgs * len(self.layers))(
-                    *[self._layer_args(i, x_res, caches[i]) for i in range(len(self.layers))])
-                self._args[key] = arr
-            if events is None:
-                check(L.mamba2_stack_step(arr, len(self.layers), wsp, ws.numel(), stream), "mamba2_stack_step")
-            else:
-                raw = [_raw_events(ev, x_res.device) for ev in events]
-                e0 = (ctypes.c_void_p * len(raw))(*[r[0] for r in raw])
-                e1 = (ctypes.c_void_p * len(raw))(*[r[1] for r in raw])
-                check(L.mamba2_stack_step_timed(arr, len(self.layers), wsp, ws.numel(), stream, e0, e1),
-                      "mamba2_stack_step_timed")
+        b = x_res.shape[0]
+        if (events is None and self.fused and self.split_batch and b >= 64 and b % 2 == 0 and b <= 256
+                and x_res.data_ptr() % 16 == 0 and x_res.stride(0) % 4 == 0 and x_res.is_cuda):
+            # two independent half batches on two streams: one half's weight-streaming
+            # products run while the other's state kernel streams the caches (each half
+            # reads the weights once; rows never interact, so the step is the same)
+            cur = torch.cuda.current_stream(x_res.device)
+            if self._side is None:
+                self._side = (torch.cuda.Stream(x_res.device), torch.cuda.Stream(x_res.device))
+            h = b // 2
+            for k, (lo, hi) in enumerate(((0, h), (h, b))):
+                st = self._side[k]
+                st.wait_stream(cur)
+                with torch.cuda.stream(st):
+                    part = [Mamba2Cache(conv_bvk=cc.conv_bvk[lo:hi], ssm_bhpr=cc.ssm_bhpr[lo:hi]) for cc in caches]
+                    self._stack_fused(x_res[lo:hi], part, None, slot=1 + k)
+            for st in self._side:
+                cur.wait_stream(st)
             return x_res
+        bufs = self.buffers(b, x_res.device)
+        if self.fused and b <= 256 and x_res.data_ptr() % 16 == 0 and x_res.stride(0) % 4 == 0:
+            return self._stack_fused(x_res, caches, events)
         prev = None
         for i, layer in enumerate(self.layers):
             rmsnorm(x_res, layer.norm_w, out=bufs["normed"], add=prev)
@@ -617,6 +625,28 @@ class Mamba2Stack:
                                   None if events is None else events[i])
             prev = bufs["out"]
         rmsnorm(x_res, None, add=prev)
+        return x_res
+
+    def _stack_fused(self, x_res: torch.Tensor, caches: List[Mamba2Cache], events, slot: int = 0):
+        """The whole stack as one mamba2_stack_step call on the current stream."""
+        bufs = self.buffers(x_res.shape[0], x_res.device, slot)
+        L = _lib.lib()
+        ws = bufs["ws"]
+        wsp, stream = ctypes.c_void_p(ws.data_ptr()), _stream(x_res.device)
+        key = ("stack", x_res.data_ptr(), x_res.shape[0]) + tuple(c.ssm_bhpr.data_ptr() for c in caches)
+        arr = self._args.get(key)
+        if arr is None:
+            arr = (Mamba2LayerArgs * len(self.layers))(
+                *[self._layer_args(i, x_res, caches[i]) for i in range(len(self.layers))])
+            self._args[key] = arr
+        if events is None:
+            check(L.mamba2_stack_step(arr, len(self.layers), wsp, ws.numel(), stream), "mamba2_stack_step")
+        else:
+            raw = [_raw_events(ev, x_res.device) for ev in events]
+            e0 = (ctypes.c_void_p * len(raw))(*[r[0] for r in raw])
+            e1 = (ctypes.c_void_p * len(raw))(*[r[1] for r in raw])
+            check(L.mamba2_stack_step_timed(arr, len(self.layers), wsp, ws.numel(), stream, e0, e1),
+                  "mamba2_stack_step_timed")
         return x_res
 
     def step(self, x: torch.Tensor, caches: Optional[List[Mamba2Cache]] = None):

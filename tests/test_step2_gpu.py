@@ -228,15 +228,15 @@ def test_mamba2_step_signature():
     np.testing.assert_allclose(cache.ssm_bhpr.cpu().numpy(), ref_ssm, **F32_TOL)
 
 
-@pytest.mark.parametrize("fused", [False, True])
-def test_stack_hip_graph_replays_equal_eager(fused):
+@pytest.mark.parametrize("fused,b", [(False, 4), (True, 40), (True, 64)])
+def test_stack_hip_graph_replays_equal_eager(fused, b):
     """Capture one stack step in a HIP graph; replay it several times with eager
-    work in between and check every replay against the eager result."""
+    work in between and check every replay against the eager result (batch 64:
+    the two-stream half-batch schedule, captured as two branches)."""
     import torch
     import mamba_hip
     cfg = mamba_hip.Mamba2Config(d_model=256, state_rank=128, per_head_dim=64)
     stack = mamba_hip.Mamba2Stack.init(cfg, 3, "cuda", torch.bfloat16, torch.Generator().manual_seed(4), fused=fused)
-    b = 4 if not fused else 40
     rng = np.random.default_rng(5)
     base = stack.new_caches(b)
     for c in base:
@@ -379,6 +379,33 @@ def _layer_step_nbg(u, p, ref, cfg):
                                          p["norm_w"], ref[1], cfg.nheads, cfg.per_head_dim, cfg.ngroups,
                                          cfg.state_rank, norm_before_gate=True)
     return u + oracle.linear(out, p["w_out"]), cs, ss
+
+
+def test_half_batch_schedule_matches_one_stream():
+    """The fused stack at batch 64 runs as two half batches on two streams; the
+    same stack with the schedule off (one mamba2_stack_step over all rows) gives
+    the same outputs and caches (the half batches' products split K the same
+    way or not, so agreement is to f32 accumulation order)."""
+    import torch
+    import mamba_hip
+    cfg = mamba_hip.Mamba2Config(d_model=512, state_rank=128, per_head_dim=64)
+    split = mamba_hip.Mamba2Stack.init(cfg, 2, "cuda", torch.bfloat16, torch.Generator().manual_seed(11))
+    whole = mamba_hip.Mamba2Stack(split.layers, split_batch=False)
+    b = 64
+    rng = np.random.default_rng(12)
+    c1 = split.new_caches(b)
+    _randomize_caches(c1, rng)
+    c2 = [mamba_hip.Mamba2Cache(c.conv_bvk.clone(), c.ssm_bhpr.clone()) for c in c1]
+    for _ in range(2):
+        x = _t(rng.standard_normal((b, 512)).astype(np.float32))
+        y1, c1 = split.step(x, c1)
+        y2, c2 = whole.step(x, c2)
+    torch.cuda.synchronize()
+    tol = dict(rtol=1e-3, atol=1e-3)
+    np.testing.assert_allclose(y1.cpu().numpy(), y2.cpu().numpy(), **tol)
+    for a, e in zip(c1, c2):
+        np.testing.assert_allclose(a.ssm_bhpr.cpu().numpy(), e.ssm_bhpr.cpu().numpy(), **tol)
+        np.testing.assert_allclose(a.conv_bvk.cpu().numpy(), e.conv_bvk.cpu().numpy(), rtol=1e-2, atol=1e-2)
 
 
 def test_fused_and_unfused_stacks_agree():
