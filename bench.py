@@ -942,6 +942,8 @@ def bench_decode(args):
     gen.manual_seed(0)
     log(f"init {cfg['n_layers']} layers (bf16 weights, reference init)")
     stack = mamba_hip.Mamba2Stack.init(c, cfg["n_layers"], dev, torch.bfloat16, gen)
+    if getattr(args, "no_split", False):
+        stack.split_batch = False
     b = cfg["batch"]
     caches = stack.new_caches(b)
     for cc in caches:  # pre-filled states: ssm ~ N(0, 0.1), conv windows ~ N(0, 1)
@@ -1003,7 +1005,9 @@ def bench_decode(args):
                    "graph": "hip graph of the whole step", "eager_ms_per_step": eager_ms,
                    "step_bytes": step_bytes, "step_hbm_gbs": step_gbs, "step_hbm_frac": step_gbs / HBM_PEAK_GBS,
                    "entry": ("mamba2_layer_step per layer (packed products, fused norm/residual)" if stack.fused
-                             else "mamba_rmsnorm + torch.mm + mamba2_step_ssm + torch.mm per layer")},
+                             else "mamba_rmsnorm + torch.mm + mamba2_step_ssm + torch.mm per layer"),
+                   "schedule": ("two half batches on two streams" if stack.splits(b)
+                                else "one stream")},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel_ms": kern_ms,
                      "algorithmic_bytes": kernel_bytes, "kernel": "step2_ssm_fast<128> (mean over all layers)"},
@@ -1310,6 +1314,9 @@ def main():
                              "mamba3_prep", "mamba2_block", "ssd2_bwd", "ssd3_bwd"])
     ap.add_argument("--batch", type=int, default=DECODE_CFG3["batch"], help="decode batch")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-split", action="store_true",
+                    help="decode: step the whole batch on one stream (no half-batch schedule), so that "
+                         "every state-kernel dispatch of a kernel trace covers the full batch")
     ap.add_argument("--no-decode", action="store_true",
                     help="ssd2 only: leave out the decode_b64 half of the headline metric")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -1375,7 +1382,8 @@ def decode_b64_summary(args):
     with the step's HBM fraction, the state-update kernel's roofline and its
     own CPU baseline."""
     import torch
-    d = bench_decode(argparse.Namespace(batch=64, steps=args.steps, warmup=args.warmup))
+    d = bench_decode(argparse.Namespace(batch=64, steps=args.steps, warmup=args.warmup,
+                                        no_split=args.no_split))
     traffic = _profiled_traffic(d["config"]["workload"])
     if traffic is not None:
         d["roofline"]["traffic"] = traffic

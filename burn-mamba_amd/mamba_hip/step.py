@@ -591,14 +591,18 @@ class Mamba2Stack:
             self._bufs[key] = bufs
         return self._bufs[key]
 
+    def splits(self, b: int) -> bool:
+        """Whether an untimed step of batch ``b`` runs as two half batches on two streams."""
+        return self.fused and self.split_batch and 64 <= b <= 256 and b % 2 == 0
+
     def step_(self, x_res: torch.Tensor, caches: List[Mamba2Cache], events=None):
         """In-place step of the whole stack: x_res [b, d_model] f32 becomes the stack output.
 
         ``events``: optional list of one torch.cuda.Event pair per layer,
         recorded around that layer's state-update kernel (benchmark timing)."""
         b = x_res.shape[0]
-        if (events is None and self.fused and self.split_batch and b >= 64 and b % 2 == 0 and b <= 256
-                and x_res.data_ptr() % 16 == 0 and x_res.stride(0) % 4 == 0 and x_res.is_cuda):
+        if (events is None and self.splits(b) and x_res.data_ptr() % 16 == 0 and x_res.stride(0) % 4 == 0
+                and x_res.is_cuda):
             # two independent half batches on two streams: one half's weight-streaming
             # products run while the other's state kernel streams the caches (each half
             # reads the weights once; rows never interact, so the step is the same)
