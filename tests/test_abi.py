@@ -158,3 +158,19 @@ def test_missing_library_raises_no_fallback():
         "sys.exit(3)\n" % os.path.join(ROOT, "burn-mamba_amd"))
     r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0 and "raised" in r.stdout, r.stdout + r.stderr
+
+
+def test_half_batch_predicate_needs_no_gpu():
+    """Mamba2Stack.splits: the two-stream half-batch schedule applies to a fused
+    stack at an even batch of 64 to 256 only, and can be switched off."""
+    import mamba_hip
+
+    def stack(fused, split_batch):  # the predicate reads only these two flags; no layers are built
+        s = object.__new__(mamba_hip.Mamba2Stack)
+        s.fused, s.split_batch = fused, split_batch
+        return s
+
+    s = stack(True, True)
+    assert [b for b in (1, 16, 62, 63, 64, 65, 66, 100, 255, 256, 258) if s.splits(b)] == [64, 66, 100, 256]
+    assert not stack(True, False).splits(64)
+    assert not stack(False, True).splits(64)

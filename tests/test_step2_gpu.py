@@ -381,17 +381,21 @@ def _layer_step_nbg(u, p, ref, cfg):
     return u + oracle.linear(out, p["w_out"]), cs, ss
 
 
-def test_half_batch_schedule_matches_one_stream():
-    """The fused stack at batch 64 runs as two half batches on two streams; the
-    same stack with the schedule off (one mamba2_stack_step over all rows) gives
-    the same outputs and caches (the half batches' products split K the same
-    way or not, so agreement is to f32 accumulation order)."""
+@pytest.mark.parametrize("b", [64, 100, 256])
+def test_half_batch_schedule_matches_one_stream(b):
+    """The fused stack at an even batch of 64 to 256 runs as two half batches on
+    two streams (100: halves of 50 rows, a ragged last row tile); the same stack
+    with the schedule off (one mamba2_stack_step over all rows) gives the same
+    outputs and caches. The half batches' products may tile rows and split K
+    differently, so f32 sums round in another order, and now and then that flips
+    the rounding of a bf16 operand the fused step writes (the pre-normed row,
+    the gated values): one bf16 ulp (2^-8 relative) of one term, hence 5e-3."""
     import torch
     import mamba_hip
     cfg = mamba_hip.Mamba2Config(d_model=512, state_rank=128, per_head_dim=64)
     split = mamba_hip.Mamba2Stack.init(cfg, 2, "cuda", torch.bfloat16, torch.Generator().manual_seed(11))
     whole = mamba_hip.Mamba2Stack(split.layers, split_batch=False)
-    b = 64
+    assert split.splits(b) and not whole.splits(b)
     rng = np.random.default_rng(12)
     c1 = split.new_caches(b)
     _randomize_caches(c1, rng)
@@ -401,7 +405,7 @@ def test_half_batch_schedule_matches_one_stream():
         y1, c1 = split.step(x, c1)
         y2, c2 = whole.step(x, c2)
     torch.cuda.synchronize()
-    tol = dict(rtol=1e-3, atol=1e-3)
+    tol = dict(rtol=5e-3, atol=5e-3)
     np.testing.assert_allclose(y1.cpu().numpy(), y2.cpu().numpy(), **tol)
     for a, e in zip(c1, c2):
         np.testing.assert_allclose(a.ssm_bhpr.cpu().numpy(), e.ssm_bhpr.cpu().numpy(), **tol)
