@@ -1394,7 +1394,7 @@ def decode_b64_summary(args):
          "step_hbm_frac": cfg["step_hbm_frac"],
          "target_us": cfg["step_bytes"] / (0.6 * HBM_PEAK_GBS * 1e9) * 1e6,
          "config": {k: cfg[k] for k in ("workload", "batch", "n_layers", "d_model", "nheads", "headdim", "dstate",
-                                        "weights", "state", "graph", "eager_ms_per_step", "entry")
+                                        "weights", "state", "graph", "eager_ms_per_step", "entry", "schedule")
                     if k in cfg},
          "roofline": d["roofline"]}
     if not args.no_cpu_baseline:
