@@ -7,4 +7,4 @@ void set_error(const std::string& msg) { g_last_error = msg; }
 }  // namespace mamba
 
 extern "C" const char* mamba_last_error(void) { return mamba::g_last_error.c_str(); }
-extern "C" const char* mamba_version(void) { return "mamba_hip 0.1.0 gfx950"; }
+extern "C" const char* mamba_version(void) { return "mamba_hip 0.2.0 gfx950"; }

@@ -226,7 +226,8 @@ def linear(x: torch.Tensor, packed_w: torch.Tensor, d_out: int, bias: Optional[t
     return out
 
 
-_DERIVED_ATTRS = ("_mamba_prefill_wt", "_mamba_packed")
+# every derived copy is kept on the weight under an attribute with this prefix
+_DERIVED_PREFIX = "_mamba_"
 
 
 def _weight_key(w: torch.Tensor):
@@ -242,11 +243,11 @@ def _weight_key(w: torch.Tensor):
 
 
 def drop_derived(w: torch.Tensor) -> None:
-    """Forget the transposed and packed copies made from ``w`` (needed only
-    after an in-place update of an inference-mode weight)."""
-    for a in _DERIVED_ATTRS:
-        if hasattr(w, a):
-            delattr(w, a)
+    """Forget every derived copy made from ``w`` (the transposed, padded and
+    packed ones; needed only after an in-place update of an inference-mode
+    weight)."""
+    for a in [a for a in vars(w) if a.startswith(_DERIVED_PREFIX)]:
+        delattr(w, a)
 
 
 def _derived(w: torch.Tensor, attr: str, make):
@@ -538,7 +539,8 @@ class Mamba2Stack:
                            fused=fused)
 
     def _layer_args(self, i: int, x_res: torch.Tensor, cache: Mamba2Cache) -> Mamba2LayerArgs:
-        key = (i, x_res.data_ptr(), x_res.shape[0], cache.conv_bvk.data_ptr(), cache.ssm_bhpr.data_ptr())
+        key = (i, x_res.data_ptr(), x_res.shape[0], x_res.stride(0), cache.conv_bvk.data_ptr(),
+               cache.ssm_bhpr.data_ptr())
         a = self._args.get(key)
         if a is not None:
             return a
@@ -637,7 +639,9 @@ class Mamba2Stack:
         L = _lib.lib()
         ws = bufs["ws"]
         wsp, stream = ctypes.c_void_p(ws.data_ptr()), _stream(x_res.device)
-        key = ("stack", x_res.data_ptr(), x_res.shape[0]) + tuple(c.ssm_bhpr.data_ptr() for c in caches)
+        # every pointer the per-layer args embed (the residual row and both caches)
+        key = ("stack", x_res.data_ptr(), x_res.shape[0], x_res.stride(0)) + tuple(
+            (c.conv_bvk.data_ptr(), c.ssm_bhpr.data_ptr()) for c in caches)
         arr = self._args.get(key)
         if arr is None:
             arr = (Mamba2LayerArgs * len(self.layers))(

@@ -51,11 +51,16 @@ fn main() {
         objs.push(obj);
         println!("cargo:rerun-if-changed={}", src.display());
     }
-    for h in ["common.h", "bwd_core.h", "ssd3_core.h", "lin.h", "mamba3_internal.h"] {
-        let p: &Path = &csrc.join(h);
-        if p.exists() {
-            println!("cargo:rerun-if-changed={}", p.display());
-        }
+    // every header the sources include, found the same way as the sources
+    let mut headers: Vec<PathBuf> = std::fs::read_dir(&csrc)
+        .unwrap()
+        .filter_map(|e| e.ok().map(|e| e.path()))
+        .filter(|p| p.extension().map_or(false, |x| x == "h"))
+        .collect();
+    headers.sort();
+    for h in &headers {
+        let p: &Path = h;
+        println!("cargo:rerun-if-changed={}", p.display());
     }
     println!("cargo:rerun-if-changed={}", include.join("mamba_hip.h").display());
     let lib = out.join("libmamba_hip.so");

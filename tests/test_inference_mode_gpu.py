@@ -50,3 +50,29 @@ def test_mamba3_forward_and_step_inference_mode_weights():
     torch.cuda.synchronize()
     assert torch.equal(o1, o2) and torch.equal(s1, s2)
     assert torch.equal(c1.ssm_bhpr, c2.ssm_bhpr)
+
+
+def test_mamba3_inference_mode_weight_update_then_drop_derived():
+    """An in-place update of an inference-mode in_proj weight, followed by
+    drop_derived, reaches forward: the padded prefill copy (in_proj rows are
+    padded to 8 elements, d_in_proj = 2 d_inner + ... is rarely a multiple of
+    8) is forgotten with the others."""
+    import torch
+    import mamba_hip
+    cfg = mamba_hip.Mamba3Config(d_model=128, state_rank=128, per_head_dim=64, mimo_rank=4)
+    m = cfg.init("cuda", torch.bfloat16, torch.Generator(device="cuda").manual_seed(7))
+    assert m.in_proj_w.shape[1] % 8 != 0  # the padded-copy case
+    mi = _inference_copy(m)
+    gen = torch.Generator(device="cuda").manual_seed(8)
+    x = torch.randn((2, 40, 128), generator=gen, device="cuda").to(torch.bfloat16)
+    delta = (0.05 * torch.randn(m.in_proj_w.shape, generator=gen, device="cuda")).to(torch.bfloat16)
+    with torch.inference_mode():
+        before, _ = mi.forward(x, None, chunk_len=32)
+        mi.in_proj_w.add_(delta)
+        mamba_hip.drop_derived(mi.in_proj_w)
+        got, _ = mi.forward(x, None, chunk_len=32)
+    fresh = dataclasses.replace(m, in_proj_w=(m.in_proj_w + delta).contiguous())
+    want, _ = fresh.forward(x, None, chunk_len=32)
+    torch.cuda.synchronize()
+    assert not torch.equal(before, want)
+    assert torch.equal(got, want)

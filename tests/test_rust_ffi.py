@@ -64,3 +64,10 @@ def test_repr_c_layouts_equal_the_c_layouts():
         got = _c_layout(cname, [f for f, _ in fields])
         assert got[0] == size, cname
         assert got[1:] == offs, cname
+
+
+def test_library_version_matches_the_crate():
+    import mamba_hip
+    cargo = open(os.path.join(CRATE, "Cargo.toml")).read()
+    want = re.search(r'^version = "([^"]+)"', cargo, re.M).group(1)
+    assert mamba_hip.lib().mamba_version().decode().split()[1] == want
