@@ -41,6 +41,33 @@ FILE_FLAGS = {
 }
 
 
+# kernels whose memory waits are hand-counted (an explicit s_waitcnt vmcnt(n)
+# with n > 0 after direct-to-LDS loads): a scratch access added by the compiler
+# would make the count retire too early, so a build of them with scratch is
+# refused.  Checked from the compiler's kernel-resource-usage remarks.
+NO_SCRATCH = {
+    "mamba1.hip": ("mamba1_scan_tm16",),
+}
+
+
+def _check_no_scratch(src: str, stderr: str) -> None:
+    kernels = NO_SCRATCH.get(os.path.basename(src), ())
+    cur = None
+    seen = set()
+    for ln in stderr.splitlines():
+        if "Function Name:" in ln:
+            cur = next((k for k in kernels if k in ln), None)
+        elif cur and "ScratchSize [bytes/lane]:" in ln:
+            size = int(ln.split("ScratchSize [bytes/lane]:")[1].split()[0])
+            if size != 0:
+                raise RuntimeError(f"{cur} in {src} uses {size} bytes/lane of scratch; "
+                                   "its hand-counted memory waits assume none")
+            seen.add(cur)
+    missing = set(kernels) - seen
+    if missing:
+        raise RuntimeError(f"no resource-usage remark for {sorted(missing)} in {src}")
+
+
 def _deps_newer(obj: str, src: str) -> bool:
     if not os.path.exists(obj):
         return True
@@ -52,10 +79,17 @@ def _deps_newer(obj: str, src: str) -> bool:
 def _compile(src: str, force: bool) -> str:
     obj = os.path.join(OBJDIR, os.path.basename(src).replace(".hip", ".o"))
     if force or _deps_newer(obj, src):
-        cmd = [HIPCC, *CFLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
+        check = os.path.basename(src) in NO_SCRATCH
+        cmd = [HIPCC, *CFLAGS, *FILE_FLAGS.get(os.path.basename(src), []),
+               *(["-Rpass-analysis=kernel-resource-usage"] if check else []), "-c", src, "-o", obj]
         r = subprocess.run(cmd, capture_output=True, text=True)
         if r.returncode != 0:
             raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")
+        if check:
+            _check_no_scratch(src, r.stderr or "")
+            r.stderr = "\n".join(ln for ln in (r.stderr or "").splitlines()
+                                  if "kernel-resource-usage" not in ln and not ln.lstrip().startswith(("|", "^"))
+                                  and not ln.lstrip()[:1].isdigit())
         # the host pass does not know the gfx feature flag: that warning is expected
         noise = "'-packed-fp32-ops' is not a recognized feature"
         msgs = [ln for ln in (r.stderr or "").splitlines() if noise not in ln and ln.strip()]

@@ -335,10 +335,15 @@ __global__ __launch_bounds__(256, 3) void mamba1_scan_tm16(Mamba1Params p) {
         // 15), so the one barrier per tile is for B/C: every wave's writes of
         // this tile's B/C are visible, and every wave is done with the buffer
         // the next tile's B/C will overwrite
-        if (GATE)
-            __builtin_amdgcn_s_waitcnt(0xF74);  // vmcnt(4) expcnt(7) lgkmcnt(15)
-        else
-            __builtin_amdgcn_s_waitcnt(0xF72);  // vmcnt(2)
+        // The count is exact only while no other vector-memory operation sits
+        // between them: a register spill (scratch access) would break it, and
+        // the build refuses a build of this kernel with scratch.
+        constexpr int kStoresPerTile = 2;          // the epilogue's two 16-byte stores
+        constexpr int kZLoadsPerTile = GATE ? 2 : 0;  // load_z
+        constexpr int kAfterDma = kStoresPerTile + kZLoadsPerTile;
+        static_assert(kAfterDma < 16, "vmcnt immediate is 4 bits (low field)");
+        // s_waitcnt: vmcnt in bits 3:0, expcnt(7) bits 6:4, lgkmcnt(15) bits 11:8
+        __builtin_amdgcn_s_waitcnt(0xF70 | kAfterDma);
         __syncthreads();
         load_bc(tk + 1);
         if (tk + 1 < ntile) dma_tile(tk + 1, buf ^ 1);
