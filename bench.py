@@ -35,6 +35,37 @@ HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, published
 BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA, published
 F32_MFMA_PEAK_TFLOPS = 157.3   # MI355X dense f32 MFMA, published
 
+# The reference's benches warm up by time (criterion's warm-up of
+# BENCH_TIME_MS / 5 = 1 s, benches/layer.rs:199-205) with an iteration floor
+# on top (BENCH_WARMUP_ITERS, :189-198).  The same here: the W requested
+# untimed steps are the floor, and untimed steps continue until the warm-up
+# has kept the GPU busy for WARMUP_S seconds, so that a short step count
+# still starts the timed region at the steady clock.
+WARMUP_S = 1.0
+_RAMP = {"steps": 0, "s": 0.0}
+
+
+def warm(step, floor):
+    """Run `floor` untimed steps, then more until WARMUP_S seconds have passed
+    (synchronised); the totals go into the JSON line's warmup_ramp."""
+    import torch
+    t0 = time.perf_counter()
+    n = 0
+    for _ in range(floor):
+        step()
+        n += 1
+    torch.cuda.synchronize()
+    batch = 1
+    while time.perf_counter() - t0 < WARMUP_S:
+        for _ in range(batch):
+            step()
+        n += batch
+        torch.cuda.synchronize()
+        batch = min(batch * 2, 256)
+    _RAMP["steps"] += n
+    _RAMP["s"] += time.perf_counter() - t0
+    log(f"warm-up: {n} untimed steps in {time.perf_counter() - t0:.2f} s")
+
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
@@ -236,9 +267,7 @@ def bench_mamba1_step(args):
     with torch.cuda.graph(graph):
         eager()
     log(f"warmup {args.warmup}")
-    for _ in range(args.warmup):
-        graph.replay()
-    torch.cuda.synchronize()
+    warm(graph.replay, args.warmup)
     log(f"timing {args.steps} graph replays")
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -372,9 +401,7 @@ def bench_mamba3_step(args):
     with torch.cuda.graph(graph):
         eager()
     log(f"warmup {args.warmup}")
-    for _ in range(args.warmup):
-        graph.replay()
-    torch.cuda.synchronize()
+    warm(graph.replay, args.warmup)
     log(f"timing {args.steps} graph replays")
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -476,9 +503,7 @@ def bench_mamba3_prep(args):
                                   b_bias=m.b_bias, c_bias=m.c_bias, mimo_x=m.mimo_x)
 
     log(f"warmup {args.warmup}")
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    warm(step, args.warmup)
     log(f"timing {args.steps} steps")
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
@@ -969,9 +994,7 @@ def bench_decode(args):
         eager()
 
     log(f"warmup {args.warmup}")
-    for _ in range(args.warmup):
-        graph.replay()
-    torch.cuda.synchronize()
+    warm(graph.replay, args.warmup)
     log(f"timing {args.steps} graph replays")
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -1083,9 +1106,7 @@ def _time_steps(args, step):
     kernel (mean kernel ms)."""
     import torch
     log(f"warmup {args.warmup}")
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    warm(step, args.warmup)
     log(f"timing {args.steps} steps")
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -1118,9 +1139,7 @@ def bench_ssd2(args):
                            chunk_len=cfg["chunk"], y=y, final_state=hT, events=events)
 
     log(f"inputs ready {tuple(inp['x'].shape)}; warmup {args.warmup}")
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    warm(step, args.warmup)
     log(f"timing {args.steps} steps")
     # whole-step timing: K back-to-back calls, synchronised on both sides
     t0 = time.perf_counter()
@@ -1217,9 +1236,7 @@ def bench_mamba2_block(args):
         m.forward(x, cache, chunk_len=cfg["chunk"], events=events)
 
     log(f"warmup {args.warmup}")
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    warm(step, args.warmup)
     log(f"timing {args.steps} steps")
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -1371,6 +1388,9 @@ def main():
         out["cpu_baseline"] = base()
     if args.workload == "ssd2" and not args.no_decode:
         out["decode_b64"] = decode_b64_summary(args)
+    out["warmup_ramp"] = {"min_s": WARMUP_S, "steps_run": _RAMP["steps"], "seconds": round(_RAMP["s"], 3),
+                          "note": "untimed steps: the W requested, then more until WARMUP_S s have passed "
+                                  "(time-bounded warm-up as the reference's benches/layer.rs)"}
     print(json.dumps(out), flush=True)
 
 
