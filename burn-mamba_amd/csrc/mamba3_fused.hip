@@ -15,11 +15,12 @@
 //   * coefficients: each fused position's thread forms dt, da, lambda of its
 //     step (and dt, lambda of the next step for scale) from dd_dt, dd_A,
 //     lambda_raw; da enters the chunk's cumulative sum once per step;
-//   * angles: thread (a, q) takes angle a over a quarter of the chunk's steps:
-//     increments dt range pi tanh(rot), a local running sum, the quarters'
-//     exclusive prefix by DPP inside the quad, the carried angle added and
-//     wrapped; cos / sin go to an LDS table [step][pair] (1, 0 past the rotated
-//     pairs), and the chunk's last angle is carried to the next chunk;
+//   * angles: thread (a, q) takes angle a over an eighth of the chunk's steps:
+//     increments dt range pi tanh(rot) on the fixed-point angle grid of
+//     mamba3_internal.h, a local running sum, the eighths' exclusive prefix by
+//     DPP inside the group of 8, the carried angle added; cos / sin go to an LDS
+//     table [step][pair] (1, 0 past the rotated pairs), and the chunk's last
+//     angle is carried to the next chunk;
 //   * B rows (row-major LDS tile, the shared MFMA operand): RMS over the row's
 //     16 lanes, norm weight and per-(head, rank) bias, the (k, k + N/2)
 //     rotation with the partner column from lane ^ 8, rounded to bf16;
@@ -45,9 +46,15 @@ struct M3FusedParams {
     bf16_t* y;  // [b, L, M, H, 64] contiguous
 };
 
+// y staged in LDS for whole-line stores, except at M = 2, whose cos / sin
+// tables leave no room for the staging tiles: y is then stored straight from
+// the accumulators (8 bytes per lane and row)
+template <int M>
+constexpr int m3f_ny() { return M == 2 ? 1 : 4; }
+
 template <int M>
 struct __align__(16) M3FusedLds {
-    Ssd3Lds<128> core;
+    Ssd3Lds<128, 1, m3f_ny<M>()> core;  // one chunk-entry state buffer: written at the next chunk's start
     bf16_t C[128][136];                      // C rows of the chunk (the y tiles' MFMA B operand)
     float cs[128 / M][64], sn[128 / M][64];  // cos / sin per step and pair index k, at m3f_pos(k)
     float4 bwb[M][4][16], cwb[M][4][16];     // (w, bias, w, bias) of columns 8 nv + 2 e2 (+1) of B / C
@@ -62,31 +69,35 @@ __device__ __forceinline__ float m3f_bf(uint32_t u) { return __uint_as_float(u <
 // pairs 8 j .. 8 j + 7 reads them as two 16-byte vectors, and the 8 threads j = 0..7
 // of a row read 32 consecutive dwords per instruction (no bank conflicts).
 __device__ __forceinline__ int m3f_pos(int k) { return ((k & 4) << 3) + ((k >> 3) << 2) + (k & 3); }
-// tanh and sigmoid through the hardware reciprocal (1 ulp)
-__device__ __forceinline__ float m3f_tanh(float x) {
-    const float e = __expf(-2.f * fabsf(x));
-    return copysignf((1.f - e) * __builtin_amdgcn_rcpf(1.f + e), x);
-}
-__device__ __forceinline__ float m3f_sigmoid(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 // value of lane ^ 8 inside a 16-lane row (row_ror:8; every lane is written)
 __device__ __forceinline__ float m3f_xor8(float x) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x128, 0xf, 0xf, false));
 }
 // value of lane - K inside a 16-lane row (row_shr:K), 0 where that leaves the row
 template <int K>
-__device__ __forceinline__ float m3f_shr(float x) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x110 + K, 0xf, 0xf, false));
+__device__ __forceinline__ int m3f_shr(int x) {
+    return __builtin_amdgcn_update_dpp(0, x, 0x110 + K, 0xf, 0xf, false);
+}
+template <int K>
+__device__ __forceinline__ long long m3f_shr64(long long x) {
+    const uint64_t u = (uint64_t)x;
+    const uint32_t lo = (uint32_t)m3f_shr<K>((int)(uint32_t)u), hi = (uint32_t)m3f_shr<K>((int)(uint32_t)(u >> 32));
+    return (long long)(((uint64_t)hi << 32) | lo);
 }
 // value of lane 8 (lane / 8) + 7: the last lane of each aligned group of 8 (ds_swizzle bit masks)
-__device__ __forceinline__ float m3f_last8(float x) {
-    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x18 | (0x7 << 5)));
+__device__ __forceinline__ long long m3f_last8_64(long long x) {
+    const uint64_t u = (uint64_t)x;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_swizzle((int)(uint32_t)u, 0x18 | (0x7 << 5));
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_swizzle((int)(uint32_t)(u >> 32), 0x18 | (0x7 << 5));
+    return (long long)(((uint64_t)hi << 32) | lo);
 }
 
 // Two rows (ranks m0 and m0 + 1 of one step) x 8 columns (8 nv ..) of raw
 // group-form B or C: the RMS over the row's 16 lanes, norm weight and bias,
 // the (k, k + N/2) rotation with the partner columns from lane ^ 8 (k = n mod
 // N/2; cs / sn point at the step's table entries for this thread's first four
-// pairs, the next four 32 entries on: the m3f_pos layout).
+// pairs, the next four 32 entries on: the m3f_pos layout).  The arithmetic is
+// mamba3_internal.h's, as in the segment prep: the same bits.
 // Writes the bf16 rows to the LDS tile and leaves the f32 rows in y0 / y1.
 __device__ __forceinline__ void m3f_rows(uint4 r0, uint4 r1, const float (&w)[8], const float (&b0)[8],
                                          const float (&b1)[8], const float* cs, const float* sn, float sgn,
@@ -97,21 +108,13 @@ __device__ __forceinline__ void m3f_rows(uint4 r0, uint4 r1, const float (&w)[8]
         y0[2 * e] = s3_lo(a0[e]); y0[2 * e + 1] = s3_hi(a0[e]);
         y1[2 * e] = s3_lo(a1[e]); y1[2 * e + 1] = s3_hi(a1[e]);
     }
-    float ss0 = 0.f, ss1 = 0.f;
+    const float ss0 = m3_group_sum<16>(m3_sumsq8(y0));
+    const float ss1 = m3_group_sum<16>(m3_sumsq8(y1));
+    const float rms0 = m3_rms_inv(ss0, 128), rms1 = m3_rms_inv(ss1, 128);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        ss0 += y0[e] * y0[e];
-        ss1 += y1[e] * y1[e];
-    }
-    ss0 = m3_group_sum<16>(ss0);
-    ss1 = m3_group_sum<16>(ss1);
-    // 1 / sqrt(mean + eps) (the argument is >= eps, a normal number)
-    const float rms0 = __builtin_amdgcn_rsqf(ss0 * (1.f / 128.f) + kDivEpsF32);
-    const float rms1 = __builtin_amdgcn_rsqf(ss1 * (1.f / 128.f) + kDivEpsF32);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        y0[e] = (y0[e] * rms0) * w[e] + b0[e];
-        y1[e] = (y1[e] * rms1) * w[e] + b1[e];
+        y0[e] = m3_norm(y0[e], rms0, w[e], b0[e]);
+        y1[e] = m3_norm(y1[e], rms1, w[e], b1[e]);
     }
     float o0[8], o1[8];
 #pragma unroll
@@ -125,8 +128,8 @@ __device__ __forceinline__ void m3f_rows(uint4 r0, uint4 r1, const float (&w)[8]
     const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        y0[e] = cv[e] * y0[e] + (sgn * sv[e]) * o0[e];
-        y1[e] = cv[e] * y1[e] + (sgn * sv[e]) * o1[e];
+        y0[e] = m3_rot(cv[e], y0[e], sgn * sv[e], o0[e]);
+        y1[e] = m3_rot(cv[e], y1[e], sgn * sv[e], o1[e]);
     }
     *(uint4*)dst0 = make_uint4(pack_bf16x2(y0[0], y0[1]), pack_bf16x2(y0[2], y0[3]), pack_bf16x2(y0[4], y0[5]),
                                pack_bf16x2(y0[6], y0[7]));
@@ -152,15 +155,16 @@ __device__ __forceinline__ void m3f_st(bf16_t* dst, const float* v) {
 // wave) while waves 4-7 update the state (dstate columns 32 (wave - 4) ..).
 template <int M>
 __global__ __launch_bounds__(512, 1) void mamba3_ssd_fused(M3FusedParams p) {
-    constexpr int QF = 128, N = 128, KS = QF / 16;
+    constexpr int QF = 128, N = 128;
     constexpr int TS = QF / M;                    // steps per chunk
     constexpr int lgM = M == 2 ? 1 : (M == 4 ? 2 : 3);
     static_assert(M == 2 || M == 4 || M == 8, "MIMO rank 2, 4 or 8");
     constexpr int JA = TS / 8;                    // steps per angle thread (8 threads per angle)
     constexpr int XI = TS * 8, XPT = (XI + 511) / 512;  // x items: (step, 4-wide headdim piece)
     constexpr int RP = 2;                         // B row pairs and C row pairs per thread
+    constexpr bool STAGE_Y = m3f_ny<M>() == 4;
     __shared__ M3FusedLds<M> SF;
-    Ssd3Lds<QF>& S = SF.core;
+    Ssd3Lds<QF, 1, m3f_ny<M>()>& S = SF.core;
 
     const int tid_ = threadIdx.x, r_ = tid_ & 31, half_ = (tid_ >> 5) & 1;
     const int wv = wave_id(), w4 = wv & 3;
@@ -194,9 +198,7 @@ __global__ __launch_bounds__(512, 1) void mamba3_ssd_fused(M3FusedParams p) {
             const int pp = p0 + 8 * (v >> 2) + 4 * half_ + (v & 3);
             hacc[v] = p.h0[hbase + pp * N + w4 * 32 + r_];
         }
-#pragma unroll
-        for (int v = 0; v < 16; ++v)
-            S.h[0][8 * (v >> 2) + 4 * half_ + (v & 3)][w4 * 32 + r_] = __builtin_bit_cast(bf16_t, (__bf16)hacc[v]);
+        ssd3_put_state(S, hacc, 0, w4, r_, half_);
     }
 
     const float dtb = p.dt_bias[h];
@@ -275,14 +277,15 @@ __global__ __launch_bounds__(512, 1) void mamba3_ssd_fused(M3FusedParams p) {
     };
     // the same issue order as inside the loop (small loads, then rows): the
     // waits at the loop head then count the same way on entry and on the back-edge
-    float theta = (tid_ >> 3) < p.A ? p.ang[bh * p.A + (tid_ >> 3)] : 0.f;  // loaded before the prefetch
+    // the cumulative angle of this thread's angle (grid units, mamba3_internal.h): loaded
+    // before the prefetch
+    long long theta = (tid_ >> 3) < p.A ? m3_ang_fix(p.ang[bh * p.A + (tid_ >> 3)]) : 0ll;
     fetch(0);
     __builtin_amdgcn_sched_barrier(0);
     fetch_rows(0);
     __builtin_amdgcn_sched_barrier(0);
 
     for (int c = 0; c < p.nch; ++c) {
-        const int cur = c & 1;
         const int t0 = c * TS;
         // thread coordinates redefined per chunk: LDS addresses derived from them are
         // formed inside the loop instead of being hoisted (and spilled) as invariants
@@ -296,22 +299,25 @@ __global__ __launch_bounds__(512, 1) void mamba3_ssd_fused(M3FusedParams p) {
         const int bm0 = (2 * b_fp) & (M - 1);
         const int kq4 = (b_nv & 7) * 4;  // m3f_pos of the thread's first pair index 8 (nv & 7)
         const float sgn = b_nv < 8 ? -1.f : 1.f;
+        // ---- the state entering this chunk into its one LDS buffer (waves 4-7;
+        // the y tiles of the previous chunk have read it before the last barrier,
+        // this chunk's read it after the next one)
+        if (c > 0 && wv >= 4) ssd3_put_state(S, hacc, 0, w4, r, half);
         // ---- A: coefficients of this thread's position; the block scan of da
         float daq = 0.f, scq = 0.f, gmq = 0.f;
         if (tid < QF) {
             const int t = t0 + cf_tl;
             float dt = 0.f;
             if (t < p.L) {
-                dt = fminf(fmaxf(m3p_softplus(m3f_bf(kq[0]) + dtb), p.dt_lo), p.dt_hi);
-                const float da = dt * -fmaxf(m3p_softplus(m3f_bf(kq[1])), p.a_floor);
-                const float lam = m3f_sigmoid(m3f_bf(kq[2]));
-                float nxt = 0.f;
+                float da, lam;
+                m3_coef(m3f_bf(kq[0]), m3f_bf(kq[1]), m3f_bf(kq[2]), dtb, p.a_floor, p.dt_lo, p.dt_hi, dt, da, lam);
+                float dt1 = 0.f, lam1 = 0.f;  // the next step's (scale's shift); 0 past the end
                 if (t + 1 < p.L) {
-                    const float dt1 = fminf(fmaxf(m3p_softplus(m3f_bf(kq[3]) + dtb), p.dt_lo), p.dt_hi);
-                    nxt = (1.f - m3f_sigmoid(m3f_bf(kq[4]))) * dt1;
+                    dt1 = fminf(fmaxf(m3p_softplus(m3f_bf(kq[3]) + dtb), p.dt_lo), p.dt_hi);
+                    lam1 = m3_sigmoid(m3f_bf(kq[4]));
                 }
                 gmq = lam * dt;
-                scq = gmq + nxt;
+                scq = __builtin_fmaf(1.f - lam1, dt1, gmq);
                 daq = cf_first ? da : 0.f;  // da enters the cumulative sum once per step
             }
             if (cf_first) SF.dt[cf_tl] = dt;
@@ -339,36 +345,40 @@ __global__ __launch_bounds__(512, 1) void mamba3_ssd_fused(M3FusedParams p) {
             }
         }
         {
-            float cum[JA];
-            float run = 0.f;
+            // increments on the fixed-point angle grid: integer sums, so every
+            // position's angle is the one the segment prep forms
+            long long cum[JA];
+            long long run = 0ll;
 #pragma unroll
             for (int j = 0; j < JA; ++j) {
-                run += SF.dt[ang_q * JA + j] * (m3f_tanh(m3f_bf(rq[j])) * p.span);
+                run += m3_ang_fix(m3_angle_inc(SF.dt[ang_q * JA + j], m3f_bf(rq[j]), p.span));
                 cum[j] = run;
             }
             // inclusive scan of the 8 parts' totals inside each aligned group of 8 lanes
-            float incl = run;
+            long long incl = run;
             {
-                const float t1 = m3f_shr<1>(incl);
-                incl += ang_q >= 1 ? t1 : 0.f;
-                const float t2 = m3f_shr<2>(incl);
-                incl += ang_q >= 2 ? t2 : 0.f;
-                const float t4 = m3f_shr<4>(incl);
-                incl += ang_q >= 4 ? t4 : 0.f;
+                const long long t1 = m3f_shr64<1>(incl);
+                incl += ang_q >= 1 ? t1 : 0ll;
+                const long long t2 = m3f_shr64<2>(incl);
+                incl += ang_q >= 2 ? t2 : 0ll;
+                const long long t4 = m3f_shr64<4>(incl);
+                incl += ang_q >= 4 ? t4 : 0ll;
             }
-            const float base = theta + (incl - run);
-            const float total = m3f_last8(incl);
+            const long long base = theta + (incl - run);
+            const long long total = m3f_last8_64(incl);
             const bool rot_on = ang_a < p.npair;
 #pragma unroll
             for (int j = 0; j < JA; ++j) {
-                const float th = m3p_wrap(base + cum[j]);
-                SF.cs[ang_q * JA + j][m3f_pos(ang_a)] = rot_on ? __cosf(th) : 1.f;
-                SF.sn[ang_q * JA + j][m3f_pos(ang_a)] = rot_on ? __sinf(th) : 0.f;
+                float c = 1.f, sn = 0.f;
+                if (rot_on) m3_cossin(m3_ang_rad(m3_ang_reduce(base + cum[j])), c, sn);
+                SF.cs[ang_q * JA + j][m3f_pos(ang_a)] = c;
+                SF.sn[ang_q * JA + j][m3f_pos(ang_a)] = sn;
             }
-            theta = m3p_wrap(theta + total);  // the chunk's last angle, carried wrapped
+            theta = m3_ang_reduce(theta + total);  // the chunk's last angle
         }
         __syncthreads();
-        if (c > 0 && wv < 4) store_y(c - 1, lane);
+        if constexpr (STAGE_Y)
+            if (c > 0 && wv < 4) store_y(c - 1, lane);
 #pragma unroll
         for (int k = 0; k < XPT; ++k) {
             const int item = tid + 512 * k;
@@ -377,7 +387,7 @@ __global__ __launch_bounds__(512, 1) void mamba3_ssd_fused(M3FusedParams p) {
                 const float xv[4] = {s3_lo(xq[k].x), s3_hi(xq[k].x), s3_lo(xq[k].y), s3_hi(xq[k].y)};
                 if (t0 + tl == p.L - 1)  // the cache tail: the last step's x
                     *(float4*)(p.vst + bh * 64 + p0 + pv * 4) = make_float4(xv[0], xv[1], xv[2], xv[3]);
-                float vt[4][M], vw[4][M];
+                float vt[4][M], vw[4][M], vwl[4][M];
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
                     const float wf = S.w[tl * M + m];
@@ -387,13 +397,17 @@ __global__ __launch_bounds__(512, 1) void mamba3_ssd_fused(M3FusedParams p) {
                     for (int e = 0; e < 4; ++e) {
                         const float vb = (float)(__bf16)(xv[e] * mxa[e]);  // v as the SSD seam holds it (bf16)
                         vt[e][m] = vb;
-                        vw[e][m] = vb * wf;
+                        // w v as hi + lo (hi exact in bf16, lo rounded by the store)
+                        const float x = vb * wf;
+                        vw[e][m] = (float)(__bf16)x;
+                        vwl[e][m] = x - vw[e][m];
                     }
                 }
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     m3f_st<M>(&S.xT[pv * 4 + e][tl * M], vt[e]);
                     m3f_st<M>(&S.xTw[pv * 4 + e][tl * M], vw[e]);
+                    m3f_st<M>(&S.xTwl[pv * 4 + e][tl * M], vwl[e]);
                 }
             }
         }
@@ -442,19 +456,7 @@ __global__ __launch_bounds__(512, 1) void mamba3_ssd_fused(M3FusedParams p) {
             const float dec = __builtin_amdgcn_exp2f(cs_end);
 #pragma unroll
             for (int v = 0; v < 16; ++v) hacc[v] *= dec;
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                const int j0 = ks * 16 + 8 * half;
-                const s3_bf16x8_t a = *(const s3_bf16x8_t*)&S.xTw[r][j0];
-                s3_bf16x8_t bo8;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) bo8[e] = __builtin_bit_cast(__bf16, S.B[j0 + e][w4 * 32 + r]);
-                hacc = s3_mfma(a, bo8, hacc);
-            }
-#pragma unroll
-            for (int v = 0; v < 16; ++v)
-                S.h[cur ^ 1][8 * (v >> 2) + 4 * half + (v & 3)][w4 * 32 + r] =
-                    __builtin_bit_cast(bf16_t, (__bf16)hacc[v]);
+            ssd3_state_update(S, hacc, w4, r, half);
         } else {
             // ---- D (waves 0-3): y for output tile = wave, plus D v
             s3_bf16x8_t cfr[8];
@@ -462,10 +464,10 @@ __global__ __launch_bounds__(512, 1) void mamba3_ssd_fused(M3FusedParams p) {
             for (int kn = 0; kn < 8; ++kn) cfr[kn] = *(const s3_bf16x8_t*)&SF.C[wv * 32 + r][kn * 16 + 8 * half];
             s3_f32x16_t yacc;
             switch (wv) {
-                case 0: ssd3_y_tile<QF, 0, true>(S, cfr, cur, r, half, yacc); break;
-                case 1: ssd3_y_tile<QF, 1, true>(S, cfr, cur, r, half, yacc); break;
-                case 2: ssd3_y_tile<QF, 2, true>(S, cfr, cur, r, half, yacc); break;
-                default: ssd3_y_tile<QF, 3, true>(S, cfr, cur, r, half, yacc); break;
+                case 0: ssd3_y_tile<QF, 0, true>(S, cfr, 0, r, half, yacc); break;
+                case 1: ssd3_y_tile<QF, 1, true>(S, cfr, 0, r, half, yacc); break;
+                case 2: ssd3_y_tile<QF, 2, true>(S, cfr, 0, r, half, yacc); break;
+                default: ssd3_y_tile<QF, 3, true>(S, cfr, 0, r, half, yacc); break;
             }
             if (p.Dh) {
 #pragma unroll
@@ -474,19 +476,31 @@ __global__ __launch_bounds__(512, 1) void mamba3_ssd_fused(M3FusedParams p) {
                     yacc[v] += Dv * bf16_to_f32(S.xT[pp][wv * 32 + r]);
                 }
             }
-            // stage the 32 (position) x 32 (p) tile: lane holds y[i][p = 8(v/4) + 4 half + v%4]
+            // lane holds y[i][p = 8(v/4) + 4 half + v%4]
+            if constexpr (STAGE_Y) {
+                // stage the 32 (position) x 32 (p) tile
 #pragma unroll
-            for (int gq = 0; gq < 4; ++gq) {
-                const s3_bf16x4_t q = {(__bf16)yacc[4 * gq], (__bf16)yacc[4 * gq + 1], (__bf16)yacc[4 * gq + 2],
-                                       (__bf16)yacc[4 * gq + 3]};
-                *(s3_bf16x4_t*)&S.y[wv][r][8 * gq + 4 * half] = q;
+                for (int gq = 0; gq < 4; ++gq) {
+                    const s3_bf16x4_t q = {(__bf16)yacc[4 * gq], (__bf16)yacc[4 * gq + 1], (__bf16)yacc[4 * gq + 2],
+                                           (__bf16)yacc[4 * gq + 3]};
+                    *(s3_bf16x4_t*)&S.y[wv][r][8 * gq + 4 * half] = q;
+                }
+                // stored from the staging tile during the next chunk (store_y), after that
+                // chunk's waits on its prefetched loads, which then never wait on these stores
+            } else {
+                const int rows = min(QF, (p.L - t0) * M);
+                const __amdgpu_buffer_rsrc_t ry = buf_rsrc(yhead + (int64_t)t0 * M * p.H * 64, (uint32_t)rows * y_rs);
+#pragma unroll
+                for (int gq = 0; gq < 4; ++gq)
+                    buf_st8(ry, (uint32_t)(wv * 32 + r) * y_rs + (8 * gq + 4 * half) * 2,
+                            make_uint2(pack_bf16x2(yacc[4 * gq], yacc[4 * gq + 1]),
+                                       pack_bf16x2(yacc[4 * gq + 2], yacc[4 * gq + 3])));
             }
-            // stored from the staging tile during the next chunk (store_y), after that
-            // chunk's waits on its prefetched loads, which then never wait on these stores
         }
         __syncthreads();  // LDS reads of this chunk done before the next commit
     }
-    if (wv < 4) store_y(p.nch - 1, tid_ & 63);
+    if constexpr (STAGE_Y)
+        if (wv < 4) store_y(p.nch - 1, tid_ & 63);
     if (wv >= 4) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
@@ -494,7 +508,7 @@ __global__ __launch_bounds__(512, 1) void mamba3_ssd_fused(M3FusedParams p) {
             p.hT[hbase + pp * N + w4 * 32 + r_] = hacc[v];
         }
     }
-    if (ph == 0 && (tid_ & 7) == 0 && (tid_ >> 3) < p.A) p.ang_out[bh * p.A + (tid_ >> 3)] = theta;
+    if (ph == 0 && (tid_ & 7) == 0 && (tid_ >> 3) < p.A) p.ang_out[bh * p.A + (tid_ >> 3)] = m3_ang_rad(theta);
 }
 
 // Validates the arguments (-1 with the error set when invalid), fills the

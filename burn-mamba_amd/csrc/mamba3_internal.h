@@ -19,11 +19,80 @@ struct M3PrepParams {
     float* h0;
 };
 
+// ---- the prologue's arithmetic, shared by every Mamba-3 prefill kernel.
+// The segment-parallel prep (mamba3_prep.hip) and the prologue fused into the
+// scan (mamba3_fused.hip) form the same coefficients, angles and B / C rows
+// from the same in_proj row with these functions, bit for bit: the fused
+// kernel then equals the prep followed by the seam scan exactly.  Hardware
+// exp / reciprocal / rsqrt / sin / cos (a few ulp; the library's correctly
+// rounded forms measured 50 % slower in the fused kernel and moved no B / C
+// element closer to the f64 oracle: the f32 angle recurrence sets that
+// distance) and explicit fmas (no contraction choice left to the compiler).
+
 __device__ __forceinline__ float m3p_softplus(float x) { return x > 18.f ? x : log1pf(__expf(x)); }
-__device__ __forceinline__ float m3p_wrap(float a) {
-    const float two_pi = 6.28318530717958647692f;
-    return a - rintf(a * (1.f / two_pi)) * two_pi;
+__device__ __forceinline__ float m3_sigmoid(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
+// tanh from one exponential: sign(x) (1 - e) / (1 + e), e = exp(-2 |x|) <= 1
+__device__ __forceinline__ float m3_tanh(float x) {
+    const float e = __expf(-2.f * fabsf(x));
+    return copysignf((1.f - e) * __builtin_amdgcn_rcpf(1.f + e), x);
 }
+// cos and sin of an angle in [-pi, pi]
+__device__ __forceinline__ void m3_cossin(float a, float& c, float& s) {
+    c = __cosf(a);
+    s = __sinf(a);
+}
+// dt, da = dt A, lambda of one (position, head) from its raw dd_dt, dd_A, lambda columns
+// (trapezoidal_coefficients, helpers.rs:42-73)
+__device__ __forceinline__ void m3_coef(float raw_dt, float raw_da, float raw_lam, float dt_bias, float a_floor,
+                                        float dt_lo, float dt_hi, float& dt, float& da, float& lam) {
+    dt = fminf(fmaxf(m3p_softplus(raw_dt + dt_bias), dt_lo), dt_hi);
+    da = dt * -fmaxf(m3p_softplus(raw_da), a_floor);
+    lam = m3_sigmoid(raw_lam);
+}
+// angle increment dt range pi tanh(rot) (rotation/mod.rs:653-679)
+__device__ __forceinline__ float m3_angle_inc(float dt, float raw_rot, float span) {
+    return dt * (m3_tanh(raw_rot) * span);
+}
+
+// Cumulative angles in fixed point: multiples of 2^-32 rad in an int64,
+// reduced modulo Q2PI (2 pi in those units) to the canonical range
+// [-(Q2PI - 1) / 2, (Q2PI - 1) / 2].  Integer sums do not depend on their
+// association, so every kernel (whatever its segmentation of the sequence)
+// gets the same angle at every position: the cache's angle plus the sum of
+// the increments before it, each rounded to the 2^-32 grid (2.3e-10 rad; the
+// reference's f32 cumsum drifts by far more over long sequences).
+constexpr double kAngUnit = 4294967296.0;        // units per radian
+constexpr long long kQ2Pi = 26986075409ll;       // rint(2 pi 2^32), odd
+__device__ __forceinline__ long long m3_ang_reduce(long long q) {
+    // the quotient's estimate may be off by one: the two corrections below
+    // make the result exact and canonical
+    const double k = rint((double)q * (1.0 / (double)kQ2Pi));
+    q -= (long long)k * kQ2Pi;
+    if (q > kQ2Pi / 2) q -= kQ2Pi;
+    if (q < -(kQ2Pi / 2)) q += kQ2Pi;
+    return q;
+}
+// an angle in radians (a cache angle or one increment) onto the grid
+__device__ __forceinline__ long long m3_ang_fix(float a) { return m3_ang_reduce((long long)rint((double)a * kAngUnit)); }
+// a canonical grid angle as f32 radians in [-pi, pi]
+__device__ __forceinline__ float m3_ang_rad(long long q) { return (float)((double)q * (1.0 / kAngUnit)); }
+
+// One B / C row piece of 8 columns: the sum of squares (to be completed over
+// the row's lanes), the norm weight and bias, the rotation
+// y' = c y + s y_partner (s carries the pair's sign).
+__device__ __forceinline__ float m3_sumsq8(const float* y) {
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(y[e], y[e], ss);
+    return ss;
+}
+__device__ __forceinline__ float m3_rms_inv(float ss, int n) {
+    return __builtin_amdgcn_rsqf(ss / (float)n + kDivEpsF32);  // the argument is >= eps: a normal number
+}
+__device__ __forceinline__ float m3_norm(float y, float rms, float w, float bias) {
+    return __builtin_fmaf(y * rms, w, bias);
+}
+__device__ __forceinline__ float m3_rot(float c, float y, float s, float o) { return __builtin_fmaf(c, y, s * o); }
 // Lane exchanges inside aligned groups of a wave, without LDS addressing:
 // DPP for the quad and 16-lane-row patterns, ds_swizzle (bit-mask mode) for
 // the other xor distances below 32.
@@ -49,11 +118,6 @@ __device__ __forceinline__ float m3_group_sum(float x) {
     return x;
 }
 
-// tanh from one exponential: sign(x) (1 - e) / (1 + e), e = exp(-2 |x|) <= 1
-__device__ __forceinline__ float m3_tanh(float x) {
-    const float e = __expf(-2.f * fabsf(x));
-    return copysignf((1.f - e) / (1.f + e), x);
-}
 
 // Host side (mamba3_prep.hip): the prologue's parameter block from the C-ABI
 // arguments (with need_outputs = false the v / B / C / da / gamma / scale

@@ -15,9 +15,10 @@
 //    reads the starting angle).
 //  * mamba3_finish_fwd (step 9 before out_proj, :288-332): y += D v, the silu
 //    gate (or per-head gated RMSNorm) with mimo_z, and the mimo_o merge.
-// The cumulative angle is carried wrapped to [-pi, pi] at every position (the
-// same cos/sin as the reference's unwrapped f32 cumsum, without its drift on
-// long sequences).
+// The cumulative angle is carried on a fixed-point grid (2^-32 rad, reduced
+// modulo 2 pi): the same cos / sin as the reference's unwrapped f32 cumsum,
+// without its drift on long sequences, and the same value at every position
+// whatever the kernel's segmentation.
 #include "mamba3_internal.h"
 
 namespace mamba {
@@ -41,9 +42,8 @@ __device__ __forceinline__ void m3p_coef(const M3PrepParams& p, int b, int l, in
         return;
     }
     const int o = 2 * p.H * p.P + 2 * p.M * p.G * p.N;
-    dt = fminf(fmaxf(m3p_softplus(m3p_ld(p, b, l, o + h) + p.dt_bias[h]), p.dt_lo), p.dt_hi);
-    da = dt * -fmaxf(m3p_softplus(m3p_ld(p, b, l, o + p.H + h)), p.a_floor);
-    lam = 1.f / (1.f + __expf(-m3p_ld(p, b, l, o + 2 * p.H + h)));
+    m3_coef(m3p_ld(p, b, l, o + h), m3p_ld(p, b, l, o + p.H + h), m3p_ld(p, b, l, o + 2 * p.H + h), p.dt_bias[h],
+            p.a_floor, p.dt_lo, p.dt_hi, dt, da, lam);
 }
 
 // Beta seed of the initial state: reads the previous token's K / v_state
@@ -131,7 +131,7 @@ __global__ __launch_bounds__(256) void mamba3_prep_kernel(M3PrepParams p) {
     const int cp = t % np1, rp0 = t / np1, rsp = np1 >= 256 ? 1 : 256 / np1;
     const int cx = t % P, rx0 = t / P, rsx = P >= 256 ? 1 : 256 / P;
 
-    float theta = (t < A) ? p.ang[bh * A + t] : 0.f;
+    long long theta = (t < A) ? m3_ang_fix(p.ang[bh * A + t]) : 0ll;  // grid units
     for (int l0 = 0; l0 < p.L; l0 += TS) {
         const int nt = min(TS, p.L - l0);
         // coefficients of the tile (+ the next position for scale)
@@ -166,10 +166,10 @@ __global__ __launch_bounds__(256) void mamba3_prep_kernel(M3PrepParams p) {
         __syncthreads();
         // angle increments dt range pi tanh(rot), spread over all threads
         if (A <= 256) {
-            for (int r = ra0; r < nt; r += rsa) s_th[r * A + ca] = s_dt[r] * (tanhf(s_th[r * A + ca]) * p.span);
+            for (int r = ra0; r < nt; r += rsa) s_th[r * A + ca] = m3_angle_inc(s_dt[r], s_th[r * A + ca], p.span);
         } else {
             for (int r = 0; r < nt; ++r)
-                for (int k = t; k < A; k += 256) s_th[r * A + k] = s_dt[r] * (tanhf(s_th[r * A + k]) * p.span);
+                for (int k = t; k < A; k += 256) s_th[r * A + k] = m3_angle_inc(s_dt[r], s_th[r * A + k], p.span);
         }
         // QK-norm sums of squares: 2 TS rows, one wave per row (strided)
         for (int rr = wave; rr < 2 * TS; rr += 4) {
@@ -177,18 +177,18 @@ __global__ __launch_bounds__(256) void mamba3_prep_kernel(M3PrepParams p) {
             float ss = 0.f;
             for (int n = lane; n < N; n += 64) ss += src[n] * src[n];
             ss = wave_sum(ss);
-            if (lane == 0) s_rms[rr] = 1.f / sqrtf(ss / (float)N + 8.1584695e-8f);
+            if (lane == 0) s_rms[rr] = m3_rms_inv(ss, N);
         }
         __syncthreads();
-        // cumulative angle: sequential per angle over the tile (LDS only), wrapped at every position
+        // cumulative angle: sequential per angle over the tile (LDS only), on the fixed-point grid
         if (t < A)
             for (int r = 0; r < nt; ++r) {
-                theta = m3p_wrap(theta + s_th[r * A + t]);
-                s_th[r * A + t] = theta;
+                theta = m3_ang_reduce(theta + m3_ang_fix(s_th[r * A + t]));
+                s_th[r * A + t] = m3_ang_rad(theta);
             }
         // normalise + bias in place
         for (int r = row0; r < 2 * TS; r += RS)
-            s_raw[r * N + col] = (s_raw[r * N + col] * s_rms[r]) * (r < TS ? bnw : cnw) + (r < TS ? bbias : cbias);
+            s_raw[r * N + col] = m3_norm(s_raw[r * N + col], s_rms[r], r < TS ? bnw : cnw, r < TS ? bbias : cbias);
         __syncthreads();
         // cos / sin of the rotated pairs' angles, spread over all threads
         if (npair > 0 && npair <= 256) {
@@ -213,7 +213,7 @@ __global__ __launch_bounds__(256) void mamba3_prep_kernel(M3PrepParams p) {
             if (rotated) {
                 const float cs = s_cs[rr * npair + k_of], sn = s_sn[rr * npair + k_of];
                 const float o = s_raw[r * N + partner];
-                v = first ? cs * v - sn * o : sn * o + cs * v;
+                v = m3_rot(cs, v, first ? -sn : sn, o);
             }
             const int64_t oi = ((((int64_t)b * p.L + l0 + rr) * p.M + m) * p.H + h) * N + col;
             m3p_st(p.io_bf16, r < TS ? p.Bo : p.Co, oi, v);
@@ -233,12 +233,12 @@ __global__ __launch_bounds__(256) void mamba3_prep_kernel(M3PrepParams p) {
             const float gmv = s_lam[t] * s_dt[t];
             p.da[o] = s_da[t];
             p.gm[o] = gmv;
-            p.sc[o] = gmv + (1.f - s_lam[t + 1]) * s_dt[t + 1];
+            p.sc[o] = __builtin_fmaf(1.f - s_lam[t + 1], s_dt[t + 1], gmv);
         }
         // the rest of the cache tail (m == 0): the last x and the wrapped angle
         if (l0 + nt == p.L && m == 0) {
             for (int pp = t; pp < P; pp += 256) p.vst[bh * P + pp] = s_x[(nt - 1) * P + pp];
-            if (t < A) p.ang_out[bh * A + t] = theta;
+            if (t < A) p.ang_out[bh * A + t] = m3_ang_rad(theta);
         }
         __syncthreads();  // LDS reuse by the next tile
     }
@@ -246,10 +246,10 @@ __global__ __launch_bounds__(256) void mamba3_prep_kernel(M3PrepParams p) {
 
 // ---- segment-parallel fast path -------------------------------------------
 // The sequence is cut into segments of kM3Seg positions.  A first kernel sums
-// each segment's angle increments dt range pi tanh(rot) per (head, angle) in
-// f64; the main kernel then runs one workgroup per (b, h, segment) over every
-// MIMO rank, starting from the wrapped sum of the earlier segments' totals, and
-// carries the angle wrapped at every position inside its segment.  Loads and
+// each segment's angle increments dt range pi tanh(rot) per (head, angle) on
+// the fixed-point angle grid; the main kernel then runs one workgroup per (b,
+// h, segment) over every MIMO rank, starting from the cache's angle plus the
+// earlier segments' totals, and adds the increments position by position.  Loads and
 // stores of proj rows, B, C and v are 8- or 4-wide vectors; proj and the
 // outputs are typed by template parameters.
 constexpr int kM3Seg = 256, kM3Tile = 32;
@@ -322,11 +322,6 @@ template <> __device__ __forceinline__ void m3_st4<bf16_t>(bf16_t* q, const floa
     *(uint2*)q = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
 }
 
-__device__ __forceinline__ double m3_wrap_d(double a) {
-    const double two_pi = 6.283185307179586476925286766559;
-    return a - rint(a / two_pi) * two_pi;
-}
-
 template <typename TP>
 __device__ __forceinline__ void m3_coef_t(const M3PrepParams& p, const TP* proj, int b, int l, int h, float& dt,
                                           float& da, float& lam) {
@@ -335,19 +330,19 @@ __device__ __forceinline__ void m3_coef_t(const M3PrepParams& p, const TP* proj,
         return;
     }
     const TP* row = proj + (int64_t)b * p.proj_sb + (int64_t)l * p.proj_sl + 2 * p.H * p.P + 2 * p.M * p.G * p.N;
-    dt = fminf(fmaxf(m3p_softplus(m3_ld1(row + h) + p.dt_bias[h]), p.dt_lo), p.dt_hi);
-    da = dt * -fmaxf(m3p_softplus(m3_ld1(row + p.H + h)), p.a_floor);
-    lam = 1.f / (1.f + __expf(-m3_ld1(row + 2 * p.H + h)));
+    m3_coef(m3_ld1(row + h), m3_ld1(row + p.H + h), m3_ld1(row + 2 * p.H + h), p.dt_bias[h], p.a_floor, p.dt_lo,
+            p.dt_hi, dt, da, lam);
 }
 
 // Per (b, segment): tot[b][seg][h][a] = sum over the segment's positions of
-// dt[b, l, h] * (tanh(rot[b, l, a]) * span), each term rounded to f32 exactly
-// as the main kernel forms it, the sum in f64.  Grid (b * nseg, head groups):
+// dt[b, l, h] * (tanh(rot[b, l, a]) * span), each term formed exactly as the
+// main kernel forms it and put on the fixed-point angle grid, the sum reduced
+// modulo 2 pi on that grid.  Grid (b * nseg, head groups):
 // a workgroup takes hpw heads (hpw * A <= 256 where possible, one (h, a) pair
 // per thread) so that b * nseg * H / hpw workgroups share the segments.
 // Dynamic LDS: [tile][hpw] dt and [tile][A] tanh(rot) * span.
 template <typename TP>
-__global__ __launch_bounds__(256) void mamba3_angle_tot_kernel(M3PrepParams p, int nseg, int hpw, double* tot) {
+__global__ __launch_bounds__(256) void mamba3_angle_tot_kernel(M3PrepParams p, int nseg, int hpw, long long* tot) {
     const int b = blockIdx.x / nseg, seg = blockIdx.x % nseg, t = threadIdx.x;
     const TP* proj = static_cast<const TP*>(p.proj);
     const int H = p.H, A = p.A, HA = H * A;
@@ -359,9 +354,9 @@ __global__ __launch_bounds__(256) void mamba3_angle_tot_kernel(M3PrepParams p, i
     float* s_tr = s_dtt + kM3Tile * hpw;   // [kM3Tile][A]
     constexpr int KP = 4;                  // (h, a) pairs per thread and pass
     for (int pb = 0; pb < np; pb += 256 * KP) {
-        double acc[KP];
+        long long acc[KP];
 #pragma unroll
-        for (int k = 0; k < KP; ++k) acc[k] = 0.0;
+        for (int k = 0; k < KP; ++k) acc[k] = 0ll;
         for (int l0 = l_begin; l0 < l_end; l0 += kM3Tile) {
             const int nt = min(kM3Tile, l_end - l0);
             for (int i = t; i < kM3Tile * nh; i += 256) {
@@ -372,8 +367,7 @@ __global__ __launch_bounds__(256) void mamba3_angle_tot_kernel(M3PrepParams p, i
             }
             for (int i = t; i < kM3Tile * A; i += 256) {
                 const int r = i / A, a = i % A;
-                s_tr[i] = r < nt ? m3_tanh(m3_ld1(proj + (int64_t)b * p.proj_sb + (int64_t)(l0 + r) * p.proj_sl +
-                                                  o_rot + a)) * p.span
+                s_tr[i] = r < nt ? m3_ld1(proj + (int64_t)b * p.proj_sb + (int64_t)(l0 + r) * p.proj_sl + o_rot + a)
                                  : 0.f;
             }
             __syncthreads();
@@ -382,9 +376,10 @@ __global__ __launch_bounds__(256) void mamba3_angle_tot_kernel(M3PrepParams p, i
                 const int i = pb + t + 256 * k;
                 if (i < np) {
                     const int hl = i / A, a = i % A;
-                    double sacc = acc[k];
-                    for (int r = 0; r < nt; ++r) sacc += (double)(s_dtt[r * hpw + hl] * s_tr[r * A + a]);
-                    acc[k] = sacc;
+                    long long sacc = acc[k];
+                    for (int r = 0; r < nt; ++r)
+                        sacc += m3_ang_fix(m3_angle_inc(s_dtt[r * hpw + hl], s_tr[r * A + a], p.span));
+                    acc[k] = m3_ang_reduce(sacc);
                 }
             }
             __syncthreads();
@@ -406,7 +401,7 @@ __global__ __launch_bounds__(256) void mamba3_angle_tot_kernel(M3PrepParams p, i
 // rank) and its column block for the whole segment; otherwise the rows are
 // decomposed per pass.
 template <typename TP, typename TO, int N>
-__global__ __launch_bounds__(256) void mamba3_prep_seg_kernel(M3PrepParams p, int nseg, const double* tot) {
+__global__ __launch_bounds__(256) void mamba3_prep_seg_kernel(M3PrepParams p, int nseg, const long long* tot) {
     constexpr int TPR = N / 8;         // threads per B/C row (8 columns each)
     constexpr int RPP = 256 / TPR;     // rows per pass
     constexpr int W = N / 2;           // pair indices
@@ -425,12 +420,12 @@ __global__ __launch_bounds__(256) void mamba3_prep_seg_kernel(M3PrepParams p, in
     float* s_sn = s_cs + kM3Tile * W;      // [kM3Tile][W]
     __shared__ float s_dt[kM3Tile + 1], s_lam[kM3Tile + 1], s_da[kM3Tile];
 
-    // starting angle of the segment: the cache's angle plus the earlier segments' totals
-    float theta = 0.f;
+    // starting angle of the segment (grid units): the cache's angle plus the earlier segments' totals
+    long long theta = 0ll;
     if (t < A) {
-        double acc = p.ang[bh * A + t];
-        for (int s2 = 0; s2 < seg; ++s2) acc += tot[((int64_t)b * nseg + s2) * p.H * A + (int64_t)h * A + t];
-        theta = (float)m3_wrap_d(acc);
+        theta = m3_ang_fix(p.ang[bh * A + t]);
+        for (int s2 = 0; s2 < seg; ++s2)
+            theta = m3_ang_reduce(theta + tot[((int64_t)b * nseg + s2) * p.H * A + (int64_t)h * A + t]);
     }
     // this thread's 8 columns of every B/C row, their pair indices and rotation sign
     const int col0 = (t % TPR) * 8, rsub = t / TPR;
@@ -462,13 +457,11 @@ __global__ __launch_bounds__(256) void mamba3_prep_seg_kernel(M3PrepParams p, in
     };
     auto bc_finish = [&](int l0, int r, int which, int m, const float* w, const float* bias, float* y) {
         const int l = l0 + r;
-        float ss = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ss += y[e] * y[e];
+        float ss = m3_sumsq8(y);
         ss = m3_group_sum<TPR>(ss);
-        const float rms = 1.f / sqrtf(ss / (float)N + 8.1584695e-8f);
+        const float rms = m3_rms_inv(ss, N);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) y[e] = (y[e] * rms) * w[e] + bias[e];
+        for (int e = 0; e < 8; ++e) y[e] = m3_norm(y[e], rms, w[e], bias[e]);
         const float* csr = (const float*)__builtin_assume_aligned(s_cs + r * W + kbase, 16);
         const float* snr = (const float*)__builtin_assume_aligned(s_sn + r * W + kbase, 16);
         if (pairwise) {
@@ -477,8 +470,8 @@ __global__ __launch_bounds__(256) void mamba3_prep_seg_kernel(M3PrepParams p, in
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const float y0 = y[2 * j], y1 = y[2 * j + 1];
-                y[2 * j] = cv[j] * y0 - sv[j] * y1;
-                y[2 * j + 1] = sv[j] * y0 + cv[j] * y1;
+                y[2 * j] = m3_rot(cv[j], y0, -sv[j], y1);
+                y[2 * j + 1] = m3_rot(cv[j], y1, sv[j], y0);
             }
         } else if (TPR == 1) {  // N == 8: the pairs (k, k + 4) are both in this thread
             const float4 c4 = *(const float4*)csr, s4 = *(const float4*)snr;
@@ -486,8 +479,8 @@ __global__ __launch_bounds__(256) void mamba3_prep_seg_kernel(M3PrepParams p, in
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const float y0 = y[j], y1 = y[j + 4];
-                y[j] = cv[j] * y0 - sv[j] * y1;
-                y[j + 4] = sv[j] * y0 + cv[j] * y1;
+                y[j] = m3_rot(cv[j], y0, -sv[j], y1);
+                y[j + 4] = m3_rot(cv[j], y1, sv[j], y0);
             }
         } else {
             float o[8];
@@ -498,7 +491,7 @@ __global__ __launch_bounds__(256) void mamba3_prep_seg_kernel(M3PrepParams p, in
             const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
             const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
 #pragma unroll
-            for (int e = 0; e < 8; ++e) y[e] = cv[e] * y[e] + (sgn * sv[e]) * o[e];
+            for (int e = 0; e < 8; ++e) y[e] = m3_rot(cv[e], y[e], sgn * sv[e], o[e]);
         }
         const int64_t oi = ((((int64_t)b * p.L + l) * M + m) * p.H + h) * N + col0;
         m3_st8(static_cast<TO*>(which ? p.Co : p.Bo) + oi, y);
@@ -530,26 +523,21 @@ __global__ __launch_bounds__(256) void mamba3_prep_seg_kernel(M3PrepParams p, in
         // angle increments dt range pi tanh(rot)
         for (int i = t; i < nt * A; i += 256) {
             const int r = i / A, a = i - r * A;
-            s_th[r * A4 + a] =
-                s_dt[r] * (m3_tanh(m3_ld1(projb + (int64_t)(l0 + r) * p.proj_sl + o_rot + a)) * p.span);
+            s_th[r * A4 + a] = m3_angle_inc(s_dt[r], m3_ld1(projb + (int64_t)(l0 + r) * p.proj_sl + o_rot + a), p.span);
         }
         __syncthreads();
-        // cumulative angle, wrapped at every position
+        // cumulative angle on the fixed-point grid, in radians ([-pi, pi]) at every position
         if (t < A)
             for (int r = 0; r < nt; ++r) {
-                theta = m3p_wrap(theta + s_th[r * A4 + t]);
-                s_th[r * A4 + t] = theta;
+                theta = m3_ang_reduce(theta + m3_ang_fix(s_th[r * A4 + t]));
+                s_th[r * A4 + t] = m3_ang_rad(theta);
             }
         __syncthreads();
         // cos / sin of the wrapped angles (|angle| <= pi); identity past the rotated pairs
         for (int i = t; i < nt * W; i += 256) {
             const int r = i / W, k = i % W;
             float c = 1.f, sn = 0.f;
-            if (k < npair) {
-                const float th = s_th[r * A4 + k];
-                c = __cosf(th);
-                sn = __sinf(th);
-            }
+            if (k < npair) m3_cossin(s_th[r * A4 + k], c, sn);
             s_cs[i] = c;
             s_sn[i] = sn;
         }
@@ -621,13 +609,13 @@ __global__ __launch_bounds__(256) void mamba3_prep_seg_kernel(M3PrepParams p, in
             const float gmv = s_lam[t] * s_dt[t];
             p.da[o] = s_da[t];
             p.gm[o] = gmv;
-            p.sc[o] = gmv + (1.f - s_lam[t + 1]) * s_dt[t + 1];
+            p.sc[o] = __builtin_fmaf(1.f - s_lam[t + 1], s_dt[t + 1], gmv);
         }
         // the rest of the cache tail: the last x and the wrapped angle
         if (l0 + nt == p.L) {
             for (int pp = t; pp < P; pp += 256)
                 p.vst[bh * P + pp] = m3_ld1(projb + (int64_t)(p.L - 1) * p.proj_sl + d_inner + h * P + pp);
-            if (t < A) p.ang_out[bh * A + t] = theta;
+            if (t < A) p.ang_out[bh * A + t] = m3_ang_rad(theta);
         }
         __syncthreads();  // LDS reuse by the next tile
     }
@@ -818,11 +806,11 @@ extern "C" size_t mamba3_prep_workspace_size(const mamba3_prep_args* a) {
     if (m3_prep_params(a, &p, true) != MAMBA_OK) return 0;
     const int nseg = m3_nseg(p);
     if (!m3_prep_fast(p) || nseg == 1) return 0;
-    return (size_t)p.nb * nseg * p.H * p.A * sizeof(double);
+    return (size_t)p.nb * nseg * p.H * p.A * sizeof(long long);
 }
 
 template <typename TP, typename TO>
-static void m3_launch_fast(const M3PrepParams& p, double* tot, hipStream_t s) {
+static void m3_launch_fast(const M3PrepParams& p, long long* tot, hipStream_t s) {
     const int nseg = m3_nseg(p);
     if (nseg > 1) {
         const int hpw = p.A >= 256 ? 1 : (256 / p.A < p.H ? 256 / p.A : p.H);  // heads per workgroup
@@ -832,7 +820,7 @@ static void m3_launch_fast(const M3PrepParams& p, double* tot, hipStream_t s) {
     const dim3 grid(p.nb * p.H * nseg), block(256);
     const size_t lds = (size_t)kM3Tile * (((p.A + 3) & ~3) + p.N) * sizeof(float);
 #define MAMBA3_SEG_N(NN) \
-    hipLaunchKernelGGL((mamba3_prep_seg_kernel<TP, TO, NN>), grid, block, lds, s, p, nseg, (const double*)tot);
+    hipLaunchKernelGGL((mamba3_prep_seg_kernel<TP, TO, NN>), grid, block, lds, s, p, nseg, (const long long*)tot);
     switch (p.N) {
         case 8: MAMBA3_SEG_N(8) break;
         case 16: MAMBA3_SEG_N(16) break;
@@ -858,7 +846,7 @@ extern "C" int mamba3_prep_fwd(const mamba3_prep_args* a, void* workspace, size_
     m3_launch_seed(p, s);
     MAMBA_CHECK_LAUNCH();
     if (m3_prep_fast(p)) {
-        double* tot = (double*)workspace;
+        long long* tot = (long long*)workspace;
         if (p.proj_bf16 && p.io_bf16) m3_launch_fast<bf16_t, bf16_t>(p, tot, s);
         else if (p.proj_bf16) m3_launch_fast<bf16_t, float>(p, tot, s);
         else if (p.io_bf16) m3_launch_fast<float, bf16_t>(p, tot, s);

@@ -1,8 +1,8 @@
 // Shared pieces of the Mamba-3 single-SSD MFMA scans (bf16 operands, f32
 // accumulators, headdim 64 in two 32-wide halves, dstate 128, 128 fused
-// positions per chunk): the MFMA helpers, the per-workgroup LDS layout and the
-// y tile of one wave.  Included by the SSD-seam kernel and by the fused
-// prologue + SSD kernel.
+// positions per chunk): the MFMA helpers, the per-workgroup LDS layout, and
+// the y tile and the state update of one wave.  Included by the SSD-seam
+// kernel and by the fused prologue + SSD kernel.
 #pragma once
 
 #include "common.h"
@@ -41,14 +41,32 @@ __device__ __forceinline__ float s3_bld4(__amdgpu_buffer_rsrc_t r, uint32_t off)
 __device__ __forceinline__ float s3_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float s3_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// LDS of one workgroup (about 83 KB at QF = 128).
-template <int QF>
+// Two-term bf16 operands.  The inputs (v, B, C) are bf16, but three operands
+// of the scan are formed inside it in f32: the state entering a chunk (the A
+// operand of C.h), the decay-weighted C.B^T (the B operand of v^T.M) and the
+// weighted v^T of the state update.  Each is carried as hi + lo, two bf16
+// values with hi = bf16(x) and lo = bf16(x - hi) (about 16 significant bits),
+// and enters its product as two MFMAs, so that the products are exact to
+// ~2^-17 relative instead of bf16's 2^-9: with QK-normed B / C (|C.B| ~ N) a
+// single bf16 rounding of these operands moves outputs near zero by more than
+// 1e-2.
+__device__ __forceinline__ __bf16 s3_h16(float x) { return (__bf16)x; }
+__device__ __forceinline__ __bf16 s3_l16(float x) { return (__bf16)(x - (float)(__bf16)x); }
+
+// LDS of one workgroup (about 109 KB at QF = 128 with HB = 2).  HB: buffers
+// of the chunk-entry state (2: the next chunk's state is written while this
+// chunk's is read; 1: the writer waits for the next chunk).  NY: y tiles
+// staged for the store (one per wave; a caller that stores y straight from
+// its accumulators keeps one unused tile).
+template <int QF, int HB = 2, int NY = 4>
 struct __align__(16) Ssd3Lds {
     bf16_t xT[32][QF + 8];      // v^T of the chunk (headdim half x positions)
-    bf16_t xTw[32][QF + 8];     // w_j v^T[p][j], the state GEMM's A operand
+    bf16_t xTw[32][QF + 8];     // w_j v^T[p][j], the state GEMM's A operand (hi part)
+    bf16_t xTwl[32][QF + 8];    // its lo part
     bf16_t B[QF][136];          // B rows of the chunk (positions x dstate)
-    bf16_t h[2][32][136];       // state entering the chunk (bf16 MFMA operand), double-buffered
-    bf16_t y[4][32][40];        // per-wave y tile staging
+    bf16_t h[HB][32][136];      // state entering the chunk (MFMA operand, hi part)
+    bf16_t hl[HB][32][136];     // its lo part
+    bf16_t y[NY][32][40];       // per-wave y tile staging
     float cs2[QF];              // within-chunk cumulative da, log2 units
     float sc[QF], gm[QF];       // scale and gamma per position
     float st[QF];               // step index of each position (read per chunk: keeps the
@@ -66,8 +84,8 @@ struct __align__(16) Ssd3Lds {
 // LEAN: a scheduling barrier between the lower-tile blocks, so that the
 // compiler does not hoist every block's LDS operands at once (for callers
 // that run two waves per SIMD within 256 registers).
-template <int QF, int IT, bool LEAN = false>
-__device__ __forceinline__ void ssd3_y_tile(Ssd3Lds<QF>& S, const s3_bf16x8_t (&cfr)[8], int cur, int r, int half,
+template <int QF, int IT, bool LEAN = false, int HB, int NY>
+__device__ __forceinline__ void ssd3_y_tile(Ssd3Lds<QF, HB, NY>& S, const s3_bf16x8_t (&cfr)[8], int cur, int r, int half,
                                             s3_f32x16_t& y) {
     constexpr int NK = 8;
     const int il = IT * 32 + r;
@@ -77,8 +95,10 @@ __device__ __forceinline__ void ssd3_y_tile(Ssd3Lds<QF>& S, const s3_bf16x8_t (&
     const float ti = S.st[il];  // chunks and tiles start on step boundaries
     y = s3_zero();
 #pragma unroll
-    for (int kn = 0; kn < NK; ++kn)
+    for (int kn = 0; kn < NK; ++kn) {
         y = s3_mfma(*(const s3_bf16x8_t*)&S.h[cur][r][kn * 16 + 8 * half], cfr[kn], y);
+        y = s3_mfma(*(const s3_bf16x8_t*)&S.hl[cur][r][kn * 16 + 8 * half], cfr[kn], y);
+    }
     {
         const float e0 = __builtin_amdgcn_exp2f(cs_r0);
 #pragma unroll
@@ -121,16 +141,55 @@ __device__ __forceinline__ void ssd3_y_tile(Ssd3Lds<QF>& S, const s3_bf16x8_t (&
         }
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-            s3_bf16x8_t bop;
+            s3_bf16x8_t bop, bopl;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) bop[e] = (__bf16)(d[8 * kk + e] * fac[8 * kk + e]);
+            for (int e = 0; e < 8; ++e) {
+                const float x = d[8 * kk + e] * fac[8 * kk + e];
+                bop[e] = s3_h16(x);
+                bopl[e] = s3_l16(x);
+            }
             // v^T[p][j] in the same permuted k order: j = 32 jt + 16 kk + 4 half + {0..3, 8..11}
             const int j0 = jt * 32 + 16 * kk + 4 * half;
             const s3_bf16x4_t lo = *(const s3_bf16x4_t*)&S.xT[r][j0];
             const s3_bf16x4_t hi = *(const s3_bf16x4_t*)&S.xT[r][j0 + 8];
             const s3_bf16x8_t a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
             y = s3_mfma(a, bop, y);
+            y = s3_mfma(a, bopl, y);
         }
+    }
+}
+
+// The chunk-entry state of one wave's dstate tile (columns 32 nt .. 32 nt + 31,
+// accumulator layout: row 8 (v / 4) + 4 half + v % 4, column r) into buffer
+// `buf` as hi + lo.
+template <int QF, int HB, int NY>
+__device__ __forceinline__ void ssd3_put_state(Ssd3Lds<QF, HB, NY>& S, const s3_f32x16_t& h, int buf, int nt, int r,
+                                               int half) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const int row = 8 * (v >> 2) + 4 * half + (v & 3);
+        S.h[buf][row][nt * 32 + r] = __builtin_bit_cast(bf16_t, s3_h16(h[v]));
+        S.hl[buf][row][nt * 32 + r] = __builtin_bit_cast(bf16_t, s3_l16(h[v]));
+    }
+}
+
+// One wave's state update h <- h + sum_j (w_j v^T[p][j]) B[j][n] over the
+// chunk (the caller has applied exp(cs_end)), n tile = nt; the B operand is
+// gathered column-wise from the row-major B tile, the weighted v^T enters as
+// hi + lo.
+template <int QF, int HB, int NY>
+__device__ __forceinline__ void ssd3_state_update(Ssd3Lds<QF, HB, NY>& S, s3_f32x16_t& h, int nt, int r, int half) {
+    constexpr int KS = QF / 16;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        const int j0 = ks * 16 + 8 * half;
+        const s3_bf16x8_t a = *(const s3_bf16x8_t*)&S.xTw[r][j0];
+        const s3_bf16x8_t al = *(const s3_bf16x8_t*)&S.xTwl[r][j0];
+        s3_bf16x8_t bo;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) bo[e] = __builtin_bit_cast(__bf16, S.B[j0 + e][nt * 32 + r]);
+        h = s3_mfma(a, bo, h);
+        h = s3_mfma(al, bo, h);
     }
 }
 

@@ -50,7 +50,6 @@ __global__ __launch_bounds__(256, 1) void ssd3_scan_mfma(Ssd3MfmaParams p) {
     constexpr int T = QF / 32;            // output tiles per chunk (one per wave)
     static_assert(T == 4, "one output tile per wave");
     constexpr int NK = N / 16;            // k-steps over dstate
-    constexpr int KS = QF / 16;           // k-steps over the chunk
     constexpr int XI = (QF / 2) * 4;      // v staging items: (position pair, 8-wide headdim piece)
     constexpr int BI = (QF / 2) * (N / 8);  // B staging items: (position pair, 8-wide dstate piece)
     constexpr int XPT = (XI + 255) / 256, BPT = BI / 256;
@@ -75,9 +74,7 @@ __global__ __launch_bounds__(256, 1) void ssd3_scan_mfma(Ssd3MfmaParams p) {
         const int pp = p0 + 8 * (v >> 2) + 4 * half + (v & 3);
         hacc[v] = p.h0 ? p.h0[hbase + pp * N + wave * 32 + r] : 0.f;
     }
-#pragma unroll
-    for (int v = 0; v < 16; ++v)
-        S.h[0][8 * (v >> 2) + 4 * half + (v & 3)][wave * 32 + r] = __builtin_bit_cast(bf16_t, (__bf16)hacc[v]);
+    ssd3_put_state(S, hacc, 0, wave, r, half);
 
     const bf16_t* vhead = p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh + p0;
     const bf16_t* bhead = p.Bm + (int64_t)b * p.B_sb + (int64_t)g * p.B_sg;
@@ -195,11 +192,14 @@ __global__ __launch_bounds__(256, 1) void ssd3_scan_mfma(Ssd3MfmaParams p) {
                 for (int e = 0; e < 4; ++e) {
                     *(uint32_t*)&S.xT[pv * 8 + 2 * e][2 * fp] = (a0[e] & 0xffffu) | (a1[e] << 16);
                     *(uint32_t*)&S.xT[pv * 8 + 2 * e + 1][2 * fp] = (a0[e] >> 16) | (a1[e] & 0xffff0000u);
-                    const s3_bf16x4_t q = {(__bf16)(s3_lo(a0[e]) * w0), (__bf16)(s3_lo(a1[e]) * w1),
-                                           (__bf16)(s3_hi(a0[e]) * w0), (__bf16)(s3_hi(a1[e]) * w1)};
-                    const uint2 qq = __builtin_bit_cast(uint2, q);
+                    const float wv[4] = {s3_lo(a0[e]) * w0, s3_lo(a1[e]) * w1, s3_hi(a0[e]) * w0, s3_hi(a1[e]) * w1};
+                    const s3_bf16x4_t q = {s3_h16(wv[0]), s3_h16(wv[1]), s3_h16(wv[2]), s3_h16(wv[3])};
+                    const s3_bf16x4_t ql = {s3_l16(wv[0]), s3_l16(wv[1]), s3_l16(wv[2]), s3_l16(wv[3])};
+                    const uint2 qq = __builtin_bit_cast(uint2, q), qql = __builtin_bit_cast(uint2, ql);
                     *(uint32_t*)&S.xTw[pv * 8 + 2 * e][2 * fp] = qq.x;
                     *(uint32_t*)&S.xTw[pv * 8 + 2 * e + 1][2 * fp] = qq.y;
+                    *(uint32_t*)&S.xTwl[pv * 8 + 2 * e][2 * fp] = qql.x;
+                    *(uint32_t*)&S.xTwl[pv * 8 + 2 * e + 1][2 * fp] = qql.y;
                 }
             }
         }
@@ -209,25 +209,13 @@ __global__ __launch_bounds__(256, 1) void ssd3_scan_mfma(Ssd3MfmaParams p) {
         // ---- the next chunk's loads land during this chunk's MFMA work
         if (c + 1 < p.nch) fetch(c + 1);
         __syncthreads();
-        // ---- state: h <- exp(cs_end) h + sum_j (w_j v^T[p][j]) B[j][n], n tile = wave;
-        // the B operand is gathered column-wise from the row-major B tile
+        // ---- state: h <- exp(cs_end) h + sum_j (w_j v^T[p][j]) B[j][n], n tile = wave
         {
             const float dec = __builtin_amdgcn_exp2f(cs_end);
 #pragma unroll
             for (int v = 0; v < 16; ++v) hacc[v] *= dec;
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                const int j0 = ks * 16 + 8 * half;
-                const s3_bf16x8_t a = *(const s3_bf16x8_t*)&S.xTw[r][j0];
-                s3_bf16x8_t bo;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) bo[e] = __builtin_bit_cast(__bf16, S.B[j0 + e][wave * 32 + r]);
-                hacc = s3_mfma(a, bo, hacc);
-            }
-#pragma unroll
-            for (int v = 0; v < 16; ++v)
-                S.h[cur ^ 1][8 * (v >> 2) + 4 * half + (v & 3)][wave * 32 + r] =
-                    __builtin_bit_cast(bf16_t, (__bf16)hacc[v]);
+            ssd3_state_update(S, hacc, wave, r, half);
+            ssd3_put_state(S, hacc, cur ^ 1, wave, r, half);
         }
         // ---- y for output tile = wave
         {

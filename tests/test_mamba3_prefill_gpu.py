@@ -188,7 +188,7 @@ def test_mamba3_forward_double_equals_single(dtype, M):
         tdt, tol, stol = torch.float32, dict(rtol=1e-3, atol=1e-4), dict(rtol=1e-3, atol=1e-4)
     else:
         cfg = mamba_hip.Mamba3Config(d_model=128, state_rank=128, per_head_dim=64, mimo_rank=M)
-        tdt, tol, stol = torch.bfloat16, dict(rtol=0, atol=3e-2), dict(rtol=2e-2, atol=1e-2)
+        tdt, tol, stol = torch.bfloat16, dict(rtol=2e-2, atol=1e-2), dict(rtol=2e-2, atol=1e-2)
     gen = torch.Generator(device="cuda")
     gen.manual_seed(40 + M)
     m = cfg.init("cuda", tdt, gen)
@@ -206,8 +206,7 @@ def test_mamba3_forward_double_equals_single(dtype, M):
     torch.cuda.synchronize()
     assert cs.pathway == "single" and cd.pathway == "double"
     for o_s, o_d in outs:
-        scale = float(o_s.float().abs().max())
-        np.testing.assert_allclose(o_d.float().cpu().numpy() / scale, o_s.float().cpu().numpy() / scale, **tol)
+        np.testing.assert_allclose(o_d.float().cpu().numpy(), o_s.float().cpu().numpy(), **tol)
     for nm in ("ssm_bhpr", "k_state_bmhr", "v_state_bhp", "angle_bha"):
         np.testing.assert_allclose(getattr(cd, nm).cpu().numpy(), getattr(cs, nm).cpu().numpy(), **stol)
 

@@ -440,17 +440,19 @@ def test_fused_and_unfused_stacks_agree():
         np.testing.assert_allclose(a.conv_bvk.cpu().numpy(), e.conv_bvk.cpu().numpy(), **tol)
 
 
-def test_fused_stack_config3_layer_shape():
-    """BASELINE.json configs[3]'s layer shape at batch 64: d_model 2560, 80
-    heads x 64, dstate 128, conv width 4, in_proj 2560 -> 10576 and out_proj
-    5120 -> 2560 (the split-K products the benchmark runs).  Two fused layers
-    (one mamba2_stack_step call) step two tokens from random caches, against
+@pytest.mark.parametrize("b", [1, 16, 64, 256])
+def test_fused_stack_config3_layer_shape(b):
+    """BASELINE.json configs[3]'s layer shape at each of its batches (1, 16,
+    64, 256): d_model 2560, 80 heads x 64, dstate 128, conv width 4, in_proj
+    2560 -> 10576 and out_proj 5120 -> 2560 (the split-K products the
+    benchmark runs; batches 64 and 256 step as two half batches on two
+    streams).  Two fused layers step two tokens from random caches, against
     the oracle's pre-norm layer step (src/modules/layer.rs:224-228) on the same
     bf16 weights: outputs and both caches of every layer."""
     import torch
     import mamba_hip
     import oracle
-    b, d_model = 64, 2560
+    d_model = 2560
     cfg = mamba_hip.Mamba2Config(d_model=d_model)
     assert (cfg.nheads, cfg.d_in_proj, cfg.state_rank) == (80, 10576, 128)
     stack = mamba_hip.Mamba2Stack.init(cfg, 2, "cuda", torch.bfloat16, torch.Generator().manual_seed(64), fused=True)
