@@ -210,6 +210,85 @@ def bench_mamba1(args):
     }
 
 
+# The Mamba-1 block forward at the reference's own bench shape (benches/layer.rs:
+# batch 2, sequence 256, d_model 256, state_rank 16 for Mamba-1, f32), whose
+# median the reference publishes (bench.md:17), and at the config-2 layer shape.
+MAMBA1_BLOCK_SHAPES = {
+    "ref": dict(batch=2, seqlen=256, d_model=256, dstate=16),
+    "cfg2": dict(batch=8, seqlen=2048, d_model=2560, dstate=16),
+}
+MAMBA1_BLOCK_PUBLISHED_MS = {"flex (CPU)": 71.78, "cuda": 23.36, "cuda + fusion + autotune": 40.56}
+
+
+def bench_mamba1_block(args):
+    """Mamba1::forward (src/mamba1/mamba1.rs:278-352) of one block from an
+    empty cache: in_proj, the causal conv (mamba2_conv_fwd without dt heads),
+    x_proj / dt_proj formed time-major, the selective scan (mamba1_scan_fwd
+    with dt bias, softplus, D and the silu gate fused) and out_proj, f32 with
+    reference-init weights.  `value` is tokens/s of the whole forward; the
+    roofline is the scan kernel's (HIP events around it, every call)."""
+    import torch
+
+    import mamba_hip
+    shp = dict(MAMBA1_BLOCK_SHAPES[args.m1_shape])
+    dev = torch.device("cuda:0")
+    cfg = mamba_hip.Mamba1Config(d_model=shp["d_model"], state_rank=shp["dstate"])
+    m = cfg.init("cuda", torch.Generator(device=dev).manual_seed(0))
+    x = torch.randn((shp["batch"], shp["seqlen"], shp["d_model"]), generator=torch.Generator(device=dev).manual_seed(1),
+                    device=dev)
+
+    def step(events=None):
+        m.forward(x, None, events=events)
+
+    ms_per_step, kern_ms = _time_steps(args, step)
+    scan = dict(batch=shp["batch"], dim=cfg.d_inner, seqlen=shp["seqlen"], dstate=shp["dstate"])
+    nbytes, _ = mamba1_algorithmic(scan)
+    tokens = shp["batch"] * shp["seqlen"]
+    achieved = nbytes / (kern_ms * 1e-3) / 1e9
+    out = {
+        "metric": f"Mamba-1 block forward tokens/s (B={shp['batch']} L={shp['seqlen']} d_model={shp['d_model']} "
+                  f"N={shp['dstate']}, f32) + scan % HBM roofline",
+        "value": tokens / (ms_per_step * 1e-3), "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (x ~ N(0,1), reference init, seed 0)",
+        "config": {"workload": f"mamba1_block_{args.m1_shape}", **shp, "d_inner": cfg.d_inner,
+                   "dt_rank": cfg.dt_rank, "entry": "Mamba1.forward (products on rocBLAS, conv + scan here)"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel_ms": kern_ms,
+                     "algorithmic_bytes": nbytes, "kernel": "mamba1 scan inside the block"},
+    }
+    if args.m1_shape == "ref":
+        # published medians of this row on other hardware (the reference's own shape)
+        out["reference_published_ms"] = dict(MAMBA1_BLOCK_PUBLISHED_MS, source="bench.md:17")
+    return out
+
+
+def cpu_baseline_mamba1_block(shape, budget_tokens=2048, seed=0):
+    """oracle.mamba1_block_fwd (f32 C restatement, OpenMP) on one batch row of
+    the same shape, at most `budget_tokens` tokens, scaled per token."""
+    import numpy as np
+
+    import oracle
+    import torch
+    import mamba_hip
+    shp = dict(MAMBA1_BLOCK_SHAPES[shape])
+    cfg = mamba_hip.Mamba1Config(d_model=shp["d_model"], state_rank=shp["dstate"])
+    m = cfg.init("cpu", torch.Generator().manual_seed(seed))
+    f = lambda t: None if t is None else t.float().numpy()  # noqa: E731
+    p = dict(in_proj_w=f(m.in_proj_w), conv_w=f(m.conv_w), conv_b=f(m.conv_b), x_proj_w=f(m.x_proj_w),
+             dt_proj_w=f(m.dt_proj_w), dt_proj_b=f(m.dt_proj_b), A=f(m.A), D=f(m.d), out_proj_w=f(m.out_proj_w))
+    L = min(shp["seqlen"], budget_tokens)
+    x = np.random.default_rng(seed).standard_normal((1, L, shp["d_model"])).astype(np.float32)
+    cs = np.zeros((1, cfg.d_inner, cfg.conv_kernel), np.float32)
+    ss = np.zeros((1, cfg.d_inner, cfg.state_rank), np.float32)
+    t0 = time.perf_counter()
+    oracle.mamba1_block_fwd(x, p, cs, ss, prec=32)
+    el = time.perf_counter() - t0
+    return {"value": L / el, "unit": "tokens/s", "cores": int(os.environ.get("OMP_NUM_THREADS", os.cpu_count())),
+            "kind": "port", "sample": f"one batch row, {L} tokens, f32 restatement of Mamba1::forward ({el:.2f} s)"}
+
+
 MAMBA1_STEP_CFG = dict(n_layers=64, dim=5120, dstate=16, conv_kernel=4)
 
 
@@ -1328,7 +1407,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", default="ssd2",
                     choices=["ssd2", "mamba1", "decode", "ssd3", "mamba3_fused", "mamba1_step", "mamba3_step",
-                             "mamba3_prep", "mamba2_block", "ssd2_bwd", "ssd3_bwd"])
+                             "mamba3_prep", "mamba2_block", "ssd2_bwd", "ssd3_bwd", "mamba1_block"])
+    ap.add_argument("--m1-shape", default="ref", choices=sorted(MAMBA1_BLOCK_SHAPES),
+                    help="mamba1_block: the reference's bench shape (ref) or config 2's layer shape (cfg2)")
     ap.add_argument("--batch", type=int, default=DECODE_CFG3["batch"], help="decode batch")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-split", action="store_true",
@@ -1345,7 +1426,10 @@ def main():
               "(the hot path shards by batch/head with no communication)",
               file=sys.stderr)
         sys.exit(2)
-    if args.workload == "ssd3_bwd":
+    if args.workload == "mamba1_block":
+        out = bench_mamba1_block(args)
+        base = (lambda: cpu_baseline_mamba1_block(args.m1_shape))
+    elif args.workload == "ssd3_bwd":
         out = bench_ssd3_bwd(args)
         base = (lambda: cpu_baseline_ssd3_bwd(SSD3_CFG4))
     elif args.workload == "ssd2_bwd":

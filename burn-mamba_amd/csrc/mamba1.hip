@@ -41,8 +41,16 @@ constexpr int kTT = 16;  // tokens per staged tile (32 measured slower: the stag
 
 // softplus(x) = log(1 + e^x); above 20 it equals x to f32 precision (the
 // reference's Burn softplus overflows to inf above ~88.7 instead).
+// softplus(x) = log1p(exp(x)), x itself above 20 (where the two agree in f32).
+// log1p through the hardware log with Goldberg's correction, log(u) e / (u - 1)
+// for u = 1 + e (a few ulp for every e > 0, no cancellation for small e): the
+// library log1pf is a long polynomial sequence, and the scan's tile applies
+// softplus to every (token, channel)
 __device__ __forceinline__ float m1_softplus(float x) {
-    return x > 20.f ? x : log1pf(__expf(x));
+    if (x > 20.f) return x;
+    const float e = __expf(x);
+    const float u = 1.f + e;
+    return u == 1.f ? e : __logf(u) * (e * __builtin_amdgcn_rcpf(u - 1.f));
 }
 
 __device__ __forceinline__ float quad_sum(float v) {

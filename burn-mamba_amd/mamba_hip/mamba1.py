@@ -255,6 +255,14 @@ class Mamba1Config:
         )
 
 
+def _wt(w: torch.Tensor, attr: str, col0: int) -> torch.Tensor:
+    """The contiguous transpose of w[:, col0:], made once, kept on the weight
+    and remade when the weight is updated in place (the derived-copy cache of
+    the decode products, mamba_hip.step)."""
+    from .step import _derived
+    return _derived(w, attr, lambda t: t[:, col0:].t().contiguous())
+
+
 @dataclass
 class Mamba1:
     """Mamba1 block, forward and step (parameters of src/mamba1/mamba1.rs:124-227);
@@ -279,11 +287,12 @@ class Mamba1:
         return Mamba1Cache(conv_bik=torch.zeros(batch, c.d_inner, c.conv_kernel, device=dev),
                            ssm_bir=torch.zeros(batch, c.d_inner, c.state_rank, device=dev))
 
-    def forward(self, x: torch.Tensor, cache: Optional[Mamba1Cache] = None):
+    def forward(self, x: torch.Tensor, cache: Optional[Mamba1Cache] = None, events=None):
         """Mamba1::forward (src/mamba1/mamba1.rs:278-352): x [b, l, d_model] ->
         (y [b, l, d_model], cache).  The cache (zero when None) supplies the
         initial conv window and SSM state and is updated in place, so a
-        sequence can be run in segments (chunked prefill, then step)."""
+        sequence can be run in segments (chunked prefill, then step).
+        `events` (start, stop) are recorded around the scan kernel."""
         c = self.cfg
         b, L, dm = x.shape
         if L < 1:
@@ -291,26 +300,32 @@ class Mamba1:
         if cache is None:
             cache = self.new_cache(b)
         di, r, n = c.d_inner, c.dt_rank, c.state_rank
-        x2 = x.reshape(b * L, dm).float()
-        # layer 1, in_proj, as its two halves so each is a dense [b, l, d_inner]
+        xf = x.float()
+        x2 = xf.reshape(b * L, dm)
+        # The scan streams u, delta, z and y as time-contiguous rows [b, d, l]
+        # (its tuned kernel reads 32-token tiles of whole 128-byte lines), so
+        # the products around it are formed in that layout: z and delta as
+        # W^T x^T per batch row, y consumed through its transposed view.
+        # layer 1, in_proj: the conv half channels-last [b, l, d_inner], the
+        # gate half z time-major [b, d_inner, l]
         xs = torch.mm(x2, self.in_proj_w[:, :di]).view(b, L, di)
-        res = torch.mm(x2, self.in_proj_w[:, di:]).view(b, L, di)
+        zt = torch.matmul(_wt(self.in_proj_w, "_mamba_t_res", di), xf.transpose(1, 2))
         # layer 2: causal conv over [cached window | xs] + SiLU; window updated
         u = conv1d_fwd(xs, cache.conv_bik, self.conv_w, self.conv_b)
         # ssm (mamba1.rs:366-399): x_proj, dt_proj (its bias and the softplus go
         # to the scan), then the selective scan with D u and the silu(res) gate
-        x_dbl = torch.mm(u.view(b * L, di), self.x_proj_w).view(b, L, r + 2 * n)
-        delta = torch.mm(x_dbl.view(b * L, r + 2 * n)[:, :r], self.dt_proj_w).view(b, L, di)
-        y = torch.empty((b, L, di), device=x.device, dtype=torch.float32)
+        # (x_proj and dt_proj time-major too: B and C then stream as whole rows)
+        ut = u.transpose(1, 2).contiguous()
+        x_dbl = torch.matmul(_wt(self.x_proj_w, "_mamba_t", 0), ut)          # [b, r + 2n, l]
+        dt = torch.matmul(_wt(self.dt_proj_w, "_mamba_t", 0), x_dbl[:, :r])  # [b, d_inner, l]
+        yt = torch.empty((b, di, L), device=x.device, dtype=torch.float32)
         final = torch.empty_like(cache.ssm_bir)
-        # [b, l, *] tensors as the scan's [b, d, l] views: u, delta, z and y
-        # share one stride pair
-        mamba1_scan(u.transpose(1, 2), delta.transpose(1, 2), self.A,
-                    x_dbl[:, :, r:r + n].transpose(1, 2), x_dbl[:, :, r + n:].transpose(1, 2),
-                    D=self.d, z=res.transpose(1, 2), delta_bias=self.dt_proj_b, delta_softplus=True,
-                    initial_state=cache.ssm_bir, y=y.transpose(1, 2), final_state=final)
+        mamba1_scan(ut, dt, self.A, x_dbl[:, r:r + n], x_dbl[:, r + n:],
+                    D=self.d, z=zt, delta_bias=self.dt_proj_b, delta_softplus=True,
+                    initial_state=cache.ssm_bir, y=yt, final_state=final, events=events)
         cache.ssm_bir.copy_(final)
-        return torch.mm(y.view(b * L, di), self.out_proj_w).view(b, L, dm), cache
+        return torch.matmul(yt.transpose(1, 2), self.out_proj_w), cache
+
 
     def step(self, x: torch.Tensor, cache: Optional[Mamba1Cache] = None):
         """Mamba1::step (mamba1.rs:533-612): returns (y [b, d_model], cache); the cache
