@@ -78,19 +78,8 @@ template <int K>
 __device__ __forceinline__ int m3f_shr(int x) {
     return __builtin_amdgcn_update_dpp(0, x, 0x110 + K, 0xf, 0xf, false);
 }
-template <int K>
-__device__ __forceinline__ long long m3f_shr64(long long x) {
-    const uint64_t u = (uint64_t)x;
-    const uint32_t lo = (uint32_t)m3f_shr<K>((int)(uint32_t)u), hi = (uint32_t)m3f_shr<K>((int)(uint32_t)(u >> 32));
-    return (long long)(((uint64_t)hi << 32) | lo);
-}
 // value of lane 8 (lane / 8) + 7: the last lane of each aligned group of 8 (ds_swizzle bit masks)
-__device__ __forceinline__ long long m3f_last8_64(long long x) {
-    const uint64_t u = (uint64_t)x;
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_swizzle((int)(uint32_t)u, 0x18 | (0x7 << 5));
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_swizzle((int)(uint32_t)(u >> 32), 0x18 | (0x7 << 5));
-    return (long long)(((uint64_t)hi << 32) | lo);
-}
+__device__ __forceinline__ int m3f_last8(int x) { return __builtin_amdgcn_ds_swizzle(x, 0x18 | (0x7 << 5)); }
 
 // Two rows (ranks m0 and m0 + 1 of one step) x 8 columns (8 nv ..) of raw
 // group-form B or C: the RMS over the row's 16 lanes, norm weight and bias,
@@ -279,7 +268,7 @@ __global__ __launch_bounds__(512, 1) void mamba3_ssd_fused(M3FusedParams p) {
     // waits at the loop head then count the same way on entry and on the back-edge
     // the cumulative angle of this thread's angle (grid units, mamba3_internal.h): loaded
     // before the prefetch
-    long long theta = (tid_ >> 3) < p.A ? m3_ang_fix(p.ang[bh * p.A + (tid_ >> 3)]) : 0ll;
+    int theta = (tid_ >> 3) < p.A ? m3_ang_fix(p.ang[bh * p.A + (tid_ >> 3)]) : 0;
     fetch(0);
     __builtin_amdgcn_sched_barrier(0);
     fetch_rows(0);
@@ -347,25 +336,28 @@ __global__ __launch_bounds__(512, 1) void mamba3_ssd_fused(M3FusedParams p) {
         {
             // increments on the fixed-point angle grid: integer sums, so every
             // position's angle is the one the segment prep forms
-            long long cum[JA];
-            long long run = 0ll;
+            // (every term canonical, |.| <= pi on the grid: the partial sums
+            // below stay far from int32 overflow)
+            int cum[JA];
+            int run = 0;
 #pragma unroll
             for (int j = 0; j < JA; ++j) {
                 run += m3_ang_fix(m3_angle_inc(SF.dt[ang_q * JA + j], m3f_bf(rq[j]), p.span));
                 cum[j] = run;
             }
-            // inclusive scan of the 8 parts' totals inside each aligned group of 8 lanes
-            long long incl = run;
+            run = m3_ang_reduce(run);
+            // inclusive scan of the 8 parts' (reduced) totals inside each aligned group of 8 lanes
+            int incl = run;
             {
-                const long long t1 = m3f_shr64<1>(incl);
-                incl += ang_q >= 1 ? t1 : 0ll;
-                const long long t2 = m3f_shr64<2>(incl);
-                incl += ang_q >= 2 ? t2 : 0ll;
-                const long long t4 = m3f_shr64<4>(incl);
-                incl += ang_q >= 4 ? t4 : 0ll;
+                const int t1 = m3f_shr<1>(incl);
+                incl += ang_q >= 1 ? t1 : 0;
+                const int t2 = m3f_shr<2>(incl);
+                incl += ang_q >= 2 ? t2 : 0;
+                const int t4 = m3f_shr<4>(incl);
+                incl += ang_q >= 4 ? t4 : 0;
             }
-            const long long base = theta + (incl - run);
-            const long long total = m3f_last8_64(incl);
+            const int base = theta + (incl - run);
+            const int total = m3f_last8(incl);
             const bool rot_on = ang_a < p.npair;
 #pragma unroll
             for (int j = 0; j < JA; ++j) {

@@ -54,28 +54,37 @@ __device__ __forceinline__ float m3_angle_inc(float dt, float raw_rot, float spa
     return dt * (m3_tanh(raw_rot) * span);
 }
 
-// Cumulative angles in fixed point: multiples of 2^-32 rad in an int64,
-// reduced modulo Q2PI (2 pi in those units) to the canonical range
+// Cumulative angles in fixed point: multiples of 2^-24 rad in an int32,
+// reduced modulo Q2PI (2 pi in those units, odd) to the canonical range
 // [-(Q2PI - 1) / 2, (Q2PI - 1) / 2].  Integer sums do not depend on their
 // association, so every kernel (whatever its segmentation of the sequence)
 // gets the same angle at every position: the cache's angle plus the sum of
-// the increments before it, each rounded to the 2^-32 grid (2.3e-10 rad; the
-// reference's f32 cumsum drifts by far more over long sequences).
-constexpr double kAngUnit = 4294967296.0;        // units per radian
-constexpr long long kQ2Pi = 26986075409ll;       // rint(2 pi 2^32), odd
-__device__ __forceinline__ long long m3_ang_reduce(long long q) {
-    // the quotient's estimate may be off by one: the two corrections below
-    // make the result exact and canonical
-    const double k = rint((double)q * (1.0 / (double)kQ2Pi));
-    q -= (long long)k * kQ2Pi;
+// the increments before it, each put on the 6e-8 rad grid (the reference's
+// f32 cumsum drifts by far more over long sequences).  Every value added is
+// canonical, and sums of at most 16 of them stay below 2^31.
+constexpr float kAngUnit = 16777216.f;           // units per radian (2^24)
+constexpr int kQ2Pi = 105414357;                 // rint(2 pi 2^24) - 1, odd
+constexpr float kInvQ2Pi = 1.f / 105414357.f;
+__device__ __forceinline__ int m3_ang_reduce(int q) {
+    // the quotient's estimate may be off by one: the two corrections make the
+    // result exact and canonical
+    q -= (int)rintf((float)q * kInvQ2Pi) * kQ2Pi;
     if (q > kQ2Pi / 2) q -= kQ2Pi;
     if (q < -(kQ2Pi / 2)) q += kQ2Pi;
     return q;
 }
-// an angle in radians (a cache angle or one increment) onto the grid
-__device__ __forceinline__ long long m3_ang_fix(float a) { return m3_ang_reduce((long long)rint((double)a * kAngUnit)); }
+// an angle in radians (a cache angle or one increment) onto the grid: first
+// reduced to [-pi, pi] in f32 (so that its grid value fits an int32), then its
+// whole radians and its fraction (exact in f32) scaled separately, so that the
+// fraction keeps the grid's full resolution
+__device__ __forceinline__ int m3_ang_fix(float a) {
+    constexpr float two_pi = 6.28318530717958647692f;
+    const float r = a - rintf(a * (1.f / two_pi)) * two_pi;
+    const float w = rintf(r);
+    return m3_ang_reduce((int)w * (int)kAngUnit + (int)rintf((r - w) * kAngUnit));
+}
 // a canonical grid angle as f32 radians in [-pi, pi]
-__device__ __forceinline__ float m3_ang_rad(long long q) { return (float)((double)q * (1.0 / kAngUnit)); }
+__device__ __forceinline__ float m3_ang_rad(int q) { return (float)q * (1.f / kAngUnit); }
 
 // One B / C row piece of 8 columns: the sum of squares (to be completed over
 // the row's lanes), the norm weight and bias, the rotation

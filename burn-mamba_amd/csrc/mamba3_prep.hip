@@ -131,7 +131,7 @@ __global__ __launch_bounds__(256) void mamba3_prep_kernel(M3PrepParams p) {
     const int cp = t % np1, rp0 = t / np1, rsp = np1 >= 256 ? 1 : 256 / np1;
     const int cx = t % P, rx0 = t / P, rsx = P >= 256 ? 1 : 256 / P;
 
-    long long theta = (t < A) ? m3_ang_fix(p.ang[bh * A + t]) : 0ll;  // grid units
+    int theta = (t < A) ? m3_ang_fix(p.ang[bh * A + t]) : 0;  // grid units
     for (int l0 = 0; l0 < p.L; l0 += TS) {
         const int nt = min(TS, p.L - l0);
         // coefficients of the tile (+ the next position for scale)
@@ -342,7 +342,7 @@ __device__ __forceinline__ void m3_coef_t(const M3PrepParams& p, const TP* proj,
 // per thread) so that b * nseg * H / hpw workgroups share the segments.
 // Dynamic LDS: [tile][hpw] dt and [tile][A] tanh(rot) * span.
 template <typename TP>
-__global__ __launch_bounds__(256) void mamba3_angle_tot_kernel(M3PrepParams p, int nseg, int hpw, long long* tot) {
+__global__ __launch_bounds__(256) void mamba3_angle_tot_kernel(M3PrepParams p, int nseg, int hpw, int* tot) {
     const int b = blockIdx.x / nseg, seg = blockIdx.x % nseg, t = threadIdx.x;
     const TP* proj = static_cast<const TP*>(p.proj);
     const int H = p.H, A = p.A, HA = H * A;
@@ -354,9 +354,9 @@ __global__ __launch_bounds__(256) void mamba3_angle_tot_kernel(M3PrepParams p, i
     float* s_tr = s_dtt + kM3Tile * hpw;   // [kM3Tile][A]
     constexpr int KP = 4;                  // (h, a) pairs per thread and pass
     for (int pb = 0; pb < np; pb += 256 * KP) {
-        long long acc[KP];
+        int acc[KP];
 #pragma unroll
-        for (int k = 0; k < KP; ++k) acc[k] = 0ll;
+        for (int k = 0; k < KP; ++k) acc[k] = 0;
         for (int l0 = l_begin; l0 < l_end; l0 += kM3Tile) {
             const int nt = min(kM3Tile, l_end - l0);
             for (int i = t; i < kM3Tile * nh; i += 256) {
@@ -376,7 +376,7 @@ __global__ __launch_bounds__(256) void mamba3_angle_tot_kernel(M3PrepParams p, i
                 const int i = pb + t + 256 * k;
                 if (i < np) {
                     const int hl = i / A, a = i % A;
-                    long long sacc = acc[k];
+                    int sacc = acc[k];
                     for (int r = 0; r < nt; ++r)
                         sacc += m3_ang_fix(m3_angle_inc(s_dtt[r * hpw + hl], s_tr[r * A + a], p.span));
                     acc[k] = m3_ang_reduce(sacc);
@@ -401,7 +401,7 @@ __global__ __launch_bounds__(256) void mamba3_angle_tot_kernel(M3PrepParams p, i
 // rank) and its column block for the whole segment; otherwise the rows are
 // decomposed per pass.
 template <typename TP, typename TO, int N>
-__global__ __launch_bounds__(256) void mamba3_prep_seg_kernel(M3PrepParams p, int nseg, const long long* tot) {
+__global__ __launch_bounds__(256) void mamba3_prep_seg_kernel(M3PrepParams p, int nseg, const int* tot) {
     constexpr int TPR = N / 8;         // threads per B/C row (8 columns each)
     constexpr int RPP = 256 / TPR;     // rows per pass
     constexpr int W = N / 2;           // pair indices
@@ -421,7 +421,7 @@ __global__ __launch_bounds__(256) void mamba3_prep_seg_kernel(M3PrepParams p, in
     __shared__ float s_dt[kM3Tile + 1], s_lam[kM3Tile + 1], s_da[kM3Tile];
 
     // starting angle of the segment (grid units): the cache's angle plus the earlier segments' totals
-    long long theta = 0ll;
+    int theta = 0;
     if (t < A) {
         theta = m3_ang_fix(p.ang[bh * A + t]);
         for (int s2 = 0; s2 < seg; ++s2)
@@ -806,11 +806,11 @@ extern "C" size_t mamba3_prep_workspace_size(const mamba3_prep_args* a) {
     if (m3_prep_params(a, &p, true) != MAMBA_OK) return 0;
     const int nseg = m3_nseg(p);
     if (!m3_prep_fast(p) || nseg == 1) return 0;
-    return (size_t)p.nb * nseg * p.H * p.A * sizeof(long long);
+    return (size_t)p.nb * nseg * p.H * p.A * sizeof(int);
 }
 
 template <typename TP, typename TO>
-static void m3_launch_fast(const M3PrepParams& p, long long* tot, hipStream_t s) {
+static void m3_launch_fast(const M3PrepParams& p, int* tot, hipStream_t s) {
     const int nseg = m3_nseg(p);
     if (nseg > 1) {
         const int hpw = p.A >= 256 ? 1 : (256 / p.A < p.H ? 256 / p.A : p.H);  // heads per workgroup
@@ -820,7 +820,7 @@ static void m3_launch_fast(const M3PrepParams& p, long long* tot, hipStream_t s)
     const dim3 grid(p.nb * p.H * nseg), block(256);
     const size_t lds = (size_t)kM3Tile * (((p.A + 3) & ~3) + p.N) * sizeof(float);
 #define MAMBA3_SEG_N(NN) \
-    hipLaunchKernelGGL((mamba3_prep_seg_kernel<TP, TO, NN>), grid, block, lds, s, p, nseg, (const long long*)tot);
+    hipLaunchKernelGGL((mamba3_prep_seg_kernel<TP, TO, NN>), grid, block, lds, s, p, nseg, (const int*)tot);
     switch (p.N) {
         case 8: MAMBA3_SEG_N(8) break;
         case 16: MAMBA3_SEG_N(16) break;
@@ -846,7 +846,7 @@ extern "C" int mamba3_prep_fwd(const mamba3_prep_args* a, void* workspace, size_
     m3_launch_seed(p, s);
     MAMBA_CHECK_LAUNCH();
     if (m3_prep_fast(p)) {
-        long long* tot = (long long*)workspace;
+        int* tot = (int*)workspace;
         if (p.proj_bf16 && p.io_bf16) m3_launch_fast<bf16_t, bf16_t>(p, tot, s);
         else if (p.proj_bf16) m3_launch_fast<bf16_t, float>(p, tot, s);
         else if (p.io_bf16) m3_launch_fast<float, bf16_t>(p, tot, s);

@@ -272,7 +272,10 @@ def test_mamba3_prep_fwd_segments(case, dtype):
             assert not bad.any(), f"{k}: {int(bad.sum())} elements beyond rtol 1e-4 of their row's scale"
     for k in ("da", "gamma", "scale", "h0"):
         np.testing.assert_allclose(out[k].cpu().numpy(), r[k], **F32_TOL, err_msg=k)
-    np.testing.assert_allclose(cg.k_state_bmhr.cpu().numpy(), r["k_state"], **F32_TOL)
+    # the cache tail's k_state is the last rotated B row (f32): the same row-relative bar
+    got, want = cg.k_state_bmhr.cpu().numpy(), r["k_state"]
+    row = np.abs(want).max(axis=-1, keepdims=True)
+    assert np.all(np.abs(got - want) <= F32_TOL["atol"] + F32_TOL["rtol"] * row), "k_state"
     np.testing.assert_allclose(cg.v_state_bhp.cpu().numpy(), r["v_state"], **F32_TOL)
     ag = cg.angle_bha.cpu().numpy()
     np.testing.assert_allclose(np.cos(ag), np.cos(r["angle"]), atol=5e-5)
