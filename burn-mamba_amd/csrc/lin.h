@@ -34,7 +34,12 @@ struct LinParams {
     int M, N, K, MT;         // MT = lin_mt(M)
     int S;                   // k-splits across workgroups (grid.y)
     const lin_bf16x8_t* W;   // packed weight
-    const lin_bf16x8_t* A;   // packed activation
+    const lin_bf16x8_t* A;   // packed activation, or NULL when X is given
+    // row-major bf16 activation [M][x_ld] read in place (16-byte aligned rows):
+    // lane l of block (s, i) holds 8 consecutive k of one row, 16 contiguous
+    // bytes, so no packing pass is needed
+    const bf16_t* X; int64_t x_ld;
+    int NW;                  // waves per workgroup (0: the default for MT)
     // LIN_STORE (S == 1): out[m, n] = acc + bias
     const float* bias;       // [N] or NULL
     void* out; int64_t out_ld; bool out_bf16;

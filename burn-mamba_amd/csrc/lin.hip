@@ -63,14 +63,35 @@ __device__ __forceinline__ lin_bf16x8_t lin_ld(__amdgpu_buffer_rsrc_t r, uint32_
     return __builtin_bit_cast(lin_bf16x8_t, buf_ld16(r, off));
 }
 
-template <int MT>
+// Byte offset of activation block (s, i) for this lane: packed blocks are
+// 1 KB runs; a row-major activation is read in place (lane -> row 32 i + r,
+// k 16 s + 8 half .. + 7), rows past M beyond the resource's extent read zero.
+template <int MT, bool RM>
+struct LinAct {
+    uint32_t lane_off, row_tile;  // RM: lane's (row r, k 8 half) offset; 32 rows of x
+    __device__ __forceinline__ LinAct(int lane, int64_t x_ld) {
+        if (RM) {
+            lane_off = (uint32_t)(((int64_t)(lane & 31) * x_ld + 8 * (lane >> 5)) * 2);
+            row_tile = (uint32_t)(32 * x_ld * 2);
+        } else {
+            lane_off = (uint32_t)lane * 16u;
+            row_tile = 0;
+        }
+    }
+    __device__ __forceinline__ uint32_t off(int s, int i) const {
+        return RM ? lane_off + (uint32_t)i * row_tile + (uint32_t)s * 32u
+                  : ((uint32_t)s * MT + i) * 1024u + lane_off;
+    }
+};
+
+template <int MT, bool RM>
 __device__ __forceinline__ void lin_load(LinStage<MT>& st, __amdgpu_buffer_rsrc_t rw, __amdgpu_buffer_rsrc_t ra,
-                                         uint32_t lo, int s) {
+                                         uint32_t lo, const LinAct<MT, RM>& ao, int s) {
 #pragma unroll
     for (int u = 0; u < LinStage<MT>::U; ++u) {
         st.w[u] = lin_ld(rw, (uint32_t)(s + u) * 1024u + lo);
 #pragma unroll
-        for (int i = 0; i < MT; ++i) st.a[u][i] = lin_ld(ra, ((uint32_t)(s + u) * MT + i) * 1024u + lo);
+        for (int i = 0; i < MT; ++i) st.a[u][i] = lin_ld(ra, ao.off(s + u, i));
     }
 }
 
@@ -82,10 +103,12 @@ __device__ __forceinline__ void lin_compute(const LinStage<MT>& st, lin_f32x16_t
         for (int i = 0; i < MT; ++i) acc[i] = lin_mfma(st.a[u][i], st.w[u], acc[i]);
 }
 
-// grid: (ceil(N / 32), S) workgroups of NW waves.
-template <int MT, int NW, int EPI>
+// grid: (ceil(N / 32), S) workgroups of NW waves.  RM: the activation is
+// p.X (row-major bf16) instead of the packed p.A.
+template <int MT, int NW, int EPI, bool RM = false>
 __global__ __launch_bounds__(64 * NW) void lin_stream(LinParams p) {
-    __shared__ float s_red[NW][2][16][64];
+    constexpr int RT = (MT < 2 || NW >= 16) ? 1 : 2;  // 32-row tiles reduced per LDS round
+    __shared__ float s_red[NW][RT][16][64];
     const int j = blockIdx.x, z = blockIdx.y;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int KS = p.K >> 4;
@@ -94,7 +117,9 @@ __global__ __launch_bounds__(64 * NW) void lin_stream(LinParams p) {
 
     // this tile's column of weight blocks, and the activation blocks
     const __amdgpu_buffer_rsrc_t rw = buf_rsrc(p.W + (int64_t)j * KS * 64, (uint32_t)KS * 1024u);
-    const __amdgpu_buffer_rsrc_t ra = buf_rsrc(p.A, (uint32_t)KS * MT * 1024u);
+    const __amdgpu_buffer_rsrc_t ra = RM ? buf_rsrc(p.X, (uint32_t)((int64_t)p.M * p.x_ld * 2))
+                                         : buf_rsrc(p.A, (uint32_t)KS * MT * 1024u);
+    const LinAct<MT, RM> ao(lane, p.x_ld);
     const uint32_t lo = (uint32_t)lane * 16u;
     lin_f32x16_t acc[MT];
 #pragma unroll
@@ -112,13 +137,13 @@ __global__ __launch_bounds__(64 * NW) void lin_stream(LinParams p) {
         const int rot = MAMBA_LIN_ROTATE ? (int)(blockIdx.x % (unsigned)nstage) : 0;
         auto kstep = [&](int st) { int q = st + rot; q -= q >= nstage ? nstage : 0; return s0 + U * q; };
         LinStage<MT> sa, sb;
-        lin_load<MT>(sa, rw, ra, lo, kstep(0));
+        lin_load<MT, RM>(sa, rw, ra, lo, ao, kstep(0));
         for (int st = 0; st < nstage; st += 2) {
             const bool more1 = st + 1 < nstage;
-            if (more1) lin_load<MT>(sb, rw, ra, lo, kstep(st + 1));
+            if (more1) lin_load<MT, RM>(sb, rw, ra, lo, ao, kstep(st + 1));
             lin_compute<MT>(sa, acc);
             if (more1) {
-                if (st + 2 < nstage) lin_load<MT>(sa, rw, ra, lo, kstep(st + 2));
+                if (st + 2 < nstage) lin_load<MT, RM>(sa, rw, ra, lo, ao, kstep(st + 2));
                 lin_compute<MT>(sb, acc);
             }
         }
@@ -127,19 +152,19 @@ __global__ __launch_bounds__(64 * NW) void lin_stream(LinParams p) {
     for (; s < s1; ++s) {
         const lin_bf16x8_t w = lin_ld(rw, (uint32_t)s * 1024u + lo);
 #pragma unroll
-        for (int i = 0; i < MT; ++i) acc[i] = lin_mfma(lin_ld(ra, ((uint32_t)s * MT + i) * 1024u + lo), w, acc[i]);
+        for (int i = 0; i < MT; ++i) acc[i] = lin_mfma(lin_ld(ra, ao.off(s, i)), w, acc[i]);
     }
 
-    // cross-wave reduction through LDS, two 32-row tiles at a time
+    // cross-wave reduction through LDS, RT 32-row tiles at a time
 #pragma unroll
-    for (int ig = 0; ig < MT; ig += 2) {
+    for (int ig = 0; ig < MT; ig += RT) {
 #pragma unroll
-        for (int t2 = 0; t2 < 2; ++t2)
+        for (int t2 = 0; t2 < RT; ++t2)
             if (ig + t2 < MT)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) s_red[wave][t2][v][lane] = acc[ig + t2 < MT ? ig + t2 : 0][v];
         __syncthreads();
-        for (int e = threadIdx.x; e < 2 * 1024; e += 64 * NW) {
+        for (int e = threadIdx.x; e < RT * 1024; e += 64 * NW) {
             const int t2 = e >> 10, v = (e >> 6) & 15, ln = e & 63;
             if (ig + t2 >= MT) break;
             const int m = 32 * (ig + t2) + 8 * (v >> 2) + 4 * (ln >> 5) + (v & 3);
@@ -162,12 +187,34 @@ __global__ __launch_bounds__(64 * NW) void lin_stream(LinParams p) {
     }
 }
 
+template <int MT, int NW, bool RM>
+static void lin_launch_nw(const LinParams& p, int epi, hipStream_t stream) {
+    const dim3 grid((p.N + 31) / 32, p.S);
+    if (epi == LIN_STORE) hipLaunchKernelGGL((lin_stream<MT, NW, LIN_STORE, RM>), grid, dim3(64 * NW), 0, stream, p);
+    else hipLaunchKernelGGL((lin_stream<MT, NW, LIN_PARTIAL, RM>), grid, dim3(64 * NW), 0, stream, p);
+}
+
 template <int MT>
 static void lin_launch_mt(const LinParams& p, int epi, hipStream_t stream) {
-    const dim3 grid((p.N + 31) / 32, p.S);
-    constexpr int NW = MT <= 2 ? MAMBA_LIN_NW : MAMBA_LIN_NW_BIGM;
-    if (epi == LIN_STORE) hipLaunchKernelGGL((lin_stream<MT, NW, LIN_STORE>), grid, dim3(64 * NW), 0, stream, p);
-    else hipLaunchKernelGGL((lin_stream<MT, NW, LIN_PARTIAL>), grid, dim3(64 * NW), 0, stream, p);
+    constexpr int NWD = MT <= 2 ? MAMBA_LIN_NW : MAMBA_LIN_NW_BIGM;
+    const int nw = p.NW ? p.NW : NWD;
+    const bool rm = p.X != nullptr;
+    if constexpr (MT <= 2) {
+        // 16 waves (1024 threads, at most 128 registers each) only for up to
+        // two 32-row tiles, whose accumulators and operand stages fit
+        if (nw == 16) {
+            if (rm) lin_launch_nw<MT, 16, true>(p, epi, stream);
+            else lin_launch_nw<MT, 16, false>(p, epi, stream);
+            return;
+        }
+    }
+    if (nw >= 8) {
+        if (rm) lin_launch_nw<MT, 8, true>(p, epi, stream);
+        else lin_launch_nw<MT, 8, false>(p, epi, stream);
+    } else {
+        if (rm) lin_launch_nw<MT, 4, true>(p, epi, stream);
+        else lin_launch_nw<MT, 4, false>(p, epi, stream);
+    }
 }
 
 void lin_launch(const LinParams& p, int epi, hipStream_t stream) {
@@ -281,11 +328,55 @@ __global__ __launch_bounds__(256) void lin_reduce_kernel(const float* part, int 
     }
 }
 
+// The entry's plan for one product.  A bf16 row-major x with 16-byte aligned
+// rows is read in place (no packing pass).  With one 32-row tile (rows <= 32),
+// weights up to LINFWD_ONE_SPLIT bytes are streamed with one k-split, so the
+// product writes y directly (no partial planes, no summing pass), with enough
+// waves per workgroup for LINFWD_MIN_WAVES streaming waves.  Measured on the
+// 64-layer Mamba-3 decode step (in_proj 10.8 MB, out_proj 4.2 MB): at batch 1
+// this takes the step from 1.59 to 1.45 ms, while at batch 64 (two row tiles)
+// the one-split product is slower than the k-split one plus its summing pass
+// (4.09 against 3.80 ms), so larger batches keep the k-split plan.
+#ifndef MAMBA_LINFWD_RM
+#define MAMBA_LINFWD_RM 1
+#endif
+#ifndef MAMBA_LINFWD_ONE_SPLIT
+#define MAMBA_LINFWD_ONE_SPLIT (16ll << 20)
+#endif
+#ifndef MAMBA_LINFWD_ONE_SPLIT_MT
+#define MAMBA_LINFWD_ONE_SPLIT_MT 1
+#endif
+#ifndef MAMBA_LINFWD_MIN_WAVES
+#define MAMBA_LINFWD_MIN_WAVES 1024
+#endif
+struct LinPlan {
+    bool rm;  // x read in place
+    int S, NW;
+};
+
+static LinPlan linear_plan(const mamba_linear_args* a) {
+    LinPlan pl;
+    pl.rm = MAMBA_LINFWD_RM && a->x_dtype == MAMBA_BF16 && a->x_ld % 8 == 0 && ((uintptr_t)a->x & 15u) == 0 &&
+            (int64_t)a->rows * a->x_ld * 2 < (1ll << 31);
+    const int mt = lin_mt(a->rows), tiles = (a->d_out + 31) / 32, ks = a->d_in / 16;
+    if (mt <= MAMBA_LINFWD_ONE_SPLIT_MT && (int64_t)a->d_in * tiles * 32 * 2 <= MAMBA_LINFWD_ONE_SPLIT) {
+        pl.S = 1;
+        const int nw_max = mt <= 2 ? 16 : 8;
+        int nw = 4;
+        while (nw < nw_max && tiles * nw < MAMBA_LINFWD_MIN_WAVES && ks / (2 * nw) >= 3) nw *= 2;
+        pl.NW = nw;
+    } else {
+        pl.S = lin_splits(a->rows, a->d_in, a->d_out);
+        pl.NW = 0;
+    }
+    return pl;
+}
+
 static size_t linear_ws(const mamba_linear_args* a, size_t* part_off) {
-    const size_t act = align_up(lin_act_elems(a->rows, a->d_in) * 2, 256);
-    const int S = lin_splits(a->rows, a->d_in, a->d_out);
+    const LinPlan pl = linear_plan(a);
+    const size_t act = pl.rm ? 0 : align_up(lin_act_elems(a->rows, a->d_in) * 2, 256);
     *part_off = act;
-    return act + (S > 1 ? align_up(lin_part_elems(a->rows, a->d_out, S) * 4, 256) : 0);
+    return act + (pl.S > 1 ? align_up(lin_part_elems(a->rows, a->d_out, pl.S) * 4, 256) : 0);
 }
 
 }  // namespace mamba
@@ -307,20 +398,26 @@ extern "C" int mamba_linear_fwd(const mamba_linear_args* a, void* ws, size_t ws_
     MAMBA_CHECK_ARG(((uintptr_t)a->packed_w & 15u) == 0, "packed_w must be 16-byte aligned");
     size_t part_off;
     const size_t need = linear_ws(a, &part_off);
-    if (ws == nullptr || ws_bytes < need || ((uintptr_t)ws & 15u) != 0) {
+    if ((need > 0 && ws == nullptr) || ws_bytes < need || ((uintptr_t)ws & 15u) != 0) {
         set_error("mamba_linear_fwd: a 16-byte aligned workspace of " + std::to_string(need) + " bytes is required");
         return MAMBA_ERR_WORKSPACE;
     }
     const int mt = lin_mt(a->rows);
     hipStream_t s = (hipStream_t)stream;
-    const int64_t total = (int64_t)a->rows * (a->d_in / 8);
-    hipLaunchKernelGGL(lin_act_pack_kernel, dim3((int)std::min<int64_t>((total + 255) / 256, 4096)), dim3(256), 0, s,
-                       a->x, a->rows, a->d_in, a->x_ld, a->x_dtype == MAMBA_BF16, static_cast<bf16_t*>(ws), mt);
-    MAMBA_CHECK_LAUNCH();
+    const LinPlan pl = linear_plan(a);
     LinParams p = {};
-    p.M = a->rows; p.N = a->d_out; p.K = a->d_in; p.MT = mt; p.S = lin_splits(a->rows, a->d_in, a->d_out);
+    p.M = a->rows; p.N = a->d_out; p.K = a->d_in; p.MT = mt; p.S = pl.S; p.NW = pl.NW;
     p.W = static_cast<const lin_bf16x8_t*>(a->packed_w);
-    p.A = static_cast<const lin_bf16x8_t*>(ws);
+    if (pl.rm) {
+        p.X = static_cast<const bf16_t*>(a->x);
+        p.x_ld = a->x_ld;
+    } else {
+        const int64_t total = (int64_t)a->rows * (a->d_in / 8);
+        hipLaunchKernelGGL(lin_act_pack_kernel, dim3((int)std::min<int64_t>((total + 255) / 256, 4096)), dim3(256), 0,
+                           s, a->x, a->rows, a->d_in, a->x_ld, a->x_dtype == MAMBA_BF16, static_cast<bf16_t*>(ws), mt);
+        MAMBA_CHECK_LAUNCH();
+        p.A = static_cast<const lin_bf16x8_t*>(ws);
+    }
     if (p.S == 1) {
         p.bias = a->bias;
         p.out = a->y; p.out_ld = a->y_ld; p.out_bf16 = a->y_dtype == MAMBA_BF16;

@@ -628,7 +628,10 @@ int mamba_linear_pack(const void* weight, int32_t d_in, int32_t d_out, int64_t l
 /* W packed by mamba_linear_pack: burn::nn::Linear::forward as the decode      */
 /* steps use it (in_proj/x_proj/dt_proj/out_proj, src/mamba1/mamba1.rs:551,    */
 /* 633-644,609; src/mamba2/mamba2.rs:850,1000).  bf16 operands, f32            */
-/* accumulation; x is repacked into the workspace.                            */
+/* accumulation.  A bf16 x with 16-byte aligned rows (x_ld a multiple of 8) is */
+/* read in place; any other x is repacked into the workspace first.  The       */
+/* workspace also holds k-split partial sums for large weights; its size may   */
+/* be 0 (then workspace may be NULL).                                          */
 typedef struct mamba_linear_args {
     int32_t rows, d_in, d_out;
     int32_t x_dtype, y_dtype;         /* mamba_dtype                            */

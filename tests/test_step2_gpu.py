@@ -295,13 +295,20 @@ def test_step_invalid_args_raise():
 # ------------------------------------------------------------- fused path --
 
 LIN_CASES = [
-    # (rows, d_in, d_out, x dtype, y dtype, bias)
+    # (rows, d_in, d_out, x dtype, y dtype, bias[, extra columns of x's row stride])
+    # bf16 x with 16-byte aligned rows is read in place, anything else packed first;
+    # weights up to 16 MB take one k-split with 4 / 8 / 16 waves per workgroup
     (1, 256, 1000, "f32", "f32", False),     # MT 1, 4 waves, tail loop only, ragged last tile
-    (3, 1024, 96, "bf16", "f32", True),      # MT 1, two pipeline stages per wave
-    (40, 512, 320, "bf16", "bf16", False),   # MT 2
+    (3, 1024, 96, "bf16", "f32", True),      # MT 1, in place, 16 waves, two pipeline stages per wave
+    (40, 512, 320, "bf16", "bf16", False),   # MT 2, in place: rows 40..63 read past x's end (zero)
     (100, 2048, 64, "f32", "f32", True),     # MT 4
-    (200, 4096, 200, "bf16", "f32", False),  # MT 8, 8 waves per workgroup
+    (200, 4096, 200, "bf16", "f32", False),  # MT 8, in place, 8 waves per workgroup
     (256, 64, 33, "f32", "f32", True),       # full 256 rows, K smaller than one stage
+    (64, 2048, 1024, "bf16", "bf16", False),  # the Mamba-3 out_proj shape: 32 tiles x 16 waves
+    (1, 1024, 5280, "bf16", "bf16", True),   # the Mamba-3 in_proj shape at batch 1
+    (5, 1024, 2048, "bf16", "f32", False, 8),  # strided rows read in place, 8 waves
+    (7, 512, 160, "bf16", "f32", True, 3),   # rows not 16-byte aligned: packed first
+    (64, 2560, 10576, "bf16", "f32", False),  # 54 MB weight: k-split partial planes, summed
 ]
 
 
@@ -312,7 +319,8 @@ def test_linear_fwd_matches_oracle(case):
     import torch
     import mamba_hip
     import oracle
-    rows, d_in, d_out, xd, yd, has_b = case
+    rows, d_in, d_out, xd, yd, has_b = case[:6]
+    pad = case[6] if len(case) > 6 else 0
     dts = {"f32": torch.float32, "bf16": torch.bfloat16}
     rng = np.random.default_rng(rows + d_in)
     W = (rng.standard_normal((d_in, d_out)) / np.sqrt(d_in)).astype(np.float32)
@@ -320,7 +328,7 @@ def test_linear_fwd_matches_oracle(case):
     bias = rng.standard_normal(d_out).astype(np.float32) if has_b else None
     Wd = _t(W, torch.bfloat16)
     packed = mamba_hip.pack_linear(Wd)
-    xdev = _t(x, dts[xd])
+    xdev = _t(np.pad(x, ((0, 0), (0, pad))), dts[xd])[:, :d_in]
     y = torch.empty(rows, d_out, device="cuda", dtype=dts[yd])
     mamba_hip.linear(xdev, packed, d_out, None if bias is None else _t(bias), out=y)
     torch.cuda.synchronize()
