@@ -17,7 +17,7 @@
 // with B, C QK-normed, biased and rotated by the cumulative angle, K the
 // previous token's rotated B, G the silu gate or the per-head gated RMSNorm.
 // The state tile (P x N f32) is read and written once: the step is HBM-bound.
-#include "common.h"
+#include "mamba3_internal.h"
 
 namespace mamba {
 
@@ -35,8 +35,7 @@ struct M3StepParams {
 
 constexpr int kM3MaxPN = 8192;  // state tile elements held in registers (P*N)
 
-__device__ __forceinline__ float m3_softplus(float x) { return x > 18.f ? x : log1pf(__expf(x)); }
-__device__ __forceinline__ float m3_silu(float x) { return x / (1.f + __expf(-x)); }
+__device__ __forceinline__ float m3_silu(float x) { return x * m3_sigmoid(x); }
 
 __device__ __forceinline__ float m3_proj(const M3StepParams& p, const void* row, int i) {
     return p.proj_bf16 ? bf16_to_f32(static_cast<const bf16_t*>(row)[i]) : static_cast<const float*>(row)[i];
@@ -62,8 +61,13 @@ __global__ __launch_bounds__(256) void mamba3_step_kernel(M3StepParams p) {
     const int64_t bh = (int64_t)b * p.H + h;
     float* st = p.ssm + bh * P * N;
 
+    // the readout's row sums: QS lanes by DPP, then SL partials per row and
+    // rank through LDS (row pitch padded by one word)
+    constexpr int QS = N4 < 4 ? N4 : 4, SL = N4 / QS, PS = SL * MM + 1;
+    constexpr int PMAX = kM3MaxPN / N < 256 ? kM3MaxPN / N : 256;
     __shared__ __align__(16) float s_B[MM][N], s_C[MM][N], s_K[MM][N];
     __shared__ float s_gv[MM][256], s_bx[MM][256], s_v[MM][256], s_out[MM][256];
+    __shared__ float s_part[PMAX * PS];
     __shared__ float s_cs[128], s_sn[128], s_rms[2 * MM], s_coef[3];
 
     const void* row = static_cast<const char*>(p.proj) + (int64_t)b * p.proj_sb * (p.proj_bf16 ? 2 : 4);
@@ -151,25 +155,20 @@ __global__ __launch_bounds__(256) void mamba3_step_kernel(M3StepParams p) {
 
     // ---- trapezoid coefficients and the cumulative angle, on the waves that
     // hold angles (wave 0 at least); the others read the coefficients from LDS
+    // (the prefill's arithmetic: hardware exp / reciprocal / sin / cos)
     if (wave * 64 < (p.A > 64 ? p.A : 64)) {
-        float dt = m3_softplus(raw_dt + dtb);
-        dt = fminf(fmaxf(dt, p.dt_lo), p.dt_hi);
+        float dt, da, lam;
+        m3_coef(raw_dt, raw_a, raw_l, dtb, p.a_floor, p.dt_lo, p.dt_hi, dt, da, lam);
         if (t == 0) {
-            const float a = -fmaxf(m3_softplus(raw_a), p.a_floor);
-            const float lam = 1.f / (1.f + __expf(-raw_l));
-            const float alpha = __expf(dt * a);
+            const float alpha = __expf(da);
             s_coef[0] = alpha;
             s_coef[1] = (1.f - lam) * dt * alpha;  // beta
             s_coef[2] = lam * dt;                  // gamma
         }
         if (t < p.A) {
-            const float th = m3_wrap(ang0 + dt * (tanhf(raw_rot) * p.span));
+            const float th = m3_wrap(ang0 + m3_angle_inc(dt, raw_rot, p.span));
             p.ang[bh * p.A + t] = th;
-            const float tw = m3_wrap(th);
-            if (t < 128) {
-                s_cs[t] = cosf(tw);
-                s_sn[t] = sinf(tw);
-            }
+            if (t < 128) m3_cossin(m3_wrap(th), s_cs[t], s_sn[t]);
         }
     }
     // ---- the previous token's K; QK-norm of the B/C rows (sum of squares over
@@ -186,11 +185,11 @@ __global__ __launch_bounds__(256) void mamba3_step_kernel(M3StepParams p) {
         for (int e = 0; e < PPL; ++e) ss += x0[j][e] * x0[j][e] + x1[j][e] * x1[j][e];
         ss = group_sum_last<GS>(ss);
         ss = __shfl(ss, (lane & ~(GS - 1)) + GS - 1, 64);
-        const float rms = 1.f / sqrtf(ss / (float)N + 8.1584695e-8f);
+        const float rms = m3_rms_inv(ss, N);
 #pragma unroll
         for (int e = 0; e < PPL; ++e) {
-            x0[j][e] = (x0[j][e] * rms) * w0[j][e] + c0[j][e];
-            x1[j][e] = (x1[j][e] * rms) * w1[j][e] + c1[j][e];
+            x0[j][e] = m3_norm(x0[j][e], rms, w0[j][e], c0[j][e]);
+            x1[j][e] = m3_norm(x1[j][e], rms, w1[j][e], c1[j][e]);
         }
     }
     __syncthreads();
@@ -255,22 +254,32 @@ __global__ __launch_bounds__(256) void mamba3_step_kernel(M3StepParams p) {
 #pragma unroll
         for (int m = 0; m < MM; ++m) {
             const float gv = s_gv[m][pc], bx = s_bx[m][pc];
-            hn.x += gv * bq[m].x + bx * kq[m].x;
-            hn.y += gv * bq[m].y + bx * kq[m].y;
-            hn.z += gv * bq[m].z + bx * kq[m].z;
-            hn.w += gv * bq[m].w + bx * kq[m].w;
+            hn.x = __builtin_fmaf(bx, kq[m].x, __builtin_fmaf(gv, bq[m].x, hn.x));
+            hn.y = __builtin_fmaf(bx, kq[m].y, __builtin_fmaf(gv, bq[m].y, hn.y));
+            hn.z = __builtin_fmaf(bx, kq[m].z, __builtin_fmaf(gv, bq[m].z, hn.z));
+            hn.w = __builtin_fmaf(bx, kq[m].w, __builtin_fmaf(gv, bq[m].w, hn.w));
         }
 #pragma unroll
-        for (int m = 0; m < MM; ++m) acc[m] = cq[m].x * hn.x + cq[m].y * hn.y + cq[m].z * hn.z + cq[m].w * hn.w;
-        // the row's sum over its N4 lanes, in the row's last lane
+        for (int m = 0; m < MM; ++m)
+            acc[m] = __builtin_fmaf(cq[m].w, hn.w, __builtin_fmaf(cq[m].z, hn.z, __builtin_fmaf(cq[m].y, hn.y, cq[m].x * hn.x)));
+        // the sum over QS lanes lands in the last of them
 #pragma unroll
-        for (int m = 0; m < MM; ++m) acc[m] = group_sum_last<N4>(acc[m]);
+        for (int m = 0; m < MM; ++m) acc[m] = group_sum_last<QS>(acc[m]);
         if (live) {
             st_nt4(reinterpret_cast<float4*>(st + (int64_t)pr * N) + q, hn);
-            if (q == N4 - 1)
+            if (q % QS == QS - 1)
 #pragma unroll
-                for (int m = 0; m < MM; ++m) s_out[m][pr] = acc[m] + Dv * s_v[m][pr];
+                for (int m = 0; m < MM; ++m) s_part[pr * PS + (q / QS) * MM + m] = acc[m];
         }
+    }
+    __syncthreads();
+    // the rows' readout: SL partials per (row, rank), in order
+    for (int i = t; i < P * MM; i += 256) {
+        const int pr = i / MM, m = i % MM;
+        float sum = 0.f;
+#pragma unroll
+        for (int j = 0; j < SL; ++j) sum += s_part[pr * PS + j * MM + m];
+        s_out[m][pr] = __builtin_fmaf(Dv, s_v[m][pr], sum);
     }
     __syncthreads();
     // ---- gate (or per-head gated norm over P), MIMO merge
@@ -279,7 +288,7 @@ __global__ __launch_bounds__(256) void mamba3_step_kernel(M3StepParams p) {
             float ss = 0.f;
             for (int i = lane; i < P; i += 64) ss += s_out[m][i] * s_out[m][i];
             ss = wave_sum(ss);
-            if (lane == 0) s_rms[m] = 1.f / sqrtf(ss / (float)P + 8.1584695e-8f);
+            if (lane == 0) s_rms[m] = m3_rms_inv(ss, P);
         }
         __syncthreads();
     }
