@@ -642,8 +642,26 @@ static void rows_launch(const RowsParams& rp, int S, hipStream_t stream) {
 }
 
 struct LayerGeom {
-    int M, d_model, H, d_inner, conv_dim, d_in_proj, nbc, mt, S_in, S_out;
+    int M, d_model, H, d_inner, conv_dim, d_in_proj, nbc, mt, S_in, S_out, nw_in, nw_out;
 };
+
+// Products of a call that runs beside another stream's layers (a batch split
+// over two streams) with one 32-row tile: in_proj with one k-split and 8 waves
+// per workgroup, out_proj with two k-splits and 16 waves.  Measured on the
+// 64-layer config-3 step at batch 64 (two 32-row halves): 6.04 -> 5.88 ms; the
+// same plan on one stream at batch 32 measured 2.8 % slower than lin_splits'.
+#ifndef MAMBA_STEP2_CC_S_IN
+#define MAMBA_STEP2_CC_S_IN 1
+#endif
+#ifndef MAMBA_STEP2_CC_NW_IN
+#define MAMBA_STEP2_CC_NW_IN 8
+#endif
+#ifndef MAMBA_STEP2_CC_S_OUT
+#define MAMBA_STEP2_CC_S_OUT 2
+#endif
+#ifndef MAMBA_STEP2_CC_NW_OUT
+#define MAMBA_STEP2_CC_NW_OUT 16
+#endif
 
 struct LayerWs {
     bf16_t* a_in; float* zx_part; bf16_t* a_out; float* ssq; float* out_part; size_t total;
@@ -659,6 +677,13 @@ static LayerGeom layer_geom(const mamba2_layer_args* a) {
     g.mt = lin_mt(g.M);
     g.S_in = lin_splits(g.M, g.d_model, g.d_in_proj);
     g.S_out = lin_splits(g.M, g.d_inner, g.d_model);
+    g.nw_in = g.nw_out = 0;
+    if (a->concurrent && g.mt == 1) {
+        g.S_in = MAMBA_STEP2_CC_S_IN;
+        g.S_out = MAMBA_STEP2_CC_S_OUT;
+        g.nw_in = MAMBA_STEP2_CC_NW_IN;
+        g.nw_out = MAMBA_STEP2_CC_NW_OUT;
+    }
     return g;
 }
 
@@ -700,7 +725,7 @@ static int layer_check(const mamba2_layer_args* a, const mamba2_layer_args* firs
         MAMBA_CHECK_ARG(a->batch == first->batch && a->d_model == first->d_model && a->nheads == first->nheads &&
                             a->headdim == first->headdim && a->ngroups == first->ngroups &&
                             a->dstate == first->dstate && a->conv_kernel == first->conv_kernel &&
-                            a->x == first->x && a->x_sb == first->x_sb,
+                            a->x == first->x && a->x_sb == first->x_sb && a->concurrent == first->concurrent,
                         "every layer of a stack must share the shapes and the residual stream x");
     }
     return MAMBA_OK;
@@ -711,7 +736,7 @@ static int layer_check(const mamba2_layer_args* a, const mamba2_layer_args* firs
 static int layer_core(const mamba2_layer_args* a, const LayerGeom& g, const LayerWs& w, hipStream_t stream,
                       hipEvent_t ev0, hipEvent_t ev1) {
     LinParams li = {};
-    li.M = g.M; li.N = g.d_in_proj; li.K = g.d_model; li.MT = g.mt; li.S = g.S_in;
+    li.M = g.M; li.N = g.d_in_proj; li.K = g.d_model; li.MT = g.mt; li.S = g.S_in; li.NW = g.nw_in;
     li.W = static_cast<const lin_bf16x8_t*>(a->in_proj);
     li.A = reinterpret_cast<const lin_bf16x8_t*>(w.a_in);
     li.part = w.zx_part;
@@ -752,7 +777,7 @@ static int layer_core(const mamba2_layer_args* a, const LayerGeom& g, const Laye
     if (ev1) MAMBA_CHECK_HIP(hipEventRecord(ev1, stream));
 
     LinParams lo = {};
-    lo.M = g.M; lo.N = g.d_model; lo.K = g.d_inner; lo.MT = g.mt; lo.S = g.S_out;
+    lo.M = g.M; lo.N = g.d_model; lo.K = g.d_inner; lo.MT = g.mt; lo.S = g.S_out; lo.NW = g.nw_out;
     lo.W = static_cast<const lin_bf16x8_t*>(a->out_proj);
     lo.A = reinterpret_cast<const lin_bf16x8_t*>(w.a_out);
     lo.part = w.out_part;

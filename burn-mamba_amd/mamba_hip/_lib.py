@@ -279,7 +279,7 @@ class Mamba2LayerArgs(ctypes.Structure):
         ("conv_state", c_vp), ("conv_w", c_vp), ("conv_b", c_vp),
         ("dt_bias", c_vp), ("A", c_vp), ("D", c_vp),
         ("dt_min", ctypes.c_float), ("dt_max", ctypes.c_float),
-        ("norm_w", c_vp), ("ssm_state", c_vp),
+        ("norm_w", c_vp), ("ssm_state", c_vp), ("concurrent", c_i32),
     ]
 
 

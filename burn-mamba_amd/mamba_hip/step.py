@@ -538,9 +538,9 @@ class Mamba2Stack:
                                         mixer=cfg.init(device, dtype, generator)) for _ in range(n_layers)],
                            fused=fused)
 
-    def _layer_args(self, i: int, x_res: torch.Tensor, cache: Mamba2Cache) -> Mamba2LayerArgs:
+    def _layer_args(self, i: int, x_res: torch.Tensor, cache: Mamba2Cache, concurrent: bool = False) -> Mamba2LayerArgs:
         key = (i, x_res.data_ptr(), x_res.shape[0], x_res.stride(0), cache.conv_bvk.data_ptr(),
-               cache.ssm_bhpr.data_ptr())
+               cache.ssm_bhpr.data_ptr(), concurrent)
         a = self._args.get(key)
         if a is not None:
             return a
@@ -565,6 +565,7 @@ class Mamba2Stack:
         a.dt_bias, a.A, a.D = m.dt_bias.data_ptr(), m.A.data_ptr(), m.d.data_ptr()
         a.dt_min, a.dt_max = float(c.dt_limit[0]), float(c.dt_limit[1])
         a.norm_w, a.ssm_state = m.norm_w.data_ptr(), cache.ssm_bhpr.data_ptr()
+        a.concurrent = int(concurrent)
         self._args[key] = a
         return a
 
@@ -588,7 +589,8 @@ class Mamba2Stack:
                 la.batch, la.d_model, la.nheads, la.headdim = batch, c.d_model, c.nheads, c.per_head_dim
                 la.ngroups, la.dstate, la.conv_kernel = c.ngroups, c.state_rank, c.conv_kernel
                 la.zxbcdt_dtype = _lib.MAMBA_BF16 if dt == torch.bfloat16 else _lib.MAMBA_F32
-                n = max(n, _lib.lib().mamba2_layer_workspace_size(ctypes.byref(la)))
+                for la.concurrent in (0, 1):
+                    n = max(n, _lib.lib().mamba2_layer_workspace_size(ctypes.byref(la)))
             bufs["ws"] = torch.empty(n, device=device, dtype=torch.uint8)
             self._bufs[key] = bufs
         return self._bufs[key]
@@ -639,13 +641,15 @@ class Mamba2Stack:
         L = _lib.lib()
         ws = bufs["ws"]
         wsp, stream = ctypes.c_void_p(ws.data_ptr()), _stream(x_res.device)
-        # every pointer the per-layer args embed (the residual row and both caches)
-        key = ("stack", x_res.data_ptr(), x_res.shape[0], x_res.stride(0)) + tuple(
+        # every pointer the per-layer args embed (the residual row and both caches);
+        # slots 1 and 2 are the halves of the two-stream schedule (concurrent calls)
+        concurrent = slot > 0
+        key = ("stack", x_res.data_ptr(), x_res.shape[0], x_res.stride(0), concurrent) + tuple(
             (c.conv_bvk.data_ptr(), c.ssm_bhpr.data_ptr()) for c in caches)
         arr = self._args.get(key)
         if arr is None:
             arr = (Mamba2LayerArgs * len(self.layers))(
-                *[self._layer_args(i, x_res, caches[i]) for i in range(len(self.layers))])
+                *[self._layer_args(i, x_res, caches[i], concurrent) for i in range(len(self.layers))])
             self._args[key] = arr
         if events is None:
             check(L.mamba2_stack_step(arr, len(self.layers), wsp, ws.numel(), stream), "mamba2_stack_step")

@@ -683,6 +683,12 @@ typedef struct mamba2_layer_args {
     float dt_min, dt_max;
     const float* norm_w;              /* [d_inner] gated-RMSNorm gamma          */
     float* ssm_state;                 /* [b, nheads, headdim, dstate], in/out   */
+    int32_t concurrent;               /* 1: another stream runs other rows' layers */
+                                      /* beside this call (a batch split over two */
+                                      /* streams); with at most 32 rows the products */
+                                      /* then stream in fewer, wider workgroups,  */
+                                      /* which run faster beside a state kernel.  */
+                                      /* Results do not depend on it.  0 otherwise. */
 } mamba2_layer_args;
 
 size_t mamba2_layer_workspace_size(const mamba2_layer_args* args);

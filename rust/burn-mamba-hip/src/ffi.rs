@@ -660,6 +660,7 @@ pub struct Mamba2LayerArgs {
     pub dt_max: f32,
     pub norm_w: *const f32,
     pub ssm_state: *mut f32,
+    pub concurrent: i32,
 }
 
 impl Default for Mamba2LayerArgs {
