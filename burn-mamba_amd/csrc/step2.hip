@@ -103,22 +103,29 @@ __device__ __forceinline__ float block_sum_256(float v, float* s_red) {
 // ---------------------------------------------------------------------------
 // Fast path: headdim 64, dstate N in {64, 128}, conv width 4, 256 threads.
 // Thread t owns float4 column n4 = t % (N/4) of rows row0 + i*RPI, i < R.
+// RS > 1 (the packed layer path, few batch rows): RS workgroups per (row,
+// head), each owning PR = 64 / RS state rows, so that a batch of one still
+// launches hundreds of workgroups; each writes its own sum of squares
+// (ssq_ws[(b H + h) RS + rs]).
 // ---------------------------------------------------------------------------
-template <int N, bool PACK, int ZS = 0>
+template <int N, bool PACK, int ZS = 0, int RS = 1>
 __global__ __launch_bounds__(256) void step2_ssm_fast(Step2Params p) {
     constexpr int P = 64;
+    constexpr int PR = P / RS;      // state rows of this workgroup
     constexpr int LPR = N / 4;      // lanes per state row
     constexpr int RPI = 256 / LPR;  // rows covered by one pass of the workgroup
-    constexpr int R = P / RPI;      // float4 per thread (= LPR / 4)
-    static_assert(R * 4 == LPR, "reduce-scatter assumes R = LPR / 4");
-    __shared__ float s_x[P];
+    constexpr int R = PR / RPI;     // float4 per thread
+    static_assert(RS == 1 ? R * 4 == LPR : R >= 1 && PR >= 8, "reduce-scatter assumes R = LPR / 4");
+    static_assert(RS == 1 || PACK, "row splits are for the packed layer path");
+    __shared__ float s_x[PR];
     __shared__ __align__(16) float s_B[N];
     __shared__ __align__(16) float s_C[N];
     __shared__ float s_red[4];
-    __shared__ __align__(16) float s_pk[PACK ? P : 1];
+    __shared__ __align__(16) float s_pk[PACK ? PR : 1];
 
     const int t = threadIdx.x;
-    const int bh = blockIdx.x;
+    const int bh = RS == 1 ? (int)blockIdx.x : (int)blockIdx.x / RS;
+    const int rs = RS == 1 ? 0 : (int)blockIdx.x % RS, r0 = rs * PR;
     const int b = bh / p.H, h = bh - b * p.H;
     const int g = h / p.hpg;
     const int n4 = t % LPR, row0 = t / LPR;
@@ -129,17 +136,17 @@ __global__ __launch_bounds__(256) void step2_ssm_fast(Step2Params p) {
     const char* zrow = static_cast<const char*>(p.zx) + b * p.zx_sb * (p.zx_bf16 ? 2 : 4);
     float4* win_base = reinterpret_cast<float4*>(p.conv) + (int64_t)b * p.conv_dim;
     const float4* cw = reinterpret_cast<const float4*>(p.conv_w);
-    constexpr int CI = (P + 2 * N + 255) / 256;  // conv channels per thread
+    constexpr int CI = (PR + 2 * N + 255) / 256;  // conv channels per thread
     int chs[CI];
     float4 cwin[CI], cwt[CI];
     float cxin[CI], cbias[CI];
 #pragma unroll
     for (int j = 0; j < CI; ++j) {
-        const int c = min(t + 256 * j, P + 2 * N - 1);  // clamped: the duplicate is not used
+        const int c = min(t + 256 * j, PR + 2 * N - 1);  // clamped: the duplicate is not used
         int ch;
-        if (c < P) ch = h * P + c;
-        else if (c < P + N) ch = p.d_inner + g * N + (c - P);
-        else ch = p.d_inner + (p.G + g) * N + (c - P - N);
+        if (c < PR) ch = h * P + r0 + c;
+        else if (c < PR + N) ch = p.d_inner + g * N + (c - PR);
+        else ch = p.d_inner + (p.G + g) * N + (c - PR - N);
         chs[j] = ch;
         cwin[j] = win_base[ch];
         cwt[j] = cw[ch];
@@ -149,7 +156,7 @@ __global__ __launch_bounds__(256) void step2_ssm_fast(Step2Params p) {
     const float dt_raw = zx_at<ZS>(p, zrow, b, p.d_inner + p.conv_dim + h) + (p.dt_bias ? p.dt_bias[h] : 0.f);
 
     // 2. the state tile: the bytes that matter (read and written once: non-temporal)
-    float4* st = reinterpret_cast<float4*>(p.ssm) + (int64_t)bh * (P * LPR);
+    float4* st = reinterpret_cast<float4*>(p.ssm) + (int64_t)bh * (P * LPR) + r0 * LPR;
     float4 hv[R];
 #pragma unroll
     for (int i = 0; i < R; ++i) hv[i] = ld_nt4(&st[(row0 + i * RPI) * LPR + n4]);
@@ -158,7 +165,7 @@ __global__ __launch_bounds__(256) void step2_ssm_fast(Step2Params p) {
 #pragma unroll
     for (int j = 0; j < CI; ++j) {
         const int c = t + 256 * j;
-        if (c >= P + 2 * N) break;
+        if (c >= PR + 2 * N) break;
         const int ch = chs[j];
         const float4 win = cwin[j], w = cwt[j];
         const float xin = cxin[j];
@@ -168,13 +175,13 @@ __global__ __launch_bounds__(256) void step2_ssm_fast(Step2Params p) {
         acc += xin * w.w;
         acc += cbias[j];
         const float v = silu_fast(acc);
-        if (c < P) {
+        if (c < PR) {
             s_x[c] = v;
             win_base[ch] = make_float4(win.y, win.z, win.w, xin);
-        } else if (c < P + N) {
-            s_B[c - P] = v;
+        } else if (c < PR + N) {
+            s_B[c - PR] = v;
         } else {
-            s_C[c - P - N] = v;
+            s_C[c - PR - N] = v;
         }
     }
     // dt = clamp(softplus(dt_raw + dt_bias), lo, hi), mamba2.rs:924 with the f32
@@ -201,43 +208,54 @@ __global__ __launch_bounds__(256) void step2_ssm_fast(Step2Params p) {
         v[i] = hn.x * C4.x + hn.y * C4.y + hn.z * C4.z + hn.w * C4.w;
     }
 
-    // 4. reduce-scatter over the LPR lanes of each row group: at xor distance
-    //    s the lane with bit s set keeps the upper half of its partials.  After
-    //    log2(R) steps lane n4 holds row index (n4 >> 2), summed over 8 lanes;
-    //    two more butterflies finish the sum over all LPR lanes.
-#pragma unroll
-    for (int half = R / 2, s = 2 * R; half >= 1; half >>= 1, s >>= 1) {
-        const bool up = (n4 & s) != 0;
-#pragma unroll
-        for (int j = 0; j < half; ++j) {
-            const float keep = up ? v[j + half] : v[j];
-            const float send = up ? v[j] : v[j + half];
-            v[j] = keep + __shfl_xor(send, s, 64);
-        }
-    }
-    float ysum = v[0];
-    ysum += __shfl_xor(ysum, 2, 64);
-    ysum += __shfl_xor(ysum, 1, 64);
-
-    // 5. y = C.h + D x, gate, write gated value and its square
+    // 5. y = C.h + D x, gate, write gated value and its square (row pr of the
+    //    workgroup, ysum its C.h)
     float sq = 0.f;
-    if ((n4 & 3) == 0) {
-        const int pr = row0 + (n4 >> 2) * RPI;
+    auto finish_row = [&](int pr, float ysum) {
         const float y = ysum + Dh * s_x[pr];
+        const int ci = h * P + r0 + pr;  // channel
         float gv = y;
         if (PACK) {
-            const float zg = silu_fast(zx_at<ZS>(p, zrow, b, h * P + pr));
+            const float zg = silu_fast(zx_at<ZS>(p, zrow, b, ci));
             if (!p.norm_before_gate) gv *= zg;
-            s_pk[pr] = p.norm_before_gate ? y * p.norm_w[h * P + pr] * zg : gv * p.norm_w[h * P + pr];
+            s_pk[pr] = p.norm_before_gate ? y * p.norm_w[ci] * zg : gv * p.norm_w[ci];
         } else {
-            if (!p.norm_before_gate) gv *= silu_fast(zx_at<ZS>(p, zrow, b, h * P + pr));
-            p.g_ws[(int64_t)b * p.d_inner + h * P + pr] = gv;
+            if (!p.norm_before_gate) gv *= silu_fast(zx_at<ZS>(p, zrow, b, ci));
+            p.g_ws[(int64_t)b * p.d_inner + ci] = gv;
         }
-        sq = gv * gv;
+        sq += gv * gv;
+    };
+    if (RS == 1) {
+        // 4. reduce-scatter over the LPR lanes of each row group: at xor distance
+        //    s the lane with bit s set keeps the upper half of its partials.  After
+        //    log2(R) steps lane n4 holds row index (n4 >> 2), summed over 8 lanes;
+        //    two more butterflies finish the sum over all LPR lanes.
+#pragma unroll
+        for (int half = R / 2, s = 2 * R; half >= 1; half >>= 1, s >>= 1) {
+            const bool up = (n4 & s) != 0;
+#pragma unroll
+            for (int j = 0; j < half; ++j) {
+                const float keep = up ? v[j + half] : v[j];
+                const float send = up ? v[j] : v[j + half];
+                v[j] = keep + __shfl_xor(send, s, 64);
+            }
+        }
+        float ysum = v[0];
+        ysum += __shfl_xor(ysum, 2, 64);
+        ysum += __shfl_xor(ysum, 1, 64);
+        if ((n4 & 3) == 0) finish_row(row0 + (n4 >> 2) * RPI, ysum);
+    } else {
+        // 4'. R rows per thread: each row's sum over its LPR lanes by DPP, in
+        //     the row's last lane
+#pragma unroll
+        for (int i = 0; i < R; ++i) v[i] = group_sum_last<LPR>(v[i]);
+        if (n4 == LPR - 1)
+#pragma unroll
+            for (int i = 0; i < R; ++i) finish_row(row0 + i * RPI, v[i]);
     }
     sq = block_sum_256(sq, s_red);  // its barriers also publish s_pk
-    if (t == 0) p.ssq_ws[bh] = sq;
-    if (PACK && t < P / 8) {
+    if (t == 0) p.ssq_ws[(int64_t)bh * RS + rs] = sq;
+    if (PACK && t < PR / 8) {
         // 8 consecutive channels are one 16-byte run of the packed layout
         const float4 lo = reinterpret_cast<const float4*>(s_pk)[2 * t];
         const float4 hi = reinterpret_cast<const float4*>(s_pk)[2 * t + 1];
@@ -246,7 +264,7 @@ __global__ __launch_bounds__(256) void step2_ssm_fast(Step2Params p) {
         v.y = (uint32_t)f32_to_bf16(lo.z) | ((uint32_t)f32_to_bf16(lo.w) << 16);
         v.z = (uint32_t)f32_to_bf16(hi.x) | ((uint32_t)f32_to_bf16(hi.y) << 16);
         v.w = (uint32_t)f32_to_bf16(hi.z) | ((uint32_t)f32_to_bf16(hi.w) << 16);
-        *reinterpret_cast<uint4*>(p.a_out + lin_act_offset(b, h * P + 8 * t, p.a_mt)) = v;
+        *reinterpret_cast<uint4*>(p.a_out + lin_act_offset(b, h * P + r0 + 8 * t, p.a_mt)) = v;
     }
 }
 
@@ -516,6 +534,7 @@ namespace mamba {
 // Every thread keeps its columns in registers between the two parts.
 struct RowsParams {
     int M, cols, H, d_inner, conv_dim, conv_k, nbc;  // nbc: B/C channels (2 G N)
+    int nssq;  // sum-of-squares partials per row (heads x state-kernel row splits)
     float* x; int64_t x_ld;
     const float* part; const float* bias; const float* ssq;
     float* conv; const float* zx_part; int zx_S; int64_t zx_ld; const float* zx_bias;
@@ -587,7 +606,7 @@ __global__ __launch_bounds__(kRowsThreads) void layer_rows(RowsParams p) {
         }
     }
     float ss_h = 0.f;
-    if (S > 0 && t < p.H) ss_h = p.ssq[(int64_t)m * p.H + t];
+    if (S > 0 && t < p.nssq) ss_h = p.ssq[(int64_t)m * p.nssq + t];
     if (S > 0) {
         // ---- residual of the layer just computed ----
         const float rms = sqrtf(block_sum_rows(ss_h, s_red) / (float)p.d_inner + kDivEpsF32);
@@ -643,7 +662,20 @@ static void rows_launch(const RowsParams& rp, int S, hipStream_t stream) {
 
 struct LayerGeom {
     int M, d_model, H, d_inner, conv_dim, d_in_proj, nbc, mt, S_in, S_out, nw_in, nw_out;
+    int rs;  // state-kernel workgroups per (row, head)
 };
+
+// Row splits of the state kernel: with few batch rows, one workgroup per
+// (row, head) leaves most CUs idle (80 workgroups at batch 1 for the 2.7B
+// layer), so each head's 64 state rows are shared by up to 8 workgroups, until
+// the launch has at least kStep2MinGroups of them.
+constexpr int kStep2MinGroups = 512;
+static int step2_row_splits(int rows, int heads, int N) {
+    const int cap = N == 128 ? 8 : 4;  // R >= 1 float4 per thread, 8 rows per workgroup
+    int rs = 1;
+    while (rs < cap && rows * heads * rs < kStep2MinGroups) rs *= 2;
+    return rs;
+}
 
 // Products of a call that runs beside another stream's layers (a batch split
 // over two streams) with one 32-row tile: in_proj with one k-split and 8 waves
@@ -677,6 +709,7 @@ static LayerGeom layer_geom(const mamba2_layer_args* a) {
     g.mt = lin_mt(g.M);
     g.S_in = lin_splits(g.M, g.d_model, g.d_in_proj);
     g.S_out = lin_splits(g.M, g.d_inner, g.d_model);
+    g.rs = step2_row_splits(g.M, g.H, a->dstate);
     g.nw_in = g.nw_out = 0;
     if (a->concurrent && g.mt == 1) {
         g.S_in = MAMBA_STEP2_CC_S_IN;
@@ -695,7 +728,7 @@ static LayerWs layer_ws_layout(const LayerGeom& g, void* base) {
     w.a_in = reinterpret_cast<bf16_t*>(take(lin_act_elems(g.M, g.d_model) * 2));
     w.zx_part = reinterpret_cast<float*>(take(lin_part_elems(g.M, g.d_in_proj, g.S_in) * 4));
     w.a_out = reinterpret_cast<bf16_t*>(take(lin_act_elems(g.M, g.d_inner) * 2));
-    w.ssq = reinterpret_cast<float*>(take((size_t)g.M * g.H * 4));
+    w.ssq = reinterpret_cast<float*>(take((size_t)g.M * g.H * g.rs * 4));
     w.out_part = reinterpret_cast<float*>(take(lin_part_elems(g.M, g.d_model, g.S_out) * 4));
     w.total = off;
     return w;
@@ -759,18 +792,27 @@ static int layer_core(const mamba2_layer_args* a, const LayerGeom& g, const Laye
     p.a_out = w.a_out; p.a_mt = g.mt;
     p.zx_part = w.zx_part; p.zx_S = g.S_in; p.zx_ld = g.d_in_proj; p.zx_bias = a->in_proj_b;
     if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, stream));
-    const dim3 kg(p.nb * p.H), kb(256);
-#define MAMBA_STEP2_PACKED(NN)                                                                        \
+    const dim3 kg(p.nb * p.H * g.rs), kb(256);
+#define MAMBA_STEP2_PACKED(NN, RS)                                                                     \
     switch (g.S_in) {                                                                                  \
-        case 1: hipLaunchKernelGGL((step2_ssm_fast<NN, true, 1>), kg, kb, 0, stream, p); break;        \
-        case 2: hipLaunchKernelGGL((step2_ssm_fast<NN, true, 2>), kg, kb, 0, stream, p); break;        \
-        case 4: hipLaunchKernelGGL((step2_ssm_fast<NN, true, 4>), kg, kb, 0, stream, p); break;        \
-        default: hipLaunchKernelGGL((step2_ssm_fast<NN, true, 0>), kg, kb, 0, stream, p); break;       \
+        case 1: hipLaunchKernelGGL((step2_ssm_fast<NN, true, 1, RS>), kg, kb, 0, stream, p); break;    \
+        case 2: hipLaunchKernelGGL((step2_ssm_fast<NN, true, 2, RS>), kg, kb, 0, stream, p); break;    \
+        case 4: hipLaunchKernelGGL((step2_ssm_fast<NN, true, 4, RS>), kg, kb, 0, stream, p); break;    \
+        default: hipLaunchKernelGGL((step2_ssm_fast<NN, true, 0, RS>), kg, kb, 0, stream, p); break;   \
     }
     if (p.N == 128) {
-        MAMBA_STEP2_PACKED(128)
+        switch (g.rs) {
+            case 1: MAMBA_STEP2_PACKED(128, 1) break;
+            case 2: MAMBA_STEP2_PACKED(128, 2) break;
+            case 4: MAMBA_STEP2_PACKED(128, 4) break;
+            default: MAMBA_STEP2_PACKED(128, 8) break;
+        }
     } else {
-        MAMBA_STEP2_PACKED(64)
+        switch (g.rs) {
+            case 1: MAMBA_STEP2_PACKED(64, 1) break;
+            case 2: MAMBA_STEP2_PACKED(64, 2) break;
+            default: MAMBA_STEP2_PACKED(64, 4) break;
+        }
     }
 #undef MAMBA_STEP2_PACKED
     MAMBA_CHECK_LAUNCH();
@@ -789,6 +831,7 @@ static int layer_core(const mamba2_layer_args* a, const LayerGeom& g, const Laye
 static RowsParams rows_params(const mamba2_layer_args* a, const LayerGeom& g, const LayerWs& w) {
     RowsParams rp = {};
     rp.M = g.M; rp.cols = g.d_model; rp.H = g.H; rp.d_inner = g.d_inner; rp.conv_dim = g.conv_dim;
+    rp.nssq = g.H * g.rs;
     rp.conv_k = a->conv_kernel; rp.nbc = g.nbc;
     rp.x = a->x; rp.x_ld = a->x_sb;
     rp.part = w.out_part; rp.bias = a->out_proj_b; rp.ssq = w.ssq;
