@@ -117,7 +117,12 @@ __device__ __forceinline__ float group_sum_last(float v) {
 __device__ __forceinline__ float wave_sum_dpp(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(group_sum_last<64>(v)), 63));
 }
+// Inclusive prefix sum over the wave.  The input is made opaque first: a
+// caller's product (a scan of dt A) would otherwise be contracted into the
+// first add as an fma in some kernels and not in others, and kernels that
+// must agree bit for bit scan the same values.
 __device__ __forceinline__ float wave_incl_scan(float v) {
+    asm volatile("" : "+v"(v));
     v += dpp_term(v, 0x111, 0xf);  // row_shr:1
     v += dpp_term(v, 0x112, 0xf);  // row_shr:2
     v += dpp_term(v, 0x114, 0xf);  // row_shr:4

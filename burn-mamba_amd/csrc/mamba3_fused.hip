@@ -23,7 +23,10 @@
 //     angle is carried to the next chunk;
 //   * B rows (row-major LDS tile, the shared MFMA operand): RMS over the row's
 //     16 lanes, norm weight and per-(head, rank) bias, the (k, k + N/2)
-//     rotation with the partner column from lane ^ 8, rounded to bf16;
+//     rotation with the partner column from lane ^ 8, rounded to bf16; at
+//     MIMO rank 1 (SISO) the (2k, 2k + 1) rotation inside the lane, with the
+//     angles tabulated per (step, pair) and their cos / sin formed by the row
+//     threads (a per-step cos / sin table of 128 steps does not fit in LDS);
 //   * C rows (each wave's MFMA fragments, in registers): the same, the RMS
 //     completed with lane ^ 32 and both rotation partners in the same lane;
 //   * v^T = (x mimo_x)^T and its w-scaled copy from the x columns.
@@ -46,21 +49,24 @@ struct M3FusedParams {
     bf16_t* y;  // [b, L, M, H, 64] contiguous
 };
 
-// y staged in LDS for whole-line stores, except at M = 2, whose cos / sin
-// tables leave no room for the staging tiles: y is then stored straight from
-// the accumulators (8 bytes per lane and row)
+// y staged in LDS for whole-line stores, except at M = 1 and 2, whose angle
+// or cos / sin tables leave no room for the staging tiles: y is then stored
+// straight from the accumulators (8 bytes per lane and row)
 template <int M>
-constexpr int m3f_ny() { return M == 2 ? 1 : 4; }
+constexpr int m3f_ny() { return M <= 2 ? 1 : 4; }
 
 template <int M>
 struct __align__(16) M3FusedLds {
+    static constexpr int TS = 128 / M;                   // steps per chunk
+    static constexpr int TCS = M == 1 ? 1 : TS;          // rows of the cos / sin tables
     Ssd3Lds<128, 1, m3f_ny<M>()> core;  // one chunk-entry state buffer: written at the next chunk's start
-    bf16_t C[128][136];                      // C rows of the chunk (the y tiles' MFMA B operand)
-    float cs[128 / M][64], sn[128 / M][64];  // cos / sin per step and pair index k, at m3f_pos(k)
-    float4 bwb[M][4][16], cwb[M][4][16];     // (w, bias, w, bias) of columns 8 nv + 2 e2 (+1) of B / C
-                                             // per rank, at [m][e2][nv]
-    float mx[M][32];                         // mimo_x of this headdim half
-    float dt[128 / M];                       // dt per step of the chunk (0 past the end)
+    bf16_t C[128][136];                  // C rows of the chunk (the y tiles' MFMA B operand)
+    float cs[TCS][64], sn[TCS][64];      // M > 1: cos / sin per step and pair index k, at m3f_pos(k)
+    int ang[M == 1 ? TS : 1][64];        // M = 1: the angle per step and pair index k (grid units)
+    float4 bwb[M][4][16], cwb[M][4][16];  // (w, bias, w, bias) of columns 8 nv + 2 e2 (+1) of B / C
+                                          // per rank, at [m][e2][nv]
+    float mx[M][32];                      // mimo_x of this headdim half
+    float dt[TS];                         // dt per step of the chunk (0 past the end)
 };
 
 __device__ __forceinline__ float m3f_bf(uint32_t u) { return __uint_as_float(u << 16); }
@@ -126,10 +132,49 @@ __device__ __forceinline__ void m3f_rows(uint4 r0, uint4 r1, const float (&w)[8]
                                pack_bf16x2(y1[6], y1[7]));
 }
 
+// Two consecutive steps' rows at M = 1 x 8 columns: the RMS, weight and bias
+// as m3f_rows, then the (2k, 2k + 1) rotation inside the lane with the cos /
+// sin of the thread's pairs 4 nv .. 4 nv + 3 of each row's step (c0 / s0,
+// c1 / s1), as the segment prep rotates SISO rows.
+__device__ __forceinline__ void m3f_rows1(uint4 r0, uint4 r1, const float (&w)[8], const float (&bias)[8],
+                                          const float (&c0)[4], const float (&s0)[4], const float (&c1)[4],
+                                          const float (&s1)[4], bf16_t* dst0, bf16_t* dst1, float (&y0)[8],
+                                          float (&y1)[8]) {
+    const uint32_t a0[4] = {r0.x, r0.y, r0.z, r0.w}, a1[4] = {r1.x, r1.y, r1.z, r1.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        y0[2 * e] = s3_lo(a0[e]); y0[2 * e + 1] = s3_hi(a0[e]);
+        y1[2 * e] = s3_lo(a1[e]); y1[2 * e + 1] = s3_hi(a1[e]);
+    }
+    const float ss0 = m3_group_sum<16>(m3_sumsq8(y0));
+    const float ss1 = m3_group_sum<16>(m3_sumsq8(y1));
+    const float rms0 = m3_rms_inv(ss0, 128), rms1 = m3_rms_inv(ss1, 128);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        y0[e] = m3_norm(y0[e], rms0, w[e], bias[e]);
+        y1[e] = m3_norm(y1[e], rms1, w[e], bias[e]);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float u0 = y0[2 * j], u1 = y0[2 * j + 1];
+        y0[2 * j] = m3_rot(c0[j], u0, -s0[j], u1);
+        y0[2 * j + 1] = m3_rot(c0[j], u1, s0[j], u0);
+        const float v0 = y1[2 * j], v1 = y1[2 * j + 1];
+        y1[2 * j] = m3_rot(c1[j], v0, -s1[j], v1);
+        y1[2 * j + 1] = m3_rot(c1[j], v1, s1[j], v0);
+    }
+    *(uint4*)dst0 = make_uint4(pack_bf16x2(y0[0], y0[1]), pack_bf16x2(y0[2], y0[3]), pack_bf16x2(y0[4], y0[5]),
+                               pack_bf16x2(y0[6], y0[7]));
+    *(uint4*)dst1 = make_uint4(pack_bf16x2(y1[0], y1[1]), pack_bf16x2(y1[2], y1[3]), pack_bf16x2(y1[4], y1[5]),
+                               pack_bf16x2(y1[6], y1[7]));
+}
+
 // M bf16 values to LDS as one store (2 M bytes, aligned to its size)
 template <int M>
 __device__ __forceinline__ void m3f_st(bf16_t* dst, const float* v) {
-    if constexpr (M == 2) {
+    if constexpr (M == 1) {
+        *dst = __builtin_bit_cast(bf16_t, s3_h16(v[0]));  // the hardware conversion, as for M > 1
+    } else if constexpr (M == 2) {
         *(uint32_t*)dst = pack_bf16x2(v[0], v[1]);
     } else if constexpr (M == 4) {
         *(uint2*)dst = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
@@ -146,8 +191,8 @@ template <int M>
 __global__ __launch_bounds__(512, 1) void mamba3_ssd_fused(M3FusedParams p) {
     constexpr int QF = 128, N = 128;
     constexpr int TS = QF / M;                    // steps per chunk
-    constexpr int lgM = M == 2 ? 1 : (M == 4 ? 2 : 3);
-    static_assert(M == 2 || M == 4 || M == 8, "MIMO rank 2, 4 or 8");
+    constexpr int lgM = M == 1 ? 0 : M == 2 ? 1 : (M == 4 ? 2 : 3);
+    static_assert(M == 1 || M == 2 || M == 4 || M == 8, "MIMO rank 1, 2, 4 or 8");
     constexpr int JA = TS / 8;                    // steps per angle thread (8 threads per angle)
     constexpr int XI = TS * 8, XPT = (XI + 511) / 512;  // x items: (step, 4-wide headdim piece)
     constexpr int RP = 2;                         // B row pairs and C row pairs per thread
@@ -204,11 +249,12 @@ __global__ __launch_bounds__(512, 1) void mamba3_ssd_fused(M3FusedParams p) {
     // angles: a = tid / 8 over steps q JA .. q JA + JA - 1, q = tid % 8
     const uint32_t ao = (uint32_t)((tid_ & 7) * JA) * rs + (uint32_t)(p.o_dt + 3 * p.H + min(tid_ >> 3, p.A - 1)) * 2;
     // B and C rows: pairs fp = tid / 16 + 32 k (rows 2 fp, 2 fp + 1: ranks bm0, bm0 + 1 of one
-    // step), columns 8 nv .. 8 nv + 7
+    // step; at M = 1 steps 2 fp and 2 fp + 1), columns 8 nv .. 8 nv + 7
     const uint32_t bro = (uint32_t)((2 * (tid_ >> 4)) >> lgM) * rs +
                          (uint32_t)((((2 * (tid_ >> 4)) & (M - 1)) * p.G + g) * N + (tid_ & 15) * 8) * 2;
     const uint32_t bo = bro + (uint32_t)p.o_b * 2, cofs = bro + (uint32_t)p.o_c * 2;
-    const uint32_t r2 = (uint32_t)p.G * N * 2;  // the pair's second row (rank bm0 + 1)
+    // the pair's second row: rank bm0 + 1 of the step, or at M = 1 the next step's row
+    const uint32_t r2 = M == 1 ? rs : (uint32_t)p.G * N * 2;
 
     // ---- register prefetch of one chunk's raw proj data
     uint2 xq[XPT];
@@ -359,12 +405,19 @@ __global__ __launch_bounds__(512, 1) void mamba3_ssd_fused(M3FusedParams p) {
             const int base = theta + (incl - run);
             const int total = m3f_last8(incl);
             const bool rot_on = ang_a < p.npair;
+            if constexpr (M == 1) {
+                // the angles themselves; the row threads form their cos / sin
+                if (ang_a < 64)
 #pragma unroll
-            for (int j = 0; j < JA; ++j) {
-                float c = 1.f, sn = 0.f;
-                if (rot_on) m3_cossin(m3_ang_rad(m3_ang_reduce(base + cum[j])), c, sn);
-                SF.cs[ang_q * JA + j][m3f_pos(ang_a)] = c;
-                SF.sn[ang_q * JA + j][m3f_pos(ang_a)] = sn;
+                    for (int j = 0; j < JA; ++j) SF.ang[ang_q * JA + j][ang_a] = m3_ang_reduce(base + cum[j]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < JA; ++j) {
+                    float c = 1.f, sn = 0.f;
+                    if (rot_on) m3_cossin(m3_ang_rad(m3_ang_reduce(base + cum[j])), c, sn);
+                    SF.cs[ang_q * JA + j][m3f_pos(ang_a)] = c;
+                    SF.sn[ang_q * JA + j][m3f_pos(ang_a)] = sn;
+                }
             }
             theta = m3_ang_reduce(theta + total);  // the chunk's last angle
         }
@@ -389,10 +442,10 @@ __global__ __launch_bounds__(512, 1) void mamba3_ssd_fused(M3FusedParams p) {
                     for (int e = 0; e < 4; ++e) {
                         const float vb = (float)(__bf16)(xv[e] * mxa[e]);  // v as the SSD seam holds it (bf16)
                         vt[e][m] = vb;
-                        // w v as hi + lo (hi exact in bf16, lo rounded by the store)
-                        const float x = vb * wf;
-                        vw[e][m] = (float)(__bf16)x;
-                        vwl[e][m] = x - vw[e][m];
+                        // w v as hi + lo, split as the seam splits it (hi exact in bf16, lo
+                        // rounded by the store)
+                        vw[e][m] = (float)(__bf16)(vb * wf);
+                        vwl[e][m] = s3_res(vb, wf, vw[e][m]);
                     }
                 }
 #pragma unroll
@@ -408,7 +461,44 @@ __global__ __launch_bounds__(512, 1) void mamba3_ssd_fused(M3FusedParams p) {
         fetch(c + 1);
         __builtin_amdgcn_sched_barrier(0);
         // ---- C: B and C rows to LDS; v^T and w-scaled v^T
-        {
+        if constexpr (M == 1) {
+            float bw[8], bb[8], cw[8], cb[8];
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                const float4 u = SF.bwb[0][e >> 1][b_nv], v = SF.cwb[0][e >> 1][b_nv];
+                bw[e] = u.x; bb[e] = u.y; bw[e + 1] = u.z; bb[e + 1] = u.w;
+                cw[e] = v.x; cb[e] = v.y; cw[e + 1] = v.z; cb[e + 1] = v.w;
+            }
+#pragma unroll
+            for (int k = 0; k < RP; ++k) {
+                const int f0 = 2 * (b_fp + 32 * k);  // steps f0 and f0 + 1 of the chunk
+                // cos / sin of the thread's pairs 4 nv .. 4 nv + 3 at both steps ((1, 0) past
+                // the rotated pairs)
+                float c0[4], s0[4], c1[4], s1[4];
+                const int4 q0 = *(const int4*)&SF.ang[f0][4 * b_nv], q1 = *(const int4*)&SF.ang[f0 + 1][4 * b_nv];
+                const int qa0[4] = {q0.x, q0.y, q0.z, q0.w}, qa1[4] = {q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    c0[j] = 1.f; s0[j] = 0.f; c1[j] = 1.f; s1[j] = 0.f;
+                    if (4 * b_nv + j < p.npair) {
+                        m3_cossin(m3_ang_rad(qa0[j]), c0[j], s0[j]);
+                        m3_cossin(m3_ang_rad(qa1[j]), c1[j], s1[j]);
+                    }
+                }
+                float y0[8], y1[8];
+                m3f_rows1(bq[k][0], bq[k][1], bw, bb, c0, s0, c1, s1, &S.B[f0][b_nv * 8], &S.B[f0 + 1][b_nv * 8],
+                          y0, y1);
+                // the cache tail: the last step's rotated B (f32)
+                if (ph == 0 && t0 + f0 + 1 >= p.L - 1 && t0 + f0 <= p.L - 1) {
+                    const float* yl = t0 + f0 == p.L - 1 ? y0 : y1;
+                    float* k0 = p.kst + ((int64_t)b * p.H + h) * N + b_nv * 8;
+                    *(float4*)k0 = make_float4(yl[0], yl[1], yl[2], yl[3]);
+                    *(float4*)(k0 + 4) = make_float4(yl[4], yl[5], yl[6], yl[7]);
+                }
+                m3f_rows1(cq[k][0], cq[k][1], cw, cb, c0, s0, c1, s1, &SF.C[f0][b_nv * 8], &SF.C[f0 + 1][b_nv * 8],
+                          y0, y1);
+            }
+        } else {
             float bw[8], bb0[8], bb1[8], cw[8], cb0[8], cb1[8];
 #pragma unroll
             for (int e = 0; e < 8; e += 2) {
@@ -515,7 +605,7 @@ static int m3_fused_params(const mamba3_fused_args* a, M3PrepParams* pp, M3Fused
     const int M = p.M;
     const int TS = M > 0 ? 128 / M : 0;
     auto al16 = [](const void* q) { return ((uintptr_t)q & 15u) == 0; };
-    *ok = p.proj_bf16 && p.P == 64 && p.N == 128 && (M == 2 || M == 4 || M == 8) && al16(p.proj) &&
+    *ok = p.proj_bf16 && p.P == 64 && p.N == 128 && (M == 1 || M == 2 || M == 4 || M == 8) && al16(p.proj) &&
           al16(a->y) && al16(p.kst) && al16(p.vst) && p.proj_sl % 8 == 0 && (p.nb == 1 || p.proj_sb % 8 == 0) && p.A <= 64 &&
           (int64_t)(TS + 1) * p.proj_sl * 2 < (1ll << 31) && (int64_t)p.L * M < (1ll << 30) &&
           (int64_t)p.nb * p.H * 2 < (1ll << 31);
@@ -544,6 +634,7 @@ static int m3_fused_run(const mamba3_fused_args* a, hipStream_t s, hipEvent_t ev
     MAMBA_CHECK_LAUNCH();
     const dim3 grid(fp.nb * fp.H * 2), block(512);
     switch (pp.M) {
+        case 1: hipLaunchKernelGGL(mamba3_ssd_fused<1>, grid, block, 0, s, fp); break;
         case 2: hipLaunchKernelGGL(mamba3_ssd_fused<2>, grid, block, 0, s, fp); break;
         case 4: hipLaunchKernelGGL(mamba3_ssd_fused<4>, grid, block, 0, s, fp); break;
         default: hipLaunchKernelGGL(mamba3_ssd_fused<8>, grid, block, 0, s, fp); break;

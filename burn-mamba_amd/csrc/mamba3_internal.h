@@ -79,7 +79,7 @@ __device__ __forceinline__ int m3_ang_reduce(int q) {
 // fraction keeps the grid's full resolution
 __device__ __forceinline__ int m3_ang_fix(float a) {
     constexpr float two_pi = 6.28318530717958647692f;
-    const float r = a - rintf(a * (1.f / two_pi)) * two_pi;
+    const float r = __builtin_fmaf(-rintf(a * (1.f / two_pi)), two_pi, a);  // explicit: no contraction choice
     const float w = rintf(r);
     return m3_ang_reduce((int)w * (int)kAngUnit + (int)rintf((r - w) * kAngUnit));
 }

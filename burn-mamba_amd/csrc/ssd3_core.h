@@ -52,6 +52,16 @@ __device__ __forceinline__ float s3_hi(uint32_t w) { return __uint_as_float(w & 
 // 1e-2.
 __device__ __forceinline__ __bf16 s3_h16(float x) { return (__bf16)x; }
 __device__ __forceinline__ __bf16 s3_l16(float x) { return (__bf16)(x - (float)(__bf16)x); }
+// hi + lo of a product a b: hi = bf16(a b), and the residual a b - hi formed
+// by an explicit fma (exact before its rounding), so that no kernel's result
+// depends on whether the compiler contracts a b - hi into an fma: the kernels
+// that must agree bit for bit (the fused Mamba-3 prefill and the seam scan)
+// split their products this way.
+__device__ __forceinline__ float s3_res(float a, float b, float hi) { return __builtin_fmaf(a, b, -hi); }
+__device__ __forceinline__ void s3_split(float a, float b, __bf16& hi, __bf16& lo) {
+    hi = (__bf16)(a * b);
+    lo = (__bf16)s3_res(a, b, (float)hi);
+}
 
 // LDS of one workgroup (about 109 KB at QF = 128 with HB = 2).  HB: buffers
 // of the chunk-entry state (2: the next chunk's state is written while this
@@ -144,9 +154,10 @@ __device__ __forceinline__ void ssd3_y_tile(Ssd3Lds<QF, HB, NY>& S, const s3_bf1
             s3_bf16x8_t bop, bopl;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float x = d[8 * kk + e] * fac[8 * kk + e];
-                bop[e] = s3_h16(x);
-                bopl[e] = s3_l16(x);
+                __bf16 hi, lo;
+                s3_split(d[8 * kk + e], fac[8 * kk + e], hi, lo);
+                bop[e] = hi;
+                bopl[e] = lo;
             }
             // v^T[p][j] in the same permuted k order: j = 32 jt + 16 kk + 4 half + {0..3, 8..11}
             const int j0 = jt * 32 + 16 * kk + 4 * half;

@@ -192,9 +192,16 @@ __global__ __launch_bounds__(256, 1) void ssd3_scan_mfma(Ssd3MfmaParams p) {
                 for (int e = 0; e < 4; ++e) {
                     *(uint32_t*)&S.xT[pv * 8 + 2 * e][2 * fp] = (a0[e] & 0xffffu) | (a1[e] << 16);
                     *(uint32_t*)&S.xT[pv * 8 + 2 * e + 1][2 * fp] = (a0[e] >> 16) | (a1[e] & 0xffff0000u);
-                    const float wv[4] = {s3_lo(a0[e]) * w0, s3_lo(a1[e]) * w1, s3_hi(a0[e]) * w0, s3_hi(a1[e]) * w1};
-                    const s3_bf16x4_t q = {s3_h16(wv[0]), s3_h16(wv[1]), s3_h16(wv[2]), s3_h16(wv[3])};
-                    const s3_bf16x4_t ql = {s3_l16(wv[0]), s3_l16(wv[1]), s3_l16(wv[2]), s3_l16(wv[3])};
+                    const float va[4] = {s3_lo(a0[e]), s3_lo(a1[e]), s3_hi(a0[e]), s3_hi(a1[e])};
+                    const float wa[4] = {w0, w1, w0, w1};
+                    s3_bf16x4_t q, ql;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        __bf16 hi, lo;
+                        s3_split(va[i], wa[i], hi, lo);
+                        q[i] = hi;
+                        ql[i] = lo;
+                    }
                     const uint2 qq = __builtin_bit_cast(uint2, q), qql = __builtin_bit_cast(uint2, ql);
                     *(uint32_t*)&S.xTw[pv * 8 + 2 * e][2 * fp] = qq.x;
                     *(uint32_t*)&S.xTw[pv * 8 + 2 * e + 1][2 * fp] = qq.y;

@@ -16,9 +16,11 @@ C ABI), checked on identical inputs stage by stage (single_ssd/single_ssd/mod.rs
 
 Cases: the config-4 head shape (headdim 64, dstate 128, MIMO 4, every pair
 rotated) over several chunks with a ragged tail, MIMO 2 with two groups and
-half the pairs rotated, MIMO 8 with the rotation off; split calls; the block
-forward taking the fused path, and against the oracle pipeline with
-block-init weights."""
+half the pairs rotated, MIMO 8 with the rotation off, SISO (MIMO 1: 128-step
+chunks, adjacent rotation pairs) with every pair rotated and with two groups
+and half the pairs rotated; split calls; the block forward taking the fused
+path (MIMO 4 and SISO), and against the oracle pipeline with block-init
+weights."""
 
 import numpy as np
 import pytest
@@ -34,7 +36,11 @@ CASES = [
     (1, 257, 2, 1, 4, 128),   # one step past a chunk boundary
     (1, 70, 4, 2, 2, 64),     # MIMO 2 (64-step chunks), two groups, half the pairs rotated
     (2, 45, 2, 1, 8, 0),      # MIMO 8 (16-step chunks), rotation off
+    (2, 300, 4, 1, 1, 128),   # SISO: 128-step chunks, ragged third chunk, every pair rotated
+    (1, 129, 2, 2, 1, 64),    # SISO: one step past a chunk, two groups, half the pairs rotated
 ]
+# the cases of the bit-for-bit comparison with the unfused sequence
+EQUAL_CASES = CASES[:3] + CASES[4:]
 
 # north_star's bar for bf16 in / f32 accumulate, element by element
 BF16_TOL = dict(rtol=2e-2, atol=1e-2)
@@ -172,7 +178,7 @@ def test_mamba3_fused_matches_oracle(case):
         assert bool((getattr(cg, nm) == getattr(cu, nm)).all()), nm
 
 
-@pytest.mark.parametrize("case", CASES[:3])
+@pytest.mark.parametrize("case", EQUAL_CASES)
 def test_mamba3_fused_equals_prep_then_seam(case):
     """With D = NULL the fused kernel is the unfused sequence mamba3_prep_fwd ->
     mamba_ssd3_fwd (per-head v, B, C and coefficients in HBM), bit for bit."""
@@ -208,14 +214,16 @@ def test_mamba3_fused_split_carries_cache():
     np.testing.assert_array_equal(c2.v_state_bhp.cpu().numpy(), cg.v_state_bhp.cpu().numpy())
 
 
-def test_mamba3_block_forward_takes_fused_path():
-    """Mamba3.forward (single-ssd cache) at the config-4 head shape runs the
-    fused scan, and equals the same block through the unfused sequence."""
+@pytest.mark.parametrize("mimo", [4, 1])
+def test_mamba3_block_forward_takes_fused_path(mimo):
+    """Mamba3.forward (single-ssd cache) at the config-4 head shape (and its
+    SISO twin) runs the fused scan, and equals the same block through the
+    unfused sequence."""
     import torch
     import mamba_hip
     from mamba_hip import mamba3 as m3mod
-    print("block forward fused", flush=True)
-    cfg = mamba_hip.Mamba3Config(d_model=128, state_rank=128, per_head_dim=64, mimo_rank=4)
+    print("block forward fused, mimo", mimo, flush=True)
+    cfg = mamba_hip.Mamba3Config(d_model=128, state_rank=128, per_head_dim=64, mimo_rank=mimo)
     gen = torch.Generator(device="cuda")
     gen.manual_seed(11)
     m = cfg.init("cuda", torch.bfloat16, gen)
