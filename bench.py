@@ -741,11 +741,16 @@ def mamba3_fused_algorithmic(cfg):
 def bench_mamba3_fused(args):
     """The config-4 Mamba-3 prefill from the in_proj rows to y per rank
     (B=4 L=8192 H=32 P=64 N=128 MIMO 4, full rotation): mamba3_ssd_fused_fwd
-    (beta-seed kernel + the fused prologue / SSD scan), reference init."""
+    (beta-seed kernel + the fused prologue / SSD scan), reference init.
+    ``--mimo`` runs the same head shape at another MIMO rank (1: SISO, the
+    reference's default block)."""
     import torch
 
     import mamba_hip
     cfg = dict(SSD3_CFG4)
+    mimo = getattr(args, "mimo", 4)
+    cfg["mimo"] = mimo
+    wl = "mamba3_fused_prefill_cfg4" if mimo == 4 else f"mamba3_fused_prefill_cfg4_mimo{mimo}"
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev)
     gen.manual_seed(0)
@@ -758,7 +763,7 @@ def bench_mamba3_fused(args):
     a = mamba_hip.mamba3_fused_args(c, proj, cache, dt_bias=m.dt_bias, b_norm_w=m.b_norm_w, c_norm_w=m.c_norm_w,
                                     b_bias=m.b_bias, c_bias=m.c_bias, mimo_x=m.mimo_x, D=m.D)
     if mamba_hip.mamba3_fused_supported(a) != 1:
-        raise RuntimeError("config 4 is outside the fused kernel")
+        raise RuntimeError(f"config 4 at MIMO {mimo} is outside the fused kernel")
 
     def step(events=None):
         mamba_hip.mamba3_fused_run(a, cache, events)
@@ -774,19 +779,19 @@ def bench_mamba3_fused(args):
     else:
         roof = {"bound": "mfma", "achieved": tflops, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": tflops / BF16_PEAK_TFLOPS}
-    roof.update({"traffic": _profiled_traffic("mamba3_fused_prefill_cfg4"), "kernel_ms": kern_ms,
+    roof.update({"traffic": _profiled_traffic(wl), "kernel_ms": kern_ms,
                  "algorithmic_bytes": nbytes, "algorithmic_flops": flops, "hbm_gbs": gbs,
                  "timing": "HIP events around the seed and fused scan kernels on their stream, per call"})
     return {
-        "metric": "Mamba-3 prefill tokens/s, in_proj rows -> y per rank (B=4 L=8192 H=32 P=64 N=128 MIMO 4) "
-                  "+ % MFMA roofline",
+        "metric": f"Mamba-3 prefill tokens/s, in_proj rows -> y per rank (B=4 L=8192 H=32 P=64 N=128 MIMO {mimo}) "
+                  f"+ % {'MFMA' if not hbm_bound else 'HBM'} roofline",
         "value": tokens / (ms_per_step * 1e-3), "unit": "tokens/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": "synthetic (config-4 shapes, reference init, in_proj rows ~N(0,1), seed 0)",
-        "config": {"workload": "mamba3_fused_prefill_cfg4", **cfg, "rope_dim": c.rope_dim,
+        "config": {"workload": wl, **cfg, "rope_dim": c.rope_dim,
                    "io": "proj and y bf16, state f32",
-                   "entry": "mamba3_ssd_fused_fwd (mamba3_seed_kernel + mamba3_ssd_fused<4>)"},
+                   "entry": f"mamba3_ssd_fused_fwd (mamba3_seed_kernel + mamba3_ssd_fused<{mimo}>)"},
         "roofline": roof,
     }
 
@@ -1408,6 +1413,8 @@ def main():
     ap.add_argument("--workload", default="ssd2",
                     choices=["ssd2", "mamba1", "decode", "ssd3", "mamba3_fused", "mamba1_step", "mamba3_step",
                              "mamba3_prep", "mamba2_block", "ssd2_bwd", "ssd3_bwd", "mamba1_block"])
+    ap.add_argument("--mimo", type=int, default=4, choices=(1, 2, 4, 8),
+                    help="mamba3_fused: MIMO rank at config 4's head shape (4 is config 4; 1 is SISO)")
     ap.add_argument("--m1-shape", default="ref", choices=sorted(MAMBA1_BLOCK_SHAPES),
                     help="mamba1_block: the reference's bench shape (ref) or config 2's layer shape (cfg2)")
     ap.add_argument("--batch", type=int, default=DECODE_CFG3["batch"], help="decode batch")
@@ -1449,7 +1456,7 @@ def main():
         base = (lambda: cpu_baseline_mamba1_step(MAMBA1_STEP_CFG, args.batch))
     elif args.workload == "mamba3_fused":
         out = bench_mamba3_fused(args)
-        base = (lambda: cpu_baseline_mamba3_fused(SSD3_CFG4))
+        base = (lambda: cpu_baseline_mamba3_fused(dict(SSD3_CFG4, mimo=args.mimo)))
     elif args.workload == "ssd3":
         out = bench_ssd3(args)
         base = (lambda: cpu_baseline_ssd3(SSD3_CFG4))

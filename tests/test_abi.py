@@ -127,7 +127,10 @@ def test_fused_predicate_needs_no_gpu():
         setattr(p, name, 4096 * (i + 1))  # never dereferenced
     a.y, a.final_state = 4096 * 20, 4096 * 21
     assert L.mamba3_ssd_fused_supported(ctypes.byref(a)) == 1
-    for field, bad in (("headdim", 32), ("mimo", 1), ("proj_dtype", 0)):
+    p.mimo = 1  # SISO (its in_proj row is shorter than proj_sl: allowed)
+    assert L.mamba3_ssd_fused_supported(ctypes.byref(a)) == 1
+    p.mimo = 4
+    for field, bad in (("headdim", 32), ("proj_dtype", 0)):
         old = getattr(p, field)
         setattr(p, field, bad)
         assert L.mamba3_ssd_fused_supported(ctypes.byref(a)) == 0, field
