@@ -264,6 +264,100 @@ def bench_mamba1_block(args):
     return out
 
 
+# The reference's own published rows (bench.md:17-45, criterion medians of one
+# block at batch 2, sequence 256, d_model 256, state_rank 64 (16 for Mamba-1),
+# per_head_dim 64, in the backend's default float, f32): forward and step.
+REF_BLOCK_SHAPE = dict(batch=2, seqlen=256, d_model=256, state_rank=64, per_head_dim=64)
+REF_BLOCK_PUBLISHED_MS = {
+    ("forward", "mamba1"): ({"flex (CPU)": 71.78, "cuda": 23.36, "cuda + fusion + autotune": 40.56}, "bench.md:17"),
+    ("forward", "mamba2"): ({"flex (CPU)": 23.79, "cuda": 1.80, "cuda + fusion + autotune": 2.11}, "bench.md:18"),
+    ("forward", "mamba3/siso"): ({"flex (CPU)": 23.89, "cuda": 3.33, "cuda + fusion + autotune": 3.99}, "bench.md:19"),
+    ("forward", "mamba3/mimo-rank4"): ({"flex (CPU)": 122.58, "cuda": 9.27, "cuda + fusion + autotune": 4.78},
+                                       "bench.md:21"),
+    ("forward", "mamba3/siso-double-ssd"): ({"flex (CPU)": 30.55, "cuda": 3.40, "cuda + fusion + autotune": 4.85},
+                                            "bench.md:23"),
+    ("step", "mamba1"): ({"flex (CPU)": 0.346, "cuda": 0.777, "cuda + fusion + autotune": 0.704}, "bench.md:41"),
+    ("step", "mamba2"): ({"flex (CPU)": 0.296, "cuda": 0.738, "cuda + fusion + autotune": 0.933}, "bench.md:42"),
+    ("step", "mamba3/siso"): ({"flex (CPU)": 0.337, "cuda": 1.46, "cuda + fusion + autotune": 1.97}, "bench.md:43"),
+    ("step", "mamba3/mimo-rank4"): ({"flex (CPU)": 0.533, "cuda": 1.97, "cuda + fusion + autotune": 2.50},
+                                    "bench.md:45"),
+    ("step", "mamba3/siso-double-ssd"): ({"flex (CPU)": 0.321, "cuda": 1.46, "cuda + fusion + autotune": 1.99},
+                                         "bench.md:47"),
+}
+
+
+def bench_ref_block(args):
+    """One block at the reference's own bench shape and methodology
+    (benches/layer.rs:89-101, 176-205, 293-395): f32 (the default float of the
+    reference's backends), reference-init weights, input ~ N(0, 1); forward
+    from an empty cache (a double-SSD cache for siso-double-ssd), or a decode
+    step fed by the cache the previous step produced.  Every iteration is
+    issued eagerly (no HIP graph) and the device is drained once per timed
+    batch, as criterion's iter_custom does there.  `value` is ms per
+    iteration; the line carries the reference's published medians of the same
+    row (other hardware).  mimo-rank1 is the same block as siso here (the
+    reference's siso_specialization switch changes its own kernels only)."""
+    import torch
+
+    import mamba_hip
+    mode, case = args.ref_mode, args.ref_case
+    shp = dict(REF_BLOCK_SHAPE)
+    b, L, dm = shp["batch"], shp["seqlen"], shp["d_model"]
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(0)
+    f32 = torch.float32
+    if case == "mamba1":
+        m = mamba_hip.Mamba1Config(d_model=dm, state_rank=16).init("cuda", gen)
+    elif case == "mamba2":
+        m = mamba_hip.Mamba2Config(d_model=dm, state_rank=shp["state_rank"],
+                                   per_head_dim=shp["per_head_dim"]).init(dev, f32, gen)
+    else:
+        mimo = 4 if case == "mamba3/mimo-rank4" else 1
+        m = mamba_hip.Mamba3Config(d_model=dm, state_rank=shp["state_rank"], per_head_dim=shp["per_head_dim"],
+                                   mimo_rank=mimo).init(dev, f32, gen)
+    double = case == "mamba3/siso-double-ssd"
+
+    def fresh_cache():
+        return m.new_cache(b, "double") if double else (m.new_cache(b) if mode == "step" else None)
+
+    if mode == "forward":
+        x = torch.randn((b, L, dm), generator=gen, device=dev)
+
+        def it():
+            m.forward(x, fresh_cache())
+    else:
+        x = torch.randn((b, dm), generator=gen, device=dev)
+        state = {"cache": fresh_cache()}
+
+        def it():
+            _, state["cache"] = m.step(x, state["cache"])
+    log(f"warmup {args.warmup}")
+    warm(it, args.warmup)
+    log(f"timing {args.steps} iterations")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        it()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    pub, src = REF_BLOCK_PUBLISHED_MS[(mode, case)]
+    tokens = b * (L if mode == "forward" else 1)
+    return {
+        "metric": f"{case} block {mode} ms per iteration at the reference's bench shape (B={b} "
+                  f"{'L=' + str(L) + ' ' if mode == 'forward' else ''}d_model={dm}, f32)",
+        "value": ms, "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (x ~ N(0,1), reference init, seed 0)",
+        "config": {"workload": f"ref_block_{mode}_{case.replace('/', '_')}", **shp,
+                   "state_rank_used": 16 if case == "mamba1" else shp["state_rank"],
+                   "tokens_per_s": tokens / (ms * 1e-3),
+                   "timing": "eager iterations, one device drain per timed batch (as benches/layer.rs:176-187)"},
+        "roofline": None,
+        "reference_published_ms": dict(pub, source=src,
+                                       note="criterion medians on unnamed CPU / NVIDIA hardware"),
+    }
+
+
 def cpu_baseline_mamba1_block(shape, budget_tokens=2048, seed=0):
     """oracle.mamba1_block_fwd (f32 C restatement, OpenMP) on one batch row of
     the same shape, at most `budget_tokens` tokens, scaled per token."""
@@ -1412,7 +1506,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", default="ssd2",
                     choices=["ssd2", "mamba1", "decode", "ssd3", "mamba3_fused", "mamba1_step", "mamba3_step",
-                             "mamba3_prep", "mamba2_block", "ssd2_bwd", "ssd3_bwd", "mamba1_block"])
+                             "mamba3_prep", "mamba2_block", "ssd2_bwd", "ssd3_bwd", "mamba1_block", "ref_block"])
+    ap.add_argument("--ref-mode", default="forward", choices=("forward", "step"),
+                    help="ref_block: the reference bench's forward or step group")
+    ap.add_argument("--ref-case", default="mamba2",
+                    choices=("mamba1", "mamba2", "mamba3/siso", "mamba3/mimo-rank4", "mamba3/siso-double-ssd"),
+                    help="ref_block: the reference bench's case")
     ap.add_argument("--mimo", type=int, default=4, choices=(1, 2, 4, 8),
                     help="mamba3_fused: MIMO rank at config 4's head shape (4 is config 4; 1 is SISO)")
     ap.add_argument("--m1-shape", default="ref", choices=sorted(MAMBA1_BLOCK_SHAPES),
@@ -1433,7 +1532,13 @@ def main():
               "(the hot path shards by batch/head with no communication)",
               file=sys.stderr)
         sys.exit(2)
-    if args.workload == "mamba1_block":
+    if args.workload == "ref_block":
+        out = bench_ref_block(args)
+        # the reference's own CPU medians of the row are in the line; the oracle
+        # baseline of the Mamba-1 block is the one restated at this shape
+        base = (lambda: cpu_baseline_mamba1_block("ref")) if args.ref_case == "mamba1" and args.ref_mode == "forward" \
+            else None
+    elif args.workload == "mamba1_block":
         out = bench_mamba1_block(args)
         base = (lambda: cpu_baseline_mamba1_block(args.m1_shape))
     elif args.workload == "ssd3_bwd":
@@ -1472,9 +1577,9 @@ def main():
     if args.calibrate_copy:
         calibrate_copy()
     traffic = _profiled_traffic(out["config"]["workload"])
-    if traffic is not None:
+    if traffic is not None and out.get("roofline"):
         out["roofline"]["traffic"] = traffic
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and base is not None:
         log("cpu baseline")
         out["cpu_baseline"] = base()
     if args.workload == "ssd2" and not args.no_decode:

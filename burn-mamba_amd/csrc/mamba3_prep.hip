@@ -245,7 +245,10 @@ __global__ __launch_bounds__(256) void mamba3_prep_kernel(M3PrepParams p) {
 }
 
 // ---- segment-parallel fast path -------------------------------------------
-// The sequence is cut into segments of kM3Seg positions.  A first kernel sums
+// The sequence is cut into segments of kM3Seg positions (fewer, down to one
+// 32-position tile, where the launch would have under 512 (b, h, segment)
+// workgroups: the angles are integer sums, so the segmentation does not change
+// any result).  A first kernel sums
 // each segment's angle increments dt range pi tanh(rot) per (head, angle) on
 // the fixed-point angle grid; the main kernel then runs one workgroup per (b,
 // h, segment) over every MIMO rank, starting from the cache's angle plus the
@@ -342,12 +345,13 @@ __device__ __forceinline__ void m3_coef_t(const M3PrepParams& p, const TP* proj,
 // per thread) so that b * nseg * H / hpw workgroups share the segments.
 // Dynamic LDS: [tile][hpw] dt and [tile][A] tanh(rot) * span.
 template <typename TP>
-__global__ __launch_bounds__(256) void mamba3_angle_tot_kernel(M3PrepParams p, int nseg, int hpw, int* tot) {
+__global__ __launch_bounds__(256) void mamba3_angle_tot_kernel(M3PrepParams p, int nseg, int seg_len, int hpw,
+                                                               int* tot) {
     const int b = blockIdx.x / nseg, seg = blockIdx.x % nseg, t = threadIdx.x;
     const TP* proj = static_cast<const TP*>(p.proj);
     const int H = p.H, A = p.A, HA = H * A;
     const int h0 = blockIdx.y * hpw, nh = min(hpw, H - h0), np = nh * A;  // this group's pairs
-    const int l_begin = seg * kM3Seg, l_end = min(p.L, l_begin + kM3Seg);
+    const int l_begin = seg * seg_len, l_end = min(p.L, l_begin + seg_len);
     const int o_rot = 2 * H * p.P + 2 * p.M * p.G * p.N + 3 * H;
     extern __shared__ __align__(16) float s_dyn[];
     float* s_dtt = s_dyn;                  // [kM3Tile][hpw]
@@ -401,7 +405,7 @@ __global__ __launch_bounds__(256) void mamba3_angle_tot_kernel(M3PrepParams p, i
 // rank) and its column block for the whole segment; otherwise the rows are
 // decomposed per pass.
 template <typename TP, typename TO, int N>
-__global__ __launch_bounds__(256) void mamba3_prep_seg_kernel(M3PrepParams p, int nseg, const int* tot) {
+__global__ __launch_bounds__(256) void mamba3_prep_seg_kernel(M3PrepParams p, int nseg, int seg_len, const int* tot) {
     constexpr int TPR = N / 8;         // threads per B/C row (8 columns each)
     constexpr int RPP = 256 / TPR;     // rows per pass
     constexpr int W = N / 2;           // pair indices
@@ -412,7 +416,7 @@ __global__ __launch_bounds__(256) void mamba3_prep_seg_kernel(M3PrepParams p, in
     const int d_inner = p.H * P, bc = M * p.G * N;
     const int o_rot = 2 * d_inner + 2 * bc + 3 * p.H;
     const int64_t bh = (int64_t)b * p.H + h;
-    const int l_begin = seg * kM3Seg, l_end = min(p.L, l_begin + kM3Seg);
+    const int l_begin = seg * seg_len, l_end = min(p.L, l_begin + seg_len);
     const TP* projb = proj + (int64_t)b * p.proj_sb;
     extern __shared__ __align__(16) float s_dyn[];
     float* s_th = s_dyn;                   // [kM3Tile][A4]
@@ -793,7 +797,12 @@ static bool m3_prep_fast(const M3PrepParams& p) {
     if ((size_t)kM3Tile * (p.H + p.A) * sizeof(float) > 64 * 1024) return false;
     return true;
 }
-static int m3_nseg(const M3PrepParams& p) { return (p.L + kM3Seg - 1) / kM3Seg; }
+static int m3_seg_len(const M3PrepParams& p) {
+    int seg = kM3Seg;
+    while (seg > kM3Tile && (int64_t)p.nb * p.H * ((p.L + seg - 1) / seg) < 512) seg /= 2;
+    return seg;
+}
+static int m3_nseg(const M3PrepParams& p) { return (p.L + m3_seg_len(p) - 1) / m3_seg_len(p); }
 
 extern "C" int mamba3_prep_fast_path(const mamba3_prep_args* a) {
     M3PrepParams p;
@@ -815,12 +824,13 @@ static void m3_launch_fast(const M3PrepParams& p, int* tot, hipStream_t s) {
     if (nseg > 1) {
         const int hpw = p.A >= 256 ? 1 : (256 / p.A < p.H ? 256 / p.A : p.H);  // heads per workgroup
         hipLaunchKernelGGL((mamba3_angle_tot_kernel<TP>), dim3(p.nb * nseg, (p.H + hpw - 1) / hpw), dim3(256),
-                           (size_t)kM3Tile * (hpw + p.A) * sizeof(float), s, p, nseg, hpw, tot);
+                           (size_t)kM3Tile * (hpw + p.A) * sizeof(float), s, p, nseg, m3_seg_len(p), hpw, tot);
     }
     const dim3 grid(p.nb * p.H * nseg), block(256);
     const size_t lds = (size_t)kM3Tile * (((p.A + 3) & ~3) + p.N) * sizeof(float);
 #define MAMBA3_SEG_N(NN) \
-    hipLaunchKernelGGL((mamba3_prep_seg_kernel<TP, TO, NN>), grid, block, lds, s, p, nseg, (const int*)tot);
+    hipLaunchKernelGGL((mamba3_prep_seg_kernel<TP, TO, NN>), grid, block, lds, s, p, nseg, m3_seg_len(p), \
+                       (const int*)tot);
     switch (p.N) {
         case 8: MAMBA3_SEG_N(8) break;
         case 16: MAMBA3_SEG_N(16) break;

@@ -74,9 +74,14 @@ __device__ void ssd3_chunk_tables(const Ssd3Params& p, int b, int c, int h, floa
 
 // ------------------------------------------------------------ K1 + K3 --
 // S[b,c,h,p,n] = sum_{l, m} v[l,m,p] * B[l,m,n] * scale_l * exp(cs_end - cs_l)
+// One workgroup per (head, chunk x slice of kSsd3StateSlice state entries,
+// batch): a few entries per thread, so that short sequences still launch
+// enough workgroups to hide the LDS and memory latency of each.
+constexpr int kSsd3StateSlice = 1024;
 __global__ __launch_bounds__(256) void ssd3_chunk_state_generic(Ssd3Params p, float* states, float* da_end) {
     extern __shared__ float smem[];
-    const int h = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
+    const int nslice = (p.P * p.N + kSsd3StateSlice - 1) / kSsd3StateSlice;
+    const int h = blockIdx.x, c = blockIdx.y / nslice, slice = blockIdx.y % nslice, b = blockIdx.z;
     const int g = h / (p.H / p.G);
     const int Q = p.Q, P = p.P, N = p.N, M = p.M;
     const bool bf = p.io_dtype == MAMBA_BF16;
@@ -89,11 +94,12 @@ __global__ __launch_bounds__(256) void ssd3_chunk_state_generic(Ssd3Params p, fl
     float* bt = vt + TL * P;  // [TL][N]
     ssd3_chunk_tables(p, b, c, h, cs, scl, gmm, sh4);
     const float cs_end = cs[Q - 1];
-    if (threadIdx.x == 0) da_end[((int64_t)b * p.H + h) * p.nch + c] = cs_end;
+    if (threadIdx.x == 0 && slice == 0) da_end[((int64_t)b * p.H + h) * p.nch + c] = cs_end;
     float* Sout = states + (((int64_t)b * p.nch + c) * p.H + h) * P * N;
     const int QM = Q * M;
-    constexpr int OPT = 32;
-    for (int e0 = 0; e0 < P * N; e0 += 256 * OPT) {
+    constexpr int OPT = kSsd3StateSlice / 256;
+    {
+        const int e0 = slice * kSsd3StateSlice;
         float acc[OPT];
 #pragma unroll
         for (int k = 0; k < OPT; ++k) acc[k] = 0.f;
@@ -154,64 +160,143 @@ __global__ __launch_bounds__(256) void ssd3_state_pass_generic(Ssd3Params p, flo
 }
 
 // ------------------------------------------------------------ K2 + K5 --
-// One workgroup per (head, chunk, batch); R fused output rows per pass with
-// their C.B^T row segments staged in LDS.
-__global__ __launch_bounds__(256) void ssd3_chunk_scan_generic(Ssd3Params p, const float* states) {
+// One workgroup per (head, chunk x row pass, batch), R fused output rows per pass:
+//   y[i][p] = exp(cs_i) C_i.h_in[p] + sum_{j <= i} W[i][j] v[j][p],
+//   W[i][j] = (C_i.B_j) scale_j exp(cs_i - cs_j) for step(j) < step(i),
+//             (C_i.B_j) gamma_i for step(j) == step(i), 0 after.
+// The pass first forms its rows of W in LDS (one exp per (row, source)), then
+// thread (column p, row slot rs) accumulates RR rows of one column, so that
+// each v[j][p] it loads serves all of them.  The chunk's B rows and the entry
+// state are staged in LDS when they fit (flags from the host).
+struct Ssd3ScanLds {
+    int R, RR, TP;       // rows per pass, rows per thread, row slots (256 / P)
+    bool h_lds;          // h_in staged in LDS
+};
+constexpr int kSsd3BT = 32;  // B rows staged per step of the W product
+
+__global__ __launch_bounds__(256) void ssd3_chunk_scan_generic(Ssd3Params p, const float* states, Ssd3ScanLds ly) {
     extern __shared__ float smem[];
-    const int h = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
+    const int npass = (p.Q * p.M + ly.R - 1) / ly.R;
+    const int h = blockIdx.x, c = blockIdx.y / npass, pass = blockIdx.y % npass, b = blockIdx.z;
     const int g = h / (p.H / p.G);
     const int Q = p.Q, P = p.P, N = p.N, M = p.M;
     const bool bf = p.io_dtype == MAMBA_BF16;
+    const int QM = Q * M, R = ly.R, RR = ly.RR, TP = ly.TP;
     float* cs = smem;
     float* scl = cs + Q;
     float* gmm = scl + Q;
     float* sh4 = gmm + Q;
-    float* cb = sh4 + 4;  // [R][Q*M]
+    float* W = sh4 + 4;              // [R][QM]
+    float* Cs = W + R * QM;          // [R][N]
+    const int NB = N + 1;            // Bt row pitch: consecutive sources on different banks
+    float* Bt = Cs + R * N;          // [kSsd3BT][NB]: B rows of one step of the W product
+    float* Hs = Bt + kSsd3BT * NB;   // [N][P] (h_lds)
     ssd3_chunk_tables(p, b, c, h, cs, scl, gmm, sh4);
     const float* hin = states + (((int64_t)b * p.nch + c) * p.H + h) * P * N;
-    const int QM = Q * M;
-    const int R = P >= 256 ? 1 : 256 / P;
     const int qvalid = min(Q, p.L - c * Q);
     const int fvalid = qvalid * M;
     auto cptr = [&](int t, int m) { return (int64_t)b * p.C_sb + (int64_t)t * p.C_sl + (int64_t)m * p.C_sm + (int64_t)g * p.C_sg; };
     auto bptr = [&](int t, int m) { return (int64_t)b * p.B_sb + (int64_t)t * p.B_sl + (int64_t)m * p.B_sm + (int64_t)g * p.B_sg; };
-    for (int f0 = 0; f0 < fvalid; f0 += R) {
+    if (ly.h_lds)
+        for (int k = threadIdx.x; k < P * N; k += 256) {
+            const int pp = k / N, n = k % N;
+            Hs[n * P + pp] = hin[k];
+        }
+    const int pp = threadIdx.x % P, rs = threadIdx.x / P;
+    const bool active = rs < TP;
+    {
+        const int f0 = pass * R;
+        if (f0 >= fvalid) return;  // a pass past the chunk's end (the last chunk): nothing to write
         __syncthreads();
-        // C.B^T for rows f0..f0+R against every source up to the row's step
-        for (int k = threadIdx.x; k < R * QM; k += 256) {
-            const int fi = f0 + k / QM, fj = k % QM;
-            const int li = fi / M, lj = fj / M;
-            float v = 0.f;
-            if (fi < fvalid && lj <= li) {
-                const int64_t ci = cptr(c * Q + li, fi % M), bj = bptr(c * Q + lj, fj % M);
-                for (int n = 0; n < N; ++n) v += ld_io(p.Cm, ci + n, bf) * ld_io(p.Bm, bj + n, bf);
-            }
-            cb[k] = v;
+        // the pass's C rows
+        for (int k = threadIdx.x; k < R * N; k += 256) {
+            const int fi = f0 + k / N;
+            Cs[k] = fi < fvalid ? ld_io(p.Cm, cptr(c * Q + fi / M, fi % M) + k % N, bf) : 0.f;
         }
         __syncthreads();
-        for (int k = threadIdx.x; k < R * P; k += 256) {
-            const int fi = f0 + k / P, pp = k % P;
+        // its rows of W, weights folded in (sources up to the last row's
+        // step), kSsd3BT sources at a time: their B rows staged with coalesced
+        // loads, then one (row, source) dot per thread
+        const int li_last = (min(f0 + R, fvalid) - 1) / M;
+        const int nsrc = (li_last + 1) * M;
+        for (int s0 = 0; s0 < nsrc; s0 += kSsd3BT) {
+            for (int k = threadIdx.x; k < kSsd3BT * N; k += 256) {
+                const int j = k / N, n = k % N, fj = s0 + j;
+                Bt[j * NB + n] = fj < nsrc ? ld_io(p.Bm, bptr(c * Q + fj / M, fj % M) + n, bf) : 0.f;
+            }
+            __syncthreads();
+            for (int k = threadIdx.x; k < R * kSsd3BT; k += 256) {
+                const int r = k / kSsd3BT, j = k % kSsd3BT, fj = s0 + j, fi = f0 + r;
+                if (fj >= nsrc) continue;
+                const int li = fi / M, lj = fj / M;
+                float v = 0.f;
+                if (fi < fvalid && lj <= li) {
+                    const float* cr = Cs + r * N;
+                    const float* br = Bt + j * NB;
+                    // four independent partial sums: four LDS loads in flight
+                    float d0 = 0.f, d1 = 0.f, d2 = 0.f, d3 = 0.f;
+                    int n = 0;
+                    for (; n + 4 <= N; n += 4) {
+                        d0 = __builtin_fmaf(cr[n], br[n], d0);
+                        d1 = __builtin_fmaf(cr[n + 1], br[n + 1], d1);
+                        d2 = __builtin_fmaf(cr[n + 2], br[n + 2], d2);
+                        d3 = __builtin_fmaf(cr[n + 3], br[n + 3], d3);
+                    }
+                    for (; n < N; ++n) d0 = __builtin_fmaf(cr[n], br[n], d0);
+                    const float dot = (d0 + d1) + (d2 + d3);
+                    v = dot * (lj < li ? __expf(cs[li] - cs[lj]) * scl[lj] : gmm[li]);
+                }
+                W[r * QM + fj] = v;
+            }
+            __syncthreads();
+        }
+        if (!active) return;
+        // RR rows of column pp per thread: rows f0 + rs + TP k
+        float acc[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) acc[k] = 0.f;
+        // sources in groups of 16: their v loads are issued together
+        constexpr int U = 16;
+        for (int fj0 = 0; fj0 < nsrc; fj0 += U) {
+            float vv[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int fj = min(fj0 + u, nsrc - 1);  // clamped: its W entries below are skipped
+                vv[u] = ld_io(p.v, (int64_t)b * p.v_sb + (int64_t)(c * Q + fj / M) * p.v_sl +
+                                       (int64_t)(fj % M) * p.v_sm + (int64_t)h * p.v_sh + pp, bf);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if (fj0 + u >= nsrc) break;
+#pragma unroll
+                for (int k = 0; k < 16; ++k)
+                    if (k < RR) acc[k] = __builtin_fmaf(W[(rs + TP * k) * QM + fj0 + u], vv[u], acc[k]);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            if (k >= RR) break;
+            const int r = rs + TP * k, fi = f0 + r;
             if (fi >= fvalid) continue;
             const int li = fi / M, mo = fi % M, ti = c * Q + li;
-            const int64_t ci = cptr(ti, mo);
-            float blue = 0.f;
-            for (int n = 0; n < N; ++n) blue += ld_io(p.Cm, ci + n, bf) * hin[pp * N + n];
-            blue *= __expf(cs[li]);
-            const float* cbr = cb + (k / P) * QM;
-            float lower = 0.f;
-            for (int fj = 0; fj < li * M; ++fj) {
-                const int lj = fj / M, tj = c * Q + lj;
-                const float vv = ld_io(p.v, (int64_t)b * p.v_sb + (int64_t)tj * p.v_sl + (int64_t)(fj % M) * p.v_sm +
-                                                (int64_t)h * p.v_sh + pp, bf);
-                lower += (cbr[fj] * (__expf(cs[li] - cs[lj]) * scl[lj])) * vv;
+            const float* cr = Cs + r * N;
+            float b0 = 0.f, b1 = 0.f;
+            int n = 0;
+            if (ly.h_lds) {
+                for (; n + 2 <= N; n += 2) {
+                    b0 = __builtin_fmaf(cr[n], Hs[n * P + pp], b0);
+                    b1 = __builtin_fmaf(cr[n + 1], Hs[(n + 1) * P + pp], b1);
+                }
+                for (; n < N; ++n) b0 = __builtin_fmaf(cr[n], Hs[n * P + pp], b0);
+            } else {
+                for (; n + 2 <= N; n += 2) {
+                    b0 = __builtin_fmaf(cr[n], hin[pp * N + n], b0);
+                    b1 = __builtin_fmaf(cr[n + 1], hin[pp * N + n + 1], b1);
+                }
+                for (; n < N; ++n) b0 = __builtin_fmaf(cr[n], hin[pp * N + n], b0);
             }
-            float diag = 0.f;
-            for (int mi = 0; mi < M; ++mi) {
-                const float vv = ld_io(p.v, (int64_t)b * p.v_sb + (int64_t)ti * p.v_sl + (int64_t)mi * p.v_sm +
-                                                (int64_t)h * p.v_sh + pp, bf);
-                diag += cbr[li * M + mi] * vv;
-            }
-            const float out = (blue + lower) + diag * gmm[li];
+            const float blue = b0 + b1;
+            const float out = __builtin_fmaf(blue, __expf(cs[li]), acc[k]);
             const int64_t yi = (int64_t)b * p.y_sb + (int64_t)ti * p.y_sl + (int64_t)mo * p.y_sm + (int64_t)h * p.y_sh + pp;
             if (bf)
                 static_cast<bf16_t*>(p.y)[yi] = f32_to_bf16(out);
@@ -219,6 +304,24 @@ __global__ __launch_bounds__(256) void ssd3_chunk_scan_generic(Ssd3Params p, con
                 static_cast<float*>(p.y)[yi] = out;
         }
     }
+}
+
+// The pass geometry and LDS staging of the chunk scan for these shapes, and
+// its dynamic LDS bytes (0 when even the unstaged form does not fit).
+static size_t ssd3_scan_layout(const Ssd3Params& p, Ssd3ScanLds* ly, size_t limit_bytes) {
+    const int TP = p.P >= 256 ? 1 : 256 / p.P;
+    const size_t QM = (size_t)p.Q * p.M;
+    const size_t limit = limit_bytes / 4;  // words
+    const size_t fixed = 3 * (size_t)p.Q + 4 + (size_t)kSsd3BT * (p.N + 1);
+    // rows per thread: up to 16 rows per pass, fewer where the W rows would not fit
+    int RR = TP >= 16 ? 1 : 16 / TP;
+    while (RR > 1 && fixed + (size_t)TP * RR * (QM + p.N) > limit) RR /= 2;
+    ly->TP = TP; ly->RR = RR; ly->R = TP * RR;
+    size_t words = fixed + (size_t)ly->R * (QM + p.N);
+    if (words > limit) return 0;
+    ly->h_lds = words + (size_t)p.P * p.N <= limit;
+    if (ly->h_lds) words += (size_t)p.P * p.N;
+    return words * 4;
 }
 
 // ------------------------------------------------------------ host side --
@@ -269,21 +372,26 @@ static int ssd3_dispatch(const mamba_ssd3_args* a, void* ws, size_t ws_bytes, hi
         set_error("mamba_ssd3_fwd: workspace of " + std::to_string(need) + " bytes required");
         return MAMBA_ERR_WORKSPACE;
     }
-    const int R = p.P >= 256 ? 1 : 256 / p.P;
+    Ssd3ScanLds ly;
     const size_t sm_state = (3 * (size_t)p.Q + 4 + 16 * (size_t)p.P + 16 * (size_t)p.N) * 4;
-    const size_t sm_scan = (3 * (size_t)p.Q + 4 + (size_t)R * p.Q * p.M) * 4;
-    MAMBA_CHECK_ARG(sm_scan <= 160 * 1024 && sm_state <= 160 * 1024, "chunk_len * mimo too large for the generic path");
+    const size_t sm_scan = ssd3_scan_layout(p, &ly, 64 * 1024);
+    MAMBA_CHECK_ARG(sm_scan > 0 && sm_state <= 160 * 1024, "chunk_len * mimo too large for the generic path");
     float* states = static_cast<float*>(ws);
     float* daend = reinterpret_cast<float*>(static_cast<char*>(ws) +
                                             align_up((size_t)p.nb * p.nch * p.H * p.P * p.N * 4, 256));
-    const dim3 grid(p.H, p.nch, p.nb);
-    hipLaunchKernelGGL(ssd3_chunk_state_generic, grid, dim3(256), sm_state, stream, p, states, daend);
+    const int npass = (p.Q * p.M + ly.R - 1) / ly.R;
+    const int nslice = (p.P * p.N + kSsd3StateSlice - 1) / kSsd3StateSlice;
+    MAMBA_CHECK_ARG((int64_t)p.nch * npass < 65536 && (int64_t)p.nch * nslice < 65536,
+                    "too many chunks x row passes for the generic path");
+    hipLaunchKernelGGL(ssd3_chunk_state_generic, dim3(p.H, p.nch * nslice, p.nb), dim3(256), sm_state, stream, p,
+                       states, daend);
     MAMBA_CHECK_LAUNCH();
     hipLaunchKernelGGL(ssd3_state_pass_generic, dim3(ceil_div(p.P * p.N, 256), p.H, p.nb), dim3(256), 0, stream, p,
                        states, daend);
     MAMBA_CHECK_LAUNCH();
     if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, stream));
-    hipLaunchKernelGGL(ssd3_chunk_scan_generic, grid, dim3(256), sm_scan, stream, p, states);
+    hipLaunchKernelGGL(ssd3_chunk_scan_generic, dim3(p.H, p.nch * npass, p.nb), dim3(256), sm_scan, stream, p,
+                       states, ly);
     MAMBA_CHECK_LAUNCH();
     if (ev1) MAMBA_CHECK_HIP(hipEventRecord(ev1, stream));
     return MAMBA_OK;
