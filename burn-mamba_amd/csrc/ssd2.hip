@@ -136,17 +136,33 @@ __global__ __launch_bounds__(256) void ssd2_state_pass_generic(Ssd2Params p, flo
 }
 
 // ------------------------------------------------------- K2 + K5 (generic) --
-// y[i,p] = exp(cs_i) C_i.h_in[p,:] + sum_{j<=i} (C_i.B_j) exp(cs_i-cs_j) dt_j x[j,p] + D x[i,p]
+// One workgroup per (head, chunk x pass of R rows, batch):
+//   y[i][p] = exp(cs_i) C_i.h_in[p] + sum_{j <= i} W[i][j] x[j][p] + D x[i][p],
+//   W[i][j] = (C_i.B_j) exp(cs_i - cs_j) dt_j  (serial.rs:170-230, K2 + K5).
+// The pass forms its rows of W in LDS once per (row, source), its B rows
+// staged 32 at a time (padded rows: consecutive sources on different banks);
+// then thread (column p, row slot rs) accumulates RR rows of one column, each
+// x load serving all of them.
+struct Ssd2ScanLds {
+    int R, RR, TP;  // rows per pass, rows per thread, row slots (256 / P)
+    bool h_lds;     // h_in staged in LDS
+};
+constexpr int kSsd2BT = 32;
+
 template <typename T>
-__global__ __launch_bounds__(256) void ssd2_chunk_scan_generic(Ssd2Params p, const float* states) {
+__global__ __launch_bounds__(256) void ssd2_chunk_scan_generic(Ssd2Params p, const float* states, Ssd2ScanLds ly) {
     extern __shared__ float smem[];
-    const int h = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
+    const int npass = (p.Q + ly.R - 1) / ly.R;
+    const int h = blockIdx.x, c = blockIdx.y / npass, pass = blockIdx.y % npass, b = blockIdx.z;
     const int g = h / (p.H / p.G);
-    const int Q = p.Q, P = p.P, N = p.N;
-    float* cs = smem;       // [Q]
-    float* dts = cs + Q;    // [Q]
-    float* sh4 = dts + Q;   // [4]
-    float* cb = sh4 + 4;    // [R][Q]
+    const int Q = p.Q, P = p.P, N = p.N, R = ly.R, RR = ly.RR, TP = ly.TP, NB = N + 1;
+    float* cs = smem;            // [Q]
+    float* dts = cs + Q;         // [Q]
+    float* sh4 = dts + Q;        // [4]
+    float* W = sh4 + 4;          // [R][Q]
+    float* Cs = W + R * Q;       // [R][N]
+    float* Bt = Cs + R * N;      // [kSsd2BT][NB]
+    float* Hs = Bt + kSsd2BT * NB;  // [N][P] (h_lds)
     chunk_cumsum(p, b, c, h, cs, dts, sh4);
     const T* X = (const T*)p.x;
     const T* Bm = (const T*)p.Bm;
@@ -154,43 +170,110 @@ __global__ __launch_bounds__(256) void ssd2_chunk_scan_generic(Ssd2Params p, con
     T* Y = (T*)p.y;
     const float* hin = states + (((int64_t)b * p.nch + c) * p.H + h) * P * N;
     const float Dh = p.D ? p.D[h] : 0.f;
-    const int R = P >= 256 ? 1 : 256 / P;  // rows per pass
     const int qvalid = min(Q, p.L - c * Q);
-    for (int i0 = 0; i0 < qvalid; i0 += R) {
+    const int i0 = pass * R;
+    if (i0 >= qvalid) return;  // a pass past the last chunk's end (workgroup-uniform)
+    if (ly.h_lds)
+        for (int k = threadIdx.x; k < P * N; k += 256) Hs[(k % N) * P + k / N] = hin[k];
+    for (int k = threadIdx.x; k < R * N; k += 256) {
+        const int ii = i0 + k / N;
+        Cs[k] = ii < qvalid ? load_f32(Cm + (int64_t)b * p.C_sb + (int64_t)(c * Q + ii) * p.C_sl + (int64_t)g * p.C_sg + k % N)
+                            : 0.f;
+    }
+    __syncthreads();
+    const int nsrc = min(i0 + R, qvalid);  // sources up to the pass's last row
+    for (int s0 = 0; s0 < nsrc; s0 += kSsd2BT) {
+        for (int k = threadIdx.x; k < kSsd2BT * N; k += 256) {
+            const int jj = k / N, j = s0 + jj;
+            Bt[jj * NB + k % N] =
+                j < nsrc ? load_f32(Bm + (int64_t)b * p.B_sb + (int64_t)(c * Q + j) * p.B_sl + (int64_t)g * p.B_sg + k % N)
+                         : 0.f;
+        }
         __syncthreads();
-        // CB rows i0..i0+R (K2, serial.rs:170-185), lower triangle only
-        for (int k = threadIdx.x; k < R * Q; k += 256) {
-            const int ii = i0 + k / Q, j = k % Q;
+        for (int k = threadIdx.x; k < R * kSsd2BT; k += 256) {
+            const int r = k / kSsd2BT, jj = k % kSsd2BT, j = s0 + jj, ii = i0 + r;
+            if (j >= nsrc) continue;
             float v = 0.f;
             if (ii < qvalid && j <= ii) {
-                const int ti = c * Q + ii, tj = c * Q + j;
-                const T* crow = Cm + (int64_t)b * p.C_sb + (int64_t)ti * p.C_sl + (int64_t)g * p.C_sg;
-                const T* brow = Bm + (int64_t)b * p.B_sb + (int64_t)tj * p.B_sl + (int64_t)g * p.B_sg;
-                for (int n = 0; n < N; ++n) v += load_f32(crow + n) * load_f32(brow + n);
+                const float* cr = Cs + r * N;
+                const float* br = Bt + jj * NB;
+                float d0 = 0.f, d1 = 0.f, d2 = 0.f, d3 = 0.f;
+                int n = 0;
+                for (; n + 4 <= N; n += 4) {
+                    d0 = __builtin_fmaf(cr[n], br[n], d0);
+                    d1 = __builtin_fmaf(cr[n + 1], br[n + 1], d1);
+                    d2 = __builtin_fmaf(cr[n + 2], br[n + 2], d2);
+                    d3 = __builtin_fmaf(cr[n + 3], br[n + 3], d3);
+                }
+                for (; n < N; ++n) d0 = __builtin_fmaf(cr[n], br[n], d0);
+                v = ((d0 + d1) + (d2 + d3)) * expf(cs[ii] - cs[j]) * dts[j];
             }
-            cb[k] = v;
+            W[r * Q + j] = v;
         }
         __syncthreads();
-        for (int k = threadIdx.x; k < R * P; k += 256) {
-            const int ii = i0 + k / P, pp = k % P;
-            if (ii >= qvalid) continue;
-            const int ti = c * Q + ii;
-            const T* crow = Cm + (int64_t)b * p.C_sb + (int64_t)ti * p.C_sl + (int64_t)g * p.C_sg;
-            float blue = 0.f;
-            for (int n = 0; n < N; ++n) blue += load_f32(crow + n) * hin[pp * N + n];
-            blue *= expf(cs[ii]);
-            float orange = 0.f;
-            const float* cbr = cb + (k / P) * Q;
-            for (int j = 0; j <= ii; ++j) {
-                const int tj = c * Q + j;
-                const float xv = load_f32(X + (int64_t)b * p.x_sb + (int64_t)tj * p.x_sl + (int64_t)h * p.x_sh + pp);
-                orange += ((cbr[j] * expf(cs[ii] - cs[j])) * dts[j]) * xv;
-            }
-            const float xi = load_f32(X + (int64_t)b * p.x_sb + (int64_t)ti * p.x_sl + (int64_t)h * p.x_sh + pp);
-            store_f32(Y + (int64_t)b * p.y_sb + (int64_t)ti * p.y_sl + (int64_t)h * p.y_sh + pp,
-                      (blue + orange) + Dh * xi);
+    }
+    const int pp = threadIdx.x % P, rs = threadIdx.x / P;
+    if (rs >= TP) return;
+    float acc[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) acc[k] = 0.f;
+    constexpr int U = 16;  // sources whose x loads are issued together
+    for (int j0 = 0; j0 < nsrc; j0 += U) {
+        float xv[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int j = min(j0 + u, nsrc - 1);  // clamped: its W entries below are skipped
+            xv[u] = load_f32(X + (int64_t)b * p.x_sb + (int64_t)(c * Q + j) * p.x_sl + (int64_t)h * p.x_sh + pp);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (j0 + u >= nsrc) break;
+#pragma unroll
+            for (int k = 0; k < 16; ++k)
+                if (k < RR) acc[k] = __builtin_fmaf(W[(rs + TP * k) * Q + j0 + u], xv[u], acc[k]);
         }
     }
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        if (k >= RR) break;
+        const int r = rs + TP * k, ii = i0 + r;
+        if (ii >= qvalid) continue;
+        const int ti = c * Q + ii;
+        const float* cr = Cs + r * N;
+        float b0 = 0.f, b1 = 0.f;
+        int n = 0;
+        if (ly.h_lds) {
+            for (; n + 2 <= N; n += 2) {
+                b0 = __builtin_fmaf(cr[n], Hs[n * P + pp], b0);
+                b1 = __builtin_fmaf(cr[n + 1], Hs[(n + 1) * P + pp], b1);
+            }
+            for (; n < N; ++n) b0 = __builtin_fmaf(cr[n], Hs[n * P + pp], b0);
+        } else {
+            for (; n + 2 <= N; n += 2) {
+                b0 = __builtin_fmaf(cr[n], hin[pp * N + n], b0);
+                b1 = __builtin_fmaf(cr[n + 1], hin[pp * N + n + 1], b1);
+            }
+            for (; n < N; ++n) b0 = __builtin_fmaf(cr[n], hin[pp * N + n], b0);
+        }
+        const float xi = load_f32(X + (int64_t)b * p.x_sb + (int64_t)ti * p.x_sl + (int64_t)h * p.x_sh + pp);
+        store_f32(Y + (int64_t)b * p.y_sb + (int64_t)ti * p.y_sl + (int64_t)h * p.y_sh + pp,
+                  __builtin_fmaf((b0 + b1), expf(cs[ii]), acc[k]) + Dh * xi);
+    }
+}
+
+// The chunk scan's pass geometry and its dynamic LDS bytes (0: does not fit).
+static size_t ssd2_scan_layout(const Ssd2Params& p, Ssd2ScanLds* ly) {
+    const int TP = p.P >= 256 ? 1 : 256 / p.P;
+    const size_t limit = 64 * 1024 / 4;  // words
+    const size_t fixed = 2 * (size_t)p.Q + 4 + (size_t)kSsd2BT * (p.N + 1);
+    int RR = TP >= 16 ? 1 : 16 / TP;
+    while (RR > 1 && fixed + (size_t)TP * RR * ((size_t)p.Q + p.N) > limit) RR /= 2;
+    ly->TP = TP; ly->RR = RR; ly->R = TP * RR;
+    size_t words = fixed + (size_t)ly->R * ((size_t)p.Q + p.N);
+    if (words > limit) return 0;
+    ly->h_lds = words + (size_t)p.P * p.N <= limit;
+    if (ly->h_lds) words += (size_t)p.P * p.N;
+    return words * 4;
 }
 
 // ------------------------------------------------------------ host side --
@@ -206,8 +289,11 @@ int ssd2_generic_launch(const Ssd2Params& p, void* ws, hipStream_t stream, hipEv
     float* daend = (float*)((char*)ws + align_up((size_t)p.nb * p.nch * p.H * p.P * p.N * sizeof(float), 256));
     dim3 grid(p.H, p.nch, p.nb);
     const size_t sm_state = (2 * (size_t)p.Q + 4 + 16 * (size_t)p.P + 16 * (size_t)p.N) * sizeof(float);
-    const int R = p.P >= 256 ? 1 : 256 / p.P;
-    const size_t sm_scan = (2 * (size_t)p.Q + 4 + (size_t)R * p.Q) * sizeof(float);
+    Ssd2ScanLds ly;
+    const size_t sm_scan = ssd2_scan_layout(p, &ly);
+    const int npass = (p.Q + ly.R - 1) / ly.R;
+    MAMBA_CHECK_ARG(sm_scan > 0 && (int64_t)p.nch * npass < 65536, "chunk too large for the generic path");
+    const dim3 gscan(p.H, p.nch * npass, p.nb);
     if (p.io_dtype == MAMBA_BF16) {
         hipLaunchKernelGGL(ssd2_chunk_state_generic<bf16_t>, grid, dim3(256), sm_state, stream, p, states, daend);
     } else {
@@ -219,9 +305,9 @@ int ssd2_generic_launch(const Ssd2Params& p, void* ws, hipStream_t stream, hipEv
     MAMBA_CHECK_LAUNCH();
     if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, stream));
     if (p.io_dtype == MAMBA_BF16) {
-        hipLaunchKernelGGL(ssd2_chunk_scan_generic<bf16_t>, grid, dim3(256), sm_scan, stream, p, states);
+        hipLaunchKernelGGL(ssd2_chunk_scan_generic<bf16_t>, gscan, dim3(256), sm_scan, stream, p, states, ly);
     } else {
-        hipLaunchKernelGGL(ssd2_chunk_scan_generic<float>, grid, dim3(256), sm_scan, stream, p, states);
+        hipLaunchKernelGGL(ssd2_chunk_scan_generic<float>, gscan, dim3(256), sm_scan, stream, p, states, ly);
     }
     MAMBA_CHECK_LAUNCH();
     if (ev1) MAMBA_CHECK_HIP(hipEventRecord(ev1, stream));
