@@ -54,11 +54,15 @@ __device__ void chunk_cumsum(const Ssd2Params& p, int b, int c, int h, float* cs
 
 // ------------------------------------------------------- K1 + K3 (generic) --
 // S[b,c,h,p,n] = sum_l x[l,p] * (B[l,n] * (exp(cs_end - cs_l) * dt_l))
+// One workgroup per (head, chunk x slice of kSsd2StateSlice entries, batch):
+// a few entries per thread, so that short sequences launch enough workgroups.
+constexpr int kSsd2StateSlice = 1024;
 template <typename T>
 __global__ __launch_bounds__(256) void ssd2_chunk_state_generic(Ssd2Params p, float* states,
                                                                 float* da_end) {
     extern __shared__ float smem[];
-    const int h = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
+    const int nslice = (p.P * p.N + kSsd2StateSlice - 1) / kSsd2StateSlice;
+    const int h = blockIdx.x, c = blockIdx.y / nslice, slice = blockIdx.y % nslice, b = blockIdx.z;
     const int g = h / (p.H / p.G);
     const int Q = p.Q, P = p.P, N = p.N;
     float* cs = smem;            // [Q]
@@ -69,12 +73,13 @@ __global__ __launch_bounds__(256) void ssd2_chunk_state_generic(Ssd2Params p, fl
     float* bt = xt + TL * P;     // [TL][N]
     chunk_cumsum(p, b, c, h, cs, dts, sh4);
     const float cs_end = cs[Q - 1];
-    if (threadIdx.x == 0) da_end[((int64_t)b * p.H + h) * p.nch + c] = cs_end;
+    if (threadIdx.x == 0 && slice == 0) da_end[((int64_t)b * p.H + h) * p.nch + c] = cs_end;
     const T* X = (const T*)p.x;
     const T* Bm = (const T*)p.Bm;
     float* Sout = states + (((int64_t)b * p.nch + c) * p.H + h) * P * N;
-    constexpr int OPT = 32;  // outputs per thread per pass
-    for (int e0 = 0; e0 < P * N; e0 += 256 * OPT) {
+    constexpr int OPT = kSsd2StateSlice / 256;  // outputs per thread
+    {
+        const int e0 = slice * kSsd2StateSlice;
         float acc[OPT];
 #pragma unroll
         for (int k = 0; k < OPT; ++k) acc[k] = 0.f;
@@ -294,10 +299,13 @@ int ssd2_generic_launch(const Ssd2Params& p, void* ws, hipStream_t stream, hipEv
     const int npass = (p.Q + ly.R - 1) / ly.R;
     MAMBA_CHECK_ARG(sm_scan > 0 && (int64_t)p.nch * npass < 65536, "chunk too large for the generic path");
     const dim3 gscan(p.H, p.nch * npass, p.nb);
+    const int nslice = (p.P * p.N + kSsd2StateSlice - 1) / kSsd2StateSlice;
+    MAMBA_CHECK_ARG((int64_t)p.nch * nslice < 65536, "too many chunks for the generic path");
+    const dim3 gstate(p.H, p.nch * nslice, p.nb);
     if (p.io_dtype == MAMBA_BF16) {
-        hipLaunchKernelGGL(ssd2_chunk_state_generic<bf16_t>, grid, dim3(256), sm_state, stream, p, states, daend);
+        hipLaunchKernelGGL(ssd2_chunk_state_generic<bf16_t>, gstate, dim3(256), sm_state, stream, p, states, daend);
     } else {
-        hipLaunchKernelGGL(ssd2_chunk_state_generic<float>, grid, dim3(256), sm_state, stream, p, states, daend);
+        hipLaunchKernelGGL(ssd2_chunk_state_generic<float>, gstate, dim3(256), sm_state, stream, p, states, daend);
     }
     MAMBA_CHECK_LAUNCH();
     dim3 gpass(ceil_div(p.P * p.N, 256), p.H, p.nb);
