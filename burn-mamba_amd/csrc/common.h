@@ -74,6 +74,10 @@ __device__ __forceinline__ float silu_f32(float x) { return x / (expf(-x) + 1.f)
 // div_eps(F32) of src/utils/mod.rs:59-65
 constexpr float kDivEpsF32 = 8.1584695e-8f;
 
+// The generic SSD chunk-state kernels take wide slices (32 entries per thread)
+// when (head, chunk, batch) alone gives at least this many workgroups.
+constexpr int64_t kGenericStateWide = 2048;
+
 // ---------------------------------------------------- wave/block scans ---
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

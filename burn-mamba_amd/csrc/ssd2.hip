@@ -54,14 +54,15 @@ __device__ void chunk_cumsum(const Ssd2Params& p, int b, int c, int h, float* cs
 
 // ------------------------------------------------------- K1 + K3 (generic) --
 // S[b,c,h,p,n] = sum_l x[l,p] * (B[l,n] * (exp(cs_end - cs_l) * dt_l))
-// One workgroup per (head, chunk x slice of kSsd2StateSlice entries, batch):
-// a few entries per thread, so that short sequences launch enough workgroups.
-constexpr int kSsd2StateSlice = 1024;
-template <typename T>
+// One workgroup per (head, chunk x slice of 256 OPT entries, batch), OPT
+// entries per thread: the launch takes OPT = 4 when (head, chunk, batch) alone
+// would give few workgroups (short sequences), else 32 (each slice stages the
+// chunk's x and weighted B rows once, so fewer slices stage less).
+template <typename T, int OPT>
 __global__ __launch_bounds__(256) void ssd2_chunk_state_generic(Ssd2Params p, float* states,
                                                                 float* da_end) {
     extern __shared__ float smem[];
-    const int nslice = (p.P * p.N + kSsd2StateSlice - 1) / kSsd2StateSlice;
+    const int nslice = (p.P * p.N + 256 * OPT - 1) / (256 * OPT);
     const int h = blockIdx.x, c = blockIdx.y / nslice, slice = blockIdx.y % nslice, b = blockIdx.z;
     const int g = h / (p.H / p.G);
     const int Q = p.Q, P = p.P, N = p.N;
@@ -77,9 +78,8 @@ __global__ __launch_bounds__(256) void ssd2_chunk_state_generic(Ssd2Params p, fl
     const T* X = (const T*)p.x;
     const T* Bm = (const T*)p.Bm;
     float* Sout = states + (((int64_t)b * p.nch + c) * p.H + h) * P * N;
-    constexpr int OPT = kSsd2StateSlice / 256;  // outputs per thread
     {
-        const int e0 = slice * kSsd2StateSlice;
+        const int e0 = slice * 256 * OPT;
         float acc[OPT];
 #pragma unroll
         for (int k = 0; k < OPT; ++k) acc[k] = 0.f;
@@ -299,14 +299,14 @@ int ssd2_generic_launch(const Ssd2Params& p, void* ws, hipStream_t stream, hipEv
     const int npass = (p.Q + ly.R - 1) / ly.R;
     MAMBA_CHECK_ARG(sm_scan > 0 && (int64_t)p.nch * npass < 65536, "chunk too large for the generic path");
     const dim3 gscan(p.H, p.nch * npass, p.nb);
-    const int nslice = (p.P * p.N + kSsd2StateSlice - 1) / kSsd2StateSlice;
+    const bool wide = (int64_t)p.H * p.nch * p.nb >= kGenericStateWide;
+    const int opt = wide ? 32 : 4, nslice = (p.P * p.N + 256 * opt - 1) / (256 * opt);
     MAMBA_CHECK_ARG((int64_t)p.nch * nslice < 65536, "too many chunks for the generic path");
     const dim3 gstate(p.H, p.nch * nslice, p.nb);
-    if (p.io_dtype == MAMBA_BF16) {
-        hipLaunchKernelGGL(ssd2_chunk_state_generic<bf16_t>, gstate, dim3(256), sm_state, stream, p, states, daend);
-    } else {
-        hipLaunchKernelGGL(ssd2_chunk_state_generic<float>, gstate, dim3(256), sm_state, stream, p, states, daend);
-    }
+    const bool bf = p.io_dtype == MAMBA_BF16;
+    auto state_kernel = wide ? (bf ? ssd2_chunk_state_generic<bf16_t, 32> : ssd2_chunk_state_generic<float, 32>)
+                             : (bf ? ssd2_chunk_state_generic<bf16_t, 4> : ssd2_chunk_state_generic<float, 4>);
+    hipLaunchKernelGGL(state_kernel, gstate, dim3(256), sm_state, stream, p, states, daend);
     MAMBA_CHECK_LAUNCH();
     dim3 gpass(ceil_div(p.P * p.N, 256), p.H, p.nb);
     hipLaunchKernelGGL(ssd2_state_pass_generic, gpass, dim3(256), 0, stream, p, states, daend);

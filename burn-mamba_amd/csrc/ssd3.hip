@@ -74,13 +74,15 @@ __device__ void ssd3_chunk_tables(const Ssd3Params& p, int b, int c, int h, floa
 
 // ------------------------------------------------------------ K1 + K3 --
 // S[b,c,h,p,n] = sum_{l, m} v[l,m,p] * B[l,m,n] * scale_l * exp(cs_end - cs_l)
-// One workgroup per (head, chunk x slice of kSsd3StateSlice state entries,
-// batch): a few entries per thread, so that short sequences still launch
-// enough workgroups to hide the LDS and memory latency of each.
-constexpr int kSsd3StateSlice = 1024;
+// One workgroup per (head, chunk x slice of 256 OPT state entries, batch),
+// OPT entries per thread: the launch takes OPT = 4 when (head, chunk, batch)
+// alone would give few workgroups (short sequences: more workgroups hide the
+// LDS and memory latency of each), else 32 (each slice stages the chunk's v
+// and weighted B rows once, so fewer slices stage less).
+template <int OPT>
 __global__ __launch_bounds__(256) void ssd3_chunk_state_generic(Ssd3Params p, float* states, float* da_end) {
     extern __shared__ float smem[];
-    const int nslice = (p.P * p.N + kSsd3StateSlice - 1) / kSsd3StateSlice;
+    const int nslice = (p.P * p.N + 256 * OPT - 1) / (256 * OPT);
     const int h = blockIdx.x, c = blockIdx.y / nslice, slice = blockIdx.y % nslice, b = blockIdx.z;
     const int g = h / (p.H / p.G);
     const int Q = p.Q, P = p.P, N = p.N, M = p.M;
@@ -97,9 +99,8 @@ __global__ __launch_bounds__(256) void ssd3_chunk_state_generic(Ssd3Params p, fl
     if (threadIdx.x == 0 && slice == 0) da_end[((int64_t)b * p.H + h) * p.nch + c] = cs_end;
     float* Sout = states + (((int64_t)b * p.nch + c) * p.H + h) * P * N;
     const int QM = Q * M;
-    constexpr int OPT = kSsd3StateSlice / 256;
     {
-        const int e0 = slice * kSsd3StateSlice;
+        const int e0 = slice * 256 * OPT;
         float acc[OPT];
 #pragma unroll
         for (int k = 0; k < OPT; ++k) acc[k] = 0.f;
@@ -380,11 +381,12 @@ static int ssd3_dispatch(const mamba_ssd3_args* a, void* ws, size_t ws_bytes, hi
     float* daend = reinterpret_cast<float*>(static_cast<char*>(ws) +
                                             align_up((size_t)p.nb * p.nch * p.H * p.P * p.N * 4, 256));
     const int npass = (p.Q * p.M + ly.R - 1) / ly.R;
-    const int nslice = (p.P * p.N + kSsd3StateSlice - 1) / kSsd3StateSlice;
+    const bool wide = (int64_t)p.H * p.nch * p.nb >= kGenericStateWide;
+    const int opt = wide ? 32 : 4, nslice = (p.P * p.N + 256 * opt - 1) / (256 * opt);
     MAMBA_CHECK_ARG((int64_t)p.nch * npass < 65536 && (int64_t)p.nch * nslice < 65536,
                     "too many chunks x row passes for the generic path");
-    hipLaunchKernelGGL(ssd3_chunk_state_generic, dim3(p.H, p.nch * nslice, p.nb), dim3(256), sm_state, stream, p,
-                       states, daend);
+    hipLaunchKernelGGL(wide ? ssd3_chunk_state_generic<32> : ssd3_chunk_state_generic<4>,
+                       dim3(p.H, p.nch * nslice, p.nb), dim3(256), sm_state, stream, p, states, daend);
     MAMBA_CHECK_LAUNCH();
     hipLaunchKernelGGL(ssd3_state_pass_generic, dim3(ceil_div(p.P * p.N, 256), p.H, p.nb), dim3(256), 0, stream, p,
                        states, daend);
