@@ -784,6 +784,11 @@ def bench_ssd3(args):
     hT = torch.empty((cfg["batch"], cfg["nheads"], cfg["headdim"], cfg["dstate"]), device=dev)
 
     def step(events=None):
+        if args.generic:
+            _call_events(lambda: mamba_hip.ssd3_fwd(inp["v"], inp["da"], inp["B"], inp["C"], inp["gamma"],
+                                                    inp["scale"], None, chunk_len=cfg["chunk"], y=y,
+                                                    final_state=hT, generic=True), events)
+            return
         mamba_hip.ssd3_fwd(inp["v"], inp["da"], inp["B"], inp["C"], inp["gamma"], inp["scale"], None,
                            chunk_len=cfg["chunk"], y=y, final_state=hT, events=events)
 
@@ -799,7 +804,8 @@ def bench_ssd3(args):
     else:
         roof = {"bound": "mfma", "achieved": tflops, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": tflops / BF16_PEAK_TFLOPS}
-    roof.update({"traffic": _profiled_traffic("mamba3_ssd_prefill_cfg4"), "kernel_ms": kern_ms,
+    roof.update({"traffic": None if args.generic else _profiled_traffic("mamba3_ssd_prefill_cfg4"),
+                 "kernel_ms": kern_ms,
                  "algorithmic_bytes": nbytes, "algorithmic_flops": flops, "mfma_tflops": tflops})
     fast = mamba_hip.ssd3_fast_path(inp["v"], inp["da"], inp["B"], inp["C"], inp["gamma"], inp["scale"])
     return {
@@ -808,9 +814,12 @@ def bench_ssd3(args):
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": "synthetic (BASELINE.json configs[4] distributions at the SSD seam, seed 0)",
-        "config": {"workload": "mamba3_ssd_prefill_cfg4", **cfg, "io": "v/B/C/y bf16 (per-head B/C), da/gamma/scale f32",
-                   "entry": "mamba_ssd3_fwd", "kernel": "ssd3_scan_mfma (128 fused positions per chunk)" if fast
-                   else "generic", "hbm_gbs": gbs},
+        "config": {"workload": "mamba3_ssd_prefill_cfg4" + ("_generic" if args.generic else ""), **cfg,
+                   "io": "v/B/C/y bf16 (per-head B/C), da/gamma/scale f32",
+                   "entry": "mamba_ssd3_fwd_generic (events around the whole call)" if args.generic
+                   else "mamba_ssd3_fwd",
+                   "kernel": "generic" if args.generic or not fast else "ssd3_scan_mfma (128 fused positions per chunk)",
+                   "hbm_gbs": gbs},
         "roofline": roof,
     }
 
@@ -1301,6 +1310,17 @@ def _time_steps(args, step):
     return ms_per_step, kern_ms
 
 
+def _call_events(call, events):
+    """Run call() with torch events recorded around it on the current stream
+    (the generic path has no timed entry point: its events bracket the whole
+    call, the three SIMT kernels)."""
+    if events is not None:
+        events[0].record()
+    call()
+    if events is not None:
+        events[1].record()
+
+
 def bench_ssd2(args):
     import torch
 
@@ -1313,6 +1333,11 @@ def bench_ssd2(args):
     hT = torch.empty((b, h, p, cfg["dstate"]), dtype=torch.float32, device=dev)
 
     def step(events=None):
+        if args.generic:
+            _call_events(lambda: mamba_hip.ssd2_fwd(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"],
+                                                    None, chunk_len=cfg["chunk"], y=y, final_state=hT,
+                                                    generic=True), events)
+            return
         mamba_hip.ssd2_fwd(inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"], None,
                            chunk_len=cfg["chunk"], y=y, final_state=hT, events=events)
 
@@ -1345,8 +1370,10 @@ def bench_ssd2(args):
         "ms_per_step": ms_per_step,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": "synthetic (BASELINE.json configs[1] distributions, seed 0)",
-        "config": {"workload": "mamba2_ssd_prefill_cfg1", **cfg, "io": "x/B/C/y bf16, dt/A/D/state f32",
-                   "entry": "mamba_ssd2_fwd"},
+        "config": {"workload": "mamba2_ssd_prefill_cfg1" + ("_generic" if args.generic else ""), **cfg,
+                   "io": "x/B/C/y bf16, dt/A/D/state f32",
+                   "entry": "mamba_ssd2_fwd_generic (events around the whole call)" if args.generic
+                   else "mamba_ssd2_fwd"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None,
                      "kernel_ms": kern_ms, "algorithmic_bytes": nbytes,
@@ -1516,6 +1543,9 @@ def main():
                     help="mamba3_fused: MIMO rank at config 4's head shape (4 is config 4; 1 is SISO)")
     ap.add_argument("--m1-shape", default="ref", choices=sorted(MAMBA1_BLOCK_SHAPES),
                     help="mamba1_block: the reference's bench shape (ref) or config 2's layer shape (cfg2)")
+    ap.add_argument("--generic", action="store_true",
+                    help="ssd2 / ssd3: run the shape-generic SIMT kernels (the fallback path) instead of the "
+                         "MFMA path; the events then bracket the whole call")
     ap.add_argument("--batch", type=int, default=DECODE_CFG3["batch"], help="decode batch")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-split", action="store_true",
