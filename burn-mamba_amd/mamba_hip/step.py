@@ -509,10 +509,12 @@ class Mamba2Stack:
     RmsNorm of layer l+1 (one mamba_rmsnorm call) around torch.mm products and
     mamba2_step_ssm.  All activations live in buffers allocated once per batch
     size, so ``step_`` allocates nothing and can be captured in a HIP graph.
-    With ``split_batch`` (the default), a fused step of an even batch of 64 to
+    With ``split_batch`` (the default), a fused step of an even batch of 34 to
     256 rows runs as two half batches on two streams: the rows never interact,
     and one half's weight-streaming products overlap the other half's state
-    kernel (each half reads the weights once)."""
+    kernel (each half reads the weights once).  From 34 rows on, one stream
+    would run the products on two 32-row tiles while the halves run on one
+    each; at 32 rows and below the schedule measured slower."""
 
     def __init__(self, layers: List[Mamba2Layer], fused: bool = True, split_batch: bool = True):
         assert layers
@@ -597,7 +599,7 @@ class Mamba2Stack:
 
     def splits(self, b: int) -> bool:
         """Whether an untimed step of batch ``b`` runs as two half batches on two streams."""
-        return self.fused and self.split_batch and 64 <= b <= 256 and b % 2 == 0
+        return self.fused and self.split_batch and 34 <= b <= 256 and b % 2 == 0
 
     def step_(self, x_res: torch.Tensor, caches: List[Mamba2Cache], events=None):
         """In-place step of the whole stack: x_res [b, d_model] f32 becomes the stack output.

@@ -165,7 +165,7 @@ def test_missing_library_raises_no_fallback():
 
 def test_half_batch_predicate_needs_no_gpu():
     """Mamba2Stack.splits: the two-stream half-batch schedule applies to a fused
-    stack at an even batch of 64 to 256 only, and can be switched off."""
+    stack at an even batch of 34 to 256 only, and can be switched off."""
     import mamba_hip
 
     def stack(fused, split_batch):  # the predicate reads only these two flags; no layers are built
@@ -174,6 +174,7 @@ def test_half_batch_predicate_needs_no_gpu():
         return s
 
     s = stack(True, True)
-    assert [b for b in (1, 16, 62, 63, 64, 65, 66, 100, 255, 256, 258) if s.splits(b)] == [64, 66, 100, 256]
+    assert [b for b in (1, 16, 32, 33, 34, 35, 36, 64, 65, 66, 100, 255, 256, 258) if s.splits(b)] == \
+        [34, 36, 64, 66, 100, 256]
     assert not stack(True, False).splits(64)
     assert not stack(False, True).splits(64)
