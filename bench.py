@@ -546,23 +546,56 @@ def bench_mamba3_step(args):
         cc.v_state_bhp.normal_(0.0, 1.0, generator=gen)
         caches.append(cc)
     x0 = torch.randn((b, c.d_model), generator=gen, device=dev)
-    projs = [torch.empty((b, c.d_in_proj), device=dev, dtype=torch.bfloat16) for _ in range(2)]
-    ys = torch.empty((b, c.d_inner), device=dev, dtype=torch.bfloat16)
-    xs = [torch.empty((b, c.d_model), device=dev, dtype=torch.bfloat16) for _ in range(2)]
-    lin_ws = torch.empty(8 << 20, device=dev, dtype=torch.uint8)  # product workspace, shared in order
-    argl = [mamba_hip.mamba3_step_ssm_args(c, projs[i % 2], caches[i], dt_bias=m.dt_bias, b_norm_w=m.b_norm_w,
-                                           c_norm_w=m.c_norm_w, b_bias=m.b_bias, c_bias=m.c_bias, D=m.D,
-                                           mimo_x=m.mimo_x, mimo_z=m.mimo_z, mimo_o=m.mimo_o, out=ys)
-            for i, m in enumerate(blocks)]
+
+    def rows(lo, hi):
+        """Buffers and step arguments of batch rows lo .. hi - 1 (cache slices)."""
+        n = hi - lo
+        projs = [torch.empty((n, c.d_in_proj), device=dev, dtype=torch.bfloat16) for _ in range(2)]
+        ys = torch.empty((n, c.d_inner), device=dev, dtype=torch.bfloat16)
+        xs = [torch.empty((n, c.d_model), device=dev, dtype=torch.bfloat16) for _ in range(2)]
+        ws = torch.empty(8 << 20, device=dev, dtype=torch.uint8)  # product workspace, shared in order
+        argl = []
+        for i, m in enumerate(blocks):
+            cc = caches[i]
+            part = mamba_hip.Mamba3Cache(cc.ssm_bhpr[lo:hi], cc.k_state_bmhr[lo:hi], cc.v_state_bhp[lo:hi],
+                                         cc.angle_bha[lo:hi], cc.pathway)
+            argl.append(mamba_hip.mamba3_step_ssm_args(c, projs[i % 2], part, dt_bias=m.dt_bias,
+                                                       b_norm_w=m.b_norm_w, c_norm_w=m.c_norm_w, b_bias=m.b_bias,
+                                                       c_bias=m.c_bias, D=m.D, mimo_x=m.mimo_x, mimo_z=m.mimo_z,
+                                                       mimo_o=m.mimo_o, out=ys))
+        return lo, hi, projs, ys, xs, ws, argl
+
+    # the host schedule of Mamba2Stack: an even batch of 34 to 256 rows steps
+    # as two half batches on two streams, one half's weight-streaming products
+    # beside the other half's state kernel (rows never interact; each half
+    # reads the weights once).  Per-layer kernel events time the one-stream
+    # whole-batch step.
+    split = not getattr(args, "no_split", False) and 34 <= b <= 256 and b % 2 == 0
+    whole = rows(0, b)
+    halves = [rows(0, b // 2), rows(b // 2, b)] if split else None
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()] if split else None
+
+    def run(part, events=None):
+        lo, hi, projs, ys, xs, ws, argl = part
+        xs[0].copy_(x0[lo:hi])
+        for i, m in enumerate(blocks):
+            mamba_hip.step_mm(xs[0], m.in_proj_w, out=projs[i % 2], workspace=ws)
+            mamba_hip.mamba3_step_ssm(argl[i], dev, None if events is None else events[i])
+            mamba_hip.step_mm(ys, m.out_proj_w, out=xs[1], workspace=ws)
 
     # every block reads the same input row (no norm/residual between blocks
     # here, so chaining 64 of them would only grow or shrink the activations)
     def eager(events=None):
-        xs[0].copy_(x0)
-        for i, m in enumerate(blocks):
-            mamba_hip.step_mm(xs[0], m.in_proj_w, out=projs[i % 2], workspace=lin_ws)
-            mamba_hip.mamba3_step_ssm(argl[i], dev, None if events is None else events[i])
-            mamba_hip.step_mm(ys, m.out_proj_w, out=xs[1], workspace=lin_ws)
+        if events is not None or not split:
+            run(whole, events)
+            return
+        cur = torch.cuda.current_stream()
+        for part, st in zip(halves, streams):
+            st.wait_stream(cur)
+            with torch.cuda.stream(st):
+                run(part)
+        for st in streams:
+            cur.wait_stream(st)
 
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -600,7 +633,8 @@ def bench_mamba3_step(args):
         "dtype": "bf16", "data": "synthetic (config-4 block shapes, reference init, states ~N(0,0.1), seed 0)",
         "config": {"workload": "mamba3_decode_step", **cfg, "batch": b, "graph": "hip graph of the 64-layer step",
                    "step_bytes": step_bytes, "step_hbm_gbs": step_bytes / (ms_per_step * 1e-3) / 1e9,
-                   "entry": "mamba_linear_fwd in_proj + mamba3_step_ssm + mamba_linear_fwd out_proj per layer"},
+                   "entry": "mamba_linear_fwd in_proj + mamba3_step_ssm + mamba_linear_fwd out_proj per layer",
+                   "schedule": "two half batches on two streams" if split else "one stream"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel_ms": kern_ms,
                      "algorithmic_bytes": kernel_bytes, "kernel": "mamba3_step_kernel (mean over all layers)"},
@@ -1549,8 +1583,8 @@ def main():
     ap.add_argument("--batch", type=int, default=DECODE_CFG3["batch"], help="decode batch")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-split", action="store_true",
-                    help="decode: step the whole batch on one stream (no half-batch schedule), so that "
-                         "every state-kernel dispatch of a kernel trace covers the full batch")
+                    help="decode / mamba3_step: step the whole batch on one stream (no half-batch schedule), "
+                         "so that every state-kernel dispatch of a kernel trace covers the full batch")
     ap.add_argument("--no-decode", action="store_true",
                     help="ssd2 only: leave out the decode_b64 half of the headline metric")
     ap.add_argument("--calibrate-copy", action="store_true",
