@@ -583,9 +583,23 @@ def bench_mamba3_step(args):
             mamba_hip.mamba3_step_ssm(argl[i], dev, None if events is None else events[i])
             mamba_hip.step_mm(ys, m.out_proj_w, out=xs[1], workspace=ws)
 
+    if getattr(args, "m3_stack", False):
+        # the library's stack: pre-norm residual layers (Layers::step), one
+        # rmsnorm per layer on top of the blocks, the same schedule
+        stack = mamba_hip.Mamba3Stack([mamba_hip.Mamba3Layer(torch.ones(c.d_model, device=dev), m) for m in blocks],
+                                      split_batch=not getattr(args, "no_split", False))
+        x_res = torch.empty((b, c.d_model), device=dev)
+        stack.buffers(b, dev)
+
+        def eager(events=None):
+            x_res.copy_(x0)
+            stack.step_(x_res, caches, events)
+    else:
+        eager = None
+
     # every block reads the same input row (no norm/residual between blocks
     # here, so chaining 64 of them would only grow or shrink the activations)
-    def eager(events=None):
+    def eager_blocks(events=None):
         if events is not None or not split:
             run(whole, events)
             return
@@ -597,6 +611,8 @@ def bench_mamba3_step(args):
         for st in streams:
             cur.wait_stream(st)
 
+    if eager is None:
+        eager = eager_blocks
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -634,7 +650,9 @@ def bench_mamba3_step(args):
         "config": {"workload": "mamba3_decode_step", **cfg, "batch": b, "graph": "hip graph of the 64-layer step",
                    "step_bytes": step_bytes, "step_hbm_gbs": step_bytes / (ms_per_step * 1e-3) / 1e9,
                    "entry": "mamba_linear_fwd in_proj + mamba3_step_ssm + mamba_linear_fwd out_proj per layer",
-                   "schedule": "two half batches on two streams" if split else "one stream"},
+                   "schedule": "two half batches on two streams" if split else "one stream",
+                   "layers": "Mamba3Stack: pre-norm residual layers (rmsnorm + block per layer)"
+                   if getattr(args, "m3_stack", False) else "blocks (each reads the same input row)"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel_ms": kern_ms,
                      "algorithmic_bytes": kernel_bytes, "kernel": "mamba3_step_kernel (mean over all layers)"},
@@ -1585,6 +1603,9 @@ def main():
     ap.add_argument("--no-split", action="store_true",
                     help="decode / mamba3_step: step the whole batch on one stream (no half-batch schedule), "
                          "so that every state-kernel dispatch of a kernel trace covers the full batch")
+    ap.add_argument("--m3-stack", action="store_true",
+                    help="mamba3_step: step the library's Mamba3Stack (pre-norm residual layers) instead of "
+                         "the bare blocks")
     ap.add_argument("--no-decode", action="store_true",
                     help="ssd2 only: leave out the decode_b64 half of the headline metric")
     ap.add_argument("--calibrate-copy", action="store_true",

@@ -16,7 +16,7 @@ from .step import conv_fwd as mamba2_conv_fwd, div_eps, gated_rmsnorm as mamba2_
 from .step import drop_derived, packed_weight, prefill_mm, step_mm, step_mm_ok  # noqa: F401
 from .ssd3 import (Mamba3DoubleSsdInput, Mamba3SingleSsdInput, ssd3_double_fast_path, ssd3_double_fwd,  # noqa: F401
                    ssd3_autograd, ssd3_bwd, ssd3_fast_path, ssd3_fwd)
-from .mamba3 import Mamba3, Mamba3Cache, Mamba3Config  # noqa: F401
+from .mamba3 import Mamba3, Mamba3Cache, Mamba3Config, Mamba3Layer, Mamba3Stack  # noqa: F401
 from .mamba3 import step_ssm as mamba3_step_ssm, step_ssm_args as mamba3_step_ssm_args  # noqa: F401
 from .mamba3 import finish_fwd as mamba3_finish_fwd, prep_fwd as mamba3_prep_fwd  # noqa: F401
 from .mamba3 import prep_args as mamba3_prep_args, prep_fast_path as mamba3_prep_fast_path  # noqa: F401

@@ -477,3 +477,144 @@ class Mamba3:
         for w in (self.in_proj_w, self.out_proj_w):
             if w.dtype == torch.bfloat16 and w.shape[0] % 16 == 0:
                 packed_weight(w)
+
+
+@dataclass
+class Mamba3Layer:
+    """Pre-norm residual layer (src/modules/layer.rs:224-232) around a Mamba3 block."""
+    norm_w: torch.Tensor   # [d_model] f32 RmsNorm gamma
+    mixer: Mamba3
+
+
+class Mamba3Stack:
+    """A stack of pre-norm Mamba3 layers stepped one token at a time
+    (Layers::step, src/modules/layers.rs:427-520, without class latents; each
+    layer Layer::step_one, layer.rs:224-232).
+
+    The residual stream is kept in f32.  Per layer: one mamba_rmsnorm (the
+    previous layer's residual add fused with this layer's pre-norm, into a bf16
+    operand), in_proj on the packed streaming product, mamba3_step_ssm,
+    out_proj; a last mamba_rmsnorm adds the final residual.  bf16 blocks whose
+    products the packed kernel takes (d_model and d_inner multiples of 16).
+    Buffers and step arguments are made once per batch size, so ``step_``
+    allocates nothing and can be captured in a HIP graph.  With
+    ``split_batch`` (the default) an even batch of 34 to 256 rows steps as two
+    half batches on two streams, the schedule of Mamba2Stack: one half's
+    weight-streaming products overlap the other half's step kernel (each half
+    reads the weights once; rows never interact)."""
+
+    def __init__(self, layers, split_batch: bool = True):
+        from .step import linear  # noqa: F401  (fails early if the product entry is missing)
+        assert layers
+        self.layers = list(layers)
+        self.cfg = self.layers[0].mixer.cfg
+        c = self.cfg
+        for l in self.layers:
+            m = l.mixer
+            if m.in_proj_w.dtype != torch.bfloat16 or m.out_proj_w.dtype != torch.bfloat16:
+                raise _lib.MambaHipError("Mamba3Stack steps bf16 blocks (packed products)")
+        if c.d_model % 16 or c.d_inner % 16:
+            raise _lib.MambaHipError("Mamba3Stack needs d_model and d_inner multiples of 16")
+        self.split_batch = split_batch
+        self._packed = [(packed_weight(l.mixer.in_proj_w), packed_weight(l.mixer.out_proj_w)) for l in self.layers]
+        self._bias = [tuple(None if t is None else t.float().contiguous()
+                            for t in (l.mixer.in_proj_b, l.mixer.out_proj_b)) for l in self.layers]
+        self._bufs = {}
+        self._args = {}
+        self._side = None
+
+    @staticmethod
+    def init(cfg: Mamba3Config, n_layers: int, device, dtype=torch.bfloat16,
+             generator: Optional[torch.Generator] = None, split_batch: bool = True) -> "Mamba3Stack":
+        return Mamba3Stack([Mamba3Layer(norm_w=torch.ones(cfg.d_model, device=device, dtype=torch.float32),
+                                        mixer=cfg.init(device, dtype, generator)) for _ in range(n_layers)],
+                           split_batch=split_batch)
+
+    def new_caches(self, batch: int, pathway: str = "single"):
+        return [l.mixer.new_cache(batch, pathway) for l in self.layers]
+
+    def splits(self, b: int) -> bool:
+        """Whether an untimed step of batch ``b`` runs as two half batches on two streams."""
+        return self.split_batch and 34 <= b <= 256 and b % 2 == 0
+
+    def buffers(self, batch: int, device, slot: int = 0):
+        key = (batch, str(device), slot)
+        if key not in self._bufs:
+            from ._lib import LinearArgs
+            c = self.cfg
+            bf = torch.bfloat16
+            bufs = dict(
+                normed=torch.empty((batch, c.d_model), device=device, dtype=bf),
+                proj=torch.empty((batch, c.d_in_proj), device=device, dtype=bf),
+                y=torch.empty((batch, c.d_inner), device=device, dtype=bf),
+                out=torch.empty((batch, c.d_model), device=device, dtype=bf))
+            # one workspace for both products (used in order): the larger need
+            need = 256
+            for d_in, d_out in ((c.d_model, c.d_in_proj), (c.d_inner, c.d_model)):
+                la = LinearArgs()
+                la.rows, la.d_in, la.d_out = batch, d_in, d_out
+                la.x_dtype = la.y_dtype = _lib.MAMBA_BF16
+                la.x_ld, la.y_ld = d_in, d_out
+                need = max(need, _lib.lib().mamba_linear_workspace_size(ctypes.byref(la)))
+            bufs["ws"] = torch.empty(need, device=device, dtype=torch.uint8)
+            self._bufs[key] = bufs
+        return self._bufs[key]
+
+    def _layer_args(self, i: int, slot: int, bufs, cache: Mamba3Cache) -> Mamba3StepArgs:
+        key = (i, slot, bufs["proj"].data_ptr(), cache.ssm_bhpr.data_ptr(), cache.k_state_bmhr.data_ptr(),
+               cache.v_state_bhp.data_ptr(), cache.angle_bha.data_ptr(), cache.ssm_bhpr.shape[0])
+        a = self._args.get(key)
+        if a is None:
+            m = self.layers[i].mixer
+            a = step_ssm_args(self.cfg, bufs["proj"], cache, dt_bias=m.dt_bias, b_norm_w=m.b_norm_w,
+                              c_norm_w=m.c_norm_w, b_bias=m.b_bias, c_bias=m.c_bias, D=m.D, mimo_x=m.mimo_x,
+                              mimo_z=m.mimo_z, mimo_o=m.mimo_o, out_norm_w=m.out_norm_w, out=bufs["y"])
+            self._args[key] = a
+        return a
+
+    def _run(self, x_res: torch.Tensor, caches, events, slot: int):
+        from .step import linear, rmsnorm
+        c = self.cfg
+        bufs = self.buffers(x_res.shape[0], x_res.device, slot)
+        prev = None
+        for i, layer in enumerate(self.layers):
+            rmsnorm(x_res, layer.norm_w, out=bufs["normed"], add=prev)
+            (pin, pout), (bin_, bout) = self._packed[i], self._bias[i]
+            linear(bufs["normed"], pin, c.d_in_proj, bias=bin_, out=bufs["proj"], workspace=bufs["ws"])
+            step_ssm(self._layer_args(i, slot, bufs, caches[i]), x_res.device, None if events is None else events[i])
+            linear(bufs["y"], pout, c.d_model, bias=bout, out=bufs["out"], workspace=bufs["ws"])
+            prev = bufs["out"]
+        rmsnorm(x_res, None, add=prev)
+        return x_res
+
+    def step_(self, x_res: torch.Tensor, caches, events=None):
+        """In-place step of the whole stack: x_res [b, d_model] f32 becomes the
+        stack output.  ``events``: optional list of one torch.cuda.Event pair per
+        layer, recorded around that layer's mamba3_step_ssm (one stream)."""
+        if x_res.dtype != torch.float32 or x_res.dim() != 2 or x_res.stride(1) != 1:
+            raise _lib.MambaHipError("x_res must be a row-contiguous [b, d_model] float32 tensor")
+        b = x_res.shape[0]
+        if events is None and self.splits(b):
+            cur = torch.cuda.current_stream(x_res.device)
+            if self._side is None:
+                self._side = (torch.cuda.Stream(x_res.device), torch.cuda.Stream(x_res.device))
+            h = b // 2
+            for k, (lo, hi) in enumerate(((0, h), (h, b))):
+                st = self._side[k]
+                st.wait_stream(cur)
+                with torch.cuda.stream(st):
+                    part = [Mamba3Cache(cc.ssm_bhpr[lo:hi], cc.k_state_bmhr[lo:hi], cc.v_state_bhp[lo:hi],
+                                        cc.angle_bha[lo:hi], cc.pathway) for cc in caches]
+                    self._run(x_res[lo:hi], part, None, 1 + k)
+            for st in self._side:
+                cur.wait_stream(st)
+            return x_res
+        return self._run(x_res, caches, events, 0)
+
+    def step(self, x: torch.Tensor, caches=None):
+        """Out-of-place convenience: returns (y [b, d_model] f32, caches)."""
+        if caches is None:
+            caches = self.new_caches(x.shape[0])
+        x_res = x.to(torch.float32).clone()
+        self.step_(x_res, caches)
+        return x_res, caches

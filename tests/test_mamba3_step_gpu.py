@@ -209,3 +209,52 @@ def test_mamba3_step_validation():
     with pytest.raises(mamba_hip.MambaHipError, match="mimo_o"):
         _run_gpu(cfg, prm, _gpu_cache(cache), proj)
     del torch
+
+
+def _stack_reference(stack, x, caches):
+    """Layers::step over the stack's layers from Mamba3.step and torch ops:
+    x += block(RmsNorm(x) * w) per layer (layer.rs:224-232), f32 residual."""
+    import torch
+    x = x.clone()
+    for layer, cache in zip(stack.layers, caches):
+        # RmsNorm with div_eps(F32) (src/utils/mod.rs:59-65), as the stack's kernel
+        xn = x / torch.sqrt(x.pow(2).mean(-1, keepdim=True) + 8.1584695e-8) * layer.norm_w
+        out, _ = layer.mixer.step(xn.to(torch.bfloat16), cache)
+        x = x + out.float()
+    return x
+
+
+@pytest.mark.parametrize("b", [3, 36])
+def test_mamba3_stack_step(b):
+    """Mamba3Stack.step_ (rmsnorm + packed products + mamba3_step_ssm per layer;
+    at 36 rows two half batches on two streams) against the same layers stepped
+    through Mamba3.step with torch's norm and residual, two tokens, caches
+    carried; then the same stack with the schedule off agrees."""
+    import torch
+    import mamba_hip
+    cfg = mamba_hip.Mamba3Config(d_model=256, state_rank=128, per_head_dim=64, mimo_rank=4)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(41 + b)
+    stack = mamba_hip.Mamba3Stack.init(cfg, 3, "cuda", torch.bfloat16, gen)
+    for layer in stack.layers:
+        layer.norm_w.uniform_(0.5, 1.5, generator=gen)
+    whole = mamba_hip.Mamba3Stack(stack.layers, split_batch=False)
+    assert stack.splits(b) == (b == 36) and not whole.splits(b)
+    c_stack, c_ref, c_whole = stack.new_caches(b), stack.new_caches(b), stack.new_caches(b)
+    eps = None
+    for _ in range(2):
+        x = torch.randn((b, cfg.d_model), generator=gen, device="cuda")
+        got = x.clone()
+        stack.step_(got, c_stack)
+        alt = x.clone()
+        whole.step_(alt, c_whole)
+        want = _stack_reference(stack, x, c_ref)
+        torch.cuda.synchronize()
+        eps = torch.finfo(torch.bfloat16).eps
+        np.testing.assert_allclose(got.cpu().numpy(), want.cpu().numpy(), rtol=2e-2, atol=1e-2)
+        # the half batches may split the products' k sums differently: a bf16
+        # operand may round one ulp apart
+        np.testing.assert_allclose(got.cpu().numpy(), alt.cpu().numpy(), rtol=4 * eps, atol=5e-3)
+    for cs, cr in zip(c_stack, c_ref):
+        np.testing.assert_allclose(cs.ssm_bhpr.cpu().numpy(), cr.ssm_bhpr.cpu().numpy(), rtol=2e-2, atol=1e-2)
+        np.testing.assert_allclose(cs.angle_bha.cpu().numpy(), cr.angle_bha.cpu().numpy(), rtol=1e-5, atol=1e-5)
