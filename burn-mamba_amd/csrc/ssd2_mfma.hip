@@ -445,24 +445,29 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
         f32x16_t yacc[T];
 #pragma unroll
         for (int it = 0; it < T; ++it) yacc[it] = zero16();
+        // the entering state as bf16 A operands, once: the y tiles and the
+        // rare steep path read it after the state update below has moved on
+        bf16x8_t hpk[NK];
+#pragma unroll
+        for (int kn = 0; kn < NK; ++kn) {
+            float hv[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) hv[e] = hacc[kn >> 1][8 * (kn & 1) + e];
+            hpk[kn] = pack8(hv);
+        }
         bf16x8_t cnext[T];
 #pragma unroll
         for (int it = 0; it < T; ++it) cnext[it] = *(const bf16x8_t*)(F0 + ((FL::C0 + it * NK) * 64 + lane) * 8);
 #pragma unroll
         for (int kn = 0; kn < NK; ++kn) {
-            const int nt = kn >> 1, q = kn & 1;
             bf16x8_t cop[T];
 #pragma unroll
             for (int it = 0; it < T; ++it) {
                 cop[it] = cnext[it];
                 if (kn + 1 < NK) cnext[it] = *(const bf16x8_t*)(F0 + ((FL::C0 + it * NK + kn + 1) * 64 + lane) * 8);
             }
-            float hv[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) hv[e] = hacc[nt][8 * q + e];
-            const bf16x8_t a = pack8(hv);
-#pragma unroll
-            for (int it = 0; it < T; ++it) yacc[it] = mfma32x32x16(a, cop[it], yacc[it]);
+            for (int it = 0; it < T; ++it) yacc[it] = mfma32x32x16(hpk[kn], cop[it], yacc[it]);
         }
         // ---- every tile as if no block were steep, the tiles' chains side by
         // side: block jt's xg operands serve all tiles it >= jt
@@ -484,6 +489,38 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
                 for (int it = jt; it < T; ++it)
                     yacc[it] = mfma32x32x16(
                         a, *(const bf16x8_t*)(F0 + ((it * (it + 1) + ks) * 64 + lane) * 8), yacc[it]);
+            }
+        }
+        // ---- K3 + K4 (issued before the y tiles' epilogue, whose VALU work
+        // can then run beside these MFMAs): h-hat^T <- h-hat^T + B_k^T . (xg_k / phi_k) over the
+        // blocks (phi applied on events only; each k step's operands read one
+        // step ahead)
+        bf16x8_t bnext[NTN], xnext = *(const bf16x8_t*)&s_xg[wave][r][8 * half];
+#pragma unroll
+        for (int nt = 0; nt < NTN; ++nt) bnext[nt] = *(const bf16x8_t*)(F0 + ((FL::B0 + nt * KS) * 64 + lane) * 8);
+#pragma unroll
+        for (int jt = 0; jt < T; ++jt) {
+            if (ev[jt]) {
+#pragma unroll
+                for (int nt = 0; nt < NTN; ++nt)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) hacc[nt][v] *= rho[jt];
+            }
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                const int ks = 2 * jt + kk;
+                const bf16x8_t bx = xnext;
+                bf16x8_t bop[NTN];
+#pragma unroll
+                for (int nt = 0; nt < NTN; ++nt) bop[nt] = bnext[nt];
+                if (ks + 1 < KS) {
+                    xnext = *(const bf16x8_t*)&s_xg[wave][r][(ks + 1) * 16 + 8 * half];
+#pragma unroll
+                    for (int nt = 0; nt < NTN; ++nt)
+                        bnext[nt] = *(const bf16x8_t*)(F0 + ((FL::B0 + nt * KS + ks + 1) * 64 + lane) * 8);
+                }
+#pragma unroll
+                for (int nt = 0; nt < NTN; ++nt) hacc[nt] = mfma32x32x16(bop[nt], bx, hacc[nt]);
             }
         }
         // y_i = exp(cs_i - cs_{e_it}) phi_it acc + D x_i, x_i raw from the chunk's
@@ -534,13 +571,9 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
                 // each lower block's S_k / phi_k times phi_k
                 f32x16_t acc = zero16();
 #pragma unroll
-                for (int kn = 0; kn < NK; ++kn) {
-                    float hv[8];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) hv[e] = hacc[kn >> 1][8 * (kn & 1) + e];
-                    acc = mfma32x32x16(pack8(hv),
-                                       *(const bf16x8_t*)(F0 + ((FL::C0 + it * NK + kn) * 64 + lane) * 8), acc);
-                }
+                for (int kn = 0; kn < NK; ++kn)
+                    acc = mfma32x32x16(hpk[kn], *(const bf16x8_t*)(F0 + ((FL::C0 + it * NK + kn) * 64 + lane) * 8),
+                                       acc);
                 const float phin = __builtin_amdgcn_exp2f(lphi_in);
 #pragma unroll
                 for (int v = 0; v < 16; ++v) acc[v] *= phin;
@@ -594,37 +627,6 @@ __global__ __launch_bounds__(64 * HPW, HPW >= 5 ? 1 : 8 / HPW) void ssd2_scan_wu
             }
         }
 
-        // ---- K3 + K4: h-hat^T <- h-hat^T + B_k^T . (xg_k / phi_k) over the
-        // blocks (phi applied on events only; each k step's operands read one
-        // step ahead)
-        bf16x8_t bnext[NTN], xnext = *(const bf16x8_t*)&s_xg[wave][r][8 * half];
-#pragma unroll
-        for (int nt = 0; nt < NTN; ++nt) bnext[nt] = *(const bf16x8_t*)(F0 + ((FL::B0 + nt * KS) * 64 + lane) * 8);
-#pragma unroll
-        for (int jt = 0; jt < T; ++jt) {
-            if (ev[jt]) {
-#pragma unroll
-                for (int nt = 0; nt < NTN; ++nt)
-#pragma unroll
-                    for (int v = 0; v < 16; ++v) hacc[nt][v] *= rho[jt];
-            }
-#pragma unroll
-            for (int kk = 0; kk < 2; ++kk) {
-                const int ks = 2 * jt + kk;
-                const bf16x8_t bx = xnext;
-                bf16x8_t bop[NTN];
-#pragma unroll
-                for (int nt = 0; nt < NTN; ++nt) bop[nt] = bnext[nt];
-                if (ks + 1 < KS) {
-                    xnext = *(const bf16x8_t*)&s_xg[wave][r][(ks + 1) * 16 + 8 * half];
-#pragma unroll
-                    for (int nt = 0; nt < NTN; ++nt)
-                        bnext[nt] = *(const bf16x8_t*)(F0 + ((FL::B0 + nt * KS + ks + 1) * 64 + lane) * 8);
-                }
-#pragma unroll
-                for (int nt = 0; nt < NTN; ++nt) hacc[nt] = mfma32x32x16(bop[nt], bx, hacc[nt]);
-            }
-        }
         // ---- this wave's loads done (chunk c + 1's fragments and x), then
         // the chunk's barrier: every wave's fragments for c + 1 have landed and
         // every wave is done with chunk c's buffer
