@@ -258,3 +258,56 @@ def test_mamba3_stack_step(b):
     for cs, cr in zip(c_stack, c_ref):
         np.testing.assert_allclose(cs.ssm_bhpr.cpu().numpy(), cr.ssm_bhpr.cpu().numpy(), rtol=2e-2, atol=1e-2)
         np.testing.assert_allclose(cs.angle_bha.cpu().numpy(), cr.angle_bha.cpu().numpy(), rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("b", [3, 36])
+def test_mamba3_stack_hip_graph_replays_equal_eager(b):
+    """Capture one Mamba3Stack step in a HIP graph (36 rows: the two-stream
+    half-batch schedule, two branches); replay it several times with eager work
+    in between and check every replay against the eager step, bit for bit."""
+    import torch
+    import mamba_hip
+    cfg = mamba_hip.Mamba3Config(d_model=256, state_rank=128, per_head_dim=64, mimo_rank=4)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(61 + b)
+    stack = mamba_hip.Mamba3Stack.init(cfg, 2, "cuda", torch.bfloat16, gen)
+    base = stack.new_caches(b)
+    for c in base:
+        c.ssm_bhpr.normal_(0.0, 0.1, generator=gen)
+        c.k_state_bmhr.normal_(0.0, 0.1, generator=gen)
+        c.v_state_bhp.normal_(0.0, 1.0, generator=gen)
+        c.angle_bha.uniform_(-3.0, 3.0, generator=gen)
+    x0 = torch.randn((b, cfg.d_model), generator=gen, device="cuda")
+    names = ("ssm_bhpr", "k_state_bmhr", "v_state_bhp", "angle_bha")
+
+    def clone(cs):
+        return [mamba_hip.Mamba3Cache(*(getattr(c, n).clone() for n in names), c.pathway) for c in cs]
+
+    eager = clone(base)
+    x_e = x0.clone()
+    stack.step_(x_e, eager)
+    torch.cuda.synchronize()
+    gcaches = clone(base)
+    x_g = x0.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):  # buffers, arguments and streams made outside the capture
+        stack.step_(x_g.clone(), gcaches)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        stack.step_(x_g, gcaches)
+    for rep in range(3):
+        x_g.copy_(x0)
+        for dst, src in zip(gcaches, base):
+            for n in names:
+                getattr(dst, n).copy_(getattr(src, n))
+        _ = (x0 * 2).sum().item()  # eager work and a sync between replays
+        g.replay()
+        torch.cuda.synchronize()
+        print(f"replay {rep}", flush=True)
+        assert torch.equal(x_g, x_e)
+        for a, e in zip(gcaches, eager):
+            for n in names:
+                assert torch.equal(getattr(a, n), getattr(e, n)), n
