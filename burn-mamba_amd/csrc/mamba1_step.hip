@@ -115,6 +115,16 @@ __global__ __launch_bounds__(256) void mamba1_step_kernel(M1StepParams p) {
     }
 }
 
+// Measured on the 64-layer config-2 step (dstate 16), interleaved: four
+// channels per thread at batch 64 (1 280 workgroups; 1.15 ms against 1.23 /
+// 1.35 ms with 2 / 1) and 32 (0.73 ms; 0.75 with 2); two at batch 16 (0.52 ms
+// against 0.55 with 4); one at batch 1 (80 workgroups; 0.30 ms against 0.36
+// with 4).
+#ifndef MAMBA_M1STEP_MIN_GROUPS
+#define MAMBA_M1STEP_MIN_GROUPS 512
+#endif
+constexpr int64_t kM1StepMinGroups = MAMBA_M1STEP_MIN_GROUPS;
+
 // Any dstate: one thread per channel.
 __global__ __launch_bounds__(256) void mamba1_step_generic(M1StepParams p) {
     const int b = blockIdx.y;
@@ -138,6 +148,12 @@ __global__ __launch_bounds__(256) void mamba1_step_generic(M1StepParams p) {
         out *= zv / (1.f + __expf(-zv));
     }
     p.y[(int64_t)b * p.y_sb + d] = out;
+}
+
+template <int N, int CPT>
+static void m1_step_launch(const M1StepParams& p, hipStream_t s) {
+    hipLaunchKernelGGL((mamba1_step_kernel<N, CPT>), dim3(ceil_div(p.D, (256 / (N / 4)) * CPT), p.nb), dim3(256), 0, s,
+                       p);
 }
 
 // ---------------------------------------------------------------------------
@@ -209,20 +225,27 @@ static int m1_step_dispatch(const mamba1_step_args* a, hipStream_t s, hipEvent_t
     p.dbias = a->delta_bias; p.softplus = a->delta_softplus != 0;
     p.h = a->state; p.y = a->y; p.y_sb = a->y_sb;
     const bool aligned = ((uintptr_t)p.h & 15u) == 0;
-    constexpr int CPT = 4;
     if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, s));
-    switch (aligned ? p.N : 0) {
-        case 16:
-            hipLaunchKernelGGL((mamba1_step_kernel<16, CPT>), dim3(ceil_div(p.D, 64 * CPT), p.nb), dim3(256), 0, s, p);
-            break;
-        case 32:
-            hipLaunchKernelGGL((mamba1_step_kernel<32, CPT>), dim3(ceil_div(p.D, 32 * CPT), p.nb), dim3(256), 0, s, p);
-            break;
-        case 64:
-            hipLaunchKernelGGL((mamba1_step_kernel<64, CPT>), dim3(ceil_div(p.D, 16 * CPT), p.nb), dim3(256), 0, s, p);
-            break;
-        default:
-            hipLaunchKernelGGL(mamba1_step_generic, dim3(ceil_div(p.D, 256), p.nb), dim3(256), 0, s, p);
+    if (aligned && (p.N == 16 || p.N == 32 || p.N == 64)) {
+        // channels per thread: 4 (every load of four channels in flight before
+        // any arithmetic) while that still gives kM1StepMinGroups workgroups,
+        // else fewer, so that small batches spread over more CUs
+        const int cpb = 256 / (p.N / 4);
+        int cpt = 4;
+        while (cpt > 1 && (int64_t)ceil_div(p.D, cpb * cpt) * p.nb < kM1StepMinGroups) cpt /= 2;
+        switch (p.N * 8 + cpt) {
+            case 16 * 8 + 4: m1_step_launch<16, 4>(p, s); break;
+            case 16 * 8 + 2: m1_step_launch<16, 2>(p, s); break;
+            case 16 * 8 + 1: m1_step_launch<16, 1>(p, s); break;
+            case 32 * 8 + 4: m1_step_launch<32, 4>(p, s); break;
+            case 32 * 8 + 2: m1_step_launch<32, 2>(p, s); break;
+            case 32 * 8 + 1: m1_step_launch<32, 1>(p, s); break;
+            case 64 * 8 + 4: m1_step_launch<64, 4>(p, s); break;
+            case 64 * 8 + 2: m1_step_launch<64, 2>(p, s); break;
+            default: m1_step_launch<64, 1>(p, s); break;
+        }
+    } else {
+        hipLaunchKernelGGL(mamba1_step_generic, dim3(ceil_div(p.D, 256), p.nb), dim3(256), 0, s, p);
     }
     MAMBA_CHECK_LAUNCH();
     if (ev1) MAMBA_CHECK_HIP(hipEventRecord(ev1, s));
