@@ -44,18 +44,25 @@ struct Ssd3MfmaParams {
 };
 
 // UNIT: the double-SSD seam, scale = gamma = 1 at every position (no tables read)
+// 8 waves: waves 0-3 each form one 32-position output tile, waves 4-7 each
+// update one 32-column dstate tile of the state, so the two halves of the
+// chunk's MFMA work run side by side on every SIMD (two waves per SIMD);
+// every wave shares the staging.
 template <int QF, bool UNIT>
-__global__ __launch_bounds__(256, 1) void ssd3_scan_mfma(Ssd3MfmaParams p) {
+__global__ __launch_bounds__(512, 1) void ssd3_scan_mfma(Ssd3MfmaParams p) {
     constexpr int N = 128;
     constexpr int T = QF / 32;            // output tiles per chunk (one per wave)
     static_assert(T == 4, "one output tile per wave");
     constexpr int NK = N / 16;            // k-steps over dstate
     constexpr int XI = (QF / 2) * 4;      // v staging items: (position pair, 8-wide headdim piece)
     constexpr int BI = (QF / 2) * (N / 8);  // B staging items: (position pair, 8-wide dstate piece)
-    constexpr int XPT = (XI + 255) / 256, BPT = BI / 256;
+    constexpr int NT = 512;               // threads
+    constexpr int XPT = (XI + NT - 1) / NT, BPT = BI / NT;
     __shared__ Ssd3Lds<QF> S;
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 31, half = lane >> 5;
+    const bool st_wave = wave >= 4;       // waves 4-7: the state; 0-3: the y tiles
+    const int w4 = wave & 3;              // the state wave's dstate tile / the y wave's output tile
     // XCD-aware mapping: the two headdim halves of a head (same B/C rows) and
     // neighbouring heads of a batch row land on one XCD
     const int nwg = p.nb * p.H * 2;
@@ -66,15 +73,15 @@ __global__ __launch_bounds__(256, 1) void ssd3_scan_mfma(Ssd3MfmaParams p) {
     const int p0 = ph * 32;
     const int lgM = __builtin_ctz(p.M);  // the MIMO rank is a power of two dividing 32
 
-    // state tile of this wave: headdim rows p0..p0+31, dstate columns 32 wave..
+    // state tile of a state wave: headdim rows p0..p0+31, dstate columns 32 w4..
     s3_f32x16_t hacc;
     const int64_t hbase = ((int64_t)b * p.H + h) * 64 * N;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
         const int pp = p0 + 8 * (v >> 2) + 4 * half + (v & 3);
-        hacc[v] = p.h0 ? p.h0[hbase + pp * N + wave * 32 + r] : 0.f;
+        hacc[v] = (st_wave && p.h0) ? p.h0[hbase + pp * N + w4 * 32 + r] : 0.f;
     }
-    ssd3_put_state(S, hacc, 0, wave, r, half);
+    if (st_wave) ssd3_put_state(S, hacc, 0, w4, r, half);
 
     const bf16_t* vhead = p.v + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh + p0;
     const bf16_t* bhead = p.Bm + (int64_t)b * p.B_sb + (int64_t)g * p.B_sg;
@@ -86,12 +93,15 @@ __global__ __launch_bounds__(256, 1) void ssd3_scan_mfma(Ssd3MfmaParams p) {
 
     // per-thread byte offsets within a chunk (the host bounds a chunk's span below 2^31 bytes)
     const uint32_t v_rs = (uint32_t)p.v_sf * 2, b_rs = (uint32_t)p.B_sf * 2, c_rs = (uint32_t)p.C_sf * 2;
-    const uint32_t vo = (uint32_t)(threadIdx.x >> 2) * 2 * v_rs + (threadIdx.x & 3) * 16;
-    // B items: position pair fp = tid / 16 (+16 per k), 8-wide dstate piece nv
+    // v items: position pair threadIdx.x / 4 (threads 0-255), 8-wide headdim piece threadIdx.x % 4
+    const uint32_t vo = (uint32_t)((threadIdx.x & 255) >> 2) * 2 * v_rs + (threadIdx.x & 3) * 16;
+    // B items: position pair fp = tid / 16 (+32 per k), 8-wide dstate piece nv
     const int b_fp = threadIdx.x >> 4, b_nv = threadIdx.x & 15;
     const uint32_t bo = (uint32_t)b_fp * 2 * b_rs + b_nv * 16;
-    const uint32_t co = (uint32_t)(wave * 32 + r) * c_rs + 16 * half;
-    const int tpos = threadIdx.x >> lgM;  // step of this thread's position within the chunk
+    const uint32_t co = (uint32_t)(w4 * 32 + r) * c_rs + 16 * half;
+    // step of this thread's position within the chunk; threads past the chunk's
+    // positions read one step past its end (zero through the buffer's extent)
+    const int tpos = min((int)threadIdx.x, QF) >> lgM;
     const uint32_t dao = (uint32_t)tpos * (uint32_t)p.da_sl * 4, sco = (uint32_t)tpos * (uint32_t)p.sc_sl * 4,
                    gmo = (uint32_t)tpos * (uint32_t)p.gm_sl * 4;
     const bool first_m = (threadIdx.x & ((1 << lgM) - 1)) == 0;
@@ -104,14 +114,15 @@ __global__ __launch_bounds__(256, 1) void ssd3_scan_mfma(Ssd3MfmaParams p) {
         const int rows = min(QF, p.L - c * QF);  // valid positions of the chunk
         const int steps = rows >> lgM;
         const int64_t f0 = (int64_t)c * QF;
-        const __amdgpu_buffer_rsrc_t rv = s3_rsrc(vhead + f0 * p.v_sf, (uint32_t)rows * v_rs);
+        // the v items sit in waves 0-3: the state waves' copies read nothing
+        const __amdgpu_buffer_rsrc_t rv = s3_rsrc(vhead + f0 * p.v_sf, (uint32_t)(wave < 4 ? rows : 0) * v_rs);
         const __amdgpu_buffer_rsrc_t rb = s3_rsrc(bhead + f0 * p.B_sf, (uint32_t)rows * b_rs);
         xq[0][0] = s3_bld16(rv, vo);
         xq[0][1] = s3_bld16(rv, vo + v_rs);
 #pragma unroll
         for (int k = 0; k < BPT; ++k) {
-            bq[k][0] = s3_bld16(rb, bo + (uint32_t)k * 32 * b_rs);
-            bq[k][1] = s3_bld16(rb, bo + (uint32_t)k * 32 * b_rs + b_rs);
+            bq[k][0] = s3_bld16(rb, bo + (uint32_t)k * 64 * b_rs);
+            bq[k][1] = s3_bld16(rb, bo + (uint32_t)k * 64 * b_rs + b_rs);
         }
         const int64_t t0 = f0 >> lgM;
         const __amdgpu_buffer_rsrc_t rda = s3_rsrc(dahead + t0 * p.da_sl, (uint32_t)steps * (uint32_t)p.da_sl * 4);
@@ -137,14 +148,20 @@ __global__ __launch_bounds__(256, 1) void ssd3_scan_mfma(Ssd3MfmaParams p) {
         for (int kn = 0; kn < NK; ++kn) cn[kn] = s3_bld16(rc, co + 32 * kn);
     };
     fetch(0);
-    fetch_c(0);
+    if (!st_wave) fetch_c(0);
 
     for (int c = 0; c < p.nch; ++c) {
         const int cur = c & 1;
+        // the lane coordinates as opaque values: the per-lane LDS addresses of
+        // the tiles below are loop-invariant, and hoisted out of the chunk loop
+        // they would hold registers the two wave roles cannot spare
+        int tid_o = (int)threadIdx.x;
+        asm volatile("" : "+v"(tid_o));
+        const int lane = tid_o & 63, r = lane & 31, half = lane >> 5;
         // ---- per-position tables: one block scan of da (log2 units); the
         // wave totals and the local values at tile starts go through LDS
         const float loc = wave_incl_scan(daq * kLog2eS3);
-        if (lane == 63) S.red[wave] = loc;
+        if (lane == 63 && wave < 4) S.red[wave] = loc;
         if ((threadIdx.x & 31) == 0 && threadIdx.x < QF) S.anc[threadIdx.x >> 5] = loc;
         __syncthreads();
         const float cs_end = (S.red[0] + S.red[1]) + (S.red[2] + S.red[3]);
@@ -174,7 +191,7 @@ __global__ __launch_bounds__(256, 1) void ssd3_scan_mfma(Ssd3MfmaParams p) {
         // ---- commit B (row-major) to LDS
 #pragma unroll
         for (int k = 0; k < BPT; ++k) {
-            const int fp = b_fp + 16 * k;
+            const int fp = b_fp + 32 * k;
             *(uint4*)&S.B[2 * fp][b_nv * 8] = bq[k][0];
             *(uint4*)&S.B[2 * fp + 1][b_nv * 8] = bq[k][1];
         }
@@ -182,7 +199,7 @@ __global__ __launch_bounds__(256, 1) void ssd3_scan_mfma(Ssd3MfmaParams p) {
         // ---- commit v^T and w-scaled v^T
 #pragma unroll
         for (int k = 0; k < XPT; ++k) {
-            const int item = threadIdx.x + 256 * k;
+            const int item = threadIdx.x + NT * k;
             if (item < XI) {
                 const int fp = item >> 2, pv = item & 3;
                 const float w0 = S.w[2 * fp], w1 = S.w[2 * fp + 1];
@@ -212,20 +229,19 @@ __global__ __launch_bounds__(256, 1) void ssd3_scan_mfma(Ssd3MfmaParams p) {
         }
         s3_bf16x8_t cfr[NK];
 #pragma unroll
-        for (int kn = 0; kn < NK; ++kn) cfr[kn] = __builtin_bit_cast(s3_bf16x8_t, cn[kn]);
+        for (int kn = 0; kn < NK; ++kn) cfr[kn] = __builtin_bit_cast(s3_bf16x8_t, cn[kn]);  // y waves' only
         // ---- the next chunk's loads land during this chunk's MFMA work
         if (c + 1 < p.nch) fetch(c + 1);
         __syncthreads();
-        // ---- state: h <- exp(cs_end) h + sum_j (w_j v^T[p][j]) B[j][n], n tile = wave
-        {
+        if (st_wave) {
+            // ---- state: h <- exp(cs_end) h + sum_j (w_j v^T[p][j]) B[j][n], n tile = w4
             const float dec = __builtin_amdgcn_exp2f(cs_end);
 #pragma unroll
             for (int v = 0; v < 16; ++v) hacc[v] *= dec;
-            ssd3_state_update(S, hacc, wave, r, half);
-            ssd3_put_state(S, hacc, cur ^ 1, wave, r, half);
-        }
-        // ---- y for output tile = wave
-        {
+            ssd3_state_update(S, hacc, w4, r, half);
+            ssd3_put_state(S, hacc, cur ^ 1, w4, r, half);
+        } else {
+            // ---- y for output tile = wave
             s3_f32x16_t yacc;
             switch (wave) {
                 case 0: ssd3_y_tile<QF, 0>(S, cfr, cur, r, half, yacc); break;
@@ -256,11 +272,12 @@ __global__ __launch_bounds__(256, 1) void ssd3_scan_mfma(Ssd3MfmaParams p) {
         }
         __syncthreads();  // LDS reads of this chunk done before the next commit
     }
+    if (st_wave)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-        const int pp = p0 + 8 * (v >> 2) + 4 * half + (v & 3);
-        p.hT[hbase + pp * N + wave * 32 + r] = hacc[v];
-    }
+        for (int v = 0; v < 16; ++v) {
+            const int pp = p0 + 8 * (v >> 2) + 4 * half + (v & 3);
+            p.hT[hbase + pp * N + w4 * 32 + r] = hacc[v];
+        }
 }
 
 // Fast-path conditions (the caller has validated the arguments).
@@ -294,9 +311,9 @@ int ssd3_mfma_launch(const mamba_ssd3_args* a, hipStream_t stream, hipEvent_t ev
     if (ev0) MAMBA_CHECK_HIP(hipEventRecord(ev0, stream));
     // gamma and scale are NULL only for the double-SSD seam (unit coefficients)
     if (a->gamma == nullptr)
-        hipLaunchKernelGGL((ssd3_scan_mfma<QF, true>), dim3(p.nb * p.H * 2), dim3(256), 0, stream, p);
+        hipLaunchKernelGGL((ssd3_scan_mfma<QF, true>), dim3(p.nb * p.H * 2), dim3(512), 0, stream, p);
     else
-        hipLaunchKernelGGL((ssd3_scan_mfma<QF, false>), dim3(p.nb * p.H * 2), dim3(256), 0, stream, p);
+        hipLaunchKernelGGL((ssd3_scan_mfma<QF, false>), dim3(p.nb * p.H * 2), dim3(512), 0, stream, p);
     MAMBA_CHECK_LAUNCH();
     if (ev1) MAMBA_CHECK_HIP(hipEventRecord(ev1, stream));
     return MAMBA_OK;
