@@ -320,6 +320,40 @@ __global__ __launch_bounds__(512, 1) void mamba3_ssd_fused(M3FusedParams p) {
     fetch_rows(0);
     __builtin_amdgcn_sched_barrier(0);
 
+    // ---- A, on waves 4-5 (fused position tid - 256): coefficients of the
+    // position from the raw columns of chunk cc (kq), SF.dt, and the block scan
+    // of da (the two waves' totals and the tile anchors into LDS); the values
+    // the tables need stay in this thread's registers until phase B
+    float loc_a = 0.f, scq_a = 0.f, gmq_a = 0.f;
+    auto phase_a = [&](int cc, int tid) __attribute__((always_inline)) {
+        const int cf_tl = (tid & (QF - 1)) >> lgM;
+        const bool cf_first = (tid & (M - 1)) == 0;
+        float daq = 0.f, scq = 0.f, gmq = 0.f;
+        const int t = cc * TS + cf_tl;
+        float dt = 0.f;
+        if (t < p.L) {
+            float da, lam;
+            m3_coef(m3f_bf(kq[0]), m3f_bf(kq[1]), m3f_bf(kq[2]), dtb, p.a_floor, p.dt_lo, p.dt_hi, dt, da, lam);
+            float dt1 = 0.f, lam1 = 0.f;  // the next step's (scale's shift); 0 past the end
+            if (t + 1 < p.L) {
+                dt1 = fminf(fmaxf(m3p_softplus(m3f_bf(kq[3]) + dtb), p.dt_lo), p.dt_hi);
+                lam1 = m3_sigmoid(m3f_bf(kq[4]));
+            }
+            gmq = lam * dt;
+            scq = __builtin_fmaf(1.f - lam1, dt1, gmq);
+            daq = cf_first ? da : 0.f;  // da enters the cumulative sum once per step
+        }
+        if (cf_first) SF.dt[cf_tl] = dt;
+        const float loc = wave_incl_scan(daq * kLog2eS3);
+        if ((tid & 63) == 63) S.red[(tid >> 6) - 4] = loc;
+        if ((tid & 31) == 0) S.anc[(tid - 256) >> 5] = loc;
+        loc_a = loc;
+        scq_a = scq;
+        gmq_a = gmq;
+    };
+    if (wv == 4 || wv == 5) phase_a(0, tid_);
+    __syncthreads();
+
     for (int c = 0; c < p.nch; ++c) {
         const int t0 = c * TS;
         // thread coordinates redefined per chunk: LDS addresses derived from them are
@@ -327,8 +361,6 @@ __global__ __launch_bounds__(512, 1) void mamba3_ssd_fused(M3FusedParams p) {
         int tid = tid_;
         asm volatile("" : "+v"(tid));
         const int lane = tid & 63, r = lane & 31, half = lane >> 5;
-        const int cf_tl = (tid & (QF - 1)) >> lgM;
-        const bool cf_first = (tid & (M - 1)) == 0;
         const int ang_a = tid >> 3, ang_q = tid & 7;
         const int b_fp = tid >> 4, b_nv = tid & 15;
         const int bm0 = (2 * b_fp) & (M - 1);
@@ -338,44 +370,24 @@ __global__ __launch_bounds__(512, 1) void mamba3_ssd_fused(M3FusedParams p) {
         // the y tiles of the previous chunk have read it before the last barrier,
         // this chunk's read it after the next one)
         if (c > 0 && wv >= 4) ssd3_put_state(S, hacc, 0, w4, r, half);
-        // ---- A: coefficients of this thread's position; the block scan of da
-        float daq = 0.f, scq = 0.f, gmq = 0.f;
-        if (tid < QF) {
-            const int t = t0 + cf_tl;
-            float dt = 0.f;
-            if (t < p.L) {
-                float da, lam;
-                m3_coef(m3f_bf(kq[0]), m3f_bf(kq[1]), m3f_bf(kq[2]), dtb, p.a_floor, p.dt_lo, p.dt_hi, dt, da, lam);
-                float dt1 = 0.f, lam1 = 0.f;  // the next step's (scale's shift); 0 past the end
-                if (t + 1 < p.L) {
-                    dt1 = fminf(fmaxf(m3p_softplus(m3f_bf(kq[3]) + dtb), p.dt_lo), p.dt_hi);
-                    lam1 = m3_sigmoid(m3f_bf(kq[4]));
-                }
-                gmq = lam * dt;
-                scq = __builtin_fmaf(1.f - lam1, dt1, gmq);
-                daq = cf_first ? da : 0.f;  // da enters the cumulative sum once per step
-            }
-            if (cf_first) SF.dt[cf_tl] = dt;
-        }
-        const float loc = wave_incl_scan(daq * kLog2eS3);  // waves 0 and 1 hold the chunk's positions
-        if (lane == 63 && wv < 2) S.red[wv] = loc;
-        if ((tid & 31) == 0 && tid < QF) S.anc[tid >> 5] = loc;
-        __syncthreads();
-        // ---- B: per-position tables; angles and their cos / sin
+        // ---- A ran for this chunk on waves 4-5 during the previous chunk's
+        // MFMA phase (phase_a below; before the loop for chunk 0)
+        // ---- B: per-position tables (waves 4-5, whose registers hold phase
+        // A's values); angles and their cos / sin
         const float cs_end = S.red[0] + S.red[1];
-        if (tid < QF) {
-            const int j = tid;
-            const float csj = loc + (wv == 1 ? S.red[0] : 0.f);
+        if (wv == 4 || wv == 5) {
+            const int j = tid - 256;
+            const float csj = loc_a + (wv == 5 ? S.red[0] : 0.f);
             S.cs2[j] = csj;
             S.st[j] = (float)(j >> lgM);
-            S.sc[j] = scq;
-            S.gm[j] = gmq;
-            S.w[j] = scq * __builtin_amdgcn_exp2f(cs_end - csj);
+            S.sc[j] = scq_a;
+            S.gm[j] = gmq_a;
+            S.w[j] = scq_a * __builtin_amdgcn_exp2f(cs_end - csj);
 #pragma unroll
             for (int it = 1; it < 4; ++it) {
                 if (j < it * 32) {
                     const float anchor = S.anc[it] + (it >= 2 ? S.red[0] : 0.f);
-                    S.f[it - 1][j] = scq * __builtin_amdgcn_exp2f(anchor - csj);
+                    S.f[it - 1][j] = scq_a * __builtin_amdgcn_exp2f(anchor - csj);
                 }
             }
         }
@@ -539,6 +551,9 @@ __global__ __launch_bounds__(512, 1) void mamba3_ssd_fused(M3FusedParams p) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) hacc[v] *= dec;
             ssd3_state_update(S, hacc, w4, r, half);
+            // ---- A of the next chunk (its raw columns were fetched in phase C;
+            // SF.dt, S.red and S.anc were last read in this chunk's phase B)
+            if ((wv == 4 || wv == 5) && c + 1 < p.nch) phase_a(c + 1, tid);
         } else {
             // ---- D (waves 0-3): y for output tile = wave, plus D v
             s3_bf16x8_t cfr[8];
