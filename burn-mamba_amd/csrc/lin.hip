@@ -37,7 +37,7 @@ __device__ __forceinline__ lin_f32x16_t lin_mfma(lin_bf16x8_t a, lin_bf16x8_t b,
 #define MAMBA_LIN_NW_BIGM 8     // waves per workgroup for four or eight 32-row tiles
 #endif
 #ifndef MAMBA_LIN_U1
-#define MAMBA_LIN_U1 3          // k-steps per pipeline stage for one 32-row tile
+#define MAMBA_LIN_U1 0          // k-steps per pipeline stage for one 32-row tile (0: lin_depth1)
 #endif
 #ifndef MAMBA_LIN_U2
 #define MAMBA_LIN_U2 3          // k-steps per pipeline stage for two 32-row tiles
@@ -49,12 +49,15 @@ __device__ __forceinline__ lin_f32x16_t lin_mfma(lin_bf16x8_t a, lin_bf16x8_t b,
 #define MAMBA_LIN_ROTATE 0      // 1: each workgroup starts its k walk at a different stage
 #endif
 
-template <int MT>
+// One pipeline stage: U k-steps of weight and activation blocks.
+template <int MT, int U>
 struct LinStage {
-    static constexpr int U = MT == 1 ? MAMBA_LIN_U1 : MT == 2 ? MAMBA_LIN_U2 : MT == 4 ? 2 : 1;  // k-steps per stage
     lin_bf16x8_t w[U];
     lin_bf16x8_t a[U][MT];
 };
+// k-steps per stage for two or more 32-row tiles (their operands fill the registers)
+template <int MT>
+constexpr int lin_depth_fixed() { return MT == 2 ? MAMBA_LIN_U2 : MT == 4 ? 2 : 1; }
 
 // Operand blocks through buffer resources (scalar base, 32-bit byte offsets):
 // a load's address costs no 64-bit VGPR pair, which keeps the wave within the
@@ -84,28 +87,35 @@ struct LinAct {
     }
 };
 
-template <int MT, bool RM>
-__device__ __forceinline__ void lin_load(LinStage<MT>& st, __amdgpu_buffer_rsrc_t rw, __amdgpu_buffer_rsrc_t ra,
-                                         uint32_t lo, const LinAct<MT, RM>& ao, int s) {
+// A byte offset past every operand's extent: the load reads zero.
+constexpr uint32_t kLinOut = 0x80000000u;
+
+// One stage: k-steps s .. s + U - 1; those at or past s1 (the wave's end, in a
+// last partial stage) read zero weights and activations, so they add nothing
+// and every k-step of the wave is software-pipelined whatever U divides.
+template <int MT, int U, bool RM>
+__device__ __forceinline__ void lin_load(LinStage<MT, U>& st, __amdgpu_buffer_rsrc_t rw, __amdgpu_buffer_rsrc_t ra,
+                                         uint32_t lo, const LinAct<MT, RM>& ao, int s, int s1) {
 #pragma unroll
-    for (int u = 0; u < LinStage<MT>::U; ++u) {
-        st.w[u] = lin_ld(rw, (uint32_t)(s + u) * 1024u + lo);
+    for (int u = 0; u < U; ++u) {
+        const bool ok = s + u < s1;
+        st.w[u] = lin_ld(rw, ok ? (uint32_t)(s + u) * 1024u + lo : kLinOut);
 #pragma unroll
-        for (int i = 0; i < MT; ++i) st.a[u][i] = lin_ld(ra, ao.off(s + u, i));
+        for (int i = 0; i < MT; ++i) st.a[u][i] = lin_ld(ra, ok ? ao.off(s + u, i) : kLinOut);
     }
 }
 
-template <int MT>
-__device__ __forceinline__ void lin_compute(const LinStage<MT>& st, lin_f32x16_t (&acc)[MT]) {
+template <int MT, int U>
+__device__ __forceinline__ void lin_compute(const LinStage<MT, U>& st, lin_f32x16_t (&acc)[MT]) {
 #pragma unroll
-    for (int u = 0; u < LinStage<MT>::U; ++u)
+    for (int u = 0; u < U; ++u)
 #pragma unroll
         for (int i = 0; i < MT; ++i) acc[i] = lin_mfma(st.a[u][i], st.w[u], acc[i]);
 }
 
 // grid: (ceil(N / 32), S) workgroups of NW waves.  RM: the activation is
-// p.X (row-major bf16) instead of the packed p.A.
-template <int MT, int NW, int EPI, bool RM = false>
+// p.X (row-major bf16) instead of the packed p.A.  U: k-steps per stage.
+template <int MT, int NW, int EPI, bool RM, int U>
 __global__ __launch_bounds__(64 * NW) void lin_stream(LinParams p) {
     constexpr int RT = (MT < 2 || NW >= 16) ? 1 : 2;  // 32-row tiles reduced per LDS round
     __shared__ float s_red[NW][RT][16][64];
@@ -127,32 +137,24 @@ __global__ __launch_bounds__(64 * NW) void lin_stream(LinParams p) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[i][v] = 0.f;
 
-    constexpr int U = LinStage<MT>::U;
-    const int nstage = (s1 - s0) / U;
-    int s = s0;
+    const int nstage = (s1 - s0 + U - 1) / U;  // the last stage may be partial
     if (nstage > 0) {
         // stage st covers k-steps s0 + U * ((st + rot) % nstage) .. + U - 1: with
         // rot varying over workgroups, concurrent waves read different blocks of
         // the (shared, L2-resident) activation instead of the same one
         const int rot = MAMBA_LIN_ROTATE ? (int)(blockIdx.x % (unsigned)nstage) : 0;
         auto kstep = [&](int st) { int q = st + rot; q -= q >= nstage ? nstage : 0; return s0 + U * q; };
-        LinStage<MT> sa, sb;
-        lin_load<MT, RM>(sa, rw, ra, lo, ao, kstep(0));
+        LinStage<MT, U> sa, sb;
+        lin_load<MT, U, RM>(sa, rw, ra, lo, ao, kstep(0), s1);
         for (int st = 0; st < nstage; st += 2) {
             const bool more1 = st + 1 < nstage;
-            if (more1) lin_load<MT, RM>(sb, rw, ra, lo, ao, kstep(st + 1));
-            lin_compute<MT>(sa, acc);
+            if (more1) lin_load<MT, U, RM>(sb, rw, ra, lo, ao, kstep(st + 1), s1);
+            lin_compute<MT, U>(sa, acc);
             if (more1) {
-                if (st + 2 < nstage) lin_load<MT, RM>(sa, rw, ra, lo, ao, kstep(st + 2));
-                lin_compute<MT>(sb, acc);
+                if (st + 2 < nstage) lin_load<MT, U, RM>(sa, rw, ra, lo, ao, kstep(st + 2), s1);
+                lin_compute<MT, U>(sb, acc);
             }
         }
-        s = s0 + nstage * U;
-    }
-    for (; s < s1; ++s) {
-        const lin_bf16x8_t w = lin_ld(rw, (uint32_t)s * 1024u + lo);
-#pragma unroll
-        for (int i = 0; i < MT; ++i) acc[i] = lin_mfma(lin_ld(ra, ao.off(s, i)), w, acc[i]);
     }
 
     // cross-wave reduction through LDS, RT 32-row tiles at a time
@@ -187,11 +189,47 @@ __global__ __launch_bounds__(64 * NW) void lin_stream(LinParams p) {
     }
 }
 
+template <int MT, int NW, bool RM, int U>
+static void lin_launch_u(const LinParams& p, int epi, hipStream_t stream) {
+    const dim3 grid((p.N + 31) / 32, p.S);
+    if (epi == LIN_STORE) hipLaunchKernelGGL((lin_stream<MT, NW, LIN_STORE, RM, U>), grid, dim3(64 * NW), 0, stream, p);
+    else hipLaunchKernelGGL((lin_stream<MT, NW, LIN_PARTIAL, RM, U>), grid, dim3(64 * NW), 0, stream, p);
+}
+
+// Stage depth for one 32-row tile, from kw, the most k-steps a wave walks:
+// at least two stages (one would leave nothing to overlap), as few masked
+// k-steps in the last stage as possible, and of those the deepest stage (the
+// most weight bytes in flight per wave).  At a fixed depth of 3 a wave's walk
+// of 8 k-steps ran its last two outside the pipeline; chosen this way (depth 4
+// for walks of 8, 5 for walks of 10 and 20) the 64-layer decode steps went
+// 3.36 -> 3.07 ms (Mamba-3, batch 64), 1.38 -> 1.30 ms (batch 1) and 5.87 ->
+// 5.78 ms (Mamba-2, batch 64), 3.03 -> 2.97 ms (batch 16).
+static int lin_depth1(int kw) {
+    if (MAMBA_LIN_U1) return MAMBA_LIN_U1;
+    int best = 3, waste = 1 << 30;
+    for (int u = 5; u >= 3; --u) {
+        const int ns = (kw + u - 1) / u;
+        if (ns < 2) continue;
+        if (ns * u - kw < waste) {
+            waste = ns * u - kw;
+            best = u;
+        }
+    }
+    return best;
+}
+
 template <int MT, int NW, bool RM>
 static void lin_launch_nw(const LinParams& p, int epi, hipStream_t stream) {
-    const dim3 grid((p.N + 31) / 32, p.S);
-    if (epi == LIN_STORE) hipLaunchKernelGGL((lin_stream<MT, NW, LIN_STORE, RM>), grid, dim3(64 * NW), 0, stream, p);
-    else hipLaunchKernelGGL((lin_stream<MT, NW, LIN_PARTIAL, RM>), grid, dim3(64 * NW), 0, stream, p);
+    if constexpr (MT == 1) {
+        const int ks = p.K >> 4, kz = (ks + p.S - 1) / p.S, kw = (kz + NW - 1) / NW;
+        switch (lin_depth1(kw)) {
+            case 5: lin_launch_u<1, NW, RM, 5>(p, epi, stream); return;
+            case 4: lin_launch_u<1, NW, RM, 4>(p, epi, stream); return;
+            default: lin_launch_u<1, NW, RM, 3>(p, epi, stream); return;
+        }
+    } else {
+        lin_launch_u<MT, NW, RM, lin_depth_fixed<MT>()>(p, epi, stream);
+    }
 }
 
 template <int MT>
