@@ -39,8 +39,14 @@ __device__ __forceinline__ lin_f32x16_t lin_mfma(lin_bf16x8_t a, lin_bf16x8_t b,
 #ifndef MAMBA_LIN_U1
 #define MAMBA_LIN_U1 0          // k-steps per pipeline stage for one 32-row tile (0: lin_depth1)
 #endif
+#ifndef MAMBA_LIN_UMAX
+#define MAMBA_LIN_UMAX 5        // deepest stage lin_depth1 picks (5, 6 or 8)
+#endif
 #ifndef MAMBA_LIN_U2
-#define MAMBA_LIN_U2 3          // k-steps per pipeline stage for two 32-row tiles
+#define MAMBA_LIN_U2 0          // k-steps per pipeline stage for two 32-row tiles (0: lin_depth)
+#endif
+#ifndef MAMBA_LIN_UMAX2
+#define MAMBA_LIN_UMAX2 3       // deepest stage lin_depth picks for two 32-row tiles (3 or 4)
 #endif
 #ifndef MAMBA_LIN_NT
 #define MAMBA_LIN_NT 0          // 1: weight loads carry the non-temporal hint (read once)
@@ -55,9 +61,9 @@ struct LinStage {
     lin_bf16x8_t w[U];
     lin_bf16x8_t a[U][MT];
 };
-// k-steps per stage for two or more 32-row tiles (their operands fill the registers)
+// k-steps per stage for four or eight 32-row tiles (their operands fill the registers)
 template <int MT>
-constexpr int lin_depth_fixed() { return MT == 2 ? MAMBA_LIN_U2 : MT == 4 ? 2 : 1; }
+constexpr int lin_depth_fixed() { return MT == 4 ? 2 : 1; }
 
 // Operand blocks through buffer resources (scalar base, 32-bit byte offsets):
 // a load's address costs no 64-bit VGPR pair, which keeps the wave within the
@@ -196,18 +202,17 @@ static void lin_launch_u(const LinParams& p, int epi, hipStream_t stream) {
     else hipLaunchKernelGGL((lin_stream<MT, NW, LIN_PARTIAL, RM, U>), grid, dim3(64 * NW), 0, stream, p);
 }
 
-// Stage depth for one 32-row tile, from kw, the most k-steps a wave walks:
-// at least two stages (one would leave nothing to overlap), as few masked
-// k-steps in the last stage as possible, and of those the deepest stage (the
-// most weight bytes in flight per wave).  At a fixed depth of 3 a wave's walk
-// of 8 k-steps ran its last two outside the pipeline; chosen this way (depth 4
-// for walks of 8, 5 for walks of 10 and 20) the 64-layer decode steps went
-// 3.36 -> 3.07 ms (Mamba-3, batch 64), 1.38 -> 1.30 ms (batch 1) and 5.87 ->
-// 5.78 ms (Mamba-2, batch 64), 3.03 -> 2.97 ms (batch 16).
-static int lin_depth1(int kw) {
-    if (MAMBA_LIN_U1) return MAMBA_LIN_U1;
-    int best = 3, waste = 1 << 30;
-    for (int u = 5; u >= 3; --u) {
+// Stage depth from kw, the most k-steps a wave walks: at least two stages (one
+// would leave nothing to overlap), as few masked k-steps in the last stage as
+// possible, and of those the deepest stage in [umin, umax] (the most weight
+// bytes in flight per wave).  At a fixed depth of 3 a wave's walk of 8
+// k-steps ran its last two outside the pipeline; chosen this way (depth 4 for
+// walks of 8, 5 for walks of 10 and 20) the 64-layer decode steps went 3.36 ->
+// 3.07 ms (Mamba-3, batch 64), 1.38 -> 1.30 ms (batch 1) and 5.87 -> 5.78 ms
+// (Mamba-2, batch 64), 3.03 -> 2.97 ms (batch 16).
+static int lin_depth(int kw, int umax, int umin) {
+    int best = umin, waste = 1 << 30;
+    for (int u = umax; u >= umin; --u) {
         const int ns = (kw + u - 1) / u;
         if (ns < 2) continue;
         if (ns * u - kw < waste) {
@@ -220,12 +225,33 @@ static int lin_depth1(int kw) {
 
 template <int MT, int NW, bool RM>
 static void lin_launch_nw(const LinParams& p, int epi, hipStream_t stream) {
+    const int ks = p.K >> 4, kz = (ks + p.S - 1) / p.S, kw = (kz + NW - 1) / NW;
     if constexpr (MT == 1) {
-        const int ks = p.K >> 4, kz = (ks + p.S - 1) / p.S, kw = (kz + NW - 1) / NW;
-        switch (lin_depth1(kw)) {
+        // 16 waves (at most 128 registers each) hold stages of up to 6 k-steps
+        const int u = MAMBA_LIN_U1 ? MAMBA_LIN_U1 : lin_depth(kw, NW >= 16 ? std::min(MAMBA_LIN_UMAX, 6) : MAMBA_LIN_UMAX, 3);
+        switch (u) {
+#if MAMBA_LIN_UMAX >= 8
+            case 8: if constexpr (NW < 16) { lin_launch_u<1, NW, RM, 8>(p, epi, stream); return; }
+            [[fallthrough]];
+            case 7: if constexpr (NW < 16) { lin_launch_u<1, NW, RM, 7>(p, epi, stream); return; }
+            [[fallthrough]];
+#endif
+#if MAMBA_LIN_UMAX >= 6
+            case 6: lin_launch_u<1, NW, RM, 6>(p, epi, stream); return;
+#endif
             case 5: lin_launch_u<1, NW, RM, 5>(p, epi, stream); return;
             case 4: lin_launch_u<1, NW, RM, 4>(p, epi, stream); return;
             default: lin_launch_u<1, NW, RM, 3>(p, epi, stream); return;
+        }
+    } else if constexpr (MT == 2) {
+        const int u = MAMBA_LIN_U2 ? MAMBA_LIN_U2 : lin_depth(kw, NW >= 16 ? 3 : MAMBA_LIN_UMAX2, 2);
+        switch (u) {
+#if MAMBA_LIN_UMAX2 >= 4
+            case 4: if constexpr (NW < 16) { lin_launch_u<2, NW, RM, 4>(p, epi, stream); return; }
+            [[fallthrough]];
+#endif
+            case 3: lin_launch_u<2, NW, RM, 3>(p, epi, stream); return;
+            default: lin_launch_u<2, NW, RM, 2>(p, epi, stream); return;
         }
     } else {
         lin_launch_u<MT, NW, RM, lin_depth_fixed<MT>()>(p, epi, stream);
