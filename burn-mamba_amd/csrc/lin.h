@@ -40,6 +40,12 @@ struct LinParams {
     // bytes, so no packing pass is needed
     const bf16_t* X; int64_t x_ld;
     int NW;                  // waves per workgroup (0: the default for MT)
+    // column parts per 32-column tile (0 or 1: one; 2 or 4): CS workgroups
+    // share a tile, each loading only its 32 / CS columns' lanes of every
+    // weight block (the other lanes read zero) and storing only its columns,
+    // so a product with few column tiles streams from CS times the
+    // workgroups without a summing pass
+    int CS;
     // LIN_STORE (S == 1): out[m, n] = acc + bias
     const float* bias;       // [N] or NULL
     void* out; int64_t out_ld; bool out_bf16;

@@ -99,6 +99,8 @@ constexpr uint32_t kLinOut = 0x80000000u;
 // One stage: k-steps s .. s + U - 1; those at or past s1 (the wave's end, in a
 // last partial stage) read zero weights and activations, so they add nothing
 // and every k-step of the wave is software-pipelined whatever U divides.
+// `lo` is the lane's byte offset inside a weight block, or kLinOut for a lane
+// whose column belongs to another column part (it then reads zero weights).
 template <int MT, int U, bool RM>
 __device__ __forceinline__ void lin_load(LinStage<MT, U>& st, __amdgpu_buffer_rsrc_t rw, __amdgpu_buffer_rsrc_t ra,
                                          uint32_t lo, const LinAct<MT, RM>& ao, int s, int s1) {
@@ -125,7 +127,9 @@ template <int MT, int NW, int EPI, bool RM, int U>
 __global__ __launch_bounds__(64 * NW) void lin_stream(LinParams p) {
     constexpr int RT = (MT < 2 || NW >= 16) ? 1 : 2;  // 32-row tiles reduced per LDS round
     __shared__ float s_red[NW][RT][16][64];
-    const int j = blockIdx.x, z = blockIdx.y;
+    const int cs = p.CS > 1 ? p.CS : 1;
+    const int j = blockIdx.x / cs, z = blockIdx.y;
+    const int cw = 32 / cs, c0 = (blockIdx.x % cs) * cw;  // this workgroup's columns 32 j + c0 ..
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int KS = p.K >> 4;
     const int z0 = (KS * z) / p.S, z1 = (KS * (z + 1)) / p.S;
@@ -136,7 +140,10 @@ __global__ __launch_bounds__(64 * NW) void lin_stream(LinParams p) {
     const __amdgpu_buffer_rsrc_t ra = RM ? buf_rsrc(p.X, (uint32_t)((int64_t)p.M * p.x_ld * 2))
                                          : buf_rsrc(p.A, (uint32_t)KS * MT * 1024u);
     const LinAct<MT, RM> ao(lane, p.x_ld);
-    const uint32_t lo = (uint32_t)lane * 16u;
+    const int lcol = lane & 31;
+    uint32_t lo = (uint32_t)lane * 16u;
+    lo = (lcol >= c0 && lcol < c0 + cw) ? lo : kLinOut;
+    asm volatile("" : "+v"(lo));  // one select, not a branch around every load
     lin_f32x16_t acc[MT];
 #pragma unroll
     for (int i = 0; i < MT; ++i)
@@ -177,7 +184,7 @@ __global__ __launch_bounds__(64 * NW) void lin_stream(LinParams p) {
             if (ig + t2 >= MT) break;
             const int m = 32 * (ig + t2) + 8 * (v >> 2) + 4 * (ln >> 5) + (v & 3);
             const int n = 32 * j + (ln & 31);
-            if (m >= p.M || n >= p.N) continue;
+            if (m >= p.M || n >= p.N || (ln & 31) < c0 || (ln & 31) >= c0 + cw) continue;
             float sum = 0.f;
 #pragma unroll
             for (int w = 0; w < NW; ++w) sum += s_red[w][t2][v][ln];
@@ -197,7 +204,7 @@ __global__ __launch_bounds__(64 * NW) void lin_stream(LinParams p) {
 
 template <int MT, int NW, bool RM, int U>
 static void lin_launch_u(const LinParams& p, int epi, hipStream_t stream) {
-    const dim3 grid((p.N + 31) / 32, p.S);
+    const dim3 grid(((p.N + 31) / 32) * (p.CS > 1 ? p.CS : 1), p.S);
     if (epi == LIN_STORE) hipLaunchKernelGGL((lin_stream<MT, NW, LIN_STORE, RM, U>), grid, dim3(64 * NW), 0, stream, p);
     else hipLaunchKernelGGL((lin_stream<MT, NW, LIN_PARTIAL, RM, U>), grid, dim3(64 * NW), 0, stream, p);
 }
@@ -413,9 +420,12 @@ __global__ __launch_bounds__(256) void lin_reduce_kernel(const float* part, int 
 #ifndef MAMBA_LINFWD_MIN_WAVES
 #define MAMBA_LINFWD_MIN_WAVES 1024
 #endif
+#ifndef MAMBA_LINFWD_MAX_CS
+#define MAMBA_LINFWD_MAX_CS 4
+#endif
 struct LinPlan {
     bool rm;  // x read in place
-    int S, NW;
+    int S, NW, CS;
 };
 
 static LinPlan linear_plan(const mamba_linear_args* a) {
@@ -429,9 +439,15 @@ static LinPlan linear_plan(const mamba_linear_args* a) {
         int nw = 4;
         while (nw < nw_max && tiles * nw < MAMBA_LINFWD_MIN_WAVES && ks / (2 * nw) >= 3) nw *= 2;
         pl.NW = nw;
+        // few column tiles even at the widest workgroups (out_proj, d_out =
+        // d_model): column parts, still one pass and no partial planes
+        int cs = 1;
+        while (cs < MAMBA_LINFWD_MAX_CS && tiles * nw * cs < MAMBA_LINFWD_MIN_WAVES) cs *= 2;
+        pl.CS = cs;
     } else {
         pl.S = lin_splits(a->rows, a->d_in, a->d_out);
         pl.NW = 0;
+        pl.CS = 1;
     }
     return pl;
 }
@@ -470,7 +486,7 @@ extern "C" int mamba_linear_fwd(const mamba_linear_args* a, void* ws, size_t ws_
     hipStream_t s = (hipStream_t)stream;
     const LinPlan pl = linear_plan(a);
     LinParams p = {};
-    p.M = a->rows; p.N = a->d_out; p.K = a->d_in; p.MT = mt; p.S = pl.S; p.NW = pl.NW;
+    p.M = a->rows; p.N = a->d_out; p.K = a->d_in; p.MT = mt; p.S = pl.S; p.NW = pl.NW; p.CS = pl.CS;
     p.W = static_cast<const lin_bf16x8_t*>(a->packed_w);
     if (pl.rm) {
         p.X = static_cast<const bf16_t*>(a->x);
