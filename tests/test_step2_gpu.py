@@ -297,9 +297,11 @@ def test_step_invalid_args_raise():
 LIN_CASES = [
     # (rows, d_in, d_out, x dtype, y dtype, bias[, extra columns of x's row stride])
     # bf16 x with 16-byte aligned rows is read in place, anything else packed first;
-    # weights up to 16 MB take one k-split with 4 / 8 / 16 waves per workgroup
-    (1, 256, 1000, "f32", "f32", False),     # MT 1, 4 waves, tail loop only, ragged last tile
-    (3, 1024, 96, "bf16", "f32", True),      # MT 1, in place, 16 waves, two pipeline stages per wave
+    # weights up to 16 MB take one k-split with 4 / 8 / 16 waves per workgroup, and
+    # 2 or 4 column parts per 32-column tile when the tiles are few
+    (1, 256, 1000, "f32", "f32", False),     # MT 1, 4 waves, masked last stage, ragged last tile, 4 parts
+    (3, 1024, 96, "bf16", "f32", True),      # MT 1, in place, 16 waves, two pipeline stages per wave, 4 parts
+    (32, 2048, 1024, "bf16", "bf16", True),  # the Mamba-3 half-batch out_proj: 32 tiles x 16 waves x 2 parts
     (40, 512, 320, "bf16", "bf16", False),   # MT 2, in place: rows 40..63 read past x's end (zero)
     (100, 2048, 64, "f32", "f32", True),     # MT 4
     (200, 4096, 200, "bf16", "f32", False),  # MT 8, in place, 8 waves per workgroup
