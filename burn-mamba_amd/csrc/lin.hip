@@ -11,9 +11,12 @@
 //     L2: it is small and shared by every workgroup);
 //   * one workgroup owns one 32-column tile over a 1/S slice of K (grid.y =
 //     S); its NW waves split that slice again, each software-pipelines its
-//     loads two stages deep, and the wave accumulators are reduced through
-//     LDS.  Small slices on many workgroups (~1300) is what streams a weight
-//     at full HBM rate (a workgroup's ramp-up and tail are then short);
+//     loads two stages deep (stages of U k-steps, U chosen per launch from
+//     the walk length, a last partial stage reading zero past the walk), and
+//     the wave accumulators are reduced through LDS.  Small slices on many
+//     workgroups (~1300) is what streams a weight at full HBM rate (a
+//     workgroup's ramp-up and tail are then short); a product with few
+//     column tiles may also split each tile into column parts (LinParams::CS);
 //   * epilogues: plain store (+bias) when S = 1, else one f32 partial plane
 //     per k-slice, summed in a fixed order by the consumer (deterministic, no
 //     atomics).
