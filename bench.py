@@ -565,15 +565,17 @@ def bench_mamba3_step(args):
                                                        mimo_o=m.mimo_o, out=ys))
         return lo, hi, projs, ys, xs, ws, argl
 
-    # the host schedule of Mamba2Stack: an even batch of 34 to 256 rows steps
-    # as two half batches on two streams, one half's weight-streaming products
-    # beside the other half's state kernel (rows never interact; each half
-    # reads the weights once).  Per-layer kernel events time the one-stream
-    # whole-batch step.
-    split = not getattr(args, "no_split", False) and 34 <= b <= 256 and b % 2 == 0
+    # the host schedule of Mamba3Stack: a batch of 34 to 256 rows steps as row
+    # parts of at most 32 rows on up to four streams (batch_parts), one part's
+    # weight-streaming products beside another part's state kernel (rows never
+    # interact; each part reads the weights once).  Per-layer kernel events
+    # time the one-stream whole-batch step.
+    K = 1 if getattr(args, "no_split", False) else mamba_hip.batch_parts(b, mamba_hip.Mamba3Stack.max_parts)
+    split = K > 1
     whole = rows(0, b)
-    halves = [rows(0, b // 2), rows(b // 2, b)] if split else None
-    streams = [torch.cuda.Stream(), torch.cuda.Stream()] if split else None
+    bounds = [(b * k) // K for k in range(K + 1)]
+    halves = [rows(bounds[k], bounds[k + 1]) for k in range(K)] if split else None
+    streams = [torch.cuda.Stream() for _ in range(K)] if split else None
 
     def run(part, events=None):
         lo, hi, projs, ys, xs, ws, argl = part
@@ -650,7 +652,7 @@ def bench_mamba3_step(args):
         "config": {"workload": "mamba3_decode_step", **cfg, "batch": b, "graph": "hip graph of the 64-layer step",
                    "step_bytes": step_bytes, "step_hbm_gbs": step_bytes / (ms_per_step * 1e-3) / 1e9,
                    "entry": "mamba_linear_fwd in_proj + mamba3_step_ssm + mamba_linear_fwd out_proj per layer",
-                   "schedule": "two half batches on two streams" if split else "one stream",
+                   "schedule": f"{K} row parts on {K} streams" if split else "one stream",
                    "layers": "Mamba3Stack: pre-norm residual layers (rmsnorm + block per layer)"
                    if getattr(args, "m3_stack", False) else "blocks (each reads the same input row)"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -1268,7 +1270,7 @@ def bench_decode(args):
                    "step_bytes": step_bytes, "step_hbm_gbs": step_gbs, "step_hbm_frac": step_gbs / HBM_PEAK_GBS,
                    "entry": ("mamba2_layer_step per layer (packed products, fused norm/residual)" if stack.fused
                              else "mamba_rmsnorm + torch.mm + mamba2_step_ssm + torch.mm per layer"),
-                   "schedule": ("two half batches on two streams" if stack.splits(b)
+                   "schedule": (f"{stack.parts(b)} row parts on {stack.parts(b)} streams" if stack.splits(b)
                                 else "one stream")},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel_ms": kern_ms,
@@ -1601,7 +1603,7 @@ def main():
     ap.add_argument("--batch", type=int, default=DECODE_CFG3["batch"], help="decode batch")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-split", action="store_true",
-                    help="decode / mamba3_step: step the whole batch on one stream (no half-batch schedule), "
+                    help="decode / mamba3_step: step the whole batch on one stream (no row-part schedule), "
                          "so that every state-kernel dispatch of a kernel trace covers the full batch")
     ap.add_argument("--m3-stack", action="store_true",
                     help="mamba3_step: step the library's Mamba3Stack (pre-norm residual layers) instead of "

@@ -13,7 +13,7 @@ from .ssd import ssd2_autograd, ssd2_bwd  # noqa: F401
 from .step import (Mamba2, Mamba2Cache, Mamba2Config, Mamba2Layer, Mamba2Stack, linear, pack_linear,  # noqa: F401
                    rmsnorm, step_ssm, step_ssm_args)
 from .step import conv_fwd as mamba2_conv_fwd, div_eps, gated_rmsnorm as mamba2_gated_rmsnorm  # noqa: F401
-from .step import drop_derived, packed_weight, prefill_mm, step_mm, step_mm_ok  # noqa: F401
+from .step import batch_parts, drop_derived, packed_weight, prefill_mm, step_mm, step_mm_ok  # noqa: F401
 from .ssd3 import (Mamba3DoubleSsdInput, Mamba3SingleSsdInput, ssd3_double_fast_path, ssd3_double_fwd,  # noqa: F401
                    ssd3_autograd, ssd3_bwd, ssd3_fast_path, ssd3_fwd)
 from .mamba3 import Mamba3, Mamba3Cache, Mamba3Config, Mamba3Layer, Mamba3Stack  # noqa: F401

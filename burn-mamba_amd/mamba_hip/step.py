@@ -292,6 +292,19 @@ def prefill_mm_rows(x2d: torch.Tensor, w: torch.Tensor, align: int = 8) -> torch
     return torch.mm(x2d, wt.t())[:, :d_out]
 
 
+def batch_parts(b: int, max_parts: int) -> int:
+    """Row parts of the batch-split decode schedule for a batch of ``b`` rows:
+    1 (one stream) below 34 rows or above 256, else ceil(b / 32) parts (at
+    most 32 rows each, one MFMA row tile of the weight-streaming products), at
+    least 2 and at most ``max_parts``.  Parts are independent row ranges of
+    the batch stepped on their own streams: one part's latency-bound products
+    overlap another's bandwidth-bound state kernel, and every part reads the
+    weights once, which is what ``max_parts`` trades against."""
+    if not 34 <= b <= 256:
+        return 1
+    return max(2, min(max_parts, -(-b // 32)))
+
+
 def step_mm(x2d: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = None,
             workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
     """x2d [rows, d_in] @ w [d_in, d_out] for decode-sized rows (<= 256) through
@@ -509,12 +522,13 @@ class Mamba2Stack:
     RmsNorm of layer l+1 (one mamba_rmsnorm call) around torch.mm products and
     mamba2_step_ssm.  All activations live in buffers allocated once per batch
     size, so ``step_`` allocates nothing and can be captured in a HIP graph.
-    With ``split_batch`` (the default), a fused step of an even batch of 34 to
-    256 rows runs as two half batches on two streams: the rows never interact,
-    and one half's weight-streaming products overlap the other half's state
-    kernel (each half reads the weights once).  From 34 rows on, one stream
-    would run the products on two 32-row tiles while the halves run on one
-    each; at 32 rows and below the schedule measured slower."""
+    With ``split_batch`` (the default), a fused step of a batch of 34 to 256
+    rows runs as two row parts (halves) on two streams (``parts``,
+    ``batch_parts``): the rows never interact, and one half's weight-streaming
+    products overlap the other half's state kernel (each half reads the
+    weights once).  From 34 rows on, one stream would run the products on two
+    32-row tiles while the halves run on one each; at 32 rows and below the
+    schedule measured slower."""
 
     def __init__(self, layers: List[Mamba2Layer], fused: bool = True, split_batch: bool = True):
         assert layers
@@ -523,7 +537,7 @@ class Mamba2Stack:
         self._bufs = {}
         self._args = {}
         self.split_batch = split_batch
-        self._side = None  # the two streams of the half-batch schedule, made on first use
+        self._side = None  # the streams of the batch-split schedule, made on first use
         c = self.cfg
         self.fused = fused and c.per_head_dim == 64 and c.state_rank in (64, 128) and c.conv_kernel == 4 \
             and c.d_model % 16 == 0 and c.d_model <= 4096 and c.nheads <= 256
@@ -597,9 +611,20 @@ class Mamba2Stack:
             self._bufs[key] = bufs
         return self._bufs[key]
 
+    # Streams of the batch-split schedule.  Each part reads every layer's
+    # weights once, and this stack's weights are large next to its caches:
+    # at 96 / 128 rows three or four parts measured 8.09 -> 8.32 ms and
+    # 9.99 -> 10.77 ms per 64-layer step against two, at 256 rows four tied
+    # with two and eight lost.
+    max_parts = 2
+
+    def parts(self, b: int) -> int:
+        """Row parts of an untimed step of batch ``b``, each on its own stream (batch_parts)."""
+        return batch_parts(b, self.max_parts) if (self.fused and self.split_batch) else 1
+
     def splits(self, b: int) -> bool:
-        """Whether an untimed step of batch ``b`` runs as two half batches on two streams."""
-        return self.fused and self.split_batch and 34 <= b <= 256 and b % 2 == 0
+        """Whether an untimed step of batch ``b`` runs as row parts on several streams."""
+        return self.parts(b) > 1
 
     def step_(self, x_res: torch.Tensor, caches: List[Mamba2Cache], events=None):
         """In-place step of the whole stack: x_res [b, d_model] f32 becomes the stack output.
@@ -607,22 +632,23 @@ class Mamba2Stack:
         ``events``: optional list of one torch.cuda.Event pair per layer,
         recorded around that layer's state-update kernel (benchmark timing)."""
         b = x_res.shape[0]
-        if (events is None and self.splits(b) and x_res.data_ptr() % 16 == 0 and x_res.stride(0) % 4 == 0
-                and x_res.is_cuda):
-            # two independent half batches on two streams: one half's weight-streaming
-            # products run while the other's state kernel streams the caches (each half
-            # reads the weights once; rows never interact, so the step is the same)
+        K = self.parts(b) if events is None else 1
+        if K > 1 and x_res.data_ptr() % 16 == 0 and x_res.stride(0) % 4 == 0 and x_res.is_cuda:
+            # independent row parts on K streams: one part's weight-streaming products
+            # run while another's state kernel streams the caches (each part reads the
+            # weights once; rows never interact, so the step is the same)
             cur = torch.cuda.current_stream(x_res.device)
-            if self._side is None:
-                self._side = (torch.cuda.Stream(x_res.device), torch.cuda.Stream(x_res.device))
-            h = b // 2
-            for k, (lo, hi) in enumerate(((0, h), (h, b))):
+            if self._side is None or len(self._side) < K:
+                self._side = tuple(torch.cuda.Stream(x_res.device) for _ in range(K))
+            bounds = [(b * k) // K for k in range(K + 1)]
+            for k in range(K):
+                lo, hi = bounds[k], bounds[k + 1]
                 st = self._side[k]
                 st.wait_stream(cur)
                 with torch.cuda.stream(st):
                     part = [Mamba2Cache(conv_bvk=cc.conv_bvk[lo:hi], ssm_bhpr=cc.ssm_bhpr[lo:hi]) for cc in caches]
                     self._stack_fused(x_res[lo:hi], part, None, slot=1 + k)
-            for st in self._side:
+            for st in self._side[:K]:
                 cur.wait_stream(st)
             return x_res
         bufs = self.buffers(b, x_res.device)
@@ -644,7 +670,7 @@ class Mamba2Stack:
         ws = bufs["ws"]
         wsp, stream = ctypes.c_void_p(ws.data_ptr()), _stream(x_res.device)
         # every pointer the per-layer args embed (the residual row and both caches);
-        # slots 1 and 2 are the halves of the two-stream schedule (concurrent calls)
+        # slots 1 .. K are the row parts of the batch-split schedule (concurrent calls)
         concurrent = slot > 0
         key = ("stack", x_res.data_ptr(), x_res.shape[0], x_res.stride(0), concurrent) + tuple(
             (c.conv_bvk.data_ptr(), c.ssm_bhpr.data_ptr()) for c in caches)

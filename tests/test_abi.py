@@ -163,10 +163,16 @@ def test_missing_library_raises_no_fallback():
     assert r.returncode == 0 and "raised" in r.stdout, r.stdout + r.stderr
 
 
-def test_half_batch_predicate_needs_no_gpu():
-    """Mamba2Stack.splits: the two-stream half-batch schedule applies to a fused
-    stack at an even batch of 34 to 256 only, and can be switched off."""
+def test_batch_parts_need_no_gpu():
+    """The batch-split decode schedule: batch_parts gives ceil(b / 32) row parts
+    for 34 to 256 rows, at least 2 and at most the stack's cap; Mamba2Stack
+    caps at two (halves) and applies to a fused stack only, Mamba3Stack at
+    four; both can be switched off."""
     import mamba_hip
+
+    bs = (1, 16, 32, 33, 34, 35, 36, 48, 64, 65, 66, 96, 97, 100, 128, 255, 256, 258)
+    assert [mamba_hip.batch_parts(b, 4) for b in bs] == [1, 1, 1, 1, 2, 2, 2, 2, 2, 3, 3, 3, 4, 4, 4, 4, 4, 1]
+    assert [mamba_hip.batch_parts(b, 2) for b in bs] == [1, 1, 1, 1, 2, 2, 2, 2, 2, 2, 2, 2, 2, 2, 2, 2, 2, 1]
 
     def stack(fused, split_batch):  # the predicate reads only these two flags; no layers are built
         s = object.__new__(mamba_hip.Mamba2Stack)
@@ -174,7 +180,12 @@ def test_half_batch_predicate_needs_no_gpu():
         return s
 
     s = stack(True, True)
-    assert [b for b in (1, 16, 32, 33, 34, 35, 36, 64, 65, 66, 100, 255, 256, 258) if s.splits(b)] == \
-        [34, 36, 64, 66, 100, 256]
+    assert [b for b in bs if s.splits(b)] == [34, 35, 36, 48, 64, 65, 66, 96, 97, 100, 128, 255, 256]
+    assert all(s.parts(b) == 2 for b in bs if s.splits(b))
     assert not stack(True, False).splits(64)
     assert not stack(False, True).splits(64)
+    m3 = object.__new__(mamba_hip.Mamba3Stack)
+    m3.split_batch = True
+    assert [m3.parts(b) for b in (33, 34, 48, 64, 96, 100, 128, 256)] == [1, 2, 2, 2, 3, 4, 4, 4]
+    m3.split_batch = False
+    assert m3.parts(100) == 1
