@@ -40,13 +40,13 @@ __device__ __forceinline__ lin_f32x16_t lin_mfma(lin_bf16x8_t a, lin_bf16x8_t b,
 #define MAMBA_LIN_NW_BIGM 8     // waves per workgroup for four or eight 32-row tiles
 #endif
 #ifndef MAMBA_LIN_U1
-#define MAMBA_LIN_U1 0          // k-steps per pipeline stage for one 32-row tile (0: lin_depth1)
+#define MAMBA_LIN_U1 0          // k-steps per pipeline stage for one 32-row tile (0: lin_depth; 3..8)
 #endif
 #ifndef MAMBA_LIN_UMAX
-#define MAMBA_LIN_UMAX 5        // deepest stage lin_depth1 picks (5, 6 or 8)
+#define MAMBA_LIN_UMAX 5        // deepest stage lin_depth picks for one 32-row tile (5, 6 or 8)
 #endif
 #ifndef MAMBA_LIN_U2
-#define MAMBA_LIN_U2 0          // k-steps per pipeline stage for two 32-row tiles (0: lin_depth)
+#define MAMBA_LIN_U2 0          // k-steps per pipeline stage for two 32-row tiles (0: lin_depth; 2..4)
 #endif
 #ifndef MAMBA_LIN_UMAX2
 #define MAMBA_LIN_UMAX2 3       // deepest stage lin_depth picks for two 32-row tiles (3 or 4)
@@ -96,6 +96,10 @@ struct LinAct {
     }
 };
 
+// Column parts per 32-column tile: 2 or 4 as asked, anything else one (a
+// part count that does not divide the tile would leave columns unwritten).
+__host__ __device__ __forceinline__ int lin_parts(const LinParams& p) { return p.CS == 2 || p.CS == 4 ? p.CS : 1; }
+
 // A byte offset past every operand's extent: the load reads zero.
 constexpr uint32_t kLinOut = 0x80000000u;
 
@@ -130,7 +134,7 @@ template <int MT, int NW, int EPI, bool RM, int U>
 __global__ __launch_bounds__(64 * NW) void lin_stream(LinParams p) {
     constexpr int RT = (MT < 2 || NW >= 16) ? 1 : 2;  // 32-row tiles reduced per LDS round
     __shared__ float s_red[NW][RT][16][64];
-    const int cs = p.CS > 1 ? p.CS : 1;
+    const int cs = lin_parts(p);
     const int j = blockIdx.x / cs, z = blockIdx.y;
     const int cw = 32 / cs, c0 = (blockIdx.x % cs) * cw;  // this workgroup's columns 32 j + c0 ..
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -207,7 +211,7 @@ __global__ __launch_bounds__(64 * NW) void lin_stream(LinParams p) {
 
 template <int MT, int NW, bool RM, int U>
 static void lin_launch_u(const LinParams& p, int epi, hipStream_t stream) {
-    const dim3 grid(((p.N + 31) / 32) * (p.CS > 1 ? p.CS : 1), p.S);
+    const dim3 grid(((p.N + 31) / 32) * lin_parts(p), p.S);
     if (epi == LIN_STORE) hipLaunchKernelGGL((lin_stream<MT, NW, LIN_STORE, RM, U>), grid, dim3(64 * NW), 0, stream, p);
     else hipLaunchKernelGGL((lin_stream<MT, NW, LIN_PARTIAL, RM, U>), grid, dim3(64 * NW), 0, stream, p);
 }
