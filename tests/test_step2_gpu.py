@@ -302,6 +302,8 @@ LIN_CASES = [
     (1, 256, 1000, "f32", "f32", False),     # MT 1, 4 waves, masked last stage, ragged last tile, 4 parts
     (3, 1024, 96, "bf16", "f32", True),      # MT 1, in place, 16 waves, two pipeline stages per wave, 4 parts
     (32, 2048, 1024, "bf16", "bf16", True),  # the Mamba-3 half-batch out_proj: 32 tiles x 16 waves x 2 parts
+    (16, 2560, 2560, "bf16", "bf16", True),  # 16 waves, walks of 10 k-steps: two stages of 5
+    (8, 1792, 1024, "bf16", "f32", False),   # walks of 7: stages of 4, the second with one masked k-step; 2 parts
     (40, 512, 320, "bf16", "bf16", False),   # MT 2, in place: rows 40..63 read past x's end (zero)
     (100, 2048, 64, "f32", "f32", True),     # MT 4
     (200, 4096, 200, "bf16", "f32", False),  # MT 8, in place, 8 waves per workgroup
