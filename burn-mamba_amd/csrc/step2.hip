@@ -405,6 +405,64 @@ __global__ __launch_bounds__(256) void rmsnorm_residual(RmsParams p) {
     }
 }
 
+// The same with the row in registers, a float4 per thread and step (V steps:
+// cols <= 1024 V), every load of the row issued before any arithmetic (one
+// memory round trip instead of a load per column step and a second pass over
+// x).  Needs cols % 4 == 0 and 16-byte rows (8-byte for bf16 operands); the
+// per-element arithmetic is the scalar kernel's.
+template <int V>
+__global__ __launch_bounds__(256) void rmsnorm_residual_v(RmsParams p) {
+    __shared__ float s_red[4];
+    const int r = blockIdx.x, t = threadIdx.x;
+    const int nv = p.cols >> 2;
+    float4* x = reinterpret_cast<float4*>(p.x + (int64_t)r * p.x_sr);
+    float4 v[V], a[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        const int c4 = t + 256 * i;
+        const bool in = c4 < nv;
+        v[i] = in ? x[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
+        a[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (p.add && in) {
+            if (p.add_bf16) {
+                const uint2 u = reinterpret_cast<const uint2*>(static_cast<const bf16_t*>(p.add) + (int64_t)r * p.add_sr)[c4];
+                a[i] = make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                                   __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
+            } else {
+                a[i] = reinterpret_cast<const float4*>(static_cast<const float*>(p.add) + (int64_t)r * p.add_sr)[c4];
+            }
+        }
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        const int c4 = t + 256 * i;
+        if (p.add) {
+            v[i].x += a[i].x; v[i].y += a[i].y; v[i].z += a[i].z; v[i].w += a[i].w;
+            if (c4 < nv) x[c4] = v[i];
+        }
+        ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
+    }
+    if (!p.out) return;
+    ss = block_sum_256(ss, s_red);
+    const float rms = sqrtf(ss / (float)p.cols + kDivEpsF32);
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        const int c4 = t + 256 * i;
+        if (c4 >= nv) continue;
+        const float4 w4 = reinterpret_cast<const float4*>(p.w)[c4];
+        const float4 o = make_float4((v[i].x / rms) * w4.x, (v[i].y / rms) * w4.y, (v[i].z / rms) * w4.z,
+                                     (v[i].w / rms) * w4.w);
+        if (p.out_bf16) {
+            reinterpret_cast<uint2*>(static_cast<bf16_t*>(p.out) + (int64_t)r * p.out_sr)[c4] =
+                make_uint2((uint32_t)f32_to_bf16(o.x) | ((uint32_t)f32_to_bf16(o.y) << 16),
+                           (uint32_t)f32_to_bf16(o.z) | ((uint32_t)f32_to_bf16(o.w) << 16));
+        } else {
+            reinterpret_cast<float4*>(static_cast<float*>(p.out) + (int64_t)r * p.out_sr)[c4] = o;
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
@@ -513,7 +571,19 @@ extern "C" int mamba_rmsnorm(const mamba_rmsnorm_args* a, mamba_stream_t stream)
     p.add_bf16 = a->add_dtype == MAMBA_BF16; p.out_bf16 = a->out_dtype == MAMBA_BF16;
     p.x = a->x; p.x_sr = a->x_sr; p.add = a->add; p.add_sr = a->add_sr;
     p.w = a->weight; p.out = a->out; p.out_sr = a->out_sr;
-    hipLaunchKernelGGL(rmsnorm_residual, dim3(p.rows), dim3(256), 0, (hipStream_t)stream, p);
+    // the register form where every row is 16-byte aligned (8-byte for bf16)
+    auto rows_ok = [](const void* ptr, int64_t sr, bool bf16) {
+        return ptr == nullptr || (((uintptr_t)ptr & (bf16 ? 7u : 15u)) == 0 && sr % 4 == 0);
+    };
+    const bool vec = p.cols % 4 == 0 && p.cols <= 4096 && rows_ok(p.x, p.x_sr, false) &&
+                     rows_ok(p.add, p.add_sr, p.add_bf16) && rows_ok(p.out, p.out_sr, p.out_bf16) &&
+                     (p.out == nullptr || ((uintptr_t)p.w & 15u) == 0);
+    const hipStream_t s = (hipStream_t)stream;
+    if (!vec) hipLaunchKernelGGL(rmsnorm_residual, dim3(p.rows), dim3(256), 0, s, p);
+    else if (p.cols <= 1024) hipLaunchKernelGGL(rmsnorm_residual_v<1>, dim3(p.rows), dim3(256), 0, s, p);
+    else if (p.cols <= 2048) hipLaunchKernelGGL(rmsnorm_residual_v<2>, dim3(p.rows), dim3(256), 0, s, p);
+    else if (p.cols <= 3072) hipLaunchKernelGGL(rmsnorm_residual_v<3>, dim3(p.rows), dim3(256), 0, s, p);
+    else hipLaunchKernelGGL(rmsnorm_residual_v<4>, dim3(p.rows), dim3(256), 0, s, p);
     MAMBA_CHECK_LAUNCH();
     return MAMBA_OK;
 }

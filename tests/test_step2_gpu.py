@@ -486,3 +486,42 @@ def test_fused_stack_config3_layer_shape(b):
         for i, c in enumerate(caches):
             np.testing.assert_allclose(c.conv_bvk.cpu().numpy(), refs[i][0], **BF16_TOL)
             np.testing.assert_allclose(c.ssm_bhpr.cpu().numpy(), refs[i][1], **BF16_TOL)
+
+
+@pytest.mark.parametrize("cols,add_dt,out_dt,pad", [
+    (1024, "bf16", "bf16", 0),   # register form, one float4 per thread: the Mamba-3 stack's norm
+    (2560, "f32", "f32", 0),     # two float4 steps
+    (3000, None, "bf16", 8),     # three steps, the last partial; strided rows (16-byte aligned)
+    (4096, "bf16", "f32", 0),    # four steps
+    (1000, "f32", "bf16", 0),    # register form with a 4000-byte row stride
+    (1002, "bf16", "f32", 0),    # cols % 4 != 0: the scalar kernel
+])
+def test_rmsnorm_matches_oracle(cols, add_dt, out_dt, pad):
+    """mamba_rmsnorm: x += add (in place, f32), out = RmsNorm(x) * w (rms_norm.rs:53-98)
+    against the oracle's f64 RmsNorm of the same f32 sums; bf16 outputs within one bf16
+    rounding, f32 within sum-order rounding."""
+    import torch
+    import mamba_hip
+    import oracle
+    rows = 7
+    rng = np.random.default_rng(cols)
+    dts = {"f32": torch.float32, "bf16": torch.bfloat16}
+    x0 = rng.standard_normal((rows, cols)).astype(np.float32)
+    w = (0.5 + rng.random(cols)).astype(np.float32)
+    xd = torch.tensor(np.pad(x0, ((0, 0), (0, pad))), device="cuda")[:, :cols]
+    add = None
+    want_x = x0.copy()
+    if add_dt is not None:
+        a = rng.standard_normal((rows, cols)).astype(np.float32)
+        add = torch.tensor(a, device="cuda").to(dts[add_dt])
+        want_x = x0 + add.float().cpu().numpy()
+    out = torch.empty((rows, cols + pad), device="cuda", dtype=dts[out_dt])[:, :cols]
+    mamba_hip.step.rmsnorm(xd, torch.tensor(w, device="cuda"), out=out, add=add)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(xd.cpu().numpy(), want_x, rtol=1e-6, atol=1e-6)
+    want = oracle.rmsnorm(want_x, w)
+    got = out.float().cpu().numpy()
+    if out_dt == "bf16":
+        np.testing.assert_allclose(got, want, rtol=2 ** -8, atol=1e-6)
+    else:
+        np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6)
