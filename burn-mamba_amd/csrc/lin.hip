@@ -27,6 +27,7 @@
 namespace mamba {
 
 typedef float lin_f32x16_t __attribute__((ext_vector_type(16)));
+typedef __bf16 lin_bf16x2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ lin_f32x16_t lin_mfma(lin_bf16x8_t a, lin_bf16x8_t b, lin_f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -209,6 +210,125 @@ __global__ __launch_bounds__(64 * NW) void lin_stream(LinParams p) {
     }
 }
 
+#ifndef MAMBA_LIN_GEMV
+#define MAMBA_LIN_GEMV 1        // 1: products of one row take lin_gemv
+#endif
+
+// The product for one row (MM = 1; the code takes MM rows, M <= MM, but two
+// rows measured slower than the MFMA kernel: 64-layer decode steps at batch 2
+// 2.16 -> 2.19 ms for Mamba-2, 1.32 -> 1.40 ms for Mamba-3, against batch 1
+// 2.08 -> 1.89 ms and 1.32 -> 1.28 ms): the same weight stream,
+// plans and epilogues as lin_stream, but no MFMA.  A lane holds 8 k of one
+// column of each weight block; the row's 8 matching activation values are one
+// 16-byte load that every lane of the wave half shares (two addresses per wave
+// and row, where the MFMA operand would be a 1 KB block whose other 31 rows
+// are zero), and the products accumulate in f32 on the VALU by packed bf16
+// dots (v_dot2c_f32_bf16: two products per instruction).  The two wave halves
+// (k 0..7 and 8..15 of each block) are summed at the end.
+template <int NW, int EPI, bool RM, int U, int MM>
+__global__ __launch_bounds__(64 * NW) void lin_gemv(LinParams p) {
+    __shared__ float s_red[NW][MM][32];
+    const int cs = lin_parts(p);
+    const int j = blockIdx.x / cs, z = blockIdx.y;
+    const int cw = 32 / cs, c0 = (blockIdx.x % cs) * cw;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5;
+    const int KS = p.K >> 4;
+    const int z0 = (KS * z) / p.S, z1 = (KS * (z + 1)) / p.S;
+    const int s0 = z0 + ((z1 - z0) * wave) / NW, s1 = z0 + ((z1 - z0) * (wave + 1)) / NW;
+    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(p.W + (int64_t)j * KS * 64, (uint32_t)KS * 1024u);
+    const __amdgpu_buffer_rsrc_t ra = RM ? buf_rsrc(p.X, (uint32_t)((int64_t)p.M * p.x_ld * 2))
+                                         : buf_rsrc(p.A, (uint32_t)KS * 1024u);
+    const int lcol = lane & 31;
+    uint32_t lo = (uint32_t)lane * 16u;
+    lo = (lcol >= c0 && lcol < c0 + cw) ? lo : kLinOut;
+    asm volatile("" : "+v"(lo));
+    // byte offset of row m's k = 16 s + 8 h .. + 7 (the packed operand of one row tile: lane m + 32 h)
+    auto aoff = [&](int m, int s) -> uint32_t {
+        return RM ? (uint32_t)(((int64_t)m * p.x_ld + 16 * s + 8 * h) * 2) : (uint32_t)((s * 64 + m + 32 * h) * 16);
+    };
+    struct Stage { uint4 w[U]; uint4 a[U][MM]; };
+    auto load = [&](Stage& st, int s) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const bool ok = s + u < s1;
+            st.w[u] = buf_ld16(rw, ok ? (uint32_t)(s + u) * 1024u + lo : kLinOut);
+#pragma unroll
+            for (int m = 0; m < MM; ++m) st.a[u][m] = buf_ld16(ra, ok && m < p.M ? aoff(m, s + u) : kLinOut);
+        }
+    };
+    // four partial sums per row (k pairs e = 0..3 of each block), so that the
+    // packed bf16 dots (two products into f32 per instruction) form four
+    // independent chains
+    float acc4[MM][4];
+#pragma unroll
+    for (int m = 0; m < MM; ++m)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc4[m][e] = 0.f;
+    auto compute = [&](const Stage& st) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t wv[4] = {st.w[u].x, st.w[u].y, st.w[u].z, st.w[u].w};
+#pragma unroll
+            for (int m = 0; m < MM; ++m) {
+                const uint32_t xv[4] = {st.a[u][m].x, st.a[u][m].y, st.a[u][m].z, st.a[u][m].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    acc4[m][e] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(lin_bf16x2_t, wv[e]),
+                                                                 __builtin_bit_cast(lin_bf16x2_t, xv[e]), acc4[m][e], false);
+            }
+        }
+    };
+    const int nstage = (s1 - s0 + U - 1) / U;
+    if (nstage > 0) {
+        Stage sa, sb;
+        load(sa, s0);
+        for (int st = 0; st < nstage; st += 2) {
+            const bool more1 = st + 1 < nstage;
+            if (more1) load(sb, s0 + U * (st + 1));
+            compute(sa);
+            if (more1) {
+                if (st + 2 < nstage) load(sa, s0 + U * (st + 2));
+                compute(sb);
+            }
+        }
+    }
+    // the partial sums, the two halves of each column, then the waves
+    float acc[MM];
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+        acc[m] = (acc4[m][0] + acc4[m][1]) + (acc4[m][2] + acc4[m][3]);
+        acc[m] += __shfl_xor(acc[m], 32, 64);
+    }
+    if (lane < 32)
+#pragma unroll
+        for (int m = 0; m < MM; ++m) s_red[wave][m][lane] = acc[m];
+    __syncthreads();
+    if ((int)threadIdx.x < MM * 32) {
+        const int m = threadIdx.x >> 5, c = threadIdx.x & 31, n = 32 * j + c;
+        if (m < p.M && n < p.N && c >= c0 && c < c0 + cw) {
+            float sum = 0.f;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) sum += s_red[w][m][c];
+            if (EPI == LIN_STORE) {
+                if (p.bias) sum += p.bias[n];
+                if (p.out_bf16)
+                    static_cast<bf16_t*>(p.out)[(int64_t)m * p.out_ld + n] = f32_to_bf16(sum);
+                else
+                    static_cast<float*>(p.out)[(int64_t)m * p.out_ld + n] = sum;
+            } else {
+                p.part[((int64_t)z * p.M + m) * p.N + n] = sum;
+            }
+        }
+    }
+}
+
+template <int NW, bool RM, int U, int MM>
+static void lin_launch_gemv(const LinParams& p, int epi, hipStream_t stream) {
+    const dim3 grid(((p.N + 31) / 32) * lin_parts(p), p.S);
+    if (epi == LIN_STORE) hipLaunchKernelGGL((lin_gemv<NW, LIN_STORE, RM, U, MM>), grid, dim3(64 * NW), 0, stream, p);
+    else hipLaunchKernelGGL((lin_gemv<NW, LIN_PARTIAL, RM, U, MM>), grid, dim3(64 * NW), 0, stream, p);
+}
+
 template <int MT, int NW, bool RM, int U>
 static void lin_launch_u(const LinParams& p, int epi, hipStream_t stream) {
     const dim3 grid(((p.N + 31) / 32) * lin_parts(p), p.S);
@@ -241,6 +361,13 @@ template <int MT, int NW, bool RM>
 static void lin_launch_nw(const LinParams& p, int epi, hipStream_t stream) {
     const int ks = p.K >> 4, kz = (ks + p.S - 1) / p.S, kw = (kz + NW - 1) / NW;
     if constexpr (MT == 1) {
+        if (MAMBA_LIN_GEMV && p.M == 1) {
+            const int ug = lin_depth(kw, 5, 3);
+            if (ug == 5) lin_launch_gemv<NW, RM, 5, 1>(p, epi, stream);
+            else if (ug == 4) lin_launch_gemv<NW, RM, 4, 1>(p, epi, stream);
+            else lin_launch_gemv<NW, RM, 3, 1>(p, epi, stream);
+            return;
+        }
         // 16 waves (at most 128 registers each) hold stages of up to 6 k-steps
         const int u = MAMBA_LIN_U1 ? MAMBA_LIN_U1 : lin_depth(kw, NW >= 16 ? std::min(MAMBA_LIN_UMAX, 6) : MAMBA_LIN_UMAX, 3);
         switch (u) {

@@ -299,7 +299,9 @@ LIN_CASES = [
     # bf16 x with 16-byte aligned rows is read in place, anything else packed first;
     # weights up to 16 MB take one k-split with 4 / 8 / 16 waves per workgroup, and
     # 2 or 4 column parts per 32-column tile when the tiles are few
-    (1, 256, 1000, "f32", "f32", False),     # MT 1, 4 waves, masked last stage, ragged last tile, 4 parts
+    (1, 256, 1000, "f32", "f32", False),     # one row (lin_gemv, packed), masked last stage, ragged last tile, 4 parts
+    (1, 2560, 2560, "bf16", "bf16", True),   # one row (lin_gemv, in place), 16 waves, stages of 5
+    (2, 512, 160, "f32", "f32", False),      # two rows (the MFMA kernel), packed operand, 4 parts
     (3, 1024, 96, "bf16", "f32", True),      # MT 1, in place, 16 waves, two pipeline stages per wave, 4 parts
     (32, 2048, 1024, "bf16", "bf16", True),  # the Mamba-3 half-batch out_proj: 32 tiles x 16 waves x 2 parts
     (16, 2560, 2560, "bf16", "bf16", True),  # 16 waves, walks of 10 k-steps: two stages of 5
