@@ -765,10 +765,18 @@ static int step2_row_splits(int rows, int heads, int N) {
 #define MAMBA_STEP2_CC_NW_OUT 16
 #endif
 
-// Products of a one-row call (lin_gemv): in_proj two k-splits of 8 waves,
-// out_proj two of 16, in place of lin_splits' 4 and 8 of 4 waves.  Measured on
-// the 64-layer config-3 step at batch 1: 1.89 -> 1.86 ms (each change alone
-// about 1 %; one k-split, or 8 in_proj k-splits, measured slower).
+// Products of a one-stream call with one row tile: in_proj two k-splits of 8
+// waves (up to 32 rows), and at one row (lin_gemv) out_proj two of 16, in
+// place of lin_splits' 4 and 8 of 4 waves.  Measured on the 64-layer config-3
+// step: batch 1 1.89 -> 1.86 ms (each change alone about 1 %; one k-split, or 8
+// in_proj k-splits, slower); the in_proj plan at batch 8 / 16 / 24 2.50 /
+// 3.01 / 3.52 -> 2.47 / 2.97 / 3.48 ms, where the out_proj one did not pay.
+#ifndef MAMBA_STEP2_R1_ROWS
+#define MAMBA_STEP2_R1_ROWS 32
+#endif
+#ifndef MAMBA_STEP2_R1_OUT_ROWS
+#define MAMBA_STEP2_R1_OUT_ROWS 1
+#endif
 #ifndef MAMBA_STEP2_R1_S_IN
 #define MAMBA_STEP2_R1_S_IN 2
 #endif
@@ -803,11 +811,13 @@ static LayerGeom layer_geom(const mamba2_layer_args* a) {
         g.S_out = MAMBA_STEP2_CC_S_OUT;
         g.nw_in = MAMBA_STEP2_CC_NW_IN;
         g.nw_out = MAMBA_STEP2_CC_NW_OUT;
-    } else if (g.M == 1) {
+    } else if (g.mt == 1 && g.M <= MAMBA_STEP2_R1_ROWS) {
         if (MAMBA_STEP2_R1_S_IN) g.S_in = MAMBA_STEP2_R1_S_IN;
-        if (MAMBA_STEP2_R1_S_OUT) g.S_out = MAMBA_STEP2_R1_S_OUT;
         if (MAMBA_STEP2_R1_NW_IN) g.nw_in = MAMBA_STEP2_R1_NW_IN;
-        if (MAMBA_STEP2_R1_NW_OUT) g.nw_out = MAMBA_STEP2_R1_NW_OUT;
+        if (g.M <= MAMBA_STEP2_R1_OUT_ROWS) {
+            if (MAMBA_STEP2_R1_S_OUT) g.S_out = MAMBA_STEP2_R1_S_OUT;
+            if (MAMBA_STEP2_R1_NW_OUT) g.nw_out = MAMBA_STEP2_R1_NW_OUT;
+        }
     }
     return g;
 }
